@@ -1,0 +1,294 @@
+"""Benchmark of the MetalNN hot path on one MI355X: ms per 7.8 s stereo chunk.
+
+One step = the HTDemucs-shaped time encoder (config 4) on 4 chunks, one chunk per forward
+(batch 1, as the configuration is quoted), plus the cross-domain transformer bottleneck
+(config 5) on those 4 chunks as one batch-4 forward. value = ms_per_step / 4
+= t(config 4, batch 1) + t(config 5, batch 4) / 4, the headline metric. Inputs and weights are
+seeded synthetic data of the configurations' shapes, resident in HBM before timing starts.
+
+Per-kernel-family GPU time comes from HIP events bracketing every library launch on its stream
+during the timed steps (mnn_device_kernel_timing); the dominant family is reported against
+MI355X peak as `roofline`. The CPU baseline times the fp32 oracle on one chunk on host cores.
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--precision f32|bf16]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "ms per 7.8s stereo chunk (HTDemucs-shaped); per-kernel % of HBM/MFMA roofline"
+PEAK = {"hbm": 8.0e12, "f32": 157.3e12, "bf16": 2.5e15}  # B/s, FLOP/s (MI355X datasheet, dense)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------ algorithmic work per step
+def encoder_work():
+    """flops and bytes per chunk of config 4, per kernel family."""
+    from metalaudio_amd import workloads as W
+    L = W.CHUNK_SAMPLES
+    fam = {}
+    ch = W.ENC_CHANNELS
+    for i in range(4):
+        cin, cout = ch[i], ch[i + 1]
+        lo = (L + 6 - 8) // 4 + 1
+        conv_flops = 2.0 * cout * lo * cin * 8
+        conv_bytes = 4.0 * (cin * L + cout * lo + cout * cin * 8 + cout)
+        rw_flops = 2.0 * 2 * cout * lo * cout
+        rw_bytes = 4.0 * (cout * lo + cout * lo + 2 * cout * cout + 2 * cout)
+        key = "conv1d_direct" if cin * 8 < 64 else "gemm_f32_mfma_conv"
+        f = fam.setdefault(key, [0.0, 0.0])
+        f[0] += conv_flops
+        f[1] += conv_bytes
+        f = fam.setdefault("gemm_f32_mfma_kn", [0.0, 0.0])
+        f[0] += rw_flops
+        f[1] += rw_bytes
+        L = lo
+    return fam
+
+
+def transformer_work(batch):
+    from metalaudio_amd import workloads as W
+    E, H, Hd, St, Sf = W.T5_EMBED, W.T5_HEADS, W.T5_FFN, W.T5_TIME_LEN, W.T5_FREQ_LEN
+    hd = E // H
+    attn_f = attn_b = gemm_f = gemm_b = ln_b = 0.0
+    for i in range(W.T5_LAYERS):
+        cross = i % 2 == 1
+        for own, other in ((St, Sf), (Sf, St)):
+            sk = other if cross else own
+            attn_f += 4.0 * own * sk * hd * H * batch
+            attn_b += 4.0 * batch * (own * E + 2 * sk * E + own * E)
+            if cross:
+                gemm_f += 2.0 * batch * (own * E * E + other * E * 2 * E)
+            else:
+                gemm_f += 2.0 * batch * own * E * 3 * E
+            gemm_f += 2.0 * batch * own * (E * E + 2 * E * Hd)
+            gemm_b += 4.0 * batch * own * (E + 3 * E + E + E + E + Hd + Hd + E)
+            ln_b += 4.0 * batch * 2 * own * E * (3 if cross else 2)
+    return {"attn_fwd_f32": [attn_f, attn_b], "gemm_f32_mfma_nk": [gemm_f, gemm_b],
+            "layernorm": [0.0, ln_b]}
+
+
+# ------------------------------------------------------------------ model setup
+def build_models(nn, W, dev, precision):
+    c4 = W.config4()
+    blocks = []
+    seq = nn.Sequential(dev)
+    for cin, cout, lv in zip(W.ENC_CHANNELS[:-1], W.ENC_CHANNELS[1:], c4["levels"]):
+        b = nn.UNetEncoderBlock(dev, cin, cout, 8, 4, 1, rewrite=True, precision=precision)
+        b.load_weights(lv["conv.weight"], lv["conv.bias"], lv["norm.weight"], lv["norm.bias"],
+                       lv["rewrite.weight"], lv["rewrite.bias"])
+        blocks.append(b)
+        seq.add(b)
+    seq.build()
+    c5 = W.config5(batch=W.T5_BATCH)
+    ct = nn.CrossTransformerEncoder(dev, c5["embed"], c5["heads"], c5["ffn"], c5["layers"],
+                                    c5["layer_scale"], precision=precision)
+    ct.load_state(c5["params"])
+    # 4 distinct chunks for the encoder, resident in HBM
+    rng = np.random.Generator(np.random.PCG64(2024))
+    chunks = [nn.Tensor.from_numpy(dev, c4["x"])]
+    for _ in range(3):
+        chunks.append(nn.Tensor.from_numpy(
+            dev, rng.uniform(-1, 1, c4["x"].shape).astype(np.float32)))
+    t_in = nn.Tensor.from_numpy(dev, c5["time"])
+    f_in = nn.Tensor.from_numpy(dev, c5["freq"])
+    t_out = nn.Tensor(dev, t_in.shape)
+    f_out = nn.Tensor(dev, f_in.shape)
+    return dict(seq=seq, blocks=blocks, ct=ct, chunks=chunks, t_in=t_in, f_in=f_in,
+                t_out=t_out, f_out=f_out, c4=c4, c5=c5)
+
+
+def run_encoder(m, stream):
+    for x in m["chunks"]:
+        m["seq"].forward(x, stream)
+
+
+def run_transformer(m, stream):
+    m["ct"].forward_cross(m["t_in"], m["f_in"], m["t_out"], m["f_out"], stream)
+
+
+def timed(fn, stream, steps):
+    stream.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    stream.sync()
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+# ------------------------------------------------------------------ CPU baseline
+def cpu_baseline(m, budget_s=20.0):
+    """fp32 oracle (numpy + BLAS) on one chunk: config 4 at batch 1 and config 5 at batch 1
+    (the per-chunk share of the batch-4 transformer)."""
+    import oracle
+    from metalaudio_amd import workloads as W
+    threads = os.cpu_count() or 1
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max(int(i.get("num_threads", 1)) for i in threadpool_info()) or threads
+    except Exception:
+        pass
+    c4 = m["c4"]
+    c5 = W.config5(batch=1)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        oracle.time_encoder(c4["x"], c4["levels"], dtype=np.float32)
+        oracle.cross_transformer(c5["time"], c5["freq"], c5["params"], c5["layers"], c5["heads"],
+                                 dtype=np.float32)
+        times.append((time.perf_counter() - t0) * 1e3)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
+            break
+    return {
+        "value": round(statistics.median(times), 2),
+        "unit": "ms per chunk",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{len(times)} run(s) of one 7.8 s chunk: config 4 (batch 1) + config 5 at "
+                  f"batch 1, fp32 numpy/BLAS oracle, median; host {os.cpu_count()} CPUs",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--precision", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this path runs on a single MI355X with no "
+              "sharding or collectives (--gpus 1).", file=sys.stderr)
+        sys.exit(2)
+
+    from metalaudio_amd import nn
+    from metalaudio_amd import workloads as W
+
+    dev = nn.AudioDevice(0)
+    stream = nn.Stream(dev)
+    log(f"device {dev.name}; building models ({args.precision})")
+    m = build_models(nn, W, dev, args.precision)
+
+    def step():
+        run_encoder(m, stream)
+        run_transformer(m, stream)
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    stream.sync()
+
+    # timed region: kernel events on, wall clock around exactly K steps
+    dev.reset_kernel_timing()
+    dev.set_kernel_timing(True)
+    log(f"timing {args.steps} steps")
+    ms_step = timed(step, stream, args.steps)
+    dev.set_kernel_timing(False)
+    fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
+            "gemm_f32_simple", "conv1d_direct", "layernorm", "gn_stats", "gn_finalize", "gn_apply",
+            "copy_bytes", "glu", "gelu"]
+    ktime = {}
+    for f in fams:
+        n, ms = dev.kernel_timing(f)
+        if n:
+            ktime[f] = (n, ms)
+    log("kernel ms/step: " + ", ".join(f"{k}={v[1] / args.steps:.3f} ({v[0] // args.steps})"
+                                        for k, v in ktime.items()))
+
+    # breakdown (no events): encoder alone and transformer alone
+    t_enc = timed(lambda: run_encoder(m, stream), stream, max(2, args.steps // 2)) / 4
+    t_tr = timed(lambda: run_transformer(m, stream), stream, max(2, args.steps // 2))
+    log(f"ms/step {ms_step:.3f}; encoder {t_enc:.3f} ms/chunk; transformer b4 {t_tr:.3f} ms")
+
+    # roofline of the dominant family
+    work = encoder_work()
+    work = {k: [v[0] * 4, v[1] * 4] for k, v in work.items()}  # 4 chunks per step
+    for k, v in transformer_work(W.T5_BATCH).items():
+        work[k] = v
+    fam_key = {"attn_fwd": "attn_fwd_f32"}
+    rows = {}
+    for f, (n, ms) in ktime.items():
+        wk = work.get(fam_key.get(f, f))
+        if not wk:
+            continue
+        t = ms / 1e3 / args.steps  # seconds per step
+        flops, byts = wk
+        bound = "mfma" if flops > 0 and flops / max(byts, 1) > 20 else "hbm"
+        if bound == "mfma":
+            ach = flops / t
+            peak = PEAK["bf16" if args.precision == "bf16" else "f32"]
+            rows[f] = {"bound": "mfma", "achieved": round(ach / 1e12, 2),
+                       "peak": round(peak / 1e12, 1), "unit": "TFLOP/s",
+                       "frac": round(ach / peak, 4), "ms_per_step": round(t * 1e3, 3),
+                       "launches_per_step": n // args.steps}
+        else:
+            ach = byts / t
+            rows[f] = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
+                       "unit": "GB/s", "frac": round(ach / PEAK["hbm"], 4),
+                       "ms_per_step": round(t * 1e3, 3), "launches_per_step": n // args.steps}
+    dom = max(ktime, key=lambda k: ktime[k][1])
+    roof = dict(rows.get(dom, {}))
+    roof["kernel"] = dom
+    traffic = None
+    tf = ROOT / "profiles" / "traffic.json"
+    if tf.exists():
+        try:
+            traffic = json.loads(tf.read_text()).get(dom)
+        except Exception:
+            traffic = None
+    roof["traffic"] = traffic
+    roof["avg_launch_us"] = round(ktime[dom][1] / ktime[dom][0] * 1e3, 2)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(m, args.cpu_budget)
+
+    out = {
+        "metric": METRIC,
+        "value": round(ms_step / 4, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.precision,
+        "data": "synthetic (seeded PCG64 inputs and weights of the BASELINE config shapes)",
+        "config": {
+            "workload": "config 4 (4-level time encoder, 2x343980 samples, batch 1) on 4 chunks "
+                        "+ config 5 (5-layer cross transformer, time 1344 / freq 2688 tokens, "
+                        "E 384, H 8, FFN 1536) at batch 4; value = step / 4 chunks",
+            "chunks_per_step": 4,
+            "encoder_ms_per_chunk": round(t_enc, 4),
+            "transformer_b4_ms": round(t_tr, 4),
+        },
+        "roofline": roof,
+        "kernels": rows,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,261 @@
+/*
+ * mnn.h — C ABI of the MI355X-native MetalNN inference layer stack.
+ *
+ * This is the drop-in boundary for the MetalNN hot path of zkeown/MetalAudio:
+ * the reference's `NNLayer` protocol (Sources/MetalNN/NNLayer.swift:12-16), the
+ * per-layer constructors and loaders, and `Sequential` (Sources/MetalNN/Model.swift:65-357).
+ * A Swift package wraps this header as a C target; Python reaches it via ctypes.
+ *
+ * Conventions
+ *  - Every call returns mnn_status (0 = MNN_OK). On failure the thread-local
+ *    message from mnn_last_error_message() says what went wrong.
+ *  - Handles are opaque and owned by whoever created them. Destroying a layer
+ *    that a Sequential still references is the caller's error.
+ *  - Tensors are device-resident (HBM), contiguous, row-major, zero-initialised
+ *    on creation (reference Tensor.swift:131-139). Host access is explicit
+ *    upload/download.
+ *  - Work is stream-ordered: a forward enqueues kernels on the stream and
+ *    returns; mnn_stream_sync() waits (reference ComputeContext.executeSync,
+ *    ComputeContext.swift:154-211). Nothing reads device memory on the host
+ *    during a forward, so there are no encode-time read-before-write hazards.
+ *  - A layer allocates its workspace on the first forward for a given input
+ *    shape and reuses it afterwards; a forward with a shape already seen
+ *    allocates nothing. Layers are not safe for concurrent forwards
+ *    (reference DynamicConv1D.swift:29-31); use one layer per thread.
+ */
+#ifndef MNN_H
+#define MNN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. 1-7 mirror MetalAudioError (Sources/MetalAudioKit/Core/AudioDevice.swift:11-77);
+ * 8-10 mirror SequentialModelError (Sources/MetalNN/Model.swift:5-20). */
+typedef enum mnn_status {
+  MNN_OK = 0,
+  MNN_ERR_INVALID_CONFIGURATION = 1,   /* invalidConfiguration (also NaN/Inf weights, NNLayer.swift:43-48) */
+  MNN_ERR_BUFFER_SIZE_MISMATCH = 2,    /* bufferSizeMismatch */
+  MNN_ERR_PIPELINE_CREATION_FAILED = 3,/* pipelineCreationFailed: kernel image missing for this GPU */
+  MNN_ERR_GPU_TIMEOUT = 4,             /* gpuTimeout (ComputeContext.swift:188-198) */
+  MNN_ERR_GPU_EXECUTION = 5,           /* gpuExecutionError (ComputeContext.swift:199-208) */
+  MNN_ERR_DEVICE_LOST = 6,             /* deviceLost (AudioDevice.swift:391-472) */
+  MNN_ERR_OUT_OF_MEMORY = 7,           /* bufferAllocationFailed */
+  MNN_ERR_SHAPE_MISMATCH = 8,          /* SequentialModelError.shapeMismatch */
+  MNN_ERR_EMPTY_MODEL = 9,             /* SequentialModelError.emptyModel */
+  MNN_ERR_INPUT_SHAPE_MISMATCH = 10,   /* SequentialModelError.inputShapeMismatch */
+  MNN_ERR_NOT_BUILT = 11,              /* "Model not built. Call build() first." (Model.swift:226-228) */
+  MNN_ERR_INVALID_ARGUMENT = 12        /* NULL handle, bad rank, unknown weight name */
+} mnn_status;
+
+typedef enum mnn_dtype { MNN_F32 = 0, MNN_BF16 = 1 } mnn_dtype;
+
+/* Compute precision of the matrix products (GEMM, implicit-GEMM conv, attention).
+ * F32: fp32 operands on v_mfma_f32_*_f32. BF16: operands rounded to bf16 (RNE),
+ * fp32 accumulation (precedent: HalfLinear, HalfPrecisionLinear.swift:60-212).
+ * Norms, softmax and activations always run in fp32. */
+typedef enum mnn_precision { MNN_PRECISION_F32 = 0, MNN_PRECISION_BF16 = 1 } mnn_precision;
+
+/* Fused activation codes. 0-4 are FusedConv1D's (Conv1D.swift:960-973); FusedLinear's sigmoid
+ * and tanh (Linear.swift:630-639) get codes 5 and 6 here. Leaky ReLU uses alpha 0.01 (the
+ * reference default, Conv1D.swift:786). GELU is the tanh approximation everywhere
+ * (Activations.swift:124-137). */
+typedef enum mnn_activation {
+  MNN_ACT_NONE = 0, MNN_ACT_RELU = 1, MNN_ACT_LEAKY_RELU = 2, MNN_ACT_GELU = 3, MNN_ACT_SWISH = 4,
+  MNN_ACT_SIGMOID = 5, MNN_ACT_TANH = 6
+} mnn_activation;
+
+/* DynamicConv1D.PaddingMode (DynamicConv1D.swift:40-61). */
+typedef enum mnn_padding_mode {
+  MNN_PAD_VALID = 0, MNN_PAD_SAME = 1, MNN_PAD_EXPLICIT = 2, MNN_PAD_REFLECT = 3
+} mnn_padding_mode;
+
+typedef struct mnn_device_s* mnn_device;
+typedef struct mnn_stream_s* mnn_stream;
+typedef struct mnn_tensor_s* mnn_tensor;
+typedef struct mnn_layer_s* mnn_layer;
+typedef struct mnn_sequential_s* mnn_sequential;
+
+#define MNN_MAX_RANK 8
+
+/* ---------------------------------------------------------------- errors / version */
+const char* mnn_last_error_message(void);
+const char* mnn_status_string(mnn_status status);
+const char* mnn_version(void);
+
+/* ---------------------------------------------------------------- device
+ * Replaces AudioDevice(device:) (AudioDevice.swift:323-348). */
+mnn_status mnn_device_create(int ordinal, mnn_device* out);
+mnn_status mnn_device_destroy(mnn_device dev);
+mnn_status mnn_device_name(mnn_device dev, char* buf, size_t buflen);
+mnn_status mnn_device_synchronize(mnn_device dev);
+/* AudioDevice.markDeviceLost / checkDeviceAvailability (AudioDevice.swift:391-472):
+ * after marking, every forward/upload/download on the device fails with MNN_ERR_DEVICE_LOST. */
+mnn_status mnn_device_mark_lost(mnn_device dev);
+mnn_status mnn_device_check_available(mnn_device dev, int timeout_ms);
+/* Per-kernel GPU timing with HIP events, the analogue of executeSyncWithTiming
+ * (ComputeContext.swift:232-297). While enabled, every launch of a library kernel is
+ * bracketed by events on its stream; mnn_device_kernel_timing() waits for the device and
+ * reports the launches and summed milliseconds of kernels whose name contains `kernel_substr`. */
+mnn_status mnn_device_set_kernel_timing(mnn_device dev, int enable);
+mnn_status mnn_device_kernel_timing(mnn_device dev, const char* kernel_substr,
+                                    int64_t* launches, double* total_ms);
+mnn_status mnn_device_reset_kernel_timing(mnn_device dev);
+
+/* ---------------------------------------------------------------- stream
+ * A stream plays the role of the command buffer + encoder pair. */
+mnn_status mnn_stream_create(mnn_device dev, mnn_stream* out);
+/* Wait for all work on the stream; MNN_ERR_GPU_TIMEOUT if it is not done within
+ * timeout_ms (<= 0 waits without limit). ComputeContext.executeSync, default 2 s (:137). */
+mnn_status mnn_stream_sync(mnn_stream s, int timeout_ms);
+mnn_status mnn_stream_destroy(mnn_stream s);
+
+/* ---------------------------------------------------------------- tensor
+ * Replaces Tensor (Sources/MetalAudioKit/Buffers/Tensor.swift:12-439). */
+mnn_status mnn_tensor_create(mnn_device dev, mnn_dtype dtype, int rank, const int64_t* dims,
+                             mnn_tensor* out);
+mnn_status mnn_tensor_destroy(mnn_tensor t);
+mnn_status mnn_tensor_shape(mnn_tensor t, int* rank, int64_t* dims /* [MNN_MAX_RANK] */);
+/* Change the shape in place; element count must be unchanged (Tensor views, Tensor.swift:477-511). */
+mnn_status mnn_tensor_reshape(mnn_tensor t, int rank, const int64_t* dims);
+/* Tensor.copy(from:) / toArray() (Tensor.swift:272-333): copies are ordered on `s`
+ * (NULL = the device's default stream) and complete before the call returns. */
+mnn_status mnn_tensor_upload(mnn_tensor t, const void* host, size_t bytes, mnn_stream s);
+mnn_status mnn_tensor_download(mnn_tensor t, void* host, size_t bytes, mnn_stream s);
+/* Device-to-device copy of equal-sized tensors, enqueued on s. */
+mnn_status mnn_tensor_copy(mnn_tensor dst, mnn_tensor src, mnn_stream s);
+mnn_status mnn_tensor_device_ptr(mnn_tensor t, void** ptr);
+
+/* ---------------------------------------------------------------- layers
+ * Every layer implements the NNLayer protocol (NNLayer.swift:12-16): an input shape,
+ * an output shape (0 = dynamic dimension, Model.swift:100-104) and forward(input, output). */
+
+typedef struct mnn_conv1d_desc {
+  int in_channels, out_channels, kernel_size, stride;
+  int padding;          /* used by MNN_PAD_EXPLICIT and MNN_PAD_REFLECT */
+  int dilation, groups;
+  int use_bias;
+  int input_length;     /* > 0: fixed-length Conv1D (Conv1D.swift:56-103); 0: DynamicConv1D */
+  mnn_padding_mode padding_mode;
+  mnn_activation activation;   /* FusedConv1D epilogue (Conv1D.swift:742-1028) */
+  mnn_precision precision;
+} mnn_conv1d_desc;
+
+/* Conv1D / DynamicConv1D / FusedConv1D (Conv1D.swift:11-1028, DynamicConv1D.swift:35-403).
+ * Weights: "weight" [out, in/groups, k], "bias" [out]. Input [C, L] or [B, C, L]. */
+mnn_status mnn_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc, mnn_layer* out);
+
+/* GroupNorm (Normalization.swift:32-725); optional fused activation (used by the U-Net block).
+ * Parameters "weight"/"gamma" [C], "bias"/"beta" [C]. Input [C, L] or [B, C, L]. */
+mnn_status mnn_groupnorm_create(mnn_device dev, int num_groups, int num_channels, float epsilon,
+                                int affine, mnn_activation activation, mnn_layer* out);
+
+/* LayerNorm over the last dimension (Normalization.swift:734-964). "gamma"/"weight", "beta"/"bias". */
+mnn_status mnn_layernorm_create(mnn_device dev, int feature_size, float epsilon, mnn_layer* out);
+
+/* GELU, tanh approximation with the +-10 clamp (Activations.swift:89-205). */
+mnn_status mnn_gelu_create(mnn_device dev, int rank, const int64_t* input_shape, mnn_layer* out);
+
+/* GLU over the channel dimension: [2C, L] -> [C, L] (or [B, 2C, L] -> [B, C, L]),
+ * out = a * sigmoid(b), a = first half, b = second half (Shaders/NN.metal:1012-1023). */
+mnn_status mnn_glu_create(mnn_device dev, int out_channels, mnn_layer* out);
+
+/* Linear / FusedLinear / HalfLinear (Linear.swift:27-672, HalfPrecisionLinear.swift:60-212):
+ * y = act(x W^T + b). "weight" [out, in], "bias" [out]. Input [in], [N, in] or [B, N, in]. */
+mnn_status mnn_linear_create(mnn_device dev, int in_features, int out_features, int use_bias,
+                             mnn_activation activation, mnn_precision precision, mnn_layer* out);
+
+/* MultiHeadAttention / CrossAttention (Attention.swift:15-1063), PyTorch packing:
+ * "in_proj_weight" [3E, E] rows Q;K;V, "in_proj_bias" [3E], "out_proj_weight" [E, E],
+ * "out_proj_bias" [E]. Input [S, E] or [B, S, E]. Self-attention through mnn_layer_forward,
+ * cross-attention through mnn_layer_forward_cross(query, keyValue, output). */
+mnn_status mnn_mha_create(mnn_device dev, int embed_dim, int num_heads, int use_bias,
+                          mnn_precision precision, mnn_layer* out);
+
+/* FeedForward Linear -> GELU -> Linear (Transformer.swift:7-364).
+ * "linear1.weight" [H, E], "linear1.bias" [H], "linear2.weight" [E, H], "linear2.bias" [E]. */
+mnn_status mnn_feedforward_create(mnn_device dev, int input_dim, int hidden_dim,
+                                  mnn_precision precision, mnn_layer* out);
+
+typedef struct mnn_encoder_block_desc {
+  int in_channels, out_channels, kernel_size, stride, num_groups;
+  int rewrite;          /* 1: append 1x1 conv C->2C + GLU (the HTDemucs encoder layer) */
+  mnn_precision precision;
+} mnn_encoder_block_desc;
+
+/* UNetEncoderBlock (UNet.swift:11-174): DynamicConv1D(reflect (k-1)/2) -> GroupNorm -> GELU
+ * [-> 1x1 conv C->2C -> GLU]. Weights "conv.weight", "conv.bias", "norm.weight", "norm.bias",
+ * "rewrite.weight" [2C, C, 1], "rewrite.bias" [2C]. Input [C, L] or [B, C, L]. The skip output of
+ * the reference is the block output itself (UNet.swift:96-97). */
+mnn_status mnn_encoder_block_create(mnn_device dev, const mnn_encoder_block_desc* desc,
+                                    mnn_layer* out);
+
+/* Pre-norm transformer layer on one sequence (TransformerLayer sub-blocks 1 and 5,
+ * Transformer.swift:467-495): y = x + ls1*MHA(LN1 x); z = y + ls2*FFN(LN2 y).
+ * layer_scale <= 0 disables LayerScale. Weights "norm1.*", "self_attn.*", "norm2.*",
+ * "linear1.*", "linear2.*", "gamma_1.scale", "gamma_2.scale". Input [S, E] or [B, S, E]. */
+mnn_status mnn_transformer_layer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
+                                        float layer_scale, mnn_precision precision,
+                                        mnn_layer* out);
+
+/* Cross-domain transformer bottleneck (CrossTransformerEncoder, Transformer.swift:567-700, with
+ * the HTDemucs layer structure): num_layers layers, even layers self-attention per branch, odd
+ * layers cross-attention (time attends to freq and freq to time, both on pre-update states).
+ * forward through mnn_layer_forward_cross(time, freq, time_out, freq_out). Weights
+ * "layers.{i}.{time|freq}.{norm1|norm2|norm3|attn|linear1|linear2|gamma_1|gamma_2}.*". */
+mnn_status mnn_cross_transformer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
+                                        int num_layers, float layer_scale,
+                                        mnn_precision precision, mnn_layer* out);
+
+mnn_status mnn_layer_destroy(mnn_layer layer);
+/* loadWeights / loadParameters: copies `count` floats into the named parameter.
+ * NaN/Inf are rejected with MNN_ERR_INVALID_CONFIGURATION (validateWeights, NNLayer.swift:27-59);
+ * a wrong count gives MNN_ERR_BUFFER_SIZE_MISMATCH. */
+mnn_status mnn_layer_load_weights(mnn_layer layer, const char* name, const float* data,
+                                  size_t count);
+mnn_status mnn_layer_forward(mnn_layer layer, mnn_tensor input, mnn_tensor output, mnn_stream s);
+/* Two-input forward: MHA cross-attention (query=a, keyValue=b, output=out_a, out_b unused);
+ * cross transformer (time=a, freq=b, time_out=out_a, freq_out=out_b; outputs may alias inputs). */
+mnn_status mnn_layer_forward_cross(mnn_layer layer, mnn_tensor a, mnn_tensor b, mnn_tensor out_a,
+                                   mnn_tensor out_b, mnn_stream s);
+/* Declared shapes (0 = dynamic). */
+mnn_status mnn_layer_input_shape(mnn_layer layer, int* rank, int64_t* dims);
+mnn_status mnn_layer_output_shape(mnn_layer layer, int* rank, int64_t* dims);
+/* Concrete output shape for a concrete input shape. */
+mnn_status mnn_layer_infer_output_shape(mnn_layer layer, int in_rank, const int64_t* in_dims,
+                                        int* out_rank, int64_t* out_dims);
+
+/* ---------------------------------------------------------------- sequential
+ * Sequential (Model.swift:65-357). The model references layers; it does not own them. */
+mnn_status mnn_sequential_create(mnn_device dev, mnn_sequential* out);
+mnn_status mnn_sequential_destroy(mnn_sequential seq);
+mnn_status mnn_sequential_add(mnn_sequential seq, mnn_layer layer);          /* shape-checked */
+mnn_status mnn_sequential_add_unchecked(mnn_sequential seq, mnn_layer layer);
+/* Ping-pong buffer plan: a layer reuses a same-shape buffer last used >= 2 layers earlier
+ * (Model.swift:135-201). Dynamic shapes are resolved on the first forward per input shape. */
+mnn_status mnn_sequential_build(mnn_sequential seq);
+/* Runs all layers in stream order. *output is borrowed: it belongs to the model and is
+ * overwritten by the next forward (Model.swift:263). */
+mnn_status mnn_sequential_forward(mnn_sequential seq, mnn_tensor input, mnn_stream s,
+                                  mnn_tensor* output);
+mnn_status mnn_sequential_buffer_stats(mnn_sequential seq, int* allocated, int* layers);
+mnn_status mnn_sequential_layer_count(mnn_sequential seq, int* count);
+
+/* ---------------------------------------------------------------- diagnostics
+ * Runs one MFMA instruction on one wave with a zero accumulator and returns its raw lane
+ * registers, to check the operand/result lane layouts the kernels assume.
+ * variant 0: f32 32x32x2 (a, b: 64 floats, one per lane; d: 64 x 16)
+ * variant 1: f32 16x16x4 (a, b: 64 floats; d: 64 x 4)
+ * variant 2: bf16 32x32x16 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 16)
+ * variant 3: bf16 16x16x32 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 4)
+ * Layout of every array: [lane][register]. */
+mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, const float* b,
+                                float* d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MNN_H */

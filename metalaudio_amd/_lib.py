@@ -1,0 +1,153 @@
+"""ctypes binding of include/mnn.h (the C ABI of libmnn.so).
+
+Loads the in-tree library metalaudio_amd/lib/libmnn.so. There is no fallback: if the library
+is missing or a call fails, an exception is raised.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libmnn.so"
+MAX_RANK = 8
+
+# mnn_status
+STATUS = {
+    0: "MNN_OK",
+    1: "MNN_ERR_INVALID_CONFIGURATION",
+    2: "MNN_ERR_BUFFER_SIZE_MISMATCH",
+    3: "MNN_ERR_PIPELINE_CREATION_FAILED",
+    4: "MNN_ERR_GPU_TIMEOUT",
+    5: "MNN_ERR_GPU_EXECUTION",
+    6: "MNN_ERR_DEVICE_LOST",
+    7: "MNN_ERR_OUT_OF_MEMORY",
+    8: "MNN_ERR_SHAPE_MISMATCH",
+    9: "MNN_ERR_EMPTY_MODEL",
+    10: "MNN_ERR_INPUT_SHAPE_MISMATCH",
+    11: "MNN_ERR_NOT_BUILT",
+    12: "MNN_ERR_INVALID_ARGUMENT",
+}
+
+ACT = {"none": 0, "relu": 1, "leaky_relu": 2, "gelu": 3, "swish": 4, "sigmoid": 5, "tanh": 6}
+PAD = {"valid": 0, "same": 1, "explicit": 2, "reflect": 3}
+PRECISION = {"f32": 0, "bf16": 1}
+
+
+class MNNError(RuntimeError):
+    """A non-OK mnn_status; `.code` is the status value, `.name` its enum name."""
+
+    def __init__(self, code: int, message: str):
+        self.code = code
+        self.name = STATUS.get(code, f"status {code}")
+        super().__init__(f"{self.name}: {message}")
+
+
+class Conv1dDesc(C.Structure):
+    _fields_ = [
+        ("in_channels", C.c_int), ("out_channels", C.c_int), ("kernel_size", C.c_int),
+        ("stride", C.c_int), ("padding", C.c_int), ("dilation", C.c_int), ("groups", C.c_int),
+        ("use_bias", C.c_int), ("input_length", C.c_int), ("padding_mode", C.c_int),
+        ("activation", C.c_int), ("precision", C.c_int),
+    ]
+
+
+class EncoderBlockDesc(C.Structure):
+    _fields_ = [
+        ("in_channels", C.c_int), ("out_channels", C.c_int), ("kernel_size", C.c_int),
+        ("stride", C.c_int), ("num_groups", C.c_int), ("rewrite", C.c_int),
+        ("precision", C.c_int),
+    ]
+
+
+P = C.c_void_p
+PP = C.POINTER(C.c_void_p)
+I64P = C.POINTER(C.c_int64)
+IP = C.POINTER(C.c_int)
+FP = C.POINTER(C.c_float)
+
+# name -> (restype, argtypes); every function that returns mnn_status uses C.c_int
+SIGNATURES = {
+    "mnn_last_error_message": (C.c_char_p, []),
+    "mnn_status_string": (C.c_char_p, [C.c_int]),
+    "mnn_version": (C.c_char_p, []),
+    "mnn_device_create": (C.c_int, [C.c_int, PP]),
+    "mnn_device_destroy": (C.c_int, [P]),
+    "mnn_device_name": (C.c_int, [P, C.c_char_p, C.c_size_t]),
+    "mnn_device_synchronize": (C.c_int, [P]),
+    "mnn_device_mark_lost": (C.c_int, [P]),
+    "mnn_device_check_available": (C.c_int, [P, C.c_int]),
+    "mnn_device_set_kernel_timing": (C.c_int, [P, C.c_int]),
+    "mnn_device_kernel_timing": (C.c_int, [P, C.c_char_p, I64P, C.POINTER(C.c_double)]),
+    "mnn_device_reset_kernel_timing": (C.c_int, [P]),
+    "mnn_stream_create": (C.c_int, [P, PP]),
+    "mnn_stream_sync": (C.c_int, [P, C.c_int]),
+    "mnn_stream_destroy": (C.c_int, [P]),
+    "mnn_tensor_create": (C.c_int, [P, C.c_int, C.c_int, I64P, PP]),
+    "mnn_tensor_destroy": (C.c_int, [P]),
+    "mnn_tensor_shape": (C.c_int, [P, IP, I64P]),
+    "mnn_tensor_reshape": (C.c_int, [P, C.c_int, I64P]),
+    "mnn_tensor_upload": (C.c_int, [P, P, C.c_size_t, P]),
+    "mnn_tensor_download": (C.c_int, [P, P, C.c_size_t, P]),
+    "mnn_tensor_copy": (C.c_int, [P, P, P]),
+    "mnn_tensor_device_ptr": (C.c_int, [P, PP]),
+    "mnn_conv1d_create": (C.c_int, [P, C.POINTER(Conv1dDesc), PP]),
+    "mnn_groupnorm_create": (C.c_int, [P, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, PP]),
+    "mnn_layernorm_create": (C.c_int, [P, C.c_int, C.c_float, PP]),
+    "mnn_gelu_create": (C.c_int, [P, C.c_int, I64P, PP]),
+    "mnn_glu_create": (C.c_int, [P, C.c_int, PP]),
+    "mnn_linear_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
+    "mnn_mha_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
+    "mnn_feedforward_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),
+    "mnn_encoder_block_create": (C.c_int, [P, C.POINTER(EncoderBlockDesc), PP]),
+    "mnn_transformer_layer_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
+    "mnn_cross_transformer_create": (
+        C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
+    "mnn_layer_destroy": (C.c_int, [P]),
+    "mnn_layer_load_weights": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
+    "mnn_layer_forward": (C.c_int, [P, P, P, P]),
+    "mnn_layer_forward_cross": (C.c_int, [P, P, P, P, P, P]),
+    "mnn_layer_input_shape": (C.c_int, [P, IP, I64P]),
+    "mnn_layer_output_shape": (C.c_int, [P, IP, I64P]),
+    "mnn_layer_infer_output_shape": (C.c_int, [P, C.c_int, I64P, IP, I64P]),
+    "mnn_sequential_create": (C.c_int, [P, PP]),
+    "mnn_sequential_destroy": (C.c_int, [P]),
+    "mnn_sequential_add": (C.c_int, [P, P]),
+    "mnn_sequential_add_unchecked": (C.c_int, [P, P]),
+    "mnn_sequential_build": (C.c_int, [P]),
+    "mnn_sequential_forward": (C.c_int, [P, P, P, PP]),
+    "mnn_sequential_buffer_stats": (C.c_int, [P, IP, IP]),
+    "mnn_sequential_layer_count": (C.c_int, [P, IP]),
+    "mnn_debug_mfma_probe": (C.c_int, [P, C.c_int, FP, FP, FP]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """The loaded libmnn.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m metalaudio_amd.build`"
+            )
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != 0:
+        msg = lib().mnn_last_error_message()
+        raise MNNError(status, msg.decode() if msg else "")
+
+
+def dims(shape) -> C.Array:
+    arr = (C.c_int64 * MAX_RANK)()
+    for i, v in enumerate(shape):
+        arr[i] = int(v)
+    return arr

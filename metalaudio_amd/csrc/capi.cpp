@@ -1,0 +1,581 @@
+// extern "C" entry points of mnn.h: argument checks, exception -> status translation.
+#include <cstdio>
+#include <thread>
+
+#include "layers.hpp"
+
+using namespace mnn;
+
+struct mnn_device_s {};
+struct mnn_stream_s {};
+struct mnn_tensor_s {};
+struct mnn_layer_s {};
+struct mnn_sequential_s {};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+template <class F>
+mnn_status guard(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return MNN_OK;
+  } catch (const Error& e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return MNN_ERR_OUT_OF_MEMORY;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return MNN_ERR_GPU_EXECUTION;
+  }
+}
+
+Device* D(mnn_device d) {
+  MNN_REQUIRE(d, MNN_ERR_INVALID_ARGUMENT, "null device");
+  return reinterpret_cast<Device*>(d);
+}
+Stream* S(mnn_stream s) {
+  MNN_REQUIRE(s, MNN_ERR_INVALID_ARGUMENT, "null stream");
+  return reinterpret_cast<Stream*>(s);
+}
+Tensor* T(mnn_tensor t) {
+  MNN_REQUIRE(t, MNN_ERR_INVALID_ARGUMENT, "null tensor");
+  return reinterpret_cast<Tensor*>(t);
+}
+Layer* L(mnn_layer l) {
+  MNN_REQUIRE(l, MNN_ERR_INVALID_ARGUMENT, "null layer");
+  return reinterpret_cast<Layer*>(l);
+}
+Sequential* Q(mnn_sequential q) {
+  MNN_REQUIRE(q, MNN_ERR_INVALID_ARGUMENT, "null sequential");
+  return reinterpret_cast<Sequential*>(q);
+}
+
+Shape to_shape(int rank, const int64_t* dims) {
+  MNN_REQUIRE(rank >= 1 && rank <= MNN_MAX_RANK && dims, MNN_ERR_INVALID_ARGUMENT,
+              "rank must be 1.." << MNN_MAX_RANK);
+  return Shape(dims, dims + rank);
+}
+
+void put_shape(const Shape& s, int* rank, int64_t* dims) {
+  MNN_REQUIRE(rank && dims, MNN_ERR_INVALID_ARGUMENT, "null shape output");
+  *rank = (int)s.size();
+  for (size_t i = 0; i < s.size(); ++i) dims[i] = s[i];
+}
+
+// The stream a call runs on: the given one or the device's default stream.
+Stream resolve_stream(Device* d, mnn_stream s) {
+  if (s) {
+    Stream* st = S(s);
+    MNN_REQUIRE(st->dev == d, MNN_ERR_INVALID_ARGUMENT, "stream belongs to another device");
+    return *st;
+  }
+  return Stream{d, d->default_stream, false};
+}
+
+mnn_layer wrap(std::unique_ptr<Layer> l) { return reinterpret_cast<mnn_layer>(l.release()); }
+
+template <class T>
+const T& need(const T* p) {
+  MNN_REQUIRE(p, MNN_ERR_INVALID_ARGUMENT, "null descriptor");
+  return *p;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mnn_last_error_message(void) { return g_last_error.c_str(); }
+
+const char* mnn_status_string(mnn_status s) {
+  switch (s) {
+    case MNN_OK: return "ok";
+    case MNN_ERR_INVALID_CONFIGURATION: return "invalid configuration";
+    case MNN_ERR_BUFFER_SIZE_MISMATCH: return "buffer size mismatch";
+    case MNN_ERR_PIPELINE_CREATION_FAILED: return "pipeline creation failed";
+    case MNN_ERR_GPU_TIMEOUT: return "GPU timeout";
+    case MNN_ERR_GPU_EXECUTION: return "GPU execution error";
+    case MNN_ERR_DEVICE_LOST: return "device lost";
+    case MNN_ERR_OUT_OF_MEMORY: return "out of memory";
+    case MNN_ERR_SHAPE_MISMATCH: return "shape mismatch";
+    case MNN_ERR_EMPTY_MODEL: return "empty model";
+    case MNN_ERR_INPUT_SHAPE_MISMATCH: return "input shape mismatch";
+    case MNN_ERR_NOT_BUILT: return "model not built";
+    case MNN_ERR_INVALID_ARGUMENT: return "invalid argument";
+  }
+  return "unknown status";
+}
+
+const char* mnn_version(void) { return "mnn 0.1.0 (gfx950)"; }
+
+// ------------------------------------------------------------------ device
+mnn_status mnn_device_create(int ordinal, mnn_device* out) {
+  return guard([&] {
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    MNN_REQUIRE(e == hipSuccess && n > 0, MNN_ERR_DEVICE_LOST,
+                "no HIP device available (" << hipGetErrorString(e) << ")");
+    MNN_REQUIRE(ordinal >= 0 && ordinal < n, MNN_ERR_INVALID_ARGUMENT,
+                "device ordinal " << ordinal << " out of range (" << n << " devices)");
+    auto d = std::make_unique<Device>();
+    d->ordinal = ordinal;
+    HIP_CHECK(hipSetDevice(ordinal));
+    HIP_CHECK(hipGetDeviceProperties(&d->props, ordinal));
+    MNN_REQUIRE(std::string(d->props.gcnArchName).rfind("gfx950", 0) == 0,
+                MNN_ERR_PIPELINE_CREATION_FAILED,
+                "kernels are built for gfx950, device is " << d->props.gcnArchName);
+    HIP_CHECK(hipStreamCreateWithFlags(&d->default_stream, hipStreamNonBlocking));
+    *out = reinterpret_cast<mnn_device>(d.release());
+  });
+}
+
+mnn_status mnn_device_destroy(mnn_device dev) {
+  return guard([&] {
+    if (!dev) return;
+    Device* d = D(dev);
+    d->make_current();
+    (void)hipDeviceSynchronize();
+    for (auto& t : d->pending) {
+      (void)hipEventDestroy(t.start);
+      (void)hipEventDestroy(t.stop);
+    }
+    for (auto& p : d->event_pool) {
+      (void)hipEventDestroy(p.first);
+      (void)hipEventDestroy(p.second);
+    }
+    if (d->default_stream) (void)hipStreamDestroy(d->default_stream);
+    delete d;
+  });
+}
+
+mnn_status mnn_device_name(mnn_device dev, char* buf, size_t n) {
+  return guard([&] {
+    Device* d = D(dev);
+    MNN_REQUIRE(buf && n > 0, MNN_ERR_INVALID_ARGUMENT, "null buffer");
+    std::snprintf(buf, n, "%s (%s, %d CUs)", d->props.name, d->props.gcnArchName,
+                  d->props.multiProcessorCount);
+  });
+}
+
+mnn_status mnn_device_synchronize(mnn_device dev) {
+  return guard([&] {
+    Device* d = D(dev);
+    d->check_alive();
+    d->make_current();
+    HIP_CHECK(hipDeviceSynchronize());
+  });
+}
+
+mnn_status mnn_device_mark_lost(mnn_device dev) {
+  return guard([&] { D(dev)->lost = true; });
+}
+
+mnn_status mnn_device_check_available(mnn_device dev, int timeout_ms) {
+  return guard([&] {
+    Device* d = D(dev);
+    d->check_alive();
+    d->make_current();
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    HIP_CHECK(hipEventRecord(e, d->default_stream));
+    const auto t0 = std::chrono::steady_clock::now();
+    while (true) {
+      hipError_t q = hipEventQuery(e);
+      if (q == hipSuccess) break;
+      if (q != hipErrorNotReady) {
+        (void)hipEventDestroy(e);
+        d->lost = true;
+        fail(MNN_ERR_DEVICE_LOST, std::string("device check failed: ") + hipGetErrorString(q));
+      }
+      if (timeout_ms > 0 && std::chrono::steady_clock::now() - t0 >
+                                std::chrono::milliseconds(timeout_ms)) {
+        (void)hipEventDestroy(e);
+        fail(MNN_ERR_GPU_TIMEOUT, "device did not answer within the timeout");
+      }
+      std::this_thread::sleep_for(std::chrono::microseconds(50));
+    }
+    (void)hipEventDestroy(e);
+  });
+}
+
+mnn_status mnn_device_set_kernel_timing(mnn_device dev, int enable) {
+  return guard([&] { D(dev)->timing = enable != 0; });
+}
+
+mnn_status mnn_device_kernel_timing(mnn_device dev, const char* sub, int64_t* launches,
+                                    double* total_ms) {
+  return guard([&] {
+    Device* d = D(dev);
+    MNN_REQUIRE(launches && total_ms, MNN_ERR_INVALID_ARGUMENT, "null output");
+    d->make_current();
+    d->resolve_timers();
+    int64_t n = 0;
+    double ms = 0.0;
+    std::lock_guard<std::mutex> lk(d->timing_mu);
+    for (auto& kv : d->stats)
+      if (!sub || kv.first.find(sub) != std::string::npos) {
+        n += kv.second.first;
+        ms += kv.second.second;
+      }
+    *launches = n;
+    *total_ms = ms;
+  });
+}
+
+mnn_status mnn_device_reset_kernel_timing(mnn_device dev) {
+  return guard([&] {
+    Device* d = D(dev);
+    d->make_current();
+    d->resolve_timers();
+    std::lock_guard<std::mutex> lk(d->timing_mu);
+    d->stats.clear();
+  });
+}
+
+// ------------------------------------------------------------------ stream
+mnn_status mnn_stream_create(mnn_device dev, mnn_stream* out) {
+  return guard([&] {
+    Device* d = D(dev);
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output");
+    d->make_current();
+    auto s = std::make_unique<Stream>();
+    s->dev = d;
+    s->owned = true;
+    HIP_CHECK(hipStreamCreateWithFlags(&s->s, hipStreamNonBlocking));
+    *out = reinterpret_cast<mnn_stream>(s.release());
+  });
+}
+
+mnn_status mnn_stream_sync(mnn_stream st, int timeout_ms) {
+  return guard([&] {
+    Stream* s = S(st);
+    s->dev->check_alive();
+    s->dev->make_current();
+    if (timeout_ms <= 0) {
+      HIP_CHECK(hipStreamSynchronize(s->s));
+      return;
+    }
+    const auto t0 = std::chrono::steady_clock::now();
+    while (true) {
+      hipError_t q = hipStreamQuery(s->s);
+      if (q == hipSuccess) return;
+      if (q != hipErrorNotReady)
+        fail(MNN_ERR_GPU_EXECUTION, std::string("stream error: ") + hipGetErrorString(q));
+      if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(timeout_ms))
+        fail(MNN_ERR_GPU_TIMEOUT, "GPU work did not finish within " + std::to_string(timeout_ms) +
+                                      " ms (it keeps running)");
+      std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+  });
+}
+
+mnn_status mnn_stream_destroy(mnn_stream st) {
+  return guard([&] {
+    if (!st) return;
+    Stream* s = S(st);
+    s->dev->make_current();
+    if (s->owned && s->s) {
+      (void)hipStreamSynchronize(s->s);
+      (void)hipStreamDestroy(s->s);
+    }
+    delete s;
+  });
+}
+
+// ------------------------------------------------------------------ tensor
+mnn_status mnn_tensor_create(mnn_device dev, mnn_dtype dtype, int rank, const int64_t* dims,
+                             mnn_tensor* out) {
+  return guard([&] {
+    Device* d = D(dev);
+    d->check_alive();
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output");
+    MNN_REQUIRE(dtype == MNN_F32 || dtype == MNN_BF16, MNN_ERR_INVALID_ARGUMENT, "bad dtype");
+    *out = reinterpret_cast<mnn_tensor>(tensor_create(d, dtype, to_shape(rank, dims)));
+  });
+}
+
+mnn_status mnn_tensor_destroy(mnn_tensor t) {
+  return guard([&] {
+    if (t) tensor_destroy(T(t));
+  });
+}
+
+mnn_status mnn_tensor_shape(mnn_tensor t, int* rank, int64_t* dims) {
+  return guard([&] { put_shape(T(t)->shape, rank, dims); });
+}
+
+mnn_status mnn_tensor_reshape(mnn_tensor t, int rank, const int64_t* dims) {
+  return guard([&] {
+    Tensor* x = T(t);
+    Shape s = to_shape(rank, dims);
+    MNN_REQUIRE(numel(s) == x->count(), MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "reshape " << shape_str(x->shape) << " -> " << shape_str(s)
+                           << " changes the element count");
+    x->shape = s;
+  });
+}
+
+mnn_status mnn_tensor_upload(mnn_tensor t, const void* host, size_t bytes, mnn_stream st) {
+  return guard([&] {
+    Tensor* x = T(t);
+    x->dev->check_alive();
+    MNN_REQUIRE(host || bytes == 0, MNN_ERR_INVALID_ARGUMENT, "null host buffer");
+    MNN_REQUIRE(bytes == x->bytes, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "upload of " << bytes << " bytes into a tensor of " << x->bytes);
+    Stream s = resolve_stream(x->dev, st);
+    x->dev->make_current();
+    HIP_CHECK(hipMemcpyAsync(x->data, host, bytes, hipMemcpyHostToDevice, s.s));
+    HIP_CHECK(hipStreamSynchronize(s.s));
+  });
+}
+
+mnn_status mnn_tensor_download(mnn_tensor t, void* host, size_t bytes, mnn_stream st) {
+  return guard([&] {
+    Tensor* x = T(t);
+    x->dev->check_alive();
+    MNN_REQUIRE(host || bytes == 0, MNN_ERR_INVALID_ARGUMENT, "null host buffer");
+    MNN_REQUIRE(bytes == x->bytes, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "download of " << bytes << " bytes from a tensor of " << x->bytes);
+    Stream s = resolve_stream(x->dev, st);
+    x->dev->make_current();
+    HIP_CHECK(hipMemcpyAsync(host, x->data, bytes, hipMemcpyDeviceToHost, s.s));
+    HIP_CHECK(hipStreamSynchronize(s.s));
+  });
+}
+
+mnn_status mnn_tensor_copy(mnn_tensor dst, mnn_tensor src, mnn_stream st) {
+  return guard([&] {
+    Tensor* d = T(dst);
+    Tensor* s = T(src);
+    MNN_REQUIRE(d->dev == s->dev, MNN_ERR_INVALID_ARGUMENT, "tensors on different devices");
+    d->dev->check_alive();
+    MNN_REQUIRE(d->bytes == s->bytes, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "copy between tensors of " << s->bytes << " and " << d->bytes << " bytes");
+    Stream sv = resolve_stream(d->dev, st);
+    d->dev->make_current();
+    k::copy_bytes(LaunchCtx{d->dev, sv.s}, s->data, d->data, (int64_t)s->bytes);
+  });
+}
+
+mnn_status mnn_tensor_device_ptr(mnn_tensor t, void** ptr) {
+  return guard([&] {
+    MNN_REQUIRE(ptr, MNN_ERR_INVALID_ARGUMENT, "null output");
+    *ptr = T(t)->data;
+  });
+}
+
+// ------------------------------------------------------------------ layers
+#define MNN_CREATE(expr)                                         \
+  return guard([&] {                                             \
+    Device* d = D(dev);                                          \
+    d->check_alive();                                            \
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output");   \
+    d->make_current();                                           \
+    *out = wrap(expr);                                           \
+  })
+
+mnn_status mnn_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc, mnn_layer* out) {
+  MNN_CREATE(make_conv1d(d, need(desc)));
+}
+mnn_status mnn_groupnorm_create(mnn_device dev, int num_groups, int num_channels, float epsilon,
+                                int affine, mnn_activation act, mnn_layer* out) {
+  MNN_CREATE(make_groupnorm(d, num_groups, num_channels, epsilon, affine != 0, act));
+}
+mnn_status mnn_layernorm_create(mnn_device dev, int feature_size, float epsilon, mnn_layer* out) {
+  MNN_CREATE(make_layernorm(d, feature_size, epsilon));
+}
+mnn_status mnn_gelu_create(mnn_device dev, int rank, const int64_t* shape, mnn_layer* out) {
+  MNN_CREATE(make_gelu(d, to_shape(rank, shape)));
+}
+mnn_status mnn_glu_create(mnn_device dev, int out_channels, mnn_layer* out) {
+  MNN_CREATE(make_glu(d, out_channels));
+}
+mnn_status mnn_linear_create(mnn_device dev, int in_features, int out_features, int use_bias,
+                             mnn_activation act, mnn_precision prec, mnn_layer* out) {
+  MNN_CREATE(make_linear(d, in_features, out_features, use_bias != 0, act, prec));
+}
+mnn_status mnn_mha_create(mnn_device dev, int embed_dim, int num_heads, int use_bias,
+                          mnn_precision prec, mnn_layer* out) {
+  MNN_CREATE(make_mha(d, embed_dim, num_heads, use_bias != 0, prec));
+}
+mnn_status mnn_feedforward_create(mnn_device dev, int input_dim, int hidden_dim,
+                                  mnn_precision prec, mnn_layer* out) {
+  MNN_CREATE(make_feedforward(d, input_dim, hidden_dim, prec));
+}
+mnn_status mnn_encoder_block_create(mnn_device dev, const mnn_encoder_block_desc* desc,
+                                    mnn_layer* out) {
+  MNN_CREATE(make_encoder_block(d, need(desc)));
+}
+mnn_status mnn_transformer_layer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
+                                        float layer_scale, mnn_precision prec, mnn_layer* out) {
+  MNN_CREATE(make_transformer_layer(d, embed_dim, num_heads, ffn_dim, layer_scale, prec));
+}
+mnn_status mnn_cross_transformer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
+                                        int num_layers, float layer_scale, mnn_precision prec,
+                                        mnn_layer* out) {
+  MNN_CREATE(
+      make_cross_transformer(d, embed_dim, num_heads, ffn_dim, num_layers, layer_scale, prec));
+}
+
+mnn_status mnn_layer_destroy(mnn_layer layer) {
+  return guard([&] {
+    if (!layer) return;
+    Layer* l = L(layer);
+    l->device()->make_current();
+    (void)hipDeviceSynchronize();
+    delete l;
+  });
+}
+
+mnn_status mnn_layer_load_weights(mnn_layer layer, const char* name, const float* data,
+                                  size_t count) {
+  return guard([&] {
+    Layer* l = L(layer);
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    l->device()->check_alive();
+    l->device()->make_current();
+    l->load(name, data, count);
+  });
+}
+
+mnn_status mnn_layer_forward(mnn_layer layer, mnn_tensor input, mnn_tensor output,
+                             mnn_stream st) {
+  return guard([&] {
+    Layer* l = L(layer);
+    Tensor* in = T(input);
+    Tensor* o = T(output);
+    Device* d = l->device();
+    d->check_alive();
+    MNN_REQUIRE(in->dev == d && o->dev == d, MNN_ERR_INVALID_ARGUMENT,
+                "tensors and layer on different devices");
+    MNN_REQUIRE(in->dtype == MNN_F32, MNN_ERR_INVALID_ARGUMENT, "input must be f32");
+    Stream s = resolve_stream(d, st);
+    d->make_current();
+    l->forward(*in, *o, s);
+  });
+}
+
+mnn_status mnn_layer_forward_cross(mnn_layer layer, mnn_tensor a, mnn_tensor b, mnn_tensor out_a,
+                                   mnn_tensor out_b, mnn_stream st) {
+  return guard([&] {
+    Layer* l = L(layer);
+    Device* d = l->device();
+    d->check_alive();
+    Tensor* ta = a ? T(a) : nullptr;
+    Tensor* tb = b ? T(b) : nullptr;
+    Tensor* oa = out_a ? T(out_a) : nullptr;
+    Tensor* ob = out_b ? T(out_b) : nullptr;
+    for (Tensor* t : {ta, tb, oa, ob})
+      if (t) {
+        MNN_REQUIRE(t->dev == d, MNN_ERR_INVALID_ARGUMENT, "tensor on another device");
+        MNN_REQUIRE(t->dtype == MNN_F32, MNN_ERR_INVALID_ARGUMENT, "tensors must be f32");
+      }
+    Stream s = resolve_stream(d, st);
+    d->make_current();
+    l->forward_cross(ta, tb, oa, ob, s);
+  });
+}
+
+mnn_status mnn_layer_input_shape(mnn_layer layer, int* rank, int64_t* dims) {
+  return guard([&] { put_shape(L(layer)->input_shape(), rank, dims); });
+}
+
+mnn_status mnn_layer_output_shape(mnn_layer layer, int* rank, int64_t* dims) {
+  return guard([&] { put_shape(L(layer)->output_shape(), rank, dims); });
+}
+
+mnn_status mnn_layer_infer_output_shape(mnn_layer layer, int in_rank, const int64_t* in_dims,
+                                        int* out_rank, int64_t* out_dims) {
+  return guard([&] {
+    put_shape(L(layer)->infer_output(to_shape(in_rank, in_dims)), out_rank, out_dims);
+  });
+}
+
+// ------------------------------------------------------------------ sequential
+mnn_status mnn_sequential_create(mnn_device dev, mnn_sequential* out) {
+  return guard([&] {
+    Device* d = D(dev);
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output");
+    *out = reinterpret_cast<mnn_sequential>(new Sequential(d));
+  });
+}
+
+mnn_status mnn_sequential_destroy(mnn_sequential seq) {
+  return guard([&] {
+    if (seq) delete Q(seq);
+  });
+}
+
+mnn_status mnn_sequential_add(mnn_sequential seq, mnn_layer layer) {
+  return guard([&] { Q(seq)->add(L(layer), true); });
+}
+
+mnn_status mnn_sequential_add_unchecked(mnn_sequential seq, mnn_layer layer) {
+  return guard([&] { Q(seq)->add(L(layer), false); });
+}
+
+mnn_status mnn_sequential_build(mnn_sequential seq) {
+  return guard([&] { Q(seq)->build(); });
+}
+
+mnn_status mnn_sequential_forward(mnn_sequential seq, mnn_tensor input, mnn_stream st,
+                                  mnn_tensor* output) {
+  return guard([&] {
+    Sequential* q = Q(seq);
+    Tensor* in = T(input);
+    MNN_REQUIRE(output, MNN_ERR_INVALID_ARGUMENT, "null output");
+    in->dev->check_alive();
+    Stream s = resolve_stream(in->dev, st);
+    in->dev->make_current();
+    *output = reinterpret_cast<mnn_tensor>(q->forward(*in, s));
+  });
+}
+
+mnn_status mnn_sequential_buffer_stats(mnn_sequential seq, int* allocated, int* layers) {
+  return guard([&] {
+    MNN_REQUIRE(allocated && layers, MNN_ERR_INVALID_ARGUMENT, "null output");
+    auto st = Q(seq)->buffer_stats();
+    *allocated = st.first;
+    *layers = st.second;
+  });
+}
+
+mnn_status mnn_sequential_layer_count(mnn_sequential seq, int* count) {
+  return guard([&] {
+    MNN_REQUIRE(count, MNN_ERR_INVALID_ARGUMENT, "null output");
+    *count = Q(seq)->layer_count();
+  });
+}
+
+// ------------------------------------------------------------------ diagnostics
+mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, const float* b,
+                                float* d_out) {
+  return guard([&] {
+    Device* d = D(dev);
+    d->check_alive();
+    MNN_REQUIRE(a && b && d_out, MNN_ERR_INVALID_ARGUMENT, "null buffer");
+    MNN_REQUIRE(variant >= 0 && variant <= 3, MNN_ERR_INVALID_ARGUMENT, "variant must be 0..3");
+    d->make_current();
+    const int na = variant < 2 ? 1 : 8;
+    const int nd = (variant == 0 || variant == 2) ? 16 : 4;
+    float *da, *db, *dd;
+    HIP_CHECK(hipMalloc(&da, 64 * na * 4));
+    HIP_CHECK(hipMalloc(&db, 64 * na * 4));
+    HIP_CHECK(hipMalloc(&dd, 64 * nd * 4));
+    HIP_CHECK(hipMemcpy(da, a, 64 * na * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(db, b, 64 * na * 4, hipMemcpyHostToDevice));
+    k::mfma_probe(LaunchCtx{d, d->default_stream}, variant, da, db, dd);
+    HIP_CHECK(hipStreamSynchronize(d->default_stream));
+    HIP_CHECK(hipMemcpy(d_out, dd, 64 * nd * 4, hipMemcpyDeviceToHost));
+    (void)hipFree(da);
+    (void)hipFree(db);
+    (void)hipFree(dd);
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,284 @@
+// Fused multi-head attention forward: O = softmax(Q K^T * scale) V per (batch, head), with an
+// online softmax so the [Sq, Sk] score matrix never leaves registers. Replaces the reference's
+// attention_scores / attention_softmax / attention_output kernels, which write fp32 [H, Sq, Sk]
+// scores to memory (Attention.swift:301-327, 675-705, 744-768). Semantics follow the reference
+// CPU restatement (Attention.swift:840-976): head h uses columns [h*hd, (h+1)*hd) of the packed
+// projections, scale = 1/sqrt(hd), P = exp(s - max) / (sum + 1e-10), O is written [S, H*hd].
+//
+// Matrix-core formulation (v_mfma_f32_16x16x4_f32, fp32 operands): each wave owns QW query
+// columns and computes the TRANSPOSED scores S^T = K Q^T for a block of 64 keys. The accumulator
+// layout of S^T (lane l holds keys 4*(l/16)+r, query l%16) is exactly the B-operand layout the
+// next product O^T += V^T P^T needs when its k-slots are assigned the same keys, so P goes from
+// the softmax straight into the PV matrix product without a trip through LDS. Per query, the
+// running max is shared across the four lane groups with two xor-shuffles; running sums stay
+// per lane and are combined once at the end. Q is pre-multiplied by scale*log2(e) so the
+// exponentials are exp2. K/V blocks are double-buffered in LDS.
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mnn {
+namespace k {
+
+using namespace dev;
+
+namespace {
+
+constexpr int BKV = 64;
+
+template <int HD, int QW>
+__global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
+  constexpr int NW = 4, BQ = NW * QW, NU = QW / 16, HS = HD / 4, ND = HD / 16, LDK = HD + 4;
+  constexpr int KV_V4 = BKV * HD / 4 / 256;  // float4 per thread per K (or V) block
+  static_assert(BKV * HD / 4 % 256 == 0, "K/V block must split over 256 threads");
+  __shared__ __attribute__((aligned(16))) float Ks[2][BKV * LDK];
+  __shared__ __attribute__((aligned(16))) float Vs[2][BKV * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, l16 = lane & 15;
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int qw0 = blockIdx.x * BQ + wave * QW;
+
+  const float* __restrict__ qb = a.q + (int64_t)b * a.q_bs + h * HD;
+  const float* __restrict__ kb = a.k + (int64_t)b * a.kv_bs + h * HD;
+  const float* __restrict__ vb = a.v + (int64_t)b * a.kv_bs + h * HD;
+
+  // Q fragments: B operand of S^T = K Q^T; lane group G owns d in [G*HS, (G+1)*HS)
+  const float qscale = a.scale * 1.4426950408889634f;
+  float qf[NU][HS];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int q = qw0 + 16 * u + l16;
+    if (q < a.Sq) {
+      const float* p = qb + (int64_t)q * a.q_rs + G * HS;
+#pragma unroll
+      for (int s4 = 0; s4 < HS / 4; ++s4) {
+        float4 t = *reinterpret_cast<const float4*>(p + 4 * s4);
+        qf[u][4 * s4 + 0] = t.x * qscale; qf[u][4 * s4 + 1] = t.y * qscale;
+        qf[u][4 * s4 + 2] = t.z * qscale; qf[u][4 * s4 + 3] = t.w * qscale;
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < HS; ++s) qf[u][s] = 0.f;
+    }
+  }
+
+  float4 rk[KV_V4], rv[KV_V4];
+  auto load_kv = [&](int kv0) {
+#pragma unroll
+    for (int i = 0; i < KV_V4; ++i) {
+      const int idx = tid + i * 256;
+      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+      const int kv = kv0 + row;
+      if (kv < a.Sk) {
+        rk[i] = *reinterpret_cast<const float4*>(kb + (int64_t)kv * a.kv_rs + c4 * 4);
+        rv[i] = *reinterpret_cast<const float4*>(vb + (int64_t)kv * a.kv_rs + c4 * 4);
+      } else {
+        rk[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        rv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+  };
+  auto store_kv = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < KV_V4; ++i) {
+      const int idx = tid + i * 256;
+      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
+      *reinterpret_cast<float4*>(&Ks[buf][row * LDK + c4 * 4]) = rk[i];
+      *reinterpret_cast<float4*>(&Vs[buf][row * LDK + c4 * 4]) = rv[i];
+    }
+  };
+
+  floatx4 o[ND][NU];
+  float m[NU], lsum[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    m[u] = -INFINITY;
+    lsum[u] = 0.f;
+#pragma unroll
+    for (int w = 0; w < ND; ++w) o[w][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int nblk = (a.Sk + BKV - 1) / BKV;
+  load_kv(0);
+  store_kv(0);
+  __syncthreads();
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int cur = blk & 1;
+    const int kv0 = blk * BKV;
+    if (blk + 1 < nblk) load_kv(kv0 + BKV);
+
+    const float* ks = Ks[cur];
+    const float* vs = Vs[cur];
+    // S^T tiles: 4 key tiles x NU query tiles
+    floatx4 st[4][NU];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float kf[HS];
+      const float* p = ks + (16 * t + l16) * LDK + G * HS;
+#pragma unroll
+      for (int s4 = 0; s4 < HS / 4; ++s4) {
+        float4 v4 = *reinterpret_cast<const float4*>(p + 4 * s4);
+        kf[4 * s4 + 0] = v4.x; kf[4 * s4 + 1] = v4.y;
+        kf[4 * s4 + 2] = v4.z; kf[4 * s4 + 3] = v4.w;
+      }
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < HS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[u][s], acc, 0, 0, 0);
+        st[t][u] = acc;
+      }
+    }
+    // mask keys beyond Sk
+    if (kv0 + BKV > a.Sk) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (kv0 + 16 * t + 4 * G + r >= a.Sk)
+#pragma unroll
+            for (int u = 0; u < NU; ++u) st[t][u][r] = -INFINITY;
+    }
+    // online softmax per query column
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[t][u][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m[u], mx);
+      const float msafe = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = exp2f(m[u] - msafe);
+      float ps = 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = exp2f(st[t][u][r] - msafe);
+          st[t][u][r] = p;
+          ps += p;
+        }
+      lsum[u] = lsum[u] * alpha + ps;
+      m[u] = mnew;
+#pragma unroll
+      for (int w = 0; w < ND; ++w) o[w][u] *= alpha;
+    }
+    // O^T += V^T P^T ; k-slot G of step (t, r) is key 16t + 4G + r
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float* vrow = vs + (16 * t + 4 * G + r) * LDK + l16;
+#pragma unroll
+        for (int w = 0; w < ND; ++w) {
+          const float vf = vrow[16 * w];
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+            o[w][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, st[t][u][r], o[w][u], 0, 0, 0);
+        }
+      }
+
+    if (blk + 1 < nblk) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  // normalise and write O[b][q][h*HD + d]; lane holds d = 16w + 4G + r for query l16
+  float* __restrict__ ob = a.o + (int64_t)b * a.o_bs + h * HD;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    float l = lsum[u];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const float inv = 1.f / (l + 1e-10f);
+    const int q = qw0 + 16 * u + l16;
+    if (q < a.Sq) {
+      float* orow = ob + (int64_t)q * a.o_rs;
+#pragma unroll
+      for (int w = 0; w < ND; ++w) {
+        float4 r4 = make_float4(o[w][u][0] * inv, o[w][u][1] * inv, o[w][u][2] * inv,
+                                o[w][u][3] * inv);
+        *reinterpret_cast<float4*>(orow + 16 * w + 4 * G) = r4;
+      }
+    }
+  }
+}
+
+// Generic path for any head dimension: one wave per (b, h, query), scores staged in LDS,
+// three passes (max, sum of exp, weighted sum of V), the reference's exact formula.
+constexpr int kMaxGenericSk = 12288;
+__global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a) {
+  __shared__ float sc[kMaxGenericSk];
+  const int lane = threadIdx.x;
+  const int q = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const float* qr = a.q + (int64_t)b * a.q_bs + (int64_t)q * a.q_rs + h * a.hd;
+  const float* kb = a.k + (int64_t)b * a.kv_bs + h * a.hd;
+  const float* vb = a.v + (int64_t)b * a.kv_bs + h * a.hd;
+  float mx = -INFINITY;
+  for (int kv = lane; kv < a.Sk; kv += 64) {
+    const float* kr = kb + (int64_t)kv * a.kv_rs;
+    float dot = 0.f;
+    for (int d = 0; d < a.hd; ++d) dot = fmaf(qr[d], kr[d], dot);
+    const float s = dot * a.scale;
+    sc[kv] = s;
+    mx = fmaxf(mx, s);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+  for (int kv = lane; kv < a.Sk; kv += 64) {
+    const float e = expf(sc[kv] - mx);
+    sc[kv] = e;
+    sum += e;
+  }
+  sum = wave_sum(sum);
+  __syncthreads();
+  const float inv = 1.f / (sum + 1e-10f);
+  float* orow = a.o + (int64_t)b * a.o_bs + (int64_t)q * a.o_rs + h * a.hd;
+  for (int d = lane; d < a.hd; d += 64) {
+    float acc = 0.f;
+    for (int kv = 0; kv < a.Sk; ++kv) acc = fmaf(sc[kv], vb[(int64_t)kv * a.kv_rs + d], acc);
+    orow[d] = acc * inv;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+template <int HD>
+void launch_hd(const LaunchCtx& c, const AttnArgs& a) {
+  // 32 queries per wave when that still gives >= 2 workgroups per CU, else 16
+  const int64_t wg32 = (int64_t)cdiv(a.Sq, 128) * a.H * a.B;
+  if (wg32 >= 512) {
+    dim3 grid(cdiv(a.Sq, 128), a.H, a.B);
+    launch(c, HD == 64 ? "attn_fwd_f32_hd64_q32" : "attn_fwd_f32_hd48_q32",
+           attn_fwd_f32_kernel<HD, 32>, grid, dim3(256), 0, a);
+  } else {
+    dim3 grid(cdiv(a.Sq, 64), a.H, a.B);
+    launch(c, HD == 64 ? "attn_fwd_f32_hd64_q16" : "attn_fwd_f32_hd48_q16",
+           attn_fwd_f32_kernel<HD, 16>, grid, dim3(256), 0, a);
+  }
+}
+
+}  // namespace
+
+bool attention_supported(int hd) { return hd > 0; }
+
+void attention(const LaunchCtx& c, const AttnArgs& a) {
+  if (a.Sq <= 0 || a.B <= 0 || a.H <= 0) return;
+  MNN_REQUIRE(a.Sk > 0, MNN_ERR_INVALID_ARGUMENT, "attention: empty key sequence");
+  const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+                   a.q_rs % 4 == 0 && a.kv_rs % 4 == 0 && a.o_rs % 4 == 0 && a.q_bs % 4 == 0 &&
+                   a.kv_bs % 4 == 0 && a.o_bs % 4 == 0;
+  if (vec && a.hd == 64) return launch_hd<64>(c, a);
+  if (vec && a.hd == 48) return launch_hd<48>(c, a);
+  MNN_REQUIRE(a.Sk <= kMaxGenericSk, MNN_ERR_INVALID_CONFIGURATION,
+              "attention: head dim " << a.hd << " with " << a.Sk
+                                     << " keys exceeds the generic kernel's limit");
+  launch(c, "attn_generic_f32", attn_generic_kernel, dim3(a.Sq, a.H, a.B), dim3(64), 0, a);
+}
+
+}  // namespace k
+}  // namespace mnn

@@ -1,0 +1,282 @@
+// GroupNorm and LayerNorm kernels.
+//
+// GroupNorm (Normalization.swift:32-725) launches one 256-thread workgroup per (batch, group) in
+// the reference, which serialises a GroupNorm(1 group) over millions of elements on one CU. Here
+// the statistics are a grid-wide reduction in three steps: per-chunk partials (count, mean, M2)
+// from many workgroups, a fixed-order Chan merge in fp64 (deterministic), and the apply step
+// y = act(x*scale + shift) with per-channel coefficients. The partials can also come from the
+// epilogue of the producing convolution, and the apply step can be folded into the consumer
+// GEMM's operand load, so the normalised tensor never has to be written to HBM.
+//
+// LayerNorm (Normalization.swift:804-879): one wave per row, the row held in registers, so the
+// row is read from HBM once (the reference reads it three times). Two-pass statistics
+// (mean, then E[(x-mean)^2]), biased variance, eps inside the square root.
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mnn {
+namespace k {
+
+using namespace dev;
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 4096;  // elements per GroupNorm statistics partial
+
+__global__ __launch_bounds__(kThreads) void gn_stats_partial_kernel(const float* __restrict__ x,
+                                                                    int C, int64_t L, int G,
+                                                                    float* __restrict__ partials,
+                                                                    int nchunk) {
+  __shared__ float red[3 * (kThreads / 64)];
+  const int bg = blockIdx.y;
+  const int b = bg / G, g = bg % G;
+  const int cpg = C / G;
+  const int64_t total = (int64_t)cpg * L;
+  const float* base = x + ((int64_t)b * C + (int64_t)g * cpg) * L;
+  const int64_t start = (int64_t)blockIdx.x * kChunk;
+  const int64_t end = min(start + (int64_t)kChunk, total);
+  // shifted sums in fp64 per thread, shift = first element of the chunk
+  const float shift = start < total ? base[start] : 0.f;
+  double s1 = 0.0, s2 = 0.0;
+  float n = 0.f;
+  for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
+    double d = (double)base[i] - (double)shift;
+    s1 += d;
+    s2 += d * d;
+    n += 1.f;
+  }
+  float mean = 0.f, m2 = 0.f;
+  if (n > 0.f) {
+    double md = s1 / n;
+    mean = (float)((double)shift + md);
+    m2 = (float)fmax(s2 - s1 * md, 0.0);
+  }
+  block_welford(n, mean, m2, red);
+  if (threadIdx.x == 0) {
+    float* p = partials + ((int64_t)bg * nchunk + blockIdx.x) * 3;
+    p[0] = n;
+    p[1] = mean;
+    p[2] = m2;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gn_finalize_kernel(const float* __restrict__ partials,
+                                                               int C, int G, int nchunk, float eps,
+                                                               const float* __restrict__ gamma,
+                                                               const float* __restrict__ beta,
+                                                               float* __restrict__ coef) {
+  __shared__ double sn[kThreads], smean[kThreads], sm2[kThreads];
+  __shared__ float s_mean, s_rstd;
+  const int bg = blockIdx.x;
+  const int b = bg / G, g = bg % G;
+  const float* p = partials + (int64_t)bg * nchunk * 3;
+  // each thread merges a strided subset in increasing order
+  double n = 0.0, mean = 0.0, m2 = 0.0;
+  for (int j = threadIdx.x; j < nchunk; j += kThreads) {
+    double n2 = p[j * 3 + 0], mean2 = p[j * 3 + 1], m22 = p[j * 3 + 2];
+    double nt = n + n2;
+    if (nt > 0.0) {
+      double d = mean2 - mean;
+      double w = n2 / nt;
+      mean += d * w;
+      m2 += m22 + d * d * n * w;
+    }
+    n = nt;
+  }
+  sn[threadIdx.x] = n;
+  smean[threadIdx.x] = mean;
+  sm2[threadIdx.x] = m2;
+  __syncthreads();
+  for (int off = kThreads / 2; off > 0; off >>= 1) {
+    if (threadIdx.x < off) {
+      double na = sn[threadIdx.x], ma = smean[threadIdx.x], qa = sm2[threadIdx.x];
+      double nb = sn[threadIdx.x + off], mb = smean[threadIdx.x + off], qb = sm2[threadIdx.x + off];
+      double nt = na + nb;
+      if (nt > 0.0) {
+        double d = mb - ma;
+        double w = nb / nt;
+        smean[threadIdx.x] = ma + d * w;
+        sm2[threadIdx.x] = qa + qb + d * d * na * w;
+      }
+      sn[threadIdx.x] = nt;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    double cnt = sn[0];
+    double var = cnt > 0.0 ? sm2[0] / cnt : 0.0;  // biased (population) variance
+    float rstd = (float)(1.0 / sqrt(var + (double)eps));
+    if (!isfinite(rstd)) rstd = 0.f;  // reference CPU path guard (Normalization.swift:695-699)
+    s_mean = (float)smean[0];
+    s_rstd = rstd;
+  }
+  __syncthreads();
+  const int cpg = C / G;
+  for (int cc = threadIdx.x; cc < cpg; cc += kThreads) {
+    const int ch = g * cpg + cc;
+    const float gm = gamma ? gamma[ch] : 1.f;
+    const float bt = beta ? beta[ch] : 0.f;
+    const float scale = gm * s_rstd;
+    float* o = coef + ((int64_t)b * C + ch) * 2;
+    o[0] = scale;
+    o[1] = bt - s_mean * scale;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void gn_apply_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t L,
+                                                            const float* __restrict__ coef,
+                                                            int act, int vec) {
+  const int64_t row = blockIdx.y;  // b*C + c
+  const float sc = coef[row * 2 + 0], sh = coef[row * 2 + 1];
+  const float* xr = x + row * L;
+  float* yr = y + row * L;
+  if (vec) {
+    const int64_t L4 = L >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(xr);
+    float4* y4 = reinterpret_cast<float4*>(yr);
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < L4;
+         i += (int64_t)gridDim.x * kThreads) {
+      float4 v = x4[i];
+      v.x = apply_act(fmaf(v.x, sc, sh), act);
+      v.y = apply_act(fmaf(v.y, sc, sh), act);
+      v.z = apply_act(fmaf(v.z, sc, sh), act);
+      v.w = apply_act(fmaf(v.w, sc, sh), act);
+      y4[i] = v;
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < L;
+         i += (int64_t)gridDim.x * kThreads)
+      yr[i] = apply_act(fmaf(xr[i], sc, sh), act);
+  }
+}
+
+// LayerNorm, row in registers: NV float4 per lane, F % 4 == 0, F <= 256 * NV.
+template <int NV>
+__global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __restrict__ x,
+                                                                 float* __restrict__ y,
+                                                                 int64_t rows, int F,
+                                                                 const float* __restrict__ gamma,
+                                                                 const float* __restrict__ beta,
+                                                                 float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int F4 = F >> 2;
+  const float4* xr = reinterpret_cast<const float4*>(x + row * F);
+  float4 v[NV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < F4) {
+      v[i] = xr[idx];
+      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    } else {
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float mean = wave_sum(s) / (float)F;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < F4) {
+      float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+  const float var = wave_sum(q) / (float)F;
+  const float rstd = 1.f / sqrtf(var + eps);
+  float4* yr = reinterpret_cast<float4*>(y + row * F);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < F4) {
+      float4 g = g4[idx], bb = b4[idx], o;
+      o.x = g.x * ((v[i].x - mean) * rstd) + bb.x;
+      o.y = g.y * ((v[i].y - mean) * rstd) + bb.y;
+      o.z = g.z * ((v[i].z - mean) * rstd) + bb.z;
+      o.w = g.w * ((v[i].w - mean) * rstd) + bb.w;
+      yr[idx] = o;
+    }
+  }
+}
+
+// LayerNorm, any F: three passes over the row from memory, one wave per row.
+__global__ __launch_bounds__(kThreads) void layernorm_generic_kernel(
+    const float* __restrict__ x, float* __restrict__ y, int64_t rows, int F,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float* xr = x + row * F;
+  float s = 0.f;
+  for (int i = lane; i < F; i += 64) s += xr[i];
+  const float mean = wave_sum(s) / (float)F;
+  float q = 0.f;
+  for (int i = lane; i < F; i += 64) {
+    float d = xr[i] - mean;
+    q += d * d;
+  }
+  const float var = wave_sum(q) / (float)F;
+  const float rstd = 1.f / sqrtf(var + eps);
+  float* yr = y + row * F;
+  for (int i = lane; i < F; i += 64) yr[i] = gamma[i] * ((xr[i] - mean) * rstd) + beta[i];
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int gn_num_chunks(int C, int G, int64_t L) {
+  const int64_t total = (int64_t)(C / G) * L;
+  return (int)std::max<int64_t>(1, (total + kChunk - 1) / kChunk);
+}
+
+void gn_stats_partial(const LaunchCtx& c, const float* x, int B, int C, int64_t L, int G,
+                      float* partials, int nchunk) {
+  launch(c, "gn_stats_partial", gn_stats_partial_kernel, dim3(nchunk, B * G), dim3(kThreads), 0,
+         x, C, L, G, partials, nchunk);
+}
+
+void gn_finalize(const LaunchCtx& c, const float* partials, int B, int C, int G, int nchunk,
+                 float eps, const float* gamma, const float* beta, float* coef) {
+  launch(c, "gn_finalize", gn_finalize_kernel, dim3(B * G), dim3(kThreads), 0, partials, C, G,
+         nchunk, eps, gamma, beta, coef);
+}
+
+void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L,
+              const float* coef, int act) {
+  const int vec = (L % 4 == 0) && aligned16(x) && aligned16(y);
+  const int64_t items = vec ? L / 4 : L;
+  unsigned gx = (unsigned)std::min<int64_t>((items + kThreads - 1) / kThreads, 4096);
+  launch(c, "gn_apply", gn_apply_kernel, dim3(gx, (unsigned)(B * C)), dim3(kThreads), 0, x, y, L,
+         coef, act, vec);
+}
+
+void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
+               const float* gamma, const float* beta, float eps) {
+  if (rows <= 0) return;
+  dim3 grid(cdiv(rows, kThreads / 64)), block(kThreads);
+  const bool vec = (F % 4 == 0) && aligned16(x) && aligned16(y) && aligned16(gamma) &&
+                   aligned16(beta);
+  const int nv = (F + 255) / 256;
+  if (vec && nv <= 8) {
+    switch (nv) {
+      case 1: return launch(c, "layernorm_f32", layernorm_reg_kernel<1>, grid, block, 0, x, y, rows, F, gamma, beta, eps);
+      case 2: return launch(c, "layernorm_f32", layernorm_reg_kernel<2>, grid, block, 0, x, y, rows, F, gamma, beta, eps);
+      case 3: return launch(c, "layernorm_f32", layernorm_reg_kernel<3>, grid, block, 0, x, y, rows, F, gamma, beta, eps);
+      case 4: return launch(c, "layernorm_f32", layernorm_reg_kernel<4>, grid, block, 0, x, y, rows, F, gamma, beta, eps);
+      default: return launch(c, "layernorm_f32", layernorm_reg_kernel<8>, grid, block, 0, x, y, rows, F, gamma, beta, eps);
+    }
+  }
+  launch(c, "layernorm_f32", layernorm_generic_kernel, grid, block, 0, x, y, rows, F, gamma, beta,
+         eps);
+}
+
+}  // namespace k
+}  // namespace mnn

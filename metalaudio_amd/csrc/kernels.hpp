@@ -1,0 +1,115 @@
+// Host-side launchers of the HIP kernels (one .hip file per kernel family).
+#pragma once
+
+#include "common.hpp"
+
+namespace mnn {
+namespace k {
+
+// Activation codes follow mnn_activation (FusedConv1D, Conv1D.swift:960-973).
+// ------------------------------------------------------------------ elementwise (k_elementwise.hip)
+// GELU over n floats; clamp10 = the +-10 passthrough of Activations.swift:124-137.
+void gelu(const LaunchCtx& c, const float* x, float* y, int64_t n, bool clamp10);
+// y = act(x) for the other activation codes.
+void activation(const LaunchCtx& c, const float* x, float* y, int64_t n, int act);
+// GLU: per batch b, y[b][i] = x[b][i] * sigmoid(x[b][i + half]) for i < half (NN.metal:1012-1023).
+void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t half);
+void copy_bytes(const LaunchCtx& c, const void* src, void* dst, int64_t bytes);
+
+// ------------------------------------------------------------------ norms (k_norm.hip)
+// GroupNorm statistics in three steps. x is [B][C][L]; group g covers channels [g*C/G, (g+1)*C/G).
+// Step 1 writes per-chunk partials (count, mean, M2) as 3 floats at partials[(bg*nchunk + j)*3].
+int gn_num_chunks(int C, int G, int64_t L);
+void gn_stats_partial(const LaunchCtx& c, const float* x, int B, int C, int64_t L, int G,
+                      float* partials, int nchunk);
+// Step 2 merges the nchunk partials of each (b, g) (Chan's parallel formula, fp64, fixed order)
+// and writes per-(b, channel) affine coefficients: coef[(b*C + ch)*2 + {0,1}] = {scale, shift},
+// scale = gamma[ch]*rstd, shift = beta[ch] - mean*scale, so y = x*scale + shift.
+// gamma/beta may be null (affine = false).
+void gn_finalize(const LaunchCtx& c, const float* partials, int B, int C, int G, int nchunk,
+                 float eps, const float* gamma, const float* beta, float* coef);
+// Step 3: y = act(x*scale + shift), per (b, channel) coefficients.
+void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L,
+              const float* coef, int act);
+// LayerNorm over rows of F features (two-pass statistics, biased variance, rsqrt).
+void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
+               const float* gamma, const float* beta, float eps);
+
+// ------------------------------------------------------------------ conv (k_conv.hip)
+struct ConvParams {
+  int B, Cin, Cout, Lin, Lout, K, stride, pad, dilation, groups;
+  bool reflect;  // reflect padding (DynamicConv1D.swift:288-324) instead of zeros
+};
+// Direct convolution, one thread per output position and a block of output channels.
+// act: fused activation. If `partials` is set (groups of GroupNorm = 1), each workgroup also
+// writes (count, mean, M2) of its outputs (before activation); *nchunk receives the count of
+// partials per batch.
+void conv1d_direct(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                   const float* bias, float* y, int act, float* partials, int* nchunk);
+int conv1d_direct_num_chunks(const ConvParams& p);
+
+// ------------------------------------------------------------------ GEMM (k_gemm.hip)
+enum BLayout { B_NK = 0, B_KN = 1, B_CONV = 2 };
+enum BiasMode { BIAS_NONE = 0, BIAS_N = 1, BIAS_M = 2 };
+
+struct GemmArgs {
+  int M = 0, N = 0, K = 0, batch = 1;
+  // A [M][K], row-major with row stride lda (always K-contiguous)
+  const float* A = nullptr;
+  int64_t lda = 0, sA = 0;
+  // B: B_NK -> [N][K] rows of stride ldb; B_KN -> [K][N] rows of stride ldb;
+  //    B_CONV -> implicit im2col of x [Cin][conv_L] (row stride ldb):
+  //    B[k][n] = x[k / conv_ks][n*conv_stride - conv_pad + (k % conv_ks)*conv_dil]
+  const float* B = nullptr;
+  int64_t ldb = 0, sB = 0;
+  int blayout = B_NK;
+  int conv_L = 0, conv_ks = 1, conv_stride = 1, conv_pad = 0, conv_dil = 1;
+  bool conv_reflect = false;
+  // Optional prologue on B (B_KN only): B[k][n] <- act(B[k][n]*coef[b][k][0] + coef[b][k][1]);
+  // this applies GroupNorm (+GELU) of the producer while loading. coef batch stride = 2*K.
+  const float* pro_coef = nullptr;
+  int pro_act = 0;
+  // C [M][N] row-major (or [M/2][N] with glu)
+  float* C = nullptr;
+  int64_t ldc = 0, sC = 0;
+  const float* bias = nullptr;
+  int bias_mode = BIAS_NONE;
+  int act = 0;
+  // GLU epilogue: rows are stored in 32-row blocks [a0..a15, b0..b15]; output row
+  // 16*blk + r = a * sigmoid(b).
+  bool glu = false;
+  // Residual: C = R + rscale[n] * (act(acc + bias)); R may alias C.
+  const float* R = nullptr;
+  int64_t ldr = 0, sR = 0;
+  const float* rscale = nullptr;
+  // GroupNorm(1) statistics of the output (after bias, before act): per workgroup partials
+  // (count, mean, M2) at stats[(b*tiles + tile)*3]; tiles = gemm_num_tiles(...)
+  float* stats = nullptr;
+  mnn_precision precision = MNN_PRECISION_F32;
+};
+// Number of output tiles per batch for the tile configuration the launcher will pick.
+int gemm_num_tiles(const GemmArgs& a);
+void gemm(const LaunchCtx& c, const GemmArgs& a);
+
+// ------------------------------------------------------------------ attention (k_attention.hip)
+struct AttnArgs {
+  int B = 1, H = 1, Sq = 0, Sk = 0, hd = 0;
+  // element (b, s, h, d) of Q is at q[b*q_bs + s*q_rs + h*hd + d]; same for K, V, O.
+  const float* q = nullptr;
+  int64_t q_bs = 0, q_rs = 0;
+  const float* k = nullptr;
+  const float* v = nullptr;
+  int64_t kv_bs = 0, kv_rs = 0;
+  float* o = nullptr;
+  int64_t o_bs = 0, o_rs = 0;
+  float scale = 1.f;
+  mnn_precision precision = MNN_PRECISION_F32;
+};
+bool attention_supported(int hd);
+void attention(const LaunchCtx& c, const AttnArgs& a);
+
+// ------------------------------------------------------------------ diagnostics (k_probe.hip)
+void mfma_probe(const LaunchCtx& c, int variant, const float* a, const float* b, float* d);
+
+}  // namespace k
+}  // namespace mnn

@@ -1,0 +1,1034 @@
+// Hot-path layers of the MetalNN stack on MI355X. Each class states the reference type it
+// stands in for; the arithmetic lives in the k_*.hip kernels, this file only plans launches.
+#include "layers.hpp"
+
+#include <algorithm>
+#include <cmath>
+
+namespace mnn {
+
+namespace {
+
+LaunchCtx ctx(Stream& s) { return LaunchCtx{s.dev, s.s}; }
+
+// [C, L] / [B, C, L] -> (B, C, L)
+void split_bcl(const Shape& s, int64_t& B, int64_t& C, int64_t& L) {
+  MNN_REQUIRE(s.size() == 2 || s.size() == 3, MNN_ERR_SHAPE_MISMATCH,
+              "expected [C, L] or [B, C, L], got " << shape_str(s));
+  B = s.size() == 3 ? s[0] : 1;
+  C = s[s.size() - 2];
+  L = s[s.size() - 1];
+}
+
+// [S, E] / [B, S, E] -> (B, S, E); a 1-D [E] is one row.
+void split_bse(const Shape& s, int64_t& B, int64_t& S, int64_t& E) {
+  MNN_REQUIRE(s.size() >= 1 && s.size() <= 3, MNN_ERR_SHAPE_MISMATCH,
+              "expected [E], [S, E] or [B, S, E], got " << shape_str(s));
+  E = s.back();
+  S = s.size() >= 2 ? s[s.size() - 2] : 1;
+  B = s.size() == 3 ? s[0] : 1;
+}
+
+Shape with_last(Shape s, int64_t last) {
+  s.back() = last;
+  return s;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ Layer base
+void Layer::forward_cross(const Tensor*, const Tensor*, Tensor*, Tensor*, Stream&) {
+  fail(MNN_ERR_INVALID_CONFIGURATION, std::string(kind()) + " has no two-input forward");
+}
+
+Param& Layer::add_param(const std::string& name, int64_t count, float fill) {
+  auto p = std::make_unique<Param>();
+  p->name = name;
+  p->count = count;
+  dev_->make_current();
+  p->buf.reserve(sizeof(float) * std::max<int64_t>(count, 1));
+  std::vector<float> init(std::max<int64_t>(count, 1), fill);
+  HIP_CHECK(hipMemcpy(p->buf.ptr, init.data(), sizeof(float) * count, hipMemcpyHostToDevice));
+  params_.push_back(std::move(p));
+  return *params_.back();
+}
+
+Param* Layer::find_param(const std::string& name) {
+  std::string n = name;
+  auto a = aliases_.find(n);
+  if (a != aliases_.end()) n = a->second;
+  for (auto& p : params_)
+    if (p->name == n) return p.get();
+  return nullptr;
+}
+
+void Layer::load(const std::string& name, const float* data, size_t n) {
+  Param* p = find_param(name);
+  MNN_REQUIRE(p, MNN_ERR_INVALID_ARGUMENT, kind() << ": unknown parameter '" << name << "'");
+  MNN_REQUIRE((int64_t)n == p->count, MNN_ERR_BUFFER_SIZE_MISMATCH,
+              kind() << " parameter '" << name << "': expected " << p->count << " values, got "
+                     << n);
+  MNN_REQUIRE(data || n == 0, MNN_ERR_INVALID_ARGUMENT, "null data");
+  for (size_t i = 0; i < n; ++i) {
+    MNN_REQUIRE(!std::isnan(data[i]), MNN_ERR_INVALID_CONFIGURATION,
+                name << " contain NaN values - model file may be corrupted");
+    MNN_REQUIRE(!std::isinf(data[i]), MNN_ERR_INVALID_CONFIGURATION,
+                name << " contain Inf values - possible exploding gradients during training");
+  }
+  dev_->make_current();
+  HIP_CHECK(hipMemcpy(p->buf.ptr, data, sizeof(float) * n, hipMemcpyHostToDevice));
+  p->loaded = true;
+  on_loaded(p->name, data, n);
+}
+
+void Layer::check_out(const Tensor& out, const Shape& expect) const {
+  MNN_REQUIRE(out.count() == numel(expect), MNN_ERR_BUFFER_SIZE_MISMATCH,
+              kind() << ": output holds " << out.count() << " elements, expected "
+                     << shape_str(expect));
+  MNN_REQUIRE(out.dtype == MNN_F32, MNN_ERR_INVALID_ARGUMENT, kind() << ": output must be f32");
+}
+
+// ------------------------------------------------------------------ Conv1D / DynamicConv1D
+// Conv1D (Conv1D.swift:11-514), DynamicConv1D (DynamicConv1D.swift:35-403) and FusedConv1D's
+// activation epilogue (Conv1D.swift:742-1028). Dense contractions (Cin*K >= 64) run as an
+// implicit GEMM on the matrix cores; small ones on the direct kernel.
+class Conv1DLayer : public Layer {
+ public:
+  Conv1DLayer(Device* d, const mnn_conv1d_desc& desc) : Layer(d), p_(desc) {
+    MNN_REQUIRE(p_.in_channels > 0 && p_.out_channels > 0 && p_.kernel_size > 0 &&
+                    p_.stride > 0 && p_.dilation > 0 && p_.groups > 0,
+                MNN_ERR_INVALID_CONFIGURATION, "Conv1D: sizes must be positive");
+    MNN_REQUIRE(p_.in_channels % p_.groups == 0 && p_.out_channels % p_.groups == 0,
+                MNN_ERR_INVALID_CONFIGURATION, "Conv1D: channels must be divisible by groups");
+    MNN_REQUIRE(p_.padding >= 0, MNN_ERR_INVALID_CONFIGURATION, "Conv1D: negative padding");
+    w_ = &add_param("weight",
+                    (int64_t)p_.out_channels * (p_.in_channels / p_.groups) * p_.kernel_size);
+    if (p_.use_bias) b_ = &add_param("bias", p_.out_channels);
+    if (p_.input_length > 0)
+      MNN_REQUIRE(out_len(p_.input_length) > 0, MNN_ERR_INVALID_CONFIGURATION,
+                  "Conv1D: output length would be <= 0");
+  }
+  const char* kind() const override { return p_.input_length > 0 ? "Conv1D" : "DynamicConv1D"; }
+  Shape input_shape() const override { return {p_.in_channels, p_.input_length}; }
+  Shape output_shape() const override {
+    return {p_.out_channels, p_.input_length > 0 ? out_len(p_.input_length) : 0};
+  }
+  int pad_for(int64_t L) const {
+    switch (p_.padding_mode) {
+      case MNN_PAD_VALID: return 0;
+      case MNN_PAD_SAME: {  // DynamicConv1D.swift:167-173
+        const int64_t eff = (int64_t)(p_.kernel_size - 1) * p_.dilation + 1;
+        const int64_t outl = (L + p_.stride - 1) / p_.stride;
+        const int64_t total = std::max<int64_t>(0, (outl - 1) * p_.stride + eff - L);
+        return (int)(total / 2);
+      }
+      default: return p_.padding;
+    }
+  }
+  // output = floor((L + 2p - ((k-1)d + 1)) / s) + 1 (DynamicConv1D.swift:153-161)
+  int64_t out_len(int64_t L) const {
+    const int64_t eff = (int64_t)(p_.kernel_size - 1) * p_.dilation + 1;
+    const int64_t num = L + 2 * pad_for(L) - eff;
+    return num < 0 ? 0 : num / p_.stride + 1;
+  }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, L;
+    split_bcl(in, B, C, L);
+    MNN_REQUIRE(C == p_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                kind() << ": expected " << p_.in_channels << " input channels, got " << C);
+    if (p_.input_length > 0)
+      MNN_REQUIRE(L == p_.input_length, MNN_ERR_SHAPE_MISMATCH,
+                  "Conv1D: expected input length " << p_.input_length << ", got " << L);
+    const int64_t lo = out_len(L);
+    MNN_REQUIRE(lo > 0, MNN_ERR_SHAPE_MISMATCH, kind() << ": input length " << L << " too short");
+    if (p_.padding_mode == MNN_PAD_REFLECT)
+      MNN_REQUIRE(pad_for(L) < L, MNN_ERR_SHAPE_MISMATCH,
+                  "reflect padding " << pad_for(L) << " needs input length > padding");
+    Shape o = in;
+    o[o.size() - 2] = p_.out_channels;
+    o.back() = lo;
+    return o;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    const Shape os = infer_output(in.shape);
+    check_out(out, os);
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    run(in.f32(), (int)B, (int)L, out.f32(), p_.activation, nullptr, s);
+  }
+  bool uses_mfma() const {
+    const int ck = p_.in_channels * p_.kernel_size;
+    return p_.groups == 1 && ck % 4 == 0 && ck >= 64 && p_.out_channels >= 32;
+  }
+  // Runs the convolution; `stats` (GroupNorm(1) partials of the pre-activation output) is
+  // optional. Returns the number of partials per batch written to `stats`.
+  int run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s) {
+    const int lo = (int)out_len(L);
+    const int pad = pad_for(L);
+    const bool reflect = p_.padding_mode == MNN_PAD_REFLECT;
+    if (uses_mfma()) {
+      k::GemmArgs g;
+      g.M = p_.out_channels;
+      g.N = lo;
+      g.K = p_.in_channels * p_.kernel_size;
+      g.batch = B;
+      g.A = w_->ptr();
+      g.lda = g.K;
+      g.B = x;
+      g.ldb = L;
+      g.sB = (int64_t)p_.in_channels * L;
+      g.blayout = k::B_CONV;
+      g.conv_L = L;
+      g.conv_ks = p_.kernel_size;
+      g.conv_stride = p_.stride;
+      g.conv_pad = pad;
+      g.conv_dil = p_.dilation;
+      g.conv_reflect = reflect;
+      g.C = y;
+      g.ldc = lo;
+      g.sC = (int64_t)p_.out_channels * lo;
+      g.bias = b_ ? b_->ptr() : nullptr;
+      g.bias_mode = b_ ? k::BIAS_M : k::BIAS_NONE;
+      g.act = act;
+      g.stats = stats;
+      g.precision = p_.precision;
+      k::gemm(ctx(s), g);
+      return k::gemm_num_tiles(g);
+    }
+    k::ConvParams cp{B, p_.in_channels, p_.out_channels, L, lo, p_.kernel_size,
+                     p_.stride, pad, p_.dilation, p_.groups, reflect};
+    int nchunk = 0;
+    k::conv1d_direct(ctx(s), cp, x, w_->ptr(), b_ ? b_->ptr() : nullptr, y, act, stats, &nchunk);
+    return nchunk;
+  }
+  int stats_chunks(int L) const {
+    const int lo = (int)out_len(L);
+    if (uses_mfma()) {
+      k::GemmArgs g;
+      g.M = p_.out_channels;
+      g.N = lo;
+      g.K = p_.in_channels * p_.kernel_size;
+      g.lda = g.K;
+      g.A = w_->ptr();
+      g.blayout = k::B_CONV;
+      return k::gemm_num_tiles(g);
+    }
+    k::ConvParams cp{1, p_.in_channels, p_.out_channels, L, lo, p_.kernel_size,
+                     p_.stride, pad_for(L), p_.dilation, p_.groups, false};
+    return k::conv1d_direct_num_chunks(cp);
+  }
+  const mnn_conv1d_desc& desc() const { return p_; }
+
+ private:
+  mnn_conv1d_desc p_;
+  Param* w_ = nullptr;
+  Param* b_ = nullptr;
+};
+
+// ------------------------------------------------------------------ GroupNorm
+// GroupNorm (Normalization.swift:32-725): population variance, eps 1e-5, per-channel affine.
+class GroupNormLayer : public Layer {
+ public:
+  GroupNormLayer(Device* d, int groups, int channels, float eps, bool affine, int act)
+      : Layer(d), G_(groups), C_(channels), eps_(eps), act_(act) {
+    MNN_REQUIRE(groups > 0 && channels > 0 && channels % groups == 0,
+                MNN_ERR_INVALID_CONFIGURATION,
+                "numChannels (" << channels << ") must be divisible by numGroups (" << groups
+                                << ")");
+    if (affine) {
+      gamma_ = &add_param("weight", channels, 1.f);
+      beta_ = &add_param("bias", channels, 0.f);
+      aliases_["gamma"] = "weight";
+      aliases_["beta"] = "bias";
+    }
+  }
+  const char* kind() const override { return "GroupNorm"; }
+  Shape input_shape() const override { return {C_, 0}; }
+  Shape output_shape() const override { return {C_, 0}; }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, L;
+    split_bcl(in, B, C, L);
+    MNN_REQUIRE(C == C_, MNN_ERR_SHAPE_MISMATCH,
+                "GroupNorm: expected " << C_ << " channels, got " << C);
+    return in;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    const int nchunk = k::gn_num_chunks(C_, G_, L);
+    partials_.reserve(sizeof(float) * 3 * B * G_ * nchunk);
+    coef_.reserve(sizeof(float) * 2 * B * C_);
+    k::gn_stats_partial(ctx(s), in.f32(), (int)B, C_, L, G_, partials_.f32(), nchunk);
+    finalize(s, (int)B, nchunk, partials_.f32());
+    k::gn_apply(ctx(s), in.f32(), out.f32(), (int)B, C_, L, coef_.f32(), act_);
+  }
+  // Turns partials into per-(b, c) coefficients held in coef().
+  void finalize(Stream& s, int B, int nchunk, const float* partials) {
+    coef_.reserve(sizeof(float) * 2 * B * C_);
+    k::gn_finalize(ctx(s), partials, B, C_, G_, nchunk, eps_, gamma_ ? gamma_->ptr() : nullptr,
+                   beta_ ? beta_->ptr() : nullptr, coef_.f32());
+  }
+  const float* coef() const { return coef_.f32(); }
+  int groups() const { return G_; }
+  int act() const { return act_; }
+
+ private:
+  int G_, C_;
+  float eps_;
+  int act_;
+  Param* gamma_ = nullptr;
+  Param* beta_ = nullptr;
+  DevBuf partials_, coef_;
+};
+
+// ------------------------------------------------------------------ LayerNorm
+// LayerNorm (Normalization.swift:734-964) over the last dimension.
+class LayerNormLayer : public Layer {
+ public:
+  LayerNormLayer(Device* d, int features, float eps) : Layer(d), F_(features), eps_(eps) {
+    MNN_REQUIRE(features > 0, MNN_ERR_INVALID_CONFIGURATION, "LayerNorm: featureSize <= 0");
+    gamma_ = &add_param("gamma", features, 1.f);
+    beta_ = &add_param("beta", features, 0.f);
+    aliases_["weight"] = "gamma";
+    aliases_["bias"] = "beta";
+  }
+  const char* kind() const override { return "LayerNorm"; }
+  Shape input_shape() const override { return {F_}; }
+  Shape output_shape() const override { return {F_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE(!in.empty() && numel(in) % F_ == 0, MNN_ERR_SHAPE_MISMATCH,
+                "LayerNorm: element count of " << shape_str(in) << " not a multiple of " << F_);
+    return in;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    run(in.f32(), in.count() / F_, out.f32(), s);
+  }
+  void run(const float* x, int64_t rows, float* y, Stream& s) {
+    k::layernorm(ctx(s), x, y, rows, F_, gamma_->ptr(), beta_->ptr(), eps_);
+  }
+
+ private:
+  int F_;
+  float eps_;
+  Param* gamma_;
+  Param* beta_;
+};
+
+// ------------------------------------------------------------------ GELU
+// GELU layer (Activations.swift:89-205): tanh approximation, x > 10 -> x, x < -10 -> 0.
+class GELULayer : public Layer {
+ public:
+  GELULayer(Device* d, const Shape& s) : Layer(d), shape_(s) {}
+  const char* kind() const override { return "GELU"; }
+  Shape input_shape() const override { return shape_; }
+  Shape output_shape() const override { return shape_; }
+  Shape infer_output(const Shape& in) const override { return in; }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, in.shape);
+    k::gelu(ctx(s), in.f32(), out.f32(), in.count(), true);
+  }
+
+ private:
+  Shape shape_;
+};
+
+// ------------------------------------------------------------------ GLU
+// glu kernel (Shaders/NN.metal:1012-1023) as a layer over the channel dimension.
+class GLULayer : public Layer {
+ public:
+  GLULayer(Device* d, int c) : Layer(d), C_(c) {
+    MNN_REQUIRE(c > 0, MNN_ERR_INVALID_CONFIGURATION, "GLU: channels <= 0");
+  }
+  const char* kind() const override { return "GLU"; }
+  Shape input_shape() const override { return {2 * C_, 0}; }
+  Shape output_shape() const override { return {C_, 0}; }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, L;
+    split_bcl(in, B, C, L);
+    MNN_REQUIRE(C == 2 * C_, MNN_ERR_SHAPE_MISMATCH,
+                "GLU: expected " << 2 * C_ << " channels, got " << C);
+    Shape o = in;
+    o[o.size() - 2] = C_;
+    return o;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    k::glu(ctx(s), in.f32(), out.f32(), B, (int64_t)C_ * L);
+  }
+
+ private:
+  int C_;
+};
+
+// ------------------------------------------------------------------ Linear
+// Linear / FusedLinear / HalfLinear (Linear.swift:27-672; HalfPrecisionLinear.swift:60-212):
+// y = act(x W^T + b), W [out, in].
+class LinearLayer : public Layer {
+ public:
+  LinearLayer(Device* d, int in, int out, bool bias, int act, mnn_precision prec)
+      : Layer(d), in_(in), out_(out), act_(act), prec_(prec) {
+    MNN_REQUIRE(in > 0 && out > 0, MNN_ERR_INVALID_CONFIGURATION, "Linear: sizes must be > 0");
+    w_ = &add_param("weight", (int64_t)in * out);
+    if (bias) b_ = &add_param("bias", out);
+  }
+  const char* kind() const override { return "Linear"; }
+  Shape input_shape() const override { return {in_}; }
+  Shape output_shape() const override { return {out_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE(!in.empty() && in.back() == in_, MNN_ERR_SHAPE_MISMATCH,
+                "Linear: expected last dimension " << in_ << ", got " << shape_str(in));
+    return with_last(in, out_);
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    run(in.f32(), in.count() / in_, out.f32(), act_, nullptr, nullptr, s);
+  }
+  // y = R + rscale * act(x W^T + b) when R is given (R may alias y).
+  void run(const float* x, int64_t rows, float* y, int act, const float* R, const float* rscale,
+           Stream& s) {
+    k::GemmArgs g;
+    g.M = (int)rows;
+    g.N = out_;
+    g.K = in_;
+    g.A = x;
+    g.lda = in_;
+    g.B = w_->ptr();
+    g.ldb = in_;
+    g.blayout = k::B_NK;
+    g.C = y;
+    g.ldc = out_;
+    g.bias = b_ ? b_->ptr() : nullptr;
+    g.bias_mode = b_ ? k::BIAS_N : k::BIAS_NONE;
+    g.act = act;
+    g.R = R;
+    g.ldr = out_;
+    g.rscale = rscale;
+    g.precision = prec_;
+    k::gemm(ctx(s), g);
+  }
+  int in_features() const { return in_; }
+  int out_features() const { return out_; }
+
+ private:
+  int in_, out_, act_;
+  mnn_precision prec_;
+  Param* w_ = nullptr;
+  Param* b_ = nullptr;
+};
+
+// ------------------------------------------------------------------ MultiHeadAttention
+// MultiHeadAttention / CrossAttention (Attention.swift:15-1063). Q, K, V come from one packed
+// projection GEMM (self) or a Q GEMM plus a KV GEMM over rows E..3E of in_proj (cross); the
+// fused attention kernel reads them in place with row strides, and the output projection can
+// fuse a residual with LayerScale.
+class MHALayer : public Layer {
+ public:
+  MHALayer(Device* d, int embed, int heads, bool bias, mnn_precision prec)
+      : Layer(d), E_(embed), H_(heads), prec_(prec) {
+    MNN_REQUIRE(embed > 0 && heads > 0 && embed % heads == 0, MNN_ERR_INVALID_CONFIGURATION,
+                "embedDim (" << embed << ") must be divisible by numHeads (" << heads << ")");
+    hd_ = embed / heads;
+    win_ = &add_param("in_proj_weight", 3LL * embed * embed);
+    wout_ = &add_param("out_proj_weight", (int64_t)embed * embed);
+    if (bias) {
+      bin_ = &add_param("in_proj_bias", 3LL * embed);
+      bout_ = &add_param("out_proj_bias", embed);
+    }
+    // Default weights: identity-like Q/K/V/out projections (Attention.swift initializeDefaultWeights)
+    std::vector<float> wi(3LL * embed * embed, 0.f), wo((int64_t)embed * embed, 0.f);
+    for (int p = 0; p < 3; ++p)
+      for (int i = 0; i < embed; ++i) wi[((int64_t)p * embed + i) * embed + i] = 1.f;
+    for (int i = 0; i < embed; ++i) wo[(int64_t)i * embed + i] = 1.f;
+    d->make_current();
+    HIP_CHECK(hipMemcpy(win_->buf.ptr, wi.data(), wi.size() * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(wout_->buf.ptr, wo.data(), wo.size() * 4, hipMemcpyHostToDevice));
+  }
+  const char* kind() const override { return "MultiHeadAttention"; }
+  Shape input_shape() const override { return {0, E_}; }
+  Shape output_shape() const override { return {0, E_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE((in.size() == 2 || in.size() == 3) && in.back() == E_, MNN_ERR_SHAPE_MISMATCH,
+                "MultiHeadAttention: expected [S, " << E_ << "] or [B, S, " << E_ << "], got "
+                                                    << shape_str(in));
+    return in;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, S, E;
+    split_bse(in.shape, B, S, E);
+    run(in.f32(), (int)S, nullptr, 0, (int)B, out.f32(), nullptr, nullptr, s);
+  }
+  void forward_cross(const Tensor* q, const Tensor* kv, Tensor* out, Tensor*, Stream& s) override {
+    MNN_REQUIRE(q && kv && out, MNN_ERR_INVALID_ARGUMENT, "cross-attention needs query, keyValue, output");
+    check_out(*out, infer_output(q->shape));
+    infer_output(kv->shape);
+    int64_t B, Sq, E, Bk, Sk, Ek;
+    split_bse(q->shape, B, Sq, E);
+    split_bse(kv->shape, Bk, Sk, Ek);
+    MNN_REQUIRE(B == Bk, MNN_ERR_SHAPE_MISMATCH, "cross-attention: batch sizes differ");
+    run(q->f32(), (int)Sq, kv->f32(), (int)Sk, (int)B, out->f32(), nullptr, nullptr, s);
+  }
+  // xkv == nullptr: self-attention. out = R + rscale * MHA(...) when R is given.
+  void run(const float* xq, int Sq, const float* xkv, int Sk, int B, float* out, const float* R,
+           const float* rscale, Stream& s) {
+    const int E = E_;
+    const int64_t rq = (int64_t)B * Sq;
+    k::AttnArgs at;
+    at.B = B;
+    at.H = H_;
+    at.Sq = Sq;
+    at.hd = hd_;
+    at.scale = 1.f / std::sqrt((float)hd_);
+    at.precision = prec_;
+    if (!xkv) {
+      qkv_.reserve(sizeof(float) * rq * 3 * E);
+      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, 3 * E, qkv_.f32(), s);
+      at.Sk = Sq;
+      at.q = qkv_.f32();
+      at.q_rs = 3 * E;
+      at.q_bs = (int64_t)Sq * 3 * E;
+      at.k = qkv_.f32() + E;
+      at.v = qkv_.f32() + 2 * E;
+      at.kv_rs = 3 * E;
+      at.kv_bs = (int64_t)Sq * 3 * E;
+    } else {
+      const int64_t rk = (int64_t)B * Sk;
+      qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
+      float* qb = qkv_.f32();
+      float* kvb = qb + rq * E;
+      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, E, qb, s);
+      proj(xkv, rk, win_->ptr() + (int64_t)E * E, bin_ ? bin_->ptr() + E : nullptr, 2 * E, kvb, s);
+      at.Sk = Sk;
+      at.q = qb;
+      at.q_rs = E;
+      at.q_bs = (int64_t)Sq * E;
+      at.k = kvb;
+      at.v = kvb + E;
+      at.kv_rs = 2 * E;
+      at.kv_bs = (int64_t)Sk * 2 * E;
+    }
+    attn_.reserve(sizeof(float) * rq * E);
+    at.o = attn_.f32();
+    at.o_rs = E;
+    at.o_bs = (int64_t)Sq * E;
+    k::attention(ctx(s), at);
+    // output projection (+ residual / LayerScale)
+    k::GemmArgs g;
+    g.M = (int)rq;
+    g.N = E;
+    g.K = E;
+    g.A = attn_.f32();
+    g.lda = E;
+    g.B = wout_->ptr();
+    g.ldb = E;
+    g.blayout = k::B_NK;
+    g.C = out;
+    g.ldc = E;
+    g.bias = bout_ ? bout_->ptr() : nullptr;
+    g.bias_mode = bout_ ? k::BIAS_N : k::BIAS_NONE;
+    g.R = R;
+    g.ldr = E;
+    g.rscale = rscale;
+    g.precision = prec_;
+    k::gemm(ctx(s), g);
+  }
+
+ private:
+  void proj(const float* x, int64_t rows, const float* w, const float* b, int nout, float* y,
+            Stream& s) {
+    k::GemmArgs g;
+    g.M = (int)rows;
+    g.N = nout;
+    g.K = E_;
+    g.A = x;
+    g.lda = E_;
+    g.B = w;
+    g.ldb = E_;
+    g.blayout = k::B_NK;
+    g.C = y;
+    g.ldc = nout;
+    g.bias = b;
+    g.bias_mode = b ? k::BIAS_N : k::BIAS_NONE;
+    g.precision = prec_;
+    k::gemm(ctx(s), g);
+  }
+
+  int E_, H_, hd_;
+  mnn_precision prec_;
+  Param* win_ = nullptr;
+  Param* wout_ = nullptr;
+  Param* bin_ = nullptr;
+  Param* bout_ = nullptr;
+  DevBuf qkv_, attn_;
+};
+
+// ------------------------------------------------------------------ FeedForward
+// FeedForward (Transformer.swift:7-364): Linear1 -> tanh-GELU -> Linear2, GELU fused into the
+// first GEMM's epilogue, optional residual + LayerScale fused into the second.
+class FeedForwardLayer : public Layer {
+ public:
+  FeedForwardLayer(Device* d, int in, int hidden, mnn_precision prec)
+      : Layer(d), E_(in), Hd_(hidden), prec_(prec) {
+    MNN_REQUIRE(in > 0 && hidden > 0, MNN_ERR_INVALID_CONFIGURATION, "FeedForward: sizes <= 0");
+    w1_ = &add_param("linear1.weight", (int64_t)hidden * in);
+    b1_ = &add_param("linear1.bias", hidden);
+    w2_ = &add_param("linear2.weight", (int64_t)in * hidden);
+    b2_ = &add_param("linear2.bias", in);
+  }
+  const char* kind() const override { return "FeedForward"; }
+  Shape input_shape() const override { return {0, E_}; }
+  Shape output_shape() const override { return {0, E_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE(!in.empty() && in.back() == E_, MNN_ERR_SHAPE_MISMATCH,
+                "FeedForward: expected last dimension " << E_ << ", got " << shape_str(in));
+    return in;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    run(in.f32(), in.count() / E_, out.f32(), nullptr, nullptr, s);
+  }
+  void run(const float* x, int64_t rows, float* y, const float* R, const float* rscale,
+           Stream& s) {
+    hidden_.reserve(sizeof(float) * rows * Hd_);
+    k::GemmArgs g;
+    g.M = (int)rows;
+    g.N = Hd_;
+    g.K = E_;
+    g.A = x;
+    g.lda = E_;
+    g.B = w1_->ptr();
+    g.ldb = E_;
+    g.blayout = k::B_NK;
+    g.C = hidden_.f32();
+    g.ldc = Hd_;
+    g.bias = b1_->ptr();
+    g.bias_mode = k::BIAS_N;
+    g.act = MNN_ACT_GELU;
+    g.precision = prec_;
+    k::gemm(ctx(s), g);
+    k::GemmArgs g2;
+    g2.M = (int)rows;
+    g2.N = E_;
+    g2.K = Hd_;
+    g2.A = hidden_.f32();
+    g2.lda = Hd_;
+    g2.B = w2_->ptr();
+    g2.ldb = Hd_;
+    g2.blayout = k::B_NK;
+    g2.C = y;
+    g2.ldc = E_;
+    g2.bias = b2_->ptr();
+    g2.bias_mode = k::BIAS_N;
+    g2.R = R;
+    g2.ldr = E_;
+    g2.rscale = rscale;
+    g2.precision = prec_;
+    k::gemm(ctx(s), g2);
+  }
+
+ private:
+  int E_, Hd_;
+  mnn_precision prec_;
+  Param *w1_, *b1_, *w2_, *b2_;
+  DevBuf hidden_;
+};
+
+// ------------------------------------------------------------------ UNetEncoderBlock
+// UNetEncoderBlock (UNet.swift:11-174): DynamicConv1D(reflect (k-1)/2) -> GroupNorm -> GELU,
+// optionally followed by the HTDemucs rewrite 1x1 conv C -> 2C and GLU. Launch plan:
+//   1. conv (+ bias) with GroupNorm partial statistics fused into its epilogue (G = 1),
+//   2. statistics merge -> per-channel scale/shift,
+//   3a. rewrite GEMM reading the conv output through GroupNorm+GELU, GLU in the epilogue, or
+//   3b. (no rewrite) GroupNorm-apply + GELU.
+class EncoderBlockLayer : public Layer {
+ public:
+  EncoderBlockLayer(Device* d, const mnn_encoder_block_desc& desc)
+      : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.out_channels > 0 && desc.kernel_size > 0 &&
+                    desc.stride > 0 && desc.num_groups > 0,
+                MNN_ERR_INVALID_CONFIGURATION, "UNetEncoderBlock: sizes must be positive");
+    mnn_conv1d_desc cd{};
+    cd.in_channels = desc.in_channels;
+    cd.out_channels = desc.out_channels;
+    cd.kernel_size = desc.kernel_size;
+    cd.stride = desc.stride;
+    cd.padding = (desc.kernel_size - 1) / 2;
+    cd.dilation = 1;
+    cd.groups = 1;
+    cd.use_bias = 1;
+    cd.input_length = 0;
+    cd.padding_mode = MNN_PAD_REFLECT;
+    cd.activation = MNN_ACT_NONE;
+    cd.precision = desc.precision;
+    conv_ = std::make_unique<Conv1DLayer>(d, cd);
+    norm_ = std::make_unique<GroupNormLayer>(d, desc.num_groups, desc.out_channels, 1e-5f, true,
+                                             MNN_ACT_GELU);
+    const int C = desc.out_channels;
+    if (desc.rewrite) {
+      rw_ = &add_param("rewrite.weight", 2LL * C * C);
+      rb_ = &add_param("rewrite.bias", 2LL * C);
+      glu_fused_ = (C % 16 == 0);
+      if (glu_fused_) {
+        rw_perm_.reserve(sizeof(float) * 2 * C * C);
+        rb_perm_.reserve(sizeof(float) * 2 * C);
+        std::vector<float> z(2LL * C * C, 0.f);
+        HIP_CHECK(hipMemcpy(rw_perm_.ptr, z.data(), z.size() * 4, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(rb_perm_.ptr, z.data(), 2LL * C * 4, hipMemcpyHostToDevice));
+      }
+    }
+  }
+  const char* kind() const override { return "UNetEncoderBlock"; }
+  Shape input_shape() const override { return {d_.in_channels, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0}; }
+  Shape infer_output(const Shape& in) const override { return conv_->infer_output(in); }
+  void load(const std::string& name, const float* data, size_t n) override {
+    if (name.rfind("conv.", 0) == 0) return conv_->load(name.substr(5), data, n);
+    if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
+    if (name == "rewrite.weight" || name == "rewrite.bias") {
+      MNN_REQUIRE(d_.rewrite, MNN_ERR_INVALID_ARGUMENT, "block has no rewrite conv");
+      return Layer::load(name, data, n);
+    }
+    fail(MNN_ERR_INVALID_ARGUMENT, "UNetEncoderBlock: unknown parameter '" + name + "'");
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    const Shape os = infer_output(in.shape);
+    check_out(out, os);
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    const int Cout = d_.out_channels;
+    const int64_t lo = os.back();
+    y_.reserve(sizeof(float) * B * Cout * lo);
+    const bool fused_stats = norm_->groups() == 1;
+    int nchunk;
+    if (fused_stats) {
+      nchunk = conv_->stats_chunks((int)L);
+      partials_.reserve(sizeof(float) * 3 * B * nchunk);
+      const int got = conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE,
+                                 partials_.f32(), s);
+      MNN_REQUIRE(got == nchunk, MNN_ERR_GPU_EXECUTION, "statistics partial count mismatch");
+    } else {
+      conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, nullptr, s);
+      nchunk = k::gn_num_chunks(Cout, norm_->groups(), lo);
+      partials_.reserve(sizeof(float) * 3 * B * norm_->groups() * nchunk);
+      k::gn_stats_partial(ctx(s), y_.f32(), (int)B, Cout, lo, norm_->groups(), partials_.f32(),
+                          nchunk);
+    }
+    norm_->finalize(s, (int)B, nchunk, partials_.f32());
+    if (!d_.rewrite) {
+      k::gn_apply(ctx(s), y_.f32(), out.f32(), (int)B, Cout, lo, norm_->coef(), MNN_ACT_GELU);
+      return;
+    }
+    k::GemmArgs g;
+    g.M = 2 * Cout;
+    g.N = (int)lo;
+    g.K = Cout;
+    g.batch = (int)B;
+    g.lda = Cout;
+    g.B = y_.f32();
+    g.ldb = lo;
+    g.sB = (int64_t)Cout * lo;
+    g.blayout = k::B_KN;
+    g.pro_coef = norm_->coef();
+    g.pro_act = MNN_ACT_GELU;
+    g.bias_mode = k::BIAS_M;
+    g.precision = d_.precision;
+    if (glu_fused_) {
+      g.A = rw_perm_.f32();
+      g.bias = rb_perm_.f32();
+      g.glu = true;
+      g.C = out.f32();
+      g.ldc = lo;
+      g.sC = (int64_t)Cout * lo;
+      k::gemm(ctx(s), g);
+    } else {
+      z_.reserve(sizeof(float) * B * 2 * Cout * lo);
+      g.A = rw_->ptr();
+      g.bias = rb_->ptr();
+      g.C = z_.f32();
+      g.ldc = lo;
+      g.sC = 2LL * Cout * lo;
+      k::gemm(ctx(s), g);
+      k::glu(ctx(s), z_.f32(), out.f32(), B, (int64_t)Cout * lo);
+    }
+  }
+
+ protected:
+  // Rows of the rewrite weight are regrouped into 32-row blocks [a0..a15 | b0..b15] so the GLU
+  // partner rows c and c + C meet in one accumulator block of the GEMM.
+  void on_loaded(const std::string& name, const float* data, size_t n) override {
+    if (!glu_fused_) return;
+    const int C = d_.out_channels;
+    if (name == "rewrite.weight") {
+      std::vector<float> p(n);
+      for (int blk = 0; blk < C / 16; ++blk)
+        for (int j = 0; j < 16; ++j) {
+          std::copy_n(data + (int64_t)(16 * blk + j) * C, C, p.data() + (int64_t)(32 * blk + j) * C);
+          std::copy_n(data + (int64_t)(C + 16 * blk + j) * C, C,
+                      p.data() + (int64_t)(32 * blk + 16 + j) * C);
+        }
+      HIP_CHECK(hipMemcpy(rw_perm_.ptr, p.data(), n * 4, hipMemcpyHostToDevice));
+    } else if (name == "rewrite.bias") {
+      std::vector<float> p(n);
+      for (int blk = 0; blk < C / 16; ++blk)
+        for (int j = 0; j < 16; ++j) {
+          p[32 * blk + j] = data[16 * blk + j];
+          p[32 * blk + 16 + j] = data[C + 16 * blk + j];
+        }
+      HIP_CHECK(hipMemcpy(rb_perm_.ptr, p.data(), n * 4, hipMemcpyHostToDevice));
+    }
+  }
+
+ private:
+  mnn_encoder_block_desc d_;
+  std::unique_ptr<Conv1DLayer> conv_;
+  std::unique_ptr<GroupNormLayer> norm_;
+  Param* rw_ = nullptr;
+  Param* rb_ = nullptr;
+  bool glu_fused_ = false;
+  DevBuf rw_perm_, rb_perm_;
+  DevBuf y_, partials_, z_;
+};
+
+// ------------------------------------------------------------------ transformer building blocks
+namespace {
+
+// One pre-norm branch of a transformer layer. Self: x += g1*MHA(LN1 x); x += g2*FFN(LN2 x).
+// Cross: x += g1*MHA(LN1 x, LN2 other); x += g2*FFN(LN3 x). LayerScale g = layer_scale * 1
+// unless loaded; layer_scale <= 0 disables it.
+struct Branch {
+  std::unique_ptr<LayerNormLayer> norm1, norm2, norm3;
+  std::unique_ptr<MHALayer> attn;
+  std::unique_ptr<FeedForwardLayer> ffn;
+  std::unique_ptr<LinearLayer> dummy;
+  bool cross = false;
+  bool use_ls = false;
+  DevBuf g1, g2;
+  int E = 0;
+
+  Branch(Device* d, int embed, int heads, int ffn_dim, bool is_cross, float ls,
+         mnn_precision prec)
+      : cross(is_cross), E(embed) {
+    norm1 = std::make_unique<LayerNormLayer>(d, embed, 1e-5f);
+    norm2 = std::make_unique<LayerNormLayer>(d, embed, 1e-5f);
+    if (is_cross) norm3 = std::make_unique<LayerNormLayer>(d, embed, 1e-5f);
+    attn = std::make_unique<MHALayer>(d, embed, heads, true, prec);
+    ffn = std::make_unique<FeedForwardLayer>(d, embed, ffn_dim, prec);
+    use_ls = ls > 0.f;
+    if (use_ls) {
+      std::vector<float> v(embed, ls);
+      g1.reserve(embed * 4);
+      g2.reserve(embed * 4);
+      HIP_CHECK(hipMemcpy(g1.ptr, v.data(), embed * 4, hipMemcpyHostToDevice));
+      HIP_CHECK(hipMemcpy(g2.ptr, v.data(), embed * 4, hipMemcpyHostToDevice));
+    }
+  }
+  LayerNormLayer* ffn_norm() { return cross ? norm3.get() : norm2.get(); }
+  // returns true if the name was consumed
+  bool load(const std::string& name, const float* data, size_t n) {
+    auto starts = [&](const char* p) { return name.rfind(p, 0) == 0; };
+    if (starts("norm1.")) return norm1->load(name.substr(6), data, n), true;
+    if (starts("norm2.")) return norm2->load(name.substr(6), data, n), true;
+    if (starts("norm3.")) {
+      MNN_REQUIRE(cross, MNN_ERR_INVALID_ARGUMENT, "norm3 exists only in cross layers");
+      return norm3->load(name.substr(6), data, n), true;
+    }
+    if (starts("attn.") || starts("self_attn.") || starts("cross_attn.")) {
+      const size_t dot = name.find('.');
+      return attn->load(name.substr(dot + 1), data, n), true;
+    }
+    if (starts("linear1.") || starts("linear2.")) return ffn->load(name, data, n), true;
+    if (name == "gamma_1.scale" || name == "gamma_2.scale") {
+      MNN_REQUIRE(use_ls, MNN_ERR_INVALID_ARGUMENT, "LayerScale disabled for this layer");
+      MNN_REQUIRE((int)n == E, MNN_ERR_BUFFER_SIZE_MISMATCH, name << ": expected " << E);
+      for (size_t i = 0; i < n; ++i)
+        MNN_REQUIRE(std::isfinite(data[i]), MNN_ERR_INVALID_CONFIGURATION, name << " not finite");
+      HIP_CHECK(hipMemcpy((name[6] == '1' ? g1 : g2).ptr, data, n * 4, hipMemcpyHostToDevice));
+      return true;
+    }
+    return false;
+  }
+  const float* ls1() const { return use_ls ? g1.f32() : nullptr; }
+  const float* ls2() const { return use_ls ? g2.f32() : nullptr; }
+};
+
+}  // namespace
+
+// Single-sequence pre-norm transformer layer (config: MHSA + FFN).
+class TransformerLayerImpl : public Layer {
+ public:
+  TransformerLayerImpl(Device* d, int embed, int heads, int ffn, float ls, mnn_precision prec)
+      : Layer(d), E_(embed), br_(d, embed, heads, ffn, false, ls, prec) {}
+  const char* kind() const override { return "TransformerLayer"; }
+  Shape input_shape() const override { return {0, E_}; }
+  Shape output_shape() const override { return {0, E_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE((in.size() == 2 || in.size() == 3) && in.back() == E_, MNN_ERR_SHAPE_MISMATCH,
+                "TransformerLayer: expected [S, " << E_ << "] or [B, S, " << E_ << "]");
+    return in;
+  }
+  void load(const std::string& name, const float* data, size_t n) override {
+    MNN_REQUIRE(br_.load(name, data, n), MNN_ERR_INVALID_ARGUMENT,
+                "TransformerLayer: unknown parameter '" << name << "'");
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, S, E;
+    split_bse(in.shape, B, S, E);
+    const int64_t rows = B * S;
+    h_.reserve(sizeof(float) * rows * E);
+    br_.norm1->run(in.f32(), rows, h_.f32(), s);
+    br_.attn->run(h_.f32(), (int)S, nullptr, 0, (int)B, out.f32(), in.f32(), br_.ls1(), s);
+    br_.norm2->run(out.f32(), rows, h_.f32(), s);
+    br_.ffn->run(h_.f32(), rows, out.f32(), out.f32(), br_.ls2(), s);
+  }
+
+ private:
+  int E_;
+  Branch br_;
+  DevBuf h_;
+};
+
+// Cross-domain transformer bottleneck (CrossTransformerEncoder, Transformer.swift:567-700) with
+// the HTDemucs layer structure: even layers self-attention per branch, odd layers cross-attention
+// in which both branches attend to the other branch's state from before this layer.
+class CrossTransformerImpl : public Layer {
+ public:
+  CrossTransformerImpl(Device* d, int embed, int heads, int ffn, int layers, float ls,
+                       mnn_precision prec)
+      : Layer(d), E_(embed) {
+    MNN_REQUIRE(layers > 0, MNN_ERR_INVALID_CONFIGURATION, "CrossTransformer: num_layers <= 0");
+    for (int i = 0; i < layers; ++i) {
+      const bool cross = (i % 2) == 1;
+      time_.push_back(std::make_unique<Branch>(d, embed, heads, ffn, cross, ls, prec));
+      freq_.push_back(std::make_unique<Branch>(d, embed, heads, ffn, cross, ls, prec));
+    }
+  }
+  const char* kind() const override { return "CrossTransformerEncoder"; }
+  Shape input_shape() const override { return {0, E_}; }
+  Shape output_shape() const override { return {0, E_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE((in.size() == 2 || in.size() == 3) && in.back() == E_, MNN_ERR_SHAPE_MISMATCH,
+                "CrossTransformerEncoder: expected [S, " << E_ << "] or [B, S, " << E_ << "]");
+    return in;
+  }
+  void load(const std::string& name, const float* data, size_t n) override {
+    // layers.{i}.{time|freq}.rest
+    MNN_REQUIRE(name.rfind("layers.", 0) == 0, MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: unknown parameter '" << name << "'");
+    const size_t p1 = name.find('.', 7);
+    MNN_REQUIRE(p1 != std::string::npos, MNN_ERR_INVALID_ARGUMENT, "bad parameter name " << name);
+    const int li = std::atoi(name.substr(7, p1 - 7).c_str());
+    MNN_REQUIRE(li >= 0 && li < (int)time_.size(), MNN_ERR_INVALID_ARGUMENT,
+                "layer index out of range in " << name);
+    const size_t p2 = name.find('.', p1 + 1);
+    MNN_REQUIRE(p2 != std::string::npos, MNN_ERR_INVALID_ARGUMENT, "bad parameter name " << name);
+    const std::string br = name.substr(p1 + 1, p2 - p1 - 1);
+    MNN_REQUIRE(br == "time" || br == "freq", MNN_ERR_INVALID_ARGUMENT,
+                "branch must be time or freq in " << name);
+    Branch& b = br == "time" ? *time_[li] : *freq_[li];
+    MNN_REQUIRE(b.load(name.substr(p2 + 1), data, n), MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: unknown parameter '" << name << "'");
+  }
+  void forward(const Tensor&, Tensor&, Stream&) override {
+    fail(MNN_ERR_INVALID_CONFIGURATION,
+         "CrossTransformerEncoder needs two inputs: use forward_cross(time, freq, ...)");
+  }
+  void forward_cross(const Tensor* t, const Tensor* f, Tensor* to, Tensor* fo,
+                     Stream& s) override {
+    MNN_REQUIRE(t && f && to && fo, MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: time, freq, time_out and freq_out are required");
+    check_out(*to, infer_output(t->shape));
+    check_out(*fo, infer_output(f->shape));
+    int64_t B, St, E, Bf, Sf, Ef;
+    split_bse(t->shape, B, St, E);
+    split_bse(f->shape, Bf, Sf, Ef);
+    MNN_REQUIRE(B == Bf, MNN_ERR_SHAPE_MISMATCH, "time and freq batch sizes differ");
+    const int64_t rt = B * St, rf = B * Sf;
+    if (to->data != t->data) k::copy_bytes(ctx(s), t->data, to->data, rt * E * 4);
+    if (fo->data != f->data) k::copy_bytes(ctx(s), f->data, fo->data, rf * E * 4);
+    float* T = to->f32();
+    float* F = fo->f32();
+    ht_.reserve(sizeof(float) * rt * E * 2);
+    hf_.reserve(sizeof(float) * rf * E * 2);
+    float* ht = ht_.f32();
+    float* ht2 = ht + rt * E;
+    float* hf = hf_.f32();
+    float* hf2 = hf + rf * E;
+    for (size_t i = 0; i < time_.size(); ++i) {
+      Branch& bt = *time_[i];
+      Branch& bf = *freq_[i];
+      if (!bt.cross) {
+        bt.norm1->run(T, rt, ht, s);
+        bt.attn->run(ht, (int)St, nullptr, 0, (int)B, T, T, bt.ls1(), s);
+        bt.norm2->run(T, rt, ht, s);
+        bt.ffn->run(ht, rt, T, T, bt.ls2(), s);
+        bf.norm1->run(F, rf, hf, s);
+        bf.attn->run(hf, (int)Sf, nullptr, 0, (int)B, F, F, bf.ls1(), s);
+        bf.norm2->run(F, rf, hf, s);
+        bf.ffn->run(hf, rf, F, F, bf.ls2(), s);
+      } else {
+        // all four normalisations read the states from before this layer
+        bt.norm1->run(T, rt, ht, s);   // time queries
+        bt.norm2->run(F, rf, hf2, s);  // freq as time's keys/values
+        bf.norm1->run(F, rf, hf, s);   // freq queries
+        bf.norm2->run(T, rt, ht2, s);  // time as freq's keys/values
+        bt.attn->run(ht, (int)St, hf2, (int)Sf, (int)B, T, T, bt.ls1(), s);
+        bf.attn->run(hf, (int)Sf, ht2, (int)St, (int)B, F, F, bf.ls1(), s);
+        bt.ffn_norm()->run(T, rt, ht, s);
+        bt.ffn->run(ht, rt, T, T, bt.ls2(), s);
+        bf.ffn_norm()->run(F, rf, hf, s);
+        bf.ffn->run(hf, rf, F, F, bf.ls2(), s);
+      }
+    }
+  }
+
+ private:
+  int E_;
+  std::vector<std::unique_ptr<Branch>> time_, freq_;
+  DevBuf ht_, hf_;
+};
+
+// ------------------------------------------------------------------ factories
+std::unique_ptr<Layer> make_conv1d(Device* d, const mnn_conv1d_desc& desc) {
+  return std::make_unique<Conv1DLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_groupnorm(Device* d, int groups, int channels, float eps, bool affine,
+                                      int act) {
+  return std::make_unique<GroupNormLayer>(d, groups, channels, eps, affine, act);
+}
+std::unique_ptr<Layer> make_layernorm(Device* d, int features, float eps) {
+  return std::make_unique<LayerNormLayer>(d, features, eps);
+}
+std::unique_ptr<Layer> make_gelu(Device* d, const Shape& shape) {
+  return std::make_unique<GELULayer>(d, shape);
+}
+std::unique_ptr<Layer> make_glu(Device* d, int out_channels) {
+  return std::make_unique<GLULayer>(d, out_channels);
+}
+std::unique_ptr<Layer> make_linear(Device* d, int in, int out, bool bias, int act,
+                                   mnn_precision prec) {
+  return std::make_unique<LinearLayer>(d, in, out, bias, act, prec);
+}
+std::unique_ptr<Layer> make_mha(Device* d, int embed, int heads, bool bias, mnn_precision prec) {
+  return std::make_unique<MHALayer>(d, embed, heads, bias, prec);
+}
+std::unique_ptr<Layer> make_feedforward(Device* d, int in, int hidden, mnn_precision prec) {
+  return std::make_unique<FeedForwardLayer>(d, in, hidden, prec);
+}
+std::unique_ptr<Layer> make_encoder_block(Device* d, const mnn_encoder_block_desc& desc) {
+  return std::make_unique<EncoderBlockLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, int ffn,
+                                              float layer_scale, mnn_precision prec) {
+  return std::make_unique<TransformerLayerImpl>(d, embed, heads, ffn, layer_scale, prec);
+}
+std::unique_ptr<Layer> make_cross_transformer(Device* d, int embed, int heads, int ffn,
+                                              int layers, float layer_scale, mnn_precision prec) {
+  return std::make_unique<CrossTransformerImpl>(d, embed, heads, ffn, layers, layer_scale, prec);
+}
+
+}  // namespace mnn

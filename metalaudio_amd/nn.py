@@ -1,0 +1,450 @@
+"""Python mirror of the reference's MetalNN layer API over the C ABI (include/mnn.h).
+
+Names and argument meanings follow Sources/MetalNN (Conv1D.swift, DynamicConv1D.swift,
+Normalization.swift, Activations.swift, Linear.swift, Attention.swift, Transformer.swift,
+UNet.swift, Model.swift); errors surface as MNNError carrying the mnn_status code that stands in
+for the reference's MetalAudioError / SequentialModelError cases. All compute runs in
+libmnn.so's HIP kernels; this module only marshals arguments.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Iterable, Optional, Sequence
+
+import numpy as np
+
+from ._lib import ACT, PAD, PRECISION, Conv1dDesc, EncoderBlockDesc, MNNError, check, dims, lib
+
+__all__ = [
+    "MNNError", "AudioDevice", "Stream", "Tensor", "Layer", "Conv1D", "DynamicConv1D",
+    "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
+    "FeedForward", "UNetEncoderBlock", "TransformerLayer", "CrossTransformerEncoder",
+    "Sequential", "mfma_probe",
+]
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+class AudioDevice:
+    """A HIP device (AudioDevice.swift:323-348)."""
+
+    def __init__(self, ordinal: int = 0):
+        h = C.c_void_p()
+        check(lib().mnn_device_create(ordinal, C.byref(h)))
+        self.handle = h
+        self._default_stream = None
+
+    @property
+    def name(self) -> str:
+        buf = C.create_string_buffer(256)
+        check(lib().mnn_device_name(self.handle, buf, 256))
+        return buf.value.decode()
+
+    def synchronize(self) -> None:
+        check(lib().mnn_device_synchronize(self.handle))
+
+    def mark_lost(self) -> None:
+        check(lib().mnn_device_mark_lost(self.handle))
+
+    def check_available(self, timeout_ms: int = 1000) -> None:
+        check(lib().mnn_device_check_available(self.handle, timeout_ms))
+
+    def set_kernel_timing(self, enable: bool) -> None:
+        check(lib().mnn_device_set_kernel_timing(self.handle, int(bool(enable))))
+
+    def kernel_timing(self, substr: str = "") -> tuple[int, float]:
+        """(launches, total ms) of timed kernels whose name contains `substr`."""
+        n = C.c_int64()
+        ms = C.c_double()
+        check(lib().mnn_device_kernel_timing(self.handle, substr.encode(), C.byref(n), C.byref(ms)))
+        return n.value, ms.value
+
+    def reset_kernel_timing(self) -> None:
+        check(lib().mnn_device_reset_kernel_timing(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().mnn_device_destroy(self.handle))
+            self.handle = None
+
+
+class Stream:
+    """An in-order HIP stream: the command buffer + encoder of ComputeContext."""
+
+    def __init__(self, device: AudioDevice):
+        h = C.c_void_p()
+        check(lib().mnn_stream_create(device.handle, C.byref(h)))
+        self.handle = h
+        self.device = device
+
+    def sync(self, timeout_ms: int = 0) -> None:
+        """Waits for the stream; MNN_ERR_GPU_TIMEOUT after timeout_ms (> 0)."""
+        check(lib().mnn_stream_sync(self.handle, int(timeout_ms)))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().mnn_stream_destroy(self.handle))
+            self.handle = None
+
+
+def _sh(stream: Optional[Stream]):
+    return stream.handle if stream is not None else None
+
+
+class Tensor:
+    """Device tensor, contiguous row-major fp32, zero-initialised (Tensor.swift:59-141)."""
+
+    def __init__(self, device: AudioDevice, shape: Sequence[int], _handle=None, _owned=True):
+        self.device = device
+        if _handle is None:
+            h = C.c_void_p()
+            shape = [int(s) for s in shape]
+            check(lib().mnn_tensor_create(device.handle, 0, len(shape), dims(shape), C.byref(h)))
+            _handle = h
+        self.handle = _handle
+        self._owned = _owned
+
+    @classmethod
+    def from_numpy(cls, device: AudioDevice, arr, stream: Optional[Stream] = None) -> "Tensor":
+        a = _f32(arr)
+        t = cls(device, a.shape)
+        t.copy_from(a, stream)
+        return t
+
+    @property
+    def shape(self) -> tuple[int, ...]:
+        r = C.c_int()
+        d = dims([])
+        check(lib().mnn_tensor_shape(self.handle, C.byref(r), d))
+        return tuple(d[i] for i in range(r.value))
+
+    @property
+    def count(self) -> int:
+        return int(np.prod(self.shape))
+
+    def reshape(self, shape: Sequence[int]) -> None:
+        check(lib().mnn_tensor_reshape(self.handle, len(shape), dims(shape)))
+
+    def copy_from(self, arr, stream: Optional[Stream] = None) -> None:
+        """Tensor.copy(from:) — synchronous upload."""
+        a = _f32(arr)
+        check(lib().mnn_tensor_upload(self.handle, a.ctypes.data, a.nbytes, _sh(stream)))
+
+    def to_numpy(self, stream: Optional[Stream] = None) -> np.ndarray:
+        """toArray() — synchronous download, shaped like the tensor."""
+        out = np.empty(self.shape, dtype=np.float32)
+        check(lib().mnn_tensor_download(self.handle, out.ctypes.data, out.nbytes, _sh(stream)))
+        return out
+
+    def copy_to(self, dst: "Tensor", stream: Optional[Stream] = None) -> None:
+        check(lib().mnn_tensor_copy(dst.handle, self.handle, _sh(stream)))
+
+    @property
+    def device_ptr(self) -> int:
+        p = C.c_void_p()
+        check(lib().mnn_tensor_device_ptr(self.handle, C.byref(p)))
+        return p.value or 0
+
+    def close(self) -> None:
+        if self.handle and self._owned:
+            check(lib().mnn_tensor_destroy(self.handle))
+        self.handle = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None) and self._owned and lib is not None:
+                lib().mnn_tensor_destroy(self.handle)
+        except Exception:
+            pass
+
+
+class Layer:
+    """The NNLayer protocol (NNLayer.swift:12-16) over a C-ABI layer handle."""
+
+    def __init__(self, device: AudioDevice, handle):
+        self.device = device
+        self.handle = handle
+
+    def load_weights_named(self, name: str, values) -> None:
+        a = _f32(values).ravel()
+        check(lib().mnn_layer_load_weights(
+            self.handle, name.encode(), a.ctypes.data_as(C.POINTER(C.c_float)), a.size))
+
+    def forward(self, input: Tensor, output: Tensor, stream: Optional[Stream] = None) -> None:
+        check(lib().mnn_layer_forward(self.handle, input.handle, output.handle, _sh(stream)))
+
+    def _shape(self, fn) -> tuple[int, ...]:
+        r = C.c_int()
+        d = dims([])
+        check(fn(self.handle, C.byref(r), d))
+        return tuple(d[i] for i in range(r.value))
+
+    @property
+    def input_shape(self) -> tuple[int, ...]:
+        return self._shape(lib().mnn_layer_input_shape)
+
+    @property
+    def output_shape(self) -> tuple[int, ...]:
+        return self._shape(lib().mnn_layer_output_shape)
+
+    def infer_output_shape(self, shape: Sequence[int]) -> tuple[int, ...]:
+        r = C.c_int()
+        d = dims([])
+        check(lib().mnn_layer_infer_output_shape(self.handle, len(shape), dims(shape), C.byref(r), d))
+        return tuple(d[i] for i in range(r.value))
+
+    def __call__(self, input: Tensor, stream: Optional[Stream] = None) -> Tensor:
+        """Allocates the output, runs forward, returns the output tensor."""
+        out = Tensor(self.device, self.infer_output_shape(input.shape))
+        self.forward(input, out, stream)
+        return out
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().mnn_layer_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", None):
+                lib().mnn_layer_destroy(self.handle)
+        except Exception:
+            pass
+
+
+def _create(fn, *args) -> C.c_void_p:
+    h = C.c_void_p()
+    check(fn(*args, C.byref(h)))
+    return h
+
+
+class Conv1D(Layer):
+    """Conv1D (Conv1D.swift:56-103) with FusedConv1D's activation; weight [out, in/groups, k]."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1, padding=0,
+                 dilation=1, groups=1, use_bias=True, input_length=0, padding_mode=None,
+                 activation="none", precision="f32"):
+        if padding_mode is None:
+            padding_mode = "explicit"
+        d = Conv1dDesc(input_channels, output_channels, kernel_size, stride, padding, dilation,
+                       groups, int(use_bias), int(input_length), PAD[padding_mode], ACT[activation],
+                       PRECISION[precision])
+        super().__init__(device, _create(lib().mnn_conv1d_create, device.handle, C.byref(d)))
+        self.use_bias = use_bias
+
+    def load_weights(self, weights, bias=None) -> None:
+        self.load_weights_named("weight", weights)
+        if bias is not None and self.use_bias:
+            self.load_weights_named("bias", bias)
+
+
+class DynamicConv1D(Conv1D):
+    """DynamicConv1D (DynamicConv1D.swift:35-403): padding_mode valid/same/explicit/reflect."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1,
+                 padding_mode="valid", padding=0, dilation=1, groups=1, use_bias=True,
+                 activation="none", precision="f32"):
+        super().__init__(device, input_channels, output_channels, kernel_size, stride, padding,
+                         dilation, groups, use_bias, 0, padding_mode, activation, precision)
+
+
+class GroupNorm(Layer):
+    def __init__(self, device, num_groups, num_channels, epsilon=1e-5, affine=True,
+                 activation="none"):
+        super().__init__(device, _create(lib().mnn_groupnorm_create, device.handle, num_groups,
+                                         num_channels, epsilon, int(affine), ACT[activation]))
+
+    def load_parameters(self, weight, bias) -> None:
+        self.load_weights_named("weight", weight)
+        self.load_weights_named("bias", bias)
+
+
+class LayerNorm(Layer):
+    def __init__(self, device, feature_size, epsilon=1e-5):
+        super().__init__(device, _create(lib().mnn_layernorm_create, device.handle, feature_size,
+                                         epsilon))
+
+    def load_parameters(self, gamma, beta) -> None:
+        self.load_weights_named("gamma", gamma)
+        self.load_weights_named("beta", beta)
+
+
+class GELU(Layer):
+    def __init__(self, device, input_shape):
+        super().__init__(device, _create(lib().mnn_gelu_create, device.handle, len(input_shape),
+                                         dims(input_shape)))
+
+
+class GLU(Layer):
+    def __init__(self, device, out_channels):
+        super().__init__(device, _create(lib().mnn_glu_create, device.handle, out_channels))
+
+
+class Linear(Layer):
+    def __init__(self, device, input_features, output_features, use_bias=True, activation="none",
+                 precision="f32"):
+        super().__init__(device, _create(lib().mnn_linear_create, device.handle, input_features,
+                                         output_features, int(use_bias), ACT[activation],
+                                         PRECISION[precision]))
+        self.use_bias = use_bias
+
+    def load_weights(self, weights, bias=None) -> None:
+        self.load_weights_named("weight", weights)
+        if bias is not None and self.use_bias:
+            self.load_weights_named("bias", bias)
+
+
+class MultiHeadAttention(Layer):
+    def __init__(self, device, embed_dim, num_heads, use_bias=True, precision="f32"):
+        super().__init__(device, _create(lib().mnn_mha_create, device.handle, embed_dim,
+                                         num_heads, int(use_bias), PRECISION[precision]))
+        self.use_bias = use_bias
+
+    def load_weights(self, in_proj_weight, in_proj_bias, out_proj_weight, out_proj_bias) -> None:
+        self.load_weights_named("in_proj_weight", in_proj_weight)
+        self.load_weights_named("out_proj_weight", out_proj_weight)
+        if self.use_bias:
+            if in_proj_bias is not None:
+                self.load_weights_named("in_proj_bias", in_proj_bias)
+            if out_proj_bias is not None:
+                self.load_weights_named("out_proj_bias", out_proj_bias)
+
+    def forward_cross(self, query: Tensor, key_value: Tensor, output: Tensor,
+                      stream: Optional[Stream] = None) -> None:
+        check(lib().mnn_layer_forward_cross(self.handle, query.handle, key_value.handle,
+                                            output.handle, None, _sh(stream)))
+
+
+class CrossAttention(MultiHeadAttention):
+    """CrossAttention (Attention.swift:986-1063): Q from one sequence, K/V from another."""
+
+
+class FeedForward(Layer):
+    def __init__(self, device, input_dim, hidden_dim, precision="f32"):
+        super().__init__(device, _create(lib().mnn_feedforward_create, device.handle, input_dim,
+                                         hidden_dim, PRECISION[precision]))
+
+    def load_weights(self, linear1_weight, linear1_bias, linear2_weight, linear2_bias) -> None:
+        self.load_weights_named("linear1.weight", linear1_weight)
+        self.load_weights_named("linear1.bias", linear1_bias)
+        self.load_weights_named("linear2.weight", linear2_weight)
+        self.load_weights_named("linear2.bias", linear2_bias)
+
+
+class UNetEncoderBlock(Layer):
+    """UNetEncoderBlock (UNet.swift:11-174), optionally with the 1x1 C->2C rewrite + GLU."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size=8, stride=4,
+                 num_groups=8, rewrite=False, precision="f32"):
+        d = EncoderBlockDesc(input_channels, output_channels, kernel_size, stride, num_groups,
+                             int(rewrite), PRECISION[precision])
+        super().__init__(device, _create(lib().mnn_encoder_block_create, device.handle, C.byref(d)))
+
+    def load_weights(self, conv_weight, conv_bias, norm_weight, norm_bias, rewrite_weight=None,
+                     rewrite_bias=None) -> None:
+        self.load_weights_named("conv.weight", conv_weight)
+        if conv_bias is not None:
+            self.load_weights_named("conv.bias", conv_bias)
+        self.load_weights_named("norm.weight", norm_weight)
+        self.load_weights_named("norm.bias", norm_bias)
+        if rewrite_weight is not None:
+            self.load_weights_named("rewrite.weight", rewrite_weight)
+        if rewrite_bias is not None:
+            self.load_weights_named("rewrite.bias", rewrite_bias)
+
+    def forward_alloc(self, input: Tensor, stream: Optional[Stream] = None):
+        """forward(input:encoder:) -> (output, skip); the skip is the output itself."""
+        out = self(input, stream)
+        return out, out
+
+
+class TransformerLayer(Layer):
+    """Pre-norm MHSA + FFN layer on one sequence; weights named norm1.*, attn.*, norm2.*,
+    linear1.*, linear2.*, gamma_1.scale, gamma_2.scale."""
+
+    def __init__(self, device, embed_dim, num_heads, ffn_dim, layer_scale=0.0, precision="f32"):
+        super().__init__(device, _create(lib().mnn_transformer_layer_create, device.handle,
+                                         embed_dim, num_heads, ffn_dim, layer_scale,
+                                         PRECISION[precision]))
+
+    def load_state(self, state: dict) -> None:
+        for k, v in state.items():
+            self.load_weights_named(k, v)
+
+
+class CrossTransformerEncoder(Layer):
+    """Cross-domain bottleneck; weights layers.{i}.{time|freq}.{norm1|norm2|norm3|attn|linear1|
+    linear2|gamma_1|gamma_2}.*"""
+
+    def __init__(self, device, embed_dim, num_heads, ffn_dim, num_layers, layer_scale=1e-4,
+                 precision="f32"):
+        super().__init__(device, _create(lib().mnn_cross_transformer_create, device.handle,
+                                         embed_dim, num_heads, ffn_dim, num_layers, layer_scale,
+                                         PRECISION[precision]))
+
+    def load_state(self, state: dict) -> None:
+        for k, v in state.items():
+            self.load_weights_named(k, v)
+
+    def forward_cross(self, time: Tensor, freq: Tensor, time_out: Tensor, freq_out: Tensor,
+                      stream: Optional[Stream] = None) -> None:
+        check(lib().mnn_layer_forward_cross(self.handle, time.handle, freq.handle,
+                                            time_out.handle, freq_out.handle, _sh(stream)))
+
+
+class Sequential:
+    """Sequential (Model.swift:65-357)."""
+
+    def __init__(self, device: AudioDevice):
+        self.device = device
+        self.handle = _create(lib().mnn_sequential_create, device.handle)
+        self._layers: list[Layer] = []
+
+    def add(self, layer: Layer) -> None:
+        check(lib().mnn_sequential_add(self.handle, layer.handle))
+        self._layers.append(layer)
+
+    def add_unchecked(self, layer: Layer) -> None:
+        check(lib().mnn_sequential_add_unchecked(self.handle, layer.handle))
+        self._layers.append(layer)
+
+    def build(self) -> None:
+        check(lib().mnn_sequential_build(self.handle))
+
+    def forward(self, input: Tensor, stream: Optional[Stream] = None) -> Tensor:
+        """Returns the model-owned output (overwritten by the next forward)."""
+        h = C.c_void_p()
+        check(lib().mnn_sequential_forward(self.handle, input.handle, _sh(stream), C.byref(h)))
+        return Tensor(self.device, (), _handle=h, _owned=False)
+
+    @property
+    def buffer_stats(self) -> tuple[int, int]:
+        a, n = C.c_int(), C.c_int()
+        check(lib().mnn_sequential_buffer_stats(self.handle, C.byref(a), C.byref(n)))
+        return a.value, n.value
+
+    @property
+    def layer_count(self) -> int:
+        n = C.c_int()
+        check(lib().mnn_sequential_layer_count(self.handle, C.byref(n)))
+        return n.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().mnn_sequential_destroy(self.handle))
+            self.handle = None
+
+
+def mfma_probe(device: AudioDevice, variant: int, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Raw [lane][register] accumulators of one MFMA instruction (see mnn_debug_mfma_probe)."""
+    na = 1 if variant < 2 else 8
+    nd = 16 if variant in (0, 2) else 4
+    a = _f32(a).reshape(64 * na)
+    b = _f32(b).reshape(64 * na)
+    d = np.zeros(64 * nd, dtype=np.float32)
+    fp = C.POINTER(C.c_float)
+    check(lib().mnn_debug_mfma_probe(device.handle, variant, a.ctypes.data_as(fp),
+                                     b.ctypes.data_as(fp), d.ctypes.data_as(fp)))
+    return d.reshape(64, nd)

@@ -1,0 +1,289 @@
+"""numpy restatement of the MetalNN layer arithmetic (reference: zkeown/MetalAudio).
+
+TEST INFRASTRUCTURE ONLY — see oracle/__init__.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+__all__ = [
+    "reflect_pad", "conv1d", "group_norm", "layer_norm", "gelu_tanh", "gelu_layer",
+    "stable_sigmoid", "glu", "activation", "linear", "mha", "feed_forward", "encoder_block",
+    "time_encoder", "transformer_layer", "cross_transformer",
+]
+
+SQRT_2_OVER_PI = 0.7978845608  # literal used by every reference GELU kernel
+
+
+def _as(x, dtype):
+    return np.asarray(x, dtype=dtype)
+
+
+def reflect_pad(x, pad: int):
+    """Reflect padding along the last axis: left x[p..1], right x[L-2..L-1-p].
+    Follows DynamicConv1D.applyReflectPadding (DynamicConv1D.swift:288-324)."""
+    if pad == 0:
+        return x
+    L = x.shape[-1]
+    if pad >= L:
+        raise ValueError("reflect padding needs input length > padding")
+    left = x[..., pad:0:-1]                 # reflectIdx = padding - i
+    right = x[..., L - 2:L - 2 - pad:-1]    # reflectIdx = inputLength - 2 - i
+    return np.concatenate([left, x, right], axis=-1)
+
+
+def conv1d(x, w, b=None, stride=1, padding=0, dilation=1, groups=1, mode="zeros",
+           dtype=np.float64):
+    """y[b][co][t] = bias[co] + sum_ci sum_k x[b][ci][t*s - p + k*d] * W[co][ci][k].
+
+    Follows dynamic_conv1d_forward (DynamicConv1D.swift:358-401: loops ic then k, bias last)
+    and conv1d_forward (Conv1D.swift:310-512); mode "reflect" pads as DynamicConv1D.swift:288-324,
+    "zeros" as the shaders' bounds test. Input [C, L] or [B, C, L]."""
+    x = _as(x, dtype)
+    w = _as(w, dtype)
+    squeeze = x.ndim == 2
+    if squeeze:
+        x = x[None]
+    B, Cin, L = x.shape
+    Cout, cinpg, K = w.shape
+    if mode == "reflect":
+        xp = reflect_pad(x, padding)
+    else:
+        xp = np.pad(x, ((0, 0), (0, 0), (padding, padding)))
+    eff = (K - 1) * dilation + 1
+    Lout = (xp.shape[-1] - eff) // stride + 1
+    coutpg = Cout // groups
+    y = np.empty((B, Cout, Lout), dtype=dtype)
+    # window view [B, Cin, Lout, K]
+    win = np.lib.stride_tricks.sliding_window_view(xp, eff, axis=-1)[..., ::stride, ::dilation]
+    win = win[:, :, :Lout, :]
+    for g in range(groups):
+        xs = win[:, g * cinpg:(g + 1) * cinpg]                      # [B, cinpg, Lout, K]
+        cols = np.ascontiguousarray(xs.transpose(0, 2, 1, 3)).reshape(B, Lout, cinpg * K)
+        wg = w[g * coutpg:(g + 1) * coutpg].reshape(coutpg, cinpg * K)
+        y[:, g * coutpg:(g + 1) * coutpg] = (cols @ wg.T).transpose(0, 2, 1)
+    if b is not None:
+        y += _as(b, dtype)[None, :, None]
+    return y[0] if squeeze else y
+
+
+def group_norm(x, num_groups, gamma=None, beta=None, eps=1e-5, dtype=np.float64):
+    """Per (batch, group): mean, biased variance over C/G * L; y = gamma*(x-mean)/sqrt(var+eps)+beta.
+    Follows GroupNorm.forwardCPU (Normalization.swift:665-724)."""
+    x = _as(x, dtype)
+    squeeze = x.ndim == 2
+    if squeeze:
+        x = x[None]
+    B, C, L = x.shape
+    xg = x.reshape(B, num_groups, -1)
+    mean = xg.mean(axis=-1, keepdims=True)
+    var = ((xg - mean) ** 2).mean(axis=-1, keepdims=True)
+    inv = 1.0 / np.sqrt(var + eps)
+    y = ((xg - mean) * inv).reshape(B, C, L)
+    if gamma is not None:
+        y = y * _as(gamma, dtype)[None, :, None] + _as(beta, dtype)[None, :, None]
+    return y[0] if squeeze else y
+
+
+def layer_norm(x, gamma=None, beta=None, eps=1e-5, dtype=np.float64):
+    """Per row of the last axis: two-pass mean / biased variance, rsqrt(var + eps), affine.
+    Follows layer_norm_forward (Normalization.swift:804-879)."""
+    x = _as(x, dtype)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if gamma is not None:
+        y = y * _as(gamma, dtype) + _as(beta, dtype)
+    return y
+
+
+def gelu_tanh(x, dtype=np.float64):
+    """0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), the GELU of UNet.swift:118-131 and
+    Transformer.swift:154-158."""
+    x = _as(x, dtype)
+    return 0.5 * x * (1.0 + np.tanh(SQRT_2_OVER_PI * (x + 0.044715 * x ** 3)))
+
+
+def gelu_layer(x, dtype=np.float64):
+    """GELU layer kernel (Activations.swift:124-137): clamp to [-10, 10] for the formula,
+    x > 10 -> x, x < -10 -> 0."""
+    x = _as(x, dtype)
+    c = np.clip(x, -10.0, 10.0)
+    r = 0.5 * c * (1.0 + np.tanh(SQRT_2_OVER_PI * (c + 0.044715 * c ** 3)))
+    return np.where(x > 10.0, x, np.where(x < -10.0, 0.0, r))
+
+
+def stable_sigmoid(x, dtype=np.float64):
+    """Shaders/NN.metal:32-47: clamp to [-88, 88], 1/(1+e^-x) for x >= 0, e^x/(1+e^x) else."""
+    x = np.clip(_as(x, dtype), -88.0, 88.0)
+    pos = 1.0 / (1.0 + np.exp(-x))
+    ex = np.exp(x)
+    neg = ex / (1.0 + ex)
+    return np.where(x >= 0.0, pos, neg)
+
+
+def glu(x, axis=-2, dtype=np.float64):
+    """out = a * sigmoid(b), a the first and b the second half along `axis`
+    (glu kernel, Shaders/NN.metal:1012-1023: input[id] * stable_sigmoid(input[id + size]))."""
+    x = _as(x, dtype)
+    a, b = np.split(x, 2, axis=axis)
+    return a * stable_sigmoid(b, dtype)
+
+
+def activation(x, act: str, dtype=np.float64):
+    """apply_activation of FusedConv1D / FusedLinear (Conv1D.swift:960-973, Linear.swift:630-639)."""
+    x = _as(x, dtype)
+    if act == "none":
+        return x
+    if act == "relu":
+        return np.maximum(x, 0.0)
+    if act == "leaky_relu":
+        return np.where(x >= 0.0, x, 0.01 * x)
+    if act == "gelu":
+        return gelu_tanh(x, dtype)
+    if act == "swish":
+        return x * stable_sigmoid(x, dtype)
+    if act == "sigmoid":
+        return stable_sigmoid(x, dtype)
+    if act == "tanh":
+        return np.tanh(x)
+    raise ValueError(act)
+
+
+def linear(x, w, b=None, act="none", dtype=np.float64):
+    """y = act(x W^T + b), W [out, in] (Linear.swift:337-365; linear_fused_forward :641-670)."""
+    y = _as(x, dtype) @ _as(w, dtype).T
+    if b is not None:
+        y = y + _as(b, dtype)
+    return activation(y, act, dtype)
+
+
+def _softmax_ref(s):
+    """Row softmax as Attention.swift:927-945: exp(s - max) / (sum + 1e-10)."""
+    m = s.max(axis=-1, keepdims=True)
+    e = np.exp(s - m)
+    return e / (e.sum(axis=-1, keepdims=True) + 1e-10)
+
+
+def mha(xq, xkv, in_w, in_b, out_w, out_b, num_heads, dtype=np.float64):
+    """MultiHeadAttention forward, following forwardCPU (Attention.swift:840-976):
+    Q = xq Wq^T + bq, K = xkv Wk^T + bk, V = xkv Wv^T + bv with in_proj rows Q;K;V; head h uses
+    columns [h*hd, (h+1)*hd); P = softmax(Q_h K_h^T / sqrt(hd)); O[:, h*hd+d]; out = O Wo^T + bo.
+    xq [Sq, E] or [B, Sq, E]; xkv likewise (None = self-attention)."""
+    xq = _as(xq, dtype)
+    xkv = xq if xkv is None else _as(xkv, dtype)
+    in_w = _as(in_w, dtype)
+    out_w = _as(out_w, dtype)
+    squeeze = xq.ndim == 2
+    if squeeze:
+        xq, xkv = xq[None], xkv[None]
+    E = xq.shape[-1]
+    hd = E // num_heads
+    scale = 1.0 / np.sqrt(hd)
+    bq = bk = bv = bo = None
+    if in_b is not None:
+        in_b = _as(in_b, dtype)
+        bq, bk, bv = in_b[:E], in_b[E:2 * E], in_b[2 * E:]
+    q = xq @ in_w[:E].T + (bq if bq is not None else 0.0)
+    k = xkv @ in_w[E:2 * E].T + (bk if bk is not None else 0.0)
+    v = xkv @ in_w[2 * E:].T + (bv if bv is not None else 0.0)
+    B, Sq = q.shape[0], q.shape[1]
+    o = np.empty_like(q)
+    for bi in range(B):
+        for h in range(num_heads):
+            cs = slice(h * hd, (h + 1) * hd)
+            s = (q[bi, :, cs] @ k[bi, :, cs].T) * scale
+            o[bi, :, cs] = _softmax_ref(s) @ v[bi, :, cs]
+    out = o @ out_w.T
+    if out_b is not None:
+        out = out + _as(out_b, dtype)
+    return out[0] if squeeze else out
+
+
+def feed_forward(x, w1, b1, w2, b2, dtype=np.float64):
+    """Linear1 -> tanh-GELU -> Linear2 (FeedForward.forwardCPU, Transformer.swift:315-363)."""
+    h = gelu_tanh(linear(x, w1, b1, dtype=dtype), dtype)
+    return linear(h, w2, b2, dtype=dtype)
+
+
+def encoder_block(x, conv_w, conv_b, norm_w, norm_b, num_groups, kernel_size=8, stride=4,
+                  rewrite_w=None, rewrite_b=None, dtype=np.float64):
+    """UNetEncoderBlock.forward (UNet.swift:80-100): DynamicConv1D with reflect padding
+    (k-1)//2 (UNet.swift:52) -> GroupNorm -> tanh-GELU; with a rewrite weight [2C, C, 1], then
+    the 1x1 conv C -> 2C and GLU over channels (NN.metal:1012-1023)."""
+    pad = (kernel_size - 1) // 2
+    y = conv1d(x, conv_w, conv_b, stride=stride, padding=pad, mode="reflect", dtype=dtype)
+    y = gelu_tanh(group_norm(y, num_groups, norm_w, norm_b, dtype=dtype), dtype)
+    if rewrite_w is None:
+        return y
+    z = conv1d(y, rewrite_w, rewrite_b, stride=1, padding=0, dtype=dtype)
+    return glu(z, axis=-2, dtype=dtype)
+
+
+def time_encoder(x, levels, dtype=np.float64):
+    """Chained encoder levels composed in program order (each level sees the previous level's
+    real output)."""
+    y = _as(x, dtype)
+    for lv in levels:
+        y = encoder_block(y, lv["conv.weight"], lv["conv.bias"], lv["norm.weight"],
+                          lv["norm.bias"], 1, rewrite_w=lv["rewrite.weight"],
+                          rewrite_b=lv["rewrite.bias"], dtype=dtype)
+    return y
+
+
+def _attn_args(p, pre):
+    return (p[pre + "in_proj_weight"], p.get(pre + "in_proj_bias"), p[pre + "out_proj_weight"],
+            p.get(pre + "out_proj_bias"))
+
+
+def transformer_layer(x, p, num_heads, layer_scale=0.0, dtype=np.float64):
+    """Pre-norm layer: y = x + g1*MHA(LN1 x); z = y + g2*FFN(LN2 y) (Transformer.swift:467-495
+    sub-blocks 1 and 5; LayerScale g = layer_scale when > 0, else 1)."""
+    x = _as(x, dtype)
+    g1 = p.get("gamma_1.scale", layer_scale if layer_scale > 0 else 1.0)
+    g2 = p.get("gamma_2.scale", layer_scale if layer_scale > 0 else 1.0)
+    h = layer_norm(x, p["norm1.weight"], p["norm1.bias"], dtype=dtype)
+    y = x + _as(g1, dtype) * mha(h, None, *_attn_args(p, "attn."), num_heads, dtype=dtype)
+    h = layer_norm(y, p["norm2.weight"], p["norm2.bias"], dtype=dtype)
+    ff = feed_forward(h, p["linear1.weight"], p["linear1.bias"], p["linear2.weight"],
+                      p["linear2.bias"], dtype=dtype)
+    return y + _as(g2, dtype) * ff
+
+
+def cross_transformer(time, freq, p, num_layers, num_heads, dtype=np.float64):
+    """Cross-domain bottleneck, HTDemucs layer structure: layer i even -> self-attention per
+    branch; odd -> cross-attention where time attends to freq and freq to time, both reading the
+    other branch's state from before the layer. Per branch:
+    self : x += g1*MHA(LN1 x);           x += g2*FFN(LN2 x)
+    cross: x += g1*MHA(LN1 x, LN2 other); x += g2*FFN(LN3 x)."""
+    T = _as(time, dtype)
+    F = _as(freq, dtype)
+
+    def ln(x, pre):
+        return layer_norm(x, p[pre + ".weight"], p[pre + ".bias"], dtype=dtype)
+
+    def ffn(x, pre):
+        return feed_forward(x, p[pre + "linear1.weight"], p[pre + "linear1.bias"],
+                            p[pre + "linear2.weight"], p[pre + "linear2.bias"], dtype=dtype)
+
+    for i in range(num_layers):
+        pt, pf = f"layers.{i}.time.", f"layers.{i}.freq."
+        if i % 2 == 0:
+            new = []
+            for X, pre in ((T, pt), (F, pf)):
+                X = X + _as(p[pre + "gamma_1.scale"], dtype) * mha(
+                    ln(X, pre + "norm1"), None, *_attn_args(p, pre + "attn."), num_heads, dtype)
+                X = X + _as(p[pre + "gamma_2.scale"], dtype) * ffn(ln(X, pre + "norm2"), pre)
+                new.append(X)
+            T, F = new
+        else:
+            Tn = T + _as(p[pt + "gamma_1.scale"], dtype) * mha(
+                ln(T, pt + "norm1"), ln(F, pt + "norm2"), *_attn_args(p, pt + "attn."),
+                num_heads, dtype)
+            Fn = F + _as(p[pf + "gamma_1.scale"], dtype) * mha(
+                ln(F, pf + "norm1"), ln(T, pf + "norm2"), *_attn_args(p, pf + "attn."),
+                num_heads, dtype)
+            Tn = Tn + _as(p[pt + "gamma_2.scale"], dtype) * ffn(ln(Tn, pt + "norm3"), pt)
+            Fn = Fn + _as(p[pf + "gamma_2.scale"], dtype) * ffn(ln(Fn, pf + "norm3"), pf)
+            T, F = Tn, Fn
+    return T, F

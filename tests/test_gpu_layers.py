@@ -1,0 +1,449 @@
+"""GPU parity of every hot-path layer against the fp64 oracle, through the C ABI.
+
+fp32 bar (stated by the path's spec): |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| per element.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from metalaudio_amd import nn
+from metalaudio_amd import workloads
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 1e-4, 1e-3
+RNG = np.random.default_rng(11)
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    d = nn.AudioDevice(0)
+    yield d
+
+
+@pytest.fixture(scope="module")
+def stream(dev):
+    s = nn.Stream(dev)
+    yield s
+
+
+def run_layer(layer, x, dev, stream):
+    xt = nn.Tensor.from_numpy(dev, x)
+    out = layer(xt, stream)
+    stream.sync(60000)
+    return out.to_numpy()
+
+
+# ----------------------------------------------------------------------------- MFMA layouts
+def _expected_raw(variant, a, b):
+    """Expected raw registers under the lane layouts the kernels are written against."""
+    lanes = np.arange(64)
+    if variant in (0, 2):
+        M = 32
+        kper = 1 if variant == 0 else 8
+        K = 2 * kper
+        A = np.zeros((32, K))
+        B = np.zeros((K, 32))
+        for l in lanes:
+            for t in range(kper):
+                A[l % 32, kper * (l // 32) + t] = a[l * kper + t]
+                B[kper * (l // 32) + t, l % 32] = b[l * kper + t]
+        D = A @ B
+        raw = np.zeros((64, 16))
+        for l in lanes:
+            for v in range(16):
+                raw[l, v] = D[8 * (v // 4) + 4 * (l // 32) + v % 4, l % 32]
+        return raw
+    kper = 1 if variant == 1 else 8
+    K = 4 * kper
+    A = np.zeros((16, K))
+    B = np.zeros((K, 16))
+    for l in lanes:
+        for t in range(kper):
+            A[l % 16, kper * (l // 16) + t] = a[l * kper + t]
+            B[kper * (l // 16) + t, l % 16] = b[l * kper + t]
+    D = A @ B
+    raw = np.zeros((64, 4))
+    for l in lanes:
+        for v in range(4):
+            raw[l, v] = D[4 * (l // 16) + v, l % 16]
+    return raw
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+def test_mfma_lane_layout(dev, variant):
+    say(f"mfma probe variant {variant}")
+    n = 64 if variant < 2 else 512
+    # small integers / 4: exact in bf16 and in fp32 products and sums
+    a = RNG.integers(-8, 9, n).astype(np.float32) / 4
+    b = RNG.integers(-8, 9, n).astype(np.float32) / 4
+    got = nn.mfma_probe(dev, variant, a, b)
+    np.testing.assert_array_equal(got, _expected_raw(variant, a.astype(np.float64),
+                                                      b.astype(np.float64)))
+
+
+# ----------------------------------------------------------------------------- Conv1D
+CONV_CASES = [
+    # B, cin, cout, k, s, p, d, g, mode, act, L
+    (1, 2, 48, 8, 4, 0, 1, 1, "explicit", "none", 44100),      # config 1 conv (direct)
+    (1, 2, 48, 8, 4, 3, 1, 1, "reflect", "none", 4099),        # level-1 conv, ragged length
+    (2, 48, 96, 8, 4, 3, 1, 1, "reflect", "none", 1031),       # implicit-GEMM MFMA, reflect
+    (1, 96, 192, 8, 4, 3, 1, 1, "reflect", "gelu", 517),       # MFMA + fused GELU
+    (1, 16, 32, 4, 1, 2, 1, 1, "explicit", "relu", 300),       # MFMA, zero padding
+    (1, 6, 12, 5, 2, 2, 2, 3, "explicit", "swish", 203),       # groups + dilation (direct)
+    (1, 1, 1, 3, 1, 1, 1, 1, "explicit", "none", 5),           # tiny
+    (1, 8, 8, 3, 1, 0, 1, 1, "valid", "leaky_relu", 50),
+    (1, 4, 16, 4, 2, 0, 1, 1, "same", "tanh", 33),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[str(c) for c in CONV_CASES])
+def test_conv1d_parity(dev, stream, case):
+    B, cin, cout, k, s, p, d, g, mode, act, L = case
+    say(f"conv1d {case}")
+    x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin // g, k)) * np.sqrt(2 / (cin // g * k))).astype(np.float32)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    layer = nn.DynamicConv1D(dev, cin, cout, k, s, padding_mode=mode, padding=p, dilation=d,
+                             groups=g, activation=act)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    if mode == "same":
+        eff = (k - 1) * d + 1
+        lo = -(-L // s)
+        p = max(0, (lo - 1) * s + eff - L) // 2
+    elif mode == "valid":
+        p = 0
+    ref = oracle.conv1d(x, w, b, stride=s, padding=p, dilation=d, groups=g,
+                        mode="reflect" if mode == "reflect" else "zeros")
+    ref = oracle.activation(ref, act)
+    assert_close(got, ref, ATOL, RTOL, f"conv {case}")
+
+
+def test_conv1d_closed_forms(dev, stream):
+    """Conv1DTests.swift:66-146: identity and averaging kernels, fixed-length Conv1D, padding 1."""
+    say("conv closed forms")
+    c = nn.Conv1D(dev, 1, 1, 3, padding=1, use_bias=False, input_length=5)
+    c.load_weights([0, 1, 0])
+    np.testing.assert_allclose(run_layer(c, np.array([[1, 2, 3, 4, 5.0]]), dev, stream),
+                               [[1, 2, 3, 4, 5]], atol=1e-6)
+    c.load_weights([1 / 3, 1 / 3, 1 / 3])
+    np.testing.assert_allclose(run_layer(c, np.full((1, 5), 3.0), dev, stream),
+                               [[2, 3, 3, 3, 2]], atol=1e-6)
+    assert c.output_shape == (1, 5)
+
+
+# ----------------------------------------------------------------------------- norms / activations
+@pytest.mark.parametrize("B,C,L,G,act", [(1, 48, 11024, 1, "gelu"), (2, 48, 1000, 8, "none"),
+                                         (1, 96, 4097, 3, "gelu"), (1, 4, 7, 2, "none")])
+def test_groupnorm_parity(dev, stream, B, C, L, G, act):
+    say(f"groupnorm {B, C, L, G, act}")
+    x = (RNG.standard_normal((B, C, L)) * 3 + 0.7).astype(np.float32)
+    gm = (1 + 0.2 * RNG.standard_normal(C)).astype(np.float32)
+    bt = (0.2 * RNG.standard_normal(C)).astype(np.float32)
+    layer = nn.GroupNorm(dev, G, C, activation=act)
+    layer.load_parameters(gm, bt)
+    got = run_layer(layer, x, dev, stream)
+    ref = oracle.activation(oracle.group_norm(x, G, gm, bt), act)
+    assert_close(got, ref, ATOL, RTOL, "groupnorm")
+
+
+@pytest.mark.parametrize("rows,F", [(4, 4), (1000, 384), (333, 512), (2048, 2048), (17, 100)])
+def test_layernorm_parity(dev, stream, rows, F):
+    say(f"layernorm {rows}x{F}")
+    x = (RNG.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
+    gm = (1 + 0.2 * RNG.standard_normal(F)).astype(np.float32)
+    bt = (0.2 * RNG.standard_normal(F)).astype(np.float32)
+    layer = nn.LayerNorm(dev, F)
+    layer.load_parameters(gm, bt)
+    got = run_layer(layer, x, dev, stream)
+    assert_close(got, oracle.layer_norm(x, gm, bt), ATOL, RTOL, "layernorm")
+
+
+def test_layernorm_closed_form(dev, stream):
+    """IntegrationTests.swift:336-374."""
+    say("layernorm closed form")
+    got = run_layer(nn.LayerNorm(dev, 4), np.array([1.0, 2, 3, 4]), dev, stream)
+    np.testing.assert_allclose(got, [-1.3416407, -0.4472136, 0.4472136, 1.3416407], atol=1e-4)
+
+
+def test_gelu_parity_and_table(dev, stream):
+    """IntegrationTests.swift:28-67 table at 1e-3, clamp semantics, and random values."""
+    say("gelu")
+    x = np.array([-3.0, -2.0, -1.0, -0.5, 0.0, 0.5, 1.0, 2.0, 3.0, 5.0], np.float32)
+    got = run_layer(nn.GELU(dev, [10]), x, dev, stream)
+    exp = [-0.00364, -0.04550, -0.1588, -0.1543, 0.0, 0.3457, 0.8412, 1.9546, 2.9964, 5.0]
+    assert np.all(np.abs(got - exp) <= 1e-3)
+    x = np.concatenate([RNG.standard_normal(100003) * 4, [-50, -10.5, 10.5, 50]]).astype(np.float32)
+    got = run_layer(nn.GELU(dev, [x.size]), x, dev, stream)
+    assert_close(got, oracle.gelu_layer(x), ATOL, RTOL, "gelu")
+    assert got[-4] == 0.0 and got[-1] == 50.0
+
+
+def test_glu_parity(dev, stream):
+    say("glu")
+    x = (RNG.standard_normal((2, 64, 1001)) * 5).astype(np.float32)
+    got = run_layer(nn.GLU(dev, 32), x, dev, stream)
+    assert_close(got, oracle.glu(x, axis=-2), ATOL, RTOL, "glu")
+
+
+# ----------------------------------------------------------------------------- Linear
+@pytest.mark.parametrize("shape,nin,nout,act", [
+    ((2048, 512), 512, 2048, "none"), ((5, 7, 384), 384, 1536, "gelu"), ((300, 37), 37, 50, "relu"),
+    ((130, 64), 64, 96, "sigmoid"), ((64,), 64, 33, "tanh")])
+def test_linear_parity(dev, stream, shape, nin, nout, act):
+    say(f"linear {shape} {nin}->{nout} {act}")
+    x = RNG.standard_normal(shape).astype(np.float32)
+    w = (RNG.standard_normal((nout, nin)) * 0.05).astype(np.float32)
+    b = (RNG.standard_normal(nout) * 0.1).astype(np.float32)
+    layer = nn.Linear(dev, nin, nout, activation=act)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    assert_close(got, oracle.linear(x, w, b, act=act), ATOL, RTOL, "linear")
+
+
+def test_linear_closed_forms(dev, stream):
+    """IntegrationTests.swift:259-324."""
+    say("linear closed forms")
+    l = nn.Linear(dev, 3, 2)
+    l.load_weights([1, 2, 3, 4, 5, 6], [0.1, 0.2])
+    np.testing.assert_allclose(run_layer(l, np.array([1.0, 2, 3]), dev, stream), [14.1, 32.2],
+                               atol=1e-4)
+    l2 = nn.Linear(dev, 3, 2, use_bias=False)
+    l2.load_weights([1, 0, 0, 0, 1, 0])
+    np.testing.assert_allclose(run_layer(l2, np.array([[1.0, 2, 3], [4, 5, 6]]), dev, stream),
+                               [[1, 2], [4, 5]], atol=1e-4)
+
+
+# ----------------------------------------------------------------------------- attention
+MHA_CASES = [
+    # B, E, H, Sq, Sk, cross
+    (1, 512, 8, 300, 300, False),     # hd 64, ragged 64-blocks
+    (2, 384, 8, 200, 200, False),     # hd 48
+    (1, 384, 8, 130, 257, True),      # cross, Sq != Sk
+    (2, 384, 8, 700, 90, True),       # cross, short keys
+    (1, 64, 4, 33, 33, False),        # hd 16 (generic kernel)
+    (1, 512, 8, 1, 1, False),         # single token
+]
+
+
+@pytest.mark.parametrize("case", MHA_CASES, ids=[str(c) for c in MHA_CASES])
+def test_mha_parity(dev, stream, case):
+    B, E, H, Sq, Sk, cross = case
+    say(f"mha {case}")
+    w_in = (RNG.standard_normal((3 * E, E)) * 0.05).astype(np.float32)
+    b_in = (RNG.standard_normal(3 * E) * 0.05).astype(np.float32)
+    w_out = (RNG.standard_normal((E, E)) * 0.05).astype(np.float32)
+    b_out = (RNG.standard_normal(E) * 0.05).astype(np.float32)
+    q = RNG.standard_normal((B, Sq, E)).astype(np.float32)
+    kv = RNG.standard_normal((B, Sk, E)).astype(np.float32)
+    layer = nn.MultiHeadAttention(dev, E, H)
+    layer.load_weights(w_in, b_in, w_out, b_out)
+    qt = nn.Tensor.from_numpy(dev, q)
+    out = nn.Tensor(dev, q.shape)
+    if cross:
+        layer.forward_cross(qt, nn.Tensor.from_numpy(dev, kv), out, stream)
+    else:
+        layer.forward(qt, out, stream)
+    stream.sync(60000)
+    ref = oracle.mha(q, kv if cross else None, w_in, b_in, w_out, b_out, H)
+    assert_close(out.to_numpy(), ref, ATOL, RTOL, "mha")
+
+
+def test_feedforward_parity(dev, stream):
+    say("feedforward")
+    E, Hd = 384, 1536
+    x = RNG.standard_normal((3, 257, E)).astype(np.float32)
+    w1 = (RNG.standard_normal((Hd, E)) * 0.05).astype(np.float32)
+    b1 = (RNG.standard_normal(Hd) * 0.05).astype(np.float32)
+    w2 = (RNG.standard_normal((E, Hd)) * 0.05).astype(np.float32)
+    b2 = (RNG.standard_normal(E) * 0.05).astype(np.float32)
+    f = nn.FeedForward(dev, E, Hd)
+    f.load_weights(w1, b1, w2, b2)
+    got = run_layer(f, x, dev, stream)
+    assert_close(got, oracle.feed_forward(x, w1, b1, w2, b2), ATOL, RTOL, "ffn")
+
+
+# ----------------------------------------------------------------------------- blocks
+@pytest.mark.parametrize("name", ["time_encoder_level0", "time_encoder_level1"])
+def test_encoder_block_reference_fixture(dev, stream, golden_dir, name):
+    """The reference's own fixtures (HTDemucsValidationTests.swift:37-117): abs 1e-4 or rel 1e-3."""
+    say(f"encoder fixture {name}")
+    d = np.load(golden_dir / f"{name}.npz")
+    cin, cout, k, s, g = (int(v) for v in d["config"])
+    blk = nn.UNetEncoderBlock(dev, cin, cout, k, s, g)
+    blk.load_weights(d["conv_weight"], d["conv_bias"], d["norm_weight"], d["norm_bias"])
+    got = run_layer(blk, d["input"], dev, stream)
+    ref = d["output"].astype(np.float64)
+    err = np.abs(got - ref)
+    assert np.all((err <= 1e-4) | (err <= 1e-3 * np.abs(ref))), f"max abs {err.max():.3e}"
+
+
+@pytest.mark.parametrize("cin,cout,L,B", [(2, 48, 5000, 1), (48, 96, 3001, 2), (192, 384, 700, 1),
+                                          (8, 24, 400, 1)])
+def test_encoder_block_rewrite_parity(dev, stream, cin, cout, L, B):
+    say(f"encoder block rewrite {cin}->{cout} L={L} B={B}")
+    x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin, 8)) * np.sqrt(2 / (cin * 8))).astype(np.float32)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    rw = (RNG.standard_normal((2 * cout, cout, 1)) * np.sqrt(2 / cout)).astype(np.float32)
+    rb = (RNG.standard_normal(2 * cout) * 0.1).astype(np.float32)
+    blk = nn.UNetEncoderBlock(dev, cin, cout, 8, 4, 1, rewrite=True)
+    blk.load_weights(w, b, gm, bt, rw, rb)
+    got = run_layer(blk, x, dev, stream)
+    ref = oracle.encoder_block(x, w, b, gm, bt, 1, rewrite_w=rw, rewrite_b=rb)
+    assert_close(got, ref, ATOL, RTOL, "encoder block")
+
+
+def test_transformer_layer_parity(dev, stream):
+    say("transformer layer (config 3 shape, seq 333, stress params)")
+    cfg = workloads.config3(stress=True, seq=333)
+    t = nn.TransformerLayer(dev, cfg["embed"], cfg["heads"], cfg["ffn"])
+    t.load_state(cfg["params"])
+    got = run_layer(t, cfg["x"], dev, stream)
+    assert_close(got, oracle.transformer_layer(cfg["x"], cfg["params"], cfg["heads"]), ATOL, RTOL,
+                 "transformer layer")
+
+
+def test_cross_transformer_parity_strong_layerscale(dev, stream):
+    say("cross transformer small, LayerScale 0.5")
+    cfg = workloads.config5(stress=True, batch=2, time_len=150, freq_len=301, layers=4)
+    p = dict(cfg["params"])
+    for k in p:
+        if "gamma_" in k:
+            p[k] = np.full_like(p[k], 0.5)
+    ct = nn.CrossTransformerEncoder(dev, cfg["embed"], cfg["heads"], cfg["ffn"], 4, 1e-4)
+    ct.load_state(p)
+    tt, ft = nn.Tensor.from_numpy(dev, cfg["time"]), nn.Tensor.from_numpy(dev, cfg["freq"])
+    to, fo = nn.Tensor(dev, tt.shape), nn.Tensor(dev, ft.shape)
+    ct.forward_cross(tt, ft, to, fo, stream)
+    stream.sync(60000)
+    rt, rf = oracle.cross_transformer(cfg["time"], cfg["freq"], p, 4, cfg["heads"])
+    assert_close(to.to_numpy(), rt, ATOL, RTOL, "time branch")
+    assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
+
+
+# ----------------------------------------------------------------------------- Sequential / errors
+def test_sequential_pingpong_and_forward(dev, stream):
+    """ModelTests.swift:114-162: 6 same-shape layers use <= 2 buffers; 3 shapes use 3."""
+    say("sequential")
+    seq = nn.Sequential(dev)
+    layers = []
+    for i in range(6):
+        l = nn.Linear(dev, 16, 16, activation="relu" if i % 2 else "none")
+        l.load_weights(RNG.standard_normal((16, 16)).astype(np.float32) * 0.3,
+                       RNG.standard_normal(16).astype(np.float32) * 0.1)
+        layers.append(l)
+        seq.add(l)
+    seq.build()
+    x = RNG.standard_normal((16,)).astype(np.float32)
+    out = seq.forward(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(10000)
+    assert seq.buffer_stats[0] <= 2 and seq.buffer_stats[1] == 6
+    ref = x.astype(np.float64)
+    for i, l in enumerate(layers):
+        pass
+    # recompute with the oracle from the weights we drew: re-draw deterministically instead
+    assert out.to_numpy().shape == (16,)
+
+    seq3 = nn.Sequential(dev)
+    for a, b in ((8, 16), (16, 32), (32, 4)):
+        seq3.add(nn.Linear(dev, a, b))
+    seq3.build()
+    assert seq3.buffer_stats == (3, 3)
+
+
+def test_sequential_matches_oracle_chain(dev, stream):
+    say("sequential numeric chain")
+    ws = [(RNG.standard_normal((24, 24)) * 0.2).astype(np.float32) for _ in range(4)]
+    bs = [(RNG.standard_normal(24) * 0.1).astype(np.float32) for _ in range(4)]
+    seq = nn.Sequential(dev)
+    keep = []
+    for w, b in zip(ws, bs):
+        l = nn.Linear(dev, 24, 24, activation="gelu")
+        l.load_weights(w, b)
+        keep.append(l)
+        seq.add(l)
+    seq.build()
+    x = RNG.standard_normal((5, 24)).astype(np.float32)
+    out = seq.forward(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(10000)
+    ref = x.astype(np.float64)
+    for w, b in zip(ws, bs):
+        ref = oracle.linear(ref, w, b, act="gelu")
+    assert_close(out.to_numpy().reshape(5, 24), ref, ATOL, RTOL, "sequential chain")
+
+
+def test_sequential_errors(dev, stream):
+    say("sequential errors")
+    seq = nn.Sequential(dev)
+    with pytest.raises(nn.MNNError) as e:
+        seq.forward(nn.Tensor(dev, [4]), stream)
+    assert e.value.name == "MNN_ERR_EMPTY_MODEL"
+    seq.add(nn.Linear(dev, 4, 8))
+    with pytest.raises(nn.MNNError) as e:
+        seq.add(nn.Linear(dev, 5, 2))
+    assert e.value.name == "MNN_ERR_SHAPE_MISMATCH"
+    with pytest.raises(nn.MNNError) as e:
+        seq.forward(nn.Tensor(dev, [4]), stream)
+    assert e.value.name == "MNN_ERR_NOT_BUILT"
+    seq.build()
+    with pytest.raises(nn.MNNError) as e:
+        seq.forward(nn.Tensor(dev, [5]), stream)
+    assert e.value.name == "MNN_ERR_INPUT_SHAPE_MISMATCH"
+
+
+def test_weight_validation_errors(dev):
+    say("weight validation")
+    l = nn.Linear(dev, 4, 2)
+    w = np.ones(8, np.float32)
+    w[3] = np.nan
+    with pytest.raises(nn.MNNError) as e:
+        l.load_weights(w)
+    assert e.value.name == "MNN_ERR_INVALID_CONFIGURATION"
+    w[3] = np.inf
+    with pytest.raises(nn.MNNError) as e:
+        l.load_weights(w)
+    assert e.value.name == "MNN_ERR_INVALID_CONFIGURATION"
+    with pytest.raises(nn.MNNError) as e:
+        l.load_weights(np.ones(7, np.float32))
+    assert e.value.name == "MNN_ERR_BUFFER_SIZE_MISMATCH"
+    with pytest.raises(nn.MNNError) as e:
+        nn.MultiHeadAttention(dev, 10, 3)
+    assert e.value.name == "MNN_ERR_INVALID_CONFIGURATION"
+
+
+def test_shape_errors(dev, stream):
+    say("shape errors")
+    c = nn.DynamicConv1D(dev, 2, 4, 8, 4, padding_mode="reflect", padding=3)
+    with pytest.raises(nn.MNNError) as e:
+        c(nn.Tensor(dev, [3, 100]), stream)
+    assert e.value.name == "MNN_ERR_SHAPE_MISMATCH"
+    with pytest.raises(nn.MNNError) as e:
+        c.forward(nn.Tensor(dev, [2, 100]), nn.Tensor(dev, [4, 10]), stream)
+    assert e.value.name == "MNN_ERR_BUFFER_SIZE_MISMATCH"
+
+
+def test_device_lost_and_stream_sync(dev):
+    say("device lost")
+    d2 = nn.AudioDevice(0)
+    s2 = nn.Stream(d2)
+    d2.check_available(2000)
+    t = nn.Tensor(d2, [4])
+    s2.sync(2000)
+    d2.mark_lost()
+    with pytest.raises(nn.MNNError) as e:
+        t.copy_from(np.ones(4, np.float32))
+    assert e.value.name == "MNN_ERR_DEVICE_LOST"
+    with pytest.raises(nn.MNNError) as e:
+        nn.Linear(d2, 2, 2)
+    assert e.value.name == "MNN_ERR_DEVICE_LOST"

@@ -1,0 +1,315 @@
+"""Pins the CPU oracle (oracle/layers.py) before it is trusted as the parity reference.
+
+Each oracle function is checked against something that does not restate its formula:
+  * the reference's committed golden vectors (time_encoder_level{0,1}, converted to npz),
+  * closed-form known-answer tests taken from the reference's own test suite,
+  * independent library routines (torch CPU: conv1d, group_norm, layer_norm, gelu, glu,
+    linear, nn.MultiheadAttention, nn.TransformerEncoderLayer),
+  * invariants (normalised mean 0 / variance 1, softmax rows, length formulas).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from metalaudio_amd import workloads
+from tests.conftest import assert_close
+
+torch.set_num_threads(4)
+RNG = np.random.default_rng(7)
+
+
+def t64(a):
+    return torch.from_numpy(np.asarray(a, np.float64))
+
+
+# ----------------------------------------------------------------------------- golden vectors
+@pytest.mark.parametrize("name", ["time_encoder_level0", "time_encoder_level1"])
+def test_encoder_block_matches_reference_fixture(golden_dir, name):
+    """HTDemucsValidationTests.swift:37-117 fixtures: per element abs <= 1e-4 or rel <= 1e-3."""
+    d = np.load(golden_dir / f"{name}.npz")
+    cin, cout, k, s, g = (int(v) for v in d["config"])
+    y = oracle.encoder_block(d["input"], d["conv_weight"], d["conv_bias"], d["norm_weight"],
+                             d["norm_bias"], g, kernel_size=k, stride=s)
+    ref = d["output"].astype(np.float64)
+    err = np.abs(y - ref)
+    ok = (err <= 1e-4) | (err <= 1e-3 * np.abs(ref))
+    assert ok.all(), f"max abs {err.max():.3e}"
+    assert err.max() < 1e-5  # the fixture is fp32 torch output; the oracle is fp64
+
+
+# ----------------------------------------------------------------------------- closed forms
+def test_gelu_reference_table():
+    """IntegrationTests.swift:28-67 (tanh-approximation table, accuracy 1e-3)."""
+    x = np.array([-3.0, -2.0, -1.0, -0.5, 0.0, 0.5, 1.0, 2.0, 3.0, 5.0])
+    expected = np.array([-0.00364, -0.04550, -0.1588, -0.1543, 0.0, 0.3457, 0.8412, 1.9546,
+                         2.9964, 5.0000])
+    assert np.all(np.abs(oracle.gelu_layer(x) - expected) <= 1e-3)
+    assert np.all(np.abs(oracle.gelu_tanh(x) - expected) <= 1e-3)
+
+
+def test_gelu_clamp_semantics():
+    """Activations.swift:124-137: x > 10 -> x, x < -10 -> 0."""
+    x = np.array([-50.0, -10.5, 10.5, 50.0])
+    np.testing.assert_array_equal(oracle.gelu_layer(x), [0.0, 0.0, 10.5, 50.0])
+
+
+def test_gelu_matches_torch_tanh_gelu():
+    x = RNG.standard_normal(10000) * 4
+    ref = F.gelu(t64(x), approximate="tanh").numpy()
+    # the reference literal 0.7978845608 differs from sqrt(2/pi) by 2.9e-12
+    np.testing.assert_allclose(oracle.gelu_tanh(x), ref, rtol=0, atol=1e-10)
+
+
+def test_layernorm_closed_form():
+    """IntegrationTests.swift:336-374: [1,2,3,4] -> [-1.3416407, -0.4472136, 0.4472136, 1.3416407]."""
+    y = oracle.layer_norm(np.array([1.0, 2.0, 3.0, 4.0]))
+    np.testing.assert_allclose(y, [-1.3416407, -0.4472136, 0.4472136, 1.3416407], atol=1e-4)
+    assert abs(y.mean()) < 1e-5 and abs(y.var() - 1.0) < 1e-4
+
+
+def test_layernorm_matches_torch():
+    x = RNG.standard_normal((37, 384)) * 3 + 1
+    g, b = RNG.standard_normal(384), RNG.standard_normal(384)
+    ref = F.layer_norm(t64(x), (384,), t64(g), t64(b), eps=1e-5).numpy()
+    np.testing.assert_allclose(oracle.layer_norm(x, g, b), ref, rtol=1e-12, atol=1e-12)
+
+
+def test_linear_closed_forms():
+    """IntegrationTests.swift:259-324: W [[1,2,3],[4,5,6]], b [.1,.2], x [1,2,3] -> [14.1, 32.2];
+    batch through identity-like weights."""
+    w = np.array([[1, 2, 3], [4, 5, 6]], np.float64)
+    np.testing.assert_allclose(oracle.linear(np.array([1.0, 2.0, 3.0]), w, [0.1, 0.2]),
+                               [14.1, 32.2], atol=1e-12)
+    wi = np.array([[1, 0, 0], [0, 1, 0]], np.float64)
+    np.testing.assert_allclose(oracle.linear(np.array([[1, 2, 3], [4, 5, 6.0]]), wi),
+                               [[1, 2], [4, 5]], atol=0)
+
+
+@pytest.mark.parametrize("act", ["none", "relu", "leaky_relu", "gelu", "swish", "sigmoid", "tanh"])
+def test_linear_matches_torch(act):
+    x = RNG.standard_normal((13, 24))
+    w, b = RNG.standard_normal((17, 24)), RNG.standard_normal(17)
+    z = F.linear(t64(x), t64(w), t64(b))
+    ref = {"none": z, "relu": F.relu(z), "leaky_relu": F.leaky_relu(z, 0.01),
+           "gelu": F.gelu(z, approximate="tanh"), "swish": F.silu(z), "sigmoid": torch.sigmoid(z),
+           "tanh": torch.tanh(z)}[act].numpy()
+    np.testing.assert_allclose(oracle.linear(x, w, b, act=act), ref, rtol=1e-9, atol=1e-9)
+
+
+def test_conv_identity_and_averaging():
+    """Conv1DTests.swift:66-146 (padding 1, k 3)."""
+    y = oracle.conv1d(np.array([[1.0, 2, 3, 4, 5]]), np.array([[[0.0, 1, 0]]]), padding=1)
+    np.testing.assert_allclose(y, [[1, 2, 3, 4, 5]], atol=1e-12)
+    w = np.full((1, 1, 3), 1.0 / 3.0)
+    y = oracle.conv1d(np.array([[3.0] * 5]), w, padding=1)
+    np.testing.assert_allclose(y, [[2, 3, 3, 3, 2]], atol=1e-12)
+
+
+def test_conv_output_lengths():
+    """DynamicConv1DTests.swift:373-390 (441000 -> 110250, reflect 3) and the config chains."""
+    def lout(L, k=8, s=4, p=3):
+        return (L + 2 * p - k) // s + 1
+    assert lout(441000) == 110250
+    L, chain = workloads.CHUNK_SAMPLES, []
+    for _ in range(4):
+        L = lout(L)
+        chain.append(L)
+    assert chain == [85995, 21499, 5375, 1344]
+    assert lout(44100, p=0) == 11024
+
+
+@pytest.mark.parametrize("cin,cout,k,s,p,d,g,mode", [
+    (2, 48, 8, 4, 0, 1, 1, "zeros"),
+    (2, 48, 8, 4, 3, 1, 1, "reflect"),
+    (6, 12, 5, 2, 2, 2, 3, "zeros"),
+    (48, 96, 8, 4, 3, 1, 1, "reflect"),
+    (8, 8, 1, 1, 0, 1, 1, "zeros"),
+])
+def test_conv_matches_torch(cin, cout, k, s, p, d, g, mode):
+    x = RNG.standard_normal((2, cin, 257))
+    w = RNG.standard_normal((cout, cin // g, k))
+    b = RNG.standard_normal(cout)
+    xt = t64(x)
+    if mode == "reflect":
+        xt = F.pad(xt, (p, p), mode="reflect")
+        ref = F.conv1d(xt, t64(w), t64(b), stride=s, dilation=d, groups=g)
+    else:
+        ref = F.conv1d(xt, t64(w), t64(b), stride=s, padding=p, dilation=d, groups=g)
+    y = oracle.conv1d(x, w, b, stride=s, padding=p, dilation=d, groups=g, mode=mode)
+    np.testing.assert_allclose(y, ref.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_reflect_pad_matches_torch():
+    x = RNG.standard_normal((3, 11))
+    ref = F.pad(t64(x)[None], (3, 3), mode="reflect")[0].numpy()
+    np.testing.assert_array_equal(oracle.reflect_pad(x, 3), ref)
+
+
+@pytest.mark.parametrize("groups", [1, 8])
+def test_group_norm_matches_torch_and_invariants(groups):
+    x = RNG.standard_normal((2, 48, 301)) * 2 + 0.5
+    g, b = RNG.standard_normal(48), RNG.standard_normal(48)
+    ref = F.group_norm(t64(x), groups, t64(g), t64(b), eps=1e-5).numpy()
+    np.testing.assert_allclose(oracle.group_norm(x, groups, g, b), ref, rtol=1e-10, atol=1e-10)
+    y = oracle.group_norm(x, groups).reshape(2, groups, -1)   # GroupNormTests.swift:478-533
+    assert np.all(np.abs(y.mean(-1)) < 1e-10) and np.all(np.abs(y.var(-1) - 1) < 1e-3)
+
+
+def test_glu_matches_torch_and_sigmoid_extremes():
+    x = RNG.standard_normal((2, 20, 33)) * 5
+    np.testing.assert_allclose(oracle.glu(x, axis=-2), F.glu(t64(x), dim=-2).numpy(), rtol=1e-12,
+                               atol=1e-14)
+    s = oracle.stable_sigmoid(np.array([-1000.0, -88.0, 0.0, 88.0, 1000.0]))
+    assert s[0] == s[1] and s[3] == s[4] and s[2] == 0.5 and np.all(np.isfinite(s))
+
+
+def _torch_mha(E, H, w_in, b_in, w_out, b_out):
+    m = torch.nn.MultiheadAttention(E, H, bias=True, batch_first=True, dtype=torch.float64)
+    with torch.no_grad():
+        m.in_proj_weight.copy_(t64(w_in))
+        m.in_proj_bias.copy_(t64(b_in))
+        m.out_proj.weight.copy_(t64(w_out))
+        m.out_proj.bias.copy_(t64(b_out))
+    return m.eval()
+
+
+@pytest.mark.parametrize("E,H,Sq,Sk,cross", [(64, 4, 19, 19, False), (96, 2, 17, 29, True),
+                                             (384, 8, 33, 65, True)])
+def test_mha_matches_torch(E, H, Sq, Sk, cross):
+    """Packed in_proj rows Q;K;V and out_proj as nn.MultiheadAttention (Attention.swift:10-14)."""
+    w_in, b_in = RNG.standard_normal((3 * E, E)) * 0.1, RNG.standard_normal(3 * E) * 0.1
+    w_out, b_out = RNG.standard_normal((E, E)) * 0.1, RNG.standard_normal(E) * 0.1
+    q = RNG.standard_normal((2, Sq, E))
+    kv = RNG.standard_normal((2, Sk, E)) if cross else q
+    m = _torch_mha(E, H, w_in, b_in, w_out, b_out)
+    with torch.no_grad():
+        ref = m(t64(q), t64(kv), t64(kv), need_weights=False)[0].numpy()
+    got = oracle.mha(q, kv if cross else None, w_in, b_in, w_out, b_out, H)
+    np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-8)
+
+
+def test_mha_scale_and_identity_weights():
+    """AttentionTests.swift:505-519 (scale 1/sqrt(hd)) and :586-642 (identity weights bounded):
+    with identity projections and one key, the output equals the value row."""
+    E, H = 8, 2
+    w_in = np.concatenate([np.eye(E)] * 3)
+    x = RNG.standard_normal((1, E))
+    y = oracle.mha(x, None, w_in, np.zeros(3 * E), np.eye(E), np.zeros(E), H)
+    np.testing.assert_allclose(y, x, atol=1e-9)
+    xs = RNG.standard_normal((5, E))
+    y = oracle.mha(xs, None, w_in, None, np.eye(E), None, H)
+    assert np.all(np.abs(y) <= np.abs(xs).max(0) + 1e-12)
+
+
+def test_feed_forward_matches_torch():
+    x = RNG.standard_normal((9, 32))
+    w1, b1 = RNG.standard_normal((64, 32)), RNG.standard_normal(64)
+    w2, b2 = RNG.standard_normal((32, 64)), RNG.standard_normal(32)
+    ref = F.linear(F.gelu(F.linear(t64(x), t64(w1), t64(b1)), approximate="tanh"), t64(w2), t64(b2))
+    np.testing.assert_allclose(oracle.feed_forward(x, w1, b1, w2, b2), ref.numpy(), rtol=1e-10,
+                               atol=1e-10)
+
+
+def test_transformer_layer_matches_torch_encoder_layer():
+    """Config-3 layer (pre-norm, no LayerScale) against nn.TransformerEncoderLayer(norm_first)."""
+    cfg = workloads.config3(stress=True, seq=40)
+    E, H, Hd, p = cfg["embed"], cfg["heads"], cfg["ffn"], cfg["params"]
+    m = torch.nn.TransformerEncoderLayer(E, H, Hd, dropout=0.0, batch_first=True, norm_first=True,
+                                         activation=lambda z: F.gelu(z, approximate="tanh"),
+                                         dtype=torch.float64).eval()
+    with torch.no_grad():
+        m.self_attn.in_proj_weight.copy_(t64(p["attn.in_proj_weight"]))
+        m.self_attn.in_proj_bias.copy_(t64(p["attn.in_proj_bias"]))
+        m.self_attn.out_proj.weight.copy_(t64(p["attn.out_proj_weight"]))
+        m.self_attn.out_proj.bias.copy_(t64(p["attn.out_proj_bias"]))
+        for n in ("linear1", "linear2"):
+            getattr(m, n).weight.copy_(t64(p[n + ".weight"]))
+            getattr(m, n).bias.copy_(t64(p[n + ".bias"]))
+        for n in ("norm1", "norm2"):
+            getattr(m, n).weight.copy_(t64(p[n + ".weight"]))
+            getattr(m, n).bias.copy_(t64(p[n + ".bias"]))
+        ref = m(t64(cfg["x"])[None])[0].numpy()
+    np.testing.assert_allclose(oracle.transformer_layer(cfg["x"], p, H), ref, rtol=1e-9,
+                               atol=1e-9)
+
+
+def test_cross_transformer_matches_torch_composition():
+    """Config-5 structure composed from torch library routines with strong LayerScale."""
+    cfg = workloads.config5(stress=True, batch=1, time_len=21, freq_len=37, layers=3)
+    p = dict(cfg["params"])
+    for k in p:
+        if "gamma_" in k:
+            p[k] = np.full_like(p[k], 0.7)
+    E, H = cfg["embed"], cfg["heads"]
+
+    def ln(x, pre):
+        return F.layer_norm(x, (E,), t64(p[pre + ".weight"]), t64(p[pre + ".bias"]), 1e-5)
+
+    def attn(q, kv, pre):
+        m = _torch_mha(E, H, p[pre + "in_proj_weight"], p[pre + "in_proj_bias"],
+                       p[pre + "out_proj_weight"], p[pre + "out_proj_bias"])
+        return m(q, kv, kv, need_weights=False)[0]
+
+    def ffn(x, pre):
+        h = F.gelu(F.linear(x, t64(p[pre + "linear1.weight"]), t64(p[pre + "linear1.bias"])),
+                   approximate="tanh")
+        return F.linear(h, t64(p[pre + "linear2.weight"]), t64(p[pre + "linear2.bias"]))
+
+    with torch.no_grad():
+        T, Fr = t64(cfg["time"]), t64(cfg["freq"])
+        for i in range(3):
+            a, b = f"layers.{i}.time.", f"layers.{i}.freq."
+            if i % 2 == 0:
+                outs = []
+                for X, pre in ((T, a), (Fr, b)):
+                    h = ln(X, pre + "norm1")
+                    X = X + t64(p[pre + "gamma_1.scale"]) * attn(h, h, pre + "attn.")
+                    X = X + t64(p[pre + "gamma_2.scale"]) * ffn(ln(X, pre + "norm2"), pre)
+                    outs.append(X)
+                T, Fr = outs
+            else:
+                Tn = T + t64(p[a + "gamma_1.scale"]) * attn(ln(T, a + "norm1"),
+                                                            ln(Fr, a + "norm2"), a + "attn.")
+                Fn = Fr + t64(p[b + "gamma_1.scale"]) * attn(ln(Fr, b + "norm1"),
+                                                             ln(T, b + "norm2"), b + "attn.")
+                Tn = Tn + t64(p[a + "gamma_2.scale"]) * ffn(ln(Tn, a + "norm3"), a)
+                Fn = Fn + t64(p[b + "gamma_2.scale"]) * ffn(ln(Fn, b + "norm3"), b)
+                T, Fr = Tn, Fn
+    ot, of = oracle.cross_transformer(cfg["time"], cfg["freq"], p, 3, H)
+    np.testing.assert_allclose(ot, T.numpy(), rtol=1e-9, atol=1e-9)
+    np.testing.assert_allclose(of, Fr.numpy(), rtol=1e-9, atol=1e-9)
+
+
+def test_time_encoder_matches_torch_composition():
+    cfg = workloads.config4(stress=True, samples=4000)
+    with torch.no_grad():
+        y = t64(cfg["x"])
+        for lv in cfg["levels"]:
+            y = F.conv1d(F.pad(y, (3, 3), mode="reflect"), t64(lv["conv.weight"]),
+                         t64(lv["conv.bias"]), stride=4)
+            y = F.gelu(F.group_norm(y, 1, t64(lv["norm.weight"]), t64(lv["norm.bias"]), 1e-5),
+                       approximate="tanh")
+            y = F.glu(F.conv1d(y, t64(lv["rewrite.weight"]), t64(lv["rewrite.bias"])), dim=1)
+    np.testing.assert_allclose(oracle.time_encoder(cfg["x"], cfg["levels"]), y.numpy(),
+                               rtol=1e-9, atol=1e-10)
+
+
+def test_planted_mistakes_are_caught(golden_dir):
+    """Plausible oracle slips fail the golden fixture: GELU on the wrong side of GroupNorm,
+    zero instead of reflect padding, and a transposed conv weight."""
+    d = np.load(golden_dir / "time_encoder_level0.npz")
+    ref = d["output"]
+    y = oracle.conv1d(d["input"], d["conv_weight"], d["conv_bias"], stride=4, padding=3,
+                      mode="reflect")
+    wrong = oracle.group_norm(oracle.gelu_tanh(y), 8, d["norm_weight"], d["norm_bias"])
+    assert np.abs(wrong - ref).max() > 1e-2
+    yz = oracle.conv1d(d["input"], d["conv_weight"], d["conv_bias"], stride=4, padding=3,
+                       mode="zeros")
+    wrong = oracle.gelu_tanh(oracle.group_norm(yz, 8, d["norm_weight"], d["norm_bias"]))
+    assert np.abs(wrong - ref).max() > 1e-3
+    wt = d["conv_weight"][:, :, ::-1]
+    wrong = oracle.encoder_block(d["input"], wt, d["conv_bias"], d["norm_weight"],
+                                 d["norm_bias"], 8)
+    assert np.abs(wrong - ref).max() > 1e-2
