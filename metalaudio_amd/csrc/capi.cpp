@@ -157,7 +157,7 @@ mnn_status mnn_device_name(mnn_device dev, char* buf, size_t n) {
   return guard([&] {
     Device* d = D(dev);
     MNN_REQUIRE(buf && n > 0, MNN_ERR_INVALID_ARGUMENT, "null buffer");
-    std::snprintf(buf, n, "%s (%s, %d CUs)", d->props.name, d->props.gcnArchName,
+    std::snprintf(buf, n, "%s [%s, %d CUs]", d->props.name[0] ? d->props.name : "AMD GPU", d->props.gcnArchName,
                   d->props.multiProcessorCount);
   });
 }

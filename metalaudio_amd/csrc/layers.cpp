@@ -160,62 +160,56 @@ class Conv1DLayer : public Layer {
     const int ck = p_.in_channels * p_.kernel_size;
     return p_.groups == 1 && ck % 4 == 0 && ck >= 64 && p_.out_channels >= 32;
   }
-  // Runs the convolution; `stats` (GroupNorm(1) partials of the pre-activation output) is
-  // optional. Returns the number of partials per batch written to `stats`.
-  int run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s) {
+  // Implicit-GEMM arguments of the matrix-core path (one place, so the statistics partial
+  // count and the launch always agree).
+  k::GemmArgs gemm_args(const float* x, int B, int L, float* y, int act, float* stats) const {
     const int lo = (int)out_len(L);
-    const int pad = pad_for(L);
-    const bool reflect = p_.padding_mode == MNN_PAD_REFLECT;
-    if (uses_mfma()) {
-      k::GemmArgs g;
-      g.M = p_.out_channels;
-      g.N = lo;
-      g.K = p_.in_channels * p_.kernel_size;
-      g.batch = B;
-      g.A = w_->ptr();
-      g.lda = g.K;
-      g.B = x;
-      g.ldb = L;
-      g.sB = (int64_t)p_.in_channels * L;
-      g.blayout = k::B_CONV;
-      g.conv_L = L;
-      g.conv_ks = p_.kernel_size;
-      g.conv_stride = p_.stride;
-      g.conv_pad = pad;
-      g.conv_dil = p_.dilation;
-      g.conv_reflect = reflect;
-      g.C = y;
-      g.ldc = lo;
-      g.sC = (int64_t)p_.out_channels * lo;
-      g.bias = b_ ? b_->ptr() : nullptr;
-      g.bias_mode = b_ ? k::BIAS_M : k::BIAS_NONE;
-      g.act = act;
-      g.stats = stats;
-      g.precision = p_.precision;
-      k::gemm(ctx(s), g);
-      return k::gemm_num_tiles(g);
-    }
-    k::ConvParams cp{B, p_.in_channels, p_.out_channels, L, lo, p_.kernel_size,
-                     p_.stride, pad, p_.dilation, p_.groups, reflect};
-    int nchunk = 0;
-    k::conv1d_direct(ctx(s), cp, x, w_->ptr(), b_ ? b_->ptr() : nullptr, y, act, stats, &nchunk);
-    return nchunk;
+    k::GemmArgs g;
+    g.M = p_.out_channels;
+    g.N = lo;
+    g.K = p_.in_channels * p_.kernel_size;
+    g.batch = B;
+    g.A = w_->ptr();
+    g.lda = g.K;
+    g.B = x;
+    g.ldb = L;
+    g.sB = (int64_t)p_.in_channels * L;
+    g.blayout = k::B_CONV;
+    g.conv_L = L;
+    g.conv_ks = p_.kernel_size;
+    g.conv_stride = p_.stride;
+    g.conv_pad = pad_for(L);
+    g.conv_dil = p_.dilation;
+    g.conv_reflect = p_.padding_mode == MNN_PAD_REFLECT;
+    g.C = y;
+    g.ldc = lo;
+    g.sC = (int64_t)p_.out_channels * lo;
+    g.bias = b_ ? b_->ptr() : nullptr;
+    g.bias_mode = b_ ? k::BIAS_M : k::BIAS_NONE;
+    g.act = act;
+    g.stats = stats;
+    g.precision = p_.precision;
+    return g;
   }
-  int stats_chunks(int L) const {
-    const int lo = (int)out_len(L);
+  k::ConvParams direct_params(int B, int L) const {
+    return k::ConvParams{B, p_.in_channels, p_.out_channels, L, (int)out_len(L), p_.kernel_size,
+                         p_.stride, pad_for(L), p_.dilation, p_.groups,
+                         p_.padding_mode == MNN_PAD_REFLECT};
+  }
+  // Number of GroupNorm(1) statistics partials per batch that run() writes for this input.
+  int stats_chunks(int B, int L) const {
+    if (uses_mfma()) return k::gemm_num_tiles(gemm_args(nullptr, B, L, nullptr, 0, nullptr));
+    return k::conv1d_direct_num_chunks(direct_params(B, L));
+  }
+  // Runs the convolution; `stats` (GroupNorm(1) partials of the pre-activation output) is
+  // optional and must hold 3 * B * stats_chunks(B, L) floats.
+  void run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s) {
     if (uses_mfma()) {
-      k::GemmArgs g;
-      g.M = p_.out_channels;
-      g.N = lo;
-      g.K = p_.in_channels * p_.kernel_size;
-      g.lda = g.K;
-      g.A = w_->ptr();
-      g.blayout = k::B_CONV;
-      return k::gemm_num_tiles(g);
+      k::gemm(ctx(s), gemm_args(x, B, L, y, act, stats));
+      return;
     }
-    k::ConvParams cp{1, p_.in_channels, p_.out_channels, L, lo, p_.kernel_size,
-                     p_.stride, pad_for(L), p_.dilation, p_.groups, false};
-    return k::conv1d_direct_num_chunks(cp);
+    k::conv1d_direct(ctx(s), direct_params(B, L), x, w_->ptr(), b_ ? b_->ptr() : nullptr, y, act,
+                     stats, nullptr);
   }
   const mnn_conv1d_desc& desc() const { return p_; }
 
@@ -705,11 +699,9 @@ class EncoderBlockLayer : public Layer {
     const bool fused_stats = norm_->groups() == 1;
     int nchunk;
     if (fused_stats) {
-      nchunk = conv_->stats_chunks((int)L);
+      nchunk = conv_->stats_chunks((int)B, (int)L);
       partials_.reserve(sizeof(float) * 3 * B * nchunk);
-      const int got = conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE,
-                                 partials_.f32(), s);
-      MNN_REQUIRE(got == nchunk, MNN_ERR_GPU_EXECUTION, "statistics partial count mismatch");
+      conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, partials_.f32(), s);
     } else {
       conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, nullptr, s);
       nchunk = k::gn_num_chunks(Cout, norm_->groups(), lo);

@@ -147,9 +147,13 @@ Tensor* Sequential::forward(const Tensor& in, Stream& s) {
   std::lock_guard<std::mutex> lk(forward_mu_);
   MNN_REQUIRE(!layers_.empty(), MNN_ERR_EMPTY_MODEL, "Cannot run inference on empty model");
   MNN_REQUIRE(built_, MNN_ERR_NOT_BUILT, "Model not built. Call build() first.");
+  // Model.swift:231-236 compares the whole shape; here leading batch dimensions are allowed
+  // (layers take [C, L] or [B, C, L], [F] or [N, F]) and 0 in the declared shape is dynamic.
   const Shape expect = layers_[0]->input_shape();
-  bool ok = expect.size() == in.shape.size();
-  for (size_t i = 0; ok && i < expect.size(); ++i) ok = expect[i] == 0 || expect[i] == in.shape[i];
+  bool ok = in.shape.size() >= expect.size();
+  const size_t off = ok ? in.shape.size() - expect.size() : 0;
+  for (size_t i = 0; ok && i < expect.size(); ++i)
+    ok = expect[i] == 0 || expect[i] == in.shape[off + i];
   MNN_REQUIRE(ok, MNN_ERR_INPUT_SHAPE_MISMATCH,
               "Model input shape mismatch: expected " << shape_str(expect) << ", got "
                                                       << shape_str(in.shape));
