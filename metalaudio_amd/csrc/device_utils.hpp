@@ -119,5 +119,69 @@ __device__ __forceinline__ void block_welford(float& n, float& mean, float& m2, 
   }
 }
 
+// Running (count, mean, M2) of a thread's values without a division per value: sums of
+// (v - shift) and (v - shift)^2 around the thread's first value, converted once at the end.
+struct ShiftedStats {
+  float n = 0.f, shift = 0.f, s1 = 0.f, s2 = 0.f;
+  __device__ __forceinline__ void add(float v) {
+    if (n == 0.f) shift = v;
+    const float d = v - shift;
+    n += 1.f;
+    s1 += d;
+    s2 = fmaf(d, d, s2);
+  }
+  __device__ __forceinline__ void finish(float& cnt, float& mean, float& m2) const {
+    cnt = n;
+    if (n > 0.f) {
+      const float md = s1 / n;
+      mean = shift + md;
+      m2 = fmaxf(s2 - s1 * md, 0.f);
+    } else {
+      mean = 0.f;
+      m2 = 0.f;
+    }
+  }
+};
+
+// Block-wide fixed-order sum of one double per thread (wave shuffles, then the waves in order).
+// `sh` needs blockDim.x / 64 doubles; every thread receives the total.
+__device__ __forceinline__ double block_sum_d(double v, double* sh) {
+  v = wave_sum_d(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) sh[wid] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int w = 0; w < nw; ++w) t += sh[w];
+  __syncthreads();
+  return t;
+}
+
+// Merge of GroupNorm(1) partials (count, mean, M2) written by a previous kernel, by every thread
+// of a workgroup: N = sum n_j, mean = sum n_j mean_j / N, M2 = sum (M2_j + n_j (mean_j - mean)^2),
+// accumulated in fp64 in a fixed order, so every workgroup obtains the same (mean, rstd).
+// `sh` needs blockDim.x / 64 doubles of LDS.
+__device__ __forceinline__ float2 gn1_merge(const float* __restrict__ partials, int nparts,
+                                           float eps, double* sh) {
+  double n = 0.0, s1 = 0.0;
+  for (int j = threadIdx.x; j < nparts; j += blockDim.x) {
+    const float* p = partials + (int64_t)j * 3;
+    n += p[0];
+    s1 += (double)p[0] * (double)p[1];
+  }
+  const double ntot = block_sum_d(n, sh);
+  const double mean = ntot > 0.0 ? block_sum_d(s1, sh) / ntot : 0.0;
+  double m2 = 0.0;
+  for (int j = threadIdx.x; j < nparts; j += blockDim.x) {
+    const float* p = partials + (int64_t)j * 3;
+    const double d = (double)p[1] - mean;
+    m2 += (double)p[2] + (double)p[0] * d * d;
+  }
+  m2 = block_sum_d(m2, sh);
+  const double var = ntot > 0.0 ? m2 / ntot : 0.0;  // biased (population) variance
+  float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  if (!isfinite(rstd)) rstd = 0.f;  // reference CPU path guard (Normalization.swift:695-699)
+  return make_float2((float)mean, rstd);
+}
+
 }  // namespace dev
 }  // namespace mnn

@@ -110,26 +110,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
 
     const float* ks = Ks[cur];
     const float* vs = Vs[cur];
-    // S^T tiles: 4 key tiles x NU query tiles
+    // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
+    // accumulators interleave and no MFMA waits on the previous one
     floatx4 st[4][NU];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float kf[HS];
-      const float* p = ks + (16 * t + l16) * LDK + G * HS;
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int s4 = 0; s4 < HS / 4; ++s4) {
-        float4 v4 = *reinterpret_cast<const float4*>(p + 4 * s4);
-        kf[4 * s4 + 0] = v4.x; kf[4 * s4 + 1] = v4.y;
-        kf[4 * s4 + 2] = v4.z; kf[4 * s4 + 3] = v4.w;
+      for (int u = 0; u < NU; ++u) st[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < HS / 4; ++s4) {
+      float kf[4][4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float4 v4 =
+            *reinterpret_cast<const float4*>(ks + (16 * t + l16) * LDK + G * HS + 4 * s4);
+        kf[t][0] = v4.x; kf[t][1] = v4.y; kf[t][2] = v4.z; kf[t][3] = v4.w;
       }
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < 4; ++s)
 #pragma unroll
-        for (int s = 0; s < HS; ++s)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qf[u][s], acc, 0, 0, 0);
-        st[t][u] = acc;
-      }
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+            st[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t][s], qf[u][4 * s4 + s], st[t][u],
+                                                             0, 0, 0);
     }
     // mask keys beyond Sk
     if (kv0 + BKV > a.Sk) {

@@ -20,6 +20,7 @@ using namespace dev;
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kMaxRegCout = 128;
 
 template <int COB>
 __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
@@ -59,22 +60,19 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
       }
     }
   }
-  float n = 0.f, mean = 0.f, m2 = 0.f;
+  ShiftedStats st;
 #pragma unroll
   for (int j = 0; j < COB; ++j) {
     const int co = co0 + j;
     if (valid && co < p.Cout) {
       float v = acc[j] + (bias ? bias[co] : 0.f);
-      if (partials) {
-        n += 1.f;
-        float d = v - mean;
-        mean += d / n;
-        m2 += d * (v - mean);
-      }
-      y[((int64_t)b * p.Cout + co) * p.Lout + t] = apply_act(v, act);
+      if (partials) st.add(v);
+      if (y) y[((int64_t)b * p.Cout + co) * p.ldy + t] = apply_act(v, act);
     }
   }
   if (partials) {
+    float n, mean, m2;
+    st.finish(n, mean, m2);
     block_welford(n, mean, m2, red);
     if (threadIdx.x == 0) {
       const int nchunk = gridDim.x * gridDim.y;
@@ -86,6 +84,95 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
   }
 }
 
+// Small contractions (groups = 1, Cin*K = CK <= 32): each thread loads its whole input window
+// (CK samples) into registers with all loads in flight together, then produces the COB output
+// channels of its workgroup (grid.y spreads the channels, so there are enough waves per SIMD to
+// hide memory latency). Weights are staged in LDS and read as broadcasts.
+template <int CK, int COB>
+__global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams p,
+                                                                     const float* __restrict__ x,
+                                                                     const float* __restrict__ w,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ y, int act,
+                                                                     float* __restrict__ partials) {
+  __shared__ float red[3 * (kThreads / 64)];
+  // this workgroup's COB output channels, weights transposed to [e][co] so one 16-byte LDS
+  // read serves four output channels
+  __shared__ __attribute__((aligned(16))) float wt[CK * COB];
+  const int b = blockIdx.z;
+  const int cob0 = blockIdx.y * COB;
+  const int t = blockIdx.x * kThreads + threadIdx.x;
+  const bool valid = t < p.Lout;
+  for (int i = threadIdx.x; i < CK * COB; i += kThreads) {
+    const int co = i / CK, e = i - co * CK;
+    wt[e * COB + co] = w[(int64_t)(cob0 + co) * CK + e];
+  }
+  __syncthreads();
+  const float* xb = x + (int64_t)b * p.Cin * p.Lin;
+  float xv[CK];
+  const int base = t * p.stride - p.pad;
+#pragma unroll
+  for (int e = 0; e < CK; ++e) {
+    const int ci = e / p.K, kk = e - ci * p.K;
+    int pos = base + kk * p.dilation;
+    float v = 0.f;
+    if (valid) {
+      if (p.reflect) {
+        pos = pos < 0 ? -pos : pos;
+        pos = pos >= p.Lin ? 2 * (p.Lin - 1) - pos : pos;
+        v = xb[(int64_t)ci * p.Lin + pos];
+      } else if (pos >= 0 && pos < p.Lin) {
+        v = xb[(int64_t)ci * p.Lin + pos];
+      }
+    }
+    xv[e] = v;
+  }
+  ShiftedStats st;
+  {
+    const int co0 = cob0;
+    float acc[COB];
+#pragma unroll
+    for (int j = 0; j < COB; ++j) acc[j] = bias ? bias[co0 + j] : 0.f;
+#pragma unroll
+    for (int e = 0; e < CK; ++e)
+#pragma unroll
+      for (int j4 = 0; j4 < COB; j4 += 4) {
+        const float4 w4 = *reinterpret_cast<const float4*>(wt + e * COB + j4);
+        acc[j4 + 0] = fmaf(xv[e], w4.x, acc[j4 + 0]);
+        acc[j4 + 1] = fmaf(xv[e], w4.y, acc[j4 + 1]);
+        acc[j4 + 2] = fmaf(xv[e], w4.z, acc[j4 + 2]);
+        acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
+      }
+    if (valid) {
+#pragma unroll
+      for (int j = 0; j < COB; ++j) {
+        if (partials) st.add(acc[j]);
+        if (y) y[((int64_t)b * p.Cout + co0 + j) * p.ldy + t] = apply_act(acc[j], act);
+      }
+    }
+  }
+  if (partials) {
+    float n, mean, m2;
+    st.finish(n, mean, m2);
+    block_welford(n, mean, m2, red);
+    float* pb = partials + (int64_t)b * gridDim.x * gridDim.y * 3;
+    if (threadIdx.x == 0) {
+      float* o = pb + (int64_t)(blockIdx.y * gridDim.x + blockIdx.x) * 3;
+      o[0] = n;
+      o[1] = mean;
+      o[2] = m2;
+    }
+  }
+}
+
+// Register-window variant applies when groups = 1, Cin*K is 8, 16, 24 or 32, Cout % 16 == 0
+// and Cout <= kMaxRegCout.
+int reg_ck(const ConvParams& p) {
+  const int ck = p.Cin * p.K;
+  if (p.groups != 1 || p.Cout % 16 != 0 || p.Cout > kMaxRegCout) return 0;
+  return (ck == 8 || ck == 16 || ck == 24 || ck == 32) ? ck : 0;
+}
+
 int co_block(const ConvParams& p) {
   const int coutpg = p.Cout / p.groups;
   return (coutpg % 16 == 0) ? 16 : 1;
@@ -94,11 +181,25 @@ int co_block(const ConvParams& p) {
 }  // namespace
 
 int conv1d_direct_num_chunks(const ConvParams& p) {
+  if (reg_ck(p)) return (int)cdiv(p.Lout, kThreads) * (p.Cout / 16);
   return (int)cdiv(p.Lout, kThreads) * (p.Cout / co_block(p));
 }
 
-void conv1d_direct(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+void conv1d_direct(const LaunchCtx& c, const ConvParams& p0, const float* x, const float* w,
                    const float* bias, float* y, int act, float* partials, int* nchunk) {
+  ConvParams p = p0;
+  if (p.ldy == 0) p.ldy = p.Lout;
+  if (const int ck = reg_ck(p)) {
+    dim3 grid(cdiv(p.Lout, kThreads), p.Cout / 16, p.B);
+    if (nchunk) *nchunk = (int)(grid.x * grid.y);
+    switch (ck) {
+      case 8: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<8, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
+      case 16: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<16, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
+      case 24: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<24, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
+      default: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<32, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
+    }
+  }
+  MNN_REQUIRE(y, MNN_ERR_INVALID_ARGUMENT, "conv1d_direct: output required");
   const int cob = co_block(p);
   dim3 grid(cdiv(p.Lout, kThreads), p.Cout / cob, p.B);
   if (nchunk) *nchunk = (int)(grid.x * grid.y);
@@ -109,6 +210,8 @@ void conv1d_direct(const LaunchCtx& c, const ConvParams& p, const float* x, cons
     launch(c, "conv1d_direct_f32", conv1d_direct_kernel<1>, grid, dim3(kThreads), 0, p, x, w,
            bias, y, act, partials);
 }
+
+bool conv1d_direct_fusable(const ConvParams& p) { return reg_ck(p) != 0; }
 
 }  // namespace k
 }  // namespace mnn

@@ -39,17 +39,27 @@ void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F
 struct ConvParams {
   int B, Cin, Cout, Lin, Lout, K, stride, pad, dilation, groups;
   bool reflect;  // reflect padding (DynamicConv1D.swift:288-324) instead of zeros
+  int64_t ldy = 0;  // output row pitch (0 = Lout)
 };
 // Direct convolution, one thread per output position and a block of output channels.
 // act: fused activation. If `partials` is set (groups of GroupNorm = 1), each workgroup also
 // writes (count, mean, M2) of its outputs (before activation); *nchunk receives the count of
 // partials per batch.
+// y may be null (statistics only; the register-window kernel).
 void conv1d_direct(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
                    const float* bias, float* y, int act, float* partials, int* nchunk);
 int conv1d_direct_num_chunks(const ConvParams& p);
+// True when the register-window kernel runs (it supports statistics-only and fused finalize).
+bool conv1d_direct_fusable(const ConvParams& p);
+// GEMM tuning override: MNN_GEMM_TILE=<tile id> forces a tile configuration where it applies.
 
 // ------------------------------------------------------------------ GEMM (k_gemm.hip)
-enum BLayout { B_NK = 0, B_KN = 1, B_CONV = 2 };
+// B operand modes. B_KN4 and B_CONVW are the vectorised / windowed forms the launcher picks
+// when the operands allow (16-byte aligned rows; conv with k = 8, stride 4, dilation 1).
+// B_CONVREC: B[k][n] = act(coef[k].x * conv(x)[k][n] + coef[k].y), conv being a small direct
+// conv (Cin * kernel = 16, e.g. the 2-channel first encoder level, weights rc_w [K][16], bias
+// rc_b [K]) recomputed while the operand is loaded, so the conv output never goes to HBM.
+enum BLayout { B_NK = 0, B_KN = 1, B_CONV = 2, B_KN4 = 3, B_CONVW = 4, B_CONVREC = 5 };
 enum BiasMode { BIAS_NONE = 0, BIAS_N = 1, BIAS_M = 2 };
 
 struct GemmArgs {
@@ -57,7 +67,8 @@ struct GemmArgs {
   // A [M][K], row-major with row stride lda (always K-contiguous)
   const float* A = nullptr;
   int64_t lda = 0, sA = 0;
-  // B: B_NK -> [N][K] rows of stride ldb; B_KN -> [K][N] rows of stride ldb;
+  // B: B_NK -> [N][K] rows of stride ldb; B_KN -> [K][N] rows of stride ldb (rows may be
+  //    padded: ldb >= N, elements between N and ldb are read but never used);
   //    B_CONV -> implicit im2col of x [Cin][conv_L] (row stride ldb):
   //    B[k][n] = x[k / conv_ks][n*conv_stride - conv_pad + (k % conv_ks)*conv_dil]
   const float* B = nullptr;
@@ -65,9 +76,17 @@ struct GemmArgs {
   int blayout = B_NK;
   int conv_L = 0, conv_ks = 1, conv_stride = 1, conv_pad = 0, conv_dil = 1;
   bool conv_reflect = false;
-  // Optional prologue on B (B_KN only): B[k][n] <- act(B[k][n]*coef[b][k][0] + coef[b][k][1]);
-  // this applies GroupNorm (+GELU) of the producer while loading. coef batch stride = 2*K.
+  // Optional prologue on B (B_KN / B_CONVREC): B[k][n] <- act(B[k][n]*scale_k + shift_k); this
+  // applies GroupNorm (+GELU) of the producer while loading. The coefficients come either from
+  // pro_coef[b][k][2] (batch stride 2*K) or, with pro_stats, from GroupNorm(1) partials
+  // (count, mean, M2) of the producer (pro_nparts per batch) merged by every workgroup:
+  // scale_k = pro_gamma[k] * rstd, shift_k = pro_beta[k] - mean * scale_k.
   const float* pro_coef = nullptr;
+  const float* pro_stats = nullptr;
+  int pro_nparts = 0;
+  const float* pro_gamma = nullptr;
+  const float* pro_beta = nullptr;
+  float pro_eps = 1e-5f;
   int pro_act = 0;
   // C [M][N] row-major (or [M/2][N] with glu)
   float* C = nullptr;
@@ -85,6 +104,9 @@ struct GemmArgs {
   // GroupNorm(1) statistics of the output (after bias, before act): per workgroup partials
   // (count, mean, M2) at stats[(b*tiles + tile)*3]; tiles = gemm_num_tiles(...)
   float* stats = nullptr;
+  // B_CONVREC conv: weights [K][16] and bias [K]
+  const float* rc_w = nullptr;
+  const float* rc_b = nullptr;
   mnn_precision precision = MNN_PRECISION_F32;
 };
 // Number of output tiles per batch for the tile configuration the launcher will pick.

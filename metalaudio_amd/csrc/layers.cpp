@@ -162,8 +162,20 @@ class Conv1DLayer : public Layer {
   }
   // Implicit-GEMM arguments of the matrix-core path (one place, so the statistics partial
   // count and the launch always agree).
-  k::GemmArgs gemm_args(const float* x, int B, int L, float* y, int act, float* stats) const {
+  const float* weight_ptr() const { return w_->ptr(); }
+  const float* bias_ptr() const { return b_ ? b_->ptr() : nullptr; }
+  // The small direct conv can be recomputed inside a consumer GEMM's operand loader
+  // (B_CONVREC). Measured slower than storing the conv output on MI355X for the 2-channel
+  // encoder level, so the encoder does not select it; kept for shapes where it pays.
+  bool recompute_ok(int B, int L) const {
+    (void)B;
+    (void)L;
+    return false;
+  }
+  k::GemmArgs gemm_args(const float* x, int B, int L, float* y, int act, float* stats,
+                        int64_t ldy = 0) const {
     const int lo = (int)out_len(L);
+    if (ldy == 0) ldy = lo;
     k::GemmArgs g;
     g.M = p_.out_channels;
     g.N = lo;
@@ -182,8 +194,8 @@ class Conv1DLayer : public Layer {
     g.conv_dil = p_.dilation;
     g.conv_reflect = p_.padding_mode == MNN_PAD_REFLECT;
     g.C = y;
-    g.ldc = lo;
-    g.sC = (int64_t)p_.out_channels * lo;
+    g.ldc = ldy;
+    g.sC = (int64_t)p_.out_channels * ldy;
     g.bias = b_ ? b_->ptr() : nullptr;
     g.bias_mode = b_ ? k::BIAS_M : k::BIAS_NONE;
     g.act = act;
@@ -191,10 +203,10 @@ class Conv1DLayer : public Layer {
     g.precision = p_.precision;
     return g;
   }
-  k::ConvParams direct_params(int B, int L) const {
+  k::ConvParams direct_params(int B, int L, int64_t ldy = 0) const {
     return k::ConvParams{B, p_.in_channels, p_.out_channels, L, (int)out_len(L), p_.kernel_size,
                          p_.stride, pad_for(L), p_.dilation, p_.groups,
-                         p_.padding_mode == MNN_PAD_REFLECT};
+                         p_.padding_mode == MNN_PAD_REFLECT, ldy};
   }
   // Number of GroupNorm(1) statistics partials per batch that run() writes for this input.
   int stats_chunks(int B, int L) const {
@@ -202,14 +214,17 @@ class Conv1DLayer : public Layer {
     return k::conv1d_direct_num_chunks(direct_params(B, L));
   }
   // Runs the convolution; `stats` (GroupNorm(1) partials of the pre-activation output) is
-  // optional and must hold 3 * B * stats_chunks(B, L) floats.
-  void run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s) {
+  // optional and must hold 3 * B * stats_chunks(B, L) floats. Output rows are `ldy` apart
+  // (0 = contiguous).
+  // y may be null on the direct path (statistics only).
+  void run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s,
+           int64_t ldy = 0) {
     if (uses_mfma()) {
-      k::gemm(ctx(s), gemm_args(x, B, L, y, act, stats));
+      k::gemm(ctx(s), gemm_args(x, B, L, y, act, stats, ldy));
       return;
     }
-    k::conv1d_direct(ctx(s), direct_params(B, L), x, w_->ptr(), b_ ? b_->ptr() : nullptr, y, act,
-                     stats, nullptr);
+    k::conv1d_direct(ctx(s), direct_params(B, L, ldy), x, w_->ptr(), b_ ? b_->ptr() : nullptr,
+                     y, act, stats, nullptr);
   }
   const mnn_conv1d_desc& desc() const { return p_; }
 
@@ -264,6 +279,13 @@ class GroupNormLayer : public Layer {
                    beta_ ? beta_->ptr() : nullptr, coef_.f32());
   }
   const float* coef() const { return coef_.f32(); }
+  float* reserve_coef(int B) {
+    coef_.reserve(sizeof(float) * 2 * B * C_);
+    return coef_.f32();
+  }
+  float eps() const { return eps_; }
+  const float* gamma() const { return gamma_ ? gamma_->ptr() : nullptr; }
+  const float* beta() const { return beta_ ? beta_->ptr() : nullptr; }
   int groups() const { return G_; }
   int act() const { return act_; }
 
@@ -695,10 +717,53 @@ class EncoderBlockLayer : public Layer {
     split_bcl(in.shape, B, C, L);
     const int Cout = d_.out_channels;
     const int64_t lo = os.back();
+    const bool g1 = norm_->groups() == 1;
+    if (d_.rewrite && g1 && glu_fused_) {
+      // Two launches: (1) conv writing GroupNorm statistics partials; (2) the rewrite GEMM,
+      // whose workgroups merge the partials and read the conv output through GroupNorm + GELU,
+      // GLU in the epilogue.
+      const int nchunk = conv_->stats_chunks((int)B, (int)L);
+      partials_.reserve(sizeof(float) * 3 * B * nchunk);
+      k::GemmArgs g = rewrite_args((int)B, lo, out.f32());
+      if (conv_->recompute_ok((int)B, (int)L)) {
+        // small conv: statistics pass only; the GEMM recomputes the conv while loading
+        conv_->run(in.f32(), (int)B, (int)L, nullptr, MNN_ACT_NONE, partials_.f32(), s, 0);
+        const auto& cd = conv_->desc();
+        g.blayout = k::B_CONVREC;
+        g.B = in.f32();
+        g.ldb = L;
+        g.sB = (int64_t)cd.in_channels * L;
+        g.conv_L = (int)L;
+        g.conv_ks = cd.kernel_size;
+        g.conv_stride = cd.stride;
+        g.conv_pad = cd.padding;
+        g.conv_dil = 1;
+        g.conv_reflect = true;
+        g.rc_w = conv_->weight_ptr();
+        g.rc_b = conv_->bias_ptr();
+      } else {
+        // conv rows get a 16-byte pitch so the rewrite GEMM loads them as 16-byte vectors
+        const int64_t pitch = (lo + 3) / 4 * 4;
+        y_.reserve(sizeof(float) * B * Cout * pitch);
+        conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, partials_.f32(), s, pitch);
+        g.B = y_.f32();
+        g.ldb = pitch;
+        g.sB = (int64_t)Cout * pitch;
+        g.blayout = k::B_KN;
+      }
+      g.pro_stats = partials_.f32();
+      g.pro_nparts = nchunk;
+      g.pro_gamma = norm_->gamma();
+      g.pro_beta = norm_->beta();
+      g.pro_eps = norm_->eps();
+      k::gemm(ctx(s), g);
+      return;
+    }
+    // General path (GroupNorm with several groups, no rewrite, or channel counts the fused GLU
+    // epilogue does not take): conv -> statistics -> merge -> apply / GEMM (+ GLU kernel).
     y_.reserve(sizeof(float) * B * Cout * lo);
-    const bool fused_stats = norm_->groups() == 1;
     int nchunk;
-    if (fused_stats) {
+    if (g1) {
       nchunk = conv_->stats_chunks((int)B, (int)L);
       partials_.reserve(sizeof(float) * 3 * B * nchunk);
       conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, partials_.f32(), s);
@@ -714,40 +779,47 @@ class EncoderBlockLayer : public Layer {
       k::gn_apply(ctx(s), y_.f32(), out.f32(), (int)B, Cout, lo, norm_->coef(), MNN_ACT_GELU);
       return;
     }
-    k::GemmArgs g;
-    g.M = 2 * Cout;
-    g.N = (int)lo;
-    g.K = Cout;
-    g.batch = (int)B;
-    g.lda = Cout;
+    k::GemmArgs g = rewrite_args((int)B, lo, out.f32());
     g.B = y_.f32();
     g.ldb = lo;
     g.sB = (int64_t)Cout * lo;
     g.blayout = k::B_KN;
     g.pro_coef = norm_->coef();
-    g.pro_act = MNN_ACT_GELU;
-    g.bias_mode = k::BIAS_M;
-    g.precision = d_.precision;
     if (glu_fused_) {
-      g.A = rw_perm_.f32();
-      g.bias = rb_perm_.f32();
-      g.glu = true;
-      g.C = out.f32();
-      g.ldc = lo;
-      g.sC = (int64_t)Cout * lo;
       k::gemm(ctx(s), g);
     } else {
       z_.reserve(sizeof(float) * B * 2 * Cout * lo);
       g.A = rw_->ptr();
       g.bias = rb_->ptr();
+      g.glu = false;
       g.C = z_.f32();
-      g.ldc = lo;
       g.sC = 2LL * Cout * lo;
       k::gemm(ctx(s), g);
       k::glu(ctx(s), z_.f32(), out.f32(), B, (int64_t)Cout * lo);
     }
   }
 
+ private:
+  // Rewrite 1x1 conv C -> 2C as a GEMM over the block's conv output (operand set by the caller).
+  k::GemmArgs rewrite_args(int B, int64_t lo, float* out) const {
+    const int Cout = d_.out_channels;
+    k::GemmArgs g;
+    g.M = 2 * Cout;
+    g.N = (int)lo;
+    g.K = Cout;
+    g.batch = B;
+    g.lda = Cout;
+    g.A = glu_fused_ ? rw_perm_.f32() : rw_->ptr();
+    g.bias = glu_fused_ ? rb_perm_.f32() : rb_->ptr();
+    g.bias_mode = k::BIAS_M;
+    g.glu = glu_fused_;
+    g.pro_act = MNN_ACT_GELU;
+    g.C = out;
+    g.ldc = lo;
+    g.sC = (int64_t)Cout * lo;
+    g.precision = d_.precision;
+    return g;
+  }
  protected:
   // Rows of the rewrite weight are regrouped into 32-row blocks [a0..a15 | b0..b15] so the GLU
   // partner rows c and c + C meet in one accumulator block of the GEMM.
