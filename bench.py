@@ -164,6 +164,110 @@ def cpu_baseline(m, budget_s=20.0):
     }
 
 
+# ------------------------------------------------------------------ per-configuration table
+def time_gpu(fn, stream, reps):
+    fn()
+    stream.sync()
+    return timed(fn, stream, reps)
+
+
+def time_cpu(fn, budget_s=3.0, max_reps=5):
+    ts = []
+    t_start = time.perf_counter()
+    while len(ts) < max_reps and (not ts or time.perf_counter() - t_start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(ts)
+
+
+def config_table(nn, W, dev, stream, m, cpu=True):
+    """GPU ms, achieved rate and roofline fraction of each BASELINE configuration, with the fp32
+    oracle's CPU time on the host beside it (the oracle is only the CPU baseline here)."""
+    if cpu:
+        import oracle
+    out = {}
+
+    def row(name, gpu_ms, flops=None, byts=None, prec="f32", cpu_ms=None):
+        r = {"gpu_ms": round(gpu_ms, 4)}
+        if flops:
+            r["tflops"] = round(flops / gpu_ms / 1e9, 2)
+            r["mfma_frac"] = round(flops / (gpu_ms * 1e-3) / PEAK[prec], 4)
+        if byts:
+            r["gbps"] = round(byts / gpu_ms / 1e6, 1)
+            r["hbm_frac"] = round(byts / (gpu_ms * 1e-3) / PEAK["hbm"], 4)
+        if cpu_ms is not None:
+            r["cpu_ms"] = round(cpu_ms, 2)
+        out[name] = r
+
+    # config 1: Conv1D 2->48 k8 s4 -> GroupNorm(1) -> GELU (HBM-bound; bytes = x + y)
+    c1 = W.config1()
+    conv = nn.Conv1D(dev, 2, 48, 8, stride=4, padding=0, input_length=44100)
+    conv.load_weights(c1["conv_w"], c1["conv_b"])
+    gn = nn.GroupNorm(dev, 1, 48, activation="gelu")
+    gn.load_parameters(c1["gn_w"], c1["gn_b"])
+    x1 = nn.Tensor.from_numpy(dev, c1["x"])
+    y1 = nn.Tensor(dev, (1, 48, 11024))
+    z1 = nn.Tensor(dev, (1, 48, 11024))
+
+    def f1():
+        conv.forward(x1, y1, stream)
+        gn.forward(y1, z1, stream)
+    cpu1 = time_cpu(lambda: oracle.gelu_layer(oracle.group_norm(oracle.conv1d(
+        c1["x"], c1["conv_w"], c1["conv_b"], stride=4, dtype=np.float32), 1, c1["gn_w"],
+        c1["gn_b"], dtype=np.float32), dtype=np.float32)) if cpu else None
+    row("1_conv_gn_gelu", time_gpu(f1, stream, 20), flops=2.0 * 48 * 11024 * 16,
+        byts=4.0 * (2 * 44100 + 48 * 11024), cpu_ms=cpu1)
+
+    # config 2: Linear 512 -> 2048 on [2048, 512] + LayerNorm(2048), fp32 and bf16 operands
+    c2 = W.config2()
+    x2 = nn.Tensor.from_numpy(dev, c2["x"])
+    y2 = nn.Tensor(dev, (2048, 2048))
+    z2 = nn.Tensor(dev, (2048, 2048))
+    ln = nn.LayerNorm(dev, 2048)
+    ln.load_parameters(c2["ln_w"], c2["ln_b"])
+    cpu2 = time_cpu(lambda: oracle.layer_norm(oracle.linear(c2["x"], c2["w"], c2["b"],
+                                                            dtype=np.float32),
+                                              c2["ln_w"], c2["ln_b"], dtype=np.float32)) \
+        if cpu else None
+    for prec in ("f32", "bf16"):
+        lin = nn.Linear(dev, 512, 2048, precision=prec)
+        lin.load_weights(c2["w"], c2["b"])
+
+        def f2():
+            lin.forward(x2, y2, stream)
+            ln.forward(y2, z2, stream)
+        row(f"2_linear_ln_{prec}", time_gpu(f2, stream, 20), flops=2.0 * 2048 * 2048 * 512,
+            prec=prec, cpu_ms=cpu2 if prec == "f32" else None)
+
+    # config 3: pre-norm MHSA + FFN layer, S 2048, E 512
+    c3 = W.config3()
+    tl = nn.TransformerLayer(dev, c3["embed"], c3["heads"], c3["ffn"])
+    tl.load_state(c3["params"])
+    x3 = nn.Tensor.from_numpy(dev, c3["x"])
+    y3 = nn.Tensor(dev, x3.shape)
+    cpu3 = time_cpu(lambda: oracle.transformer_layer(c3["x"], c3["params"], c3["heads"],
+                                                     dtype=np.float32)) if cpu else None
+    S, E = 2048, 512
+    f3 = 2.0 * S * E * 3 * E + 4.0 * S * S * E + 2.0 * S * E * E + 4.0 * S * E * 2048
+    row("3_transformer_layer", time_gpu(lambda: tl.forward(x3, y3, stream), stream, 10),
+        flops=f3, cpu_ms=cpu3)
+
+    # configs 4 and 5 (the headline pair)
+    enc = encoder_work()
+    f4 = sum(v[0] for v in enc.values())
+    row("4_encoder_b1", time_gpu(lambda: m["seq"].forward(m["chunks"][0], stream), stream, 10),
+        flops=f4)
+    f5 = sum(v[0] for v in transformer_work(W.T5_BATCH).values())
+    row("5_transformer_b4", time_gpu(lambda: run_transformer(m, stream), stream, 5), flops=f5)
+    t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
+    q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
+    to5, fo5 = nn.Tensor(dev, t5.shape), nn.Tensor(dev, q5.shape)
+    row("5_transformer_b1", time_gpu(lambda: m["ct"].forward_cross(t5, q5, to5, fo5, stream),
+                                     stream, 5), flops=f5 / W.T5_BATCH)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +276,7 @@ def main():
     ap.add_argument("--precision", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration table")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -257,6 +362,11 @@ def main():
     roof["traffic"] = traffic
     roof["avg_launch_us"] = round(ktime[dom][1] / ktime[dom][0] * 1e3, 2)
 
+    configs = None
+    if not args.no_configs:
+        log("per-configuration table")
+        configs = config_table(nn, W, dev, stream, m, cpu=not args.no_cpu_baseline)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -285,6 +395,7 @@ def main():
         },
         "roofline": roof,
         "kernels": rows,
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -1,4 +1,7 @@
-// GEMM on the CDNA4 matrix cores, fp32 operands (v_mfma_f32_32x32x2_f32), fp32 accumulation.
+// GEMM on the CDNA4 matrix cores, fp32 accumulation. fp32 operands use v_mfma_f32_32x32x2_f32;
+// with precision BF16 the operands are rounded to bf16 (round to nearest even) as they are read
+// from LDS and multiplied with v_mfma_f32_32x32x16_bf16 (HalfLinear's fp16-in/fp32-accumulate
+// contract, HalfPrecisionLinear.swift:60-212, with bf16). Modes without a bf16 form run in fp32.
 //
 // C[b] = epilogue(A[b] * B[b]) with A [M][K] row-major and these operand modes for B:
 //   B_NK    : B^T stored [N][K] (Linear / attention projections, PyTorch weight layout;
@@ -80,7 +83,7 @@ __device__ __forceinline__ int reflect_index(int p, int L) {
   return p >= L ? 2 * (L - 1) - p : p;
 }
 
-template <int WAVES_M, int WAVES_N, int WM, int WN, int BMODE, int BK>
+template <int WAVES_M, int WAVES_N, int WM, int WN, int BMODE, int BK, bool BF = false>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, 2) void gemm_f32_mfma_kernel(GemmArgs a,
                                                                                  int m_fastest) {
   using Cfg = GemmCfg<WAVES_M, WAVES_N, WM, WN, BMODE, BK>;
@@ -353,6 +356,48 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, 2) void gemm_f32_mfma_kernel
 
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb) {
+      if constexpr (BF) {
+        // bf16 operands (rounded to nearest even from the fp32 tiles), fp32 accumulation:
+        // v_mfma_f32_32x32x16_bf16, lane group g supplies k in [kq, kq + 8) of each step
+#pragma unroll
+        for (int s8 = 0; s8 < 2; ++s8) {
+          const int kq = 32 * kb + 16 * g + 8 * s8;
+          bf16x8 a8[WM], b8[WN];
+#pragma unroll
+          for (int i = 0; i < WM; ++i) {
+            const float* p = As + (arow0 + i * 32) * LDA + kq;
+            const float4 t0 = *reinterpret_cast<const float4*>(p);
+            const float4 t1 = *reinterpret_cast<const float4*>(p + 4);
+            a8[i] = bf16x8{(__bf16)t0.x, (__bf16)t0.y, (__bf16)t0.z, (__bf16)t0.w,
+                           (__bf16)t1.x, (__bf16)t1.y, (__bf16)t1.z, (__bf16)t1.w};
+          }
+#pragma unroll
+          for (int j = 0; j < WN; ++j) {
+            float v[8];
+            if constexpr (Cfg::KN) {
+#pragma unroll
+              for (int t = 0; t < 8; ++t) v[t] = Bs[(kq + t) * LDB + bcol0 + j * 32];
+            } else {
+              const float* p = BMODE == B_CONVW
+                                   ? Bs + (kq >> 3) * Cfg::WP + 4 * (bcol0 + j * 32)
+                                   : Bs + (bcol0 + j * 32) * LDB + kq;
+              const float4 t0 = *reinterpret_cast<const float4*>(p);
+              const float4 t1 = *reinterpret_cast<const float4*>(p + 4);
+              v[0] = t0.x; v[1] = t0.y; v[2] = t0.z; v[3] = t0.w;
+              v[4] = t1.x; v[5] = t1.y; v[6] = t1.z; v[7] = t1.w;
+            }
+            b8[j] = bf16x8{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3],
+                           (__bf16)v[4], (__bf16)v[5], (__bf16)v[6], (__bf16)v[7]};
+          }
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+              acc[s8 % NCH][i][j] =
+                  __builtin_amdgcn_mfma_f32_32x32x16_bf16(a8[i], b8[j], acc[s8 % NCH][i][j], 0, 0, 0);
+        }
+        continue;
+      }
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {  // four groups of four k sub-steps
         const int kq = 32 * kb + 16 * g + 4 * q4;  // first k of this lane's group
@@ -618,6 +663,23 @@ Tile choose_tiles(const GemmArgs& a) {
 template <int WAVES_M, int WAVES_N, int WM, int WN, int BK>
 void launch_mode(const LaunchCtx& c, const GemmArgs& a, dim3 grid, dim3 block, int lay,
                  int m_fastest) {
+  if (a.precision == MNN_PRECISION_BF16 && BK == 32 &&
+      (lay == B_NK || lay == B_KN4 || lay == B_CONVW)) {
+    switch (lay) {
+      case B_NK:
+        return launch(c, "gemm_bf16_mfma_nk",
+                      gemm_f32_mfma_kernel<WAVES_M, WAVES_N, WM, WN, B_NK, 32, true>, grid, block,
+                      0, a, m_fastest);
+      case B_KN4:
+        return launch(c, "gemm_bf16_mfma_kn",
+                      gemm_f32_mfma_kernel<WAVES_M, WAVES_N, WM, WN, B_KN4, 32, true>, grid,
+                      block, 0, a, m_fastest);
+      default:
+        return launch(c, "gemm_bf16_mfma_conv",
+                      gemm_f32_mfma_kernel<WAVES_M, WAVES_N, WM, WN, B_CONVW, 32, true>, grid,
+                      block, 0, a, m_fastest);
+    }
+  }
   if constexpr (BK == 128) {
     switch (lay) {
       case B_NK:

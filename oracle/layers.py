@@ -7,7 +7,7 @@ from __future__ import annotations
 import numpy as np
 
 __all__ = [
-    "reflect_pad", "conv1d", "group_norm", "layer_norm", "gelu_tanh", "gelu_layer",
+    "round_bf16", "reflect_pad", "conv1d", "group_norm", "layer_norm", "gelu_tanh", "gelu_layer",
     "stable_sigmoid", "glu", "activation", "linear", "mha", "feed_forward", "encoder_block",
     "time_encoder", "transformer_layer", "cross_transformer",
 ]
@@ -17,6 +17,19 @@ SQRT_2_OVER_PI = 0.7978845608  # literal used by every reference GELU kernel
 
 def _as(x, dtype):
     return np.asarray(x, dtype=dtype)
+
+
+def round_bf16(x):
+    """fp32 -> bf16 -> fp32 with round-to-nearest-even (the operand rounding of the bf16-input /
+    fp32-accumulate variant; HalfLinear's fp16 contract, HalfPrecisionLinear.swift:60-212)."""
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = a.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    nan = np.isnan(a)
+    if nan.any():
+        out = np.where(nan, np.float32(np.nan), out)
+    return out.reshape(a.shape)
 
 
 def reflect_pad(x, pad: int):

@@ -222,6 +222,58 @@ def test_linear_closed_forms(dev, stream):
                                [[1, 2], [4, 5]], atol=1e-4)
 
 
+# ----------------------------------------------------------------------------- bf16 variant
+# bf16-input / fp32-accumulate: operands rounded to bf16 (RNE), fp32 accumulation.
+# Stated tolerances: against the oracle fed the same bf16-rounded operands, fp32 accumulation
+# only -> |gpu - ref| <= 1e-4 + 1e-3 |ref|; against the fp32 oracle (the north-star bar for
+# bf16 paths) -> max |gpu - ref| <= 2e-2 * max |ref|.
+BF16_RTOL = 2e-2
+
+
+@pytest.mark.parametrize("shape,nin,nout", [((2048, 512), 512, 2048), ((300, 384), 384, 1152)])
+def test_linear_bf16_parity(dev, stream, shape, nin, nout):
+    from tests.conftest import assert_rel_norm
+    say(f"linear bf16 {shape} {nin}->{nout}")
+    x = RNG.standard_normal(shape).astype(np.float32)
+    w = (RNG.standard_normal((nout, nin)) * 0.02).astype(np.float32)
+    b = (RNG.standard_normal(nout) * 0.1).astype(np.float32)
+    layer = nn.Linear(dev, nin, nout, precision="bf16")
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    ref_rounded = oracle.linear(oracle.round_bf16(x), oracle.round_bf16(w), b)
+    assert_close(got, ref_rounded, ATOL, RTOL, "linear bf16 vs rounded-operand oracle")
+    assert_rel_norm(got, oracle.linear(x, w, b), BF16_RTOL, "linear bf16 vs fp32 oracle")
+    # and it is not silently fp32
+    assert np.abs(got - oracle.linear(x, w, b)).max() > 1e-6
+
+
+def test_encoder_block_bf16_parity(dev, stream):
+    from tests.conftest import assert_rel_norm
+    say("encoder block bf16 48->96")
+    x = RNG.uniform(-1, 1, (1, 48, 3001)).astype(np.float32)
+    w = (RNG.standard_normal((96, 48, 8)) * np.sqrt(2 / 384)).astype(np.float32)
+    b = (RNG.standard_normal(96) * 0.1).astype(np.float32)
+    gm, bt = np.ones(96, np.float32), np.zeros(96, np.float32)
+    rw = (RNG.standard_normal((192, 96, 1)) * np.sqrt(2 / 96)).astype(np.float32)
+    rb = np.zeros(192, np.float32)
+    blk = nn.UNetEncoderBlock(dev, 48, 96, 8, 4, 1, rewrite=True, precision="bf16")
+    blk.load_weights(w, b, gm, bt, rw, rb)
+    got = run_layer(blk, x, dev, stream)
+    ref = oracle.encoder_block(x, w, b, gm, bt, 1, rewrite_w=rw, rewrite_b=rb)
+    assert_rel_norm(got, ref, BF16_RTOL, "encoder block bf16")
+
+
+def test_transformer_layer_bf16_parity(dev, stream):
+    from tests.conftest import assert_rel_norm
+    say("transformer layer bf16 (config 3 shape, seq 257)")
+    cfg = workloads.config3(stress=True, seq=257)
+    t = nn.TransformerLayer(dev, cfg["embed"], cfg["heads"], cfg["ffn"], precision="bf16")
+    t.load_state(cfg["params"])
+    got = run_layer(t, cfg["x"], dev, stream)
+    ref = oracle.transformer_layer(cfg["x"], cfg["params"], cfg["heads"])
+    assert_rel_norm(got, ref, BF16_RTOL, "transformer layer bf16")
+
+
 # ----------------------------------------------------------------------------- attention
 MHA_CASES = [
     # B, E, H, Sq, Sk, cross

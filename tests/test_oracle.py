@@ -141,6 +141,13 @@ def test_conv_matches_torch(cin, cout, k, s, p, d, g, mode):
     np.testing.assert_allclose(y, ref.numpy(), rtol=1e-10, atol=1e-10)
 
 
+def test_round_bf16_matches_torch():
+    x = np.concatenate([RNG.standard_normal(20000) * 10, [0.0, -0.0, 1e-40, 3.4e38, -2.5]])
+    x = x.astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).to(torch.float32).numpy()
+    np.testing.assert_array_equal(oracle.round_bf16(x), ref)
+
+
 def test_reflect_pad_matches_torch():
     x = RNG.standard_normal((3, 11))
     ref = F.pad(t64(x)[None], (3, 3), mode="reflect")[0].numpy()
