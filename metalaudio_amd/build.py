@@ -1,6 +1,6 @@
 """Builds libmnn.so (HIP kernels + C++ runtime + C ABI) for gfx950, in-tree.
 
-Usage: python -m metalaudio_amd.build [--jobs N] [--debug]
+Usage: python -m metalaudio_amd.build [--jobs N] [--debug] [--incremental]
 
 The library lands in metalaudio_amd/lib/libmnn.so; every source is compiled by hipcc with
 --offload-arch=gfx950 and packed-fp32 instruction selection disabled.
@@ -60,14 +60,27 @@ def _compile(src: Path, opt: list[str]) -> Path:
     return obj
 
 
-def build(jobs: int | None = None, debug: bool = False, verbose: bool = True) -> Path:
+def _stale(src: Path) -> bool:
+    obj = BUILD / (src.name + ".o")
+    if not obj.exists():
+        return True
+    deps = [src, *CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")]
+    return max(d.stat().st_mtime for d in deps) > obj.stat().st_mtime
+
+
+def build(jobs: int | None = None, debug: bool = False, verbose: bool = True,
+          incremental: bool = False) -> Path:
+    """Compiles every source (or, with incremental, those older than a source or header) and
+    links libmnn.so."""
     BUILD.mkdir(parents=True, exist_ok=True)
     LIB.parent.mkdir(parents=True, exist_ok=True)
     opt = ["-O0", "-g"] if debug else ["-O3"]
     srcs = sources()
-    jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)
+    todo = [s for s in srcs if _stale(s)] if incremental else srcs
+    jobs = jobs or min(max(len(todo), 1), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, opt), srcs))
+        list(ex.map(lambda s: _compile(s, opt), todo))
+    objs = [BUILD / (s.name + ".o") for s in srcs]
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -83,8 +96,10 @@ def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--debug", action="store_true")
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only sources older than a source or header")
     args = ap.parse_args()
-    build(args.jobs, args.debug)
+    build(args.jobs, args.debug, incremental=args.incremental)
 
 
 if __name__ == "__main__":

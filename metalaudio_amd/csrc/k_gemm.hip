@@ -745,6 +745,8 @@ void launch_cfg(const LaunchCtx& c, const GemmArgs& a, const Tile& t) {
 }  // namespace
 
 int gemm_num_tiles(const GemmArgs& a) {
+  MNN_REQUIRE(!gemm_nk_lds_supported(a), MNN_ERR_INVALID_ARGUMENT,
+              "gemm_num_tiles: only GEMMs with per-tile statistics have a tile count");
   const Tile t = choose_tiles(a);
   return (int)(cdiv(a.N, t.bn) * cdiv(a.M, t.bm));
 }
@@ -752,6 +754,7 @@ int gemm_num_tiles(const GemmArgs& a) {
 void gemm(const LaunchCtx& c, const GemmArgs& a) {
   if (a.M <= 0 || a.N <= 0 || a.batch <= 0) return;
   MNN_REQUIRE(a.K > 0, MNN_ERR_INVALID_ARGUMENT, "gemm: K must be positive");
+  if (gemm_nk_lds_supported(a)) return gemm_nk_lds(c, a);
   const Tile t = choose_tiles(a);
   MNN_REQUIRE(!(a.glu && t.id < 0), MNN_ERR_INVALID_CONFIGURATION,
               "gemm: GLU epilogue needs M % 32 == 0 and 16-byte aligned operands");

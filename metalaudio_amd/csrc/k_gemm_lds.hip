@@ -1,0 +1,300 @@
+// fp32 GEMM C = epilogue(A * B^T) for B stored [N][K] (Linear / attention projections / FFN,
+// PyTorch weight layout; Linear.swift:337-352 computes y = x W^T + b), on v_mfma_f32_32x32x2_f32.
+//
+// Operand tiles move from HBM to LDS with the CDNA4 LDS-DMA load (global_load_lds_dwordx4): the
+// data never passes through VGPRs and no ds_write is issued, so the only per-step work besides
+// the matrix cores is one s_barrier and the wave's fragment reads. K advances in 32-deep stages
+// held in a ring of S LDS buffers; the loads of stage kt+S-1 are issued right after the barrier
+// of stage kt, so S-1 stages of HBM/L2 latency are in flight behind the matrix work.
+//
+// LDS layout of one stage: A rows [BM][32 floats] then B rows [BN][32 floats], unpadded
+// (LDS-DMA writes each wave's 64 x 16 bytes contiguously). A row's 16-byte chunk c is stored at
+// slot c ^ f(r), f(r) = (r + r/8) mod 8; the lane that fills slot s of row r fetches chunk s ^ f(r)
+// from global memory (the 8 lanes of a row still read one contiguous 128-byte segment). The
+// fragment reads (32 rows x one chunk per lane group) then hit distinct banks for 32- and 64-bank
+// LDS alike.
+//
+// The loads are issued by inline asm: the compiler's own tracking of LDS-DMA would make every
+// LDS read wait for all outstanding loads (it cannot tell the ring buffers apart), and a
+// __syncthreads would wait for them at every barrier. Here the kernel waits itself for exactly the
+// stage it is about to read (s_waitcnt vmcnt((S-2) * loads per stage)) before the barrier.
+//
+// Within a stage, lane group g = lane/32 owns k in [16g, 16g+16): the MFMA's two k slots are fed
+// k = 16g + 4q + s in sub-step (q, s). A and B use the same assignment, so the sum over k is
+// unchanged, and each lane reads its 4 consecutive k of a row with one 16-byte LDS read.
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mnn {
+namespace k {
+
+using namespace dev;
+
+namespace {
+
+constexpr int kXcds = 8;
+constexpr int BK = 32;
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ int chunk_swizzle(int r) { return (r + (r >> 3)) & 7; }
+
+// Workgroup barrier without the memory fence of __syncthreads (which would wait for every
+// outstanding load). The empty asm statements keep the compiler from moving LDS accesses across
+// it: the s_barrier intrinsic alone is not a memory operation to the optimiser.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16 bytes per lane from `src` into LDS at byte address `lds` + 16 * lane (lds wave-uniform).
+// M0 is named as clobbered for the reader; the compiler treats it as reserved and sets it itself
+// before any instruction of its own that reads it (none in these kernels).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const float* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int WMW, int WNW, int WM, int WN, int S>
+struct LdsCfg {
+  static constexpr int BM = WMW * WM * 32, BN = WNW * WN * 32;
+  static constexpr int NW = WMW * WNW, NT = NW * 64;
+  static constexpr int A_INS = BM / 8 / NW, B_INS = BN / 8 / NW;  // 8 rows per wave load
+  static constexpr int L = A_INS + B_INS;                         // loads per wave per stage
+  static constexpr int STAGE = (BM + BN) * BK;                    // floats
+  static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split over waves");
+  static_assert((S - 2) * L < 64, "vmcnt range");
+};
+
+// C = R + rscale[n] * act(acc + bias) (R, rscale optional). ACT = -1: activation code at run time.
+// Accumulator layout of a 32x32 block: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4,
+// column l%32; each store instruction writes two 128-byte row segments.
+template <int WMW, int WNW, int WM, int WN, int ACT, bool RES>
+__device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
+                                           int n0, int wm, int wn, int lane) {
+  const int g = lane >> 5, l32 = lane & 31;
+  const int bz = blockIdx.z;
+  float* __restrict__ Cp = a.C + (int64_t)bz * a.sC;
+  const float* __restrict__ Rp = RES && a.R ? a.R + (int64_t)bz * a.sR : nullptr;
+  const bool full_m = m0 + WMW * WM * 32 <= a.M;
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+    if (gn >= a.N) continue;
+    const float bn = a.bias_mode == BIAS_N ? a.bias[gn] : 0.f;
+    const float rs = RES && Rp ? (a.rscale ? a.rscale[gn] : 1.f) : 0.f;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int mblk = m0 + wm * WM * 32 + i * 32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
+        if (full_m || gm < a.M) {
+          float val = acc[i][j][v] + bn;
+          if (a.bias_mode == BIAS_M) val += a.bias[gm];
+          val = ACT < 0 ? apply_act(val, a.act) : apply_act(val, ACT);
+          if (RES && Rp) val = Rp[(int64_t)gm * a.ldr + gn] + rs * val;
+          Cp[(int64_t)gm * a.ldc + gn] = val;
+        }
+      }
+    }
+  }
+}
+
+template <int WMW, int WNW, int WM, int WN, int S>
+__global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) {
+  using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, A_INS = Cfg::A_INS, B_INS = Cfg::B_INS;
+  constexpr int STAGE = Cfg::STAGE;
+  __shared__ __attribute__((aligned(1024))) float smem[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int bz = blockIdx.z;
+  // XCD-aware renumbering (workgroups go round robin over the 8 XCDs): consecutive logical tiles,
+  // N fastest, land on one XCD and share the A panel in its L2.
+  const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
+  const int lin = blockIdx.x + gx * blockIdx.y;
+  const int xcd = lin % kXcds, slot = lin / kXcds;
+  const int q = total / kXcds, r = total % kXcds;
+  const int logical = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+  const int tn = logical % gx, tm = logical / gx;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = a.M, N = a.N, K = a.K;
+  const float* __restrict__ A = a.A + (int64_t)bz * a.sA;
+  const float* __restrict__ B = a.B + (int64_t)bz * a.sB;
+
+  // Per-lane global sources of this wave's stage loads (rows past M / N are clamped to the last
+  // row: they are read but their products are never stored).
+  const int lr = lane >> 3, ls = lane & 7;
+  const float* asrc[A_INS];
+  const float* bsrc[B_INS];
+#pragma unroll
+  for (int i = 0; i < A_INS; ++i) {
+    const int rr = (wave * A_INS + i) * 8 + lr;
+    const int gm = min(m0 + rr, M - 1);
+    asrc[i] = A + (int64_t)gm * a.lda + 4 * (ls ^ chunk_swizzle(rr));
+  }
+#pragma unroll
+  for (int i = 0; i < B_INS; ++i) {
+    const int rr = (wave * B_INS + i) * 8 + lr;
+    const int gn = min(n0 + rr, N - 1);
+    bsrc[i] = B + (int64_t)gn * a.ldb + 4 * (ls ^ chunk_swizzle(rr));
+  }
+  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) float*)smem;
+  auto issue = [&](int kt) {
+    const unsigned base = lds0 + 4u * (unsigned)((kt % S) * STAGE);
+#pragma unroll
+    for (int i = 0; i < A_INS; ++i)
+      lds_dma16(asrc[i] + kt * BK,
+                __builtin_amdgcn_readfirstlane(base + 4u * ((wave * A_INS + i) * 8 * BK)));
+#pragma unroll
+    for (int i = 0; i < B_INS; ++i)
+      lds_dma16(bsrc[i] + kt * BK,
+                __builtin_amdgcn_readfirstlane(base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
+  };
+
+  floatx16 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int g = lane >> 5, l32 = lane & 31;
+  int aoff[WM], boff[WN], asw[WM], bsw[WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int rr = wm * WM * 32 + 32 * i + l32;
+    aoff[i] = rr * BK;
+    asw[i] = chunk_swizzle(rr);
+  }
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int rr = wn * WN * 32 + 32 * j + l32;
+    boff[j] = BM * BK + rr * BK;
+    bsw[j] = chunk_swizzle(rr);
+  }
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int s = 0; s < S - 1; ++s)
+    if (s < nk) issue(s);
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt is complete for this wave once at most the S-2 newer stages are outstanding
+    if (kt + S - 2 < nk) wait_vmcnt<(S - 2) * Cfg::L>();
+    else wait_vmcnt<0>();
+    stage_barrier();  // ... and for every wave; stage kt-1 is no longer read
+    if (kt + S - 1 < nk) issue(kt + S - 1);
+    const float* base = smem + (kt % S) * STAGE;
+    float4 fa[4][WM], fb[4][WN];
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int c = 4 * g + q4;
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+        fa[q4][i] = *reinterpret_cast<const float4*>(base + aoff[i] + 4 * (c ^ asw[i]));
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+        fb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
+    }
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q4][i][s], fb[q4][j][s],
+                                                             acc[i][j], 0, 0, 0);
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  // The activation and residual form are uniform: one specialised copy of the store loop each
+  // for the forms the transformer uses, a generic one for the rest.
+  const bool res = a.R != nullptr;
+  if (a.act == 0 && !res) store_tile<WMW, WNW, WM, WN, 0, false>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 0) store_tile<WMW, WNW, WM, WN, 0, true>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 3 && !res) store_tile<WMW, WNW, WM, WN, 3, false>(a, acc, m0, n0, wm, wn, lane);
+  else store_tile<WMW, WNW, WM, WN, -1, true>(a, acc, m0, n0, wm, wn, lane);
+}
+
+struct LdsTile {
+  int id, bm, bn;
+  double eff;  // relative matrix-core efficiency of the tile shape (measured)
+};
+constexpr LdsTile kLdsTiles[] = {
+    {0, 128, 128, 1.00},  // <2,2,2,2> S2, 64 KB LDS, 2 workgroups per CU
+    {1, 128, 64, 0.93},   // <2,2,2,1> S3
+    {2, 64, 128, 0.93},   // <2,2,1,2> S3
+    {3, 64, 64, 0.88},    // <2,2,1,1> S4
+};
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int forced_lds_tile() {
+  static const int v = [] {
+    const char* e = std::getenv("MNN_GEMM_LDS_TILE");
+    return e ? std::atoi(e) : -1;
+  }();
+  return v;
+}
+
+// Per-CU critical path: rounds of 256 concurrent tiles x tile area / shape efficiency.
+const LdsTile& choose_lds_tile(const GemmArgs& a) {
+  const int f = forced_lds_tile();
+  if (f >= 0 && f < (int)(sizeof(kLdsTiles) / sizeof(kLdsTiles[0]))) return kLdsTiles[f];
+  const LdsTile* best = &kLdsTiles[0];
+  double best_cost = 1e300;
+  for (const LdsTile& t : kLdsTiles) {
+    const int64_t tiles = (int64_t)cdiv(a.M, t.bm) * cdiv(a.N, t.bn) * a.batch;
+    const double cost = (double)cdiv(tiles, (int64_t)256) * t.bm * t.bn / t.eff;
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = &t;
+    }
+  }
+  return *best;
+}
+
+template <int WMW, int WNW, int WM, int WN, int S>
+void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
+  using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
+  dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch), block(Cfg::NT);
+  launch(c, "gemm_f32_mfma_nk", gemm_nk_lds_kernel<WMW, WNW, WM, WN, S>, grid, block, 0, a);
+}
+
+}  // namespace
+
+bool gemm_nk_lds_supported(const GemmArgs& a) {
+  return a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
+         a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
+         aligned16(a.B) && !a.glu && a.stats == nullptr && a.pro_coef == nullptr &&
+         a.pro_stats == nullptr;
+}
+
+void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {
+  MNN_REQUIRE(gemm_nk_lds_supported(a), MNN_ERR_INVALID_ARGUMENT,
+              "gemm_nk_lds: operands outside the LDS-DMA path's contract");
+  switch (choose_lds_tile(a).id) {
+    case 0: return launch_lds<2, 2, 2, 2, 2>(c, a);
+    case 1: return launch_lds<2, 2, 2, 1, 3>(c, a);
+    case 2: return launch_lds<2, 2, 1, 2, 3>(c, a);
+    default: return launch_lds<2, 2, 1, 1, 4>(c, a);
+  }
+}
+
+}  // namespace k
+}  // namespace mnn

@@ -111,7 +111,13 @@ struct GemmArgs {
 };
 // Number of output tiles per batch for the tile configuration the launcher will pick.
 int gemm_num_tiles(const GemmArgs& a);
+// Dispatches to the LDS-DMA kernel (k_gemm_lds.hip) when gemm_nk_lds_supported(a), else to the
+// register-staged kernel of k_gemm.hip.
 void gemm(const LaunchCtx& c, const GemmArgs& a);
+// fp32 B_NK GEMM with LDS-DMA operand staging: K % 32 == 0, 16-byte aligned rows, epilogue bias /
+// activation / residual with LayerScale (no GLU, statistics or B prologue).
+bool gemm_nk_lds_supported(const GemmArgs& a);
+void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
 
 // ------------------------------------------------------------------ attention (k_attention.hip)
 struct AttnArgs {
