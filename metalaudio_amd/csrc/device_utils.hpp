@@ -32,6 +32,15 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x / (1.f + __expf(-2.f * u));
 }
 
+// The same function with the division replaced by the hardware reciprocal (about 1 ulp): for
+// operand transforms inside matrix-core loops, where an IEEE division would dominate the work.
+__device__ __forceinline__ float gelu_tanh_fast(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float k1 = 0.044715f;
+  const float u = k0 * fmaf(k1 * x, x * x, x);
+  return x * __builtin_amdgcn_rcpf(1.f + __expf(-2.f * u));
+}
+
 // Reference GELU layer semantics: x > 10 -> x, x < -10 -> 0, else the tanh formula.
 __device__ __forceinline__ float gelu_clamped(float x) {
   return x > 10.f ? x : (x < -10.f ? 0.f : gelu_tanh(x));
@@ -178,6 +187,48 @@ __device__ __forceinline__ float2 gn1_merge(const float* __restrict__ partials, 
   }
   m2 = block_sum_d(m2, sh);
   const double var = ntot > 0.0 ? m2 / ntot : 0.0;  // biased (population) variance
+  float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  if (!isfinite(rstd)) rstd = 0.f;  // reference CPU path guard (Normalization.swift:695-699)
+  return make_float2((float)mean, rstd);
+}
+
+// One-round variant for consumers that merge at every workgroup: each thread sums, in fp64 and in
+// a fixed order, N = sum n_j, S1 = sum n_j mean_j and S2 = sum (M2_j + n_j mean_j^2); one
+// workgroup reduction of the three sums then gives mean = S1 / N and M2 = S2 - N mean^2 (the
+// cancellation costs ~1e-16 * mean^2 / var relative to var in fp64). Uses only LDS barriers
+// (no memory fence), so LDS-DMA loads issued earlier stay in flight. `sh` needs
+// 3 * blockDim.x / 64 doubles of LDS. Returns (mean, rstd) to every thread.
+__device__ __forceinline__ float2 gn1_merge_one_round(const float* __restrict__ partials,
+                                                     int nparts, float eps, double* sh) {
+  double n = 0.0, s1 = 0.0, s2 = 0.0;
+  for (int j = threadIdx.x; j < nparts; j += blockDim.x) {
+    const float* p = partials + (int64_t)j * 3;
+    const double pn = p[0], pm = p[1];
+    n += pn;
+    s1 += pn * pm;
+    s2 += (double)p[2] + pn * pm * pm;
+  }
+  n = wave_sum_d(n);
+  s1 = wave_sum_d(s1);
+  s2 = wave_sum_d(s2);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if (lane == 0) {
+    sh[3 * wid] = n;
+    sh[3 * wid + 1] = s1;
+    sh[3 * wid + 2] = s2;
+  }
+  __builtin_amdgcn_s_waitcnt((0xF) | (0x3 << 14) | (0x7 << 4));  // this wave's LDS writes done
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  double N = 0.0, S1 = 0.0, S2 = 0.0;
+  for (int w = 0; w < nw; ++w) {
+    N += sh[3 * w];
+    S1 += sh[3 * w + 1];
+    S2 += sh[3 * w + 2];
+  }
+  const double mean = N > 0.0 ? S1 / N : 0.0;
+  const double var = N > 0.0 ? fmax(S2 - N * mean * mean, 0.0) / N : 0.0;  // biased variance
   float rstd = (float)(1.0 / sqrt(var + (double)eps));
   if (!isfinite(rstd)) rstd = 0.f;  // reference CPU path guard (Normalization.swift:695-699)
   return make_float2((float)mean, rstd);

@@ -24,6 +24,7 @@
 // unchanged, and each lane reads its 4 consecutive k of a row with one 16-byte LDS read.
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace mnn {
 namespace k {
@@ -32,37 +33,7 @@ using namespace dev;
 
 namespace {
 
-constexpr int kXcds = 8;
 constexpr int BK = 32;
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  // gfx9 s_waitcnt encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-__device__ __forceinline__ int chunk_swizzle(int r) { return (r + (r >> 3)) & 7; }
-
-// Workgroup barrier without the memory fence of __syncthreads (which would wait for every
-// outstanding load). The empty asm statements keep the compiler from moving LDS accesses across
-// it: the s_barrier intrinsic alone is not a memory operation to the optimiser.
-__device__ __forceinline__ void stage_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// 16 bytes per lane from `src` into LDS at byte address `lds` + 16 * lane (lds wave-uniform).
-// M0 is named as clobbered for the reader; the compiler treats it as reserved and sets it itself
-// before any instruction of its own that reads it (none in these kernels).
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void lds_dma16(const float* src, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
 
 template <int WMW, int WNW, int WM, int WN, int S>
 struct LdsCfg {
@@ -123,11 +94,8 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   const int bz = blockIdx.z;
   // XCD-aware renumbering (workgroups go round robin over the 8 XCDs): consecutive logical tiles,
   // N fastest, land on one XCD and share the A panel in its L2.
-  const int gx = gridDim.x, gy = gridDim.y, total = gx * gy;
-  const int lin = blockIdx.x + gx * blockIdx.y;
-  const int xcd = lin % kXcds, slot = lin / kXcds;
-  const int q = total / kXcds, r = total % kXcds;
-  const int logical = xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
+  const int gx = gridDim.x;
+  const int logical = xcd_logical_tile(blockIdx.x + gx * blockIdx.y, gx * gridDim.y);
   const int tn = logical % gx, tm = logical / gx;
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = a.M, N = a.N, K = a.K;
@@ -151,7 +119,7 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
     const int gn = min(n0 + rr, N - 1);
     bsrc[i] = B + (int64_t)gn * a.ldb + 4 * (ls ^ chunk_swizzle(rr));
   }
-  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) float*)smem;
+  const unsigned lds0 = lds_address(smem);
   auto issue = [&](int kt) {
     const unsigned base = lds0 + 4u * (unsigned)((kt % S) * STAGE);
 #pragma unroll
@@ -209,6 +177,7 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
       for (int j = 0; j < WN; ++j)
         fb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
     }
+    __builtin_amdgcn_sched_barrier(0);  // all reads of the stage ahead of the matrix work
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll

@@ -119,6 +119,55 @@ void gemm(const LaunchCtx& c, const GemmArgs& a);
 bool gemm_nk_lds_supported(const GemmArgs& a);
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
 
+// ------------------------------------------------------------------ encoder levels (k_enc.hip)
+// Strided conv (kernel 8, stride 4, dilation 1, groups 1, pad < 4) as an LDS-DMA implicit GEMM:
+// y[b][co][t] (row pitch ldy) = bias + conv. The weights are [Cout][Cinp * 8] with
+// Cinp = enc_conv_padded_cin(Cin) (input channels rounded up to 4, the extra taps zero). With
+// parts set, GroupNorm(1) statistics partials (count, mean, M2) of y before activation:
+// enc_conv_parts per batch, 3 floats each.
+// The kernel is persistent: each workgroup walks a set of output tiles with one LDS-DMA stage
+// ring running across tile boundaries.
+struct EncConvArgs {
+  int B = 1, Cin = 0, Cout = 0;
+  int64_t L = 0, Lout = 0;
+  int pad = 0;
+  bool reflect = true;
+  const float* x = nullptr;  // [B][Cin][L]
+  const float* w = nullptr;  // [Cout][enc_conv_padded_cin(Cin) * 8]
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int64_t ldy = 0;
+  float* parts = nullptr;
+};
+bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
+                        int64_t L);
+int enc_conv_padded_cin(int Cin);
+// Statistics partials per batch the launch writes; K = enc_conv_padded_cin(Cin) * 8.
+int enc_conv_parts(int Cout, int64_t Lout, int K, int batch);
+void enc_conv(const LaunchCtx& c, const EncConvArgs& a);
+// Rewrite 1x1 conv C -> 2C with GLU: out[b][c][t] = z[c] * sigmoid(z[c + C]),
+// z = w * GELU(GroupNorm(y)) + bias, with w / bias regrouped into 32-row blocks
+// [a0..a15 | b0..b15] (GLU partners in one block). GroupNorm(1) comes from the producer's
+// statistics partials (parts, nparts per batch; merged in fp64 in a fixed order) with gamma /
+// beta and eps, or from per-row coefficients coef[b][c] = (scale, shift).
+struct EncRewriteArgs {
+  int B = 1, C = 0;
+  int64_t Lout = 0;
+  const float* w = nullptr;     // [2C][C], regrouped
+  const float* bias = nullptr;  // [2C], regrouped
+  const float* y = nullptr;     // [B][C][ldy], ldy % 4 == 0
+  int64_t ldy = 0;
+  const float* parts = nullptr;
+  int nparts = 0;
+  float eps = 1e-5f;
+  const float* coef = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float* out = nullptr;  // [B][C][ldo]
+  int64_t ldo = 0;
+};
+void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& a);
+
 // ------------------------------------------------------------------ attention (k_attention.hip)
 struct AttnArgs {
   int B = 1, H = 1, Sq = 0, Sk = 0, hd = 0;

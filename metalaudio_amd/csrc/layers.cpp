@@ -702,7 +702,11 @@ class EncoderBlockLayer : public Layer {
   Shape output_shape() const override { return {d_.out_channels, 0}; }
   Shape infer_output(const Shape& in) const override { return conv_->infer_output(in); }
   void load(const std::string& name, const float* data, size_t n) override {
-    if (name.rfind("conv.", 0) == 0) return conv_->load(name.substr(5), data, n);
+    if (name.rfind("conv.", 0) == 0) {
+      conv_->load(name.substr(5), data, n);
+      if (name == "conv.weight") pad_conv_weight(data);
+      return;
+    }
     if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
     if (name == "rewrite.weight" || name == "rewrite.bias") {
       MNN_REQUIRE(d_.rewrite, MNN_ERR_INVALID_ARGUMENT, "block has no rewrite conv");
@@ -718,6 +722,62 @@ class EncoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t lo = os.back();
     const bool g1 = norm_->groups() == 1;
+    if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32 && Cout >= 32 &&
+        Cout <= 512) {
+      // LDS-DMA matrix-core path (k_enc.hip): the conv writes its output with a 16-byte row pitch
+      // and GroupNorm statistics partials; the rewrite GEMM merges them, applies GroupNorm + GELU
+      // to its operand and GLU in its epilogue. A conv outside the implicit-GEMM kernel's
+      // contract (kernel size other than 8 / stride 4) runs on the generic conv path.
+      const auto& cd = conv_->desc();
+      const int pad = conv_->pad_for(L);
+      const int64_t pitch = (lo + 3) / 4 * 4;
+      y_.reserve(sizeof(float) * B * Cout * pitch);
+      k::EncRewriteArgs r;
+      r.B = (int)B;
+      r.C = Cout;
+      r.Lout = lo;
+      r.w = rw_perm_.f32();
+      r.bias = rb_perm_.f32();
+      r.y = y_.f32();
+      r.ldy = pitch;
+      r.gamma = norm_->gamma();
+      r.beta = norm_->beta();
+      r.out = out.f32();
+      r.ldo = lo;
+      if (k::enc_conv_supported(cd.in_channels, Cout, cd.kernel_size, cd.stride, cd.dilation,
+                                cd.groups, pad, L)) {
+        const int nparts =
+            k::enc_conv_parts(Cout, lo, k::enc_conv_padded_cin(cd.in_channels) * 8, (int)B);
+        partials_.reserve(sizeof(float) * 3 * B * nparts);
+        k::EncConvArgs c;
+        c.B = (int)B;
+        c.Cin = cd.in_channels;
+        c.Cout = Cout;
+        c.L = L;
+        c.Lout = lo;
+        c.pad = pad;
+        c.reflect = cd.padding_mode == MNN_PAD_REFLECT;
+        c.x = in.f32();
+        c.w = enc_conv_weight();
+        c.bias = conv_->bias_ptr();
+        c.y = y_.f32();
+        c.ldy = pitch;
+        c.parts = partials_.f32();
+        k::enc_conv(ctx(s), c);
+        r.parts = partials_.f32();
+        r.nparts = nparts;
+        r.eps = norm_->eps();
+      } else {
+        const int nchunk = conv_->stats_chunks((int)B, (int)L);
+        partials_.reserve(sizeof(float) * 3 * B * nchunk);
+        conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, partials_.f32(), s, pitch);
+        r.parts = partials_.f32();
+        r.nparts = nchunk;
+        r.eps = norm_->eps();
+      }
+      k::enc_rewrite(ctx(s), r);
+      return;
+    }
     if (d_.rewrite && g1 && glu_fused_) {
       // Two launches: (1) conv writing GroupNorm statistics partials; (2) the rewrite GEMM,
       // whose workgroups merge the partials and read the conv output through GroupNorm + GELU,
@@ -800,6 +860,27 @@ class EncoderBlockLayer : public Layer {
   }
 
  private:
+  // The implicit-GEMM conv takes input channels in groups of 4: a conv with Cin % 4 != 0 (the
+  // 2-channel first level) gets a copy of its weights with zero taps for the extra channels.
+  void pad_conv_weight(const float* w) {
+    const int cin = d_.in_channels, cip = k::enc_conv_padded_cin(cin), ks = d_.kernel_size;
+    if (cip == cin || ks != 8) return;
+    std::vector<float> p((size_t)d_.out_channels * cip * ks, 0.f);
+    for (int co = 0; co < d_.out_channels; ++co)
+      std::copy_n(w + (size_t)co * cin * ks, (size_t)cin * ks, p.data() + (size_t)co * cip * ks);
+    wpad_.reserve(p.size() * sizeof(float));
+    HIP_CHECK(hipMemcpy(wpad_.ptr, p.data(), p.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+  const float* enc_conv_weight() {
+    if (k::enc_conv_padded_cin(d_.in_channels) == d_.in_channels) return conv_->weight_ptr();
+    if (!wpad_.ptr) {  // weights never loaded: pad the layer's initial values
+      std::vector<float> w((size_t)d_.out_channels * d_.in_channels * d_.kernel_size);
+      HIP_CHECK(hipMemcpy(w.data(), conv_->weight_ptr(), w.size() * sizeof(float),
+                          hipMemcpyDeviceToHost));
+      pad_conv_weight(w.data());
+    }
+    return wpad_.f32();
+  }
   // Rewrite 1x1 conv C -> 2C as a GEMM over the block's conv output (operand set by the caller).
   k::GemmArgs rewrite_args(int B, int64_t lo, float* out) const {
     const int Cout = d_.out_channels;
@@ -854,7 +935,7 @@ class EncoderBlockLayer : public Layer {
   Param* rb_ = nullptr;
   bool glu_fused_ = false;
   DevBuf rw_perm_, rb_perm_;
-  DevBuf y_, partials_, z_;
+  DevBuf y_, partials_, z_, wpad_;
 };
 
 // ------------------------------------------------------------------ transformer building blocks
