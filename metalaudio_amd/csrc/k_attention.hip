@@ -12,9 +12,11 @@
 // the softmax straight into the PV matrix product without a trip through LDS. Per query, the
 // running max is shared across the four lane groups with two xor-shuffles; running sums stay
 // per lane and are combined once at the end. Q is pre-multiplied by scale*log2(e) so the
-// exponentials are exp2. K/V blocks are double-buffered in LDS.
+// exponentials are exp2. K/V blocks move HBM -> LDS by LDS-DMA (lds_dma.hpp) into a two-stage
+// ring, with one barrier per block.
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace mnn {
 namespace k {
@@ -25,15 +27,31 @@ namespace {
 
 constexpr int BKV = 64;
 
-template <int HD, int QW>
-__global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
-  constexpr int NW = 4, BQ = NW * QW, NU = QW / 16, HS = HD / 4, ND = HD / 16, LDK = HD + 4;
-  constexpr int KV_V4 = BKV * HD / 4 / 256;  // float4 per thread per K (or V) block
-  static_assert(BKV * HD / 4 % 256 == 0, "K/V block must split over 256 threads");
-  __shared__ __attribute__((aligned(16))) float Ks[2][BKV * LDK];
-  __shared__ __attribute__((aligned(16))) float Vs[2][BKV * LDK];
+// Stage layout: K rows then V rows of the block, HD/4 16-byte chunks per row plus one padding
+// chunk (row pitch HD + 4 floats keeps 16 consecutive rows on distinct banks). One LDS-DMA
+// instruction fills 64 consecutive chunks, i.e. the K half and the V half are PC instructions each;
+// the padding chunk is loaded as a harmless duplicate of the row's last chunk.
+template <int HD>
+struct AttnCfg {
+  static constexpr int PC = HD / 4 + 1;       // chunks per padded row
+  static constexpr int LDK = PC * 4;          // floats per padded row
+  static constexpr int WL = 2 * PC;           // wave loads (64 chunks each) per stage
+  static constexpr int STAGE = WL * 256;      // floats per stage
+  static constexpr int S = 2;
+  // workgroups per CU the LDS allows (160 KiB per CU); head dim 48 fits three
+  static constexpr int OCC = (S * STAGE * 4) * 3 <= 160 * 1024 ? 3 : 2;
+};
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+template <int HD, int QW>
+__global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(AttnArgs a) {
+  using Cfg = AttnCfg<HD>;
+  constexpr int NW = 4, BQ = NW * QW, NU = QW / 16, HS = HD / 4, ND = HD / 16;
+  constexpr int LDK = Cfg::LDK, PC = Cfg::PC, STAGE = Cfg::STAGE, S = Cfg::S;
+  constexpr int LW = (Cfg::WL + NW - 1) / NW;  // wave loads per wave (the last ones may be idle)
+  __shared__ __attribute__((aligned(1024))) float smem[S * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = lane >> 4, l16 = lane & 15;
   const int b = blockIdx.z, h = blockIdx.y;
   const int qw0 = blockIdx.x * BQ + wave * QW;
@@ -41,6 +59,36 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
   const float* __restrict__ qb = a.q + (int64_t)b * a.q_bs + h * HD;
   const float* __restrict__ kb = a.k + (int64_t)b * a.kv_bs + h * HD;
   const float* __restrict__ vb = a.v + (int64_t)b * a.kv_bs + h * HD;
+
+  // wave load j = i*NW + wave of a stage covers chunks [64j, 64j+64): K rows for j < PC, V rows
+  // after. Lane offsets (row * kv_rs + 4 * chunk) of a full block are computed once.
+  int soff[LW];
+#pragma unroll
+  for (int i = 0; i < LW; ++i) {
+    const int e = ((i * NW + wave) % PC) * 64 + lane;
+    soff[i] = (e / PC) * (int)a.kv_rs + 4 * min(e % PC, PC - 2);
+  }
+  const unsigned lds0 = lds_address(smem);
+  auto issue = [&](int blk) {
+    const unsigned base = lds0 + 4u * (unsigned)((blk % S) * STAGE);
+    const int64_t rowbase = (int64_t)blk * BKV * a.kv_rs;
+    const bool tail = blk * BKV + BKV > a.Sk;
+#pragma unroll
+    for (int i = 0; i < LW; ++i) {
+      const int j = i * NW + wave;
+      if (j < Cfg::WL) {
+        int off = soff[i];
+        if (tail) {  // rows past the last key re-read the last key (their scores are masked)
+          const int e = (j % PC) * 64 + lane;
+          off = min(e / PC, a.Sk - 1 - blk * BKV) * (int)a.kv_rs + 4 * min(e % PC, PC - 2);
+        }
+        lds_dma16((j < PC ? kb : vb) + rowbase + off,
+                  __builtin_amdgcn_readfirstlane(base + 4u * (unsigned)(j * 256)));
+      }
+    }
+  };
+  const int nblk = (a.Sk + BKV - 1) / BKV;
+  issue(0);
 
   // Q fragments: B operand of S^T = K Q^T; lane group G owns d in [G*HS, (G+1)*HS)
   const float qscale = a.scale * 1.4426950408889634f;
@@ -62,32 +110,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     }
   }
 
-  float4 rk[KV_V4], rv[KV_V4];
-  auto load_kv = [&](int kv0) {
-#pragma unroll
-    for (int i = 0; i < KV_V4; ++i) {
-      const int idx = tid + i * 256;
-      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
-      const int kv = kv0 + row;
-      if (kv < a.Sk) {
-        rk[i] = *reinterpret_cast<const float4*>(kb + (int64_t)kv * a.kv_rs + c4 * 4);
-        rv[i] = *reinterpret_cast<const float4*>(vb + (int64_t)kv * a.kv_rs + c4 * 4);
-      } else {
-        rk[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        rv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
-  };
-  auto store_kv = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KV_V4; ++i) {
-      const int idx = tid + i * 256;
-      const int row = idx / (HD / 4), c4 = idx % (HD / 4);
-      *reinterpret_cast<float4*>(&Ks[buf][row * LDK + c4 * 4]) = rk[i];
-      *reinterpret_cast<float4*>(&Vs[buf][row * LDK + c4 * 4]) = rv[i];
-    }
-  };
-
+  // O^T accumulators: MFMA w holds output rows d = ND*i + w (i = MFMA row), so a lane's ND
+  // values of one V row are adjacent (one LDS read) and its outputs are contiguous
   floatx4 o[ND][NU];
   float m[NU], lsum[NU];
 #pragma unroll
@@ -98,18 +122,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     for (int w = 0; w < ND; ++w) o[w][u] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int nblk = (a.Sk + BKV - 1) / BKV;
-  load_kv(0);
-  store_kv(0);
-  __syncthreads();
-
   for (int blk = 0; blk < nblk; ++blk) {
-    const int cur = blk & 1;
+    wait_vmcnt<0>();  // this wave's loads of block blk
+    stage_barrier();  // ... everyone's; block blk-1 is no longer read
+    if (blk + 1 < nblk) issue(blk + 1);
     const int kv0 = blk * BKV;
-    if (blk + 1 < nblk) load_kv(kv0 + BKV);
-
-    const float* ks = Ks[cur];
-    const float* vs = Vs[cur];
+    const float* ks = smem + (blk % S) * STAGE;
+    const float* vs = ks + BKV * LDK;
     // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
     // accumulators interleave and no MFMA waits on the previous one
     floatx4 st[4][NU];
@@ -117,24 +136,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int u = 0; u < NU; ++u) st[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float4 kfr[HS / 4][4];
 #pragma unroll
-    for (int s4 = 0; s4 < HS / 4; ++s4) {
-      float kf[4][4];
+    for (int s4 = 0; s4 < HS / 4; ++s4)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float4 v4 =
-            *reinterpret_cast<const float4*>(ks + (16 * t + l16) * LDK + G * HS + 4 * s4);
-        kf[t][0] = v4.x; kf[t][1] = v4.y; kf[t][2] = v4.z; kf[t][3] = v4.w;
-      }
+      for (int t = 0; t < 4; ++t)
+        kfr[s4][t] = *reinterpret_cast<const float4*>(ks + (16 * t + l16) * LDK + G * HS + 4 * s4);
+    __builtin_amdgcn_sched_barrier(0);  // all K reads ahead of the matrix work
+#pragma unroll
+    for (int s4 = 0; s4 < HS / 4; ++s4)
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-          for (int u = 0; u < NU; ++u)
-            st[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t][s], qf[u][4 * s4 + s], st[t][u],
-                                                             0, 0, 0);
-    }
+          for (int u = 0; u < NU; ++u) {
+            const float kv = s == 0 ? kfr[s4][t].x : s == 1 ? kfr[s4][t].y : s == 2 ? kfr[s4][t].z : kfr[s4][t].w;
+            st[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv, qf[u][4 * s4 + s], st[t][u], 0, 0, 0);
+          }
     // mask keys beyond Sk
     if (kv0 + BKV > a.Sk) {
 #pragma unroll
@@ -157,13 +176,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       const float mnew = fmaxf(m[u], mx);
       const float msafe = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f(m[u] - msafe);
+      const float alpha = __builtin_amdgcn_exp2f(m[u] - msafe);
       float ps = 0.f;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = exp2f(st[t][u][r] - msafe);
+          const float p = __builtin_amdgcn_exp2f(st[t][u][r] - msafe);
           st[t][u][r] = p;
           ps += p;
         }
@@ -172,26 +191,37 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
 #pragma unroll
       for (int w = 0; w < ND; ++w) o[w][u] *= alpha;
     }
-    // O^T += V^T P^T ; k-slot G of step (t, r) is key 16t + 4G + r
+    // V rows this lane needs (key 16t + 4G + r, d = ND*l16 .. +ND-1), read once the scores are
+    // final: holding them across the softmax would exceed the three-workgroups-per-CU budget
+    float vf[4][4][ND];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* vrow = vs + (16 * t + 4 * G + r) * LDK + l16;
+        const float* vrow = vs + (16 * t + 4 * G + r) * LDK + ND * l16;
+        if constexpr (ND == 4) {
+          const float4 v4 = *reinterpret_cast<const float4*>(vrow);
+          vf[t][r][0] = v4.x; vf[t][r][1] = v4.y; vf[t][r][2] = v4.z; vf[t][r][3] = v4.w;
+        } else {
 #pragma unroll
-        for (int w = 0; w < ND; ++w) {
-          const float vf = vrow[16 * w];
-#pragma unroll
-          for (int u = 0; u < NU; ++u)
-            o[w][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf, st[t][u][r], o[w][u], 0, 0, 0);
+          for (int w = 0; w < ND; ++w) vf[t][r][w] = vrow[w];
         }
       }
-
-    if (blk + 1 < nblk) store_kv(cur ^ 1);
-    __syncthreads();
+    // O^T += V^T P^T ; k-slot G of step (t, r) is key 16t + 4G + r
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int w = 0; w < ND; ++w)
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+            o[w][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[t][r][w], st[t][u][r], o[w][u], 0,
+                                                           0, 0);
   }
 
-  // normalise and write O[b][q][h*HD + d]; lane holds d = 16w + 4G + r for query l16
+  // normalise and write O[b][q][h*HD + d]; lane holds d = ND*(4G + r) + w for query l16, i.e.
+  // 4*ND consecutive values
   float* __restrict__ ob = a.o + (int64_t)b * a.o_bs + h * HD;
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
@@ -201,13 +231,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_f32_kernel(AttnArgs a) {
     const float inv = 1.f / (l + 1e-10f);
     const int q = qw0 + 16 * u + l16;
     if (q < a.Sq) {
-      float* orow = ob + (int64_t)q * a.o_rs;
+      float* orow = ob + (int64_t)q * a.o_rs + 4 * ND * G;
 #pragma unroll
-      for (int w = 0; w < ND; ++w) {
-        float4 r4 = make_float4(o[w][u][0] * inv, o[w][u][1] * inv, o[w][u][2] * inv,
-                                o[w][u][3] * inv);
-        *reinterpret_cast<float4*>(orow + 16 * w + 4 * G) = r4;
-      }
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int w = 0; w < ND; ++w) orow[ND * r + w] = o[w][u][r] * inv;
     }
   }
 }
@@ -253,9 +281,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 template <int HD>
 void launch_hd(const LaunchCtx& c, const AttnArgs& a) {
-  // 32 queries per wave when that still gives >= 2 workgroups per CU, else 16
+  // queries per wave: 32 or 16, whichever needs fewer workgroup rounds x queries per workgroup
+  // over the chip's workgroup slots (fewer, longer rounds win ties: K fragments are reused twice)
+  const int64_t slots = (int64_t)c.dev->props.multiProcessorCount * AttnCfg<HD>::OCC;
   const int64_t wg32 = (int64_t)cdiv(a.Sq, 128) * a.H * a.B;
-  if (wg32 >= 512) {
+  const int64_t wg16 = (int64_t)cdiv(a.Sq, 64) * a.H * a.B;
+  const int64_t cost32 = (int64_t)cdiv(wg32, slots) * 2, cost16 = cdiv(wg16, slots);
+  if (cost32 <= cost16) {
     dim3 grid(cdiv(a.Sq, 128), a.H, a.B);
     launch(c, HD == 64 ? "attn_fwd_f32_hd64_q32" : "attn_fwd_f32_hd48_q32",
            attn_fwd_f32_kernel<HD, 32>, grid, dim3(256), 0, a);

@@ -1082,6 +1082,12 @@ class CrossTransformerImpl : public Layer {
     fail(MNN_ERR_INVALID_CONFIGURATION,
          "CrossTransformerEncoder needs two inputs: use forward_cross(time, freq, ...)");
   }
+  // The time and freq branches only meet at the cross-attention exchange, so they run on two
+  // streams: freq on the caller's stream, time on a side stream forked from it, joined back at the
+  // end. Kernels of one branch then fill the CUs the other branch's grid leaves idle. A cross layer
+  // starts with a two-way sync (the exchange buffers of the previous cross layer are free again),
+  // and each attention waits for the other branch's normalised state. With kernel timing on,
+  // everything runs on the caller's stream so launch durations are not stretched by overlap.
   void forward_cross(const Tensor* t, const Tensor* f, Tensor* to, Tensor* fo,
                      Stream& s) override {
     MNN_REQUIRE(t && f && to && fo, MNN_ERR_INVALID_ARGUMENT,
@@ -1093,12 +1099,21 @@ class CrossTransformerImpl : public Layer {
     split_bse(f->shape, Bf, Sf, Ef);
     MNN_REQUIRE(B == Bf, MNN_ERR_SHAPE_MISMATCH, "time and freq batch sizes differ");
     const int64_t rt = B * St, rf = B * Sf;
-    if (to->data != t->data) k::copy_bytes(ctx(s), t->data, to->data, rt * E * 4);
-    if (fo->data != f->data) k::copy_bytes(ctx(s), f->data, fo->data, rf * E * 4);
-    float* T = to->f32();
-    float* F = fo->f32();
     ht_.reserve(sizeof(float) * rt * E * 2);
     hf_.reserve(sizeof(float) * rf * E * 2);
+    const bool two = !dev_->timing;
+    next_event_ = 0;
+    Stream side{s.dev, s.s, false};
+    if (two) {
+      side.s = side_stream();
+      link(s, side);
+    }
+    Stream& ts = side;  // time branch
+    Stream& fs = s;     // freq branch
+    if (to->data != t->data) k::copy_bytes(ctx(ts), t->data, to->data, rt * E * 4);
+    if (fo->data != f->data) k::copy_bytes(ctx(fs), f->data, fo->data, rf * E * 4);
+    float* T = to->f32();
+    float* F = fo->f32();
     float* ht = ht_.f32();
     float* ht2 = ht + rt * E;
     float* hf = hf_.f32();
@@ -1107,34 +1122,70 @@ class CrossTransformerImpl : public Layer {
       Branch& bt = *time_[i];
       Branch& bf = *freq_[i];
       if (!bt.cross) {
-        bt.norm1->run(T, rt, ht, s);
-        bt.attn->run(ht, (int)St, nullptr, 0, (int)B, T, T, bt.ls1(), s);
-        bt.norm2->run(T, rt, ht, s);
-        bt.ffn->run(ht, rt, T, T, bt.ls2(), s);
-        bf.norm1->run(F, rf, hf, s);
-        bf.attn->run(hf, (int)Sf, nullptr, 0, (int)B, F, F, bf.ls1(), s);
-        bf.norm2->run(F, rf, hf, s);
-        bf.ffn->run(hf, rf, F, F, bf.ls2(), s);
+        bt.norm1->run(T, rt, ht, ts);
+        bt.attn->run(ht, (int)St, nullptr, 0, (int)B, T, T, bt.ls1(), ts);
+        bt.norm2->run(T, rt, ht, ts);
+        bt.ffn->run(ht, rt, T, T, bt.ls2(), ts);
+        bf.norm1->run(F, rf, hf, fs);
+        bf.attn->run(hf, (int)Sf, nullptr, 0, (int)B, F, F, bf.ls1(), fs);
+        bf.norm2->run(F, rf, hf, fs);
+        bf.ffn->run(hf, rf, F, F, bf.ls2(), fs);
       } else {
+        if (two) {
+          link(ts, fs);
+          link(fs, ts);
+        }
         // all four normalisations read the states from before this layer
-        bt.norm1->run(T, rt, ht, s);   // time queries
-        bt.norm2->run(F, rf, hf2, s);  // freq as time's keys/values
-        bf.norm1->run(F, rf, hf, s);   // freq queries
-        bf.norm2->run(T, rt, ht2, s);  // time as freq's keys/values
-        bt.attn->run(ht, (int)St, hf2, (int)Sf, (int)B, T, T, bt.ls1(), s);
-        bf.attn->run(hf, (int)Sf, ht2, (int)St, (int)B, F, F, bf.ls1(), s);
-        bt.ffn_norm()->run(T, rt, ht, s);
-        bt.ffn->run(ht, rt, T, T, bt.ls2(), s);
-        bf.ffn_norm()->run(F, rf, hf, s);
-        bf.ffn->run(hf, rf, F, F, bf.ls2(), s);
+        bt.norm1->run(T, rt, ht, ts);   // time queries
+        bf.norm2->run(T, rt, ht2, ts);  // time as freq's keys/values
+        bf.norm1->run(F, rf, hf, fs);   // freq queries
+        bt.norm2->run(F, rf, hf2, fs);  // freq as time's keys/values
+        if (two) {
+          link(fs, ts);  // hf2 ready
+          link(ts, fs);  // ht2 ready
+        }
+        bt.attn->run(ht, (int)St, hf2, (int)Sf, (int)B, T, T, bt.ls1(), ts);
+        bf.attn->run(hf, (int)Sf, ht2, (int)St, (int)B, F, F, bf.ls1(), fs);
+        bt.ffn_norm()->run(T, rt, ht, ts);
+        bt.ffn->run(ht, rt, T, T, bt.ls2(), ts);
+        bf.ffn_norm()->run(F, rf, hf, fs);
+        bf.ffn->run(hf, rf, F, F, bf.ls2(), fs);
       }
     }
+    if (two) link(ts, s);
+  }
+  ~CrossTransformerImpl() override {
+    if (side_) (void)hipStreamDestroy(side_);
+    for (hipEvent_t e : events_) (void)hipEventDestroy(e);
   }
 
  private:
+  hipStream_t side_stream() {
+    if (!side_) {
+      dev_->make_current();
+      HIP_CHECK(hipStreamCreateWithFlags(&side_, hipStreamNonBlocking));
+    }
+    return side_;
+  }
+  // `to` waits for the work queued so far on `from`. Each link of a forward has its own event
+  // (next_event_ restarts at every forward), so no event is recorded twice within one forward.
+  void link(Stream& from, Stream& to) {
+    if (next_event_ == events_.size()) {
+      hipEvent_t e;
+      HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      events_.push_back(e);
+    }
+    hipEvent_t e = events_[next_event_++];
+    HIP_CHECK(hipEventRecord(e, from.s));
+    HIP_CHECK(hipStreamWaitEvent(to.s, e, 0));
+  }
+
   int E_;
   std::vector<std::unique_ptr<Branch>> time_, freq_;
   DevBuf ht_, hf_;
+  hipStream_t side_ = nullptr;
+  std::vector<hipEvent_t> events_;
+  size_t next_event_ = 0;
 };
 
 // ------------------------------------------------------------------ factories
