@@ -4,8 +4,9 @@
 // Operand tiles move from HBM to LDS with the CDNA4 LDS-DMA load (global_load_lds_dwordx4): the
 // data never passes through VGPRs and no ds_write is issued, so the only per-step work besides
 // the matrix cores is one s_barrier and the wave's fragment reads. K advances in 32-deep stages
-// held in a ring of S LDS buffers; the loads of stage kt+S-1 are issued right after the barrier
-// of stage kt, so S-1 stages of HBM/L2 latency are in flight behind the matrix work.
+// held in a ring of S LDS buffers; the loads of stage kt+S are issued once every wave has read
+// stage kt into registers, so up to S-1 stages of HBM/L2 latency are in flight behind the
+// matrix work.
 //
 // LDS layout of one stage: A rows [BM][32 floats] then B rows [BN][32 floats], unpadded
 // (LDS-DMA writes each wave's 64 x 16 bytes contiguously). A row's 16-byte chunk c is stored at
@@ -18,6 +19,7 @@
 // LDS read wait for all outstanding loads (it cannot tell the ring buffers apart), and a
 // __syncthreads would wait for them at every barrier. Here the kernel waits itself for exactly the
 // stage it is about to read (s_waitcnt vmcnt((S-2) * loads per stage)) before the barrier.
+// S = 2 is allowed: the slot of stage kt is refilled as soon as its fragments are in registers.
 //
 // Within a stage, lane group g = lane/32 owns k in [16g, 16g+16): the MFMA's two k slots are fed
 // k = 16g + 4q + s in sub-step (q, s). A and B use the same assignment, so the sum over k is
@@ -43,7 +45,7 @@ struct LdsCfg {
   static constexpr int L = A_INS + B_INS;                         // loads per wave per stage
   static constexpr int STAGE = (BM + BN) * BK;                    // floats
   static_assert(BM % (8 * NW) == 0 && BN % (8 * NW) == 0, "tile rows must split over waves");
-  static_assert((S - 2) * L < 64, "vmcnt range");
+  static_assert((S - 1) * L < 64, "vmcnt range");
 };
 
 // C = R + rscale[n] * act(acc + bias) (R, rscale optional). ACT = -1: activation code at run time.
@@ -155,40 +157,76 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
     bsw[j] = chunk_swizzle(rr);
   }
 
+  // Software pipeline: the fragments of stage kt sit in registers while the matrix cores work on
+  // them. Halfway through stage kt (after the MFMAs of its first two 8-deep k slices) the waves
+  // meet at the barrier that makes stage kt+1 visible and frees the slot of stage kt, issue the
+  // loads of stage kt+S into that slot, and read stage kt+1's fragments interleaved with the
+  // second half's MFMAs, so neither the barrier nor the LDS latency stalls the matrix pipe.
   const int nk = K / BK;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s)
+  for (int s = 0; s < S; ++s)
     if (s < nk) issue(s);
-  for (int kt = 0; kt < nk; ++kt) {
-    // stage kt is complete for this wave once at most the S-2 newer stages are outstanding
-    if (kt + S - 2 < nk) wait_vmcnt<(S - 2) * Cfg::L>();
-    else wait_vmcnt<0>();
-    stage_barrier();  // ... and for every wave; stage kt-1 is no longer read
-    if (kt + S - 1 < nk) issue(kt + S - 1);
+  float4 fa[4][WM], fb[4][WN];
+  auto read_frags = [&](int kt, float4 (&xa)[4][WM], float4 (&xb)[4][WN]) {
     const float* base = smem + (kt % S) * STAGE;
-    float4 fa[4][WM], fb[4][WN];
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int c = 4 * g + q4;
 #pragma unroll
       for (int i = 0; i < WM; ++i)
-        fa[q4][i] = *reinterpret_cast<const float4*>(base + aoff[i] + 4 * (c ^ asw[i]));
+        xa[q4][i] = *reinterpret_cast<const float4*>(base + aoff[i] + 4 * (c ^ asw[i]));
 #pragma unroll
       for (int j = 0; j < WN; ++j)
-        fb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
+        xb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
     }
-    __builtin_amdgcn_sched_barrier(0);  // all reads of the stage ahead of the matrix work
+  };
+  auto mfma_slice = [&](int q4) {
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
+        for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q4][i][s], fb[q4][j][s], acc[i][j],
+                                                           0, 0, 0);
+  };
+  // stage 0: at most the S-1 newer stages may still be in flight
+  if (S - 1 < nk) wait_vmcnt<(S - 1) * Cfg::L>();
+  else wait_vmcnt<0>();
+  stage_barrier();
+  read_frags(0, fa, fb);
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    mfma_slice(0);
+    mfma_slice(1);
+    __builtin_amdgcn_sched_barrier(0);  // the first half's MFMAs stay ahead of the barrier
+    // stage kt+1 is complete for this wave once at most the S-2 newer stages are outstanding
+    if (kt + S - 1 < nk) wait_vmcnt<(S - 2) * Cfg::L>();
+    else wait_vmcnt<0>();
+    stage_barrier();  // ... and for every wave; every wave's reads of stage kt are done
+    if (kt + S < nk) issue(kt + S);
+    float4 na[4][WM], nb[4][WN];
+    read_frags(kt + 1, na, nb);
+    mfma_slice(2);
+    mfma_slice(3);
+    // fragment reads alternate with the first MFMAs of the second half, so the last read has the
+    // remaining MFMAs to complete before the next stage needs it
+    constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
 #pragma unroll
-          for (int j = 0; j < WN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q4][i][s], fb[q4][j][s],
-                                                             acc[i][j], 0, 0, 0);
+    for (int r = 0; r < kReads; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+#pragma unroll
+      for (int i = 0; i < WM; ++i) fa[q4][i] = na[q4][i];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) fb[q4][j] = nb[q4][j];
+    }
   }
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) mfma_slice(q4);
 
   // ---------------------------------------------------------------- epilogue
   // The activation and residual form are uniform: one specialised copy of the store loop each
