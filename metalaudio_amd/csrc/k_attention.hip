@@ -12,8 +12,8 @@
 // the softmax straight into the PV matrix product without a trip through LDS. Per query, the
 // running max is shared across the four lane groups with two xor-shuffles; running sums stay
 // per lane and are combined once at the end. Q is pre-multiplied by scale*log2(e) so the
-// exponentials are exp2. K/V blocks move HBM -> LDS by LDS-DMA (lds_dma.hpp) into a two-stage
-// ring, with one barrier per block.
+// exponentials are exp2. K/V blocks move HBM -> LDS by LDS-DMA (lds_dma.hpp) into two-slot K and
+// V rings, with one barrier per block.
 #include "device_utils.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -27,28 +27,31 @@ namespace {
 
 constexpr int BKV = 64;
 
-// Stage layout: K rows then V rows of the block, HD/4 16-byte chunks per row plus one padding
-// chunk (row pitch HD + 4 floats keeps 16 consecutive rows on distinct banks). One LDS-DMA
-// instruction fills 64 consecutive chunks, i.e. the K half and the V half are PC instructions each;
-// the padding chunk is loaded as a harmless duplicate of the row's last chunk.
+// LDS layout: two K slots then two V slots, each one 64-key block of HD/4 16-byte chunks per row
+// plus one padding chunk (row pitch HD + 4 floats keeps 16 consecutive rows on distinct banks).
+// One LDS-DMA instruction fills 64 consecutive chunks, so a slot is PC instructions; the padding
+// chunk is loaded as a harmless duplicate of the row's last chunk.
 template <int HD>
 struct AttnCfg {
   static constexpr int PC = HD / 4 + 1;       // chunks per padded row
   static constexpr int LDK = PC * 4;          // floats per padded row
-  static constexpr int WL = 2 * PC;           // wave loads (64 chunks each) per stage
-  static constexpr int STAGE = WL * 256;      // floats per stage
-  static constexpr int S = 2;
+  static constexpr int SLOT = PC * 256;       // floats per slot (64 rows)
   // workgroups per CU the LDS allows (160 KiB per CU); head dim 48 fits three
-  static constexpr int OCC = (S * STAGE * 4) * 3 <= 160 * 1024 ? 3 : 2;
+  static constexpr int OCC = (4 * SLOT * 4) * 3 <= 160 * 1024 ? 3 : 2;
 };
 
+// Pipeline per 64-key block j: the K fragments of block j are already in registers, so the
+// scores S^T = K Q^T and the softmax run without touching LDS; then the waves meet at the one
+// barrier of the block, which makes V(j) and K(j+1) visible and frees the slots of K(j) and
+// V(j-1); the loads of K(j+2) and V(j+1) go into those slots, and the PV product of block j runs
+// with V(j)'s fragment reads in front of it and K(j+1)'s fragment reads interleaved with it.
 template <int HD, int QW>
 __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(AttnArgs a) {
   using Cfg = AttnCfg<HD>;
   constexpr int NW = 4, BQ = NW * QW, NU = QW / 16, HS = HD / 4, ND = HD / 16;
-  constexpr int LDK = Cfg::LDK, PC = Cfg::PC, STAGE = Cfg::STAGE, S = Cfg::S;
-  constexpr int LW = (Cfg::WL + NW - 1) / NW;  // wave loads per wave (the last ones may be idle)
-  __shared__ __attribute__((aligned(1024))) float smem[S * STAGE];
+  constexpr int LDK = Cfg::LDK, PC = Cfg::PC, SLOT = Cfg::SLOT;
+  constexpr int LW = (PC + NW - 1) / NW;  // wave loads per wave and slot (the last may be idle)
+  __shared__ __attribute__((aligned(1024))) float smem[4 * SLOT];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -60,35 +63,38 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   const float* __restrict__ kb = a.k + (int64_t)b * a.kv_bs + h * HD;
   const float* __restrict__ vb = a.v + (int64_t)b * a.kv_bs + h * HD;
 
-  // wave load j = i*NW + wave of a stage covers chunks [64j, 64j+64): K rows for j < PC, V rows
-  // after. Lane offsets (row * kv_rs + 4 * chunk) of a full block are computed once.
-  int soff[LW];
+  // wave load j = i*NW + wave of a slot covers chunks [64j, 64j+64); lane byte offsets
+  // (row * kv_rs + 4 * chunk) * 4 of a full block are the same for K and V and computed once
+  unsigned soff[LW];
 #pragma unroll
   for (int i = 0; i < LW; ++i) {
-    const int e = ((i * NW + wave) % PC) * 64 + lane;
-    soff[i] = (e / PC) * (int)a.kv_rs + 4 * min(e % PC, PC - 2);
+    const int e = min(i * NW + wave, PC - 1) * 64 + lane;
+    soff[i] = 4u * (unsigned)((e / PC) * (int)a.kv_rs + 4 * min(e % PC, PC - 2));
   }
   const unsigned lds0 = lds_address(smem);
-  auto issue = [&](int blk) {
-    const unsigned base = lds0 + 4u * (unsigned)((blk % S) * STAGE);
-    const int64_t rowbase = (int64_t)blk * BKV * a.kv_rs;
+  // K block blk -> slot blk % 2, V block blk -> slot 2 + blk % 2
+  auto issue = [&](int blk, bool isv) {
+    const unsigned base = lds0 + 4u * (unsigned)(((isv ? 2 : 0) + (blk & 1)) * SLOT);
+    const float* src = (isv ? vb : kb) + (int64_t)blk * BKV * a.kv_rs;
     const bool tail = blk * BKV + BKV > a.Sk;
 #pragma unroll
     for (int i = 0; i < LW; ++i) {
       const int j = i * NW + wave;
-      if (j < Cfg::WL) {
-        int off = soff[i];
+      if (j < PC) {
+        unsigned off = soff[i];
         if (tail) {  // rows past the last key re-read the last key (their scores are masked)
-          const int e = (j % PC) * 64 + lane;
-          off = min(e / PC, a.Sk - 1 - blk * BKV) * (int)a.kv_rs + 4 * min(e % PC, PC - 2);
+          const int e = j * 64 + lane;
+          off = 4u * (unsigned)(min(e / PC, a.Sk - 1 - blk * BKV) * (int)a.kv_rs +
+                                4 * min(e % PC, PC - 2));
         }
-        lds_dma16((j < PC ? kb : vb) + rowbase + off,
-                  __builtin_amdgcn_readfirstlane(base + 4u * (unsigned)(j * 256)));
+        lds_dma16_s(src, off, base + 4u * (unsigned)(j * 256));
       }
     }
   };
   const int nblk = (a.Sk + BKV - 1) / BKV;
-  issue(0);
+  issue(0, false);
+  issue(0, true);
+  if (nblk > 1) issue(1, false);
 
   // Q fragments: B operand of S^T = K Q^T; lane group G owns d in [G*HS, (G+1)*HS)
   const float qscale = a.scale * 1.4426950408889634f;
@@ -113,36 +119,39 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   // O^T accumulators: MFMA w holds output rows d = ND*i + w (i = MFMA row), so a lane's ND
   // values of one V row are adjacent (one LDS read) and its outputs are contiguous
   floatx4 o[ND][NU];
-  float m[NU], lsum[NU];
+  float mref[NU], lsum[NU];
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
-    m[u] = -INFINITY;
+    mref[u] = 0.f;
     lsum[u] = 0.f;
 #pragma unroll
     for (int w = 0; w < ND; ++w) o[w][u] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int blk = 0; blk < nblk; ++blk) {
-    wait_vmcnt<0>();  // this wave's loads of block blk
-    stage_barrier();  // ... everyone's; block blk-1 is no longer read
-    if (blk + 1 < nblk) issue(blk + 1);
-    const int kv0 = blk * BKV;
-    const float* ks = smem + (blk % S) * STAGE;
-    const float* vs = ks + BKV * LDK;
-    // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
-    // accumulators interleave and no MFMA waits on the previous one
-    floatx4 st[4][NU];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int u = 0; u < NU; ++u) st[t][u] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float4 kfr[HS / 4][4];
+  // K fragments of key tile t: rows 16t + l16, d in [G*HS, (G+1)*HS)
+  float4 kfr[HS / 4][4];
+  auto read_k = [&](int blk, float4 (&kr)[HS / 4][4]) {
+    const float* ks = smem + (blk & 1) * SLOT;
 #pragma unroll
     for (int s4 = 0; s4 < HS / 4; ++s4)
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        kfr[s4][t] = *reinterpret_cast<const float4*>(ks + (16 * t + l16) * LDK + G * HS + 4 * s4);
-    __builtin_amdgcn_sched_barrier(0);  // all K reads ahead of the matrix work
+        kr[s4][t] = *reinterpret_cast<const float4*>(ks + (16 * t + l16) * LDK + G * HS + 4 * s4);
+  };
+  wait_vmcnt<0>();
+  stage_barrier();
+  read_k(0, kfr);
+
+  for (int blk = 0; blk < nblk; ++blk) {
+    const int kv0 = blk * BKV;
+    // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
+    // accumulators interleave and no MFMA waits on the previous one
+    // accumulators start at -mref, so the scores come out relative to the reference maximum
+    floatx4 st[4][NU];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int u = 0; u < NU; ++u) st[t][u] = floatx4{-mref[u], -mref[u], -mref[u], -mref[u]};
 #pragma unroll
     for (int s4 = 0; s4 < HS / 4; ++s4)
 #pragma unroll
@@ -164,7 +173,11 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
 #pragma unroll
             for (int u = 0; u < NU; ++u) st[t][u][r] = -INFINITY;
     }
-    // online softmax per query column
+    // Online softmax with a lazily moved reference: p = exp2(s - mref). The first block sets mref
+    // to its maximum; later blocks move it (rescaling l and O) only when their maximum exceeds
+    // it by more than kTau, so p <= 2^kTau and most blocks skip the rescale. l >= 1 always holds
+    // (the block that set mref contributes exp2(0)), so nothing underflows.
+    constexpr float kTau = 8.f;
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       float mx = -INFINITY;
@@ -174,50 +187,75 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
         for (int r = 0; r < 4; ++r) mx = fmaxf(mx, st[t][u][r]);
       mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float mnew = fmaxf(m[u], mx);
-      const float msafe = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(m[u] - msafe);
+      if (blk == 0 || mx > kTau) {  // uniform per query column
+        const float alpha = __builtin_amdgcn_exp2f(-mx);
+        lsum[u] *= alpha;
+        mref[u] += mx;
+#pragma unroll
+        for (int w = 0; w < ND; ++w) o[w][u] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st[t][u][r] -= mx;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float p = __builtin_amdgcn_exp2f(st[t][u][r] - msafe);
+          const float p = __builtin_amdgcn_exp2f(st[t][u][r]);
           st[t][u][r] = p;
           ps += p;
         }
-      lsum[u] = lsum[u] * alpha + ps;
-      m[u] = mnew;
-#pragma unroll
-      for (int w = 0; w < ND; ++w) o[w][u] *= alpha;
+      lsum[u] += ps;
     }
-    // V rows this lane needs (key 16t + 4G + r, d = ND*l16 .. +ND-1), read once the scores are
-    // final: holding them across the softmax would exceed the three-workgroups-per-CU budget
-    float vf[4][4][ND];
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
+    __builtin_amdgcn_sched_barrier(0);  // scores and softmax stay ahead of the barrier
+    // V(blk) and K(blk+1) have landed for this wave (they are the only loads in flight) ...
+    wait_vmcnt<0>();
+    stage_barrier();  // ... and for every wave; K(blk) and V(blk-1) are no longer read
+    if (blk + 2 < nblk) issue(blk + 2, false);
+    if (blk + 1 < nblk) issue(blk + 1, true);
+    // PV in four key tiles t. The V rows of tile t+1 (key 16(t+1) + 4G + r, d = ND*l16 ..
+    // +ND-1) and the K fragments of tile t of the next block are read while tile t's MFMAs run;
+    // the scheduling barriers keep each tile's reads next to it, which bounds the live registers.
+    const float* vs = smem + (2 + (blk & 1)) * SLOT;
+    const float* ksn = smem + ((blk + 1) & 1) * SLOT;
+    const bool next = blk + 1 < nblk;
+    auto read_v = [&](int t, float (&vr)[4][ND]) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const float* vrow = vs + (16 * t + 4 * G + r) * LDK + ND * l16;
         if constexpr (ND == 4) {
           const float4 v4 = *reinterpret_cast<const float4*>(vrow);
-          vf[t][r][0] = v4.x; vf[t][r][1] = v4.y; vf[t][r][2] = v4.z; vf[t][r][3] = v4.w;
+          vr[r][0] = v4.x; vr[r][1] = v4.y; vr[r][2] = v4.z; vr[r][3] = v4.w;
         } else {
 #pragma unroll
-          for (int w = 0; w < ND; ++w) vf[t][r][w] = vrow[w];
+          for (int w = 0; w < ND; ++w) vr[r][w] = vrow[w];
         }
       }
-    // O^T += V^T P^T ; k-slot G of step (t, r) is key 16t + 4G + r
+    };
+    float vf[2][4][ND];
+    read_v(0, vf[0]);
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int t = 0; t < 4; ++t) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (t + 1 < 4) read_v(t + 1, vf[(t + 1) & 1]);
+      if (next) {
+#pragma unroll
+        for (int s4 = 0; s4 < HS / 4; ++s4)
+          kfr[s4][t] = *reinterpret_cast<const float4*>(ksn + (16 * t + l16) * LDK + G * HS + 4 * s4);
+      }
+      // O^T += V^T P^T ; k-slot G of step (t, r) is key 16t + 4G + r
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
         for (int w = 0; w < ND; ++w)
 #pragma unroll
           for (int u = 0; u < NU; ++u)
-            o[w][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[t][r][w], st[t][u][r], o[w][u], 0,
-                                                           0, 0);
+            o[w][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[t & 1][r][w], st[t][u][r], o[w][u],
+                                                           0, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // normalise and write O[b][q][h*HD + d]; lane holds d = ND*(4G + r) + w for query l16, i.e.
@@ -282,20 +320,22 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 template <int HD>
 void launch_hd(const LaunchCtx& c, const AttnArgs& a) {
   // queries per wave: 32 or 16, whichever needs fewer workgroup rounds x queries per workgroup
-  // over the chip's workgroup slots (fewer, longer rounds win ties: K fragments are reused twice)
+  // over the chip's workgroup slots (fewer, longer rounds win ties: K fragments are reused twice).
+  // At three workgroups per CU (head dim 48) the 32-query form does not fit the register budget.
   const int64_t slots = (int64_t)c.dev->props.multiProcessorCount * AttnCfg<HD>::OCC;
   const int64_t wg32 = (int64_t)cdiv(a.Sq, 128) * a.H * a.B;
   const int64_t wg16 = (int64_t)cdiv(a.Sq, 64) * a.H * a.B;
   const int64_t cost32 = (int64_t)cdiv(wg32, slots) * 2, cost16 = cdiv(wg16, slots);
-  if (cost32 <= cost16) {
-    dim3 grid(cdiv(a.Sq, 128), a.H, a.B);
-    launch(c, HD == 64 ? "attn_fwd_f32_hd64_q32" : "attn_fwd_f32_hd48_q32",
-           attn_fwd_f32_kernel<HD, 32>, grid, dim3(256), 0, a);
-  } else {
-    dim3 grid(cdiv(a.Sq, 64), a.H, a.B);
-    launch(c, HD == 64 ? "attn_fwd_f32_hd64_q16" : "attn_fwd_f32_hd48_q16",
-           attn_fwd_f32_kernel<HD, 16>, grid, dim3(256), 0, a);
+  if constexpr (AttnCfg<HD>::OCC < 3) {
+    if (cost32 <= cost16) {
+      dim3 grid(cdiv(a.Sq, 128), a.H, a.B);
+      return launch(c, "attn_fwd_f32_hd64_q32", attn_fwd_f32_kernel<HD, 32>, grid, dim3(256), 0,
+                    a);
+    }
   }
+  dim3 grid(cdiv(a.Sq, 64), a.H, a.B);
+  launch(c, HD == 64 ? "attn_fwd_f32_hd64_q16" : "attn_fwd_f32_hd48_q16",
+         attn_fwd_f32_kernel<HD, 16>, grid, dim3(256), 0, a);
 }
 
 }  // namespace

@@ -43,6 +43,13 @@ __device__ __forceinline__ void lds_dma16(const float* src, unsigned lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
                : "memory", "m0");
 }
+// Same copy with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset: the
+// address arithmetic of a moving window is then one scalar add per load, no VALU work.
+__device__ __forceinline__ void lds_dma16_s(const float* sbase, unsigned voff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+               "s"(lds)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // LDS byte address of a __shared__ object.
