@@ -55,6 +55,9 @@ def encoder_work():
         f = fam.setdefault("enc_rewrite_f32", [0.0, 0.0])
         f[0] += rw_flops
         f[1] += rw_bytes
+        # GroupNorm + GELU pass: reads the conv output, writes the rewrite operand
+        f = fam.setdefault("enc_gn_gelu_t_f32", [0.0, 0.0])
+        f[1] += 4.0 * 2 * cout * lo
         L = lo
     return fam
 
@@ -312,8 +315,9 @@ def main():
     ms_step_events = timed(step, stream, args.steps)
     dev.set_kernel_timing(False)
     fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
-            "gemm_f32_simple", "enc_conv_f32", "enc_rewrite_f32", "conv1d_direct", "layernorm",
-            "gn_stats", "gn_finalize", "gn_apply", "copy_bytes", "glu", "gelu"]
+            "gemm_f32_simple", "enc_conv_f32", "enc_conv_reduce_f32", "enc_gn_gelu_t_f32",
+            "enc_rewrite_f32", "conv1d_direct", "layernorm", "gn_stats", "gn_finalize",
+            "gn_apply", "copy_bytes", "glu_f32", "gelu_f32"]
     ktime = {}
     for f in fams:
         n, ms = dev.kernel_timing(f)

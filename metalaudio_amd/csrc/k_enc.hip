@@ -1,31 +1,32 @@
-// Encoder-level kernels on the matrix cores (v_mfma_f32_32x32x2_f32) with LDS-DMA staging:
+// Encoder-level kernels (one UNet encoder block = strided conv -> GroupNorm(1) + GELU -> 1x1
+// rewrite conv C -> 2C -> GLU):
 //
-//   enc_conv     strided Conv1D, kernel 8 / stride 4 / dilation 1 / groups 1, zero or reflect
-//                padding < 4 (DynamicConv1D.swift:288-324,358-401; UNet.swift:52), as an implicit
-//                GEMM C[co][t] = bias[co] + sum_{ci,k} W[co][ci*8+k] * x[ci][4t - pad + k], with
-//                per-workgroup GroupNorm(1) statistics partials of C (Normalization.swift:479-597:
-//                biased variance);
-//   enc_rewrite  the 1x1 rewrite conv C -> 2C as a GEMM over the conv output read through
-//                GroupNorm + GELU (statistics merged once per workgroup, applied to the operand
-//                fragments in registers), with GLU (NN.metal:1012-1023) in the epilogue.
+//   enc_conv_kernel       strided Conv1D, kernel 8 / stride 4 / dilation 1 / groups 1, zero or
+//                         reflect padding < 4 (DynamicConv1D.swift:288-324,358-401; UNet.swift:52),
+//                         as an implicit GEMM on v_mfma_f32_32x32x2_f32:
+//                         y[co][t] = bias[co] + sum_{ci,j} W[co][ci*8+j] * x[ci][4t - pad + j],
+//                         with per-workgroup GroupNorm(1) statistics partials of y (biased
+//                         variance, Normalization.swift:479-597); deep levels split K over
+//                         workgroups and finish in enc_conv_reduce_kernel;
+//   enc_gn_gelu_t_kernel  z = GELU(GroupNorm(y)) written transposed, z^T[t][k] (k padded to a
+//                         multiple of 32 with zeros): the B operand of the rewrite GEMM;
+//   rewrite               the fp32 LDS-DMA GEMM of k_gemm_lds.hip over z^T with the GLU epilogue
+//                         (NN.metal:1012-1023).
 //
-// Both kernels are persistent (one or two workgroups per CU, each walking a set of output tiles).
-// The statistics hand-off needs no cross-workgroup synchronisation inside the conv: a
-// device-scope fence there writes back and invalidates the XCD's L2 under the other workgroups.
+// The conv kernel has the structure of the transformer GEMM (k_gemm_lds.hip): 64x64 output blocks
+// per wave, operands staged by LDS-DMA in a ring of S stages of 32 k (= 4 input channels), the
+// one barrier per stage placed halfway through the stage, and the next stage's fragments read
+// while the second half's MFMAs run. A is the padded weight matrix [Cout][Cinp*8] in the swizzled
+// [rows][32 floats] layout. B is never materialised: a stage holds, per input channel, the window
+// of BN + 1 consecutive 16-byte chunks x[ci][4*n0 - pad + 4c .. +3] (c = 0..BN), and the operand
+// of output column t, taps 4h..4h+3 (h = 0, 1), is chunk t - n0 + h: one 16-byte LDS read. Chunks
+// that cross a signal end are loaded clamped to x[0..3] / x[L-4..L-1], which holds every sample
+// their reflect (or zero) padding needs, and are rewritten in LDS by the lane that loaded them
+// (edge tiles only).
 //
-// Both stage their operands in a ring of S LDS buffers filled by LDS-DMA loads (lds_dma.hpp) and
-// meet at one barrier per stage. A (the weights, [M][K] rows) uses the swizzled [rows][32 floats]
-// layout of the transformer GEMM. The conv's B operand is the raw input: per stage 4 channels x
-// (4*BN + 4) consecutive samples, fetched as 16-byte chunks from 4-byte aligned addresses; im2col
-// exists neither in HBM nor in LDS, and lane (t, k) reads its 4 taps x[ci][4t + k..k+3] as one
-// 16-byte LDS read. Chunks that cross the signal ends are rewritten in LDS with their reflect /
-// zero values after they land (first and last tiles only). The rewrite's B operand is [K][N] rows
-// with a 16-byte pitch; row r's chunk j sits at slot j ^ 8*((r/16) mod 2), which keeps the two
-// lane halves (k and k + 16) on different banks.
-//
-// Deep, narrow levels (few output tiles, long K) split K inside the workgroup: KG groups of waves
-// each own a 32-deep slice of every stage, and their accumulators are summed through LDS at the
-// end, so a 32x64 tile still keeps 8 waves busy on its CU.
+// GroupNorm + GELU is applied once per element in its own pass (HBM bound) rather than on the
+// rewrite GEMM's operand fragments: on CDNA4 the VALU work of a wave does not overlap fp32 MFMAs
+// on its SIMD, and the operand transform would be repeated for every M tile.
 #include "device_utils.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -37,212 +38,139 @@ using namespace dev;
 
 namespace {
 
-enum { ENC_CONV = 0, ENC_RW = 1 };
-constexpr int kMaxM = 1024;  // output rows (bias staged in LDS)
-constexpr int kMaxK = 512;   // rewrite operand rows (GroupNorm coefficients staged in LDS)
+constexpr int BK = 32;
 
-template <int MODE, int WMW, int WNW, int WM, int WN, int KG, int S>
-struct EncCfg {
+template <int WMW, int WNW, int WM, int WN, int S>
+struct ConvCfg {
   static constexpr int BM = WMW * WM * 32, BN = WNW * WN * 32;
-  static constexpr int NWO = WMW * WNW;  // waves per k-group: one output tile
-  static constexpr int NW = NWO * KG, NT = NW * 64;
-  static constexpr int BK = 32 * KG;  // k per stage
-  static constexpr int A_FLOATS = KG * BM * 32;
-  static constexpr int A_INS = KG * BM / 8;  // 8 rows of 32 floats per wave load
-  static constexpr int WCH = BN + 1;         // conv: 16-byte chunks per channel window
-  static constexpr int B_RAW = MODE == ENC_CONV ? KG * 4 * WCH : KG * 32 * BN / 4;
-  static constexpr int B_INS = (B_RAW + 64 * NW - 1) / (64 * NW) * NW;
-  static constexpr int B_FLOATS = B_INS * 256;
-  static constexpr int A_INS_W = A_INS / NW, B_INS_W = B_INS / NW;
-  static constexpr int L = A_INS_W + B_INS_W;  // loads per wave per stage
-  static constexpr int STAGE = A_FLOATS + B_FLOATS;
-  static constexpr int RED = (KG - 1) * BM * BN;  // k-group reduction area after the ring
-  static_assert(A_INS % NW == 0, "A loads must split evenly over the waves");
-  static_assert(MODE == ENC_CONV || BN >= 64, "rewrite B swizzle needs 16 chunks per row");
-  static_assert((S - 2) * L < 64, "vmcnt range");
-  static_assert(S >= 2, "ring depth");
+  static constexpr int NW = WMW * WNW, NT = NW * 64;
+  static constexpr int A_WL = BM / 8;            // A wave loads per stage (8 rows of 32 floats)
+  static constexpr int WCH = BN + 1;             // chunks per channel window
+  static constexpr int B_CH = 4 * WCH;           // B chunks per stage
+  static constexpr int B_WL = (B_CH + 63) / 64;  // B wave loads per stage
+  static constexpr int T = A_WL + B_WL;          // wave loads per stage
+  static constexpr int L = (T + NW - 1) / NW;    // per wave (waves >= T % NW issue L - 1)
+  static constexpr int A_FLOATS = BM * 32;
+  static constexpr int STAGE = A_FLOATS + B_WL * 256;
+  static_assert((S - 1) * L < 64, "vmcnt range");
 };
 
-struct EncArgs {
-  int M = 0, N = 0, K = 0, batch = 1;
-  const float* A = nullptr;  // weights [M][K], row stride lda
-  int64_t lda = 0;
-  // conv: input x[b][ci][L] (batch stride x_bs)
-  const float* x = nullptr;
+struct ConvKArgs {
+  int M = 0, N = 0, K = 0;  // Cout, Lout, Cinp * 8
+  int Cin = 0, L = 0, pad = 0;
+  bool reflect = true;
+  const float* W = nullptr;  // [M][K]
+  const float* x = nullptr;  // [b][Cin][L]
   int64_t x_bs = 0;
-  int Cin = 0;  // real input channels; K = 8 * Cin rounded up to 4 channels (zero weights)
-  int L = 0, pad = 0;
-  bool reflect = false;
-  // rewrite: B rows [K][ldb] (ldb % 4 == 0, >= N rounded up to 4), batch stride sB
-  const float* Bm = nullptr;
-  int64_t ldb = 0, sB = 0;
-  const float* coef = nullptr;  // [batch][K][2] (scale, shift) per operand row, or null and ...
-  const float* gamma = nullptr;
-  const float* beta = nullptr;
-  // output: C[b][m][n] (conv) or GLU rows C[b][m/2][n] (rewrite), row stride ldc
-  float* C = nullptr;
-  int64_t ldc = 0, sC = 0;
-  const float* bias = nullptr;  // per row m
-  // ... GroupNorm(1) statistics partials (count, mean, M2): written by the conv (one per
-  // workgroup, nparts per batch), merged by the rewrite
-  float* parts = nullptr;
-  int nparts = 0;
-  float eps = 1e-5f;
+  const float* bias = nullptr;
+  float* y = nullptr;  // splits == 1: y[b][m][n], row pitch ldy
+  int64_t ldy = 0, y_bs = 0;
+  float* parts = nullptr;  // splits == 1: statistics partial per workgroup
+  float* ws = nullptr;     // splits > 1: ws[((b * splits + s) * M + m) * N + n]
+  int splits = 1;
 };
 
-__device__ __forceinline__ int reflect_or_clamp(int p, int L) {
-  p = p < 0 ? -p : p;
-  p = p >= L ? 2 * (L - 1) - p : p;
-  return min(max(p, 0), L - 1);  // columns past the output never need more than a valid sample
+// Value of padded-signal position p given the 4 samples of the clamped chunk starting at q0.
+__device__ __forceinline__ float padded_sample(const float4& v, int p, int q0, int L,
+                                               bool reflect) {
+  int q = p;
+  if (reflect) {
+    q = q < 0 ? -q : q;
+    q = q > L - 1 ? 2 * (L - 1) - q : q;
+  } else if (p < 0 || p > L - 1) {
+    return 0.f;
+  }
+  const int i = min(max(q - q0, 0), 3);  // outside 0..3 only for chunks no stored column uses
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
 }
 
-template <int MODE, int WMW, int WNW, int WM, int WN, int KG, int S>
-__global__ __launch_bounds__(WMW* WNW* KG * 64) void enc_gemm_kernel(EncArgs a) {
-  using Cfg = EncCfg<MODE, WMW, WNW, WM, WN, KG, S>;
-  constexpr int BM = Cfg::BM, BN = Cfg::BN, NWO = Cfg::NWO, NT = Cfg::NT, BK = Cfg::BK;
-  constexpr int STAGE = Cfg::STAGE, WCH = Cfg::WCH;
-  __shared__ __attribute__((aligned(1024))) float smem[S * STAGE + Cfg::RED];
-  __shared__ float2 coef_s[MODE == ENC_RW ? kMaxK : 1];
-  __shared__ float bias_s[kMaxM];
-  __shared__ float red[3 * (NT / 64)];
-  __shared__ double redd[3 * (NT / 64)];
+template <int WMW, int WNW, int WM, int WN, int S, bool SPLIT>
+__global__ __launch_bounds__(WMW* WNW * 64) void enc_conv_kernel(ConvKArgs a) {
+  using Cfg = ConvCfg<WMW, WNW, WM, WN, S>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::NW, L = Cfg::L, T = Cfg::T;
+  constexpr int A_WL = Cfg::A_WL, WCH = Cfg::WCH, STAGE = Cfg::STAGE;
+  __shared__ __attribute__((aligned(1024))) float smem[S * STAGE];
+  __shared__ float red[3 * NW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = wave / NWO, wo = wave % NWO;
-  const int wm = wo / WNW, wn = wo % WNW;
-  const int b = blockIdx.z;
-  const int M = a.M, N = a.N, K = a.K;
-  const int mt = (M + BM - 1) / BM, ntl = (N + BN - 1) / BN;
-  const int tiles = mt * ntl;  // per batch
-  const int G = gridDim.x;
-  // persistent: workgroup wg takes tiles wg, wg + G, ...; workgroups of one XCD get consecutive
-  // ids, so the tiles in flight on an XCD are neighbours (M fastest: they share a B panel)
-  const int wg = xcd_logical_tile(blockIdx.x, G);
-  const int my_tiles = wg < tiles ? (tiles - 1 - wg) / G + 1 : 0;
-  const int nk = (K + BK - 1) / BK;
-  const int iters = my_tiles * nk;
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int b = blockIdx.z / a.splits, sp = blockIdx.z % a.splits;
+  const int gx = gridDim.x;
+  const int tile = xcd_logical_tile(blockIdx.x + gx * blockIdx.y, gx * gridDim.y);
+  const int tn = tile % gx, tm = tile / gx;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int M = a.M, N = a.N, K = a.K, Ls = a.L;
+  const int nk = K / BK / a.splits, kt0 = sp * nk;
+  const float* __restrict__ xb = a.x + (int64_t)b * a.x_bs;
 
-  // ------------------------------------------------ per-lane, tile-independent load geometry
-  int arow[Cfg::A_INS_W], acol[Cfg::A_INS_W];
+  // ---- per-lane load geometry: wave load j = i*NW + wave of a stage is A (j < A_WL) or B
+  unsigned off[L];      // byte offset from the stage's scalar base
+  int bpos[L], bch[L];  // B: window chunk start position (unclamped), channel within the stage
+  bool bvalid[L];
 #pragma unroll
-  for (int i = 0; i < Cfg::A_INS_W; ++i) {
-    const int ins = wave * Cfg::A_INS_W + i;
-    const int kgi = ins / (BM / 8), r = (ins % (BM / 8)) * 8 + (lane >> 3);
-    arow[i] = r;
-    acol[i] = kgi * 32 + 4 * ((lane & 7) ^ chunk_swizzle(r));
-  }
-  // conv: channel within the stage and window chunk; rewrite: row within the stage and chunk
-  int bsel[Cfg::B_INS_W], bchk[Cfg::B_INS_W];
-  bool bval[Cfg::B_INS_W];
-#pragma unroll
-  for (int i = 0; i < Cfg::B_INS_W; ++i) {
-    const int e = (wave * Cfg::B_INS_W + i) * 64 + lane;
-    bval[i] = e < Cfg::B_RAW;
-    const int ee = bval[i] ? e : 0;  // padding chunks load a valid, unused address
-    if constexpr (MODE == ENC_CONV) {
-      bsel[i] = ee / WCH;  // kg * 4 + channel within the slice
-      bchk[i] = ee % WCH;
+  for (int i = 0; i < L; ++i) {
+    const int j = i * NW + wave;
+    bpos[i] = 0;
+    bch[i] = 0;
+    bvalid[i] = false;
+    if (j < A_WL) {
+      const int rr = j * 8 + (lane >> 3);
+      off[i] = 4u * (unsigned)(min(m0 + rr, M - 1) * K + 4 * ((lane & 7) ^ chunk_swizzle(rr)));
     } else {
-      const int kgi = ee / (8 * BN), rem = ee % (8 * BN);
-      const int r = rem / (BN / 4);
-      bchk[i] = (rem % (BN / 4)) ^ (8 * ((r >> 4) & 1));
-      bsel[i] = r + 32 * kgi;
+      const int e = (j - A_WL) * 64 + lane;
+      bvalid[i] = j < T && e < Cfg::B_CH;
+      const int ee = bvalid[i] ? e : 0;  // past the window: a valid address, never read
+      bch[i] = ee / WCH;
+      bpos[i] = 4 * n0 - a.pad + 4 * (ee % WCH);
+      off[i] = 4u * (unsigned)(bch[i] * Ls + min(max(bpos[i], 0), Ls - 4));
     }
   }
-  const float* bbase = MODE == ENC_CONV ? a.x + (int64_t)b * a.x_bs : a.Bm + (int64_t)b * a.sB;
-  auto tile_mn = [&](int ti, int& m0, int& n0) {
-    const int t = wg + ti * G;
-    m0 = (t % mt) * BM;
-    n0 = (t / mt) * BN;
-  };
+  // tiles whose window crosses a signal end rewrite those chunks after they land
+  const bool edge = 4 * n0 - a.pad < 0 || 4 * (n0 + BN) - a.pad + 3 > Ls - 1;
   const unsigned lds0 = lds_address(smem);
-  auto issue = [&](int it) {
-    const int ti = it / nk, kt = it - ti * nk;
-    int m0, n0;
-    tile_mn(ti, m0, n0);
-    const unsigned base = lds0 + 4u * (unsigned)((it % S) * STAGE);
+  auto issue = [&](int kl) {
+    const int kt = kt0 + kl;
+    const unsigned base = lds0 + 4u * (unsigned)((kl % S) * STAGE);
+    const float* asrc = a.W + kt * BK;
+    const float* bsrc = xb + (int64_t)(4 * kt) * Ls;
+    const bool chan_tail = 4 * kt + 4 > a.Cin;  // padded input channels read the last real one
 #pragma unroll
-    for (int i = 0; i < Cfg::A_INS_W; ++i) {
-      const int ins = wave * Cfg::A_INS_W + i;
-      // chunks past K (rewrite tail) are clamped into the row; their B rows are zero
-      const float* src = a.A + (int64_t)min(m0 + arow[i], M - 1) * a.lda +
-                         min(kt * BK + acol[i], K - 4);
-      lds_dma16(src, __builtin_amdgcn_readfirstlane(base + 4u * (ins * 256)));
-    }
-#pragma unroll
-    for (int i = 0; i < Cfg::B_INS_W; ++i) {
-      const int ins = wave * Cfg::B_INS_W + i;
-      const unsigned dst =
-          __builtin_amdgcn_readfirstlane(base + 4u * (Cfg::A_FLOATS + ins * 256));
-      if constexpr (MODE == ENC_CONV) {
-        // channels past Cin (zero weights) read the last real channel
-        const int chan = min(kt * 4 * KG + bsel[i], a.Cin - 1);
-        const int pos = min(max(4 * n0 - a.pad + 4 * bchk[i], 0), a.L - 4);
-        lds_dma16(bbase + (int64_t)chan * a.L + pos, dst);
-      } else {
-        const int row = min(kt * BK + bsel[i], K - 1);
-        lds_dma16(bbase + (int64_t)row * a.ldb + min((int64_t)(n0 + 4 * bchk[i]), a.ldb - 4),
-                  dst);
+    for (int i = 0; i < L; ++i) {
+      const int j = i * NW + wave;
+      if (j < A_WL) {
+        lds_dma16_s(asrc, off[i], base + 4u * (unsigned)(j * 256));
+      } else if (j < T) {
+        unsigned o = off[i];
+        if (chan_tail)
+          o = 4u * (unsigned)((min(4 * kt + bch[i], a.Cin - 1) - 4 * kt) * Ls +
+                              min(max(bpos[i], 0), Ls - 4));
+        lds_dma16_s(bsrc, o, base + 4u * (unsigned)(Cfg::A_FLOATS + (j - A_WL) * 256));
       }
     }
   };
-  // conv: chunks crossing the signal ends get their padded values once the stage has landed
-  auto fix_edges = [&](int it) {
-    if constexpr (MODE == ENC_CONV) {
-      const int ti = it / nk, kt = it - ti * nk;
-      int m0, n0;
-      tile_mn(ti, m0, n0);
-      float* stage = smem + (it % S) * STAGE + Cfg::A_FLOATS;
+  // rewrites this lane's landed chunks of stage kl that cross a signal end (before the barrier)
+  auto fix_edges = [&](int kl) {
+    float* stage = smem + (kl % S) * STAGE + Cfg::A_FLOATS;
 #pragma unroll
-      for (int i = 0; i < Cfg::B_INS_W; ++i) {
-        const int pos = 4 * n0 - a.pad + 4 * bchk[i];
-        if (bval[i] && (pos < 0 || pos + 3 > a.L - 1)) {
-          const int e = (wave * Cfg::B_INS_W + i) * 64 + lane;
-          const float* row = bbase + (int64_t)min(kt * 4 * KG + bsel[i], a.Cin - 1) * a.L;
-          float v[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int p = pos + t;
-            if (a.reflect) v[t] = row[reflect_or_clamp(p, a.L)];
-            else v[t] = (p >= 0 && p < a.L) ? row[p] : 0.f;
-          }
-          *reinterpret_cast<float4*>(stage + 4 * e) = make_float4(v[0], v[1], v[2], v[3]);
-        }
+    for (int i = 0; i < L; ++i) {
+      const int j = i * NW + wave;
+      if (j >= A_WL && j < T && bvalid[i] && (bpos[i] < 0 || bpos[i] + 3 > Ls - 1)) {
+        float4* cp = reinterpret_cast<float4*>(stage + 4 * ((j - A_WL) * 64 + lane));
+        const float4 v = *cp;
+        const int q0 = min(max(bpos[i], 0), Ls - 4);
+        float4 r;
+        r.x = padded_sample(v, bpos[i] + 0, q0, Ls, a.reflect);
+        r.y = padded_sample(v, bpos[i] + 1, q0, Ls, a.reflect);
+        r.z = padded_sample(v, bpos[i] + 2, q0, Ls, a.reflect);
+        r.w = padded_sample(v, bpos[i] + 3, q0, Ls, a.reflect);
+        *cp = r;
       }
     }
+    wait_lgkmcnt0();
   };
-
-  // first stages in flight while the coefficients are prepared
-#pragma unroll
-  for (int s = 0; s < S - 1; ++s)
-    if (s < iters) issue(s);
-  for (int m = tid; m < M; m += NT) bias_s[m] = a.bias ? a.bias[m] : 0.f;
-  // rewrite: GroupNorm coefficients of the operand rows (zero past K); with statistics
-  // partials of the producer, every workgroup merges them the same way (fixed order, fp64)
-  if constexpr (MODE == ENC_RW) {
-    float mean = 0.f, rstd = 0.f;
-    if (!a.coef) {
-      const float2 ms =
-          gn1_merge_one_round(a.parts + (int64_t)b * a.nparts * 3, a.nparts, a.eps, redd);
-      mean = ms.x;
-      rstd = ms.y;
-    }
-    for (int k = tid; k < nk * BK; k += NT) {
-      float2 cf = make_float2(0.f, 0.f);
-      if (k < K) {
-        if (a.coef) {
-          cf = *reinterpret_cast<const float2*>(a.coef + ((int64_t)b * K + k) * 2);
-        } else {
-          const float sc = (a.gamma ? a.gamma[k] : 1.f) * rstd;
-          cf = make_float2(sc, (a.beta ? a.beta[k] : 0.f) - mean * sc);
-        }
-      }
-      coef_s[k] = cf;
-    }
-  }
-  wait_lgkmcnt0();
-  stage_barrier();  // coefficients and bias visible; no memory fence (the stages stay in flight)
+  // this wave's loads: L per stage, or L - 1 for waves past T % NW
+  const bool full = (T % NW == 0) || wave < T % NW;
 
   floatx16 acc[WM][WN];
 #pragma unroll
@@ -253,183 +181,148 @@ __global__ __launch_bounds__(WMW* WNW* KG * 64) void enc_gemm_kernel(EncArgs a) 
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int g = lane >> 5, l32 = lane & 31;
-  int aoff[WM], asw[WM];
+  int aoff[WM], asw[WM], boff[WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
-    const int r = wm * WM * 32 + 32 * i + l32;
-    aoff[i] = kg * BM * 32 + r * 32;
-    asw[i] = chunk_swizzle(r);
+    const int rr = wm * WM * 32 + 32 * i + l32;
+    aoff[i] = rr * BK;
+    asw[i] = chunk_swizzle(rr);
   }
-  int bcol[WN];
 #pragma unroll
-  for (int j = 0; j < WN; ++j) bcol[j] = wn * WN * 32 + 32 * j + l32;
+  for (int j = 0; j < WN; ++j) boff[j] = Cfg::A_FLOATS + 4 * (wn * WN * 32 + 32 * j + l32);
 
-  ShiftedStats st;  // conv: statistics of every output this thread stores
-  float* __restrict__ Cp = a.C + (int64_t)b * a.sC;
-
-  int kt = 0, ti = 0;
-  for (int it = 0; it < iters; ++it) {
-    if (it + S - 2 < iters) wait_vmcnt<(S - 2) * Cfg::L>();
-    else wait_vmcnt<0>();
-    fix_edges(it);
-    if constexpr (MODE == ENC_CONV) wait_lgkmcnt0();
-    stage_barrier();  // stage it is complete everywhere; stage it-1 is no longer read
-    if (it + S - 1 < iters) issue(it + S - 1);
-    const float* As = smem + (it % S) * STAGE;
-    const float* Bs = As + Cfg::A_FLOATS;
-    // all fragment reads of the stage first, so their latency overlaps the matrix work
-    float4 fa[4][WM], fb[4][WN];
+  float4 fa[4][WM], fb[4][WN];
+  // k = 16g + 4q + s of a stage: A column k; B channel (16g + 4q) / 8 = 2g + q/2, taps
+  // 4(q%2)..+3 of output column t = chunk t - n0 + q%2 of that channel's window
+  auto read_frags = [&](int kl, float4 (&xa)[4][WM], float4 (&xb)[4][WN]) {
+    const float* base = smem + (kl % S) * STAGE;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int c = 4 * g + q4;
 #pragma unroll
       for (int i = 0; i < WM; ++i)
-        fa[q4][i] = *reinterpret_cast<const float4*>(As + aoff[i] + 4 * (c ^ asw[i]));
-      if constexpr (MODE == ENC_CONV) {
-        // k = 16g + 4q (within the slice): channel kg*4 + 2g + q/2, taps 4(q%2)..+3
-        const int chan = kg * 4 + 2 * g + (q4 >> 1);
+        xa[q4][i] = *reinterpret_cast<const float4*>(base + aoff[i] + 4 * (c ^ asw[i]));
+      const int chan = 2 * g + (q4 >> 1);
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-          fb[q4][j] = *reinterpret_cast<const float4*>(Bs + chan * (4 * WCH) + 4 * bcol[j] +
-                                                       4 * (q4 & 1));
-      } else {
-        const float* rowp = Bs + (kg * 32 + 16 * g + 4 * q4) * BN;
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          const int col = 4 * ((bcol[j] >> 2) ^ (8 * g)) + (bcol[j] & 3);
-          fb[q4][j] = make_float4(rowp[col], rowp[BN + col], rowp[2 * BN + col],
-                                  rowp[3 * BN + col]);
-        }
-      }
+      for (int j = 0; j < WN; ++j)
+        xb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + chan * (4 * WCH) +
+                                                     4 * (q4 & 1));
     }
-    // keep the reads ahead of the matrix work (the scheduler would otherwise sink each read next
-    // to its first use to save registers, exposing the LDS latency every four MFMAs)
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (MODE == ENC_RW) {
-      // GroupNorm + GELU of the operand rows this lane holds (row k = 16g + 4q + s)
+  };
+  auto mfma_slice = [&](int q4) {
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int kglob = kt * BK + kg * 32 + 16 * g + 4 * q4;
-        float2 cf[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) cf[s] = coef_s[kglob + s];
-#pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          fb[q4][j].x = gelu_tanh_fast(fmaf(fb[q4][j].x, cf[0].x, cf[0].y));
-          fb[q4][j].y = gelu_tanh_fast(fmaf(fb[q4][j].y, cf[1].x, cf[1].y));
-          fb[q4][j].z = gelu_tanh_fast(fmaf(fb[q4][j].z, cf[2].x, cf[2].y));
-          fb[q4][j].w = gelu_tanh_fast(fmaf(fb[q4][j].w, cf[3].x, cf[3].y));
-        }
-      }
-    }
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int i = 0; i < WM; ++i)
-#pragma unroll
-          for (int j = 0; j < WN; ++j) {
-            const float av = s == 0 ? fa[q4][i].x : s == 1 ? fa[q4][i].y : s == 2 ? fa[q4][i].z : fa[q4][i].w;
-            const float bv = s == 0 ? fb[q4][j].x : s == 1 ? fb[q4][j].y : s == 2 ? fb[q4][j].z : fb[q4][j].w;
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc[i][j], 0, 0, 0);
-          }
-
-    if (kt == nk - 1) {
-      // ---------------------------------------------- tile done: k-group reduction, epilogue
-      int m0, n0;
-      tile_mn(ti, m0, n0);
-      if constexpr (KG > 1) {
-        // the reduction area is outside the ring (the next tile's stages are in flight); the
-        // previous tile's reads of it are separated from these writes by a stage barrier
-        float* redf = smem + S * STAGE;
-        if (kg > 0) {
-          float* dst = redf + ((kg - 1) * NWO + wo) * (WM * WN * 1024);
-#pragma unroll
-          for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-#pragma unroll
-              for (int v = 0; v < 16; ++v) dst[((i * WN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
-        }
-        wait_lgkmcnt0();
-        stage_barrier();
-        if (kg == 0) {
-#pragma unroll
-          for (int q = 1; q < KG; ++q) {
-            const float* src = redf + ((q - 1) * NWO + wo) * (WM * WN * 1024);
-#pragma unroll
-            for (int i = 0; i < WM; ++i)
-#pragma unroll
-              for (int j = 0; j < WN; ++j)
-#pragma unroll
-                for (int v = 0; v < 16; ++v)
-                  acc[i][j][v] += src[((i * WN + j) * 16 + v) * 64 + lane];
-          }
-        }
-      }
-      // accumulator layout (32x32 block): lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4,
-      // column l%32
-      if (kg == 0) {
-        if constexpr (MODE == ENC_RW) {
-#pragma unroll
-          for (int i = 0; i < WM; ++i) {
-            const int mblk = m0 + wm * WM * 32 + i * 32;
-            if (mblk >= M) continue;
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-              const int gn = n0 + bcol[j];
-              if (gn >= N) continue;
-#pragma unroll
-              for (int v = 0; v < 8; ++v) {
-                const int rr = 8 * (v / 4) + 4 * g + (v % 4);  // < 16
-                const float va = acc[i][j][v] + bias_s[mblk + rr];
-                const float vb = acc[i][j][v + 8] + bias_s[mblk + 16 + rr];
-                Cp[(int64_t)((mblk >> 5) * 16 + rr) * a.ldc + gn] = va * stable_sigmoid(vb);
-              }
-            }
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < WM; ++i) {
-            const int mblk = m0 + wm * WM * 32 + i * 32;
-#pragma unroll
-            for (int j = 0; j < WN; ++j) {
-              const int gn = n0 + bcol[j];
-#pragma unroll
-              for (int v = 0; v < 16; ++v) {
-                const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
-                if (gm < M && gn < N) {
-                  const float val = acc[i][j][v] + bias_s[gm];
-                  st.add(val);
-                  Cp[(int64_t)gm * a.ldc + gn] = val;
-                }
-              }
-            }
-          }
-        }
-      }
+    for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q4][i][s], fb[q4][j][s], acc[i][j],
+                                                           0, 0, 0);
+  };
+
 #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-      kt = 0;
-      ++ti;
+  for (int s = 0; s < S; ++s)
+    if (s < nk) issue(s);
+  // stage 0: at most the S-1 newer stages may still be in flight
+  if (S - 1 < nk) {
+    if (full) wait_vmcnt<(S - 1) * L>();
+    else wait_vmcnt<(S - 1) * (L - 1)>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  if (edge) fix_edges(0);
+  stage_barrier();
+  read_frags(0, fa, fb);
+  for (int kl = 0; kl + 1 < nk; ++kl) {
+    mfma_slice(0);
+    mfma_slice(1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kl + S - 1 < nk) {
+      if (full) wait_vmcnt<(S - 2) * L>();
+      else wait_vmcnt<(S - 2) * (L - 1)>();
     } else {
-      ++kt;
+      wait_vmcnt<0>();
+    }
+    if (edge) fix_edges(kl + 1);
+    stage_barrier();  // stage kl+1 complete everywhere; every wave's reads of stage kl are done
+    if (kl + S < nk) issue(kl + S);
+    float4 na[4][WM], nb[4][WN];
+    read_frags(kl + 1, na, nb);
+    mfma_slice(2);
+    mfma_slice(3);
+    constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
+#pragma unroll
+    for (int r = 0; r < kReads; ++r) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+#pragma unroll
+      for (int i = 0; i < WM; ++i) fa[q4][i] = na[q4][i];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) fb[q4][j] = nb[q4][j];
     }
   }
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) mfma_slice(q4);
 
-  // ------------------------------------------------ conv: GroupNorm(1) statistics partial
-  if constexpr (MODE == ENC_CONV) {
+  // ---- epilogue; accumulator layout of a 32x32 block: lane l, register v -> row
+  // 8*(v/4) + 4*(l/32) + v%4, column l%32
+  if constexpr (SPLIT) {
+    float* __restrict__ wp = a.ws + ((int64_t)blockIdx.z * M) * N;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int mblk = m0 + wm * WM * 32 + i * 32;
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+        if (gn >= N) continue;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
+          if (gm < M) wp[(int64_t)gm * N + gn] = acc[i][j][v];
+        }
+      }
+    }
+  } else {
+    // bias rows first (the compiler may not move these loads past the stores to y); four
+    // statistics accumulators so the per-element updates are not one dependent chain
+    ShiftedStats st[4];
+    float* __restrict__ yp = a.y + (int64_t)b * a.y_bs;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const int mblk = m0 + wm * WM * 32 + i * 32;
+      float bv[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) bv[v] = a.bias[min(mblk + 8 * (v / 4) + 4 * g + (v % 4), M - 1)];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
+          if (gm < M && gn < N) {
+            const float val = acc[i][j][v] + bv[v];
+            st[v & 3].add(val);
+            yp[(int64_t)gm * a.ldy + gn] = val;
+          }
+        }
+      }
+    }
     if (a.parts) {
       float sn, smean, sm2;
-      st.finish(sn, smean, sm2);
+      st[0].finish(sn, smean, sm2);
+#pragma unroll
+      for (int q = 1; q < 4; ++q) {
+        float n2, mean2, m22;
+        st[q].finish(n2, mean2, m22);
+        welford_combine(sn, smean, sm2, n2, mean2, m22);
+      }
       block_welford(sn, smean, sm2, red);
       if (tid == 0) {
-        float* o = a.parts + ((int64_t)b * G + wg) * 3;
+        float* o = a.parts + ((int64_t)b * gx * gridDim.y + tile) * 3;
         o[0] = sn;
         o[1] = smean;
         o[2] = sm2;
@@ -438,25 +331,111 @@ __global__ __launch_bounds__(WMW* WNW* KG * 64) void enc_gemm_kernel(EncArgs a) 
   }
 }
 
+// Split-K finish: y[b][m][n] = sum_s ws[b][s][m][n] + bias[m] (fixed order). Workgroup (x, m, b)
+// covers columns [kRedCols*x, kRedCols*(x+1)) of row m and writes one GroupNorm(1) statistics
+// partial at parts[(b * M + m) * gridDim.x + x].
+constexpr int kRedThreads = 256, kRedCols = 1024;
+__global__ __launch_bounds__(kRedThreads) void enc_conv_reduce_kernel(
+    const float* __restrict__ ws, int splits, int M, int N, const float* __restrict__ bias,
+    float* __restrict__ y, int64_t ldy, int64_t y_bs, float* __restrict__ parts) {
+  __shared__ float red[3 * kRedThreads / 64];
+  const int m = blockIdx.y, b = blockIdx.z;
+  const int64_t total = (int64_t)M * N;
+  const float* __restrict__ wr = ws + (int64_t)b * splits * total + (int64_t)m * N;
+  float* __restrict__ yr = y + (int64_t)b * y_bs + (int64_t)m * ldy;
+  const float bm = bias[m];
+  ShiftedStats st;
+  const int c0 = blockIdx.x * kRedCols;
+#pragma unroll
+  for (int u = 0; u < kRedCols / kRedThreads; ++u) {
+    const int n = c0 + u * kRedThreads + threadIdx.x;
+    if (n < N) {
+      float v = 0.f;
+      for (int s = 0; s < splits; ++s) v += wr[(int64_t)s * total + n];
+      v += bm;
+      st.add(v);
+      yr[n] = v;
+    }
+  }
+  float sn, smean, sm2;
+  st.finish(sn, smean, sm2);
+  block_welford(sn, smean, sm2, red);
+  if (threadIdx.x == 0) {
+    float* o = parts + (((int64_t)b * M + m) * gridDim.x + blockIdx.x) * 3;
+    o[0] = sn;
+    o[1] = smean;
+    o[2] = sm2;
+  }
+}
+
+// z^T[b][t][k] = GELU(y[b][k][t] * scale_k + shift_k) for k < C, 0 for C <= k < kp. GroupNorm(1)
+// comes from the producer's statistics partials (merged in fp64 in a fixed order, once per
+// workgroup) with gamma / beta, or from per-row coefficients coef[b][k] = (scale, shift).
+// Workgroups walk the 64 x 64 tiles of their batch (grid-stride), transposing through LDS.
+constexpr int kTT = 64;
+__global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
+  __shared__ float tileb[kTT][kTT + 1];
+  __shared__ float2 cf[kTT];
+  __shared__ double redd[3 * 4];
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  float mean = 0.f, rstd = 0.f;
+  if (!a.coef) {
+    const float2 ms =
+        gn1_merge_one_round(a.parts + (int64_t)b * a.nparts * 3, a.nparts, a.eps, redd);
+    mean = ms.x;
+    rstd = ms.y;
+  }
+  const int ntt = (int)((a.Lout + kTT - 1) / kTT), nkt = (a.kp + kTT - 1) / kTT;
+  const float* __restrict__ yb = a.y + (int64_t)b * a.C * a.ldy;
+  float* __restrict__ zb = a.zt + (int64_t)b * a.Lout * a.kp;
+  for (int tile = blockIdx.x; tile < ntt * nkt; tile += gridDim.x) {
+    const int t0 = (tile % ntt) * kTT, k0 = (tile / ntt) * kTT;
+    __syncthreads();  // the previous tile's reads of tileb / cf are done
+    if (tid < kTT) {
+      const int k = k0 + tid;
+      float2 c = make_float2(0.f, 0.f);
+      if (k < a.C) {
+        if (a.coef) {
+          c = *reinterpret_cast<const float2*>(a.coef + ((int64_t)b * a.C + k) * 2);
+        } else {
+          const float sc = (a.gamma ? a.gamma[k] : 1.f) * rstd;
+          c = make_float2(sc, (a.beta ? a.beta[k] : 0.f) - mean * sc);
+        }
+      }
+      cf[tid] = c;
+    }
+    __syncthreads();
+    // load: rows k (channels), columns t contiguous
+    for (int e = tid; e < kTT * kTT; e += 256) {
+      const int r = e / kTT, cidx = e % kTT;
+      const int k = k0 + r, t = t0 + cidx;
+      float v = 0.f;
+      if (k < a.C && t < a.Lout)
+        v = gelu_tanh_fast(fmaf(yb[(int64_t)k * a.ldy + t], cf[r].x, cf[r].y));
+      tileb[r][cidx] = v;
+    }
+    __syncthreads();
+    // store: rows t, columns k contiguous
+    for (int e = tid; e < kTT * kTT; e += 256) {
+      const int r = e / kTT, cidx = e % kTT;
+      const int t = t0 + r, k = k0 + cidx;
+      if (t < a.Lout && k < a.kp) zb[(int64_t)t * a.kp + k] = tileb[cidx][r];
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host-side selection
-struct EncTile {
-  int id, bm, bn, kg, nw, lds_kb;
+struct ConvTile {
+  int id, bm, bn;
+  int lds_kb;  // LDS per workgroup (KiB, rounded up)
+  double eff;  // relative matrix-core efficiency of the shape
 };
-// conv configurations (id -> template arguments in enc_conv); lds_kb: LDS per workgroup as
-// compiled, which bounds the resident workgroups per CU
-// (KiB, rounded up; 160 KiB per CU)
-constexpr EncTile kConvTiles[] = {
-    {0, 32, 64, 1, 2, 75},   // <1,2,1,1> KG1 S7
-    {1, 32, 64, 2, 4, 133},  // <1,2,1,1> KG2 S6
-    {2, 64, 64, 2, 8, 149},  // <2,2,1,1> KG2 S4
-    {3, 32, 64, 4, 8, 149},  // <1,2,1,1> KG4 S3
-    {4, 64, 64, 1, 4, 101},  // <2,2,1,1> KG1 S6
-};
-constexpr EncTile kRwTiles[] = {
-    {0, 64, 64, 1, 4, 105},  // <2,2,1,1> KG1 S6
-    {1, 32, 64, 1, 2, 69},   // <1,2,1,1> KG1 S5
-    {2, 64, 64, 2, 8, 153},  // <2,2,1,1> KG2 S4
-    {3, 32, 64, 2, 4, 137},  // <1,2,1,1> KG2 S5
+constexpr ConvTile kConvTiles[] = {
+    {0, 128, 128, 76, 1.00},  // <2,2,2,2> S3
+    {1, 128, 64, 64, 0.93},   // <2,2,2,1> S3
+    {2, 64, 128, 52, 0.93},   // <2,2,1,2> S3
+    {3, 64, 64, 53, 0.85},    // <2,2,1,1> S4
 };
 constexpr int kCUs = 256;
 
@@ -465,50 +444,59 @@ int env_int(const char* name) {
   return e ? std::atoi(e) : -1;
 }
 
-int occupancy(const EncTile& t) { return std::max(1, std::min(160 / t.lds_kb, 32 / t.nw)); }
+struct ConvPlan {
+  const ConvTile* t = nullptr;
+  int splits = 1;
+  int tiles = 0;  // output tiles per batch
+};
 
-// Persistent grid: workgroups per batch.
-int grid_per_batch(const EncTile& t, int tiles, int batch) {
-  return std::max(1, std::min(tiles, kCUs * occupancy(t) / std::max(batch, 1)));
-}
-
-// Critical path in MFMA units per SIMD: tiles per workgroup x waves sharing a SIMD x per-wave
-// work per tile (block area x K / k-groups), over an efficiency that grows with the waves a SIMD
-// can interleave.
-// whole_stages: K must be a multiple of the stage depth 32 * kg (the conv has no K tail).
-template <size_t NT>
-const EncTile& choose(const EncTile (&tiles)[NT], int M, int N, int K, int batch, int forced,
-                      bool whole_stages) {
-  auto fits = [&](const EncTile& t) { return !whole_stages || K % (32 * t.kg) == 0; };
-  if (forced >= 0 && forced < (int)NT && fits(tiles[forced])) return tiles[forced];
-  const EncTile* best = nullptr;
+// Critical path per CU: rounds of concurrent workgroups x per-workgroup time (its stages plus a
+// fixed prologue / epilogue share, scaled by tile area / efficiency), slowed when a CU holds few
+// workgroups, plus the split-K partial traffic (written and read once) in the same units.
+ConvPlan plan_conv(int M, int N, int K, int batch) {
+  const int nk = K / BK;
+  const int ft = env_int("MNN_ENC_CONV_TILE"), fs = env_int("MNN_ENC_CONV_SPLIT");
+  ConvPlan best;
   double best_cost = 1e300;
-  for (const EncTile& t : tiles) {
-    if (!fits(t)) continue;
-    const int per_b = (int)(cdiv(M, t.bm) * cdiv(N, t.bn));
-    const int64_t total = (int64_t)per_b * batch;
-    const int64_t wgs = (int64_t)grid_per_batch(t, per_b, batch) * batch;
-    const double tiles_per_wg = std::ceil((double)total / wgs);
-    const double waves_simd = (double)wgs * t.nw / (4.0 * kCUs);
-    const double eff = waves_simd >= 2 ? 1.0 : waves_simd >= 1 ? 0.8 : 0.55;
-    const double per_wave = (double)t.bm * t.bn / (t.nw / t.kg) * ((double)K / t.kg);
-    const double cost = tiles_per_wg * std::max(1.0, waves_simd) * per_wave / eff;
-    if (!best || cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = &t;
+  for (const ConvTile& t : kConvTiles) {
+    if (ft >= 0 && t.id != ft) continue;
+    const int tiles = (int)(cdiv(M, t.bm) * cdiv(N, t.bn));
+    const int occ = std::max(1, std::min(160 / t.lds_kb, 8));
+    for (int s : {1, 2, 3, 4, 6, 8, 12, 16}) {
+      // a forced split applies where it divides the stages
+      if (nk % s != 0 || (fs > 0 && nk % fs == 0 && s != fs)) continue;
+      const int64_t wgs = (int64_t)tiles * batch * s;
+      const double rounds = std::ceil((double)wgs / (kCUs * occ));
+      const double fill = std::min(1.0, (double)wgs / (kCUs * occ));
+      const double per_wg = ((double)nk / s + 3.0) * t.bm * t.bn / t.eff;
+      // unit: one 128x128 x 32-k stage on a CU (~2 us); HBM at ~8 TB/s
+      const double split_cost =
+          s > 1 ? (8.0 * s * M * N * batch / 8e12 / 2e-6 + 1.0) * 16384.0 : 0.0;
+      const double cost = rounds * per_wg / (0.6 + 0.4 * fill) + split_cost;
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best.t = &t;
+        best.splits = s;
+        best.tiles = tiles;
+      }
     }
   }
-  MNN_REQUIRE(best, MNN_ERR_INVALID_ARGUMENT, "enc: no tile configuration fits K = " << K);
-  return *best;
+  MNN_REQUIRE(best.t, MNN_ERR_INVALID_ARGUMENT, "enc_conv: no tile configuration fits K = " << K);
+  return best;
 }
 
-template <int MODE, int WMW, int WNW, int WM, int WN, int KG, int S>
-void launch_enc(const LaunchCtx& c, const EncArgs& a, const EncTile& t, const char* name) {
-  using Cfg = EncCfg<MODE, WMW, WNW, WM, WN, KG, S>;
-  static_assert(Cfg::BM > 0, "");
-  const int per_b = (int)(cdiv(a.M, Cfg::BM) * cdiv(a.N, Cfg::BN));
-  dim3 grid(grid_per_batch(t, per_b, a.batch), 1, a.batch), block(Cfg::NT);
-  launch(c, name, enc_gemm_kernel<MODE, WMW, WNW, WM, WN, KG, S>, grid, block, 0, a);
+int conv_parts(const ConvPlan& p, int M, int N) {
+  return p.splits > 1 ? M * (int)cdiv(N, kRedCols) : p.tiles;
+}
+
+template <int WMW, int WNW, int WM, int WN, int S>
+void launch_conv(const LaunchCtx& c, const ConvKArgs& a, int batch) {
+  using Cfg = ConvCfg<WMW, WNW, WM, WN, S>;
+  dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), batch * a.splits), block(Cfg::NT);
+  if (a.splits > 1)
+    launch(c, "enc_conv_f32", enc_conv_kernel<WMW, WNW, WM, WN, S, true>, grid, block, 0, a);
+  else
+    launch(c, "enc_conv_f32", enc_conv_kernel<WMW, WNW, WM, WN, S, false>, grid, block, 0, a);
 }
 
 }  // namespace
@@ -516,81 +504,91 @@ void launch_enc(const LaunchCtx& c, const EncArgs& a, const EncTile& t, const ch
 bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
                         int64_t L) {
   return Cin > 0 && Cout > 0 && ks == 8 && stride == 4 && dil == 1 && groups == 1 && pad >= 0 &&
-         pad < 4 && L >= 8 && L < (1LL << 30) / std::max(Cin, 4);
+         pad < 4 && L >= 8 && (int64_t)enc_conv_padded_cin(Cin) * L < (1LL << 29) &&
+         (int64_t)Cout * 8 * enc_conv_padded_cin(Cin) < (1LL << 28);
 }
 
 int enc_conv_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
 
 int enc_conv_parts(int Cout, int64_t Lout, int K, int batch) {
-  const EncTile& t =
-      choose(kConvTiles, Cout, (int)Lout, K, batch, env_int("MNN_ENC_CONV_TILE"), true);
-  return grid_per_batch(t, (int)(cdiv(Cout, t.bm) * cdiv(Lout, t.bn)), batch);
+  return conv_parts(plan_conv(Cout, (int)Lout, K, batch), Cout, (int)Lout);
+}
+
+int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch) {
+  const ConvPlan p = plan_conv(Cout, (int)Lout, K, batch);
+  return p.splits > 1 ? (int64_t)p.splits * batch * Cout * Lout : 0;
 }
 
 void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
-  EncArgs a;
+  ConvKArgs a;
   a.M = p.Cout;
   a.N = (int)p.Lout;
   a.K = enc_conv_padded_cin(p.Cin) * 8;
-  a.batch = p.B;
-  a.A = p.w;
-  a.lda = a.K;
-  a.x = p.x;
-  a.x_bs = (int64_t)p.Cin * p.L;
   a.Cin = p.Cin;
   a.L = (int)p.L;
   a.pad = p.pad;
   a.reflect = p.reflect;
-  a.C = p.y;
-  a.ldc = p.ldy;
-  a.sC = (int64_t)p.Cout * p.ldy;
+  a.W = p.w;
+  a.x = p.x;
+  a.x_bs = (int64_t)p.Cin * p.L;
   a.bias = p.bias;
-  a.parts = p.parts;
-  MNN_REQUIRE(enc_conv_supported(p.Cin, p.Cout, 8, 4, 1, 1, p.pad, p.L) && a.K % 32 == 0 &&
-                  p.ldy >= p.Lout && p.Cout <= kMaxM,
+  a.y = p.y;
+  a.ldy = p.ldy;
+  a.y_bs = (int64_t)p.Cout * p.ldy;
+  MNN_REQUIRE(enc_conv_supported(p.Cin, p.Cout, 8, 4, 1, 1, p.pad, p.L) && p.ldy >= p.Lout &&
+                  p.Lout >= 1 && p.bias && p.parts && (p.Lout - 1) * 4 + 8 <= p.L + 2 * p.pad,
               MNN_ERR_INVALID_ARGUMENT, "enc_conv: unsupported configuration");
-  const EncTile& t =
-      choose(kConvTiles, a.M, a.N, a.K, a.batch, env_int("MNN_ENC_CONV_TILE"), true);
-  switch (t.id) {
-    case 0: return launch_enc<ENC_CONV, 1, 2, 1, 1, 1, 7>(c, a, t, "enc_conv_f32");
-    case 1: return launch_enc<ENC_CONV, 1, 2, 1, 1, 2, 6>(c, a, t, "enc_conv_f32");
-    case 2: return launch_enc<ENC_CONV, 2, 2, 1, 1, 2, 4>(c, a, t, "enc_conv_f32");
-    case 3: return launch_enc<ENC_CONV, 1, 2, 1, 1, 4, 3>(c, a, t, "enc_conv_f32");
-    default: return launch_enc<ENC_CONV, 2, 2, 1, 1, 1, 6>(c, a, t, "enc_conv_f32");
+  const ConvPlan plan = plan_conv(a.M, a.N, a.K, p.B);
+  a.splits = plan.splits;
+  if (plan.splits > 1) {
+    MNN_REQUIRE(p.ws, MNN_ERR_INVALID_ARGUMENT, "enc_conv: split-K needs a workspace");
+    a.ws = p.ws;
+  } else {
+    a.parts = p.parts;
   }
+  switch (plan.t->id) {
+    case 0: launch_conv<2, 2, 2, 2, 3>(c, a, p.B); break;
+    case 1: launch_conv<2, 2, 2, 1, 3>(c, a, p.B); break;
+    case 2: launch_conv<2, 2, 1, 2, 3>(c, a, p.B); break;
+    default: launch_conv<2, 2, 1, 1, 4>(c, a, p.B); break;
+  }
+  if (plan.splits > 1)
+    launch(c, "enc_conv_reduce_f32", enc_conv_reduce_kernel, dim3(cdiv(a.N, kRedCols), a.M, p.B),
+           dim3(kRedThreads), 0, (const float*)p.ws, plan.splits, a.M, a.N, p.bias, p.y, p.ldy,
+           a.y_bs, p.parts);
 }
 
+int enc_rewrite_kp(int C) { return (C + 31) / 32 * 32; }
+
 void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& p) {
-  EncArgs a;
-  a.M = 2 * p.C;
-  a.N = (int)p.Lout;
-  a.K = p.C;
-  a.batch = p.B;
-  a.A = p.w;
-  a.lda = p.C;
-  a.Bm = p.y;
-  a.ldb = p.ldy;
-  a.sB = (int64_t)p.C * p.ldy;
-  a.parts = const_cast<float*>(p.parts);
-  a.nparts = p.nparts;
-  a.eps = p.eps;
-  a.coef = p.coef;
-  a.gamma = p.gamma;
-  a.beta = p.beta;
-  a.C = p.out;
-  a.ldc = p.ldo;
-  a.sC = (int64_t)p.C * p.ldo;
-  a.bias = p.bias;
-  MNN_REQUIRE(p.C % 16 == 0 && p.C >= 32 && p.C <= kMaxK && 2 * p.C <= kMaxM && p.ldy % 4 == 0 &&
-                  p.ldy >= (p.Lout + 3) / 4 * 4 && ((p.parts && p.nparts > 0) || p.coef) && p.bias,
+  MNN_REQUIRE(p.C % 16 == 0 && p.C > 0 && p.kp == enc_rewrite_kp(p.C) && p.zt && p.w && p.bias &&
+                  p.ldy >= p.Lout && p.ldo >= p.Lout && ((p.parts && p.nparts > 0) || p.coef),
               MNN_ERR_INVALID_ARGUMENT, "enc_rewrite: unsupported configuration");
-  const EncTile& t = choose(kRwTiles, a.M, a.N, a.K, a.batch, env_int("MNN_ENC_RW_TILE"), false);
-  switch (t.id) {
-    case 0: return launch_enc<ENC_RW, 2, 2, 1, 1, 1, 6>(c, a, t, "enc_rewrite_f32");
-    case 1: return launch_enc<ENC_RW, 1, 2, 1, 1, 1, 5>(c, a, t, "enc_rewrite_f32");
-    case 2: return launch_enc<ENC_RW, 2, 2, 1, 1, 2, 4>(c, a, t, "enc_rewrite_f32");
-    default: return launch_enc<ENC_RW, 1, 2, 1, 1, 2, 5>(c, a, t, "enc_rewrite_f32");
-  }
+  const int64_t tiles = (int64_t)cdiv(p.Lout, kTT) * cdiv(p.kp, kTT);
+  launch(c, "enc_gn_gelu_t_f32", enc_gn_gelu_t_kernel,
+         dim3((unsigned)std::min<int64_t>(tiles, std::max<int64_t>(1, 1024 / p.B)), 1, p.B),
+         dim3(256), 0, p);
+  GemmArgs g;
+  g.M = 2 * p.C;
+  g.N = (int)p.Lout;
+  g.K = p.kp;
+  g.batch = p.B;
+  g.A = p.w;
+  g.lda = p.kp;
+  g.B = p.zt;
+  g.ldb = p.kp;
+  g.sB = (int64_t)p.Lout * p.kp;
+  g.blayout = B_NK;
+  g.C = p.out;
+  g.ldc = p.ldo;
+  g.sC = (int64_t)p.C * p.ldo;
+  g.bias = p.bias;
+  g.bias_mode = BIAS_M;
+  g.glu = true;
+  g.name = "enc_rewrite_f32";
+  MNN_REQUIRE(gemm_nk_lds_supported(g), MNN_ERR_INVALID_ARGUMENT,
+              "enc_rewrite: operands outside the LDS GEMM's contract");
+  gemm_nk_lds(c, g);
 }
 
 }  // namespace k

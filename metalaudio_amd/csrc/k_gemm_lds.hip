@@ -57,27 +57,92 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
   const int g = lane >> 5, l32 = lane & 31;
   const int bz = blockIdx.z;
   float* __restrict__ Cp = a.C + (int64_t)bz * a.sC;
-  const float* __restrict__ Rp = RES && a.R ? a.R + (int64_t)bz * a.sR : nullptr;
+  const float* Rp = RES && a.R ? a.R + (int64_t)bz * a.sR : nullptr;
   const bool full_m = m0 + WMW * WM * 32 <= a.M;
+  // The values a 32-row block's stores depend on are loaded before any of its stores. R may be C
+  // itself (in-place residual, element for element), so the compiler may not move a load of R
+  // or of the bias past an earlier store to C: loads interleaved with the stores would wait for
+  // memory once per element. No lane stores an element another lane reads, so loading first is
+  // exact; going block by block bounds the registers held.
+  float bnv[WN], rsv[WN];
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
-    const int gn = n0 + wn * WN * 32 + j * 32 + l32;
-    if (gn >= a.N) continue;
-    const float bn = a.bias_mode == BIAS_N ? a.bias[gn] : 0.f;
-    const float rs = RES && Rp ? (a.rscale ? a.rscale[gn] : 1.f) : 0.f;
+    const int gn = min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1);
+    bnv[j] = a.bias_mode == BIAS_N ? a.bias[gn] : 0.f;
+    rsv[j] = RES && Rp ? (a.rscale ? a.rscale[gn] : 1.f) : 0.f;
+  }
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
-      const int mblk = m0 + wm * WM * 32 + i * 32;
+  for (int i = 0; i < WM; ++i) {
+    const int mblk = m0 + wm * WM * 32 + i * 32;
+    float bmv[16];
+    float rv[RES ? WN : 1][16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int gm = min(mblk + 8 * (v / 4) + 4 * g + (v % 4), a.M - 1);
+      bmv[v] = a.bias_mode == BIAS_M ? a.bias[gm] : 0.f;
+      if constexpr (RES) {
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const int gn = min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1);
+          rv[j][v] = Rp ? Rp[(int64_t)gm * a.ldr + gn] : 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+      if (gn >= a.N) continue;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
         if (full_m || gm < a.M) {
-          float val = acc[i][j][v] + bn;
-          if (a.bias_mode == BIAS_M) val += a.bias[gm];
+          float val = acc[i][j][v] + bnv[j] + bmv[v];
           val = ACT < 0 ? apply_act(val, a.act) : apply_act(val, ACT);
-          if (RES && Rp) val = Rp[(int64_t)gm * a.ldr + gn] + rs * val;
+          if constexpr (RES) {
+            if (Rp) val = rv[j][v] + rsv[j] * val;
+          }
           Cp[(int64_t)gm * a.ldc + gn] = val;
         }
+      }
+    }
+  }
+}
+
+// GLU epilogue: rows come in 32-row blocks [a0..a15 | b0..b15] (weights regrouped by the caller);
+// output row 16*blk + r = (a_r + bias) * sigmoid(b_r + bias). In the accumulator layout register v
+// (< 8) holds row rr = 8*(v/4) + 4*(l/32) + v%4 < 16 and register v + 8 holds row rr + 16, so every
+// lane has both GLU partners.
+template <int WMW, int WNW, int WM, int WN>
+__device__ __forceinline__ void store_glu(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
+                                          int n0, int wm, int wn, int lane) {
+  const int g = lane >> 5, l32 = lane & 31;
+  float* __restrict__ Cp = a.C + (int64_t)blockIdx.z * a.sC;
+  // bias values first (the compiler may not move these loads past the stores)
+  float ba[WM][8], bb[WM][8];
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int mblk = min(m0 + wm * WM * 32 + i * 32, a.M - 32);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      const int rr = 8 * (v / 4) + 4 * g + (v % 4);
+      ba[i][v] = a.bias ? a.bias[mblk + rr] : 0.f;
+      bb[i][v] = a.bias ? a.bias[mblk + 16 + rr] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int mblk = m0 + wm * WM * 32 + i * 32;
+    if (mblk >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+      if (gn >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        const int rr = 8 * (v / 4) + 4 * g + (v % 4);
+        const float va = acc[i][j][v] + ba[i][v];
+        const float vb = acc[i][j][v + 8] + bb[i][v];
+        Cp[(int64_t)((mblk >> 5) * 16 + rr) * a.ldc + gn] = va * stable_sigmoid(vb);
       }
     }
   }
@@ -232,7 +297,8 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   // The activation and residual form are uniform: one specialised copy of the store loop each
   // for the forms the transformer uses, a generic one for the rest.
   const bool res = a.R != nullptr;
-  if (a.act == 0 && !res) store_tile<WMW, WNW, WM, WN, 0, false>(a, acc, m0, n0, wm, wn, lane);
+  if (a.glu) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 0 && !res) store_tile<WMW, WNW, WM, WN, 0, false>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0) store_tile<WMW, WNW, WM, WN, 0, true>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 3 && !res) store_tile<WMW, WNW, WM, WN, 3, false>(a, acc, m0, n0, wm, wn, lane);
   else store_tile<WMW, WNW, WM, WN, -1, true>(a, acc, m0, n0, wm, wn, lane);
@@ -280,7 +346,8 @@ template <int WMW, int WNW, int WM, int WN, int S>
 void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch), block(Cfg::NT);
-  launch(c, "gemm_f32_mfma_nk", gemm_nk_lds_kernel<WMW, WNW, WM, WN, S>, grid, block, 0, a);
+  launch(c, a.name ? a.name : "gemm_f32_mfma_nk", gemm_nk_lds_kernel<WMW, WNW, WM, WN, S>, grid,
+         block, 0, a);
 }
 
 }  // namespace
@@ -288,8 +355,8 @@ void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
 bool gemm_nk_lds_supported(const GemmArgs& a) {
   return a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
-         aligned16(a.B) && !a.glu && a.stats == nullptr && a.pro_coef == nullptr &&
-         a.pro_stats == nullptr;
+         aligned16(a.B) && a.stats == nullptr && a.pro_coef == nullptr && a.pro_stats == nullptr &&
+         (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0));
 }
 
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {

@@ -108,6 +108,7 @@ struct GemmArgs {
   const float* rc_w = nullptr;
   const float* rc_b = nullptr;
   mnn_precision precision = MNN_PRECISION_F32;
+  const char* name = nullptr;  // kernel-timing name of the launch (default: by kernel family)
 };
 // Number of output tiles per batch for the tile configuration the launcher will pick.
 int gemm_num_tiles(const GemmArgs& a);
@@ -115,18 +116,17 @@ int gemm_num_tiles(const GemmArgs& a);
 // register-staged kernel of k_gemm.hip.
 void gemm(const LaunchCtx& c, const GemmArgs& a);
 // fp32 B_NK GEMM with LDS-DMA operand staging: K % 32 == 0, 16-byte aligned rows, epilogue bias /
-// activation / residual with LayerScale (no GLU, statistics or B prologue).
+// activation / residual with LayerScale, or GLU over 32-row blocks (M % 32 == 0, bias per row, no
+// activation or residual); no statistics or B prologue.
 bool gemm_nk_lds_supported(const GemmArgs& a);
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
 
 // ------------------------------------------------------------------ encoder levels (k_enc.hip)
 // Strided conv (kernel 8, stride 4, dilation 1, groups 1, pad < 4) as an LDS-DMA implicit GEMM:
 // y[b][co][t] (row pitch ldy) = bias + conv. The weights are [Cout][Cinp * 8] with
-// Cinp = enc_conv_padded_cin(Cin) (input channels rounded up to 4, the extra taps zero). With
-// parts set, GroupNorm(1) statistics partials (count, mean, M2) of y before activation:
-// enc_conv_parts per batch, 3 floats each.
-// The kernel is persistent: each workgroup walks a set of output tiles with one LDS-DMA stage
-// ring running across tile boundaries.
+// Cinp = enc_conv_padded_cin(Cin) (input channels rounded up to 4, the extra taps zero). Writes
+// GroupNorm(1) statistics partials (count, mean, M2) of y: enc_conv_parts per batch, 3 floats
+// each. Deep levels split K over workgroups: they need a workspace of enc_conv_ws_floats floats.
 struct EncConvArgs {
   int B = 1, Cin = 0, Cout = 0;
   int64_t L = 0, Lout = 0;
@@ -138,24 +138,28 @@ struct EncConvArgs {
   float* y = nullptr;
   int64_t ldy = 0;
   float* parts = nullptr;
+  float* ws = nullptr;
 };
 bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
                         int64_t L);
 int enc_conv_padded_cin(int Cin);
 // Statistics partials per batch the launch writes; K = enc_conv_padded_cin(Cin) * 8.
 int enc_conv_parts(int Cout, int64_t Lout, int K, int batch);
+int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch);
 void enc_conv(const LaunchCtx& c, const EncConvArgs& a);
 // Rewrite 1x1 conv C -> 2C with GLU: out[b][c][t] = z[c] * sigmoid(z[c + C]),
-// z = w * GELU(GroupNorm(y)) + bias, with w / bias regrouped into 32-row blocks
-// [a0..a15 | b0..b15] (GLU partners in one block). GroupNorm(1) comes from the producer's
+// z = w * GELU(GroupNorm(y)) + bias, in two launches: GroupNorm + GELU of y written transposed to
+// zt [B][Lout][kp] (kp = enc_rewrite_kp(C), columns past C zero), then the LDS GEMM with the GLU
+// epilogue. w / bias are regrouped into 32-row blocks [a0..a15 | b0..b15] (GLU partners in one
+// block) and w is [2C][kp] with zero columns past C. GroupNorm(1) comes from the producer's
 // statistics partials (parts, nparts per batch; merged in fp64 in a fixed order) with gamma /
 // beta and eps, or from per-row coefficients coef[b][c] = (scale, shift).
 struct EncRewriteArgs {
   int B = 1, C = 0;
   int64_t Lout = 0;
-  const float* w = nullptr;     // [2C][C], regrouped
+  const float* w = nullptr;     // [2C][kp], regrouped
   const float* bias = nullptr;  // [2C], regrouped
-  const float* y = nullptr;     // [B][C][ldy], ldy % 4 == 0
+  const float* y = nullptr;     // [B][C][ldy]
   int64_t ldy = 0;
   const float* parts = nullptr;
   int nparts = 0;
@@ -163,9 +167,12 @@ struct EncRewriteArgs {
   const float* coef = nullptr;
   const float* gamma = nullptr;
   const float* beta = nullptr;
+  float* zt = nullptr;  // workspace [B][Lout][kp]
+  int kp = 0;
   float* out = nullptr;  // [B][C][ldo]
   int64_t ldo = 0;
 };
+int enc_rewrite_kp(int C);
 void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& a);
 
 // ------------------------------------------------------------------ attention (k_attention.hip)

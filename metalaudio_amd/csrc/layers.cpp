@@ -689,10 +689,13 @@ class EncoderBlockLayer : public Layer {
       rb_ = &add_param("rewrite.bias", 2LL * C);
       glu_fused_ = (C % 16 == 0);
       if (glu_fused_) {
+        const int kp = k::enc_rewrite_kp(C);
         rw_perm_.reserve(sizeof(float) * 2 * C * C);
+        rw_pad_.reserve(sizeof(float) * 2 * C * kp);
         rb_perm_.reserve(sizeof(float) * 2 * C);
-        std::vector<float> z(2LL * C * C, 0.f);
-        HIP_CHECK(hipMemcpy(rw_perm_.ptr, z.data(), z.size() * 4, hipMemcpyHostToDevice));
+        std::vector<float> z(2LL * C * kp, 0.f);
+        HIP_CHECK(hipMemcpy(rw_perm_.ptr, z.data(), 2LL * C * C * 4, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(rw_pad_.ptr, z.data(), z.size() * 4, hipMemcpyHostToDevice));
         HIP_CHECK(hipMemcpy(rb_perm_.ptr, z.data(), 2LL * C * 4, hipMemcpyHostToDevice));
       }
     }
@@ -722,33 +725,39 @@ class EncoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t lo = os.back();
     const bool g1 = norm_->groups() == 1;
-    if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32 && Cout >= 32 &&
-        Cout <= 512) {
-      // LDS-DMA matrix-core path (k_enc.hip): the conv writes its output with a 16-byte row pitch
-      // and GroupNorm statistics partials; the rewrite GEMM merges them, applies GroupNorm + GELU
-      // to its operand and GLU in its epilogue. A conv outside the implicit-GEMM kernel's
-      // contract (kernel size other than 8 / stride 4) runs on the generic conv path.
+    if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32) {
+      // Matrix-core path (k_enc.hip): the implicit-GEMM conv writes y and GroupNorm statistics
+      // partials; the rewrite applies GroupNorm + GELU once (transposed into zt_) and runs the
+      // LDS GEMM with GLU in its epilogue. A conv outside the implicit-GEMM kernel's contract
+      // (kernel size other than 8 / stride 4) runs on the generic conv path.
       const auto& cd = conv_->desc();
       const int pad = conv_->pad_for(L);
       const int64_t pitch = (lo + 3) / 4 * 4;
+      const int kp = k::enc_rewrite_kp(Cout);
       y_.reserve(sizeof(float) * B * Cout * pitch);
+      zt_.reserve(sizeof(float) * B * lo * kp);
       k::EncRewriteArgs r;
       r.B = (int)B;
       r.C = Cout;
       r.Lout = lo;
-      r.w = rw_perm_.f32();
+      r.w = rw_pad_.f32();
       r.bias = rb_perm_.f32();
       r.y = y_.f32();
       r.ldy = pitch;
       r.gamma = norm_->gamma();
       r.beta = norm_->beta();
+      r.eps = norm_->eps();
+      r.zt = zt_.f32();
+      r.kp = kp;
       r.out = out.f32();
       r.ldo = lo;
       if (k::enc_conv_supported(cd.in_channels, Cout, cd.kernel_size, cd.stride, cd.dilation,
                                 cd.groups, pad, L)) {
-        const int nparts =
-            k::enc_conv_parts(Cout, lo, k::enc_conv_padded_cin(cd.in_channels) * 8, (int)B);
+        const int K = k::enc_conv_padded_cin(cd.in_channels) * 8;
+        const int nparts = k::enc_conv_parts(Cout, lo, K, (int)B);
         partials_.reserve(sizeof(float) * 3 * B * nparts);
+        const int64_t wsf = k::enc_conv_ws_floats(Cout, lo, K, (int)B);
+        if (wsf > 0) ws_.reserve(sizeof(float) * wsf);
         k::EncConvArgs c;
         c.B = (int)B;
         c.Cin = cd.in_channels;
@@ -763,17 +772,16 @@ class EncoderBlockLayer : public Layer {
         c.y = y_.f32();
         c.ldy = pitch;
         c.parts = partials_.f32();
+        c.ws = wsf > 0 ? ws_.f32() : nullptr;
         k::enc_conv(ctx(s), c);
         r.parts = partials_.f32();
         r.nparts = nparts;
-        r.eps = norm_->eps();
       } else {
         const int nchunk = conv_->stats_chunks((int)B, (int)L);
         partials_.reserve(sizeof(float) * 3 * B * nchunk);
         conv_->run(in.f32(), (int)B, (int)L, y_.f32(), MNN_ACT_NONE, partials_.f32(), s, pitch);
         r.parts = partials_.f32();
         r.nparts = nchunk;
-        r.eps = norm_->eps();
       }
       k::enc_rewrite(ctx(s), r);
       return;
@@ -916,6 +924,12 @@ class EncoderBlockLayer : public Layer {
                       p.data() + (int64_t)(32 * blk + 16 + j) * C);
         }
       HIP_CHECK(hipMemcpy(rw_perm_.ptr, p.data(), n * 4, hipMemcpyHostToDevice));
+      // the same rows with the operand depth padded to a multiple of 32 (zero columns)
+      const int kp = k::enc_rewrite_kp(C);
+      std::vector<float> q(2LL * C * kp, 0.f);
+      for (int r = 0; r < 2 * C; ++r)
+        std::copy_n(p.data() + (int64_t)r * C, C, q.data() + (int64_t)r * kp);
+      HIP_CHECK(hipMemcpy(rw_pad_.ptr, q.data(), q.size() * 4, hipMemcpyHostToDevice));
     } else if (name == "rewrite.bias") {
       std::vector<float> p(n);
       for (int blk = 0; blk < C / 16; ++blk)
@@ -934,8 +948,8 @@ class EncoderBlockLayer : public Layer {
   Param* rw_ = nullptr;
   Param* rb_ = nullptr;
   bool glu_fused_ = false;
-  DevBuf rw_perm_, rb_perm_;
-  DevBuf y_, partials_, z_, wpad_;
+  DevBuf rw_perm_, rb_perm_, rw_pad_;
+  DevBuf y_, partials_, z_, wpad_, ws_, zt_;
 };
 
 // ------------------------------------------------------------------ transformer building blocks
