@@ -84,9 +84,6 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
-// Workgroup-wide (count, mean, M2) of per-thread values, merged with Chan's formula.
-// Each thread passes its own (n, mean, m2); thread 0 receives the workgroup result.
-// `red` must hold 3 * (blockDim.x / 64) floats of LDS.
 // Chan's merge of statistics (n2, mean2, m22) into (n, mean, m2).
 __device__ __forceinline__ void welford_combine(float& n, float& mean, float& m2, float n2,
                                                 float mean2, float m22) {
@@ -100,6 +97,9 @@ __device__ __forceinline__ void welford_combine(float& n, float& mean, float& m2
   n = nt;
 }
 
+// Workgroup-wide (count, mean, M2) of per-thread values, merged with Chan's formula.
+// Each thread passes its own (n, mean, m2); thread 0 receives the workgroup result.
+// `red` must hold 3 * (blockDim.x / 64) floats of LDS.
 __device__ __forceinline__ void block_welford(float& n, float& mean, float& m2, float* red) {
   // wave level: tree over lanes
 #pragma unroll

@@ -371,14 +371,45 @@ __global__ __launch_bounds__(kRedThreads) void enc_conv_reduce_kernel(
 // z^T[b][t][k] = GELU(y[b][k][t] * scale_k + shift_k) for k < C, 0 for C <= k < kp. GroupNorm(1)
 // comes from the producer's statistics partials (merged in fp64 in a fixed order, once per
 // workgroup) with gamma / beta, or from per-row coefficients coef[b][k] = (scale, shift).
-// Workgroups walk the 64 x 64 tiles of their batch (grid-stride), transposing through LDS.
+// Workgroups walk the 64 x 64 tiles of their batch (grid-stride) and transpose through LDS; each
+// thread moves 16-byte vectors (4 t of one row in, 4 k of one row out), and the next tile's loads
+// are issued before the current tile is transformed (the first tile's before the merge).
 constexpr int kTT = 64;
 __global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
-  __shared__ float tileb[kTT][kTT + 1];
+  __shared__ float tileb[kTT][kTT + 4];
   __shared__ float2 cf[kTT];
   __shared__ double redd[3 * 4];
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
+  const int ntt = (int)((a.Lout + kTT - 1) / kTT), nkt = (a.kp + kTT - 1) / kTT;
+  const float* __restrict__ yb = a.y + (int64_t)b * a.C * a.ldy;
+  float* __restrict__ zb = a.zt + (int64_t)b * a.Lout * a.kp;
+  // loads: thread covers rows r = tid/16 + 16i (i < 4), columns 4*(tid%16) .. +3
+  const int lr = tid >> 4, lc = 4 * (tid & 15);
+  const bool vec = (a.ldy & 3) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0;
+  auto load_tile = [&](int tile, float4 (&v)[4]) {
+    const int t0 = (tile % ntt) * kTT, k0 = (tile / ntt) * kTT;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = k0 + lr + 16 * i, t = t0 + lc;
+      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (k < a.C) {
+        const float* row = yb + (int64_t)k * a.ldy;
+        if (vec && t + 3 < a.Lout) {
+          v[i] = *reinterpret_cast<const float4*>(row + t);
+        } else {
+          if (t + 0 < a.Lout) v[i].x = row[t + 0];
+          if (t + 1 < a.Lout) v[i].y = row[t + 1];
+          if (t + 2 < a.Lout) v[i].z = row[t + 2];
+          if (t + 3 < a.Lout) v[i].w = row[t + 3];
+        }
+      }
+    }
+  };
+  const int ntiles = ntt * nkt;
+  int tile = blockIdx.x;
+  float4 cur[4];
+  if (tile < ntiles) load_tile(tile, cur);
   float mean = 0.f, rstd = 0.f;
   if (!a.coef) {
     const float2 ms =
@@ -386,11 +417,10 @@ __global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
     mean = ms.x;
     rstd = ms.y;
   }
-  const int ntt = (int)((a.Lout + kTT - 1) / kTT), nkt = (a.kp + kTT - 1) / kTT;
-  const float* __restrict__ yb = a.y + (int64_t)b * a.C * a.ldy;
-  float* __restrict__ zb = a.zt + (int64_t)b * a.Lout * a.kp;
-  for (int tile = blockIdx.x; tile < ntt * nkt; tile += gridDim.x) {
+  for (; tile < ntiles; tile += gridDim.x) {
     const int t0 = (tile % ntt) * kTT, k0 = (tile / ntt) * kTT;
+    float4 nxt[4];
+    if (tile + (int)gridDim.x < ntiles) load_tile(tile + gridDim.x, nxt);
     __syncthreads();  // the previous tile's reads of tileb / cf are done
     if (tid < kTT) {
       const int k = k0 + tid;
@@ -406,22 +436,34 @@ __global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
       cf[tid] = c;
     }
     __syncthreads();
-    // load: rows k (channels), columns t contiguous
-    for (int e = tid; e < kTT * kTT; e += 256) {
-      const int r = e / kTT, cidx = e % kTT;
-      const int k = k0 + r, t = t0 + cidx;
-      float v = 0.f;
-      if (k < a.C && t < a.Lout)
-        v = gelu_tanh_fast(fmaf(yb[(int64_t)k * a.ldy + t], cf[r].x, cf[r].y));
-      tileb[r][cidx] = v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = lr + 16 * i;
+      const float2 c = cf[r];
+      const bool live = k0 + r < a.C;  // padded rows stay zero
+      float4 z;
+      z.x = live ? gelu_tanh_fast(fmaf(cur[i].x, c.x, c.y)) : 0.f;
+      z.y = live ? gelu_tanh_fast(fmaf(cur[i].y, c.x, c.y)) : 0.f;
+      z.z = live ? gelu_tanh_fast(fmaf(cur[i].z, c.x, c.y)) : 0.f;
+      z.w = live ? gelu_tanh_fast(fmaf(cur[i].w, c.x, c.y)) : 0.f;
+      tileb[r][lc + 0] = z.x;
+      tileb[r][lc + 1] = z.y;
+      tileb[r][lc + 2] = z.z;
+      tileb[r][lc + 3] = z.w;
     }
     __syncthreads();
-    // store: rows t, columns k contiguous
-    for (int e = tid; e < kTT * kTT; e += 256) {
-      const int r = e / kTT, cidx = e % kTT;
-      const int t = t0 + r, k = k0 + cidx;
-      if (t < a.Lout && k < a.kp) zb[(int64_t)t * a.kp + k] = tileb[cidx][r];
+    // stores: thread covers rows t = t0 + tid/16 + 16i, columns k = k0 + 4*(tid%16) .. +3
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tr = lr + 16 * i, t = t0 + tr, k = k0 + lc;
+      if (t < a.Lout && k < a.kp) {
+        const float4 z = make_float4(tileb[lc + 0][tr], tileb[lc + 1][tr], tileb[lc + 2][tr],
+                                     tileb[lc + 3][tr]);
+        *reinterpret_cast<float4*>(zb + (int64_t)t * a.kp + k) = z;
+      }
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -564,9 +606,10 @@ void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& p) {
   MNN_REQUIRE(p.C % 16 == 0 && p.C > 0 && p.kp == enc_rewrite_kp(p.C) && p.zt && p.w && p.bias &&
                   p.ldy >= p.Lout && p.ldo >= p.Lout && ((p.parts && p.nparts > 0) || p.coef),
               MNN_ERR_INVALID_ARGUMENT, "enc_rewrite: unsupported configuration");
+  // about 1024 workgroups in all, each with the same number of tiles
   const int64_t tiles = (int64_t)cdiv(p.Lout, kTT) * cdiv(p.kp, kTT);
-  launch(c, "enc_gn_gelu_t_f32", enc_gn_gelu_t_kernel,
-         dim3((unsigned)std::min<int64_t>(tiles, std::max<int64_t>(1, 1024 / p.B)), 1, p.B),
+  const int64_t per = cdiv(tiles, std::max<int64_t>(1, 1024 / p.B));
+  launch(c, "enc_gn_gelu_t_f32", enc_gn_gelu_t_kernel, dim3((unsigned)cdiv(tiles, per), 1, p.B),
          dim3(256), 0, p);
   GemmArgs g;
   g.M = 2 * p.C;
