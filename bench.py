@@ -35,6 +35,31 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+class Markers:
+    """roctx ranges around the bench's passes, so that a `rocprofv3 --marker-trace` run can
+    attribute kernel dispatches to them (metalaudio_amd.profsummary trace --range ...). No-ops when
+    the marker library is absent."""
+
+    def __init__(self):
+        import ctypes
+        self.lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1",
+                     "libroctx64.so", "/opt/rocm/lib/libroctx64.so"):
+            try:
+                self.lib = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+
+    def push(self, msg):
+        if self.lib:
+            self.lib.roctxRangePushA(msg.encode())
+
+    def pop(self):
+        if self.lib:
+            self.lib.roctxRangePop()
+
+
 # ------------------------------------------------------------------ algorithmic work per step
 def encoder_work():
     """flops and bytes per chunk of config 4, per kernel family."""
@@ -303,16 +328,21 @@ def main():
         step()
     stream.sync()
 
+    markers = Markers()
     # timed region: wall clock around exactly K steps (no per-launch events)
     log(f"timing {args.steps} steps")
+    markers.push("bench:timed")
     ms_step = timed(step, stream, args.steps)
+    markers.pop()
 
     # kernel-timing pass: K more steps with a HIP event pair around every launch, recorded on the
     # stream the kernel runs on; gives each family's average launch duration (the events add
     # gaps between launches, which is why the headline above is timed without them)
     dev.reset_kernel_timing()
     dev.set_kernel_timing(True)
+    markers.push("bench:kernel_timing")
     ms_step_events = timed(step, stream, args.steps)
+    markers.pop()
     dev.set_kernel_timing(False)
     fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
             "gemm_f32_simple", "enc_conv_f32", "enc_conv_reduce_f32", "enc_gn_gelu_t_f32",

@@ -4,6 +4,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <atomic>
 #include <cstdint>
@@ -142,6 +143,9 @@ struct LaunchCtx {
   hipStream_t stream;
 };
 
+// Kernel timing: timing_begin hands out a pair of events (pooled) that the launch passes to
+// hipExtLaunchKernel, which stamps them at the kernel's start and end; timing_end queues the pair
+// for resolution under `name`.
 void timing_begin(const LaunchCtx& c, const char* name, hipEvent_t* ev_start, hipEvent_t* ev_stop);
 void timing_end(const LaunchCtx& c, const char* name, hipEvent_t ev_start, hipEvent_t ev_stop);
 
@@ -150,8 +154,13 @@ inline void launch(const LaunchCtx& c, const char* name, Kernel k, dim3 grid, di
                    size_t shmem, Args... args) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
   hipEvent_t e0 = nullptr, e1 = nullptr;
-  if (c.dev && c.dev->timing) timing_begin(c, name, &e0, &e1);
-  hipLaunchKernelGGL(k, grid, block, shmem, c.stream, args...);
+  if (c.dev && c.dev->timing) {
+    // the events take the kernel's own start / end timestamps (no extra packets around it)
+    timing_begin(c, name, &e0, &e1);
+    hipExtLaunchKernelGGL(k, grid, block, (std::uint32_t)shmem, c.stream, e0, e1, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(k, grid, block, shmem, c.stream, args...);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess)
     fail(err == hipErrorNoBinaryForGpu || err == hipErrorInvalidDeviceFunction

@@ -148,7 +148,8 @@ __device__ __forceinline__ void store_glu(const GemmArgs& a, const floatx16 (&ac
   }
 }
 
-template <int WMW, int WNW, int WM, int WN, int S>
+// GLU: the GLU epilogue (a separate instantiation: only the encoder's rewrite GEMMs use it)
+template <int WMW, int WNW, int WM, int WN, int S, bool GLU>
 __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, A_INS = Cfg::A_INS, B_INS = Cfg::B_INS;
@@ -297,7 +298,7 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   // The activation and residual form are uniform: one specialised copy of the store loop each
   // for the forms the transformer uses, a generic one for the rest.
   const bool res = a.R != nullptr;
-  if (a.glu) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
+  if constexpr (GLU) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0 && !res) store_tile<WMW, WNW, WM, WN, 0, false>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0) store_tile<WMW, WNW, WM, WN, 0, true>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 3 && !res) store_tile<WMW, WNW, WM, WN, 3, false>(a, acc, m0, n0, wm, wn, lane);
@@ -346,8 +347,9 @@ template <int WMW, int WNW, int WM, int WN, int S>
 void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch), block(Cfg::NT);
-  launch(c, a.name ? a.name : "gemm_f32_mfma_nk", gemm_nk_lds_kernel<WMW, WNW, WM, WN, S>, grid,
-         block, 0, a);
+  const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
+  if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, true>, grid, block, 0, a);
+  else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, false>, grid, block, 0, a);
 }
 
 }  // namespace

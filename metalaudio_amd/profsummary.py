@@ -1,0 +1,197 @@
+"""Summaries of rocprofv3 output for the profiles/ folder.
+
+Subcommands:
+  trace DIR --cmd "..." [--out FILE]
+      per-kernel table (calls, average / min / total microseconds, share) from the
+      *kernel_trace.csv of a `rocprofv3 --kernel-trace` run;
+  copy --mib N
+      a plain device copy of N MiB (torch), the calibration run for the HBM counters;
+  traffic --fetch DIR --write DIR --copy-fetch DIR --copy-write DIR --copy-mib N [--out FILE]
+      HBM bytes per dispatch of each kernel family from two `rocprofv3 --pmc` runs (FETCH_SIZE,
+      then WRITE_SIZE, KiB per dispatch), each scaled by the factor that makes the same counter
+      read the known size of the copy run; written as JSON {family: bytes per launch}.
+
+Kernel families are the names the library's kernel timing uses (bench.py reports them).
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import glob
+import json
+import re
+import statistics
+import subprocess
+import sys
+from pathlib import Path
+
+# kernel symbol (substring) -> kernel-timing family of the library
+FAMILIES = [
+    ("attn_fwd_f32_kernel", "attn_fwd"),
+    ("attn_generic_kernel", "attn_fwd"),
+    ("gemm_nk_lds_kernel", "gemm_f32_mfma_nk"),
+    ("enc_conv_reduce_kernel", "enc_conv_reduce_f32"),
+    ("enc_conv_kernel", "enc_conv_f32"),
+    ("enc_gn_gelu_t_kernel", "enc_gn_gelu_t_f32"),
+    ("layernorm", "layernorm"),
+    ("copy_kernel", "copy_bytes"),
+]
+
+
+def _demangle(names):
+    try:
+        out = subprocess.run(["c++filt"], input="\n".join(names), capture_output=True, text=True,
+                             check=True).stdout.splitlines()
+        return dict(zip(names, out))
+    except (OSError, subprocess.CalledProcessError):
+        return {n: n for n in names}
+
+
+def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
+    name = re.sub(r"\(.*", "", name)
+    return name.split("::")[-1] if "<" not in name else name[name.rfind("::", 0, name.find("<")) + 2:]
+
+
+def _family(name: str) -> str:
+    if "gemm_nk_lds_kernel" in name and name.replace(" ", "").endswith(",true>"):
+        return "enc_rewrite_f32"  # the GLU instantiation
+    for key, fam in FAMILIES:
+        if key in name:
+            return fam
+    return name
+
+
+def _csvs(d: str, suffix: str):
+    return glob.glob(str(Path(d) / "**" / f"*{suffix}"), recursive=True)
+
+
+def _range(d: str, name: str):
+    """(start, end) of the first roctx range `name` in a --marker-trace run."""
+    for p in _csvs(d, "marker_api_trace.csv"):
+        for r in csv.DictReader(open(p)):
+            msg = r.get("Message") or r.get("Marker_Message") or r.get("Function", "")
+            if msg == name:
+                return int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+    raise SystemExit(f"range {name!r} not found in the marker trace under {d}")
+
+
+def trace(args) -> str:
+    rows = []
+    for p in _csvs(args.dir, "kernel_trace.csv"):
+        rows += list(csv.DictReader(open(p)))
+    if args.range:
+        t0, t1 = _range(args.dir, args.range)
+        rows = [r for r in rows if int(r["Start_Timestamp"]) >= t0 and int(r["End_Timestamp"]) <= t1]
+    dm = _demangle(sorted({r["Kernel_Name"] for r in rows}))
+    by = collections.defaultdict(list)
+    for r in rows:
+        k = _short(dm[r["Kernel_Name"]])
+        by[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in by.values()) or 1.0
+    scope = (f"dispatches inside the roctx range `{args.range}`" if args.range
+             else "dispatches over the whole run")
+    lines = [f"# {args.title}", "", "Command (repo root, GPU box):", "", "```", args.cmd, "```", "",
+             f"Per kernel instantiation: {scope}, duration from the kernel trace.", "",
+             "| kernel | family | calls | avg us | min us | total us | % |",
+             "|---|---|---|---|---|---|---|"]
+    for k, v in sorted(by.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| `{k}` | {_family(k)} | {len(v)} | {statistics.mean(v):.1f} | "
+                     f"{min(v):.1f} | {sum(v):.0f} | {100 * sum(v) / total:.1f} |")
+    fam = collections.defaultdict(list)
+    for k, v in by.items():
+        fam[_family(k)] += v
+    lines += ["", "Per family:", "", "| family | calls | avg us | total us |", "|---|---|---|---|"]
+    for f, v in sorted(fam.items(), key=lambda kv: -sum(kv[1])):
+        lines.append(f"| {f} | {len(v)} | {statistics.mean(v):.1f} | {sum(v):.0f} |")
+    return "\n".join(lines) + "\n"
+
+
+def _counter_per_dispatch(d: str, counter: str):
+    """{kernel name: [counter value per dispatch]} from a --pmc run."""
+    per = collections.defaultdict(float)
+    names = {}
+    for p in _csvs(d, "counter_collection.csv"):
+        for r in csv.DictReader(open(p)):
+            if r["Counter_Name"] != counter:
+                continue
+            key = (p, r["Dispatch_Id"])
+            per[key] += float(r["Counter_Value"])  # summed over XCDs / instances
+            names[key] = r["Kernel_Name"]
+    out = collections.defaultdict(list)
+    for key, v in per.items():
+        out[names[key]].append(v)
+    return out
+
+
+def traffic(args) -> dict:
+    copy_bytes = args.copy_mib * 1024 * 1024
+    res = {}
+    for counter, d, cd in (("FETCH_SIZE", args.fetch, args.copy_fetch),
+                           ("WRITE_SIZE", args.write, args.copy_write)):
+        cal = _counter_per_dispatch(cd, counter)
+        big = max((max(v) for v in cal.values()), default=0.0)  # the copy is the largest dispatch
+        factor = copy_bytes / (big * 1024.0) if big > 0 else 1.0
+        res[counter] = {"factor": factor}
+        per = _counter_per_dispatch(d, counter)
+        dm = _demangle(sorted(per))
+        fam = collections.defaultdict(list)
+        for k, v in per.items():
+            fam[_family(_short(dm[k]))] += v
+        for f, v in fam.items():
+            res[counter][f] = statistics.mean(v) * 1024.0 * factor
+    out = {"_note": "HBM bytes per dispatch: FETCH_SIZE + WRITE_SIZE (KiB) x copy-calibrated factor",
+           "_factors": {"FETCH_SIZE": res["FETCH_SIZE"]["factor"],
+                        "WRITE_SIZE": res["WRITE_SIZE"]["factor"]}}
+    for f in set(res["FETCH_SIZE"]) | set(res["WRITE_SIZE"]):
+        if f == "factor":
+            continue
+        out[f] = round(res["FETCH_SIZE"].get(f, 0.0) + res["WRITE_SIZE"].get(f, 0.0))
+    return out
+
+
+def copy(args) -> None:
+    import torch
+    n = args.mib * 1024 * 1024 // 4
+    src = torch.ones(n, device="cuda", dtype=torch.float32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"copied {args.mib} MiB x 3", flush=True)
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawTextHelpFormatter)
+    sub = ap.add_subparsers(dest="cmd_name", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("dir")
+    t.add_argument("--cmd", required=True)
+    t.add_argument("--title", default="rocprofv3 kernel trace")
+    t.add_argument("--range", help="only dispatches inside this roctx range")
+    t.add_argument("--out")
+    c = sub.add_parser("copy")
+    c.add_argument("--mib", type=int, default=1024)
+    f = sub.add_parser("traffic")
+    for k in ("fetch", "write", "copy_fetch", "copy_write"):
+        f.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
+    f.add_argument("--copy-mib", type=int, required=True)
+    f.add_argument("--out")
+    a = ap.parse_args(argv)
+    if a.cmd_name == "trace":
+        text = trace(a)
+        if a.out:
+            Path(a.out).write_text(text)
+        print(text)
+    elif a.cmd_name == "copy":
+        copy(a)
+    else:
+        d = traffic(a)
+        if a.out:
+            Path(a.out).write_text(json.dumps(d, indent=1) + "\n")
+        print(json.dumps(d, indent=1))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1:])
