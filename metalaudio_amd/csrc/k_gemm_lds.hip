@@ -326,7 +326,10 @@ int forced_lds_tile() {
   return v;
 }
 
-// Per-CU critical path: rounds of 256 concurrent tiles x tile area / shape efficiency.
+// Per-CU critical path: the most tiles any CU runs x tile area / shape efficiency. A CU that holds a
+// single workgroup runs it at about 0.6 of the rate of two co-resident ones (the issuing wave waits
+// for each LDS-DMA load to be accepted, and no other workgroup's MFMAs fill those cycles; measured on
+// the transformer shapes), so a grid of at most one tile per CU is charged 1/0.6.
 const LdsTile& choose_lds_tile(const GemmArgs& a) {
   const int f = forced_lds_tile();
   if (f >= 0 && f < (int)(sizeof(kLdsTiles) / sizeof(kLdsTiles[0]))) return kLdsTiles[f];
@@ -334,7 +337,8 @@ const LdsTile& choose_lds_tile(const GemmArgs& a) {
   double best_cost = 1e300;
   for (const LdsTile& t : kLdsTiles) {
     const int64_t tiles = (int64_t)cdiv(a.M, t.bm) * cdiv(a.N, t.bn) * a.batch;
-    const double cost = (double)cdiv(tiles, (int64_t)256) * t.bm * t.bn / t.eff;
+    const int64_t per_cu = cdiv(tiles, (int64_t)256);
+    const double cost = (double)per_cu * t.bm * t.bn / t.eff / (per_cu == 1 ? 0.6 : 1.0);
     if (cost < best_cost * 0.999) {
       best_cost = cost;
       best = &t;
