@@ -170,34 +170,36 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   const float* __restrict__ A = a.A + (int64_t)bz * a.sA;
   const float* __restrict__ B = a.B + (int64_t)bz * a.sB;
 
-  // Per-lane global sources of this wave's stage loads (rows past M / N are clamped to the last
-  // row: they are read but their products are never stored).
+  // Per-lane byte offsets of this wave's stage loads from the operand base (rows past M / N are
+  // clamped to the last row: they are read but their products are never stored). The base moves
+  // by one stage per load round in SGPRs, so the loads need no per-stage VALU address work.
   const int lr = lane >> 3, ls = lane & 7;
-  const float* asrc[A_INS];
-  const float* bsrc[B_INS];
+  unsigned aoffg[A_INS], boffg[B_INS];
 #pragma unroll
   for (int i = 0; i < A_INS; ++i) {
     const int rr = (wave * A_INS + i) * 8 + lr;
     const int gm = min(m0 + rr, M - 1);
-    asrc[i] = A + (int64_t)gm * a.lda + 4 * (ls ^ chunk_swizzle(rr));
+    aoffg[i] = 4u * (unsigned)(gm * a.lda + 4 * (ls ^ chunk_swizzle(rr)));
   }
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
     const int rr = (wave * B_INS + i) * 8 + lr;
     const int gn = min(n0 + rr, N - 1);
-    bsrc[i] = B + (int64_t)gn * a.ldb + 4 * (ls ^ chunk_swizzle(rr));
+    boffg[i] = 4u * (unsigned)(gn * a.ldb + 4 * (ls ^ chunk_swizzle(rr)));
   }
   const unsigned lds0 = lds_address(smem);
-  auto issue = [&](int kt) {
-    const unsigned base = lds0 + 4u * (unsigned)((kt % S) * STAGE);
+  auto issue = [&](int kt, int slot) {
+    const unsigned base = lds0 + 4u * (unsigned)(slot * STAGE);
+    const float* ak = A + kt * BK;
+    const float* bk = B + kt * BK;
 #pragma unroll
     for (int i = 0; i < A_INS; ++i)
-      lds_dma16(asrc[i] + kt * BK,
-                __builtin_amdgcn_readfirstlane(base + 4u * ((wave * A_INS + i) * 8 * BK)));
+      lds_dma16_s(ak, aoffg[i],
+                  __builtin_amdgcn_readfirstlane(base + 4u * ((wave * A_INS + i) * 8 * BK)));
 #pragma unroll
     for (int i = 0; i < B_INS; ++i)
-      lds_dma16(bsrc[i] + kt * BK,
-                __builtin_amdgcn_readfirstlane(base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
+      lds_dma16_s(bk, boffg[i],
+                  __builtin_amdgcn_readfirstlane(base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
   };
 
   floatx16 acc[WM][WN];
@@ -208,6 +210,7 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
+  // LDS word offsets of this lane's fragment rows in slot 0 (other slots: a constant offset)
   const int g = lane >> 5, l32 = lane & 31;
   int aoff[WM], boff[WN], asw[WM], bsw[WN];
 #pragma unroll
@@ -228,13 +231,16 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   // meet at the barrier that makes stage kt+1 visible and frees the slot of stage kt, issue the
   // loads of stage kt+S into that slot, and read stage kt+1's fragments interleaved with the
   // second half's MFMAs, so neither the barrier nor the LDS latency stalls the matrix pipe.
+  // The stage loop is unrolled by U (a multiple of S and of 2), so every ring slot and the two
+  // fragment register sets are compile-time choices: no address arithmetic and no register copies
+  // between stages.
   const int nk = K / BK;
 #pragma unroll
   for (int s = 0; s < S; ++s)
-    if (s < nk) issue(s);
-  float4 fa[4][WM], fb[4][WN];
-  auto read_frags = [&](int kt, float4 (&xa)[4][WM], float4 (&xb)[4][WN]) {
-    const float* base = smem + (kt % S) * STAGE;
+    if (s < nk) issue(s, s);
+  float4 fa[2][4][WM], fb[2][4][WN];
+  auto read_frags = [&](int slot, float4 (&xa)[4][WM], float4 (&xb)[4][WN]) {
+    const float* base = smem + slot * STAGE;
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int c = 4 * g + q4;
@@ -246,53 +252,64 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
         xb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
     }
   };
-  auto mfma_slice = [&](int q4) {
+  auto mfma_slice = [&](const float4 (&xa)[4][WM], const float4 (&xb)[4][WN], int q4) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[q4][i][s], fb[q4][j][s], acc[i][j],
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q4][i][s], xb[q4][j][s], acc[i][j],
                                                            0, 0, 0);
   };
   // stage 0: at most the S-1 newer stages may still be in flight
   if (S - 1 < nk) wait_vmcnt<(S - 1) * Cfg::L>();
   else wait_vmcnt<0>();
   stage_barrier();
-  read_frags(0, fa, fb);
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    mfma_slice(0);
-    mfma_slice(1);
-    __builtin_amdgcn_sched_barrier(0);  // the first half's MFMAs stay ahead of the barrier
-    // stage kt+1 is complete for this wave once at most the S-2 newer stages are outstanding
-    if (kt + S - 1 < nk) wait_vmcnt<(S - 2) * Cfg::L>();
-    else wait_vmcnt<0>();
-    stage_barrier();  // ... and for every wave; every wave's reads of stage kt are done
-    if (kt + S < nk) issue(kt + S);
-    float4 na[4][WM], nb[4][WN];
-    read_frags(kt + 1, na, nb);
-    mfma_slice(2);
-    mfma_slice(3);
-    // fragment reads alternate with the first MFMAs of the second half, so the last read has the
-    // remaining MFMAs to complete before the next stage needs it
-    constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
+  read_frags(0, fa[0], fb[0]);
+  constexpr int U = S % 2 == 0 ? S : 2 * S;
+  for (int kt0 = 0; kt0 + 1 < nk; kt0 += U) {
 #pragma unroll
-    for (int r = 0; r < kReads; ++r) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    for (int u = 0; u < U; ++u) {
+      const int kt = kt0 + u;
+      if (kt + 1 < nk) {
+        const int cur = u % 2, nxt = 1 - u % 2;
+        mfma_slice(fa[cur], fb[cur], 0);
+        mfma_slice(fa[cur], fb[cur], 1);
+        __builtin_amdgcn_sched_barrier(0);  // the first half's MFMAs stay ahead of the barrier
+        // stage kt+1 is complete for this wave once at most the S-2 newer stages are outstanding
+        if (kt + S - 1 < nk) wait_vmcnt<(S - 2) * Cfg::L>();
+        else wait_vmcnt<0>();
+        stage_barrier();  // ... and for every wave; every wave's reads of stage kt are done
+        if (kt + S < nk) issue(kt + S, u % S);  // stage kt+S goes to the slot stage kt frees
+        read_frags((u + 1) % S, fa[nxt], fb[nxt]);
+        mfma_slice(fa[cur], fb[cur], 2);
+        mfma_slice(fa[cur], fb[cur], 3);
+        // fragment reads alternate with the first MFMAs of the second half, so the last read has
+        // the remaining MFMAs to complete before the next stage needs it
+        constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
+#pragma unroll
+        for (int r = 0; r < kReads; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
+  }
+  // last stage: its fragments are in set (nk - 1) % 2 (moved to set 0 once, so a single copy of
+  // the MFMAs owns the accumulators)
+  if ((nk - 1) & 1) {
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
 #pragma unroll
-      for (int i = 0; i < WM; ++i) fa[q4][i] = na[q4][i];
+      for (int i = 0; i < WM; ++i) fa[0][q4][i] = fa[1][q4][i];
 #pragma unroll
-      for (int j = 0; j < WN; ++j) fb[q4][j] = nb[q4][j];
+      for (int j = 0; j < WN; ++j) fb[0][q4][j] = fb[1][q4][j];
     }
   }
 #pragma unroll
-  for (int q4 = 0; q4 < 4; ++q4) mfma_slice(q4);
+  for (int q4 = 0; q4 < 4; ++q4) mfma_slice(fa[0], fb[0], q4);
 
   // ---------------------------------------------------------------- epilogue
   // The activation and residual form are uniform: one specialised copy of the store loop each
@@ -359,7 +376,10 @@ void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
 }  // namespace
 
 bool gemm_nk_lds_supported(const GemmArgs& a) {
-  return a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
+  // per-lane load offsets are 32-bit byte offsets from the operand (batch) base
+  const bool off32 = ((int64_t)(a.M - 1) * a.lda + a.K) * 4 < ((int64_t)1 << 32) &&
+                     ((int64_t)(a.N - 1) * a.ldb + a.K) * 4 < ((int64_t)1 << 32);
+  return off32 && a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
          aligned16(a.B) && a.stats == nullptr && a.pro_coef == nullptr && a.pro_stats == nullptr &&
          (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0));

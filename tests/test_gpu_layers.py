@@ -339,7 +339,10 @@ def test_encoder_block_reference_fixture(dev, stream, golden_dir, name):
 
 
 @pytest.mark.parametrize("cin,cout,L,B", [(2, 48, 5000, 1), (48, 96, 3001, 2), (192, 384, 700, 1),
-                                          (8, 24, 400, 1)])
+                                          (8, 24, 400, 1),
+                                          # fused small-input blocks: batch, ragged tile, Cin 1 / 3 / 4
+                                          (2, 48, 5003, 2), (4, 32, 777, 1), (1, 16, 64, 3),
+                                          (3, 48, 1031, 1)])
 def test_encoder_block_rewrite_parity(dev, stream, cin, cout, L, B):
     say(f"encoder block rewrite {cin}->{cout} L={L} B={B}")
     x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
