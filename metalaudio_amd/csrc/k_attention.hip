@@ -18,6 +18,8 @@
 #include "kernels.hpp"
 #include "lds_dma.hpp"
 
+#include <type_traits>
+
 namespace mnn {
 namespace k {
 
@@ -72,9 +74,10 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     soff[i] = 4u * (unsigned)((e / PC) * (int)a.kv_rs + 4 * min(e % PC, PC - 2));
   }
   const unsigned lds0 = lds_address(smem);
-  // K block blk -> slot blk % 2, V block blk -> slot 2 + blk % 2
-  auto issue = [&](int blk, bool isv) {
-    const unsigned base = lds0 + 4u * (unsigned)(((isv ? 2 : 0) + (blk & 1)) * SLOT);
+  // K block blk -> slot blk % 2, V block blk -> slot 2 + blk % 2 (`par` = blk % 2, compile-time at
+  // the call sites in the block loop)
+  auto issue = [&](int blk, bool isv, int par) {
+    const unsigned base = lds0 + 4u * (unsigned)(((isv ? 2 : 0) + par) * SLOT);
     const float* src = (isv ? vb : kb) + (int64_t)blk * BKV * a.kv_rs;
     const bool tail = blk * BKV + BKV > a.Sk;
 #pragma unroll
@@ -92,9 +95,9 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     }
   };
   const int nblk = (a.Sk + BKV - 1) / BKV;
-  issue(0, false);
-  issue(0, true);
-  if (nblk > 1) issue(1, false);
+  issue(0, false, 0);
+  issue(0, true, 0);
+  if (nblk > 1) issue(1, false, 1);
 
   // Q fragments: B operand of S^T = K Q^T; lane group G owns d in [G*HS, (G+1)*HS)
   const float qscale = a.scale * 1.4426950408889634f;
@@ -116,8 +119,11 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     }
   }
 
-  // O^T accumulators: MFMA w holds output rows d = ND*i + w (i = MFMA row), so a lane's ND
-  // values of one V row are adjacent (one LDS read) and its outputs are contiguous
+  // O^T accumulators: MFMA w holds output rows d = dmap(i, w) (i = MFMA row). Head dim 64 uses
+  // d = 4i + w: a lane's four values of one V row are one 16-byte LDS read and its outputs are
+  // contiguous. Other head dims use d = i + 16w: a lane's values of one V row sit 16 floats apart,
+  // so the reads of a key tile's four rows are all within the 8-bit offset range of paired LDS
+  // reads from one base address (no per-read address arithmetic).
   floatx4 o[ND][NU];
   float mref[NU], lsum[NU];
 #pragma unroll
@@ -130,8 +136,8 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
 
   // K fragments of key tile t: rows 16t + l16, d in [G*HS, (G+1)*HS)
   float4 kfr[HS / 4][4];
-  auto read_k = [&](int blk, float4 (&kr)[HS / 4][4]) {
-    const float* ks = smem + (blk & 1) * SLOT;
+  auto read_k = [&](int par, float4 (&kr)[HS / 4][4]) {
+    const float* ks = smem + par * SLOT;
 #pragma unroll
     for (int s4 = 0; s4 < HS / 4; ++s4)
 #pragma unroll
@@ -142,7 +148,10 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   stage_barrier();
   read_k(0, kfr);
 
-  for (int blk = 0; blk < nblk; ++blk) {
+  // One 64-key block; PAR = blk % 2 selects the ring slots at compile time, so every LDS address
+  // below is a lane base plus an immediate offset. The block loop runs the two parities in turn.
+  auto block_step = [&](int blk, auto parc) {
+    constexpr int PAR = decltype(parc)::value;
     const int kv0 = blk * BKV;
     // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
     // accumulators interleave and no MFMA waits on the previous one
@@ -213,24 +222,25 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     // V(blk) and K(blk+1) have landed for this wave (they are the only loads in flight) ...
     wait_vmcnt<0>();
     stage_barrier();  // ... and for every wave; K(blk) and V(blk-1) are no longer read
-    if (blk + 2 < nblk) issue(blk + 2, false);
-    if (blk + 1 < nblk) issue(blk + 1, true);
-    // PV in four key tiles t. The V rows of tile t+1 (key 16(t+1) + 4G + r, d = ND*l16 ..
-    // +ND-1) and the K fragments of tile t of the next block are read while tile t's MFMAs run;
-    // the scheduling barriers keep each tile's reads next to it, which bounds the live registers.
-    const float* vs = smem + (2 + (blk & 1)) * SLOT;
-    const float* ksn = smem + ((blk + 1) & 1) * SLOT;
+    if (blk + 2 < nblk) issue(blk + 2, false, PAR);
+    if (blk + 1 < nblk) issue(blk + 1, true, 1 - PAR);
+    // PV in four key tiles t. The V rows of tile t+1 (key 16(t+1) + 4G + r, this lane's d) and
+    // the K fragments of tile t of the next block are read while tile t's MFMAs run; the
+    // scheduling barriers keep each tile's reads next to it, which bounds the live registers.
+    const float* vs = smem + (2 + PAR) * SLOT;
+    const float* ksn = smem + (1 - PAR) * SLOT;
     const bool next = blk + 1 < nblk;
     auto read_v = [&](int t, float (&vr)[4][ND]) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float* vrow = vs + (16 * t + 4 * G + r) * LDK + ND * l16;
         if constexpr (ND == 4) {
-          const float4 v4 = *reinterpret_cast<const float4*>(vrow);
+          const float4 v4 =
+              *reinterpret_cast<const float4*>(vs + (16 * t + 4 * G + r) * LDK + 4 * l16);
           vr[r][0] = v4.x; vr[r][1] = v4.y; vr[r][2] = v4.z; vr[r][3] = v4.w;
         } else {
+          const float* vrow = vs + (16 * t + 4 * G + r) * LDK + l16;
 #pragma unroll
-          for (int w = 0; w < ND; ++w) vr[r][w] = vrow[w];
+          for (int w = 0; w < ND; ++w) vr[r][w] = vrow[16 * w];
         }
       }
     };
@@ -256,10 +266,16 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
                                                            0, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+  };
+  int blk = 0;
+  for (; blk + 1 < nblk; blk += 2) {
+    block_step(blk, std::integral_constant<int, 0>{});
+    block_step(blk + 1, std::integral_constant<int, 1>{});
   }
+  if (blk < nblk) block_step(blk, std::integral_constant<int, 0>{});
 
-  // normalise and write O[b][q][h*HD + d]; lane holds d = ND*(4G + r) + w for query l16, i.e.
-  // 4*ND consecutive values
+  // normalise and write O[b][q][h*HD + d]; for query l16 a lane holds d = dmap(4G + r, w):
+  // 16 consecutive values (head dim 64) or ND runs of 4 (d = 16w + 4G + r)
   float* __restrict__ ob = a.o + (int64_t)b * a.o_bs + h * HD;
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
@@ -269,11 +285,18 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     const float inv = 1.f / (l + 1e-10f);
     const int q = qw0 + 16 * u + l16;
     if (q < a.Sq) {
-      float* orow = ob + (int64_t)q * a.o_rs + 4 * ND * G;
+      float* orow = ob + (int64_t)q * a.o_rs;
+      if constexpr (ND == 4) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int w = 0; w < ND; ++w) orow[ND * r + w] = o[w][u][r] * inv;
+          for (int w = 0; w < ND; ++w) orow[16 * G + 4 * r + w] = o[w][u][r] * inv;
+      } else {
+#pragma unroll
+        for (int w = 0; w < ND; ++w)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) orow[16 * w + 4 * G + r] = o[w][u][r] * inv;
+      }
     }
   }
 }
