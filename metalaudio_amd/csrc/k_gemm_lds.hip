@@ -51,7 +51,17 @@ struct LdsCfg {
 // C = R + rscale[n] * act(acc + bias) (R, rscale optional). ACT = -1: activation code at run time.
 // Accumulator layout of a 32x32 block: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4,
 // column l%32; each store instruction writes two 128-byte row segments.
-template <int WMW, int WNW, int WM, int WN, int ACT, bool RES>
+//
+// The values the stores depend on are loaded before the stores, and one explicit wait separates
+// them. The vector memory counter counts stores as well as loads, so a load issued between stores
+// (or one the compiler cannot track through a branch) makes each later store wait for every
+// earlier store, and the epilogue would run at one memory latency per store. R may be C itself
+// (in-place residual, element for element); no lane stores an element another lane reads, so
+// loading before storing is exact. FAST (no bias along M, no residual): the few loads of the tile
+// come first. Otherwise one 32-row block at a time: its loads, a wait, its stores (holding every
+// residual of the tile at once would push the kernel past the register budget of two workgroups
+// per CU).
+template <int WMW, int WNW, int WM, int WN, int ACT, bool RES, bool FAST>
 __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
                                            int n0, int wm, int wn, int lane) {
   const int g = lane >> 5, l32 = lane & 31;
@@ -59,34 +69,53 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
   float* __restrict__ Cp = a.C + (int64_t)bz * a.sC;
   const float* Rp = RES && a.R ? a.R + (int64_t)bz * a.sR : nullptr;
   const bool full_m = m0 + WMW * WM * 32 <= a.M;
-  // The values a 32-row block's stores depend on are loaded before any of its stores. R may be C
-  // itself (in-place residual, element for element), so the compiler may not move a load of R
-  // or of the bias past an earlier store to C: loads interleaved with the stores would wait for
-  // memory once per element. No lane stores an element another lane reads, so loading first is
-  // exact; going block by block bounds the registers held.
+  constexpr int RI = FAST ? WM : 1;  // 32-row blocks whose residuals are held at once
   float bnv[WN], rsv[WN];
+  float rv[RES ? RI : 1][RES ? WN : 1][16];
+  if (a.bias_mode == BIAS_N) {
 #pragma unroll
-  for (int j = 0; j < WN; ++j) {
-    const int gn = min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1);
-    bnv[j] = a.bias_mode == BIAS_N ? a.bias[gn] : 0.f;
-    rsv[j] = RES && Rp ? (a.rscale ? a.rscale[gn] : 1.f) : 0.f;
+    for (int j = 0; j < WN; ++j) bnv[j] = a.bias[min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1)];
+  } else {
+#pragma unroll
+    for (int j = 0; j < WN; ++j) bnv[j] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < WN; ++j)
+    rsv[j] = RES && Rp && a.rscale ? a.rscale[min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1)] : 1.f;
+  // residuals of blocks [i0, i0 + RI)
+  auto load_res = [&](int i0) {
+    if constexpr (RES) {
+#pragma unroll
+      for (int ii = 0; ii < RI; ++ii)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const int gn = min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int gm =
+                min(m0 + wm * WM * 32 + (i0 + ii) * 32 + 8 * (v / 4) + 4 * g + (v % 4), a.M - 1);
+            rv[ii][j][v] = Rp ? Rp[(int64_t)gm * a.ldr + gn] : 0.f;
+          }
+        }
+    }
+  };
+  if constexpr (FAST) {
+    load_res(0);
+    wait_vmcnt<0>();
   }
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int mblk = m0 + wm * WM * 32 + i * 32;
     float bmv[16];
-    float rv[RES ? WN : 1][16];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int gm = min(mblk + 8 * (v / 4) + 4 * g + (v % 4), a.M - 1);
-      bmv[v] = a.bias_mode == BIAS_M ? a.bias[gm] : 0.f;
-      if constexpr (RES) {
+    for (int v = 0; v < 16; ++v) bmv[v] = 0.f;
+    if constexpr (!FAST) {
+      if (a.bias_mode == BIAS_M) {
 #pragma unroll
-        for (int j = 0; j < WN; ++j) {
-          const int gn = min(n0 + wn * WN * 32 + j * 32 + l32, a.N - 1);
-          rv[j][v] = Rp ? Rp[(int64_t)gm * a.ldr + gn] : 0.f;
-        }
+        for (int v = 0; v < 16; ++v) bmv[v] = a.bias[min(mblk + 8 * (v / 4) + 4 * g + (v % 4), a.M - 1)];
       }
+      load_res(i);
+      wait_vmcnt<0>();
     }
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
@@ -98,9 +127,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
         if (full_m || gm < a.M) {
           float val = acc[i][j][v] + bnv[j] + bmv[v];
           val = ACT < 0 ? apply_act(val, a.act) : apply_act(val, ACT);
-          if constexpr (RES) {
-            if (Rp) val = rv[j][v] + rsv[j] * val;
-          }
+          if constexpr (RES) val = rv[FAST ? i : 0][j][v] + rsv[j] * val;
           Cp[(int64_t)gm * a.ldc + gn] = val;
         }
       }
@@ -150,7 +177,7 @@ __device__ __forceinline__ void store_glu(const GemmArgs& a, const floatx16 (&ac
 
 // GLU: the GLU epilogue (a separate instantiation: only the encoder's rewrite GEMMs use it)
 template <int WMW, int WNW, int WM, int WN, int S, bool GLU>
-__global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) {
+__global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, A_INS = Cfg::A_INS, B_INS = Cfg::B_INS;
   constexpr int STAGE = Cfg::STAGE;
@@ -314,12 +341,15 @@ __global__ __launch_bounds__(WMW* WNW * 64) void gemm_nk_lds_kernel(GemmArgs a) 
   // ---------------------------------------------------------------- epilogue
   // The activation and residual form are uniform: one specialised copy of the store loop each
   // for the forms the transformer uses, a generic one for the rest.
-  const bool res = a.R != nullptr;
+  const bool res = a.R != nullptr, bm = a.bias_mode == BIAS_M;
   if constexpr (GLU) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
-  else if (a.act == 0 && !res) store_tile<WMW, WNW, WM, WN, 0, false>(a, acc, m0, n0, wm, wn, lane);
-  else if (a.act == 0) store_tile<WMW, WNW, WM, WN, 0, true>(a, acc, m0, n0, wm, wn, lane);
-  else if (a.act == 3 && !res) store_tile<WMW, WNW, WM, WN, 3, false>(a, acc, m0, n0, wm, wn, lane);
-  else store_tile<WMW, WNW, WM, WN, -1, true>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 0 && !res && !bm)
+    store_tile<WMW, WNW, WM, WN, 0, false, true>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 0 && !bm)
+    store_tile<WMW, WNW, WM, WN, 0, true, false>(a, acc, m0, n0, wm, wn, lane);
+  else if (a.act == 3 && !res && !bm)
+    store_tile<WMW, WNW, WM, WN, 3, false, true>(a, acc, m0, n0, wm, wn, lane);
+  else store_tile<WMW, WNW, WM, WN, -1, true, false>(a, acc, m0, n0, wm, wn, lane);
 }
 
 struct LdsTile {
