@@ -13,6 +13,7 @@
 // (mean, then E[(x-mean)^2]), biased variance, eps inside the square root.
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "lds_dma.hpp"  // wait_vmcnt
 
 namespace mnn {
 namespace k {
@@ -165,16 +166,22 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
   if (row >= rows) return;
   const int F4 = F >> 2;
   const float4* xr = reinterpret_cast<const float4*>(x + row * F);
-  float4 v[NV];
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  // gamma and beta are loaded with the row: a load between the stores below would make each
+  // store wait for the earlier ones
+  float4 v[NV], gv[NV], bv[NV];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
     if (idx < F4) {
       v[i] = xr[idx];
+      gv[i] = g4[idx];
+      bv[i] = b4[idx];
       s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     } else {
-      v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      v[i] = gv[i] = bv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
   const float mean = wave_sum(s) / (float)F;
@@ -190,13 +197,13 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
   const float var = wave_sum(q) / (float)F;
   const float rstd = 1.f / sqrtf(var + eps);
   float4* yr = reinterpret_cast<float4*>(y + row * F);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
-  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  wait_vmcnt<0>();  // every load has landed: the stores below need no waits between them
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
     if (idx < F4) {
-      float4 g = g4[idx], bb = b4[idx], o;
+      const float4 g = gv[i], bb = bv[i];
+      float4 o;
       o.x = g.x * ((v[i].x - mean) * rstd) + bb.x;
       o.y = g.y * ((v[i].y - mean) * rstd) + bb.y;
       o.z = g.z * ((v[i].z - mean) * rstd) + bb.z;
