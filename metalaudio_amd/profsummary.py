@@ -4,6 +4,9 @@ Subcommands:
   trace DIR --cmd "..." [--out FILE]
       per-kernel table (calls, average / min / total microseconds, share) from the
       *kernel_trace.csv of a `rocprofv3 --kernel-trace` run;
+  stats DIR --cmd "..." [--out FILE]
+      the *kernel_stats.csv of a `rocprofv3 --stats` run as a table (calls, average / min / max /
+      total microseconds, share);
   copy --mib N
       a plain device copy of N MiB (torch), the calibration run for the HBM counters;
   traffic --fetch DIR --write DIR --copy-fetch DIR --copy-write DIR --copy-mib N [--out FILE]
@@ -108,6 +111,24 @@ def trace(args) -> str:
     return "\n".join(lines) + "\n"
 
 
+def stats(args) -> str:
+    rows = []
+    for p in _csvs(args.dir, "kernel_stats.csv"):
+        rows += list(csv.DictReader(open(p)))
+    dm = _demangle(sorted({r["Name"] for r in rows}))
+    lines = [f"# {args.title}", "", "Command (repo root, GPU box):", "", "```", args.cmd, "```", "",
+             "`*_kernel_stats.csv` of the run, durations in microseconds.", "",
+             "| kernel | family | calls | avg us | min us | max us | total us | % |",
+             "|---|---|---|---|---|---|---|---|"]
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    for r in rows:
+        k = _short(dm[r["Name"]])
+        lines.append(f"| `{k}` | {_family(k)} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                     f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                     f"{float(r['TotalDurationNs']) / 1e3:.0f} | {float(r['Percentage']):.1f} |")
+    return "\n".join(lines) + "\n"
+
+
 def _counter_per_dispatch(d: str, counter: str):
     """{kernel name: [counter value per dispatch]} from a --pmc run."""
     per = collections.defaultdict(float)
@@ -171,6 +192,11 @@ def main(argv=None) -> None:
     t.add_argument("--title", default="rocprofv3 kernel trace")
     t.add_argument("--range", help="only dispatches inside this roctx range")
     t.add_argument("--out")
+    st = sub.add_parser("stats")
+    st.add_argument("dir")
+    st.add_argument("--cmd", required=True)
+    st.add_argument("--title", default="rocprofv3 --stats")
+    st.add_argument("--out")
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=1024)
     f = sub.add_parser("traffic")
@@ -179,8 +205,8 @@ def main(argv=None) -> None:
     f.add_argument("--copy-mib", type=int, required=True)
     f.add_argument("--out")
     a = ap.parse_args(argv)
-    if a.cmd_name == "trace":
-        text = trace(a)
+    if a.cmd_name in ("trace", "stats"):
+        text = trace(a) if a.cmd_name == "trace" else stats(a)
         if a.out:
             Path(a.out).write_text(text)
         print(text)
