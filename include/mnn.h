@@ -193,6 +193,37 @@ typedef struct mnn_encoder_block_desc {
 mnn_status mnn_encoder_block_create(mnn_device dev, const mnn_encoder_block_desc* desc,
                                     mnn_layer* out);
 
+typedef struct mnn_conv_transpose1d_desc {
+  int in_channels, out_channels, kernel_size, stride;
+  int padding, output_padding, dilation, groups;
+  int use_bias;
+} mnn_conv_transpose1d_desc;
+
+/* DynamicConvTranspose1D (DynamicConv1D.swift:411-645). Weights "weight" [in, out/groups, k],
+ * "bias" [out]. Input [C, L] or [B, C, L]; output length
+ * (L - 1) * stride - 2 * padding + dilation * (k - 1) + output_padding + 1. */
+mnn_status mnn_conv_transpose1d_create(mnn_device dev, const mnn_conv_transpose1d_desc* desc,
+                                       mnn_layer* out);
+
+typedef struct mnn_decoder_block_desc {
+  int in_channels, skip_channels, out_channels, kernel_size, stride, num_groups;
+} mnn_decoder_block_desc;
+
+/* UNetDecoderBlock (UNet.swift:184-388): concat(input, skip) -> ConvTranspose1D (padding
+ * (k-1)/2, output_padding stride-2+k%2) -> GroupNorm -> GELU. Weights "conv_tr.weight"
+ * [in+skip, out, k], "conv_tr.bias" [out], "norm.weight", "norm.bias". Forward through
+ * mnn_layer_forward_cross(input, skip, output, NULL); input and skip share B and L. */
+mnn_status mnn_decoder_block_create(mnn_device dev, const mnn_decoder_block_desc* desc,
+                                    mnn_layer* out);
+
+/* UNetPaddingCalculator (UNet.swift:393-448): left/right zero padding that makes the length a
+ * multiple of stride^levels (remainder split evenly, the odd sample on the right), and the length
+ * after `levels` downsamplings by `stride`. */
+mnn_status mnn_unet_padding(int64_t input_length, int levels, int kernel_size, int stride,
+                            int64_t* left_pad, int64_t* right_pad, int64_t* output_length);
+mnn_status mnn_unet_bottleneck_length(int64_t input_length, int levels, int stride,
+                                      int64_t* length);
+
 /* Pre-norm transformer layer on one sequence (TransformerLayer sub-blocks 1 and 5,
  * Transformer.swift:467-495): y = x + ls1*MHA(LN1 x); z = y + ls2*FFN(LN2 y).
  * layer_scale <= 0 disables LayerScale. Weights "norm1.*", "self_attn.*", "norm2.*",

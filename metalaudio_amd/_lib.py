@@ -59,6 +59,21 @@ class EncoderBlockDesc(C.Structure):
     ]
 
 
+class ConvTranspose1dDesc(C.Structure):
+    _fields_ = [
+        ("in_channels", C.c_int), ("out_channels", C.c_int), ("kernel_size", C.c_int),
+        ("stride", C.c_int), ("padding", C.c_int), ("output_padding", C.c_int),
+        ("dilation", C.c_int), ("groups", C.c_int), ("use_bias", C.c_int),
+    ]
+
+
+class DecoderBlockDesc(C.Structure):
+    _fields_ = [
+        ("in_channels", C.c_int), ("skip_channels", C.c_int), ("out_channels", C.c_int),
+        ("kernel_size", C.c_int), ("stride", C.c_int), ("num_groups", C.c_int),
+    ]
+
+
 P = C.c_void_p
 PP = C.POINTER(C.c_void_p)
 I64P = C.POINTER(C.c_int64)
@@ -99,6 +114,10 @@ SIGNATURES = {
     "mnn_mha_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_feedforward_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_encoder_block_create": (C.c_int, [P, C.POINTER(EncoderBlockDesc), PP]),
+    "mnn_conv_transpose1d_create": (C.c_int, [P, C.POINTER(ConvTranspose1dDesc), PP]),
+    "mnn_decoder_block_create": (C.c_int, [P, C.POINTER(DecoderBlockDesc), PP]),
+    "mnn_unet_padding": (C.c_int, [C.c_int64, C.c_int, C.c_int, C.c_int, I64P, I64P, I64P]),
+    "mnn_unet_bottleneck_length": (C.c_int, [C.c_int64, C.c_int, C.c_int, I64P]),
     "mnn_transformer_layer_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
     "mnn_cross_transformer_create": (
         C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),

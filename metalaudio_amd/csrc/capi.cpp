@@ -411,6 +411,44 @@ mnn_status mnn_encoder_block_create(mnn_device dev, const mnn_encoder_block_desc
                                     mnn_layer* out) {
   MNN_CREATE(make_encoder_block(d, need(desc)));
 }
+mnn_status mnn_conv_transpose1d_create(mnn_device dev, const mnn_conv_transpose1d_desc* desc,
+                                       mnn_layer* out) {
+  MNN_CREATE(make_conv_transpose1d(d, need(desc)));
+}
+mnn_status mnn_decoder_block_create(mnn_device dev, const mnn_decoder_block_desc* desc,
+                                    mnn_layer* out) {
+  MNN_CREATE(make_decoder_block(d, need(desc)));
+}
+mnn_status mnn_unet_padding(int64_t input_length, int levels, int kernel_size, int stride,
+                            int64_t* left_pad, int64_t* right_pad, int64_t* output_length) {
+  return guard([&] {
+    MNN_REQUIRE(left_pad && right_pad && output_length, MNN_ERR_INVALID_ARGUMENT,
+                "null output pointer");
+    MNN_REQUIRE(input_length >= 0 && levels >= 0 && stride > 0 && kernel_size > 0,
+                MNN_ERR_INVALID_ARGUMENT, "invalid padding query");
+    int64_t divisor = 1;
+    for (int i = 0; i < levels; ++i) {
+      MNN_REQUIRE(divisor <= (INT64_MAX / stride), MNN_ERR_INVALID_ARGUMENT,
+                  "stride^levels overflows");
+      divisor *= stride;
+    }
+    const int64_t rem = input_length % divisor;
+    const int64_t total = rem == 0 ? 0 : divisor - rem;
+    *left_pad = total / 2;
+    *right_pad = total - total / 2;
+    *output_length = input_length + total;
+  });
+}
+mnn_status mnn_unet_bottleneck_length(int64_t input_length, int levels, int stride,
+                                      int64_t* length) {
+  return guard([&] {
+    MNN_REQUIRE(length && stride > 0 && levels >= 0, MNN_ERR_INVALID_ARGUMENT,
+                "invalid bottleneck query");
+    int64_t l = input_length;
+    for (int i = 0; i < levels; ++i) l /= stride;
+    *length = l;
+  });
+}
 mnn_status mnn_transformer_layer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
                                         float layer_scale, mnn_precision prec, mnn_layer* out) {
   MNN_CREATE(make_transformer_layer(d, embed_dim, num_heads, ffn_dim, layer_scale, prec));

@@ -1,0 +1,184 @@
+// Transposed 1-D convolution (DynamicConvTranspose1D, DynamicConv1D.swift:411-645) and the channel
+// concat of UNetDecoderBlock (UNet.swift:262-280, concatenateChannels :303-331).
+//
+// Reference semantics (dynamic_conv_transpose1d_forward, DynamicConv1D.swift:588-640):
+//   y[oc][o] = bias[oc] + sum_ic sum_k x[ic][i] * W[ic][oc_g][k],  i = (o + pad - k*dil) / stride
+// over the (ic, k) for which the division is exact and 0 <= i < L; W is [Cin][Cout/groups][K].
+//
+// Matrix-core form (groups 1, dilation 1, K = T * stride): with o + pad = stride*q + r
+// (0 <= r < stride) the taps that reach o are k = r + stride*t at input i = q - t, t < T, so
+//   y[oc][stride*q + r - pad] = bias[oc] + sum_t sum_ic x[ic][q - t] * W[ic][oc][r + stride*t].
+// That is a GEMM over K' = T * Cp (Cp = Cin rounded up to 32, padded channels zero):
+//   rows m = stride*oc + r, A[m][(t, ic)] = W[ic][oc][r + stride*t]   (weights, packed at load)
+//   columns q, B[q][(t, ic)] = x[ic][q - t] (zero outside [0, L))      (convt_pack_kernel)
+// on the LDS-DMA GEMM with its transposed-conv epilogue, which scatters row m, column q to
+// y[oc][stride*q + r - pad] (+bias). The pack kernel reads the input rows once and writes their
+// unfolded transpose (T times the input), concatenating the decoder's skip on the way.
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mnn {
+namespace k {
+
+using namespace dev;
+
+namespace {
+
+constexpr int kPQ = 64;   // output rows q per pack tile
+constexpr int kPC = 64;   // channels per pack tile
+
+// One tile: channels [c0, c0 + 64) x rows q in [q0, q0 + 64). The input window of a channel is
+// positions q0 - (T - 1) .. q0 + 63, staged in LDS; the unfolded rows are written 16 bytes per
+// thread along the channel dimension.
+template <int T>
+__global__ __launch_bounds__(256) void convt_pack_kernel(ConvTPackArgs a) {
+  constexpr int W = kPQ + T - 1;  // window positions per channel
+  constexpr int PITCH = W + 1;
+  __shared__ float tile[kPC * PITCH];
+  const int b = blockIdx.z;
+  const int64_t q0 = (int64_t)blockIdx.x * kPQ;
+  const int c0 = blockIdx.y * kPC;
+  const int tid = threadIdx.x;
+  const float* x1 = a.x1 + (int64_t)b * a.C1 * a.L;
+  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * a.L : nullptr;
+  for (int e = tid; e < kPC * W; e += 256) {
+    const int i = e / W, jj = e % W;
+    const int c = c0 + i;
+    const int64_t p = q0 - (T - 1) + jj;
+    float v = 0.f;
+    if (p >= 0 && p < a.L) {
+      if (c < a.C1) v = x1[(int64_t)c * a.L + p];
+      else if (c < a.C1 + a.C2) v = x2[(int64_t)(c - a.C1) * a.L + p];
+    }
+    tile[i * PITCH + jj] = v;
+  }
+  __syncthreads();
+  const int kp = T * a.Cp;
+  float* __restrict__ ub = a.u + (int64_t)b * a.Lq * kp;
+  for (int e = tid; e < T * kPQ * (kPC / 4); e += 256) {
+    const int c4 = e % (kPC / 4), qq = (e / (kPC / 4)) % kPQ, t = e / ((kPC / 4) * kPQ);
+    const int64_t q = q0 + qq;
+    const int c = c0 + 4 * c4;
+    if (q >= a.Lq || c >= a.Cp) continue;
+    const int col = qq + (T - 1) - t;
+    const float4 v = make_float4(tile[(4 * c4 + 0) * PITCH + col], tile[(4 * c4 + 1) * PITCH + col],
+                                 tile[(4 * c4 + 2) * PITCH + col], tile[(4 * c4 + 3) * PITCH + col]);
+    *reinterpret_cast<float4*>(ub + q * kp + t * a.Cp + c) = v;
+  }
+}
+
+// Direct form for every other configuration (groups, dilation, K not a multiple of the stride):
+// one thread per output, the reference's gather loop (ic, then k; bias last).
+__global__ __launch_bounds__(256) void convt_direct_kernel(ConvTArgs a) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t per_b = (int64_t)a.Cout * a.Lout;
+  if (idx >= per_b * a.B) return;
+  const int b = (int)(idx / per_b);
+  const int oc = (int)((idx % per_b) / a.Lout);
+  const int64_t o = idx % a.Lout;
+  const int Cin = a.C1 + a.C2;
+  const int coutpg = a.Cout / a.groups, cinpg = Cin / a.groups;
+  const int g = oc / coutpg, ocg = oc % coutpg;
+  float sum = 0.f;
+  for (int icg = 0; icg < cinpg; ++icg) {
+    const int ic = g * cinpg + icg;
+    const float* xr = ic < a.C1 ? a.x1 + ((int64_t)b * a.C1 + ic) * a.L
+                                : a.x2 + ((int64_t)b * a.C2 + (ic - a.C1)) * a.L;
+    for (int k = 0; k < a.K; ++k) {
+      const int64_t num = o + a.pad - (int64_t)k * a.dil;
+      if (num >= 0 && num % a.stride == 0) {
+        const int64_t i = num / a.stride;
+        if (i < a.L) sum = fmaf(xr[i], a.w[((int64_t)ic * coutpg + ocg) * a.K + k], sum);
+      }
+    }
+  }
+  if (a.bias) sum += a.bias[oc];
+  a.y[idx] = sum;
+}
+
+}  // namespace
+
+bool convt_gemm_supported(int Cin, int Cout, int K, int stride, int dil, int groups) {
+  return groups == 1 && dil == 1 && stride >= 1 && K % stride == 0 && (K / stride == 1 ||
+         K / stride == 2 || K / stride == 4) && Cin > 0 && Cout > 0;
+}
+
+int convt_padded_cin(int Cin) { return (Cin + 31) / 32 * 32; }
+
+int64_t convt_rows(int64_t Lout, int stride, int pad) { return (Lout - 1 + pad) / stride + 1; }
+
+void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, float* out) {
+  const int T = K / stride, Cp = convt_padded_cin(Cin), kp = T * Cp;
+  for (int64_t i = 0; i < (int64_t)stride * Cout * kp; ++i) out[i] = 0.f;
+  for (int oc = 0; oc < Cout; ++oc)
+    for (int r = 0; r < stride; ++r)
+      for (int t = 0; t < T; ++t)
+        for (int ic = 0; ic < Cin; ++ic)
+          out[((int64_t)stride * oc + r) * kp + t * Cp + ic] =
+              w[((int64_t)ic * Cout + oc) * K + r + stride * t];
+}
+
+void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold) {
+  const int Cin = a.C1 + a.C2;
+  MNN_REQUIRE(convt_gemm_supported(Cin, a.Cout, a.K, a.stride, a.dil, a.groups) && wpack &&
+                  unfold && a.x1 && (a.C2 == 0 || a.x2) && a.y && a.L > 0 && a.Lout > 0,
+              MNN_ERR_INVALID_ARGUMENT, "convt_gemm: configuration outside the GEMM form");
+  const int T = a.K / a.stride, Cp = convt_padded_cin(Cin);
+  ConvTPackArgs p;
+  p.x1 = a.x1;
+  p.x2 = a.C2 ? a.x2 : nullptr;
+  p.C1 = a.C1;
+  p.C2 = a.C2;
+  p.L = a.L;
+  p.Cp = Cp;
+  p.Lq = convt_rows(a.Lout, a.stride, a.pad);
+  p.u = unfold;
+  const dim3 grid((unsigned)cdiv(p.Lq, kPQ), (unsigned)cdiv(Cp, kPC), (unsigned)a.B);
+  switch (T) {
+    case 1: launch(c, "convt_pack_f32", convt_pack_kernel<1>, grid, dim3(256), 0, p); break;
+    case 2: launch(c, "convt_pack_f32", convt_pack_kernel<2>, grid, dim3(256), 0, p); break;
+    default: launch(c, "convt_pack_f32", convt_pack_kernel<4>, grid, dim3(256), 0, p); break;
+  }
+  GemmArgs g;
+  g.M = a.stride * a.Cout;
+  g.N = (int)p.Lq;
+  g.K = T * Cp;
+  g.batch = a.B;
+  g.A = wpack;
+  g.lda = g.K;
+  g.sA = 0;
+  g.B = unfold;
+  g.ldb = g.K;
+  g.sB = p.Lq * g.K;
+  g.blayout = B_NK;
+  g.C = a.y;
+  g.ldc = a.Lout;
+  g.sC = (int64_t)a.Cout * a.Lout;
+  g.bias = a.bias;
+  g.bias_mode = a.bias ? BIAS_M : BIAS_NONE;
+  g.ct_stride = a.stride;
+  g.ct_pad = a.pad;
+  g.ct_len = a.Lout;
+  g.name = "convt_f32_mfma";
+  MNN_REQUIRE(gemm_nk_lds_supported(g), MNN_ERR_INVALID_ARGUMENT,
+              "convt_gemm: operands outside the LDS GEMM contract");
+  gemm_nk_lds(c, g);
+}
+
+int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout) {
+  return (int64_t)B * convt_rows(Lout, stride, pad) * (K / stride) * convt_padded_cin(Cin);
+}
+
+void convt_direct(const LaunchCtx& c, const ConvTArgs& a) {
+  const int Cin = a.C1 + a.C2;
+  MNN_REQUIRE(a.groups > 0 && Cin % a.groups == 0 && a.Cout % a.groups == 0 && a.stride > 0 &&
+                  a.dil > 0 && a.K > 0 && a.x1 && (a.C2 == 0 || a.x2) && a.w && a.y,
+              MNN_ERR_INVALID_ARGUMENT, "convt_direct: invalid configuration");
+  const int64_t n = (int64_t)a.B * a.Cout * a.Lout;
+  if (n == 0) return;
+  launch(c, "convt_direct_f32", convt_direct_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+         a);
+}
+
+}  // namespace k
+}  // namespace mnn

@@ -175,8 +175,46 @@ __device__ __forceinline__ void store_glu(const GemmArgs& a, const floatx16 (&ac
   }
 }
 
-// GLU: the GLU epilogue (a separate instantiation: only the encoder's rewrite GEMMs use it)
-template <int WMW, int WNW, int WM, int WN, int S, bool GLU>
+// Transposed-conv epilogue: row m = s*oc + r (phase r of output channel oc), column n = q; the value
+// (+ bias[oc]) belongs at output position o = s*q + r - ct_pad of channel oc:
+// C[oc * ldc + o] when 0 <= o < ct_len. A lane holds the s phases of one (oc, q) in registers
+// v..v+s-1 (s = 4: rows 4i..4i+3 of a 32-row block), so consecutive lanes cover consecutive
+// 4-sample runs of one output row. Bias values are loaded first (see store_tile).
+template <int WMW, int WNW, int WM, int WN>
+__device__ __forceinline__ void store_ct(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
+                                         int n0, int wm, int wn, int lane) {
+  const int g = lane >> 5, l32 = lane & 31;
+  float* __restrict__ Cp = a.C + (int64_t)blockIdx.z * a.sC;
+  const int s = a.ct_stride;
+  float bmv[WM][16];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int gm = min(m0 + wm * WM * 32 + i * 32 + 8 * (v / 4) + 4 * g + (v % 4), a.M - 1);
+      bmv[i][v] = a.bias ? a.bias[gm / s] : 0.f;
+    }
+  wait_vmcnt<0>();
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int mblk = m0 + wm * WM * 32 + i * 32;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int q = n0 + wn * WN * 32 + j * 32 + l32;
+      if (q >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
+        const int oc = gm / s, o = s * q + (gm - oc * s) - a.ct_pad;
+        if (gm < a.M && o >= 0 && o < a.ct_len) Cp[(int64_t)oc * a.ldc + o] = acc[i][j][v] + bmv[i][v];
+      }
+    }
+  }
+}
+
+// EPI: 0 bias / activation / residual (store_tile), 1 GLU (store_glu: only the encoder's rewrite
+// GEMMs use it), 2 transposed-conv scatter (store_ct); each a separate instantiation.
+template <int WMW, int WNW, int WM, int WN, int S, int EPI>
 __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, A_INS = Cfg::A_INS, B_INS = Cfg::B_INS;
@@ -342,7 +380,8 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   // The activation and residual form are uniform: one specialised copy of the store loop each
   // for the forms the transformer uses, a generic one for the rest.
   const bool res = a.R != nullptr, bm = a.bias_mode == BIAS_M;
-  if constexpr (GLU) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
+  if constexpr (EPI == 1) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
+  else if constexpr (EPI == 2) store_ct<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0 && !res && !bm)
     store_tile<WMW, WNW, WM, WN, 0, false, true>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0 && !bm)
@@ -399,8 +438,10 @@ void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch), block(Cfg::NT);
   const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
-  if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, true>, grid, block, 0, a);
-  else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, false>, grid, block, 0, a);
+  if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
+  else if (a.ct_stride > 0)
+    launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 2>, grid, block, 0, a);
+  else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0>, grid, block, 0, a);
 }
 
 }  // namespace
@@ -412,7 +453,8 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
   return off32 && a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
          aligned16(a.B) && a.stats == nullptr && a.pro_coef == nullptr && a.pro_stats == nullptr &&
-         (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0));
+         (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0)) &&
+         (a.ct_stride == 0 || (!a.glu && a.R == nullptr && a.act == 0 && a.bias_mode != BIAS_N));
 }
 
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {

@@ -104,6 +104,10 @@ struct GemmArgs {
   // GroupNorm(1) statistics of the output (after bias, before act): per workgroup partials
   // (count, mean, M2) at stats[(b*tiles + tile)*3]; tiles = gemm_num_tiles(...)
   float* stats = nullptr;
+  // Transposed-conv scatter epilogue (ct_stride = s > 0, LDS path only): row m = s*oc + r, column
+  // n = q; C[oc * ldc + s*q + r - ct_pad] = acc + bias[oc] where that position is in [0, ct_len).
+  int ct_stride = 0, ct_pad = 0;
+  int64_t ct_len = 0;
   // B_CONVREC conv: weights [K][16] and bias [K]
   const float* rc_w = nullptr;
   const float* rc_b = nullptr;
@@ -120,6 +124,39 @@ void gemm(const LaunchCtx& c, const GemmArgs& a);
 // activation or residual); no statistics or B prologue.
 bool gemm_nk_lds_supported(const GemmArgs& a);
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
+
+// ------------------------------------------------------------------ transposed conv (k_convt.hip)
+// DynamicConvTranspose1D (DynamicConv1D.swift:411-645) over the channel concat [x1; x2] (x2 may be
+// absent: C2 = 0): y[b][oc][o] (row pitch Lout) = bias + sum over (ic, k) with
+// o = i*stride - pad + k*dil. Weights w [C1 + C2][Cout/groups][K].
+struct ConvTArgs {
+  int B = 1, C1 = 0, C2 = 0, Cout = 0, K = 0, stride = 1, pad = 0, dil = 1, groups = 1;
+  int64_t L = 0, Lout = 0;
+  const float* x1 = nullptr;  // [B][C1][L]
+  const float* x2 = nullptr;  // [B][C2][L]
+  const float* w = nullptr;
+  const float* bias = nullptr;
+  float* y = nullptr;  // [B][Cout][Lout]
+};
+struct ConvTPackArgs {
+  const float* x1 = nullptr;
+  const float* x2 = nullptr;
+  int C1 = 0, C2 = 0, Cp = 0;
+  int64_t L = 0, Lq = 0;
+  float* u = nullptr;  // [B][Lq][T * Cp]
+};
+// The matrix-core form: groups 1, dilation 1, K = T * stride with T in {1, 2, 4}.
+bool convt_gemm_supported(int Cin, int Cout, int K, int stride, int dil, int groups);
+int convt_padded_cin(int Cin);
+// Output rows q of the GEMM form: (Lout - 1 + pad) / stride + 1.
+int64_t convt_rows(int64_t Lout, int stride, int pad);
+// Host packing of the weights for the GEMM form: out [stride * Cout][T * Cp],
+// out[stride*oc + r][t*Cp + ic] = w[ic][oc][r + stride*t] (zero for padded channels).
+void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, float* out);
+// Floats of the unfolded-input workspace the GEMM form needs.
+int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout);
+void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold);
+void convt_direct(const LaunchCtx& c, const ConvTArgs& a);
 
 // ------------------------------------------------------------------ encoder levels (k_enc.hip)
 // Strided conv (kernel 8, stride 4, dilation 1, groups 1, pad < 4) as an LDS-DMA implicit GEMM:

@@ -952,6 +952,193 @@ class EncoderBlockLayer : public Layer {
   DevBuf y_, partials_, z_, wpad_, ws_, zt_;
 };
 
+// ------------------------------------------------------------------ ConvTranspose1D
+// DynamicConvTranspose1D (DynamicConv1D.swift:411-645): weight [in, out/groups, k], bias [out];
+// output length (L - 1) * stride - 2 * padding + dilation * (k - 1) + output_padding + 1
+// (DynamicConv1D.swift:483-487). Groups 1, dilation 1 and k a multiple of the stride (1, 2 or 4
+// taps per phase) run as a GEMM on the matrix cores (k_convt.hip: operand unfold + LDS GEMM with a
+// scatter epilogue; the weights are repacked for it when loaded); every other configuration runs
+// the reference's gather loop as one thread per output.
+class ConvTranspose1DLayer : public Layer {
+ public:
+  ConvTranspose1DLayer(Device* d, const mnn_conv_transpose1d_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.out_channels > 0 && desc.kernel_size > 0 &&
+                    desc.stride > 0 && desc.dilation > 0 && desc.groups > 0 &&
+                    desc.padding >= 0 && desc.output_padding >= 0 &&
+                    desc.in_channels % desc.groups == 0 && desc.out_channels % desc.groups == 0,
+                MNN_ERR_INVALID_CONFIGURATION, "ConvTranspose1D: invalid configuration");
+    w_ = &add_param("weight", (int64_t)desc.in_channels * (desc.out_channels / desc.groups) *
+                                  desc.kernel_size);
+    if (desc.use_bias) b_ = &add_param("bias", desc.out_channels);
+    gemm_ = k::convt_gemm_supported(desc.in_channels, desc.out_channels, desc.kernel_size,
+                                    desc.stride, desc.dilation, desc.groups);
+    if (gemm_) {
+      std::vector<float> zero((size_t)w_->count, 0.f);
+      pack(zero.data());
+    }
+  }
+  const char* kind() const override { return "ConvTranspose1D"; }
+  Shape input_shape() const override { return {d_.in_channels, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0}; }
+  int64_t out_len(int64_t L) const {
+    return (L - 1) * d_.stride - 2LL * d_.padding + (int64_t)d_.dilation * (d_.kernel_size - 1) +
+           d_.output_padding + 1;
+  }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, L;
+    split_bcl(in, B, C, L);
+    MNN_REQUIRE(C == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose1D: expected " << d_.in_channels << " channels, got " << C);
+    MNN_REQUIRE(L > 0 && out_len(L) > 0, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose1D: input length " << L << " gives no output");
+    Shape o = in;
+    o[o.size() - 2] = d_.out_channels;
+    o.back() = out_len(L);
+    return o;
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    run(in.f32(), (int)C, nullptr, 0, (int)B, L, out.f32(), s);
+  }
+  // y [B][out][out_len(L)] from the channel concat [x1 (C1 channels); x2 (C2)], C1 + C2 = in.
+  void run(const float* x1, int C1, const float* x2, int C2, int B, int64_t L, float* y,
+           Stream& s) {
+    MNN_REQUIRE(C1 + C2 == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose1D: channel count mismatch");
+    k::ConvTArgs a;
+    a.B = B;
+    a.C1 = C1;
+    a.C2 = C2;
+    a.Cout = d_.out_channels;
+    a.K = d_.kernel_size;
+    a.stride = d_.stride;
+    a.pad = d_.padding;
+    a.dil = d_.dilation;
+    a.groups = d_.groups;
+    a.L = L;
+    a.Lout = out_len(L);
+    a.x1 = x1;
+    a.x2 = x2;
+    a.w = w_->ptr();
+    a.bias = b_ ? b_->ptr() : nullptr;
+    a.y = y;
+    if (gemm_) {
+      unfold_.reserve(sizeof(float) * k::convt_unfold_floats(B, d_.in_channels, d_.kernel_size,
+                                                              d_.stride, d_.padding, a.Lout));
+      k::convt_gemm(ctx(s), a, wpack_.f32(), unfold_.f32());
+    } else {
+      k::convt_direct(ctx(s), a);
+    }
+  }
+  const mnn_conv_transpose1d_desc& desc() const { return d_; }
+
+ protected:
+  void on_loaded(const std::string& name, const float* data, size_t) override {
+    if (name == "weight" && gemm_) pack(data);
+  }
+
+ private:
+  void pack(const float* w) {
+    const int T = d_.kernel_size / d_.stride, Cp = k::convt_padded_cin(d_.in_channels);
+    std::vector<float> h((size_t)d_.stride * d_.out_channels * T * Cp);
+    k::convt_pack_weights(w, d_.in_channels, d_.out_channels, d_.kernel_size, d_.stride, h.data());
+    dev_->make_current();
+    wpack_.reserve(sizeof(float) * h.size());
+    HIP_CHECK(hipMemcpy(wpack_.ptr, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice));
+  }
+  mnn_conv_transpose1d_desc d_;
+  Param* w_ = nullptr;
+  Param* b_ = nullptr;
+  bool gemm_ = false;
+  DevBuf wpack_, unfold_;
+};
+
+// ------------------------------------------------------------------ UNetDecoderBlock
+// UNetDecoderBlock (UNet.swift:184-388): concat(input, skip) over channels -> ConvTranspose1D with
+// padding (k - 1) / 2 and output_padding stride - 2 + k % 2 (UNet.swift:229-241; output length
+// stride * L for even k) -> GroupNorm -> tanh-GELU. The concat is folded into the transposed
+// conv's operand unfold, so no concatenated tensor is written (the reference copies both inputs
+// through the CPU, UNet.swift:303-331). Two inputs: mnn_layer_forward_cross(input, skip, out).
+class DecoderBlockLayer : public Layer {
+ public:
+  DecoderBlockLayer(Device* d, const mnn_decoder_block_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.skip_channels >= 0 && desc.out_channels > 0 &&
+                    desc.kernel_size > 0 && desc.stride > 0 && desc.num_groups > 0,
+                MNN_ERR_INVALID_CONFIGURATION, "UNetDecoderBlock: invalid configuration");
+    mnn_conv_transpose1d_desc c{};
+    c.in_channels = desc.in_channels + desc.skip_channels;
+    c.out_channels = desc.out_channels;
+    c.kernel_size = desc.kernel_size;
+    c.stride = desc.stride;
+    c.padding = (desc.kernel_size - 1) / 2;
+    c.output_padding = desc.stride - 2 + desc.kernel_size % 2;
+    c.dilation = 1;
+    c.groups = 1;
+    c.use_bias = 1;
+    MNN_REQUIRE(c.output_padding >= 0, MNN_ERR_INVALID_CONFIGURATION,
+                "UNetDecoderBlock: stride " << desc.stride << " gives a negative output padding");
+    convt_ = std::make_unique<ConvTranspose1DLayer>(d, c);
+    norm_ = std::make_unique<GroupNormLayer>(d, desc.num_groups, desc.out_channels, 1e-5f, true,
+                                             MNN_ACT_GELU);
+  }
+  const char* kind() const override { return "UNetDecoderBlock"; }
+  Shape input_shape() const override { return {d_.in_channels, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0}; }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, L;
+    split_bcl(in, B, C, L);
+    MNN_REQUIRE(C == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "UNetDecoderBlock: expected " << d_.in_channels << " channels, got " << C);
+    Shape o = in;
+    o[o.size() - 2] = d_.out_channels;
+    o.back() = convt_->out_len(L);
+    return o;
+  }
+  void load(const std::string& name, const float* data, size_t n) override {
+    if (name.rfind("conv_tr.", 0) == 0) return convt_->load(name.substr(8), data, n);
+    if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
+    fail(MNN_ERR_INVALID_ARGUMENT, "UNetDecoderBlock: unknown parameter '" + name + "'");
+  }
+  void forward(const Tensor&, Tensor&, Stream&) override {
+    fail(MNN_ERR_INVALID_CONFIGURATION,
+         "UNetDecoderBlock: forward takes (input, skip); use the two-input forward");
+  }
+  void forward_cross(const Tensor* in, const Tensor* skip, Tensor* out, Tensor*,
+                     Stream& s) override {
+    MNN_REQUIRE(in && skip && out, MNN_ERR_INVALID_ARGUMENT,
+                "UNetDecoderBlock: input, skip and output are required");
+    int64_t B, C, L, Bs, Cs, Ls;
+    split_bcl(in->shape, B, C, L);
+    split_bcl(skip->shape, Bs, Cs, Ls);
+    MNN_REQUIRE(C == d_.in_channels && Cs == d_.skip_channels && Bs == B && Ls == L,
+                MNN_ERR_SHAPE_MISMATCH,
+                "UNetDecoderBlock: input " << shape_str(in->shape) << " and skip "
+                                           << shape_str(skip->shape) << " do not match ["
+                                           << d_.in_channels << "|" << d_.skip_channels
+                                           << ", L]");
+    const Shape os = infer_output(in->shape);
+    check_out(*out, os);
+    const int Cout = d_.out_channels;
+    const int64_t lo = os.back();
+    y_.reserve(sizeof(float) * B * Cout * lo);
+    convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, L, y_.f32(), s);
+    const int G = norm_->groups();
+    const int nchunk = k::gn_num_chunks(Cout, G, lo);
+    partials_.reserve(sizeof(float) * 3 * B * G * nchunk);
+    k::gn_stats_partial(ctx(s), y_.f32(), (int)B, Cout, lo, G, partials_.f32(), nchunk);
+    norm_->finalize(s, (int)B, nchunk, partials_.f32());
+    k::gn_apply(ctx(s), y_.f32(), out->f32(), (int)B, Cout, lo, norm_->coef(), MNN_ACT_GELU);
+  }
+
+ private:
+  mnn_decoder_block_desc d_;
+  std::unique_ptr<ConvTranspose1DLayer> convt_;
+  std::unique_ptr<GroupNormLayer> norm_;
+  DevBuf y_, partials_;
+};
+
 // ------------------------------------------------------------------ transformer building blocks
 namespace {
 
@@ -1231,6 +1418,12 @@ std::unique_ptr<Layer> make_feedforward(Device* d, int in, int hidden, mnn_preci
 }
 std::unique_ptr<Layer> make_encoder_block(Device* d, const mnn_encoder_block_desc& desc) {
   return std::make_unique<EncoderBlockLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_conv_transpose1d(Device* d, const mnn_conv_transpose1d_desc& desc) {
+  return std::make_unique<ConvTranspose1DLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_decoder_block(Device* d, const mnn_decoder_block_desc& desc) {
+  return std::make_unique<DecoderBlockLayer>(d, desc);
 }
 std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, int ffn,
                                               float layer_scale, mnn_precision prec) {

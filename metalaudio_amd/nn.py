@@ -13,13 +13,15 @@ from typing import Iterable, Optional, Sequence
 
 import numpy as np
 
-from ._lib import ACT, PAD, PRECISION, Conv1dDesc, EncoderBlockDesc, MNNError, check, dims, lib
+from ._lib import (ACT, PAD, PRECISION, Conv1dDesc, ConvTranspose1dDesc, DecoderBlockDesc,
+                   EncoderBlockDesc, MNNError, check, dims, lib)
 
 __all__ = [
     "MNNError", "AudioDevice", "Stream", "Tensor", "Layer", "Conv1D", "DynamicConv1D",
     "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
-    "FeedForward", "UNetEncoderBlock", "TransformerLayer", "CrossTransformerEncoder",
-    "Sequential", "mfma_probe",
+    "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
+    "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
+    "CrossTransformerEncoder", "Sequential", "mfma_probe",
 ]
 
 
@@ -358,6 +360,79 @@ class UNetEncoderBlock(Layer):
         """forward(input:encoder:) -> (output, skip); the skip is the output itself."""
         out = self(input, stream)
         return out, out
+
+
+class ConvTranspose1D(Layer):
+    """DynamicConvTranspose1D (DynamicConv1D.swift:411-645); weight [in, out/groups, k]."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1, padding=0,
+                 output_padding=0, dilation=1, groups=1, use_bias=True):
+        d = ConvTranspose1dDesc(input_channels, output_channels, kernel_size, stride, padding,
+                                output_padding, dilation, groups, int(use_bias))
+        super().__init__(device, _create(lib().mnn_conv_transpose1d_create, device.handle,
+                                         C.byref(d)))
+        self.stride, self.padding, self.output_padding = stride, padding, output_padding
+        self.kernel_size, self.dilation, self.use_bias = kernel_size, dilation, use_bias
+
+    def output_length(self, input_length: int) -> int:
+        """outputLength(for:) (DynamicConv1D.swift:483-487)."""
+        return ((input_length - 1) * self.stride - 2 * self.padding
+                + self.dilation * (self.kernel_size - 1) + self.output_padding + 1)
+
+    def load_weights(self, weights, bias=None) -> None:
+        self.load_weights_named("weight", weights)
+        if bias is not None and self.use_bias:
+            self.load_weights_named("bias", bias)
+
+
+DynamicConvTranspose1D = ConvTranspose1D
+
+
+class UNetDecoderBlock(Layer):
+    """UNetDecoderBlock (UNet.swift:184-388): concat(input, skip) -> ConvTranspose1D -> GroupNorm
+    -> GELU; forward(input, skip)."""
+
+    def __init__(self, device, input_channels, skip_channels, output_channels, kernel_size=8,
+                 stride=4, num_groups=8):
+        d = DecoderBlockDesc(input_channels, skip_channels, output_channels, kernel_size, stride,
+                             num_groups)
+        super().__init__(device, _create(lib().mnn_decoder_block_create, device.handle,
+                                         C.byref(d)))
+
+    def load_weights(self, conv_transpose_weight, conv_transpose_bias, norm_weight,
+                     norm_bias) -> None:
+        self.load_weights_named("conv_tr.weight", conv_transpose_weight)
+        if conv_transpose_bias is not None:
+            self.load_weights_named("conv_tr.bias", conv_transpose_bias)
+        self.load_weights_named("norm.weight", norm_weight)
+        self.load_weights_named("norm.bias", norm_bias)
+
+    def forward(self, input: Tensor, skip: Tensor, output: Tensor,  # type: ignore[override]
+                stream: Optional[Stream] = None) -> None:
+        check(lib().mnn_layer_forward_cross(self.handle, input.handle, skip.handle,
+                                            output.handle, None, _sh(stream)))
+
+    def forward_alloc(self, input: Tensor, skip: Tensor,
+                      stream: Optional[Stream] = None) -> Tensor:
+        out = Tensor(self.device, self.infer_output_shape(input.shape))
+        self.forward(input, skip, out, stream)
+        return out
+
+
+def unet_padding(input_length: int, levels: int, kernel_size: int = 8,
+                 stride: int = 4) -> tuple[int, int, int]:
+    """UNetPaddingCalculator.calculatePadding (UNet.swift:393-430): (left, right, padded length)."""
+    lp, rp, ol = C.c_int64(), C.c_int64(), C.c_int64()
+    check(lib().mnn_unet_padding(input_length, levels, kernel_size, stride, C.byref(lp),
+                                 C.byref(rp), C.byref(ol)))
+    return lp.value, rp.value, ol.value
+
+
+def unet_bottleneck_length(input_length: int, levels: int, stride: int = 4) -> int:
+    """UNetPaddingCalculator.bottleneckLength (UNet.swift:432-447)."""
+    out = C.c_int64()
+    check(lib().mnn_unet_bottleneck_length(input_length, levels, stride, C.byref(out)))
+    return out.value
 
 
 class TransformerLayer(Layer):

@@ -37,6 +37,8 @@ FAMILIES = [
     ("enc_conv_reduce_kernel", "enc_conv_reduce_f32"),
     ("enc_conv_kernel", "enc_conv_f32"),
     ("enc_gn_gelu_t_kernel", "enc_gn_gelu_t_f32"),
+    ("convt_pack_kernel", "convt_pack_f32"),
+    ("convt_direct_kernel", "convt_direct_f32"),
     ("layernorm", "layernorm"),
     ("copy_kernel", "copy_bytes"),
 ]
@@ -58,8 +60,12 @@ def _short(name: str) -> str:
 
 
 def _family(name: str) -> str:
-    if "gemm_nk_lds_kernel" in name and name.replace(" ", "").endswith(",true>"):
-        return "enc_rewrite_f32"  # the GLU instantiation
+    if "gemm_nk_lds_kernel" in name:
+        epi = name.replace(" ", "").rsplit(",", 1)[-1]
+        if epi == "1>":
+            return "enc_rewrite_f32"  # the GLU epilogue instantiation
+        if epi == "2>":
+            return "convt_f32_mfma"  # the transposed-conv epilogue instantiation
     for key, fam in FAMILIES:
         if key in name:
             return fam

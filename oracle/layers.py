@@ -9,7 +9,8 @@ import numpy as np
 __all__ = [
     "round_bf16", "reflect_pad", "conv1d", "group_norm", "layer_norm", "gelu_tanh", "gelu_layer",
     "stable_sigmoid", "glu", "activation", "linear", "mha", "feed_forward", "encoder_block",
-    "time_encoder", "transformer_layer", "cross_transformer",
+    "time_encoder", "conv_transpose1d", "conv_transpose1d_gather", "decoder_block", "unet_padding",
+    "unet_bottleneck_length", "time_unet", "transformer_layer", "cross_transformer",
 ]
 
 SQRT_2_OVER_PI = 0.7978845608  # literal used by every reference GELU kernel
@@ -241,6 +242,119 @@ def time_encoder(x, levels, dtype=np.float64):
         y = encoder_block(y, lv["conv.weight"], lv["conv.bias"], lv["norm.weight"],
                           lv["norm.bias"], 1, rewrite_w=lv["rewrite.weight"],
                           rewrite_b=lv["rewrite.bias"], dtype=dtype)
+    return y
+
+
+def conv_transpose1d_length(L, kernel_size, stride=1, padding=0, output_padding=0, dilation=1):
+    """outputLength(for:) (DynamicConv1D.swift:483-487)."""
+    return (L - 1) * stride - 2 * padding + dilation * (kernel_size - 1) + output_padding + 1
+
+
+def conv_transpose1d(x, w, b=None, stride=1, padding=0, output_padding=0, dilation=1, groups=1,
+                     dtype=np.float64):
+    """Transposed conv in scatter form: every input sample i of channel ic adds
+    x[ic][i] * W[ic][oc][k] to output o = i*stride - padding + k*dilation (kept when
+    0 <= o < Lout); weights [Cin, Cout/groups, K]. The same sum as the reference's per-output
+    gather (dynamic_conv_transpose1d_forward, DynamicConv1D.swift:588-640), organised per tap k so
+    each tap is one matrix product. Input [C, L] or [B, C, L]."""
+    x = _as(x, dtype)
+    w = _as(w, dtype)
+    squeeze = x.ndim == 2
+    if squeeze:
+        x = x[None]
+    B, Cin, L = x.shape
+    cin_w, coutpg, K = w.shape
+    assert cin_w == Cin and Cin % groups == 0
+    Cout = coutpg * groups
+    cinpg = Cin // groups
+    Lout = conv_transpose1d_length(L, K, stride, padding, output_padding, dilation)
+    y = np.zeros((B, Cout, Lout), dtype=dtype)
+    i = np.arange(L)
+    for g in range(groups):
+        xg = x[:, g * cinpg:(g + 1) * cinpg]                      # [B, cinpg, L]
+        for k in range(K):
+            o = i * stride - padding + k * dilation
+            keep = (o >= 0) & (o < Lout)
+            if not keep.any():
+                continue
+            contrib = np.einsum("bcl,co->bol", xg[:, :, keep], w[g * cinpg:(g + 1) * cinpg, :, k])
+            y[:, g * coutpg:(g + 1) * coutpg][:, :, o[keep]] += contrib
+    if b is not None:
+        y += _as(b, dtype)[None, :, None]
+    return y[0] if squeeze else y
+
+
+def conv_transpose1d_gather(x, w, b=None, stride=1, padding=0, output_padding=0, dilation=1,
+                            groups=1, dtype=np.float64):
+    """The reference kernel's loop, one output at a time (DynamicConv1D.swift:588-640: ic, then k,
+    input i = (o + padding - k*dilation) / stride when exact and in range, bias last). Pure Python:
+    for small cases only (it pins conv_transpose1d)."""
+    x = _as(x, dtype)
+    w = _as(w, dtype)
+    C, L = x.shape
+    _, coutpg, K = w.shape
+    Cout = coutpg * groups
+    cinpg = C // groups
+    Lout = conv_transpose1d_length(L, K, stride, padding, output_padding, dilation)
+    y = np.zeros((Cout, Lout), dtype=dtype)
+    for oc in range(Cout):
+        g, ocg = divmod(oc, coutpg)
+        for o in range(Lout):
+            acc = 0.0
+            for icg in range(cinpg):
+                ic = g * cinpg + icg
+                for k in range(K):
+                    num = o + padding - k * dilation
+                    if num >= 0 and num % stride == 0 and num // stride < L:
+                        acc += x[ic, num // stride] * w[ic, ocg, k]
+            y[oc, o] = acc + (b[oc] if b is not None else 0.0)
+    return y
+
+
+def decoder_block(x, skip, convt_w, convt_b, norm_w, norm_b, num_groups, kernel_size=8, stride=4,
+                  dtype=np.float64):
+    """UNetDecoderBlock.forward (UNet.swift:262-280): concat over channels (input first, then
+    skip, UNet.swift:303-331) -> ConvTranspose1D with padding (k-1)//2 and output_padding
+    stride - 2 + k % 2 (UNet.swift:229-241) -> GroupNorm -> tanh-GELU."""
+    z = np.concatenate([_as(x, dtype), _as(skip, dtype)], axis=-2)
+    y = conv_transpose1d(z, convt_w, convt_b, stride=stride, padding=(kernel_size - 1) // 2,
+                         output_padding=stride - 2 + kernel_size % 2, dtype=dtype)
+    return gelu_tanh(group_norm(y, num_groups, norm_w, norm_b, dtype=dtype), dtype)
+
+
+def unet_padding(input_length, levels, kernel_size=8, stride=4):
+    """UNetPaddingCalculator.calculatePadding (UNet.swift:393-430): pad to a multiple of
+    stride**levels, half (rounded down) on the left."""
+    divisor = stride ** levels
+    rem = input_length % divisor
+    if rem == 0:
+        return 0, 0, input_length
+    total = divisor - rem
+    return total // 2, total - total // 2, input_length + total
+
+
+def unet_bottleneck_length(input_length, levels, stride=4):
+    """UNetPaddingCalculator.bottleneckLength (UNet.swift:432-447)."""
+    for _ in range(levels):
+        input_length //= stride
+    return input_length
+
+
+def time_unet(x, enc_levels, dec_levels, enc_groups=1, dtype=np.float64):
+    """HTDemucs.forwardTimeUNet (HTDemucs.swift:521-548): the encoder chain keeps each level's
+    output as its skip; decoder i takes the running signal and the skip of encoder level
+    n-1-i. Encoder levels are the rewrite blocks of encoder_block; dec_levels hold
+    conv_tr.weight / conv_tr.bias / norm.weight / norm.bias / groups."""
+    y = _as(x, dtype)
+    skips = []
+    for lv in enc_levels:
+        y = encoder_block(y, lv["conv.weight"], lv["conv.bias"], lv["norm.weight"],
+                          lv["norm.bias"], enc_groups, rewrite_w=lv.get("rewrite.weight"),
+                          rewrite_b=lv.get("rewrite.bias"), dtype=dtype)
+        skips.append(y)
+    for i, dv in enumerate(dec_levels):
+        y = decoder_block(y, skips[len(skips) - 1 - i], dv["conv_tr.weight"], dv["conv_tr.bias"],
+                          dv["norm.weight"], dv["norm.bias"], dv["groups"], dtype=dtype)
     return y
 
 

@@ -498,3 +498,108 @@ def test_device_lost_and_stream_sync(dev):
     with pytest.raises(nn.MNNError) as e:
         nn.Linear(d2, 2, 2)
     assert e.value.name == "MNN_ERR_DEVICE_LOST"
+
+
+# ----------------------------------------------------------------------------- decoder path
+@pytest.mark.parametrize("cin,cout,k,s,p,op,d,g,L,B", [
+    (96, 24, 8, 4, 3, 2, 1, 1, 513, 2),    # decoder-block form (matrix cores, 2 taps per phase)
+    (20, 2, 8, 4, 3, 2, 1, 1, 1000, 1),    # padded channels, 8-row GEMM
+    (64, 16, 4, 4, 0, 0, 1, 1, 300, 2),    # one tap per phase
+    (16, 8, 8, 2, 1, 1, 1, 1, 77, 1),      # four taps per phase
+    (8, 6, 5, 2, 1, 1, 2, 2, 50, 2),       # groups + dilation: direct kernel
+    (5, 3, 3, 2, 0, 0, 1, 1, 40, 1),       # k not a multiple of the stride: direct kernel
+])
+def test_conv_transpose1d_parity(dev, stream, cin, cout, k, s, p, op, d, g, L, B):
+    say(f"conv transpose {cin}->{cout} k{k} s{s} p{p} op{op} d{d} g{g} L={L} B={B}")
+    x = RNG.standard_normal((B, cin, L)).astype(np.float32)
+    w = (RNG.standard_normal((cin, cout // g, k)) / np.sqrt(cin * k / s)).astype(np.float32)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    layer = nn.ConvTranspose1D(dev, cin, cout, k, s, p, op, d, g)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    ref = oracle.conv_transpose1d(x, w, b, s, p, op, d, g)
+    assert got.shape == ref.shape == (B, cout, layer.output_length(L))
+    assert_close(got, ref, ATOL, RTOL, "conv transpose")
+
+
+@pytest.mark.parametrize("cin,cskip,cout,groups,L,B", [
+    (48, 48, 24, 8, 513, 2),
+    (16, 16, 2, 2, 1024, 1),
+    (96, 96, 48, 8, 1344, 1),
+])
+def test_decoder_block_parity(dev, stream, cin, cskip, cout, groups, L, B):
+    say(f"decoder block {cin}+{cskip}->{cout} G={groups} L={L} B={B}")
+    x = RNG.standard_normal((B, cin, L)).astype(np.float32)
+    sk = RNG.standard_normal((B, cskip, L)).astype(np.float32)
+    w = (RNG.standard_normal((cin + cskip, cout, 8)) / np.sqrt((cin + cskip) * 2)).astype(
+        np.float32)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    blk = nn.UNetDecoderBlock(dev, cin, cskip, cout, 8, 4, groups)
+    blk.load_weights(w, b, gm, bt)
+    xt, st = nn.Tensor.from_numpy(dev, x), nn.Tensor.from_numpy(dev, sk)
+    out = blk.forward_alloc(xt, st, stream)
+    stream.sync(60000)
+    ref = oracle.decoder_block(x, sk, w, b, gm, bt, groups)
+    assert out.shape == ref.shape == (B, cout, 4 * L)
+    assert_close(out.to_numpy(), ref, ATOL, RTOL, "decoder block")
+
+
+def test_decoder_block_rejects_mismatched_skip(dev, stream):
+    blk = nn.UNetDecoderBlock(dev, 8, 8, 4, 8, 4, 2)
+    x = nn.Tensor.from_numpy(dev, np.zeros((1, 8, 32), np.float32))
+    sk = nn.Tensor.from_numpy(dev, np.zeros((1, 8, 31), np.float32))
+    out = nn.Tensor(dev, (1, 4, 128))
+    with pytest.raises(nn.MNNError):
+        blk.forward(x, sk, out, stream)
+    with pytest.raises(nn.MNNError):
+        blk(x, stream)  # the block needs its skip input
+
+
+def test_time_unet_parity(dev, stream):
+    """Two rewrite encoder levels and the two decoder levels back to the padded length
+    (HTDemucs.forwardTimeUNet composition, HTDemucs.swift:521-548)."""
+    left, right, L = nn.unet_padding(3000, 2, 8, 4)
+    assert (left, right, L) == oracle.unet_padding(3000, 2, 8, 4)
+    say(f"time U-Net 2 levels, padded length {L}")
+    ch = [2, 16, 32]
+    x = RNG.uniform(-1, 1, (1, 2, L)).astype(np.float32)
+    enc_p, dec_p, enc, dec = [], [], [], []
+    for i in range(2):
+        c0, c1 = ch[i], ch[i + 1]
+        lv = {"conv.weight": (RNG.standard_normal((c1, c0, 8)) * np.sqrt(2 / (8 * c0))),
+              "conv.bias": RNG.standard_normal(c1) * 0.1, "norm.weight": np.ones(c1),
+              "norm.bias": np.zeros(c1),
+              "rewrite.weight": RNG.standard_normal((2 * c1, c1, 1)) * np.sqrt(2 / c1),
+              "rewrite.bias": RNG.standard_normal(2 * c1) * 0.1}
+        lv = {k: v.astype(np.float32) for k, v in lv.items()}
+        blk = nn.UNetEncoderBlock(dev, c0, c1, 8, 4, 1, rewrite=True)
+        blk.load_weights(lv["conv.weight"], lv["conv.bias"], lv["norm.weight"], lv["norm.bias"],
+                         lv["rewrite.weight"], lv["rewrite.bias"])
+        enc_p.append(lv)
+        enc.append(blk)
+    for i in reversed(range(2)):
+        c1, c0 = ch[i + 1], ch[i]
+        g = min(8, c0)
+        dv = {"conv_tr.weight": (RNG.standard_normal((2 * c1, c0, 8)) / np.sqrt(4 * c1)),
+              "conv_tr.bias": RNG.standard_normal(c0) * 0.1, "norm.weight": np.ones(c0),
+              "norm.bias": np.zeros(c0)}
+        dv = {k: v.astype(np.float32) for k, v in dv.items()}
+        blk = nn.UNetDecoderBlock(dev, c1, c1, c0, 8, 4, g)
+        blk.load_weights(dv["conv_tr.weight"], dv["conv_tr.bias"], dv["norm.weight"],
+                         dv["norm.bias"])
+        dv["groups"] = g
+        dec_p.append(dv)
+        dec.append(blk)
+    y = nn.Tensor.from_numpy(dev, x)
+    skips = []
+    for blk in enc:
+        y = blk(y, stream)
+        skips.append(y)
+    for i, blk in enumerate(dec):
+        y = blk.forward_alloc(y, skips[len(skips) - 1 - i], stream)
+    stream.sync(60000)
+    ref = oracle.time_unet(x, enc_p, dec_p)
+    assert y.shape == ref.shape == (1, 2, L)
+    assert_close(y.to_numpy(), ref, ATOL, RTOL, "time U-Net")

@@ -320,3 +320,83 @@ def test_planted_mistakes_are_caught(golden_dir):
     wrong = oracle.encoder_block(d["input"], wt, d["conv_bias"], d["norm_weight"],
                                  d["norm_bias"], 8)
     assert np.abs(wrong - ref).max() > 1e-2
+
+
+# ----------------------------------------------------------------------------- decoder path
+@pytest.mark.parametrize("cin,cout,k,s,p,op,d,g", [
+    (3, 4, 8, 4, 3, 2, 1, 1),    # the decoder block's transposed conv
+    (6, 4, 5, 2, 1, 1, 2, 2),    # groups and dilation
+    (4, 6, 3, 1, 0, 0, 1, 1),
+    (2, 3, 4, 4, 0, 0, 1, 1),    # k == stride: no overlap between inputs
+])
+def test_conv_transpose1d_matches_gather_and_torch(cin, cout, k, s, p, op, d, g):
+    """The scatter-form oracle against the reference kernel's per-output gather loop
+    (DynamicConv1D.swift:588-640) and torch.nn.functional.conv_transpose1d."""
+    x = RNG.standard_normal((cin, 11))
+    w = RNG.standard_normal((cin, cout // g, k))
+    b = RNG.standard_normal(cout)
+    y = oracle.conv_transpose1d(x, w, b, s, p, op, d, g)
+    np.testing.assert_allclose(y, oracle.conv_transpose1d_gather(x, w, b, s, p, op, d, g),
+                               rtol=1e-12, atol=1e-12)
+    ref = F.conv_transpose1d(t64(x)[None], t64(w), t64(b), s, p, op, g, d)[0]
+    np.testing.assert_allclose(y, ref.numpy(), rtol=1e-12, atol=1e-12)
+    assert y.shape[-1] == oracle.layers.conv_transpose1d_length(11, k, s, p, op, d)
+
+
+def test_conv_transpose1d_closed_forms():
+    """Nearest-neighbour upsampling (k == stride, ones) and a 1x1 transposed conv (W^T x)."""
+    x = np.array([[1.0, -2.0, 3.0]])
+    y = oracle.conv_transpose1d(x, np.ones((1, 1, 4)), stride=4)
+    np.testing.assert_allclose(y, [[1, 1, 1, 1, -2, -2, -2, -2, 3, 3, 3, 3]])
+    xm = RNG.standard_normal((3, 7))
+    w = RNG.standard_normal((3, 5, 1))
+    np.testing.assert_allclose(oracle.conv_transpose1d(xm, w), w[:, :, 0].T @ xm, atol=1e-12)
+
+
+def test_decoder_block_shapes_and_composition():
+    """UNetDecoderBlock: output length stride * L for k = 8, s = 4 (UNetTests.swift:405-440,
+    upsampling); the block is concat -> conv_transpose1d -> GroupNorm -> GELU, checked against
+    torch's ops."""
+    cin, cskip, cout, L = 6, 6, 4, 13
+    x, sk = RNG.standard_normal((2, cin, L)), RNG.standard_normal((2, cskip, L))
+    w = RNG.standard_normal((cin + cskip, cout, 8)) * 0.3
+    b, gm, bt = RNG.standard_normal(cout), 1 + RNG.standard_normal(cout) * 0.1, \
+        RNG.standard_normal(cout) * 0.1
+    y = oracle.decoder_block(x, sk, w, b, gm, bt, 2)
+    assert y.shape == (2, cout, 4 * L)
+    z = F.conv_transpose1d(torch.cat([t64(x), t64(sk)], 1), t64(w), t64(b), 4, 3, 2)
+    ref = F.gelu(F.group_norm(z, 2, t64(gm), t64(bt), 1e-5), approximate="tanh")
+    np.testing.assert_allclose(y, ref.numpy(), rtol=1e-10, atol=1e-10)
+    # a skip given in the wrong order is not the same block
+    wrong = oracle.decoder_block(sk, x, w, b, gm, bt, 2)
+    assert np.abs(wrong - y).max() > 1e-2
+
+
+@pytest.mark.parametrize("length,levels", [(1000, 1), (44_100, 5), (1024, 5), (343_980, 4),
+                                           (1, 3), (257, 4)])
+def test_unet_padding(length, levels):
+    """UNetPaddingCalculatorTests (UNetTests.swift:635-690): the padded length is a multiple of
+    stride**levels and the split is even with the odd sample on the right."""
+    left, right, out = oracle.unet_padding(length, levels, 8, 4)
+    assert out == length + left + right and out % 4 ** levels == 0
+    assert out - length < 4 ** levels and right - left in (0, 1)
+    if length % 4 ** levels == 0:
+        assert left == right == 0
+    assert oracle.unet_bottleneck_length(out, levels, 4) == out // 4 ** levels
+
+
+def test_time_unet_lengths_round_trip():
+    """A padded signal goes down 4 levels and back to its own length (HTDemucs.swift:521-548)."""
+    _, _, L = oracle.unet_padding(3000, 2, 8, 4)
+    ch = [2, 8, 16]
+    enc, dec = [], []
+    for i in range(2):
+        enc.append({"conv.weight": RNG.standard_normal((ch[i + 1], ch[i], 8)) * 0.2,
+                    "conv.bias": np.zeros(ch[i + 1]), "norm.weight": np.ones(ch[i + 1]),
+                    "norm.bias": np.zeros(ch[i + 1])})
+    for i in reversed(range(2)):
+        dec.append({"conv_tr.weight": RNG.standard_normal((2 * ch[i + 1], ch[i], 8)) * 0.2,
+                    "conv_tr.bias": np.zeros(ch[i]), "norm.weight": np.ones(ch[i]),
+                    "norm.bias": np.zeros(ch[i]), "groups": min(8, ch[i])})
+    y = oracle.time_unet(RNG.standard_normal((1, 2, L)), enc, dec)
+    assert y.shape == (1, 2, L)
