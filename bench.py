@@ -208,6 +208,38 @@ def time_cpu(fn, budget_s=3.0, max_reps=5):
     return statistics.median(ts)
 
 
+DEC_LEVELS = [(384, 192, 1344, 8), (192, 96, 5376, 8), (96, 48, 21504, 8), (48, 2, 86016, 2)]
+
+
+def decoder_setup(nn, dev):
+    """UNetDecoderBlock levels of the time branch (in = skip channels, out channels, input
+    length, groups), seeded synthetic weights, inputs and skips."""
+    r = np.random.default_rng(1006)
+    blocks, skips, outs, params, flops = [], [], [], [], 0.0
+    x = r.standard_normal((1, DEC_LEVELS[0][0], DEC_LEVELS[0][2])).astype(np.float32)
+    for cin, cout, L, g in DEC_LEVELS:
+        w = (r.standard_normal((2 * cin, cout, 8)) * np.sqrt(2.0 / (2 * cin * 2))).astype(np.float32)
+        b = np.zeros(cout, np.float32)
+        gm, bt = np.ones(cout, np.float32), np.zeros(cout, np.float32)
+        sk = r.standard_normal((1, cin, L)).astype(np.float32)
+        blk = nn.UNetDecoderBlock(dev, cin, cin, cout, 8, 4, g)
+        blk.load_weights(w, b, gm, bt)
+        blocks.append(blk)
+        skips.append(nn.Tensor.from_numpy(dev, sk))
+        outs.append(nn.Tensor(dev, (1, cout, 4 * L)))
+        params.append((w, b, gm, bt, g, sk))
+        flops += 2.0 * 2 * cin * cout * 8 * L
+    return {"blocks": blocks, "skips": skips, "outs": outs, "params": params, "flops": flops,
+            "x": nn.Tensor.from_numpy(dev, x), "x_host": x}
+
+
+def decoder_oracle(oracle, dec):
+    y = dec["x_host"]
+    for w, b, gm, bt, g, sk in dec["params"]:
+        y = oracle.decoder_block(y, sk, w, b, gm, bt, g, dtype=np.float32)
+    return y
+
+
 def config_table(nn, W, dev, stream, m, cpu=True):
     """GPU ms, achieved rate and roofline fraction of each BASELINE configuration, with the fp32
     oracle's CPU time on the host beside it (the oracle is only the CPU baseline here)."""
@@ -287,6 +319,18 @@ def config_table(nn, W, dev, stream, m, cpu=True):
         flops=f4)
     f5 = sum(v[0] for v in transformer_work(W.T5_BATCH).values())
     row("5_transformer_b4", time_gpu(lambda: run_transformer(m, stream), stream, 5), flops=f5)
+    # time-branch decoder (next row of the hot path): the four UNetDecoderBlock levels at the
+    # config-4 lengths of a padded chunk (344064 samples -> 86016 / 21504 / 5376 / 1344), with
+    # synthetic inputs and skips of those shapes
+    dec = decoder_setup(nn, dev)
+
+    def f6():
+        y = dec["x"]
+        for blk, sk, out in zip(dec["blocks"], dec["skips"], dec["outs"]):
+            blk.forward(y, sk, out, stream)
+            y = out
+    cpu6 = time_cpu(lambda: decoder_oracle(oracle, dec), max_reps=1) if cpu else None
+    row("6_time_decoder_b1", time_gpu(f6, stream, 10), flops=dec["flops"], cpu_ms=cpu6)
     t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
     q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
     to5, fo5 = nn.Tensor(dev, t5.shape), nn.Tensor(dev, q5.shape)

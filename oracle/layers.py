@@ -277,7 +277,8 @@ def conv_transpose1d(x, w, b=None, stride=1, padding=0, output_padding=0, dilati
             keep = (o >= 0) & (o < Lout)
             if not keep.any():
                 continue
-            contrib = np.einsum("bcl,co->bol", xg[:, :, keep], w[g * cinpg:(g + 1) * cinpg, :, k])
+            contrib = np.einsum("bcl,co->bol", xg[:, :, keep], w[g * cinpg:(g + 1) * cinpg, :, k],
+                                optimize=True)
             y[:, g * coutpg:(g + 1) * coutpg][:, :, o[keep]] += contrib
     if b is not None:
         y += _as(b, dtype)[None, :, None]
