@@ -96,7 +96,106 @@ __global__ __launch_bounds__(256) void convt_direct_kernel(ConvTArgs a) {
   a.y[idx] = sum;
 }
 
+// Few output channels (stride * Cout < 32, e.g. the decoder's last, 2-channel level): a 64-row
+// matrix-core tile would be mostly padding, so one thread computes all Cout * S outputs of one
+// column q in registers from the input read straight from HBM (no unfold): per input channel, T
+// samples from the LDS window and Cout * S * T weights read at wave-uniform addresses. One wave
+// per workgroup and 64 columns, so the grid has many small workgroups; every window load of a
+// channel chunk is issued before the first LDS store.
+template <int COUT, int S, int T>
+__global__ __launch_bounds__(64) void convt_small_kernel(ConvTArgs a) {
+  constexpr int NQ = 64;              // columns per workgroup (one per lane)
+  constexpr int CC = 32;              // input channels per LDS chunk
+  constexpr int W = NQ + T - 1;       // window positions: q0 - (T - 1) .. q0 + NQ - 1
+  constexpr int PITCH = W + 1;
+  constexpr int kIt = (CC * W + 63) / 64;
+  __shared__ float xs[CC * PITCH];
+  __shared__ __attribute__((aligned(16))) float wl[CC * COUT * S * T];
+  const int b = blockIdx.y, lane = threadIdx.x;
+  const int64_t q0 = (int64_t)blockIdx.x * NQ, q = q0 + lane;
+  const int Cin = a.C1 + a.C2;
+  const float* x1 = a.x1 + (int64_t)b * a.C1 * a.L;
+  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * a.L : nullptr;
+  float acc[COUT][S];
+#pragma unroll
+  for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+    for (int r = 0; r < S; ++r) acc[oc][r] = 0.f;
+  for (int c0 = 0; c0 < Cin; c0 += CC) {
+    float v[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = lane + 64 * it, i = e / W, jj = e % W, c = c0 + i;
+      const int64_t p = q0 - (T - 1) + jj;
+      v[it] = 0.f;
+      if (e < CC * W && p >= 0 && p < a.L) {
+        if (c < a.C1) v[it] = x1[(int64_t)c * a.L + p];
+        else if (c < Cin) v[it] = x2[(int64_t)(c - a.C1) * a.L + p];
+      }
+    }
+    // this chunk's weights W[c][oc][k] (k = r + S*t), contiguous over the chunk's channels
+    constexpr int kW = CC * COUT * S * T;
+    const int cn = min(CC, Cin - c0);
+    float wv[kW / 64];
+#pragma unroll
+    for (int it = 0; it < kW / 64; ++it) {
+      const int e = lane + 64 * it;
+      wv[it] = e < cn * COUT * S * T ? a.w[(int64_t)c0 * COUT * S * T + e] : 0.f;
+    }
+    __syncthreads();  // the previous chunk's window and weight reads are done
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+      const int e = lane + 64 * it;
+      if (e < CC * W) xs[(e / W) * PITCH + e % W] = v[it];
+    }
+#pragma unroll
+    for (int it = 0; it < kW / 64; ++it) wl[lane + 64 * it] = wv[it];
+    __syncthreads();
+#pragma unroll 4
+    for (int i = 0; i < cn; ++i) {
+      const float* wc = wl + i * COUT * (S * T);  // same address in every lane: LDS broadcast
+      float xv[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) xv[t] = xs[i * PITCH + lane + (T - 1) - t];
+#pragma unroll
+      for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+          for (int r = 0; r < S; ++r)
+            acc[oc][r] = fmaf(xv[t], wc[oc * (S * T) + r + S * t], acc[oc][r]);
+    }
+  }
+  float* yb = a.y + (int64_t)b * a.Cout * a.Lout;
+#pragma unroll
+  for (int oc = 0; oc < COUT; ++oc) {
+    const float bv = a.bias ? a.bias[oc] : 0.f;
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+      const int64_t o = S * q + r - a.pad;
+      if (o >= 0 && o < a.Lout) yb[(int64_t)oc * a.Lout + o] = acc[oc][r] + bv;
+    }
+  }
+}
+
 }  // namespace
+
+bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int groups) {
+  return groups == 1 && dil == 1 && stride == 4 && K == 8 && Cin > 0 &&
+         (Cout == 1 || Cout == 2 || Cout == 4);
+}
+
+void convt_small(const LaunchCtx& c, const ConvTArgs& a) {
+  MNN_REQUIRE(convt_small_supported(a.C1 + a.C2, a.Cout, a.K, a.stride, a.dil, a.groups) &&
+                  a.x1 && (a.C2 == 0 || a.x2) && a.w && a.y && a.L > 0 && a.Lout > 0,
+              MNN_ERR_INVALID_ARGUMENT, "convt_small: configuration outside the kernel's form");
+  const dim3 grid((unsigned)cdiv(convt_rows(a.Lout, a.stride, a.pad), 64), (unsigned)a.B);
+  switch (a.Cout) {
+    case 1: return launch(c, "convt_small_f32", convt_small_kernel<1, 4, 2>, grid, dim3(64), 0, a);
+    case 2: return launch(c, "convt_small_f32", convt_small_kernel<2, 4, 2>, grid, dim3(64), 0, a);
+    default: return launch(c, "convt_small_f32", convt_small_kernel<4, 4, 2>, grid, dim3(64), 0, a);
+  }
+}
 
 bool convt_gemm_supported(int Cin, int Cout, int K, int stride, int dil, int groups) {
   return groups == 1 && dil == 1 && stride >= 1 && K % stride == 0 && (K / stride == 1 ||

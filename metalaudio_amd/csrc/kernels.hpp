@@ -157,6 +157,9 @@ void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, fl
 int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout);
 void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold);
 void convt_direct(const LaunchCtx& c, const ConvTArgs& a);
+// Few output channels (k 8, stride 4, Cout 1, 2 or 4): registers per column, no unfold.
+bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int groups);
+void convt_small(const LaunchCtx& c, const ConvTArgs& a);
 
 // ------------------------------------------------------------------ encoder levels (k_enc.hip)
 // Strided conv (kernel 8, stride 4, dilation 1, groups 1, pad < 4) as an LDS-DMA implicit GEMM:

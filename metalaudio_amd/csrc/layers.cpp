@@ -957,8 +957,9 @@ class EncoderBlockLayer : public Layer {
 // output length (L - 1) * stride - 2 * padding + dilation * (k - 1) + output_padding + 1
 // (DynamicConv1D.swift:483-487). Groups 1, dilation 1 and k a multiple of the stride (1, 2 or 4
 // taps per phase) run as a GEMM on the matrix cores (k_convt.hip: operand unfold + LDS GEMM with a
-// scatter epilogue; the weights are repacked for it when loaded); every other configuration runs
-// the reference's gather loop as one thread per output.
+// scatter epilogue; the weights are repacked for it when loaded), except k 8 / stride 4 with at
+// most 4 output channels, which runs a register kernel (a 64-row matrix tile would be mostly
+// padding); every other configuration runs the reference's gather loop as one thread per output.
 class ConvTranspose1DLayer : public Layer {
  public:
   ConvTranspose1DLayer(Device* d, const mnn_conv_transpose1d_desc& desc) : Layer(d), d_(desc) {
@@ -970,8 +971,11 @@ class ConvTranspose1DLayer : public Layer {
     w_ = &add_param("weight", (int64_t)desc.in_channels * (desc.out_channels / desc.groups) *
                                   desc.kernel_size);
     if (desc.use_bias) b_ = &add_param("bias", desc.out_channels);
-    gemm_ = k::convt_gemm_supported(desc.in_channels, desc.out_channels, desc.kernel_size,
-                                    desc.stride, desc.dilation, desc.groups);
+    small_ = k::convt_small_supported(desc.in_channels, desc.out_channels, desc.kernel_size,
+                                      desc.stride, desc.dilation, desc.groups);
+    gemm_ = !small_ && k::convt_gemm_supported(desc.in_channels, desc.out_channels,
+                                               desc.kernel_size, desc.stride, desc.dilation,
+                                               desc.groups);
     if (gemm_) {
       std::vector<float> zero((size_t)w_->count, 0.f);
       pack(zero.data());
@@ -1024,7 +1028,9 @@ class ConvTranspose1DLayer : public Layer {
     a.w = w_->ptr();
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
-    if (gemm_) {
+    if (small_) {
+      k::convt_small(ctx(s), a);
+    } else if (gemm_) {
       unfold_.reserve(sizeof(float) * k::convt_unfold_floats(B, d_.in_channels, d_.kernel_size,
                                                               d_.stride, d_.padding, a.Lout));
       k::convt_gemm(ctx(s), a, wpack_.f32(), unfold_.f32());
@@ -1051,7 +1057,7 @@ class ConvTranspose1DLayer : public Layer {
   mnn_conv_transpose1d_desc d_;
   Param* w_ = nullptr;
   Param* b_ = nullptr;
-  bool gemm_ = false;
+  bool small_ = false, gemm_ = false;
   DevBuf wpack_, unfold_;
 };
 

@@ -503,7 +503,10 @@ def test_device_lost_and_stream_sync(dev):
 # ----------------------------------------------------------------------------- decoder path
 @pytest.mark.parametrize("cin,cout,k,s,p,op,d,g,L,B", [
     (96, 24, 8, 4, 3, 2, 1, 1, 513, 2),    # decoder-block form (matrix cores, 2 taps per phase)
-    (20, 2, 8, 4, 3, 2, 1, 1, 1000, 1),    # padded channels, 8-row GEMM
+    (20, 2, 8, 4, 3, 2, 1, 1, 1000, 1),    # 2 output channels: register kernel
+    (24, 1, 8, 4, 3, 2, 1, 1, 777, 2),     # 1 output channel, batch 2
+    (40, 4, 8, 4, 3, 0, 1, 1, 300, 1),     # 4 output channels, no output padding
+    (20, 8, 8, 4, 3, 2, 1, 1, 1000, 1),    # padded channels, 32-row GEMM
     (64, 16, 4, 4, 0, 0, 1, 1, 300, 2),    # one tap per phase
     (16, 8, 8, 2, 1, 1, 1, 1, 77, 1),      # four taps per phase
     (8, 6, 5, 2, 1, 1, 2, 2, 50, 2),       # groups + dilation: direct kernel
