@@ -346,15 +346,38 @@ __global__ __launch_bounds__(kRedThreads) void enc_conv_reduce_kernel(
   const float bm = bias[m];
   ShiftedStats st;
   const int c0 = blockIdx.x * kRedCols;
+  constexpr int U = kRedCols / kRedThreads;
+  // partials summed in split order (as before), four splits' loads in flight at a time; every
+  // load precedes the stores
+  float v[U];
+  int nn[U];
 #pragma unroll
-  for (int u = 0; u < kRedCols / kRedThreads; ++u) {
+  for (int u = 0; u < U; ++u) {
+    v[u] = 0.f;
+    nn[u] = min(c0 + u * kRedThreads + (int)threadIdx.x, N - 1);
+  }
+  int s = 0;
+  for (; s + 4 <= splits; s += 4) {
+    float t[4][U];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < U; ++u) t[j][u] = wr[(int64_t)(s + j) * total + nn[u]];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] += t[j][u];
+  }
+  for (; s < splits; ++s)
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] += wr[(int64_t)s * total + nn[u]];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
     const int n = c0 + u * kRedThreads + threadIdx.x;
     if (n < N) {
-      float v = 0.f;
-      for (int s = 0; s < splits; ++s) v += wr[(int64_t)s * total + n];
-      v += bm;
-      st.add(v);
-      yr[n] = v;
+      v[u] += bm;
+      st.add(v[u]);
+      yr[n] = v[u];
     }
   }
   float sn, smean, sm2;
