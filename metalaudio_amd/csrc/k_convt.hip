@@ -178,7 +178,52 @@ __global__ __launch_bounds__(64) void convt_small_kernel(ConvTArgs a) {
   }
 }
 
+// Sum of the K parts of the GEMM form, then the scatter of convt's epilogue:
+// y[b][oc][s*q + r - pad] = bias[oc] + sum_p ws[b][p][s*oc + r][q]. One thread per column q of one
+// output channel: it reads the s phase rows (coalesced over q) and writes s consecutive samples.
+__global__ __launch_bounds__(256) void convt_reduce_kernel(const float* __restrict__ ws, int ksplit,
+                                                           int M, int64_t N, int stride, int pad,
+                                                           const float* __restrict__ bias,
+                                                           float* __restrict__ y, int64_t Lout,
+                                                           int Cout) {
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= N) return;
+  const float* wb = ws + (int64_t)b * ksplit * M * N + (int64_t)stride * oc * N + q;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int p = 0; p < ksplit; ++p)
+    for (int r = 0; r < stride && r < 4; ++r) v[r] += wb[(int64_t)p * M * N + (int64_t)r * N];
+  const float bv = bias ? bias[oc] : 0.f;
+  float* yr = y + ((int64_t)b * Cout + oc) * Lout;
+  for (int r = 0; r < stride && r < 4; ++r) {
+    const int64_t o = stride * q + r - pad;
+    if (o >= 0 && o < Lout) yr[o] = v[r] + bv;
+  }
+}
+
+// K split of the GEMM form, for grids of at most ~1.5 64 x 64 tiles per CU: the most parts
+// (dividing the stage count, at least 6 stages each) that keep the grid within about four tiles
+// per CU. The deepest decoder level has few output columns and a long contraction; without a
+// split a CU runs one long tile alone. Larger grids lose more to the reduce pass than they gain
+// (measured on the decoder levels).
+int convt_ksplit(int B, int Cin, int Cout, int K, int stride, int pad, int64_t Lout) {
+  if (stride > 4) return 1;
+  const int64_t M = (int64_t)stride * Cout, N = convt_rows(Lout, stride, pad);
+  const int nk = (K / stride) * convt_padded_cin(Cin) / 32;
+  const int64_t tiles = cdiv(M, 64) * (int64_t)cdiv(N, 64) * B;
+  int best = 1;
+  if (tiles > 384) return best;
+  for (int p : {2, 3, 4, 6, 8})
+    if (nk % p == 0 && nk / p >= 6 && tiles * p <= 1024) best = p;
+  return best;
+}
+
 }  // namespace
+
+int64_t convt_split_ws_floats(int B, int Cin, int Cout, int K, int stride, int pad, int64_t Lout) {
+  const int p = convt_ksplit(B, Cin, Cout, K, stride, pad, Lout);
+  return p > 1 ? (int64_t)B * p * stride * Cout * convt_rows(Lout, stride, pad) : 0;
+}
 
 bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int groups) {
   return groups == 1 && dil == 1 && stride == 4 && K == 8 && Cin > 0 &&
@@ -217,7 +262,8 @@ void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, fl
               w[((int64_t)ic * Cout + oc) * K + r + stride * t];
 }
 
-void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold) {
+void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold,
+                float* split_ws) {
   const int Cin = a.C1 + a.C2;
   MNN_REQUIRE(convt_gemm_supported(Cin, a.Cout, a.K, a.stride, a.dil, a.groups) && wpack &&
                   unfold && a.x1 && (a.C2 == 0 || a.x2) && a.y && a.L > 0 && a.Lout > 0,
@@ -259,9 +305,23 @@ void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, floa
   g.ct_pad = a.pad;
   g.ct_len = a.Lout;
   g.name = "convt_f32_mfma";
+  const int parts = convt_ksplit(a.B, Cin, a.Cout, a.K, a.stride, a.pad, a.Lout);
+  if (parts > 1) {
+    MNN_REQUIRE(split_ws, MNN_ERR_INVALID_ARGUMENT, "convt_gemm: the K split needs a workspace");
+    g.ksplit = parts;
+    g.ws = split_ws;
+    g.ct_stride = 0;  // partial products only; the reduce applies bias and scatter
+    g.bias = nullptr;
+    g.bias_mode = BIAS_NONE;
+  }
   MNN_REQUIRE(gemm_nk_lds_supported(g), MNN_ERR_INVALID_ARGUMENT,
               "convt_gemm: operands outside the LDS GEMM contract");
   gemm_nk_lds(c, g);
+  if (parts > 1)
+    launch(c, "convt_reduce_f32", convt_reduce_kernel,
+           dim3((unsigned)cdiv(p.Lq, 256), (unsigned)a.Cout, (unsigned)a.B), dim3(256), 0,
+           (const float*)split_ws, parts, g.M, (int64_t)g.N, a.stride, a.pad, a.bias, a.y,
+           a.Lout, a.Cout);
 }
 
 int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout) {

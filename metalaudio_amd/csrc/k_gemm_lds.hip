@@ -212,8 +212,32 @@ __device__ __forceinline__ void store_ct(const GemmArgs& a, const floatx16 (&acc
   }
 }
 
+// K-split partial: the raw accumulators of K part p of batch b go to
+// ws[((b * ksplit + p) * M + m) * N + n]; the caller reduces the parts (and applies the epilogue).
+template <int WMW, int WNW, int WM, int WN>
+__device__ __forceinline__ void store_part(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
+                                           int n0, int wm, int wn, int lane) {
+  const int g = lane >> 5, l32 = lane & 31;
+  float* __restrict__ wp = a.ws + (int64_t)blockIdx.z * a.M * a.N;
+#pragma unroll
+  for (int i = 0; i < WM; ++i) {
+    const int mblk = m0 + wm * WM * 32 + i * 32;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int gn = n0 + wn * WN * 32 + j * 32 + l32;
+      if (gn >= a.N) continue;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
+        if (gm < a.M) wp[(int64_t)gm * a.N + gn] = acc[i][j][v];
+      }
+    }
+  }
+}
+
 // EPI: 0 bias / activation / residual (store_tile), 1 GLU (store_glu: only the encoder's rewrite
-// GEMMs use it), 2 transposed-conv scatter (store_ct); each a separate instantiation.
+// GEMMs use it), 2 transposed-conv scatter (store_ct), 3 K-split partials (store_part); each a
+// separate instantiation.
 template <int WMW, int WNW, int WM, int WN, int S, int EPI>
 __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
@@ -224,7 +248,9 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / WNW, wn = wave % WNW;
-  const int bz = blockIdx.z;
+  // blockIdx.z = batch * ksplit + K part (ksplit = 1 unless EPI == 3)
+  const int ks = EPI == 3 ? a.ksplit : 1;
+  const int bz = blockIdx.z / ks;
   // XCD-aware renumbering (workgroups go round robin over the 8 XCDs): consecutive logical tiles,
   // N fastest, land on one XCD and share the A panel in its L2.
   const int gx = gridDim.x;
@@ -232,6 +258,7 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   const int tn = logical % gx, tm = logical / gx;
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = a.M, N = a.N, K = a.K;
+  const int nk = K / BK / ks, kt0 = (int)(blockIdx.z % ks) * nk;  // this workgroup's stages
   const float* __restrict__ A = a.A + (int64_t)bz * a.sA;
   const float* __restrict__ B = a.B + (int64_t)bz * a.sB;
 
@@ -255,8 +282,8 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   const unsigned lds0 = lds_address(smem);
   auto issue = [&](int kt, int slot) {
     const unsigned base = lds0 + 4u * (unsigned)(slot * STAGE);
-    const float* ak = A + kt * BK;
-    const float* bk = B + kt * BK;
+    const float* ak = A + (kt0 + kt) * BK;
+    const float* bk = B + (kt0 + kt) * BK;
 #pragma unroll
     for (int i = 0; i < A_INS; ++i)
       lds_dma16_s(ak, aoffg[i],
@@ -299,7 +326,6 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   // The stage loop is unrolled by U (a multiple of S and of 2), so every ring slot and the two
   // fragment register sets are compile-time choices: no address arithmetic and no register copies
   // between stages.
-  const int nk = K / BK;
 #pragma unroll
   for (int s = 0; s < S; ++s)
     if (s < nk) issue(s, s);
@@ -382,6 +408,7 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   const bool res = a.R != nullptr, bm = a.bias_mode == BIAS_M;
   if constexpr (EPI == 1) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if constexpr (EPI == 2) store_ct<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
+  else if constexpr (EPI == 3) store_part<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0 && !res && !bm)
     store_tile<WMW, WNW, WM, WN, 0, false, true>(a, acc, m0, n0, wm, wn, lane);
   else if (a.act == 0 && !bm)
@@ -422,7 +449,7 @@ const LdsTile& choose_lds_tile(const GemmArgs& a) {
   const LdsTile* best = &kLdsTiles[0];
   double best_cost = 1e300;
   for (const LdsTile& t : kLdsTiles) {
-    const int64_t tiles = (int64_t)cdiv(a.M, t.bm) * cdiv(a.N, t.bn) * a.batch;
+    const int64_t tiles = (int64_t)cdiv(a.M, t.bm) * cdiv(a.N, t.bn) * a.batch * a.ksplit;
     const int64_t per_cu = cdiv(tiles, (int64_t)256);
     const double cost = (double)per_cu * t.bm * t.bn / t.eff / (per_cu == 1 ? 0.6 : 1.0);
     if (cost < best_cost * 0.999) {
@@ -436,9 +463,10 @@ const LdsTile& choose_lds_tile(const GemmArgs& a) {
 template <int WMW, int WNW, int WM, int WN, int S>
 void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
-  dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch), block(Cfg::NT);
+  dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch * a.ksplit), block(Cfg::NT);
   const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
-  if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
+  if (a.ksplit > 1) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 3>, grid, block, 0, a);
+  else if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
   else if (a.ct_stride > 0)
     launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 2>, grid, block, 0, a);
   else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0>, grid, block, 0, a);
@@ -454,7 +482,9 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
          aligned16(a.B) && a.stats == nullptr && a.pro_coef == nullptr && a.pro_stats == nullptr &&
          (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0)) &&
-         (a.ct_stride == 0 || (!a.glu && a.R == nullptr && a.act == 0 && a.bias_mode != BIAS_N));
+         (a.ct_stride == 0 || (!a.glu && a.R == nullptr && a.act == 0 && a.bias_mode != BIAS_N)) &&
+         a.ksplit >= 1 && (a.K / BK) % a.ksplit == 0 &&
+         (a.ksplit == 1 || (a.ws != nullptr && !a.glu && a.stats == nullptr));
 }
 
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {

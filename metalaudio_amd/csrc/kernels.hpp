@@ -108,6 +108,10 @@ struct GemmArgs {
   // n = q; C[oc * ldc + s*q + r - ct_pad] = acc + bias[oc] where that position is in [0, ct_len).
   int ct_stride = 0, ct_pad = 0;
   int64_t ct_len = 0;
+  // K split (LDS path only): ksplit > 1 writes the raw partial products of each K part to
+  // ws[((b * ksplit + p) * M + m) * N + n] and applies no epilogue (the caller reduces the parts).
+  int ksplit = 1;
+  float* ws = nullptr;
   // B_CONVREC conv: weights [K][16] and bias [K]
   const float* rc_w = nullptr;
   const float* rc_b = nullptr;
@@ -155,8 +159,11 @@ int64_t convt_rows(int64_t Lout, int stride, int pad);
 void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, float* out);
 // Floats of the unfolded-input workspace the GEMM form needs.
 int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout);
-void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold);
+void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold,
+                float* split_ws);
 void convt_direct(const LaunchCtx& c, const ConvTArgs& a);
+// Workspace floats convt_gemm needs beside the unfold for the K split it will choose.
+int64_t convt_split_ws_floats(int B, int Cin, int Cout, int K, int stride, int pad, int64_t Lout);
 // Few output channels (k 8, stride 4, Cout 1, 2 or 4): registers per column, no unfold.
 bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int groups);
 void convt_small(const LaunchCtx& c, const ConvTArgs& a);

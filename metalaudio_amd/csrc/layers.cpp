@@ -1033,7 +1033,10 @@ class ConvTranspose1DLayer : public Layer {
     } else if (gemm_) {
       unfold_.reserve(sizeof(float) * k::convt_unfold_floats(B, d_.in_channels, d_.kernel_size,
                                                               d_.stride, d_.padding, a.Lout));
-      k::convt_gemm(ctx(s), a, wpack_.f32(), unfold_.f32());
+      const int64_t wsf = k::convt_split_ws_floats(B, d_.in_channels, d_.out_channels,
+                                                   d_.kernel_size, d_.stride, d_.padding, a.Lout);
+      if (wsf > 0) split_.reserve(sizeof(float) * wsf);
+      k::convt_gemm(ctx(s), a, wpack_.f32(), unfold_.f32(), wsf > 0 ? split_.f32() : nullptr);
     } else {
       k::convt_direct(ctx(s), a);
     }
@@ -1058,7 +1061,7 @@ class ConvTranspose1DLayer : public Layer {
   Param* w_ = nullptr;
   Param* b_ = nullptr;
   bool small_ = false, gemm_ = false;
-  DevBuf wpack_, unfold_;
+  DevBuf wpack_, unfold_, split_;
 };
 
 // ------------------------------------------------------------------ UNetDecoderBlock

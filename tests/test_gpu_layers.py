@@ -503,6 +503,8 @@ def test_device_lost_and_stream_sync(dev):
 # ----------------------------------------------------------------------------- decoder path
 @pytest.mark.parametrize("cin,cout,k,s,p,op,d,g,L,B", [
     (96, 24, 8, 4, 3, 2, 1, 1, 513, 2),    # decoder-block form (matrix cores, 2 taps per phase)
+    (768, 192, 8, 4, 3, 2, 1, 1, 1344, 1),  # deepest decoder level: K split in 3 + reduce
+    (384, 96, 8, 4, 3, 2, 1, 1, 300, 2),   # K split in 2, batch 2
     (20, 2, 8, 4, 3, 2, 1, 1, 1000, 1),    # 2 output channels: register kernel
     (24, 1, 8, 4, 3, 2, 1, 1, 777, 2),     # 1 output channel, batch 2
     (40, 4, 8, 4, 3, 0, 1, 1, 300, 1),     # 4 output channels, no output padding
