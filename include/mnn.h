@@ -48,7 +48,12 @@ typedef enum mnn_status {
   MNN_ERR_EMPTY_MODEL = 9,             /* SequentialModelError.emptyModel */
   MNN_ERR_INPUT_SHAPE_MISMATCH = 10,   /* SequentialModelError.inputShapeMismatch */
   MNN_ERR_NOT_BUILT = 11,              /* "Model not built. Call build() first." (Model.swift:226-228) */
-  MNN_ERR_INVALID_ARGUMENT = 12        /* NULL handle, bad rank, unknown weight name */
+  MNN_ERR_INVALID_ARGUMENT = 12,       /* NULL handle, bad rank, unknown weight name */
+  /* SafeTensorsLoader.LoaderError (SafeTensorsLoader.swift:95-128) */
+  MNN_ERR_FILE_NOT_FOUND = 13,         /* fileNotFound */
+  MNN_ERR_INVALID_FILE = 14,           /* headerTooLarge, invalidHeaderJSON, invalidUTF8Header,
+                                          offsetOutOfBounds, dataTruncated */
+  MNN_ERR_TENSOR_NOT_FOUND = 15        /* tensorNotFound */
 } mnn_status;
 
 typedef enum mnn_dtype { MNN_F32 = 0, MNN_BF16 = 1 } mnn_dtype;
@@ -223,6 +228,35 @@ mnn_status mnn_unet_padding(int64_t input_length, int levels, int kernel_size, i
                             int64_t* left_pad, int64_t* right_pad, int64_t* output_length);
 mnn_status mnn_unet_bottleneck_length(int64_t input_length, int levels, int stride,
                                       int64_t* length);
+
+/* ---------------------------------------------------------------- weight files
+ * SafeTensorsLoader (SafeTensorsLoader.swift:41-660): 8-byte little-endian header length, JSON
+ * header, raw data. Entries with a malformed description or an unknown dtype are skipped (as the
+ * reference). Reads convert to fp32 (F32, F16, BF16, I32, I64, I16, I8, U8, BOOL) and reject
+ * NaN / Inf with MNN_ERR_INVALID_CONFIGURATION. Host-only; one handle is not safe for concurrent
+ * reads. */
+typedef struct mnn_safetensors_s* mnn_safetensors;
+typedef enum mnn_st_dtype {
+  MNN_ST_F32 = 0, MNN_ST_F16 = 1, MNN_ST_BF16 = 2, MNN_ST_I32 = 3, MNN_ST_I64 = 4,
+  MNN_ST_I16 = 5, MNN_ST_I8 = 6, MNN_ST_U8 = 7, MNN_ST_BOOL = 8
+} mnn_st_dtype;
+mnn_status mnn_safetensors_open(const char* path, mnn_safetensors* out);
+mnn_status mnn_safetensors_close(mnn_safetensors st);
+/* availableTensors: the names in sorted order. */
+mnn_status mnn_safetensors_tensor_count(mnn_safetensors st, int* count);
+mnn_status mnn_safetensors_tensor_name(mnn_safetensors st, int index, char* buf, size_t cap);
+/* tensorInfo(name:): dtype, shape (rank <= MNN_MAX_RANK) and the element count of its bytes. */
+mnn_status mnn_safetensors_tensor_info(mnn_safetensors st, const char* name, mnn_st_dtype* dtype,
+                                       int* rank, int64_t* dims, size_t* count);
+/* loadTensor(name:) into `out` (count must equal the tensor's element count). */
+mnn_status mnn_safetensors_read_f32(mnn_safetensors st, const char* name, float* out,
+                                    size_t count);
+/* __metadata__[key] (MNN_ERR_TENSOR_NOT_FOUND when absent). */
+mnn_status mnn_safetensors_metadata(mnn_safetensors st, const char* key, char* buf, size_t cap);
+/* loadTensor(name:into:) for a layer parameter: reads `tensor_name` and loads it as the layer's
+ * parameter `param_name` (mnn_layer_load_weights semantics). */
+mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
+                                      const char* tensor_name, const char* param_name);
 
 /* Pre-norm transformer layer on one sequence (TransformerLayer sub-blocks 1 and 5,
  * Transformer.swift:467-495): y = x + ls1*MHA(LN1 x); z = y + ls2*FFN(LN2 y).

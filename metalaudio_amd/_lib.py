@@ -26,6 +26,9 @@ STATUS = {
     10: "MNN_ERR_INPUT_SHAPE_MISMATCH",
     11: "MNN_ERR_NOT_BUILT",
     12: "MNN_ERR_INVALID_ARGUMENT",
+    13: "MNN_ERR_FILE_NOT_FOUND",
+    14: "MNN_ERR_INVALID_FILE",
+    15: "MNN_ERR_TENSOR_NOT_FOUND",
 }
 
 ACT = {"none": 0, "relu": 1, "leaky_relu": 2, "gelu": 3, "swish": 4, "sigmoid": 5, "tanh": 6}
@@ -121,6 +124,15 @@ SIGNATURES = {
     "mnn_transformer_layer_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
     "mnn_cross_transformer_create": (
         C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
+    "mnn_safetensors_open": (C.c_int, [C.c_char_p, PP]),
+    "mnn_safetensors_close": (C.c_int, [P]),
+    "mnn_safetensors_tensor_count": (C.c_int, [P, IP]),
+    "mnn_safetensors_tensor_name": (C.c_int, [P, C.c_int, C.c_char_p, C.c_size_t]),
+    "mnn_safetensors_tensor_info": (
+        C.c_int, [P, C.c_char_p, IP, IP, I64P, C.POINTER(C.c_size_t)]),
+    "mnn_safetensors_read_f32": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
+    "mnn_safetensors_metadata": (C.c_int, [P, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "mnn_layer_load_safetensors": (C.c_int, [P, P, C.c_char_p, C.c_char_p]),
     "mnn_layer_destroy": (C.c_int, [P]),
     "mnn_layer_load_weights": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
     "mnn_layer_forward": (C.c_int, [P, P, P, P]),

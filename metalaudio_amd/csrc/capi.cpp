@@ -1,8 +1,10 @@
 // extern "C" entry points of mnn.h: argument checks, exception -> status translation.
 #include <cstdio>
+#include <cstring>
 #include <thread>
 
 #include "layers.hpp"
+#include "safetensors.hpp"
 
 using namespace mnn;
 
@@ -11,6 +13,7 @@ struct mnn_stream_s {};
 struct mnn_tensor_s {};
 struct mnn_layer_s {};
 struct mnn_sequential_s {};
+struct mnn_safetensors_s {};
 
 namespace {
 
@@ -106,6 +109,9 @@ const char* mnn_status_string(mnn_status s) {
     case MNN_ERR_INPUT_SHAPE_MISMATCH: return "input shape mismatch";
     case MNN_ERR_NOT_BUILT: return "model not built";
     case MNN_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MNN_ERR_FILE_NOT_FOUND: return "file not found";
+    case MNN_ERR_INVALID_FILE: return "invalid file";
+    case MNN_ERR_TENSOR_NOT_FOUND: return "tensor not found";
   }
   return "unknown status";
 }
@@ -449,6 +455,89 @@ mnn_status mnn_unet_bottleneck_length(int64_t input_length, int levels, int stri
     *length = l;
   });
 }
+// ------------------------------------------------------------------ SafeTensors
+namespace {
+SafeTensorsFile* ST(mnn_safetensors s) {
+  MNN_REQUIRE(s, MNN_ERR_INVALID_ARGUMENT, "null safetensors handle");
+  return reinterpret_cast<SafeTensorsFile*>(s);
+}
+void put_string(const std::string& v, char* buf, size_t cap) {
+  MNN_REQUIRE(buf && cap > v.size(), MNN_ERR_BUFFER_SIZE_MISMATCH,
+              "buffer of " << cap << " bytes is too small for " << v.size() + 1);
+  std::memcpy(buf, v.c_str(), v.size() + 1);
+}
+}  // namespace
+
+mnn_status mnn_safetensors_open(const char* path, mnn_safetensors* out) {
+  return guard([&] {
+    MNN_REQUIRE(path && out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *out = reinterpret_cast<mnn_safetensors>(new SafeTensorsFile(path));
+  });
+}
+mnn_status mnn_safetensors_close(mnn_safetensors st) {
+  return guard([&] { delete reinterpret_cast<SafeTensorsFile*>(st); });
+}
+mnn_status mnn_safetensors_tensor_count(mnn_safetensors st, int* count) {
+  return guard([&] {
+    MNN_REQUIRE(count, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *count = (int)ST(st)->names().size();
+  });
+}
+mnn_status mnn_safetensors_tensor_name(mnn_safetensors st, int index, char* buf, size_t cap) {
+  return guard([&] {
+    const auto& n = ST(st)->names();
+    MNN_REQUIRE(index >= 0 && index < (int)n.size(), MNN_ERR_INVALID_ARGUMENT,
+                "tensor index " << index << " out of range");
+    put_string(n[index], buf, cap);
+  });
+}
+mnn_status mnn_safetensors_tensor_info(mnn_safetensors st, const char* name, mnn_st_dtype* dtype,
+                                       int* rank, int64_t* dims, size_t* count) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const StTensorInfo& ti = ST(st)->info(name);
+    MNN_REQUIRE((int)ti.shape.size() <= MNN_MAX_RANK, MNN_ERR_INVALID_ARGUMENT,
+                "tensor rank " << ti.shape.size() << " exceeds " << MNN_MAX_RANK);
+    if (dtype) *dtype = (mnn_st_dtype)ti.dtype;
+    if (rank) *rank = (int)ti.shape.size();
+    if (dims)
+      for (size_t i = 0; i < ti.shape.size(); ++i) dims[i] = ti.shape[i];
+    if (count) *count = ti.end >= ti.begin ? (size_t)ti.count() : 0;
+  });
+}
+mnn_status mnn_safetensors_read_f32(mnn_safetensors st, const char* name, float* out,
+                                    size_t count) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    ST(st)->read_f32(name, out, count);
+  });
+}
+mnn_status mnn_safetensors_metadata(mnn_safetensors st, const char* key, char* buf, size_t cap) {
+  return guard([&] {
+    MNN_REQUIRE(key, MNN_ERR_INVALID_ARGUMENT, "null key");
+    const auto& m = ST(st)->metadata();
+    auto it = m.find(key);
+    MNN_REQUIRE(it != m.end(), MNN_ERR_TENSOR_NOT_FOUND, "metadata key '" << key << "' absent");
+    put_string(it->second, buf, cap);
+  });
+}
+mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
+                                      const char* tensor_name, const char* param_name) {
+  return guard([&] {
+    Layer* l = L(layer);
+    SafeTensorsFile* f = ST(st);
+    MNN_REQUIRE(tensor_name && param_name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const StTensorInfo& ti = f->info(tensor_name);
+    MNN_REQUIRE(ti.end >= ti.begin, MNN_ERR_INVALID_FILE,
+                "Tensor '" << tensor_name << "' has a negative byte range");
+    std::vector<float> host((size_t)ti.count());
+    f->read_f32(tensor_name, host.data(), host.size());
+    l->device()->check_alive();
+    l->device()->make_current();
+    l->load(param_name, host.data(), host.size());
+  });
+}
+
 mnn_status mnn_transformer_layer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,
                                         float layer_scale, mnn_precision prec, mnn_layer* out) {
   MNN_CREATE(make_transformer_layer(d, embed_dim, num_heads, ffn_dim, layer_scale, prec));

@@ -21,7 +21,7 @@ __all__ = [
     "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
     "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
     "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
-    "CrossTransformerEncoder", "Sequential", "mfma_probe",
+    "CrossTransformerEncoder", "Sequential", "SafeTensors", "mfma_probe",
 ]
 
 
@@ -433,6 +433,66 @@ def unet_bottleneck_length(input_length: int, levels: int, stride: int = 4) -> i
     out = C.c_int64()
     check(lib().mnn_unet_bottleneck_length(input_length, levels, stride, C.byref(out)))
     return out.value
+
+
+ST_DTYPES = ["F32", "F16", "BF16", "I32", "I64", "I16", "I8", "U8", "BOOL"]
+
+
+class SafeTensors:
+    """SafeTensorsLoader (SafeTensorsLoader.swift:41-660) over the C ABI: tensor names, shapes,
+    fp32 reads (F32/F16/BF16/integer/bool converted) and loads into layer parameters."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().mnn_safetensors_open(str(path).encode(), C.byref(h)))
+        self.handle = h
+
+    @property
+    def available_tensors(self) -> list[str]:
+        n = C.c_int()
+        check(lib().mnn_safetensors_tensor_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            buf = C.create_string_buffer(4096)
+            check(lib().mnn_safetensors_tensor_name(self.handle, i, buf, len(buf)))
+            out.append(buf.value.decode())
+        return out
+
+    def tensor_info(self, name: str) -> tuple[str, tuple[int, ...], int]:
+        """(dtype, shape, element count of its bytes)."""
+        dt, rank, cnt = C.c_int(), C.c_int(), C.c_size_t()
+        d = dims(())
+        check(lib().mnn_safetensors_tensor_info(self.handle, name.encode(), C.byref(dt),
+                                                C.byref(rank), d, C.byref(cnt)))
+        return ST_DTYPES[dt.value], tuple(d[i] for i in range(rank.value)), cnt.value
+
+    def load_tensor(self, name: str) -> np.ndarray:
+        """loadTensor(name:) as fp32, shaped."""
+        _, shape, count = self.tensor_info(name)
+        out = np.empty(count, np.float32)
+        check(lib().mnn_safetensors_read_f32(self.handle, name.encode(),
+                                             out.ctypes.data_as(C.POINTER(C.c_float)), count))
+        return out.reshape(shape) if int(np.prod(shape, dtype=np.int64)) == count else out
+
+    def metadata(self, key: str) -> str:
+        buf = C.create_string_buffer(1 << 16)
+        check(lib().mnn_safetensors_metadata(self.handle, key.encode(), buf, len(buf)))
+        return buf.value.decode()
+
+    def load_into(self, layer: "Layer", tensor_name: str, param_name: str) -> None:
+        check(lib().mnn_layer_load_safetensors(layer.handle, self.handle, tensor_name.encode(),
+                                               param_name.encode()))
+
+    def close(self) -> None:
+        if self.handle:
+            lib().mnn_safetensors_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class TransformerLayer(Layer):

@@ -608,3 +608,32 @@ def test_time_unet_parity(dev, stream):
     ref = oracle.time_unet(x, enc_p, dec_p)
     assert y.shape == ref.shape == (1, 2, L)
     assert_close(y.to_numpy(), ref, ATOL, RTOL, "time U-Net")
+
+
+def test_layer_weights_from_safetensors(dev, stream, tmp_path):
+    """A rewrite encoder block loaded from a SafeTensors file (F32 and F16 entries) matches the
+    oracle on the file's values (SafeTensorsLoader.loadTensor(name:into:))."""
+    from safetensors.numpy import save_file
+    say("encoder block weights from safetensors")
+    cin, cout, L = 2, 16, 999
+    w = {"enc.0.conv.weight": (RNG.standard_normal((cout, cin, 8)) * 0.3).astype(np.float32),
+         "enc.0.conv.bias": (RNG.standard_normal(cout) * 0.1).astype(np.float32),
+         "enc.0.norm.weight": (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float16),
+         "enc.0.norm.bias": (0.1 * RNG.standard_normal(cout)).astype(np.float16),
+         "enc.0.rewrite.weight": (RNG.standard_normal((2 * cout, cout, 1)) * 0.3).astype(np.float32),
+         "enc.0.rewrite.bias": (RNG.standard_normal(2 * cout) * 0.1).astype(np.float32)}
+    save_file(w, str(tmp_path / "enc.safetensors"))
+    st = nn.SafeTensors(tmp_path / "enc.safetensors")
+    blk = nn.UNetEncoderBlock(dev, cin, cout, 8, 4, 1, rewrite=True)
+    for k in w:
+        st.load_into(blk, k, k[len("enc.0."):])
+    x = RNG.uniform(-1, 1, (1, cin, L)).astype(np.float32)
+    got = run_layer(blk, x, dev, stream)
+    f = {k: v.astype(np.float32) for k, v in w.items()}
+    ref = oracle.encoder_block(x, f["enc.0.conv.weight"], f["enc.0.conv.bias"],
+                               f["enc.0.norm.weight"], f["enc.0.norm.bias"], 1,
+                               rewrite_w=f["enc.0.rewrite.weight"],
+                               rewrite_b=f["enc.0.rewrite.bias"])
+    assert_close(got, ref, ATOL, RTOL, "encoder block from safetensors")
+    with pytest.raises(nn.MNNError):
+        st.load_into(blk, "enc.0.conv.bias", "conv.weight")  # wrong element count
