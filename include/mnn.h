@@ -258,6 +258,25 @@ mnn_status mnn_safetensors_metadata(mnn_safetensors st, const char* key, char* b
 mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
                                       const char* tensor_name, const char* param_name);
 
+/* "MTLA" binary model files (BinaryModelLoader, Model.swift:401-679): reader (v2 with CRC-32
+ * check, legacy v1) and writer (v2, tensors in name order). fp32 tensors, host-only. */
+typedef struct mnn_mtla_s* mnn_mtla;
+typedef struct mnn_mtla_writer_s* mnn_mtla_writer;
+mnn_status mnn_mtla_open(const char* path, mnn_mtla* out);
+mnn_status mnn_mtla_close(mnn_mtla m);
+mnn_status mnn_mtla_tensor_count(mnn_mtla m, int* count);
+mnn_status mnn_mtla_tensor_name(mnn_mtla m, int index, char* buf, size_t cap);
+mnn_status mnn_mtla_tensor_info(mnn_mtla m, const char* name, int* rank, int64_t* dims,
+                                size_t* count);
+mnn_status mnn_mtla_read_f32(mnn_mtla m, const char* name, float* out, size_t count);
+mnn_status mnn_layer_load_mtla(mnn_layer layer, mnn_mtla m, const char* tensor_name,
+                               const char* param_name);
+mnn_status mnn_mtla_writer_create(mnn_mtla_writer* out);
+mnn_status mnn_mtla_writer_add(mnn_mtla_writer w, const char* name, int rank, const int64_t* dims,
+                               const float* data);
+mnn_status mnn_mtla_writer_save(mnn_mtla_writer w, const char* path);
+mnn_status mnn_mtla_writer_destroy(mnn_mtla_writer w);
+
 /* Pre-norm transformer layer on one sequence (TransformerLayer sub-blocks 1 and 5,
  * Transformer.swift:467-495): y = x + ls1*MHA(LN1 x); z = y + ls2*FFN(LN2 y).
  * layer_scale <= 0 disables LayerScale. Weights "norm1.*", "self_attn.*", "norm2.*",

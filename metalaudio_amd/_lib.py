@@ -133,6 +133,17 @@ SIGNATURES = {
     "mnn_safetensors_read_f32": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
     "mnn_safetensors_metadata": (C.c_int, [P, C.c_char_p, C.c_char_p, C.c_size_t]),
     "mnn_layer_load_safetensors": (C.c_int, [P, P, C.c_char_p, C.c_char_p]),
+    "mnn_mtla_open": (C.c_int, [C.c_char_p, PP]),
+    "mnn_mtla_close": (C.c_int, [P]),
+    "mnn_mtla_tensor_count": (C.c_int, [P, IP]),
+    "mnn_mtla_tensor_name": (C.c_int, [P, C.c_int, C.c_char_p, C.c_size_t]),
+    "mnn_mtla_tensor_info": (C.c_int, [P, C.c_char_p, IP, I64P, C.POINTER(C.c_size_t)]),
+    "mnn_mtla_read_f32": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
+    "mnn_layer_load_mtla": (C.c_int, [P, P, C.c_char_p, C.c_char_p]),
+    "mnn_mtla_writer_create": (C.c_int, [PP]),
+    "mnn_mtla_writer_add": (C.c_int, [P, C.c_char_p, C.c_int, I64P, FP]),
+    "mnn_mtla_writer_save": (C.c_int, [P, C.c_char_p]),
+    "mnn_mtla_writer_destroy": (C.c_int, [P]),
     "mnn_layer_destroy": (C.c_int, [P]),
     "mnn_layer_load_weights": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
     "mnn_layer_forward": (C.c_int, [P, P, P, P]),

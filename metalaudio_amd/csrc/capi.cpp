@@ -1,4 +1,5 @@
 // extern "C" entry points of mnn.h: argument checks, exception -> status translation.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <thread>
@@ -14,6 +15,8 @@ struct mnn_tensor_s {};
 struct mnn_layer_s {};
 struct mnn_sequential_s {};
 struct mnn_safetensors_s {};
+struct mnn_mtla_s {};
+struct mnn_mtla_writer_s {};
 
 namespace {
 
@@ -536,6 +539,108 @@ mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
     l->device()->make_current();
     l->load(param_name, host.data(), host.size());
   });
+}
+
+// ------------------------------------------------------------------ MTLA
+namespace {
+MtlaFile* MT(mnn_mtla m) {
+  MNN_REQUIRE(m, MNN_ERR_INVALID_ARGUMENT, "null model-file handle");
+  return reinterpret_cast<MtlaFile*>(m);
+}
+using MtlaTensors = std::map<std::string, std::pair<std::vector<int64_t>, std::vector<float>>>;
+MtlaTensors* MW(mnn_mtla_writer w) {
+  MNN_REQUIRE(w, MNN_ERR_INVALID_ARGUMENT, "null writer handle");
+  return reinterpret_cast<MtlaTensors*>(w);
+}
+}  // namespace
+
+mnn_status mnn_mtla_open(const char* path, mnn_mtla* out) {
+  return guard([&] {
+    MNN_REQUIRE(path && out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *out = reinterpret_cast<mnn_mtla>(new MtlaFile(path));
+  });
+}
+mnn_status mnn_mtla_close(mnn_mtla m) {
+  return guard([&] { delete reinterpret_cast<MtlaFile*>(m); });
+}
+mnn_status mnn_mtla_tensor_count(mnn_mtla m, int* count) {
+  return guard([&] {
+    MNN_REQUIRE(count, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *count = (int)MT(m)->names().size();
+  });
+}
+mnn_status mnn_mtla_tensor_name(mnn_mtla m, int index, char* buf, size_t cap) {
+  return guard([&] {
+    const auto& n = MT(m)->names();
+    MNN_REQUIRE(index >= 0 && index < (int)n.size(), MNN_ERR_INVALID_ARGUMENT,
+                "tensor index " << index << " out of range");
+    put_string(n[index], buf, cap);
+  });
+}
+mnn_status mnn_mtla_tensor_info(mnn_mtla m, const char* name, int* rank, int64_t* dims,
+                                size_t* count) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const auto& sh = MT(m)->shape(name);
+    MNN_REQUIRE((int)sh.size() <= MNN_MAX_RANK, MNN_ERR_INVALID_ARGUMENT,
+                "tensor rank " << sh.size() << " exceeds " << MNN_MAX_RANK);
+    if (rank) *rank = (int)sh.size();
+    if (dims)
+      for (size_t i = 0; i < sh.size(); ++i) dims[i] = sh[i];
+    if (count) *count = MT(m)->data(name).size();
+  });
+}
+mnn_status mnn_mtla_read_f32(mnn_mtla m, const char* name, float* out, size_t count) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const auto& v = MT(m)->data(name);
+    MNN_REQUIRE(v.size() == count, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "Tensor '" << name << "' holds " << v.size() << " values, the destination "
+                           << count);
+    MNN_REQUIRE(out || count == 0, MNN_ERR_INVALID_ARGUMENT, "null destination");
+    std::copy(v.begin(), v.end(), out);
+  });
+}
+mnn_status mnn_layer_load_mtla(mnn_layer layer, mnn_mtla m, const char* tensor_name,
+                               const char* param_name) {
+  return guard([&] {
+    Layer* l = L(layer);
+    MNN_REQUIRE(tensor_name && param_name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const auto& v = MT(m)->data(tensor_name);
+    l->device()->check_alive();
+    l->device()->make_current();
+    l->load(param_name, v.data(), v.size());
+  });
+}
+mnn_status mnn_mtla_writer_create(mnn_mtla_writer* out) {
+  return guard([&] {
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *out = reinterpret_cast<mnn_mtla_writer>(new MtlaTensors());
+  });
+}
+mnn_status mnn_mtla_writer_add(mnn_mtla_writer w, const char* name, int rank, const int64_t* dims,
+                               const float* data) {
+  return guard([&] {
+    MNN_REQUIRE(name && rank >= 0 && rank <= 16 && (rank == 0 || dims), MNN_ERR_INVALID_ARGUMENT,
+                "invalid tensor description");
+    std::vector<int64_t> sh(dims, dims + rank);
+    int64_t n = 1;
+    for (int64_t d : sh) {
+      MNN_REQUIRE(d >= 0 && d <= UINT32_MAX, MNN_ERR_INVALID_ARGUMENT, "bad dimension");
+      n *= d;
+    }
+    MNN_REQUIRE(data || n == 0, MNN_ERR_INVALID_ARGUMENT, "null data");
+    (*MW(w))[name] = {std::move(sh), std::vector<float>(data, data + n)};
+  });
+}
+mnn_status mnn_mtla_writer_save(mnn_mtla_writer w, const char* path) {
+  return guard([&] {
+    MNN_REQUIRE(path, MNN_ERR_INVALID_ARGUMENT, "null path");
+    mtla_write(path, *MW(w));
+  });
+}
+mnn_status mnn_mtla_writer_destroy(mnn_mtla_writer w) {
+  return guard([&] { delete reinterpret_cast<MtlaTensors*>(w); });
 }
 
 mnn_status mnn_transformer_layer_create(mnn_device dev, int embed_dim, int num_heads, int ffn_dim,

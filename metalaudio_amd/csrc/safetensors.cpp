@@ -440,3 +440,153 @@ void SafeTensorsFile::read_f32(const std::string& name, float* out, size_t count
 }
 
 }  // namespace mnn
+
+// ------------------------------------------------------------------ MTLA
+namespace mnn {
+
+uint32_t crc32_ieee(const unsigned char* p, size_t n, uint32_t crc) {
+  static const auto table = [] {
+    std::vector<uint32_t> t(256);
+    for (uint32_t i = 0; i < 256; ++i) {
+      uint32_t c = i;
+      for (int k = 0; k < 8; ++k) c = (c & 1) ? (c >> 1) ^ 0xEDB88320u : (c >> 1);
+      t[i] = c;
+    }
+    return t;
+  }();
+  crc = ~crc;
+  for (size_t i = 0; i < n; ++i) crc = table[(crc ^ p[i]) & 0xFF] ^ (crc >> 8);
+  return ~crc;
+}
+
+MtlaFile::MtlaFile(const std::string& path) {
+  FILE* f = std::fopen(path.c_str(), "rb");
+  MNN_REQUIRE(f, MNN_ERR_FILE_NOT_FOUND, "model file not found at: " << path);
+  std::vector<unsigned char> d;
+  {
+    std::unique_ptr<FILE, int (*)(FILE*)> guard(f, &std::fclose);
+    MNN_REQUIRE(std::fseek(f, 0, SEEK_END) == 0, MNN_ERR_INVALID_FILE, "cannot seek " << path);
+    const long n = std::ftell(f);
+    MNN_REQUIRE(n >= 0, MNN_ERR_INVALID_FILE, "cannot size " << path);
+    std::rewind(f);
+    d.resize((size_t)n);
+    MNN_REQUIRE(d.empty() || std::fread(d.data(), 1, d.size(), f) == d.size(),
+                MNN_ERR_INVALID_FILE, "cannot read " << path);
+  }
+  size_t off = 0;
+  auto need = [&](size_t n) {
+    MNN_REQUIRE(n <= d.size() && off <= d.size() - n, MNN_ERR_INVALID_FILE,
+                "Unexpected end of file at offset " << off << ": needed " << n
+                                                    << " bytes, file size is " << d.size());
+    const size_t at = off;
+    off += n;
+    return at;
+  };
+  auto u32 = [&] { return load_le<uint32_t>(d.data() + need(4)); };
+  MNN_REQUIRE(d.size() >= 16, MNN_ERR_INVALID_FILE,
+              "File too small: expected at least 16 bytes, got " << d.size());
+  const uint32_t magic = u32();
+  MNN_REQUIRE(magic == kMagic, MNN_ERR_INVALID_FILE, "Invalid magic number: 0x" << std::hex
+                                                                              << magic);
+  const uint32_t version = u32();
+  MNN_REQUIRE(version == 1 || version == 2, MNN_ERR_INVALID_FILE,
+              "Unsupported version " << version << ", only version 2 is supported");
+  const uint32_t count = u32();
+  if (version == 1) {
+    (void)u32();  // reserved
+  } else {
+    MNN_REQUIRE(d.size() >= 20, MNN_ERR_INVALID_FILE,
+                "File too small: expected at least 20 bytes, got " << d.size());
+    const uint32_t stored = u32();
+    (void)u32();  // reserved
+    const uint32_t actual = crc32_ieee(d.data() + 20, d.size() - 20);
+    MNN_REQUIRE(stored == actual, MNN_ERR_INVALID_FILE,
+                "Checksum mismatch: expected 0x" << std::hex << stored << ", got 0x" << actual);
+  }
+  for (uint32_t k = 0; k < count; ++k) {
+    const uint32_t name_len = u32(), rank = u32();
+    (void)u32();  // data type: f32
+    const uint32_t bytes = u32();
+    MNN_REQUIRE(name_len < 1024, MNN_ERR_INVALID_FILE, "Invalid tensor name (too long)");
+    MNN_REQUIRE(rank <= 16, MNN_ERR_INVALID_CONFIGURATION,
+                "tensor has " << rank << " dimensions, maximum 16 allowed");
+    const size_t at = need(name_len);
+    MNN_REQUIRE(valid_utf8(d.data() + at, name_len), MNN_ERR_INVALID_FILE,
+                "Invalid tensor name (not valid UTF-8)");
+    std::string name(reinterpret_cast<const char*>(d.data() + at), name_len);
+    std::vector<int64_t> shape;
+    uint64_t elems = 1;
+    for (uint32_t r = 0; r < rank; ++r) {
+      const uint32_t dim = u32();
+      shape.push_back(dim);
+      MNN_REQUIRE(dim == 0 || elems <= UINT64_MAX / dim, MNN_ERR_INVALID_FILE,
+                  "tensor shape in model file overflows");
+      elems *= dim;
+    }
+    MNN_REQUIRE(elems <= UINT64_MAX / 4 && (uint64_t)bytes == elems * 4, MNN_ERR_INVALID_FILE,
+                "Tensor '" << name << "' declares " << bytes << " bytes but shape requires "
+                           << elems * 4 << " bytes");
+    const size_t dat = need(bytes);
+    std::vector<float> v((size_t)elems);
+    if (bytes) std::memcpy(v.data(), d.data() + dat, bytes);
+    t_[name] = {std::move(shape), std::move(v)};
+  }
+  for (const auto& kv : t_) names_.push_back(kv.first);  // map order: sorted
+}
+
+const std::vector<int64_t>& MtlaFile::shape(const std::string& name) const {
+  auto it = t_.find(name);
+  MNN_REQUIRE(it != t_.end(), MNN_ERR_TENSOR_NOT_FOUND, "Tensor '" << name << "' not found");
+  return it->second.first;
+}
+
+const std::vector<float>& MtlaFile::data(const std::string& name) const {
+  auto it = t_.find(name);
+  MNN_REQUIRE(it != t_.end(), MNN_ERR_TENSOR_NOT_FOUND, "Tensor '" << name << "' not found");
+  return it->second.second;
+}
+
+void mtla_write(const std::string& path,
+                const std::map<std::string, std::pair<std::vector<int64_t>, std::vector<float>>>& t) {
+  std::vector<unsigned char> body;
+  auto put32 = [&](uint32_t v) {
+    unsigned char b[4];
+    std::memcpy(b, &v, 4);
+    body.insert(body.end(), b, b + 4);
+  };
+  for (const auto& kv : t) {  // std::map: name order, as the reference's sorted keys
+    const auto& shape = kv.second.first;
+    const auto& v = kv.second.second;
+    MNN_REQUIRE(kv.first.size() < 1024 && shape.size() <= 16, MNN_ERR_INVALID_ARGUMENT,
+                "tensor '" << kv.first << "': name or rank too large");
+    uint64_t elems = 1;
+    for (int64_t dmn : shape) {
+      MNN_REQUIRE(dmn >= 0 && dmn <= UINT32_MAX, MNN_ERR_INVALID_ARGUMENT, "bad dimension");
+      elems *= (uint64_t)dmn;
+    }
+    MNN_REQUIRE(elems == v.size() && elems * 4 <= UINT32_MAX, MNN_ERR_INVALID_ARGUMENT,
+                "tensor '" << kv.first << "': data does not match its shape");
+    put32((uint32_t)kv.first.size());
+    put32((uint32_t)shape.size());
+    put32(0);
+    put32((uint32_t)(elems * 4));
+    body.insert(body.end(), kv.first.begin(), kv.first.end());
+    for (int64_t dmn : shape) put32((uint32_t)dmn);
+    const auto* p = reinterpret_cast<const unsigned char*>(v.data());
+    body.insert(body.end(), p, p + elems * 4);
+  }
+  std::vector<unsigned char> out;
+  const uint32_t hdr[5] = {MtlaFile::kMagic, 2u, (uint32_t)t.size(),
+                           crc32_ieee(body.data(), body.size()), 0u};
+  const auto* hp = reinterpret_cast<const unsigned char*>(hdr);
+  out.insert(out.end(), hp, hp + sizeof(hdr));
+  out.insert(out.end(), body.begin(), body.end());
+  FILE* f = std::fopen(path.c_str(), "wb");
+  MNN_REQUIRE(f, MNN_ERR_INVALID_ARGUMENT, "cannot write " << path);
+  const size_t wrote = std::fwrite(out.data(), 1, out.size(), f);
+  const int closed = std::fclose(f);
+  MNN_REQUIRE(wrote == out.size() && closed == 0, MNN_ERR_INVALID_ARGUMENT,
+              "write to " << path << " failed");
+}
+
+}  // namespace mnn

@@ -50,3 +50,32 @@ size_t st_dtype_size(StDType t);
 float st_half_to_float(uint16_t h);
 
 }  // namespace mnn
+
+namespace mnn {
+
+// "MTLA" binary model file (BinaryModelLoader, Model.swift:401-679): header magic 0x4D544C41,
+// version (2, or the legacy 1), tensor count, CRC-32 of everything after the header (v2 only),
+// reserved; then per tensor: name length, rank, data type (0 = f32), data bytes (u32 each),
+// UTF-8 name, u32 dims, fp32 data. Read whole, validated like the reference (name < 1024 bytes,
+// rank <= 16, overflow-checked element counts, declared bytes == 4 * elements, bounds).
+class MtlaFile {
+ public:
+  static constexpr uint32_t kMagic = 0x4D544C41u;
+  explicit MtlaFile(const std::string& path);
+  const std::vector<std::string>& names() const { return names_; }
+  const std::vector<int64_t>& shape(const std::string& name) const;
+  const std::vector<float>& data(const std::string& name) const;
+
+ private:
+  std::map<std::string, std::pair<std::vector<int64_t>, std::vector<float>>> t_;
+  std::vector<std::string> names_;
+};
+
+// BinaryModelLoader.save: version 2, tensors in name order, CRC-32 over the entries.
+void mtla_write(const std::string& path,
+                const std::map<std::string, std::pair<std::vector<int64_t>, std::vector<float>>>& t);
+
+// Reflected CRC-32 (polynomial 0xEDB88320), as computeCRC32 (Model.swift:431-449).
+uint32_t crc32_ieee(const unsigned char* p, size_t n, uint32_t crc = 0);
+
+}  // namespace mnn

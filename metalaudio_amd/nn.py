@@ -21,7 +21,7 @@ __all__ = [
     "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
     "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
     "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
-    "CrossTransformerEncoder", "Sequential", "SafeTensors", "mfma_probe",
+    "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "mfma_probe",
 ]
 
 
@@ -486,6 +486,66 @@ class SafeTensors:
     def close(self) -> None:
         if self.handle:
             lib().mnn_safetensors_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class BinaryModelFile:
+    """BinaryModelLoader's "MTLA" files (Model.swift:401-679): read (CRC-32 checked for v2) and
+    load into layer parameters; `save` writes version 2."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().mnn_mtla_open(str(path).encode(), C.byref(h)))
+        self.handle = h
+
+    @property
+    def names(self) -> list[str]:
+        n = C.c_int()
+        check(lib().mnn_mtla_tensor_count(self.handle, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            buf = C.create_string_buffer(1100)
+            check(lib().mnn_mtla_tensor_name(self.handle, i, buf, len(buf)))
+            out.append(buf.value.decode())
+        return out
+
+    def load_tensor(self, name: str) -> np.ndarray:
+        rank, cnt = C.c_int(), C.c_size_t()
+        d = dims(())
+        check(lib().mnn_mtla_tensor_info(self.handle, name.encode(), C.byref(rank), d,
+                                         C.byref(cnt)))
+        out = np.empty(cnt.value, np.float32)
+        check(lib().mnn_mtla_read_f32(self.handle, name.encode(),
+                                      out.ctypes.data_as(C.POINTER(C.c_float)), cnt.value))
+        return out.reshape(tuple(d[i] for i in range(rank.value)))
+
+    def load_into(self, layer: "Layer", tensor_name: str, param_name: str) -> None:
+        check(lib().mnn_layer_load_mtla(layer.handle, self.handle, tensor_name.encode(),
+                                        param_name.encode()))
+
+    @staticmethod
+    def save(tensors: dict, path) -> None:
+        w = C.c_void_p()
+        check(lib().mnn_mtla_writer_create(C.byref(w)))
+        try:
+            for name, arr in tensors.items():
+                a = np.ascontiguousarray(arr, dtype=np.float32)
+                d = (C.c_int64 * max(1, a.ndim))(*a.shape)
+                check(lib().mnn_mtla_writer_add(w, name.encode(), a.ndim, d,
+                                                a.ctypes.data_as(C.POINTER(C.c_float))))
+            check(lib().mnn_mtla_writer_save(w, str(path).encode()))
+        finally:
+            lib().mnn_mtla_writer_destroy(w)
+
+    def close(self) -> None:
+        if self.handle:
+            lib().mnn_mtla_close(self.handle)
             self.handle = None
 
     def __del__(self):

@@ -637,3 +637,30 @@ def test_layer_weights_from_safetensors(dev, stream, tmp_path):
     assert_close(got, ref, ATOL, RTOL, "encoder block from safetensors")
     with pytest.raises(nn.MNNError):
         st.load_into(blk, "enc.0.conv.bias", "conv.weight")  # wrong element count
+
+
+@pytest.mark.gpu
+def test_layer_weights_from_mtla(dev, stream, tmp_path):
+    """A 1x1-GLU encoder block loaded from an "MTLA" model file written by BinaryModelFile.save
+    matches the oracle on the same values (BinaryModelLoader.load, Model.swift:466-622)."""
+    say("encoder block weights from an MTLA file")
+    cin, cout, L = 2, 16, 777
+    w = {"conv.weight": (RNG.standard_normal((cout, cin, 8)) * 0.3).astype(np.float32),
+         "conv.bias": (RNG.standard_normal(cout) * 0.1).astype(np.float32),
+         "norm.weight": (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32),
+         "norm.bias": (0.1 * RNG.standard_normal(cout)).astype(np.float32),
+         "rewrite.weight": (RNG.standard_normal((2 * cout, cout, 1)) * 0.3).astype(np.float32),
+         "rewrite.bias": (RNG.standard_normal(2 * cout) * 0.1).astype(np.float32)}
+    nn.BinaryModelFile.save(w, tmp_path / "enc.bin")
+    m = nn.BinaryModelFile(tmp_path / "enc.bin")
+    blk = nn.UNetEncoderBlock(dev, cin, cout, 8, 4, 1, rewrite=True)
+    for k in m.names:
+        m.load_into(blk, k, k)
+    x = RNG.uniform(-1, 1, (1, cin, L)).astype(np.float32)
+    got = run_layer(blk, x, dev, stream)
+    ref = oracle.encoder_block(x, w["conv.weight"], w["conv.bias"], w["norm.weight"],
+                               w["norm.bias"], 1, rewrite_w=w["rewrite.weight"],
+                               rewrite_b=w["rewrite.bias"])
+    assert_close(got, ref, ATOL, RTOL, "encoder block from MTLA")
+    with pytest.raises(nn.MNNError):
+        m.load_into(blk, "conv.bias", "conv.weight")  # wrong element count
