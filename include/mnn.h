@@ -258,6 +258,30 @@ mnn_status mnn_safetensors_metadata(mnn_safetensors st, const char* key, char* b
 mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
                                       const char* tensor_name, const char* param_name);
 
+/* Weight-name conventions (WeightNameMapper.swift:7-422): MetalAudio names
+ * ("time_encoder.0.conv.weight") and Demucs names ("tencoder.0.conv.weight"). Strings out are
+ * NUL-terminated into buf; MNN_ERR_BUFFER_SIZE_MISMATCH when cap is too small. */
+typedef enum {
+  MNN_NAMES_METALAUDIO = 0,
+  MNN_NAMES_DEMUCS = 1,
+  MNN_NAMES_UNKNOWN = 2
+} mnn_weight_convention;
+/* WeightNameMapper.detectConvention(from:) */
+mnn_status mnn_weight_convention_detect(const char* const* names, int count, int* convention);
+/* SafeTensorsLoader.createWeightMapper(): detection over the file's tensor names */
+mnn_status mnn_safetensors_detect_convention(mnn_safetensors st, int* convention);
+/* toMetalAudio(name:) for a mapper of `convention` */
+mnn_status mnn_weight_name_to_metalaudio(int convention, const char* name, char* buf, size_t cap);
+/* fromMetalAudio(name:to:) */
+mnn_status mnn_weight_name_from_metalaudio(const char* name, int target, char* buf, size_t cap);
+/* isMetalAudioNaming / isDemucsNaming: *out = 0 or 1 */
+mnn_status mnn_weight_name_is_metalaudio(const char* name, int* out);
+mnn_status mnn_weight_name_is_demucs(const char* name, int* out);
+/* loadTensorMapped(metalAudioName:mapper:)'s lookup: the file's own name for the tensor, to pass to
+ * mnn_safetensors_read_f32 / mnn_layer_load_safetensors; MNN_ERR_TENSOR_NOT_FOUND if none. */
+mnn_status mnn_safetensors_find_mapped(mnn_safetensors st, int convention,
+                                       const char* metalaudio_name, char* buf, size_t cap);
+
 /* "MTLA" binary model files (BinaryModelLoader, Model.swift:401-679): reader (v2 with CRC-32
  * check, legacy v1) and writer (v2, tensors in name order). fp32 tensors, host-only. */
 typedef struct mnn_mtla_s* mnn_mtla;

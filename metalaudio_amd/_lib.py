@@ -133,6 +133,13 @@ SIGNATURES = {
     "mnn_safetensors_read_f32": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
     "mnn_safetensors_metadata": (C.c_int, [P, C.c_char_p, C.c_char_p, C.c_size_t]),
     "mnn_layer_load_safetensors": (C.c_int, [P, P, C.c_char_p, C.c_char_p]),
+    "mnn_weight_convention_detect": (C.c_int, [C.POINTER(C.c_char_p), C.c_int, IP]),
+    "mnn_safetensors_detect_convention": (C.c_int, [P, IP]),
+    "mnn_weight_name_to_metalaudio": (C.c_int, [C.c_int, C.c_char_p, C.c_char_p, C.c_size_t]),
+    "mnn_weight_name_from_metalaudio": (C.c_int, [C.c_char_p, C.c_int, C.c_char_p, C.c_size_t]),
+    "mnn_weight_name_is_metalaudio": (C.c_int, [C.c_char_p, IP]),
+    "mnn_weight_name_is_demucs": (C.c_int, [C.c_char_p, IP]),
+    "mnn_safetensors_find_mapped": (C.c_int, [P, C.c_int, C.c_char_p, C.c_char_p, C.c_size_t]),
     "mnn_mtla_open": (C.c_int, [C.c_char_p, PP]),
     "mnn_mtla_close": (C.c_int, [P]),
     "mnn_mtla_tensor_count": (C.c_int, [P, IP]),

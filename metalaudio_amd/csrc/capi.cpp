@@ -6,6 +6,7 @@
 
 #include "layers.hpp"
 #include "safetensors.hpp"
+#include "weight_names.hpp"
 
 using namespace mnn;
 
@@ -538,6 +539,68 @@ mnn_status mnn_layer_load_safetensors(mnn_layer layer, mnn_safetensors st,
     l->device()->check_alive();
     l->device()->make_current();
     l->load(param_name, host.data(), host.size());
+  });
+}
+
+// ------------------------------------------------------------------ weight names
+namespace {
+WeightConvention WCONV(int c) {
+  MNN_REQUIRE(c >= WC_METALAUDIO && c <= WC_UNKNOWN, MNN_ERR_INVALID_ARGUMENT,
+              "unknown naming convention " << c);
+  return static_cast<WeightConvention>(c);
+}
+}  // namespace
+
+mnn_status mnn_weight_convention_detect(const char* const* names, int count, int* convention) {
+  return guard([&] {
+    MNN_REQUIRE(convention && count >= 0 && (names || count == 0), MNN_ERR_INVALID_ARGUMENT,
+                "invalid argument");
+    std::vector<std::string> v;
+    for (int i = 0; i < count; ++i) {
+      MNN_REQUIRE(names[i], MNN_ERR_INVALID_ARGUMENT, "null name at " << i);
+      v.emplace_back(names[i]);
+    }
+    *convention = detect_convention(v);
+  });
+}
+mnn_status mnn_safetensors_detect_convention(mnn_safetensors st, int* convention) {
+  return guard([&] {
+    MNN_REQUIRE(convention, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *convention = detect_convention(ST(st)->names());
+  });
+}
+mnn_status mnn_weight_name_to_metalaudio(int convention, const char* name, char* buf, size_t cap) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    put_string(to_metalaudio(WCONV(convention), name), buf, cap);
+  });
+}
+mnn_status mnn_weight_name_from_metalaudio(const char* name, int target, char* buf, size_t cap) {
+  return guard([&] {
+    MNN_REQUIRE(name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    put_string(from_metalaudio(name, WCONV(target)), buf, cap);
+  });
+}
+mnn_status mnn_weight_name_is_metalaudio(const char* name, int* out) {
+  return guard([&] {
+    MNN_REQUIRE(name && out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *out = is_metalaudio_naming(name) ? 1 : 0;
+  });
+}
+mnn_status mnn_weight_name_is_demucs(const char* name, int* out) {
+  return guard([&] {
+    MNN_REQUIRE(name && out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *out = is_demucs_naming(name) ? 1 : 0;
+  });
+}
+mnn_status mnn_safetensors_find_mapped(mnn_safetensors st, int convention,
+                                       const char* metalaudio_name, char* buf, size_t cap) {
+  return guard([&] {
+    MNN_REQUIRE(metalaudio_name, MNN_ERR_INVALID_ARGUMENT, "null name");
+    const std::string n = find_mapped(ST(st)->names(), WCONV(convention), metalaudio_name);
+    MNN_REQUIRE(!n.empty(), MNN_ERR_TENSOR_NOT_FOUND,
+                "Tensor '" << metalaudio_name << "' not found");
+    put_string(n, buf, cap);
   });
 }
 

@@ -21,7 +21,8 @@ __all__ = [
     "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
     "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
     "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
-    "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "mfma_probe",
+    "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "WeightNameMapper",
+    "mfma_probe",
 ]
 
 
@@ -479,6 +480,20 @@ class SafeTensors:
         check(lib().mnn_safetensors_metadata(self.handle, key.encode(), buf, len(buf)))
         return buf.value.decode()
 
+    def create_weight_mapper(self) -> WeightNameMapper:
+        """createWeightMapper(): the convention detected from this file's tensor names."""
+        out = C.c_int()
+        check(lib().mnn_safetensors_detect_convention(self.handle, C.byref(out)))
+        return WeightNameMapper(_NAMING_BY_CODE[out.value])
+
+    def mapped_name(self, metalaudio_name: str, mapper: WeightNameMapper) -> str:
+        """The file's own name for `metalaudio_name` (loadTensorMapped's lookup)."""
+        return _name_call(lib().mnn_safetensors_find_mapped, self.handle,
+                          NAMING[mapper.convention], metalaudio_name.encode())
+
+    def load_tensor_mapped(self, metalaudio_name: str, mapper: WeightNameMapper) -> np.ndarray:
+        return self.load_tensor(self.mapped_name(metalaudio_name, mapper))
+
     def load_into(self, layer: "Layer", tensor_name: str, param_name: str) -> None:
         check(lib().mnn_layer_load_safetensors(layer.handle, self.handle, tensor_name.encode(),
                                                param_name.encode()))
@@ -493,6 +508,64 @@ class SafeTensors:
             self.close()
         except Exception:
             pass
+
+
+NAMING = {"metalaudio": 0, "demucs": 1, "unknown": 2}
+_NAMING_BY_CODE = {v: k for k, v in NAMING.items()}
+
+
+def _name_call(fn, *args) -> str:
+    buf = C.create_string_buffer(4096)
+    check(fn(*args, buf, len(buf)))
+    return buf.value.decode()
+
+
+class WeightNameMapper:
+    """WeightNameMapper (WeightNameMapper.swift:7-422): conventions "metalaudio", "demucs" or
+    "unknown"; built from a convention or detected from tensor names."""
+
+    def __init__(self, convention: str | None = None, tensor_names: Iterable[str] | None = None):
+        if (convention is None) == (tensor_names is None):
+            raise ValueError("give either a convention or tensor names")
+        if tensor_names is not None:
+            convention = self.detect_convention(tensor_names)
+        if convention not in NAMING:
+            raise ValueError(f"unknown naming convention {convention!r}")
+        self.convention = convention
+
+    @staticmethod
+    def detect_convention(names: Iterable[str]) -> str:
+        enc = [n.encode() for n in names]
+        arr = (C.c_char_p * max(1, len(enc)))(*enc)
+        out = C.c_int()
+        check(lib().mnn_weight_convention_detect(arr, len(enc), C.byref(out)))
+        return _NAMING_BY_CODE[out.value]
+
+    def to_metalaudio(self, name: str) -> str:
+        return _name_call(lib().mnn_weight_name_to_metalaudio, NAMING[self.convention],
+                          name.encode())
+
+    @staticmethod
+    def from_metalaudio(name: str, target: str) -> str:
+        return _name_call(lib().mnn_weight_name_from_metalaudio, name.encode(), NAMING[target])
+
+    def map_all_to_metalaudio(self, weights: dict) -> dict:
+        return {self.to_metalaudio(k): v for k, v in weights.items()}
+
+    def generate_mapping(self, names: Iterable[str]) -> dict:
+        return {n: self.to_metalaudio(n) for n in names}
+
+    @staticmethod
+    def is_metalaudio_naming(name: str) -> bool:
+        out = C.c_int()
+        check(lib().mnn_weight_name_is_metalaudio(name.encode(), C.byref(out)))
+        return bool(out.value)
+
+    @staticmethod
+    def is_demucs_naming(name: str) -> bool:
+        out = C.c_int()
+        check(lib().mnn_weight_name_is_demucs(name.encode(), C.byref(out)))
+        return bool(out.value)
 
 
 class BinaryModelFile:
