@@ -221,6 +221,54 @@ typedef struct mnn_decoder_block_desc {
 mnn_status mnn_decoder_block_create(mnn_device dev, const mnn_decoder_block_desc* desc,
                                     mnn_layer* out);
 
+/* ---------------------------------------------------------------- frequency branch (2-D) */
+typedef struct mnn_conv2d_desc {
+  int in_channels, out_channels, kernel_h, kernel_w, stride_h, stride_w;
+  int padding_mode;     /* mnn_padding_mode */
+  int pad_h, pad_w;     /* used by MNN_PAD_EXPLICIT and MNN_PAD_REFLECT */
+  int dilation_h, dilation_w, groups;
+  int use_bias;
+} mnn_conv2d_desc;
+
+/* DynamicConv2D (DynamicConv2D.swift:37-592). Weights "weight" [out, in/groups, kh, kw], "bias"
+ * [out]. Input [C, H, W] or [B, C, H, W]; output floor((n + 2p - ((k-1)d + 1)) / s) + 1 per
+ * axis, "same" padding total/2 per side (computePadding :212-238). */
+mnn_status mnn_conv2d_create(mnn_device dev, const mnn_conv2d_desc* desc, mnn_layer* out);
+
+typedef struct mnn_conv_transpose2d_desc {
+  int in_channels, out_channels, kernel_h, kernel_w, stride_h, stride_w;
+  int pad_h, pad_w, output_pad_h, output_pad_w, dilation_h, dilation_w, groups;
+  int use_bias;
+} mnn_conv_transpose2d_desc;
+
+/* DynamicConvTranspose2D (DynamicConv2D.swift:598-959). Weights "weight" [in, out/groups, kh, kw],
+ * "bias" [out]; output (n-1)s - 2p + (k-1)d + 1 + output_pad per axis. */
+mnn_status mnn_conv_transpose2d_create(mnn_device dev, const mnn_conv_transpose2d_desc* desc,
+                                       mnn_layer* out);
+
+typedef struct mnn_freq_block_desc {
+  int in_channels, skip_channels, out_channels, kernel_h, kernel_w, stride_h, stride_w;
+  int num_groups;
+} mnn_freq_block_desc;
+
+/* FreqUNetEncoderBlock2D (FreqUNet2D.swift:12-192): Conv2D with reflect padding (k-1)/2 and the
+ * stride -> GroupNorm over [C, H*W] -> GELU. skip_channels must be 0. Weights "conv.weight",
+ * "conv.bias", "norm.weight", "norm.bias". The block's output is also its skip. */
+mnn_status mnn_freq_encoder_block_create(mnn_device dev, const mnn_freq_block_desc* desc,
+                                         mnn_layer* out);
+/* FreqUNetDecoderBlock2D (FreqUNet2D.swift:198-428): concat(input, skip) -> ConvTranspose2D
+ * (padding (k-1)/2, output padding stride-1) -> GroupNorm -> GELU. Weights "conv_tr.weight" (or
+ * "conv_transpose.weight"), "conv_tr.bias", "norm.weight", "norm.bias". Two inputs:
+ * mnn_layer_forward_cross(input, skip, out). */
+mnn_status mnn_freq_decoder_block_create(mnn_device dev, const mnn_freq_block_desc* desc,
+                                         mnn_layer* out);
+/* UNetPaddingCalculator2D (FreqUNet2D.swift:461-513): out = {pad_top, pad_bottom, pad_left,
+ * pad_right, out_height, out_width}; bottleneck = {height, width}. */
+mnn_status mnn_unet_padding_2d(int64_t height, int64_t width, int levels, int stride,
+                               int64_t out[6]);
+mnn_status mnn_unet_bottleneck_2d(int64_t height, int64_t width, int levels, int stride,
+                                  int64_t out[2]);
+
 /* UNetPaddingCalculator (UNet.swift:393-448): left/right zero padding that makes the length a
  * multiple of stride^levels (remainder split evenly, the odd sample on the right), and the length
  * after `levels` downsamplings by `stride`. */

@@ -77,6 +77,25 @@ class DecoderBlockDesc(C.Structure):
     ]
 
 
+class Conv2dDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "in_channels", "out_channels", "kernel_h", "kernel_w", "stride_h", "stride_w",
+        "padding_mode", "pad_h", "pad_w", "dilation_h", "dilation_w", "groups", "use_bias")]
+
+
+class ConvTranspose2dDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "in_channels", "out_channels", "kernel_h", "kernel_w", "stride_h", "stride_w", "pad_h",
+        "pad_w", "output_pad_h", "output_pad_w", "dilation_h", "dilation_w", "groups",
+        "use_bias")]
+
+
+class FreqBlockDesc(C.Structure):
+    _fields_ = [(n, C.c_int) for n in (
+        "in_channels", "skip_channels", "out_channels", "kernel_h", "kernel_w", "stride_h",
+        "stride_w", "num_groups")]
+
+
 P = C.c_void_p
 PP = C.POINTER(C.c_void_p)
 I64P = C.POINTER(C.c_int64)
@@ -121,6 +140,12 @@ SIGNATURES = {
     "mnn_decoder_block_create": (C.c_int, [P, C.POINTER(DecoderBlockDesc), PP]),
     "mnn_unet_padding": (C.c_int, [C.c_int64, C.c_int, C.c_int, C.c_int, I64P, I64P, I64P]),
     "mnn_unet_bottleneck_length": (C.c_int, [C.c_int64, C.c_int, C.c_int, I64P]),
+    "mnn_conv2d_create": (C.c_int, [P, C.POINTER(Conv2dDesc), PP]),
+    "mnn_conv_transpose2d_create": (C.c_int, [P, C.POINTER(ConvTranspose2dDesc), PP]),
+    "mnn_freq_encoder_block_create": (C.c_int, [P, C.POINTER(FreqBlockDesc), PP]),
+    "mnn_freq_decoder_block_create": (C.c_int, [P, C.POINTER(FreqBlockDesc), PP]),
+    "mnn_unet_padding_2d": (C.c_int, [C.c_int64, C.c_int64, C.c_int, C.c_int, I64P]),
+    "mnn_unet_bottleneck_2d": (C.c_int, [C.c_int64, C.c_int64, C.c_int, C.c_int, I64P]),
     "mnn_transformer_layer_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
     "mnn_cross_transformer_create": (
         C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),

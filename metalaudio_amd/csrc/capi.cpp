@@ -429,34 +429,78 @@ mnn_status mnn_decoder_block_create(mnn_device dev, const mnn_decoder_block_desc
                                     mnn_layer* out) {
   MNN_CREATE(make_decoder_block(d, need(desc)));
 }
+mnn_status mnn_conv2d_create(mnn_device dev, const mnn_conv2d_desc* desc, mnn_layer* out) {
+  MNN_CREATE(make_conv2d(d, need(desc)));
+}
+mnn_status mnn_conv_transpose2d_create(mnn_device dev, const mnn_conv_transpose2d_desc* desc,
+                                       mnn_layer* out) {
+  MNN_CREATE(make_conv_transpose2d(d, need(desc)));
+}
+mnn_status mnn_freq_encoder_block_create(mnn_device dev, const mnn_freq_block_desc* desc,
+                                         mnn_layer* out) {
+  MNN_CREATE(make_freq_encoder_block(d, need(desc)));
+}
+mnn_status mnn_freq_decoder_block_create(mnn_device dev, const mnn_freq_block_desc* desc,
+                                         mnn_layer* out) {
+  MNN_CREATE(make_freq_decoder_block(d, need(desc)));
+}
+namespace {
+// Zero padding that makes n a multiple of stride^levels, split total/2 left, rest right.
+void unet_pad(int64_t n, int levels, int stride, int64_t& left, int64_t& right, int64_t& out) {
+  MNN_REQUIRE(n >= 0 && levels >= 0 && stride > 0, MNN_ERR_INVALID_ARGUMENT,
+              "invalid padding query");
+  int64_t divisor = 1;
+  for (int i = 0; i < levels; ++i) {
+    MNN_REQUIRE(divisor <= (INT64_MAX / stride), MNN_ERR_INVALID_ARGUMENT,
+                "stride^levels overflows");
+    divisor *= stride;
+  }
+  const int64_t rem = n % divisor;
+  const int64_t total = rem == 0 ? 0 : divisor - rem;
+  left = total / 2;
+  right = total - total / 2;
+  out = n + total;
+}
+int64_t unet_bottleneck(int64_t n, int levels, int stride) {
+  MNN_REQUIRE(stride > 0 && levels >= 0, MNN_ERR_INVALID_ARGUMENT, "invalid bottleneck query");
+  for (int i = 0; i < levels; ++i) n /= stride;
+  return n;
+}
+}  // namespace
+
 mnn_status mnn_unet_padding(int64_t input_length, int levels, int kernel_size, int stride,
                             int64_t* left_pad, int64_t* right_pad, int64_t* output_length) {
   return guard([&] {
     MNN_REQUIRE(left_pad && right_pad && output_length, MNN_ERR_INVALID_ARGUMENT,
                 "null output pointer");
-    MNN_REQUIRE(input_length >= 0 && levels >= 0 && stride > 0 && kernel_size > 0,
-                MNN_ERR_INVALID_ARGUMENT, "invalid padding query");
-    int64_t divisor = 1;
-    for (int i = 0; i < levels; ++i) {
-      MNN_REQUIRE(divisor <= (INT64_MAX / stride), MNN_ERR_INVALID_ARGUMENT,
-                  "stride^levels overflows");
-      divisor *= stride;
-    }
-    const int64_t rem = input_length % divisor;
-    const int64_t total = rem == 0 ? 0 : divisor - rem;
-    *left_pad = total / 2;
-    *right_pad = total - total / 2;
-    *output_length = input_length + total;
+    MNN_REQUIRE(kernel_size > 0, MNN_ERR_INVALID_ARGUMENT, "invalid padding query");
+    unet_pad(input_length, levels, stride, *left_pad, *right_pad, *output_length);
   });
 }
 mnn_status mnn_unet_bottleneck_length(int64_t input_length, int levels, int stride,
                                       int64_t* length) {
   return guard([&] {
-    MNN_REQUIRE(length && stride > 0 && levels >= 0, MNN_ERR_INVALID_ARGUMENT,
-                "invalid bottleneck query");
-    int64_t l = input_length;
-    for (int i = 0; i < levels; ++i) l /= stride;
-    *length = l;
+    MNN_REQUIRE(length, MNN_ERR_INVALID_ARGUMENT, "invalid bottleneck query");
+    *length = unet_bottleneck(input_length, levels, stride);
+  });
+}
+mnn_status mnn_unet_padding_2d(int64_t height, int64_t width, int levels, int stride,
+                               int64_t out[6]) {
+  return guard([&] {
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output pointer");
+    int64_t o[6];
+    unet_pad(height, levels, stride, o[0], o[1], o[4]);
+    unet_pad(width, levels, stride, o[2], o[3], o[5]);
+    std::copy(o, o + 6, out);
+  });
+}
+mnn_status mnn_unet_bottleneck_2d(int64_t height, int64_t width, int levels, int stride,
+                                  int64_t out[2]) {
+  return guard([&] {
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null output pointer");
+    const int64_t h = unet_bottleneck(height, levels, stride);
+    out[1] = unet_bottleneck(width, levels, stride);
+    out[0] = h;
   });
 }
 // ------------------------------------------------------------------ SafeTensors

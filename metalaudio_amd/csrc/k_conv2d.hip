@@ -1,0 +1,314 @@
+// 2-D convolution and transposed convolution of the frequency branch (DynamicConv2D and
+// DynamicConvTranspose2D, DynamicConv2D.swift:37-959). Layout [B][C][H][W], fp32.
+//
+// Conv2D (dynamic_conv2d_forward, DynamicConv2D.swift:525-590):
+//   y[oc][oh][ow] = bias[oc] + sum_{icg, kh, kw} x[ic][ih][iw] * w[oc][icg][kh][kw],
+//   ih = oh*sh - ph + kh*dh, iw = ow*sw - pw + kw*dw, ic = group(oc)*Cin/G + icg,
+// zero outside the input; with reflect padding the input is first padded by (ph, pw) with
+// mirrored samples (applyReflectPadding2D, :424-475: i < 0 -> -i, i >= n -> 2n - i - 2, then
+// clamped to [0, n)) and the conv runs unpadded on the padded input.
+// Matrix-core form (groups 1): per batch a GEMM Y[oc][(oh, ow)] = W[oc][k] * U[(oh, ow)][k] over
+// k = (icg, kh, kw) (rounded up to 32 with zero columns): conv2d_unfold_kernel writes U (the
+// padding resolved there) and the LDS-DMA GEMM adds the bias per row. 1x1 stride-1 unpadded
+// convs skip the unfold: the input [C][H*W] is the GEMM's [K][N] operand as it is.
+//
+// ConvTranspose2D (dynamic_conv_transpose2d_forward, :890-955): W is [Cin][Cout/G][KH][KW],
+//   y[oc][oh][ow] = bias[oc] + sum x[ic][ih][iw] * W[ic][ocg][kh][kw] over the (ic, kh, kw) with
+//   oh + ph - kh*dh = ih*sh and ow + pw - kw*dw = iw*sw exactly, 0 <= ih < H, 0 <= iw < W.
+// Matrix-core form (groups 1): Z[(oc, kh, kw)][(ih, iw)] = sum_ic W[ic][oc][kh][kw] x[ic][ih][iw]
+// is a GEMM with the input as its [K][N] operand (the decoder's channel concat becomes a second
+// GEMM accumulating into Z), then convt2d_gather_kernel sums the taps that land on each output
+// (KH*KW / (sh*sw) of them on average) and adds the bias. No atomics; fixed summation order.
+#include "device_utils.hpp"
+#include "kernels.hpp"
+
+namespace mnn {
+namespace k {
+
+using namespace dev;
+
+namespace {
+
+__device__ __forceinline__ int reflect_index(int i, int n) {
+  if (i < 0) i = -i;
+  if (i >= n) i = 2 * n - i - 2;
+  return min(max(i, 0), n - 1);
+}
+
+// Input sample for padded-frame coordinates (r, s) relative to the unpadded origin: zero padding
+// reads zero outside, reflect padding mirrors (r, s already shifted by -pad).
+__device__ __forceinline__ float conv2d_sample(const float* xc, int r, int s, int H, int W,
+                                               bool reflect) {
+  if (reflect) return xc[(int64_t)reflect_index(r, H) * W + reflect_index(s, W)];
+  if (r < 0 || r >= H || s < 0 || s >= W) return 0.f;
+  return xc[(int64_t)r * W + s];
+}
+
+// U[b][n][k] for n = oh*Wo + ow, k = (ic, kh, kw) < K, zero for K <= k < Kp; four k per thread
+// (one 16-byte store).
+__global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
+  const int64_t N = (int64_t)a.Ho * a.Wo;
+  const int kq = a.Kp / 4;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= N * kq) return;
+  const int b = blockIdx.y;
+  const int64_t n = e / kq;
+  const int k0 = (int)(e % kq) * 4;
+  const int oh = (int)(n / a.Wo), ow = (int)(n % a.Wo);
+  const int ks = a.KH * a.KW, K = a.Cin * ks;
+  const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
+  float v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int k = k0 + j;
+    v[j] = 0.f;
+    if (k < K) {
+      const int ic = k / ks, kh = (k % ks) / a.KW, kw = k % a.KW;
+      v[j] = conv2d_sample(xb + (int64_t)ic * a.H * a.W, oh * a.sh - a.ph + kh * a.dh,
+                           ow * a.sw - a.pw + kw * a.dw, a.H, a.W, a.reflect);
+    }
+  }
+  *reinterpret_cast<float4*>(a.u + ((int64_t)b * N + n) * a.Kp + k0) =
+      make_float4(v[0], v[1], v[2], v[3]);
+}
+
+__global__ __launch_bounds__(256) void conv2d_direct_kernel(Conv2DArgs a) {
+  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= per_b * a.B) return;
+  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
+  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const int cinpg = a.Cin / a.groups, coutpg = a.Cout / a.groups, g = oc / coutpg;
+  const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
+  float sum = 0.f;
+  for (int icg = 0; icg < cinpg; ++icg) {
+    const float* xc = xb + (int64_t)(g * cinpg + icg) * a.H * a.W;
+    const float* wr = a.w + ((int64_t)oc * cinpg + icg) * a.KH * a.KW;
+    for (int kh = 0; kh < a.KH; ++kh)
+      for (int kw = 0; kw < a.KW; ++kw)
+        sum = fmaf(conv2d_sample(xc, oh * a.sh - a.ph + kh * a.dh, ow * a.sw - a.pw + kw * a.dw,
+                                 a.H, a.W, a.reflect),
+                   wr[kh * a.KW + kw], sum);
+  }
+  if (a.bias) sum += a.bias[oc];
+  a.y[idx] = sum;
+}
+
+// y[b][oc][oh][ow] = bias[oc] + the taps of Z[b][(oc*KH + kh)*KW + kw][ih*W + iw] that reach it,
+// summed in (kh, kw) order.
+__global__ __launch_bounds__(256) void convt2d_gather_kernel(ConvT2DArgs a) {
+  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= per_b * a.B) return;
+  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
+  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const int64_t n_in = (int64_t)a.H * a.W;
+  const float* zb = a.z + ((int64_t)b * a.Cout + oc) * a.KH * a.KW * n_in;
+  float sum = 0.f;
+  for (int kh = 0; kh < a.KH; ++kh) {
+    const int nh = oh + a.ph - kh * a.dh;
+    if (nh < 0 || nh % a.sh) continue;
+    const int ih = nh / a.sh;
+    if (ih >= a.H) continue;
+    for (int kw = 0; kw < a.KW; ++kw) {
+      const int nw = ow + a.pw - kw * a.dw;
+      if (nw < 0 || nw % a.sw) continue;
+      const int iw = nw / a.sw;
+      if (iw >= a.W) continue;
+      sum += zb[(int64_t)(kh * a.KW + kw) * n_in + (int64_t)ih * a.W + iw];
+    }
+  }
+  if (a.bias) sum += a.bias[oc];
+  a.y[idx] = sum;
+}
+
+__global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
+  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= per_b * a.B) return;
+  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
+  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const int Cin = a.C1 + a.C2;
+  const int coutpg = a.Cout / a.groups, cinpg = Cin / a.groups;
+  const int g = oc / coutpg, ocg = oc % coutpg;
+  const int64_t n_in = (int64_t)a.H * a.W;
+  float sum = 0.f;
+  for (int icg = 0; icg < cinpg; ++icg) {
+    const int ic = g * cinpg + icg;
+    const float* xc = ic < a.C1 ? a.x1 + ((int64_t)b * a.C1 + ic) * n_in
+                                : a.x2 + ((int64_t)b * a.C2 + (ic - a.C1)) * n_in;
+    const float* wr = a.w + ((int64_t)ic * coutpg + ocg) * a.KH * a.KW;
+    for (int kh = 0; kh < a.KH; ++kh) {
+      const int nh = oh + a.ph - kh * a.dh;
+      if (nh < 0 || nh % a.sh) continue;
+      const int ih = nh / a.sh;
+      if (ih >= a.H) continue;
+      for (int kw = 0; kw < a.KW; ++kw) {
+        const int nw = ow + a.pw - kw * a.dw;
+        if (nw < 0 || nw % a.sw) continue;
+        const int iw = nw / a.sw;
+        if (iw >= a.W) continue;
+        sum = fmaf(xc[(int64_t)ih * a.W + iw], wr[kh * a.KW + kw], sum);
+      }
+    }
+  }
+  if (a.bias) sum += a.bias[oc];
+  a.y[idx] = sum;
+}
+
+void check_conv2d(const Conv2DArgs& a) {
+  MNN_REQUIRE(a.B > 0 && a.Cin > 0 && a.Cout > 0 && a.groups > 0 && a.Cin % a.groups == 0 &&
+                  a.Cout % a.groups == 0 && a.KH > 0 && a.KW > 0 && a.sh > 0 && a.sw > 0 &&
+                  a.dh > 0 && a.dw > 0 && a.ph >= 0 && a.pw >= 0 && a.H > 0 && a.W > 0 &&
+                  a.Ho > 0 && a.Wo > 0 && a.x && a.w && a.y,
+              MNN_ERR_INVALID_ARGUMENT, "conv2d: invalid configuration");
+  // every tap of every output lies in the (padded) input
+  MNN_REQUIRE((int64_t)(a.Ho - 1) * a.sh + (int64_t)(a.KH - 1) * a.dh < (int64_t)a.H + 2 * a.ph &&
+                  (int64_t)(a.Wo - 1) * a.sw + (int64_t)(a.KW - 1) * a.dw <
+                      (int64_t)a.W + 2 * a.pw,
+              MNN_ERR_INVALID_ARGUMENT, "conv2d: output size exceeds the padded input");
+}
+
+void check_convt2d(const ConvT2DArgs& a) {
+  const int Cin = a.C1 + a.C2;
+  MNN_REQUIRE(a.B > 0 && Cin > 0 && a.Cout > 0 && a.groups > 0 && Cin % a.groups == 0 &&
+                  a.Cout % a.groups == 0 && a.KH > 0 && a.KW > 0 && a.sh > 0 && a.sw > 0 &&
+                  a.dh > 0 && a.dw > 0 && a.ph >= 0 && a.pw >= 0 && a.H > 0 && a.W > 0 &&
+                  a.Ho > 0 && a.Wo > 0 && a.x1 && (a.C2 == 0 || a.x2) && a.y,
+              MNN_ERR_INVALID_ARGUMENT, "conv_transpose2d: invalid configuration");
+}
+
+}  // namespace
+
+int conv2d_padded_k(int Cin, int KH, int KW) { return (Cin * KH * KW + 31) / 32 * 32; }
+
+bool conv2d_gemm_supported(const Conv2DArgs& a) { return a.groups == 1; }
+
+bool conv2d_pointwise(const Conv2DArgs& a) {
+  return a.groups == 1 && a.KH == 1 && a.KW == 1 && a.sh == 1 && a.sw == 1 && a.ph == 0 &&
+         a.pw == 0 && a.Ho == a.H && a.Wo == a.W;
+}
+
+int64_t conv2d_unfold_floats(const Conv2DArgs& a) {
+  return conv2d_pointwise(a) ? 0 : (int64_t)a.B * a.Ho * a.Wo * conv2d_padded_k(a.Cin, a.KH, a.KW);
+}
+
+void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out) {
+  const int K = Cin * KH * KW, Kp = conv2d_padded_k(Cin, KH, KW);
+  for (int oc = 0; oc < Cout; ++oc)
+    for (int k = 0; k < Kp; ++k) out[(int64_t)oc * Kp + k] = k < K ? w[(int64_t)oc * K + k] : 0.f;
+}
+
+void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack, float* unfold) {
+  Conv2DArgs a = a_in;
+  check_conv2d(a);
+  MNN_REQUIRE(conv2d_gemm_supported(a) && wpack, MNN_ERR_INVALID_ARGUMENT,
+              "conv2d_gemm: configuration outside the GEMM form");
+  const int64_t N = (int64_t)a.Ho * a.Wo;
+  MNN_REQUIRE(N < (1LL << 31), MNN_ERR_INVALID_ARGUMENT, "conv2d_gemm: output plane too large");
+  GemmArgs g;
+  g.M = a.Cout;
+  g.N = (int)N;
+  g.batch = a.B;
+  g.A = wpack;
+  g.C = a.y;
+  g.ldc = N;
+  g.sC = (int64_t)a.Cout * N;
+  g.bias = a.bias;
+  g.bias_mode = a.bias ? BIAS_M : BIAS_NONE;
+  g.name = "conv2d_f32_mfma";
+  if (conv2d_pointwise(a)) {
+    g.K = a.Cin;
+    g.lda = conv2d_padded_k(a.Cin, 1, 1);
+    g.B = a.x;
+    g.blayout = B_KN;
+    g.ldb = N;
+    g.sB = (int64_t)a.Cin * N;
+    return gemm(c, g);
+  }
+  MNN_REQUIRE(unfold, MNN_ERR_INVALID_ARGUMENT, "conv2d_gemm: unfold buffer required");
+  a.Kp = conv2d_padded_k(a.Cin, a.KH, a.KW);
+  a.u = unfold;
+  launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel,
+         dim3((unsigned)cdiv(N * (a.Kp / 4), 256), (unsigned)a.B), dim3(256), 0, a);
+  g.K = a.Kp;
+  g.lda = a.Kp;
+  g.B = unfold;
+  g.blayout = B_NK;
+  g.ldb = a.Kp;
+  g.sB = N * a.Kp;
+  gemm(c, g);
+}
+
+void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a) {
+  check_conv2d(a);
+  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
+  launch(c, "conv2d_direct_f32", conv2d_direct_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
+         a);
+}
+
+int convt2d_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
+
+bool convt2d_gemm_supported(const ConvT2DArgs& a) { return a.groups == 1; }
+
+int64_t convt2d_z_floats(const ConvT2DArgs& a) {
+  return (int64_t)a.B * a.Cout * a.KH * a.KW * a.H * a.W;
+}
+
+void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, float* out) {
+  const int ks = KH * KW, Cp = convt2d_padded_cin(Cin);
+  for (int m = 0; m < Cout * ks; ++m)
+    for (int ic = 0; ic < Cp; ++ic)
+      out[(int64_t)m * Cp + ic] = ic < Cin ? w[((int64_t)ic * Cout + m / ks) * ks + m % ks] : 0.f;
+}
+
+void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z) {
+  check_convt2d(a);
+  MNN_REQUIRE(convt2d_gemm_supported(a) && wpack && z, MNN_ERR_INVALID_ARGUMENT,
+              "convt2d_gemm: configuration outside the GEMM form");
+  const int64_t n_in = (int64_t)a.H * a.W;
+  MNN_REQUIRE(n_in < (1LL << 31), MNN_ERR_INVALID_ARGUMENT, "convt2d_gemm: input plane too large");
+  const int ks = a.KH * a.KW;
+  GemmArgs g;
+  g.M = a.Cout * ks;
+  g.N = (int)n_in;
+  g.batch = a.B;
+  g.lda = convt2d_padded_cin(a.C1 + a.C2);
+  g.blayout = B_KN;
+  g.ldb = n_in;
+  g.C = z;
+  g.ldc = n_in;
+  g.sC = (int64_t)g.M * n_in;
+  g.name = "convt2d_f32_mfma";
+  g.A = wpack;
+  g.K = a.C1;
+  g.B = a.x1;
+  g.sB = (int64_t)a.C1 * n_in;
+  gemm(c, g);
+  if (a.C2 > 0) {  // the concatenated channels: Z += W[:, C1:] * x2
+    g.A = wpack + a.C1;
+    g.K = a.C2;
+    g.B = a.x2;
+    g.sB = (int64_t)a.C2 * n_in;
+    g.R = z;
+    g.ldr = n_in;
+    g.sR = g.sC;
+    gemm(c, g);
+  }
+  ConvT2DArgs t = a;
+  t.z = z;
+  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
+  launch(c, "convt2d_gather_f32", convt2d_gather_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256),
+         0, t);
+}
+
+void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a) {
+  check_convt2d(a);
+  MNN_REQUIRE(a.w, MNN_ERR_INVALID_ARGUMENT, "convt2d_direct: weights required");
+  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
+  launch(c, "convt2d_direct_f32", convt2d_direct_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256),
+         0, a);
+}
+
+}  // namespace k
+}  // namespace mnn

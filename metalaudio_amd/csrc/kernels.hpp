@@ -129,6 +129,52 @@ void gemm(const LaunchCtx& c, const GemmArgs& a);
 bool gemm_nk_lds_supported(const GemmArgs& a);
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
 
+// ------------------------------------------------------------------ 2-D conv (k_conv2d.hip)
+// DynamicConv2D (DynamicConv2D.swift:37-592): x [B][Cin][H][W] -> y [B][Cout][Ho][Wo], weights
+// [Cout][Cin/groups][KH][KW]; zero padding (ph, pw), or mirrored samples with reflect.
+struct Conv2DArgs {
+  int B = 0, Cin = 0, Cout = 0, H = 0, W = 0, Ho = 0, Wo = 0;
+  int KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1, groups = 1;
+  bool reflect = false;
+  const float* x = nullptr;
+  const float* w = nullptr;  // direct form: [Cout][Cin/groups][KH][KW]
+  const float* bias = nullptr;
+  float* y = nullptr;
+  int Kp = 0;            // unfold row length (set by conv2d_gemm)
+  float* u = nullptr;    // unfold [B][Ho*Wo][Kp] (set by conv2d_gemm)
+};
+// Matrix-core form (groups 1): weights packed [Cout][conv2d_padded_k] (zero columns past
+// Cin*KH*KW) by conv2d_pack_weights; unfold workspace of conv2d_unfold_floats floats (0 for
+// pointwise convs, which read the input directly).
+int conv2d_padded_k(int Cin, int KH, int KW);
+bool conv2d_gemm_supported(const Conv2DArgs& a);
+bool conv2d_pointwise(const Conv2DArgs& a);
+int64_t conv2d_unfold_floats(const Conv2DArgs& a);
+void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out);
+void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a, const float* wpack, float* unfold);
+void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a);
+
+// DynamicConvTranspose2D (DynamicConv2D.swift:598-959) over the channel concat [x1; x2] (C2 may
+// be 0): y [B][Cout][Ho][Wo], weights [C1 + C2][Cout/groups][KH][KW].
+struct ConvT2DArgs {
+  int B = 0, C1 = 0, C2 = 0, Cout = 0, H = 0, W = 0, Ho = 0, Wo = 0;
+  int KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1, groups = 1;
+  const float* x1 = nullptr;
+  const float* x2 = nullptr;
+  const float* w = nullptr;  // direct form
+  const float* bias = nullptr;
+  float* y = nullptr;
+  const float* z = nullptr;  // GEMM form: tap products [B][Cout*KH*KW][H*W] (set by convt2d_gemm)
+};
+// Matrix-core form (groups 1): weights packed [Cout*KH*KW][convt2d_padded_cin] by
+// convt2d_pack_weights; tap-product workspace of convt2d_z_floats floats.
+int convt2d_padded_cin(int Cin);
+bool convt2d_gemm_supported(const ConvT2DArgs& a);
+int64_t convt2d_z_floats(const ConvT2DArgs& a);
+void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, float* out);
+void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z);
+void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
+
 // ------------------------------------------------------------------ transposed conv (k_convt.hip)
 // DynamicConvTranspose1D (DynamicConv1D.swift:411-645) over the channel concat [x1; x2] (x2 may be
 // absent: C2 = 0): y[b][oc][o] (row pitch Lout) = bias + sum over (ic, k) with

@@ -1107,6 +1107,7 @@ class DecoderBlockLayer : public Layer {
   }
   void load(const std::string& name, const float* data, size_t n) override {
     if (name.rfind("conv_tr.", 0) == 0) return convt_->load(name.substr(8), data, n);
+    if (name.rfind("conv_transpose.", 0) == 0) return convt_->load(name.substr(15), data, n);
     if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
     fail(MNN_ERR_INVALID_ARGUMENT, "UNetDecoderBlock: unknown parameter '" + name + "'");
   }
@@ -1144,6 +1145,401 @@ class DecoderBlockLayer : public Layer {
  private:
   mnn_decoder_block_desc d_;
   std::unique_ptr<ConvTranspose1DLayer> convt_;
+  std::unique_ptr<GroupNormLayer> norm_;
+  DevBuf y_, partials_;
+};
+
+// ------------------------------------------------------------------ 2-D convolutions
+namespace {
+
+// [C, H, W] / [B, C, H, W] -> (B, C, H, W)
+void split_bchw(const Shape& s, int64_t& B, int64_t& C, int64_t& H, int64_t& W) {
+  MNN_REQUIRE(s.size() == 3 || s.size() == 4, MNN_ERR_SHAPE_MISMATCH,
+              "expected [C, H, W] or [B, C, H, W], got " << shape_str(s));
+  B = s.size() == 4 ? s[0] : 1;
+  C = s[s.size() - 3];
+  H = s[s.size() - 2];
+  W = s[s.size() - 1];
+}
+
+Shape with_chw(const Shape& in, int64_t C, int64_t H, int64_t W) {
+  Shape o = in;
+  o[o.size() - 3] = C;
+  o[o.size() - 2] = H;
+  o[o.size() - 1] = W;
+  return o;
+}
+
+}  // namespace
+
+// DynamicConv2D (DynamicConv2D.swift:37-592): valid / same / explicit / reflect padding, stride,
+// dilation, groups. Output size floor((n + 2p - ((k-1)d + 1)) / s) + 1 (outputSize, :193-205),
+// "same" padding total/2 on both sides for ceil(n / s) outputs (computePadding, :212-238).
+class Conv2DLayer : public Layer {
+ public:
+  Conv2DLayer(Device* d, const mnn_conv2d_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.out_channels > 0 && desc.kernel_h > 0 &&
+                    desc.kernel_w > 0 && desc.stride_h > 0 && desc.stride_w > 0 &&
+                    desc.dilation_h > 0 && desc.dilation_w > 0 && desc.groups > 0 &&
+                    desc.in_channels % desc.groups == 0 && desc.out_channels % desc.groups == 0 &&
+                    desc.padding_mode >= MNN_PAD_VALID && desc.padding_mode <= MNN_PAD_REFLECT &&
+                    desc.pad_h >= 0 && desc.pad_w >= 0,
+                MNN_ERR_INVALID_CONFIGURATION, "Conv2D: invalid configuration");
+    const int cpg = desc.in_channels / desc.groups;
+    w_ = &add_param("weight",
+                    (int64_t)desc.out_channels * cpg * desc.kernel_h * desc.kernel_w);
+    if (desc.use_bias) b_ = &add_param("bias", desc.out_channels);
+    gemm_ = desc.groups == 1;
+    if (gemm_) {
+      std::vector<float> zero((size_t)w_->count, 0.f);
+      pack(zero.data());
+    }
+  }
+  const char* kind() const override { return "Conv2D"; }
+  Shape input_shape() const override { return {d_.in_channels, 0, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0, 0}; }
+  std::pair<int, int> padding(int64_t H, int64_t W) const {
+    switch (d_.padding_mode) {
+      case MNN_PAD_VALID: return {0, 0};
+      case MNN_PAD_SAME: {
+        const int64_t ekh = (int64_t)(d_.kernel_h - 1) * d_.dilation_h + 1;
+        const int64_t ekw = (int64_t)(d_.kernel_w - 1) * d_.dilation_w + 1;
+        const int64_t oh = (H + d_.stride_h - 1) / d_.stride_h;
+        const int64_t ow = (W + d_.stride_w - 1) / d_.stride_w;
+        return {(int)(std::max<int64_t>(0, (oh - 1) * d_.stride_h + ekh - H) / 2),
+                (int)(std::max<int64_t>(0, (ow - 1) * d_.stride_w + ekw - W) / 2)};
+      }
+      default: return {d_.pad_h, d_.pad_w};
+    }
+  }
+  std::pair<int64_t, int64_t> out_size(int64_t H, int64_t W) const {
+    const auto p = padding(H, W);
+    const int64_t nh = H + 2LL * p.first - ((int64_t)(d_.kernel_h - 1) * d_.dilation_h + 1);
+    const int64_t nw = W + 2LL * p.second - ((int64_t)(d_.kernel_w - 1) * d_.dilation_w + 1);
+    if (nh < 0 || nw < 0) return {0, 0};
+    return {nh / d_.stride_h + 1, nw / d_.stride_w + 1};
+  }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, H, W;
+    split_bchw(in, B, C, H, W);
+    MNN_REQUIRE(C == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "Conv2D: expected " << d_.in_channels << " channels, got " << C);
+    const auto o = out_size(H, W);
+    MNN_REQUIRE(H > 0 && W > 0 && o.first > 0 && o.second > 0, MNN_ERR_SHAPE_MISMATCH,
+                "Conv2D: input " << H << "x" << W << " gives no output");
+    return with_chw(in, d_.out_channels, o.first, o.second);
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, H, W;
+    split_bchw(in.shape, B, C, H, W);
+    run(in.f32(), (int)B, H, W, out.f32(), s);
+  }
+  void run(const float* x, int B, int64_t H, int64_t W, float* y, Stream& s) {
+    const auto o = out_size(H, W);
+    const auto p = padding(H, W);
+    MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH, "Conv2D: input too large");
+    k::Conv2DArgs a;
+    a.B = B;
+    a.Cin = d_.in_channels;
+    a.Cout = d_.out_channels;
+    a.H = (int)H;
+    a.W = (int)W;
+    a.Ho = (int)o.first;
+    a.Wo = (int)o.second;
+    a.KH = d_.kernel_h;
+    a.KW = d_.kernel_w;
+    a.sh = d_.stride_h;
+    a.sw = d_.stride_w;
+    a.ph = p.first;
+    a.pw = p.second;
+    a.dh = d_.dilation_h;
+    a.dw = d_.dilation_w;
+    a.groups = d_.groups;
+    a.reflect = d_.padding_mode == MNN_PAD_REFLECT;
+    a.x = x;
+    a.w = w_->ptr();
+    a.bias = b_ ? b_->ptr() : nullptr;
+    a.y = y;
+    if (gemm_) {
+      const int64_t uf = k::conv2d_unfold_floats(a);
+      if (uf > 0) unfold_.reserve(sizeof(float) * uf);
+      k::conv2d_gemm(ctx(s), a, wpack_.f32(), uf > 0 ? unfold_.f32() : nullptr);
+    } else {
+      k::conv2d_direct(ctx(s), a);
+    }
+  }
+
+ protected:
+  void on_loaded(const std::string& name, const float* data, size_t) override {
+    if (name == "weight" && gemm_) pack(data);
+  }
+
+ private:
+  void pack(const float* w) {
+    const int Kp = k::conv2d_padded_k(d_.in_channels, d_.kernel_h, d_.kernel_w);
+    std::vector<float> h((size_t)d_.out_channels * Kp);
+    k::conv2d_pack_weights(w, d_.out_channels, d_.in_channels, d_.kernel_h, d_.kernel_w,
+                           h.data());
+    dev_->make_current();
+    wpack_.reserve(sizeof(float) * h.size());
+    HIP_CHECK(hipMemcpy(wpack_.ptr, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice));
+  }
+  mnn_conv2d_desc d_;
+  Param* w_ = nullptr;
+  Param* b_ = nullptr;
+  bool gemm_ = false;
+  DevBuf wpack_, unfold_;
+};
+
+// DynamicConvTranspose2D (DynamicConv2D.swift:598-959): output (n - 1)s - 2p + (k - 1)d + 1 + op
+// per axis (outputSize, :727-736).
+class ConvTranspose2DLayer : public Layer {
+ public:
+  ConvTranspose2DLayer(Device* d, const mnn_conv_transpose2d_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.out_channels > 0 && desc.kernel_h > 0 &&
+                    desc.kernel_w > 0 && desc.stride_h > 0 && desc.stride_w > 0 &&
+                    desc.dilation_h > 0 && desc.dilation_w > 0 && desc.groups > 0 &&
+                    desc.pad_h >= 0 && desc.pad_w >= 0 && desc.output_pad_h >= 0 &&
+                    desc.output_pad_w >= 0 && desc.in_channels % desc.groups == 0 &&
+                    desc.out_channels % desc.groups == 0,
+                MNN_ERR_INVALID_CONFIGURATION, "ConvTranspose2D: invalid configuration");
+    w_ = &add_param("weight", (int64_t)desc.in_channels * (desc.out_channels / desc.groups) *
+                                  desc.kernel_h * desc.kernel_w);
+    if (desc.use_bias) b_ = &add_param("bias", desc.out_channels);
+    gemm_ = desc.groups == 1;
+    if (gemm_) {
+      std::vector<float> zero((size_t)w_->count, 0.f);
+      pack(zero.data());
+    }
+  }
+  const char* kind() const override { return "ConvTranspose2D"; }
+  Shape input_shape() const override { return {d_.in_channels, 0, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0, 0}; }
+  std::pair<int64_t, int64_t> out_size(int64_t H, int64_t W) const {
+    return {(H - 1) * d_.stride_h - 2LL * d_.pad_h + (int64_t)d_.dilation_h * (d_.kernel_h - 1) +
+                d_.output_pad_h + 1,
+            (W - 1) * d_.stride_w - 2LL * d_.pad_w + (int64_t)d_.dilation_w * (d_.kernel_w - 1) +
+                d_.output_pad_w + 1};
+  }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, H, W;
+    split_bchw(in, B, C, H, W);
+    MNN_REQUIRE(C == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose2D: expected " << d_.in_channels << " channels, got " << C);
+    const auto o = out_size(H, W);
+    MNN_REQUIRE(H > 0 && W > 0 && o.first > 0 && o.second > 0, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose2D: input " << H << "x" << W << " gives no output");
+    return with_chw(in, d_.out_channels, o.first, o.second);
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, H, W;
+    split_bchw(in.shape, B, C, H, W);
+    run(in.f32(), (int)C, nullptr, 0, (int)B, H, W, out.f32(), s);
+  }
+  // y from the channel concat [x1 (C1); x2 (C2)], C1 + C2 = in_channels.
+  void run(const float* x1, int C1, const float* x2, int C2, int B, int64_t H, int64_t W,
+           float* y, Stream& s) {
+    MNN_REQUIRE(C1 + C2 == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose2D: channel count mismatch");
+    MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH,
+                "ConvTranspose2D: input too large");
+    const auto o = out_size(H, W);
+    k::ConvT2DArgs a;
+    a.B = B;
+    a.C1 = C1;
+    a.C2 = C2;
+    a.Cout = d_.out_channels;
+    a.H = (int)H;
+    a.W = (int)W;
+    a.Ho = (int)o.first;
+    a.Wo = (int)o.second;
+    a.KH = d_.kernel_h;
+    a.KW = d_.kernel_w;
+    a.sh = d_.stride_h;
+    a.sw = d_.stride_w;
+    a.ph = d_.pad_h;
+    a.pw = d_.pad_w;
+    a.dh = d_.dilation_h;
+    a.dw = d_.dilation_w;
+    a.groups = d_.groups;
+    a.x1 = x1;
+    a.x2 = x2;
+    a.w = w_->ptr();
+    a.bias = b_ ? b_->ptr() : nullptr;
+    a.y = y;
+    if (gemm_) {
+      z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
+      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32());
+    } else {
+      k::convt2d_direct(ctx(s), a);
+    }
+  }
+
+ protected:
+  void on_loaded(const std::string& name, const float* data, size_t) override {
+    if (name == "weight" && gemm_) pack(data);
+  }
+
+ private:
+  void pack(const float* w) {
+    const int Cp = k::convt2d_padded_cin(d_.in_channels);
+    std::vector<float> h((size_t)d_.out_channels * d_.kernel_h * d_.kernel_w * Cp);
+    k::convt2d_pack_weights(w, d_.in_channels, d_.out_channels, d_.kernel_h, d_.kernel_w,
+                            h.data());
+    dev_->make_current();
+    wpack_.reserve(sizeof(float) * h.size());
+    HIP_CHECK(hipMemcpy(wpack_.ptr, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice));
+  }
+  mnn_conv_transpose2d_desc d_;
+  Param* w_ = nullptr;
+  Param* b_ = nullptr;
+  bool gemm_ = false;
+  DevBuf wpack_, z_;
+};
+
+// FreqUNetEncoderBlock2D (FreqUNet2D.swift:12-192): Conv2D (reflect padding ((k-1)/2 per axis),
+// stride) -> GroupNorm over [C, H*W] -> tanh-GELU. Parameters "conv.weight", "conv.bias",
+// "norm.weight", "norm.bias".
+class FreqEncoderBlockLayer : public Layer {
+ public:
+  FreqEncoderBlockLayer(Device* d, const mnn_freq_block_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.out_channels > 0 && desc.kernel_h > 0 &&
+                    desc.kernel_w > 0 && desc.stride_h > 0 && desc.stride_w > 0 &&
+                    desc.num_groups > 0 && desc.skip_channels == 0,
+                MNN_ERR_INVALID_CONFIGURATION, "FreqUNetEncoderBlock2D: invalid configuration");
+    mnn_conv2d_desc c{};
+    c.in_channels = desc.in_channels;
+    c.out_channels = desc.out_channels;
+    c.kernel_h = desc.kernel_h;
+    c.kernel_w = desc.kernel_w;
+    c.stride_h = desc.stride_h;
+    c.stride_w = desc.stride_w;
+    c.padding_mode = MNN_PAD_REFLECT;
+    c.pad_h = (desc.kernel_h - 1) / 2;
+    c.pad_w = (desc.kernel_w - 1) / 2;
+    c.dilation_h = c.dilation_w = 1;
+    c.groups = 1;
+    c.use_bias = 1;
+    conv_ = std::make_unique<Conv2DLayer>(d, c);
+    norm_ = std::make_unique<GroupNormLayer>(d, desc.num_groups, desc.out_channels, 1e-5f, true,
+                                             MNN_ACT_GELU);
+  }
+  const char* kind() const override { return "FreqUNetEncoderBlock2D"; }
+  Shape input_shape() const override { return {d_.in_channels, 0, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0, 0}; }
+  Shape infer_output(const Shape& in) const override { return conv_->infer_output(in); }
+  void load(const std::string& name, const float* data, size_t n) override {
+    if (name.rfind("conv.", 0) == 0) return conv_->load(name.substr(5), data, n);
+    if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
+    fail(MNN_ERR_INVALID_ARGUMENT, "FreqUNetEncoderBlock2D: unknown parameter '" + name + "'");
+  }
+  void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    const Shape os = infer_output(in.shape);
+    check_out(out, os);
+    int64_t B, C, H, W;
+    split_bchw(in.shape, B, C, H, W);
+    const int Cout = d_.out_channels;
+    const int64_t L = os[os.size() - 2] * os.back();
+    y_.reserve(sizeof(float) * B * Cout * L);
+    conv_->run(in.f32(), (int)B, H, W, y_.f32(), s);
+    gn_gelu(norm_.get(), partials_, y_.f32(), out.f32(), (int)B, Cout, L, s);
+  }
+
+  static void gn_gelu(GroupNormLayer* norm, DevBuf& partials, const float* y, float* out, int B,
+                      int C, int64_t L, Stream& s) {
+    const int G = norm->groups();
+    const int nchunk = k::gn_num_chunks(C, G, L);
+    partials.reserve(sizeof(float) * 3 * B * G * nchunk);
+    k::gn_stats_partial(ctx(s), y, B, C, L, G, partials.f32(), nchunk);
+    norm->finalize(s, B, nchunk, partials.f32());
+    k::gn_apply(ctx(s), y, out, B, C, L, norm->coef(), MNN_ACT_GELU);
+  }
+
+ private:
+  mnn_freq_block_desc d_;
+  std::unique_ptr<Conv2DLayer> conv_;
+  std::unique_ptr<GroupNormLayer> norm_;
+  DevBuf y_, partials_;
+};
+
+// FreqUNetDecoderBlock2D (FreqUNet2D.swift:198-428): concat(input, skip) over channels ->
+// ConvTranspose2D (padding (k-1)/2, output padding stride-1 per axis) -> GroupNorm -> tanh-GELU.
+// The concat is folded into the transposed conv (a second GEMM over the skip channels), so no
+// concatenated tensor is written. Parameters "conv_tr.*" (or "conv_transpose.*") and "norm.*".
+class FreqDecoderBlockLayer : public Layer {
+ public:
+  FreqDecoderBlockLayer(Device* d, const mnn_freq_block_desc& desc) : Layer(d), d_(desc) {
+    MNN_REQUIRE(desc.in_channels > 0 && desc.skip_channels >= 0 && desc.out_channels > 0 &&
+                    desc.kernel_h > 0 && desc.kernel_w > 0 && desc.stride_h > 0 &&
+                    desc.stride_w > 0 && desc.num_groups > 0,
+                MNN_ERR_INVALID_CONFIGURATION, "FreqUNetDecoderBlock2D: invalid configuration");
+    mnn_conv_transpose2d_desc c{};
+    c.in_channels = desc.in_channels + desc.skip_channels;
+    c.out_channels = desc.out_channels;
+    c.kernel_h = desc.kernel_h;
+    c.kernel_w = desc.kernel_w;
+    c.stride_h = desc.stride_h;
+    c.stride_w = desc.stride_w;
+    c.pad_h = (desc.kernel_h - 1) / 2;
+    c.pad_w = (desc.kernel_w - 1) / 2;
+    c.output_pad_h = desc.stride_h - 1;
+    c.output_pad_w = desc.stride_w - 1;
+    c.dilation_h = c.dilation_w = 1;
+    c.groups = 1;
+    c.use_bias = 1;
+    convt_ = std::make_unique<ConvTranspose2DLayer>(d, c);
+    norm_ = std::make_unique<GroupNormLayer>(d, desc.num_groups, desc.out_channels, 1e-5f, true,
+                                             MNN_ACT_GELU);
+  }
+  const char* kind() const override { return "FreqUNetDecoderBlock2D"; }
+  Shape input_shape() const override { return {d_.in_channels, 0, 0}; }
+  Shape output_shape() const override { return {d_.out_channels, 0, 0}; }
+  Shape infer_output(const Shape& in) const override {
+    int64_t B, C, H, W;
+    split_bchw(in, B, C, H, W);
+    MNN_REQUIRE(C == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
+                "FreqUNetDecoderBlock2D: expected " << d_.in_channels << " channels, got " << C);
+    const auto o = convt_->out_size(H, W);
+    MNN_REQUIRE(H > 0 && W > 0 && o.first > 0 && o.second > 0, MNN_ERR_SHAPE_MISMATCH,
+                "FreqUNetDecoderBlock2D: input gives no output");
+    return with_chw(in, d_.out_channels, o.first, o.second);
+  }
+  void load(const std::string& name, const float* data, size_t n) override {
+    if (name.rfind("conv_tr.", 0) == 0) return convt_->load(name.substr(8), data, n);
+    if (name.rfind("conv_transpose.", 0) == 0) return convt_->load(name.substr(15), data, n);
+    if (name.rfind("norm.", 0) == 0) return norm_->load(name.substr(5), data, n);
+    fail(MNN_ERR_INVALID_ARGUMENT, "FreqUNetDecoderBlock2D: unknown parameter '" + name + "'");
+  }
+  void forward(const Tensor&, Tensor&, Stream&) override {
+    fail(MNN_ERR_INVALID_CONFIGURATION,
+         "FreqUNetDecoderBlock2D: forward takes (input, skip); use the two-input forward");
+  }
+  void forward_cross(const Tensor* in, const Tensor* skip, Tensor* out, Tensor*,
+                     Stream& s) override {
+    MNN_REQUIRE(in && skip && out, MNN_ERR_INVALID_ARGUMENT,
+                "FreqUNetDecoderBlock2D: input, skip and output are required");
+    int64_t B, C, H, W, Bs, Cs, Hs, Ws;
+    split_bchw(in->shape, B, C, H, W);
+    split_bchw(skip->shape, Bs, Cs, Hs, Ws);
+    MNN_REQUIRE(C == d_.in_channels && Cs == d_.skip_channels && Bs == B && Hs == H && Ws == W,
+                MNN_ERR_SHAPE_MISMATCH,
+                "FreqUNetDecoderBlock2D: input " << shape_str(in->shape) << " and skip "
+                                                 << shape_str(skip->shape) << " do not match");
+    const Shape os = infer_output(in->shape);
+    check_out(*out, os);
+    const int Cout = d_.out_channels;
+    const int64_t L = os[os.size() - 2] * os.back();
+    y_.reserve(sizeof(float) * B * Cout * L);
+    convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, H, W, y_.f32(), s);
+    FreqEncoderBlockLayer::gn_gelu(norm_.get(), partials_, y_.f32(), out->f32(), (int)B, Cout, L,
+                                   s);
+  }
+
+ private:
+  mnn_freq_block_desc d_;
+  std::unique_ptr<ConvTranspose2DLayer> convt_;
   std::unique_ptr<GroupNormLayer> norm_;
   DevBuf y_, partials_;
 };
@@ -1430,6 +1826,18 @@ std::unique_ptr<Layer> make_encoder_block(Device* d, const mnn_encoder_block_des
 }
 std::unique_ptr<Layer> make_conv_transpose1d(Device* d, const mnn_conv_transpose1d_desc& desc) {
   return std::make_unique<ConvTranspose1DLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_conv2d(Device* d, const mnn_conv2d_desc& desc) {
+  return std::make_unique<Conv2DLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_conv_transpose2d(Device* d, const mnn_conv_transpose2d_desc& desc) {
+  return std::make_unique<ConvTranspose2DLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_freq_encoder_block(Device* d, const mnn_freq_block_desc& desc) {
+  return std::make_unique<FreqEncoderBlockLayer>(d, desc);
+}
+std::unique_ptr<Layer> make_freq_decoder_block(Device* d, const mnn_freq_block_desc& desc) {
+  return std::make_unique<FreqDecoderBlockLayer>(d, desc);
 }
 std::unique_ptr<Layer> make_decoder_block(Device* d, const mnn_decoder_block_desc& desc) {
   return std::make_unique<DecoderBlockLayer>(d, desc);

@@ -59,6 +59,10 @@ std::unique_ptr<Layer> make_feedforward(Device* d, int in, int hidden, mnn_preci
 std::unique_ptr<Layer> make_encoder_block(Device* d, const mnn_encoder_block_desc& desc);
 std::unique_ptr<Layer> make_conv_transpose1d(Device* d, const mnn_conv_transpose1d_desc& desc);
 std::unique_ptr<Layer> make_decoder_block(Device* d, const mnn_decoder_block_desc& desc);
+std::unique_ptr<Layer> make_conv2d(Device* d, const mnn_conv2d_desc& desc);
+std::unique_ptr<Layer> make_conv_transpose2d(Device* d, const mnn_conv_transpose2d_desc& desc);
+std::unique_ptr<Layer> make_freq_encoder_block(Device* d, const mnn_freq_block_desc& desc);
+std::unique_ptr<Layer> make_freq_decoder_block(Device* d, const mnn_freq_block_desc& desc);
 std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, int ffn,
                                               float layer_scale, mnn_precision prec);
 std::unique_ptr<Layer> make_cross_transformer(Device* d, int embed, int heads, int ffn,

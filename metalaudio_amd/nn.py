@@ -13,8 +13,9 @@ from typing import Iterable, Optional, Sequence
 
 import numpy as np
 
-from ._lib import (ACT, PAD, PRECISION, Conv1dDesc, ConvTranspose1dDesc, DecoderBlockDesc,
-                   EncoderBlockDesc, MNNError, check, dims, lib)
+from ._lib import (ACT, PAD, PRECISION, Conv1dDesc, Conv2dDesc, ConvTranspose1dDesc,
+                   ConvTranspose2dDesc, DecoderBlockDesc, EncoderBlockDesc, FreqBlockDesc, MNNError,
+                   check, dims, lib)
 
 __all__ = [
     "MNNError", "AudioDevice", "Stream", "Tensor", "Layer", "Conv1D", "DynamicConv1D",
@@ -22,6 +23,8 @@ __all__ = [
     "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
     "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
     "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "WeightNameMapper",
+    "Conv2D", "DynamicConv2D", "ConvTranspose2D", "DynamicConvTranspose2D",
+    "FreqUNetEncoderBlock2D", "FreqUNetDecoderBlock2D", "unet_padding_2d", "unet_bottleneck_2d",
     "mfma_probe",
 ]
 
@@ -434,6 +437,100 @@ def unet_bottleneck_length(input_length: int, levels: int, stride: int = 4) -> i
     out = C.c_int64()
     check(lib().mnn_unet_bottleneck_length(input_length, levels, stride, C.byref(out)))
     return out.value
+
+
+def _pair(v) -> tuple[int, int]:
+    return (v, v) if isinstance(v, int) else (int(v[0]), int(v[1]))
+
+
+class Conv2D(Layer):
+    """DynamicConv2D (DynamicConv2D.swift:37-592); weight [out, in/groups, kh, kw]. padding:
+    "valid", "same", "explicit" or "reflect" (the last two with `pad` = (h, w))."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1,
+                 padding="valid", pad=0, dilation=1, groups=1, use_bias=True):
+        (kh, kw), (sh, sw), (ph, pw), (dh, dw) = map(_pair, (kernel_size, stride, pad, dilation))
+        d = Conv2dDesc(input_channels, output_channels, kh, kw, sh, sw, PAD[padding], ph, pw, dh,
+                       dw, groups, int(use_bias))
+        super().__init__(device, _create(lib().mnn_conv2d_create, device.handle, C.byref(d)))
+        self.use_bias = use_bias
+
+    def load_weights(self, weights, bias=None) -> None:
+        self.load_weights_named("weight", weights)
+        if bias is not None and self.use_bias:
+            self.load_weights_named("bias", bias)
+
+
+DynamicConv2D = Conv2D
+
+
+class ConvTranspose2D(Layer):
+    """DynamicConvTranspose2D (DynamicConv2D.swift:598-959); weight [in, out/groups, kh, kw]."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1, padding=0,
+                 output_padding=0, dilation=1, groups=1, use_bias=True):
+        (kh, kw), (sh, sw), (ph, pw), (oph, opw), (dh, dw) = map(
+            _pair, (kernel_size, stride, padding, output_padding, dilation))
+        d = ConvTranspose2dDesc(input_channels, output_channels, kh, kw, sh, sw, ph, pw, oph, opw,
+                                dh, dw, groups, int(use_bias))
+        super().__init__(device, _create(lib().mnn_conv_transpose2d_create, device.handle,
+                                         C.byref(d)))
+        self.use_bias = use_bias
+
+    def load_weights(self, weights, bias=None) -> None:
+        self.load_weights_named("weight", weights)
+        if bias is not None and self.use_bias:
+            self.load_weights_named("bias", bias)
+
+
+DynamicConvTranspose2D = ConvTranspose2D
+
+
+class FreqUNetEncoderBlock2D(Layer):
+    """FreqUNetEncoderBlock2D (FreqUNet2D.swift:12-192): Conv2D (reflect padding (k-1)/2, stride)
+    -> GroupNorm -> GELU; the output is also the block's skip."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size=3, stride=2,
+                 num_groups=8):
+        (kh, kw), (sh, sw) = _pair(kernel_size), _pair(stride)
+        d = FreqBlockDesc(input_channels, 0, output_channels, kh, kw, sh, sw, num_groups)
+        super().__init__(device, _create(lib().mnn_freq_encoder_block_create, device.handle,
+                                         C.byref(d)))
+
+    def load_weights(self, conv_weight, conv_bias, norm_weight, norm_bias) -> None:
+        self.load_weights_named("conv.weight", conv_weight)
+        if conv_bias is not None:
+            self.load_weights_named("conv.bias", conv_bias)
+        self.load_weights_named("norm.weight", norm_weight)
+        self.load_weights_named("norm.bias", norm_bias)
+
+
+class FreqUNetDecoderBlock2D(UNetDecoderBlock):
+    """FreqUNetDecoderBlock2D (FreqUNet2D.swift:198-428): concat(input, skip) -> ConvTranspose2D
+    (padding (k-1)/2, output padding stride-1) -> GroupNorm -> GELU; forward(input, skip)."""
+
+    def __init__(self, device, input_channels, skip_channels, output_channels, kernel_size=3,
+                 stride=2, num_groups=8):
+        (kh, kw), (sh, sw) = _pair(kernel_size), _pair(stride)
+        d = FreqBlockDesc(input_channels, skip_channels, output_channels, kh, kw, sh, sw,
+                          num_groups)
+        Layer.__init__(self, device, _create(lib().mnn_freq_decoder_block_create, device.handle,
+                                             C.byref(d)))
+
+
+def unet_padding_2d(height: int, width: int, levels: int, stride: int = 2):
+    """UNetPaddingCalculator2D.calculatePadding (FreqUNet2D.swift:471-497): (top, bottom, left,
+    right, padded height, padded width)."""
+    out = (C.c_int64 * 6)()
+    check(lib().mnn_unet_padding_2d(height, width, levels, stride, out))
+    return tuple(out)
+
+
+def unet_bottleneck_2d(height: int, width: int, levels: int, stride: int = 2):
+    """UNetPaddingCalculator2D.bottleneckDimensions (FreqUNet2D.swift:500-512)."""
+    out = (C.c_int64 * 2)()
+    check(lib().mnn_unet_bottleneck_2d(height, width, levels, stride, out))
+    return tuple(out)
 
 
 ST_DTYPES = ["F32", "F16", "BF16", "I32", "I64", "I16", "I8", "U8", "BOOL"]

@@ -11,6 +11,8 @@ __all__ = [
     "stable_sigmoid", "glu", "activation", "linear", "mha", "feed_forward", "encoder_block",
     "time_encoder", "conv_transpose1d", "conv_transpose1d_gather", "decoder_block", "unet_padding",
     "unet_bottleneck_length", "time_unet", "transformer_layer", "cross_transformer",
+    "reflect_index", "conv2d", "conv2d_output_size", "conv_transpose2d", "freq_encoder_block",
+    "freq_decoder_block", "unet_padding_2d",
 ]
 
 SQRT_2_OVER_PI = 0.7978845608  # literal used by every reference GELU kernel
@@ -415,3 +417,145 @@ def cross_transformer(time, freq, p, num_layers, num_heads, dtype=np.float64):
             Fn = Fn + _as(p[pf + "gamma_2.scale"], dtype) * ffn(ln(Fn, pf + "norm3"), pf)
             T, F = Tn, Fn
     return T, F
+
+
+# ---------------------------------------------------------------- frequency branch (2-D)
+
+def reflect_index(i, n):
+    """Mirrored source index of padded position i - pad (applyReflectPadding2D,
+    DynamicConv2D.swift:441-470): i < 0 -> -i, i >= n -> 2n - i - 2, then clamped to [0, n)."""
+    i = np.asarray(i)
+    i = np.where(i < 0, -i, i)
+    i = np.where(i >= n, 2 * n - i - 2, i)
+    return np.clip(i, 0, n - 1)
+
+
+def conv2d_padding(H, W, kernel, stride, mode, pad, dilation):
+    """computePadding (DynamicConv2D.swift:212-238)."""
+    (kh, kw), (sh, sw), (dh, dw) = kernel, stride, dilation
+    if mode == "valid":
+        return 0, 0
+    if mode == "same":
+        ekh, ekw = (kh - 1) * dh + 1, (kw - 1) * dw + 1
+        oh, ow = -(-H // sh), -(-W // sw)
+        return max(0, (oh - 1) * sh + ekh - H) // 2, max(0, (ow - 1) * sw + ekw - W) // 2
+    return pad
+
+
+def conv2d_output_size(H, W, kernel, stride=(1, 1), mode="valid", pad=(0, 0), dilation=(1, 1)):
+    """outputSize(forHeight:width:) (DynamicConv2D.swift:193-205)."""
+    ph, pw = conv2d_padding(H, W, kernel, stride, mode, pad, dilation)
+    nh = H + 2 * ph - ((kernel[0] - 1) * dilation[0] + 1)
+    nw = W + 2 * pw - ((kernel[1] - 1) * dilation[1] + 1)
+    if nh < 0 or nw < 0:
+        return 0, 0
+    return nh // stride[0] + 1, nw // stride[1] + 1
+
+
+def conv2d(x, w, b=None, stride=(1, 1), mode="valid", pad=(0, 0), dilation=(1, 1), groups=1,
+           dtype=np.float64):
+    """y[oc][oh][ow] = bias[oc] + sum_{icg,kh,kw} xp[ic][oh*sh + kh*dh][ow*sw + kw*dw] * W[oc][icg][kh][kw]
+    over the padded input xp: zeros, or mirrored samples for mode "reflect" (the reference pads
+    first and runs the conv unpadded, DynamicConv2D.swift:309-383 and dynamic_conv2d_forward
+    :525-590). Input [C, H, W] or [B, C, H, W]; W is [Cout, Cin/groups, KH, KW]."""
+    x = _as(x, dtype)
+    w = _as(w, dtype)
+    squeeze = x.ndim == 3
+    if squeeze:
+        x = x[None]
+    B, Cin, H, W = x.shape
+    Cout, cinpg, KH, KW = w.shape
+    assert Cin == cinpg * groups and Cout % groups == 0
+    ph, pw = conv2d_padding(H, W, (KH, KW), stride, mode, pad, dilation)
+    Ho, Wo = conv2d_output_size(H, W, (KH, KW), stride, mode, pad, dilation)
+    if mode == "reflect":
+        ri = reflect_index(np.arange(H + 2 * ph) - ph, H)
+        ci = reflect_index(np.arange(W + 2 * pw) - pw, W)
+        xp = x[:, :, ri][:, :, :, ci]
+    else:
+        xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)))
+    y = np.zeros((B, Cout, Ho, Wo), dtype=dtype)
+    coutpg = Cout // groups
+    for g in range(groups):
+        xs = xp[:, g * cinpg:(g + 1) * cinpg]
+        ws = w[g * coutpg:(g + 1) * coutpg]
+        for kh in range(KH):
+            for kw in range(KW):
+                r0, c0 = kh * dilation[0], kw * dilation[1]
+                patch = xs[:, :, r0:r0 + (Ho - 1) * stride[0] + 1:stride[0],
+                           c0:c0 + (Wo - 1) * stride[1] + 1:stride[1]]
+                y[:, g * coutpg:(g + 1) * coutpg] += np.einsum("bchw,oc->bohw", patch,
+                                                              ws[:, :, kh, kw])
+    if b is not None:
+        y += _as(b, dtype)[None, :, None, None]
+    return y[0] if squeeze else y
+
+
+def conv_transpose2d(x, w, b=None, stride=(1, 1), padding=(0, 0), output_padding=(0, 0),
+                     dilation=(1, 1), groups=1, dtype=np.float64):
+    """Scatter form of dynamic_conv_transpose2d_forward (DynamicConv2D.swift:890-955): input
+    sample (ih, iw) of channel ic adds x * W[ic][ocg][kh][kw] to output (ih*sh - ph + kh*dh,
+    iw*sw - pw + kw*dw) when inside; output size from outputSize (:727-736). W is
+    [Cin, Cout/groups, KH, KW]; input [C, H, W] or [B, C, H, W]."""
+    x = _as(x, dtype)
+    w = _as(w, dtype)
+    squeeze = x.ndim == 3
+    if squeeze:
+        x = x[None]
+    B, Cin, H, W = x.shape
+    cin_w, coutpg, KH, KW = w.shape
+    assert cin_w == Cin and Cin % groups == 0
+    Cout, cinpg = coutpg * groups, Cin // groups
+    (sh, sw), (ph, pw), (oph, opw), (dh, dw) = stride, padding, output_padding, dilation
+    Ho = (H - 1) * sh - 2 * ph + dh * (KH - 1) + oph + 1
+    Wo = (W - 1) * sw - 2 * pw + dw * (KW - 1) + opw + 1
+    # full (uncropped) canvas, then crop the padding
+    Hf = max((H - 1) * sh + dh * (KH - 1) + 1, ph + Ho)
+    Wf = max((W - 1) * sw + dw * (KW - 1) + 1, pw + Wo)
+    full = np.zeros((B, Cout, Hf, Wf), dtype=dtype)
+    for g in range(groups):
+        xs = x[:, g * cinpg:(g + 1) * cinpg]
+        for kh in range(KH):
+            for kw in range(KW):
+                contrib = np.einsum("bchw,co->bohw", xs, w[g * cinpg:(g + 1) * cinpg, :, kh, kw])
+                full[:, g * coutpg:(g + 1) * coutpg, kh * dh:kh * dh + (H - 1) * sh + 1:sh,
+                     kw * dw:kw * dw + (W - 1) * sw + 1:sw] += contrib
+    y = full[:, :, ph:ph + Ho, pw:pw + Wo].copy()
+    if b is not None:
+        y += _as(b, dtype)[None, :, None, None]
+    return y[0] if squeeze else y
+
+
+def freq_encoder_block(x, conv_w, conv_b, norm_w, norm_b, num_groups, kernel=(3, 3),
+                       stride=(2, 2), dtype=np.float64):
+    """FreqUNetEncoderBlock2D.forward (FreqUNet2D.swift:84-117): Conv2D with reflect padding
+    ((k-1)//2 per axis, :52-64) -> GroupNorm over [C, H*W] -> tanh-GELU."""
+    pad = ((kernel[0] - 1) // 2, (kernel[1] - 1) // 2)
+    y = conv2d(x, conv_w, conv_b, stride=stride, mode="reflect", pad=pad, dtype=dtype)
+    shp = y.shape
+    y = y.reshape(shp[:-2] + (shp[-2] * shp[-1],))
+    y = gelu_tanh(group_norm(y, num_groups, norm_w, norm_b, dtype=dtype), dtype)
+    return y.reshape(shp)
+
+
+def freq_decoder_block(x, skip, convt_w, convt_b, norm_w, norm_b, num_groups, kernel=(3, 3),
+                       stride=(2, 2), dtype=np.float64):
+    """FreqUNetDecoderBlock2D.forward (FreqUNet2D.swift:281-306): concat over channels ->
+    ConvTranspose2D (padding (k-1)//2, output padding stride-1, :245-260) -> GroupNorm ->
+    tanh-GELU."""
+    cat = np.concatenate([_as(x, dtype), _as(skip, dtype)], axis=-3)
+    pad = ((kernel[0] - 1) // 2, (kernel[1] - 1) // 2)
+    y = conv_transpose2d(cat, convt_w, convt_b, stride=stride, padding=pad,
+                         output_padding=(stride[0] - 1, stride[1] - 1), dtype=dtype)
+    shp = y.shape
+    y = y.reshape(shp[:-2] + (shp[-2] * shp[-1],))
+    y = gelu_tanh(group_norm(y, num_groups, norm_w, norm_b, dtype=dtype), dtype)
+    return y.reshape(shp)
+
+
+def unet_padding_2d(H, W, levels, stride):
+    """UNetPaddingCalculator2D.calculatePadding (FreqUNet2D.swift:471-497)."""
+    div = stride ** levels
+    th = 0 if H % div == 0 else div - H % div
+    tw = 0 if W % div == 0 else div - W % div
+    return th // 2, th - th // 2, tw // 2, tw - tw // 2, H + th, W + tw

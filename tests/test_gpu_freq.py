@@ -1,0 +1,213 @@
+"""GPU parity of the frequency-branch layers (DynamicConv2D, DynamicConvTranspose2D,
+FreqUNetEncoderBlock2D / DecoderBlock2D) through the C ABI: the reference's own fixtures, then
+the fp64 oracle on seeded inputs over the kernel forms (unfold + matrix-core GEMM, pointwise
+GEMM, direct kernels for grouped convs, tap GEMM + gather for the transposed conv, the decoder's
+concat as a second GEMM) and at the HTDemucs frequency-encoder shapes.
+
+fp32 bar: |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| per element (the reference's
+Conv2DValidationTests / HTDemucsValidationTests tolerance)."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from metalaudio_amd import nn
+from tests.conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+ATOL, RTOL = 1e-4, 1e-3
+RNG = np.random.default_rng(17)
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return nn.AudioDevice(0)
+
+
+@pytest.fixture(scope="module")
+def stream(dev):
+    return nn.Stream(dev)
+
+
+def run_layer(layer, x, dev, stream):
+    out = layer(nn.Tensor.from_numpy(dev, np.ascontiguousarray(x, np.float32)), stream)
+    stream.sync(60000)
+    return out.to_numpy()
+
+
+def scaled(shape, fan_in):
+    return (RNG.standard_normal(shape) / np.sqrt(fan_in)).astype(np.float32)
+
+
+@pytest.mark.parametrize("name", ["1x1_pointwise", "3x3_asymmetric_input", "3x3_no_bias",
+                                  "3x3_same_padding", "3x3_stride2_htdemucs",
+                                  "basic_3x3_no_padding", "identity_like", "conv_transpose_basic",
+                                  "conv_transpose_htdemucs"])
+def test_conv2d_reference_fixtures(dev, stream, golden_dir, name):
+    z = np.load(golden_dir / "conv2d_reference.npz")
+    x, w, want = z[f"{name}/input"], z[f"{name}/weight"], z[f"{name}/output"]
+    b = z[f"{name}/bias"] if f"{name}/bias" in z.files else None
+    cin, cout, kh, kw, sh, sw, ph, pw, oph, opw, dh, dw, g, transposed = (int(v) for v in
+                                                                        z[f"{name}/config"])
+    say(f"Conv2DReference {name}")
+    if transposed:
+        layer = nn.ConvTranspose2D(dev, cin, cout, (kh, kw), (sh, sw), (ph, pw), (oph, opw),
+                                   (dh, dw), g, use_bias=b is not None)
+    else:
+        layer = nn.Conv2D(dev, cin, cout, (kh, kw), (sh, sw), "explicit", (ph, pw), (dh, dw), g,
+                          use_bias=b is not None)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    assert got.shape == want.shape
+    assert_close(got, want, ATOL, RTOL, name)
+
+
+@pytest.mark.parametrize("level", [0, 1])
+def test_freq_encoder_fixtures(dev, stream, golden_dir, level):
+    z = np.load(golden_dir / f"freq_encoder_level{level}.npz")
+    cin, cout, kh, kw, sh, sw, groups = (int(v) for v in z["config"])
+    say(f"freq encoder fixture level {level}")
+    blk = nn.FreqUNetEncoderBlock2D(dev, cin, cout, (kh, kw), (sh, sw), groups)
+    blk.load_weights(z["conv_weight"], z["conv_bias"], z["norm_weight"], z["norm_bias"])
+    got = run_layer(blk, z["input"], dev, stream)
+    assert_close(got, z["output"], ATOL, RTOL, f"freq encoder level {level}")
+    # the same block on a batch of two (the second sample scaled) matches per sample
+    xb = np.stack([z["input"], 0.5 * z["input"]])
+    gotb = run_layer(blk, xb, dev, stream)
+    ref1 = oracle.freq_encoder_block(xb[1], z["conv_weight"], z["conv_bias"], z["norm_weight"],
+                                     z["norm_bias"], groups, (kh, kw), (sh, sw))
+    assert_close(gotb[0], z["output"], ATOL, RTOL, "batch sample 0")
+    assert_close(gotb[1], ref1, ATOL, RTOL, "batch sample 1")
+
+
+CONV_CASES = [
+    # B, cin, cout, H, W, k, s, mode, pad, dil, groups
+    (2, 4, 48, 64, 32, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),     # unfold + GEMM
+    (1, 48, 96, 32, 16, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),
+    (1, 4, 48, 256, 40, (8, 1), (4, 1), "reflect", (3, 0), (1, 1), 1),   # HTDemucs (8,1)/(4,1)
+    (2, 3, 5, 17, 13, (3, 2), (2, 1), "explicit", (1, 1), (1, 2), 1),
+    (1, 6, 10, 9, 11, (3, 3), (1, 1), "same", (0, 0), (1, 1), 1),
+    (1, 5, 7, 12, 10, (2, 2), (1, 1), "same", (0, 0), (1, 1), 1),          # even kernel "same"
+    (1, 8, 4, 10, 9, (3, 3), (1, 1), "valid", (0, 0), (2, 1), 1),
+    (2, 48, 16, 16, 8, (1, 1), (1, 1), "valid", (0, 0), (1, 1), 1),        # pointwise GEMM
+    (1, 37, 19, 9, 7, (1, 1), (1, 1), "valid", (0, 0), (1, 1), 1),         # pointwise, odd sizes
+    (2, 8, 12, 9, 8, (3, 3), (2, 1), "explicit", (1, 0), (1, 1), 4),       # grouped: direct
+    (1, 6, 6, 12, 12, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 6),        # depthwise: direct
+]
+
+
+@pytest.mark.parametrize("B,cin,cout,H,W,k,s,mode,pad,d,g", CONV_CASES)
+def test_conv2d_parity(dev, stream, B, cin, cout, H, W, k, s, mode, pad, d, g):
+    say(f"conv2d B={B} {cin}->{cout} {H}x{W} k={k} s={s} {mode} pad={pad} d={d} g={g}")
+    x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
+    w = scaled((cout, cin // g, *k), cin // g * k[0] * k[1])
+    b = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    layer = nn.Conv2D(dev, cin, cout, k, s, mode, pad, d, g)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    ref = oracle.conv2d(x, w, b, s, mode, pad, d, g)
+    assert got.shape == ref.shape
+    assert_close(got, ref, ATOL, RTOL, "conv2d")
+
+
+CONVT_CASES = [
+    # B, c1, c2, cout, H, W, k, s, p, op, dil, groups
+    (1, 96, 0, 48, 8, 4, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),      # tap GEMM + gather
+    (2, 48, 48, 24, 16, 8, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),    # concat: second GEMM
+    (1, 96, 0, 48, 32, 40, (8, 1), (4, 1), (2, 0), (0, 0), (1, 1), 1),    # HTDemucs decoder form
+    (1, 5, 3, 7, 6, 5, (3, 3), (2, 3), (1, 1), (1, 2), (1, 1), 1),        # odd channel concat
+    (1, 7, 0, 5, 6, 5, (3, 4), (2, 3), (1, 2), (1, 2), (1, 1), 1),        # odd sizes
+    (2, 6, 0, 4, 5, 6, (3, 3), (1, 2), (0, 1), (0, 1), (2, 1), 1),        # dilation
+    (2, 8, 0, 6, 5, 4, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 2),        # grouped: direct
+]
+
+
+@pytest.mark.parametrize("B,c1,c2,cout,H,W,k,s,p,op,d,g", CONVT_CASES)
+def test_conv_transpose2d_parity(dev, stream, B, c1, c2, cout, H, W, k, s, p, op, d, g):
+    say(f"conv_transpose2d B={B} {c1}+{c2}->{cout} {H}x{W} k={k} s={s} p={p} op={op} d={d} g={g}")
+    cin = c1 + c2
+    x1 = RNG.standard_normal((B, c1, H, W)).astype(np.float32)
+    x2 = RNG.standard_normal((B, c2, H, W)).astype(np.float32)
+    w = scaled((cin, cout // g, *k), cin)
+    b = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    ref = oracle.conv_transpose2d(np.concatenate([x1, x2], 1), w, b, s, p, op, d, g)
+    if c2 == 0:
+        layer = nn.ConvTranspose2D(dev, cin, cout, k, s, p, op, d, g)
+        layer.load_weights(w, b)
+        got = run_layer(layer, x1, dev, stream)
+    else:
+        # the concat form is exercised through the decoder block's conv (no norm): check the
+        # block against the oracle of the same concat instead
+        gm, bt = np.ones(cout, np.float32), np.zeros(cout, np.float32)
+        blk = nn.FreqUNetDecoderBlock2D(dev, c1, c2, cout, k, s, 1)
+        assert p == ((k[0] - 1) // 2, (k[1] - 1) // 2) and op == (s[0] - 1, s[1] - 1)
+        blk.load_weights(w, b, gm, bt)
+        out = blk.forward_alloc(nn.Tensor.from_numpy(dev, x1), nn.Tensor.from_numpy(dev, x2),
+                                stream)
+        stream.sync(60000)
+        got = out.to_numpy()
+        sh = ref.shape
+        ref = oracle.gelu_tanh(oracle.group_norm(ref.reshape(B, cout, -1), 1, gm, bt)).reshape(sh)
+    assert got.shape == ref.shape
+    assert_close(got, ref, ATOL, RTOL, "conv_transpose2d")
+
+
+@pytest.mark.parametrize("B,cin,cskip,cout,H,W,groups", [(1, 96, 96, 48, 8, 4, 8),
+                                                         (2, 16, 16, 8, 12, 10, 4),
+                                                         (1, 7, 0, 5, 6, 6, 1)])
+def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, groups):
+    say(f"freq decoder block B={B} {cin}+{cskip}->{cout} {H}x{W} G={groups}")
+    x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
+    sk = RNG.standard_normal((B, cskip, H, W)).astype(np.float32)
+    w = scaled((cin + cskip, cout, 3, 3), cin + cskip)
+    b = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    blk = nn.FreqUNetDecoderBlock2D(dev, cin, cskip, cout, 3, 2, groups)
+    blk.load_weights(w, b, gm, bt)
+    out = blk.forward_alloc(nn.Tensor.from_numpy(dev, x), nn.Tensor.from_numpy(dev, sk), stream)
+    stream.sync(60000)
+    ref = oracle.freq_decoder_block(x, sk, w, b, gm, bt, groups)
+    assert out.shape == ref.shape == (B, cout, 2 * H, 2 * W)
+    assert_close(out.to_numpy(), ref, ATOL, RTOL, "freq decoder block")
+
+
+def test_freq_encoder_htdemucs_level_shapes(dev, stream):
+    """HTDemucs' first two frequency levels at a 336-frame chunk: (8,1) kernels, (4,1) strides,
+    4 -> 48 -> 96 channels over 2048 -> 512 -> 128 bins."""
+    x = RNG.standard_normal((1, 4, 2048, 336)).astype(np.float32)
+    for cin, cout in ((4, 48), (48, 96)):
+        say(f"HTDemucs freq level {cin}->{cout} input {x.shape}")
+        w = scaled((cout, cin, 8, 1), cin * 8)
+        b = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+        gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+        bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+        blk = nn.FreqUNetEncoderBlock2D(dev, cin, cout, (8, 1), (4, 1), 8)
+        blk.load_weights(w, b, gm, bt)
+        got = run_layer(blk, x, dev, stream)
+        ref = oracle.freq_encoder_block(x, w, b, gm, bt, 8, (8, 1), (4, 1))
+        assert_close(got, ref, ATOL, RTOL, f"freq level {cin}->{cout}")
+        x = got
+
+
+def test_freq_layers_reject_bad_inputs(dev, stream):
+    with pytest.raises(nn.MNNError):
+        nn.Conv2D(dev, 6, 4, 3, groups=4)  # 6 channels not divisible by 4 groups
+    conv = nn.Conv2D(dev, 2, 4, 3)
+    with pytest.raises(nn.MNNError):
+        conv(nn.Tensor.from_numpy(dev, np.zeros((1, 3, 8, 8), np.float32)), stream)
+    with pytest.raises(nn.MNNError):
+        conv(nn.Tensor.from_numpy(dev, np.zeros((1, 2, 2, 8), np.float32)), stream)  # no rows
+    with pytest.raises(nn.MNNError):
+        conv.load_weights_named("weight", np.zeros(7, np.float32))
+    blk = nn.FreqUNetDecoderBlock2D(dev, 8, 8, 4, 3, 2, 2)
+    x = nn.Tensor.from_numpy(dev, np.zeros((1, 8, 4, 4), np.float32))
+    sk = nn.Tensor.from_numpy(dev, np.zeros((1, 8, 4, 5), np.float32))
+    with pytest.raises(nn.MNNError):
+        blk.forward(x, sk, nn.Tensor(dev, (1, 4, 8, 8)), stream)
