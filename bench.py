@@ -240,6 +240,74 @@ def decoder_oracle(oracle, dec):
     return y
 
 
+# Frequency branch as the reference's HTDemucs builds it (HTDemucs.swift:295-331): stereo
+# magnitude spectrogram of a 7.8 s chunk, nfft 4096 -> 2049 bins padded to 2064 (a multiple of
+# 2^4, UNetPaddingCalculator2D) x 336 frames; 3x3 kernels, stride (2, 2), channels
+# 2 -> 48 -> 96 -> 192 -> 384, GroupNorm min(8, C) groups; decoders mirror with skips.
+FREQ_CH = [2, 48, 96, 192, 384]
+FREQ_BINS, FREQ_FRAMES = 2064, 336
+
+
+def freq_setup(nn, dev):
+    """FreqUNetEncoderBlock2D levels down and FreqUNetDecoderBlock2D levels back up (skips of
+    the encoder's shapes), seeded synthetic weights and inputs."""
+    r = np.random.default_rng(1007)
+    enc = {"blocks": [], "outs": [], "params": [], "flops": 0.0}
+    dec = {"blocks": [], "skips": [], "outs": [], "params": [], "flops": 0.0}
+    H, W = FREQ_BINS, FREQ_FRAMES
+    x = r.standard_normal((1, FREQ_CH[0], H, W)).astype(np.float32)
+    dims = []
+    for i in range(4):
+        cin, cout = FREQ_CH[i], FREQ_CH[i + 1]
+        g = min(8, cin) if i == 0 else 8
+        g = min(8, cout) if cout < 8 else g
+        w = (r.standard_normal((cout, cin, 3, 3)) * np.sqrt(2.0 / (9 * cin))).astype(np.float32)
+        b = np.zeros(cout, np.float32)
+        gm, bt = np.ones(cout, np.float32), np.zeros(cout, np.float32)
+        blk = nn.FreqUNetEncoderBlock2D(dev, cin, cout, 3, 2, g)
+        blk.load_weights(w, b, gm, bt)
+        dims.append((H // 2, W // 2))
+        enc["blocks"].append(blk)
+        enc["outs"].append(nn.Tensor(dev, (1, cout, H // 2, W // 2)))
+        enc["params"].append((w, b, gm, bt, g))
+        enc["flops"] += 2.0 * cout * cin * 9 * (H // 2) * (W // 2)
+        H, W = H // 2, W // 2
+    for i in reversed(range(4)):
+        cin, cout = FREQ_CH[i + 1], FREQ_CH[i]
+        g = min(8, cout)
+        h, w_ = dims[i]
+        w = (r.standard_normal((2 * cin, cout, 3, 3)) * np.sqrt(2.0 / (2 * cin * 9 / 4))).astype(
+            np.float32)
+        b = np.zeros(cout, np.float32)
+        gm, bt = np.ones(cout, np.float32), np.zeros(cout, np.float32)
+        sk = r.standard_normal((1, cin, h, w_)).astype(np.float32)
+        blk = nn.FreqUNetDecoderBlock2D(dev, cin, cin, cout, 3, 2, g)
+        blk.load_weights(w, b, gm, bt)
+        dec["blocks"].append(blk)
+        dec["skips"].append(nn.Tensor.from_numpy(dev, sk))
+        dec["outs"].append(nn.Tensor(dev, (1, cout, 2 * h, 2 * w_)))
+        dec["params"].append((w, b, gm, bt, g, sk))
+        dec["flops"] += 2.0 * 2 * cin * cout * 9 * h * w_
+    enc["x"], enc["x_host"] = nn.Tensor.from_numpy(dev, x), x
+    xd = r.standard_normal((1, FREQ_CH[-1], H, W)).astype(np.float32)
+    dec["x"], dec["x_host"] = nn.Tensor.from_numpy(dev, xd), xd
+    return enc, dec
+
+
+def freq_encoder_oracle(oracle, enc):
+    y = enc["x_host"]
+    for w, b, gm, bt, g in enc["params"]:
+        y = oracle.freq_encoder_block(y, w, b, gm, bt, g, dtype=np.float32)
+    return y
+
+
+def freq_decoder_oracle(oracle, dec):
+    y = dec["x_host"]
+    for w, b, gm, bt, g, sk in dec["params"]:
+        y = oracle.freq_decoder_block(y, sk, w, b, gm, bt, g, dtype=np.float32)
+    return y
+
+
 def config_table(nn, W, dev, stream, m, cpu=True):
     """GPU ms, achieved rate and roofline fraction of each BASELINE configuration, with the fp32
     oracle's CPU time on the host beside it (the oracle is only the CPU baseline here)."""
@@ -331,6 +399,25 @@ def config_table(nn, W, dev, stream, m, cpu=True):
             y = out
     cpu6 = time_cpu(lambda: decoder_oracle(oracle, dec), max_reps=1) if cpu else None
     row("6_time_decoder_b1", time_gpu(f6, stream, 10), flops=dec["flops"], cpu_ms=cpu6)
+    # frequency branch (next rows): the four 2-D encoder levels and the four decoder levels of
+    # the reference's HTDemucs at one chunk's spectrogram (synthetic inputs and skips)
+    fenc, fdec = freq_setup(nn, dev)
+
+    def f7():
+        y = fenc["x"]
+        for blk, out in zip(fenc["blocks"], fenc["outs"]):
+            blk.forward(y, out, stream)
+            y = out
+
+    def f8():
+        y = fdec["x"]
+        for blk, sk, out in zip(fdec["blocks"], fdec["skips"], fdec["outs"]):
+            blk.forward(y, sk, out, stream)
+            y = out
+    cpu7 = time_cpu(lambda: freq_encoder_oracle(oracle, fenc), max_reps=1) if cpu else None
+    cpu8 = time_cpu(lambda: freq_decoder_oracle(oracle, fdec), max_reps=1) if cpu else None
+    row("7_freq_encoder_b1", time_gpu(f7, stream, 10), flops=fenc["flops"], cpu_ms=cpu7)
+    row("8_freq_decoder_b1", time_gpu(f8, stream, 10), flops=fdec["flops"], cpu_ms=cpu8)
     t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
     q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
     to5, fo5 = nn.Tensor(dev, t5.shape), nn.Tensor(dev, q5.shape)

@@ -16,8 +16,8 @@
 //   y[oc][oh][ow] = bias[oc] + sum x[ic][ih][iw] * W[ic][ocg][kh][kw] over the (ic, kh, kw) with
 //   oh + ph - kh*dh = ih*sh and ow + pw - kw*dw = iw*sw exactly, 0 <= ih < H, 0 <= iw < W.
 // Matrix-core form (groups 1): Z[(oc, kh, kw)][(ih, iw)] = sum_ic W[ic][oc][kh][kw] x[ic][ih][iw]
-// is a GEMM with the input as its [K][N] operand (the decoder's channel concat becomes a second
-// GEMM accumulating into Z), then convt2d_gather_kernel sums the taps that land on each output
+// is a GEMM with the input as its [K][N] operand (the decoder's channel concat is copied into one
+// operand first, so the GEMM runs over all of K), then convt2d_gather_kernel sums the taps that land on each output
 // (KH*KW / (sh*sw) of them on average) and adds the bias. No atomics; fixed summation order.
 #include "device_utils.hpp"
 #include "kernels.hpp"
@@ -46,15 +46,16 @@ __device__ __forceinline__ float conv2d_sample(const float* xc, int r, int s, in
 
 // U[b][n][k] for n = oh*Wo + ow, k = (ic, kh, kw) < K, zero for K <= k < Kp; four k per thread
 // (one 16-byte store).
+// Index math is 32-bit (the host checks N * Kp / 4 < 2^31).
 __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
-  const int64_t N = (int64_t)a.Ho * a.Wo;
-  const int kq = a.Kp / 4;
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const unsigned N = (unsigned)a.Ho * (unsigned)a.Wo;
+  const unsigned kq = (unsigned)a.Kp / 4;
+  const unsigned e = blockIdx.x * 256u + threadIdx.x;
   if (e >= N * kq) return;
   const int b = blockIdx.y;
-  const int64_t n = e / kq;
-  const int k0 = (int)(e % kq) * 4;
-  const int oh = (int)(n / a.Wo), ow = (int)(n % a.Wo);
+  const unsigned n = e / kq;
+  const int k0 = (int)(e - n * kq) * 4;
+  const int oh = (int)(n / (unsigned)a.Wo), ow = (int)(n - (unsigned)oh * a.Wo);
   const int ks = a.KH * a.KW, K = a.Cin * ks;
   const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
   float v[4];
@@ -72,12 +73,14 @@ __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
       make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Grid (output plane / 256, Cout, B); 32-bit plane index (host-checked).
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(Conv2DArgs a) {
-  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= per_b * a.B) return;
-  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
-  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
+  const unsigned n = blockIdx.x * 256u + threadIdx.x;
+  if (n >= hw) return;
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int oh = (int)(n / (unsigned)a.Wo), ow = (int)(n - (unsigned)oh * a.Wo);
+  const int64_t idx = ((int64_t)b * a.Cout + oc) * hw + n;
   const int cinpg = a.Cin / a.groups, coutpg = a.Cout / a.groups, g = oc / coutpg;
   const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
   float sum = 0.f;
@@ -97,11 +100,12 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(Conv2DArgs a) {
 // y[b][oc][oh][ow] = bias[oc] + the taps of Z[b][(oc*KH + kh)*KW + kw][ih*W + iw] that reach it,
 // summed in (kh, kw) order.
 __global__ __launch_bounds__(256) void convt2d_gather_kernel(ConvT2DArgs a) {
-  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= per_b * a.B) return;
-  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
-  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
+  const unsigned n = blockIdx.x * 256u + threadIdx.x;
+  if (n >= hw) return;
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int oh = (int)(n / (unsigned)a.Wo), ow = (int)(n - (unsigned)oh * a.Wo);
+  const int64_t idx = ((int64_t)b * a.Cout + oc) * hw + n;
   const int64_t n_in = (int64_t)a.H * a.W;
   const float* zb = a.z + ((int64_t)b * a.Cout + oc) * a.KH * a.KW * n_in;
   float sum = 0.f;
@@ -123,11 +127,12 @@ __global__ __launch_bounds__(256) void convt2d_gather_kernel(ConvT2DArgs a) {
 }
 
 __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
-  const int64_t hw = (int64_t)a.Ho * a.Wo, per_b = (int64_t)a.Cout * hw;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= per_b * a.B) return;
-  const int b = (int)(idx / per_b), oc = (int)((idx % per_b) / hw);
-  const int oh = (int)((idx % hw) / a.Wo), ow = (int)(idx % a.Wo);
+  const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
+  const unsigned n = blockIdx.x * 256u + threadIdx.x;
+  if (n >= hw) return;
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int oh = (int)(n / (unsigned)a.Wo), ow = (int)(n - (unsigned)oh * a.Wo);
+  const int64_t idx = ((int64_t)b * a.Cout + oc) * hw + n;
   const int Cin = a.C1 + a.C2;
   const int coutpg = a.Cout / a.groups, cinpg = Cin / a.groups;
   const int g = oc / coutpg, ocg = oc % coutpg;
@@ -154,6 +159,39 @@ __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
   }
   if (a.bias) sum += a.bias[oc];
   a.y[idx] = sum;
+}
+
+// cat[b] = [x1[b] (C1 rows); x2[b] (C2 rows)], rows of n floats; four floats per thread when
+// n % 4 == 0 (16-byte rows).
+__global__ __launch_bounds__(256) void concat2_kernel(const float* __restrict__ x1,
+                                                      const float* __restrict__ x2,
+                                                      float* __restrict__ cat, int C1, int C2,
+                                                      unsigned n, bool vec) {
+  const int b = blockIdx.y;
+  const unsigned C = (unsigned)(C1 + C2);
+  const unsigned per = vec ? C * (n / 4) : C * n;
+  const unsigned e = blockIdx.x * 256u + threadIdx.x;
+  if (e >= per) return;
+  float* dst = cat + (int64_t)b * C * n;
+  if (vec) {
+    const unsigned q = n / 4, c = e / q, j = e - c * q;
+    const float* src = (int)c < C1 ? x1 + ((int64_t)b * C1 + c) * n
+                                   : x2 + ((int64_t)b * C2 + (c - C1)) * n;
+    reinterpret_cast<float4*>(dst + (int64_t)c * n)[j] = reinterpret_cast<const float4*>(src)[j];
+  } else {
+    const unsigned c = e / n, j = e - c * n;
+    const float* src = (int)c < C1 ? x1 + ((int64_t)b * C1 + c) * n
+                                   : x2 + ((int64_t)b * C2 + (c - C1)) * n;
+    dst[(int64_t)c * n + j] = src[j];
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+dim3 plane_grid(int64_t hw, int C, int B) {
+  MNN_REQUIRE(hw > 0 && hw < (1LL << 31) && C > 0 && C <= 65535 && B > 0 && B <= 65535,
+              MNN_ERR_INVALID_ARGUMENT, "2-D conv: output plane / channel / batch count too large");
+  return dim3((unsigned)cdiv(hw, 256), (unsigned)C, (unsigned)B);
 }
 
 void check_conv2d(const Conv2DArgs& a) {
@@ -229,6 +267,8 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
   MNN_REQUIRE(unfold, MNN_ERR_INVALID_ARGUMENT, "conv2d_gemm: unfold buffer required");
   a.Kp = conv2d_padded_k(a.Cin, a.KH, a.KW);
   a.u = unfold;
+  MNN_REQUIRE(N * (a.Kp / 4) < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
+              "conv2d_gemm: unfold too large");
   launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel,
          dim3((unsigned)cdiv(N * (a.Kp / 4), 256), (unsigned)a.B), dim3(256), 0, a);
   g.K = a.Kp;
@@ -242,9 +282,8 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
 
 void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a) {
   check_conv2d(a);
-  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
-  launch(c, "conv2d_direct_f32", conv2d_direct_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256), 0,
-         a);
+  launch(c, "conv2d_direct_f32", conv2d_direct_kernel,
+         plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, a);
 }
 
 int convt2d_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
@@ -262,52 +301,55 @@ void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, flo
       out[(int64_t)m * Cp + ic] = ic < Cin ? w[((int64_t)ic * Cout + m / ks) * ks + m % ks] : 0.f;
 }
 
-void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z) {
+void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
+                  float* cat) {
   check_convt2d(a);
-  MNN_REQUIRE(convt2d_gemm_supported(a) && wpack && z, MNN_ERR_INVALID_ARGUMENT,
-              "convt2d_gemm: configuration outside the GEMM form");
+  MNN_REQUIRE(convt2d_gemm_supported(a) && wpack && z && (a.C2 == 0 || cat),
+              MNN_ERR_INVALID_ARGUMENT, "convt2d_gemm: configuration outside the GEMM form");
   const int64_t n_in = (int64_t)a.H * a.W;
-  MNN_REQUIRE(n_in < (1LL << 31), MNN_ERR_INVALID_ARGUMENT, "convt2d_gemm: input plane too large");
+  const int Cin = a.C1 + a.C2;
+  MNN_REQUIRE(n_in * Cin < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
+              "convt2d_gemm: input too large");
+  const float* x = a.x1;
+  if (a.C2 > 0) {  // the decoder's channel concat, one pass, so the GEMM runs over all of K
+    const bool vec = n_in % 4 == 0 && aligned16(a.x1) && aligned16(a.x2) && aligned16(cat);
+    const int64_t per = vec ? Cin * (n_in / 4) : Cin * n_in;
+    launch(c, "concat2_f32", concat2_kernel, dim3((unsigned)cdiv(per, 256), (unsigned)a.B),
+           dim3(256), 0, a.x1, a.x2, cat, a.C1, a.C2, (unsigned)n_in, vec);
+    x = cat;
+  }
   const int ks = a.KH * a.KW;
   GemmArgs g;
   g.M = a.Cout * ks;
   g.N = (int)n_in;
+  g.K = Cin;
   g.batch = a.B;
-  g.lda = convt2d_padded_cin(a.C1 + a.C2);
+  g.A = wpack;
+  g.lda = convt2d_padded_cin(Cin);
+  g.B = x;
   g.blayout = B_KN;
   g.ldb = n_in;
+  g.sB = (int64_t)Cin * n_in;
   g.C = z;
   g.ldc = n_in;
   g.sC = (int64_t)g.M * n_in;
   g.name = "convt2d_f32_mfma";
-  g.A = wpack;
-  g.K = a.C1;
-  g.B = a.x1;
-  g.sB = (int64_t)a.C1 * n_in;
   gemm(c, g);
-  if (a.C2 > 0) {  // the concatenated channels: Z += W[:, C1:] * x2
-    g.A = wpack + a.C1;
-    g.K = a.C2;
-    g.B = a.x2;
-    g.sB = (int64_t)a.C2 * n_in;
-    g.R = z;
-    g.ldr = n_in;
-    g.sR = g.sC;
-    gemm(c, g);
-  }
   ConvT2DArgs t = a;
   t.z = z;
-  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
-  launch(c, "convt2d_gather_f32", convt2d_gather_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256),
-         0, t);
+  launch(c, "convt2d_gather_f32", convt2d_gather_kernel,
+         plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, t);
+}
+
+int64_t convt2d_cat_floats(const ConvT2DArgs& a) {
+  return a.C2 > 0 ? (int64_t)a.B * (a.C1 + a.C2) * a.H * a.W : 0;
 }
 
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a) {
   check_convt2d(a);
   MNN_REQUIRE(a.w, MNN_ERR_INVALID_ARGUMENT, "convt2d_direct: weights required");
-  const int64_t n = (int64_t)a.B * a.Cout * a.Ho * a.Wo;
-  launch(c, "convt2d_direct_f32", convt2d_direct_kernel, dim3((unsigned)cdiv(n, 256)), dim3(256),
-         0, a);
+  launch(c, "convt2d_direct_f32", convt2d_direct_kernel,
+         plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, a);
 }
 
 }  // namespace k

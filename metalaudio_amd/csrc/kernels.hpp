@@ -167,12 +167,15 @@ struct ConvT2DArgs {
   const float* z = nullptr;  // GEMM form: tap products [B][Cout*KH*KW][H*W] (set by convt2d_gemm)
 };
 // Matrix-core form (groups 1): weights packed [Cout*KH*KW][convt2d_padded_cin] by
-// convt2d_pack_weights; tap-product workspace of convt2d_z_floats floats.
+// convt2d_pack_weights; tap-product workspace of convt2d_z_floats floats and, with a second
+// input, a concat workspace of convt2d_cat_floats floats.
 int convt2d_padded_cin(int Cin);
 bool convt2d_gemm_supported(const ConvT2DArgs& a);
 int64_t convt2d_z_floats(const ConvT2DArgs& a);
+int64_t convt2d_cat_floats(const ConvT2DArgs& a);
 void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, float* out);
-void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z);
+void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
+                  float* cat);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
 
 // ------------------------------------------------------------------ transposed conv (k_convt.hip)

@@ -1371,7 +1371,9 @@ class ConvTranspose2DLayer : public Layer {
     a.y = y;
     if (gemm_) {
       z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
-      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32());
+      const int64_t cf = k::convt2d_cat_floats(a);
+      if (cf > 0) cat_.reserve(sizeof(float) * cf);
+      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), cf > 0 ? cat_.f32() : nullptr);
     } else {
       k::convt2d_direct(ctx(s), a);
     }
@@ -1396,7 +1398,7 @@ class ConvTranspose2DLayer : public Layer {
   Param* w_ = nullptr;
   Param* b_ = nullptr;
   bool gemm_ = false;
-  DevBuf wpack_, z_;
+  DevBuf wpack_, z_, cat_;
 };
 
 // FreqUNetEncoderBlock2D (FreqUNet2D.swift:12-192): Conv2D (reflect padding ((k-1)/2 per axis),

@@ -485,7 +485,7 @@ def conv2d(x, w, b=None, stride=(1, 1), mode="valid", pad=(0, 0), dilation=(1, 1
                 patch = xs[:, :, r0:r0 + (Ho - 1) * stride[0] + 1:stride[0],
                            c0:c0 + (Wo - 1) * stride[1] + 1:stride[1]]
                 y[:, g * coutpg:(g + 1) * coutpg] += np.einsum("bchw,oc->bohw", patch,
-                                                              ws[:, :, kh, kw])
+                                                              ws[:, :, kh, kw], optimize=True)
     if b is not None:
         y += _as(b, dtype)[None, :, None, None]
     return y[0] if squeeze else y
@@ -517,7 +517,8 @@ def conv_transpose2d(x, w, b=None, stride=(1, 1), padding=(0, 0), output_padding
         xs = x[:, g * cinpg:(g + 1) * cinpg]
         for kh in range(KH):
             for kw in range(KW):
-                contrib = np.einsum("bchw,co->bohw", xs, w[g * cinpg:(g + 1) * cinpg, :, kh, kw])
+                contrib = np.einsum("bchw,co->bohw", xs, w[g * cinpg:(g + 1) * cinpg, :, kh, kw],
+                                    optimize=True)
                 full[:, g * coutpg:(g + 1) * coutpg, kh * dh:kh * dh + (H - 1) * sh + 1:sh,
                      kw * dw:kw * dw + (W - 1) * sw + 1:sw] += contrib
     y = full[:, :, ph:ph + Ho, pw:pw + Wo].copy()
