@@ -269,6 +269,33 @@ mnn_status mnn_unet_padding_2d(int64_t height, int64_t width, int levels, int st
 mnn_status mnn_unet_bottleneck_2d(int64_t height, int64_t width, int levels, int stride,
                                   int64_t out[2]);
 
+/* STFT / iSTFT (STFT.swift:20-533 over FFT.swift): frames of fft_size samples every hop_size
+ * samples (no centring), window applied, full DFT without scaling; spectra [B?, frames, bins]
+ * (layout 0, STFTResult's order) or [B?, bins, frames] (layout 1, the frequency branch's
+ * spectrogram), bins = fft_size/2 + 1 (onesided) or fft_size. The inverse takes the real part of
+ * each frame's inverse DFT (1/N), windows it, overlap-adds and divides by the overlap-added
+ * squared window floored at window_floor (STFT.swift:482-531; the reference's default is 1e-10).
+ * fft_size: power of 2 in [4, 16384]. */
+typedef enum {
+  MNN_WINDOW_NONE = 0,
+  MNN_WINDOW_HANN = 1,
+  MNN_WINDOW_HAMMING = 2,
+  MNN_WINDOW_BLACKMAN = 3
+} mnn_window;
+typedef struct mnn_stft_s* mnn_stft;
+mnn_status mnn_stft_create(mnn_device dev, int fft_size, int hop_size, int window, mnn_stft* out);
+mnn_status mnn_stft_destroy(mnn_stft plan);
+/* WindowType.coefficient(at:length:) for all fft_size indices, into a host array */
+mnn_status mnn_stft_window(mnn_stft plan, float* out, size_t count);
+mnn_status mnn_stft_frame_count(mnn_stft plan, int64_t samples, int64_t* frames);
+mnn_status mnn_stft_output_length(mnn_stft plan, int64_t frames, int64_t* samples);
+/* input [n] or [B, n] (f32 tensors on the plan's device) */
+mnn_status mnn_stft_forward(mnn_stft plan, mnn_tensor input, mnn_tensor real, mnn_tensor imag,
+                            int onesided, int layout, mnn_stream stream);
+/* output [L] or [B, L], L = (frames - 1) * hop + fft_size */
+mnn_status mnn_stft_inverse(mnn_stft plan, mnn_tensor real, mnn_tensor imag, int onesided,
+                            int layout, float window_floor, mnn_tensor output, mnn_stream stream);
+
 /* UNetPaddingCalculator (UNet.swift:393-448): left/right zero padding that makes the length a
  * multiple of stride^levels (remainder split evenly, the odd sample on the right), and the length
  * after `levels` downsamplings by `stride`. */

@@ -140,6 +140,13 @@ SIGNATURES = {
     "mnn_decoder_block_create": (C.c_int, [P, C.POINTER(DecoderBlockDesc), PP]),
     "mnn_unet_padding": (C.c_int, [C.c_int64, C.c_int, C.c_int, C.c_int, I64P, I64P, I64P]),
     "mnn_unet_bottleneck_length": (C.c_int, [C.c_int64, C.c_int, C.c_int, I64P]),
+    "mnn_stft_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),
+    "mnn_stft_destroy": (C.c_int, [P]),
+    "mnn_stft_window": (C.c_int, [P, FP, C.c_size_t]),
+    "mnn_stft_frame_count": (C.c_int, [P, C.c_int64, I64P]),
+    "mnn_stft_output_length": (C.c_int, [P, C.c_int64, I64P]),
+    "mnn_stft_forward": (C.c_int, [P, P, P, P, C.c_int, C.c_int, P]),
+    "mnn_stft_inverse": (C.c_int, [P, P, P, C.c_int, C.c_int, C.c_float, P, P]),
     "mnn_conv2d_create": (C.c_int, [P, C.POINTER(Conv2dDesc), PP]),
     "mnn_conv_transpose2d_create": (C.c_int, [P, C.POINTER(ConvTranspose2dDesc), PP]),
     "mnn_freq_encoder_block_create": (C.c_int, [P, C.POINTER(FreqBlockDesc), PP]),

@@ -6,6 +6,7 @@
 
 #include "layers.hpp"
 #include "safetensors.hpp"
+#include "stft.hpp"
 #include "weight_names.hpp"
 
 using namespace mnn;
@@ -17,6 +18,7 @@ struct mnn_layer_s {};
 struct mnn_sequential_s {};
 struct mnn_safetensors_s {};
 struct mnn_mtla_s {};
+struct mnn_stft_s {};
 struct mnn_mtla_writer_s {};
 
 namespace {
@@ -503,6 +505,78 @@ mnn_status mnn_unet_bottleneck_2d(int64_t height, int64_t width, int levels, int
     out[0] = h;
   });
 }
+// ------------------------------------------------------------------ STFT
+namespace {
+StftPlan* SP(mnn_stft p) {
+  MNN_REQUIRE(p, MNN_ERR_INVALID_ARGUMENT, "null STFT handle");
+  return reinterpret_cast<StftPlan*>(p);
+}
+}  // namespace
+
+mnn_status mnn_stft_create(mnn_device dev, int fft_size, int hop_size, int window, mnn_stft* out) {
+  return guard([&] {
+    MNN_REQUIRE(out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    Device* d = D(dev);
+    d->check_alive();
+    *out = reinterpret_cast<mnn_stft>(new StftPlan(d, fft_size, hop_size, window));
+  });
+}
+mnn_status mnn_stft_destroy(mnn_stft plan) {
+  return guard([&] {
+    StftPlan* p = reinterpret_cast<StftPlan*>(plan);
+    if (p) p->device()->make_current();
+    delete p;
+  });
+}
+mnn_status mnn_stft_window(mnn_stft plan, float* out, size_t count) {
+  return guard([&] {
+    const auto& w = SP(plan)->window();
+    MNN_REQUIRE(out && count == w.size(), MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "window holds " << w.size() << " values");
+    std::copy(w.begin(), w.end(), out);
+  });
+}
+mnn_status mnn_stft_frame_count(mnn_stft plan, int64_t samples, int64_t* frames) {
+  return guard([&] {
+    MNN_REQUIRE(frames, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *frames = SP(plan)->frame_count(samples);
+  });
+}
+mnn_status mnn_stft_output_length(mnn_stft plan, int64_t frames, int64_t* samples) {
+  return guard([&] {
+    MNN_REQUIRE(samples, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    *samples = SP(plan)->output_length(frames);
+  });
+}
+mnn_status mnn_stft_forward(mnn_stft plan, mnn_tensor input, mnn_tensor real, mnn_tensor imag,
+                            int onesided, int layout, mnn_stream st) {
+  return guard([&] {
+    StftPlan* p = SP(plan);
+    Tensor *x = T(input), *re = T(real), *im = T(imag);
+    Device* d = p->device();
+    d->check_alive();
+    MNN_REQUIRE(x->dev == d && re->dev == d && im->dev == d, MNN_ERR_INVALID_ARGUMENT,
+                "tensors and plan on different devices");
+    Stream s = resolve_stream(d, st);
+    d->make_current();
+    p->forward(*x, *re, *im, onesided != 0, layout, s);
+  });
+}
+mnn_status mnn_stft_inverse(mnn_stft plan, mnn_tensor real, mnn_tensor imag, int onesided,
+                            int layout, float window_floor, mnn_tensor output, mnn_stream st) {
+  return guard([&] {
+    StftPlan* p = SP(plan);
+    Tensor *re = T(real), *im = T(imag), *y = T(output);
+    Device* d = p->device();
+    d->check_alive();
+    MNN_REQUIRE(y->dev == d && re->dev == d && im->dev == d, MNN_ERR_INVALID_ARGUMENT,
+                "tensors and plan on different devices");
+    Stream s = resolve_stream(d, st);
+    d->make_current();
+    p->inverse(*re, *im, onesided != 0, layout, window_floor, *y, s);
+  });
+}
+
 // ------------------------------------------------------------------ SafeTensors
 namespace {
 SafeTensorsFile* ST(mnn_safetensors s) {

@@ -178,6 +178,29 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
                   float* cat);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
 
+// ------------------------------------------------------------------ STFT (k_stft.hip)
+// STFT / iSTFT (STFT.swift:40-533): frames of N samples every hop, window win[N]; twiddles
+// tw[k] = e^{-2 pi i k / N}, k < N/2 (float2). Spectra are [batch][frames][bins] (layout 0) or
+// [batch][bins][frames] (layout 1), bins = N/2 + 1 (onesided) or N.
+constexpr int kStftMaxN = 16384;
+struct StftArgs {
+  int N = 0, logM = 0, hop = 0, batch = 0, onesided = 1, layout = 0;
+  int64_t n = 0;       // forward: samples per signal
+  int64_t frames = 0;
+  const float* win = nullptr;
+  const float2* tw = nullptr;
+  const float* x = nullptr;   // forward input [batch][n]
+  float* re = nullptr;        // forward outputs
+  float* im = nullptr;
+  const float* cre = nullptr; // inverse inputs
+  const float* cim = nullptr;
+  float* frames_buf = nullptr;  // inverse workspace [batch][frames][N]
+  float* y = nullptr;           // inverse output [batch][(frames - 1) * hop + N]
+  float floor = 1e-10f;
+};
+void stft_forward(const LaunchCtx& c, const StftArgs& a);
+void stft_inverse(const LaunchCtx& c, const StftArgs& a);
+
 // ------------------------------------------------------------------ transposed conv (k_convt.hip)
 // DynamicConvTranspose1D (DynamicConv1D.swift:411-645) over the channel concat [x1; x2] (x2 may be
 // absent: C2 = 0): y[b][oc][o] (row pitch Lout) = bias + sum over (ic, k) with

@@ -25,6 +25,7 @@ __all__ = [
     "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "WeightNameMapper",
     "Conv2D", "DynamicConv2D", "ConvTranspose2D", "DynamicConvTranspose2D",
     "FreqUNetEncoderBlock2D", "FreqUNetDecoderBlock2D", "unet_padding_2d", "unet_bottleneck_2d",
+    "STFT", "WINDOWS",
     "mfma_probe",
 ]
 
@@ -516,6 +517,77 @@ class FreqUNetDecoderBlock2D(UNetDecoderBlock):
                           num_groups)
         Layer.__init__(self, device, _create(lib().mnn_freq_decoder_block_create, device.handle,
                                              C.byref(d)))
+
+
+WINDOWS = {"none": 0, "hann": 1, "hamming": 2, "blackman": 3}
+
+
+class STFT:
+    """STFT (STFT.swift:20-533) on the GPU: `stft(x)` -> (real, imag) tensors, `istft(real, imag)`
+    -> signal. layout "frames" = [B?, frames, bins] (STFTResult), "bins" = [B?, bins, frames];
+    onesided keeps bins 0..N/2."""
+
+    def __init__(self, device, fft_size: int, hop_size: Optional[int] = None,
+                 window: str = "hann"):
+        self.device = device
+        self.fft_size = fft_size
+        self.hop_size = hop_size if hop_size is not None else fft_size // 4
+        h = C.c_void_p()
+        check(lib().mnn_stft_create(device.handle, fft_size, self.hop_size, WINDOWS[window],
+                                    C.byref(h)))
+        self.handle = h
+
+    @property
+    def window(self) -> np.ndarray:
+        out = np.empty(self.fft_size, np.float32)
+        check(lib().mnn_stft_window(self.handle, out.ctypes.data_as(C.POINTER(C.c_float)),
+                                    self.fft_size))
+        return out
+
+    def frame_count(self, samples: int) -> int:
+        out = C.c_int64()
+        check(lib().mnn_stft_frame_count(self.handle, samples, C.byref(out)))
+        return out.value
+
+    def output_length(self, frames: int) -> int:
+        out = C.c_int64()
+        check(lib().mnn_stft_output_length(self.handle, frames, C.byref(out)))
+        return out.value
+
+    def _spec_shape(self, batch, frames, onesided, layout):
+        bins = self.fft_size // 2 + 1 if onesided else self.fft_size
+        s = (frames, bins) if layout == "frames" else (bins, frames)
+        return s if batch is None else (batch,) + s
+
+    def stft(self, x: Tensor, onesided: bool = True, layout: str = "frames",
+             stream: Optional[Stream] = None) -> tuple[Tensor, Tensor]:
+        batch = x.shape[0] if len(x.shape) == 2 else None
+        shp = self._spec_shape(batch, self.frame_count(x.shape[-1]), onesided, layout)
+        re, im = Tensor(self.device, shp), Tensor(self.device, shp)
+        check(lib().mnn_stft_forward(self.handle, x.handle, re.handle, im.handle, int(onesided),
+                                     0 if layout == "frames" else 1, _sh(stream)))
+        return re, im
+
+    def istft(self, real: Tensor, imag: Tensor, onesided: bool = True, layout: str = "frames",
+              window_floor: float = 1e-10, stream: Optional[Stream] = None) -> Tensor:
+        frames = real.shape[-2] if layout == "frames" else real.shape[-1]
+        L = self.output_length(frames)
+        out = Tensor(self.device, (real.shape[0], L) if len(real.shape) == 3 else (L,))
+        check(lib().mnn_stft_inverse(self.handle, real.handle, imag.handle, int(onesided),
+                                     0 if layout == "frames" else 1, window_floor, out.handle,
+                                     _sh(stream)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().mnn_stft_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def unet_padding_2d(height: int, width: int, levels: int, stride: int = 2):
