@@ -418,6 +418,32 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     cpu8 = time_cpu(lambda: freq_decoder_oracle(oracle, fdec), max_reps=1) if cpu else None
     row("7_freq_encoder_b1", time_gpu(f7, stream, 10), flops=fenc["flops"], cpu_ms=cpu7)
     row("8_freq_decoder_b1", time_gpu(f8, stream, 10), flops=fdec["flops"], cpu_ms=cpu8)
+    # STFT / iSTFT of one stereo 7.8 s chunk at HTDemucs' nfft 4096 / hop 1024 (bin-major
+    # spectrogram, as the frequency branch consumes it); bytes = signal read + spectra written
+    # (forward), spectra read + frames written and re-read + signal written (inverse)
+    from oracle import dsp as odsp  # noqa: E402  (CPU baseline only)
+    xs = np.random.default_rng(1008).uniform(-1, 1, (2, 343980)).astype(np.float32)
+    plan = nn.STFT(dev, 4096, 1024, "hann")
+    xst = nn.Tensor.from_numpy(dev, xs)
+    nf = plan.frame_count(343980)
+    re9, im9 = nn.Tensor(dev, (2, 2049, nf)), nn.Tensor(dev, (2, 2049, nf))
+    y9 = nn.Tensor(dev, (2, plan.output_length(nf)))
+    from metalaudio_amd._lib import check as check9, lib as lib9
+
+    def fwd():
+        check9(lib9().mnn_stft_forward(plan.handle, xst.handle, re9.handle, im9.handle, 1, 1,
+                                       stream.handle))
+
+    def inv():
+        check9(lib9().mnn_stft_inverse(plan.handle, re9.handle, im9.handle, 1, 1, 1e-10,
+                                       y9.handle, stream.handle))
+    spec_b = 2 * nf * 2049 * 8.0
+    cpu9 = time_cpu(lambda: odsp.stft(xs, 4096, 1024, dtype=np.float32)) if cpu else None
+    X9 = odsp.stft(xs, 4096, 1024) if cpu else None
+    cpu10 = time_cpu(lambda: odsp.istft(X9, 4096, 1024, dtype=np.float32)) if cpu else None
+    row("9_stft_b1", time_gpu(fwd, stream, 20), byts=4.0 * xs.size + spec_b, cpu_ms=cpu9)
+    row("10_istft_b1", time_gpu(inv, stream, 20),
+        byts=spec_b + 2 * 4.0 * 2 * nf * 4096 + 4.0 * 2 * plan.output_length(nf), cpu_ms=cpu10)
     t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
     q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
     to5, fo5 = nn.Tensor(dev, t5.shape), nn.Tensor(dev, q5.shape)
