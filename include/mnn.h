@@ -296,6 +296,38 @@ mnn_status mnn_stft_forward(mnn_stft plan, mnn_tensor input, mnn_tensor real, mn
 mnn_status mnn_stft_inverse(mnn_stft plan, mnn_tensor real, mnn_tensor imag, int onesided,
                             int layout, float window_floor, mnn_tensor output, mnn_stream stream);
 
+/* ---------------------------------------------------------------- separation driver */
+/* Time-domain HTDemucs (HTDemucs.swift: time U-Net :260-293 + :521-548, one 1x1 Conv1D output
+ * head per stem :333-350, forward :376-392, separate :617-691): interleaved input -> UNet zero
+ * padding -> encoders -> decoders with skips -> heads -> crop -> interleaved stems. */
+typedef struct mnn_separator_desc {
+  int input_channels;   /* 2 (stereo) */
+  int num_stems;        /* 4: drums, bass, other, vocals */
+  int levels;           /* <= 8 */
+  int channels[8];      /* encoder channels per level, e.g. 48, 96, 192, 384, 768 */
+  int kernel_size, stride, num_groups;   /* 8, 4, 8 */
+} mnn_separator_desc;
+typedef struct mnn_separator_s* mnn_separator;
+mnn_status mnn_separator_create(mnn_device dev, const mnn_separator_desc* desc,
+                                mnn_separator* out);
+mnn_status mnn_separator_destroy(mnn_separator sep);
+/* "time_encoder.{i}.{conv,norm}.{weight,bias}", "time_decoder.{j}.{conv_transpose|conv_tr,norm}.
+ * {weight,bias}" (j = 0 is the deepest level, the order of HTDemucs.loadWeights), and
+ * "output_heads.{s}.{weight,bias}". */
+mnn_status mnn_separator_load(mnn_separator sep, const char* name, const float* data, size_t n);
+/* HTDemucs.separate(input:mode: .timeOnly) on device tensors: input [n * C] interleaved, output
+ * [num_stems, n * C] interleaved stems. */
+mnn_status mnn_separator_separate(mnn_separator sep, mnn_tensor input, mnn_tensor output,
+                                  mnn_stream stream);
+/* Long audio (HTDEMUCS_GUIDE.md:170-191): segments of segment_frames frames starting every
+ * segment_frames - overlap_frames frames, each separated as above and written into output with a
+ * linear crossfade, weight (i + 1) / (F + 1) for the new segment, over the F frames it shares with
+ * the previous one. The guide's crossfadeAppend helper is not defined by the reference; this is
+ * the definition used here. segment_frames <= 0 or >= n: one pass. */
+mnn_status mnn_separator_separate_long(mnn_separator sep, mnn_tensor input, mnn_tensor output,
+                                       int64_t segment_frames, int64_t overlap_frames,
+                                       mnn_stream stream);
+
 /* UNetPaddingCalculator (UNet.swift:393-448): left/right zero padding that makes the length a
  * multiple of stride^levels (remainder split evenly, the odd sample on the right), and the length
  * after `levels` downsamplings by `stride`. */

@@ -96,6 +96,12 @@ class FreqBlockDesc(C.Structure):
         "stride_w", "num_groups")]
 
 
+class SeparatorDesc(C.Structure):
+    _fields_ = [("input_channels", C.c_int), ("num_stems", C.c_int), ("levels", C.c_int),
+                ("channels", C.c_int * 8), ("kernel_size", C.c_int), ("stride", C.c_int),
+                ("num_groups", C.c_int)]
+
+
 P = C.c_void_p
 PP = C.POINTER(C.c_void_p)
 I64P = C.POINTER(C.c_int64)
@@ -140,6 +146,11 @@ SIGNATURES = {
     "mnn_decoder_block_create": (C.c_int, [P, C.POINTER(DecoderBlockDesc), PP]),
     "mnn_unet_padding": (C.c_int, [C.c_int64, C.c_int, C.c_int, C.c_int, I64P, I64P, I64P]),
     "mnn_unet_bottleneck_length": (C.c_int, [C.c_int64, C.c_int, C.c_int, I64P]),
+    "mnn_separator_create": (C.c_int, [P, C.POINTER(SeparatorDesc), PP]),
+    "mnn_separator_destroy": (C.c_int, [P]),
+    "mnn_separator_load": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
+    "mnn_separator_separate": (C.c_int, [P, P, P, P]),
+    "mnn_separator_separate_long": (C.c_int, [P, P, P, C.c_int64, C.c_int64, P]),
     "mnn_stft_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_stft_destroy": (C.c_int, [P]),
     "mnn_stft_window": (C.c_int, [P, FP, C.c_size_t]),

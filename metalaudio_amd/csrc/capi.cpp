@@ -7,6 +7,7 @@
 #include "layers.hpp"
 #include "safetensors.hpp"
 #include "stft.hpp"
+#include "separate.hpp"
 #include "weight_names.hpp"
 
 using namespace mnn;
@@ -19,6 +20,7 @@ struct mnn_sequential_s {};
 struct mnn_safetensors_s {};
 struct mnn_mtla_s {};
 struct mnn_stft_s {};
+struct mnn_separator_s {};
 struct mnn_mtla_writer_s {};
 
 namespace {
@@ -575,6 +577,67 @@ mnn_status mnn_stft_inverse(mnn_stft plan, mnn_tensor real, mnn_tensor imag, int
     d->make_current();
     p->inverse(*re, *im, onesided != 0, layout, window_floor, *y, s);
   });
+}
+
+// ------------------------------------------------------------------ separator
+namespace {
+TimeSeparator* SEP(mnn_separator p) {
+  MNN_REQUIRE(p, MNN_ERR_INVALID_ARGUMENT, "null separator handle");
+  return reinterpret_cast<TimeSeparator*>(p);
+}
+}  // namespace
+
+mnn_status mnn_separator_create(mnn_device dev, const mnn_separator_desc* desc,
+                                mnn_separator* out) {
+  return guard([&] {
+    MNN_REQUIRE(desc && out, MNN_ERR_INVALID_ARGUMENT, "null argument");
+    Device* d = D(dev);
+    d->check_alive();
+    d->make_current();
+    *out = reinterpret_cast<mnn_separator>(new TimeSeparator(d, *desc));
+  });
+}
+mnn_status mnn_separator_destroy(mnn_separator sep) {
+  return guard([&] {
+    TimeSeparator* p = reinterpret_cast<TimeSeparator*>(sep);
+    if (p) p->device()->make_current();
+    delete p;
+  });
+}
+mnn_status mnn_separator_load(mnn_separator sep, const char* name, const float* data, size_t n) {
+  return guard([&] {
+    MNN_REQUIRE(name && (data || n == 0), MNN_ERR_INVALID_ARGUMENT, "null argument");
+    TimeSeparator* p = SEP(sep);
+    p->device()->check_alive();
+    p->load(name, data, n);
+  });
+}
+namespace {
+mnn_status separate_call(mnn_separator sep, mnn_tensor input, mnn_tensor output, int64_t seg,
+                         int64_t ovl, mnn_stream st) {
+  return guard([&] {
+    TimeSeparator* p = SEP(sep);
+    Tensor *x = T(input), *y = T(output);
+    Device* d = p->device();
+    d->check_alive();
+    MNN_REQUIRE(x->dev == d && y->dev == d, MNN_ERR_INVALID_ARGUMENT,
+                "tensors and separator on different devices");
+    MNN_REQUIRE(x->data != y->data, MNN_ERR_INVALID_ARGUMENT, "input and output must differ");
+    Stream s = resolve_stream(d, st);
+    d->make_current();
+    p->separate_long(*x, *y, seg, ovl, s);
+  });
+}
+}  // namespace
+mnn_status mnn_separator_separate(mnn_separator sep, mnn_tensor input, mnn_tensor output,
+                                  mnn_stream stream) {
+  return separate_call(sep, input, output, 0, 0, stream);
+}
+mnn_status mnn_separator_separate_long(mnn_separator sep, mnn_tensor input, mnn_tensor output,
+                                       int64_t segment_frames, int64_t overlap_frames,
+                                       mnn_stream stream) {
+  return separate_call(sep, input, output, segment_frames <= 0 ? 0 : segment_frames,
+                       overlap_frames, stream);
 }
 
 // ------------------------------------------------------------------ SafeTensors

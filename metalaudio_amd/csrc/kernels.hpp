@@ -178,6 +178,21 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
                   float* cat);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
 
+// ------------------------------------------------------------------ separation (k_separate.hip)
+// One segment [start, start + len) of interleaved audio x [n][C]: planar padded network input
+// xp [C][Lp] (left pad lp), stems y [S][C][Lp] written back into out [S][n][C] with a linear
+// crossfade over the first `fade` frames.
+struct SegmentArgs {
+  int C = 0, S = 0;
+  int64_t n = 0, start = 0, len = 0, Lp = 0, lp = 0, fade = 0;
+  const float* x = nullptr;
+  float* xp = nullptr;
+  const float* y = nullptr;
+  float* out = nullptr;
+};
+void segment_deinterleave_pad(const LaunchCtx& c, const SegmentArgs& a);
+void segment_crossfade_store(const LaunchCtx& c, const SegmentArgs& a);
+
 // ------------------------------------------------------------------ STFT (k_stft.hip)
 // STFT / iSTFT (STFT.swift:40-533): frames of N samples every hop, window win[N]; twiddles
 // tw[k] = e^{-2 pi i k / N}, k < N/2 (float2). Spectra are [batch][frames][bins] (layout 0) or

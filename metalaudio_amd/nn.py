@@ -15,7 +15,7 @@ import numpy as np
 
 from ._lib import (ACT, PAD, PRECISION, Conv1dDesc, Conv2dDesc, ConvTranspose1dDesc,
                    ConvTranspose2dDesc, DecoderBlockDesc, EncoderBlockDesc, FreqBlockDesc, MNNError,
-                   check, dims, lib)
+                   SeparatorDesc, check, dims, lib)
 
 __all__ = [
     "MNNError", "AudioDevice", "Stream", "Tensor", "Layer", "Conv1D", "DynamicConv1D",
@@ -25,7 +25,7 @@ __all__ = [
     "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "WeightNameMapper",
     "Conv2D", "DynamicConv2D", "ConvTranspose2D", "DynamicConvTranspose2D",
     "FreqUNetEncoderBlock2D", "FreqUNetDecoderBlock2D", "unet_padding_2d", "unet_bottleneck_2d",
-    "STFT", "WINDOWS",
+    "STFT", "WINDOWS", "Separator", "STEM_NAMES",
     "mfma_probe",
 ]
 
@@ -517,6 +517,62 @@ class FreqUNetDecoderBlock2D(UNetDecoderBlock):
                           num_groups)
         Layer.__init__(self, device, _create(lib().mnn_freq_decoder_block_create, device.handle,
                                              C.byref(d)))
+
+
+STEM_NAMES = ["drums", "bass", "other", "vocals", "guitar", "piano"]
+
+
+class Separator:
+    """Time-domain HTDemucs separation (HTDemucs.swift:260-392, separate :617-691) and the
+    long-audio segment driver. Parameters by name: "time_encoder.{i}.*", "time_decoder.{j}.*"
+    (j = 0 deepest), "output_heads.{s}.*"."""
+
+    def __init__(self, device, input_channels=2, num_stems=4,
+                 channels=(48, 96, 192, 384, 768), kernel_size=8, stride=4, num_groups=8):
+        ch = (C.c_int * 8)(*channels)
+        d = SeparatorDesc(input_channels, num_stems, len(channels), ch, kernel_size, stride,
+                          num_groups)
+        h = C.c_void_p()
+        check(lib().mnn_separator_create(device.handle, C.byref(d), C.byref(h)))
+        self.handle, self.device = h, device
+        self.input_channels, self.num_stems = input_channels, num_stems
+
+    def load(self, name: str, data) -> None:
+        a = _f32(data).reshape(-1)
+        check(lib().mnn_separator_load(self.handle, name.encode(),
+                                       a.ctypes.data_as(C.POINTER(C.c_float)), a.size))
+
+    def load_state(self, params: dict) -> None:
+        """params: {"time_encoder.0": {"conv.weight": ..., ...}, ...} or flat names."""
+        for k, v in params.items():
+            if isinstance(v, dict):
+                for kk, vv in v.items():
+                    self.load(f"{k}.{kk}", vv)
+            else:
+                self.load(k, v)
+
+    def separate(self, x: Tensor, stream: Optional[Stream] = None) -> Tensor:
+        out = Tensor(self.device, (self.num_stems, x.shape[0]))
+        check(lib().mnn_separator_separate(self.handle, x.handle, out.handle, _sh(stream)))
+        return out
+
+    def separate_long(self, x: Tensor, segment_frames: int, overlap_frames: int,
+                      stream: Optional[Stream] = None) -> Tensor:
+        out = Tensor(self.device, (self.num_stems, x.shape[0]))
+        check(lib().mnn_separator_separate_long(self.handle, x.handle, out.handle,
+                                                segment_frames, overlap_frames, _sh(stream)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            lib().mnn_separator_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 WINDOWS = {"none": 0, "hann": 1, "hamming": 2, "blackman": 3}
