@@ -444,6 +444,47 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     row("9_stft_b1", time_gpu(fwd, stream, 20), byts=4.0 * xs.size + spec_b, cpu_ms=cpu9)
     row("10_istft_b1", time_gpu(inv, stream, 20),
         byts=spec_b + 2 * 4.0 * 2 * nf * 4096 + 4.0 * 2 * plan.output_length(nf), cpu_ms=cpu10)
+    # long-audio driver: 60 s of stereo audio through the reference's default time-domain
+    # HTDemucs (5 levels 48..768, k 8, s 4, 4 stems) in the guide's 30 s segments with 2 s
+    # overlap (HTDEMUCS_GUIDE.md:170-191); synthetic weights and audio
+    from oracle import separate as osep  # noqa: E402  (CPU baseline only)
+    r11 = np.random.default_rng(1009)
+    ch11 = [48, 96, 192, 384, 768]
+    cfg11 = {"input_channels": 2, "num_stems": 4, "channels": ch11, "kernel_size": 8,
+             "stride": 4, "num_groups": 8}
+    P11, chans = {}, [2] + ch11
+    for i in range(5):
+        ci, co = chans[i], chans[i + 1]
+        P11[f"time_encoder.{i}"] = {
+            "conv.weight": (r11.standard_normal((co, ci, 8)) * np.sqrt(2 / (8 * ci))).astype(
+                np.float32), "conv.bias": np.zeros(co, np.float32),
+            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
+    for j in range(5):
+        i = 4 - j
+        ci, co = chans[i + 1], (2 if i == 0 else chans[i])
+        P11[f"time_decoder.{j}"] = {
+            "conv_transpose.weight": (r11.standard_normal((2 * ci, co, 8)) * np.sqrt(
+                1 / (4 * ci))).astype(np.float32), "conv_transpose.bias": np.zeros(co, np.float32),
+            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
+    for h in range(4):
+        P11[f"output_heads.{h}"] = {"weight": r11.standard_normal((2, 2, 1)).astype(np.float32),
+                                    "bias": np.zeros(2, np.float32)}
+    sep = nn.Separator(dev)
+    sep.load_state(P11)
+    n11 = 44100 * 60
+    x11 = nn.Tensor.from_numpy(dev, r11.uniform(-1, 1, 2 * n11).astype(np.float32))
+    o11 = nn.Tensor(dev, (4, 2 * n11))
+    from metalaudio_amd._lib import check as check11, lib as lib11
+
+    def f11():
+        check11(lib11().mnn_separator_separate_long(sep.handle, x11.handle, o11.handle,
+                                                    44100 * 30, 44100 * 2, stream.handle))
+    seg_cpu = r11.uniform(-1, 1, 2 * 44100 * 10).astype(np.float32)
+    cpu11 = time_cpu(lambda: osep.separate_time(seg_cpu, P11, cfg11, dtype=np.float32),
+                     max_reps=1) * 6.0 if cpu else None
+    g11 = time_gpu(f11, stream, 3)
+    row("11_long_audio_60s", g11, cpu_ms=cpu11)
+    out["11_long_audio_60s"]["x_realtime"] = round(60e3 / g11, 1)
     t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
     q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
     to5, fo5 = nn.Tensor(dev, t5.shape), nn.Tensor(dev, q5.shape)
