@@ -39,6 +39,22 @@ FAMILIES = [
     ("enc_gn_gelu_t_kernel", "enc_gn_gelu_t_f32"),
     ("convt_pack_kernel", "convt_pack_f32"),
     ("convt_direct_kernel", "convt_direct_f32"),
+    ("convt_small_kernel", "convt_small_f32"),
+    ("convt_reduce_kernel", "convt_reduce_f32"),
+    ("conv2d_unfold_kernel", "conv2d_unfold_f32"),
+    ("conv2d_direct_kernel", "conv2d_direct_f32"),
+    ("convt2d_gather_kernel", "convt2d_gather_f32"),
+    ("convt2d_direct_kernel", "convt2d_direct_f32"),
+    ("concat2_kernel", "concat2_f32"),
+    ("stft_forward_kernel", "stft_forward_f32"),
+    ("stft_inverse_kernel", "istft_frames_f32"),
+    ("stft_overlap_add_kernel", "istft_overlap_add_f32"),
+    ("deinterleave_pad_kernel", "deinterleave_pad_f32"),
+    ("crossfade_store_kernel", "crossfade_store_f32"),
+    ("gn_stats_partial_kernel", "gn_stats"),
+    ("gn_finalize_kernel", "gn_finalize"),
+    ("gn_apply_kernel", "gn_apply"),
+    ("gemm_f32_mfma_kernel", "gemm_f32_mfma"),
     ("layernorm", "layernorm"),
     ("copy_kernel", "copy_bytes"),
 ]
