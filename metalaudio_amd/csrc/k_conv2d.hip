@@ -16,8 +16,9 @@
 //   y[oc][oh][ow] = bias[oc] + sum x[ic][ih][iw] * W[ic][ocg][kh][kw] over the (ic, kh, kw) with
 //   oh + ph - kh*dh = ih*sh and ow + pw - kw*dw = iw*sw exactly, 0 <= ih < H, 0 <= iw < W.
 // Matrix-core form (groups 1): Z[(oc, kh, kw)][(ih, iw)] = sum_ic W[ic][oc][kh][kw] x[ic][ih][iw]
-// is a GEMM with the input as its [K][N] operand (the decoder's channel concat is copied into one
-// operand first, so the GEMM runs over all of K), then convt2d_gather_kernel sums the taps that land on each output
+// is a GEMM on the LDS-DMA path: the input (with the decoder's skip, the concat folded in) is
+// packed transposed to [H*W][Cp] by the 1-D transposed conv's pack kernel, then
+// convt2d_gather_kernel sums the taps that land on each output
 // (KH*KW / (sh*sw) of them on average) and adds the bias. No atomics; fixed summation order.
 #include "device_utils.hpp"
 #include "kernels.hpp"
@@ -126,6 +127,47 @@ __global__ __launch_bounds__(256) void convt2d_gather_kernel(ConvT2DArgs a) {
   a.y[idx] = sum;
 }
 
+// Dilation 1, stride_w <= 8: one thread per (oh, q) computes the sw outputs ow = sw*q + r. For
+// each r the taps kw = (r + pw) mod sw, + sw, ... are the same for every lane, and lanes with
+// consecutive q read consecutive iw = (ow + pw - kw) / sw, so the reads coalesce and no lane
+// diverges on the column taps. Per output the taps are summed kh-major, kw ascending, as in
+// convt2d_gather_kernel.
+__global__ __launch_bounds__(256) void convt2d_gather_phase_kernel(ConvT2DArgs a) {
+  constexpr int kMaxSW = 8;
+  const unsigned nq = ((unsigned)a.Wo + a.sw - 1) / a.sw;
+  const unsigned e = blockIdx.x * 256u + threadIdx.x;
+  if (e >= (unsigned)a.Ho * nq) return;
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int oh = (int)(e / nq), q = (int)(e - (unsigned)oh * nq);
+  const int64_t n_in = (int64_t)a.H * a.W;
+  const float* zb = a.z + ((int64_t)b * a.Cout + oc) * a.KH * a.KW * n_in;
+  float acc[kMaxSW];
+#pragma unroll
+  for (int r = 0; r < kMaxSW; ++r) acc[r] = 0.f;
+  const int th = oh + a.ph;
+  for (int kh = th % a.sh; kh < a.KH && kh <= th; kh += a.sh) {
+    const int ih = (th - kh) / a.sh;
+    if (ih >= a.H) continue;
+    const float* zr = zb + (int64_t)kh * a.KW * n_in + (int64_t)ih * a.W;
+#pragma unroll
+    for (int r = 0; r < kMaxSW; ++r) {
+      if (r >= a.sw) break;
+      const int tw = a.sw * q + r + a.pw;
+      for (int kw = tw % a.sw; kw < a.KW && kw <= tw; kw += a.sw) {
+        const int iw = (tw - kw) / a.sw;
+        if (iw < a.W) acc[r] += zr[(int64_t)kw * n_in + iw];
+      }
+    }
+  }
+  float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + oh) * a.Wo;
+  const float bias = a.bias ? a.bias[oc] : 0.f;
+#pragma unroll
+  for (int r = 0; r < kMaxSW; ++r) {
+    const int ow = a.sw * q + r;
+    if (r < a.sw && ow < a.Wo) yr[ow] = acc[r] + bias;
+  }
+}
+
 __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
   const unsigned n = blockIdx.x * 256u + threadIdx.x;
@@ -159,31 +201,6 @@ __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
   }
   if (a.bias) sum += a.bias[oc];
   a.y[idx] = sum;
-}
-
-// cat[b] = [x1[b] (C1 rows); x2[b] (C2 rows)], rows of n floats; four floats per thread when
-// n % 4 == 0 (16-byte rows).
-__global__ __launch_bounds__(256) void concat2_kernel(const float* __restrict__ x1,
-                                                      const float* __restrict__ x2,
-                                                      float* __restrict__ cat, int C1, int C2,
-                                                      unsigned n, bool vec) {
-  const int b = blockIdx.y;
-  const unsigned C = (unsigned)(C1 + C2);
-  const unsigned per = vec ? C * (n / 4) : C * n;
-  const unsigned e = blockIdx.x * 256u + threadIdx.x;
-  if (e >= per) return;
-  float* dst = cat + (int64_t)b * C * n;
-  if (vec) {
-    const unsigned q = n / 4, c = e / q, j = e - c * q;
-    const float* src = (int)c < C1 ? x1 + ((int64_t)b * C1 + c) * n
-                                   : x2 + ((int64_t)b * C2 + (c - C1)) * n;
-    reinterpret_cast<float4*>(dst + (int64_t)c * n)[j] = reinterpret_cast<const float4*>(src)[j];
-  } else {
-    const unsigned c = e / n, j = e - c * n;
-    const float* src = (int)c < C1 ? x1 + ((int64_t)b * C1 + c) * n
-                                   : x2 + ((int64_t)b * C2 + (c - C1)) * n;
-    dst[(int64_t)c * n + j] = src[j];
-  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -286,7 +303,7 @@ void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a) {
          plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, a);
 }
 
-int convt2d_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
+int convt2d_padded_cin(int Cin) { return (Cin + 31) / 32 * 32; }
 
 bool convt2d_gemm_supported(const ConvT2DArgs& a) { return a.groups == 1; }
 
@@ -302,34 +319,37 @@ void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, flo
 }
 
 void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
-                  float* cat) {
+                  float* unfold) {
   check_convt2d(a);
-  MNN_REQUIRE(convt2d_gemm_supported(a) && wpack && z && (a.C2 == 0 || cat),
-              MNN_ERR_INVALID_ARGUMENT, "convt2d_gemm: configuration outside the GEMM form");
+  MNN_REQUIRE(convt2d_gemm_supported(a) && wpack && z && unfold, MNN_ERR_INVALID_ARGUMENT,
+              "convt2d_gemm: configuration outside the GEMM form");
   const int64_t n_in = (int64_t)a.H * a.W;
-  const int Cin = a.C1 + a.C2;
-  MNN_REQUIRE(n_in * Cin < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
+  const int Cin = a.C1 + a.C2, Cp = convt2d_padded_cin(Cin);
+  MNN_REQUIRE(n_in * Cp < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
               "convt2d_gemm: input too large");
-  const float* x = a.x1;
-  if (a.C2 > 0) {  // the decoder's channel concat, one pass, so the GEMM runs over all of K
-    const bool vec = n_in % 4 == 0 && aligned16(a.x1) && aligned16(a.x2) && aligned16(cat);
-    const int64_t per = vec ? Cin * (n_in / 4) : Cin * n_in;
-    launch(c, "concat2_f32", concat2_kernel, dim3((unsigned)cdiv(per, 256), (unsigned)a.B),
-           dim3(256), 0, a.x1, a.x2, cat, a.C1, a.C2, (unsigned)n_in, vec);
-    x = cat;
-  }
+  // operand [H*W][Cp]: the input (and the decoder's skip) transposed, channels zero-padded
+  ConvTPackArgs p;
+  p.x1 = a.x1;
+  p.x2 = a.C2 ? a.x2 : nullptr;
+  p.C1 = a.C1;
+  p.C2 = a.C2;
+  p.Cp = Cp;
+  p.L = n_in;
+  p.Lq = n_in;
+  p.u = unfold;
+  convt_pack_t1(c, p, a.B);
   const int ks = a.KH * a.KW;
   GemmArgs g;
   g.M = a.Cout * ks;
   g.N = (int)n_in;
-  g.K = Cin;
+  g.K = Cp;
   g.batch = a.B;
   g.A = wpack;
-  g.lda = convt2d_padded_cin(Cin);
-  g.B = x;
-  g.blayout = B_KN;
-  g.ldb = n_in;
-  g.sB = (int64_t)Cin * n_in;
+  g.lda = Cp;
+  g.B = unfold;
+  g.blayout = B_NK;
+  g.ldb = Cp;
+  g.sB = n_in * Cp;
   g.C = z;
   g.ldc = n_in;
   g.sC = (int64_t)g.M * n_in;
@@ -337,12 +357,18 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
   gemm(c, g);
   ConvT2DArgs t = a;
   t.z = z;
-  launch(c, "convt2d_gather_f32", convt2d_gather_kernel,
-         plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, t);
+  if (a.dh == 1 && a.dw == 1 && a.sw <= 8) {
+    const int64_t cells = (int64_t)a.Ho * ((a.Wo + a.sw - 1) / a.sw);
+    launch(c, "convt2d_gather_f32", convt2d_gather_phase_kernel, plane_grid(cells, a.Cout, a.B),
+           dim3(256), 0, t);
+  } else {
+    launch(c, "convt2d_gather_f32", convt2d_gather_kernel,
+           plane_grid((int64_t)a.Ho * a.Wo, a.Cout, a.B), dim3(256), 0, t);
+  }
 }
 
-int64_t convt2d_cat_floats(const ConvT2DArgs& a) {
-  return a.C2 > 0 ? (int64_t)a.B * (a.C1 + a.C2) * a.H * a.W : 0;
+int64_t convt2d_unfold_floats(const ConvT2DArgs& a) {
+  return (int64_t)a.B * a.H * a.W * convt2d_padded_cin(a.C1 + a.C2);
 }
 
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a) {

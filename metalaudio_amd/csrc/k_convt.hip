@@ -324,6 +324,14 @@ void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, floa
            a.Lout, a.Cout);
 }
 
+void convt_pack_t1(const LaunchCtx& c, const ConvTPackArgs& p, int B) {
+  MNN_REQUIRE(p.x1 && (p.C2 == 0 || p.x2) && p.u && p.Cp % 4 == 0 && p.Cp >= p.C1 + p.C2 &&
+                  p.Lq == p.L && p.L > 0 && B > 0 && B <= 65535,
+              MNN_ERR_INVALID_ARGUMENT, "convt_pack_t1: invalid arguments");
+  const dim3 grid((unsigned)cdiv(p.Lq, kPQ), (unsigned)cdiv(p.Cp, kPC), (unsigned)B);
+  launch(c, "convt_pack_f32", convt_pack_kernel<1>, grid, dim3(256), 0, p);
+}
+
 int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout) {
   return (int64_t)B * convt_rows(Lout, stride, pad) * (K / stride) * convt_padded_cin(Cin);
 }

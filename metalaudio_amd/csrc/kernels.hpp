@@ -167,15 +167,15 @@ struct ConvT2DArgs {
   const float* z = nullptr;  // GEMM form: tap products [B][Cout*KH*KW][H*W] (set by convt2d_gemm)
 };
 // Matrix-core form (groups 1): weights packed [Cout*KH*KW][convt2d_padded_cin] by
-// convt2d_pack_weights; tap-product workspace of convt2d_z_floats floats and, with a second
-// input, a concat workspace of convt2d_cat_floats floats.
+// convt2d_pack_weights; tap-product workspace of convt2d_z_floats floats and an operand
+// workspace of convt2d_unfold_floats floats (the input transposed to [H*W][Cp], both inputs).
 int convt2d_padded_cin(int Cin);
 bool convt2d_gemm_supported(const ConvT2DArgs& a);
 int64_t convt2d_z_floats(const ConvT2DArgs& a);
-int64_t convt2d_cat_floats(const ConvT2DArgs& a);
+int64_t convt2d_unfold_floats(const ConvT2DArgs& a);
 void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, float* out);
 void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
-                  float* cat);
+                  float* unfold);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
 
 // ------------------------------------------------------------------ separation (k_separate.hip)
@@ -246,6 +246,9 @@ int64_t convt_rows(int64_t Lout, int stride, int pad);
 void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, float* out);
 // Floats of the unfolded-input workspace the GEMM form needs.
 int64_t convt_unfold_floats(int B, int Cin, int K, int stride, int pad, int64_t Lout);
+// The T = 1 operand pack on its own: u[b][q][c] = [x1; x2][c][q] (zero for C1 + C2 <= c < Cp),
+// q < L (= Lq); the transposed operand of the 2-D transposed conv's tap GEMM.
+void convt_pack_t1(const LaunchCtx& c, const ConvTPackArgs& p, int B);
 void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold,
                 float* split_ws);
 void convt_direct(const LaunchCtx& c, const ConvTArgs& a);

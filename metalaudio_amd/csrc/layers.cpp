@@ -1371,9 +1371,8 @@ class ConvTranspose2DLayer : public Layer {
     a.y = y;
     if (gemm_) {
       z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
-      const int64_t cf = k::convt2d_cat_floats(a);
-      if (cf > 0) cat_.reserve(sizeof(float) * cf);
-      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), cf > 0 ? cat_.f32() : nullptr);
+      unfold_.reserve(sizeof(float) * k::convt2d_unfold_floats(a));
+      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), unfold_.f32());
     } else {
       k::convt2d_direct(ctx(s), a);
     }
@@ -1398,7 +1397,7 @@ class ConvTranspose2DLayer : public Layer {
   Param* w_ = nullptr;
   Param* b_ = nullptr;
   bool gemm_ = false;
-  DevBuf wpack_, z_, cat_;
+  DevBuf wpack_, z_, unfold_;
 };
 
 // FreqUNetEncoderBlock2D (FreqUNet2D.swift:12-192): Conv2D (reflect padding ((k-1)/2 per axis),
@@ -1468,8 +1467,8 @@ class FreqEncoderBlockLayer : public Layer {
 
 // FreqUNetDecoderBlock2D (FreqUNet2D.swift:198-428): concat(input, skip) over channels ->
 // ConvTranspose2D (padding (k-1)/2, output padding stride-1 per axis) -> GroupNorm -> tanh-GELU.
-// The concat is folded into the transposed conv (a second GEMM over the skip channels), so no
-// concatenated tensor is written. Parameters "conv_tr.*" (or "conv_transpose.*") and "norm.*".
+// The concat is folded into the transposed conv's operand pack, so no concatenated tensor is
+// written. Parameters "conv_tr.*" (or "conv_transpose.*") and "norm.*".
 class FreqDecoderBlockLayer : public Layer {
  public:
   FreqDecoderBlockLayer(Device* d, const mnn_freq_block_desc& desc) : Layer(d), d_(desc) {

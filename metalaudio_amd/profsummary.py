@@ -44,8 +44,8 @@ FAMILIES = [
     ("conv2d_unfold_kernel", "conv2d_unfold_f32"),
     ("conv2d_direct_kernel", "conv2d_direct_f32"),
     ("convt2d_gather_kernel", "convt2d_gather_f32"),
+    ("convt2d_gather_phase_kernel", "convt2d_gather_f32"),
     ("convt2d_direct_kernel", "convt2d_direct_f32"),
-    ("concat2_kernel", "concat2_f32"),
     ("stft_forward_kernel", "stft_forward_f32"),
     ("stft_inverse_kernel", "istft_frames_f32"),
     ("stft_overlap_add_kernel", "istft_overlap_add_f32"),
