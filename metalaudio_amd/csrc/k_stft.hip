@@ -48,13 +48,24 @@ __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool in
   }
 }
 
+// Frame of this workgroup. Workgroups are dealt to the 8 XCDs round robin; numbering the frames
+// so that consecutive frames run on one XCD lets the bin-major layout's writes (consecutive
+// frames of one bin share a cache line) merge in that XCD's L2. The grid is padded to a multiple
+// of 8 (frames past the end return before any barrier).
+__device__ __forceinline__ int64_t frame_of_block(int64_t frames) {
+  const unsigned per = gridDim.x / 8;
+  return (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
+}
+
 __device__ __forceinline__ int bitrev(int m, int logM) {
   return logM == 0 ? 0 : (int)(__brev((unsigned)m) >> (32 - logM));
 }
 
 __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   extern __shared__ float2 z[];
-  const int f = blockIdx.x, b = blockIdx.y;
+  const int64_t f = frame_of_block(a.frames);
+  const int b = blockIdx.y;
+  if (f >= a.frames) return;
   const int M = a.N / 2;
   const float* xs = a.x + (int64_t)b * a.n + (int64_t)f * a.hop;
   for (int m = threadIdx.x; m < M; m += kThreads) {
@@ -87,7 +98,9 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
 
 __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
   extern __shared__ float2 z[];
-  const int f = blockIdx.x, b = blockIdx.y;
+  const int64_t f = frame_of_block(a.frames);
+  const int b = blockIdx.y;
+  if (f >= a.frames) return;
   const int M = a.N / 2;
   const int bins = a.onesided ? M + 1 : a.N;
   const int64_t base = (int64_t)b * a.frames * bins;
@@ -149,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void stft_overlap_add_kernel(StftArgs a) 
 
 void check(const StftArgs& a) {
   MNN_REQUIRE(a.N >= 4 && a.N <= kStftMaxN && (a.N & (a.N - 1)) == 0 && a.hop > 0 &&
-                  a.batch > 0 && a.batch <= 65535 && a.frames > 0 && a.frames <= 2147483647 &&
+                  a.batch > 0 && a.batch <= 65535 && a.frames > 0 && a.frames <= 2147483640 &&
                   a.win && a.tw,
               MNN_ERR_INVALID_ARGUMENT, "stft: invalid configuration");
 }
@@ -161,16 +174,18 @@ void stft_forward(const LaunchCtx& c, const StftArgs& a) {
   MNN_REQUIRE(a.x && a.re && a.im && a.n >= a.N &&
                   (int64_t)(a.frames - 1) * a.hop + a.N <= a.n,
               MNN_ERR_INVALID_ARGUMENT, "stft_forward: frames exceed the signal");
-  launch(c, "stft_forward_f32", stft_forward_kernel, dim3((unsigned)a.frames, (unsigned)a.batch),
-         dim3(kThreads), sizeof(float2) * (a.N / 2), a);
+  launch(c, "stft_forward_f32", stft_forward_kernel,
+         dim3((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch), dim3(kThreads),
+         sizeof(float2) * (a.N / 2), a);
 }
 
 void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
   check(a);
   MNN_REQUIRE(a.cre && a.cim && a.frames_buf && a.y, MNN_ERR_INVALID_ARGUMENT,
               "stft_inverse: missing buffers");
-  launch(c, "istft_frames_f32", stft_inverse_kernel, dim3((unsigned)a.frames, (unsigned)a.batch),
-         dim3(kThreads), sizeof(float2) * (a.N / 2), a);
+  launch(c, "istft_frames_f32", stft_inverse_kernel,
+         dim3((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch), dim3(kThreads),
+         sizeof(float2) * (a.N / 2), a);
   const int64_t L = (int64_t)(a.frames - 1) * a.hop + a.N;
   launch(c, "istft_overlap_add_f32", stft_overlap_add_kernel,
          dim3((unsigned)cdiv(L, kThreads), (unsigned)a.batch), dim3(kThreads), 0, a);
