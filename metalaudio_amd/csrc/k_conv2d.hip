@@ -47,7 +47,9 @@ __device__ __forceinline__ float conv2d_sample(const float* xc, int r, int s, in
 
 // U[b][n][k] for n = oh*Wo + ow, k = (ic, kh, kw) < K, zero for K <= k < Kp; four k per thread
 // (one 16-byte store).
-// Index math is 32-bit (the host checks N * Kp / 4 < 2^31).
+// Index math is 32-bit (the host checks N * Kp / 4 < 2^31). KH_/KW_ > 0 fix the kernel size at
+// compile time (the divisions by it become multiplications); 0 reads it from the arguments.
+template <int KH_, int KW_>
 __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
   const unsigned N = (unsigned)a.Ho * (unsigned)a.Wo;
   const unsigned kq = (unsigned)a.Kp / 4;
@@ -57,7 +59,8 @@ __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
   const unsigned n = e / kq;
   const int k0 = (int)(e - n * kq) * 4;
   const int oh = (int)(n / (unsigned)a.Wo), ow = (int)(n - (unsigned)oh * a.Wo);
-  const int ks = a.KH * a.KW, K = a.Cin * ks;
+  const int KW = KW_ > 0 ? KW_ : a.KW;
+  const int ks = KH_ > 0 ? KH_ * KW_ : a.KH * a.KW, K = a.Cin * ks;
   const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
   float v[4];
 #pragma unroll
@@ -65,7 +68,7 @@ __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
     const int k = k0 + j;
     v[j] = 0.f;
     if (k < K) {
-      const int ic = k / ks, kh = (k % ks) / a.KW, kw = k % a.KW;
+      const int ic = k / ks, kh = (k % ks) / KW, kw = k % KW;
       v[j] = conv2d_sample(xb + (int64_t)ic * a.H * a.W, oh * a.sh - a.ph + kh * a.dh,
                            ow * a.sw - a.pw + kw * a.dw, a.H, a.W, a.reflect);
     }
@@ -286,8 +289,13 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
   a.u = unfold;
   MNN_REQUIRE(N * (a.Kp / 4) < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
               "conv2d_gemm: unfold too large");
-  launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel,
-         dim3((unsigned)cdiv(N * (a.Kp / 4), 256), (unsigned)a.B), dim3(256), 0, a);
+  const dim3 ug((unsigned)cdiv(N * (a.Kp / 4), 256), (unsigned)a.B);
+  if (a.KH == 3 && a.KW == 3)
+    launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel<3, 3>, ug, dim3(256), 0, a);
+  else if (a.KH == 8 && a.KW == 1)
+    launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel<8, 1>, ug, dim3(256), 0, a);
+  else
+    launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel<0, 0>, ug, dim3(256), 0, a);
   g.K = a.Kp;
   g.lda = a.Kp;
   g.B = unfold;
