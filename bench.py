@@ -421,7 +421,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     # STFT / iSTFT of one stereo 7.8 s chunk at HTDemucs' nfft 4096 / hop 1024 (bin-major
     # spectrogram, as the frequency branch consumes it); bytes = signal read + spectra written
     # (forward), spectra read + frames written and re-read + signal written (inverse)
-    from oracle import dsp as odsp  # noqa: E402  (CPU baseline only)
+    if cpu:
+        from oracle import dsp as odsp  # CPU baseline only
     xs = np.random.default_rng(1008).uniform(-1, 1, (2, 343980)).astype(np.float32)
     plan = nn.STFT(dev, 4096, 1024, "hann")
     xst = nn.Tensor.from_numpy(dev, xs)
@@ -447,7 +448,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     # long-audio driver: 60 s of stereo audio through the reference's default time-domain
     # HTDemucs (5 levels 48..768, k 8, s 4, 4 stems) in the guide's 30 s segments with 2 s
     # overlap (HTDEMUCS_GUIDE.md:170-191); synthetic weights and audio
-    from oracle import separate as osep  # noqa: E402  (CPU baseline only)
+    if cpu:
+        from oracle import separate as osep  # CPU baseline only
     r11 = np.random.default_rng(1009)
     ch11 = [48, 96, 192, 384, 768]
     cfg11 = {"input_channels": 2, "num_stems": 4, "channels": ch11, "kernel_size": 8,
