@@ -25,6 +25,7 @@ using namespace dev;
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kStftLdsTwMaxN = 8192;  // LDS twiddles up to 64 KB of LDS per workgroup
 
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
@@ -61,19 +62,24 @@ __device__ __forceinline__ int bitrev(int m, int logM) {
   return logM == 0 ? 0 : (int)(__brev((unsigned)m) >> (32 - logM));
 }
 
+// With LDS_TW the twiddle table is copied to LDS with the input (one global-latency exposure
+// instead of one per butterfly pass); LDS holds z then the table (N/2 float2 each).
+template <bool LDS_TW>
 __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   extern __shared__ float2 z[];
   const int64_t f = frame_of_block(a.frames);
   const int b = blockIdx.y;
   if (f >= a.frames) return;
   const int M = a.N / 2;
+  float2* tws = z + M;
   const float* xs = a.x + (int64_t)b * a.n + (int64_t)f * a.hop;
   for (int m = threadIdx.x; m < M; m += kThreads) {
     const float e = xs[2 * m] * a.win[2 * m], o = xs[2 * m + 1] * a.win[2 * m + 1];
     z[bitrev(m, a.logM)] = make_float2(e, o);
+    if (LDS_TW) tws[m] = a.tw[m];
   }
   __syncthreads();
-  fft_lds(z, M, a.tw, false);
+  fft_lds(z, M, LDS_TW ? tws : a.tw, false);
   const int bins = a.onesided ? M + 1 : a.N;
   const int64_t base = (int64_t)b * a.frames * bins;
   for (int k = threadIdx.x; k <= M; k += kThreads) {
@@ -82,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
     const float2 fe = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y - zc.y));
     const float2 d = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y + zc.y));  // (Zk - conj Zc)/2
     const float2 fo = make_float2(d.y, -d.x);                                    // -i * d
-    const float2 w = k == M ? make_float2(-1.f, 0.f) : a.tw[k];
+    const float2 w = k == M ? make_float2(-1.f, 0.f) : (LDS_TW ? tws[k] : a.tw[k]);
     const float2 t = cmul(w, fo);
     const float re = fe.x + t.x, im = fe.y + t.y;
     auto put = [&](int kk, float r, float i) {
@@ -96,12 +102,14 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   }
 }
 
+template <bool LDS_TW>
 __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
   extern __shared__ float2 z[];
   const int64_t f = frame_of_block(a.frames);
   const int b = blockIdx.y;
   if (f >= a.frames) return;
   const int M = a.N / 2;
+  float2* tws = z + M;
   const int bins = a.onesided ? M + 1 : a.N;
   const int64_t base = (int64_t)b * a.frames * bins;
   auto get = [&](int kk) {
@@ -124,12 +132,14 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
     const float2 hk = herm(k), hc = herm(M - k);
     const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
     const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
-    const float2 w = make_float2(a.tw[k].x, -a.tw[k].y);  // e^{+2 pi i k / N}
+    const float2 t = a.tw[k];
+    if (LDS_TW) tws[k] = t;
+    const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
     const float2 fo = cmul(d, w);
     z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
   }
   __syncthreads();
-  fft_lds(z, M, a.tw, true);
+  fft_lds(z, M, LDS_TW ? tws : a.tw, true);
   const float s = 1.f / (float)M;
   float* out = a.frames_buf + ((int64_t)b * a.frames + f) * a.N;
   for (int m = threadIdx.x; m < M; m += kThreads) {
@@ -174,18 +184,26 @@ void stft_forward(const LaunchCtx& c, const StftArgs& a) {
   MNN_REQUIRE(a.x && a.re && a.im && a.n >= a.N &&
                   (int64_t)(a.frames - 1) * a.hop + a.N <= a.n,
               MNN_ERR_INVALID_ARGUMENT, "stft_forward: frames exceed the signal");
-  launch(c, "stft_forward_f32", stft_forward_kernel,
-         dim3((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch), dim3(kThreads),
-         sizeof(float2) * (a.N / 2), a);
+  const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
+  if (a.N <= kStftLdsTwMaxN)
+    launch(c, "stft_forward_f32", stft_forward_kernel<true>, grid, dim3(kThreads),
+           sizeof(float2) * a.N, a);
+  else
+    launch(c, "stft_forward_f32", stft_forward_kernel<false>, grid, dim3(kThreads),
+           sizeof(float2) * (a.N / 2), a);
 }
 
 void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
   check(a);
   MNN_REQUIRE(a.cre && a.cim && a.frames_buf && a.y, MNN_ERR_INVALID_ARGUMENT,
               "stft_inverse: missing buffers");
-  launch(c, "istft_frames_f32", stft_inverse_kernel,
-         dim3((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch), dim3(kThreads),
-         sizeof(float2) * (a.N / 2), a);
+  const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
+  if (a.N <= kStftLdsTwMaxN)
+    launch(c, "istft_frames_f32", stft_inverse_kernel<true>, grid, dim3(kThreads),
+           sizeof(float2) * a.N, a);
+  else
+    launch(c, "istft_frames_f32", stft_inverse_kernel<false>, grid, dim3(kThreads),
+           sizeof(float2) * (a.N / 2), a);
   const int64_t L = (int64_t)(a.frames - 1) * a.hop + a.N;
   launch(c, "istft_overlap_add_f32", stft_overlap_add_kernel,
          dim3((unsigned)cdiv(L, kThreads), (unsigned)a.batch), dim3(kThreads), 0, a);
