@@ -389,6 +389,13 @@ mnn_status mnn_weight_name_is_demucs(const char* name, int* out);
 mnn_status mnn_safetensors_find_mapped(mnn_safetensors st, int convention,
                                        const char* metalaudio_name, char* buf, size_t cap);
 
+/* Separator weights from a SafeTensors file (HTDemucs.loadWeights(from:convention:)) for the
+ * time-domain model (mnn_separator, declared with the separation driver): every tensor whose
+ * name, mapped from `convention` (mnn_weight_convention) to MetalAudio names, starts with
+ * time_encoder. / time_decoder. / output_heads. is loaded; *loaded = their count. */
+mnn_status mnn_separator_load_safetensors(mnn_separator sep, mnn_safetensors st, int convention,
+                                          int* loaded);
+
 /* "MTLA" binary model files (BinaryModelLoader, Model.swift:401-679): reader (v2 with CRC-32
  * check, legacy v1) and writer (v2, tensors in name order). fp32 tensors, host-only. */
 typedef struct mnn_mtla_s* mnn_mtla;

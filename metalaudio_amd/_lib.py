@@ -149,6 +149,7 @@ SIGNATURES = {
     "mnn_separator_create": (C.c_int, [P, C.POINTER(SeparatorDesc), PP]),
     "mnn_separator_destroy": (C.c_int, [P]),
     "mnn_separator_load": (C.c_int, [P, C.c_char_p, FP, C.c_size_t]),
+    "mnn_separator_load_safetensors": (C.c_int, [P, P, C.c_int, IP]),
     "mnn_separator_separate": (C.c_int, [P, P, P, P]),
     "mnn_separator_separate_long": (C.c_int, [P, P, P, C.c_int64, C.c_int64, P]),
     "mnn_stft_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),

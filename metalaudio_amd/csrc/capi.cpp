@@ -785,6 +785,18 @@ mnn_status mnn_safetensors_find_mapped(mnn_safetensors st, int convention,
   });
 }
 
+mnn_status mnn_separator_load_safetensors(mnn_separator sep, mnn_safetensors st, int convention,
+                                          int* loaded) {
+  return guard([&] {
+    TimeSeparator* p = SEP(sep);
+    MNN_REQUIRE(convention >= WC_METALAUDIO && convention <= WC_UNKNOWN,
+                MNN_ERR_INVALID_ARGUMENT, "unknown naming convention " << convention);
+    p->device()->check_alive();
+    const int n = p->load_safetensors(*ST(st), static_cast<WeightConvention>(convention));
+    if (loaded) *loaded = n;
+  });
+}
+
 // ------------------------------------------------------------------ MTLA
 namespace {
 MtlaFile* MT(mnn_mtla m) {

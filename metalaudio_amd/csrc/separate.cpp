@@ -97,6 +97,23 @@ void TimeSeparator::load(const std::string& name, const float* data, size_t n) {
   fail(MNN_ERR_INVALID_ARGUMENT, "separator: unknown parameter '" + name + "'");
 }
 
+int TimeSeparator::load_safetensors(const SafeTensorsFile& f, WeightConvention conv) {
+  int loaded = 0;
+  std::vector<float> buf;
+  for (const std::string& name : f.names()) {
+    const std::string m = to_metalaudio(conv, name);
+    if (m.rfind("time_encoder.", 0) != 0 && m.rfind("time_decoder.", 0) != 0 &&
+        m.rfind("output_heads.", 0) != 0)
+      continue;
+    const int64_t n = f.info(name).count();
+    buf.resize((size_t)n);
+    f.read_f32(name, buf.data(), buf.size());
+    load(m, buf.data(), buf.size());
+    ++loaded;
+  }
+  return loaded;
+}
+
 void TimeSeparator::plan(int64_t Lp) {
   if (planned_ == Lp) return;
   const int C = d_.input_channels, S = d_.num_stems, Lv = d_.levels;

@@ -4,6 +4,8 @@
 #pragma once
 
 #include "layers.hpp"
+#include "safetensors.hpp"
+#include "weight_names.hpp"
 
 namespace mnn {
 
@@ -13,6 +15,10 @@ class TimeSeparator {
   // "time_encoder.{i}.*" (level i), "time_decoder.{j}.*" (j = 0 is the deepest level, as the
   // reference's timeDecoders array), "output_heads.{s}.weight|bias".
   void load(const std::string& name, const float* data, size_t n);
+  // HTDemucs.loadWeights(from:) for the time-domain model: every tensor of the file whose name,
+  // mapped to the MetalAudio convention, addresses this model is read as fp32 and loaded; other
+  // tensors (the frequency branch, the transformer) are skipped. Returns the number loaded.
+  int load_safetensors(const SafeTensorsFile& f, WeightConvention conv);
   // x: interleaved [n * C]; out: [S, n * C] interleaved stems
   void separate(const Tensor& x, Tensor& out, Stream& s);
   // Segments of `segment` frames every segment - overlap frames, crossfaded over the frames a

@@ -551,6 +551,16 @@ class Separator:
             else:
                 self.load(k, v)
 
+    def load_safetensors(self, st: "SafeTensors", mapper: Optional["WeightNameMapper"] = None
+                         ) -> int:
+        """HTDemucs.loadWeights(from:): the file's time-domain tensors, names mapped by `mapper`
+        (detected from the file when None). Returns how many were loaded."""
+        m = mapper if mapper is not None else st.create_weight_mapper()
+        n = C.c_int()
+        check(lib().mnn_separator_load_safetensors(self.handle, st.handle, NAMING[m.convention],
+                                                   C.byref(n)))
+        return n.value
+
     def separate(self, x: Tensor, stream: Optional[Stream] = None) -> Tensor:
         out = Tensor(self.device, (self.num_stems, x.shape[0]))
         check(lib().mnn_separator_separate(self.handle, x.handle, out.handle, _sh(stream)))

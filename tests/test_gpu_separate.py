@@ -106,3 +106,35 @@ def test_separator_errors(dev, stream):
     x = nn.Tensor.from_numpy(dev, np.zeros(2 * 1000, np.float32))
     with pytest.raises(nn.MNNError):
         sep.separate_long(x, 300, 300, stream)  # overlap must be below the segment
+
+
+def test_separator_weights_from_demucs_named_safetensors(dev, stream, tmp_path):
+    """HTDemucs.loadWeights(from:) with a Demucs-named file: names mapped by the detected
+    convention (tencoder.i.norm1 -> time_encoder.i.norm, tdecoder.j.conv_tr ->
+    time_decoder.j.conv_transpose, ...), frequency-branch tensors skipped, then the separation
+    matches the oracle on the same weights."""
+    from safetensors.numpy import save_file
+    cfg, P = model(levels=2)
+    say("separator weights from a Demucs-named safetensors file")
+    flat = {}
+    for k, v in P.items():
+        for kk, vv in v.items():
+            name = f"{k}.{kk}"
+            name = (name.replace("time_encoder.", "tencoder.").replace(".norm.", ".norm1.")
+                    if name.startswith("time_encoder.") else name)
+            if name.startswith("time_decoder."):
+                name = (name.replace("time_decoder.", "tdecoder.")
+                        .replace(".conv_transpose.", ".conv_tr.").replace(".norm.", ".norm2."))
+            flat[name] = np.ascontiguousarray(vv)
+    flat["encoder.0.conv.weight"] = np.zeros((4, 2, 3, 3), np.float32)  # frequency branch
+    flat["crosstransformer.layers.0.norm1.weight"] = np.ones(8, np.float32)
+    save_file(flat, str(tmp_path / "demucs.safetensors"))
+    st = nn.SafeTensors(tmp_path / "demucs.safetensors")
+    assert st.create_weight_mapper().convention == "demucs"
+    sep = nn.Separator(dev, 2, 4, cfg["channels"], 8, 4, 4)
+    n_loaded = sep.load_safetensors(st)
+    assert n_loaded == sum(len(v) for v in P.values())
+    x = RNG.uniform(-1, 1, 2 * 3000).astype(np.float32)
+    out = sep.separate(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    assert_close(out.to_numpy(), osep.separate_time(x, P, cfg), 1e-4, 1e-3, "separate")
