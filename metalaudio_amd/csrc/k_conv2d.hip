@@ -214,6 +214,36 @@ dim3 plane_grid(int64_t hw, int C, int B) {
   return dim3((unsigned)cdiv(hw, 256), (unsigned)C, (unsigned)B);
 }
 
+// y[b][m][n] = bias[m] + sum over the K parts q (ascending) of ws[b][q][m][n].
+__global__ __launch_bounds__(256) void conv2d_split_reduce_kernel(const float* __restrict__ ws,
+                                                                  const float* __restrict__ bias,
+                                                                  float* __restrict__ y, int M,
+                                                                  unsigned N, int parts) {
+  const int b = blockIdx.y;
+  const unsigned e = blockIdx.x * 256u + threadIdx.x;
+  if (e >= (unsigned)M * N) return;
+  const int m = (int)(e / N);
+  const int64_t mn = (int64_t)M * N;
+  const float* w = ws + (int64_t)b * parts * mn + e;
+  float acc = 0.f;
+  for (int q = 0; q < parts; ++q) acc += w[q * mn];
+  y[(int64_t)b * mn + e] = acc + (bias ? bias[m] : 0.f);
+}
+
+// K split of the unfold GEMM for grids too small to fill the chip (few output tiles, long K):
+// parts p with (Kp/32) % p == 0, at least 6 K steps each, at most 1024 tiles in all.
+int conv2d_ksplit(const Conv2DArgs& a) {
+  if (conv2d_pointwise(a)) return 1;
+  const int64_t N = (int64_t)a.Ho * a.Wo;
+  const int nk = conv2d_padded_k(a.Cin, a.KH, a.KW) / 32;
+  const int64_t tiles = cdiv(a.Cout, 64) * cdiv(N, 64) * a.B;
+  int best = 1;
+  if (tiles > 384) return best;
+  for (int p : {2, 3, 4, 6, 8})
+    if (nk % p == 0 && nk / p >= 6 && tiles * p <= 1024) best = p;
+  return best;
+}
+
 void check_conv2d(const Conv2DArgs& a) {
   MNN_REQUIRE(a.B > 0 && a.Cin > 0 && a.Cout > 0 && a.groups > 0 && a.Cin % a.groups == 0 &&
                   a.Cout % a.groups == 0 && a.KH > 0 && a.KW > 0 && a.sh > 0 && a.sw > 0 &&
@@ -247,6 +277,11 @@ bool conv2d_pointwise(const Conv2DArgs& a) {
          a.pw == 0 && a.Ho == a.H && a.Wo == a.W;
 }
 
+int64_t conv2d_split_ws_floats(const Conv2DArgs& a) {
+  const int p = conv2d_ksplit(a);
+  return p > 1 ? (int64_t)a.B * p * a.Cout * a.Ho * a.Wo : 0;
+}
+
 int64_t conv2d_unfold_floats(const Conv2DArgs& a) {
   return conv2d_pointwise(a) ? 0 : (int64_t)a.B * a.Ho * a.Wo * conv2d_padded_k(a.Cin, a.KH, a.KW);
 }
@@ -257,7 +292,8 @@ void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, floa
     for (int k = 0; k < Kp; ++k) out[(int64_t)oc * Kp + k] = k < K ? w[(int64_t)oc * K + k] : 0.f;
 }
 
-void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack, float* unfold) {
+void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack, float* unfold,
+                 float* split_ws) {
   Conv2DArgs a = a_in;
   check_conv2d(a);
   MNN_REQUIRE(conv2d_gemm_supported(a) && wpack, MNN_ERR_INVALID_ARGUMENT,
@@ -302,6 +338,24 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
   g.blayout = B_NK;
   g.ldb = a.Kp;
   g.sB = N * a.Kp;
+  const int parts = conv2d_ksplit(a);
+  if (parts > 1 && split_ws) {
+    g.ksplit = parts;
+    g.ws = split_ws;
+    g.bias = nullptr;
+    g.bias_mode = BIAS_NONE;
+    if (gemm_nk_lds_supported(g)) {
+      gemm_nk_lds(c, g);
+      launch(c, "conv2d_split_reduce_f32", conv2d_split_reduce_kernel,
+             dim3((unsigned)cdiv(N * a.Cout, 256), (unsigned)a.B), dim3(256), 0, split_ws,
+             a.bias, a.y, a.Cout, (unsigned)N, parts);
+      return;
+    }
+    g.ksplit = 1;
+    g.ws = nullptr;
+    g.bias = a.bias;
+    g.bias_mode = a.bias ? BIAS_M : BIAS_NONE;
+  }
   gemm(c, g);
 }
 

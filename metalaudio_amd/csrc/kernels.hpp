@@ -150,8 +150,11 @@ int conv2d_padded_k(int Cin, int KH, int KW);
 bool conv2d_gemm_supported(const Conv2DArgs& a);
 bool conv2d_pointwise(const Conv2DArgs& a);
 int64_t conv2d_unfold_floats(const Conv2DArgs& a);
+// Workspace of the K split conv2d_gemm chooses for small grids (0: no split).
+int64_t conv2d_split_ws_floats(const Conv2DArgs& a);
 void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out);
-void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a, const float* wpack, float* unfold);
+void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a, const float* wpack, float* unfold,
+                 float* split_ws);
 void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a);
 
 // DynamicConvTranspose2D (DynamicConv2D.swift:598-959) over the channel concat [x1; x2] (C2 may

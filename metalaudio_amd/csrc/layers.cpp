@@ -1264,7 +1264,10 @@ class Conv2DLayer : public Layer {
     if (gemm_) {
       const int64_t uf = k::conv2d_unfold_floats(a);
       if (uf > 0) unfold_.reserve(sizeof(float) * uf);
-      k::conv2d_gemm(ctx(s), a, wpack_.f32(), uf > 0 ? unfold_.f32() : nullptr);
+      const int64_t wf = k::conv2d_split_ws_floats(a);
+      if (wf > 0) split_.reserve(sizeof(float) * wf);
+      k::conv2d_gemm(ctx(s), a, wpack_.f32(), uf > 0 ? unfold_.f32() : nullptr,
+                     wf > 0 ? split_.f32() : nullptr);
     } else {
       k::conv2d_direct(ctx(s), a);
     }
@@ -1289,7 +1292,7 @@ class Conv2DLayer : public Layer {
   Param* w_ = nullptr;
   Param* b_ = nullptr;
   bool gemm_ = false;
-  DevBuf wpack_, unfold_;
+  DevBuf wpack_, unfold_, split_;
 };
 
 // DynamicConvTranspose2D (DynamicConv2D.swift:598-959): output (n - 1)s - 2p + (k - 1)d + 1 + op
