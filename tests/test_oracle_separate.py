@@ -85,3 +85,43 @@ def test_model_composes_layer_oracles():
     h1 = ol.conv1d(d1, P["output_heads.1"]["weight"], P["output_heads.1"]["bias"])
     np.testing.assert_allclose(osep.separate_time(x, P, cfg)[1],
                                h1[:, lp:lp + n].T.reshape(-1), atol=1e-12)
+
+
+def test_time_unet_matches_separator_chain():
+    """oracle.layers.time_unet (the U-Net alone) against separate_time's independently written
+    chain: with num_groups = 2 every level's GroupNorm has 2 groups in both (separate_time's level-0
+    min(groups, input channels) rule gives 2 as well), and one stem whose 1x1 head is the identity
+    returns the U-Net output itself, cropped and interleaved. The decoder order (deepest first), the
+    skip each decoder level takes and the padding are thereby pinned against each other."""
+    r = np.random.default_rng(5)
+    cfg = {"input_channels": 2, "num_stems": 1, "channels": [8, 16, 32], "kernel_size": 8,
+           "stride": 4, "num_groups": 2}
+    chans = [2] + cfg["channels"]
+    P, enc, dec = {}, [], []
+    for i in range(3):
+        ci, co = chans[i], chans[i + 1]
+        P[f"time_encoder.{i}"] = {"conv.weight": r.standard_normal((co, ci, 8)) * 0.3,
+                                  "conv.bias": r.standard_normal(co) * 0.1,
+                                  "norm.weight": 1 + 0.1 * r.standard_normal(co),
+                                  "norm.bias": 0.1 * r.standard_normal(co)}
+        enc.append(P[f"time_encoder.{i}"])
+    for j in range(3):
+        i = 2 - j
+        ci, co = chans[i + 1], chans[i]
+        p = {"conv_transpose.weight": r.standard_normal((2 * ci, co, 8)) * 0.2,
+             "conv_transpose.bias": r.standard_normal(co) * 0.1,
+             "norm.weight": 1 + 0.1 * r.standard_normal(co),
+             "norm.bias": 0.1 * r.standard_normal(co)}
+        P[f"time_decoder.{j}"] = p
+        dec.append({"conv_tr.weight": p["conv_transpose.weight"],
+                    "conv_tr.bias": p["conv_transpose.bias"], "norm.weight": p["norm.weight"],
+                    "norm.bias": p["norm.bias"], "groups": 2})
+    P["output_heads.0"] = {"weight": np.eye(2)[:, :, None], "bias": np.zeros(2)}
+    n = 1500
+    x = r.standard_normal(n * 2)
+    got = osep.separate_time(x, P, cfg)[0]
+    lp, _, Lp = ol.unet_padding(n, 3, 8, 4)
+    xp = np.zeros((1, 2, Lp))
+    xp[0, :, lp:lp + n] = x.reshape(n, 2).T
+    u = ol.time_unet(xp, enc, dec, enc_groups=2)[0]
+    np.testing.assert_allclose(got, u[:, lp:lp + n].T.reshape(-1), rtol=1e-12, atol=1e-12)
