@@ -176,7 +176,9 @@ mnn_status mnn_linear_create(mnn_device dev, int in_features, int out_features, 
 /* MultiHeadAttention / CrossAttention (Attention.swift:15-1063), PyTorch packing:
  * "in_proj_weight" [3E, E] rows Q;K;V, "in_proj_bias" [3E], "out_proj_weight" [E, E],
  * "out_proj_bias" [E]. Input [S, E] or [B, S, E]. Self-attention through mnn_layer_forward,
- * cross-attention through mnn_layer_forward_cross(query, keyValue, output). */
+ * cross-attention through mnn_layer_forward_cross(query, keyValue, output).
+ * `precision` applies to the Q/K/V and output projections (MNN_PRECISION_BF16: bf16 operands,
+ * fp32 accumulation); the attention core (Q K^T, softmax, P V) always runs in fp32. */
 mnn_status mnn_mha_create(mnn_device dev, int embed_dim, int num_heads, int use_bias,
                           mnn_precision precision, mnn_layer* out);
 
@@ -313,7 +315,7 @@ mnn_status mnn_separator_create(mnn_device dev, const mnn_separator_desc* desc,
 mnn_status mnn_separator_destroy(mnn_separator sep);
 /* "time_encoder.{i}.{conv,norm}.{weight,bias}", "time_decoder.{j}.{conv_transpose|conv_tr,norm}.
  * {weight,bias}" (j = 0 is the deepest level, the order of HTDemucs.loadWeights), and
- * "output_heads.{s}.{weight,bias}". */
+ * "time_output_heads.{s}.{weight,bias}" (HTDemucs.swift:1021; "output_heads.{s}" also accepted). */
 mnn_status mnn_separator_load(mnn_separator sep, const char* name, const float* data, size_t n);
 /* HTDemucs.separate(input:mode: .timeOnly) on device tensors: input [n * C] interleaved, output
  * [num_stems, n * C] interleaved stems. */
@@ -392,7 +394,11 @@ mnn_status mnn_safetensors_find_mapped(mnn_safetensors st, int convention,
 /* Separator weights from a SafeTensors file (HTDemucs.loadWeights(from:convention:)) for the
  * time-domain model (mnn_separator, declared with the separation driver): every tensor whose
  * name, mapped from `convention` (mnn_weight_convention) to MetalAudio names, starts with
- * time_encoder. / time_decoder. / output_heads. is loaded; *loaded = their count. */
+ * time_encoder. / time_decoder. / time_output_heads. (or output_heads.) is loaded; *loaded = their
+ * count. As the reference (HTDemucs.swift:892-937), every encoder conv weight and norm weight /
+ * bias and every decoder transposed-conv weight and norm weight / bias must be in the file:
+ * otherwise MNN_ERR_TENSOR_NOT_FOUND names the first one missing and nothing is loaded. Conv
+ * biases and output heads are optional. */
 mnn_status mnn_separator_load_safetensors(mnn_separator sep, mnn_safetensors st, int convention,
                                           int* loaded);
 

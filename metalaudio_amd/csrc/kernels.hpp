@@ -327,8 +327,8 @@ struct AttnArgs {
   float* o = nullptr;
   int64_t o_bs = 0, o_rs = 0;
   float scale = 1.f;
-  mnn_precision precision = MNN_PRECISION_F32;
 };
+// fp32 throughout (operands, scores, softmax, accumulation).
 bool attention_supported(int hd);
 void attention(const LaunchCtx& c, const AttnArgs& a);
 

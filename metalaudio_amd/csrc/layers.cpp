@@ -440,7 +440,8 @@ class LinearLayer : public Layer {
 // MultiHeadAttention / CrossAttention (Attention.swift:15-1063). Q, K, V come from one packed
 // projection GEMM (self) or a Q GEMM plus a KV GEMM over rows E..3E of in_proj (cross); the
 // fused attention kernel reads them in place with row strides, and the output projection can
-// fuse a residual with LayerScale.
+// fuse a residual with LayerScale. The layer's precision applies to the projection GEMMs; the
+// attention core (scores, softmax, P.V) always runs in fp32.
 class MHALayer : public Layer {
  public:
   MHALayer(Device* d, int embed, int heads, bool bias, mnn_precision prec)
@@ -499,7 +500,6 @@ class MHALayer : public Layer {
     at.Sq = Sq;
     at.hd = hd_;
     at.scale = 1.f / std::sqrt((float)hd_);
-    at.precision = prec_;
     if (!xkv) {
       qkv_.reserve(sizeof(float) * rq * 3 * E);
       proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, 3 * E, qkv_.f32(), s);

@@ -287,7 +287,11 @@ size_t st_dtype_size(StDType t) {
   }
 }
 
-int64_t StTensorInfo::count() const { return (int64_t)((end - begin) / st_dtype_size(dtype)); }
+int64_t StTensorInfo::count() const {
+  MNN_REQUIRE(end >= begin, MNN_ERR_INVALID_FILE,
+              "tensor byte range [" << begin << ", " << end << ") is reversed");
+  return (int64_t)((end - begin) / st_dtype_size(dtype));
+}
 
 float st_half_to_float(uint16_t h) {
   const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;

@@ -91,27 +91,55 @@ void TimeSeparator::load(const std::string& name, const float* data, size_t n) {
     return true;
   };
   dev_->make_current();
+  // heads: the reference's name (HTDemucs.swift:1021) and this library's earlier short form
   if (indexed("time_encoder.", enc_) || indexed("time_decoder.", dec_) ||
-      indexed("output_heads.", heads_))
+      indexed("time_output_heads.", heads_) || indexed("output_heads.", heads_))
     return;
   fail(MNN_ERR_INVALID_ARGUMENT, "separator: unknown parameter '" + name + "'");
 }
 
+namespace {
+bool separator_tensor(const std::string& m) {
+  return m.rfind("time_encoder.", 0) == 0 || m.rfind("time_decoder.", 0) == 0 ||
+         m.rfind("time_output_heads.", 0) == 0 || m.rfind("output_heads.", 0) == 0;
+}
+}  // namespace
+
 int TimeSeparator::load_safetensors(const SafeTensorsFile& f, WeightConvention conv) {
-  int loaded = 0;
-  std::vector<float> buf;
+  // The tensors HTDemucs.loadWeights(from:mapper:) requires (HTDemucs.swift:892-937): every
+  // encoder conv weight and GroupNorm weight / bias, every decoder transposed-conv weight and
+  // GroupNorm weight / bias. Conv biases are optional (loadConv1DWeights,
+  // SafeTensorsLoader.swift:238-258) and so are the output heads (:1017-1029). All of them are
+  // checked before anything is loaded, so a file that lacks one leaves the model unchanged.
+  std::map<std::string, std::string> by_ma;  // MetalAudio name -> the file's own name
   for (const std::string& name : f.names()) {
     const std::string m = to_metalaudio(conv, name);
-    if (m.rfind("time_encoder.", 0) != 0 && m.rfind("time_decoder.", 0) != 0 &&
-        m.rfind("output_heads.", 0) != 0)
-      continue;
-    const int64_t n = f.info(name).count();
-    buf.resize((size_t)n);
-    f.read_f32(name, buf.data(), buf.size());
-    load(m, buf.data(), buf.size());
-    ++loaded;
+    if (separator_tensor(m)) by_ma[m] = name;
   }
-  return loaded;
+  auto need = [&](const std::string& a, const std::string& b = std::string()) {
+    if (by_ma.count(a) || (!b.empty() && by_ma.count(b))) return;
+    fail(MNN_ERR_TENSOR_NOT_FOUND, "separator: tensor '" + a + "' not found in the file");
+  };
+  for (size_t i = 0; i < enc_.size(); ++i) {
+    const std::string p = "time_encoder." + std::to_string(i) + ".";
+    need(p + "conv.weight");
+    need(p + "norm.weight");
+    need(p + "norm.bias");
+  }
+  for (size_t j = 0; j < dec_.size(); ++j) {
+    const std::string p = "time_decoder." + std::to_string(j) + ".";
+    need(p + "conv_transpose.weight", p + "conv_tr.weight");
+    need(p + "norm.weight");
+    need(p + "norm.bias");
+  }
+  std::vector<float> buf;
+  for (const auto& kv : by_ma) {
+    const int64_t n = f.info(kv.second).count();
+    buf.resize((size_t)n);
+    f.read_f32(kv.second, buf.data(), buf.size());
+    load(kv.first, buf.data(), buf.size());
+  }
+  return (int)by_ma.size();
 }
 
 void TimeSeparator::plan(int64_t Lp) {

@@ -13,11 +13,13 @@ class TimeSeparator {
  public:
   TimeSeparator(Device* d, const mnn_separator_desc& desc);
   // "time_encoder.{i}.*" (level i), "time_decoder.{j}.*" (j = 0 is the deepest level, as the
-  // reference's timeDecoders array), "output_heads.{s}.weight|bias".
+  // reference's timeDecoders array), "time_output_heads.{s}.weight|bias" (the reference's name,
+  // HTDemucs.swift:1021; "output_heads.{s}" is accepted as well).
   void load(const std::string& name, const float* data, size_t n);
   // HTDemucs.loadWeights(from:) for the time-domain model: every tensor of the file whose name,
   // mapped to the MetalAudio convention, addresses this model is read as fp32 and loaded; other
   // tensors (the frequency branch, the transformer) are skipped. Returns the number loaded.
+  // MNN_ERR_TENSOR_NOT_FOUND (nothing loaded) when a tensor the reference requires is absent.
   int load_safetensors(const SafeTensorsFile& f, WeightConvention conv);
   // x: interleaved [n * C]; out: [S, n * C] interleaved stems
   void separate(const Tensor& x, Tensor& out, Stream& s);

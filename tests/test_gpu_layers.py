@@ -274,6 +274,33 @@ def test_transformer_layer_bf16_parity(dev, stream):
     assert_rel_norm(got, ref, BF16_RTOL, "transformer layer bf16")
 
 
+def test_mha_bf16_projections_fp32_core(dev, stream):
+    """MultiHeadAttention with precision bf16: the Q/K/V and output projections take bf16
+    operands with fp32 accumulation and the attention core stays fp32 (the documented contract).
+    The oracle rounds exactly the projection operands (x, in_proj, the attention output, out_proj)
+    and keeps scores, softmax and P.V exact; a bf16 core (Q, K, P or V rounded) would move the
+    outputs by ~6e-3 of their scale with these peaked scores (measured on the CPU), six times the
+    1e-3 bound."""
+    from tests.conftest import assert_rel_norm
+    say("mha bf16: bf16 projections, fp32 core")
+    E, H, B, S = 384, 8, 2, 300
+    w_in = (RNG.standard_normal((3 * E, E)) * 0.1).astype(np.float32)
+    b_in = (RNG.standard_normal(3 * E) * 0.05).astype(np.float32)
+    w_out = (RNG.standard_normal((E, E)) * 0.05).astype(np.float32)
+    b_out = (RNG.standard_normal(E) * 0.05).astype(np.float32)
+    x = RNG.standard_normal((B, S, E)).astype(np.float32)
+    layer = nn.MultiHeadAttention(dev, E, H, precision="bf16")
+    layer.load_weights(w_in, b_in, w_out, b_out)
+    got = run_layer(layer, x, dev, stream)
+    r = oracle.round_bf16
+    o = oracle.mha(r(x), None, r(w_in), b_in, np.eye(E), None, H)  # attention output, exact core
+    ref = oracle.linear(r(o), r(w_out), b_out)
+    assert_rel_norm(got, ref, 1e-3, "mha bf16 vs rounded-projection oracle")
+    assert_rel_norm(got, oracle.mha(x, None, w_in, b_in, w_out, b_out, H), BF16_RTOL,
+                    "mha bf16 vs fp32 oracle")
+    assert np.abs(got - oracle.mha(x, None, w_in, b_in, w_out, b_out, H)).max() > 1e-5
+
+
 # ----------------------------------------------------------------------------- attention
 MHA_CASES = [
     # B, E, H, Sq, Sk, cross

@@ -138,3 +138,78 @@ def test_separator_weights_from_demucs_named_safetensors(dev, stream, tmp_path):
     out = sep.separate(nn.Tensor.from_numpy(dev, x), stream)
     stream.sync(60000)
     assert_close(out.to_numpy(), osep.separate_time(x, P, cfg), 1e-4, 1e-3, "separate")
+
+
+def _flat(P, head_prefix):
+    flat = {}
+    for k, v in P.items():
+        if k.startswith("output_heads."):
+            k = head_prefix + k[len("output_heads."):]
+        for kk, vv in v.items():
+            flat[f"{k}.{kk}"] = np.ascontiguousarray(vv)
+    return flat
+
+
+def test_separator_weights_with_reference_head_names(dev, stream, tmp_path):
+    """A MetalAudio-named file as HTDemucs.loadWeights reads it: output heads under
+    'time_output_heads.{i}' (HTDemucs.swift:1021). The heads must load (not stay zero), so the
+    stems match the oracle."""
+    from safetensors.numpy import save_file
+    cfg, P = model(levels=2)
+    say("separator weights, reference head names")
+    save_file(_flat(P, "time_output_heads."), str(tmp_path / "ma.safetensors"))
+    st = nn.SafeTensors(tmp_path / "ma.safetensors")
+    assert st.create_weight_mapper().convention == "metalaudio"
+    sep = nn.Separator(dev, 2, 4, cfg["channels"], 8, 4, 4)
+    assert sep.load_safetensors(st) == sum(len(v) for v in P.values())
+    x = RNG.uniform(-1, 1, 2 * 2000).astype(np.float32)
+    out = sep.separate(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    ref = osep.separate_time(x, P, cfg)
+    assert np.abs(ref).max() > 0.1
+    assert_close(out.to_numpy(), ref, 1e-4, 1e-3, "separate, reference head names")
+    # the same names through the per-tensor loader
+    sep2 = nn.Separator(dev, 2, 4, cfg["channels"], 8, 4, 4)
+    for name, v in _flat(P, "time_output_heads.").items():
+        sep2.load(name, v)
+    out2 = sep2.separate(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    assert_close(out2.to_numpy(), ref, 1e-4, 1e-3, "separate, per-tensor reference names")
+
+
+@pytest.mark.parametrize("drop", ["time_encoder.1.conv.weight", "time_encoder.0.norm.bias",
+                                  "time_decoder.0.conv_transpose.weight",
+                                  "time_decoder.1.norm.weight"])
+def test_separator_file_missing_required_tensor(dev, tmp_path, drop):
+    """HTDemucs.loadWeights throws tensorNotFound for every encoder / decoder conv and norm tensor
+    (HTDemucs.swift:892-937): a file without one is rejected and loads nothing."""
+    from safetensors.numpy import save_file
+    cfg, P = model(levels=2)
+    say(f"separator file without {drop}")
+    flat = _flat(P, "time_output_heads.")
+    del flat[drop]
+    save_file(flat, str(tmp_path / "m.safetensors"))
+    st = nn.SafeTensors(tmp_path / "m.safetensors")
+    sep = nn.Separator(dev, 2, 4, cfg["channels"], 8, 4, 4)
+    with pytest.raises(nn.MNNError) as e:
+        sep.load_safetensors(st)
+    assert e.value.name == "MNN_ERR_TENSOR_NOT_FOUND" and drop in str(e.value)
+
+
+def test_separator_file_without_optional_tensors(dev, stream, tmp_path):
+    """Conv biases and output heads are optional (loadConv1DWeights, SafeTensorsLoader.swift:
+    238-258; HTDemucs.swift:1017-1029): without them the biases stay zero and the file loads."""
+    from safetensors.numpy import save_file
+    cfg, P = model(levels=2)
+    say("separator file without conv biases")
+    flat = {k: v for k, v in _flat(P, "time_output_heads.").items()
+            if not (k.endswith("conv.bias") or k.endswith("conv_transpose.bias"))}
+    save_file(flat, str(tmp_path / "nb.safetensors"))
+    sep = nn.Separator(dev, 2, 4, cfg["channels"], 8, 4, 4)
+    assert sep.load_safetensors(nn.SafeTensors(tmp_path / "nb.safetensors")) == len(flat)
+    P0 = {k: {kk: (np.zeros_like(vv) if kk in ("conv.bias", "conv_transpose.bias") else vv)
+              for kk, vv in v.items()} for k, v in P.items()}
+    x = RNG.uniform(-1, 1, 2 * 1500).astype(np.float32)
+    out = sep.separate(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    assert_close(out.to_numpy(), osep.separate_time(x, P0, cfg), 1e-4, 1e-3, "zero conv biases")

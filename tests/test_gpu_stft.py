@@ -45,6 +45,7 @@ def spec_close(got, ref, what):
 @pytest.mark.parametrize("N,hop,kind,B,n", [
     (4, 1, "hann", 1, 37), (8, 2, "hamming", 2, 100), (64, 16, "hann", 1, 1000),
     (512, 128, "blackman", 3, 5000), (1024, 256, "none", 1, 4096), (4096, 1024, "hann", 2, 50000),
+    (8192, 2048, "hann", 1, 30000),  # largest size with the twiddle table staged in LDS
     (16384, 4096, "hann", 1, 40000),
 ])
 @pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins")])
@@ -82,7 +83,10 @@ def wsum_of(N, hop, kind, F):
 
 @pytest.mark.parametrize("N,hop,kind,B,F", [(8, 2, "hann", 1, 9), (64, 16, "hann", 2, 40),
                                             (512, 256, "hamming", 1, 30),
-                                            (4096, 1024, "hann", 2, 20)])
+                                            (4096, 1024, "hann", 2, 20),
+                                            # twiddles in LDS at its limit, then from global memory
+                                            (8192, 2048, "hann", 1, 9),
+                                            (16384, 4096, "hann", 1, 7)])
 @pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins")])
 def test_istft_parity(dev, stream, N, hop, kind, B, F, onesided, layout):
     say(f"istft N={N} hop={hop} {kind} B={B} F={F} onesided={onesided} layout={layout}")

@@ -101,7 +101,7 @@ def test_skips_malformed_entries_and_unknown_dtypes(tmp_path):
 
 @pytest.mark.parametrize("case,code", [
     ("missing", 13), ("short", 14), ("too_large", 14), ("truncated_header", 14), ("bad_json", 14),
-    ("not_utf8", 14), ("offset_oob", 14), ("ragged", 14), ("nan", 1), ("inf", 1),
+    ("not_utf8", 14), ("offset_oob", 14), ("reversed", 14), ("ragged", 14), ("nan", 1), ("inf", 1),
     ("not_found", 15), ("count", 2),
 ])
 def test_error_paths(tmp_path, case, code):
@@ -126,6 +126,10 @@ def test_error_paths(tmp_path, case, code):
         write_st(p, {"t": ("F32", (4,), ok.tobytes())},
                  header_override=json.dumps({"t": {"dtype": "F32", "shape": [4],
                                                    "data_offsets": [0, 64]}}).encode())
+    elif case == "reversed":  # end < begin: INVALID_FILE, not a huge allocation
+        write_st(p, {"t": ("F32", (4,), ok.tobytes())},
+                 header_override=json.dumps({"t": {"dtype": "F32", "shape": [4],
+                                                   "data_offsets": [16, 0]}}).encode())
     elif case == "ragged":
         write_st(p, {"t": ("F32", (1,), b"\x00\x00\x80")})
     elif case in ("nan", "inf"):
