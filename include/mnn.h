@@ -65,8 +65,9 @@ typedef enum mnn_dtype { MNN_F32 = 0, MNN_BF16 = 1 } mnn_dtype;
 typedef enum mnn_precision { MNN_PRECISION_F32 = 0, MNN_PRECISION_BF16 = 1 } mnn_precision;
 
 /* Fused activation codes. 0-4 are FusedConv1D's (Conv1D.swift:960-973); FusedLinear's sigmoid
- * and tanh (Linear.swift:630-639) get codes 5 and 6 here. Leaky ReLU uses alpha 0.01 (the
- * reference default, Conv1D.swift:786). GELU is the tanh approximation everywhere
+ * and tanh (Linear.swift:630-639) get codes 5 and 6 here. Leaky ReLU's slope is 0.01 (the
+ * reference default, Conv1D.swift:786, Linear.swift:495) unless the layer is created with
+ * mnn_fused_conv1d_create / mnn_fused_linear_create. GELU is the tanh approximation everywhere
  * (Activations.swift:124-137). */
 typedef enum mnn_activation {
   MNN_ACT_NONE = 0, MNN_ACT_RELU = 1, MNN_ACT_LEAKY_RELU = 2, MNN_ACT_GELU = 3, MNN_ACT_SWISH = 4,
@@ -152,6 +153,17 @@ typedef struct mnn_conv1d_desc {
 /* Conv1D / DynamicConv1D / FusedConv1D (Conv1D.swift:11-1028, DynamicConv1D.swift:35-403).
  * Weights: "weight" [out, in/groups, k], "bias" [out]. Input [C, L] or [B, C, L]. */
 mnn_status mnn_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc, mnn_layer* out);
+/* FusedConv1D.init(..., activation:, leakyReluAlpha:, ...) (Conv1D.swift:775-800): as
+ * mnn_conv1d_create with desc->activation fused and leaky_relu_alpha the negative slope of
+ * MNN_ACT_LEAKY_RELU (must be finite). */
+mnn_status mnn_fused_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc,
+                                   float leaky_relu_alpha, mnn_layer* out);
+/* FusedConv1D.forwardWithResidual(input:residual:output:encoder:) (Conv1D.swift:857-900) on any
+ * Conv1D layer: output = act(conv(input) + bias) + residual, the residual added AFTER the
+ * activation (Conv1D.swift:1016-1023). residual holds as many elements as the output (its
+ * shape); NULL gives the plain forward; it may be the output tensor itself. */
+mnn_status mnn_conv1d_forward_residual(mnn_layer layer, mnn_tensor input, mnn_tensor residual,
+                                       mnn_tensor output, mnn_stream s);
 
 /* GroupNorm (Normalization.swift:32-725); optional fused activation (used by the U-Net block).
  * Parameters "weight"/"gamma" [C], "bias"/"beta" [C]. Input [C, L] or [B, C, L]. */
@@ -172,6 +184,12 @@ mnn_status mnn_glu_create(mnn_device dev, int out_channels, mnn_layer* out);
  * y = act(x W^T + b). "weight" [out, in], "bias" [out]. Input [in], [N, in] or [B, N, in]. */
 mnn_status mnn_linear_create(mnn_device dev, int in_features, int out_features, int use_bias,
                              mnn_activation activation, mnn_precision precision, mnn_layer* out);
+/* FusedLinear.init(..., activation:, leakyReluAlpha:, ...) (Linear.swift:475-520): as
+ * mnn_linear_create with leaky_relu_alpha the negative slope of MNN_ACT_LEAKY_RELU. */
+mnn_status mnn_fused_linear_create(mnn_device dev, int in_features, int out_features,
+                                   int use_bias, mnn_activation activation,
+                                   float leaky_relu_alpha, mnn_precision precision,
+                                   mnn_layer* out);
 
 /* MultiHeadAttention / CrossAttention (Attention.swift:15-1063), PyTorch packing:
  * "in_proj_weight" [3E, E] rows Q;K;V, "in_proj_bias" [3E], "out_proj_weight" [E, E],
@@ -457,7 +475,10 @@ mnn_status mnn_layer_infer_output_shape(mnn_layer layer, int in_rank, const int6
                                         int* out_rank, int64_t* out_dims);
 
 /* ---------------------------------------------------------------- sequential
- * Sequential (Model.swift:65-357). The model references layers; it does not own them. */
+ * Sequential (Model.swift:65-357). The model references layers; it does not own them.
+ * A Conv1D without activation followed by GroupNorm(1 group) [and GELU] runs as one fused group
+ * (convolution with GroupNorm statistics in its epilogue, then one apply pass); the results are
+ * those of the layers run one by one. */
 mnn_status mnn_sequential_create(mnn_device dev, mnn_sequential* out);
 mnn_status mnn_sequential_destroy(mnn_sequential seq);
 mnn_status mnn_sequential_add(mnn_sequential seq, mnn_layer layer);          /* shape-checked */
@@ -469,19 +490,23 @@ mnn_status mnn_sequential_build(mnn_sequential seq);
  * overwritten by the next forward (Model.swift:263). */
 mnn_status mnn_sequential_forward(mnn_sequential seq, mnn_tensor input, mnn_stream s,
                                   mnn_tensor* output);
+/* Sequential.forwardAsync(_:completion:) (Model.swift:271-346): enqueues the forward on s and
+ * returns. completion(user, status, output) runs exactly once: on a library thread after the GPU
+ * work has finished (MNN_OK and the borrowed output, or MNN_ERR_GPU_EXECUTION and NULL), or,
+ * when the forward cannot be enqueued (empty model, not built, input shape, another forwardAsync
+ * of this model still in flight: MNN_ERR_INVALID_CONFIGURATION), on the calling thread before
+ * this returns the same status. As the reference, one forwardAsync per model at a time; the
+ * in-flight mark is cleared before the completion runs, so the completion may start the next
+ * one. The completion must not destroy the model (its destructor waits for completions). */
+typedef void (*mnn_completion_fn)(void* user, mnn_status status, mnn_tensor output);
+mnn_status mnn_sequential_forward_async(mnn_sequential seq, mnn_tensor input, mnn_stream s,
+                                        mnn_completion_fn completion, void* user);
 mnn_status mnn_sequential_buffer_stats(mnn_sequential seq, int* allocated, int* layers);
 mnn_status mnn_sequential_layer_count(mnn_sequential seq, int* count);
-
-/* ---------------------------------------------------------------- diagnostics
- * Runs one MFMA instruction on one wave with a zero accumulator and returns its raw lane
- * registers, to check the operand/result lane layouts the kernels assume.
- * variant 0: f32 32x32x2 (a, b: 64 floats, one per lane; d: 64 x 16)
- * variant 1: f32 16x16x4 (a, b: 64 floats; d: 64 x 4)
- * variant 2: bf16 32x32x16 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 16)
- * variant 3: bf16 16x16x32 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 4)
- * Layout of every array: [lane][register]. */
-mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, const float* b,
-                                float* d);
+/* layer(at:) (Model.swift:354-357): the index-th layer added, or *layer = NULL (status MNN_OK)
+ * when index is out of range, as the reference returns nil. The handle is the one passed to
+ * mnn_sequential_add. */
+mnn_status mnn_sequential_layer_at(mnn_sequential seq, int index, mnn_layer* layer);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,28 @@
+/*
+ * mnn_debug.h — diagnostic entry points of libmnn.so, kept out of the product header mnn.h.
+ * They have no counterpart in the reference; the library's tests use them to check the
+ * hardware assumptions its kernels are written against.
+ */
+#ifndef MNN_DEBUG_H
+#define MNN_DEBUG_H
+
+#include "mnn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Runs one MFMA instruction on one wave with a zero accumulator and returns its raw lane
+ * registers, to check the operand/result lane layouts the kernels assume.
+ * variant 0: f32 32x32x2 (a, b: 64 floats, one per lane; d: 64 x 16)
+ * variant 1: f32 16x16x4 (a, b: 64 floats; d: 64 x 4)
+ * variant 2: bf16 32x32x16 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 16)
+ * variant 3: bf16 16x16x32 (a, b: 64 x 8 floats, rounded to bf16; d: 64 x 4)
+ * Layout of every array: [lane][register]. */
+mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, const float* b,
+                                float* d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MNN_DEBUG_H */

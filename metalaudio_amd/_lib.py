@@ -107,6 +107,8 @@ PP = C.POINTER(C.c_void_p)
 I64P = C.POINTER(C.c_int64)
 IP = C.POINTER(C.c_int)
 FP = C.POINTER(C.c_float)
+# void (*mnn_completion_fn)(void* user, mnn_status status, mnn_tensor output)
+COMPLETION_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int, C.c_void_p)
 
 # name -> (restype, argtypes); every function that returns mnn_status uses C.c_int
 SIGNATURES = {
@@ -134,11 +136,15 @@ SIGNATURES = {
     "mnn_tensor_copy": (C.c_int, [P, P, P]),
     "mnn_tensor_device_ptr": (C.c_int, [P, PP]),
     "mnn_conv1d_create": (C.c_int, [P, C.POINTER(Conv1dDesc), PP]),
+    "mnn_fused_conv1d_create": (C.c_int, [P, C.POINTER(Conv1dDesc), C.c_float, PP]),
+    "mnn_conv1d_forward_residual": (C.c_int, [P, P, P, P, P]),
     "mnn_groupnorm_create": (C.c_int, [P, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, PP]),
     "mnn_layernorm_create": (C.c_int, [P, C.c_int, C.c_float, PP]),
     "mnn_gelu_create": (C.c_int, [P, C.c_int, I64P, PP]),
     "mnn_glu_create": (C.c_int, [P, C.c_int, PP]),
     "mnn_linear_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
+    "mnn_fused_linear_create": (
+        C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
     "mnn_mha_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_feedforward_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_encoder_block_create": (C.c_int, [P, C.POINTER(EncoderBlockDesc), PP]),
@@ -208,8 +214,10 @@ SIGNATURES = {
     "mnn_sequential_add_unchecked": (C.c_int, [P, P]),
     "mnn_sequential_build": (C.c_int, [P]),
     "mnn_sequential_forward": (C.c_int, [P, P, P, PP]),
+    "mnn_sequential_forward_async": (C.c_int, [P, P, P, COMPLETION_FN, P]),
     "mnn_sequential_buffer_stats": (C.c_int, [P, IP, IP]),
     "mnn_sequential_layer_count": (C.c_int, [P, IP]),
+    "mnn_sequential_layer_at": (C.c_int, [P, C.c_int, PP]),
     "mnn_debug_mfma_probe": (C.c_int, [P, C.c_int, FP, FP, FP]),
 }
 

@@ -5,6 +5,7 @@
 #include <thread>
 
 #include "layers.hpp"
+#include "mnn_debug.h"
 #include "safetensors.hpp"
 #include "stft.hpp"
 #include "separate.hpp"
@@ -396,6 +397,26 @@ mnn_status mnn_tensor_device_ptr(mnn_tensor t, void** ptr) {
 mnn_status mnn_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc, mnn_layer* out) {
   MNN_CREATE(make_conv1d(d, need(desc)));
 }
+mnn_status mnn_fused_conv1d_create(mnn_device dev, const mnn_conv1d_desc* desc,
+                                   float leaky_relu_alpha, mnn_layer* out) {
+  MNN_CREATE(make_conv1d(d, need(desc), leaky_relu_alpha));
+}
+mnn_status mnn_conv1d_forward_residual(mnn_layer layer, mnn_tensor input, mnn_tensor residual,
+                                       mnn_tensor output, mnn_stream st) {
+  return guard([&] {
+    Layer* l = L(layer);
+    Tensor* in = T(input);
+    Tensor* out = T(output);
+    Tensor* res = residual ? T(residual) : nullptr;
+    MNN_REQUIRE(in->dev == l->device() && out->dev == l->device() &&
+                    (!res || res->dev == l->device()),
+                MNN_ERR_INVALID_ARGUMENT, "tensors must live on the layer's device");
+    in->dev->check_alive();
+    Stream s = resolve_stream(in->dev, st);
+    in->dev->make_current();
+    conv1d_forward_residual(l, *in, res, *out, s);
+  });
+}
 mnn_status mnn_groupnorm_create(mnn_device dev, int num_groups, int num_channels, float epsilon,
                                 int affine, mnn_activation act, mnn_layer* out) {
   MNN_CREATE(make_groupnorm(d, num_groups, num_channels, epsilon, affine != 0, act));
@@ -412,6 +433,12 @@ mnn_status mnn_glu_create(mnn_device dev, int out_channels, mnn_layer* out) {
 mnn_status mnn_linear_create(mnn_device dev, int in_features, int out_features, int use_bias,
                              mnn_activation act, mnn_precision prec, mnn_layer* out) {
   MNN_CREATE(make_linear(d, in_features, out_features, use_bias != 0, act, prec));
+}
+mnn_status mnn_fused_linear_create(mnn_device dev, int in_features, int out_features,
+                                   int use_bias, mnn_activation act, float leaky_relu_alpha,
+                                   mnn_precision prec, mnn_layer* out) {
+  MNN_CREATE(make_linear(d, in_features, out_features, use_bias != 0, act, prec,
+                         leaky_relu_alpha));
 }
 mnn_status mnn_mha_create(mnn_device dev, int embed_dim, int num_heads, int use_bias,
                           mnn_precision prec, mnn_layer* out) {
@@ -1021,6 +1048,34 @@ mnn_status mnn_sequential_forward(mnn_sequential seq, mnn_tensor input, mnn_stre
     Stream s = resolve_stream(in->dev, st);
     in->dev->make_current();
     *output = reinterpret_cast<mnn_tensor>(q->forward(*in, s));
+  });
+}
+
+mnn_status mnn_sequential_forward_async(mnn_sequential seq, mnn_tensor input, mnn_stream st,
+                                        mnn_completion_fn completion, void* user) {
+  if (!completion) {
+    g_last_error = "null completion";
+    return MNN_ERR_INVALID_ARGUMENT;
+  }
+  const mnn_status status = guard([&] {
+    Sequential* q = Q(seq);
+    Tensor* in = T(input);
+    in->dev->check_alive();
+    Stream s = resolve_stream(in->dev, st);
+    in->dev->make_current();
+    q->forward_async(*in, s, [completion, user](mnn_status status, Tensor* out) {
+      completion(user, status, reinterpret_cast<mnn_tensor>(out));
+    });
+  });
+  // not enqueued: the completion still runs exactly once, here, with the failure
+  if (status != MNN_OK) completion(user, status, nullptr);
+  return status;
+}
+
+mnn_status mnn_sequential_layer_at(mnn_sequential seq, int index, mnn_layer* layer) {
+  return guard([&] {
+    MNN_REQUIRE(layer, MNN_ERR_INVALID_ARGUMENT, "null output");
+    *layer = reinterpret_cast<mnn_layer>(Q(seq)->layer_at(index));
   });
 }
 

@@ -46,10 +46,12 @@ __device__ __forceinline__ float gelu_clamped(float x) {
   return x > 10.f ? x : (x < -10.f ? 0.f : gelu_tanh(x));
 }
 
-__device__ __forceinline__ float apply_act(float x, int act) {
+// Fused activation codes of mnn_activation; `alpha` is leaky ReLU's negative slope
+// (FusedConv1D / FusedLinear leakyReluAlpha, default 0.01: Conv1D.swift:786, Linear.swift:495).
+__device__ __forceinline__ float apply_act(float x, int act, float alpha = 0.01f) {
   switch (act) {
     case 1: return fmaxf(x, 0.f);
-    case 2: return x >= 0.f ? x : 0.01f * x;
+    case 2: return x >= 0.f ? x : alpha * x;
     case 3: return gelu_tanh(x);
     case 4: return x * stable_sigmoid(x);
     case 5: return stable_sigmoid(x);

@@ -67,7 +67,9 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
     if (valid && co < p.Cout) {
       float v = acc[j] + (bias ? bias[co] : 0.f);
       if (partials) st.add(v);
-      if (y) y[((int64_t)b * p.Cout + co) * p.ldy + t] = apply_act(v, act);
+      v = apply_act(v, act, p.alpha);
+      if (p.res) v += p.res[((int64_t)b * p.Cout + co) * p.ldr + t];
+      if (y) y[((int64_t)b * p.Cout + co) * p.ldy + t] = v;
     }
   }
   if (partials) {
@@ -147,7 +149,9 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams 
 #pragma unroll
       for (int j = 0; j < COB; ++j) {
         if (partials) st.add(acc[j]);
-        if (y) y[((int64_t)b * p.Cout + co0 + j) * p.ldy + t] = apply_act(acc[j], act);
+        float v = apply_act(acc[j], act, p.alpha);
+        if (p.res) v += p.res[((int64_t)b * p.Cout + co0 + j) * p.ldr + t];
+        if (y) y[((int64_t)b * p.Cout + co0 + j) * p.ldy + t] = v;
       }
     }
   }
@@ -189,6 +193,7 @@ void conv1d_direct(const LaunchCtx& c, const ConvParams& p0, const float* x, con
                    const float* bias, float* y, int act, float* partials, int* nchunk) {
   ConvParams p = p0;
   if (p.ldy == 0) p.ldy = p.Lout;
+  if (p.ldr == 0) p.ldr = p.ldy;
   if (const int ck = reg_ck(p)) {
     dim3 grid(cdiv(p.Lout, kThreads), p.Cout / 16, p.B);
     if (nchunk) *nchunk = (int)(grid.x * grid.y);

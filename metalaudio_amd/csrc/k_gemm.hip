@@ -486,7 +486,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64, 2) void gemm_f32_mfma_kernel
             if (a.bias_mode == BIAS_N) val += a.bias[gn];
             else if (a.bias_mode == BIAS_M) val += a.bias[gm];
             if (a.stats) st.add(val);
-            val = apply_act(val, a.act);
+            val = apply_act(val, a.act, a.act_alpha);
             if (Rp) {
               const float rs = a.rscale ? a.rscale[gn] : 1.f;
               val = Rp[(int64_t)gm * a.ldr + gn] + rs * val;
@@ -546,7 +546,7 @@ __global__ __launch_bounds__(256) void gemm_f32_simple_kernel(GemmArgs a) {
       sn = 1.f;
       smean = acc;
     }
-    acc = apply_act(acc, a.act);
+    acc = apply_act(acc, a.act, a.act_alpha);
     if (a.R) {
       const float rs = a.rscale ? a.rscale[gn] : 1.f;
       acc = a.R[(int64_t)bz * a.sR + (int64_t)gm * a.ldr + gn] + rs * acc;

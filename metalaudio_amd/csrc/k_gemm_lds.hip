@@ -126,7 +126,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
         const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
         if (full_m || gm < a.M) {
           float val = acc[i][j][v] + bnv[j] + bmv[v];
-          val = ACT < 0 ? apply_act(val, a.act) : apply_act(val, ACT);
+          val = ACT < 0 ? apply_act(val, a.act, a.act_alpha) : apply_act(val, ACT);
           if constexpr (RES) val = rv[FAST ? i : 0][j][v] + rsv[j] * val;
           Cp[(int64_t)gm * a.ldc + gn] = val;
         }

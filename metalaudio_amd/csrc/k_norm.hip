@@ -153,6 +153,120 @@ __global__ __launch_bounds__(kThreads) void gn_apply_kernel(const float* __restr
   }
 }
 
+// Chan's merge of two fp64 statistics (count, mean, M2): a then b, in that order.
+__device__ __forceinline__ void chan_merge_d(double& n, double& mean, double& m2, double n2,
+                                             double mean2, double m22) {
+  const double nt = n + n2;
+  if (nt > 0.0) {
+    const double d = mean2 - mean;
+    const double w = n2 / nt;
+    mean += d * w;
+    m2 += m22 + d * d * n * w;
+  }
+  n = nt;
+}
+
+// Every lane of the calling wave receives the merge of np (count, mean, M2) partials: lane l
+// merges partials l, l + 64, ... in order, then a butterfly combines lane pairs lower lane first,
+// so both lanes of a pair compute the same value and all lanes end with the identical total
+// (deterministic, the same in every wave and workgroup).
+__device__ __forceinline__ void wave_merge_parts(const float* __restrict__ p, int np, double& n,
+                                                 double& mean, double& m2) {
+  const int lane = threadIdx.x & 63;
+  n = 0.0;
+  mean = 0.0;
+  m2 = 0.0;
+  for (int j = lane; j < np; j += 64)
+    chan_merge_d(n, mean, m2, p[3 * j], p[3 * j + 1], p[3 * j + 2]);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const double on = __shfl_xor(n, off, 64), om = __shfl_xor(mean, off, 64),
+                 oq = __shfl_xor(m2, off, 64);
+    if (lane & off) {  // this lane holds the upper half: merge(other, self)
+      double a = on, b = om, c = oq;
+      chan_merge_d(a, b, c, n, mean, m2);
+      n = a;
+      mean = b;
+      m2 = c;
+    } else {
+      chan_merge_d(n, mean, m2, on, om, oq);
+    }
+  }
+}
+
+// GroupNorm apply with the statistics merged in the workgroup: x, y [B][C][L]; group (b, g) covers
+// the contiguous cpg * L elements of channels [g * cpg, (g + 1) * cpg); its nparts partials sit
+// at parts[((b * G + g) * nparts + j) * 3]. y = act((x - mean) * rstd * gamma_c + beta_c), biased
+// variance, rsqrt(var + eps) as gn_finalize. Each workgroup handles kApplyItems float4 (vec) or
+// floats of one group; its loads are issued before the merge so the two overlap.
+constexpr int kApplyPer = 4;  // items per thread
+__global__ __launch_bounds__(kThreads) void gn_apply_parts_kernel(
+    const float* __restrict__ x, float* __restrict__ y, int C, int64_t L, int G,
+    const float* __restrict__ parts, int nparts, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, int act, int vec) {
+  const int bg = blockIdx.y;
+  const int cpg = C / G;
+  const int64_t total = (int64_t)cpg * L;
+  const int64_t gbase = (int64_t)bg * total;  // (b * G + g) * cpg * L
+  const int c0 = (bg % G) * cpg;
+  const int64_t i0 = ((int64_t)blockIdx.x * kApplyPer) * kThreads + threadIdx.x;
+  if (vec) {
+    const int64_t total4 = total >> 2, L4 = L >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x + gbase);
+    float4* y4 = reinterpret_cast<float4*>(y + gbase);
+    float4 v[kApplyPer];
+#pragma unroll
+    for (int k = 0; k < kApplyPer; ++k) {
+      const int64_t i = i0 + (int64_t)k * kThreads;
+      v[k] = i < total4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    double n, mean, m2;
+    wave_merge_parts(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
+    const double var = n > 0.0 ? m2 / n : 0.0;
+    float rstd = (float)(1.0 / sqrt(var + (double)eps));
+    if (!isfinite(rstd)) rstd = 0.f;
+    const float mf = (float)mean;
+#pragma unroll
+    for (int k = 0; k < kApplyPer; ++k) {
+      const int64_t i = i0 + (int64_t)k * kThreads;
+      if (i < total4) {
+        const int ch = c0 + (int)(i / L4);
+        const float sc = (gamma ? gamma[ch] : 1.f) * rstd;
+        const float sh = (beta ? beta[ch] : 0.f) - mf * sc;
+        float4 o;
+        o.x = apply_act(fmaf(v[k].x, sc, sh), act);
+        o.y = apply_act(fmaf(v[k].y, sc, sh), act);
+        o.z = apply_act(fmaf(v[k].z, sc, sh), act);
+        o.w = apply_act(fmaf(v[k].w, sc, sh), act);
+        y4[i] = o;
+      }
+    }
+  } else {
+    float v[kApplyPer];
+#pragma unroll
+    for (int k = 0; k < kApplyPer; ++k) {
+      const int64_t i = i0 + (int64_t)k * kThreads;
+      v[k] = i < total ? x[gbase + i] : 0.f;
+    }
+    double n, mean, m2;
+    wave_merge_parts(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
+    const double var = n > 0.0 ? m2 / n : 0.0;
+    float rstd = (float)(1.0 / sqrt(var + (double)eps));
+    if (!isfinite(rstd)) rstd = 0.f;
+    const float mf = (float)mean;
+#pragma unroll
+    for (int k = 0; k < kApplyPer; ++k) {
+      const int64_t i = i0 + (int64_t)k * kThreads;
+      if (i < total) {
+        const int ch = c0 + (int)(i / L);
+        const float sc = (gamma ? gamma[ch] : 1.f) * rstd;
+        const float sh = (beta ? beta[ch] : 0.f) - mf * sc;
+        y[gbase + i] = apply_act(fmaf(v[k], sc, sh), act);
+      }
+    }
+  }
+}
+
 // LayerNorm, row in registers: NV float4 per lane, F % 4 == 0, F <= 256 * NV.
 template <int NV>
 __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __restrict__ x,
@@ -263,6 +377,18 @@ void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_
   unsigned gx = (unsigned)std::min<int64_t>((items + kThreads - 1) / kThreads, 4096);
   launch(c, "gn_apply", gn_apply_kernel, dim3(gx, (unsigned)(B * C)), dim3(kThreads), 0, x, y, L,
          coef, act, vec);
+}
+
+void gn_apply_parts(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L, int G,
+                    const float* parts, int nparts, const float* gamma, const float* beta,
+                    float eps, int act) {
+  const int vec = (L % 4 == 0) && aligned16(x) && aligned16(y);
+  const int64_t total = (int64_t)(C / G) * L;
+  const int64_t items = vec ? total / 4 : total;
+  const int64_t per_wg = (int64_t)kApplyPer * kThreads;
+  const unsigned gx = (unsigned)std::max<int64_t>(1, (items + per_wg - 1) / per_wg);
+  launch(c, "gn_apply_parts", gn_apply_parts_kernel, dim3(gx, (unsigned)(B * G)), dim3(kThreads),
+         0, x, y, C, L, G, parts, nparts, gamma, beta, eps, act, vec);
 }
 
 void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,

@@ -31,6 +31,12 @@ void gn_finalize(const LaunchCtx& c, const float* partials, int B, int C, int G,
 // Step 3: y = act(x*scale + shift), per (b, channel) coefficients.
 void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L,
               const float* coef, int act);
+// Steps 2 + 3 in one launch: every workgroup merges the nparts partials of its (b, g) (fp64, a
+// fixed order, the same total in every workgroup) and applies y = act(GroupNorm(x)); partials at
+// parts[((b*G + g)*nparts + j)*3] (gn_stats_partial's layout, or a producer's for G = 1).
+void gn_apply_parts(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L, int G,
+                    const float* parts, int nparts, const float* gamma, const float* beta,
+                    float eps, int act);
 // LayerNorm over rows of F features (two-pass statistics, biased variance, rsqrt).
 void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
                const float* gamma, const float* beta, float eps);
@@ -40,6 +46,11 @@ struct ConvParams {
   int B, Cin, Cout, Lin, Lout, K, stride, pad, dilation, groups;
   bool reflect;  // reflect padding (DynamicConv1D.swift:288-324) instead of zeros
   int64_t ldy = 0;  // output row pitch (0 = Lout)
+  float alpha = 0.01f;  // leaky ReLU slope of the fused activation
+  // FusedConv1D residual (Conv1D.swift:1016-1023): y = act(conv + bias) + res, res [B][Cout][ldr]
+  // (ldr 0 = ldy); res may alias y.
+  const float* res = nullptr;
+  int64_t ldr = 0;
 };
 // Direct convolution, one thread per output position and a block of output channels.
 // act: fused activation. If `partials` is set (groups of GroupNorm = 1), each workgroup also
@@ -94,6 +105,7 @@ struct GemmArgs {
   const float* bias = nullptr;
   int bias_mode = BIAS_NONE;
   int act = 0;
+  float act_alpha = 0.01f;  // leaky ReLU slope (act 2)
   // GLU epilogue: rows are stored in 32-row blocks [a0..a15, b0..b15]; output row
   // 16*blk + r = a * sigmoid(b).
   bool glu = false;

@@ -94,7 +94,10 @@ void Layer::check_out(const Tensor& out, const Shape& expect) const {
 // implicit GEMM on the matrix cores; small ones on the direct kernel.
 class Conv1DLayer : public Layer {
  public:
-  Conv1DLayer(Device* d, const mnn_conv1d_desc& desc) : Layer(d), p_(desc) {
+  Conv1DLayer(Device* d, const mnn_conv1d_desc& desc, float leaky_alpha = 0.01f)
+      : Layer(d), p_(desc), alpha_(leaky_alpha) {
+    MNN_REQUIRE(std::isfinite(leaky_alpha), MNN_ERR_INVALID_CONFIGURATION,
+                "FusedConv1D: leakyReluAlpha must be finite");
     MNN_REQUIRE(p_.in_channels > 0 && p_.out_channels > 0 && p_.kernel_size > 0 &&
                     p_.stride > 0 && p_.dilation > 0 && p_.groups > 0,
                 MNN_ERR_INVALID_CONFIGURATION, "Conv1D: sizes must be positive");
@@ -150,11 +153,23 @@ class Conv1DLayer : public Layer {
     return o;
   }
   void forward(const Tensor& in, Tensor& out, Stream& s) override {
+    forward_residual(in, nullptr, out, s);
+  }
+  // FusedConv1D.forwardWithResidual (Conv1D.swift:857-900): out = act(conv + bias) + residual,
+  // the residual added after the activation (:1016-1023). residual may be null or alias out.
+  void forward_residual(const Tensor& in, const Tensor* res, Tensor& out, Stream& s) {
     const Shape os = infer_output(in.shape);
     check_out(out, os);
+    if (res) {
+      MNN_REQUIRE(res->count() == numel(os) && res->dtype == MNN_F32,
+                  MNN_ERR_BUFFER_SIZE_MISMATCH,
+                  kind() << ": residual holds " << res->count() << " elements, expected "
+                         << shape_str(os));
+    }
     int64_t B, C, L;
     split_bcl(in.shape, B, C, L);
-    run(in.f32(), (int)B, (int)L, out.f32(), p_.activation, nullptr, s);
+    run(in.f32(), (int)B, (int)L, out.f32(), p_.activation, nullptr, s, 0,
+        res ? res->f32() : nullptr);
   }
   bool uses_mfma() const {
     const int ck = p_.in_channels * p_.kernel_size;
@@ -173,7 +188,7 @@ class Conv1DLayer : public Layer {
     return false;
   }
   k::GemmArgs gemm_args(const float* x, int B, int L, float* y, int act, float* stats,
-                        int64_t ldy = 0) const {
+                        int64_t ldy = 0, const float* res = nullptr) const {
     const int lo = (int)out_len(L);
     if (ldy == 0) ldy = lo;
     k::GemmArgs g;
@@ -199,14 +214,23 @@ class Conv1DLayer : public Layer {
     g.bias = b_ ? b_->ptr() : nullptr;
     g.bias_mode = b_ ? k::BIAS_M : k::BIAS_NONE;
     g.act = act;
+    g.act_alpha = alpha_;
     g.stats = stats;
+    if (res) {
+      g.R = res;
+      g.ldr = ldy;
+      g.sR = g.sC;
+    }
     g.precision = p_.precision;
     return g;
   }
-  k::ConvParams direct_params(int B, int L, int64_t ldy = 0) const {
-    return k::ConvParams{B, p_.in_channels, p_.out_channels, L, (int)out_len(L), p_.kernel_size,
-                         p_.stride, pad_for(L), p_.dilation, p_.groups,
-                         p_.padding_mode == MNN_PAD_REFLECT, ldy};
+  k::ConvParams direct_params(int B, int L, int64_t ldy = 0, const float* res = nullptr) const {
+    k::ConvParams c{B, p_.in_channels, p_.out_channels, L, (int)out_len(L), p_.kernel_size,
+                    p_.stride, pad_for(L), p_.dilation, p_.groups,
+                    p_.padding_mode == MNN_PAD_REFLECT, ldy};
+    c.alpha = alpha_;
+    c.res = res;
+    return c;
   }
   // Number of GroupNorm(1) statistics partials per batch that run() writes for this input.
   int stats_chunks(int B, int L) const {
@@ -215,21 +239,22 @@ class Conv1DLayer : public Layer {
   }
   // Runs the convolution; `stats` (GroupNorm(1) partials of the pre-activation output) is
   // optional and must hold 3 * B * stats_chunks(B, L) floats. Output rows are `ldy` apart
-  // (0 = contiguous).
+  // (0 = contiguous); `res` (same layout as y) is added after the activation.
   // y may be null on the direct path (statistics only).
   void run(const float* x, int B, int L, float* y, int act, float* stats, Stream& s,
-           int64_t ldy = 0) {
+           int64_t ldy = 0, const float* res = nullptr) {
     if (uses_mfma()) {
-      k::gemm(ctx(s), gemm_args(x, B, L, y, act, stats, ldy));
+      k::gemm(ctx(s), gemm_args(x, B, L, y, act, stats, ldy, res));
       return;
     }
-    k::conv1d_direct(ctx(s), direct_params(B, L, ldy), x, w_->ptr(), b_ ? b_->ptr() : nullptr,
-                     y, act, stats, nullptr);
+    k::conv1d_direct(ctx(s), direct_params(B, L, ldy, res), x, w_->ptr(),
+                     b_ ? b_->ptr() : nullptr, y, act, stats, nullptr);
   }
   const mnn_conv1d_desc& desc() const { return p_; }
 
  private:
   mnn_conv1d_desc p_;
+  float alpha_ = 0.01f;
   Param* w_ = nullptr;
   Param* b_ = nullptr;
 };
@@ -261,16 +286,25 @@ class GroupNormLayer : public Layer {
                 "GroupNorm: expected " << C_ << " channels, got " << C);
     return in;
   }
+  // Two launches: per-chunk statistics partials, then the apply step whose workgroups merge
+  // their group's partials themselves (no separate finalize pass).
   void forward(const Tensor& in, Tensor& out, Stream& s) override {
     check_out(out, infer_output(in.shape));
     int64_t B, C, L;
     split_bcl(in.shape, B, C, L);
     const int nchunk = k::gn_num_chunks(C_, G_, L);
     partials_.reserve(sizeof(float) * 3 * B * G_ * nchunk);
-    coef_.reserve(sizeof(float) * 2 * B * C_);
     k::gn_stats_partial(ctx(s), in.f32(), (int)B, C_, L, G_, partials_.f32(), nchunk);
-    finalize(s, (int)B, nchunk, partials_.f32());
-    k::gn_apply(ctx(s), in.f32(), out.f32(), (int)B, C_, L, coef_.f32(), act_);
+    apply_parts(s, in.f32(), out.f32(), (int)B, L, partials_.f32(), nchunk, act_);
+  }
+  // y = act(GroupNorm(x)) from statistics partials (nparts per (b, g)).
+  void apply_parts(Stream& s, const float* x, float* y, int B, int64_t L, const float* parts,
+                   int nparts, int act) const {
+    k::gn_apply_parts(ctx(s), x, y, B, C_, L, G_, parts, nparts, gamma(), beta(), eps_, act);
+  }
+  float* reserve_partials(int64_t floats) {
+    partials_.reserve(sizeof(float) * std::max<int64_t>(floats, 1));
+    return partials_.f32();
   }
   // Turns partials into per-(b, c) coefficients held in coef().
   void finalize(Stream& s, int B, int nchunk, const float* partials) {
@@ -385,9 +419,12 @@ class GLULayer : public Layer {
 // y = act(x W^T + b), W [out, in].
 class LinearLayer : public Layer {
  public:
-  LinearLayer(Device* d, int in, int out, bool bias, int act, mnn_precision prec)
-      : Layer(d), in_(in), out_(out), act_(act), prec_(prec) {
+  LinearLayer(Device* d, int in, int out, bool bias, int act, mnn_precision prec,
+              float leaky_alpha = 0.01f)
+      : Layer(d), in_(in), out_(out), act_(act), prec_(prec), alpha_(leaky_alpha) {
     MNN_REQUIRE(in > 0 && out > 0, MNN_ERR_INVALID_CONFIGURATION, "Linear: sizes must be > 0");
+    MNN_REQUIRE(std::isfinite(leaky_alpha), MNN_ERR_INVALID_CONFIGURATION,
+                "FusedLinear: leakyReluAlpha must be finite");
     w_ = &add_param("weight", (int64_t)in * out);
     if (bias) b_ = &add_param("bias", out);
   }
@@ -420,6 +457,7 @@ class LinearLayer : public Layer {
     g.bias = b_ ? b_->ptr() : nullptr;
     g.bias_mode = b_ ? k::BIAS_N : k::BIAS_NONE;
     g.act = act;
+    g.act_alpha = alpha_;
     g.R = R;
     g.ldr = out_;
     g.rscale = rscale;
@@ -432,6 +470,7 @@ class LinearLayer : public Layer {
  private:
   int in_, out_, act_;
   mnn_precision prec_;
+  float alpha_ = 0.01f;
   Param* w_ = nullptr;
   Param* b_ = nullptr;
 };
@@ -1798,9 +1837,48 @@ class CrossTransformerImpl : public Layer {
   size_t next_event_ = 0;
 };
 
+// ------------------------------------------------------------------ Sequential fusion
+// Conv1D (no activation, no residual) -> GroupNorm(1 group) [-> GELU] inside a Sequential runs
+// as two launches: the convolution writes its output and GroupNorm statistics partials from its
+// epilogue, then one apply pass merges the partials and writes act(GroupNorm(y)) into the last
+// layer's buffer. Results are those of the layers run one by one (GELU's +-10 clamp and the
+// tanh form agree to float precision beyond |x| = 10).
+int fused_chain_length(const std::vector<Layer*>& v, size_t i) {
+  if (i + 1 >= v.size()) return 1;
+  auto* c = dynamic_cast<Conv1DLayer*>(v[i]);
+  auto* g = dynamic_cast<GroupNormLayer*>(v[i + 1]);
+  if (!c || !g || c->desc().activation != MNN_ACT_NONE || g->groups() != 1) return 1;
+  if (i + 2 < v.size() && g->act() == MNN_ACT_NONE && dynamic_cast<GELULayer*>(v[i + 2]))
+    return 3;
+  return 2;
+}
+
+void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor& in,
+                     Tensor& y, Tensor& out, Stream& s) {
+  auto* c = static_cast<Conv1DLayer*>(v[i]);
+  auto* g = static_cast<GroupNormLayer*>(v[i + 1]);
+  const Shape ys = c->infer_output(in.shape);
+  MNN_REQUIRE(y.count() == numel(ys) && out.count() == numel(ys), MNN_ERR_BUFFER_SIZE_MISMATCH,
+              "fused Conv1D -> GroupNorm: buffers do not hold " << shape_str(ys));
+  int64_t B, C, L;
+  split_bcl(in.shape, B, C, L);
+  const int nparts = c->stats_chunks((int)B, (int)L);
+  float* parts = g->reserve_partials(3LL * B * nparts);
+  c->run(in.f32(), (int)B, (int)L, y.f32(), MNN_ACT_NONE, parts, s);
+  g->apply_parts(s, y.f32(), out.f32(), (int)B, ys.back(), parts, nparts,
+                 n == 3 ? MNN_ACT_GELU : g->act());
+}
+
 // ------------------------------------------------------------------ factories
-std::unique_ptr<Layer> make_conv1d(Device* d, const mnn_conv1d_desc& desc) {
-  return std::make_unique<Conv1DLayer>(d, desc);
+std::unique_ptr<Layer> make_conv1d(Device* d, const mnn_conv1d_desc& desc, float leaky_alpha) {
+  return std::make_unique<Conv1DLayer>(d, desc, leaky_alpha);
+}
+void conv1d_forward_residual(Layer* l, const Tensor& in, const Tensor* res, Tensor& out,
+                             Stream& s) {
+  auto* c = dynamic_cast<Conv1DLayer*>(l);
+  MNN_REQUIRE(c, MNN_ERR_INVALID_ARGUMENT,
+              "forwardWithResidual needs a Conv1D layer, got " << l->kind());
+  c->forward_residual(in, res, out, s);
 }
 std::unique_ptr<Layer> make_groupnorm(Device* d, int groups, int channels, float eps, bool affine,
                                       int act) {
@@ -1816,8 +1894,8 @@ std::unique_ptr<Layer> make_glu(Device* d, int out_channels) {
   return std::make_unique<GLULayer>(d, out_channels);
 }
 std::unique_ptr<Layer> make_linear(Device* d, int in, int out, bool bias, int act,
-                                   mnn_precision prec) {
-  return std::make_unique<LinearLayer>(d, in, out, bias, act, prec);
+                                   mnn_precision prec, float leaky_alpha) {
+  return std::make_unique<LinearLayer>(d, in, out, bias, act, prec, leaky_alpha);
 }
 std::unique_ptr<Layer> make_mha(Device* d, int embed, int heads, bool bias, mnn_precision prec) {
   return std::make_unique<MHALayer>(d, embed, heads, bias, prec);

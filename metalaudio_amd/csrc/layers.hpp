@@ -2,6 +2,7 @@
 // hot-path layers of Sources/MetalNN, and Sequential (Model.swift:65-357).
 #pragma once
 
+#include <condition_variable>
 #include <functional>
 
 #include "common.hpp"
@@ -46,14 +47,18 @@ class Layer {
 };
 
 // Layer factories (definitions in layers.cpp).
-std::unique_ptr<Layer> make_conv1d(Device* d, const mnn_conv1d_desc& desc);
+std::unique_ptr<Layer> make_conv1d(Device* d, const mnn_conv1d_desc& desc,
+                                   float leaky_alpha = 0.01f);
+// FusedConv1D.forwardWithResidual on a Conv1D layer (res may be null).
+void conv1d_forward_residual(Layer* l, const Tensor& in, const Tensor* res, Tensor& out,
+                             Stream& s);
 std::unique_ptr<Layer> make_groupnorm(Device* d, int groups, int channels, float eps, bool affine,
                                       int act);
 std::unique_ptr<Layer> make_layernorm(Device* d, int features, float eps);
 std::unique_ptr<Layer> make_gelu(Device* d, const Shape& shape);
 std::unique_ptr<Layer> make_glu(Device* d, int out_channels);
 std::unique_ptr<Layer> make_linear(Device* d, int in, int out, bool bias, int act,
-                                   mnn_precision prec);
+                                   mnn_precision prec, float leaky_alpha = 0.01f);
 std::unique_ptr<Layer> make_mha(Device* d, int embed, int heads, bool bias, mnn_precision prec);
 std::unique_ptr<Layer> make_feedforward(Device* d, int in, int hidden, mnn_precision prec);
 std::unique_ptr<Layer> make_encoder_block(Device* d, const mnn_encoder_block_desc& desc);
@@ -68,16 +73,30 @@ std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, i
 std::unique_ptr<Layer> make_cross_transformer(Device* d, int embed, int heads, int ffn,
                                               int layers, float layer_scale, mnn_precision prec);
 
+// Sequential fusion (layers.cpp): the number of layers from index i that run as one fused
+// group (1 = no fusion), and the fused run (y: the first layer's buffer, out: the last one's).
+int fused_chain_length(const std::vector<Layer*>& v, size_t i);
+void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor& in, Tensor& y,
+                     Tensor& out, Stream& s);
+
 // Sequential with the reference's ping-pong buffer plan (Model.swift:135-201).
 class Sequential {
  public:
+  // forwardAsync completion: status and the borrowed output (null on failure).
+  using Completion = std::function<void(mnn_status, Tensor*)>;
   explicit Sequential(Device* d) : dev_(d) {}
   ~Sequential();
   void add(Layer* l, bool checked);
   void build();
   Tensor* forward(const Tensor& in, Stream& s);
+  // Sequential.forwardAsync (Model.swift:271-346): enqueue the forward on s and return; `done`
+  // runs once, on a library thread, after the GPU work completes. Throws (and never calls
+  // `done`) when the forward cannot be enqueued.
+  void forward_async(const Tensor& in, Stream& s, Completion done);
   std::pair<int, int> buffer_stats() const;
   int layer_count() const { return (int)layers_.size(); }
+  // layer(at:) (Model.swift:354-357): null when out of range
+  Layer* layer_at(int index) const;
 
  private:
   struct Plan {
@@ -94,6 +113,13 @@ class Sequential {
   std::map<Shape, Plan> plans_;
   const Plan* last_plan_ = nullptr;
   std::mutex forward_mu_;
+  Tensor* forward_locked(const Tensor& in, Stream& s);
+  // forwardAsync bookkeeping: one forward in flight at a time; the destructor waits for the
+  // completion threads.
+  std::atomic<bool> async_in_flight_{false};
+  std::mutex async_mu_;
+  std::condition_variable async_cv_;
+  int async_threads_ = 0;
 };
 
 Tensor* tensor_create(Device* d, mnn_dtype dt, const Shape& shape);

@@ -1,5 +1,6 @@
 // Device timing hooks, tensors and Sequential.
 #include <algorithm>
+#include <thread>
 
 #include "layers.hpp"
 
@@ -71,7 +72,13 @@ void tensor_destroy(Tensor* t) {
 }
 
 // ------------------------------------------------------------------ Sequential
-Sequential::~Sequential() { free_plans(); }
+Sequential::~Sequential() {
+  {  // completion threads of forward_async hold `this` until their callback has returned
+    std::unique_lock<std::mutex> lk(async_mu_);
+    async_cv_.wait(lk, [&] { return async_threads_ == 0; });
+  }
+  free_plans();
+}
 
 void Sequential::free_plans() {
   for (auto& kv : plans_)
@@ -143,6 +150,10 @@ Sequential::Plan* Sequential::plan_for(const Shape& in) {
 
 Tensor* Sequential::forward(const Tensor& in, Stream& s) {
   std::lock_guard<std::mutex> lk(forward_mu_);
+  return forward_locked(in, s);
+}
+
+Tensor* Sequential::forward_locked(const Tensor& in, Stream& s) {
   MNN_REQUIRE(!layers_.empty(), MNN_ERR_EMPTY_MODEL, "Cannot run inference on empty model");
   MNN_REQUIRE(built_, MNN_ERR_NOT_BUILT, "Model not built. Call build() first.");
   // Model.swift:231-236 compares the whole shape; here leading batch dimensions are allowed
@@ -158,12 +169,58 @@ Tensor* Sequential::forward(const Tensor& in, Stream& s) {
   Plan* p = plan_for(in.shape);
   last_plan_ = p;
   const Tensor* cur = &in;
-  for (size_t i = 0; i < layers_.size(); ++i) {
-    Tensor* out = p->buffers[p->buffer_index[i]];
-    layers_[i]->forward(*cur, *out, s);
+  for (size_t i = 0; i < layers_.size();) {
+    const int n = fused_chain_length(layers_, i);
+    Tensor* out = p->buffers[p->buffer_index[i + n - 1]];
+    if (n > 1) {
+      run_fused_chain(layers_, i, n, *cur, *p->buffers[p->buffer_index[i]], *out, s);
+    } else {
+      layers_[i]->forward(*cur, *out, s);
+    }
     cur = out;
+    i += n;
   }
   return p->buffers[p->buffer_index.back()];
+}
+
+void Sequential::forward_async(const Tensor& in, Stream& s, Completion done) {
+  bool expected = false;
+  // Model.swift:272-283: concurrent forwardAsync calls would corrupt the shared buffers
+  MNN_REQUIRE(async_in_flight_.compare_exchange_strong(expected, true),
+              MNN_ERR_INVALID_CONFIGURATION,
+              "Concurrent forwardAsync() calls not supported. Use separate Sequential instances.");
+  Tensor* out = nullptr;
+  hipEvent_t ev = nullptr;
+  try {
+    std::lock_guard<std::mutex> lk(forward_mu_);
+    out = forward_locked(in, s);
+    dev_->make_current();
+    HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    HIP_CHECK(hipEventRecord(ev, s.s));
+  } catch (...) {
+    if (ev) (void)hipEventDestroy(ev);
+    async_in_flight_ = false;
+    throw;
+  }
+  {
+    std::lock_guard<std::mutex> lk(async_mu_);
+    ++async_threads_;
+  }
+  const int ordinal = dev_->ordinal;
+  std::thread([this, ev, out, ordinal, done = std::move(done)]() {
+    (void)hipSetDevice(ordinal);
+    const hipError_t e = hipEventSynchronize(ev);
+    (void)hipEventDestroy(ev);
+    async_in_flight_ = false;  // as the reference, cleared before the completion runs
+    done(e == hipSuccess ? MNN_OK : MNN_ERR_GPU_EXECUTION, e == hipSuccess ? out : nullptr);
+    std::lock_guard<std::mutex> lk(async_mu_);
+    --async_threads_;
+    async_cv_.notify_all();
+  }).detach();
+}
+
+Layer* Sequential::layer_at(int index) const {
+  return index >= 0 && index < (int)layers_.size() ? layers_[index] : nullptr;
 }
 
 std::pair<int, int> Sequential::buffer_stats() const {

@@ -13,13 +13,15 @@ from typing import Iterable, Optional, Sequence
 
 import numpy as np
 
+from . import _lib
 from ._lib import (ACT, PAD, PRECISION, Conv1dDesc, Conv2dDesc, ConvTranspose1dDesc,
                    ConvTranspose2dDesc, DecoderBlockDesc, EncoderBlockDesc, FreqBlockDesc, MNNError,
                    SeparatorDesc, check, dims, lib)
 
 __all__ = [
     "MNNError", "AudioDevice", "Stream", "Tensor", "Layer", "Conv1D", "DynamicConv1D",
-    "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "MultiHeadAttention", "CrossAttention",
+    "FusedConv1D", "GroupNorm", "LayerNorm", "GELU", "GLU", "Linear", "FusedLinear",
+    "MultiHeadAttention", "CrossAttention",
     "FeedForward", "UNetEncoderBlock", "ConvTranspose1D", "DynamicConvTranspose1D",
     "UNetDecoderBlock", "unet_padding", "unet_bottleneck_length", "TransformerLayer",
     "CrossTransformerEncoder", "Sequential", "SafeTensors", "BinaryModelFile", "WeightNameMapper",
@@ -232,19 +234,43 @@ class Conv1D(Layer):
 
     def __init__(self, device, input_channels, output_channels, kernel_size, stride=1, padding=0,
                  dilation=1, groups=1, use_bias=True, input_length=0, padding_mode=None,
-                 activation="none", precision="f32"):
+                 activation="none", precision="f32", leaky_relu_alpha=None):
         if padding_mode is None:
             padding_mode = "explicit"
         d = Conv1dDesc(input_channels, output_channels, kernel_size, stride, padding, dilation,
                        groups, int(use_bias), int(input_length), PAD[padding_mode], ACT[activation],
                        PRECISION[precision])
-        super().__init__(device, _create(lib().mnn_conv1d_create, device.handle, C.byref(d)))
+        if leaky_relu_alpha is None:
+            h = _create(lib().mnn_conv1d_create, device.handle, C.byref(d))
+        else:
+            h = _create(lib().mnn_fused_conv1d_create, device.handle, C.byref(d),
+                        float(leaky_relu_alpha))
+        super().__init__(device, h)
         self.use_bias = use_bias
 
     def load_weights(self, weights, bias=None) -> None:
         self.load_weights_named("weight", weights)
         if bias is not None and self.use_bias:
             self.load_weights_named("bias", bias)
+
+    def forward_with_residual(self, input: Tensor, residual: Optional[Tensor], output: Tensor,
+                              stream: Optional[Stream] = None) -> None:
+        """FusedConv1D.forwardWithResidual: output = act(conv + bias) + residual."""
+        check(lib().mnn_conv1d_forward_residual(self.handle, input.handle,
+                                                residual.handle if residual else None,
+                                                output.handle, _sh(stream)))
+
+
+class FusedConv1D(Conv1D):
+    """FusedConv1D (Conv1D.swift:742-1028): activation (default relu, as the reference) and
+    leakyReluAlpha (default 0.01)."""
+
+    def __init__(self, device, input_channels, output_channels, kernel_size, stride=1, padding=0,
+                 dilation=1, groups=1, use_bias=True, activation="relu", leaky_relu_alpha=0.01,
+                 input_length=0):
+        super().__init__(device, input_channels, output_channels, kernel_size, stride, padding,
+                         dilation, groups, use_bias, input_length, "explicit", activation,
+                         leaky_relu_alpha=leaky_relu_alpha)
 
 
 class DynamicConv1D(Conv1D):
@@ -291,16 +317,30 @@ class GLU(Layer):
 
 class Linear(Layer):
     def __init__(self, device, input_features, output_features, use_bias=True, activation="none",
-                 precision="f32"):
-        super().__init__(device, _create(lib().mnn_linear_create, device.handle, input_features,
-                                         output_features, int(use_bias), ACT[activation],
-                                         PRECISION[precision]))
+                 precision="f32", leaky_relu_alpha=None):
+        if leaky_relu_alpha is None:
+            h = _create(lib().mnn_linear_create, device.handle, input_features, output_features,
+                        int(use_bias), ACT[activation], PRECISION[precision])
+        else:
+            h = _create(lib().mnn_fused_linear_create, device.handle, input_features,
+                        output_features, int(use_bias), ACT[activation], float(leaky_relu_alpha),
+                        PRECISION[precision])
+        super().__init__(device, h)
         self.use_bias = use_bias
 
     def load_weights(self, weights, bias=None) -> None:
         self.load_weights_named("weight", weights)
         if bias is not None and self.use_bias:
             self.load_weights_named("bias", bias)
+
+
+class FusedLinear(Linear):
+    """FusedLinear (Linear.swift:475-672): activation (default relu) and leakyReluAlpha."""
+
+    def __init__(self, device, input_features, output_features, use_bias=True, activation="relu",
+                 leaky_relu_alpha=0.01, precision="f32"):
+        super().__init__(device, input_features, output_features, use_bias, activation,
+                         precision, leaky_relu_alpha=leaky_relu_alpha)
 
 
 class MultiHeadAttention(Layer):
@@ -933,6 +973,35 @@ class Sequential:
         n = C.c_int()
         check(lib().mnn_sequential_layer_count(self.handle, C.byref(n)))
         return n.value
+
+    def layer(self, at: int) -> Optional[Layer]:
+        """layer(at:) (Model.swift:354-357): the layer object added at that index, or None."""
+        h = C.c_void_p()
+        check(lib().mnn_sequential_layer_at(self.handle, at, C.byref(h)))
+        if not h.value:
+            return None
+        for l in self._layers:
+            if l.handle and C.cast(l.handle, C.c_void_p).value == h.value:
+                return l
+        raise RuntimeError("layer handle not known to this binding")
+
+    def forward_async(self, input: Tensor, completion, stream: Optional[Stream] = None) -> int:
+        """Sequential.forwardAsync (Model.swift:271-346): completion(status, output_or_None) runs
+        once, on a library thread after the GPU work (or here, before returning, when the forward
+        cannot be enqueued; the status is then also returned). `output` is borrowed as in
+        forward()."""
+        def trampoline(_user, status, out):
+            try:
+                completion(status, Tensor(self.device, (), _handle=C.c_void_p(out), _owned=False)
+                           if status == 0 and out else None)
+            except Exception:  # a raising Python callback must not unwind into the library
+                import traceback
+                traceback.print_exc()
+        cb = _lib.COMPLETION_FN(trampoline)
+        self._callbacks = getattr(self, "_callbacks", [])
+        self._callbacks.append(cb)  # kept alive until the model is closed
+        return lib().mnn_sequential_forward_async(self.handle, input.handle, _sh(stream), cb,
+                                                  None)
 
     def close(self) -> None:
         if self.handle:

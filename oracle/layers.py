@@ -8,7 +8,8 @@ import numpy as np
 
 __all__ = [
     "round_bf16", "reflect_pad", "conv1d", "group_norm", "layer_norm", "gelu_tanh", "gelu_layer",
-    "stable_sigmoid", "glu", "activation", "linear", "mha", "feed_forward", "encoder_block",
+    "stable_sigmoid", "glu", "activation", "fused_conv1d", "linear", "mha", "feed_forward",
+    "encoder_block",
     "time_encoder", "conv_transpose1d", "conv_transpose1d_gather", "decoder_block", "unet_padding",
     "unet_bottleneck_length", "time_unet", "transformer_layer", "cross_transformer",
     "reflect_index", "conv2d", "conv2d_output_size", "conv_transpose2d", "freq_encoder_block",
@@ -146,15 +147,16 @@ def glu(x, axis=-2, dtype=np.float64):
     return a * stable_sigmoid(b, dtype)
 
 
-def activation(x, act: str, dtype=np.float64):
-    """apply_activation of FusedConv1D / FusedLinear (Conv1D.swift:960-973, Linear.swift:630-639)."""
+def activation(x, act: str, dtype=np.float64, alpha=0.01):
+    """apply_activation of FusedConv1D / FusedLinear (Conv1D.swift:960-973, Linear.swift:630-639);
+    alpha = leakyReluAlpha (default 0.01, Conv1D.swift:786)."""
     x = _as(x, dtype)
     if act == "none":
         return x
     if act == "relu":
         return np.maximum(x, 0.0)
     if act == "leaky_relu":
-        return np.where(x >= 0.0, x, 0.01 * x)
+        return np.where(x >= 0.0, x, alpha * x)
     if act == "gelu":
         return gelu_tanh(x, dtype)
     if act == "swish":
@@ -166,12 +168,23 @@ def activation(x, act: str, dtype=np.float64):
     raise ValueError(act)
 
 
-def linear(x, w, b=None, act="none", dtype=np.float64):
-    """y = act(x W^T + b), W [out, in] (Linear.swift:337-365; linear_fused_forward :641-670)."""
+def fused_conv1d(x, w, b=None, stride=1, padding=0, dilation=1, groups=1, act="none",
+                 alpha=0.01, residual=None, dtype=np.float64):
+    """FusedConv1D.forwardWithResidual (Conv1D.swift:857-900; kernel :975-1025): zero-padded
+    conv + bias, then the activation, then the residual (added after the activation,
+    :1016-1023)."""
+    y = activation(conv1d(x, w, b, stride=stride, padding=padding, dilation=dilation,
+                          groups=groups, dtype=dtype), act, dtype, alpha)
+    return y if residual is None else y + _as(residual, dtype)
+
+
+def linear(x, w, b=None, act="none", dtype=np.float64, alpha=0.01):
+    """y = act(x W^T + b), W [out, in] (Linear.swift:337-365; linear_fused_forward :641-670);
+    alpha = FusedLinear's leakyReluAlpha (Linear.swift:495)."""
     y = _as(x, dtype) @ _as(w, dtype).T
     if b is not None:
         y = y + _as(b, dtype)
-    return activation(y, act, dtype)
+    return activation(y, act, dtype, alpha)
 
 
 def _softmax_ref(s):

@@ -691,3 +691,179 @@ def test_layer_weights_from_mtla(dev, stream, tmp_path):
     assert_close(got, ref, ATOL, RTOL, "encoder block from MTLA")
     with pytest.raises(nn.MNNError):
         m.load_into(blk, "conv.bias", "conv.weight")  # wrong element count
+
+
+# ----------------------------------------------------------------------------- FusedConv1D residual
+# (B, cin, cout, k, s, p, g, act, alpha, L): the direct kernels (small contractions, groups) and
+# the matrix-core implicit GEMM (Cin * K >= 64); biases are negative so that many pre-activations
+# are negative: a residual added before ReLU / leaky ReLU instead of after fails these.
+FUSED_CASES = [
+    (1, 2, 48, 8, 4, 0, 1, "relu", 0.01, 4001),          # register-window direct kernel
+    (2, 6, 12, 5, 2, 2, 3, "leaky_relu", 0.25, 203),     # generic direct kernel, groups
+    (2, 48, 96, 8, 4, 3, 1, "relu", 0.01, 1031),         # implicit GEMM on the matrix cores
+    (1, 96, 64, 4, 1, 1, 1, "leaky_relu", 0.2, 517),     # implicit GEMM, leaky slope 0.2
+    (1, 16, 32, 3, 1, 1, 1, "gelu", 0.01, 300),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[str(c) for c in FUSED_CASES])
+def test_fused_conv1d_residual_parity(dev, stream, case):
+    B, cin, cout, k, s, p, g, act, alpha, L = case
+    say(f"fused conv1d residual {case}")
+    x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin // g, k)) * np.sqrt(2 / (cin // g * k))).astype(np.float32)
+    b = (RNG.standard_normal(cout) * 0.1 - 0.3).astype(np.float32)
+    layer = nn.FusedConv1D(dev, cin, cout, k, s, p, groups=g, activation=act,
+                           leaky_relu_alpha=alpha)
+    layer.load_weights(w, b)
+    lo = (L + 2 * p - k) // s + 1
+    res = (RNG.standard_normal((B, cout, lo)) * 2).astype(np.float32)
+    xt, rt = nn.Tensor.from_numpy(dev, x), nn.Tensor.from_numpy(dev, res)
+    out = nn.Tensor(dev, (B, cout, lo))
+    layer.forward_with_residual(xt, rt, out, stream)
+    stream.sync(60000)
+    ref = oracle.fused_conv1d(x, w, b, stride=s, padding=p, groups=g, act=act, alpha=alpha,
+                              residual=res)
+    pre = oracle.conv1d(x, w, b, stride=s, padding=p, groups=g)
+    assert (pre < 0).mean() > 0.2  # the activation's negative side is exercised
+    assert_close(out.to_numpy(), ref, ATOL, RTOL, "fused conv + residual")
+    # residual = output (in place) and no residual
+    out2 = nn.Tensor.from_numpy(dev, res)
+    layer.forward_with_residual(xt, out2, out2, stream)
+    layer.forward_with_residual(xt, None, out, stream)
+    stream.sync(60000)
+    assert_close(out2.to_numpy(), ref, ATOL, RTOL, "fused conv + residual in place")
+    assert_close(out.to_numpy(), oracle.activation(pre, act, alpha=alpha), ATOL, RTOL,
+                 "fused conv without residual")
+
+
+def test_fused_conv1d_residual_errors(dev, stream):
+    say("fused conv residual errors")
+    layer = nn.FusedConv1D(dev, 4, 8, 3, padding=1)
+    x = nn.Tensor(dev, (1, 4, 20))
+    with pytest.raises(nn.MNNError) as e:
+        layer.forward_with_residual(x, nn.Tensor(dev, (1, 8, 19)), nn.Tensor(dev, (1, 8, 20)),
+                                    stream)
+    assert e.value.name == "MNN_ERR_BUFFER_SIZE_MISMATCH"
+    with pytest.raises(nn.MNNError) as e:
+        gn = nn.GroupNorm(dev, 1, 4)
+        nn.Conv1D.forward_with_residual(gn, x, None, nn.Tensor(dev, (1, 4, 20)), stream)
+    assert e.value.name == "MNN_ERR_INVALID_ARGUMENT"
+    with pytest.raises(nn.MNNError):
+        nn.FusedConv1D(dev, 4, 8, 3, leaky_relu_alpha=float("nan"))
+
+
+def test_fused_linear_leaky_alpha(dev, stream):
+    say("fused linear leaky relu alpha 0.3")
+    x = RNG.standard_normal((300, 64)).astype(np.float32)
+    w = (RNG.standard_normal((96, 64)) * 0.1).astype(np.float32)
+    b = (RNG.standard_normal(96) * 0.1).astype(np.float32)
+    layer = nn.FusedLinear(dev, 64, 96, activation="leaky_relu", leaky_relu_alpha=0.3)
+    layer.load_weights(w, b)
+    got = run_layer(layer, x, dev, stream)
+    assert_close(got, oracle.linear(x, w, b, act="leaky_relu", alpha=0.3), ATOL, RTOL,
+                 "fused linear alpha")
+
+
+# ----------------------------------------------------------------------------- Sequential API
+def test_sequential_layer_at(dev):
+    """layer(at:) (Model.swift:354-357): the added layers in order, None out of range."""
+    say("sequential layer(at:)")
+    seq = nn.Sequential(dev)
+    ls = [nn.Linear(dev, 8, 8) for _ in range(3)]
+    for l in ls:
+        seq.add(l)
+    assert seq.layer_count == 3
+    assert [seq.layer(i) for i in range(3)] == ls
+    assert seq.layer(3) is None and seq.layer(-1) is None
+
+
+def test_sequential_forward_async(dev, stream):
+    """forwardAsync (Model.swift:271-346): the completion gets the same output forward() gives,
+    once; failures before enqueueing reach the completion on the calling thread."""
+    import threading
+    say("sequential forwardAsync")
+    seq = nn.Sequential(dev)
+    keep = []
+    for _ in range(3):
+        l = nn.Linear(dev, 32, 32, activation="gelu")
+        l.load_weights((RNG.standard_normal((32, 32)) * 0.2).astype(np.float32),
+                       (RNG.standard_normal(32) * 0.1).astype(np.float32))
+        keep.append(l)
+        seq.add(l)
+    seq.build()
+    x = RNG.standard_normal((50, 32)).astype(np.float32)
+    xt = nn.Tensor.from_numpy(dev, x)
+    want = seq.forward(xt, stream).to_numpy(stream).copy()
+    done = threading.Event()
+    got = {}
+
+    def completion(status, out):
+        got["status"] = status
+        got["value"] = out.to_numpy() if out is not None else None
+        got["thread"] = threading.get_ident()
+        got["calls"] = got.get("calls", 0) + 1
+        done.set()
+
+    rc = seq.forward_async(xt, completion, stream)
+    assert rc == 0
+    assert done.wait(30), "completion not called"
+    assert got["status"] == 0 and got["calls"] == 1
+    assert got["thread"] != threading.get_ident()
+    np.testing.assert_array_equal(got["value"], want)
+    # a completion may start the next forwardAsync (the in-flight mark is already cleared)
+    done2 = threading.Event()
+    chained = {}
+
+    def second(status, out):
+        chained["status"] = status
+        done2.set()
+
+    def first(status, out):
+        chained["rc"] = seq.forward_async(xt, second, stream)
+
+    assert seq.forward_async(xt, first, stream) == 0
+    assert done2.wait(30) and chained["rc"] == 0 and chained["status"] == 0
+    # not built / empty: reported through the completion, synchronously, and returned
+    errs = []
+    empty = nn.Sequential(dev)
+    rc = empty.forward_async(xt, lambda st, out: errs.append((st, out)), stream)
+    assert rc == 9 and errs == [(9, None)]  # MNN_ERR_EMPTY_MODEL
+    unbuilt = nn.Sequential(dev)
+    unbuilt.add(nn.Linear(dev, 32, 32))
+    rc = unbuilt.forward_async(xt, lambda st, out: errs.append((st, out)), stream)
+    assert rc == 11 and errs[-1] == (11, None)  # MNN_ERR_NOT_BUILT
+
+
+@pytest.mark.parametrize("cin,cout,L,act,gelu", [
+    (2, 48, 44100, "none", True),     # config-1 shape: direct conv, GELU layer fused
+    (48, 96, 3001, "none", False),    # matrix-core conv with GEMM statistics, GN alone
+    (8, 16, 777, "gelu", False),      # GroupNorm's own fused activation
+])
+def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu):
+    """Conv1D -> GroupNorm(1) [-> GELU] in a Sequential runs fused (two launches); the result is
+    the layers' composition, batch 2 included."""
+    say(f"sequential conv -> groupnorm fusion {cin}->{cout} L={L} act={act} gelu={gelu}")
+    x = RNG.uniform(-1, 1, (2, cin, L)).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin, 8)) * np.sqrt(2 / (cin * 8))).astype(np.float32)
+    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    gm = (1 + 0.2 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.2 * RNG.standard_normal(cout)).astype(np.float32)
+    conv = nn.DynamicConv1D(dev, cin, cout, 8, 4, padding_mode="reflect", padding=3)
+    conv.load_weights(w, b)
+    gn = nn.GroupNorm(dev, 1, cout, activation=act)
+    gn.load_parameters(gm, bt)
+    seq = nn.Sequential(dev)
+    seq.add(conv)
+    seq.add(gn)
+    layers = [conv, gn]
+    if gelu:
+        g = nn.GELU(dev, [cout, 0])
+        seq.add_unchecked(g)
+        layers.append(g)
+    seq.build()
+    out = seq.forward(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    ref = oracle.group_norm(oracle.conv1d(x, w, b, stride=4, padding=3, mode="reflect"), 1, gm, bt)
+    ref = oracle.gelu_layer(ref) if gelu else oracle.activation(ref, act)
+    assert_close(out.to_numpy().reshape(ref.shape), ref, ATOL, RTOL, "fused sequential")

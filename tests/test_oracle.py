@@ -400,3 +400,27 @@ def test_time_unet_lengths_round_trip():
                     "norm.bias": np.zeros(ch[i]), "groups": min(8, ch[i])})
     y = oracle.time_unet(RNG.standard_normal((1, 2, L)), enc, dec)
     assert y.shape == (1, 2, L)
+
+
+@pytest.mark.parametrize("act,alpha", [("relu", 0.01), ("leaky_relu", 0.01), ("leaky_relu", 0.3),
+                                       ("gelu", 0.01), ("swish", 0.01), ("none", 0.01)])
+def test_fused_conv1d_residual_vs_torch(act, alpha):
+    """FusedConv1D.forwardWithResidual: act(conv + b) + residual (Conv1D.swift:1016-1023), against
+    torch's conv1d and activations; a residual added before the activation (the plausible
+    mistake) differs wherever the pre-activation is negative."""
+    r = np.random.default_rng(61)
+    x = r.standard_normal((2, 6, 50))
+    w = r.standard_normal((8, 3, 5)) * 0.4
+    b = r.standard_normal(8) * 0.3
+    res = r.standard_normal((2, 8, 24)) * 2
+    got = oracle.fused_conv1d(x, w, b, stride=2, padding=1, dilation=1, groups=2, act=act,
+                              alpha=alpha, residual=res)
+    y = F.conv1d(t64(x), t64(w), t64(b), stride=2, padding=1, groups=2)
+    y = {"relu": F.relu, "leaky_relu": lambda v: F.leaky_relu(v, alpha),
+         "gelu": lambda v: F.gelu(v, approximate="tanh"), "swish": F.silu,
+         "none": lambda v: v}[act](y)
+    np.testing.assert_allclose(got, (y + t64(res)).numpy(), rtol=1e-12, atol=1e-12)
+    if act in ("relu", "leaky_relu"):
+        before = oracle.activation(oracle.conv1d(x, w, b, stride=2, padding=1, groups=2) + res,
+                                   act, alpha=alpha)
+        assert np.abs(before - got).max() > 0.1
