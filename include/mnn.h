@@ -170,6 +170,17 @@ mnn_status mnn_conv1d_forward_residual(mnn_layer layer, mnn_tensor input, mnn_te
 mnn_status mnn_groupnorm_create(mnn_device dev, int num_groups, int num_channels, float epsilon,
                                 int affine, mnn_activation activation, mnn_layer* out);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The forward of a layer
+ * made by mnn_groupnorm_create, as mnn_layer_forward, that allocates nothing: its statistics
+ * partials (3 floats per 4096-element chunk of each (batch, group)) go to a fixed scratch of
+ * 65536 floats per GPU, held until the process ends, instead of the layer's workspace. Inputs
+ * needing more than 21845 partials (batch * groups * ceil(C / groups * L / 4096)) fail with
+ * MNN_ERR_INVALID_CONFIGURATION. All calls on one GPU share its scratch: calls that overlap
+ * (other streams, other threads) race; calls ordered on one stream do not. */
+mnn_status mnn_groupnorm_forward_noalloc(mnn_layer layer, mnn_tensor input, mnn_tensor output,
+                                         mnn_stream s);
+
 /* LayerNorm over the last dimension (Normalization.swift:734-964). "gamma"/"weight", "beta"/"bias". */
 mnn_status mnn_layernorm_create(mnn_device dev, int feature_size, float epsilon, mnn_layer* out);
 

@@ -138,6 +138,7 @@ SIGNATURES = {
     "mnn_conv1d_create": (C.c_int, [P, C.POINTER(Conv1dDesc), PP]),
     "mnn_fused_conv1d_create": (C.c_int, [P, C.POINTER(Conv1dDesc), C.c_float, PP]),
     "mnn_conv1d_forward_residual": (C.c_int, [P, P, P, P, P]),
+    "mnn_groupnorm_forward_noalloc": (C.c_int, [P, P, P, P]),
     "mnn_groupnorm_create": (C.c_int, [P, C.c_int, C.c_int, C.c_float, C.c_int, C.c_int, PP]),
     "mnn_layernorm_create": (C.c_int, [P, C.c_int, C.c_float, PP]),
     "mnn_gelu_create": (C.c_int, [P, C.c_int, I64P, PP]),

@@ -421,6 +421,20 @@ mnn_status mnn_groupnorm_create(mnn_device dev, int num_groups, int num_channels
                                 int affine, mnn_activation act, mnn_layer* out) {
   MNN_CREATE(make_groupnorm(d, num_groups, num_channels, epsilon, affine != 0, act));
 }
+mnn_status mnn_groupnorm_forward_noalloc(mnn_layer layer, mnn_tensor input, mnn_tensor output,
+                                         mnn_stream st) {
+  return guard([&] {
+    Layer* l = L(layer);
+    Tensor* in = T(input);
+    Tensor* out = T(output);
+    MNN_REQUIRE(in->dev == l->device() && out->dev == l->device(), MNN_ERR_INVALID_ARGUMENT,
+                "tensors must live on the layer's device");
+    in->dev->check_alive();
+    Stream s = resolve_stream(in->dev, st);
+    in->dev->make_current();
+    groupnorm_forward_noalloc(l, *in, *out, s);
+  });
+}
 mnn_status mnn_layernorm_create(mnn_device dev, int feature_size, float epsilon, mnn_layer* out) {
   MNN_CREATE(make_layernorm(d, feature_size, epsilon));
 }

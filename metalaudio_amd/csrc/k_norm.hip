@@ -353,6 +353,29 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 }  // namespace
 
+// Statistics partials of the allocation-free GroupNorm entry point. One copy per GPU, held until
+// the process ends; every allocation-free call on a GPU uses that GPU's copy.
+static __device__ __align__(256) float scratch[kGnScratchFloats];
+
+float* gn_scratch(int device) {
+  // hipGetSymbolAddress once per device, with that device current (the caller made it current);
+  // host code uses the returned address, never the symbol itself
+  static std::mutex mu;
+  static std::map<int, float*> ptrs;
+  std::lock_guard<std::mutex> lk(mu);
+  auto it = ptrs.find(device);
+  if (it != ptrs.end()) return it->second;
+  int cur = -1;
+  HIP_CHECK(hipGetDevice(&cur));
+  MNN_REQUIRE(cur == device, MNN_ERR_INVALID_ARGUMENT,
+              "gn_scratch: device " << device << " is not the current device");
+  float* p = nullptr;
+  HIP_CHECK(hipGetSymbolAddress(reinterpret_cast<void**>(&p), HIP_SYMBOL(scratch)));
+  MNN_REQUIRE(p, MNN_ERR_GPU_EXECUTION, "no device address for the GroupNorm scratch");
+  ptrs.emplace(device, p);
+  return p;
+}
+
 int gn_num_chunks(int C, int G, int64_t L) {
   const int64_t total = (int64_t)(C / G) * L;
   return (int)std::max<int64_t>(1, (total + kChunk - 1) / kChunk);

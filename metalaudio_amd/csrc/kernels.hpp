@@ -37,6 +37,11 @@ void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_
 void gn_apply_parts(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L, int G,
                     const float* parts, int nparts, const float* gamma, const float* beta,
                     float eps, int act);
+// Fixed device scratch for the allocation-free GroupNorm forward: kGnScratchFloats floats per
+// GPU (a file-scope __device__ array of k_norm.hip); gn_scratch returns its address on `device`,
+// which must be current. Calls that use it concurrently on one GPU race.
+constexpr int64_t kGnScratchFloats = 65536;
+float* gn_scratch(int device);
 // LayerNorm over rows of F features (two-pass statistics, biased variance, rsqrt).
 void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
                const float* gamma, const float* beta, float eps);

@@ -297,6 +297,21 @@ class GroupNormLayer : public Layer {
     k::gn_stats_partial(ctx(s), in.f32(), (int)B, C_, L, G_, partials_.f32(), nchunk);
     apply_parts(s, in.f32(), out.f32(), (int)B, L, partials_.f32(), nchunk, act_);
   }
+  // forward() without any allocation: the partials go to the GPU's fixed scratch array.
+  void forward_noalloc(const Tensor& in, Tensor& out, Stream& s) {
+    check_out(out, infer_output(in.shape));
+    int64_t B, C, L;
+    split_bcl(in.shape, B, C, L);
+    const int nchunk = k::gn_num_chunks(C_, G_, L);
+    const int64_t need = 3 * B * G_ * (int64_t)nchunk;
+    MNN_REQUIRE(need <= k::kGnScratchFloats, MNN_ERR_INVALID_CONFIGURATION,
+                "GroupNorm without allocation: batch * groups * ceil(C / groups * L / 4096) = "
+                    << need / 3 << " statistics partials exceed the scratch's "
+                    << k::kGnScratchFloats / 3);
+    float* parts = k::gn_scratch(dev_->ordinal);
+    k::gn_stats_partial(ctx(s), in.f32(), (int)B, C_, L, G_, parts, nchunk);
+    apply_parts(s, in.f32(), out.f32(), (int)B, L, parts, nchunk, act_);
+  }
   // y = act(GroupNorm(x)) from statistics partials (nparts per (b, g)).
   void apply_parts(Stream& s, const float* x, float* y, int B, int64_t L, const float* parts,
                    int nparts, int act) const {
@@ -1867,6 +1882,13 @@ void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor
   c->run(in.f32(), (int)B, (int)L, y.f32(), MNN_ACT_NONE, parts, s);
   g->apply_parts(s, y.f32(), out.f32(), (int)B, ys.back(), parts, nparts,
                  n == 3 ? MNN_ACT_GELU : g->act());
+}
+
+void groupnorm_forward_noalloc(Layer* l, const Tensor& in, Tensor& out, Stream& s) {
+  auto* g = dynamic_cast<GroupNormLayer*>(l);
+  MNN_REQUIRE(g, MNN_ERR_INVALID_ARGUMENT,
+              "allocation-free GroupNorm forward needs a GroupNorm layer, got " << l->kind());
+  g->forward_noalloc(in, out, s);
 }
 
 // ------------------------------------------------------------------ factories

@@ -54,6 +54,8 @@ void conv1d_forward_residual(Layer* l, const Tensor& in, const Tensor* res, Tens
                              Stream& s);
 std::unique_ptr<Layer> make_groupnorm(Device* d, int groups, int channels, float eps, bool affine,
                                       int act);
+// GroupNorm forward with its statistics partials in the GPU's fixed scratch (no allocation).
+void groupnorm_forward_noalloc(Layer* l, const Tensor& in, Tensor& out, Stream& s);
 std::unique_ptr<Layer> make_layernorm(Device* d, int features, float eps);
 std::unique_ptr<Layer> make_gelu(Device* d, const Shape& shape);
 std::unique_ptr<Layer> make_glu(Device* d, int out_channels);
