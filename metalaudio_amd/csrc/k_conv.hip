@@ -90,7 +90,7 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
 // (CK samples) into registers with all loads in flight together, then produces the COB output
 // channels of its workgroup (grid.y spreads the channels, so there are enough waves per SIMD to
 // hide memory latency). Weights are staged in LDS and read as broadcasts.
-template <int CK, int COB>
+template <int CK, int COB, bool REFLECT>
 __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams p,
                                                                      const float* __restrict__ x,
                                                                      const float* __restrict__ w,
@@ -112,22 +112,23 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams 
   __syncthreads();
   const float* xb = x + (int64_t)b * p.Cin * p.Lin;
   float xv[CK];
-  const int base = t * p.stride - p.pad;
+  // every window load is issued before any is used: addresses are clamped (zero padding) or
+  // mirrored (reflect) instead of branched around (a load under a branch makes the compiler wait
+  // for it, and for all earlier loads, before the next one); out-of-range taps are zeroed after
+  const int base = min(t, p.Lout - 1) * p.stride - p.pad;
 #pragma unroll
   for (int e = 0; e < CK; ++e) {
     const int ci = e / p.K, kk = e - ci * p.K;
     int pos = base + kk * p.dilation;
-    float v = 0.f;
-    if (valid) {
-      if (p.reflect) {
-        pos = pos < 0 ? -pos : pos;
-        pos = pos >= p.Lin ? 2 * (p.Lin - 1) - pos : pos;
-        v = xb[(int64_t)ci * p.Lin + pos];
-      } else if (pos >= 0 && pos < p.Lin) {
-        v = xb[(int64_t)ci * p.Lin + pos];
-      }
+    float keep = valid ? 1.f : 0.f;
+    if constexpr (REFLECT) {
+      pos = abs(pos);
+      pos = min(pos, 2 * (p.Lin - 1) - pos);
+    } else {
+      keep = (pos >= 0 && pos < p.Lin) ? keep : 0.f;
+      pos = min(max(pos, 0), p.Lin - 1);
     }
-    xv[e] = v;
+    xv[e] = xb[(int64_t)ci * p.Lin + pos] * keep;  // x is finite: 0 * x = 0
   }
   ShiftedStats st;
   {
@@ -197,12 +198,18 @@ void conv1d_direct(const LaunchCtx& c, const ConvParams& p0, const float* x, con
   if (const int ck = reg_ck(p)) {
     dim3 grid(cdiv(p.Lout, kThreads), p.Cout / 16, p.B);
     if (nchunk) *nchunk = (int)(grid.x * grid.y);
-    switch (ck) {
-      case 8: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<8, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
-      case 16: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<16, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
-      case 24: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<24, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
-      default: return launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<32, 16>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials);
+#define MNN_REG(CKV, R) launch(c, "conv1d_direct_f32", conv1d_direct_reg_kernel<CKV, 16, R>, grid, dim3(kThreads), 0, p, x, w, bias, y, act, partials)
+    switch (ck * 2 + (p.reflect ? 1 : 0)) {
+      case 16: return MNN_REG(8, false);
+      case 17: return MNN_REG(8, true);
+      case 32: return MNN_REG(16, false);
+      case 33: return MNN_REG(16, true);
+      case 48: return MNN_REG(24, false);
+      case 49: return MNN_REG(24, true);
+      case 64: return MNN_REG(32, false);
+      default: return MNN_REG(32, true);
     }
+#undef MNN_REG
   }
   MNN_REQUIRE(y, MNN_ERR_INVALID_ARGUMENT, "conv1d_direct: output required");
   const int cob = co_block(p);

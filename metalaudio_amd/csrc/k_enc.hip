@@ -490,6 +490,229 @@ __global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- first level, fused
+// A level whose conv has few input channels (Cin * 8 = K1 <= 32) and C = 48 output channels
+// (HTDemucs' first time-encoder level): conv -> GroupNorm(1) -> GELU -> rewrite 48 -> 96 -> GLU
+// in one pass per 32 output columns, nothing but the block output written to HBM. The GroupNorm
+// statistics come from a statistics-only pass of the direct conv (k_conv.hip) and are folded into
+// the conv: GN(W1 x + b1) = (sc . W1) x + (sc b1 + sh), sc = gamma * rstd, sh = beta - mean * sc.
+//
+// Per wave and 32 columns t:
+//   conv     two 32x32 blocks of channels (48 real) on v_mfma_f32_32x32x2_f32, K1 = Cin * 8 taps:
+//            lane l feeds A = W1'[32 cb + l%32][2s + l/32] and B = x[e / 8][4t - pad + e % 8],
+//            e = 2s + l/32, straight from global memory (reflect / zero padding by index);
+//   GELU     on the accumulators: lane l, register v of block cb holds channel
+//            ch(cb, v, g) = 32 cb + 8 (v/4) + 4 g + v%4 (g = l/32) at column l%32;
+//   rewrite  three 32-row blocks of the regrouped weight [a0..a15 | b0..b15] times z, K = 48: the
+//            MFMA's k slot g of k pair p = 16 cb + v is channel ch(cb, v, g), which is exactly the
+//            value lane l already holds, so the GELU output feeds the B operand in place; the A
+//            operand (rewrite weight columns in that order) is packed on the host as
+//            a_rw[(mb * 24 + p) * 64 + lane] and held in registers for the whole kernel;
+//   GLU      registers v and v + 8 of a block are partners (rows rr and rr + 16).
+constexpr int kL1C = 48, kL1MB = 3, kL1KP = 24;
+struct EncL1KArgs {
+  int C = 0, Cin = 0, pad = 0, nparts = 0;
+  int64_t L = 0, Lout = 0, ldo = 0;
+  float eps = 1e-5f;
+  const float* x = nullptr;
+  const float* w1 = nullptr;  // [C][Cin * 8]
+  const float* b1 = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float* parts = nullptr;       // [B][nparts] GroupNorm(1) partials (written by the stats pass)
+  const float* a_rw = nullptr;  // [3][24][64] packed rewrite A operand
+  const float* rb = nullptr;    // [96] regrouped rewrite bias
+  float* out = nullptr;
+};
+
+// The conv operand of one 32-column task: lane l supplies, for MFMA k step s, the tap
+// e = 2s + l/32 of column t = 32 task + l%32, i.e. x[e / 8][4t - pad + e % 8]. Addresses are
+// mirrored (reflect) or clamped (zero padding, the value then zeroed) rather than branched around,
+// so every load of the task is in flight at once.
+template <int CIN, bool REFLECT>
+__device__ __forceinline__ void l1_load_x(const float* __restrict__ xb, int Ls, int Lout, int pad,
+                                          int task, int lane, float (&xv)[4 * CIN]) {
+  const int g = lane >> 5, l32 = lane & 31;
+  const int t = min(task * 32 + l32, Lout - 1);
+#pragma unroll
+  for (int s = 0; s < 4 * CIN; ++s) {
+    const int e = 2 * s + g, ci = e >> 3, j = e & 7;
+    int pos = 4 * t - pad + j;
+    float keep = 1.f;
+    if constexpr (REFLECT) {
+      pos = abs(pos);
+      pos = min(pos, 2 * (Ls - 1) - pos);
+    } else {
+      keep = (pos >= 0 && pos < Ls) ? 1.f : 0.f;
+      pos = min(max(pos, 0), Ls - 1);
+    }
+    xv[s] = xb[(int64_t)ci * Ls + pos] * keep;  // x is finite: 0 * x = 0
+  }
+}
+
+// Two 32-channel blocks of the conv of one task on v_mfma_f32_32x32x2_f32 (A: lane l holds the
+// weight of channel 32 cb + l%32, tap 2s + l/32; the accumulators arrive holding the bias).
+template <int CIN>
+__device__ __forceinline__ void l1_conv(const float (&acv)[2][4 * CIN],
+                                        const float (&xv)[4 * CIN], floatx16 (&ac)[2]) {
+#pragma unroll
+  for (int s = 0; s < 4 * CIN; ++s)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+      ac[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(acv[cb][s], xv[s], ac[cb], 0, 0, 0);
+}
+
+// Statistics pass of the fused first level: the conv y = W1 x + b1 of every column (as the fused
+// pass computes it), reduced to one GroupNorm(1) partial (count, mean, M2) per workgroup at
+// parts[b * gridDim.x + blockIdx.x]. Lane sums are shifted by the lane's first value; workgroup
+// merge by Chan's formula.
+template <int CIN, bool REFLECT>
+__global__ __launch_bounds__(256) void enc_l1_stats_kernel(EncL1KArgs a) {
+  constexpr int C = kL1C, KS = 4 * CIN, K1 = 8 * CIN;
+  __shared__ float red[3 * 4];
+  __shared__ float s_b1[64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int b = blockIdx.y;
+  if (tid < 64) s_b1[tid] = (tid < C && a.b1) ? a.b1[tid] : 0.f;
+  float acv[2][KS];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c = 32 * cb + l32, cc = min(c, C - 1);
+    const float live = c < C ? 1.f : 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acv[cb][s] = a.w1[cc * K1 + 2 * s + g] * live;
+  }
+  __syncthreads();
+  const float* __restrict__ xb = a.x + (int64_t)b * CIN * a.L;
+  const int Ls = (int)a.L, Lo = (int)a.Lout;
+  const int tasks = (Lo + 31) / 32;
+  const int stride = gridDim.x * 4;
+  ShiftedStats st[2];
+  int task = blockIdx.x * 4 + wave;
+  float xv[KS];
+  if (task < tasks) l1_load_x<CIN, REFLECT>(xb, Ls, Lo, a.pad, task, lane, xv);
+  for (; task < tasks; task += stride) {
+    float xn[KS];
+    if (task + stride < tasks) l1_load_x<CIN, REFLECT>(xb, Ls, Lo, a.pad, task + stride, lane, xn);
+    floatx16 ac[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) ac[cb][v] = s_b1[32 * cb + 8 * (v / 4) + 4 * g + (v % 4)];
+    l1_conv<CIN>(acv, xv, ac);
+    if (task * 32 + l32 < Lo) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) st[v & 1].add(ac[0][v]);
+#pragma unroll
+      for (int v = 0; v < 8; ++v) st[v & 1].add(ac[1][v]);  // channels 32..47
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) xv[s] = xn[s];
+  }
+  float sn, smean, sm2, n2, mean2, m22;
+  st[0].finish(sn, smean, sm2);
+  st[1].finish(n2, mean2, m22);
+  welford_combine(sn, smean, sm2, n2, mean2, m22);
+  block_welford(sn, smean, sm2, red);
+  if (tid == 0) {
+    float* o = a.parts + ((int64_t)b * gridDim.x + blockIdx.x) * 3;
+    o[0] = sn;
+    o[1] = smean;
+    o[2] = sm2;
+  }
+}
+
+// The rewrite's A operand (72 values per lane) stays in registers for the whole kernel: read
+// from LDS per MFMA, each MFMA would wait for its read (the register budget of more waves per
+// SIMD leaves no room to read ahead), which measured 4x slower.
+template <int CIN, bool REFLECT>
+__global__ __launch_bounds__(256, 2) void enc_l1_fused_kernel(EncL1KArgs a) {
+  constexpr int C = kL1C, KS = 4 * CIN, K1 = 8 * CIN;
+  __shared__ double redd[3 * 4];
+  __shared__ float s_sc[64], s_bp[64], s_rb[2 * kL1C];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int b = blockIdx.y;
+  // loaded while the statistics merge runs
+  float arw[kL1MB][kL1KP];
+#pragma unroll
+  for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p) arw[mb][p] = a.a_rw[(mb * kL1KP + p) * 64 + lane];
+  const float2 ms = gn1_merge_one_round(a.parts + (int64_t)b * a.nparts * 3, a.nparts, a.eps, redd);
+  if (tid < 64) {
+    float sc = 0.f, bp = 0.f;
+    if (tid < C) {
+      sc = (a.gamma ? a.gamma[tid] : 1.f) * ms.y;
+      bp = fmaf(a.b1 ? a.b1[tid] : 0.f, sc, (a.beta ? a.beta[tid] : 0.f) - ms.x * sc);
+    }
+    s_sc[tid] = sc;
+    s_bp[tid] = bp;
+  } else if (tid < 64 + 2 * C) {
+    s_rb[tid - 64] = a.rb[tid - 64];
+  }
+  __syncthreads();
+  // conv weights scaled by the GroupNorm scale of their channel (rows 48..63: scale 0); the
+  // loads are unconditional (clamped rows) so that they are all in flight together
+  float acv[2][KS];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c = 32 * cb + l32, cc = min(c, C - 1);
+    const float sc = s_sc[c];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acv[cb][s] = a.w1[cc * K1 + 2 * s + g] * sc;
+  }
+  const float* __restrict__ xb = a.x + (int64_t)b * CIN * a.L;
+  float* __restrict__ ob = a.out + (int64_t)b * C * a.ldo;
+  const int Ls = (int)a.L, Lo = (int)a.Lout;
+  const int tasks = (Lo + 31) / 32;
+  const int stride = gridDim.x * 4;
+  int task = blockIdx.x * 4 + wave;
+  float xv[KS];
+  if (task < tasks) l1_load_x<CIN, REFLECT>(xb, Ls, Lo, a.pad, task, lane, xv);
+  for (; task < tasks; task += stride) {
+    float xn[KS];
+    if (task + stride < tasks) l1_load_x<CIN, REFLECT>(xb, Ls, Lo, a.pad, task + stride, lane, xn);
+    floatx16 ac[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int ch = 32 * cb + 8 * (v / 4) + 4 * g + (v % 4);
+        ac[cb][v] = s_bp[ch];  // zero for the padding channels 48..63
+      }
+    l1_conv<CIN>(acv, xv, ac);
+    float z[kL1KP];
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p) z[p] = gelu_tanh_fast(ac[p / 16][p % 16]);
+    floatx16 ar[kL1MB];
+#pragma unroll
+    for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) ar[mb][v] = 0.f;
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p)
+#pragma unroll
+      for (int mb = 0; mb < kL1MB; ++mb)
+        ar[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(arw[mb][p], z[p], ar[mb], 0, 0, 0);
+    const int tc = task * 32 + l32;
+    if (tc < a.Lout) {
+#pragma unroll
+      for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int rr = 8 * (v / 4) + 4 * g + (v % 4);
+          const float va = ar[mb][v] + s_rb[32 * mb + rr];
+          const float vb = ar[mb][v + 8] + s_rb[32 * mb + 16 + rr];
+          ob[(int64_t)(16 * mb + rr) * a.ldo + tc] = va * stable_sigmoid(vb);
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) xv[s] = xn[s];
+  }
+}
+
 // ---------------------------------------------------------------- host-side selection
 struct ConvTile {
   int id, bm, bn;
@@ -621,6 +844,84 @@ void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
     launch(c, "enc_conv_reduce_f32", enc_conv_reduce_kernel, dim3(cdiv(a.N, kRedCols), a.M, p.B),
            dim3(kRedThreads), 0, (const float*)p.ws, plan.splits, a.M, a.N, p.bias, p.y, p.ldy,
            a.y_bs, p.parts);
+}
+
+bool enc_l1_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
+                      int64_t L) {
+  return Cin >= 1 && Cin <= 4 && Cout == kL1C && ks == 8 && stride == 4 && dil == 1 &&
+         groups == 1 && pad >= 0 && pad < 4 && L > pad && L >= 8 && Cin * L < (1LL << 31);
+}
+
+void enc_l1_pack_rewrite(const float* wperm, float* out) {
+  // out[(mb * 24 + p) * 64 + lane] = wperm[32 mb + lane % 32][ch(p / 16, p % 16, lane / 32)],
+  // ch(cb, v, g) = 32 cb + 8 (v / 4) + 4 g + v % 4 (the channel lane holds in register v)
+  for (int mb = 0; mb < kL1MB; ++mb)
+    for (int p = 0; p < kL1KP; ++p)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int cb = p / 16, v = p % 16, gg = lane / 32;
+        const int ch = 32 * cb + 8 * (v / 4) + 4 * gg + (v % 4);
+        out[(mb * kL1KP + p) * 64 + lane] = wperm[(32 * mb + lane % 32) * kL1C + ch];
+      }
+}
+
+int enc_l1_parts(int64_t Lout) {
+  const int f = env_int("MNN_ENC_L1_SWGS");  // tuning override: statistics-pass workgroups
+  return (int)std::min<int64_t>(cdiv(cdiv(Lout, 32), 4), f > 0 ? f : 2 * kCUs);
+}
+
+void enc_l1(const LaunchCtx& c, const EncL1Args& p) {
+  MNN_REQUIRE(enc_l1_supported(p.Cin, p.C, 8, 4, 1, 1, p.pad, p.L) && p.parts &&
+                  p.a_rw && p.rb && p.w1 && p.out && p.ldo >= p.Lout && p.Lout >= 1 &&
+                  (p.Lout - 1) * 4 + 8 <= p.L + 2 * p.pad,
+              MNN_ERR_INVALID_ARGUMENT, "enc_l1: unsupported configuration");
+  EncL1KArgs a;
+  a.C = p.C;
+  a.Cin = p.Cin;
+  a.pad = p.pad;
+  a.L = p.L;
+  a.Lout = p.Lout;
+  a.ldo = p.ldo;
+  a.eps = p.eps;
+  a.x = p.x;
+  a.w1 = p.w1;
+  a.b1 = p.b1;
+  a.gamma = p.gamma;
+  a.beta = p.beta;
+  a.parts = p.parts;
+  a.a_rw = p.a_rw;
+  a.rb = p.rb;
+  a.out = p.out;
+  const int64_t tasks = cdiv(p.Lout, 32);
+  {  // statistics pass: one partial per workgroup
+    a.nparts = enc_l1_parts(p.Lout);
+    dim3 sgrid((unsigned)a.nparts, p.B), block(256);
+#define MNN_L1S(CIN, R) launch(c, "enc_l1_stats_f32", enc_l1_stats_kernel<CIN, R>, sgrid, block, 0, a)
+    switch (p.Cin * 2 + (p.reflect ? 1 : 0)) {
+      case 2: MNN_L1S(1, false); break;
+      case 3: MNN_L1S(1, true); break;
+      case 4: MNN_L1S(2, false); break;
+      case 5: MNN_L1S(2, true); break;
+      case 6: MNN_L1S(3, false); break;
+      case 7: MNN_L1S(3, true); break;
+      case 8: MNN_L1S(4, false); break;
+      default: MNN_L1S(4, true); break;
+    }
+#undef MNN_L1S
+  }
+  const int fw = env_int("MNN_ENC_L1_WGS");  // tuning override: fused-pass workgroups
+  dim3 grid((unsigned)std::min<int64_t>(cdiv(tasks, 4), fw > 0 ? fw : 2 * kCUs), p.B), block(256);
+#define MNN_L1(CIN, R) launch(c, "enc_l1_fused_f32", enc_l1_fused_kernel<CIN, R>, grid, block, 0, a)
+  switch (p.Cin * 2 + (p.reflect ? 1 : 0)) {
+    case 2: return MNN_L1(1, false);
+    case 3: return MNN_L1(1, true);
+    case 4: return MNN_L1(2, false);
+    case 5: return MNN_L1(2, true);
+    case 6: return MNN_L1(3, false);
+    case 7: return MNN_L1(3, true);
+    case 8: return MNN_L1(4, false);
+    default: return MNN_L1(4, true);
+  }
+#undef MNN_L1
 }
 
 int enc_rewrite_kp(int C) { return (C + 31) / 32 * 32; }

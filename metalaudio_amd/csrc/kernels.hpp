@@ -331,6 +331,34 @@ struct EncRewriteArgs {
 };
 int enc_rewrite_kp(int C);
 void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& a);
+// First-level block in two passes (Cin <= 4, C = 48, kernel 8 / stride 4, pad < 4): a statistics
+// pass computes the conv on the matrix cores and writes one GroupNorm(1) partial per workgroup
+// (enc_l1_parts per batch, into parts); the second pass recomputes the conv with GroupNorm folded
+// into its weights and bias, applies GELU on the accumulators, runs the rewrite 48 -> 96 from
+// there and GLU; only out [B][48][ldo] is written. a_rw is the rewrite weight, regrouped into
+// 32-row GLU blocks ([96][48]), packed by enc_l1_pack_rewrite into the kernel's operand order
+// (3 * 24 * 64 floats); rb the regrouped rewrite bias.
+int enc_l1_parts(int64_t Lout);
+struct EncL1Args {
+  int B = 1, Cin = 0, C = 0, pad = 0;
+  int64_t L = 0, Lout = 0, ldo = 0;
+  bool reflect = true;
+  float eps = 1e-5f;
+  const float* x = nullptr;      // [B][Cin][L]
+  const float* w1 = nullptr;     // conv weight [C][Cin * 8]
+  const float* b1 = nullptr;     // conv bias [C] (may be null)
+  const float* gamma = nullptr;  // GroupNorm affine (may be null)
+  const float* beta = nullptr;
+  float* parts = nullptr;        // workspace: 3 * B * enc_l1_parts(Lout) floats
+  const float* a_rw = nullptr;
+  const float* rb = nullptr;
+  float* out = nullptr;
+};
+constexpr int kEncL1PackFloats = 3 * 24 * 64;
+bool enc_l1_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
+                      int64_t L);
+void enc_l1_pack_rewrite(const float* wperm, float* out);
+void enc_l1(const LaunchCtx& c, const EncL1Args& a);
 
 // ------------------------------------------------------------------ attention (k_attention.hip)
 struct AttnArgs {

@@ -747,10 +747,16 @@ class EncoderBlockLayer : public Layer {
         rw_perm_.reserve(sizeof(float) * 2 * C * C);
         rw_pad_.reserve(sizeof(float) * 2 * C * kp);
         rb_perm_.reserve(sizeof(float) * 2 * C);
-        std::vector<float> z(2LL * C * kp, 0.f);
+        std::vector<float> z(std::max<int64_t>(2LL * C * kp, k::kEncL1PackFloats), 0.f);
         HIP_CHECK(hipMemcpy(rw_perm_.ptr, z.data(), 2LL * C * C * 4, hipMemcpyHostToDevice));
-        HIP_CHECK(hipMemcpy(rw_pad_.ptr, z.data(), z.size() * 4, hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpy(rw_pad_.ptr, z.data(), 2LL * C * kp * 4, hipMemcpyHostToDevice));
         HIP_CHECK(hipMemcpy(rb_perm_.ptr, z.data(), 2LL * C * 4, hipMemcpyHostToDevice));
+        if (k::enc_l1_supported(desc.in_channels, C, desc.kernel_size, desc.stride, 1, 1,
+                                (desc.kernel_size - 1) / 2, 8)) {
+          l1_pack_.reserve(sizeof(float) * k::kEncL1PackFloats);
+          HIP_CHECK(hipMemcpy(l1_pack_.ptr, z.data(), sizeof(float) * k::kEncL1PackFloats,
+                              hipMemcpyHostToDevice));
+        }
       }
     }
   }
@@ -779,6 +785,34 @@ class EncoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t lo = os.back();
     const bool g1 = norm_->groups() == 1;
+    if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32 && l1_pack_.ptr &&
+        k::enc_l1_supported(d_.in_channels, Cout, d_.kernel_size, d_.stride, 1, 1,
+                            conv_->pad_for(L), L)) {
+      // Few input channels (the first level): a statistics pass, then one fused pass (conv
+      // recomputed with GroupNorm folded in, GELU, rewrite, GLU); only the output is written.
+      partials_.reserve(sizeof(float) * 3 * B * k::enc_l1_parts(lo));
+      k::EncL1Args e;
+      e.B = (int)B;
+      e.Cin = d_.in_channels;
+      e.C = Cout;
+      e.pad = conv_->pad_for(L);
+      e.L = L;
+      e.Lout = lo;
+      e.ldo = lo;
+      e.reflect = conv_->desc().padding_mode == MNN_PAD_REFLECT;
+      e.eps = norm_->eps();
+      e.x = in.f32();
+      e.w1 = conv_->weight_ptr();
+      e.b1 = conv_->bias_ptr();
+      e.gamma = norm_->gamma();
+      e.beta = norm_->beta();
+      e.parts = partials_.f32();
+      e.a_rw = l1_pack_.f32();
+      e.rb = rb_perm_.f32();
+      e.out = out.f32();
+      k::enc_l1(ctx(s), e);
+      return;
+    }
     if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32) {
       // Matrix-core path (k_enc.hip): the implicit-GEMM conv writes y and GroupNorm statistics
       // partials; the rewrite applies GroupNorm + GELU once (transposed into zt_) and runs the
@@ -984,6 +1018,11 @@ class EncoderBlockLayer : public Layer {
       for (int r = 0; r < 2 * C; ++r)
         std::copy_n(p.data() + (int64_t)r * C, C, q.data() + (int64_t)r * kp);
       HIP_CHECK(hipMemcpy(rw_pad_.ptr, q.data(), q.size() * 4, hipMemcpyHostToDevice));
+      if (l1_pack_.ptr) {  // the fused first-level kernel's register order
+        std::vector<float> pk(k::kEncL1PackFloats);
+        k::enc_l1_pack_rewrite(p.data(), pk.data());
+        HIP_CHECK(hipMemcpy(l1_pack_.ptr, pk.data(), pk.size() * 4, hipMemcpyHostToDevice));
+      }
     } else if (name == "rewrite.bias") {
       std::vector<float> p(n);
       for (int blk = 0; blk < C / 16; ++blk)
@@ -1002,7 +1041,7 @@ class EncoderBlockLayer : public Layer {
   Param* rw_ = nullptr;
   Param* rb_ = nullptr;
   bool glu_fused_ = false;
-  DevBuf rw_perm_, rb_perm_, rw_pad_;
+  DevBuf rw_perm_, rb_perm_, rw_pad_, l1_pack_;
   DevBuf y_, partials_, z_, wpad_, ws_, zt_;
 };
 

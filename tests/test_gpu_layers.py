@@ -369,7 +369,11 @@ def test_encoder_block_reference_fixture(dev, stream, golden_dir, name):
                                           (8, 24, 400, 1),
                                           # fused small-input blocks: batch, ragged tile, Cin 1 / 3 / 4
                                           (2, 48, 5003, 2), (4, 32, 777, 1), (1, 16, 64, 3),
-                                          (3, 48, 1031, 1)])
+                                          (3, 48, 1031, 1),
+                                          # fused first-level pass: Cin 1..4, C 48, ragged
+                                          # 32-column tasks, tiny inputs, batch 3
+                                          (1, 48, 777, 1), (4, 48, 2049, 2), (2, 48, 9, 3),
+                                          (2, 48, 131, 1)])
 def test_encoder_block_rewrite_parity(dev, stream, cin, cout, L, B):
     say(f"encoder block rewrite {cin}->{cout} L={L} B={B}")
     x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
