@@ -8,7 +8,9 @@ seeded synthetic data of the configurations' shapes, resident in HBM before timi
 
 The headline is the wall clock around the K timed steps. Per-kernel-family GPU time comes from a
 second pass of K steps with HIP events bracketing every library launch on its stream
-(mnn_device_kernel_timing); the dominant family is reported against MI355X peak as `roofline`. The CPU baseline times the fp32 oracle on one chunk on host cores.
+(mnn_device_kernel_timing); the dominant family is reported against MI355X peak as `roofline`,
+every family (the encoder's per level) in `kernels`. The CPU baseline times the torch-CPU
+restatement of the same layers (oracle/torch_cpu.py) on one chunk on the host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--precision f32|bf16]
 """
@@ -62,27 +64,46 @@ class Markers:
 
 # ------------------------------------------------------------------ algorithmic work per step
 def encoder_work():
-    """flops and bytes per chunk of config 4, per kernel family."""
+    """Algorithmic flops and bytes per chunk of config 4, per encoder kernel and level (the
+    kernel-timing names carry the level's channel count, e.g. "enc_conv_f32[c96]").
+    bytes = inputs read once + outputs written once + weights once; flops = 2 M N K."""
+    import ctypes
     from metalaudio_amd import workloads as W
+    from metalaudio_amd._lib import lib
     L = W.CHUNK_SAMPLES
     fam = {}
     ch = W.ENC_CHANNELS
+
+    def add(name, flops, byts):
+        f = fam.setdefault(name, [0.0, 0.0])
+        f[0] += flops
+        f[1] += byts
     for i in range(4):
         cin, cout = ch[i], ch[i + 1]
         lo = (L + 6 - 8) // 4 + 1
         conv_flops = 2.0 * cout * lo * cin * 8
-        conv_bytes = 4.0 * (cin * L + cout * lo + cout * cin * 8 + cout)
         rw_flops = 2.0 * 2 * cout * lo * cout
-        rw_bytes = 4.0 * (cout * lo + cout * lo + 2 * cout * cout + 2 * cout)
-        f = fam.setdefault("enc_conv_f32", [0.0, 0.0])
-        f[0] += conv_flops
-        f[1] += conv_bytes
-        f = fam.setdefault("enc_rewrite_f32", [0.0, 0.0])
-        f[0] += rw_flops
-        f[1] += rw_bytes
-        # GroupNorm + GELU pass: reads the conv output, writes the rewrite operand
-        f = fam.setdefault("enc_gn_gelu_t_f32", [0.0, 0.0])
-        f[1] += 4.0 * 2 * cout * lo
+        x_b, y_b = 4.0 * cin * L, 4.0 * cout * lo
+        conv_w = 4.0 * (cout * cin * 8 + cout)
+        rw_w = 4.0 * (2 * cout * cout + 2 * cout)
+        tag = f"[c{cout}]"
+        if cin <= 4 and cout == 48:
+            # fused first level: statistics pass (conv recomputed, x read) and the fused pass
+            # (conv again + rewrite; x read, block output written)
+            add("enc_l1_stats_f32" + tag, conv_flops, x_b + conv_w)
+            add("enc_l1_fused_f32" + tag, conv_flops + rw_flops, x_b + y_b + conv_w + rw_w)
+        else:
+            sp, tm, tn = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+            lib().mnn_debug_enc_conv_plan(cin, cout, lo, 1, ctypes.byref(sp), ctypes.byref(tm),
+                                          ctypes.byref(tn))
+            if sp.value > 1:
+                # the conv writes one partial product per K part, the reduce pass sums them
+                add("enc_conv_f32" + tag, conv_flops, x_b + conv_w + sp.value * y_b)
+                add("enc_conv_reduce_f32" + tag, 0.0, sp.value * y_b + y_b)
+            else:
+                add("enc_conv_f32" + tag, conv_flops, x_b + y_b + conv_w)
+            add("enc_gn_gelu_t_f32" + tag, 0.0, 2 * y_b)  # y read, GELU(GN(y)) written
+            add("enc_rewrite_f32" + tag, rw_flops, 2 * y_b + rw_w)
         L = lo
     return fam
 
@@ -158,36 +179,59 @@ def timed(fn, stream, steps):
 
 
 # ------------------------------------------------------------------ CPU baseline
-def cpu_baseline(m, budget_s=20.0):
-    """fp32 oracle (numpy + BLAS) on one chunk: config 4 at batch 1 and config 5 at batch 1
-    (the per-chunk share of the batch-4 transformer)."""
-    import oracle
+def cpu_baseline(m, warmup=3, runs=10, budget_s=40.0):
+    """The reference CPU path's stand-in: the torch-CPU restatement of the same layers
+    (oracle/torch_cpu.py; the reference's Accelerate layers need Swift and Apple frameworks) on
+    one chunk: config 4 at batch 1 and config 5 at batch 1 (the per-chunk share of the batch-4
+    transformer), fp32, torch.inference_mode, all host threads; 3 warm-ups, then the median of
+    10 runs (fewer if a run is so slow that 10 would exceed the budget)."""
+    import platform
+
+    import torch
     from metalaudio_amd import workloads as W
+    from oracle import torch_cpu as tc
     threads = os.cpu_count() or 1
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max(int(i.get("num_threads", 1)) for i in threadpool_info()) or threads
-    except Exception:
-        pass
+    torch.set_num_threads(threads)
     c4 = m["c4"]
     c5 = W.config5(batch=1)
+    x = tc.to_torch(c4["x"])
+    lv = [{k: tc.to_torch(v) for k, v in l.items()} for l in c4["levels"]]
+    t = tc.to_torch(c5["time"])
+    f = tc.to_torch(c5["freq"])
+    p = {k: tc.to_torch(v) for k, v in c5["params"].items()}
+
+    def one():
+        with torch.inference_mode():
+            tc.time_encoder(x, lv)
+            tc.cross_transformer(t, f, p, c5["layers"], c5["heads"])
+    for _ in range(warmup):
+        one()
     times = []
     t_start = time.perf_counter()
-    while True:
+    for _ in range(runs):
         t0 = time.perf_counter()
-        oracle.time_encoder(c4["x"], c4["levels"], dtype=np.float32)
-        oracle.cross_transformer(c5["time"], c5["freq"], c5["params"], c5["layers"], c5["heads"],
-                                 dtype=np.float32)
+        one()
         times.append((time.perf_counter() - t0) * 1e3)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 5:
+        if time.perf_counter() - t_start > budget_s:
             break
+    cpu_model = platform.processor() or ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": round(statistics.median(times), 2),
         "unit": "ms per chunk",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{len(times)} run(s) of one 7.8 s chunk: config 4 (batch 1) + config 5 at "
-                  f"batch 1, fp32 numpy/BLAS oracle, median; host {os.cpu_count()} CPUs",
+        "sample": f"median of {len(times)} runs after {warmup} warm-ups of one 7.8 s chunk: "
+                  f"config 4 (batch 1) + config 5 at batch 1, torch-CPU restatement "
+                  f"(oracle/torch_cpu.py), fp32, torch {torch.__version__}, "
+                  f"{threads} threads, CPU: {cpu_model}",
     }
 
 
@@ -329,17 +373,21 @@ def config_table(nn, W, dev, stream, m, cpu=True):
 
     # config 1: Conv1D 2->48 k8 s4 -> GroupNorm(1) -> GELU (HBM-bound; bytes = x + y)
     c1 = W.config1()
+    # as the reference composes it: Sequential [Conv1D, GroupNorm, GELU] (run as one fused
+    # group: the conv with GroupNorm statistics in its epilogue, then one apply pass)
     conv = nn.Conv1D(dev, 2, 48, 8, stride=4, padding=0, input_length=44100)
     conv.load_weights(c1["conv_w"], c1["conv_b"])
-    gn = nn.GroupNorm(dev, 1, 48, activation="gelu")
+    gn = nn.GroupNorm(dev, 1, 48)
     gn.load_parameters(c1["gn_w"], c1["gn_b"])
+    gelu1 = nn.GELU(dev, [1, 48, 11024])
+    seq1 = nn.Sequential(dev)
+    for layer in (conv, gn, gelu1):
+        seq1.add_unchecked(layer)
+    seq1.build()
     x1 = nn.Tensor.from_numpy(dev, c1["x"])
-    y1 = nn.Tensor(dev, (1, 48, 11024))
-    z1 = nn.Tensor(dev, (1, 48, 11024))
 
     def f1():
-        conv.forward(x1, y1, stream)
-        gn.forward(y1, z1, stream)
+        seq1.forward(x1, stream)
     cpu1 = time_cpu(lambda: oracle.gelu_layer(oracle.group_norm(oracle.conv1d(
         c1["x"], c1["conv_w"], c1["conv_b"], stride=4, dtype=np.float32), 1, c1["gn_w"],
         c1["gn_b"], dtype=np.float32), dtype=np.float32)) if cpu else None
@@ -502,7 +550,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--precision", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=40.0,
+                    help="seconds of timed CPU-baseline runs at most")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration table")
     args = ap.parse_args()
 
@@ -545,11 +594,11 @@ def main():
     markers.pop()
     dev.set_kernel_timing(False)
     fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
-            "gemm_f32_simple", "enc_conv_f32", "enc_conv_reduce_f32", "enc_gn_gelu_t_f32",
-            "enc_rewrite_f32", "conv1d_direct", "layernorm", "gn_stats", "gn_finalize",
+            "gemm_f32_simple", "conv1d_direct", "layernorm", "gn_stats", "gn_finalize",
             "gn_apply", "copy_bytes", "glu_f32", "gelu_f32"]
+    enc_kernels = list(encoder_work())  # per level, e.g. enc_conv_f32[c96]
     ktime = {}
-    for f in fams:
+    for f in fams + enc_kernels:
         n, ms = dev.kernel_timing(f)
         if n:
             ktime[f] = (n, ms)
@@ -587,7 +636,17 @@ def main():
             rows[f] = {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
                        "unit": "GB/s", "frac": round(ach / PEAK["hbm"], 4),
                        "ms_per_step": round(t * 1e3, 3), "launches_per_step": n // args.steps}
-    dom = max(ktime, key=lambda k: ktime[k][1])
+    # the encoder as a whole (all its kernels, one chunk's algorithmic flops)
+    enc_ms = sum(ktime[k][1] for k in enc_kernels if k in ktime) / args.steps
+    if enc_ms > 0:
+        ew = encoder_work()
+        ef = 4 * sum(ew[k][0] for k in enc_kernels)  # 4 chunks per step
+        rows["encoder_all_levels"] = {
+            "bound": "mfma", "achieved": round(ef / (enc_ms / 1e3) / 1e12, 2), "peak": 157.3,
+            "unit": "TFLOP/s", "frac": round(ef / (enc_ms / 1e3) / PEAK["f32"], 4),
+            "ms_per_step": round(enc_ms, 3),
+            "launches_per_step": sum(ktime[k][0] for k in enc_kernels if k in ktime) // args.steps}
+    dom = max((k for k in ktime if k in rows), key=lambda k: ktime[k][1])
     roof = dict(rows.get(dom, {}))
     roof["kernel"] = dom
     traffic = None
@@ -608,7 +667,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
-        cpu = cpu_baseline(m, args.cpu_budget)
+        cpu = cpu_baseline(m, budget_s=args.cpu_budget)
 
     out = {
         "metric": METRIC,

@@ -22,6 +22,12 @@ extern "C" {
 mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, const float* b,
                                 float* d);
 
+/* The plan the encoder's implicit-GEMM conv launcher picks for a level (input channels, output
+ * channels, output length, batch): K split count and output tile. bench.py uses it to account the
+ * split-K reduce pass's bytes. */
+mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t out_length,
+                                   int batch, int* splits, int* tile_m, int* tile_n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -220,6 +220,7 @@ SIGNATURES = {
     "mnn_sequential_layer_count": (C.c_int, [P, IP]),
     "mnn_sequential_layer_at": (C.c_int, [P, C.c_int, PP]),
     "mnn_debug_mfma_probe": (C.c_int, [P, C.c_int, FP, FP, FP]),
+    "mnn_debug_enc_conv_plan": (C.c_int, [C.c_int, C.c_int, C.c_int64, C.c_int, IP, IP, IP]),
 }
 
 _lib = None

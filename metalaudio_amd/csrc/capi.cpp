@@ -1135,4 +1135,14 @@ mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, con
   });
 }
 
+mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t out_length,
+                                   int batch, int* splits, int* tile_m, int* tile_n) {
+  return guard([&] {
+    MNN_REQUIRE(splits && tile_m && tile_n && in_channels > 0 && out_channels > 0 &&
+                    out_length > 0 && batch > 0,
+                MNN_ERR_INVALID_ARGUMENT, "invalid argument");
+    k::enc_conv_plan_info(in_channels, out_channels, out_length, batch, splits, tile_m, tile_n);
+  });
+}
+
 }  // extern "C"

@@ -714,6 +714,12 @@ __global__ __launch_bounds__(256, 2) void enc_l1_fused_kernel(EncL1KArgs a) {
 }
 
 // ---------------------------------------------------------------- host-side selection
+// Kernel-timing name of an encoder launch tagged with the level's channel count, e.g.
+// "enc_conv_f32[c96]" (timing queries match by substring, so the family name still sums them).
+std::string level_name(const char* family, int channels) {
+  return std::string(family) + "[c" + std::to_string(channels) + "]";
+}
+
 struct ConvTile {
   int id, bm, bn;
   int lds_kb;  // LDS per workgroup (KiB, rounded up)
@@ -782,9 +788,11 @@ void launch_conv(const LaunchCtx& c, const ConvKArgs& a, int batch) {
   using Cfg = ConvCfg<WMW, WNW, WM, WN, S>;
   dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), batch * a.splits), block(Cfg::NT);
   if (a.splits > 1)
-    launch(c, "enc_conv_f32", enc_conv_kernel<WMW, WNW, WM, WN, S, true>, grid, block, 0, a);
+    launch(c, level_name("enc_conv_f32", a.M).c_str(), enc_conv_kernel<WMW, WNW, WM, WN, S, true>,
+           grid, block, 0, a);
   else
-    launch(c, "enc_conv_f32", enc_conv_kernel<WMW, WNW, WM, WN, S, false>, grid, block, 0, a);
+    launch(c, level_name("enc_conv_f32", a.M).c_str(),
+           enc_conv_kernel<WMW, WNW, WM, WN, S, false>, grid, block, 0, a);
 }
 
 }  // namespace
@@ -797,6 +805,14 @@ bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int grou
 }
 
 int enc_conv_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
+
+void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, int* splits, int* bm,
+                        int* bn) {
+  const ConvPlan p = plan_conv(Cout, (int)Lout, enc_conv_padded_cin(Cin) * 8, batch);
+  *splits = p.splits;
+  *bm = p.t->bm;
+  *bn = p.t->bn;
+}
 
 int enc_conv_parts(int Cout, int64_t Lout, int K, int batch) {
   return conv_parts(plan_conv(Cout, (int)Lout, K, batch), Cout, (int)Lout);
@@ -841,7 +857,8 @@ void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
     default: launch_conv<2, 2, 1, 1, 4>(c, a, p.B); break;
   }
   if (plan.splits > 1)
-    launch(c, "enc_conv_reduce_f32", enc_conv_reduce_kernel, dim3(cdiv(a.N, kRedCols), a.M, p.B),
+    launch(c, level_name("enc_conv_reduce_f32", a.M).c_str(), enc_conv_reduce_kernel,
+           dim3(cdiv(a.N, kRedCols), a.M, p.B),
            dim3(kRedThreads), 0, (const float*)p.ws, plan.splits, a.M, a.N, p.bias, p.y, p.ldy,
            a.y_bs, p.parts);
 }
@@ -895,7 +912,8 @@ void enc_l1(const LaunchCtx& c, const EncL1Args& p) {
   {  // statistics pass: one partial per workgroup
     a.nparts = enc_l1_parts(p.Lout);
     dim3 sgrid((unsigned)a.nparts, p.B), block(256);
-#define MNN_L1S(CIN, R) launch(c, "enc_l1_stats_f32", enc_l1_stats_kernel<CIN, R>, sgrid, block, 0, a)
+    const std::string sname = level_name("enc_l1_stats_f32", p.C);
+#define MNN_L1S(CIN, R) launch(c, sname.c_str(), enc_l1_stats_kernel<CIN, R>, sgrid, block, 0, a)
     switch (p.Cin * 2 + (p.reflect ? 1 : 0)) {
       case 2: MNN_L1S(1, false); break;
       case 3: MNN_L1S(1, true); break;
@@ -910,7 +928,8 @@ void enc_l1(const LaunchCtx& c, const EncL1Args& p) {
   }
   const int fw = env_int("MNN_ENC_L1_WGS");  // tuning override: fused-pass workgroups
   dim3 grid((unsigned)std::min<int64_t>(cdiv(tasks, 4), fw > 0 ? fw : 2 * kCUs), p.B), block(256);
-#define MNN_L1(CIN, R) launch(c, "enc_l1_fused_f32", enc_l1_fused_kernel<CIN, R>, grid, block, 0, a)
+  const std::string fname = level_name("enc_l1_fused_f32", p.C);
+#define MNN_L1(CIN, R) launch(c, fname.c_str(), enc_l1_fused_kernel<CIN, R>, grid, block, 0, a)
   switch (p.Cin * 2 + (p.reflect ? 1 : 0)) {
     case 2: return MNN_L1(1, false);
     case 3: return MNN_L1(1, true);
@@ -933,7 +952,8 @@ void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& p) {
   // about 1024 workgroups in all, each with the same number of tiles
   const int64_t tiles = (int64_t)cdiv(p.Lout, kTT) * cdiv(p.kp, kTT);
   const int64_t per = cdiv(tiles, std::max<int64_t>(1, 1024 / p.B));
-  launch(c, "enc_gn_gelu_t_f32", enc_gn_gelu_t_kernel, dim3((unsigned)cdiv(tiles, per), 1, p.B),
+  launch(c, level_name("enc_gn_gelu_t_f32", p.C).c_str(), enc_gn_gelu_t_kernel,
+         dim3((unsigned)cdiv(tiles, per), 1, p.B),
          dim3(256), 0, p);
   GemmArgs g;
   g.M = 2 * p.C;
@@ -952,7 +972,8 @@ void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& p) {
   g.bias = p.bias;
   g.bias_mode = BIAS_M;
   g.glu = true;
-  g.name = "enc_rewrite_f32";
+  const std::string rname = level_name("enc_rewrite_f32", p.C);
+  g.name = rname.c_str();
   MNN_REQUIRE(gemm_nk_lds_supported(g), MNN_ERR_INVALID_ARGUMENT,
               "enc_rewrite: operands outside the LDS GEMM's contract");
   gemm_nk_lds(c, g);

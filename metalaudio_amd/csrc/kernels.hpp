@@ -303,6 +303,9 @@ int enc_conv_padded_cin(int Cin);
 // Statistics partials per batch the launch writes; K = enc_conv_padded_cin(Cin) * 8.
 int enc_conv_parts(int Cout, int64_t Lout, int K, int batch);
 int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch);
+// The K split and output tile the conv launcher picks (for measurement accounting).
+void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, int* splits, int* bm,
+                        int* bn);
 void enc_conv(const LaunchCtx& c, const EncConvArgs& a);
 // Rewrite 1x1 conv C -> 2C with GLU: out[b][c][t] = z[c] * sigmoid(z[c + C]),
 // z = w * GELU(GroupNorm(y)) + bias, in two launches: GroupNorm + GELU of y written transposed to

@@ -424,3 +424,23 @@ def test_fused_conv1d_residual_vs_torch(act, alpha):
         before = oracle.activation(oracle.conv1d(x, w, b, stride=2, padding=1, groups=2) + res,
                                    act, alpha=alpha)
         assert np.abs(before - got).max() > 0.1
+
+
+def test_torch_cpu_baseline_matches_oracle():
+    """The torch-CPU restatement bench.py times as the CPU baseline computes the same function
+    as the numpy oracle (config 4 on a short signal, config 5 at reduced lengths, stress
+    parameters so that biases and affine terms are exercised)."""
+    from oracle import torch_cpu as tc
+    c4 = workloads.config4(stress=True, samples=6000)
+    lv = [{k: tc.to_torch(v) for k, v in l.items()} for l in c4["levels"]]
+    with torch.inference_mode():
+        got = tc.time_encoder(tc.to_torch(c4["x"]), lv).numpy()
+    assert_close(got, oracle.time_encoder(c4["x"], c4["levels"]), 1e-4, 1e-3, "torch encoder")
+    c5 = workloads.config5(stress=True, batch=2, time_len=70, freq_len=130, layers=3)
+    p = {k: (np.full_like(v, 0.5) if "gamma_" in k else v) for k, v in c5["params"].items()}
+    pt = {k: tc.to_torch(v) for k, v in p.items()}
+    with torch.inference_mode():
+        t, f = tc.cross_transformer(tc.to_torch(c5["time"]), tc.to_torch(c5["freq"]), pt, 3, 8)
+    rt, rf = oracle.cross_transformer(c5["time"], c5["freq"], p, 3, 8)
+    assert_close(t.numpy(), rt, 1e-4, 1e-3, "torch transformer time")
+    assert_close(f.numpy(), rf, 1e-4, 1e-3, "torch transformer freq")
