@@ -405,15 +405,23 @@ def config_table(nn, W, dev, stream, m, cpu=True):
                                                             dtype=np.float32),
                                               c2["ln_w"], c2["ln_b"], dtype=np.float32)) \
         if cpu else None
+    x2b = nn.Tensor.from_numpy(dev, c2["x"], dtype="bf16")  # bf16 X: 2 MB
     for prec in ("f32", "bf16"):
         lin = nn.Linear(dev, 512, 2048, precision=prec)
         lin.load_weights(c2["w"], c2["b"])
+        xin = x2b if prec == "bf16" else x2
 
         def f2():
-            lin.forward(x2, y2, stream)
+            lin.forward(xin, y2, stream)
             ln.forward(y2, z2, stream)
         row(f"2_linear_ln_{prec}", time_gpu(f2, stream, 20), flops=2.0 * 2048 * 2048 * 512,
             prec=prec, cpu_ms=cpu2 if prec == "f32" else None)
+        # the Linear alone: fp32 on the matrix cores; bf16 (X and W bf16, Y fp32: 2 + 2 + 16 MB)
+        # bound by HBM
+        es = 2 if prec == "bf16" else 4
+        row(f"2_linear_{prec}", time_gpu(lambda: lin.forward(xin, y2, stream), stream, 20),
+            flops=2.0 * 2048 * 2048 * 512, prec=prec,
+            byts=es * (2048 * 512 * 2) + 4.0 * 2048 * 2048)
 
     # config 3: pre-norm MHSA + FFN layer, S 2048, E 512
     c3 = W.config3()

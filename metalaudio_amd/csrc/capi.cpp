@@ -982,7 +982,8 @@ mnn_status mnn_layer_forward(mnn_layer layer, mnn_tensor input, mnn_tensor outpu
     d->check_alive();
     MNN_REQUIRE(in->dev == d && o->dev == d, MNN_ERR_INVALID_ARGUMENT,
                 "tensors and layer on different devices");
-    MNN_REQUIRE(in->dtype == MNN_F32, MNN_ERR_INVALID_ARGUMENT, "input must be f32");
+    MNN_REQUIRE(in->dtype == MNN_F32 || l->accepts_bf16(), MNN_ERR_INVALID_ARGUMENT,
+                l->kind() << ": input must be f32");
     Stream s = resolve_stream(d, st);
     d->make_current();
     l->forward(*in, *o, s);

@@ -76,7 +76,31 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const uint8_t* __restric
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+__global__ __launch_bounds__(kThreads) void f32_to_bf16_kernel(const float* __restrict__ x,
+                                                               uint16_t* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = f32_to_bf16_bits(x[i]);
+}
+
+__global__ __launch_bounds__(kThreads) void bf16_to_f32_kernel(const uint16_t* __restrict__ x,
+                                                               float* __restrict__ y, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    y[i] = __uint_as_float((uint32_t)x[i] << 16);
+}
+
 }  // namespace
+
+void f32_to_bf16(const LaunchCtx& c, const float* x, uint16_t* y, int64_t n) {
+  if (n <= 0) return;
+  launch(c, "f32_to_bf16", f32_to_bf16_kernel, dim3(grid_for(n)), dim3(kThreads), 0, x, y, n);
+}
+
+void bf16_to_f32(const LaunchCtx& c, const uint16_t* x, float* y, int64_t n) {
+  if (n <= 0) return;
+  launch(c, "bf16_to_f32", bf16_to_f32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, x, y, n);
+}
 
 void gelu(const LaunchCtx& c, const float* x, float* y, int64_t n, bool clamp10) {
   if (n <= 0) return;

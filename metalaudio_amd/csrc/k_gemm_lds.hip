@@ -135,6 +135,102 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
   }
 }
 
+// The same epilogue with the tile transposed through LDS into row order, for outputs whose rows
+// are 16-byte aligned (N % 4 == 0, ldc % 4 == 0; residual likewise): the accumulators are written
+// to LDS ([rows][BN + 8 floats]: rows four apart, which the two lane groups write together, sit 32
+// banks apart), read back as float4 along rows and stored so that consecutive lanes cover
+// consecutive 16-byte pieces of a row — 512-byte row runs per half-wave for BN = 128 instead of the
+// accumulator layout's 128-byte pieces of 32 rows, which the memory system served at about 2 TB/s.
+// Bias (along N), activation, residual and LayerScale apply in row order. Tiles whose rows do not
+// fit the LDS ring at once go in passes of whole wave rows. The caller has synchronised the
+// workgroup after its last LDS read of the main loop.
+template <int WMW, int WNW, int WM, int WN, int ACT, bool RES, int LDS_FLOATS>
+__device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16 (&acc)[WM][WN],
+                                               int m0, int n0, int wm, int wn, int lane,
+                                               float* smem) {
+  constexpr int BM = WMW * WM * 32, BN = WNW * WN * 32, NT = WMW * WNW * 64;
+  constexpr int PITCH = BN + 8;
+  constexpr int WROWS = WM * 32;  // rows per wave row
+  constexpr int PASS_WM = (BM * PITCH <= LDS_FLOATS) ? WMW : 1;  // wave rows per pass
+  constexpr int PROWS = PASS_WM * WROWS;                          // rows per pass
+  static_assert(PROWS * PITCH <= LDS_FLOATS, "epilogue tile does not fit the LDS ring");
+  constexpr int C4 = BN / 4;                  // float4 per row
+  constexpr int RPI = NT / C4;                // rows per thread iteration
+  constexpr int IT = PROWS / RPI;             // iterations per pass
+  static_assert(NT % C4 == 0 && PROWS % RPI == 0, "epilogue thread layout");
+  const int g = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x;
+  const int bz = blockIdx.z;
+  float* __restrict__ Cp = a.C + (int64_t)bz * a.sC;
+  const float* Rp = RES && a.R ? a.R + (int64_t)bz * a.sR : nullptr;
+  const int c4 = tid % C4, rr0 = tid / C4;
+  const int gn = n0 + 4 * c4;
+  const bool col_ok = gn < a.N;  // N % 4 == 0: a float4 is all in or all out
+  float4 bn = make_float4(0.f, 0.f, 0.f, 0.f), rs = make_float4(1.f, 1.f, 1.f, 1.f);
+  if (col_ok && a.bias_mode == BIAS_N) bn = *reinterpret_cast<const float4*>(a.bias + gn);
+  if (RES && Rp && a.rscale && col_ok) rs = *reinterpret_cast<const float4*>(a.rscale + gn);
+#pragma unroll
+  for (int pass = 0; pass < WMW / PASS_WM; ++pass) {
+    if (pass > 0) __syncthreads();  // the previous pass's reads are done
+    if (wm / PASS_WM == pass) {
+      const int wr0 = (wm % PASS_WM) * WROWS;
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int r = wr0 + 32 * i + 8 * (v / 4) + 4 * g + (v % 4);
+            const int c = wn * WN * 32 + 32 * j + l32;
+            smem[r * PITCH + c] = acc[i][j][v];
+          }
+    }
+    __syncthreads();
+    const int prow0 = m0 + pass * PROWS;
+    // residual rows first (loads before any store), then the stores
+    float4 rv[RES ? IT : 1];
+    if constexpr (RES) {
+#pragma unroll
+      for (int it = 0; it < IT; ++it) {
+        const int gm = min(prow0 + rr0 + it * RPI, a.M - 1);
+        rv[it] = (Rp && col_ok) ? *reinterpret_cast<const float4*>(Rp + (int64_t)gm * a.ldr + gn)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      wait_vmcnt<0>();
+    }
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      const int r = rr0 + it * RPI;
+      const int gm = prow0 + r;
+      float4 v = *reinterpret_cast<const float4*>(smem + r * PITCH + 4 * c4);
+      v.x += bn.x;
+      v.y += bn.y;
+      v.z += bn.z;
+      v.w += bn.w;
+      if (ACT < 0) {
+        v.x = apply_act(v.x, a.act, a.act_alpha);
+        v.y = apply_act(v.y, a.act, a.act_alpha);
+        v.z = apply_act(v.z, a.act, a.act_alpha);
+        v.w = apply_act(v.w, a.act, a.act_alpha);
+      } else if (ACT > 0) {
+        v.x = apply_act(v.x, ACT);
+        v.y = apply_act(v.y, ACT);
+        v.z = apply_act(v.z, ACT);
+        v.w = apply_act(v.w, ACT);
+      }
+      if constexpr (RES) {
+        if (Rp) {
+          v.x = rv[it].x + rs.x * v.x;
+          v.y = rv[it].y + rs.y * v.y;
+          v.z = rv[it].z + rs.z * v.z;
+          v.w = rv[it].w + rs.w * v.w;
+        }
+      }
+      if (col_ok && gm < a.M) *reinterpret_cast<float4*>(Cp + (int64_t)gm * a.ldc + gn) = v;
+    }
+  }
+}
+
 // GLU epilogue: rows come in 32-row blocks [a0..a15 | b0..b15] (weights regrouped by the caller);
 // output row 16*blk + r = (a_r + bias) * sigmoid(b_r + bias). In the accumulator layout register v
 // (< 8) holds row rr = 8*(v/4) + 4*(l/32) + v%4 < 16 and register v + 8 holds row rr + 16, so every
@@ -238,11 +334,21 @@ __device__ __forceinline__ void store_part(const GemmArgs& a, const floatx16 (&a
 // EPI: 0 bias / activation / residual (store_tile), 1 GLU (store_glu: only the encoder's rewrite
 // GEMMs use it), 2 transposed-conv scatter (store_ct), 3 K-split partials (store_part); each a
 // separate instantiation.
-template <int WMW, int WNW, int WM, int WN, int S, int EPI>
-__global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs a) {
+//
+// BF: A and B hold bf16 values (lda / ldb / sA / sB count bf16 elements). A stage is still 128
+// bytes per row — 64 k — with the same swizzle; a lane's 16-byte fragment read is then 8
+// consecutive k, exactly the operand of one v_mfma_f32_32x32x16_bf16 (lane group g supplies k
+// slots 8g..8g+7), so chunk c = 4g + q4 of a stage feeds MFMA step q4 for A and B alike.
+// The second launch bound asks for two workgroups per CU where two rings fit the 160 KB of LDS.
+template <int WMW, int WNW, int WM, int WN, int S, int EPI, bool BF = false>
+__global__ __launch_bounds__(WMW* WNW * 64,
+                             (2 * S * (WMW * WM + WNW * WN) * 32 * BK * 4 <= 160 * 1024) ? 2 : 1)
+void gemm_nk_lds_kernel(GemmArgs a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, A_INS = Cfg::A_INS, B_INS = Cfg::B_INS;
   constexpr int STAGE = Cfg::STAGE;
+  constexpr int ES = BF ? 2 : 4;           // operand element bytes
+  constexpr int BKE = BF ? 2 * BK : BK;    // k per 128-byte stage row
   __shared__ __attribute__((aligned(1024))) float smem[S * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -258,9 +364,9 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   const int tn = logical % gx, tm = logical / gx;
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = a.M, N = a.N, K = a.K;
-  const int nk = K / BK / ks, kt0 = (int)(blockIdx.z % ks) * nk;  // this workgroup's stages
-  const float* __restrict__ A = a.A + (int64_t)bz * a.sA;
-  const float* __restrict__ B = a.B + (int64_t)bz * a.sB;
+  const int nk = K / BKE / ks, kt0 = (int)(blockIdx.z % ks) * nk;  // this workgroup's stages
+  const char* __restrict__ A = reinterpret_cast<const char*>(a.A) + (int64_t)bz * a.sA * ES;
+  const char* __restrict__ B = reinterpret_cast<const char*>(a.B) + (int64_t)bz * a.sB * ES;
 
   // Per-lane byte offsets of this wave's stage loads from the operand base (rows past M / N are
   // clamped to the last row: they are read but their products are never stored). The base moves
@@ -271,19 +377,19 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   for (int i = 0; i < A_INS; ++i) {
     const int rr = (wave * A_INS + i) * 8 + lr;
     const int gm = min(m0 + rr, M - 1);
-    aoffg[i] = 4u * (unsigned)(gm * a.lda + 4 * (ls ^ chunk_swizzle(rr)));
+    aoffg[i] = (unsigned)(ES * gm * a.lda + 16 * (ls ^ chunk_swizzle(rr)));
   }
 #pragma unroll
   for (int i = 0; i < B_INS; ++i) {
     const int rr = (wave * B_INS + i) * 8 + lr;
     const int gn = min(n0 + rr, N - 1);
-    boffg[i] = 4u * (unsigned)(gn * a.ldb + 4 * (ls ^ chunk_swizzle(rr)));
+    boffg[i] = (unsigned)(ES * gn * a.ldb + 16 * (ls ^ chunk_swizzle(rr)));
   }
   const unsigned lds0 = lds_address(smem);
   auto issue = [&](int kt, int slot) {
     const unsigned base = lds0 + 4u * (unsigned)(slot * STAGE);
-    const float* ak = A + (kt0 + kt) * BK;
-    const float* bk = B + (kt0 + kt) * BK;
+    const float* ak = reinterpret_cast<const float*>(A + (int64_t)(kt0 + kt) * BKE * ES);
+    const float* bk = reinterpret_cast<const float*>(B + (int64_t)(kt0 + kt) * BKE * ES);
 #pragma unroll
     for (int i = 0; i < A_INS; ++i)
       lds_dma16_s(ak, aoffg[i],
@@ -344,14 +450,24 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
     }
   };
   auto mfma_slice = [&](const float4 (&xa)[4][WM], const float4 (&xb)[4][WN], int q4) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
+    if constexpr (BF) {
 #pragma unroll
       for (int i = 0; i < WM; ++i)
 #pragma unroll
         for (int j = 0; j < WN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q4][i][s], xb[q4][j][s], acc[i][j],
-                                                           0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              __builtin_bit_cast(bf16x8, xa[q4][i]), __builtin_bit_cast(bf16x8, xb[q4][j]),
+              acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+          for (int j = 0; j < WN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[q4][i][s], xb[q4][j][s],
+                                                             acc[i][j], 0, 0, 0);
+    }
   };
   // stage 0: at most the S-1 newer stages may still be in flight
   if (S - 1 < nk) wait_vmcnt<(S - 1) * Cfg::L>();
@@ -379,12 +495,23 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
         // fragment reads alternate with the first MFMAs of the second half, so the last read has
         // the remaining MFMAs to complete before the next stage needs it
         constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
+        if constexpr (BF) {
+          // bf16: one MFMA per fragment pair and k step, 2 * WM * WN in the second half; the
+          // reads are spread over them
+          constexpr int kM = 2 * WM * WN, kR = (kReads + kM - 1) / kM;
 #pragma unroll
-        for (int r = 0; r < kReads; ++r) {
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          for (int r = 0; r < kM; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x100, kR, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          }
+        } else {
+#pragma unroll
+          for (int r = 0; r < kReads; ++r) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          }
+          __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, kMfma, 0);
       }
     }
   }
@@ -406,6 +533,27 @@ __global__ __launch_bounds__(WMW* WNW * 64, 2) void gemm_nk_lds_kernel(GemmArgs 
   // The activation and residual form are uniform: one specialised copy of the store loop each
   // for the forms the transformer uses, a generic one for the rest.
   const bool res = a.R != nullptr, bm = a.bias_mode == BIAS_M;
+  // row-ordered stores through LDS where rows are 16-byte aligned (see store_tile_lds)
+  const bool rows16 = (a.N % 4 == 0) && (a.ldc % 4 == 0) && (a.sC % 4 == 0) &&
+                      ((reinterpret_cast<uintptr_t>(a.C) & 15) == 0) &&
+                      (!res || ((a.ldr % 4 == 0) && (a.sR % 4 == 0) &&
+                                (reinterpret_cast<uintptr_t>(a.R) & 15) == 0)) &&
+                      (a.bias_mode != BIAS_N || (reinterpret_cast<uintptr_t>(a.bias) & 15) == 0) &&
+                      (!a.rscale || (reinterpret_cast<uintptr_t>(a.rscale) & 15) == 0);
+  if constexpr (EPI == 0) {
+    if (rows16 && !bm) {
+      __syncthreads();  // every wave's last fragment reads of the LDS ring are done
+      if (a.act == 0 && !res)
+        store_tile_lds<WMW, WNW, WM, WN, 0, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+      else if (a.act == 0)
+        store_tile_lds<WMW, WNW, WM, WN, 0, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+      else if (a.act == 3 && !res)
+        store_tile_lds<WMW, WNW, WM, WN, 3, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+      else
+        store_tile_lds<WMW, WNW, WM, WN, -1, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+      return;
+    }
+  }
   if constexpr (EPI == 1) store_glu<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if constexpr (EPI == 2) store_ct<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
   else if constexpr (EPI == 3) store_part<WMW, WNW, WM, WN>(a, acc, m0, n0, wm, wn, lane);
@@ -460,21 +608,37 @@ const LdsTile& choose_lds_tile(const GemmArgs& a) {
   return *best;
 }
 
-template <int WMW, int WNW, int WM, int WN, int S>
+template <int WMW, int WNW, int WM, int WN, int S, bool BF = false>
 void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
   using Cfg = LdsCfg<WMW, WNW, WM, WN, S>;
   dim3 grid(cdiv(a.N, Cfg::BN), cdiv(a.M, Cfg::BM), a.batch * a.ksplit), block(Cfg::NT);
-  const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
-  if (a.ksplit > 1) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 3>, grid, block, 0, a);
-  else if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
-  else if (a.ct_stride > 0)
-    launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 2>, grid, block, 0, a);
-  else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0>, grid, block, 0, a);
+  if constexpr (BF) {  // bf16 operands: bias / activation / residual epilogue only
+    launch(c, a.name ? a.name : "gemm_bf16_mfma_nk",
+           gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0, true>, grid, block, 0, a);
+  } else {
+    const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
+    if (a.ksplit > 1)
+      launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 3>, grid, block, 0, a);
+    else if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
+    else if (a.ct_stride > 0)
+      launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 2>, grid, block, 0, a);
+    else launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0>, grid, block, 0, a);
+  }
 }
 
 }  // namespace
 
 bool gemm_nk_lds_supported(const GemmArgs& a) {
+  if (a.ab_bf16) {
+    // bf16 operands: 64 k per stage, rows 16-byte aligned (8 elements), plain epilogue
+    const bool off32 = ((int64_t)(a.M - 1) * a.lda + a.K) * 2 < ((int64_t)1 << 32) &&
+                       ((int64_t)(a.N - 1) * a.ldb + a.K) * 2 < ((int64_t)1 << 32);
+    return off32 && a.blayout == B_NK && a.precision == MNN_PRECISION_BF16 &&
+           a.K % (2 * BK) == 0 && a.lda % 8 == 0 && a.ldb % 8 == 0 && a.sA % 8 == 0 &&
+           a.sB % 8 == 0 && aligned16(a.A) && aligned16(a.B) && a.stats == nullptr &&
+           a.pro_coef == nullptr && a.pro_stats == nullptr && !a.glu && a.ct_stride == 0 &&
+           a.ksplit == 1 && a.bias_mode != BIAS_M;
+  }
   // per-lane load offsets are 32-bit byte offsets from the operand (batch) base
   const bool off32 = ((int64_t)(a.M - 1) * a.lda + a.K) * 4 < ((int64_t)1 << 32) &&
                      ((int64_t)(a.N - 1) * a.ldb + a.K) * 4 < ((int64_t)1 << 32);
@@ -490,6 +654,15 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {
   MNN_REQUIRE(gemm_nk_lds_supported(a), MNN_ERR_INVALID_ARGUMENT,
               "gemm_nk_lds: operands outside the LDS-DMA path's contract");
+  if (a.ab_bf16) {
+    // bf16: a stage holds 64 k, so its matrix work is an eighth of the fp32 kernel's while its
+    // loads are as large: four-stage rings keep more load latency in flight. 128x128 tiles where
+    // they fill the CUs, 64x64 tiles for grids of fewer than 256 of them.
+    const int f = forced_lds_tile();
+    const int64_t big = (int64_t)cdiv(a.M, 128) * cdiv(a.N, 128) * a.batch;
+    if (f == 3 || (f < 0 && big < 256)) return launch_lds<2, 2, 1, 1, 4, true>(c, a);
+    return launch_lds<2, 2, 2, 2, 4, true>(c, a);
+  }
   switch (choose_lds_tile(a).id) {
     case 0: return launch_lds<2, 2, 2, 2, 2>(c, a);
     case 1: return launch_lds<2, 2, 2, 1, 3>(c, a);

@@ -327,6 +327,76 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
   }
 }
 
+// LayerNorm with LPR lanes per row (LPR = 16 or 32: 64 / LPR rows per wave), NV float4 per lane,
+// F % 4 == 0, F <= 4 * LPR * NV. For F = 384 (96 float4) 32 lanes x 3 float4 keep every lane
+// busy where one row per wave would leave a quarter of the lanes idle, and a wave has two rows'
+// loads in flight. Reductions are xor shuffles within the row's lane group.
+template <int LPR, int NV>
+__global__ __launch_bounds__(kThreads) void layernorm_group_kernel(const float* __restrict__ x,
+                                                                   float* __restrict__ y,
+                                                                   int64_t rows, int F,
+                                                                   const float* __restrict__ gamma,
+                                                                   const float* __restrict__ beta,
+                                                                   float eps) {
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int lane = threadIdx.x & 63, sub = lane % LPR;
+  const int64_t row = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * RPW +
+                      lane / LPR;
+  const bool live = row < rows;
+  const int F4 = F >> 2;
+  const int64_t r = live ? row : rows - 1;  // dead groups compute on a valid row, store nothing
+  const float4* xr = reinterpret_cast<const float4*>(x + r * F);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  float4 v[NV], gv[NV], bv[NV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = sub + LPR * i;
+    if (idx < F4) {
+      v[i] = xr[idx];
+      gv[i] = g4[idx];
+      bv[i] = b4[idx];
+      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    } else {
+      v[i] = gv[i] = bv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
+  const float mean = s / (float)F;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = sub + LPR * i;
+    if (idx < F4) {
+      float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+  }
+#pragma unroll
+  for (int off = LPR / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, kWave);
+  const float var = q / (float)F;
+  const float rstd = 1.f / sqrtf(var + eps);
+  float4* yr = reinterpret_cast<float4*>(y + r * F);
+  wait_vmcnt<0>();  // every load has landed: the stores below need no waits between them
+  if (live) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = sub + LPR * i;
+      if (idx < F4) {
+        const float4 g = gv[i], bb = bv[i];
+        float4 o;
+        o.x = g.x * ((v[i].x - mean) * rstd) + bb.x;
+        o.y = g.y * ((v[i].y - mean) * rstd) + bb.y;
+        o.z = g.z * ((v[i].z - mean) * rstd) + bb.z;
+        o.w = g.w * ((v[i].w - mean) * rstd) + bb.w;
+        yr[idx] = o;
+      }
+    }
+  }
+}
+
 // LayerNorm, any F: three passes over the row from memory, one wave per row.
 __global__ __launch_bounds__(kThreads) void layernorm_generic_kernel(
     const float* __restrict__ x, float* __restrict__ y, int64_t rows, int F,
@@ -421,6 +491,17 @@ void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F
   const bool vec = (F % 4 == 0) && aligned16(x) && aligned16(y) && aligned16(gamma) &&
                    aligned16(beta);
   const int nv = (F + 255) / 256;
+  // rows of at most 128 float4 with 32 lanes each busy on every load: two rows per wave
+  if (vec && F % 128 == 0 && F <= 512) {
+    const int nv32 = F / 128;  // float4 per lane with 32 lanes per row
+    dim3 g2(cdiv(rows, 2 * (kThreads / 64)));
+    switch (nv32) {
+      case 1: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 1>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
+      case 2: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 2>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
+      case 3: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 3>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
+      default: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 4>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
+    }
+  }
   if (vec && nv <= 8) {
     switch (nv) {
       case 1: return launch(c, "layernorm_f32", layernorm_reg_kernel<1>, grid, block, 0, x, y, rows, F, gamma, beta, eps);

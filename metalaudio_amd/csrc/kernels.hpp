@@ -15,6 +15,9 @@ void activation(const LaunchCtx& c, const float* x, float* y, int64_t n, int act
 // GLU: per batch b, y[b][i] = x[b][i] * sigmoid(x[b][i + half]) for i < half (NN.metal:1012-1023).
 void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t half);
 void copy_bytes(const LaunchCtx& c, const void* src, void* dst, int64_t bytes);
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet), and bf16 -> fp32 (exact).
+void f32_to_bf16(const LaunchCtx& c, const float* x, uint16_t* y, int64_t n);
+void bf16_to_f32(const LaunchCtx& c, const uint16_t* x, float* y, int64_t n);
 
 // ------------------------------------------------------------------ norms (k_norm.hip)
 // GroupNorm statistics in three steps. x is [B][C][L]; group g covers channels [g*C/G, (g+1)*C/G).
@@ -133,6 +136,9 @@ struct GemmArgs {
   const float* rc_w = nullptr;
   const float* rc_b = nullptr;
   mnn_precision precision = MNN_PRECISION_F32;
+  // A and B hold bf16 values (RNE-rounded by their producer), lda / ldb / sA / sB in elements:
+  // the LDS-DMA kernel's bf16 instantiation (precision BF16, B_NK, K % 64 == 0).
+  bool ab_bf16 = false;
   const char* name = nullptr;  // kernel-timing name of the launch (default: by kernel family)
 };
 // Number of output tiles per batch for the tile configuration the launcher will pick.

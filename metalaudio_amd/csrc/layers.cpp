@@ -442,6 +442,10 @@ class LinearLayer : public Layer {
                 "FusedLinear: leakyReluAlpha must be finite");
     w_ = &add_param("weight", (int64_t)in * out);
     if (bias) b_ = &add_param("bias", out);
+    if (prec == MNN_PRECISION_BF16) {  // zero weights until loaded, as the f32 parameter
+      std::vector<float> z((size_t)in * out, 0.f);
+      on_loaded("weight", z.data(), z.size());
+    }
   }
   const char* kind() const override { return "Linear"; }
   Shape input_shape() const override { return {in_}; }
@@ -451,9 +455,50 @@ class LinearLayer : public Layer {
                 "Linear: expected last dimension " << in_ << ", got " << shape_str(in));
     return with_last(in, out_);
   }
+  bool accepts_bf16() const override { return true; }
+  // Input f32 or bf16 (HalfLinear's half-precision input, HalfPrecisionLinear.swift:60-212).
+  // Precision BF16 with in_features % 64 == 0 runs the LDS-DMA GEMM on bf16 operands (an f32
+  // input is rounded to bf16 first, the weights were rounded when loaded); a bf16 input under
+  // precision F32 is widened to f32 (exact).
   void forward(const Tensor& in, Tensor& out, Stream& s) override {
     check_out(out, infer_output(in.shape));
-    run(in.f32(), in.count() / in_, out.f32(), act_, nullptr, nullptr, s);
+    const int64_t rows = in.count() / in_;
+    const bool lds16 = prec_ == MNN_PRECISION_BF16 && in_ % 64 == 0;
+    if (in.dtype == MNN_BF16) {
+      if (lds16) return run_bf16(static_cast<const uint16_t*>(in.data), rows, out.f32(), s);
+      x32_.reserve(sizeof(float) * rows * in_);
+      k::bf16_to_f32(ctx(s), static_cast<const uint16_t*>(in.data), x32_.f32(), rows * in_);
+      return run(x32_.f32(), rows, out.f32(), act_, nullptr, nullptr, s);
+    }
+    if (lds16) {
+      x16_.reserve(sizeof(uint16_t) * rows * in_);
+      k::f32_to_bf16(ctx(s), in.f32(), static_cast<uint16_t*>(x16_.ptr), rows * in_);
+      return run_bf16(static_cast<const uint16_t*>(x16_.ptr), rows, out.f32(), s);
+    }
+    run(in.f32(), rows, out.f32(), act_, nullptr, nullptr, s);
+  }
+  // bf16 operands on the LDS-DMA kernel: x [rows][in] bf16, the weights' bf16 copy.
+  void run_bf16(const uint16_t* x, int64_t rows, float* y, Stream& s) {
+    k::GemmArgs g;
+    g.M = (int)rows;
+    g.N = out_;
+    g.K = in_;
+    g.A = reinterpret_cast<const float*>(x);
+    g.lda = in_;
+    g.B = reinterpret_cast<const float*>(w16_.ptr);
+    g.ldb = in_;
+    g.blayout = k::B_NK;
+    g.C = y;
+    g.ldc = out_;
+    g.bias = b_ ? b_->ptr() : nullptr;
+    g.bias_mode = b_ ? k::BIAS_N : k::BIAS_NONE;
+    g.act = act_;
+    g.act_alpha = alpha_;
+    g.precision = MNN_PRECISION_BF16;
+    g.ab_bf16 = true;
+    MNN_REQUIRE(k::gemm_nk_lds_supported(g), MNN_ERR_INVALID_CONFIGURATION,
+                "Linear: bf16 operands outside the matrix-core kernel's contract");
+    k::gemm_nk_lds(ctx(s), g);
   }
   // y = R + rscale * act(x W^T + b) when R is given (R may alias y).
   void run(const float* x, int64_t rows, float* y, int act, const float* R, const float* rscale,
@@ -482,10 +527,28 @@ class LinearLayer : public Layer {
   int in_features() const { return in_; }
   int out_features() const { return out_; }
 
+ protected:
+  // precision BF16: keep a bf16 (round to nearest even) copy of the weights for the bf16 kernel
+  void on_loaded(const std::string& name, const float* data, size_t n) override {
+    if (prec_ != MNN_PRECISION_BF16 || name != "weight") return;
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = bf16_bits_rne(data[i]);
+    w16_.reserve(sizeof(uint16_t) * n);
+    HIP_CHECK(hipMemcpy(w16_.ptr, h.data(), n * sizeof(uint16_t), hipMemcpyHostToDevice));
+  }
+
  private:
+  static uint16_t bf16_bits_rne(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // quiet NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
   int in_, out_, act_;
   mnn_precision prec_;
   float alpha_ = 0.01f;
+  DevBuf w16_, x16_, x32_;
   Param* w_ = nullptr;
   Param* b_ = nullptr;
 };

@@ -30,6 +30,8 @@ class Layer {
   virtual void forward(const Tensor& in, Tensor& out, Stream& s) = 0;
   virtual void forward_cross(const Tensor* a, const Tensor* b, Tensor* out_a, Tensor* out_b,
                              Stream& s);
+  // Whether forward() takes an MNN_BF16 input tensor (otherwise inputs must be f32).
+  virtual bool accepts_bf16() const { return false; }
   // Loads a parameter by name; the default looks the name up in params_ (and aliases_).
   virtual void load(const std::string& name, const float* data, size_t n);
   Device* device() const { return dev_; }

@@ -102,23 +102,37 @@ def _sh(stream: Optional[Stream]):
     return stream.handle if stream is not None else None
 
 
-class Tensor:
-    """Device tensor, contiguous row-major fp32, zero-initialised (Tensor.swift:59-141)."""
+def bf16_bits(a) -> np.ndarray:
+    """fp32 -> bf16 bit patterns (uint16), round to nearest even, NaN kept quiet."""
+    u = _f32(a).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
 
-    def __init__(self, device: AudioDevice, shape: Sequence[int], _handle=None, _owned=True):
+
+class Tensor:
+    """Device tensor, contiguous row-major, zero-initialised (Tensor.swift:59-141); fp32 or bf16
+    (dtype "bf16": 16-bit values, host data rounded to nearest even on upload, widened to fp32
+    on download)."""
+
+    def __init__(self, device: AudioDevice, shape: Sequence[int], _handle=None, _owned=True,
+                 dtype: str = "f32"):
         self.device = device
+        self.dtype = dtype
         if _handle is None:
             h = C.c_void_p()
             shape = [int(s) for s in shape]
-            check(lib().mnn_tensor_create(device.handle, 0, len(shape), dims(shape), C.byref(h)))
+            check(lib().mnn_tensor_create(device.handle, {"f32": 0, "bf16": 1}[dtype],
+                                          len(shape), dims(shape), C.byref(h)))
             _handle = h
         self.handle = _handle
         self._owned = _owned
 
     @classmethod
-    def from_numpy(cls, device: AudioDevice, arr, stream: Optional[Stream] = None) -> "Tensor":
+    def from_numpy(cls, device: AudioDevice, arr, stream: Optional[Stream] = None,
+                   dtype: str = "f32") -> "Tensor":
         a = _f32(arr)
-        t = cls(device, a.shape)
+        t = cls(device, a.shape, dtype=dtype)
         t.copy_from(a, stream)
         return t
 
@@ -139,10 +153,17 @@ class Tensor:
     def copy_from(self, arr, stream: Optional[Stream] = None) -> None:
         """Tensor.copy(from:) — synchronous upload."""
         a = _f32(arr)
+        if self.dtype == "bf16":
+            a = np.ascontiguousarray(bf16_bits(a))
         check(lib().mnn_tensor_upload(self.handle, a.ctypes.data, a.nbytes, _sh(stream)))
 
     def to_numpy(self, stream: Optional[Stream] = None) -> np.ndarray:
-        """toArray() — synchronous download, shaped like the tensor."""
+        """toArray() — synchronous download, shaped like the tensor (fp32)."""
+        if self.dtype == "bf16":
+            raw = np.empty(self.shape, dtype=np.uint16)
+            check(lib().mnn_tensor_download(self.handle, raw.ctypes.data, raw.nbytes,
+                                            _sh(stream)))
+            return (raw.astype(np.uint32) << 16).view(np.float32)
         out = np.empty(self.shape, dtype=np.float32)
         check(lib().mnn_tensor_download(self.handle, out.ctypes.data, out.nbytes, _sh(stream)))
         return out

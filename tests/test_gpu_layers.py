@@ -155,7 +155,8 @@ def test_groupnorm_parity(dev, stream, B, C, L, G, act):
     assert_close(got, ref, ATOL, RTOL, "groupnorm")
 
 
-@pytest.mark.parametrize("rows,F", [(4, 4), (1000, 384), (333, 512), (2048, 2048), (17, 100)])
+@pytest.mark.parametrize("rows,F", [(4, 4), (1000, 384), (333, 512), (2048, 2048), (17, 100),
+                                    (3, 384), (257, 128), (10752, 384)])
 def test_layernorm_parity(dev, stream, rows, F):
     say(f"layernorm {rows}x{F}")
     x = (RNG.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
@@ -230,21 +231,60 @@ def test_linear_closed_forms(dev, stream):
 BF16_RTOL = 2e-2
 
 
-@pytest.mark.parametrize("shape,nin,nout", [((2048, 512), 512, 2048), ((300, 384), 384, 1152)])
-def test_linear_bf16_parity(dev, stream, shape, nin, nout):
+# Per element, against the fp32 oracle: rounding x and w to bf16 (unit roundoff 2^-8) moves each
+# product by at most (2^-7 + 2^-16) |x| |w|, so |gpu - ref|_ij <= 2^-7 (1.01) (|x| |w|^T)_ij plus the
+# fp32 accumulation (covered by the 1e-5 term): a per-element bound on every output.
+def assert_bf16_elementwise(got, x, w, ref, what):
+    bound = 2.0 ** -7 * 1.01 * oracle.linear(np.abs(x), np.abs(w)) + 1e-5
+    err = np.abs(np.asarray(got, np.float64) - ref)
+    assert np.all(err <= bound), f"{what}: max err / bound {float((err / bound).max()):.3f}"
+
+
+@pytest.mark.parametrize("shape,nin,nout,act,in_dtype", [
+    ((2048, 512), 512, 2048, "none", "f32"),     # config 2 shape, fp32 input rounded on device
+    ((2048, 512), 512, 2048, "none", "bf16"),    # config 2 with a bf16 input tensor
+    ((300, 384), 384, 1152, "gelu", "f32"),      # ragged rows, activation epilogue
+    ((7, 33, 128), 128, 96, "relu", "bf16"),     # batch dims, N not a tile multiple
+    ((300, 96), 96, 64, "none", "f32"),          # K % 64 != 0: the register-staged kernel
+    ((50, 96), 96, 64, "none", "bf16"),          # K % 64 != 0 with a bf16 input (widened)
+])
+def test_linear_bf16_parity(dev, stream, shape, nin, nout, act, in_dtype):
     from tests.conftest import assert_rel_norm
-    say(f"linear bf16 {shape} {nin}->{nout}")
+    say(f"linear bf16 {shape} {nin}->{nout} {act} input {in_dtype}")
     x = RNG.standard_normal(shape).astype(np.float32)
     w = (RNG.standard_normal((nout, nin)) * 0.02).astype(np.float32)
     b = (RNG.standard_normal(nout) * 0.1).astype(np.float32)
-    layer = nn.Linear(dev, nin, nout, precision="bf16")
+    layer = nn.Linear(dev, nin, nout, activation=act, precision="bf16")
     layer.load_weights(w, b)
-    got = run_layer(layer, x, dev, stream)
-    ref_rounded = oracle.linear(oracle.round_bf16(x), oracle.round_bf16(w), b)
+    xt = nn.Tensor.from_numpy(dev, x, dtype=in_dtype)
+    out = layer(xt, stream)
+    stream.sync(60000)
+    got = out.to_numpy()
+    xr, wr = oracle.round_bf16(x), oracle.round_bf16(w)
+    ref_rounded = oracle.linear(xr, wr, b, act=act)
     assert_close(got, ref_rounded, ATOL, RTOL, "linear bf16 vs rounded-operand oracle")
-    assert_rel_norm(got, oracle.linear(x, w, b), BF16_RTOL, "linear bf16 vs fp32 oracle")
+    ref = oracle.linear(x, w, b, act=act)
+    assert_rel_norm(got, ref, BF16_RTOL, "linear bf16 vs fp32 oracle")
+    if act == "none":
+        assert_bf16_elementwise(got - b, x, w, ref - b, "linear bf16 per element")
     # and it is not silently fp32
-    assert np.abs(got - oracle.linear(x, w, b)).max() > 1e-6
+    assert np.abs(got - ref).max() > 1e-6
+
+
+def test_linear_bf16_input_tensor_f32_precision(dev, stream):
+    """A bf16 input tensor into an fp32 Linear is widened exactly: the result is the fp32 GEMM of
+    the rounded input."""
+    say("linear f32 with a bf16 input tensor")
+    x = RNG.standard_normal((64, 96)).astype(np.float32)
+    w = (RNG.standard_normal((32, 96)) * 0.05).astype(np.float32)
+    layer = nn.Linear(dev, 96, 32, use_bias=False)
+    layer.load_weights(w)
+    out = layer(nn.Tensor.from_numpy(dev, x, dtype="bf16"), stream)
+    stream.sync(60000)
+    assert_close(out.to_numpy(), oracle.linear(oracle.round_bf16(x), w), ATOL, RTOL,
+                 "bf16 input, fp32 GEMM")
+    with pytest.raises(nn.MNNError):  # other layers take f32 inputs only
+        nn.LayerNorm(dev, 96)(nn.Tensor.from_numpy(dev, x, dtype="bf16"), stream)
 
 
 def test_encoder_block_bf16_parity(dev, stream):
