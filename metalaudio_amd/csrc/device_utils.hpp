@@ -60,6 +60,138 @@ __device__ __forceinline__ float apply_act(float x, int act, float alpha = 0.01f
   }
 }
 
+// Every lane of the calling wave receives the merge of np >= 1 (count, mean, M2) partials, in
+// fp64: n = sum n_j, mean = sum n_j mean_j / n, M2 = sum (M2_j + n_j (mean_j - mean)^2). Lane l
+// takes partials l, l + 64, ...; the wave sums are xor butterflies, so every lane (and every wave
+// and workgroup that merges the same partials) gets the identical value. Plain sums instead of
+// Chan's pairwise merges leave no division inside the reduction, and the first 512 partials are
+// loaded together (PartsBatch below).
+__device__ __forceinline__ double wave_sum_xor_d(double v) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// The first 64 * KB partials of a wave_merge_parts call, loaded by straight-line code (clamped
+// addresses, no branch or loop) so that a kernel can put them in flight together with its other
+// loads; merge() finishes from registers, re-reading only partials beyond the first batch.
+template <int KB>
+struct PartsBatch {
+  float pn[KB], pm[KB], pq[KB];
+  __device__ __forceinline__ void load(const float* __restrict__ p, int np) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      const int jc = max(min(lane + 64 * k, np - 1), 0);
+      pn[k] = p[3 * jc];
+      pm[k] = p[3 * jc + 1];
+      pq[k] = p[3 * jc + 2];
+    }
+  }
+  __device__ __forceinline__ void merge(const float* __restrict__ p, int np, double& n,
+                                        double& mean, double& m2) {
+    const int lane = threadIdx.x & 63;
+    // sum n_j, sum n_j mean_j, sum n_j mean_j^2, sum M2_j: four independent wave sums
+    double sn = 0.0, sm = 0.0, sm2 = 0.0, sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < KB; ++k) {
+      if (lane + 64 * k < np) {
+        const double c = pn[k], m = pm[k];
+        sn += c;
+        sm += c * m;
+        sm2 += c * m * m;
+        sq += (double)pq[k];
+      }
+    }
+    for (int j = lane + 64 * KB; j < np; j += 64) {  // beyond the first batch
+      const double c = p[3 * j], m = p[3 * j + 1];
+      sn += c;
+      sm += c * m;
+      sm2 += c * m * m;
+      sq += (double)p[3 * j + 2];
+    }
+    n = wave_sum_xor_d(sn);
+    sm = wave_sum_xor_d(sm);
+    sm2 = wave_sum_xor_d(sm2);
+    sq = wave_sum_xor_d(sq);
+    mean = n > 0.0 ? sm / n : 0.0;
+    // M2 = sum M2_j + sum n_j (mean_j - mean)^2 = sum M2_j + sum n_j mean_j^2 - n mean^2; in fp64
+    // the cancellation costs about mean^2 / var * 1e-16 relative, negligible below |mean| / std ~ 1e5
+    m2 = n > 0.0 ? fmax(sq + (sm2 - sm * mean), 0.0) : 0.0;
+  }
+};
+
+// Workgroup-wide merge of np partials (the formula of PartsBatch::merge): thread i of the
+// workgroup loads partials i, i + blockDim, ... (PER of them, straight-line), so each partial is
+// read once per workgroup; the four sums are reduced per wave, written to `sh` (4 doubles per wave)
+// and, after the caller's next __syncthreads, finish() combines the waves in order, giving every
+// thread the identical result.
+template <int PER>
+struct BlockParts {
+  float pn[PER], pm[PER], pq[PER];
+  __device__ __forceinline__ void load(const float* __restrict__ p, int np) {
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      const int jc = max(min((int)threadIdx.x + (int)blockDim.x * k, np - 1), 0);
+      pn[k] = p[3 * jc];
+      pm[k] = p[3 * jc + 1];
+      pq[k] = p[3 * jc + 2];
+    }
+  }
+  // per-wave sums into sh[wave * 4 + 0..3]; partials beyond PER * blockDim are read here
+  __device__ __forceinline__ void reduce_waves(const float* __restrict__ p, int np, double* sh) {
+    double sn = 0.0, sm = 0.0, sm2 = 0.0, sq = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      if ((int)threadIdx.x + (int)blockDim.x * k < np) {
+        const double c = pn[k], m = pm[k];
+        sn += c;
+        sm += c * m;
+        sm2 += c * m * m;
+        sq += (double)pq[k];
+      }
+    }
+    for (int j = threadIdx.x + blockDim.x * PER; j < np; j += blockDim.x) {
+      const double c = p[3 * j], m = p[3 * j + 1];
+      sn += c;
+      sm += c * m;
+      sm2 += c * m * m;
+      sq += (double)p[3 * j + 2];
+    }
+    sn = wave_sum_xor_d(sn);
+    sm = wave_sum_xor_d(sm);
+    sm2 = wave_sum_xor_d(sm2);
+    sq = wave_sum_xor_d(sq);
+    if ((threadIdx.x & 63) == 0) {
+      double* o = sh + 4 * (threadIdx.x >> 6);
+      o[0] = sn;
+      o[1] = sm;
+      o[2] = sm2;
+      o[3] = sq;
+    }
+  }
+  static __device__ __forceinline__ void finish(const double* sh, double& n, double& mean,
+                                                double& m2) {
+    double sn = 0.0, sm = 0.0, sm2 = 0.0, sq = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) {
+      sn += sh[4 * w];
+      sm += sh[4 * w + 1];
+      sm2 += sh[4 * w + 2];
+      sq += sh[4 * w + 3];
+    }
+    n = sn;
+    mean = n > 0.0 ? sm / n : 0.0;
+    m2 = n > 0.0 ? fmax(sq + (sm2 - sm * mean), 0.0) : 0.0;
+  }
+};
+
+__device__ __forceinline__ void wave_merge_parts(const float* __restrict__ p, int np, double& n,
+                                                 double& mean, double& m2) {
+  PartsBatch<8> pb;
+  pb.load(p, np);
+  pb.merge(p, np, n, mean, m2);
+}
+
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

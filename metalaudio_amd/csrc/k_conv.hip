@@ -9,6 +9,8 @@
 //
 // One thread per output position; each thread produces a block of COB output channels so the
 // input window is loaded once per block and every output is written once, coalesced along t.
+#include <type_traits>
+
 #include "device_utils.hpp"
 #include "kernels.hpp"
 
@@ -86,39 +88,20 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_kernel(ConvParams p,
   }
 }
 
-// Small contractions (groups = 1, Cin*K = CK <= 32): each thread loads its whole input window
-// (CK samples) into registers with all loads in flight together, then produces the COB output
-// channels of its workgroup (grid.y spreads the channels, so there are enough waves per SIMD to
-// hide memory latency). Weights are staged in LDS and read as broadcasts.
-template <int CK, int COB, bool REFLECT>
-__global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams p,
-                                                                     const float* __restrict__ x,
-                                                                     const float* __restrict__ w,
-                                                                     const float* __restrict__ bias,
-                                                                     float* __restrict__ y, int act,
-                                                                     float* __restrict__ partials) {
-  __shared__ float red[3 * (kThreads / 64)];
-  // this workgroup's COB output channels, weights transposed to [e][co] so one 16-byte LDS
-  // read serves four output channels
-  __shared__ __attribute__((aligned(16))) float wt[CK * COB];
-  const int b = blockIdx.z;
-  const int cob0 = blockIdx.y * COB;
-  const int t = blockIdx.x * kThreads + threadIdx.x;
-  const bool valid = t < p.Lout;
-  for (int i = threadIdx.x; i < CK * COB; i += kThreads) {
-    const int co = i / CK, e = i - co * CK;
-    wt[e * COB + co] = w[(int64_t)(cob0 + co) * CK + e];
-  }
-  __syncthreads();
-  const float* xb = x + (int64_t)b * p.Cin * p.Lin;
-  float xv[CK];
-  // every window load is issued before any is used: addresses are clamped (zero padding) or
-  // mirrored (reflect) instead of branched around (a load under a branch makes the compiler wait
-  // for it, and for all earlier loads, before the next one); out-of-range taps are zeroed after
+// ---- Conv1D -> GroupNorm(1) [-> activation] in two passes (Sequential's fused chain) ----------
+// The convolution's contraction is tiny (Cin * K <= 32), so the second pass recomputes it from the
+// input (a few hundred KB, resident in L2) instead of reading back a stored pre-norm output: the
+// only HBM stream is the output, written once. Each thread owns one output position and COB
+// channels; weights are staged in LDS transposed to [e][co] and read as 16-byte broadcasts.
+
+template <int CK, bool REFLECT>
+__device__ __forceinline__ void load_window(const ConvParams& p, const float* __restrict__ xb, int t,
+                                            bool valid, float (&xv)[CK]) {
+  // branch-free addresses (clamped or mirrored) so that every load is in flight together
   const int base = min(t, p.Lout - 1) * p.stride - p.pad;
+  int ci = 0, kk = 0;  // tap e = ci * K + kk, stepped without divisions
 #pragma unroll
   for (int e = 0; e < CK; ++e) {
-    const int ci = e / p.K, kk = e - ci * p.K;
     int pos = base + kk * p.dilation;
     float keep = valid ? 1.f : 0.f;
     if constexpr (REFLECT) {
@@ -128,31 +111,128 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams 
       keep = (pos >= 0 && pos < p.Lin) ? keep : 0.f;
       pos = min(max(pos, 0), p.Lin - 1);
     }
-    xv[e] = xb[(int64_t)ci * p.Lin + pos] * keep;  // x is finite: 0 * x = 0
+    xv[e] = xb[(int64_t)ci * p.Lin + pos] * keep;
+    if (++kk == p.K) {
+      kk = 0;
+      ++ci;
+    }
   }
-  ShiftedStats st;
-  {
-    const int co0 = cob0;
-    float acc[COB];
+}
+
+// A workgroup's constants, staged in LDS: weights transposed to [e][co], then NX vectors of COB
+// per-channel values (bias, GroupNorm gamma / beta; a null vector reads as its fill value). The
+// loads are issued into registers first (fetch) and written to LDS later (put), so that the
+// caller can put its own loads in flight between the two and wait once for all of them. Every
+// load reads a valid global address (a null vector reads the weights instead and its value is
+// replaced by the fill), so no load sits under a branch or behind a pointer select.
+template <int CK, int COB, int NX>
+struct ConstStage {
+  static_assert(NX >= 1 && NX <= 3, "one to three per-channel vectors");
+  static constexpr int N = CK * COB + NX * COB;
+  static constexpr int PER = (N + kThreads - 1) / kThreads;
+  float v[PER];
+  __device__ __forceinline__ void fetch(const float* __restrict__ w, int cob0, const float* e0,
+                                        const float* e1, const float* e2, float f0, float f1,
+                                        float f2) {
 #pragma unroll
-    for (int j = 0; j < COB; ++j) acc[j] = bias ? bias[co0 + j] : 0.f;
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kThreads;
+      const int iw = min(i, CK * COB - 1);
+      const int co = iw / CK, e = iw - co * CK;
+      const int q = min(max(i - CK * COB, 0) / COB, NX - 1);
+      const int j = min(max(i - CK * COB, 0) - q * COB, COB - 1);
+      const float* src = q == 0 ? e0 : (q == 1 ? e1 : e2);
+      const float fill = q == 0 ? f0 : (q == 1 ? f1 : f2);
+      const bool wgt = i < CK * COB, have = src != nullptr;
+      const float* addr = wgt || !have ? w + (int64_t)(cob0 + co) * CK + e : src + cob0 + j;
+      const float val = *addr;
+      v[r] = (wgt || have) ? val : fill;
+    }
+  }
+  // LDS image: wt[e * COB + co] for the weights, then the extra vectors in order
+  __device__ __forceinline__ void put(float* lds) const {
 #pragma unroll
-    for (int e = 0; e < CK; ++e)
-#pragma unroll
-      for (int j4 = 0; j4 < COB; j4 += 4) {
-        const float4 w4 = *reinterpret_cast<const float4*>(wt + e * COB + j4);
-        acc[j4 + 0] = fmaf(xv[e], w4.x, acc[j4 + 0]);
-        acc[j4 + 1] = fmaf(xv[e], w4.y, acc[j4 + 1]);
-        acc[j4 + 2] = fmaf(xv[e], w4.z, acc[j4 + 2]);
-        acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
+    for (int r = 0; r < PER; ++r) {
+      const int i = threadIdx.x + r * kThreads;
+      if (i < CK * COB) {
+        const int co = i / CK, e = i - co * CK;
+        lds[e * COB + co] = v[r];
+      } else if (i < N) {
+        lds[i] = v[r];
       }
-    if (valid) {
+    }
+  }
+};
+
+template <int CK, int COB>
+__device__ __forceinline__ void window_dot(const float (&xv)[CK], const float* wt,
+                                           float (&acc)[COB]) {
 #pragma unroll
-      for (int j = 0; j < COB; ++j) {
-        if (partials) st.add(acc[j]);
-        float v = apply_act(acc[j], act, p.alpha);
-        if (p.res) v += p.res[((int64_t)b * p.Cout + co0 + j) * p.ldr + t];
-        if (y) y[((int64_t)b * p.Cout + co0 + j) * p.ldy + t] = v;
+  for (int e = 0; e < CK; ++e)
+#pragma unroll
+    for (int j4 = 0; j4 < COB; j4 += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(wt + e * COB + j4);
+      acc[j4 + 0] = fmaf(xv[e], w4.x, acc[j4 + 0]);
+      acc[j4 + 1] = fmaf(xv[e], w4.y, acc[j4 + 1]);
+      acc[j4 + 2] = fmaf(xv[e], w4.z, acc[j4 + 2]);
+      acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
+    }
+}
+
+// Small contractions (groups = 1, Cin*K = CK <= 32): each thread loads its whole input window
+// (CK samples) into registers, then produces the COB output channels of its workgroup (grid.y
+// spreads the channels, so there are enough waves per SIMD to hide memory latency). Weights and
+// bias are staged in LDS, their loads issued before the window's so that one wait covers both.
+template <int CK, int COB, bool REFLECT>
+__global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams p,
+                                                                     const float* __restrict__ x,
+                                                                     const float* __restrict__ w,
+                                                                     const float* __restrict__ bias,
+                                                                     float* __restrict__ y, int act,
+                                                                     float* __restrict__ partials) {
+  __shared__ float red[3 * (kThreads / 64)];
+  using Stage = ConstStage<CK, COB, 1>;
+  __shared__ __attribute__((aligned(16))) float wt[Stage::N];  // weights, bias
+  const int b = blockIdx.z;
+  const int co0 = blockIdx.y * COB;
+  const int t = blockIdx.x * kThreads + threadIdx.x;
+  const bool valid = t < p.Lout;
+  Stage stg;
+  stg.fetch(w, co0, bias, nullptr, nullptr, 0.f, 0.f, 0.f);
+  float xv[CK];
+  load_window<CK, REFLECT>(p, x + (int64_t)b * p.Cin * p.Lin, t, valid, xv);
+  stg.put(wt);
+  __syncthreads();
+  ShiftedStats st;
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = wt[CK * COB + j];
+  window_dot<CK, COB>(xv, wt, acc);
+  if (valid) {
+    if (partials) {
+#pragma unroll
+      for (int j = 0; j < COB; ++j) st.add(acc[j]);
+    }
+    if (y) {
+      // one unrolled store loop per activation code, so no loop carries every code's registers
+      const float* rb = p.res ? p.res + ((int64_t)b * p.Cout + co0) * p.ldr + t : nullptr;
+      float* yb = y + ((int64_t)b * p.Cout + co0) * p.ldy + t;
+      auto store = [&](auto code) {
+        float rv[COB];
+#pragma unroll
+        for (int j = 0; j < COB; ++j) rv[j] = rb ? rb[(int64_t)j * p.ldr] : 0.f;
+#pragma unroll
+        for (int j = 0; j < COB; ++j)
+          yb[(int64_t)j * p.ldy] = apply_act(acc[j], code.value, p.alpha) + rv[j];
+      };
+      switch (act) {
+        case 1: store(std::integral_constant<int, 1>{}); break;
+        case 2: store(std::integral_constant<int, 2>{}); break;
+        case 3: store(std::integral_constant<int, 3>{}); break;
+        case 4: store(std::integral_constant<int, 4>{}); break;
+        case 5: store(std::integral_constant<int, 5>{}); break;
+        case 6: store(std::integral_constant<int, 6>{}); break;
+        default: store(std::integral_constant<int, 0>{}); break;
       }
     }
   }
@@ -166,6 +246,111 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams 
       o[0] = n;
       o[1] = mean;
       o[2] = m2;
+    }
+  }
+}
+
+// Pass 1: GroupNorm(1) statistics of conv(x) + bias, one (count, mean, M2) partial per workgroup
+// at parts[(b * nparts + blockIdx.y * gridDim.x + blockIdx.x) * 3]; nothing else is written.
+template <int CK, int COB, bool REFLECT>
+__global__ __launch_bounds__(kThreads) void conv_gn_stats_kernel(ConvParams p,
+                                                                 const float* __restrict__ x,
+                                                                 const float* __restrict__ w,
+                                                                 const float* __restrict__ bias,
+                                                                 float* __restrict__ parts) {
+  __shared__ float red[3 * (kThreads / 64)];
+  using Stage = ConstStage<CK, COB, 1>;
+  __shared__ __attribute__((aligned(16))) float wt[Stage::N];  // weights, bias
+  const int b = blockIdx.z, cob0 = blockIdx.y * COB;
+  const int t = blockIdx.x * kThreads + threadIdx.x;
+  const bool valid = t < p.Lout;
+  Stage st;
+  st.fetch(w, cob0, bias, nullptr, nullptr, 0.f, 0.f, 0.f);
+  float xv[CK];
+  load_window<CK, REFLECT>(p, x + (int64_t)b * p.Cin * p.Lin, t, valid, xv);
+  st.put(wt);
+  __syncthreads();
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = wt[CK * COB + j];
+  window_dot<CK, COB>(xv, wt, acc);
+  // this thread's COB values, two passes in registers
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < COB; ++j) s += acc[j];
+  float mean = s * (1.f / COB), m2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < COB; ++j) m2 = fmaf(acc[j] - mean, acc[j] - mean, m2);
+  float n = valid ? (float)COB : 0.f;
+  if (!valid) mean = m2 = 0.f;
+  block_welford(n, mean, m2, red);
+  if (threadIdx.x == 0) {
+    float* o = parts + ((int64_t)b * gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x) * 3;
+    o[0] = n;
+    o[1] = mean;
+    o[2] = m2;
+  }
+}
+
+// Pass 2: y = act(gamma_c * (conv(x)_c + bias_c - mean) * rstd + beta_c). The window loads are
+// issued first; every workgroup merges the nparts partials of its batch (fp64, the same order in
+// every workgroup) while they are in flight. ACT >= 0 is a fixed activation code, -1 reads `act`.
+template <int CK, int COB, bool REFLECT, int ACT>
+__global__ __launch_bounds__(kThreads) void conv_gn_apply_kernel(
+    ConvParams p, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ bias, const float* __restrict__ parts, int nparts,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps, int act,
+    float* __restrict__ y) {
+  using Stage = ConstStage<CK, COB, 3>;
+  __shared__ __attribute__((aligned(16))) float wt[Stage::N];  // weights, bias, gamma, beta
+  const int b = blockIdx.z, cob0 = blockIdx.y * COB;
+  const int t = blockIdx.x * kThreads + threadIdx.x;
+  const bool valid = t < p.Lout;
+  __shared__ double s_sums[4 * (kThreads / 64)];
+  const float* pb = parts + (int64_t)b * nparts * 3;
+  // every load is issued before any is waited for: the partials (each read once per workgroup),
+  // the workgroup's constants, the input window
+  BlockParts<2> pts;
+  pts.load(pb, nparts);
+  Stage st;
+  st.fetch(w, cob0, bias, gamma, beta, 0.f, 1.f, 0.f);
+  float xv[CK];
+  load_window<CK, REFLECT>(p, x + (int64_t)b * p.Cin * p.Lin, t, valid, xv);
+  st.put(wt);
+  pts.reduce_waves(pb, nparts, s_sums);
+  __syncthreads();
+  double n, mean, m2;
+  BlockParts<2>::finish(s_sums, n, mean, m2);
+  const double var = n > 0.0 ? m2 / n : 0.0;
+  float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  if (!isfinite(rstd)) rstd = 0.f;
+  const float mf = (float)mean;
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = 0.f;
+  window_dot<CK, COB>(xv, wt, acc);
+  if (!valid) return;
+  float* yb = y + ((int64_t)b * p.Cout + cob0) * p.ldy + t;
+  const float* cb = wt + CK * COB;  // bias, gamma, beta of this workgroup's channels
+  auto store = [&](auto code) {
+#pragma unroll
+    for (int j = 0; j < COB; ++j) {
+      const float sc = cb[COB + j] * rstd;  // scale and shift with the bias folded in
+      const float sh = cb[2 * COB + j] + (cb[j] - mf) * sc;
+      yb[(int64_t)j * p.ldy] = apply_act(fmaf(acc[j], sc, sh), code.value, p.alpha);
+    }
+  };
+  if constexpr (ACT >= 0) {
+    store(std::integral_constant<int, ACT>{});
+  } else {  // one unrolled store loop per code, so no loop carries every activation's registers
+    switch (act) {
+      case 1: store(std::integral_constant<int, 1>{}); break;
+      case 2: store(std::integral_constant<int, 2>{}); break;
+      case 3: store(std::integral_constant<int, 3>{}); break;
+      case 4: store(std::integral_constant<int, 4>{}); break;
+      case 5: store(std::integral_constant<int, 5>{}); break;
+      case 6: store(std::integral_constant<int, 6>{}); break;
+      default: store(std::integral_constant<int, 0>{}); break;
     }
   }
 }
@@ -224,6 +409,60 @@ void conv1d_direct(const LaunchCtx& c, const ConvParams& p0, const float* x, con
 }
 
 bool conv1d_direct_fusable(const ConvParams& p) { return reg_ck(p) != 0; }
+
+namespace {
+// channels per thread of the two-pass Conv1D -> GroupNorm(1) chain: the statistics pass takes
+// twice the apply pass's, halving the partials every apply workgroup merges
+constexpr int kGnCob = 8, kGnStatsCob = 16;
+}
+
+int conv_gn_num_parts(const ConvParams& p) {
+  return (int)cdiv(p.Lout, kThreads) * (p.Cout / kGnStatsCob);
+}
+
+void conv_gn_stats(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                   const float* bias, float* parts) {
+  const int ck = reg_ck(p);
+  MNN_REQUIRE(ck, MNN_ERR_INVALID_ARGUMENT, "conv_gn_stats: not a register-window convolution");
+  dim3 grid(cdiv(p.Lout, kThreads), p.Cout / kGnStatsCob, p.B);
+#define MNN_ST(CKV, R) launch(c, "conv_gn_stats_f32", conv_gn_stats_kernel<CKV, kGnStatsCob, R>, grid, dim3(kThreads), 0, p, x, w, bias, parts)
+  switch (ck * 2 + (p.reflect ? 1 : 0)) {
+    case 16: return MNN_ST(8, false);
+    case 17: return MNN_ST(8, true);
+    case 32: return MNN_ST(16, false);
+    case 33: return MNN_ST(16, true);
+    case 48: return MNN_ST(24, false);
+    case 49: return MNN_ST(24, true);
+    case 64: return MNN_ST(32, false);
+    default: return MNN_ST(32, true);
+  }
+#undef MNN_ST
+}
+
+void conv_gn_apply(const LaunchCtx& c, const ConvParams& p0, const float* x, const float* w,
+                   const float* bias, const float* parts, int nparts, const float* gamma,
+                   const float* beta, float eps, int act, float* y) {
+  ConvParams p = p0;
+  if (p.ldy == 0) p.ldy = p.Lout;
+  const int ck = reg_ck(p);
+  MNN_REQUIRE(ck, MNN_ERR_INVALID_ARGUMENT, "conv_gn_apply: not a register-window convolution");
+  dim3 grid(cdiv(p.Lout, kThreads), p.Cout / kGnCob, p.B);
+  const int a = (act == 0 || act == 3) ? act : -1;
+#define MNN_AP(CKV, R, A) launch(c, "conv_gn_apply_f32", conv_gn_apply_kernel<CKV, kGnCob, R, A>, grid, dim3(kThreads), 0, p, x, w, bias, parts, nparts, gamma, beta, eps, act, y)
+#define MNN_AP3(CKV, R) return a == 0 ? MNN_AP(CKV, R, 0) : a == 3 ? MNN_AP(CKV, R, 3) : MNN_AP(CKV, R, -1)
+  switch (ck * 2 + (p.reflect ? 1 : 0)) {
+    case 16: MNN_AP3(8, false);
+    case 17: MNN_AP3(8, true);
+    case 32: MNN_AP3(16, false);
+    case 33: MNN_AP3(16, true);
+    case 48: MNN_AP3(24, false);
+    case 49: MNN_AP3(24, true);
+    case 64: MNN_AP3(32, false);
+    default: MNN_AP3(32, true);
+  }
+#undef MNN_AP3
+#undef MNN_AP
+}
 
 }  // namespace k
 }  // namespace mnn

@@ -153,47 +153,6 @@ __global__ __launch_bounds__(kThreads) void gn_apply_kernel(const float* __restr
   }
 }
 
-// Chan's merge of two fp64 statistics (count, mean, M2): a then b, in that order.
-__device__ __forceinline__ void chan_merge_d(double& n, double& mean, double& m2, double n2,
-                                             double mean2, double m22) {
-  const double nt = n + n2;
-  if (nt > 0.0) {
-    const double d = mean2 - mean;
-    const double w = n2 / nt;
-    mean += d * w;
-    m2 += m22 + d * d * n * w;
-  }
-  n = nt;
-}
-
-// Every lane of the calling wave receives the merge of np (count, mean, M2) partials: lane l
-// merges partials l, l + 64, ... in order, then a butterfly combines lane pairs lower lane first,
-// so both lanes of a pair compute the same value and all lanes end with the identical total
-// (deterministic, the same in every wave and workgroup).
-__device__ __forceinline__ void wave_merge_parts(const float* __restrict__ p, int np, double& n,
-                                                 double& mean, double& m2) {
-  const int lane = threadIdx.x & 63;
-  n = 0.0;
-  mean = 0.0;
-  m2 = 0.0;
-  for (int j = lane; j < np; j += 64)
-    chan_merge_d(n, mean, m2, p[3 * j], p[3 * j + 1], p[3 * j + 2]);
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const double on = __shfl_xor(n, off, 64), om = __shfl_xor(mean, off, 64),
-                 oq = __shfl_xor(m2, off, 64);
-    if (lane & off) {  // this lane holds the upper half: merge(other, self)
-      double a = on, b = om, c = oq;
-      chan_merge_d(a, b, c, n, mean, m2);
-      n = a;
-      mean = b;
-      m2 = c;
-    } else {
-      chan_merge_d(n, mean, m2, on, om, oq);
-    }
-  }
-}
-
 // GroupNorm apply with the statistics merged in the workgroup: x, y [B][C][L]; group (b, g) covers
 // the contiguous cpg * L elements of channels [g * cpg, (g + 1) * cpg); its nparts partials sit
 // at parts[((b * G + g) * nparts + j) * 3]. y = act((x - mean) * rstd * gamma_c + beta_c), biased

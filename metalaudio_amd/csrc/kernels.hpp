@@ -70,6 +70,15 @@ void conv1d_direct(const LaunchCtx& c, const ConvParams& p, const float* x, cons
 int conv1d_direct_num_chunks(const ConvParams& p);
 // True when the register-window kernel runs (it supports statistics-only and fused finalize).
 bool conv1d_direct_fusable(const ConvParams& p);
+// Conv1D -> GroupNorm(1) -> activation for register-window convolutions (conv1d_direct_fusable):
+// pass 1 writes conv_gn_num_parts(p) statistics partials per batch (3 floats each), pass 2
+// recomputes the convolution and writes the normalised, activated output once.
+int conv_gn_num_parts(const ConvParams& p);
+void conv_gn_stats(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                   const float* bias, float* parts);
+void conv_gn_apply(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                   const float* bias, const float* parts, int nparts, const float* gamma,
+                   const float* beta, float eps, int act, float* y);
 // GEMM tuning override: MNN_GEMM_TILE=<tile id> forces a tile configuration where it applies.
 
 // ------------------------------------------------------------------ GEMM (k_gemm.hip)

@@ -251,6 +251,12 @@ class Conv1DLayer : public Layer {
                      b_ ? b_->ptr() : nullptr, y, act, stats, nullptr);
   }
   const mnn_conv1d_desc& desc() const { return p_; }
+  // The direct register-window kernel family applies (groups 1, Cin * K <= 32, few channels).
+  bool register_window(int B, int L) const {
+    return !uses_mfma() && k::conv1d_direct_fusable(direct_params(B, L));
+  }
+  const float* weight() const { return w_->ptr(); }
+  const float* bias() const { return b_ ? b_->ptr() : nullptr; }
 
  private:
   mnn_conv1d_desc p_;
@@ -1979,11 +1985,23 @@ void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor
               "fused Conv1D -> GroupNorm: buffers do not hold " << shape_str(ys));
   int64_t B, C, L;
   split_bcl(in.shape, B, C, L);
+  const int act = n == 3 ? MNN_ACT_GELU : g->act();
+  if (c->register_window((int)B, (int)L)) {
+    // small contraction: statistics pass, then a pass that recomputes the convolution and
+    // writes the normalised output once (y is not used)
+    k::ConvParams p = c->direct_params((int)B, (int)L);
+    p.alpha = 0.01f;  // the activation is GroupNorm's: leaky ReLU slope 0.01
+    const int nparts = k::conv_gn_num_parts(p);
+    float* parts = g->reserve_partials(3LL * B * nparts);
+    k::conv_gn_stats(ctx(s), p, in.f32(), c->weight(), c->bias(), parts);
+    k::conv_gn_apply(ctx(s), p, in.f32(), c->weight(), c->bias(), parts, nparts, g->gamma(),
+                     g->beta(), g->eps(), act, out.f32());
+    return;
+  }
   const int nparts = c->stats_chunks((int)B, (int)L);
   float* parts = g->reserve_partials(3LL * B * nparts);
   c->run(in.f32(), (int)B, (int)L, y.f32(), MNN_ACT_NONE, parts, s);
-  g->apply_parts(s, y.f32(), out.f32(), (int)B, ys.back(), parts, nparts,
-                 n == 3 ? MNN_ACT_GELU : g->act());
+  g->apply_parts(s, y.f32(), out.f32(), (int)B, ys.back(), parts, nparts, act);
 }
 
 void groupnorm_forward_noalloc(Layer* l, const Tensor& in, Tensor& out, Stream& s) {

@@ -879,21 +879,27 @@ def test_sequential_forward_async(dev, stream):
     assert rc == 11 and errs[-1] == (11, None)  # MNN_ERR_NOT_BUILT
 
 
-@pytest.mark.parametrize("cin,cout,L,act,gelu", [
-    (2, 48, 44100, "none", True),     # config-1 shape: direct conv, GELU layer fused
-    (48, 96, 3001, "none", False),    # matrix-core conv with GEMM statistics, GN alone
-    (8, 16, 777, "gelu", False),      # GroupNorm's own fused activation
+@pytest.mark.parametrize("cin,cout,L,act,gelu,k,mode,pad", [
+    (2, 48, 44100, "none", True, 8, "reflect", 3),   # config-1 shape: register-window, GELU fused
+    (48, 96, 3001, "none", False, 8, "reflect", 3),  # matrix-core conv with GEMM statistics
+    (8, 16, 777, "gelu", False, 4, "reflect", 3),    # GroupNorm's own fused activation
+    (1, 16, 5003, "relu", False, 8, "explicit", 2),  # zero padding, ReLU, ragged last workgroup
+    (3, 32, 2999, "leaky_relu", False, 8, "explicit", 5),  # Cin * K = 24
+    (4, 64, 1025, "sigmoid", False, 8, "reflect", 3),      # Cin * K = 32
+    (2, 24, 301, "tanh", False, 4, "explicit", 1),         # Cin * K = 8, three channel blocks
 ])
-def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu):
-    """Conv1D -> GroupNorm(1) [-> GELU] in a Sequential runs fused (two launches); the result is
-    the layers' composition, batch 2 included."""
-    say(f"sequential conv -> groupnorm fusion {cin}->{cout} L={L} act={act} gelu={gelu}")
+def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu, k, mode, pad):
+    """Conv1D -> GroupNorm(1) [-> activation / GELU] in a Sequential runs fused (two launches);
+    the result is the layers' composition, batch 2 included. The bias and GroupNorm shift carry
+    an offset so that a dropped bias or mean term moves the output."""
+    say(f"sequential conv -> groupnorm fusion {cin}->{cout} k{k} L={L} {mode} act={act} "
+        f"gelu={gelu}")
     x = RNG.uniform(-1, 1, (2, cin, L)).astype(np.float32)
-    w = (RNG.standard_normal((cout, cin, 8)) * np.sqrt(2 / (cin * 8))).astype(np.float32)
-    b = (RNG.standard_normal(cout) * 0.1).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin, k)) * np.sqrt(2 / (cin * k))).astype(np.float32)
+    b = (0.5 + RNG.standard_normal(cout) * 0.3).astype(np.float32)
     gm = (1 + 0.2 * RNG.standard_normal(cout)).astype(np.float32)
     bt = (0.2 * RNG.standard_normal(cout)).astype(np.float32)
-    conv = nn.DynamicConv1D(dev, cin, cout, 8, 4, padding_mode="reflect", padding=3)
+    conv = nn.DynamicConv1D(dev, cin, cout, k, 4, padding_mode=mode, padding=pad)
     conv.load_weights(w, b)
     gn = nn.GroupNorm(dev, 1, cout, activation=act)
     gn.load_parameters(gm, bt)
@@ -908,6 +914,8 @@ def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu):
     seq.build()
     out = seq.forward(nn.Tensor.from_numpy(dev, x), stream)
     stream.sync(60000)
-    ref = oracle.group_norm(oracle.conv1d(x, w, b, stride=4, padding=3, mode="reflect"), 1, gm, bt)
+    ref = oracle.group_norm(oracle.conv1d(x, w, b, stride=4, padding=pad,
+                                          mode="reflect" if mode == "reflect" else "zeros"),
+                            1, gm, bt)
     ref = oracle.gelu_layer(ref) if gelu else oracle.activation(ref, act)
     assert_close(out.to_numpy().reshape(ref.shape), ref, ATOL, RTOL, "fused sequential")
