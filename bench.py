@@ -125,7 +125,9 @@ def transformer_work(batch):
                 gemm_f += 2.0 * batch * own * E * 3 * E
             gemm_f += 2.0 * batch * own * (E * E + 2 * E * Hd)
             gemm_b += 4.0 * batch * own * (E + 3 * E + E + E + E + Hd + Hd + E)
-            ln_b += 4.0 * batch * 2 * own * E * (3 if cross else 2)
+            # self layer: two LayerNorms (read + write each); cross layer: the two normalisations
+            # of this state in one pass (one read, two writes), then the feed-forward norm
+            ln_b += 4.0 * batch * own * E * (5 if cross else 4)
     return {"attn_fwd_f32": [attn_f, attn_b], "gemm_f32_mfma_nk": [gemm_f, gemm_b],
             "layernorm": [0.0, ln_b]}
 

@@ -192,6 +192,23 @@ __device__ __forceinline__ void wave_merge_parts(const float* __restrict__ p, in
   pb.merge(p, np, n, mean, m2);
 }
 
+// Sum over each aligned group of 16 lanes (a DPP "row"), the total in every lane of the group, by
+// DPP moves instead of LDS permutes: swap neighbours (quad_perm [1,0,3,2]), swap pairs
+// ([2,3,0,1]), mirror within 8 lanes, mirror within 16. Each step adds a value to its partner's,
+// and both partners compute the same sum (a + b = b + a), so every lane ends with the identical
+// total.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   uint32_t u = __float_as_uint(f);

@@ -286,73 +286,78 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
   }
 }
 
-// LayerNorm with LPR lanes per row (LPR = 16 or 32: 64 / LPR rows per wave), NV float4 per lane,
-// F % 4 == 0, F <= 4 * LPR * NV. For F = 384 (96 float4) 32 lanes x 3 float4 keep every lane
-// busy where one row per wave would leave a quarter of the lanes idle, and a wave has two rows'
-// loads in flight. Reductions are xor shuffles within the row's lane group.
-template <int LPR, int NV>
-__global__ __launch_bounds__(kThreads) void layernorm_group_kernel(const float* __restrict__ x,
-                                                                   float* __restrict__ y,
-                                                                   int64_t rows, int F,
-                                                                   const float* __restrict__ gamma,
-                                                                   const float* __restrict__ beta,
-                                                                   float eps) {
-  constexpr int RPW = 64 / LPR;  // rows per wave
-  const int lane = threadIdx.x & 63, sub = lane % LPR;
-  const int64_t row = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * RPW +
-                      lane / LPR;
+// gamma / beta are deliberately not __restrict__: loads through restrict pointers to constant
+// data count as invariant, and the compiler then moves them freely past the wait below.
+// DUAL: a second LayerNorm of the same rows (its own gamma2 / beta2 / eps2) into y2, so two
+// normalisations of one input read it once.
+template <int NV, bool DUAL>
+__global__ __launch_bounds__(kThreads) void layernorm_row16_kernel(
+    const float* __restrict__ x, float* __restrict__ y, int64_t rows, const float* gamma,
+    const float* beta, float eps, float* __restrict__ y2, const float* gamma2, const float* beta2,
+    float eps2) {
+  constexpr int F = 64 * NV;
+  const int lane = threadIdx.x & 63, sub = lane & 15;
+  const int64_t row = ((int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6)) * 4 + lane / 16;
   const bool live = row < rows;
-  const int F4 = F >> 2;
-  const int64_t r = live ? row : rows - 1;  // dead groups compute on a valid row, store nothing
+  const int64_t r = live ? row : rows - 1;  // dead rows compute on a valid row, store nothing
   const float4* xr = reinterpret_cast<const float4*>(x + r * F);
-  const float4* g4 = reinterpret_cast<const float4*>(gamma);
-  const float4* b4 = reinterpret_cast<const float4*>(beta);
-  float4 v[NV], gv[NV], bv[NV];
-  float s = 0.f;
+  float4 v[NV], gv[NV], bv[NV], gv2[DUAL ? NV : 1], bv2[DUAL ? NV : 1];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = xr[sub + 16 * i];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = sub + LPR * i;
-    if (idx < F4) {
-      v[i] = xr[idx];
-      gv[i] = g4[idx];
-      bv[i] = b4[idx];
-      s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
-    } else {
-      v[i] = gv[i] = bv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    gv[i] = reinterpret_cast<const float4*>(gamma)[sub + 16 * i];
+    bv[i] = reinterpret_cast<const float4*>(beta)[sub + 16 * i];
+    if constexpr (DUAL) {
+      gv2[i] = reinterpret_cast<const float4*>(gamma2)[sub + 16 * i];
+      bv2[i] = reinterpret_cast<const float4*>(beta2)[sub + 16 * i];
     }
   }
+  // one wait for every load above; the scheduling barriers and the memory clobber keep the
+  // compiler from moving the gamma / beta loads behind the reductions (next to their use: a
+  // second memory round trip)
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  float s = 0.f;
 #pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
-  const float mean = s / (float)F;
+  for (int i = 0; i < NV; ++i) s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+  const float mean = row16_sum(s) * (1.f / F);
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int idx = sub + LPR * i;
-    if (idx < F4) {
-      float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
-      q += (a * a + b * b) + (c * c + d * d);
+    v[i].x -= mean;
+    v[i].y -= mean;
+    v[i].z -= mean;
+    v[i].w -= mean;
+    q += (v[i].x * v[i].x + v[i].y * v[i].y) + (v[i].z * v[i].z + v[i].w * v[i].w);
+  }
+  const float var = row16_sum(q) * (1.f / F);
+  const float rstd = 1.f / sqrtf(var + eps);
+  const float rstd2 = DUAL ? 1.f / sqrtf(var + eps2) : 0.f;
+  // outputs computed before the store branch (the loads stay in the block of the wait above)
+  float4 o[NV], o2[DUAL ? NV : 1];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    o[i].x = gv[i].x * (v[i].x * rstd) + bv[i].x;
+    o[i].y = gv[i].y * (v[i].y * rstd) + bv[i].y;
+    o[i].z = gv[i].z * (v[i].z * rstd) + bv[i].z;
+    o[i].w = gv[i].w * (v[i].w * rstd) + bv[i].w;
+    if constexpr (DUAL) {
+      o2[i].x = gv2[i].x * (v[i].x * rstd2) + bv2[i].x;
+      o2[i].y = gv2[i].y * (v[i].y * rstd2) + bv2[i].y;
+      o2[i].z = gv2[i].z * (v[i].z * rstd2) + bv2[i].z;
+      o2[i].w = gv2[i].w * (v[i].w * rstd2) + bv2[i].w;
     }
   }
-#pragma unroll
-  for (int off = LPR / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, kWave);
-  const float var = q / (float)F;
-  const float rstd = 1.f / sqrtf(var + eps);
+  if (!live) return;
   float4* yr = reinterpret_cast<float4*>(y + r * F);
-  wait_vmcnt<0>();  // every load has landed: the stores below need no waits between them
-  if (live) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int idx = sub + LPR * i;
-      if (idx < F4) {
-        const float4 g = gv[i], bb = bv[i];
-        float4 o;
-        o.x = g.x * ((v[i].x - mean) * rstd) + bb.x;
-        o.y = g.y * ((v[i].y - mean) * rstd) + bb.y;
-        o.z = g.z * ((v[i].z - mean) * rstd) + bb.z;
-        o.w = g.w * ((v[i].w - mean) * rstd) + bb.w;
-        yr[idx] = o;
-      }
-    }
+  for (int i = 0; i < NV; ++i) yr[sub + 16 * i] = o[i];
+  if constexpr (DUAL) {
+    float4* yr2 = reinterpret_cast<float4*>(y2 + r * F);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) yr2[sub + 16 * i] = o2[i];
   }
 }
 
@@ -443,6 +448,42 @@ void gn_apply_parts(const LaunchCtx& c, const float* x, float* y, int B, int C, 
          0, x, y, C, L, G, parts, nparts, gamma, beta, eps, act, vec);
 }
 
+namespace {
+void layernorm_row16(const LaunchCtx& c, const float* x, int64_t rows, int F, float* y,
+                     const float* g, const float* b, float eps, float* y2, const float* g2,
+                     const float* b2, float eps2) {
+  const dim3 grid(cdiv(rows, 4 * (kThreads / 64))), block(kThreads);
+#define MNN_LN16(NV)                                                                           \
+  return y2 ? launch(c, "layernorm_f32", layernorm_row16_kernel<NV, true>, grid, block, 0, x, y, \
+                     rows, g, b, eps, y2, g2, b2, eps2)                                         \
+            : launch(c, "layernorm_f32", layernorm_row16_kernel<NV, false>, grid, block, 0, x, \
+                     y, rows, g, b, eps, y2, g2, b2, eps2)
+  switch (F / 64) {
+    case 1: MNN_LN16(1);
+    case 2: MNN_LN16(2);
+    case 3: MNN_LN16(3);
+    case 4: MNN_LN16(4);
+    case 5: MNN_LN16(5);
+    case 6: MNN_LN16(6);
+    case 7: MNN_LN16(7);
+    default: MNN_LN16(8);
+  }
+#undef MNN_LN16
+}
+}  // namespace
+
+void layernorm2(const LaunchCtx& c, const float* x, int64_t rows, int F, float* y,
+                const float* gamma, const float* beta, float eps, float* y2,
+                const float* gamma2, const float* beta2, float eps2) {
+  if (rows <= 0) return;
+  const bool vec = (F % 4 == 0) && aligned16(x) && aligned16(y) && aligned16(y2) &&
+                   aligned16(gamma) && aligned16(beta) && aligned16(gamma2) && aligned16(beta2);
+  if (vec && F % 64 == 0 && F <= 512)
+    return layernorm_row16(c, x, rows, F, y, gamma, beta, eps, y2, gamma2, beta2, eps2);
+  layernorm(c, x, y, rows, F, gamma, beta, eps);
+  layernorm(c, x, y2, rows, F, gamma2, beta2, eps2);
+}
+
 void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
                const float* gamma, const float* beta, float eps) {
   if (rows <= 0) return;
@@ -450,17 +491,9 @@ void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F
   const bool vec = (F % 4 == 0) && aligned16(x) && aligned16(y) && aligned16(gamma) &&
                    aligned16(beta);
   const int nv = (F + 255) / 256;
-  // rows of at most 128 float4 with 32 lanes each busy on every load: two rows per wave
-  if (vec && F % 128 == 0 && F <= 512) {
-    const int nv32 = F / 128;  // float4 per lane with 32 lanes per row
-    dim3 g2(cdiv(rows, 2 * (kThreads / 64)));
-    switch (nv32) {
-      case 1: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 1>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
-      case 2: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 2>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
-      case 3: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 3>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
-      default: return launch(c, "layernorm_f32", layernorm_group_kernel<32, 4>, g2, block, 0, x, y, rows, F, gamma, beta, eps);
-    }
-  }
+  // rows of 64 * NV floats: 16 lanes per row, DPP reductions
+  if (vec && F % 64 == 0 && F <= 512)
+    return layernorm_row16(c, x, rows, F, y, gamma, beta, eps, nullptr, nullptr, nullptr, 0.f);
   if (vec && nv <= 8) {
     switch (nv) {
       case 1: return launch(c, "layernorm_f32", layernorm_reg_kernel<1>, grid, block, 0, x, y, rows, F, gamma, beta, eps);

@@ -48,6 +48,11 @@ float* gn_scratch(int device);
 // LayerNorm over rows of F features (two-pass statistics, biased variance, rsqrt).
 void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
                const float* gamma, const float* beta, float eps);
+// Two LayerNorms of the same rows (own gamma / beta / eps each) in one pass over x where the
+// row kernel applies (F % 64 == 0, F <= 512), else two launches.
+void layernorm2(const LaunchCtx& c, const float* x, int64_t rows, int F, float* y,
+                const float* gamma, const float* beta, float eps, float* y2,
+                const float* gamma2, const float* beta2, float eps2);
 
 // ------------------------------------------------------------------ conv (k_conv.hip)
 struct ConvParams {

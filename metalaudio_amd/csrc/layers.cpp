@@ -379,6 +379,13 @@ class LayerNormLayer : public Layer {
   void run(const float* x, int64_t rows, float* y, Stream& s) {
     k::layernorm(ctx(s), x, y, rows, F_, gamma_->ptr(), beta_->ptr(), eps_);
   }
+  // this LayerNorm into y and `other` (same feature size) into y2, reading x once
+  void run_pair(const LayerNormLayer& other, const float* x, int64_t rows, float* y, float* y2,
+                Stream& s) {
+    MNN_REQUIRE(other.F_ == F_, MNN_ERR_SHAPE_MISMATCH, "LayerNorm pair: feature sizes differ");
+    k::layernorm2(ctx(s), x, rows, F_, y, gamma_->ptr(), beta_->ptr(), eps_, y2,
+                  other.gamma_->ptr(), other.beta_->ptr(), other.eps_);
+  }
 
  private:
   int F_;
@@ -1907,11 +1914,11 @@ class CrossTransformerImpl : public Layer {
           link(ts, fs);
           link(fs, ts);
         }
-        // all four normalisations read the states from before this layer
-        bt.norm1->run(T, rt, ht, ts);   // time queries
-        bf.norm2->run(T, rt, ht2, ts);  // time as freq's keys/values
-        bf.norm1->run(F, rf, hf, fs);   // freq queries
-        bt.norm2->run(F, rf, hf2, fs);  // freq as time's keys/values
+        // all four normalisations read the states from before this layer; the two of each
+        // state in one pass: time queries and time as freq's keys/values, freq queries and freq
+        // as time's keys/values
+        bt.norm1->run_pair(*bf.norm2, T, rt, ht, ht2, ts);
+        bf.norm1->run_pair(*bt.norm2, F, rf, hf, hf2, fs);
         if (two) {
           link(fs, ts);  // hf2 ready
           link(ts, fs);  // ht2 ready
