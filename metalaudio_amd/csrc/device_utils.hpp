@@ -364,13 +364,29 @@ __device__ __forceinline__ float2 gn1_merge(const float* __restrict__ partials, 
 // 3 * blockDim.x / 64 doubles of LDS. Returns (mean, rstd) to every thread.
 __device__ __forceinline__ float2 gn1_merge_one_round(const float* __restrict__ partials,
                                                      int nparts, float eps, double* sh) {
+  // each round loads kBatch partials per thread with every load in flight (clamped addresses;
+  // out-of-range values are loaded but not used), instead of one dependent load per partial
+  constexpr int kBatch = 8;
   double n = 0.0, s1 = 0.0, s2 = 0.0;
-  for (int j = threadIdx.x; j < nparts; j += blockDim.x) {
-    const float* p = partials + (int64_t)j * 3;
-    const double pn = p[0], pm = p[1];
-    n += pn;
-    s1 += pn * pm;
-    s2 += (double)p[2] + pn * pm * pm;
+  for (int j0 = 0; j0 < nparts; j0 += kBatch * (int)blockDim.x) {
+    float pn[kBatch], pm[kBatch], pq[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float* p = partials + 3 * (int64_t)min(j0 + k * (int)blockDim.x + (int)threadIdx.x,
+                                                   nparts - 1);
+      pn[k] = p[0];
+      pm[k] = p[1];
+      pq[k] = p[2];
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      if (j0 + k * (int)blockDim.x + (int)threadIdx.x < nparts) {
+        const double c = pn[k], m = pm[k];
+        n += c;
+        s1 += c * m;
+        s2 += (double)pq[k] + c * m * m;
+      }
+    }
   }
   n = wave_sum_d(n);
   s1 = wave_sum_d(s1);

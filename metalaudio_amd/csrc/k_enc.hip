@@ -356,21 +356,19 @@ __global__ __launch_bounds__(kRedThreads) void enc_conv_reduce_kernel(
     v[u] = 0.f;
     nn[u] = min(c0 + u * kRedThreads + (int)threadIdx.x, N - 1);
   }
-  int s = 0;
-  for (; s + 4 <= splits; s += 4) {
+  // groups of four splits, all loads of a group in flight together (a group's splits past the
+  // last are loaded from the last and not added)
+  for (int s = 0; s < splits; s += 4) {
     float t[4][U];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int u = 0; u < U; ++u) t[j][u] = wr[(int64_t)(s + j) * total + nn[u]];
+      for (int u = 0; u < U; ++u) t[j][u] = wr[(int64_t)min(s + j, splits - 1) * total + nn[u]];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int u = 0; u < U; ++u) v[u] += t[j][u];
+      for (int u = 0; u < U; ++u) v[u] += s + j < splits ? t[j][u] : 0.f;
   }
-  for (; s < splits; ++s)
-#pragma unroll
-    for (int u = 0; u < U; ++u) v[u] += wr[(int64_t)s * total + nn[u]];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int n = c0 + u * kRedThreads + threadIdx.x;
