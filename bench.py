@@ -563,6 +563,11 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=40.0,
                     help="seconds of timed CPU-baseline runs at most")
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration table")
+    ap.add_argument("--profile-step", metavar="LOG",
+                    help="profiling mode: after the warm-up, run ONE step on one stream with the "
+                         "library's launch log on, write the log (one line per launch: name, "
+                         "grid, block) to LOG and exit; metalaudio_amd.profsummary pmc attributes "
+                         "a rocprofv3 run of this mode to the kernel names")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -586,6 +591,32 @@ def main():
     for _ in range(args.warmup):
         step()
     stream.sync()
+
+    if args.profile_step:
+        import ctypes
+        from metalaudio_amd._lib import lib
+        # kernel timing on: every launch goes to the caller's stream, in host order
+        dev.set_kernel_timing(True)
+        lib().mnn_debug_set_launch_log(dev.handle, 1)
+        step()
+        stream.sync()
+        lib().mnn_debug_set_launch_log(dev.handle, 0)
+        dev.set_kernel_timing(False)
+        need = ctypes.c_size_t()
+        lib().mnn_debug_launch_log(dev.handle, None, 0, ctypes.byref(need))
+        buf = ctypes.create_string_buffer(need.value)
+        rc = lib().mnn_debug_launch_log(dev.handle, buf, need.value, ctypes.byref(need))
+        if rc != 0:
+            log(f"launch log: status {rc}")
+            sys.exit(1)
+        text = buf.value.decode()
+        Path(args.profile_step).write_text(text)
+        work = encoder_work()
+        work = {k: [v[0] * 4, v[1] * 4] for k, v in work.items()}
+        work.update(transformer_work(W.T5_BATCH))
+        Path(args.profile_step).with_suffix(".work.json").write_text(json.dumps(work))
+        log(f"profile step: {len(text.splitlines())} launches logged to {args.profile_step}")
+        return
 
     markers = Markers()
     # timed region: wall clock around exactly K steps (no per-launch events)

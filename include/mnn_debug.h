@@ -28,6 +28,14 @@ mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, con
 mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t out_length,
                                    int batch, int* splits, int* tile_m, int* tile_n);
 
+/* Launch log, a profiling aid: while enabled, every kernel launch of the device appends a line
+ * "name grid.x grid.y grid.z block.x" (name as in mnn_device_kernel_timing). Enabling clears the
+ * log. mnn_debug_launch_log copies it, NUL-terminated, into buf (cap bytes) and sets *needed to
+ * the size required; MNN_ERR_BUFFER_SIZE_MISMATCH when cap is too small. A `rocprofv3 --pmc` run
+ * of a known sequence of launches is attributed to the library's kernel names this way. */
+mnn_status mnn_debug_set_launch_log(mnn_device dev, int enable);
+mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* needed);
+
 #ifdef __cplusplus
 }
 #endif

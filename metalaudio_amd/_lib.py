@@ -221,6 +221,8 @@ SIGNATURES = {
     "mnn_sequential_layer_at": (C.c_int, [P, C.c_int, PP]),
     "mnn_debug_mfma_probe": (C.c_int, [P, C.c_int, FP, FP, FP]),
     "mnn_debug_enc_conv_plan": (C.c_int, [C.c_int, C.c_int, C.c_int64, C.c_int, IP, IP, IP]),
+    "mnn_debug_set_launch_log": (C.c_int, [P, C.c_int]),
+    "mnn_debug_launch_log": (C.c_int, [P, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
 }
 
 _lib = None

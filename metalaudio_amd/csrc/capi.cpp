@@ -1146,4 +1146,29 @@ mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t ou
   });
 }
 
+mnn_status mnn_debug_set_launch_log(mnn_device dev, int enable) {
+  return guard([&] {
+    Device* d = D(dev);
+    std::lock_guard<std::mutex> lk(d->timing_mu);
+    if (enable) d->launches.clear();
+    d->launch_log.store(enable != 0);
+  });
+}
+
+mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* needed) {
+  return guard([&] {
+    MNN_REQUIRE(needed, MNN_ERR_INVALID_ARGUMENT, "needed is required");
+    Device* d = D(dev);
+    std::string all;
+    {
+      std::lock_guard<std::mutex> lk(d->timing_mu);
+      for (const std::string& l : d->launches) all += l + "\n";
+    }
+    *needed = all.size() + 1;
+    MNN_REQUIRE(buf && cap >= all.size() + 1, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "launch log needs " << all.size() + 1 << " bytes");
+    std::memcpy(buf, all.c_str(), all.size() + 1);
+  });
+}
+
 }  // extern "C"

@@ -79,6 +79,9 @@ struct Device {
   std::vector<KernelTimer> pending;                      // events not yet resolved
   std::map<std::string, std::pair<int64_t, double>> stats;  // name -> (launches, ms)
   std::vector<std::pair<hipEvent_t, hipEvent_t>> event_pool;
+  // launch log (a profiling aid): one line per launch, "name grid.x grid.y grid.z block.x"
+  std::atomic<bool> launch_log{false};
+  std::vector<std::string> launches;  // guarded by timing_mu
 
   void make_current() const { (void)hipSetDevice(ordinal); }
   void check_alive() const {
@@ -148,11 +151,13 @@ struct LaunchCtx {
 // for resolution under `name`.
 void timing_begin(const LaunchCtx& c, const char* name, hipEvent_t* ev_start, hipEvent_t* ev_stop);
 void timing_end(const LaunchCtx& c, const char* name, hipEvent_t ev_start, hipEvent_t ev_stop);
+void log_launch(const LaunchCtx& c, const char* name, dim3 grid, dim3 block);
 
 template <typename Kernel, typename... Args>
 inline void launch(const LaunchCtx& c, const char* name, Kernel k, dim3 grid, dim3 block,
                    size_t shmem, Args... args) {
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return;
+  if (c.dev && c.dev->launch_log.load(std::memory_order_relaxed)) log_launch(c, name, grid, block);
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (c.dev && c.dev->timing) {
     // the events take the kernel's own start / end timestamps (no extra packets around it)

@@ -28,6 +28,14 @@ void timing_end(const LaunchCtx& c, const char* name, hipEvent_t e0, hipEvent_t 
   d->pending.push_back(KernelTimer{name, e0, e1});
 }
 
+void log_launch(const LaunchCtx& c, const char* name, dim3 grid, dim3 block) {
+  Device* d = c.dev;
+  std::lock_guard<std::mutex> lk(d->timing_mu);
+  d->launches.push_back(std::string(name) + " " + std::to_string(grid.x) + " " +
+                        std::to_string(grid.y) + " " + std::to_string(grid.z) + " " +
+                        std::to_string(block.x));
+}
+
 void Device::resolve_timers() {
   std::lock_guard<std::mutex> lk(timing_mu);
   for (auto& t : pending) {

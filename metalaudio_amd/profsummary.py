@@ -9,6 +9,12 @@ Subcommands:
       total microseconds, share);
   copy --mib N
       a plain device copy of N MiB (torch), the calibration run for the HBM counters;
+  pmc --log LOG --trace DIR --passes DIR [DIR ...] --fetch DIR --write DIR --copy-fetch DIR
+      --copy-write DIR --copy-mib N --cmd "..." [--cmd "..."] [--out FILE] [--traffic-out FILE]
+      per-family table of one bench step (`bench.py --profile-step LOG`): durations from a kernel
+      trace, MFMA busy / VALU per MFMA / wait / LDS bank conflicts from SQ counter passes, HBM
+      bytes from FETCH_SIZE / WRITE_SIZE against the algorithmic bytes; dispatches are attributed
+      to the library's launch names through the launch log;
   traffic --fetch DIR --write DIR --copy-fetch DIR --copy-write DIR --copy-mib N [--out FILE]
       HBM bytes per dispatch of each kernel family from two `rocprofv3 --pmc` runs (FETCH_SIZE,
       then WRITE_SIZE, KiB per dispatch), each scaled by the factor that makes the same counter
@@ -33,6 +39,12 @@ from pathlib import Path
 FAMILIES = [
     ("attn_fwd_f32_kernel", "attn_fwd"),
     ("attn_generic_kernel", "attn_fwd"),
+    ("enc_l1_stats_kernel", "enc_l1_stats_f32"),
+    ("enc_l1_fused_kernel", "enc_l1_fused_f32"),
+    ("conv_gn_stats_kernel", "conv_gn_stats_f32"),
+    ("conv_gn_apply_kernel", "conv_gn_apply_f32"),
+    ("conv1d_direct", "conv1d_direct_f32"),
+    ("gn_apply_parts_kernel", "gn_apply_parts"),
     ("gemm_nk_lds_kernel", "gemm_f32_mfma_nk"),
     ("enc_conv_reduce_kernel", "enc_conv_reduce_f32"),
     ("enc_conv_kernel", "enc_conv_f32"),
@@ -194,6 +206,141 @@ def traffic(args) -> dict:
     return out
 
 
+# ------------------------------------------------------------------ per-family counter table
+CLOCK_HZ = 2.4e9   # MI355X peak engine clock: cycles -> seconds for the MFMA busy fraction
+SIMDS = 1024       # 256 CUs x 4 SIMDs
+PEAK = {"hbm": 8.0e12, "f32": 157.3e12}
+
+
+def _dispatches(d: str):
+    """Library dispatches of a rocprofv3 run in dispatch order: list of dicts with the kernel
+    name, total threads, workgroup size, start / end and {counter: value} (summed over
+    instances). Runtime-internal kernels (__amd_rocclr_*) are left out."""
+    disp = {}
+    for p in _csvs(d, "kernel_trace.csv"):
+        for r in csv.DictReader(open(p)):
+            if r["Kernel_Name"].startswith("__amd"):
+                continue
+            threads = (int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"]))
+            disp[(p, int(r["Dispatch_Id"]))] = {
+                "name": r["Kernel_Name"], "threads": threads,
+                "wg": int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) *
+                int(r["Workgroup_Size_Z"]),
+                "t": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3, "c": {}}
+    for p in _csvs(d, "counter_collection.csv"):
+        for r in csv.DictReader(open(p)):
+            if r["Kernel_Name"].startswith("__amd"):
+                continue
+            key = (p, int(r["Dispatch_Id"]))
+            e = disp.setdefault(key, {"name": r["Kernel_Name"], "threads": int(r["Grid_Size"]),
+                                      "wg": int(r["Workgroup_Size"]), "t": None, "c": {}})
+            e["c"][r["Counter_Name"]] = e["c"].get(r["Counter_Name"], 0.0) + \
+                float(r["Counter_Value"])
+    return [disp[k] for k in sorted(disp)]
+
+
+def _align(d: str, log):
+    """The last len(log) dispatches of run d, checked launch by launch against the log's grid
+    and workgroup sizes."""
+    ds = _dispatches(d)
+    if len(ds) < len(log):
+        raise SystemExit(f"{d}: {len(ds)} dispatches, the launch log has {len(log)}")
+    ds = ds[-len(log):]
+    for i, (e, l) in enumerate(zip(ds, log)):
+        if e["threads"] != l["threads"] or e["wg"] != l["wg"]:
+            raise SystemExit(f"{d}: dispatch {i} ({e['name'][:60]}, {e['threads']} threads) does "
+                             f"not match launch {l['name']} ({l['threads']} threads)")
+    return ds
+
+
+def _read_log(path: str):
+    out = []
+    for line in Path(path).read_text().splitlines():
+        name, gx, gy, gz, bx = line.rsplit(" ", 4)
+        out.append({"name": name, "threads": int(gx) * int(gy) * int(gz) * int(bx),
+                    "wg": int(bx)})
+    return out
+
+
+def _work_key(name: str, work: dict):
+    keys = [k for k in work if k in name]
+    return max(keys, key=len) if keys else None
+
+
+def pmc(args) -> str:
+    log = _read_log(args.log)
+    work = json.loads(Path(args.log).with_suffix(".work.json").read_text())
+    trace = _align(args.trace, log)
+    passes = [_align(d, log) for d in args.passes]
+    fetch = _align(args.fetch, log)
+    write = _align(args.write, log)
+    fac = {}
+    for counter, cd in (("FETCH_SIZE", args.copy_fetch), ("WRITE_SIZE", args.copy_write)):
+        cal = _counter_per_dispatch(cd, counter)
+        big = max((max(v) for v in cal.values()), default=0.0)
+        fac[counter] = args.copy_mib * 1024 * 1024 / (big * 1024.0) if big > 0 else 1.0
+    fam = collections.OrderedDict()
+    for i, l in enumerate(log):
+        key = _work_key(l["name"], work) or l["name"]
+        f = fam.setdefault(key, {"n": 0, "t": 0.0, "c": collections.defaultdict(float),
+                                 "hbm": 0.0, "names": set()})
+        f["n"] += 1
+        f["t"] += trace[i]["t"]
+        f["names"].add(l["name"])
+        for ps in passes:
+            for c, v in ps[i]["c"].items():
+                f["c"][c] += v
+        f["hbm"] += (fetch[i]["c"].get("FETCH_SIZE", 0.0) * fac["FETCH_SIZE"] +
+                     write[i]["c"].get("WRITE_SIZE", 0.0) * fac["WRITE_SIZE"]) * 1024.0
+    lines = [f"# {args.title}", "", "Commands (repo root, GPU box):", "", "```"] + \
+        args.cmd + ["```", "",
+                    f"One bench step ({len(log)} launches, kernel timing on so that every launch "
+                    "runs on one stream in host order), attributed to the library's launch names "
+                    "by the launch log (grid and workgroup sizes checked dispatch by dispatch). "
+                    "Per family and step:", "",
+                    "* `us`: summed kernel-trace duration; `frac`: algorithmic FLOP/s (MFMA-bound "
+                    "rows) or bytes/s (HBM-bound rows) over the MI355X peak (157.3 TFLOP/s fp32, "
+                    "8 TB/s);",
+                    "* `MFMA busy`: SQ_VALU_MFMA_BUSY_CYCLES / (duration x 2.4 GHz x 1024 SIMDs); "
+                    "`VALU/MFMA`: SQ_INSTS_VALU / SQ_INSTS_MFMA; `wait`: SQ_WAIT_INST_ANY / "
+                    "SQ_WAVE_CYCLES (share of wave time waiting on an outstanding memory / LDS "
+                    "result); `LDS confl.`: SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS;",
+                    f"* `HBM MB`: FETCH_SIZE + WRITE_SIZE (KiB per dispatch) x the factor that makes "
+                    f"the same counter read a {args.copy_mib} MiB copy's size (FETCH "
+                    f"{fac['FETCH_SIZE']:.3f}, WRITE {fac['WRITE_SIZE']:.3f}); `alg MB`: the "
+                    "algorithmic bytes bench.py prices the family with.", "",
+                    "| family | launches | us | bound | frac | MFMA busy | VALU/MFMA | wait | "
+                    "LDS confl. | HBM MB | alg MB | HBM/alg |",
+                    "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    traffic = {"_note": "HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, copy-calibrated), one "
+                        "bench step", "_factors": fac}
+    for key, f in sorted(fam.items(), key=lambda kv: -kv[1]["t"]):
+        c = f["c"]
+        t = f["t"] * 1e-6
+        flops, byts = work.get(key, [0.0, 0.0])
+        mfma_bound = flops > 0 and flops / max(byts, 1.0) > 20
+        if key in work and t > 0:
+            frac = (flops / t / PEAK["f32"]) if mfma_bound else (byts / t / PEAK["hbm"])
+            frac_s = f"{frac:.2f}"
+        else:
+            frac_s = "-"
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (t * CLOCK_HZ * SIMDS) if t > 0 else 0
+        vm = (c["SQ_INSTS_VALU"] / c["SQ_INSTS_MFMA"]) if c.get("SQ_INSTS_MFMA") else None
+        wait = (c["SQ_WAIT_INST_ANY"] / c["SQ_WAVE_CYCLES"]) if c.get("SQ_WAVE_CYCLES") else None
+        confl = (c["SQ_LDS_BANK_CONFLICT"] / c["SQ_INSTS_LDS"]) if c.get("SQ_INSTS_LDS") and \
+            "SQ_LDS_BANK_CONFLICT" in c else None
+        lines.append(
+            f"| {key} | {f['n']} | {f['t']:.1f} | {'MFMA' if mfma_bound else 'HBM'} | {frac_s} | "
+            f"{busy:.2f} | {'-' if vm is None else f'{vm:.1f}'} | "
+            f"{'-' if wait is None else f'{wait:.2f}'} | "
+            f"{'-' if confl is None else f'{confl:.2f}'} | {f['hbm'] / 1e6:.1f} | "
+            f"{byts / 1e6:.1f} | {f['hbm'] / byts if byts else 0:.2f} |")
+        traffic[key] = round(f["hbm"] / f["n"])
+    if args.traffic_out:
+        Path(args.traffic_out).write_text(json.dumps(traffic, indent=1, sort_keys=True) + "\n")
+    return "\n".join(lines) + "\n"
+
+
 def copy(args) -> None:
     import torch
     n = args.mib * 1024 * 1024 // 4
@@ -226,6 +373,17 @@ def main(argv=None) -> None:
         f.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
     f.add_argument("--copy-mib", type=int, required=True)
     f.add_argument("--out")
+    q = sub.add_parser("pmc")
+    q.add_argument("--log", required=True, help="launch log of bench.py --profile-step")
+    q.add_argument("--trace", required=True, help="rocprofv3 --kernel-trace run of the same step")
+    q.add_argument("--passes", nargs="+", required=True, help="rocprofv3 --pmc runs (SQ counters)")
+    for k in ("fetch", "write", "copy_fetch", "copy_write"):
+        q.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
+    q.add_argument("--copy-mib", type=int, required=True)
+    q.add_argument("--cmd", action="append", required=True)
+    q.add_argument("--title", default="per-family counters of one bench step")
+    q.add_argument("--traffic-out")
+    q.add_argument("--out")
     a = ap.parse_args(argv)
     if a.cmd_name in ("trace", "stats"):
         text = trace(a) if a.cmd_name == "trace" else stats(a)
@@ -234,6 +392,11 @@ def main(argv=None) -> None:
         print(text)
     elif a.cmd_name == "copy":
         copy(a)
+    elif a.cmd_name == "pmc":
+        text = pmc(a)
+        if a.out:
+            Path(a.out).write_text(text)
+        print(text)
     else:
         d = traffic(a)
         if a.out:
