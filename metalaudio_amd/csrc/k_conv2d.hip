@@ -77,6 +77,60 @@ __global__ __launch_bounds__(256) void conv2d_unfold_kernel(Conv2DArgs a) {
       make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// Tiled unfold: a workgroup takes 64 consecutive rows n = oh * Wo + ow of U (contiguous in
+// memory, across output rows when Wo is small) x 32 k. Lane c takes row n0 + c; each k = (ic,
+// kh, kw) is then a gather at input (oh * sh - ph + kh * dh, ow * sw - pw + kw * dw), its
+// padding resolved by clamped or mirrored indices and a select, so no load sits under a branch
+// and all eight of a thread's loads are in flight together. The tile is transposed through LDS
+// (row pitch 33: the column-major writes of a wave hit distinct banks) and written as 64 row
+// segments of U of 128 contiguous bytes. Grid (ceil(Ho * Wo / 64), Kp / 32, B).
+constexpr int kUfRows = 64, kUfK = 32, kUfPitch = kUfK + 1;
+__global__ __launch_bounds__(256) void conv2d_unfold_tiled_kernel(Conv2DArgs a) {
+  __shared__ float t[kUfRows * kUfPitch];
+  const int b = blockIdx.z;
+  const int k0 = blockIdx.y * kUfK;
+  const int N = a.Ho * a.Wo;
+  const int n0 = blockIdx.x * kUfRows;
+  const int ks = a.KH * a.KW, K = a.Cin * ks;
+  const float* xb = a.x + (int64_t)b * a.Cin * a.H * a.W;
+  const int tid = threadIdx.x, c = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: the k math below is too
+  const int n = min(n0 + c, N - 1);
+  const int oh = n / a.Wo, ow = n - oh * a.Wo;
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = wave + 4 * j;  // wave-uniform k row
+    const int k = min(k0 + r, K - 1);
+    const int ic = k / ks, rem = k - ic * ks, kh = rem / a.KW, kw = rem - kh * a.KW;
+    int ih = oh * a.sh - a.ph + kh * a.dh, iw = ow * a.sw - a.pw + kw * a.dw;
+    bool zero = k0 + r >= K;
+    if (a.reflect) {
+      ih = reflect_index(ih, a.H);
+      iw = reflect_index(iw, a.W);
+    } else {
+      zero = zero || ih < 0 || ih >= a.H || iw < 0 || iw >= a.W;
+    }
+    ih = min(max(ih, 0), a.H - 1);
+    iw = min(max(iw, 0), a.W - 1);
+    const float q = xb[((int64_t)ic * a.H + ih) * a.W + iw];
+    v[j] = zero ? 0.f : q;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) t[c * kUfPitch + wave + 4 * j] = v[j];
+  __syncthreads();
+  // stores: 64 rows x 8 float4 of k, two per thread (row tid / 8 + 32 i, quad tid % 8)
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rl = (tid >> 3) + 32 * i, kq = 4 * (tid & 7);
+    if (n0 + rl < N) {
+      const float* src = t + rl * kUfPitch + kq;
+      *reinterpret_cast<float4*>(a.u + ((int64_t)b * N + n0 + rl) * a.Kp + k0 + kq) =
+          make_float4(src[0], src[1], src[2], src[3]);
+    }
+  }
+}
+
 // Grid (output plane / 256, Cout, B); 32-bit plane index (host-checked).
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(Conv2DArgs a) {
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
@@ -326,7 +380,10 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
   MNN_REQUIRE(N * (a.Kp / 4) < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
               "conv2d_gemm: unfold too large");
   const dim3 ug((unsigned)cdiv(N * (a.Kp / 4), 256), (unsigned)a.B);
-  if (a.KH == 3 && a.KW == 3)
+  if (a.Kp % kUfK == 0 && a.Kp / kUfK < 65536)
+    launch(c, "conv2d_unfold_f32", conv2d_unfold_tiled_kernel,
+           dim3(cdiv(N, kUfRows), (unsigned)(a.Kp / kUfK), (unsigned)a.B), dim3(256), 0, a);
+  else if (a.KH == 3 && a.KW == 3)
     launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel<3, 3>, ug, dim3(256), 0, a);
   else if (a.KH == 8 && a.KW == 1)
     launch(c, "conv2d_unfold_f32", conv2d_unfold_kernel<8, 1>, ug, dim3(256), 0, a);

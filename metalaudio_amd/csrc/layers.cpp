@@ -1006,11 +1006,12 @@ class EncoderBlockLayer : public Layer {
       k::gn_stats_partial(ctx(s), y_.f32(), (int)B, Cout, lo, norm_->groups(), partials_.f32(),
                           nchunk);
     }
-    norm_->finalize(s, (int)B, nchunk, partials_.f32());
-    if (!d_.rewrite) {
-      k::gn_apply(ctx(s), y_.f32(), out.f32(), (int)B, Cout, lo, norm_->coef(), MNN_ACT_GELU);
+    if (!d_.rewrite) {  // the apply pass merges the partials itself (no finalize launch)
+      norm_->apply_parts(s, y_.f32(), out.f32(), (int)B, lo, partials_.f32(), nchunk,
+                         MNN_ACT_GELU);
       return;
     }
+    norm_->finalize(s, (int)B, nchunk, partials_.f32());
     k::GemmArgs g = rewrite_args((int)B, lo, out.f32());
     g.B = y_.f32();
     g.ldb = lo;
@@ -1307,8 +1308,9 @@ class DecoderBlockLayer : public Layer {
     const int nchunk = k::gn_num_chunks(Cout, G, lo);
     partials_.reserve(sizeof(float) * 3 * B * G * nchunk);
     k::gn_stats_partial(ctx(s), y_.f32(), (int)B, Cout, lo, G, partials_.f32(), nchunk);
-    norm_->finalize(s, (int)B, nchunk, partials_.f32());
-    k::gn_apply(ctx(s), y_.f32(), out->f32(), (int)B, Cout, lo, norm_->coef(), MNN_ACT_GELU);
+    // the apply pass merges the partials itself (no finalize launch)
+    norm_->apply_parts(s, y_.f32(), out->f32(), (int)B, lo, partials_.f32(), nchunk,
+                       MNN_ACT_GELU);
   }
 
  private:
@@ -1626,8 +1628,8 @@ class FreqEncoderBlockLayer : public Layer {
     const int nchunk = k::gn_num_chunks(C, G, L);
     partials.reserve(sizeof(float) * 3 * B * G * nchunk);
     k::gn_stats_partial(ctx(s), y, B, C, L, G, partials.f32(), nchunk);
-    norm->finalize(s, B, nchunk, partials.f32());
-    k::gn_apply(ctx(s), y, out, B, C, L, norm->coef(), MNN_ACT_GELU);
+    // the apply pass merges the partials itself (no finalize launch)
+    norm->apply_parts(s, y, out, B, L, partials.f32(), nchunk, MNN_ACT_GELU);
   }
 
  private:

@@ -91,6 +91,10 @@ CONV_CASES = [
     (2, 4, 48, 64, 32, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),     # unfold + GEMM
     (1, 48, 96, 32, 16, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),
     (1, 4, 48, 256, 40, (8, 1), (4, 1), "reflect", (3, 0), (1, 1), 1),   # HTDemucs (8,1)/(4,1)
+    # one-column kernels: tiled unfold (64 columns x 32 k per workgroup)
+    (2, 3, 16, 70, 67, (8, 1), (4, 1), "explicit", (2, 0), (1, 1), 1),   # zeros, K 24 -> 32, W % 4
+    (1, 48, 96, 64, 130, (8, 1), (4, 1), "reflect", (3, 0), (1, 1), 1),  # 12 k chunks, 3 col tiles
+    (1, 5, 8, 30, 20, (5, 1), (2, 1), "explicit", (2, 0), (2, 1), 1),    # row dilation 2, K 25
     (2, 3, 5, 17, 13, (3, 2), (2, 1), "explicit", (1, 1), (1, 2), 1),
     (1, 6, 10, 9, 11, (3, 3), (1, 1), "same", (0, 0), (1, 1), 1),
     (1, 5, 7, 12, 10, (2, 2), (1, 1), "same", (0, 0), (1, 1), 1),          # even kernel "same"
