@@ -467,6 +467,22 @@ mnn_status mnn_cross_transformer_create(mnn_device dev, int embed_dim, int num_h
                                         int num_layers, float layer_scale,
                                         mnn_precision precision, mnn_layer* out);
 
+/* CrossTransformerEncoder(device:embedDim:numHeads:ffnDim:numLayers:) with the reference class's
+ * own layer structure (TransformerLayer, Transformer.swift:370-560; layer loop :626-667). Each
+ * layer: T += 2*SA_t(LN_ts T) (the reference adds this residual twice, :459-460);
+ * F += SA_f(LN_fs F); tn = LN_tc T, fn = LN_fc F; T += CA_t(tn, fn); F += CA_f(fn, tn);
+ * T += FFN_t(LN_tf T); F += FFN_f(LN_ff F). No LayerScale. forward through
+ * mnn_layer_forward_cross(time, freq, time_out, freq_out); [S, E] or [B, S, E] per branch.
+ * Weights as TransformerLayer.loadWeights (:529-557): "layers.{i}.{norm_time_self,
+ * norm_freq_self, norm_time_cross, norm_freq_cross, norm_time_ffn, norm_freq_ffn}.{weight,bias}",
+ * "layers.{i}.{self_attn_time, self_attn_freq, cross_attn_time, cross_attn_freq}.{in_proj_weight,
+ * in_proj_bias, out_proj.weight, out_proj.bias}", "layers.{i}.{ffn_time, ffn_freq}.{linear1,
+ * linear2}.{weight,bias}". mnn_cross_transformer_create is the HTDemucs-structured bottleneck of
+ * the benchmark configuration instead. */
+mnn_status mnn_cross_transformer_encoder_create(mnn_device dev, int embed_dim, int num_heads,
+                                                int ffn_dim, int num_layers,
+                                                mnn_precision precision, mnn_layer* out);
+
 mnn_status mnn_layer_destroy(mnn_layer layer);
 /* loadWeights / loadParameters: copies `count` floats into the named parameter.
  * NaN/Inf are rejected with MNN_ERR_INVALID_CONFIGURATION (validateWeights, NNLayer.swift:27-59);

@@ -175,6 +175,8 @@ SIGNATURES = {
     "mnn_transformer_layer_create": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
     "mnn_cross_transformer_create": (
         C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_int, PP]),
+    "mnn_cross_transformer_encoder_create": (
+        C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, PP]),
     "mnn_safetensors_open": (C.c_int, [C.c_char_p, PP]),
     "mnn_safetensors_close": (C.c_int, [P]),
     "mnn_safetensors_tensor_count": (C.c_int, [P, IP]),

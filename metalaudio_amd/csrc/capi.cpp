@@ -951,6 +951,12 @@ mnn_status mnn_cross_transformer_create(mnn_device dev, int embed_dim, int num_h
       make_cross_transformer(d, embed_dim, num_heads, ffn_dim, num_layers, layer_scale, prec));
 }
 
+mnn_status mnn_cross_transformer_encoder_create(mnn_device dev, int embed_dim, int num_heads,
+                                                int ffn_dim, int num_layers, mnn_precision prec,
+                                                mnn_layer* out) {
+  MNN_CREATE(make_cross_transformer_encoder(d, embed_dim, num_heads, ffn_dim, num_layers, prec));
+}
+
 mnn_status mnn_layer_destroy(mnn_layer layer) {
   return guard([&] {
     if (!layer) return;

@@ -585,6 +585,9 @@ class MHALayer : public Layer {
       bin_ = &add_param("in_proj_bias", 3LL * embed);
       bout_ = &add_param("out_proj_bias", embed);
     }
+    // the names SafeTensorsLoader.loadAttentionWeights reads (SafeTensorsLoader.swift:335-339)
+    aliases_["out_proj.weight"] = "out_proj_weight";
+    aliases_["out_proj.bias"] = "out_proj_bias";
     // Default weights: identity-like Q/K/V/out projections (Attention.swift initializeDefaultWeights)
     std::vector<float> wi(3LL * embed * embed, 0.f), wo((int64_t)embed * embed, 0.f);
     for (int p = 0; p < 3; ++p)
@@ -1975,6 +1978,124 @@ class CrossTransformerImpl : public Layer {
 // epilogue, then one apply pass merges the partials and writes act(GroupNorm(y)) into the last
 // layer's buffer. Results are those of the layers run one by one (GELU's +-10 clamp and the
 // tanh form agree to float precision beyond |x| = 10).
+// CrossTransformerEncoder with the reference class's own layer structure (TransformerLayer,
+// Transformer.swift:370-560; the encoder's layer loop :626-667). Per layer, in this order:
+//   T += 2 * SA_t(LN_ts(T))   the reference adds the time self-attention residual twice (:459-460)
+//   F += SA_f(LN_fs(F))
+//   tn = LN_tc(T); fn = LN_fc(F)
+//   T += CA_t(tn, fn)         time queries, freq keys / values
+//   F += CA_f(fn, tn)         freq queries; tn is the time state from before the line above
+//   T += FFN_t(LN_tf(T)); F += FFN_f(LN_ff(F))
+// No LayerScale. Residuals go through the GEMM epilogues (out-projection, FFN second linear) as
+// C = R + rscale * (acc + bias), the doubled one with rscale = 2. Weight names follow
+// TransformerLayer.loadWeights (:529-557): layers.{i}.{norm_time_self, norm_freq_self,
+// norm_time_cross, norm_freq_cross, norm_time_ffn, norm_freq_ffn}.{weight,bias},
+// layers.{i}.{self_attn_time, self_attn_freq, cross_attn_time, cross_attn_freq}.{in_proj_weight,
+// in_proj_bias, out_proj.weight, out_proj.bias}, layers.{i}.{ffn_time, ffn_freq}.{linear1,
+// linear2}.{weight,bias}. Batched inputs [B, S, E] run every batch element (the reference sizes its
+// work buffers for one).
+class CrossTransformerEncoderImpl : public Layer {
+ public:
+  CrossTransformerEncoderImpl(Device* d, int embed, int heads, int ffn, int layers,
+                              mnn_precision prec)
+      : Layer(d), E_(embed) {
+    MNN_REQUIRE(layers > 0, MNN_ERR_INVALID_CONFIGURATION,
+                "CrossTransformerEncoder: num_layers <= 0");
+    for (int i = 0; i < layers; ++i) {
+      auto L = std::make_unique<Lyr>();
+      for (auto* n : {&L->nts, &L->nfs, &L->ntc, &L->nfc, &L->ntf, &L->nff})
+        *n = std::make_unique<LayerNormLayer>(d, embed, 1e-5f);
+      for (auto* a : {&L->sat, &L->saf, &L->cat, &L->caf})
+        *a = std::make_unique<MHALayer>(d, embed, heads, true, prec);
+      L->fft = std::make_unique<FeedForwardLayer>(d, embed, ffn, prec);
+      L->fff = std::make_unique<FeedForwardLayer>(d, embed, ffn, prec);
+      layers_.push_back(std::move(L));
+    }
+    std::vector<float> two(embed, 2.f);
+    two_.reserve(sizeof(float) * embed);
+    HIP_CHECK(hipMemcpy(two_.ptr, two.data(), sizeof(float) * embed, hipMemcpyHostToDevice));
+  }
+  const char* kind() const override { return "CrossTransformerEncoder"; }
+  Shape input_shape() const override { return {0, E_}; }
+  Shape output_shape() const override { return {0, E_}; }
+  Shape infer_output(const Shape& in) const override {
+    MNN_REQUIRE((in.size() == 2 || in.size() == 3) && in.back() == E_, MNN_ERR_SHAPE_MISMATCH,
+                "CrossTransformerEncoder: expected [S, " << E_ << "] or [B, S, " << E_ << "]");
+    return in;
+  }
+  void load(const std::string& name, const float* data, size_t n) override {
+    MNN_REQUIRE(name.rfind("layers.", 0) == 0, MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: unknown parameter '" << name << "'");
+    const size_t p1 = name.find('.', 7);
+    MNN_REQUIRE(p1 != std::string::npos, MNN_ERR_INVALID_ARGUMENT, "bad parameter name " << name);
+    const int li = std::atoi(name.substr(7, p1 - 7).c_str());
+    MNN_REQUIRE(li >= 0 && li < (int)layers_.size(), MNN_ERR_INVALID_ARGUMENT,
+                "layer index out of range in " << name);
+    const std::string rest = name.substr(p1 + 1);
+    const size_t dot = rest.find('.');
+    MNN_REQUIRE(dot != std::string::npos, MNN_ERR_INVALID_ARGUMENT, "bad parameter name " << name);
+    const std::string part = rest.substr(0, dot), tail = rest.substr(dot + 1);
+    Lyr& L = *layers_[li];
+    const std::map<std::string, Layer*> parts = {
+        {"norm_time_self", L.nts.get()},  {"norm_freq_self", L.nfs.get()},
+        {"norm_time_cross", L.ntc.get()}, {"norm_freq_cross", L.nfc.get()},
+        {"norm_time_ffn", L.ntf.get()},   {"norm_freq_ffn", L.nff.get()},
+        {"self_attn_time", L.sat.get()},  {"self_attn_freq", L.saf.get()},
+        {"cross_attn_time", L.cat.get()}, {"cross_attn_freq", L.caf.get()},
+        {"ffn_time", L.fft.get()},        {"ffn_freq", L.fff.get()}};
+    const auto it = parts.find(part);
+    MNN_REQUIRE(it != parts.end(), MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: unknown parameter '" << name << "'");
+    it->second->load(tail, data, n);
+  }
+  void forward(const Tensor&, Tensor&, Stream&) override {
+    fail(MNN_ERR_INVALID_CONFIGURATION,
+         "CrossTransformerEncoder needs two inputs: use forward_cross(time, freq, ...)");
+  }
+  void forward_cross(const Tensor* t, const Tensor* f, Tensor* to, Tensor* fo,
+                     Stream& s) override {
+    MNN_REQUIRE(t && f && to && fo, MNN_ERR_INVALID_ARGUMENT,
+                "CrossTransformerEncoder: time, freq, time_out and freq_out are required");
+    check_out(*to, infer_output(t->shape));
+    check_out(*fo, infer_output(f->shape));
+    int64_t B, St, E, Bf, Sf, Ef;
+    split_bse(t->shape, B, St, E);
+    split_bse(f->shape, Bf, Sf, Ef);
+    MNN_REQUIRE(B == Bf, MNN_ERR_SHAPE_MISMATCH, "time and freq batch sizes differ");
+    const int64_t rt = B * St, rf = B * Sf;
+    ht_.reserve(sizeof(float) * rt * E);
+    hf_.reserve(sizeof(float) * rf * E);
+    if (to->data != t->data) k::copy_bytes(ctx(s), t->data, to->data, rt * E * 4);
+    if (fo->data != f->data) k::copy_bytes(ctx(s), f->data, fo->data, rf * E * 4);
+    float *T = to->f32(), *F = fo->f32(), *ht = ht_.f32(), *hf = hf_.f32();
+    for (auto& Lp : layers_) {
+      Lyr& L = *Lp;
+      L.nts->run(T, rt, ht, s);
+      L.sat->run(ht, (int)St, nullptr, 0, (int)B, T, T, two_.f32(), s);
+      L.nfs->run(F, rf, hf, s);
+      L.saf->run(hf, (int)Sf, nullptr, 0, (int)B, F, F, nullptr, s);
+      L.ntc->run(T, rt, ht, s);
+      L.nfc->run(F, rf, hf, s);
+      L.cat->run(ht, (int)St, hf, (int)Sf, (int)B, T, T, nullptr, s);
+      L.caf->run(hf, (int)Sf, ht, (int)St, (int)B, F, F, nullptr, s);
+      L.ntf->run(T, rt, ht, s);
+      L.fft->run(ht, rt, T, T, nullptr, s);
+      L.nff->run(F, rf, hf, s);
+      L.fff->run(hf, rf, F, F, nullptr, s);
+    }
+  }
+
+ private:
+  struct Lyr {
+    std::unique_ptr<LayerNormLayer> nts, nfs, ntc, nfc, ntf, nff;
+    std::unique_ptr<MHALayer> sat, saf, cat, caf;
+    std::unique_ptr<FeedForwardLayer> fft, fff;
+  };
+  int E_;
+  std::vector<std::unique_ptr<Lyr>> layers_;
+  DevBuf two_, ht_, hf_;
+};
+
 int fused_chain_length(const std::vector<Layer*>& v, size_t i) {
   if (i + 1 >= v.size()) return 1;
   auto* c = dynamic_cast<Conv1DLayer*>(v[i]);
@@ -2078,6 +2199,10 @@ std::unique_ptr<Layer> make_decoder_block(Device* d, const mnn_decoder_block_des
 std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, int ffn,
                                               float layer_scale, mnn_precision prec) {
   return std::make_unique<TransformerLayerImpl>(d, embed, heads, ffn, layer_scale, prec);
+}
+std::unique_ptr<Layer> make_cross_transformer_encoder(Device* d, int embed, int heads, int ffn,
+                                                     int layers, mnn_precision prec) {
+  return std::make_unique<CrossTransformerEncoderImpl>(d, embed, heads, ffn, layers, prec);
 }
 std::unique_ptr<Layer> make_cross_transformer(Device* d, int embed, int heads, int ffn,
                                               int layers, float layer_scale, mnn_precision prec) {

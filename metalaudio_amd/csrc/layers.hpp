@@ -76,6 +76,9 @@ std::unique_ptr<Layer> make_transformer_layer(Device* d, int embed, int heads, i
                                               float layer_scale, mnn_precision prec);
 std::unique_ptr<Layer> make_cross_transformer(Device* d, int embed, int heads, int ffn,
                                               int layers, float layer_scale, mnn_precision prec);
+// The reference CrossTransformerEncoder's own layer structure (self + cross + FFN in every layer).
+std::unique_ptr<Layer> make_cross_transformer_encoder(Device* d, int embed, int heads, int ffn,
+                                                     int layers, mnn_precision prec);
 
 // Sequential fusion (layers.cpp): the number of layers from index i that run as one fused
 // group (1 = no fusion), and the fused run (y: the first layer's buffer, out: the last one's).

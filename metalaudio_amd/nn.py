@@ -28,7 +28,7 @@ __all__ = [
     "Conv2D", "DynamicConv2D", "ConvTranspose2D", "DynamicConvTranspose2D",
     "FreqUNetEncoderBlock2D", "FreqUNetDecoderBlock2D", "unet_padding_2d", "unet_bottleneck_2d",
     "STFT", "WINDOWS", "Separator", "STEM_NAMES",
-    "mfma_probe",
+    "mfma_probe", "MetalNNCrossTransformerEncoder",
 ]
 
 
@@ -956,6 +956,18 @@ class CrossTransformerEncoder(Layer):
                       stream: Optional[Stream] = None) -> None:
         check(lib().mnn_layer_forward_cross(self.handle, time.handle, freq.handle,
                                             time_out.handle, freq_out.handle, _sh(stream)))
+
+
+class MetalNNCrossTransformerEncoder(CrossTransformerEncoder):
+    """CrossTransformerEncoder with the reference class's own layer structure (Transformer.swift:
+    370-667): every layer self-attention (the time residual added twice, as the reference does),
+    cross-attention both ways and an FFN per branch, six LayerNorms, no LayerScale; weights
+    layers.{i}.{norm_time_self|...|self_attn_time|...|ffn_freq}.*"""
+
+    def __init__(self, device, embed_dim, num_heads, ffn_dim, num_layers, precision="f32"):
+        Layer.__init__(self, device, _create(lib().mnn_cross_transformer_encoder_create,
+                                             device.handle, embed_dim, num_heads, ffn_dim,
+                                             num_layers, PRECISION[precision]))
 
 
 class Sequential:

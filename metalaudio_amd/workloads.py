@@ -118,6 +118,41 @@ def config4(stress: bool = False, samples: int = CHUNK_SAMPLES, batch: int = 1) 
     return {"x": x, "levels": levels}
 
 
+def cross_encoder_metalnn(batch: int, time_len: int, freq_len: int, embed: int, heads: int,
+                          ffn: int, layers: int, seed: int = 1006) -> dict:
+    """Inputs and weights for the reference-structured CrossTransformerEncoder (every layer self +
+    cross + FFN per branch), reference names (TransformerLayer.loadWeights), projections scaled
+    by 1/sqrt(fan_in) so that every sub-block's update is of the order of its input."""
+    r = np.random.Generator(np.random.PCG64(seed))
+    E = embed
+
+    def w(shape, fan_in):
+        return (r.standard_normal(shape) / np.sqrt(fan_in)).astype(np.float32)
+
+    def b(n):
+        return (0.1 * r.standard_normal(n)).astype(np.float32)
+    p = {}
+    for i in range(layers):
+        L = f"layers.{i}."
+        for n in ("norm_time_self", "norm_freq_self", "norm_time_cross", "norm_freq_cross",
+                  "norm_time_ffn", "norm_freq_ffn"):
+            p[L + n + ".weight"] = (1.0 + 0.1 * r.standard_normal(E)).astype(np.float32)
+            p[L + n + ".bias"] = b(E)
+        for a in ("self_attn_time", "self_attn_freq", "cross_attn_time", "cross_attn_freq"):
+            p[L + a + ".in_proj_weight"] = w((3 * E, E), E)
+            p[L + a + ".in_proj_bias"] = b(3 * E)
+            p[L + a + ".out_proj.weight"] = w((E, E), E)
+            p[L + a + ".out_proj.bias"] = b(E)
+        for f in ("ffn_time", "ffn_freq"):
+            p[L + f + ".linear1.weight"] = w((ffn, E), E)
+            p[L + f + ".linear1.bias"] = b(ffn)
+            p[L + f + ".linear2.weight"] = w((E, ffn), ffn)
+            p[L + f + ".linear2.bias"] = b(E)
+    return {"time": r.standard_normal((batch, time_len, E)).astype(np.float32),
+            "freq": r.standard_normal((batch, freq_len, E)).astype(np.float32),
+            "params": p, "embed": E, "heads": heads, "ffn": ffn, "layers": layers}
+
+
 def config5(stress: bool = False, batch: int = T5_BATCH, time_len: int = T5_TIME_LEN,
             freq_len: int = T5_FREQ_LEN, layers: int = T5_LAYERS) -> dict:
     """Cross-domain bottleneck: E 384, H 8, FFN 1536, LayerScale 1e-4, self/cross alternating."""

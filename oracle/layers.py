@@ -12,6 +12,7 @@ __all__ = [
     "encoder_block",
     "time_encoder", "conv_transpose1d", "conv_transpose1d_gather", "decoder_block", "unet_padding",
     "unet_bottleneck_length", "time_unet", "transformer_layer", "cross_transformer",
+    "cross_transformer_metalnn",
     "reflect_index", "conv2d", "conv2d_output_size", "conv_transpose2d", "freq_encoder_block",
     "freq_decoder_block", "unet_padding_2d",
 ]
@@ -429,6 +430,45 @@ def cross_transformer(time, freq, p, num_layers, num_heads, dtype=np.float64):
             Tn = Tn + _as(p[pt + "gamma_2.scale"], dtype) * ffn(ln(Tn, pt + "norm3"), pt)
             Fn = Fn + _as(p[pf + "gamma_2.scale"], dtype) * ffn(ln(Fn, pf + "norm3"), pf)
             T, F = Tn, Fn
+    return T, F
+
+
+def cross_transformer_metalnn(time, freq, p, num_layers, num_heads, dtype=np.float64):
+    """CrossTransformerEncoder with the reference class's own layer structure: the encoder runs
+    its layers in order (Transformer.swift:626-667; the copies between layers are plain copies),
+    each layer being TransformerLayer.forward(timeInput:freqInput:...) (:441-498):
+      1. T += SA_t(LN_ts T), the residual added twice (:459-460, two addResidual calls);
+      2. F += SA_f(LN_fs F);
+      3. tn = LN_tc T, fn = LN_fc F; T += CA_t(tn, fn);
+      4. F += CA_f(fn, tn) (tn from before step 3's update);
+      5. T += FFN_t(LN_tf T); 6. F += FFN_f(LN_ff F).
+    No LayerScale. Names as TransformerLayer.loadWeights (:529-557)."""
+    T = _as(time, dtype)
+    F = _as(freq, dtype)
+
+    def ln(x, pre):
+        return layer_norm(x, p[pre + ".weight"], p[pre + ".bias"], dtype=dtype)
+
+    def ffn(x, pre):
+        return feed_forward(x, p[pre + ".linear1.weight"], p[pre + ".linear1.bias"],
+                            p[pre + ".linear2.weight"], p[pre + ".linear2.bias"], dtype=dtype)
+
+    def attn(q, kv, pre):  # SafeTensorsLoader.loadAttentionWeights names (:335-339)
+        return mha(q, kv, p[pre + ".in_proj_weight"], p[pre + ".in_proj_bias"],
+                   p[pre + ".out_proj.weight"], p[pre + ".out_proj.bias"], num_heads, dtype)
+
+    for i in range(num_layers):
+        L = f"layers.{i}."
+        a = attn(ln(T, L + "norm_time_self"), None, L + "self_attn_time")
+        T = T + a
+        T = T + a
+        F = F + attn(ln(F, L + "norm_freq_self"), None, L + "self_attn_freq")
+        tn = ln(T, L + "norm_time_cross")
+        fn = ln(F, L + "norm_freq_cross")
+        T = T + attn(tn, fn, L + "cross_attn_time")
+        F = F + attn(fn, tn, L + "cross_attn_freq")
+        T = T + ffn(ln(T, L + "norm_time_ffn"), L + "ffn_time")
+        F = F + ffn(ln(F, L + "norm_freq_ffn"), L + "ffn_freq")
     return T, F
 
 

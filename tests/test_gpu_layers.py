@@ -458,6 +458,41 @@ def test_cross_transformer_parity_strong_layerscale(dev, stream):
     assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
 
 
+@pytest.mark.parametrize("B,St,Sf,E,H,ffn,layers", [
+    (2, 150, 260, 96, 2, 192, 2),    # head dim 48: the fused attention kernel
+    (1, 97, 64, 64, 4, 128, 3),      # head dim 16: the generic attention kernel
+    (1, 336, 672, 384, 8, 1536, 1),  # the config-5 widths
+])
+def test_cross_transformer_encoder_metalnn_parity(dev, stream, B, St, Sf, E, H, ffn, layers):
+    """The reference-structured CrossTransformerEncoder (every layer self + cross + FFN per branch,
+    the time self-attention residual added twice, Transformer.swift:441-498) with weights loaded
+    by the reference's names, against the oracle; every sub-block's update is of the order of its
+    input, so a dropped or misordered term shows."""
+    say(f"reference-structured cross transformer B={B} St={St} Sf={Sf} E={E} H={H} L={layers}")
+    cfg = workloads.cross_encoder_metalnn(B, St, Sf, E, H, ffn, layers)
+    ct = nn.MetalNNCrossTransformerEncoder(dev, E, H, ffn, layers)
+    ct.load_state(cfg["params"])
+    t = cfg["time"] if B > 1 else cfg["time"][0]  # [S, E] for batch 1, as the reference takes it
+    f = cfg["freq"] if B > 1 else cfg["freq"][0]
+    tt, ft = nn.Tensor.from_numpy(dev, t), nn.Tensor.from_numpy(dev, f)
+    to, fo = nn.Tensor(dev, tt.shape), nn.Tensor(dev, ft.shape)
+    ct.forward_cross(tt, ft, to, fo, stream)
+    stream.sync(60000)
+    rt, rf = oracle.cross_transformer_metalnn(t, f, cfg["params"], layers, H)
+    assert_close(to.to_numpy(), rt, ATOL, RTOL, "time branch")
+    assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
+
+
+def test_cross_transformer_encoder_metalnn_errors(dev, stream):
+    ct = nn.MetalNNCrossTransformerEncoder(dev, 32, 4, 64, 2)
+    with pytest.raises(nn.MNNError):
+        ct.load_weights_named("layers.0.norm_time_selff.weight", np.ones(32, np.float32))
+    with pytest.raises(nn.MNNError):
+        ct.load_weights_named("layers.2.norm_time_self.weight", np.ones(32, np.float32))
+    with pytest.raises(nn.MNNError):
+        nn.MetalNNCrossTransformerEncoder(dev, 30, 4, 64, 2)  # embed not divisible by heads
+
+
 # ----------------------------------------------------------------------------- Sequential / errors
 def test_sequential_pingpong_and_forward(dev, stream):
     """ModelTests.swift:114-162: 6 same-shape layers use <= 2 buffers; 3 shapes use 3."""

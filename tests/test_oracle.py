@@ -242,6 +242,70 @@ def test_transformer_layer_matches_torch_encoder_layer():
                                atol=1e-9)
 
 
+def _metalnn_encoder_torch(cfg, double_time_self=True):
+    """The reference CrossTransformerEncoder's layer loop (Transformer.swift:441-498, 626-667)
+    composed from torch library routines: F.layer_norm, torch's MultiheadAttention with the
+    packed in_proj, and Linear -> tanh GELU -> Linear."""
+    p, E, H = cfg["params"], cfg["embed"], cfg["heads"]
+
+    def ln(x, pre):
+        return F.layer_norm(x, (E,), t64(p[pre + ".weight"]), t64(p[pre + ".bias"]), 1e-5)
+
+    def attn(q, kv, pre):
+        m = _torch_mha(E, H, p[pre + ".in_proj_weight"], p[pre + ".in_proj_bias"],
+                       p[pre + ".out_proj.weight"], p[pre + ".out_proj.bias"])
+        return m(q, kv, kv, need_weights=False)[0]
+
+    def ffn(x, pre):
+        h = F.gelu(F.linear(x, t64(p[pre + ".linear1.weight"]), t64(p[pre + ".linear1.bias"])),
+                   approximate="tanh")
+        return F.linear(h, t64(p[pre + ".linear2.weight"]), t64(p[pre + ".linear2.bias"]))
+
+    with torch.no_grad():
+        T, Fr = t64(cfg["time"]), t64(cfg["freq"])
+        for i in range(cfg["layers"]):
+            L = f"layers.{i}."
+            h = ln(T, L + "norm_time_self")
+            a = attn(h, h, L + "self_attn_time")
+            T = T + (2.0 if double_time_self else 1.0) * a
+            h = ln(Fr, L + "norm_freq_self")
+            Fr = Fr + attn(h, h, L + "self_attn_freq")
+            tn, fn = ln(T, L + "norm_time_cross"), ln(Fr, L + "norm_freq_cross")
+            T = T + attn(tn, fn, L + "cross_attn_time")
+            Fr = Fr + attn(fn, tn, L + "cross_attn_freq")
+            T = T + ffn(ln(T, L + "norm_time_ffn"), L + "ffn_time")
+            Fr = Fr + ffn(ln(Fr, L + "norm_freq_ffn"), L + "ffn_freq")
+    return T.numpy(), Fr.numpy()
+
+
+def test_cross_transformer_metalnn_matches_torch_composition():
+    """The reference-structured encoder against torch library routines; the same composition with
+    the time self-attention residual added once (the plausible 'fix' of the reference) differs."""
+    cfg = workloads.cross_encoder_metalnn(batch=2, time_len=13, freq_len=21, embed=16, heads=4,
+                                          ffn=32, layers=2)
+    T, Fq = oracle.cross_transformer_metalnn(cfg["time"], cfg["freq"], cfg["params"],
+                                             cfg["layers"], cfg["heads"])
+    Tt, Ft = _metalnn_encoder_torch(cfg)
+    np.testing.assert_allclose(T, Tt, rtol=1e-9, atol=1e-9)  # both fp64
+    np.testing.assert_allclose(Fq, Ft, rtol=1e-9, atol=1e-9)
+    T1, _ = _metalnn_encoder_torch(cfg, double_time_self=False)
+    assert np.max(np.abs(T1 - T)) > 1e-2
+
+
+def test_cross_transformer_metalnn_identity_when_updates_vanish():
+    """Every sub-block adds to its branch: with the out-projections and the FFN's second linear
+    zeroed, the encoder returns its inputs exactly."""
+    cfg = workloads.cross_encoder_metalnn(batch=1, time_len=7, freq_len=9, embed=8, heads=2,
+                                          ffn=16, layers=2)
+    p = dict(cfg["params"])
+    for k in p:
+        if ".out_proj." in k or ".linear2." in k:
+            p[k] = np.zeros_like(p[k])
+    T, Fq = oracle.cross_transformer_metalnn(cfg["time"], cfg["freq"], p, 2, cfg["heads"])
+    np.testing.assert_array_equal(T, cfg["time"].astype(np.float64))
+    np.testing.assert_array_equal(Fq, cfg["freq"].astype(np.float64))
+
+
 def test_cross_transformer_matches_torch_composition():
     """Config-5 structure composed from torch library routines with strong LayerScale."""
     cfg = workloads.config5(stress=True, batch=1, time_len=21, freq_len=37, layers=3)
