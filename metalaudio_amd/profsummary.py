@@ -89,10 +89,14 @@ def _short(name: str) -> str:
 
 def _family(name: str) -> str:
     if "gemm_nk_lds_kernel" in name:
-        epi = name.replace(" ", "").rsplit(",", 1)[-1]
-        if epi == "1>":
+        # template arguments: WMW, WNW, WM, WN, S, EPI[, BF]
+        args = name[name.find("<") + 1:name.rfind(">")].replace(" ", "").split(",")
+        epi = args[5] if len(args) > 5 else ""
+        if len(args) > 6 and args[6] == "true":
+            return "gemm_bf16_mfma_nk"
+        if epi == "1":
             return "enc_rewrite_f32"  # the GLU epilogue instantiation
-        if epi == "2>":
+        if epi == "2":
             return "convt_f32_mfma"  # the transposed-conv epilogue instantiation
     for key, fam in FAMILIES:
         if key in name:

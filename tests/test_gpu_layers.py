@@ -156,7 +156,10 @@ def test_groupnorm_parity(dev, stream, B, C, L, G, act):
 
 
 @pytest.mark.parametrize("rows,F", [(4, 4), (1000, 384), (333, 512), (2048, 2048), (17, 100),
-                                    (3, 384), (257, 128), (10752, 384)])
+                                    (3, 384), (257, 128), (10752, 384),
+                                    # every width of the 16-lanes-per-row kernel (F = 64 * NV),
+                                    # row counts that leave a partial last wave
+                                    (65, 64), (130, 192), (7, 320), (1, 448)])
 def test_layernorm_parity(dev, stream, rows, F):
     say(f"layernorm {rows}x{F}")
     x = (RNG.standard_normal((rows, F)) * 2 + 0.3).astype(np.float32)
