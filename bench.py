@@ -376,7 +376,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     # config 1: Conv1D 2->48 k8 s4 -> GroupNorm(1) -> GELU (HBM-bound; bytes = x + y)
     c1 = W.config1()
     # as the reference composes it: Sequential [Conv1D, GroupNorm, GELU] (run as one fused
-    # group: the conv with GroupNorm statistics in its epilogue, then one apply pass)
+    # launch: each workgroup keeps its conv tile in registers, the workgroups exchange their
+    # GroupNorm statistics partials, and each writes its normalised tile)
     conv = nn.Conv1D(dev, 2, 48, 8, stride=4, padding=0, input_length=44100)
     conv.load_weights(c1["conv_w"], c1["conv_b"])
     gn = nn.GroupNorm(dev, 1, 48)

@@ -36,6 +36,13 @@ mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t ou
 mnn_status mnn_debug_set_launch_log(mnn_device dev, int enable);
 mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* needed);
 
+/* Bound of the grid-wide wait in one-launch kernels (the Conv1D -> GroupNorm(1) chain of a
+ * Sequential): the number of times a workgroup polls for the other workgroups' statistics before
+ * it computes them itself. The result is the same either way; 0 makes every workgroup that does
+ * not find every partial on its first look take the self-computing path, which the tests use to
+ * check it. *previous (may be null) receives the old bound; the default is 65536. */
+mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previous);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1161,6 +1161,15 @@ mnn_status mnn_debug_set_launch_log(mnn_device dev, int enable) {
   });
 }
 
+mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previous) {
+  return guard([&] {
+    MNN_REQUIRE(polls >= 0, MNN_ERR_INVALID_ARGUMENT, "polls must be >= 0, got " << polls);
+    Device* d = D(dev);
+    const int old = d->grid_spin_limit.exchange(polls);
+    if (previous) *previous = old;
+  });
+}
+
 mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* needed) {
   return guard([&] {
     MNN_REQUIRE(needed, MNN_ERR_INVALID_ARGUMENT, "needed is required");

@@ -82,6 +82,8 @@ struct Device {
   // launch log (a profiling aid): one line per launch, "name grid.x grid.y grid.z block.x"
   std::atomic<bool> launch_log{false};
   std::vector<std::string> launches;  // guarded by timing_mu
+  // polls a workgroup makes in a grid-wide wait before it computes what it waits for itself
+  std::atomic<int> grid_spin_limit{1 << 16};
 
   void make_current() const { (void)hipSetDevice(ordinal); }
   void check_alive() const {

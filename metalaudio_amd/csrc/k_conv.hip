@@ -9,6 +9,7 @@
 //
 // One thread per output position; each thread produces a block of COB output channels so the
 // input window is loaded once per block and every output is written once, coalesced along t.
+#include <algorithm>
 #include <type_traits>
 
 #include "device_utils.hpp"
@@ -125,18 +126,18 @@ __device__ __forceinline__ void load_window(const ConvParams& p, const float* __
 // caller can put its own loads in flight between the two and wait once for all of them. Every
 // load reads a valid global address (a null vector reads the weights instead and its value is
 // replaced by the fill), so no load sits under a branch or behind a pointer select.
-template <int CK, int COB, int NX>
+template <int CK, int COB, int NX, int NT = kThreads>
 struct ConstStage {
   static_assert(NX >= 1 && NX <= 3, "one to three per-channel vectors");
   static constexpr int N = CK * COB + NX * COB;
-  static constexpr int PER = (N + kThreads - 1) / kThreads;
+  static constexpr int PER = (N + NT - 1) / NT;
   float v[PER];
   __device__ __forceinline__ void fetch(const float* __restrict__ w, int cob0, const float* e0,
                                         const float* e1, const float* e2, float f0, float f1,
                                         float f2) {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int i = threadIdx.x + r * kThreads;
+      const int i = threadIdx.x + r * NT;
       const int iw = min(i, CK * COB - 1);
       const int co = iw / CK, e = iw - co * CK;
       const int q = min(max(i - CK * COB, 0) / COB, NX - 1);
@@ -153,7 +154,7 @@ struct ConstStage {
   __device__ __forceinline__ void put(float* lds) const {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
-      const int i = threadIdx.x + r * kThreads;
+      const int i = threadIdx.x + r * NT;
       if (i < CK * COB) {
         const int co = i / CK, e = i - co * CK;
         lds[e * COB + co] = v[r];
@@ -250,6 +251,22 @@ __global__ __launch_bounds__(kThreads) void conv1d_direct_reg_kernel(ConvParams 
   }
 }
 
+// (count, mean, M2) of one thread's COB values, two passes in registers; zero when the thread's
+// position is past the output
+template <int COB>
+__device__ __forceinline__ void thread_stats(const float (&acc)[COB], bool valid, float& n,
+                                             float& mean, float& m2) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < COB; ++j) s += acc[j];
+  mean = s * (1.f / COB);
+  m2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < COB; ++j) m2 = fmaf(acc[j] - mean, acc[j] - mean, m2);
+  n = valid ? (float)COB : 0.f;
+  if (!valid) mean = m2 = 0.f;
+}
+
 // Pass 1: GroupNorm(1) statistics of conv(x) + bias, one (count, mean, M2) partial per workgroup
 // at parts[(b * nparts + blockIdx.y * gridDim.x + blockIdx.x) * 3]; nothing else is written.
 template <int CK, int COB, bool REFLECT>
@@ -274,15 +291,8 @@ __global__ __launch_bounds__(kThreads) void conv_gn_stats_kernel(ConvParams p,
 #pragma unroll
   for (int j = 0; j < COB; ++j) acc[j] = wt[CK * COB + j];
   window_dot<CK, COB>(xv, wt, acc);
-  // this thread's COB values, two passes in registers
-  float s = 0.f;
-#pragma unroll
-  for (int j = 0; j < COB; ++j) s += acc[j];
-  float mean = s * (1.f / COB), m2 = 0.f;
-#pragma unroll
-  for (int j = 0; j < COB; ++j) m2 = fmaf(acc[j] - mean, acc[j] - mean, m2);
-  float n = valid ? (float)COB : 0.f;
-  if (!valid) mean = m2 = 0.f;
+  float n, mean, m2;
+  thread_stats<COB>(acc, valid, n, mean, m2);
   block_welford(n, mean, m2, red);
   if (threadIdx.x == 0) {
     float* o = parts + ((int64_t)b * gridDim.x * gridDim.y + blockIdx.y * gridDim.x + blockIdx.x) * 3;
@@ -352,6 +362,221 @@ __global__ __launch_bounds__(kThreads) void conv_gn_apply_kernel(
       case 6: store(std::integral_constant<int, 6>{}); break;
       default: store(std::integral_constant<int, 0>{}); break;
     }
+  }
+}
+
+// Both passes in one launch. Each workgroup computes a tile of COB channels x 256 positions of
+// the convolution into registers (SPLIT x 256 threads, COB / SPLIT channels each) and publishes
+// the tile's statistics partial; it then collects every partial of its batch, merges them and
+// writes the normalised output from the registers it kept.
+//
+// The exchange uses no cache maintenance (an acquire fence in every wave and a release fence per
+// workgroup cost more than the rest of the kernel at this size): a partial is two 64-bit words,
+// (kTileTag << 32 | mean bits) and (kTileTag << 32 | M2 bits), each stored and loaded as one
+// relaxed device-scope atomic, so a reader sees either a whole published word or a cleared one,
+// and polls until every word is published. The count of a partial is fixed by the geometry (COB x
+// the tile's valid positions) and is not exchanged.
+//
+// xch layout (64-bit words): word 0 = workgroups out of this launch (low half); slots from word 8,
+// two words per partial, partial (b, v) at slot b * nparts + v. All zero before a launch: the
+// last workgroup out (the count says which) clears the slots and the count, when every workgroup
+// has finished reading them, so the next launch starts from zero again.
+//
+// The host launches this form only when the whole grid can be resident at once. The wait is
+// bounded all the same: a workgroup that has polled spin_limit times without seeing every partial
+// computes every partial of its batch itself (the same code on the same inputs as their owners,
+// so the same bits) and merges those, so each workgroup ends with the same result whatever the
+// scheduling. Launches that share `xch` must not overlap.
+constexpr int kOneMaxParts = 1024;  // partials per batch (LDS: 8 bytes each)
+constexpr int kOneMaxSlots = 4096;  // partials over all batches
+constexpr unsigned kTileTag = 1u;   // high half of a published word (cleared words read 0)
+
+__device__ __forceinline__ void put_tagged(unsigned long long* s, float lo) {
+  __hip_atomic_store(s, ((unsigned long long)kTileTag << 32) | __float_as_uint(lo),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// (mean, M2) of one tile of n values spread over NW waves, two passes over the registers: the
+// mean from a block sum, then M2 about it. Every thread returns the same bits. red: 2 * NW floats
+// of LDS; calls in a loop need no barrier between them (each reads its first half before its
+// second barrier).
+template <int CPT, int NW>
+__device__ __forceinline__ void tile_stats(const float (&acc)[CPT], bool valid, float n,
+                                           float* red, float& mean, float& m2) {
+  const int wid = threadIdx.x >> 6;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) s += acc[j];
+  s = wave_sum_dpp(valid ? s : 0.f);
+  if ((threadIdx.x & 63) == 0) red[wid] = s;
+  lds_barrier();
+  float tot = 0.f;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) tot += red[k];
+  mean = tot / n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) q = fmaf(acc[j] - mean, acc[j] - mean, q);
+  q = wave_sum_dpp(valid ? q : 0.f);
+  if ((threadIdx.x & 63) == 0) red[NW + wid] = q;
+  lds_barrier();
+  m2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < NW; ++k) m2 += red[NW + k];
+}
+
+template <int CK, int COB, int SPLIT, bool REFLECT, int ACT>
+__global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
+    ConvParams p, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ bias, unsigned long long* xch, int spin_limit,
+    const float* __restrict__ gamma, const float* __restrict__ beta, float eps, int act,
+    float* __restrict__ y) {
+  constexpr int NT = kThreads * SPLIT, NW = NT / 64, CPT = COB / SPLIT;
+  static_assert(COB % (4 * SPLIT) == 0, "whole float4 weight groups per thread");
+  using Stage = ConstStage<CK, COB, 3, NT>;
+  __shared__ __attribute__((aligned(16))) float wt[Stage::N];  // weights, bias, gamma, beta
+  __shared__ float red[2 * NW];
+  __shared__ float2 sp[kOneMaxParts];  // (mean, M2) of every partial of this batch
+  __shared__ int s_last;
+  const int b = blockIdx.z, cob0 = blockIdx.y * COB;
+  const int pos = threadIdx.x & (kThreads - 1), part = threadIdx.x / kThreads;  // part: per wave
+  const int t = blockIdx.x * kThreads + pos;
+  const bool valid = t < p.Lout;
+  const int nparts = gridDim.x * gridDim.y;
+  const float* xb = x + (int64_t)b * p.Cin * p.Lin;
+  unsigned* ctl = reinterpret_cast<unsigned*>(xch);
+  unsigned long long* slots = xch + 8 + 2 * (int64_t)b * nparts;
+  Stage st;
+  st.fetch(w, cob0, bias, gamma, beta, 0.f, 1.f, 0.f);
+  float xv[CK];
+  load_window<CK, REFLECT>(p, xb, t, valid, xv);
+  st.put(wt);
+  lds_barrier();
+  float acc[CPT];
+  const int c0 = part * CPT;  // this thread's first channel within the tile
+#pragma unroll
+  for (int j = 0; j < CPT; ++j) acc[j] = wt[CK * COB + c0 + j];
+#pragma unroll
+  for (int e = 0; e < CK; ++e)
+#pragma unroll
+    for (int j4 = 0; j4 < CPT; j4 += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(wt + e * COB + c0 + j4);
+      acc[j4 + 0] = fmaf(xv[e], w4.x, acc[j4 + 0]);
+      acc[j4 + 1] = fmaf(xv[e], w4.y, acc[j4 + 1]);
+      acc[j4 + 2] = fmaf(xv[e], w4.z, acc[j4 + 2]);
+      acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
+    }
+  auto tile_count = [&](int vx) { return (float)(COB * min(kThreads, p.Lout - vx * kThreads)); };
+  {
+    float mean, m2;
+    tile_stats<CPT, NW>(acc, valid, tile_count(blockIdx.x), red, mean, m2);
+    if (threadIdx.x == 0) {
+      const int me = blockIdx.y * gridDim.x + blockIdx.x;
+      put_tagged(slots + 2 * me, mean);
+      put_tagged(slots + 2 * me + 1, m2);
+    }
+  }
+  // collect: every thread polls its share of the partials until all are published
+  bool late = false;
+  for (int polls = 0;; ++polls) {
+    bool ok = true;
+    for (int v = threadIdx.x; v < nparts; v += NT) {
+      const unsigned long long a =
+          __hip_atomic_load(slots + 2 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long c =
+          __hip_atomic_load(slots + 2 * v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ok = ok && (unsigned)(a >> 32) == kTileTag && (unsigned)(c >> 32) == kTileTag;
+      sp[v] = make_float2(__uint_as_float((unsigned)a), __uint_as_float((unsigned)c));
+    }
+    if (!__syncthreads_or(!ok)) break;
+    if (polls >= spin_limit) {
+      late = true;
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (late) {
+    // this workgroup never saw its own partial published: let the store land before the
+    // workgroup can count out (the last one out clears the slots)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // compute every partial of this batch here, each as its owner computes it (weights and bias
+    // read from global memory hold the values the owner staged in LDS; the fmaf order over the
+    // taps is the same)
+    for (int v = 0; v < nparts; ++v) {
+      const int vx = v % gridDim.x, vy = v / gridDim.x;
+      const int tv = vx * kThreads + pos;
+      const int cv = vy * COB + c0;
+      float xw[CK], av[CPT];
+      load_window<CK, REFLECT>(p, xb, tv, tv < p.Lout, xw);
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) av[j] = bias ? bias[cv + j] : 0.f;
+#pragma unroll
+      for (int e = 0; e < CK; ++e)
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) av[j] = fmaf(xw[e], w[(int64_t)(cv + j) * CK + e], av[j]);
+      float mean, m2;
+      tile_stats<CPT, NW>(av, tv < p.Lout, tile_count(vx), red, mean, m2);
+      if (threadIdx.x == 0) sp[v] = make_float2(mean, m2);
+    }
+    lds_barrier();
+  }
+  // merge in a fixed order, in every wave (no barrier): fp64 sums over the partials by lane, then
+  // over the wave; the total count is Cout x Lout
+  double sm = 0.0, sm2 = 0.0, sq = 0.0;
+  for (int v = threadIdx.x & 63; v < nparts; v += 64) {
+    const double c = tile_count(v % gridDim.x);
+    const double m = sp[v].x;
+    sm += c * m;
+    sm2 += c * m * m;
+    sq += (double)sp[v].y;
+  }
+  sm = wave_sum_dpp_d(sm);
+  sm2 = wave_sum_dpp_d(sm2);
+  sq = wave_sum_dpp_d(sq);
+  const double ntot = (double)p.Cout * p.Lout;
+  const double mean = sm / ntot;
+  const double var = fmax(sq + (sm2 - sm * mean), 0.0) / ntot;
+  float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  if (!isfinite(rstd)) rstd = 0.f;
+  const float mf = (float)mean;
+  if (valid) {
+    float* yb = y + ((int64_t)b * p.Cout + cob0 + c0) * p.ldy + t;
+    const float* cb = wt + CK * COB + c0;  // bias, gamma, beta of this thread's channels
+    auto store = [&](auto code) {
+#pragma unroll
+      for (int j = 0; j < CPT; ++j) {
+        // acc holds conv + bias, so the shift is beta - mean * scale
+        const float sc = cb[COB + j] * rstd;
+        const float sh = cb[2 * COB + j] - mf * sc;
+        yb[(int64_t)j * p.ldy] = apply_act(fmaf(acc[j], sc, sh), code.value, p.alpha);
+      }
+    };
+    if constexpr (ACT >= 0) {
+      store(std::integral_constant<int, ACT>{});
+    } else {
+      switch (act) {
+        case 1: store(std::integral_constant<int, 1>{}); break;
+        case 2: store(std::integral_constant<int, 2>{}); break;
+        case 3: store(std::integral_constant<int, 3>{}); break;
+        case 4: store(std::integral_constant<int, 4>{}); break;
+        case 5: store(std::integral_constant<int, 5>{}); break;
+        case 6: store(std::integral_constant<int, 6>{}); break;
+        default: store(std::integral_constant<int, 0>{}); break;
+      }
+    }
+  }
+  // count this workgroup out (its reads of the slots are done); the last one out clears every
+  // slot of the launch and the count
+  const unsigned total = gridDim.x * gridDim.y * gridDim.z;
+  if (threadIdx.x == 0)
+    s_last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             total - 1;
+  lds_barrier();
+  if (s_last) {
+    unsigned long long* all = xch + 8;
+    for (int i = threadIdx.x; i < 2 * (int)total; i += NT)
+      __hip_atomic_store(all + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -462,6 +687,78 @@ void conv_gn_apply(const LaunchCtx& c, const ConvParams& p0, const float* x, con
   }
 #undef MNN_AP3
 #undef MNN_AP
+}
+
+namespace {
+constexpr int kOneCob = 16;   // channels per tile of the one-launch chain
+constexpr int kOneSplit = 2;  // threads per tile position
+
+template <int CK, bool R, int A>
+bool oneshot_dispatch(const LaunchCtx& c, const ConvParams& p, bool go, const float* x,
+                      const float* w, const float* bias, unsigned long long* xch, int spin_limit,
+                      const float* gamma, const float* beta, float eps, int act, float* y) {
+  auto* kern = conv_gn_oneshot_kernel<CK, kOneCob, kOneSplit, R, A>;
+  // workgroups of this kernel one CU holds at once (the same for every gfx950 device)
+  static const int per_cu = [&] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads * kOneSplit, 0) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    return n;
+  }();
+  const dim3 grid(cdiv(p.Lout, kThreads), p.Cout / kOneCob, p.B);
+  const int64_t nparts = (int64_t)grid.x * grid.y, blocks = nparts * grid.z;
+  if (nparts > kOneMaxParts || blocks > kOneMaxSlots ||
+      blocks > (int64_t)per_cu * c.dev->props.multiProcessorCount)
+    return false;
+  if (go)
+    launch(c, "conv_gn_oneshot_f32", kern, grid, dim3(kThreads * kOneSplit), 0, p, x, w, bias, xch,
+           spin_limit, gamma, beta, eps, act, y);
+  return true;
+}
+
+bool oneshot(const LaunchCtx& c, const ConvParams& p0, bool go, const float* x, const float* w,
+             const float* bias, unsigned long long* xch, int spin_limit, const float* gamma,
+             const float* beta, float eps, int act, float* y) {
+  ConvParams p = p0;
+  if (p.ldy == 0) p.ldy = p.Lout;
+  const int ck = reg_ck(p);
+  if (!ck || p.Cout % kOneCob != 0) return false;
+  const int a = (act == 0 || act == 3) ? act : -1;
+#define MNN_OS(CKV, R, A) oneshot_dispatch<CKV, R, A>(c, p, go, x, w, bias, xch, spin_limit, gamma, beta, eps, act, y)
+#define MNN_OS3(CKV, R) return a == 0 ? MNN_OS(CKV, R, 0) : a == 3 ? MNN_OS(CKV, R, 3) : MNN_OS(CKV, R, -1)
+  switch (ck * 2 + (p.reflect ? 1 : 0)) {
+    case 16: MNN_OS3(8, false);
+    case 17: MNN_OS3(8, true);
+    case 32: MNN_OS3(16, false);
+    case 33: MNN_OS3(16, true);
+    case 48: MNN_OS3(24, false);
+    case 49: MNN_OS3(24, true);
+    case 64: MNN_OS3(32, false);
+    default: MNN_OS3(32, true);
+  }
+#undef MNN_OS3
+#undef MNN_OS
+}
+}  // namespace
+
+size_t conv_gn_oneshot_exchange_bytes() { return 8 * (8 + 2 * (size_t)kOneMaxSlots); }
+
+bool conv_gn_oneshot_fits(const LaunchCtx& c, const ConvParams& p) {
+  return oneshot(c, p, false, nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0.f, 0,
+                 nullptr);
+}
+
+void conv_gn_oneshot(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                     const float* bias, void* xch, int spin_limit, const float* gamma,
+                     const float* beta, float eps, int act, float* y) {
+  MNN_REQUIRE(oneshot(c, p, true, x, w, bias, static_cast<unsigned long long*>(xch),
+                      std::max(spin_limit, 0), gamma, beta, eps, act, y),
+              MNN_ERR_INVALID_ARGUMENT,
+              "conv_gn_oneshot: not a register-window convolution, or the grid does not fit the "
+              "device at once");
 }
 
 }  // namespace k

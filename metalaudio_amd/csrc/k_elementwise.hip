@@ -74,6 +74,11 @@ __global__ __launch_bounds__(kThreads) void copy_kernel(const uint8_t* __restric
     d[i] = s[i];
 }
 
+__global__ __launch_bounds__(kThreads) void zero_u32_kernel(unsigned* __restrict__ d, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) d[i] = 0u;
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 __global__ __launch_bounds__(kThreads) void f32_to_bf16_kernel(const float* __restrict__ x,
@@ -120,6 +125,11 @@ void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t ha
   unsigned gx = grid_for(half);
   if (gx > 65535) gx = 65535;
   launch(c, "glu_f32", glu_kernel, dim3(gx, (unsigned)batch), dim3(kThreads), 0, x, y, half);
+}
+
+void zero_u32(const LaunchCtx& c, unsigned* d, int64_t n) {
+  if (n <= 0) return;
+  launch(c, "zero_u32", zero_u32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, d, n);
 }
 
 void copy_bytes(const LaunchCtx& c, const void* src, void* dst, int64_t bytes) {

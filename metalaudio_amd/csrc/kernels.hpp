@@ -15,6 +15,8 @@ void activation(const LaunchCtx& c, const float* x, float* y, int64_t n, int act
 // GLU: per batch b, y[b][i] = x[b][i] * sigmoid(x[b][i + half]) for i < half (NN.metal:1012-1023).
 void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t half);
 void copy_bytes(const LaunchCtx& c, const void* src, void* dst, int64_t bytes);
+// d[0 .. n) = 0, as a kernel on the stream (no memset node when the stream is captured).
+void zero_u32(const LaunchCtx& c, unsigned* d, int64_t n);
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet), and bf16 -> fp32 (exact).
 void f32_to_bf16(const LaunchCtx& c, const float* x, uint16_t* y, int64_t n);
 void bf16_to_f32(const LaunchCtx& c, const uint16_t* x, float* y, int64_t n);
@@ -84,6 +86,16 @@ void conv_gn_stats(const LaunchCtx& c, const ConvParams& p, const float* x, cons
 void conv_gn_apply(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
                    const float* bias, const float* parts, int nparts, const float* gamma,
                    const float* beta, float eps, int act, float* y);
+// The same chain in one launch, for grids that fit on the device at once (conv_gn_oneshot_fits).
+// xch is an exchange buffer of conv_gn_oneshot_exchange_bytes(), zero before its first launch
+// (zero_u32) and left ready for the next by each launch. spin_limit bounds each workgroup's wait
+// for the others; a workgroup that runs out computes the statistics itself (same result, slower).
+// Launches that share xch must not overlap.
+size_t conv_gn_oneshot_exchange_bytes();
+bool conv_gn_oneshot_fits(const LaunchCtx& c, const ConvParams& p);
+void conv_gn_oneshot(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
+                     const float* bias, void* xch, int spin_limit, const float* gamma,
+                     const float* beta, float eps, int act, float* y);
 // GEMM tuning override: MNN_GEMM_TILE=<tile id> forces a tile configuration where it applies.
 
 // ------------------------------------------------------------------ GEMM (k_gemm.hip)

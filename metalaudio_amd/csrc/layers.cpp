@@ -327,6 +327,16 @@ class GroupNormLayer : public Layer {
     partials_.reserve(sizeof(float) * std::max<int64_t>(floats, 1));
     return partials_.f32();
   }
+  // Exchange buffer of a one-launch chain (tags, a counter, the statistics partials), zeroed on
+  // the stream when allocated; each launch leaves it ready for the next.
+  void* exchange(Stream& s) {
+    if (!xch_.ptr) {
+      const size_t bytes = k::conv_gn_oneshot_exchange_bytes();
+      xch_.reserve(bytes);
+      k::zero_u32(ctx(s), xch_.as<unsigned>(), (int64_t)(bytes / 4));
+    }
+    return xch_.ptr;
+  }
   // Turns partials into per-(b, c) coefficients held in coef().
   void finalize(Stream& s, int B, int nchunk, const float* partials) {
     coef_.reserve(sizeof(float) * 2 * B * C_);
@@ -350,7 +360,7 @@ class GroupNormLayer : public Layer {
   int act_;
   Param* gamma_ = nullptr;
   Param* beta_ = nullptr;
-  DevBuf partials_, coef_;
+  DevBuf partials_, coef_, xch_;
 };
 
 // ------------------------------------------------------------------ LayerNorm
@@ -2121,6 +2131,13 @@ void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor
     // writes the normalised output once (y is not used)
     k::ConvParams p = c->direct_params((int)B, (int)L);
     p.alpha = 0.01f;  // the activation is GroupNorm's: leaky ReLU slope 0.01
+    if (k::conv_gn_oneshot_fits(ctx(s), p)) {
+      // the grid fits the device at once: both passes in one launch
+      k::conv_gn_oneshot(ctx(s), p, in.f32(), c->weight(), c->bias(), g->exchange(s),
+                         s.dev->grid_spin_limit.load(), g->gamma(), g->beta(), g->eps(), act,
+                         out.f32());
+      return;
+    }
     const int nparts = k::conv_gn_num_parts(p);
     float* parts = g->reserve_partials(3LL * B * nparts);
     k::conv_gn_stats(ctx(s), p, in.f32(), c->weight(), c->bias(), parts);

@@ -41,7 +41,9 @@ FAMILIES = [
     ("attn_generic_kernel", "attn_fwd"),
     ("enc_l1_stats_kernel", "enc_l1_stats_f32"),
     ("enc_l1_fused_kernel", "enc_l1_fused_f32"),
+    ("conv_gn_oneshot_kernel", "conv_gn_oneshot_f32"),
     ("conv_gn_stats_kernel", "conv_gn_stats_f32"),
+    ("zero_u32_kernel", "zero_u32"),
     ("conv_gn_apply_kernel", "conv_gn_apply_f32"),
     ("conv1d_direct", "conv1d_direct_f32"),
     ("gn_apply_parts_kernel", "gn_apply_parts"),

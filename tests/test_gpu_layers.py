@@ -2,13 +2,14 @@
 
 fp32 bar (stated by the path's spec): |gpu - oracle| <= 1e-4 + 1e-3 * |oracle| per element.
 """
+import ctypes
 import sys
 
 import numpy as np
 import pytest
 
 import oracle
-from metalaudio_amd import nn
+from metalaudio_amd import _lib, nn
 from metalaudio_amd import workloads
 from tests.conftest import assert_close
 
@@ -925,11 +926,13 @@ def test_sequential_forward_async(dev, stream):
     (3, 32, 2999, "leaky_relu", False, 8, "explicit", 5),  # Cin * K = 24
     (4, 64, 1025, "sigmoid", False, 8, "reflect", 3),      # Cin * K = 32
     (2, 24, 301, "tanh", False, 4, "explicit", 1),         # Cin * K = 8, three channel blocks
+    (2, 48, 343980, "none", True, 8, "reflect", 3),  # grid too large for one launch: two passes
 ])
 def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu, k, mode, pad):
-    """Conv1D -> GroupNorm(1) [-> activation / GELU] in a Sequential runs fused (two launches);
-    the result is the layers' composition, batch 2 included. The bias and GroupNorm shift carry
-    an offset so that a dropped bias or mean term moves the output."""
+    """Conv1D -> GroupNorm(1) [-> activation / GELU] in a Sequential runs fused (one launch when
+    the grid fits the device at once, else two); the result is the layers' composition, batch 2
+    included. The bias and GroupNorm shift carry an offset so that a dropped bias or mean term
+    moves the output."""
     say(f"sequential conv -> groupnorm fusion {cin}->{cout} k{k} L={L} {mode} act={act} "
         f"gelu={gelu}")
     x = RNG.uniform(-1, 1, (2, cin, L)).astype(np.float32)
@@ -957,3 +960,90 @@ def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu, 
                             1, gm, bt)
     ref = oracle.gelu_layer(ref) if gelu else oracle.activation(ref, act)
     assert_close(out.to_numpy().reshape(ref.shape), ref, ATOL, RTOL, "fused sequential")
+
+
+def _launch_names(dev, fn):
+    """Kernel names launched on `dev` while fn() runs, in launch order."""
+    lib = _lib.lib()
+    assert lib.mnn_debug_set_launch_log(dev.handle, 1) == 0
+    try:
+        fn()
+    finally:
+        lib.mnn_debug_set_launch_log(dev.handle, 0)
+    need = ctypes.c_size_t()
+    lib.mnn_debug_launch_log(dev.handle, None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(need.value)
+    assert lib.mnn_debug_launch_log(dev.handle, buf, need.value, ctypes.byref(need)) == 0
+    return [ln.split()[0] for ln in buf.value.decode().splitlines() if ln.strip()]
+
+
+def _spin_limit(dev, polls):
+    prev = ctypes.c_int()
+    assert _lib.lib().mnn_debug_set_grid_spin_limit(dev.handle, polls, ctypes.byref(prev)) == 0
+    return prev.value
+
+
+def test_conv_groupnorm_one_launch(dev, stream):
+    """The config-1 chain (Conv1D 2->48 k8 s4 -> GroupNorm(1) -> GELU) runs as one launch whose
+    workgroups wait for each other's statistics. Checked: the launch count; the oracle; repeated
+    calls and a shorter input in between (the arrival counters return to zero after each launch,
+    and the partial count follows the grid); the bounded wait's other path, forced from the host
+    with a spin limit of 0 (workgroups that arrive before the last one compute every partial
+    themselves), which gives the same bits; and a grid too large for the device going to the
+    two-launch form."""
+    say("conv -> groupnorm one launch: config-1 chain, spin limit default and 0")
+    x = RNG.uniform(-1, 1, (1, 2, 44100)).astype(np.float32)
+    xs = RNG.uniform(-1, 1, (1, 2, 9000)).astype(np.float32)
+    w = (RNG.standard_normal((48, 2, 8)) * 0.5).astype(np.float32)
+    b = (0.3 + 0.2 * RNG.standard_normal(48)).astype(np.float32)
+    gm = (1 + 0.2 * RNG.standard_normal(48)).astype(np.float32)
+    bt = (0.2 * RNG.standard_normal(48)).astype(np.float32)
+    conv = nn.Conv1D(dev, 2, 48, 8, 4)
+    conv.load_weights(w, b)
+    gn = nn.GroupNorm(dev, 1, 48)
+    gn.load_parameters(gm, bt)
+    seq = nn.Sequential(dev)
+    seq.add(conv)
+    seq.add(gn)
+    seq.add_unchecked(nn.GELU(dev, [48, 0]))
+    seq.build()
+
+    def ref(xx):
+        return oracle.gelu_layer(oracle.group_norm(oracle.conv1d(xx, w, b, stride=4), 1, gm, bt))
+
+    def run(xx):
+        o = seq.forward(nn.Tensor.from_numpy(dev, xx), stream)
+        stream.sync(60000)
+        return o.to_numpy().reshape(1, 48, -1)
+
+    r, rs = ref(x), ref(xs)
+    # the first call also zeroes the layer's arrival counters (a kernel of its own)
+    names = _launch_names(dev, lambda: run(x))
+    assert names == ["zero_u32", "conv_gn_oneshot_f32"], names
+    names = _launch_names(dev, lambda: run(x))
+    assert names == ["conv_gn_oneshot_f32"], names
+    first = run(x)
+    assert_close(first, r, ATOL, RTOL, "one launch")
+    for _ in range(3):
+        assert_close(run(xs), rs, ATOL, RTOL, "one launch, shorter input")
+        assert np.array_equal(run(x), first), "repeated one-launch calls differ"
+    prev = _spin_limit(dev, 0)
+    try:
+        assert prev > 0
+        for _ in range(2):
+            assert np.array_equal(run(x), first), "self-computed statistics differ"
+            assert_close(run(xs), rs, ATOL, RTOL, "self-computed statistics, shorter input")
+    finally:
+        _spin_limit(dev, prev)
+    assert np.array_equal(run(x), first)
+    # batch 8 of 343 980 samples: 336 x 6 x 8 workgroups, more than the device holds at once
+    xb = RNG.uniform(-1, 1, (8, 2, 343980)).astype(np.float32)
+    names = _launch_names(dev, lambda: run_batch(seq, dev, stream, xb))
+    assert names == ["conv_gn_stats_f32", "conv_gn_apply_f32"], names
+    assert _lib.lib().mnn_debug_set_grid_spin_limit(dev.handle, -1, None) == 12  # invalid
+
+
+def run_batch(seq, dev, stream, xx):
+    o = seq.forward(nn.Tensor.from_numpy(dev, xx), stream)
+    stream.sync(60000)
+    return o
