@@ -72,9 +72,34 @@ __device__ __forceinline__ double wave_sum_xor_d(double v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ double dpp_mov_d(double v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
+  return __hiloint2double(hi, lo);
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                          __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+
+// Sum over the whole wave of a double by DPP row sums (each step moves both halves) and the four
+// rows' sums read from lanes 0, 16, 32 and 48, added in that fixed order: every lane returns the
+// same bits. All 64 lanes must be active.
+__device__ __forceinline__ double wave_sum_dpp_d(double v) {
+  v += dpp_mov_d<0xB1>(v);
+  v += dpp_mov_d<0x4E>(v);
+  v += dpp_mov_d<0x141>(v);
+  v += dpp_mov_d<0x140>(v);
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
 // The first 64 * KB partials of a wave_merge_parts call, loaded by straight-line code (clamped
 // addresses, no branch or loop) so that a kernel can put them in flight together with its other
 // loads; merge() finishes from registers, re-reading only partials beyond the first batch.
+// merge() (and BlockParts::reduce_waves below) sum over the wave with DPP: every lane of the
+// wave must be active at the call.
 template <int KB>
 struct PartsBatch {
   float pn[KB], pm[KB], pq[KB];
@@ -110,10 +135,10 @@ struct PartsBatch {
       sm2 += c * m * m;
       sq += (double)p[3 * j + 2];
     }
-    n = wave_sum_xor_d(sn);
-    sm = wave_sum_xor_d(sm);
-    sm2 = wave_sum_xor_d(sm2);
-    sq = wave_sum_xor_d(sq);
+    n = wave_sum_dpp_d(sn);
+    sm = wave_sum_dpp_d(sm);
+    sm2 = wave_sum_dpp_d(sm2);
+    sq = wave_sum_dpp_d(sq);
     mean = n > 0.0 ? sm / n : 0.0;
     // M2 = sum M2_j + sum n_j (mean_j - mean)^2 = sum M2_j + sum n_j mean_j^2 - n mean^2; in fp64
     // the cancellation costs about mean^2 / var * 1e-16 relative, negligible below |mean| / std ~ 1e5
@@ -158,10 +183,10 @@ struct BlockParts {
       sm2 += c * m * m;
       sq += (double)p[3 * j + 2];
     }
-    sn = wave_sum_xor_d(sn);
-    sm = wave_sum_xor_d(sm);
-    sm2 = wave_sum_xor_d(sm2);
-    sq = wave_sum_xor_d(sq);
+    sn = wave_sum_dpp_d(sn);
+    sm = wave_sum_dpp_d(sm);
+    sm2 = wave_sum_dpp_d(sm2);
+    sq = wave_sum_dpp_d(sq);
     if ((threadIdx.x & 63) == 0) {
       double* o = sh + 4 * (threadIdx.x >> 6);
       o[0] = sn;
@@ -225,27 +250,6 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
   const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
   return (r0 + r1) + (r2 + r3);
-}
-
-template <int CTRL>
-__device__ __forceinline__ double dpp_mov_d(double v) {
-  const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xF, 0xF, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xF, 0xF, false);
-  return __hiloint2double(hi, lo);
-}
-
-__device__ __forceinline__ double readlane_d(double v, int lane) {
-  return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
-                          __builtin_amdgcn_readlane(__double2loint(v), lane));
-}
-
-// fp64 form of wave_sum_dpp (the same steps on both halves of each value).
-__device__ __forceinline__ double wave_sum_dpp_d(double v) {
-  v += dpp_mov_d<0xB1>(v);
-  v += dpp_mov_d<0x4E>(v);
-  v += dpp_mov_d<0x141>(v);
-  v += dpp_mov_d<0x140>(v);
-  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 
 // Round-to-nearest-even fp32 -> bf16 bits (NaN kept quiet).

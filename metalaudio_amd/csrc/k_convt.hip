@@ -181,23 +181,42 @@ __global__ __launch_bounds__(64) void convt_small_kernel(ConvTArgs a) {
 // Sum of the K parts of the GEMM form, then the scatter of convt's epilogue:
 // y[b][oc][s*q + r - pad] = bias[oc] + sum_p ws[b][p][s*oc + r][q]. One thread per column q of one
 // output channel: it reads the s phase rows (coalesced over q) and writes s consecutive samples.
+// With stats, each workgroup writes the GroupNorm(1) partial (count, mean, M2) of the samples it
+// stored at stats[((b * Cout + oc) * gridDim.x + blockIdx.x) * 3].
 __global__ __launch_bounds__(256) void convt_reduce_kernel(const float* __restrict__ ws, int ksplit,
                                                            int M, int64_t N, int stride, int pad,
                                                            const float* __restrict__ bias,
                                                            float* __restrict__ y, int64_t Lout,
-                                                           int Cout) {
+                                                           int Cout, float* __restrict__ stats) {
+  __shared__ float red[3 * 4];
   const int oc = blockIdx.y, b = blockIdx.z;
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (q >= N) return;
-  const float* wb = ws + (int64_t)b * ksplit * M * N + (int64_t)stride * oc * N + q;
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int p = 0; p < ksplit; ++p)
-    for (int r = 0; r < stride && r < 4; ++r) v[r] += wb[(int64_t)p * M * N + (int64_t)r * N];
-  const float bv = bias ? bias[oc] : 0.f;
-  float* yr = y + ((int64_t)b * Cout + oc) * Lout;
-  for (int r = 0; r < stride && r < 4; ++r) {
-    const int64_t o = stride * q + r - pad;
-    if (o >= 0 && o < Lout) yr[o] = v[r] + bv;
+  ShiftedStats st;
+  if (q < N) {
+    const float* wb = ws + (int64_t)b * ksplit * M * N + (int64_t)stride * oc * N + q;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int p = 0; p < ksplit; ++p)
+      for (int r = 0; r < stride && r < 4; ++r) v[r] += wb[(int64_t)p * M * N + (int64_t)r * N];
+    const float bv = bias ? bias[oc] : 0.f;
+    float* yr = y + ((int64_t)b * Cout + oc) * Lout;
+    for (int r = 0; r < stride && r < 4; ++r) {
+      const int64_t o = stride * q + r - pad;
+      if (o >= 0 && o < Lout) {
+        yr[o] = v[r] + bv;
+        st.add(v[r] + bv);
+      }
+    }
+  }
+  if (stats) {  // uniform over the grid
+    float sn, smean, sm2;
+    st.finish(sn, smean, sm2);
+    block_welford(sn, smean, sm2, red);
+    if (threadIdx.x == 0) {
+      float* o = stats + (((int64_t)b * Cout + oc) * gridDim.x + blockIdx.x) * 3;
+      o[0] = sn;
+      o[1] = smean;
+      o[2] = sm2;
+    }
   }
 }
 
@@ -262,6 +281,55 @@ void convt_pack_weights(const float* w, int Cin, int Cout, int K, int stride, fl
               w[((int64_t)ic * Cout + oc) * K + r + stride * t];
 }
 
+namespace {
+// The GEMM of the transposed conv: rows (oc, phase), columns q, K = T * Cp over the unfolded input.
+GemmArgs convt_gemm_args(const ConvTArgs& a, const float* wpack, const float* unfold,
+                         float* split_ws) {
+  const int Cin = a.C1 + a.C2;
+  const int T = a.K / a.stride, Cp = convt_padded_cin(Cin);
+  const int64_t Lq = convt_rows(a.Lout, a.stride, a.pad);
+  GemmArgs g;
+  g.M = a.stride * a.Cout;
+  g.N = (int)Lq;
+  g.K = T * Cp;
+  g.batch = a.B;
+  g.A = wpack;
+  g.lda = g.K;
+  g.sA = 0;
+  g.B = unfold;
+  g.ldb = g.K;
+  g.sB = Lq * g.K;
+  g.blayout = B_NK;
+  g.C = a.y;
+  g.ldc = a.Lout;
+  g.sC = (int64_t)a.Cout * a.Lout;
+  g.bias = a.bias;
+  g.bias_mode = a.bias ? BIAS_M : BIAS_NONE;
+  g.ct_stride = a.stride;
+  g.ct_pad = a.pad;
+  g.ct_len = a.Lout;
+  g.stats = a.stats;
+  g.name = "convt_f32_mfma";
+  const int parts = convt_ksplit(a.B, Cin, a.Cout, a.K, a.stride, a.pad, a.Lout);
+  if (parts > 1) {
+    g.ksplit = parts;
+    g.ws = split_ws;
+    g.ct_stride = 0;  // partial products only; the reduce applies bias and scatter
+    g.bias = nullptr;
+    g.bias_mode = BIAS_NONE;
+    g.stats = nullptr;  // the reduce writes the statistics
+  }
+  return g;
+}
+}  // namespace
+
+int convt_gemm_parts(const ConvTArgs& a) {
+  const int Cin = a.C1 + a.C2;
+  const int parts = convt_ksplit(a.B, Cin, a.Cout, a.K, a.stride, a.pad, a.Lout);
+  if (parts > 1) return a.Cout * (int)cdiv(convt_rows(a.Lout, a.stride, a.pad), 256);
+  return (int)gemm_nk_lds_tiles(convt_gemm_args(a, nullptr, nullptr, nullptr));
+}
+
 void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, float* unfold,
                 float* split_ws) {
   const int Cin = a.C1 + a.C2;
@@ -284,36 +352,10 @@ void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, floa
     case 2: launch(c, "convt_pack_f32", convt_pack_kernel<2>, grid, dim3(256), 0, p); break;
     default: launch(c, "convt_pack_f32", convt_pack_kernel<4>, grid, dim3(256), 0, p); break;
   }
-  GemmArgs g;
-  g.M = a.stride * a.Cout;
-  g.N = (int)p.Lq;
-  g.K = T * Cp;
-  g.batch = a.B;
-  g.A = wpack;
-  g.lda = g.K;
-  g.sA = 0;
-  g.B = unfold;
-  g.ldb = g.K;
-  g.sB = p.Lq * g.K;
-  g.blayout = B_NK;
-  g.C = a.y;
-  g.ldc = a.Lout;
-  g.sC = (int64_t)a.Cout * a.Lout;
-  g.bias = a.bias;
-  g.bias_mode = a.bias ? BIAS_M : BIAS_NONE;
-  g.ct_stride = a.stride;
-  g.ct_pad = a.pad;
-  g.ct_len = a.Lout;
-  g.name = "convt_f32_mfma";
-  const int parts = convt_ksplit(a.B, Cin, a.Cout, a.K, a.stride, a.pad, a.Lout);
-  if (parts > 1) {
-    MNN_REQUIRE(split_ws, MNN_ERR_INVALID_ARGUMENT, "convt_gemm: the K split needs a workspace");
-    g.ksplit = parts;
-    g.ws = split_ws;
-    g.ct_stride = 0;  // partial products only; the reduce applies bias and scatter
-    g.bias = nullptr;
-    g.bias_mode = BIAS_NONE;
-  }
+  const GemmArgs g = convt_gemm_args(a, wpack, unfold, split_ws);
+  const int parts = g.ksplit;
+  MNN_REQUIRE(parts == 1 || split_ws, MNN_ERR_INVALID_ARGUMENT,
+              "convt_gemm: the K split needs a workspace");
   MNN_REQUIRE(gemm_nk_lds_supported(g), MNN_ERR_INVALID_ARGUMENT,
               "convt_gemm: operands outside the LDS GEMM contract");
   gemm_nk_lds(c, g);
@@ -321,7 +363,7 @@ void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, floa
     launch(c, "convt_reduce_f32", convt_reduce_kernel,
            dim3((unsigned)cdiv(p.Lq, 256), (unsigned)a.Cout, (unsigned)a.B), dim3(256), 0,
            (const float*)split_ws, parts, g.M, (int64_t)g.N, a.stride, a.pad, a.bias, a.y,
-           a.Lout, a.Cout);
+           a.Lout, a.Cout, a.stats);
 }
 
 void convt_pack_t1(const LaunchCtx& c, const ConvTPackArgs& p, int B) {

@@ -275,7 +275,10 @@ __device__ __forceinline__ void store_glu(const GemmArgs& a, const floatx16 (&ac
 // (+ bias[oc]) belongs at output position o = s*q + r - ct_pad of channel oc:
 // C[oc * ldc + o] when 0 <= o < ct_len. A lane holds the s phases of one (oc, q) in registers
 // v..v+s-1 (s = 4: rows 4i..4i+3 of a 32-row block), so consecutive lanes cover consecutive
-// 4-sample runs of one output row. Bias values are loaded first (see store_tile).
+// 4-sample runs of one output row. Bias values are loaded first (see store_tile). Every output
+// sample is stored by exactly one (row, column), so with a.stats each workgroup also writes the
+// GroupNorm(1) partial (count, mean, M2) of the samples it stored at
+// stats[(batch * tiles + blockIdx.y * gridDim.x + blockIdx.x) * 3], tiles = gridDim.x * gridDim.y.
 template <int WMW, int WNW, int WM, int WN>
 __device__ __forceinline__ void store_ct(const GemmArgs& a, const floatx16 (&acc)[WM][WN], int m0,
                                          int n0, int wm, int wn, int lane) {
@@ -291,6 +294,8 @@ __device__ __forceinline__ void store_ct(const GemmArgs& a, const floatx16 (&acc
       bmv[i][v] = a.bias ? a.bias[gm / s] : 0.f;
     }
   wait_vmcnt<0>();
+  // four statistics accumulators, so the per-sample updates are not one dependent chain
+  ShiftedStats st[4];
 #pragma unroll
   for (int i = 0; i < WM; ++i) {
     const int mblk = m0 + wm * WM * 32 + i * 32;
@@ -302,8 +307,31 @@ __device__ __forceinline__ void store_ct(const GemmArgs& a, const floatx16 (&acc
       for (int v = 0; v < 16; ++v) {
         const int gm = mblk + 8 * (v / 4) + 4 * g + (v % 4);
         const int oc = gm / s, o = s * q + (gm - oc * s) - a.ct_pad;
-        if (gm < a.M && o >= 0 && o < a.ct_len) Cp[(int64_t)oc * a.ldc + o] = acc[i][j][v] + bmv[i][v];
+        if (gm < a.M && o >= 0 && o < a.ct_len) {
+          const float val = acc[i][j][v] + bmv[i][v];
+          if (a.stats) st[v & 3].add(val);
+          Cp[(int64_t)oc * a.ldc + o] = val;
+        }
       }
+    }
+  }
+  if (a.stats) {
+    __shared__ float red[3 * WMW * WNW];
+    float sn, smean, sm2;
+    st[0].finish(sn, smean, sm2);
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      float n2, mean2, m22;
+      st[k].finish(n2, mean2, m22);
+      welford_combine(sn, smean, sm2, n2, mean2, m22);
+    }
+    block_welford(sn, smean, sm2, red);
+    if (threadIdx.x == 0) {
+      float* o = a.stats + ((int64_t)blockIdx.z * gridDim.x * gridDim.y + blockIdx.y * gridDim.x +
+                            blockIdx.x) * 3;
+      o[0] = sn;
+      o[1] = smean;
+      o[2] = sm2;
     }
   }
 }
@@ -644,11 +672,18 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
                      ((int64_t)(a.N - 1) * a.ldb + a.K) * 4 < ((int64_t)1 << 32);
   return off32 && a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
-         aligned16(a.B) && a.stats == nullptr && a.pro_coef == nullptr && a.pro_stats == nullptr &&
+         aligned16(a.B) && a.pro_coef == nullptr && a.pro_stats == nullptr &&
          (!a.glu || (a.M % 32 == 0 && a.bias_mode != BIAS_N && a.R == nullptr && a.act == 0)) &&
          (a.ct_stride == 0 || (!a.glu && a.R == nullptr && a.act == 0 && a.bias_mode != BIAS_N)) &&
          a.ksplit >= 1 && (a.K / BK) % a.ksplit == 0 &&
-         (a.ksplit == 1 || (a.ws != nullptr && !a.glu && a.stats == nullptr));
+         (a.ksplit == 1 || (a.ws != nullptr && !a.glu)) &&
+         (a.stats == nullptr || (a.ct_stride > 0 && a.ksplit == 1));
+}
+
+int64_t gemm_nk_lds_tiles(const GemmArgs& a) {
+  if (a.ab_bf16) return -1;
+  const LdsTile& t = choose_lds_tile(a);
+  return (int64_t)cdiv(a.M, t.bm) * cdiv(a.N, t.bn);
 }
 
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {

@@ -25,10 +25,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kChunk = 4096;  // elements per GroupNorm statistics partial
 
+// One partial per chunk of kChunk consecutive elements of a group (a group's channels are
+// contiguous in [B][C][L]): every thread loads its kChunk / kThreads elements up front (16-byte
+// vectors when the rows allow), takes their mean and M2 in two passes over its registers, and the
+// workgroup merges the threads' (count, mean, M2) in a fixed order.
+constexpr int kStatPer = kChunk / kThreads;  // elements per thread
+static_assert(kStatPer % 4 == 0, "whole float4 vectors per thread");
 __global__ __launch_bounds__(kThreads) void gn_stats_partial_kernel(const float* __restrict__ x,
                                                                     int C, int64_t L, int G,
                                                                     float* __restrict__ partials,
-                                                                    int nchunk) {
+                                                                    int nchunk, int vec) {
   __shared__ float red[3 * (kThreads / 64)];
   const int bg = blockIdx.y;
   const int b = bg / G, g = bg % G;
@@ -36,23 +42,45 @@ __global__ __launch_bounds__(kThreads) void gn_stats_partial_kernel(const float*
   const int64_t total = (int64_t)cpg * L;
   const float* base = x + ((int64_t)b * C + (int64_t)g * cpg) * L;
   const int64_t start = (int64_t)blockIdx.x * kChunk;
-  const int64_t end = min(start + (int64_t)kChunk, total);
-  // shifted sums in fp64 per thread, shift = first element of the chunk
-  const float shift = start < total ? base[start] : 0.f;
-  double s1 = 0.0, s2 = 0.0;
-  float n = 0.f;
-  for (int64_t i = start + threadIdx.x; i < end; i += kThreads) {
-    double d = (double)base[i] - (double)shift;
-    s1 += d;
-    s2 += d * d;
-    n += 1.f;
+  float v[kStatPer];
+  bool ok[kStatPer];
+  if (vec) {
+    // thread t covers vectors start/4 + t + kThreads * k: coalesced 16-byte loads
+    const float4* b4 = reinterpret_cast<const float4*>(base + start);
+    const int64_t n4 = (min(start + (int64_t)kChunk, total) - start) >> 2;
+#pragma unroll
+    for (int k = 0; k < kStatPer / 4; ++k) {
+      const int64_t i = threadIdx.x + (int64_t)kThreads * k;
+      const float4 q = b4[min(i, max(n4 - 1, (int64_t)0))];
+      v[4 * k + 0] = q.x;
+      v[4 * k + 1] = q.y;
+      v[4 * k + 2] = q.z;
+      v[4 * k + 3] = q.w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ok[4 * k + e] = i < n4;
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kStatPer; ++k) {
+      const int64_t i = start + threadIdx.x + (int64_t)kThreads * k;
+      ok[k] = i < total;
+      v[k] = base[min(i, total - 1)];
+    }
   }
-  float mean = 0.f, m2 = 0.f;
-  if (n > 0.f) {
-    double md = s1 / n;
-    mean = (float)((double)shift + md);
-    m2 = (float)fmax(s2 - s1 * md, 0.0);
+  float n = 0.f, s = 0.f;
+#pragma unroll
+  for (int k = 0; k < kStatPer; ++k) {
+    n += ok[k] ? 1.f : 0.f;
+    s += ok[k] ? v[k] : 0.f;
   }
+  const float mean0 = n > 0.f ? s / n : 0.f;
+  float m2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < kStatPer; ++k) {
+    const float d = v[k] - mean0;
+    m2 = ok[k] ? fmaf(d, d, m2) : m2;
+  }
+  float mean = mean0;
   block_welford(n, mean, m2, red);
   if (threadIdx.x == 0) {
     float* p = partials + ((int64_t)bg * nchunk + blockIdx.x) * 3;
@@ -168,30 +196,43 @@ __global__ __launch_bounds__(kThreads) void gn_apply_parts_kernel(
   const int64_t total = (int64_t)cpg * L;
   const int64_t gbase = (int64_t)bg * total;  // (b * G + g) * cpg * L
   const int c0 = (bg % G) * cpg;
-  const int64_t i0 = ((int64_t)blockIdx.x * kApplyPer) * kThreads + threadIdx.x;
+  // Every load is issued before the merge: the items, their channels' gamma / beta (through an
+  // always-valid address: a missing vector reads x and is replaced by its fill), the partials.
+  // Indices are 32-bit (the host checks cpg * L < 2^31).
+  const int tot = (int)total, Li = (int)L;
+  const int j0 = (int)blockIdx.x * kApplyPer * kThreads + (int)threadIdx.x;
+  float gk[kApplyPer], bk[kApplyPer];
+  auto chan_consts = [&](int k, int ch) {
+    const float gv = *(gamma ? gamma + ch : x);
+    const float bv = *(beta ? beta + ch : x);
+    gk[k] = gamma ? gv : 1.f;
+    bk[k] = beta ? bv : 0.f;
+  };
   if (vec) {
-    const int64_t total4 = total >> 2, L4 = L >> 2;
+    const int total4 = tot >> 2, L4 = Li >> 2;
     const float4* x4 = reinterpret_cast<const float4*>(x + gbase);
     float4* y4 = reinterpret_cast<float4*>(y + gbase);
     float4 v[kApplyPer];
 #pragma unroll
     for (int k = 0; k < kApplyPer; ++k) {
-      const int64_t i = i0 + (int64_t)k * kThreads;
-      v[k] = i < total4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int i = min(j0 + k * kThreads, total4 - 1);
+      v[k] = x4[i];
+      chan_consts(k, c0 + i / L4);
     }
+    PartsBatch<8> pb;
+    pb.load(parts + (int64_t)bg * nparts * 3, nparts);
     double n, mean, m2;
-    wave_merge_parts(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
+    pb.merge(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
     const double var = n > 0.0 ? m2 / n : 0.0;
     float rstd = (float)(1.0 / sqrt(var + (double)eps));
     if (!isfinite(rstd)) rstd = 0.f;
     const float mf = (float)mean;
 #pragma unroll
     for (int k = 0; k < kApplyPer; ++k) {
-      const int64_t i = i0 + (int64_t)k * kThreads;
+      const int i = j0 + k * kThreads;
       if (i < total4) {
-        const int ch = c0 + (int)(i / L4);
-        const float sc = (gamma ? gamma[ch] : 1.f) * rstd;
-        const float sh = (beta ? beta[ch] : 0.f) - mf * sc;
+        const float sc = gk[k] * rstd;
+        const float sh = bk[k] - mf * sc;
         float4 o;
         o.x = apply_act(fmaf(v[k].x, sc, sh), act);
         o.y = apply_act(fmaf(v[k].y, sc, sh), act);
@@ -204,22 +245,24 @@ __global__ __launch_bounds__(kThreads) void gn_apply_parts_kernel(
     float v[kApplyPer];
 #pragma unroll
     for (int k = 0; k < kApplyPer; ++k) {
-      const int64_t i = i0 + (int64_t)k * kThreads;
-      v[k] = i < total ? x[gbase + i] : 0.f;
+      const int i = min(j0 + k * kThreads, tot - 1);
+      v[k] = x[gbase + i];
+      chan_consts(k, c0 + i / Li);
     }
+    PartsBatch<8> pb;
+    pb.load(parts + (int64_t)bg * nparts * 3, nparts);
     double n, mean, m2;
-    wave_merge_parts(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
+    pb.merge(parts + (int64_t)bg * nparts * 3, nparts, n, mean, m2);
     const double var = n > 0.0 ? m2 / n : 0.0;
     float rstd = (float)(1.0 / sqrt(var + (double)eps));
     if (!isfinite(rstd)) rstd = 0.f;
     const float mf = (float)mean;
 #pragma unroll
     for (int k = 0; k < kApplyPer; ++k) {
-      const int64_t i = i0 + (int64_t)k * kThreads;
-      if (i < total) {
-        const int ch = c0 + (int)(i / L);
-        const float sc = (gamma ? gamma[ch] : 1.f) * rstd;
-        const float sh = (beta ? beta[ch] : 0.f) - mf * sc;
+      const int i = j0 + k * kThreads;
+      if (i < tot) {
+        const float sc = gk[k] * rstd;
+        const float sh = bk[k] - mf * sc;
         y[gbase + i] = apply_act(fmaf(v[k], sc, sh), act);
       }
     }
@@ -417,8 +460,10 @@ int gn_num_chunks(int C, int G, int64_t L) {
 
 void gn_stats_partial(const LaunchCtx& c, const float* x, int B, int C, int64_t L, int G,
                       float* partials, int nchunk) {
+  // 16-byte loads when every group and chunk start is 16-byte aligned (chunks are 4096 floats)
+  const int vec = (L % 4 == 0) && ((int64_t)(C / G) * L) % 4 == 0 && aligned16(x);
   launch(c, "gn_stats_partial", gn_stats_partial_kernel, dim3(nchunk, B * G), dim3(kThreads), 0,
-         x, C, L, G, partials, nchunk);
+         x, C, L, G, partials, nchunk, vec);
 }
 
 void gn_finalize(const LaunchCtx& c, const float* partials, int B, int C, int G, int nchunk,
@@ -439,6 +484,8 @@ void gn_apply(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_
 void gn_apply_parts(const LaunchCtx& c, const float* x, float* y, int B, int C, int64_t L, int G,
                     const float* parts, int nparts, const float* gamma, const float* beta,
                     float eps, int act) {
+  MNN_REQUIRE((int64_t)(C / G) * L < ((int64_t)1 << 31) && nparts > 0, MNN_ERR_INVALID_ARGUMENT,
+              "gn_apply_parts: a group holds 2^31 elements or more");
   const int vec = (L % 4 == 0) && aligned16(x) && aligned16(y);
   const int64_t total = (int64_t)(C / G) * L;
   const int64_t items = vec ? total / 4 : total;

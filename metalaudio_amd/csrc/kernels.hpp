@@ -177,6 +177,9 @@ void gemm(const LaunchCtx& c, const GemmArgs& a);
 // activation or residual); no statistics or B prologue.
 bool gemm_nk_lds_supported(const GemmArgs& a);
 void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a);
+// Output tiles per batch of the tile gemm_nk_lds would choose for a (fp32 operands; -1 for bf16):
+// the number of statistics partials the transposed-conv epilogue writes per batch.
+int64_t gemm_nk_lds_tiles(const GemmArgs& a);
 
 // ------------------------------------------------------------------ 2-D conv (k_conv2d.hip)
 // DynamicConv2D (DynamicConv2D.swift:37-592): x [B][Cin][H][W] -> y [B][Cout][Ho][Wo], weights
@@ -280,6 +283,9 @@ struct ConvTArgs {
   const float* w = nullptr;
   const float* bias = nullptr;
   float* y = nullptr;  // [B][Cout][Lout]
+  // GEMM form only: GroupNorm(1) statistics partials of y (count, mean, M2), convt_gemm_parts(a)
+  // per batch at stats[(b * parts + j) * 3] (gn_apply_parts' layout for one group)
+  float* stats = nullptr;
 };
 struct ConvTPackArgs {
   const float* x1 = nullptr;
@@ -290,6 +296,8 @@ struct ConvTPackArgs {
 };
 // The matrix-core form: groups 1, dilation 1, K = T * stride with T in {1, 2, 4}.
 bool convt_gemm_supported(int Cin, int Cout, int K, int stride, int dil, int groups);
+// Statistics partials per batch that convt_gemm writes when a.stats is set.
+int convt_gemm_parts(const ConvTArgs& a);
 int convt_padded_cin(int Cin);
 // Output rows q of the GEMM form: (Lout - 1 + pad) / stride + 1.
 int64_t convt_rows(int64_t Lout, int stride, int pad);

@@ -1189,28 +1189,27 @@ class ConvTranspose1DLayer : public Layer {
     split_bcl(in.shape, B, C, L);
     run(in.f32(), (int)C, nullptr, 0, (int)B, L, out.f32(), s);
   }
-  // y [B][out][out_len(L)] from the channel concat [x1 (C1 channels); x2 (C2)], C1 + C2 = in.
+  // GroupNorm(1) statistics partials per batch that run() writes into `stats` (count, mean, M2
+  // each, gn_apply_parts' layout for one group); 0 when this layer's path does not produce them.
+  int stats_parts(int B, int64_t L) const {
+    if (small_ || !gemm_) return 0;
+    return k::convt_gemm_parts(args(d_.in_channels, 0, B, L));
+  }
+  // y [B][out][out_len(L)] from the channel concat [x1 (C1 channels); x2 (C2)], C1 + C2 = in;
+  // with stats (stats_parts(B, L) > 0 only), the GroupNorm(1) partials of y as well.
   void run(const float* x1, int C1, const float* x2, int C2, int B, int64_t L, float* y,
-           Stream& s) {
+           Stream& s, float* stats = nullptr) {
     MNN_REQUIRE(C1 + C2 == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
                 "ConvTranspose1D: channel count mismatch");
-    k::ConvTArgs a;
-    a.B = B;
-    a.C1 = C1;
-    a.C2 = C2;
-    a.Cout = d_.out_channels;
-    a.K = d_.kernel_size;
-    a.stride = d_.stride;
-    a.pad = d_.padding;
-    a.dil = d_.dilation;
-    a.groups = d_.groups;
-    a.L = L;
-    a.Lout = out_len(L);
+    MNN_REQUIRE(!stats || stats_parts(B, L) > 0, MNN_ERR_INVALID_ARGUMENT,
+                "ConvTranspose1D: this configuration writes no statistics partials");
+    k::ConvTArgs a = args(C1, C2, B, L);
     a.x1 = x1;
     a.x2 = x2;
     a.w = w_->ptr();
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
+    a.stats = stats;
     if (small_) {
       k::convt_small(ctx(s), a);
     } else if (gemm_) {
@@ -1232,6 +1231,21 @@ class ConvTranspose1DLayer : public Layer {
   }
 
  private:
+  k::ConvTArgs args(int C1, int C2, int B, int64_t L) const {
+    k::ConvTArgs a;
+    a.B = B;
+    a.C1 = C1;
+    a.C2 = C2;
+    a.Cout = d_.out_channels;
+    a.K = d_.kernel_size;
+    a.stride = d_.stride;
+    a.pad = d_.padding;
+    a.dil = d_.dilation;
+    a.groups = d_.groups;
+    a.L = L;
+    a.Lout = out_len(L);
+    return a;
+  }
   void pack(const float* w) {
     const int T = d_.kernel_size / d_.stride, Cp = k::convt_padded_cin(d_.in_channels);
     std::vector<float> h((size_t)d_.stride * d_.out_channels * T * Cp);
@@ -1316,8 +1330,18 @@ class DecoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t lo = os.back();
     y_.reserve(sizeof(float) * B * Cout * lo);
-    convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, L, y_.f32(), s);
     const int G = norm_->groups();
+    if (const int np = G == 1 ? convt_->stats_parts((int)B, L) : 0) {
+      // GroupNorm(1) statistics from the transposed conv's epilogue (or its split-K reduce); the
+      // apply pass merges them (no statistics pass over y)
+      partials_.reserve(sizeof(float) * 3 * B * np);
+      convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, L, y_.f32(), s,
+                  partials_.f32());
+      norm_->apply_parts(s, y_.f32(), out->f32(), (int)B, lo, partials_.f32(), np,
+                         MNN_ACT_GELU);
+      return;
+    }
+    convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, L, y_.f32(), s);
     const int nchunk = k::gn_num_chunks(Cout, G, lo);
     partials_.reserve(sizeof(float) * 3 * B * G * nchunk);
     k::gn_stats_partial(ctx(s), y_.f32(), (int)B, Cout, lo, G, partials_.f32(), nchunk);
