@@ -97,75 +97,95 @@ __global__ __launch_bounds__(256) void convt_direct_kernel(ConvTArgs a) {
 }
 
 // Few output channels (stride * Cout < 32, e.g. the decoder's last, 2-channel level): a 64-row
-// matrix-core tile would be mostly padding, so one thread computes all Cout * S outputs of one
-// column q in registers from the input read straight from HBM (no unfold): per input channel, T
-// samples from the LDS window and Cout * S * T weights read at wave-uniform addresses. One wave
-// per workgroup and 64 columns, so the grid has many small workgroups; every window load of a
-// channel chunk is issued before the first LDS store.
+// matrix-core tile would be mostly padding, so each lane computes all Cout * S outputs of one
+// column q in registers, reading its T input samples x[c][q - t] straight from global memory
+// (consecutive lanes read consecutive samples; no unfold). A workgroup covers 64 columns; its
+// four waves split the input channels and add their accumulators through LDS in wave order at
+// the end (more waves in flight than one wave per 64 columns would give). The channel row is the
+// same for every lane, and all the weights are staged in LDS once and read at wave-uniform
+// addresses (broadcasts). A wave's channels go in batches of CB, the next batch's loads issued
+// before the current batch is used.
+constexpr int kSmallWaves = 4, kSmallWMax = 12288;  // at most 48 KB of weights staged in LDS
 template <int COUT, int S, int T>
-__global__ __launch_bounds__(64) void convt_small_kernel(ConvTArgs a) {
-  constexpr int NQ = 64;              // columns per workgroup (one per lane)
-  constexpr int CC = 32;              // input channels per LDS chunk
-  constexpr int W = NQ + T - 1;       // window positions: q0 - (T - 1) .. q0 + NQ - 1
-  constexpr int PITCH = W + 1;
-  constexpr int kIt = (CC * W + 63) / 64;
-  __shared__ float xs[CC * PITCH];
-  __shared__ __attribute__((aligned(16))) float wl[CC * COUT * S * T];
-  const int b = blockIdx.y, lane = threadIdx.x;
-  const int64_t q0 = (int64_t)blockIdx.x * NQ, q = q0 + lane;
+__global__ __launch_bounds__(64 * kSmallWaves) void convt_small_kernel(ConvTArgs a) {
+  constexpr int CB = 8;              // channels per load batch
+  constexpr int CST = COUT * S * T;  // weights per input channel, W[c][oc][r + S*t]
+  extern __shared__ __attribute__((aligned(16))) float wl[];  // Cin * CST floats (dynamic)
+  __shared__ float part[kSmallWaves - 1][COUT * S][64];
+  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int64_t q = (int64_t)blockIdx.x * 64 + lane;
   const int Cin = a.C1 + a.C2;
-  const float* x1 = a.x1 + (int64_t)b * a.C1 * a.L;
-  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * a.L : nullptr;
+  const int64_t L = a.L;
+  const float* x1 = a.x1 + (int64_t)b * a.C1 * L;
+  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * L : x1;
+  // this wave's channels: [cb, ce), whole batches except at the end of the range
+  const int per = (Cin + kSmallWaves * CB - 1) / (kSmallWaves * CB) * CB;
+  const int cb = min(wave * per, Cin), ce = min(cb + per, Cin);
+  // tap t of column q is sample q - t (zero outside the signal): clamped address, zeroed value
+  int64_t pos[T];
+  float keep[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int64_t p = q - t;
+    keep[t] = (p >= 0 && p < L) ? 1.f : 0.f;
+    pos[t] = min(max(p, (int64_t)0), L - 1);
+  }
+  auto load_batch = [&](int c0, float (&xv)[CB][T]) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int c = min(c0 + j, Cin - 1);
+      const float* row = c < a.C1 ? x1 + (int64_t)c * L : x2 + (int64_t)(c - a.C1) * L;
+#pragma unroll
+      for (int t = 0; t < T; ++t) xv[j][t] = row[pos[t]];
+    }
+  };
+  float xv[CB][T];
+  load_batch(cb, xv);
+  for (int e = threadIdx.x; e < Cin * CST; e += 64 * kSmallWaves) wl[e] = a.w[e];
+  __syncthreads();
   float acc[COUT][S];
 #pragma unroll
   for (int oc = 0; oc < COUT; ++oc)
 #pragma unroll
     for (int r = 0; r < S; ++r) acc[oc][r] = 0.f;
-  for (int c0 = 0; c0 < Cin; c0 += CC) {
-    float v[kIt];
+  for (int c0 = cb; c0 < ce; c0 += CB) {
+    float xn[CB][T];
+    load_batch(min(c0 + CB, ce - 1), xn);  // after the last batch: reloaded, unused
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int e = lane + 64 * it, i = e / W, jj = e % W, c = c0 + i;
-      const int64_t p = q0 - (T - 1) + jj;
-      v[it] = 0.f;
-      if (e < CC * W && p >= 0 && p < a.L) {
-        if (c < a.C1) v[it] = x1[(int64_t)c * a.L + p];
-        else if (c < Cin) v[it] = x2[(int64_t)(c - a.C1) * a.L + p];
+    for (int j = 0; j < CB; ++j) {
+      if (c0 + j < ce) {  // uniform
+        const float* wc = wl + (c0 + j) * CST;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const float xt = xv[j][t] * keep[t];
+#pragma unroll
+          for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+            for (int r = 0; r < S; ++r)
+              acc[oc][r] = fmaf(xt, wc[oc * (S * T) + r + S * t], acc[oc][r]);
+        }
       }
     }
-    // this chunk's weights W[c][oc][k] (k = r + S*t), contiguous over the chunk's channels
-    constexpr int kW = CC * COUT * S * T;
-    const int cn = min(CC, Cin - c0);
-    float wv[kW / 64];
 #pragma unroll
-    for (int it = 0; it < kW / 64; ++it) {
-      const int e = lane + 64 * it;
-      wv[it] = e < cn * COUT * S * T ? a.w[(int64_t)c0 * COUT * S * T + e] : 0.f;
-    }
-    __syncthreads();  // the previous chunk's window and weight reads are done
+    for (int j = 0; j < CB; ++j)
 #pragma unroll
-    for (int it = 0; it < kIt; ++it) {
-      const int e = lane + 64 * it;
-      if (e < CC * W) xs[(e / W) * PITCH + e % W] = v[it];
-    }
-#pragma unroll
-    for (int it = 0; it < kW / 64; ++it) wl[lane + 64 * it] = wv[it];
-    __syncthreads();
-#pragma unroll 4
-    for (int i = 0; i < cn; ++i) {
-      const float* wc = wl + i * COUT * (S * T);  // same address in every lane: LDS broadcast
-      float xv[T];
-#pragma unroll
-      for (int t = 0; t < T; ++t) xv[t] = xs[i * PITCH + lane + (T - 1) - t];
-#pragma unroll
-      for (int oc = 0; oc < COUT; ++oc)
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-#pragma unroll
-          for (int r = 0; r < S; ++r)
-            acc[oc][r] = fmaf(xv[t], wc[oc * (S * T) + r + S * t], acc[oc][r]);
-    }
+      for (int t = 0; t < T; ++t) xv[j][t] = xn[j][t];
   }
+  if (wave > 0) {
+#pragma unroll
+    for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+      for (int r = 0; r < S; ++r) part[wave - 1][oc * S + r][lane] = acc[oc][r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < kSmallWaves - 1; ++w)
+#pragma unroll
+    for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+      for (int r = 0; r < S; ++r) acc[oc][r] += part[w][oc * S + r][lane];
   float* yb = a.y + (int64_t)b * a.Cout * a.Lout;
 #pragma unroll
   for (int oc = 0; oc < COUT; ++oc) {
@@ -246,18 +266,20 @@ int64_t convt_split_ws_floats(int B, int Cin, int Cout, int K, int stride, int p
 
 bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int groups) {
   return groups == 1 && dil == 1 && stride == 4 && K == 8 && Cin > 0 &&
-         (Cout == 1 || Cout == 2 || Cout == 4);
+         (Cout == 1 || Cout == 2 || Cout == 4) && (int64_t)Cin * Cout * K <= kSmallWMax;
 }
 
 void convt_small(const LaunchCtx& c, const ConvTArgs& a) {
   MNN_REQUIRE(convt_small_supported(a.C1 + a.C2, a.Cout, a.K, a.stride, a.dil, a.groups) &&
                   a.x1 && (a.C2 == 0 || a.x2) && a.w && a.y && a.L > 0 && a.Lout > 0,
               MNN_ERR_INVALID_ARGUMENT, "convt_small: configuration outside the kernel's form");
-  const dim3 grid((unsigned)cdiv(convt_rows(a.Lout, a.stride, a.pad), 64), (unsigned)a.B);
+  const dim3 grid((unsigned)cdiv(convt_rows(a.Lout, a.stride, a.pad), 64), (unsigned)a.B),
+      block(64 * kSmallWaves);
+  const size_t lds = sizeof(float) * (size_t)(a.C1 + a.C2) * a.Cout * a.K;  // the staged weights
   switch (a.Cout) {
-    case 1: return launch(c, "convt_small_f32", convt_small_kernel<1, 4, 2>, grid, dim3(64), 0, a);
-    case 2: return launch(c, "convt_small_f32", convt_small_kernel<2, 4, 2>, grid, dim3(64), 0, a);
-    default: return launch(c, "convt_small_f32", convt_small_kernel<4, 4, 2>, grid, dim3(64), 0, a);
+    case 1: return launch(c, "convt_small_f32", convt_small_kernel<1, 4, 2>, grid, block, lds, a);
+    case 2: return launch(c, "convt_small_f32", convt_small_kernel<2, 4, 2>, grid, block, lds, a);
+    default: return launch(c, "convt_small_f32", convt_small_kernel<4, 4, 2>, grid, block, lds, a);
   }
 }
 
