@@ -28,29 +28,40 @@ constexpr int kPQ = 64;   // output rows q per pack tile
 constexpr int kPC = 64;   // channels per pack tile
 
 // One tile: channels [c0, c0 + 64) x rows q in [q0, q0 + 64). The input window of a channel is
-// positions q0 - (T - 1) .. q0 + 63, staged in LDS; the unfolded rows are written 16 bytes per
-// thread along the channel dimension.
+// positions q0 - (T - 1) .. q0 + 63, staged in LDS: every thread issues all its window loads
+// (clamped addresses, out-of-range values zeroed by a select, no load under a branch) before its
+// first LDS store. The unfolded rows are written 16 bytes per thread along the channel dimension.
 template <int T>
 __global__ __launch_bounds__(256) void convt_pack_kernel(ConvTPackArgs a) {
   constexpr int W = kPQ + T - 1;  // window positions per channel
   constexpr int PITCH = W + 1;
+  constexpr int NE = (kPC * W + 255) / 256;  // window elements per thread
   __shared__ float tile[kPC * PITCH];
   const int b = blockIdx.z;
   const int64_t q0 = (int64_t)blockIdx.x * kPQ;
   const int c0 = blockIdx.y * kPC;
   const int tid = threadIdx.x;
-  const float* x1 = a.x1 + (int64_t)b * a.C1 * a.L;
-  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * a.L : nullptr;
-  for (int e = tid; e < kPC * W; e += 256) {
-    const int i = e / W, jj = e % W;
+  const int Cin = a.C1 + a.C2;
+  const int64_t L = a.L;
+  const float* x1 = a.x1 + (int64_t)b * a.C1 * L;
+  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * L : x1;
+  float v[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = tid + 256 * k, i = e / W, jj = e % W;
     const int c = c0 + i;
     const int64_t p = q0 - (T - 1) + jj;
-    float v = 0.f;
-    if (p >= 0 && p < a.L) {
-      if (c < a.C1) v = x1[(int64_t)c * a.L + p];
-      else if (c < a.C1 + a.C2) v = x2[(int64_t)(c - a.C1) * a.L + p];
-    }
-    tile[i * PITCH + jj] = v;
+    const bool ok = e < kPC * W && c < Cin && p >= 0 && p < L;
+    const int cc = min(c, Cin - 1);
+    const int64_t pp = min(max(p, (int64_t)0), L - 1);
+    const float* src = cc < a.C1 ? x1 + (int64_t)cc * L : x2 + (int64_t)(cc - a.C1) * L;
+    const float val = src[pp];
+    v[k] = ok ? val : 0.f;
+  }
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = tid + 256 * k;
+    if (e < kPC * W) tile[(e / W) * PITCH + e % W] = v[k];
   }
   __syncthreads();
   const int kp = T * a.Cp;
