@@ -225,6 +225,62 @@ __global__ __launch_bounds__(256) void convt2d_gather_phase_kernel(ConvT2DArgs a
   }
 }
 
+// The phase form for a fixed kernel and stride (dilation 1): the taps of output (oh, SW*q + r) are
+// kh = (oh + ph) mod SH + SH*jh and kw = (SW*q + r + pw) mod SW + SW*jw, so each thread loads
+// ceil(KH/SH) x SW x ceil(KW/SW) values at clamped addresses (taps outside the kernel or the input
+// zeroed by a select), every load in flight at once, and sums them in the same order as the
+// general kernels (kh ascending, then kw ascending).
+template <int KH, int KW, int SH, int SW>
+__global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a) {
+  constexpr int NJH = (KH + SH - 1) / SH, NJW = (KW + SW - 1) / SW;
+  const unsigned nq = ((unsigned)a.Wo + SW - 1) / SW, cells = (unsigned)a.Ho * nq;
+  const unsigned e = blockIdx.x * 256u + threadIdx.x;
+  const unsigned ec = min(e, cells - 1);
+  const int oc = blockIdx.y, b = blockIdx.z;
+  const int oh = (int)(ec / nq), q = (int)(ec - (unsigned)oh * nq);
+  const int64_t n_in = (int64_t)a.H * a.W;
+  const float* zb = a.z + ((int64_t)b * a.Cout + oc) * KH * KW * n_in;
+  const int th = oh + a.ph;
+  float v[NJH][SW][NJW];
+  bool ok[NJH][SW][NJW];
+#pragma unroll
+  for (int jh = 0; jh < NJH; ++jh) {
+    const int kh = th % SH + SH * jh, ih = (th - kh) / SH;
+    const bool okh = kh < KH && th - kh >= 0 && ih < a.H;
+    const int khc = min(kh, KH - 1), ihc = min(max(ih, 0), a.H - 1);
+#pragma unroll
+    for (int r = 0; r < SW; ++r) {
+      const int tw = SW * q + r + a.pw;
+#pragma unroll
+      for (int jw = 0; jw < NJW; ++jw) {
+        const int kw = tw % SW + SW * jw, iw = (tw - kw) / SW;
+        const bool okw = kw < KW && tw - kw >= 0 && iw < a.W;
+        const int kwc = min(kw, KW - 1), iwc = min(max(iw, 0), a.W - 1);
+        v[jh][r][jw] = zb[(int64_t)(khc * KW + kwc) * n_in + (int64_t)ihc * a.W + iwc];
+        ok[jh][r][jw] = okh && okw;
+      }
+    }
+  }
+  float acc[SW];
+#pragma unroll
+  for (int r = 0; r < SW; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int jh = 0; jh < NJH; ++jh)
+#pragma unroll
+    for (int r = 0; r < SW; ++r)
+#pragma unroll
+      for (int jw = 0; jw < NJW; ++jw)
+        if (ok[jh][r][jw]) acc[r] += v[jh][r][jw];
+  if (e >= cells) return;
+  float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + oh) * a.Wo;
+  const float bias = a.bias ? a.bias[oc] : 0.f;
+#pragma unroll
+  for (int r = 0; r < SW; ++r) {
+    const int ow = SW * q + r;
+    if (ow < a.Wo) yr[ow] = acc[r] + bias;
+  }
+}
+
 __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
   const unsigned n = blockIdx.x * 256u + threadIdx.x;
@@ -476,7 +532,11 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
   gemm(c, g);
   ConvT2DArgs t = a;
   t.z = z;
-  if (a.dh == 1 && a.dw == 1 && a.sw <= 8) {
+  if (a.dh == 1 && a.dw == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2) {
+    const int64_t cells = (int64_t)a.Ho * ((a.Wo + 1) / 2);
+    launch(c, "convt2d_gather_f32", convt2d_gather_fixed_kernel<3, 3, 2, 2>,
+           plane_grid(cells, a.Cout, a.B), dim3(256), 0, t);
+  } else if (a.dh == 1 && a.dw == 1 && a.sw <= 8) {
     const int64_t cells = (int64_t)a.Ho * ((a.Wo + a.sw - 1) / a.sw);
     launch(c, "convt2d_gather_f32", convt2d_gather_phase_kernel, plane_grid(cells, a.Cout, a.B),
            dim3(256), 0, t);

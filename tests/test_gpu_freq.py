@@ -129,6 +129,8 @@ CONVT_CASES = [
     (1, 7, 0, 5, 6, 5, (3, 4), (2, 3), (1, 2), (1, 2), (1, 1), 1),        # odd sizes
     (2, 6, 0, 4, 5, 6, (3, 3), (1, 2), (0, 1), (0, 1), (2, 1), 1),        # dilation
     (2, 8, 0, 6, 5, 4, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 2),        # grouped: direct
+    (1, 12, 0, 8, 7, 9, (3, 3), (2, 2), (0, 0), (0, 0), (1, 1), 1),       # 3x3 / 2 gather, no pad
+    (2, 10, 0, 6, 5, 6, (3, 3), (2, 2), (1, 1), (0, 1), (1, 1), 1),       # odd output height
 ]
 
 
