@@ -281,6 +281,151 @@ __global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a
   }
 }
 
+// Few output channels, 3x3 kernel, stride 2, padding 1, dilation 1 (the frequency decoder's last
+// level, 2 channels): a matrix-core tile over Cout * 9 tap rows would be mostly padding. Output
+// o = 2i + k - 1, so the outputs 2m and 2m + 1 of a dimension take the taps (k 1 at i = m) and
+// (k 0 at i = m + 1, k 2 at i = m). A lane owns four consecutive input cells of one row,
+// (mh, 4g .. 4g + 3), and computes their 2 x 8 outputs of every output channel from input rows mh
+// and mh + 1, columns 4g .. 4g + 4 (zero past the input): per channel and row one 16-byte load
+// (VEC: rows 16-byte aligned) and one scalar. The 64 lanes of a wave cover 4 rows x 16 column
+// groups; the four waves of a workgroup split the input channels (batches of CB, the next
+// batch's loads in flight) and add their accumulators through LDS in wave order; the weights are
+// staged in LDS once and read as broadcasts.
+constexpr int kT2Waves = 4, kT2WMax = 12288;  // at most 48 KB of weights staged in LDS
+constexpr int kT2Rows = 4, kT2Cols = 64;      // input cells per workgroup: 4 rows x 64 columns
+template <int COUT, bool VEC>
+__global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArgs a) {
+  constexpr int CB = 4;
+  constexpr int CST = COUT * 9;  // weights per input channel, w[c][oc][kh][kw]
+  extern __shared__ __attribute__((aligned(16))) float wl[];  // Cin * CST floats (dynamic)
+  __shared__ float part[kT2Waves - 1][COUT * 16][64];
+  const int b = blockIdx.z, lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int mh = blockIdx.y * kT2Rows + (lane >> 4);
+  const int mw0 = blockIdx.x * kT2Cols + 4 * (lane & 15);
+  const int Cin = a.C1 + a.C2;
+  const int64_t hw = (int64_t)a.H * a.W;
+  const float* x1 = a.x1 + (int64_t)b * a.C1 * hw;
+  const float* x2 = a.x2 ? a.x2 + (int64_t)b * a.C2 * hw : x1;
+  const int per = (Cin + kT2Waves * CB - 1) / (kT2Waves * CB) * CB;
+  const int cb = min(wave * per, Cin), ce = min(cb + per, Cin);
+  // input rows mh, mh + 1 (clamped; a row past the input reads as zero), columns mw0 .. mw0 + 4
+  const int r0 = min(mh, a.H - 1), r1 = min(mh + 1, a.H - 1);
+  const float rk1 = mh + 1 < a.H ? 1.f : 0.f;
+  float ck[5];
+  int col[5];
+#pragma unroll
+  for (int e = 0; e < 5; ++e) {
+    ck[e] = mw0 + e < a.W ? 1.f : 0.f;
+    col[e] = min(mw0 + e, a.W - 1);
+  }
+  // xv[j][row][e]: channel c0 + j, input row mh + row, column mw0 + e
+  auto load_batch = [&](int c0, float (&xv)[CB][2][5]) {
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      const int c = min(c0 + j, Cin - 1);
+      const float* pl = c < a.C1 ? x1 + (int64_t)c * hw : x2 + (int64_t)(c - a.C1) * hw;
+#pragma unroll
+      for (int row = 0; row < 2; ++row) {
+        const float* pr = pl + (int64_t)(row ? r1 : r0) * a.W;
+        if constexpr (VEC) {
+          const float4 v4 = *reinterpret_cast<const float4*>(pr + min(mw0, a.W - 4));
+          xv[j][row][0] = v4.x;
+          xv[j][row][1] = v4.y;
+          xv[j][row][2] = v4.z;
+          xv[j][row][3] = v4.w;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xv[j][row][e] = pr[col[e]];
+        }
+        xv[j][row][4] = pr[col[4]];
+      }
+    }
+  };
+  float xv[CB][2][5];
+  load_batch(cb, xv);
+  for (int e = threadIdx.x; e < Cin * CST; e += 64 * kT2Waves) wl[e] = a.w[e];
+  __syncthreads();
+  // acc[oc][rh][ocol]: output row 2 mh + rh, output column 2 mw0 + ocol
+  float acc[COUT][2][8];
+#pragma unroll
+  for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[oc][rh][e] = 0.f;
+  for (int c0 = cb; c0 < ce; c0 += CB) {
+    float xn[CB][2][5];
+    load_batch(min(c0 + CB, ce - 1), xn);  // after the last batch: reloaded, unused
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+      if (c0 + j < ce) {  // uniform
+        float x0[5], x1v[5];
+#pragma unroll
+        for (int e = 0; e < 5; ++e) {
+          x0[e] = xv[j][0][e] * ck[e];
+          x1v[e] = xv[j][1][e] * ck[e] * rk1;
+        }
+#pragma unroll
+        for (int oc = 0; oc < COUT; ++oc) {
+          const float* k = wl + (c0 + j) * CST + oc * 9;  // k[3 * kh + kw]
+          const float k0 = k[0], k1 = k[1], k2 = k[2], k3 = k[3], k4 = k[4], k5 = k[5],
+                      k6 = k[6], k7 = k[7], k8 = k[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // cell column e: x0[e] = x(mh, m), x0[e + 1] = x(mh, m + 1), x1v the row below
+            acc[oc][0][2 * e] = fmaf(x0[e], k4, acc[oc][0][2 * e]);
+            acc[oc][0][2 * e + 1] = fmaf(x0[e], k5, fmaf(x0[e + 1], k3, acc[oc][0][2 * e + 1]));
+            acc[oc][1][2 * e] = fmaf(x0[e], k7, fmaf(x1v[e], k1, acc[oc][1][2 * e]));
+            acc[oc][1][2 * e + 1] =
+                fmaf(x0[e], k8, fmaf(x0[e + 1], k6, fmaf(x1v[e], k2, fmaf(x1v[e + 1], k0,
+                                                                            acc[oc][1][2 * e + 1]))));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < CB; ++j)
+#pragma unroll
+      for (int row = 0; row < 2; ++row)
+#pragma unroll
+        for (int e = 0; e < 5; ++e) xv[j][row][e] = xn[j][row][e];
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+      for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part[wave - 1][(oc * 2 + rh) * 8 + e][lane] = acc[oc][rh][e];
+  }
+  __syncthreads();
+  if (wave != 0 || mh >= a.H || mw0 >= a.W) return;
+#pragma unroll
+  for (int w = 0; w < kT2Waves - 1; ++w)
+#pragma unroll
+    for (int oc = 0; oc < COUT; ++oc)
+#pragma unroll
+      for (int rh = 0; rh < 2; ++rh)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[oc][rh][e] += part[w][(oc * 2 + rh) * 8 + e][lane];
+#pragma unroll
+  for (int oc = 0; oc < COUT; ++oc) {
+    const float bv = a.bias ? a.bias[oc] : 0.f;
+#pragma unroll
+    for (int rh = 0; rh < 2; ++rh) {
+      const int oh = 2 * mh + rh;
+      if (oh >= a.Ho) continue;
+      float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + oh) * a.Wo;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int ow = 2 * mw0 + e;
+        if (ow < a.Wo) yr[ow] = acc[oc][rh][e] + bv;
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void convt2d_direct_kernel(ConvT2DArgs a) {
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
   const unsigned n = blockIdx.x * 256u + threadIdx.x;
@@ -548,6 +693,35 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
 
 int64_t convt2d_unfold_floats(const ConvT2DArgs& a) {
   return (int64_t)a.B * a.H * a.W * convt2d_padded_cin(a.C1 + a.C2);
+}
+
+bool convt2d_small_supported(const ConvT2DArgs& a) {
+  return a.groups == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2 && a.ph == 1 &&
+         a.pw == 1 && a.dh == 1 && a.dw == 1 && (a.Cout == 1 || a.Cout == 2 || a.Cout == 4) &&
+         (int64_t)(a.C1 + a.C2) * a.Cout * 9 <= kT2WMax && a.Ho <= 2 * a.H && a.Wo <= 2 * a.W &&
+         a.W >= 4 && a.H <= 4 * 65535 && a.B <= 65535;
+}
+
+void convt2d_small(const LaunchCtx& c, const ConvT2DArgs& a) {
+  check_convt2d(a);
+  MNN_REQUIRE(a.w && convt2d_small_supported(a), MNN_ERR_INVALID_ARGUMENT,
+              "convt2d_small: configuration outside the kernel's form");
+  const dim3 grid((unsigned)cdiv(a.W, kT2Cols), (unsigned)cdiv(a.H, kT2Rows), (unsigned)a.B),
+      block(64 * kT2Waves);
+  const size_t lds = sizeof(float) * (size_t)(a.C1 + a.C2) * a.Cout * 9;
+  // 16-byte row loads when every row start is 16-byte aligned (a column group past W - 4 loads
+  // the last four columns and uses none of them)
+  const bool vec = a.W % 4 == 0 && (reinterpret_cast<uintptr_t>(a.x1) & 15) == 0 &&
+                   (a.C2 == 0 || (reinterpret_cast<uintptr_t>(a.x2) & 15) == 0);
+#define MNN_T2S(CO) \
+  return vec ? launch(c, "convt2d_small_f32", convt2d_small_kernel<CO, true>, grid, block, lds, a) \
+             : launch(c, "convt2d_small_f32", convt2d_small_kernel<CO, false>, grid, block, lds, a)
+  switch (a.Cout) {
+    case 1: MNN_T2S(1);
+    case 2: MNN_T2S(2);
+    default: MNN_T2S(4);
+  }
+#undef MNN_T2S
 }
 
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a) {

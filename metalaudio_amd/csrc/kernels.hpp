@@ -232,6 +232,10 @@ void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, flo
 void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
                   float* unfold);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
+// Few output channels (1, 2, 4), 3x3 kernel, stride 2, padding 1, dilation 1, groups 1: a
+// direct kernel reading the input in place (no unfold, no tap products).
+bool convt2d_small_supported(const ConvT2DArgs& a);
+void convt2d_small(const LaunchCtx& c, const ConvT2DArgs& a);
 
 // ------------------------------------------------------------------ separation (k_separate.hip)
 // One segment [start, start + len) of interleaved audio x [n][C]: planar padded network input

@@ -1580,7 +1580,9 @@ class ConvTranspose2DLayer : public Layer {
     a.w = w_->ptr();
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
-    if (gemm_) {
+    if (k::convt2d_small_supported(a)) {
+      k::convt2d_small(ctx(s), a);
+    } else if (gemm_) {
       z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
       unfold_.reserve(sizeof(float) * k::convt2d_unfold_floats(a));
       k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), unfold_.f32());

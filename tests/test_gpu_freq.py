@@ -131,6 +131,12 @@ CONVT_CASES = [
     (2, 8, 0, 6, 5, 4, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 2),        # grouped: direct
     (1, 12, 0, 8, 7, 9, (3, 3), (2, 2), (0, 0), (0, 0), (1, 1), 1),       # 3x3 / 2 gather, no pad
     (2, 10, 0, 6, 5, 6, (3, 3), (2, 2), (1, 1), (0, 1), (1, 1), 1),       # odd output height
+    # few output channels, 3x3 / 2 / pad 1: the direct kernel (no unfold, no tap products)
+    (2, 12, 0, 2, 9, 70, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),      # two row workgroups
+    (1, 20, 0, 2, 6, 72, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),      # 16-byte row loads
+    (1, 40, 24, 4, 6, 5, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),      # concat, 4 channels
+    (1, 9, 0, 1, 5, 66, (3, 3), (2, 2), (1, 1), (0, 0), (1, 1), 1),       # 1 channel, Ho = 2H - 1
+    (1, 70, 0, 2, 4, 3, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),       # ragged channel split
 ]
 
 
@@ -166,7 +172,8 @@ def test_conv_transpose2d_parity(dev, stream, B, c1, c2, cout, H, W, k, s, p, op
 
 @pytest.mark.parametrize("B,cin,cskip,cout,H,W,groups", [(1, 96, 96, 48, 8, 4, 8),
                                                          (2, 16, 16, 8, 12, 10, 4),
-                                                         (1, 7, 0, 5, 6, 6, 1)])
+                                                         (1, 7, 0, 5, 6, 6, 1),
+                                                         (1, 24, 24, 2, 10, 70, 2)])
 def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, groups):
     say(f"freq decoder block B={B} {cin}+{cskip}->{cout} {H}x{W} G={groups}")
     x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
