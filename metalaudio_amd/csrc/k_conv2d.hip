@@ -131,6 +131,113 @@ __global__ __launch_bounds__(256) void conv2d_unfold_tiled_kernel(Conv2DArgs a) 
   }
 }
 
+// Few input channels (CIN * 3 * 3 taps: the frequency encoder's first level, 2 channels): the
+// contraction is too short for the matrix cores, so one thread per output position loads its
+// whole input window (CIN x 3 x 3 samples, branch-free: mirrored or clamped indices, padding
+// zeroed by a select) into registers and produces COB output channels from weights staged in
+// LDS ([tap][channel], 16-byte broadcasts). With stats, each workgroup also writes the GroupNorm
+// partial (count, mean, M2) of its outputs (two passes over a thread's registers, then the
+// workgroup merge) for the group its COB channels belong to (the host checks that COB divides the
+// group's channel count): parts[((b * G + g) * nparts + j) * 3], j = (channel block within the
+// group) * gridDim.x + blockIdx.x, nparts = (C / G / COB) * gridDim.x. Workgroups of 1024 threads
+// keep the partial count (which every apply workgroup merges) low.
+constexpr int kC2Threads = 1024;  // output positions per workgroup (one per thread)
+template <int CIN, int COB, bool REFLECT>
+__global__ __launch_bounds__(kC2Threads) void conv2d_small_kernel(Conv2DArgs a, float* stats,
+                                                                 int G) {
+  constexpr int CK = CIN * 9;
+  __shared__ __attribute__((aligned(16))) float wt[CK * COB + COB];  // [tap][co], then bias
+  __shared__ float red[3 * (kC2Threads / 64)];
+  const int b = blockIdx.z, co0 = blockIdx.y * COB;
+  const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
+  const unsigned n = blockIdx.x * (unsigned)kC2Threads + threadIdx.x;
+  const bool valid = n < hw;
+  const unsigned nc = valid ? n : hw - 1;
+  const int oh = (int)(nc / (unsigned)a.Wo), ow = (int)(nc - (unsigned)oh * a.Wo);
+  // weights and bias of this workgroup's channels (issued first)
+  constexpr int NW = CK * COB + COB, PER = (NW + kC2Threads - 1) / kC2Threads;
+  float wv[PER];
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = threadIdx.x + kC2Threads * r;
+    const int iw = min(i, CK * COB - 1), co = iw / CK, e = iw - co * CK;
+    const float* src = i < CK * COB ? a.w + (int64_t)(co0 + co) * CK + e
+                                    : (a.bias ? a.bias + co0 + min(i - CK * COB, COB - 1)
+                                              : a.w);
+    const float v = *src;
+    wv[r] = (i < CK * COB || a.bias) ? v : 0.f;
+  }
+  // the input window
+  const float* xb = a.x + (int64_t)b * CIN * a.H * a.W;
+  float xv[CK];
+#pragma unroll
+  for (int ic = 0; ic < CIN; ++ic)
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+      for (int kw = 0; kw < 3; ++kw) {
+        int r = oh * a.sh - a.ph + kh, c = ow * a.sw - a.pw + kw;
+        float keep = 1.f;
+        if constexpr (REFLECT) {
+          r = reflect_index(r, a.H);
+          c = reflect_index(c, a.W);
+        } else {
+          keep = (r >= 0 && r < a.H && c >= 0 && c < a.W) ? 1.f : 0.f;
+          r = min(max(r, 0), a.H - 1);
+          c = min(max(c, 0), a.W - 1);
+        }
+        xv[(ic * 3 + kh) * 3 + kw] = xb[((int64_t)ic * a.H + r) * a.W + c] * keep;
+      }
+#pragma unroll
+  for (int r = 0; r < PER; ++r) {
+    const int i = threadIdx.x + kC2Threads * r;
+    if (i < CK * COB) {
+      const int co = i / CK, e = i - co * CK;
+      wt[e * COB + co] = wv[r];
+    } else if (i < NW) {
+      wt[i] = wv[r];
+    }
+  }
+  __syncthreads();
+  float acc[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j) acc[j] = wt[CK * COB + j];
+#pragma unroll
+  for (int e = 0; e < CK; ++e)
+#pragma unroll
+    for (int j4 = 0; j4 < COB; j4 += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(wt + e * COB + j4);
+      acc[j4 + 0] = fmaf(xv[e], w4.x, acc[j4 + 0]);
+      acc[j4 + 1] = fmaf(xv[e], w4.y, acc[j4 + 1]);
+      acc[j4 + 2] = fmaf(xv[e], w4.z, acc[j4 + 2]);
+      acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
+    }
+  if (valid) {
+    float* yb = a.y + ((int64_t)b * a.Cout + co0) * hw + n;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) yb[(int64_t)j * hw] = acc[j];
+  }
+  if (stats) {  // uniform
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) s += acc[j];
+    float mean = s * (1.f / COB), m2 = 0.f;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) m2 = fmaf(acc[j] - mean, acc[j] - mean, m2);
+    float cnt = valid ? (float)COB : 0.f;
+    if (!valid) mean = m2 = 0.f;
+    block_welford(cnt, mean, m2, red);
+    if (threadIdx.x == 0) {
+      const int cpg = a.Cout / G, g = co0 / cpg, nblk = cpg / COB;
+      const int nparts = nblk * gridDim.x, j = (co0 % cpg) / COB * gridDim.x + blockIdx.x;
+      float* o = stats + (((int64_t)b * G + g) * nparts + j) * 3;
+      o[0] = cnt;
+      o[1] = mean;
+      o[2] = m2;
+    }
+  }
+}
+
 // Grid (output plane / 256, Cout, B); 32-bit plane index (host-checked).
 __global__ __launch_bounds__(256) void conv2d_direct_kernel(Conv2DArgs a) {
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
@@ -693,6 +800,40 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
 
 int64_t convt2d_unfold_floats(const ConvT2DArgs& a) {
   return (int64_t)a.B * a.H * a.W * convt2d_padded_cin(a.C1 + a.C2);
+}
+
+namespace {
+constexpr int kC2Cob = 8;  // output channels per thread of conv2d_small_kernel
+}
+
+bool conv2d_small_supported(const Conv2DArgs& a) {
+  return a.groups == 1 && (a.Cin == 1 || a.Cin == 2) && a.KH == 3 && a.KW == 3 && a.dh == 1 &&
+         a.dw == 1 && a.Cout % kC2Cob == 0 && (int64_t)a.Ho * a.Wo < ((int64_t)1 << 31) &&
+         a.Cout / kC2Cob <= 65535 && a.B <= 65535;
+}
+
+int conv2d_small_parts(const Conv2DArgs& a, int G) {
+  if (!conv2d_small_supported(a) || G <= 0 || a.Cout % G != 0 || (a.Cout / G) % kC2Cob != 0)
+    return 0;
+  return (a.Cout / G / kC2Cob) * (int)cdiv((int64_t)a.Ho * a.Wo, kC2Threads);
+}
+
+void conv2d_small(const LaunchCtx& c, const Conv2DArgs& a, float* stats, int G) {
+  check_conv2d(a);
+  MNN_REQUIRE(conv2d_small_supported(a) && a.w && (!stats || conv2d_small_parts(a, G) > 0),
+              MNN_ERR_INVALID_ARGUMENT, "conv2d_small: configuration outside the kernel's form");
+  const dim3 grid((unsigned)cdiv((int64_t)a.Ho * a.Wo, kC2Threads), (unsigned)(a.Cout / kC2Cob),
+                  (unsigned)a.B);
+#define MNN_C2S(CI, R) \
+  return launch(c, "conv2d_small_f32", conv2d_small_kernel<CI, kC2Cob, R>, grid, \
+                dim3(kC2Threads), 0, a, stats, G)
+  if (a.Cin == 1) {
+    if (a.reflect) MNN_C2S(1, true);
+    MNN_C2S(1, false);
+  }
+  if (a.reflect) MNN_C2S(2, true);
+  MNN_C2S(2, false);
+#undef MNN_C2S
 }
 
 bool convt2d_small_supported(const ConvT2DArgs& a) {

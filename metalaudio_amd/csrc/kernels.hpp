@@ -199,6 +199,12 @@ struct Conv2DArgs {
 // Cin*KH*KW) by conv2d_pack_weights; unfold workspace of conv2d_unfold_floats floats (0 for
 // pointwise convs, which read the input directly).
 int conv2d_padded_k(int Cin, int KH, int KW);
+// Few input channels (1 or 2), 3x3 kernel, dilation 1, groups 1, Cout a multiple of 8: a direct
+// register-window kernel (no unfold). With stats, GroupNorm partials for G groups as well,
+// conv2d_small_parts(a, G) per (batch, group) in gn_apply_parts' layout (0: not available).
+bool conv2d_small_supported(const Conv2DArgs& a);
+int conv2d_small_parts(const Conv2DArgs& a, int G);
+void conv2d_small(const LaunchCtx& c, const Conv2DArgs& a, float* stats, int G);
 bool conv2d_gemm_supported(const Conv2DArgs& a);
 bool conv2d_pointwise(const Conv2DArgs& a);
 int64_t conv2d_unfold_floats(const Conv2DArgs& a);

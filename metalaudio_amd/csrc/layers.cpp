@@ -1443,10 +1443,35 @@ class Conv2DLayer : public Layer {
     split_bchw(in.shape, B, C, H, W);
     run(in.f32(), (int)B, H, W, out.f32(), s);
   }
-  void run(const float* x, int B, int64_t H, int64_t W, float* y, Stream& s) {
+  // GroupNorm partials per (batch, group) that run() writes for G groups (0: this configuration
+  // does not produce them; the caller runs a statistics pass).
+  int stats_parts(int B, int64_t H, int64_t W, int G) const {
+    return k::conv2d_small_parts(args(nullptr, B, H, W, nullptr), G);
+  }
+  void run(const float* x, int B, int64_t H, int64_t W, float* y, Stream& s,
+           float* stats = nullptr, int G = 0) {
+    MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH, "Conv2D: input too large");
+    const k::Conv2DArgs a = args(x, B, H, W, y);
+    MNN_REQUIRE(!stats || k::conv2d_small_parts(a, G) > 0, MNN_ERR_INVALID_ARGUMENT,
+                "Conv2D: this configuration writes no GroupNorm partials");
+    if (k::conv2d_small_supported(a)) {
+      k::conv2d_small(ctx(s), a, stats, G);
+    } else if (gemm_) {
+      const int64_t uf = k::conv2d_unfold_floats(a);
+      if (uf > 0) unfold_.reserve(sizeof(float) * uf);
+      const int64_t wf = k::conv2d_split_ws_floats(a);
+      if (wf > 0) split_.reserve(sizeof(float) * wf);
+      k::conv2d_gemm(ctx(s), a, wpack_.f32(), uf > 0 ? unfold_.f32() : nullptr,
+                     wf > 0 ? split_.f32() : nullptr);
+    } else {
+      k::conv2d_direct(ctx(s), a);
+    }
+  }
+
+ private:
+  k::Conv2DArgs args(const float* x, int B, int64_t H, int64_t W, float* y) const {
     const auto o = out_size(H, W);
     const auto p = padding(H, W);
-    MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH, "Conv2D: input too large");
     k::Conv2DArgs a;
     a.B = B;
     a.Cin = d_.in_channels;
@@ -1469,16 +1494,7 @@ class Conv2DLayer : public Layer {
     a.w = w_->ptr();
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
-    if (gemm_) {
-      const int64_t uf = k::conv2d_unfold_floats(a);
-      if (uf > 0) unfold_.reserve(sizeof(float) * uf);
-      const int64_t wf = k::conv2d_split_ws_floats(a);
-      if (wf > 0) split_.reserve(sizeof(float) * wf);
-      k::conv2d_gemm(ctx(s), a, wpack_.f32(), uf > 0 ? unfold_.f32() : nullptr,
-                     wf > 0 ? split_.f32() : nullptr);
-    } else {
-      k::conv2d_direct(ctx(s), a);
-    }
+    return a;
   }
 
  protected:
@@ -1657,6 +1673,14 @@ class FreqEncoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t L = os[os.size() - 2] * os.back();
     y_.reserve(sizeof(float) * B * Cout * L);
+    const int G = norm_->groups();
+    if (const int np = conv_->stats_parts((int)B, H, W, G)) {
+      // few input channels: the direct conv writes the GroupNorm partials (no statistics pass)
+      partials_.reserve(sizeof(float) * 3 * B * G * np);
+      conv_->run(in.f32(), (int)B, H, W, y_.f32(), s, partials_.f32(), G);
+      norm_->apply_parts(s, y_.f32(), out.f32(), (int)B, L, partials_.f32(), np, MNN_ACT_GELU);
+      return;
+    }
     conv_->run(in.f32(), (int)B, H, W, y_.f32(), s);
     gn_gelu(norm_.get(), partials_, y_.f32(), out.f32(), (int)B, Cout, L, s);
   }

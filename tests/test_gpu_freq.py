@@ -103,6 +103,10 @@ CONV_CASES = [
     (1, 37, 19, 9, 7, (1, 1), (1, 1), "valid", (0, 0), (1, 1), 1),         # pointwise, odd sizes
     (2, 8, 12, 9, 8, (3, 3), (2, 1), "explicit", (1, 0), (1, 1), 4),       # grouped: direct
     (1, 6, 6, 12, 12, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 6),        # depthwise: direct
+    # 1 or 2 input channels, 3x3: the register-window kernel (no unfold)
+    (2, 2, 48, 64, 32, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),
+    (1, 1, 16, 33, 47, (3, 3), (1, 1), "explicit", (1, 1), (1, 1), 1),     # zeros, odd sizes
+    (1, 2, 8, 20, 18, (3, 3), (2, 1), "valid", (0, 0), (1, 1), 1),
 ]
 
 
@@ -207,6 +211,39 @@ def test_freq_encoder_htdemucs_level_shapes(dev, stream):
         ref = oracle.freq_encoder_block(x, w, b, gm, bt, 8, (8, 1), (4, 1))
         assert_close(got, ref, ATOL, RTOL, f"freq level {cin}->{cout}")
         x = got
+
+
+@pytest.mark.parametrize("B,cin,cout,H,W,groups", [(1, 2, 48, 130, 90, 2),
+                                                   (2, 1, 16, 40, 34, 1),
+                                                   (1, 2, 48, 64, 32, 8)])
+def test_freq_encoder_block_small_input(dev, stream, B, cin, cout, H, W, groups):
+    """One or two input channels: the register-window conv. When 8 divides a group's channel
+    count it also writes the GroupNorm partials (no statistics pass over its output)."""
+    import ctypes
+    from metalaudio_amd import _lib
+    say(f"freq encoder block B={B} {cin}->{cout} {H}x{W} G={groups}")
+    x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
+    w = scaled((cout, cin, 3, 3), cin * 9)
+    b = (0.3 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    blk = nn.FreqUNetEncoderBlock2D(dev, cin, cout, (3, 3), (2, 2), groups)
+    blk.load_weights(w, b, gm, bt)
+    lib = _lib.lib()
+    assert lib.mnn_debug_set_launch_log(dev.handle, 1) == 0
+    try:
+        got = run_layer(blk, x, dev, stream)
+    finally:
+        lib.mnn_debug_set_launch_log(dev.handle, 0)
+    need = ctypes.c_size_t()
+    lib.mnn_debug_launch_log(dev.handle, None, 0, ctypes.byref(need))
+    buf = ctypes.create_string_buffer(need.value)
+    assert lib.mnn_debug_launch_log(dev.handle, buf, need.value, ctypes.byref(need)) == 0
+    names = [ln.split()[0] for ln in buf.value.decode().splitlines() if ln.strip()]
+    assert "conv2d_small_f32" in names, names
+    assert ("gn_stats_partial" in names) == ((cout // groups) % 8 != 0), names
+    ref = oracle.freq_encoder_block(x, w, b, gm, bt, groups, (3, 3), (2, 2))
+    assert_close(got, ref, ATOL, RTOL, "freq encoder block, small input")
 
 
 def test_freq_layers_reject_bad_inputs(dev, stream):
