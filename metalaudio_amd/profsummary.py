@@ -56,6 +56,11 @@ FAMILIES = [
     ("convt_small_kernel", "convt_small_f32"),
     ("convt_reduce_kernel", "convt_reduce_f32"),
     ("conv2d_unfold_kernel", "conv2d_unfold_f32"),
+    ("conv2d_unfold_tiled_kernel", "conv2d_unfold_f32"),
+    ("conv2d_small_kernel", "conv2d_small_f32"),
+    ("conv2d_split_reduce_kernel", "conv2d_split_reduce_f32"),
+    ("convt2d_gather_fixed_kernel", "convt2d_gather_f32"),
+    ("convt2d_small_kernel", "convt2d_small_f32"),
     ("conv2d_direct_kernel", "conv2d_direct_f32"),
     ("convt2d_gather_kernel", "convt2d_gather_f32"),
     ("convt2d_gather_phase_kernel", "convt2d_gather_f32"),
