@@ -14,6 +14,8 @@
 // on the LDS-DMA GEMM with its transposed-conv epilogue, which scatters row m, column q to
 // y[oc][stride*q + r - pad] (+bias). The pack kernel reads the input rows once and writes their
 // unfolded transpose (T times the input), concatenating the decoder's skip on the way.
+#include <algorithm>
+
 #include "device_utils.hpp"
 #include "kernels.hpp"
 
@@ -212,13 +214,16 @@ __global__ __launch_bounds__(64 * kSmallWaves) void convt_small_kernel(ConvTArgs
 // Sum of the K parts of the GEMM form, then the scatter of convt's epilogue:
 // y[b][oc][s*q + r - pad] = bias[oc] + sum_p ws[b][p][s*oc + r][q]. One thread per column q of one
 // output channel: it reads the s phase rows (coalesced over q) and writes s consecutive samples.
-// With stats, each workgroup writes the GroupNorm(1) partial (count, mean, M2) of the samples it
-// stored at stats[((b * Cout + oc) * gridDim.x + blockIdx.x) * 3].
+// With stats, each workgroup writes the GroupNorm partial (count, mean, M2) of the samples it
+// stored for the group of its channel (G groups of Cout / G channels): at
+// stats[((b * G + g) * parts + j) * 3], parts = (Cout / G) * gridDim.x, j = (oc mod (Cout / G)) *
+// gridDim.x + blockIdx.x.
 __global__ __launch_bounds__(256) void convt_reduce_kernel(const float* __restrict__ ws, int ksplit,
                                                            int M, int64_t N, int stride, int pad,
                                                            const float* __restrict__ bias,
                                                            float* __restrict__ y, int64_t Lout,
-                                                           int Cout, float* __restrict__ stats) {
+                                                           int Cout, float* __restrict__ stats,
+                                                           int G) {
   __shared__ float red[3 * 4];
   const int oc = blockIdx.y, b = blockIdx.z;
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -243,7 +248,9 @@ __global__ __launch_bounds__(256) void convt_reduce_kernel(const float* __restri
     st.finish(sn, smean, sm2);
     block_welford(sn, smean, sm2, red);
     if (threadIdx.x == 0) {
-      float* o = stats + (((int64_t)b * Cout + oc) * gridDim.x + blockIdx.x) * 3;
+      const int cpg = Cout / G, gi = oc / cpg;
+      const int64_t parts = (int64_t)cpg * gridDim.x, j = (int64_t)(oc - gi * cpg) * gridDim.x + blockIdx.x;
+      float* o = stats + (((int64_t)b * G + gi) * parts + j) * 3;
       o[0] = sn;
       o[1] = smean;
       o[2] = sm2;
@@ -356,10 +363,15 @@ GemmArgs convt_gemm_args(const ConvTArgs& a, const float* wpack, const float* un
 }
 }  // namespace
 
-int convt_gemm_parts(const ConvTArgs& a) {
-  const int Cin = a.C1 + a.C2;
+int convt_stats_parts(const ConvTArgs& a) {
+  const int Cin = a.C1 + a.C2, G = std::max(a.stat_groups, 1);
+  if (a.Cout % G != 0 || convt_small_supported(Cin, a.Cout, a.K, a.stride, a.dil, a.groups) ||
+      !convt_gemm_supported(Cin, a.Cout, a.K, a.stride, a.dil, a.groups))
+    return 0;
+  const int64_t Lq = convt_rows(a.Lout, a.stride, a.pad);
   const int parts = convt_ksplit(a.B, Cin, a.Cout, a.K, a.stride, a.pad, a.Lout);
-  if (parts > 1) return a.Cout * (int)cdiv(convt_rows(a.Lout, a.stride, a.pad), 256);
+  if (parts > 1) return a.Cout / G * (int)cdiv(Lq, 256);
+  if (G > 1) return 0;
   return (int)gemm_nk_lds_tiles(convt_gemm_args(a, nullptr, nullptr, nullptr));
 }
 
@@ -396,7 +408,7 @@ void convt_gemm(const LaunchCtx& c, const ConvTArgs& a, const float* wpack, floa
     launch(c, "convt_reduce_f32", convt_reduce_kernel,
            dim3((unsigned)cdiv(p.Lq, 256), (unsigned)a.Cout, (unsigned)a.B), dim3(256), 0,
            (const float*)split_ws, parts, g.M, (int64_t)g.N, a.stride, a.pad, a.bias, a.y,
-           a.Lout, a.Cout, a.stats);
+           a.Lout, a.Cout, a.stats, std::max(a.stat_groups, 1));
 }
 
 void convt_pack_t1(const LaunchCtx& c, const ConvTPackArgs& p, int B) {

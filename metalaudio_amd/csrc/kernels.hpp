@@ -293,9 +293,11 @@ struct ConvTArgs {
   const float* w = nullptr;
   const float* bias = nullptr;
   float* y = nullptr;  // [B][Cout][Lout]
-  // GEMM form only: GroupNorm(1) statistics partials of y (count, mean, M2), convt_gemm_parts(a)
-  // per batch at stats[(b * parts + j) * 3] (gn_apply_parts' layout for one group)
+  // GroupNorm statistics partials of y (count, mean, M2) for stat_groups groups of output
+  // channels, convt_stats_parts(a) per (batch, group) at stats[((b * G + g) * parts + j) * 3]
+  // (gn_apply_parts' layout)
   float* stats = nullptr;
+  int stat_groups = 1;
 };
 struct ConvTPackArgs {
   const float* x1 = nullptr;
@@ -306,8 +308,11 @@ struct ConvTPackArgs {
 };
 // The matrix-core form: groups 1, dilation 1, K = T * stride with T in {1, 2, 4}.
 bool convt_gemm_supported(int Cin, int Cout, int K, int stride, int dil, int groups);
-// Statistics partials per batch that convt_gemm writes when a.stats is set.
-int convt_gemm_parts(const ConvTArgs& a);
+// Statistics partials per (batch, group) that convt_gemm writes when a.stats is set (a.stat_groups
+// groups): one per output tile for one group (the scatter epilogue), one per reduce workgroup
+// for any group count (the split-K reduce); 0 where it writes none (more than one group without a
+// K split, or the few-channel kernel, whose partials would be too many for the apply pass's merge).
+int convt_stats_parts(const ConvTArgs& a);
 int convt_padded_cin(int Cin);
 // Output rows q of the GEMM form: (Lout - 1 + pad) / stride + 1.
 int64_t convt_rows(int64_t Lout, int stride, int pad);

@@ -1191,17 +1191,19 @@ class ConvTranspose1DLayer : public Layer {
   }
   // GroupNorm(1) statistics partials per batch that run() writes into `stats` (count, mean, M2
   // each, gn_apply_parts' layout for one group); 0 when this layer's path does not produce them.
-  int stats_parts(int B, int64_t L) const {
-    if (small_ || !gemm_) return 0;
-    return k::convt_gemm_parts(args(d_.in_channels, 0, B, L));
+  int stats_parts(int B, int64_t L, int G) const {
+    if (!small_ && !gemm_) return 0;
+    k::ConvTArgs a = args(d_.in_channels, 0, B, L);
+    a.stat_groups = G;
+    return k::convt_stats_parts(a);
   }
   // y [B][out][out_len(L)] from the channel concat [x1 (C1 channels); x2 (C2)], C1 + C2 = in;
-  // with stats (stats_parts(B, L) > 0 only), the GroupNorm(1) partials of y as well.
+  // with stats (stats_parts(B, L, G) > 0 only), the GroupNorm partials of y for G groups as well.
   void run(const float* x1, int C1, const float* x2, int C2, int B, int64_t L, float* y,
-           Stream& s, float* stats = nullptr) {
+           Stream& s, float* stats = nullptr, int G = 1) {
     MNN_REQUIRE(C1 + C2 == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
                 "ConvTranspose1D: channel count mismatch");
-    MNN_REQUIRE(!stats || stats_parts(B, L) > 0, MNN_ERR_INVALID_ARGUMENT,
+    MNN_REQUIRE(!stats || stats_parts(B, L, G) > 0, MNN_ERR_INVALID_ARGUMENT,
                 "ConvTranspose1D: this configuration writes no statistics partials");
     k::ConvTArgs a = args(C1, C2, B, L);
     a.x1 = x1;
@@ -1210,6 +1212,7 @@ class ConvTranspose1DLayer : public Layer {
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
     a.stats = stats;
+    a.stat_groups = G;
     if (small_) {
       k::convt_small(ctx(s), a);
     } else if (gemm_) {
@@ -1331,12 +1334,12 @@ class DecoderBlockLayer : public Layer {
     const int64_t lo = os.back();
     y_.reserve(sizeof(float) * B * Cout * lo);
     const int G = norm_->groups();
-    if (const int np = G == 1 ? convt_->stats_parts((int)B, L) : 0) {
-      // GroupNorm(1) statistics from the transposed conv's epilogue (or its split-K reduce); the
-      // apply pass merges them (no statistics pass over y)
-      partials_.reserve(sizeof(float) * 3 * B * np);
+    if (const int np = convt_->stats_parts((int)B, L, G)) {
+      // GroupNorm statistics from the transposed conv itself (GEMM epilogue, split-K reduce or
+      // the few-channel kernel); the apply pass merges them (no statistics pass over y)
+      partials_.reserve(sizeof(float) * 3 * B * G * np);
       convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, L, y_.f32(), s,
-                  partials_.f32());
+                  partials_.f32(), G);
       norm_->apply_parts(s, y_.f32(), out->f32(), (int)B, lo, partials_.f32(), np,
                          MNN_ACT_GELU);
       return;
