@@ -32,9 +32,41 @@ __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
 }
 
 // In-place radix-2 DIT FFT of z[0..M) (bit-reversed input order) in LDS; inverse uses conjugate
-// twiddles (no scaling). tw[k] = e^{-2 pi i k / N}, N = 2M.
+// twiddles (no scaling). tw[k] = e^{-2 pi i k / N}, N = 2M. Two consecutive stages h and 2h run
+// per barrier: a thread takes the group i0 + {0, h, 2h, 3h} (i0 = 4h q + p, p < h) through stage
+// h (pairs (i0, i0+h), (i0+2h, i0+3h), twiddle W_2h^p) and stage 2h (pairs (i0, i0+2h) with
+// W_4h^p, (i0+h, i0+3h) with W_4h^(p+h)), the same operations in the same order as two radix-2
+// passes; an odd stage count ends with one radix-2 pass.
 __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse) {
-  for (int h = 1; h < M; h <<= 1) {
+  int h = 1;
+  for (; 2 * h < M; h <<= 2) {
+    const int s1 = M / h, s2 = M / (2 * h);  // W_2h^p = tw[p * s1], W_4h^p = tw[p * s2]
+    for (int t = threadIdx.x; t < M / 4; t += kThreads) {
+      const int p = t & (h - 1);
+      const int i0 = ((t - p) << 2) + p;
+      float2 w1 = tw[p * s1], w2 = tw[p * s2], w3 = tw[p * s2 + M / 2];
+      if (inverse) {
+        w1.y = -w1.y;
+        w2.y = -w2.y;
+        w3.y = -w3.y;
+      }
+      float2 a0 = z[i0], a1 = z[i0 + h], a2 = z[i0 + 2 * h], a3 = z[i0 + 3 * h];
+      float2 bb = cmul(a1, w1);
+      a1 = make_float2(a0.x - bb.x, a0.y - bb.y);
+      a0 = make_float2(a0.x + bb.x, a0.y + bb.y);
+      bb = cmul(a3, w1);
+      a3 = make_float2(a2.x - bb.x, a2.y - bb.y);
+      a2 = make_float2(a2.x + bb.x, a2.y + bb.y);
+      bb = cmul(a2, w2);
+      z[i0 + 2 * h] = make_float2(a0.x - bb.x, a0.y - bb.y);
+      z[i0] = make_float2(a0.x + bb.x, a0.y + bb.y);
+      bb = cmul(a3, w3);
+      z[i0 + 3 * h] = make_float2(a1.x - bb.x, a1.y - bb.y);
+      z[i0 + h] = make_float2(a1.x + bb.x, a1.y + bb.y);
+    }
+    __syncthreads();
+  }
+  if (h < M) {
     const int stride = M / h;  // W_{2h}^p = tw[p * M / h]
     for (int t = threadIdx.x; t < M / 2; t += kThreads) {
       const int p = t & (h - 1);
@@ -73,10 +105,27 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   const int M = a.N / 2;
   float2* tws = z + M;
   const float* xs = a.x + (int64_t)b * a.n + (int64_t)f * a.hop;
-  for (int m = threadIdx.x; m < M; m += kThreads) {
-    const float e = xs[2 * m] * a.win[2 * m], o = xs[2 * m + 1] * a.win[2 * m + 1];
-    z[bitrev(m, a.logM)] = make_float2(e, o);
-    if (LDS_TW) tws[m] = a.tw[m];
+  // every load of a batch of 8 samples pairs per thread (clamped indices) before any LDS store
+  for (int m0 = threadIdx.x; m0 < M; m0 += 8 * kThreads) {
+    float xe[8], xo[8], we[8], wo[8];
+    float2 tv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int m = min(m0 + u * kThreads, M - 1);
+      xe[u] = xs[2 * m];
+      xo[u] = xs[2 * m + 1];
+      we[u] = a.win[2 * m];
+      wo[u] = a.win[2 * m + 1];
+      if (LDS_TW) tv[u] = a.tw[m];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int m = m0 + u * kThreads;
+      if (m < M) {
+        z[bitrev(m, a.logM)] = make_float2(xe[u] * we[u], xo[u] * wo[u]);
+        if (LDS_TW) tws[m] = tv[u];
+      }
+    }
   }
   __syncthreads();
   fft_lds(z, M, LDS_TW ? tws : a.tw, false);
@@ -117,26 +166,43 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
                                     : base + (int64_t)kk * a.frames + f;
     return make_float2(a.cre[o], a.cim[o]);
   };
-  // Hermitian part H[k] of the input spectrum, k in [0, M]: the real part of the inverse DFT
-  // depends on nothing else.
-  auto herm = [&](int kk) {
-    float2 h = get(kk);
-    if (!a.onesided && kk > 0 && kk < M) {
-      const float2 c = get(a.N - kk);
-      h = make_float2(0.5f * (h.x + c.x), 0.5f * (h.y - c.y));
-    }
+  // Hermitian part H[k] of the input spectrum, k in [0, M], from X[k] (g) and X[N-k] (c, full
+  // spectra only): the real part of the inverse DFT depends on nothing else.
+  auto herm = [&](int kk, float2 g, float2 c) {
+    float2 h = g;
+    if (!a.onesided && kk > 0 && kk < M) h = make_float2(0.5f * (g.x + c.x), 0.5f * (g.y - c.y));
     if (kk == 0 || kk == M) h.y = 0.f;
     return h;
   };
-  for (int k = threadIdx.x; k < M; k += kThreads) {
-    const float2 hk = herm(k), hc = herm(M - k);
-    const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
-    const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
-    const float2 t = a.tw[k];
-    if (LDS_TW) tws[k] = t;
-    const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
-    const float2 fo = cmul(d, w);
-    z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+  // every load of a batch of 4 bins per thread (clamped indices) before any LDS store
+  for (int k0 = threadIdx.x; k0 < M; k0 += 4 * kThreads) {
+    float2 gk[4], gc[4], ck[4], cc[4], tv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = min(k0 + u * kThreads, M - 1), kc = M - k;
+      gk[u] = get(k);
+      gc[u] = get(kc);
+      if (!a.onesided) {
+        ck[u] = get(k > 0 ? a.N - k : k);
+        cc[u] = get(kc < M ? a.N - kc : kc);
+      } else {
+        ck[u] = cc[u] = make_float2(0.f, 0.f);  // not read for one-sided spectra
+      }
+      tv[u] = a.tw[k];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = k0 + u * kThreads;
+      if (k >= M) continue;
+      const float2 hk = herm(k, gk[u], ck[u]), hc = herm(M - k, gc[u], cc[u]);
+      const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
+      const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
+      const float2 t = tv[u];
+      if (LDS_TW) tws[k] = t;
+      const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
+      const float2 fo = cmul(d, w);
+      z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+    }
   }
   __syncthreads();
   fft_lds(z, M, LDS_TW ? tws : a.tw, true);
