@@ -125,11 +125,17 @@ def transformer_work(batch):
                 gemm_f += 2.0 * batch * own * E * 3 * E
             gemm_f += 2.0 * batch * own * (E * E + 2 * E * Hd)
             gemm_b += 4.0 * batch * own * (E + 3 * E + E + E + E + Hd + Hd + E)
-            # self layer: two LayerNorms (read + write each); cross layer: the two normalisations
-            # of this state in one pass (one read, two writes), then the feed-forward norm
+            # LayerNorms folded into the GEMMs (fp32, E % 64 == 0): the residual GEMMs write
+            # (mean, M2) per 64 columns of each row, the consumer GEMMs read them
+            gemm_b += 8.0 * batch * (E // 64) * (own * 2 + (own + other if cross else own) + own)
+            # standalone LayerNorms (the unfolded form): self layer two (read + write each);
+            # cross layer the two normalisations of this state in one pass (one read, two
+            # writes), then the feed-forward norm
             ln_b += 4.0 * batch * own * E * (5 if cross else 4)
+    # the inputs' row statistics, with the copy of each input to its output
+    parts_b = sum(batch * s * (8.0 * E + 8.0 * (E // 64)) for s in (St, Sf))
     return {"attn_fwd_f32": [attn_f, attn_b], "gemm_f32_mfma_nk": [gemm_f, gemm_b],
-            "layernorm": [0.0, ln_b]}
+            "layernorm": [0.0, ln_b], "ln_row_parts_f32": [0.0, parts_b]}
 
 
 # ------------------------------------------------------------------ model setup
@@ -636,8 +642,8 @@ def main():
     markers.pop()
     dev.set_kernel_timing(False)
     fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
-            "gemm_f32_simple", "conv1d_direct", "layernorm", "gn_stats", "gn_finalize",
-            "gn_apply", "copy_bytes", "glu_f32", "gelu_f32"]
+            "gemm_f32_simple", "conv1d_direct", "layernorm", "ln_row_parts_f32", "ln_fold_f32",
+            "gn_stats", "gn_finalize", "gn_apply", "copy_bytes", "glu_f32", "gelu_f32"]
     enc_kernels = list(encoder_work())  # per level, e.g. enc_conv_f32[c96]
     ktime = {}
     for f in fams + enc_kernels:

@@ -755,6 +755,8 @@ void gemm(const LaunchCtx& c, const GemmArgs& a) {
   if (a.M <= 0 || a.N <= 0 || a.batch <= 0) return;
   MNN_REQUIRE(a.K > 0, MNN_ERR_INVALID_ARGUMENT, "gemm: K must be positive");
   if (gemm_nk_lds_supported(a)) return gemm_nk_lds(c, a);
+  MNN_REQUIRE(!a.ln_parts && !a.row_parts, MNN_ERR_INVALID_CONFIGURATION,
+              "gemm: folded LayerNorm / row statistics need the LDS-DMA path's operand contract");
   const Tile t = choose_tiles(a);
   MNN_REQUIRE(!(a.glu && t.id < 0), MNN_ERR_INVALID_CONFIGURATION,
               "gemm: GLU epilogue needs M % 32 == 0 and 16-byte aligned operands");

@@ -135,6 +135,29 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
   }
 }
 
+// Folded LayerNorm of A's row m: (rstd, -rstd * mean) merged from the row's K / 64 partials
+// (mean, M2) of 64 features each (Chan's formula for equal counts, a fixed order; K <= 64 *
+// kLnMaxParts). Every partial is loaded before the first is used.
+constexpr int kLnMaxParts = 8;
+__device__ __forceinline__ float2 ln_row_coef(const GemmArgs& a, int m) {
+  const int P = a.K / 64;
+  const float2* pp = reinterpret_cast<const float2*>(a.ln_parts) + (int64_t)min(m, a.M - 1) * P;
+  float2 q[kLnMaxParts];
+#pragma unroll
+  for (int p = 0; p < kLnMaxParts; ++p) q[p] = pp[min(p, P - 1)];
+  float mean = q[0].x, m2 = q[0].y;
+#pragma unroll
+  for (int p = 1; p < kLnMaxParts; ++p) {
+    if (p < P) {
+      const float d = q[p].x - mean;
+      mean += d * (1.f / (float)(p + 1));
+      m2 += q[p].y + d * d * (64.f * (float)p / (float)(p + 1));
+    }
+  }
+  const float rstd = 1.f / sqrtf(m2 / (float)a.K + a.ln_eps);
+  return make_float2(rstd, -rstd * mean);
+}
+
 // The same epilogue with the tile transposed through LDS into row order, for outputs whose rows
 // are 16-byte aligned (N % 4 == 0, ldc % 4 == 0; residual likewise): the accumulators are written
 // to LDS ([rows][BN + 8 floats]: rows four apart, which the two lane groups write together, sit 32
@@ -169,6 +192,19 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16
   float4 bn = make_float4(0.f, 0.f, 0.f, 0.f), rs = make_float4(1.f, 1.f, 1.f, 1.f);
   if (col_ok && a.bias_mode == BIAS_N) bn = *reinterpret_cast<const float4*>(a.bias + gn);
   if (RES && Rp && a.rscale && col_ok) rs = *reinterpret_cast<const float4*>(a.rscale + gn);
+  // Folded LayerNorm: thread r < BM merges row m0 + r's partials into (rstd, -rstd * mean), kept
+  // at the end of the LDS ring past the rows the passes below write; the first pass's barrier
+  // makes them visible.
+  static_assert(PROWS * PITCH + 2 * BM <= LDS_FLOATS, "epilogue tile and row coefficients");
+  static_assert(BM <= NT, "one row coefficient per thread");
+  float2* lnrow = reinterpret_cast<float2*>(smem + LDS_FLOATS - 2 * BM);
+  const bool ln = a.ln_parts != nullptr;
+  float4 lc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (ln) {
+    if (col_ok) lc = *reinterpret_cast<const float4*>(a.ln_c + gn);
+    if (tid < BM) lnrow[tid] = ln_row_coef(a, m0 + tid);
+  }
+  const bool rstats = a.row_parts != nullptr;
 #pragma unroll
   for (int pass = 0; pass < WMW / PASS_WM; ++pass) {
     if (pass > 0) __syncthreads();  // the previous pass's reads are done
@@ -203,6 +239,13 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16
       const int r = rr0 + it * RPI;
       const int gm = prow0 + r;
       float4 v = *reinterpret_cast<const float4*>(smem + r * PITCH + 4 * c4);
+      if (ln) {
+        const float2 rc = lnrow[pass * PROWS + r];
+        v.x = rc.x * v.x + rc.y * lc.x;
+        v.y = rc.x * v.y + rc.y * lc.y;
+        v.z = rc.x * v.z + rc.y * lc.z;
+        v.w = rc.x * v.w + rc.y * lc.w;
+      }
       v.x += bn.x;
       v.y += bn.y;
       v.z += bn.z;
@@ -225,6 +268,17 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16
           v.z = rv[it].z + rs.z * v.z;
           v.w = rv[it].w + rs.w * v.w;
         }
+      }
+      if (rstats) {
+        // (mean, M2) of the row's 64 columns held by this lane's 16-lane group (N % 64 == 0, so
+        // col_ok is uniform over the group)
+        const bool ok = col_ok && gm < a.M;
+        const float mean = row16_sum(ok ? (v.x + v.y) + (v.z + v.w) : 0.f) * (1.f / 64.f);
+        const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+        const float m2 = row16_sum(ok ? (dx * dx + dy * dy) + (dz * dz + dw * dw) : 0.f);
+        if (ok && (c4 & 15) == 0)
+          *reinterpret_cast<float2*>(a.row_parts + ((int64_t)gm * (a.N / 64) + gn / 64) * 2) =
+              make_float2(mean, m2);
       }
       if (col_ok && gm < a.M) *reinterpret_cast<float4*>(Cp + (int64_t)gm * a.ldc + gn) = v;
     }
@@ -656,6 +710,24 @@ void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
 
 }  // namespace
 
+namespace {
+// The folded-LayerNorm and row-statistics epilogue forms exist in the row-ordered store only:
+// the conditions under which the kernel takes it (fp32, plain epilogue, 16-byte aligned rows),
+// batch 1, and whole 64-column groups.
+bool ln_fold_epilogue_ok(const GemmArgs& a) {
+  const bool res = a.R != nullptr;
+  const bool rows16 = a.N % 4 == 0 && a.ldc % 4 == 0 && aligned16(a.C) &&
+                      (!res || (a.ldr % 4 == 0 && aligned16(a.R))) &&
+                      (a.bias_mode != BIAS_N || aligned16(a.bias)) &&
+                      (!a.rscale || aligned16(a.rscale));
+  return rows16 && a.batch == 1 && !a.ab_bf16 && !a.glu && a.ct_stride == 0 && a.ksplit == 1 &&
+         a.stats == nullptr && a.bias_mode != BIAS_M &&
+         (!a.ln_parts || (a.K % 64 == 0 && a.K <= 64 * kLnMaxParts && a.ln_c &&
+                          aligned16(a.ln_c) && aligned16(a.ln_parts))) &&
+         (!a.row_parts || (a.N % 64 == 0 && (reinterpret_cast<uintptr_t>(a.row_parts) & 7) == 0));
+}
+}  // namespace
+
 bool gemm_nk_lds_supported(const GemmArgs& a) {
   if (a.ab_bf16) {
     // bf16 operands: 64 k per stage, rows 16-byte aligned (8 elements), plain epilogue
@@ -677,7 +749,8 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
          (a.ct_stride == 0 || (!a.glu && a.R == nullptr && a.act == 0 && a.bias_mode != BIAS_N)) &&
          a.ksplit >= 1 && (a.K / BK) % a.ksplit == 0 &&
          (a.ksplit == 1 || (a.ws != nullptr && !a.glu)) &&
-         (a.stats == nullptr || (a.ct_stride > 0 && a.ksplit == 1));
+         (a.stats == nullptr || (a.ct_stride > 0 && a.ksplit == 1)) &&
+         ((!a.ln_parts && !a.row_parts) || ln_fold_epilogue_ok(a));
 }
 
 int64_t gemm_nk_lds_tiles(const GemmArgs& a) {

@@ -426,9 +426,73 @@ __global__ __launch_bounds__(kThreads) void layernorm_generic_kernel(
   for (int i = lane; i < F; i += 64) yr[i] = gamma[i] * ((xr[i] - mean) * rstd) + beta[i];
 }
 
+// (mean, M2) of each 64 consecutive features of every row (F % 64 == 0): a 16-lane group per
+// 64 features, one float4 per lane, DPP reductions within the group. Optionally copies x to y on
+// the way (the same float4s).
+__global__ __launch_bounds__(kThreads) void ln_row_parts_kernel(const float* __restrict__ x,
+                                                                float* __restrict__ y,
+                                                                float* __restrict__ parts,
+                                                                int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const bool live = i < n4;
+  const float4 v = reinterpret_cast<const float4*>(x)[live ? i : n4 - 1];
+  if (y && live) reinterpret_cast<float4*>(y)[i] = v;
+  const float mean = row16_sum((v.x + v.y) + (v.z + v.w)) * (1.f / 64.f);
+  const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+  const float m2 = row16_sum((dx * dx + dy * dy) + (dz * dz + dw * dw));
+  if (live && (i & 15) == 0) reinterpret_cast<float2*>(parts)[i >> 4] = make_float2(mean, m2);
+}
+
+// LayerNorm folded into the following linear map y = LN(x) W^T + b: Wf[n][k] = W[n][k] * gamma[k],
+// c[n] = sum_k Wf[n][k], bf[n] = b[n] + sum_k W[n][k] * beta[k] (sums in fp64). One wave per n.
+__global__ __launch_bounds__(kThreads) void ln_fold_kernel(const float* __restrict__ W,
+                                                           const float* __restrict__ b,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, int N,
+                                                           int K, float* __restrict__ Wf,
+                                                           float* __restrict__ c,
+                                                           float* __restrict__ bf) {
+  const int n = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;  // whole wave
+  double cs = 0.0, bs = 0.0;
+  for (int k = lane; k < K; k += 64) {
+    const float w = W[(int64_t)n * K + k];
+    const float wf = w * gamma[k];
+    Wf[(int64_t)n * K + k] = wf;
+    cs += (double)wf;
+    bs += (double)w * (double)beta[k];
+  }
+  cs = wave_sum_dpp_d(cs);
+  bs = wave_sum_dpp_d(bs);
+  if (lane == 0) {
+    c[n] = (float)cs;
+    bf[n] = (float)((b ? (double)b[n] : 0.0) + bs);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
+
+void ln_row_parts(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F,
+                  float* parts) {
+  MNN_REQUIRE(F % 64 == 0 && aligned16(x) && (!y || aligned16(y)) &&
+                  (reinterpret_cast<uintptr_t>(parts) & 7) == 0,
+              MNN_ERR_INVALID_ARGUMENT,
+              "ln_row_parts: F % 64 == 0 and 16-byte aligned rows required");
+  if (rows <= 0) return;
+  const int64_t n4 = rows * F / 4;
+  launch(c, "ln_row_parts_f32", ln_row_parts_kernel, dim3((unsigned)cdiv(n4, kThreads)),
+         dim3(kThreads), 0, x, y, parts, n4);
+}
+
+void ln_fold(const LaunchCtx& c, const float* W, const float* b, const float* gamma,
+             const float* beta, int N, int K, float* Wf, float* cvec, float* bf) {
+  if (N <= 0) return;
+  launch(c, "ln_fold_f32", ln_fold_kernel, dim3((unsigned)cdiv(N, kThreads / 64)), dim3(kThreads),
+         0, W, b, gamma, beta, N, K, Wf, cvec, bf);
+}
 
 // Statistics partials of the allocation-free GroupNorm entry point. One copy per GPU, held until
 // the process ends; every allocation-free call on a GPU uses that GPU's copy.

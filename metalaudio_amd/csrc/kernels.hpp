@@ -56,6 +56,15 @@ void layernorm2(const LaunchCtx& c, const float* x, int64_t rows, int F, float* 
                 const float* gamma, const float* beta, float eps, float* y2,
                 const float* gamma2, const float* beta2, float eps2);
 
+// (mean, M2) of each 64 consecutive features of every row, parts[rows][F / 64][2] (F % 64 == 0,
+// 16-byte aligned rows); with y, x is copied to y in the same pass. The statistics a GEMM with a
+// folded LayerNorm (GemmArgs::ln_parts) reads.
+void ln_row_parts(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F, float* parts);
+// LayerNorm(gamma, beta) folded into the linear map that follows it: Wf = W * diag(gamma) ([N][K]),
+// cvec[n] = sum_k Wf[n][k], bf[n] = b[n] + sum_k W[n][k] * beta[k] (b may be null).
+void ln_fold(const LaunchCtx& c, const float* W, const float* b, const float* gamma,
+             const float* beta, int N, int K, float* Wf, float* cvec, float* bf);
+
 // ------------------------------------------------------------------ conv (k_conv.hip)
 struct ConvParams {
   int B, Cin, Cout, Lin, Lout, K, stride, pad, dilation, groups;
@@ -154,6 +163,17 @@ struct GemmArgs {
   // n = q; C[oc * ldc + s*q + r - ct_pad] = acc + bias[oc] where that position is in [0, ct_len).
   int ct_stride = 0, ct_pad = 0;
   int64_t ct_len = 0;
+  // LayerNorm of A's rows folded into the GEMM (LDS path, fp32, row-ordered epilogue, batch 1):
+  // B holds W * diag(gamma), bias holds b + W * beta and ln_c[n] = sum_k B[n][k]; the epilogue
+  // forms rstd_m * acc - rstd_m * mean_m * ln_c[n] + bias[n] (then activation / residual), with
+  // mean_m and rstd_m = 1 / sqrt(var_m + ln_eps) merged from ln_parts: (mean, M2) of each 64
+  // consecutive features of row m, [M][K / 64][2].
+  const float* ln_parts = nullptr;
+  const float* ln_c = nullptr;
+  float ln_eps = 1e-5f;
+  // Row statistics of the output for a following folded LayerNorm (same path): (mean, M2) of each
+  // 64 consecutive columns of the final row m of C, [M][N / 64][2].
+  float* row_parts = nullptr;
   // K split (LDS path only): ksplit > 1 writes the raw partial products of each K part to
   // ws[((b * ksplit + p) * M + m) * N + n] and applies no epilogue (the caller reduces the parts).
   int ksplit = 1;

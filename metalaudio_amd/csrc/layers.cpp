@@ -78,6 +78,7 @@ void Layer::load(const std::string& name, const float* data, size_t n) {
   dev_->make_current();
   HIP_CHECK(hipMemcpy(p->buf.ptr, data, sizeof(float) * n, hipMemcpyHostToDevice));
   p->loaded = true;
+  ++p->version;
   on_loaded(p->name, data, n);
 }
 
@@ -396,6 +397,10 @@ class LayerNormLayer : public Layer {
     k::layernorm2(ctx(s), x, rows, F_, y, gamma_->ptr(), beta_->ptr(), eps_, y2,
                   other.gamma_->ptr(), other.beta_->ptr(), other.eps_);
   }
+  int features() const { return F_; }
+  float eps() const { return eps_; }
+  const Param& gamma() const { return *gamma_; }
+  const Param& beta() const { return *beta_; }
 
  private:
   int F_;
@@ -576,6 +581,47 @@ class LinearLayer : public Layer {
   Param* b_ = nullptr;
 };
 
+// ------------------------------------------------------------------ folded LayerNorm
+// A LayerNorm whose output only feeds a linear map y = LN(x) W^T + b runs inside that map's GEMM:
+// the GEMM reads the raw rows x against W * diag(gamma), and its epilogue forms
+// rstd * acc - rstd * mean * c + b' (c[n] = sum_k W[n][k] gamma[k], b' = b + W beta), the rows'
+// mean and rstd merged from (mean, M2) partials over 64-feature groups that the producer of x
+// wrote (a residual GEMM's epilogue, or ln_row_parts). No normalised copy of x is written or read.
+struct LnFold {
+  const float* w = nullptr;      // W * diag(gamma), [N][K]
+  const float* c = nullptr;      // [N]
+  const float* b = nullptr;      // [N]
+  const float* parts = nullptr;  // row partials of x, [rows][K / 64][2]
+  float eps = 1e-5f;
+};
+
+// Folded weights of one (LayerNorm, linear map) pair: derived data, rebuilt on the stream of the
+// call when a load has changed W, b, gamma or beta since they were built.
+class LnFoldCache {
+ public:
+  // rows [row0, row0 + N) of W (row length K) and the same entries of b (b may be null)
+  LnFold get(const LaunchCtx& c, const Param& w, int64_t row0, int N, int K, const Param* b,
+             const LayerNormLayer& ln, const float* parts) {
+    const uint64_t key[4] = {w.version, b ? b->version : 0, ln.gamma().version,
+                             ln.beta().version};
+    if (!valid_ || !std::equal(key, key + 4, key_)) {
+      wf_.reserve(sizeof(float) * N * K);
+      c_.reserve(sizeof(float) * N);
+      b_.reserve(sizeof(float) * N);
+      k::ln_fold(c, w.ptr() + row0 * K, b ? b->ptr() + row0 : nullptr, ln.gamma().ptr(),
+                 ln.beta().ptr(), N, K, wf_.f32(), c_.f32(), b_.f32());
+      std::copy(key, key + 4, key_);
+      valid_ = true;
+    }
+    return LnFold{wf_.f32(), c_.f32(), b_.f32(), parts, ln.eps()};
+  }
+
+ private:
+  DevBuf wf_, c_, b_;
+  uint64_t key_[4] = {};
+  bool valid_ = false;
+};
+
 // ------------------------------------------------------------------ MultiHeadAttention
 // MultiHeadAttention / CrossAttention (Attention.swift:15-1063). Q, K, V come from one packed
 // projection GEMM (self) or a Q GEMM plus a KV GEMM over rows E..3E of in_proj (cross); the
@@ -635,6 +681,32 @@ class MHALayer : public Layer {
   // xkv == nullptr: self-attention. out = R + rscale * MHA(...) when R is given.
   void run(const float* xq, int Sq, const float* xkv, int Sk, int B, float* out, const float* R,
            const float* rscale, Stream& s) {
+    project(xq, Sq, xkv, Sk, B, nullptr, nullptr, s);
+    finish(Sq, xkv ? Sk : Sq, xkv != nullptr, B, out, R, rscale, nullptr, s);
+  }
+  // The Q / K / V projections (packed, or Q and KV for cross-attention). fq / fkv: LayerNorms
+  // folded into them (xq / xkv are then the raw rows whose statistics the folds carry).
+  void project(const float* xq, int Sq, const float* xkv, int Sk, int B, const LnFold* fq,
+               const LnFold* fkv, Stream& s) {
+    const int E = E_;
+    const int64_t rq = (int64_t)B * Sq;
+    if (!xkv) {
+      qkv_.reserve(sizeof(float) * rq * 3 * E);
+      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, 3 * E, qkv_.f32(), fq, s);
+    } else {
+      const int64_t rk = (int64_t)B * Sk;
+      qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
+      float* qb = qkv_.f32();
+      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, E, qb, fq, s);
+      proj(xkv, rk, win_->ptr() + (int64_t)E * E, bin_ ? bin_->ptr() + E : nullptr, 2 * E,
+           qb + rq * E, fkv, s);
+    }
+  }
+  // Attention over the projections of the last project() call with the same shapes, then the
+  // output projection (+ residual / LayerScale); row_parts receives the output rows' statistics
+  // for a LayerNorm folded into the next GEMM.
+  void finish(int Sq, int Sk, bool cross, int B, float* out, const float* R, const float* rscale,
+              float* row_parts, Stream& s) {
     const int E = E_;
     const int64_t rq = (int64_t)B * Sq;
     k::AttnArgs at;
@@ -643,10 +715,8 @@ class MHALayer : public Layer {
     at.Sq = Sq;
     at.hd = hd_;
     at.scale = 1.f / std::sqrt((float)hd_);
-    if (!xkv) {
-      qkv_.reserve(sizeof(float) * rq * 3 * E);
-      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, 3 * E, qkv_.f32(), s);
-      at.Sk = Sq;
+    at.Sk = Sk;
+    if (!cross) {
       at.q = qkv_.f32();
       at.q_rs = 3 * E;
       at.q_bs = (int64_t)Sq * 3 * E;
@@ -655,13 +725,8 @@ class MHALayer : public Layer {
       at.kv_rs = 3 * E;
       at.kv_bs = (int64_t)Sq * 3 * E;
     } else {
-      const int64_t rk = (int64_t)B * Sk;
-      qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
       float* qb = qkv_.f32();
       float* kvb = qb + rq * E;
-      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, E, qb, s);
-      proj(xkv, rk, win_->ptr() + (int64_t)E * E, bin_ ? bin_->ptr() + E : nullptr, 2 * E, kvb, s);
-      at.Sk = Sk;
       at.q = qb;
       at.q_rs = E;
       at.q_bs = (int64_t)Sq * E;
@@ -692,26 +757,35 @@ class MHALayer : public Layer {
     g.R = R;
     g.ldr = E;
     g.rscale = rscale;
+    g.row_parts = row_parts;
     g.precision = prec_;
     k::gemm(ctx(s), g);
   }
+  mnn_precision precision() const { return prec_; }
+  const Param& in_w() const { return *win_; }
+  const Param* in_b() const { return bin_; }
 
  private:
   void proj(const float* x, int64_t rows, const float* w, const float* b, int nout, float* y,
-            Stream& s) {
+            const LnFold* f, Stream& s) {
     k::GemmArgs g;
     g.M = (int)rows;
     g.N = nout;
     g.K = E_;
     g.A = x;
     g.lda = E_;
-    g.B = w;
+    g.B = f ? f->w : w;
     g.ldb = E_;
     g.blayout = k::B_NK;
     g.C = y;
     g.ldc = nout;
-    g.bias = b;
-    g.bias_mode = b ? k::BIAS_N : k::BIAS_NONE;
+    g.bias = f ? f->b : b;
+    g.bias_mode = (f || b) ? k::BIAS_N : k::BIAS_NONE;
+    if (f) {
+      g.ln_parts = f->parts;
+      g.ln_c = f->c;
+      g.ln_eps = f->eps;
+    }
     g.precision = prec_;
     k::gemm(ctx(s), g);
   }
@@ -750,8 +824,10 @@ class FeedForwardLayer : public Layer {
     check_out(out, infer_output(in.shape));
     run(in.f32(), in.count() / E_, out.f32(), nullptr, nullptr, s);
   }
+  // f1: a LayerNorm folded into the first linear map (x are then the raw rows); row_parts: the
+  // output rows' statistics for a LayerNorm folded into the next GEMM.
   void run(const float* x, int64_t rows, float* y, const float* R, const float* rscale,
-           Stream& s) {
+           Stream& s, const LnFold* f1 = nullptr, float* row_parts = nullptr) {
     hidden_.reserve(sizeof(float) * rows * Hd_);
     k::GemmArgs g;
     g.M = (int)rows;
@@ -759,13 +835,18 @@ class FeedForwardLayer : public Layer {
     g.K = E_;
     g.A = x;
     g.lda = E_;
-    g.B = w1_->ptr();
+    g.B = f1 ? f1->w : w1_->ptr();
     g.ldb = E_;
     g.blayout = k::B_NK;
     g.C = hidden_.f32();
     g.ldc = Hd_;
-    g.bias = b1_->ptr();
+    g.bias = f1 ? f1->b : b1_->ptr();
     g.bias_mode = k::BIAS_N;
+    if (f1) {
+      g.ln_parts = f1->parts;
+      g.ln_c = f1->c;
+      g.ln_eps = f1->eps;
+    }
     g.act = MNN_ACT_GELU;
     g.precision = prec_;
     k::gemm(ctx(s), g);
@@ -785,9 +866,14 @@ class FeedForwardLayer : public Layer {
     g2.R = R;
     g2.ldr = E_;
     g2.rscale = rscale;
+    g2.row_parts = row_parts;
     g2.precision = prec_;
     k::gemm(ctx(s), g2);
   }
+  mnn_precision precision() const { return prec_; }
+  int hidden() const { return Hd_; }
+  const Param& w1() const { return *w1_; }
+  const Param& b1() const { return *b1_; }
 
  private:
   int E_, Hd_;
@@ -1800,6 +1886,9 @@ struct Branch {
   bool use_ls = false;
   DevBuf g1, g2;
   int E = 0;
+  // folded weights: attention input projection (packed QKV, or Q for cross layers), the cross
+  // layer's KV projection, the FFN's first linear map
+  LnFoldCache fold_in, fold_kv, fold_ffn;
 
   Branch(Device* d, int embed, int heads, int ffn_dim, bool is_cross, float ls,
          mnn_precision prec)
@@ -1819,6 +1908,10 @@ struct Branch {
     }
   }
   LayerNormLayer* ffn_norm() { return cross ? norm3.get() : norm2.get(); }
+  bool foldable() const {
+    return attn->precision() == MNN_PRECISION_F32 && ffn->precision() == MNN_PRECISION_F32 &&
+           E % 64 == 0 && ffn->hidden() % 32 == 0;
+  }
   // returns true if the name was consumed
   bool load(const std::string& name, const float* data, size_t n) {
     auto starts = [&](const char* p) { return name.rfind(p, 0) == 0; };
@@ -1933,8 +2026,9 @@ class CrossTransformerImpl : public Layer {
   // streams: freq on the caller's stream, time on a side stream forked from it, joined back at the
   // end. Kernels of one branch then fill the CUs the other branch's grid leaves idle. A cross layer
   // starts with a two-way sync (the exchange buffers of the previous cross layer are free again),
-  // and each attention waits for the other branch's normalised state. With kernel timing on,
-  // everything runs on the caller's stream so launch durations are not stretched by overlap.
+  // and each attention waits for the other branch's normalised state (with the LayerNorms folded
+  // into the GEMMs: for the other branch's projections of this branch's state). With kernel timing
+  // on, everything runs on the caller's stream so launch durations are not stretched by overlap.
   void forward_cross(const Tensor* t, const Tensor* f, Tensor* to, Tensor* fo,
                      Stream& s) override {
     MNN_REQUIRE(t && f && to && fo, MNN_ERR_INVALID_ARGUMENT,
@@ -1946,8 +2040,6 @@ class CrossTransformerImpl : public Layer {
     split_bse(f->shape, Bf, Sf, Ef);
     MNN_REQUIRE(B == Bf, MNN_ERR_SHAPE_MISMATCH, "time and freq batch sizes differ");
     const int64_t rt = B * St, rf = B * Sf;
-    ht_.reserve(sizeof(float) * rt * E * 2);
-    hf_.reserve(sizeof(float) * rf * E * 2);
     const bool two = !dev_->timing;
     next_event_ = 0;
     Stream side{s.dev, s.s, false};
@@ -1957,6 +2049,13 @@ class CrossTransformerImpl : public Layer {
     }
     Stream& ts = side;  // time branch
     Stream& fs = s;     // freq branch
+    if (fold_ok(rt, rf, t->data, f->data, to->data, fo->data)) {
+      run_folded(t, f, to, fo, B, St, Sf, ts, fs, two);
+      if (two) link(ts, s);
+      return;
+    }
+    ht_.reserve(sizeof(float) * rt * E * 2);
+    hf_.reserve(sizeof(float) * rf * E * 2);
     if (to->data != t->data) k::copy_bytes(ctx(ts), t->data, to->data, rt * E * 4);
     if (fo->data != f->data) k::copy_bytes(ctx(fs), f->data, fo->data, rf * E * 4);
     float* T = to->f32();
@@ -2007,6 +2106,97 @@ class CrossTransformerImpl : public Layer {
   }
 
  private:
+  static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+  // Every LayerNorm folded into the GEMM after it: fp32 branches, 64-feature groups, rows the
+  // LDS-DMA GEMM addresses with 32-bit offsets, 16-byte aligned states.
+  bool fold_ok(int64_t rt, int64_t rf, const void* t, const void* f, const void* to,
+               const void* fo) const {
+    if (E_ % 64 != 0 || !aligned16(t) || !aligned16(f) || !aligned16(to) || !aligned16(fo))
+      return false;
+    int64_t widest = 3LL * E_;
+    for (const auto* v : {&time_, &freq_})
+      for (const auto& b : *v) {
+        if (!b->foldable()) return false;
+        widest = std::max<int64_t>(widest, b->ffn->hidden());
+      }
+    return std::max(rt, rf) * widest * 4 < ((int64_t)1 << 32);
+  }
+  // The layer loop with every LayerNorm folded into its consumer GEMM. Row statistics of the two
+  // states (64-feature partials) come from ln_row_parts for the inputs (which also copies them to
+  // the outputs) and from the residual GEMMs' epilogues after that. In a cross layer both
+  // branches first project their queries and the other state's keys / values (reading both
+  // states and both statistics buffers), and only after a two-way sync do the output projections
+  // overwrite them.
+  void run_folded(const Tensor* t, const Tensor* f, Tensor* to, Tensor* fo, int64_t B, int64_t St,
+                  int64_t Sf, Stream& ts, Stream& fs, bool two) {
+    const int E = E_;
+    const int64_t rt = B * St, rf = B * Sf;
+    pt_.reserve(sizeof(float) * rt * (E / 64) * 2);
+    pf_.reserve(sizeof(float) * rf * (E / 64) * 2);
+    float* T = to->f32();
+    float* F = fo->f32();
+    float* PT = pt_.f32();
+    float* PF = pf_.f32();
+    k::ln_row_parts(ctx(ts), t->f32(), to->data != t->data ? T : nullptr, rt, E, PT);
+    k::ln_row_parts(ctx(fs), f->f32(), fo->data != f->data ? F : nullptr, rf, E, PF);
+    for (size_t i = 0; i < time_.size(); ++i) {
+      Branch& bt = *time_[i];
+      Branch& bf = *freq_[i];
+      if (!bt.cross) {
+        for (int side = 0; side < 2; ++side) {
+          Branch& b = side ? bf : bt;
+          Stream& st = side ? fs : ts;
+          float* X = side ? F : T;
+          float* P = side ? PF : PT;
+          const int64_t S = side ? Sf : St, rows = side ? rf : rt;
+          const LnFold fq = b.fold_in.get(ctx(st), b.attn->in_w(), 0, 3 * E, E, b.attn->in_b(),
+                                          *b.norm1, P);
+          b.attn->project(X, (int)S, nullptr, 0, (int)B, &fq, nullptr, st);
+          b.attn->finish((int)S, (int)S, false, (int)B, X, X, b.ls1(), P, st);
+          const LnFold f1 = b.fold_ffn.get(ctx(st), b.ffn->w1(), 0, b.ffn->hidden(), E,
+                                           &b.ffn->b1(), *b.norm2, P);
+          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, P);
+        }
+      } else {
+        if (two) {
+          link(ts, fs);
+          link(fs, ts);
+        }
+        for (int side = 0; side < 2; ++side) {
+          Branch& b = side ? bf : bt;
+          Stream& st = side ? fs : ts;
+          float* X = side ? F : T;
+          float* Y = side ? T : F;
+          float* P = side ? PF : PT;
+          float* PY = side ? PT : PF;
+          const int64_t S = side ? Sf : St, Sy = side ? St : Sf;
+          // queries: this branch's cross norm of its own state; keys / values: this branch's
+          // second norm of the other state
+          const LnFold fq = b.fold_in.get(ctx(st), b.attn->in_w(), 0, E, E, b.attn->in_b(),
+                                          *b.norm1, P);
+          const LnFold fkv = b.fold_kv.get(ctx(st), b.attn->in_w(), E, 2 * E, E,
+                                           b.attn->in_b(), *b.norm2, PY);
+          b.attn->project(X, (int)S, Y, (int)Sy, (int)B, &fq, &fkv, st);
+        }
+        if (two) {
+          link(fs, ts);  // freq has read T and PT
+          link(ts, fs);  // time has read F and PF
+        }
+        for (int side = 0; side < 2; ++side) {
+          Branch& b = side ? bf : bt;
+          Stream& st = side ? fs : ts;
+          float* X = side ? F : T;
+          float* P = side ? PF : PT;
+          const int64_t S = side ? Sf : St, Sy = side ? St : Sf, rows = side ? rf : rt;
+          b.attn->finish((int)S, (int)Sy, true, (int)B, X, X, b.ls1(), P, st);
+          const LnFold f1 = b.fold_ffn.get(ctx(st), b.ffn->w1(), 0, b.ffn->hidden(), E,
+                                           &b.ffn->b1(), *b.ffn_norm(), P);
+          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, P);
+        }
+      }
+    }
+  }
+
   hipStream_t side_stream() {
     if (!side_) {
       dev_->make_current();
@@ -2029,7 +2219,7 @@ class CrossTransformerImpl : public Layer {
 
   int E_;
   std::vector<std::unique_ptr<Branch>> time_, freq_;
-  DevBuf ht_, hf_;
+  DevBuf ht_, hf_, pt_, pf_;
   hipStream_t side_ = nullptr;
   std::vector<hipEvent_t> events_;
   size_t next_event_ = 0;

@@ -16,6 +16,7 @@ struct Param {
   int64_t count = 0;
   DevBuf buf;
   bool loaded = false;
+  uint64_t version = 0;  // counts loads, so data derived from the parameter can tell it is stale
   const float* ptr() const { return buf.f32(); }
 };
 

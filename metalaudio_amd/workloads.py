@@ -154,10 +154,12 @@ def cross_encoder_metalnn(batch: int, time_len: int, freq_len: int, embed: int, 
 
 
 def config5(stress: bool = False, batch: int = T5_BATCH, time_len: int = T5_TIME_LEN,
-            freq_len: int = T5_FREQ_LEN, layers: int = T5_LAYERS) -> dict:
-    """Cross-domain bottleneck: E 384, H 8, FFN 1536, LayerScale 1e-4, self/cross alternating."""
+            freq_len: int = T5_FREQ_LEN, layers: int = T5_LAYERS, embed: int = T5_EMBED,
+            heads: int = T5_HEADS, ffn: int = T5_FFN) -> dict:
+    """Cross-domain bottleneck: E 384, H 8, FFN 1536, LayerScale 1e-4, self/cross alternating
+    (other widths for tests)."""
     r = _rng(5)
-    E, Hd = T5_EMBED, T5_FFN
+    E, Hd = embed, ffn
     t = r.standard_normal((batch, time_len, E)).astype(np.float32)
     f = r.standard_normal((batch, freq_len, E)).astype(np.float32)
     p = {}
@@ -177,5 +179,5 @@ def config5(stress: bool = False, batch: int = T5_BATCH, time_len: int = T5_TIME
                 (ls * (1.0 + 0.1 * r.standard_normal(E))).astype(np.float32)
             p[pre + "gamma_2.scale"] = np.full(E, ls, np.float32) if not stress else \
                 (ls * (1.0 + 0.1 * r.standard_normal(E))).astype(np.float32)
-    return {"time": t, "freq": f, "params": p, "embed": E, "heads": T5_HEADS, "ffn": Hd,
+    return {"time": t, "freq": f, "params": p, "embed": E, "heads": heads, "ffn": Hd,
             "layers": layers, "layer_scale": T5_LAYERSCALE}

@@ -462,6 +462,52 @@ def test_cross_transformer_parity_strong_layerscale(dev, stream):
     assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
 
 
+# The HTDemucs-structured cross transformer folds every LayerNorm into the GEMM that consumes it
+# when the width is a multiple of 64 (no standalone LayerNorm launch; row statistics from the
+# residual GEMMs' epilogues): LayerScale 1 so each update enters at full strength, inputs offset
+# by 3 so the rows' means are large next to their spread (the folded form subtracts
+# mean * sum_k W[n][k] gamma[k] from the GEMM of the raw rows), and a reload of one LayerNorm and
+# one projection between forwards (the folded weights must follow). Width 96 runs the standalone
+# LayerNorm kernels instead.
+@pytest.mark.parametrize("E,H,ffn,offset,folded", [(384, 8, 1536, 3.0, True),
+                                                   (96, 2, 192, 0.0, False)])
+def test_cross_transformer_folded_layernorm(dev, stream, E, H, ffn, offset, folded):
+    say(f"cross transformer E {E}: LayerNorms {'folded' if folded else 'standalone'}")
+    c = workloads.config5(stress=True, batch=2, time_len=130, freq_len=257, layers=3, embed=E,
+                          heads=H, ffn=ffn)
+    p = {k: (np.ones_like(v) if "gamma_" in k else v) for k, v in c["params"].items()}
+    t = (c["time"] + offset).astype(np.float32)
+    f = (c["freq"] + offset).astype(np.float32)
+    ct = nn.CrossTransformerEncoder(dev, E, H, ffn, 3, 1e-4)
+    ct.load_state(p)
+    tt, ft = nn.Tensor.from_numpy(dev, t), nn.Tensor.from_numpy(dev, f)
+    to, fo = nn.Tensor(dev, tt.shape), nn.Tensor(dev, ft.shape)
+
+    def run():
+        ct.forward_cross(tt, ft, to, fo, stream)
+        stream.sync(60000)
+
+    names = _launch_names(dev, run)
+    assert ("layernorm_f32" in names) != folded, sorted(set(names))
+    if folded:
+        assert names.count("ln_row_parts_f32") == 2
+        assert names.count("ln_fold_f32") == 14  # per branch: 2 per self layer, 3 per cross layer
+    rt, rf = oracle.cross_transformer(t, f, p, 3, H)
+    assert_close(to.to_numpy(), rt, ATOL, RTOL, "time branch")
+    assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
+    r = np.random.Generator(np.random.PCG64(77))
+    for k in ("layers.1.time.norm2.weight", "layers.1.freq.attn.in_proj_weight"):
+        p[k] = (p[k] * (1 + 0.3 * r.standard_normal(p[k].shape))).astype(np.float32)
+        ct.load_state({k: p[k]})
+    names = _launch_names(dev, run)
+    if folded:
+        # time norm2 of layer 1 feeds the time KV projection; freq in_proj feeds its Q and KV
+        assert names.count("ln_fold_f32") == 3
+    rt, rf = oracle.cross_transformer(t, f, p, 3, H)
+    assert_close(to.to_numpy(), rt, ATOL, RTOL, "time branch after reload")
+    assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch after reload")
+
+
 @pytest.mark.parametrize("B,St,Sf,E,H,ffn,layers", [
     (2, 150, 260, 96, 2, 192, 2),    # head dim 48: the fused attention kernel
     (1, 97, 64, 64, 4, 128, 3),      # head dim 16: the generic attention kernel
