@@ -1908,9 +1908,11 @@ struct Branch {
     }
   }
   LayerNormLayer* ffn_norm() { return cross ? norm3.get() : norm2.get(); }
+  // LayerNorms foldable into the GEMMs after them: fp32, whole 64-feature groups (at most 8),
+  // FFN width a multiple of the GEMM's k step
   bool foldable() const {
     return attn->precision() == MNN_PRECISION_F32 && ffn->precision() == MNN_PRECISION_F32 &&
-           E % 64 == 0 && ffn->hidden() % 32 == 0;
+           E % 64 == 0 && E <= 512 && ffn->hidden() % 32 == 0;
   }
   // returns true if the name was consumed
   bool load(const std::string& name, const float* data, size_t n) {
@@ -1964,6 +1966,24 @@ class TransformerLayerImpl : public Layer {
     int64_t B, S, E;
     split_bse(in.shape, B, S, E);
     const int64_t rows = B * S;
+    const auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (br_.foldable() && a16(in.data) && a16(out.data) &&
+        rows * std::max<int64_t>(3 * E, br_.ffn->hidden()) * 4 < ((int64_t)1 << 32)) {
+      // both LayerNorms folded into the GEMMs after them: row statistics of the input from
+      // ln_row_parts, of the attention block's output from the out-projection's epilogue (the
+      // QKV GEMM has read the first set by then, so one buffer holds both in turn)
+      parts_.reserve(sizeof(float) * rows * (E / 64) * 2);
+      float* P = parts_.f32();
+      k::ln_row_parts(ctx(s), in.f32(), nullptr, rows, (int)E, P);
+      const LnFold fq = br_.fold_in.get(ctx(s), br_.attn->in_w(), 0, 3 * (int)E, (int)E,
+                                        br_.attn->in_b(), *br_.norm1, P);
+      br_.attn->project(in.f32(), (int)S, nullptr, 0, (int)B, &fq, nullptr, s);
+      br_.attn->finish((int)S, (int)S, false, (int)B, out.f32(), in.f32(), br_.ls1(), P, s);
+      const LnFold f1 = br_.fold_ffn.get(ctx(s), br_.ffn->w1(), 0, br_.ffn->hidden(), (int)E,
+                                         &br_.ffn->b1(), *br_.norm2, P);
+      br_.ffn->run(out.f32(), rows, out.f32(), out.f32(), br_.ls2(), s, &f1);
+      return;
+    }
     h_.reserve(sizeof(float) * rows * E);
     br_.norm1->run(in.f32(), rows, h_.f32(), s);
     br_.attn->run(h_.f32(), (int)S, nullptr, 0, (int)B, out.f32(), in.f32(), br_.ls1(), s);
@@ -1974,7 +1994,7 @@ class TransformerLayerImpl : public Layer {
  private:
   int E_;
   Branch br_;
-  DevBuf h_;
+  DevBuf h_, parts_;
 };
 
 // Cross-domain transformer bottleneck (CrossTransformerEncoder, Transformer.swift:567-700) with
@@ -2111,8 +2131,7 @@ class CrossTransformerImpl : public Layer {
   // LDS-DMA GEMM addresses with 32-bit offsets, 16-byte aligned states.
   bool fold_ok(int64_t rt, int64_t rf, const void* t, const void* f, const void* to,
                const void* fo) const {
-    if (E_ % 64 != 0 || !aligned16(t) || !aligned16(f) || !aligned16(to) || !aligned16(fo))
-      return false;
+    if (!aligned16(t) || !aligned16(f) || !aligned16(to) || !aligned16(fo)) return false;
     int64_t widest = 3LL * E_;
     for (const auto* v : {&time_, &freq_})
       for (const auto& b : *v) {

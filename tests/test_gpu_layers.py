@@ -508,6 +508,21 @@ def test_cross_transformer_folded_layernorm(dev, stream, E, H, ffn, offset, fold
     assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch after reload")
 
 
+def test_transformer_layer_folded_layernorm(dev, stream):
+    """The single transformer layer (config-3 widths, fp32) folds both LayerNorms into the GEMMs
+    after them: one statistics pass over the input and no LayerNorm launch; inputs offset by 2."""
+    say("transformer layer: LayerNorms folded, seq 200, offset inputs")
+    cfg = workloads.config3(stress=True, seq=200)
+    x = (cfg["x"] + 2.0).astype(np.float32)
+    t = nn.TransformerLayer(dev, cfg["embed"], cfg["heads"], cfg["ffn"])
+    t.load_state(cfg["params"])
+    got = {}
+    names = _launch_names(dev, lambda: got.setdefault("y", run_layer(t, x, dev, stream)))
+    assert "layernorm_f32" not in names and names.count("ln_row_parts_f32") == 1, names
+    assert_close(got["y"], oracle.transformer_layer(x, cfg["params"], cfg["heads"]), ATOL, RTOL,
+                 "transformer layer, folded LayerNorms")
+
+
 @pytest.mark.parametrize("B,St,Sf,E,H,ffn,layers", [
     (2, 150, 260, 96, 2, 192, 2),    # head dim 48: the fused attention kernel
     (1, 97, 64, 64, 4, 128, 3),      # head dim 16: the generic attention kernel
