@@ -75,6 +75,8 @@ FAMILIES = [
     ("gn_apply_kernel", "gn_apply"),
     ("gemm_f32_mfma_kernel", "gemm_f32_mfma"),
     ("layernorm", "layernorm"),
+    ("ln_row_parts_kernel", "ln_row_parts_f32"),
+    ("ln_fold_kernel", "ln_fold_f32"),
     ("copy_kernel", "copy_bytes"),
 ]
 
