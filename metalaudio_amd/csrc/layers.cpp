@@ -694,19 +694,34 @@ class MHALayer : public Layer {
       qkv_.reserve(sizeof(float) * rq * 3 * E);
       proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, 3 * E, qkv_.f32(), fq, s);
     } else {
-      const int64_t rk = (int64_t)B * Sk;
-      qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
-      float* qb = qkv_.f32();
-      proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, E, qb, fq, s);
-      proj(xkv, rk, win_->ptr() + (int64_t)E * E, bin_ ? bin_->ptr() + E : nullptr, 2 * E,
-           qb + rq * E, fkv, s);
+      project_q(xq, Sq, Sk, B, fq, s);
+      project_kv(xkv, Sq, Sk, B, fkv, s);
     }
+  }
+  // The two halves of a cross-attention's projections (either order; same shapes for both):
+  // queries from xq, keys / values from xkv.
+  void project_q(const float* xq, int Sq, int Sk, int B, const LnFold* fq, Stream& s) {
+    const int E = E_;
+    const int64_t rq = (int64_t)B * Sq, rk = (int64_t)B * Sk;
+    qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
+    proj(xq, rq, win_->ptr(), bin_ ? bin_->ptr() : nullptr, E, qkv_.f32(), fq, s);
+  }
+  void project_kv(const float* xkv, int Sq, int Sk, int B, const LnFold* fkv, Stream& s) {
+    const int E = E_;
+    const int64_t rq = (int64_t)B * Sq, rk = (int64_t)B * Sk;
+    qkv_.reserve(sizeof(float) * (rq * E + rk * 2 * E));
+    proj(xkv, rk, win_->ptr() + (int64_t)E * E, bin_ ? bin_->ptr() + E : nullptr, 2 * E,
+         qkv_.f32() + rq * E, fkv, s);
   }
   // Attention over the projections of the last project() call with the same shapes, then the
   // output projection (+ residual / LayerScale); row_parts receives the output rows' statistics
   // for a LayerNorm folded into the next GEMM.
   void finish(int Sq, int Sk, bool cross, int B, float* out, const float* R, const float* rscale,
               float* row_parts, Stream& s) {
+    attend(Sq, Sk, cross, B, s);
+    out_proj(Sq, B, out, R, rscale, row_parts, s);
+  }
+  void attend(int Sq, int Sk, bool cross, int B, Stream& s) {
     const int E = E_;
     const int64_t rq = (int64_t)B * Sq;
     k::AttnArgs at;
@@ -740,7 +755,12 @@ class MHALayer : public Layer {
     at.o_rs = E;
     at.o_bs = (int64_t)Sq * E;
     k::attention(ctx(s), at);
-    // output projection (+ residual / LayerScale)
+  }
+  // output projection of the last attend() (+ residual / LayerScale)
+  void out_proj(int Sq, int B, float* out, const float* R, const float* rscale, float* row_parts,
+                Stream& s) {
+    const int E = E_;
+    const int64_t rq = (int64_t)B * Sq;
     k::GemmArgs g;
     g.M = (int)rq;
     g.N = E;
@@ -2184,18 +2204,14 @@ class CrossTransformerImpl : public Layer {
         for (int side = 0; side < 2; ++side) {
           Branch& b = side ? bf : bt;
           Stream& st = side ? fs : ts;
-          float* X = side ? F : T;
-          float* Y = side ? T : F;
-          float* P = side ? PF : PT;
-          float* PY = side ? PT : PF;
-          const int64_t S = side ? Sf : St, Sy = side ? St : Sf;
+          const LnFold fq = b.fold_in.get(ctx(st), b.attn->in_w(), 0, E, E, b.attn->in_b(),
+                                          *b.norm1, side ? PF : PT);
+          const LnFold fkv = b.fold_kv.get(ctx(st), b.attn->in_w(), E, 2 * E, E,
+                                           b.attn->in_b(), *b.norm2, side ? PT : PF);
           // queries: this branch's cross norm of its own state; keys / values: this branch's
           // second norm of the other state
-          const LnFold fq = b.fold_in.get(ctx(st), b.attn->in_w(), 0, E, E, b.attn->in_b(),
-                                          *b.norm1, P);
-          const LnFold fkv = b.fold_kv.get(ctx(st), b.attn->in_w(), E, 2 * E, E,
-                                           b.attn->in_b(), *b.norm2, PY);
-          b.attn->project(X, (int)S, Y, (int)Sy, (int)B, &fq, &fkv, st);
+          b.attn->project(side ? F : T, (int)(side ? Sf : St), side ? T : F,
+                          (int)(side ? St : Sf), (int)B, &fq, &fkv, st);
         }
         if (two) {
           link(fs, ts);  // freq has read T and PT
@@ -2225,7 +2241,9 @@ class CrossTransformerImpl : public Layer {
   }
   // `to` waits for the work queued so far on `from`. Each link of a forward has its own event
   // (next_event_ restarts at every forward), so no event is recorded twice within one forward.
-  void link(Stream& from, Stream& to) {
+  void link(Stream& from, Stream& to) { HIP_CHECK(hipStreamWaitEvent(to.s, mark(from), 0)); }
+  // an event recorded after the work queued so far on `from` (one per call within a forward)
+  hipEvent_t mark(Stream& from) {
     if (next_event_ == events_.size()) {
       hipEvent_t e;
       HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
@@ -2233,7 +2251,7 @@ class CrossTransformerImpl : public Layer {
     }
     hipEvent_t e = events_[next_event_++];
     HIP_CHECK(hipEventRecord(e, from.s));
-    HIP_CHECK(hipStreamWaitEvent(to.s, e, 0));
+    return e;
   }
 
   int E_;
