@@ -177,7 +177,8 @@ def test_conv_transpose2d_parity(dev, stream, B, c1, c2, cout, H, W, k, s, p, op
 @pytest.mark.parametrize("B,cin,cskip,cout,H,W,groups", [(1, 96, 96, 48, 8, 4, 8),
                                                          (2, 16, 16, 8, 12, 10, 4),
                                                          (1, 7, 0, 5, 6, 6, 1),
-                                                         (1, 24, 24, 2, 10, 70, 2)])
+                                                         (1, 24, 24, 2, 10, 70, 2),
+                                                         (2, 48, 48, 24, 40, 61, 8)])
 def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, groups):
     say(f"freq decoder block B={B} {cin}+{cskip}->{cout} {H}x{W} G={groups}")
     x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
