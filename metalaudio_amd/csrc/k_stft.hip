@@ -26,6 +26,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kStftLdsTwMaxN = 8192;  // LDS twiddles up to 64 KB of LDS per workgroup
+constexpr int kStftStageMaxN = 4096;  // inverse with the spectrum staged in LDS: 48 KB + 8 bytes
 
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
@@ -151,7 +152,10 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   }
 }
 
-template <bool LDS_TW>
+// STAGE (one-sided spectra, twiddles in LDS): each bin is loaded from global memory once into
+// LDS (the M + 1 float2 after the twiddles) and read back for both members of its Hermitian pair
+// (k and M - k), instead of being loaded twice.
+template <bool LDS_TW, bool STAGE>
 __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
   extern __shared__ float2 z[];
   const int64_t f = frame_of_block(a.frames);
@@ -174,8 +178,32 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
     if (kk == 0 || kk == M) h.y = 0.f;
     return h;
   };
+  if constexpr (STAGE) {
+    float2* xs = z + a.N;  // X[0 .. M]
+    // every load of a batch of 4 bins per thread (clamped indices) before any LDS store
+    for (int k0 = threadIdx.x; k0 <= M; k0 += 4 * kThreads) {
+      float2 g[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) g[u] = get(min(k0 + u * kThreads, M));
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (k0 + u * kThreads <= M) xs[k0 + u * kThreads] = g[u];
+    }
+    __syncthreads();
+    for (int k = threadIdx.x; k < M; k += kThreads) {
+      const float2 zero = make_float2(0.f, 0.f);
+      const float2 hk = herm(k, xs[k], zero), hc = herm(M - k, xs[M - k], zero);
+      const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
+      const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
+      const float2 t = a.tw[k];
+      tws[k] = t;
+      const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
+      const float2 fo = cmul(d, w);
+      z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+    }
+  }
   // every load of a batch of 4 bins per thread (clamped indices) before any LDS store
-  for (int k0 = threadIdx.x; k0 < M; k0 += 4 * kThreads) {
+  for (int k0 = threadIdx.x; !STAGE && k0 < M; k0 += 4 * kThreads) {
     float2 gk[4], gc[4], ck[4], cc[4], tv[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -264,11 +292,14 @@ void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
   MNN_REQUIRE(a.cre && a.cim && a.frames_buf && a.y, MNN_ERR_INVALID_ARGUMENT,
               "stft_inverse: missing buffers");
   const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
-  if (a.N <= kStftLdsTwMaxN)
-    launch(c, "istft_frames_f32", stft_inverse_kernel<true>, grid, dim3(kThreads),
+  if (a.onesided && a.N <= kStftStageMaxN)
+    launch(c, "istft_frames_f32", stft_inverse_kernel<true, true>, grid, dim3(kThreads),
+           sizeof(float2) * (a.N + a.N / 2 + 1), a);
+  else if (a.N <= kStftLdsTwMaxN)
+    launch(c, "istft_frames_f32", stft_inverse_kernel<true, false>, grid, dim3(kThreads),
            sizeof(float2) * a.N, a);
   else
-    launch(c, "istft_frames_f32", stft_inverse_kernel<false>, grid, dim3(kThreads),
+    launch(c, "istft_frames_f32", stft_inverse_kernel<false, false>, grid, dim3(kThreads),
            sizeof(float2) * (a.N / 2), a);
   const int64_t L = (int64_t)(a.frames - 1) * a.hop + a.N;
   launch(c, "istft_overlap_add_f32", stft_overlap_add_kernel,
