@@ -523,6 +523,24 @@ def test_transformer_layer_folded_layernorm(dev, stream):
                  "transformer layer, folded LayerNorms")
 
 
+@pytest.mark.parametrize("B,St,Sf", [(1, 1, 5), (3, 2, 1)])
+def test_cross_transformer_folded_layernorm_tiny(dev, stream, B, St, Sf):
+    """Folded LayerNorms with fewer rows than one GEMM tile (row statistics and row coefficients
+    of rows past the end are computed on clamped rows and never stored)."""
+    say(f"cross transformer folded LayerNorms, tiny: B {B} time {St} freq {Sf}")
+    c = workloads.config5(stress=True, batch=B, time_len=St, freq_len=Sf, layers=2)
+    p = {k: (np.ones_like(v) if "gamma_" in k else v) for k, v in c["params"].items()}
+    ct = nn.CrossTransformerEncoder(dev, c["embed"], c["heads"], c["ffn"], 2, 1e-4)
+    ct.load_state(p)
+    tt, ft = nn.Tensor.from_numpy(dev, c["time"]), nn.Tensor.from_numpy(dev, c["freq"])
+    to, fo = nn.Tensor(dev, tt.shape), nn.Tensor(dev, ft.shape)
+    ct.forward_cross(tt, ft, to, fo, stream)
+    stream.sync(60000)
+    rt, rf = oracle.cross_transformer(c["time"], c["freq"], p, 2, c["heads"])
+    assert_close(to.to_numpy(), rt, ATOL, RTOL, "time branch")
+    assert_close(fo.to_numpy(), rf, ATOL, RTOL, "freq branch")
+
+
 @pytest.mark.parametrize("B,St,Sf,E,H,ffn,layers", [
     (2, 150, 260, 96, 2, 192, 2),    # head dim 48: the fused attention kernel
     (1, 97, 64, 64, 4, 128, 3),      # head dim 16: the generic attention kernel
