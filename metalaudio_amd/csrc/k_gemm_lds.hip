@@ -135,23 +135,39 @@ __device__ __forceinline__ void store_tile(const GemmArgs& a, const floatx16 (&a
   }
 }
 
-// Folded LayerNorm of A's row m: (rstd, -rstd * mean) merged from the row's K / 64 partials
+// Folded LayerNorm of A's rows: (rstd, -rstd * mean) of row m merged from its K / 64 partials
 // (mean, M2) of 64 features each (Chan's formula for equal counts, a fixed order; K <= 64 *
-// kLnMaxParts). Every partial is loaded before the first is used.
+// kLnMaxParts). ln_row_load issues the loads before the main loop, so they complete under it
+// (GEMMs without a folded LayerNorm read a zero dummy, so no load sits under a branch), and
+// ln_row_merge combines them in the epilogue.
 constexpr int kLnMaxParts = 8;
-__device__ __forceinline__ float2 ln_row_coef(const GemmArgs& a, int m) {
-  const int P = a.K / 64;
-  const float2* pp = reinterpret_cast<const float2*>(a.ln_parts) + (int64_t)min(m, a.M - 1) * P;
+struct LnRow {
   float2 q[kLnMaxParts];
+};
+
+__device__ float2 ln_dummy_parts[kLnMaxParts];
+
+__device__ __forceinline__ LnRow ln_row_load(const GemmArgs& a, int m) {
+  const bool on = a.ln_parts != nullptr;
+  const int P = on ? a.K / 64 : 1;
+  const float2* pp =
+      on ? reinterpret_cast<const float2*>(a.ln_parts) + (int64_t)min(m, a.M - 1) * P
+         : ln_dummy_parts;
+  LnRow r;
 #pragma unroll
-  for (int p = 0; p < kLnMaxParts; ++p) q[p] = pp[min(p, P - 1)];
-  float mean = q[0].x, m2 = q[0].y;
+  for (int p = 0; p < kLnMaxParts; ++p) r.q[p] = pp[min(p, P - 1)];
+  return r;
+}
+
+__device__ __forceinline__ float2 ln_row_merge(const GemmArgs& a, const LnRow& r) {
+  const int P = a.K / 64;
+  float mean = r.q[0].x, m2 = r.q[0].y;
 #pragma unroll
   for (int p = 1; p < kLnMaxParts; ++p) {
     if (p < P) {
-      const float d = q[p].x - mean;
+      const float d = r.q[p].x - mean;
       mean += d * (1.f / (float)(p + 1));
-      m2 += q[p].y + d * d * (64.f * (float)p / (float)(p + 1));
+      m2 += r.q[p].y + d * d * (64.f * (float)p / (float)(p + 1));
     }
   }
   const float rstd = 1.f / sqrtf(m2 / (float)a.K + a.ln_eps);
@@ -170,7 +186,7 @@ __device__ __forceinline__ float2 ln_row_coef(const GemmArgs& a, int m) {
 template <int WMW, int WNW, int WM, int WN, int ACT, bool RES, int LDS_FLOATS>
 __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16 (&acc)[WM][WN],
                                                int m0, int n0, int wm, int wn, int lane,
-                                               float* smem) {
+                                               float* smem, const LnRow& lnr) {
   constexpr int BM = WMW * WM * 32, BN = WNW * WN * 32, NT = WMW * WNW * 64;
   constexpr int PITCH = BN + 8;
   constexpr int WROWS = WM * 32;  // rows per wave row
@@ -192,9 +208,9 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16
   float4 bn = make_float4(0.f, 0.f, 0.f, 0.f), rs = make_float4(1.f, 1.f, 1.f, 1.f);
   if (col_ok && a.bias_mode == BIAS_N) bn = *reinterpret_cast<const float4*>(a.bias + gn);
   if (RES && Rp && a.rscale && col_ok) rs = *reinterpret_cast<const float4*>(a.rscale + gn);
-  // Folded LayerNorm: thread r < BM merges row m0 + r's partials into (rstd, -rstd * mean), kept
-  // at the end of the LDS ring past the rows the passes below write; the first pass's barrier
-  // makes them visible.
+  // Folded LayerNorm: thread r < BM merges row m0 + r's partials (loaded before the main loop)
+  // into (rstd, -rstd * mean), kept at the end of the LDS ring past the rows the passes below
+  // write; the first pass's barrier makes them visible.
   static_assert(PROWS * PITCH + 2 * BM <= LDS_FLOATS, "epilogue tile and row coefficients");
   static_assert(BM <= NT, "one row coefficient per thread");
   float2* lnrow = reinterpret_cast<float2*>(smem + LDS_FLOATS - 2 * BM);
@@ -202,7 +218,7 @@ __device__ __forceinline__ void store_tile_lds(const GemmArgs& a, const floatx16
   float4 lc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (ln) {
     if (col_ok) lc = *reinterpret_cast<const float4*>(a.ln_c + gn);
-    if (tid < BM) lnrow[tid] = ln_row_coef(a, m0 + tid);
+    if (tid < BM) lnrow[tid] = ln_row_merge(a, lnr);
   }
   const bool rstats = a.row_parts != nullptr;
 #pragma unroll
@@ -447,6 +463,9 @@ void gemm_nk_lds_kernel(GemmArgs a) {
   const int m0 = tm * BM, n0 = tn * BN;
   const int M = a.M, N = a.N, K = a.K;
   const int nk = K / BKE / ks, kt0 = (int)(blockIdx.z % ks) * nk;  // this workgroup's stages
+  // a folded LayerNorm's row partials (thread r: row m0 + r % BM)
+  LnRow lnr;
+  if constexpr (EPI == 0 && !BF) lnr = ln_row_load(a, m0 + tid % BM);
   const char* __restrict__ A = reinterpret_cast<const char*>(a.A) + (int64_t)bz * a.sA * ES;
   const char* __restrict__ B = reinterpret_cast<const char*>(a.B) + (int64_t)bz * a.sB * ES;
 
@@ -626,13 +645,17 @@ void gemm_nk_lds_kernel(GemmArgs a) {
     if (rows16 && !bm) {
       __syncthreads();  // every wave's last fragment reads of the LDS ring are done
       if (a.act == 0 && !res)
-        store_tile_lds<WMW, WNW, WM, WN, 0, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+        store_tile_lds<WMW, WNW, WM, WN, 0, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem,
+                                                              lnr);
       else if (a.act == 0)
-        store_tile_lds<WMW, WNW, WM, WN, 0, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+        store_tile_lds<WMW, WNW, WM, WN, 0, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem,
+                                                             lnr);
       else if (a.act == 3 && !res)
-        store_tile_lds<WMW, WNW, WM, WN, 3, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+        store_tile_lds<WMW, WNW, WM, WN, 3, false, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem,
+                                                              lnr);
       else
-        store_tile_lds<WMW, WNW, WM, WN, -1, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem);
+        store_tile_lds<WMW, WNW, WM, WN, -1, true, S * STAGE>(a, acc, m0, n0, wm, wn, lane, smem,
+                                                              lnr);
       return;
     }
   }
