@@ -2181,6 +2181,7 @@ class CrossTransformerImpl : public Layer {
     for (size_t i = 0; i < time_.size(); ++i) {
       Branch& bt = *time_[i];
       Branch& bf = *freq_[i];
+      const bool last = i + 1 == time_.size();  // no LayerNorm reads the final states
       if (!bt.cross) {
         for (int side = 0; side < 2; ++side) {
           Branch& b = side ? bf : bt;
@@ -2194,7 +2195,7 @@ class CrossTransformerImpl : public Layer {
           b.attn->finish((int)S, (int)S, false, (int)B, X, X, b.ls1(), P, st);
           const LnFold f1 = b.fold_ffn.get(ctx(st), b.ffn->w1(), 0, b.ffn->hidden(), E,
                                            &b.ffn->b1(), *b.norm2, P);
-          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, P);
+          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, last ? nullptr : P);
         }
       } else {
         if (two) {
@@ -2226,7 +2227,7 @@ class CrossTransformerImpl : public Layer {
           b.attn->finish((int)S, (int)Sy, true, (int)B, X, X, b.ls1(), P, st);
           const LnFold f1 = b.fold_ffn.get(ctx(st), b.ffn->w1(), 0, b.ffn->hidden(), E,
                                            &b.ffn->b1(), *b.ffn_norm(), P);
-          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, P);
+          b.ffn->run(X, rows, X, X, b.ls2(), st, &f1, last ? nullptr : P);
         }
       }
     }
