@@ -586,7 +586,10 @@ __global__ __launch_bounds__(256) void enc_l1_stats_kernel(EncL1KArgs a) {
   const int Ls = (int)a.L, Lo = (int)a.Lout;
   const int tasks = (Lo + 31) / 32;
   const int stride = gridDim.x * 4;
-  ShiftedStats st[2];
+  // sums of (v - shift) and its square with one shift per lane, a bias of the lane's channels
+  // (outputs sit near their channel's bias), in two chains; the count is 24 per valid column
+  const float shift = s_b1[4 * g];
+  float s1[2] = {0.f, 0.f}, s2[2] = {0.f, 0.f}, cnt = 0.f;
   int task = blockIdx.x * 4 + wave;
   float xv[KS];
   if (task < tasks) l1_load_x<CIN, REFLECT>(xb, Ls, Lo, a.pad, task, lane, xv);
@@ -601,17 +604,28 @@ __global__ __launch_bounds__(256) void enc_l1_stats_kernel(EncL1KArgs a) {
     l1_conv<CIN>(acv, xv, ac);
     if (task * 32 + l32 < Lo) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) st[v & 1].add(ac[0][v]);
+      for (int v = 0; v < 16; ++v) {
+        const float d = ac[0][v] - shift;
+        s1[v & 1] += d;
+        s2[v & 1] = fmaf(d, d, s2[v & 1]);
+      }
 #pragma unroll
-      for (int v = 0; v < 8; ++v) st[v & 1].add(ac[1][v]);  // channels 32..47
+      for (int v = 0; v < 8; ++v) {  // channels 32..47
+        const float d = ac[1][v] - shift;
+        s1[v & 1] += d;
+        s2[v & 1] = fmaf(d, d, s2[v & 1]);
+      }
+      cnt += 24.f;
     }
 #pragma unroll
     for (int s = 0; s < KS; ++s) xv[s] = xn[s];
   }
-  float sn, smean, sm2, n2, mean2, m22;
-  st[0].finish(sn, smean, sm2);
-  st[1].finish(n2, mean2, m22);
-  welford_combine(sn, smean, sm2, n2, mean2, m22);
+  float sn = cnt, smean = 0.f, sm2 = 0.f;
+  if (cnt > 0.f) {
+    const float t1 = s1[0] + s1[1], md = t1 / cnt;
+    smean = shift + md;
+    sm2 = fmaxf((s2[0] + s2[1]) - t1 * md, 0.f);
+  }
   block_welford(sn, smean, sm2, red);
   if (tid == 0) {
     float* o = a.parts + ((int64_t)b * gridDim.x + blockIdx.x) * 3;
