@@ -47,7 +47,9 @@ typedef enum mnn_status {
   MNN_ERR_SHAPE_MISMATCH = 8,          /* SequentialModelError.shapeMismatch */
   MNN_ERR_EMPTY_MODEL = 9,             /* SequentialModelError.emptyModel */
   MNN_ERR_INPUT_SHAPE_MISMATCH = 10,   /* SequentialModelError.inputShapeMismatch */
-  MNN_ERR_NOT_BUILT = 11,              /* "Model not built. Call build() first." (Model.swift:226-228) */
+  MNN_ERR_NOT_BUILT = 11,              /* reserved, never returned: a Sequential used before build() is
+                                          MNN_ERR_INVALID_CONFIGURATION "Model not built. Call build()
+                                          first.", as the reference (Model.swift:228-229, :293-298) */
   MNN_ERR_INVALID_ARGUMENT = 12,       /* NULL handle, bad rank, unknown weight name */
   /* SafeTensorsLoader.LoaderError (SafeTensorsLoader.swift:95-128) */
   MNN_ERR_FILE_NOT_FOUND = 13,         /* fileNotFound */
@@ -469,8 +471,7 @@ mnn_status mnn_cross_transformer_create(mnn_device dev, int embed_dim, int num_h
 
 /* CrossTransformerEncoder(device:embedDim:numHeads:ffnDim:numLayers:) with the reference class's
  * own layer structure (TransformerLayer, Transformer.swift:370-560; layer loop :626-667). Each
- * layer: T += 2*SA_t(LN_ts T) (the reference adds this residual twice, :459-460);
- * F += SA_f(LN_fs F); tn = LN_tc T, fn = LN_fc F; T += CA_t(tn, fn); F += CA_f(fn, tn);
+ * layer, one residual per sub-block (:467-495): T += SA_t(LN_ts T); F += SA_f(LN_fs F); tn = LN_tc T, fn = LN_fc F; T += CA_t(tn, fn); F += CA_f(fn, tn);
  * T += FFN_t(LN_tf T); F += FFN_f(LN_ff F). No LayerScale. forward through
  * mnn_layer_forward_cross(time, freq, time_out, freq_out); [S, E] or [B, S, E] per branch.
  * Weights as TransformerLayer.loadWeights (:529-557): "layers.{i}.{norm_time_self,
@@ -520,11 +521,12 @@ mnn_status mnn_sequential_forward(mnn_sequential seq, mnn_tensor input, mnn_stre
 /* Sequential.forwardAsync(_:completion:) (Model.swift:271-346): enqueues the forward on s and
  * returns. completion(user, status, output) runs exactly once: on a library thread after the GPU
  * work has finished (MNN_OK and the borrowed output, or MNN_ERR_GPU_EXECUTION and NULL), or,
- * when the forward cannot be enqueued (empty model, not built, input shape, another forwardAsync
- * of this model still in flight: MNN_ERR_INVALID_CONFIGURATION), on the calling thread before
- * this returns the same status. As the reference, one forwardAsync per model at a time; the
+ * when the forward cannot be enqueued, on the calling thread before this returns the same status:
+ * MNN_ERR_EMPTY_MODEL, MNN_ERR_INVALID_CONFIGURATION (not built, or another forwardAsync of this
+ * model still in flight) or MNN_ERR_INPUT_SHAPE_MISMATCH, as Model.swift:285-320 reports them. As the reference, one forwardAsync per model at a time; the
  * in-flight mark is cleared before the completion runs, so the completion may start the next
- * one. The completion must not destroy the model (its destructor waits for completions). */
+ * one. mnn_sequential_destroy waits for the model's completions to return; called from the
+ * model's own completion, it waits only for the model's other completions. */
 typedef void (*mnn_completion_fn)(void* user, mnn_status status, mnn_tensor output);
 mnn_status mnn_sequential_forward_async(mnn_sequential seq, mnn_tensor input, mnn_stream s,
                                         mnn_completion_fn completion, void* user);

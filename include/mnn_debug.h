@@ -43,6 +43,11 @@ mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* n
  * check it. *previous (may be null) receives the old bound; the default is 65536. */
 mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previous);
 
+/* Number of device allocations (hipMalloc) the library has made in this process: tensors, layer
+ * weights and workspaces. The tests read it around a call to check that the call allocated
+ * nothing (the allocation-free entry point). */
+mnn_status mnn_debug_device_allocations(int64_t* count);
+
 #ifdef __cplusplus
 }
 #endif

@@ -226,6 +226,7 @@ SIGNATURES = {
     "mnn_debug_set_launch_log": (C.c_int, [P, C.c_int]),
     "mnn_debug_launch_log": (C.c_int, [P, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "mnn_debug_set_grid_spin_limit": (C.c_int, [P, C.c_int, C.POINTER(C.c_int)]),
+    "mnn_debug_device_allocations": (C.c_int, [I64P]),
 }
 
 _lib = None

@@ -411,6 +411,8 @@ mnn_status mnn_conv1d_forward_residual(mnn_layer layer, mnn_tensor input, mnn_te
     MNN_REQUIRE(in->dev == l->device() && out->dev == l->device() &&
                     (!res || res->dev == l->device()),
                 MNN_ERR_INVALID_ARGUMENT, "tensors must live on the layer's device");
+    MNN_REQUIRE(in->dtype == MNN_F32 && out->dtype == MNN_F32 && (!res || res->dtype == MNN_F32),
+                MNN_ERR_INVALID_ARGUMENT, "forwardWithResidual: tensors must be f32");
     in->dev->check_alive();
     Stream s = resolve_stream(in->dev, st);
     in->dev->make_current();
@@ -429,6 +431,8 @@ mnn_status mnn_groupnorm_forward_noalloc(mnn_layer layer, mnn_tensor input, mnn_
     Tensor* out = T(output);
     MNN_REQUIRE(in->dev == l->device() && out->dev == l->device(), MNN_ERR_INVALID_ARGUMENT,
                 "tensors must live on the layer's device");
+    MNN_REQUIRE(in->dtype == MNN_F32 && out->dtype == MNN_F32, MNN_ERR_INVALID_ARGUMENT,
+                "GroupNorm: tensors must be f32");
     in->dev->check_alive();
     Stream s = resolve_stream(in->dev, st);
     in->dev->make_current();
@@ -1167,6 +1171,13 @@ mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previou
     Device* d = D(dev);
     const int old = d->grid_spin_limit.exchange(polls);
     if (previous) *previous = old;
+  });
+}
+
+mnn_status mnn_debug_device_allocations(int64_t* count) {
+  return guard([&] {
+    MNN_REQUIRE(count, MNN_ERR_INVALID_ARGUMENT, "count is required");
+    *count = g_device_allocations.load();
   });
 }
 

@@ -28,6 +28,10 @@ struct Error {
 
 [[noreturn]] inline void fail(mnn_status code, const std::string& msg) { throw Error{code, msg}; }
 
+// Number of device allocations the library has made (tensors, weights, workspaces), process-wide;
+// read through mnn_debug_device_allocations so tests can check that a path allocates nothing.
+extern std::atomic<int64_t> g_device_allocations;
+
 #define MNN_REQUIRE(cond, code, msg_expr)                      \
   do {                                                         \
     if (!(cond)) {                                             \
@@ -131,6 +135,7 @@ struct DevBuf {
     if (n <= bytes) return;
     release();
     HIP_CHECK(hipMalloc(&ptr, n));
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
     bytes = n;
   }
   float* f32() const { return static_cast<float*>(ptr); }

@@ -2271,14 +2271,15 @@ class CrossTransformerImpl : public Layer {
 // tanh form agree to float precision beyond |x| = 10).
 // CrossTransformerEncoder with the reference class's own layer structure (TransformerLayer,
 // Transformer.swift:370-560; the encoder's layer loop :626-667). Per layer, in this order:
-//   T += 2 * SA_t(LN_ts(T))   the reference adds the time self-attention residual twice (:459-460)
+//   T += SA_t(LN_ts(T))       (:467-470)
 //   F += SA_f(LN_fs(F))
 //   tn = LN_tc(T); fn = LN_fc(F)
 //   T += CA_t(tn, fn)         time queries, freq keys / values
 //   F += CA_f(fn, tn)         freq queries; tn is the time state from before the line above
 //   T += FFN_t(LN_tf(T)); F += FFN_f(LN_ff(F))
-// No LayerScale. Residuals go through the GEMM epilogues (out-projection, FFN second linear) as
-// C = R + rscale * (acc + bias), the doubled one with rscale = 2. Weight names follow
+// One residual per sub-block (:467-495), no LayerScale: every residual goes through the GEMM
+// epilogue of the sub-block's last linear map (out-projection, FFN second linear) as
+// C = R + (acc + bias). Weight names follow
 // TransformerLayer.loadWeights (:529-557): layers.{i}.{norm_time_self, norm_freq_self,
 // norm_time_cross, norm_freq_cross, norm_time_ffn, norm_freq_ffn}.{weight,bias},
 // layers.{i}.{self_attn_time, self_attn_freq, cross_attn_time, cross_attn_freq}.{in_proj_weight,
@@ -2302,9 +2303,6 @@ class CrossTransformerEncoderImpl : public Layer {
       L->fff = std::make_unique<FeedForwardLayer>(d, embed, ffn, prec);
       layers_.push_back(std::move(L));
     }
-    std::vector<float> two(embed, 2.f);
-    two_.reserve(sizeof(float) * embed);
-    HIP_CHECK(hipMemcpy(two_.ptr, two.data(), sizeof(float) * embed, hipMemcpyHostToDevice));
   }
   const char* kind() const override { return "CrossTransformerEncoder"; }
   Shape input_shape() const override { return {0, E_}; }
@@ -2362,7 +2360,7 @@ class CrossTransformerEncoderImpl : public Layer {
     for (auto& Lp : layers_) {
       Lyr& L = *Lp;
       L.nts->run(T, rt, ht, s);
-      L.sat->run(ht, (int)St, nullptr, 0, (int)B, T, T, two_.f32(), s);
+      L.sat->run(ht, (int)St, nullptr, 0, (int)B, T, T, nullptr, s);
       L.nfs->run(F, rf, hf, s);
       L.saf->run(hf, (int)Sf, nullptr, 0, (int)B, F, F, nullptr, s);
       L.ntc->run(T, rt, ht, s);
@@ -2384,7 +2382,7 @@ class CrossTransformerEncoderImpl : public Layer {
   };
   int E_;
   std::vector<std::unique_ptr<Lyr>> layers_;
-  DevBuf two_, ht_, hf_;
+  DevBuf ht_, hf_;
 };
 
 int fused_chain_length(const std::vector<Layer*>& v, size_t i) {
@@ -2407,7 +2405,14 @@ void run_fused_chain(const std::vector<Layer*>& v, size_t i, int n, const Tensor
   int64_t B, C, L;
   split_bcl(in.shape, B, C, L);
   const int act = n == 3 ? MNN_ACT_GELU : g->act();
-  if (c->register_window((int)B, (int)L)) {
+  // The plan may give the chain's last layer the buffer of the layer before the chain, i.e. the
+  // chain's own input. The forms below that recompute the convolution from `in` while other
+  // workgroups already write `out` then race, so an aliased output takes the y path.
+  const char* ib = static_cast<const char*>(in.data);
+  const char* ob = static_cast<const char*>(out.data);
+  const bool aliased = ob < ib + in.count() * dtype_size(in.dtype) &&
+                       ib < ob + out.count() * dtype_size(out.dtype);
+  if (!aliased && c->register_window((int)B, (int)L)) {
     // small contraction: statistics pass, then a pass that recomputes the convolution and
     // writes the normalised output once (y is not used)
     k::ConvParams p = c->direct_params((int)B, (int)L);

@@ -122,12 +122,17 @@ class Sequential {
   const Plan* last_plan_ = nullptr;
   std::mutex forward_mu_;
   Tensor* forward_locked(const Tensor& in, Stream& s);
-  // forwardAsync bookkeeping: one forward in flight at a time; the destructor waits for the
-  // completion threads.
+  // forwardAsync bookkeeping: one forward in flight at a time. The completion threads count
+  // themselves in a state block they share with the model, so a thread whose completion
+  // destroyed the model still finds the block alive; the destructor waits for every other
+  // completion thread.
+  struct AsyncState {
+    std::mutex mu;
+    std::condition_variable cv;
+    int threads = 0;
+  };
   std::atomic<bool> async_in_flight_{false};
-  std::mutex async_mu_;
-  std::condition_variable async_cv_;
-  int async_threads_ = 0;
+  std::shared_ptr<AsyncState> async_ = std::make_shared<AsyncState>();
 };
 
 Tensor* tensor_create(Device* d, mnn_dtype dt, const Shape& shape);

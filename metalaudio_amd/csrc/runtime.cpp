@@ -8,6 +8,8 @@ namespace mnn {
 
 size_t dtype_size(mnn_dtype t) { return t == MNN_BF16 ? 2 : 4; }
 
+std::atomic<int64_t> g_device_allocations{0};
+
 // ------------------------------------------------------------------ kernel timing
 void timing_begin(const LaunchCtx& c, const char*, hipEvent_t* e0, hipEvent_t* e1) {
   Device* d = c.dev;
@@ -64,6 +66,7 @@ Tensor* tensor_create(Device* d, mnn_dtype dt, const Shape& shape) {
   d->make_current();
   if (t->bytes) {
     HIP_CHECK(hipMalloc(&t->data, t->bytes));
+    g_device_allocations.fetch_add(1, std::memory_order_relaxed);
     HIP_CHECK(hipMemsetAsync(t->data, 0, t->bytes, d->default_stream));
     HIP_CHECK(hipStreamSynchronize(d->default_stream));
   }
@@ -80,10 +83,17 @@ void tensor_destroy(Tensor* t) {
 }
 
 // ------------------------------------------------------------------ Sequential
+namespace {
+// The model whose forwardAsync completion runs on this thread, if any.
+thread_local const Sequential* tl_completing = nullptr;
+}  // namespace
+
 Sequential::~Sequential() {
-  {  // completion threads of forward_async hold `this` until their callback has returned
-    std::unique_lock<std::mutex> lk(async_mu_);
-    async_cv_.wait(lk, [&] { return async_threads_ == 0; });
+  {  // completion threads of forward_async use `this` until their callback has returned; a
+     // completion that destroys its own model waits only for the model's other threads
+    const int self = tl_completing == this ? 1 : 0;
+    std::unique_lock<std::mutex> lk(async_->mu);
+    async_->cv.wait(lk, [&] { return async_->threads <= self; });
   }
   free_plans();
 }
@@ -163,7 +173,8 @@ Tensor* Sequential::forward(const Tensor& in, Stream& s) {
 
 Tensor* Sequential::forward_locked(const Tensor& in, Stream& s) {
   MNN_REQUIRE(!layers_.empty(), MNN_ERR_EMPTY_MODEL, "Cannot run inference on empty model");
-  MNN_REQUIRE(built_, MNN_ERR_NOT_BUILT, "Model not built. Call build() first.");
+  // Model.swift:228-229 (and forwardAsync, :293-298): invalidConfiguration
+  MNN_REQUIRE(built_, MNN_ERR_INVALID_CONFIGURATION, "Model not built. Call build() first.");
   // Model.swift:231-236 compares the whole shape; here leading batch dimensions are allowed
   // (layers take [C, L] or [B, C, L], [F] or [N, F]) and 0 in the declared shape is dynamic.
   const Shape expect = layers_[0]->input_shape();
@@ -210,21 +221,36 @@ void Sequential::forward_async(const Tensor& in, Stream& s, Completion done) {
     async_in_flight_ = false;
     throw;
   }
-  {
-    std::lock_guard<std::mutex> lk(async_mu_);
-    ++async_threads_;
-  }
   const int ordinal = dev_->ordinal;
-  std::thread([this, ev, out, ordinal, done = std::move(done)]() {
-    (void)hipSetDevice(ordinal);
-    const hipError_t e = hipEventSynchronize(ev);
+  std::shared_ptr<AsyncState> st = async_;
+  {
+    std::lock_guard<std::mutex> lk(st->mu);
+    ++st->threads;
+  }
+  try {
+    std::thread([this, st, ev, out, ordinal, done = std::move(done)]() {
+      (void)hipSetDevice(ordinal);
+      const hipError_t e = hipEventSynchronize(ev);
+      (void)hipEventDestroy(ev);
+      async_in_flight_ = false;  // as the reference, cleared before the completion runs
+      tl_completing = this;
+      done(e == hipSuccess ? MNN_OK : MNN_ERR_GPU_EXECUTION, e == hipSuccess ? out : nullptr);
+      tl_completing = nullptr;
+      // `this` may be gone now (the completion may destroy the model): only `st` is used
+      std::lock_guard<std::mutex> lk(st->mu);
+      --st->threads;
+      st->cv.notify_all();
+    }).detach();
+  } catch (...) {  // no thread: undo the bookkeeping so the model stays usable and destroyable
+    {
+      std::lock_guard<std::mutex> lk(st->mu);
+      --st->threads;
+    }
+    st->cv.notify_all();
     (void)hipEventDestroy(ev);
-    async_in_flight_ = false;  // as the reference, cleared before the completion runs
-    done(e == hipSuccess ? MNN_OK : MNN_ERR_GPU_EXECUTION, e == hipSuccess ? out : nullptr);
-    std::lock_guard<std::mutex> lk(async_mu_);
-    --async_threads_;
-    async_cv_.notify_all();
-  }).detach();
+    async_in_flight_ = false;
+    fail(MNN_ERR_INVALID_CONFIGURATION, "forwardAsync: could not start the completion thread");
+  }
 }
 
 Layer* Sequential::layer_at(int index) const {

@@ -960,8 +960,7 @@ class CrossTransformerEncoder(Layer):
 
 class MetalNNCrossTransformerEncoder(CrossTransformerEncoder):
     """CrossTransformerEncoder with the reference class's own layer structure (Transformer.swift:
-    370-667): every layer self-attention (the time residual added twice, as the reference does),
-    cross-attention both ways and an FFN per branch, six LayerNorms, no LayerScale; weights
+    370-667): every layer self-attention, cross-attention both ways and an FFN per branch, six LayerNorms, no LayerScale; weights
     layers.{i}.{norm_time_self|...|self_attn_time|...|ffn_freq}.*"""
 
     def __init__(self, device, embed_dim, num_heads, ffn_dim, num_layers, precision="f32"):

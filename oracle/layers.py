@@ -436,8 +436,9 @@ def cross_transformer(time, freq, p, num_layers, num_heads, dtype=np.float64):
 def cross_transformer_metalnn(time, freq, p, num_layers, num_heads, dtype=np.float64):
     """CrossTransformerEncoder with the reference class's own layer structure: the encoder runs
     its layers in order (Transformer.swift:626-667; the copies between layers are plain copies),
-    each layer being TransformerLayer.forward(timeInput:freqInput:...) (:441-498):
-      1. T += SA_t(LN_ts T), the residual added twice (:459-460, two addResidual calls);
+    each layer being TransformerLayer.forward(timeInput:freqInput:...) (:441-498), one
+    addResidual per sub-block (:467-495):
+      1. T += SA_t(LN_ts T) (:467-470);
       2. F += SA_f(LN_fs F);
       3. tn = LN_tc T, fn = LN_fc F; T += CA_t(tn, fn);
       4. F += CA_f(fn, tn) (tn from before step 3's update);
@@ -459,9 +460,7 @@ def cross_transformer_metalnn(time, freq, p, num_layers, num_heads, dtype=np.flo
 
     for i in range(num_layers):
         L = f"layers.{i}."
-        a = attn(ln(T, L + "norm_time_self"), None, L + "self_attn_time")
-        T = T + a
-        T = T + a
+        T = T + attn(ln(T, L + "norm_time_self"), None, L + "self_attn_time")
         F = F + attn(ln(F, L + "norm_freq_self"), None, L + "self_attn_freq")
         tn = ln(T, L + "norm_time_cross")
         fn = ln(F, L + "norm_freq_cross")

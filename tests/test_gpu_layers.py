@@ -548,7 +548,7 @@ def test_cross_transformer_folded_layernorm_tiny(dev, stream, B, St, Sf):
 ])
 def test_cross_transformer_encoder_metalnn_parity(dev, stream, B, St, Sf, E, H, ffn, layers):
     """The reference-structured CrossTransformerEncoder (every layer self + cross + FFN per branch,
-    the time self-attention residual added twice, Transformer.swift:441-498) with weights loaded
+    one residual per sub-block, Transformer.swift:441-498) with weights loaded
     by the reference's names, against the oracle; every sub-block's update is of the order of its
     input, so a dropped or misordered term shows."""
     say(f"reference-structured cross transformer B={B} St={St} Sf={Sf} E={E} H={H} L={layers}")
@@ -635,7 +635,8 @@ def test_sequential_errors(dev, stream):
     assert e.value.name == "MNN_ERR_SHAPE_MISMATCH"
     with pytest.raises(nn.MNNError) as e:
         seq.forward(nn.Tensor(dev, [4]), stream)
-    assert e.value.name == "MNN_ERR_NOT_BUILT"
+    # not built: invalidConfiguration("Model not built. Call build() first."), Model.swift:228-229
+    assert e.value.name == "MNN_ERR_INVALID_CONFIGURATION" and "not built" in str(e.value)
     seq.build()
     with pytest.raises(nn.MNNError) as e:
         seq.forward(nn.Tensor(dev, [5]), stream)
@@ -926,6 +927,11 @@ def test_fused_conv1d_residual_errors(dev, stream):
         gn = nn.GroupNorm(dev, 1, 4)
         nn.Conv1D.forward_with_residual(gn, x, None, nn.Tensor(dev, (1, 4, 20)), stream)
     assert e.value.name == "MNN_ERR_INVALID_ARGUMENT"
+    for xi, ri in ((nn.Tensor(dev, (1, 4, 20), dtype="bf16"), None),  # 2-byte elements
+                   (x, nn.Tensor(dev, (1, 8, 20), dtype="bf16"))):
+        with pytest.raises(nn.MNNError) as e:
+            layer.forward_with_residual(xi, ri, nn.Tensor(dev, (1, 8, 20)), stream)
+        assert e.value.name == "MNN_ERR_INVALID_ARGUMENT"
     with pytest.raises(nn.MNNError):
         nn.FusedConv1D(dev, 4, 8, 3, leaky_relu_alpha=float("nan"))
 
@@ -1001,6 +1007,22 @@ def test_sequential_forward_async(dev, stream):
 
     assert seq.forward_async(xt, first, stream) == 0
     assert done2.wait(30) and chained["rc"] == 0 and chained["status"] == 0
+    # a completion may destroy its own model: the destroy returns (it does not wait for the
+    # completion that called it) and the library thread ends without touching the model
+    gone = nn.Sequential(dev)
+    gone.add(keep[0])
+    gone.build()
+    done3 = threading.Event()
+    closed = {}
+
+    def closing(status, out):
+        closed["status"] = status
+        gone.close()
+        closed["handle"] = gone.handle
+        done3.set()
+
+    assert gone.forward_async(xt, closing, stream) == 0
+    assert done3.wait(30) and closed == {"status": 0, "handle": None}
     # not built / empty: reported through the completion, synchronously, and returned
     errs = []
     empty = nn.Sequential(dev)
@@ -1009,7 +1031,7 @@ def test_sequential_forward_async(dev, stream):
     unbuilt = nn.Sequential(dev)
     unbuilt.add(nn.Linear(dev, 32, 32))
     rc = unbuilt.forward_async(xt, lambda st, out: errs.append((st, out)), stream)
-    assert rc == 11 and errs[-1] == (11, None)  # MNN_ERR_NOT_BUILT
+    assert rc == 1 and errs[-1] == (1, None)  # invalidConfiguration, as Model.swift:293-298
 
 
 @pytest.mark.parametrize("cin,cout,L,act,gelu,k,mode,pad", [
@@ -1054,6 +1076,34 @@ def test_sequential_conv_groupnorm_fusion(dev, stream, cin, cout, L, act, gelu, 
                             1, gm, bt)
     ref = oracle.gelu_layer(ref) if gelu else oracle.activation(ref, act)
     assert_close(out.to_numpy().reshape(ref.shape), ref, ATOL, RTOL, "fused sequential")
+
+
+@pytest.mark.parametrize("C,L", [(16, 20001), (32, 4099)])
+def test_sequential_fused_chain_output_aliases_its_input(dev, stream, C, L):
+    """GELU -> Conv1D(C -> C, k 1) -> GroupNorm(1): the ping-pong plan gives GroupNorm (the fused
+    chain's last layer) the buffer GELU wrote, i.e. the chain's own input. The result must still be
+    the layers' composition (the chain then goes through the conv's own buffer)."""
+    say(f"fused chain whose output aliases its input C={C} L={L}")
+    x = RNG.uniform(-2, 2, (C, L)).astype(np.float32)
+    w = (RNG.standard_normal((C, C, 1)) * np.sqrt(2 / C)).astype(np.float32)
+    b = (0.5 + 0.3 * RNG.standard_normal(C)).astype(np.float32)
+    gm = (1 + 0.2 * RNG.standard_normal(C)).astype(np.float32)
+    bt = (0.2 * RNG.standard_normal(C)).astype(np.float32)
+    seq = nn.Sequential(dev)
+    seq.add(nn.GELU(dev, [C, L]))
+    conv = nn.Conv1D(dev, C, C, 1, input_length=L)
+    conv.load_weights(w, b)
+    seq.add(conv)
+    gn = nn.GroupNorm(dev, 1, C, activation="relu")
+    gn.load_parameters(gm, bt)
+    seq.add_unchecked(gn)
+    seq.build()
+    assert seq.buffer_stats == (2, 3)  # GroupNorm reuses GELU's buffer
+    out = seq.forward(nn.Tensor.from_numpy(dev, x), stream)
+    stream.sync(60000)
+    ref = oracle.activation(oracle.group_norm(oracle.conv1d(oracle.gelu_layer(x), w, b), 1, gm,
+                                              bt), "relu")
+    assert_close(out.to_numpy().reshape(ref.shape), ref, ATOL, RTOL, "aliased fused chain")
 
 
 def _launch_names(dev, fn):

@@ -242,10 +242,14 @@ def test_transformer_layer_matches_torch_encoder_layer():
                                atol=1e-9)
 
 
-def _metalnn_encoder_torch(cfg, double_time_self=True):
-    """The reference CrossTransformerEncoder's layer loop (Transformer.swift:441-498, 626-667)
-    composed from torch library routines: F.layer_norm, torch's MultiheadAttention with the
-    packed in_proj, and Linear -> tanh GELU -> Linear."""
+def _metalnn_encoder_torch(cfg, plant=None):
+    """The reference CrossTransformerEncoder's layer loop (Transformer.swift:626-667) with
+    TransformerLayer.forward (:441-498) composed from torch library routines: F.layer_norm,
+    torch's MultiheadAttention with the packed in_proj, Linear -> tanh GELU -> Linear, and one
+    addResidual per sub-block, in the order of :467-495. `plant` names a mistake planted in this
+    checker ("double_time_self": the time self-attention residual added twice;
+    "cross_reads_updated_time": the freq cross-attention's keys / values normalised from the time
+    state after its own cross update instead of the timeNormed of :478)."""
     p, E, H = cfg["params"], cfg["embed"], cfg["heads"]
 
     def ln(x, pre):
@@ -265,22 +269,26 @@ def _metalnn_encoder_torch(cfg, double_time_self=True):
         T, Fr = t64(cfg["time"]), t64(cfg["freq"])
         for i in range(cfg["layers"]):
             L = f"layers.{i}."
-            h = ln(T, L + "norm_time_self")
-            a = attn(h, h, L + "self_attn_time")
-            T = T + (2.0 if double_time_self else 1.0) * a
-            h = ln(Fr, L + "norm_freq_self")
+            h = ln(T, L + "norm_time_self")                      # :468
+            a = attn(h, h, L + "self_attn_time")                 # :469
+            T = T + a                                            # :470
+            if plant == "double_time_self":
+                T = T + a
+            h = ln(Fr, L + "norm_freq_self")                     # :473-475
             Fr = Fr + attn(h, h, L + "self_attn_freq")
-            tn, fn = ln(T, L + "norm_time_cross"), ln(Fr, L + "norm_freq_cross")
-            T = T + attn(tn, fn, L + "cross_attn_time")
-            Fr = Fr + attn(fn, tn, L + "cross_attn_freq")
-            T = T + ffn(ln(T, L + "norm_time_ffn"), L + "ffn_time")
-            Fr = Fr + ffn(ln(Fr, L + "norm_freq_ffn"), L + "ffn_freq")
+            tn, fn = ln(T, L + "norm_time_cross"), ln(Fr, L + "norm_freq_cross")  # :478-479
+            T = T + attn(tn, fn, L + "cross_attn_time")          # :480-481
+            if plant == "cross_reads_updated_time":
+                tn = ln(T, L + "norm_time_cross")
+            Fr = Fr + attn(fn, tn, L + "cross_attn_freq")        # :484-485
+            T = T + ffn(ln(T, L + "norm_time_ffn"), L + "ffn_time")      # :488-490
+            Fr = Fr + ffn(ln(Fr, L + "norm_freq_ffn"), L + "ffn_freq")   # :493-495
     return T.numpy(), Fr.numpy()
 
 
 def test_cross_transformer_metalnn_matches_torch_composition():
-    """The reference-structured encoder against torch library routines; the same composition with
-    the time self-attention residual added once (the plausible 'fix' of the reference) differs."""
+    """The reference-structured encoder against torch library routines composed in the order of
+    Transformer.swift:467-495 (one residual per sub-block)."""
     cfg = workloads.cross_encoder_metalnn(batch=2, time_len=13, freq_len=21, embed=16, heads=4,
                                           ffn=32, layers=2)
     T, Fq = oracle.cross_transformer_metalnn(cfg["time"], cfg["freq"], cfg["params"],
@@ -288,8 +296,18 @@ def test_cross_transformer_metalnn_matches_torch_composition():
     Tt, Ft = _metalnn_encoder_torch(cfg)
     np.testing.assert_allclose(T, Tt, rtol=1e-9, atol=1e-9)  # both fp64
     np.testing.assert_allclose(Fq, Ft, rtol=1e-9, atol=1e-9)
-    T1, _ = _metalnn_encoder_torch(cfg, double_time_self=False)
-    assert np.max(np.abs(T1 - T)) > 1e-2
+
+
+@pytest.mark.parametrize("plant", ["double_time_self", "cross_reads_updated_time"])
+def test_cross_transformer_metalnn_planted_mistakes_fail(plant):
+    """A mistake planted in the checker moves its result well outside the oracle's agreement
+    (1e-9), so the composition above pins the residual count and the cross-attention inputs."""
+    cfg = workloads.cross_encoder_metalnn(batch=2, time_len=13, freq_len=21, embed=16, heads=4,
+                                          ffn=32, layers=2)
+    T, Fq = oracle.cross_transformer_metalnn(cfg["time"], cfg["freq"], cfg["params"],
+                                             cfg["layers"], cfg["heads"])
+    Tp, Fp = _metalnn_encoder_torch(cfg, plant=plant)
+    assert max(np.max(np.abs(Tp - T)), np.max(np.abs(Fp - Fq))) > 1e-3
 
 
 def test_cross_transformer_metalnn_identity_when_updates_vanish():

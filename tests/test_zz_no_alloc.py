@@ -1,6 +1,7 @@
 """The allocation-free GroupNorm forward (mnn_groupnorm_forward_noalloc) against the allocating
 entry point (mnn_layer_forward) through the C ABI: two calls in a row, the second smaller, each
 bitwise equal to the allocating forward (same kernels) and within the fp32 bar of the oracle."""
+import ctypes
 import sys
 
 import numpy as np
@@ -24,6 +25,12 @@ def noalloc(layer, x, out, stream):
     check(lib().mnn_groupnorm_forward_noalloc(layer.handle, x.handle, out.handle, stream.handle))
 
 
+def allocations():
+    n = ctypes.c_int64()
+    check(lib().mnn_debug_device_allocations(ctypes.byref(n)))
+    return n.value
+
+
 @pytest.mark.parametrize("G,act", [(1, "gelu"), (4, "none")])
 def test_groupnorm_noalloc_matches_forward(G, act):
     dev = nn.AudioDevice(0)
@@ -38,7 +45,10 @@ def test_groupnorm_noalloc_matches_forward(G, act):
         x = (RNG.standard_normal((B, C, L)) * 3 + 0.5).astype(np.float32)
         xt = nn.Tensor.from_numpy(dev, x)
         got, want = nn.Tensor(dev, x.shape), nn.Tensor(dev, x.shape)
-        noalloc(layer, xt, got, stream)
+        before = allocations()
+        noalloc(layer, xt, got, stream)  # first call on a fresh layer: nothing may be reserved
+        stream.sync(60000)
+        assert allocations() == before
         layer.forward(xt, want, stream)
         stream.sync(60000)
         g = got.to_numpy()
@@ -60,4 +70,9 @@ def test_groupnorm_noalloc_rejects_oversize_and_other_layers():
     lin = nn.Linear(dev, 4, 4)
     with pytest.raises(nn.MNNError) as e:
         noalloc(lin, nn.Tensor(dev, (4,)), nn.Tensor(dev, (4,)), stream)
+    assert e.value.name == "MNN_ERR_INVALID_ARGUMENT"
+    gn = nn.GroupNorm(dev, 1, 8)
+    xb = nn.Tensor(dev, (1, 8, 64), dtype="bf16")  # 2-byte elements: would be read as 4-byte
+    with pytest.raises(nn.MNNError) as e:
+        noalloc(gn, xb, nn.Tensor(dev, (1, 8, 64)), stream)
     assert e.value.name == "MNN_ERR_INVALID_ARGUMENT"
