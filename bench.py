@@ -63,10 +63,14 @@ class Markers:
 
 
 # ------------------------------------------------------------------ algorithmic work per step
-def encoder_work():
+def encoder_work(gn=True, gn_l1=None):
     """Algorithmic flops and bytes per chunk of config 4, per encoder kernel and level (the
     kernel-timing names carry the level's channel count, e.g. "enc_conv_f32[c96]").
-    bytes = inputs read once + outputs written once + weights once; flops = 2 M N K."""
+    bytes = inputs read once + outputs written once + weights once; flops = 2 M N K.
+    gn: the one-launch GroupNorm form of levels 2-4 (the split-K finish applies GroupNorm + GELU);
+    gn_l1 (default gn): the first level in one pass; else the two-pass forms."""
+    if gn_l1 is None:
+        gn_l1 = gn
     import ctypes
     from metalaudio_amd import workloads as W
     from metalaudio_amd._lib import lib
@@ -87,15 +91,27 @@ def encoder_work():
         conv_w = 4.0 * (cout * cin * 8 + cout)
         rw_w = 4.0 * (2 * cout * cout + 2 * cout)
         tag = f"[c{cout}]"
-        if cin <= 4 and cout == 48:
+        if cin <= 4 and cout == 48 and gn_l1:
+            # first level in one pass: conv, GroupNorm exchange, GELU, rewrite, GLU (x read once,
+            # block output written)
+            add("enc_l1_oneshot_f32" + tag, conv_flops + rw_flops, x_b + y_b + conv_w + rw_w)
+        elif cin <= 4 and cout == 48:
             # fused first level: statistics pass (conv recomputed, x read) and the fused pass
             # (conv again + rewrite; x read, block output written)
             add("enc_l1_stats_f32" + tag, conv_flops, x_b + conv_w)
             add("enc_l1_fused_f32" + tag, conv_flops + rw_flops, x_b + y_b + conv_w + rw_w)
         else:
             sp, tm, tn = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-            lib().mnn_debug_enc_conv_plan(cin, cout, lo, 1, ctypes.byref(sp), ctypes.byref(tm),
-                                          ctypes.byref(tn))
+            lib().mnn_debug_enc_conv_plan(cin, cout, lo, 1, int(gn), ctypes.byref(sp),
+                                          ctypes.byref(tm), ctypes.byref(tn))
+            if gn:
+                # the conv writes one partial product per K part; the finish sums them and writes
+                # GELU(GroupNorm(y))^T, the rewrite reads it
+                add("enc_conv_f32" + tag, conv_flops, x_b + conv_w + sp.value * y_b)
+                add("enc_conv_reduce_gn_f32" + tag, 0.0, sp.value * y_b + y_b)
+                add("enc_rewrite_f32" + tag, rw_flops, 2 * y_b + rw_w)
+                L = lo
+                continue
             if sp.value > 1:
                 # the conv writes one partial product per K part, the reduce pass sums them
                 add("enc_conv_f32" + tag, conv_flops, x_b + conv_w + sp.value * y_b)
@@ -244,10 +260,73 @@ def cpu_baseline(m, warmup=3, runs=10, budget_s=40.0):
 
 
 # ------------------------------------------------------------------ per-configuration table
-def time_gpu(fn, stream, reps):
+def time_gpu(fn, stream, reps=50, warmup=5):
+    """GPU ms of one call: `warmup` calls, then `reps` calls back to back, each bracketed by two
+    timing marks (HIP events) on the stream; the median of the per-call times."""
+    import ctypes
+    from metalaudio_amd._lib import check, lib
+    for _ in range(warmup):
+        fn()
+    stream.sync()
+    for i in range(reps):
+        check(lib().mnn_debug_stream_mark(stream.handle, 2 * i))
+        fn()
+        check(lib().mnn_debug_stream_mark(stream.handle, 2 * i + 1))
+    stream.sync()
+    ms = ctypes.c_float()
+    ts = []
+    for i in range(reps):
+        check(lib().mnn_debug_stream_mark_elapsed(stream.handle, 2 * i, 2 * i + 1,
+                                                  ctypes.byref(ms)))
+        ts.append(ms.value)
+    return statistics.median(ts)
+
+
+def kernel_table(dev):
+    """{kernel name: (launches, total ms)} of the device's kernel timing (exact names)."""
+    import ctypes
+    from metalaudio_amd._lib import check, lib
+    need = ctypes.c_size_t()
+    check(lib().mnn_debug_kernel_timing_table(dev.handle, None, 0, ctypes.byref(need)))
+    buf = ctypes.create_string_buffer(need.value)
+    check(lib().mnn_debug_kernel_timing_table(dev.handle, buf, need.value, ctypes.byref(need)))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, n, ms = line.rsplit(" ", 2)
+        out[name] = (int(n), float(ms))
+    return out
+
+
+def kernel_breakdown(dev, stream, fn, reps=10, work=None, prec="f32"):
+    """Per-kernel GPU time of one call (kernel-timing pass: every launch bracketed by events on
+    its stream, `reps` calls): microseconds and launches per call, share of the call's kernel
+    time and, where `work` gives the kernel's algorithmic flops or bytes per call, its fraction
+    of the MFMA or HBM peak."""
     fn()
     stream.sync()
-    return timed(fn, stream, reps)
+    dev.reset_kernel_timing()
+    dev.set_kernel_timing(True)
+    for _ in range(reps):
+        fn()
+    stream.sync()
+    dev.set_kernel_timing(False)
+    tab = kernel_table(dev)
+    dev.reset_kernel_timing()
+    total = sum(ms for _, ms in tab.values()) or 1.0
+    out = {}
+    for name, (n, ms) in sorted(tab.items(), key=lambda kv: -kv[1][1]):
+        t = ms / reps * 1e-3  # seconds per call
+        r = {"us": round(t * 1e6, 2), "launches": round(n / reps, 2),
+             "share": round(ms / total, 4)}
+        w = (work or {}).get(name)
+        if w:
+            flops, byts = w
+            if flops:
+                r["mfma_frac"] = round(flops / t / PEAK[prec], 4)
+            if byts:
+                r["hbm_frac"] = round(byts / t / PEAK["hbm"], 4)
+        out[name] = r
+    return out
 
 
 def time_cpu(fn, budget_s=3.0, max_reps=5):
@@ -268,6 +347,7 @@ def decoder_setup(nn, dev):
     length, groups), seeded synthetic weights, inputs and skips."""
     r = np.random.default_rng(1006)
     blocks, skips, outs, params, flops = [], [], [], [], 0.0
+    work = {}
     x = r.standard_normal((1, DEC_LEVELS[0][0], DEC_LEVELS[0][2])).astype(np.float32)
     for cin, cout, L, g in DEC_LEVELS:
         w = (r.standard_normal((2 * cin, cout, 8)) * np.sqrt(2.0 / (2 * cin * 2))).astype(np.float32)
@@ -280,9 +360,25 @@ def decoder_setup(nn, dev):
         skips.append(nn.Tensor.from_numpy(dev, sk))
         outs.append(nn.Tensor(dev, (1, cout, 4 * L)))
         params.append((w, b, gm, bt, g, sk))
-        flops += 2.0 * 2 * cin * cout * 8 * L
+        lf = 2.0 * 2 * cin * cout * 8 * L
+        flops += lf
+        # per kernel family: the matrix-core levels (transposed conv as a GEMM over the unfolded
+        # [input; skip], 2 taps per phase) and the few-channel last level; GroupNorm apply reads
+        # and writes the output once
+        if cout >= 8:
+            _acc(work, "convt_f32_mfma", lf, 0)
+            _acc(work, "convt_pack_f32", 0, 4.0 * 2 * cin * L * (1 + 2))
+        else:
+            _acc(work, "convt_small_f32", lf, 4.0 * (2 * cin * L + cout * 4 * L))
+        _acc(work, "gn_apply_parts", 0, 8.0 * cout * 4 * L)
     return {"blocks": blocks, "skips": skips, "outs": outs, "params": params, "flops": flops,
-            "x": nn.Tensor.from_numpy(dev, x), "x_host": x}
+            "work": work, "x": nn.Tensor.from_numpy(dev, x), "x_host": x}
+
+
+def _acc(work, name, flops, byts):
+    w = work.setdefault(name, [0.0, 0.0])
+    w[0] += flops
+    w[1] += byts
 
 
 def decoder_oracle(oracle, dec):
@@ -304,8 +400,8 @@ def freq_setup(nn, dev):
     """FreqUNetEncoderBlock2D levels down and FreqUNetDecoderBlock2D levels back up (skips of
     the encoder's shapes), seeded synthetic weights and inputs."""
     r = np.random.default_rng(1007)
-    enc = {"blocks": [], "outs": [], "params": [], "flops": 0.0}
-    dec = {"blocks": [], "skips": [], "outs": [], "params": [], "flops": 0.0}
+    enc = {"blocks": [], "outs": [], "params": [], "flops": 0.0, "work": {}}
+    dec = {"blocks": [], "skips": [], "outs": [], "params": [], "flops": 0.0, "work": {}}
     H, W = FREQ_BINS, FREQ_FRAMES
     x = r.standard_normal((1, FREQ_CH[0], H, W)).astype(np.float32)
     dims = []
@@ -322,7 +418,15 @@ def freq_setup(nn, dev):
         enc["blocks"].append(blk)
         enc["outs"].append(nn.Tensor(dev, (1, cout, H // 2, W // 2)))
         enc["params"].append((w, b, gm, bt, g))
-        enc["flops"] += 2.0 * cout * cin * 9 * (H // 2) * (W // 2)
+        lf = 2.0 * cout * cin * 9 * (H // 2) * (W // 2)
+        enc["flops"] += lf
+        ho_wo = (H // 2) * (W // 2)
+        if cin <= 2:  # direct register-window level (also writes the GroupNorm partials)
+            _acc(enc["work"], "conv2d_small_f32", lf, 4.0 * (cin * H * W + cout * ho_wo))
+        else:  # unfolded operand (written once) + matrix-core GEMM
+            _acc(enc["work"], "conv2d_f32_mfma", lf, 0)
+            _acc(enc["work"], "conv2d_unfold_f32", 0, 4.0 * (cin * H * W + 9 * cin * ho_wo))
+        _acc(enc["work"], "gn_apply_parts", 0, 8.0 * cout * ho_wo)
         H, W = H // 2, W // 2
     for i in reversed(range(4)):
         cin, cout = FREQ_CH[i + 1], FREQ_CH[i]
@@ -339,7 +443,15 @@ def freq_setup(nn, dev):
         dec["skips"].append(nn.Tensor.from_numpy(dev, sk))
         dec["outs"].append(nn.Tensor(dev, (1, cout, 2 * h, 2 * w_)))
         dec["params"].append((w, b, gm, bt, g, sk))
-        dec["flops"] += 2.0 * 2 * cin * cout * 9 * h * w_
+        lf = 2.0 * 2 * cin * cout * 9 * h * w_
+        dec["flops"] += lf
+        if cout >= 8:  # tap GEMM over the packed [input; skip], then the gather of the taps
+            _acc(dec["work"], "convt2d_f32_mfma", lf, 0)
+            _acc(dec["work"], "convt_pack_f32", 0, 4.0 * 2 * cin * h * w_ * 2)
+            _acc(dec["work"], "convt2d_gather_f32", 0, 4.0 * (9 * cout * h * w_ + cout * 4 * h * w_))
+        else:
+            _acc(dec["work"], "convt2d_small_f32", lf, 4.0 * (2 * cin * h * w_ + cout * 4 * h * w_))
+        _acc(dec["work"], "gn_apply_parts", 0, 8.0 * cout * 4 * h * w_)
     enc["x"], enc["x_host"] = nn.Tensor.from_numpy(dev, x), x
     xd = r.standard_normal((1, FREQ_CH[-1], H, W)).astype(np.float32)
     dec["x"], dec["x_host"] = nn.Tensor.from_numpy(dev, xd), xd
@@ -367,7 +479,7 @@ def config_table(nn, W, dev, stream, m, cpu=True):
         import oracle
     out = {}
 
-    def row(name, gpu_ms, flops=None, byts=None, prec="f32", cpu_ms=None):
+    def row(name, gpu_ms, flops=None, byts=None, prec="f32", cpu_ms=None, kernels=None):
         r = {"gpu_ms": round(gpu_ms, 4)}
         if flops:
             r["tflops"] = round(flops / gpu_ms / 1e9, 2)
@@ -377,6 +489,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
             r["hbm_frac"] = round(byts / (gpu_ms * 1e-3) / PEAK["hbm"], 4)
         if cpu_ms is not None:
             r["cpu_ms"] = round(cpu_ms, 2)
+        if kernels is not None:
+            r["kernels"] = kernels
         out[name] = r
 
     # config 1: Conv1D 2->48 k8 s4 -> GroupNorm(1) -> GELU (HBM-bound; bytes = x + y)
@@ -400,8 +514,11 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     cpu1 = time_cpu(lambda: oracle.gelu_layer(oracle.group_norm(oracle.conv1d(
         c1["x"], c1["conv_w"], c1["conv_b"], stride=4, dtype=np.float32), 1, c1["gn_w"],
         c1["gn_b"], dtype=np.float32), dtype=np.float32)) if cpu else None
-    row("1_conv_gn_gelu", time_gpu(f1, stream, 20), flops=2.0 * 48 * 11024 * 16,
-        byts=4.0 * (2 * 44100 + 48 * 11024), cpu_ms=cpu1)
+    b1 = 4.0 * (2 * 44100 + 48 * 11024)
+    row("1_conv_gn_gelu", time_gpu(f1, stream), flops=2.0 * 48 * 11024 * 16, byts=b1,
+        cpu_ms=cpu1, kernels=kernel_breakdown(dev, stream, f1, work={
+            "conv_gn_oneshot_f32": (0, b1), "conv_gn_stats_f32": (0, 4.0 * 2 * 44100),
+            "conv_gn_apply_f32": (0, b1)}))
 
     # config 2: Linear 512 -> 2048 on [2048, 512] + LayerNorm(2048), fp32 and bf16 operands
     c2 = W.config2()
@@ -423,14 +540,16 @@ def config_table(nn, W, dev, stream, m, cpu=True):
         def f2():
             lin.forward(xin, y2, stream)
             ln.forward(y2, z2, stream)
-        row(f"2_linear_ln_{prec}", time_gpu(f2, stream, 20), flops=2.0 * 2048 * 2048 * 512,
-            prec=prec, cpu_ms=cpu2 if prec == "f32" else None)
-        # the Linear alone: fp32 on the matrix cores; bf16 (X and W bf16, Y fp32: 2 + 2 + 16 MB)
-        # bound by HBM
+        # the Linear: fp32 on the matrix cores; bf16 (X and W bf16, Y fp32: 2 + 2 + 16 MB)
+        # bound by HBM; the LayerNorm reads and writes 16 MB
         es = 2 if prec == "bf16" else 4
-        row(f"2_linear_{prec}", time_gpu(lambda: lin.forward(xin, y2, stream), stream, 20),
-            flops=2.0 * 2048 * 2048 * 512, prec=prec,
-            byts=es * (2048 * 512 * 2) + 4.0 * 2048 * 2048)
+        g2 = (2.0 * 2048 * 2048 * 512, es * (2048 * 512 * 2) + 4.0 * 2048 * 2048)
+        w2 = {f"gemm_{prec}_mfma_nk": g2, "layernorm_f32": (0, 8.0 * 2048 * 2048)}
+        row(f"2_linear_ln_{prec}", time_gpu(f2, stream), flops=2.0 * 2048 * 2048 * 512,
+            prec=prec, cpu_ms=cpu2 if prec == "f32" else None,
+            kernels=kernel_breakdown(dev, stream, f2, work=w2, prec=prec))
+        row(f"2_linear_{prec}", time_gpu(lambda: lin.forward(xin, y2, stream), stream),
+            flops=g2[0], prec=prec, byts=g2[1])
 
     # config 3: pre-norm MHSA + FFN layer, S 2048, E 512
     c3 = W.config3()
@@ -442,16 +561,16 @@ def config_table(nn, W, dev, stream, m, cpu=True):
                                                      dtype=np.float32)) if cpu else None
     S, E = 2048, 512
     f3 = 2.0 * S * E * 3 * E + 4.0 * S * S * E + 2.0 * S * E * E + 4.0 * S * E * 2048
-    row("3_transformer_layer", time_gpu(lambda: tl.forward(x3, y3, stream), stream, 10),
+    row("3_transformer_layer", time_gpu(lambda: tl.forward(x3, y3, stream), stream),
         flops=f3, cpu_ms=cpu3)
 
     # configs 4 and 5 (the headline pair)
     enc = encoder_work()
     f4 = sum(v[0] for v in enc.values())
-    row("4_encoder_b1", time_gpu(lambda: m["seq"].forward(m["chunks"][0], stream), stream, 10),
+    row("4_encoder_b1", time_gpu(lambda: m["seq"].forward(m["chunks"][0], stream), stream),
         flops=f4)
     f5 = sum(v[0] for v in transformer_work(W.T5_BATCH).values())
-    row("5_transformer_b4", time_gpu(lambda: run_transformer(m, stream), stream, 5), flops=f5)
+    row("5_transformer_b4", time_gpu(lambda: run_transformer(m, stream), stream), flops=f5)
     # time-branch decoder (next row of the hot path): the four UNetDecoderBlock levels at the
     # config-4 lengths of a padded chunk (344064 samples -> 86016 / 21504 / 5376 / 1344), with
     # synthetic inputs and skips of those shapes
@@ -463,7 +582,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
             blk.forward(y, sk, out, stream)
             y = out
     cpu6 = time_cpu(lambda: decoder_oracle(oracle, dec), max_reps=1) if cpu else None
-    row("6_time_decoder_b1", time_gpu(f6, stream, 10), flops=dec["flops"], cpu_ms=cpu6)
+    row("6_time_decoder_b1", time_gpu(f6, stream), flops=dec["flops"], cpu_ms=cpu6,
+        kernels=kernel_breakdown(dev, stream, f6, work=dec["work"]))
     # frequency branch (next rows): the four 2-D encoder levels and the four decoder levels of
     # the reference's HTDemucs at one chunk's spectrogram (synthetic inputs and skips)
     fenc, fdec = freq_setup(nn, dev)
@@ -481,8 +601,10 @@ def config_table(nn, W, dev, stream, m, cpu=True):
             y = out
     cpu7 = time_cpu(lambda: freq_encoder_oracle(oracle, fenc), max_reps=1) if cpu else None
     cpu8 = time_cpu(lambda: freq_decoder_oracle(oracle, fdec), max_reps=1) if cpu else None
-    row("7_freq_encoder_b1", time_gpu(f7, stream, 10), flops=fenc["flops"], cpu_ms=cpu7)
-    row("8_freq_decoder_b1", time_gpu(f8, stream, 10), flops=fdec["flops"], cpu_ms=cpu8)
+    row("7_freq_encoder_b1", time_gpu(f7, stream), flops=fenc["flops"], cpu_ms=cpu7,
+        kernels=kernel_breakdown(dev, stream, f7, work=fenc["work"]))
+    row("8_freq_decoder_b1", time_gpu(f8, stream), flops=fdec["flops"], cpu_ms=cpu8,
+        kernels=kernel_breakdown(dev, stream, f8, work=fdec["work"]))
     # STFT / iSTFT of one stereo 7.8 s chunk at HTDemucs' nfft 4096 / hop 1024 (bin-major
     # spectrogram, as the frequency branch consumes it); bytes = signal read + spectra written
     # (forward), spectra read + frames written and re-read + signal written (inverse)
@@ -507,9 +629,15 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     cpu9 = time_cpu(lambda: odsp.stft(xs, 4096, 1024, dtype=np.float32)) if cpu else None
     X9 = odsp.stft(xs, 4096, 1024) if cpu else None
     cpu10 = time_cpu(lambda: odsp.istft(X9, 4096, 1024, dtype=np.float32)) if cpu else None
-    row("9_stft_b1", time_gpu(fwd, stream, 20), byts=4.0 * xs.size + spec_b, cpu_ms=cpu9)
-    row("10_istft_b1", time_gpu(inv, stream, 20),
-        byts=spec_b + 2 * 4.0 * 2 * nf * 4096 + 4.0 * 2 * plan.output_length(nf), cpu_ms=cpu10)
+    b9 = 4.0 * xs.size + spec_b
+    row("9_stft_b1", time_gpu(fwd, stream), byts=b9, cpu_ms=cpu9,
+        kernels=kernel_breakdown(dev, stream, fwd, work={"stft_forward_f32": (0, b9)}))
+    frames_b = 4.0 * 2 * nf * 4096
+    sig_b = 4.0 * 2 * plan.output_length(nf)
+    row("10_istft_b1", time_gpu(inv, stream), byts=spec_b + 2 * frames_b + sig_b, cpu_ms=cpu10,
+        kernels=kernel_breakdown(dev, stream, inv, work={
+            "istft_frames_f32": (0, spec_b + frames_b),
+            "istft_overlap_add_f32": (0, frames_b + sig_b)}))
     # long-audio driver: 60 s of stereo audio through the reference's default time-domain
     # HTDemucs (5 levels 48..768, k 8, s 4, 4 stems) in the guide's 30 s segments with 2 s
     # overlap (HTDEMUCS_GUIDE.md:170-191); synthetic weights and audio
@@ -549,8 +677,8 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     seg_cpu = r11.uniform(-1, 1, 2 * 44100 * 10).astype(np.float32)
     cpu11 = time_cpu(lambda: osep.separate_time(seg_cpu, P11, cfg11, dtype=np.float32),
                      max_reps=1) * 6.0 if cpu else None
-    g11 = time_gpu(f11, stream, 3)
-    row("11_long_audio_60s", g11, cpu_ms=cpu11)
+    g11 = time_gpu(f11, stream)
+    row("11_long_audio_60s", g11, cpu_ms=cpu11, kernels=kernel_breakdown(dev, stream, f11, reps=3))
     out["11_long_audio_60s"]["x_realtime"] = round(60e3 / g11, 1)
     t5 = nn.Tensor.from_numpy(dev, m["c5"]["time"][:1])
     q5 = nn.Tensor.from_numpy(dev, m["c5"]["freq"][:1])
@@ -618,7 +746,7 @@ def main():
             sys.exit(1)
         text = buf.value.decode()
         Path(args.profile_step).write_text(text)
-        work = encoder_work()
+        work = encoder_work("enc_conv_reduce_gn" in text, "enc_l1_oneshot" in text)
         work = {k: [v[0] * 4, v[1] * 4] for k, v in work.items()}
         work.update(transformer_work(W.T5_BATCH))
         Path(args.profile_step).with_suffix(".work.json").write_text(json.dumps(work))
@@ -644,12 +772,16 @@ def main():
     fams = ["attn_fwd", "gemm_f32_mfma_nk", "gemm_f32_mfma_kn", "gemm_f32_mfma_conv",
             "gemm_f32_simple", "conv1d_direct", "layernorm", "ln_row_parts_f32", "ln_fold_f32",
             "gn_stats", "gn_finalize", "gn_apply", "copy_bytes", "glu_f32", "gelu_f32"]
-    enc_kernels = list(encoder_work())  # per level, e.g. enc_conv_f32[c96]
+    # per level, e.g. enc_conv_f32[c96]; the forms that ran decide the accounting
+    enc_names = sorted(set(encoder_work(True)) | set(encoder_work(False)))
     ktime = {}
-    for f in fams + enc_kernels:
+    for f in fams + enc_names:
         n, ms = dev.kernel_timing(f)
         if n:
             ktime[f] = (n, ms)
+    ew = encoder_work(any(k.startswith("enc_conv_reduce_gn") for k in ktime),
+                      any(k.startswith("enc_l1_oneshot") for k in ktime))
+    enc_kernels = list(ew)
     log("kernel ms/step: " + ", ".join(f"{k}={v[1] / args.steps:.3f} ({v[0] // args.steps})"
                                         for k, v in ktime.items()))
 
@@ -659,8 +791,7 @@ def main():
     log(f"ms/step {ms_step:.3f}; encoder {t_enc:.3f} ms/chunk; transformer b4 {t_tr:.3f} ms")
 
     # roofline of the dominant family
-    work = encoder_work()
-    work = {k: [v[0] * 4, v[1] * 4] for k, v in work.items()}  # 4 chunks per step
+    work = {k: [v[0] * 4, v[1] * 4] for k, v in ew.items()}  # 4 chunks per step
     for k, v in transformer_work(W.T5_BATCH).items():
         work[k] = v
     fam_key = {"attn_fwd": "attn_fwd_f32"}
@@ -687,7 +818,6 @@ def main():
     # the encoder as a whole (all its kernels, one chunk's algorithmic flops)
     enc_ms = sum(ktime[k][1] for k in enc_kernels if k in ktime) / args.steps
     if enc_ms > 0:
-        ew = encoder_work()
         ef = 4 * sum(ew[k][0] for k in enc_kernels)  # 4 chunks per step
         rows["encoder_all_levels"] = {
             "bound": "mfma", "achieved": round(ef / (enc_ms / 1e3) / 1e12, 2), "peak": 157.3,

@@ -23,10 +23,12 @@ mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, con
                                 float* d);
 
 /* The plan the encoder's implicit-GEMM conv launcher picks for a level (input channels, output
- * channels, output length, batch): K split count and output tile. bench.py uses it to account the
- * split-K reduce pass's bytes. */
+ * channels, output length, batch; gn_finish: the plan of the GroupNorm split-K finish, which
+ * always splits K): K split count and output tile. bench.py uses it to account the split-K
+ * finish's bytes. */
 mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t out_length,
-                                   int batch, int* splits, int* tile_m, int* tile_n);
+                                   int batch, int gn_finish, int* splits, int* tile_m,
+                                   int* tile_n);
 
 /* Launch log, a profiling aid: while enabled, every kernel launch of the device appends a line
  * "name grid.x grid.y grid.z block.x" (name as in mnn_device_kernel_timing). Enabling clears the
@@ -42,6 +44,20 @@ mnn_status mnn_debug_launch_log(mnn_device dev, char* buf, size_t cap, size_t* n
  * not find every partial on its first look take the self-computing path, which the tests use to
  * check it. *previous (may be null) receives the old bound; the default is 65536. */
 mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previous);
+
+/* Every entry of the device's kernel timing (mnn_device_set_kernel_timing), one line each:
+ * "name launches total_ms", names exact (mnn_device_kernel_timing matches substrings). Copied
+ * NUL-terminated into buf (cap bytes); *needed = the size required; buf NULL only sizes it,
+ * MNN_ERR_BUFFER_SIZE_MISMATCH when cap is too small. */
+mnn_status mnn_debug_kernel_timing_table(mnn_device dev, char* buf, size_t cap, size_t* needed);
+
+/* Timing marks: mnn_debug_stream_mark records timing event `index` (0..65535; events are made on
+ * first use and kept until the stream is destroyed) on the stream; mnn_debug_stream_mark_elapsed
+ * waits for mark `to` and gives the milliseconds between marks `from` and `to`. bench.py brackets
+ * each timed call with two marks, so per-call GPU times need no host synchronisation between the
+ * calls. */
+mnn_status mnn_debug_stream_mark(mnn_stream s, int index);
+mnn_status mnn_debug_stream_mark_elapsed(mnn_stream s, int from, int to, float* ms);
 
 /* Number of device allocations (hipMalloc) the library has made in this process: tensors, layer
  * weights and workspaces. The tests read it around a call to check that the call allocated

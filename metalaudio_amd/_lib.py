@@ -222,11 +222,16 @@ SIGNATURES = {
     "mnn_sequential_layer_count": (C.c_int, [P, IP]),
     "mnn_sequential_layer_at": (C.c_int, [P, C.c_int, PP]),
     "mnn_debug_mfma_probe": (C.c_int, [P, C.c_int, FP, FP, FP]),
-    "mnn_debug_enc_conv_plan": (C.c_int, [C.c_int, C.c_int, C.c_int64, C.c_int, IP, IP, IP]),
+    "mnn_debug_enc_conv_plan": (C.c_int, [C.c_int, C.c_int, C.c_int64, C.c_int, C.c_int, IP, IP,
+                                          IP]),
     "mnn_debug_set_launch_log": (C.c_int, [P, C.c_int]),
     "mnn_debug_launch_log": (C.c_int, [P, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "mnn_debug_set_grid_spin_limit": (C.c_int, [P, C.c_int, C.POINTER(C.c_int)]),
     "mnn_debug_device_allocations": (C.c_int, [I64P]),
+    "mnn_debug_stream_mark": (C.c_int, [P, C.c_int]),
+    "mnn_debug_kernel_timing_table": (C.c_int, [P, C.c_char_p, C.c_size_t,
+                                                C.POINTER(C.c_size_t)]),
+    "mnn_debug_stream_mark_elapsed": (C.c_int, [P, C.c_int, C.c_int, C.POINTER(C.c_float)]),
 }
 
 _lib = None

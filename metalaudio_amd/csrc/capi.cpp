@@ -289,6 +289,12 @@ mnn_status mnn_stream_sync(mnn_stream st, int timeout_ms) {
   });
 }
 
+namespace {
+// Timing marks of mnn_debug_stream_mark, per stream handle.
+std::mutex g_marks_mu;
+std::map<const Stream*, std::vector<hipEvent_t>> g_marks;
+}  // namespace
+
 mnn_status mnn_stream_destroy(mnn_stream st) {
   return guard([&] {
     if (!st) return;
@@ -297,6 +303,14 @@ mnn_status mnn_stream_destroy(mnn_stream st) {
     if (s->owned && s->s) {
       (void)hipStreamSynchronize(s->s);
       (void)hipStreamDestroy(s->s);
+    }
+    {
+      std::lock_guard<std::mutex> lk(g_marks_mu);
+      auto it = g_marks.find(s);
+      if (it != g_marks.end()) {
+        for (hipEvent_t e : it->second) (void)hipEventDestroy(e);
+        g_marks.erase(it);
+      }
     }
     delete s;
   });
@@ -1147,12 +1161,14 @@ mnn_status mnn_debug_mfma_probe(mnn_device dev, int variant, const float* a, con
 }
 
 mnn_status mnn_debug_enc_conv_plan(int in_channels, int out_channels, int64_t out_length,
-                                   int batch, int* splits, int* tile_m, int* tile_n) {
+                                   int batch, int gn_finish, int* splits, int* tile_m,
+                                   int* tile_n) {
   return guard([&] {
     MNN_REQUIRE(splits && tile_m && tile_n && in_channels > 0 && out_channels > 0 &&
                     out_length > 0 && batch > 0,
                 MNN_ERR_INVALID_ARGUMENT, "invalid argument");
-    k::enc_conv_plan_info(in_channels, out_channels, out_length, batch, splits, tile_m, tile_n);
+    k::enc_conv_plan_info(in_channels, out_channels, out_length, batch, gn_finish != 0, splits,
+                          tile_m, tile_n);
   });
 }
 
@@ -1171,6 +1187,59 @@ mnn_status mnn_debug_set_grid_spin_limit(mnn_device dev, int polls, int* previou
     Device* d = D(dev);
     const int old = d->grid_spin_limit.exchange(polls);
     if (previous) *previous = old;
+  });
+}
+
+mnn_status mnn_debug_kernel_timing_table(mnn_device dev, char* buf, size_t cap, size_t* needed) {
+  return guard([&] {
+    MNN_REQUIRE(needed, MNN_ERR_INVALID_ARGUMENT, "needed is required");
+    Device* d = D(dev);
+    d->make_current();
+    d->resolve_timers();
+    std::ostringstream os;
+    {
+      std::lock_guard<std::mutex> lk(d->timing_mu);
+      for (auto& kv : d->stats) os << kv.first << ' ' << kv.second.first << ' ' << kv.second.second << '\n';
+    }
+    const std::string text = os.str();
+    *needed = text.size() + 1;
+    if (!buf) return;
+    MNN_REQUIRE(cap >= text.size() + 1, MNN_ERR_BUFFER_SIZE_MISMATCH,
+                "kernel timing table needs " << text.size() + 1 << " bytes");
+    std::memcpy(buf, text.c_str(), text.size() + 1);
+  });
+}
+
+mnn_status mnn_debug_stream_mark(mnn_stream st, int index) {
+  return guard([&] {
+    MNN_REQUIRE(st, MNN_ERR_INVALID_ARGUMENT, "a stream is required");
+    MNN_REQUIRE(index >= 0 && index < 65536, MNN_ERR_INVALID_ARGUMENT,
+                "mark index must be in [0, 65536), got " << index);
+    Stream* s = S(st);
+    s->dev->make_current();
+    std::lock_guard<std::mutex> lk(g_marks_mu);
+    auto& v = g_marks[s];
+    while ((int)v.size() <= index) {
+      hipEvent_t e;
+      HIP_CHECK(hipEventCreate(&e));
+      v.push_back(e);
+    }
+    HIP_CHECK(hipEventRecord(v[index], s->s));
+  });
+}
+
+mnn_status mnn_debug_stream_mark_elapsed(mnn_stream st, int from, int to, float* ms) {
+  return guard([&] {
+    MNN_REQUIRE(st && ms, MNN_ERR_INVALID_ARGUMENT, "a stream and an output are required");
+    Stream* s = S(st);
+    s->dev->make_current();
+    std::lock_guard<std::mutex> lk(g_marks_mu);
+    auto it = g_marks.find(s);
+    MNN_REQUIRE(it != g_marks.end() && from >= 0 && to >= 0 && from < (int)it->second.size() &&
+                    to < (int)it->second.size(),
+                MNN_ERR_INVALID_ARGUMENT, "mark " << from << " or " << to << " never recorded");
+    HIP_CHECK(hipEventSynchronize(it->second[to]));
+    HIP_CHECK(hipEventElapsedTime(ms, it->second[from], it->second[to]));
   });
 }
 

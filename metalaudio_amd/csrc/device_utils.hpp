@@ -457,5 +457,220 @@ __device__ __forceinline__ float2 gn1_merge_one_round(const float* __restrict__ 
   return make_float2((float)mean, rstd);
 }
 
+// ---------------------------------------------------------------- grid-wide statistics exchange
+// One-launch GroupNorm(1): every workgroup publishes the (mean, M2) of its tile, waits until it
+// has seen every partial of its batch, and merges them itself. No cache maintenance is used (an
+// agent-scope acquire fence per wave and a release fence per workgroup cost more than the rest of
+// such kernels): a partial is two 64-bit words (kTileTag << 32 | mean bits), (kTileTag << 32 |
+// M2 bits), each stored and loaded as one relaxed device-scope atomic, so a reader sees either a
+// whole published word or a cleared one. The count of a partial follows from the geometry and is
+// not exchanged.
+//
+// Exchange buffer layout (64-bit words): word 0 (low half) counts the workgroups out of the
+// launch; partial slots start at word 8, two words per partial, batch b's partial v at slot
+// b * nparts + v. The buffer is zero before a launch; the last workgroup out clears the slots and
+// the count, so the next launch finds it zero again. Launches that share a buffer must not
+// overlap. The host launches these kernels only when the whole grid is resident at once; each
+// wait is still bounded (xch_collect), and a workgroup that gives up computes every partial
+// itself by the same code as their owners (so the same bits).
+constexpr unsigned kTileTag = 1u;  // high half of a published word (cleared words read 0)
+
+__device__ __forceinline__ void put_tagged(unsigned long long* s, float lo) {
+  __hip_atomic_store(s, ((unsigned long long)kTileTag << 32) | __float_as_uint(lo),
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the nparts <= NT * PER partials at `slots` (NT threads, each its share) into sp[] until
+// all are published; returns true when spin_limit polls passed without that (the caller then
+// computes the partials itself). Every thread returns the same value. A thread's PER pairs of
+// words are loaded together (clamped addresses, straight-line code), so one poll costs one round
+// trip to the coherence point, not PER.
+template <int NT, int PER>
+__device__ __forceinline__ bool xch_collect(const unsigned long long* slots, int nparts,
+                                            float2* sp, int spin_limit) {
+  for (int polls = 0;; ++polls) {
+    unsigned long long a[PER], c[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int v = min((int)threadIdx.x + i * NT, nparts - 1);
+      a[i] = __hip_atomic_load(slots + 2 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      c[i] = __hip_atomic_load(slots + 2 * v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int v = (int)threadIdx.x + i * NT;
+      if (v < nparts) {
+        ok = ok && (unsigned)(a[i] >> 32) == kTileTag && (unsigned)(c[i] >> 32) == kTileTag;
+        sp[v] = make_float2(__uint_as_float((unsigned)a[i]), __uint_as_float((unsigned)c[i]));
+      }
+    }
+    if (!__syncthreads_or(!ok)) return false;
+    if (polls >= spin_limit) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// Merge of the collected (mean, M2) partials in a fixed order, in every wave of the caller (no
+// barrier): fp64 sums over the partials by lane, then over the wave; count(v) is partial v's
+// element count and ntot their sum. Every lane of every wave returns the same bits.
+template <class CountFn>
+__device__ __forceinline__ float2 xch_merge(const float2* sp, int nparts, CountFn count,
+                                            double ntot, float eps) {
+  double sm = 0.0, sm2 = 0.0, sq = 0.0;
+  for (int v = threadIdx.x & 63; v < nparts; v += 64) {
+    const double c = count(v);
+    const double m = sp[v].x;
+    sm += c * m;
+    sm2 += c * m * m;
+    sq += (double)sp[v].y;
+  }
+  sm = wave_sum_dpp_d(sm);
+  sm2 = wave_sum_dpp_d(sm2);
+  sq = wave_sum_dpp_d(sq);
+  const double mean = sm / ntot;
+  const double var = fmax(sq + (sm2 - sm * mean), 0.0) / ntot;
+  float rstd = (float)(1.0 / sqrt(var + (double)eps));
+  if (!isfinite(rstd)) rstd = 0.f;
+  return make_float2((float)mean, rstd);
+}
+
+// Counts the calling workgroup out of the launch (its reads of the slots are done); the last one
+// out clears the 2 * total slot words and the count. s_last: an int of LDS.
+template <int NT>
+__device__ __forceinline__ void xch_count_out(unsigned long long* xch, unsigned total,
+                                              int* s_last) {
+  unsigned* ctl = reinterpret_cast<unsigned*>(xch);
+  if (threadIdx.x == 0)
+    *s_last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              total - 1;
+  lds_barrier();
+  if (*s_last) {
+    unsigned long long* all = xch + 8;
+    for (int i = threadIdx.x; i < 2 * (int)total; i += NT)
+      __hip_atomic_store(all + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------- exchange with one merger
+// A variant of the exchange above for grids of several hundred workgroups. There every waiting
+// workgroup polling every partial makes traffic at the coherence point that grows with the square
+// of the grid (each 8-byte device-scope load is a transaction of its own), and any count kept by
+// read-modify-writes on one word serialises there (tens of ns each). Here workgroup 0 of each
+// batch is the merger: every workgroup publishes its partial (two tagged words, no wait, no
+// read-modify-write); the merger polls the batch's partials, merges them and publishes one result
+// pair (mean, rstd), which is all the others poll.
+//
+// Words carry a per-batch epoch tag instead of being cleared: every workgroup reads the batch's
+// epoch E at its start and tags its words (E mod 2^31) + 1. Once the merger has seen every
+// partial, every workgroup has read E, so it advances the epoch then. Stale words of earlier
+// launches (graph replays included) never carry the current tag, and no workgroup counts out.
+//
+// Termination: every workgroup publishes before it waits, and the others' waits are bounded
+// (a workgroup whose wait runs out computes every partial itself, by the same code as their
+// owners, so the same bits). So the merger's wait, which is not bounded (it must see every
+// partial before it may advance the epoch), ends once every workgroup has run: if the grid is not
+// resident at once, the bounded waiters finish and free their slots for the rest.
+//
+// Buffer layout (64-bit words): batch b's epoch at word 4 b (low half), its result at 4 b + 2
+// (tag | mean bits) and 4 b + 3 (tag | rstd bits); partial slots from word 4 * kXmMaxBatch, two
+// per partial, batch b's partial v at slot b * nparts + v. The buffer is zero before the first
+// launch. Launches that share a buffer must not overlap.
+constexpr int kXmMaxBatch = 64;
+
+__device__ __forceinline__ unsigned long long* xm_batch(unsigned long long* xch, int b) {
+  return xch + 4 * b;
+}
+__device__ __forceinline__ unsigned long long* xm_slots(unsigned long long* xch, int b,
+                                                        int nparts) {
+  return xch + 4 * kXmMaxBatch + 2 * (int64_t)b * nparts;
+}
+
+// The tag of this launch's words for batch b.
+__device__ __forceinline__ unsigned xm_tag(unsigned long long* xch, int b) {
+  const unsigned e = (unsigned)__hip_atomic_load(xm_batch(xch, b), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+  return (e & 0x7fffffffu) + 1u;
+}
+
+__device__ __forceinline__ void put_tag(unsigned long long* s, unsigned tag, float lo) {
+  __hip_atomic_store(s, ((unsigned long long)tag << 32) | __float_as_uint(lo), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Publishes partial v of batch b (thread 0).
+__device__ __forceinline__ void xm_put(unsigned long long* xch, int b, int nparts, int v,
+                                       unsigned tag, float mean, float m2) {
+  unsigned long long* sl = xm_slots(xch, b, nparts) + 2 * v;
+  put_tag(sl, tag, mean);
+  put_tag(sl + 1, tag, m2);
+}
+
+// The merger: polls the nparts partials of batch b into sp[] (NT threads, PER per thread, loaded
+// together) until every one carries this launch's tag.
+template <int NT, int PER>
+__device__ __forceinline__ void xm_collect(unsigned long long* xch, int b, int nparts,
+                                           unsigned tag, float2* sp) {
+  const unsigned long long* slots = xm_slots(xch, b, nparts);
+  for (;;) {
+    bool ok = true;
+    for (int v0 = 0; v0 < nparts; v0 += NT * PER) {
+      unsigned long long a[PER], c[PER];
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int v = min(v0 + (int)threadIdx.x + i * NT, nparts - 1);
+        a[i] = __hip_atomic_load(slots + 2 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        c[i] = __hip_atomic_load(slots + 2 * v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int v = v0 + (int)threadIdx.x + i * NT;
+        if (v < nparts) {
+          ok = ok && (unsigned)(a[i] >> 32) == tag && (unsigned)(c[i] >> 32) == tag;
+          sp[v] = make_float2(__uint_as_float((unsigned)a[i]), __uint_as_float((unsigned)c[i]));
+        }
+      }
+    }
+    if (!__syncthreads_or(!ok)) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
+// The merger, with the merged result: publishes it and advances the batch's epoch (thread 0).
+__device__ __forceinline__ void xm_publish(unsigned long long* xch, int b, unsigned tag,
+                                           float2 mr) {
+  unsigned long long* w = xm_batch(xch, b);
+  put_tag(w + 2, tag, mr.x);
+  put_tag(w + 3, tag, mr.y);
+  __hip_atomic_store(reinterpret_cast<unsigned*>(w), tag & 0x7fffffffu, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every other workgroup: polls batch b's result pair (one thread, broadcast through `s_res`)
+// until it carries this launch's tag; false when spin_limit polls passed without it.
+__device__ __forceinline__ bool xm_wait(unsigned long long* xch, int b, unsigned tag,
+                                        int spin_limit, float2* s_res) {
+  const unsigned long long* w = xm_batch(xch, b);
+  if (threadIdx.x == 0) {
+    float2 r = make_float2(0.f, -1.f);  // rstd < 0: not seen
+    for (int polls = 0;; ++polls) {
+      const unsigned long long m = __hip_atomic_load(w + 2, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long q = __hip_atomic_load(w + 3, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+      if ((unsigned)(m >> 32) == tag && (unsigned)(q >> 32) == tag) {
+        r = make_float2(__uint_as_float((unsigned)m), __uint_as_float((unsigned)q));
+        break;
+      }
+      if (polls >= spin_limit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    *s_res = r;
+  }
+  lds_barrier();
+  return s_res->y >= 0.f;
+}
+
 }  // namespace dev
 }  // namespace mnn

@@ -367,34 +367,13 @@ __global__ __launch_bounds__(kThreads) void conv_gn_apply_kernel(
 
 // Both passes in one launch. Each workgroup computes a tile of COB channels x 256 positions of
 // the convolution into registers (SPLIT x 256 threads, COB / SPLIT channels each) and publishes
-// the tile's statistics partial; it then collects every partial of its batch, merges them and
-// writes the normalised output from the registers it kept.
-//
-// The exchange uses no cache maintenance (an acquire fence in every wave and a release fence per
-// workgroup cost more than the rest of the kernel at this size): a partial is two 64-bit words,
-// (kTileTag << 32 | mean bits) and (kTileTag << 32 | M2 bits), each stored and loaded as one
-// relaxed device-scope atomic, so a reader sees either a whole published word or a cleared one,
-// and polls until every word is published. The count of a partial is fixed by the geometry (COB x
-// the tile's valid positions) and is not exchanged.
-//
-// xch layout (64-bit words): word 0 = workgroups out of this launch (low half); slots from word 8,
-// two words per partial, partial (b, v) at slot b * nparts + v. All zero before a launch: the
-// last workgroup out (the count says which) clears the slots and the count, when every workgroup
-// has finished reading them, so the next launch starts from zero again.
-//
-// The host launches this form only when the whole grid can be resident at once. The wait is
-// bounded all the same: a workgroup that has polled spin_limit times without seeing every partial
-// computes every partial of its batch itself (the same code on the same inputs as their owners,
-// so the same bits) and merges those, so each workgroup ends with the same result whatever the
-// scheduling. Launches that share `xch` must not overlap.
+// the tile's statistics partial; it then collects every partial of its batch through the
+// grid-wide exchange of device_utils.hpp (tagged words, bounded wait), merges them and writes the
+// normalised output from the registers it kept. A workgroup whose wait runs out computes every
+// partial of its batch itself (the same code on the same inputs as their owners, so the same
+// bits), so each workgroup ends with the same result whatever the scheduling.
 constexpr int kOneMaxParts = 1024;  // partials per batch (LDS: 8 bytes each)
 constexpr int kOneMaxSlots = 4096;  // partials over all batches
-constexpr unsigned kTileTag = 1u;   // high half of a published word (cleared words read 0)
-
-__device__ __forceinline__ void put_tagged(unsigned long long* s, float lo) {
-  __hip_atomic_store(s, ((unsigned long long)kTileTag << 32) | __float_as_uint(lo),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // (mean, M2) of one tile of n values spread over NW waves, two passes over the registers: the
 // mean from a block sum, then M2 about it. Every thread returns the same bits. red: 2 * NW floats
@@ -444,7 +423,6 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
   const bool valid = t < p.Lout;
   const int nparts = gridDim.x * gridDim.y;
   const float* xb = x + (int64_t)b * p.Cin * p.Lin;
-  unsigned* ctl = reinterpret_cast<unsigned*>(xch);
   unsigned long long* slots = xch + 8 + 2 * (int64_t)b * nparts;
   Stage st;
   st.fetch(w, cob0, bias, gamma, beta, 0.f, 1.f, 0.f);
@@ -477,24 +455,7 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
     }
   }
   // collect: every thread polls its share of the partials until all are published
-  bool late = false;
-  for (int polls = 0;; ++polls) {
-    bool ok = true;
-    for (int v = threadIdx.x; v < nparts; v += NT) {
-      const unsigned long long a =
-          __hip_atomic_load(slots + 2 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const unsigned long long c =
-          __hip_atomic_load(slots + 2 * v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      ok = ok && (unsigned)(a >> 32) == kTileTag && (unsigned)(c >> 32) == kTileTag;
-      sp[v] = make_float2(__uint_as_float((unsigned)a), __uint_as_float((unsigned)c));
-    }
-    if (!__syncthreads_or(!ok)) break;
-    if (polls >= spin_limit) {
-      late = true;
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
+  const bool late = xch_collect<NT, (kOneMaxParts + NT - 1) / NT>(slots, nparts, sp, spin_limit);
   if (late) {
     // this workgroup never saw its own partial published: let the store land before the
     // workgroup can count out (the last one out clears the slots)
@@ -520,25 +481,10 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
     }
     lds_barrier();
   }
-  // merge in a fixed order, in every wave (no barrier): fp64 sums over the partials by lane, then
-  // over the wave; the total count is Cout x Lout
-  double sm = 0.0, sm2 = 0.0, sq = 0.0;
-  for (int v = threadIdx.x & 63; v < nparts; v += 64) {
-    const double c = tile_count(v % gridDim.x);
-    const double m = sp[v].x;
-    sm += c * m;
-    sm2 += c * m * m;
-    sq += (double)sp[v].y;
-  }
-  sm = wave_sum_dpp_d(sm);
-  sm2 = wave_sum_dpp_d(sm2);
-  sq = wave_sum_dpp_d(sq);
-  const double ntot = (double)p.Cout * p.Lout;
-  const double mean = sm / ntot;
-  const double var = fmax(sq + (sm2 - sm * mean), 0.0) / ntot;
-  float rstd = (float)(1.0 / sqrt(var + (double)eps));
-  if (!isfinite(rstd)) rstd = 0.f;
-  const float mf = (float)mean;
+  // merge in a fixed order, in every wave; the total count is Cout x Lout
+  const float2 mr = xch_merge(sp, nparts, [&](int v) { return tile_count(v % gridDim.x); },
+                              (double)p.Cout * p.Lout, eps);
+  const float rstd = mr.y, mf = mr.x;
   if (valid) {
     float* yb = y + ((int64_t)b * p.Cout + cob0 + c0) * p.ldy + t;
     const float* cb = wt + CK * COB + c0;  // bias, gamma, beta of this thread's channels
@@ -565,19 +511,8 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
       }
     }
   }
-  // count this workgroup out (its reads of the slots are done); the last one out clears every
-  // slot of the launch and the count
-  const unsigned total = gridDim.x * gridDim.y * gridDim.z;
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             total - 1;
-  lds_barrier();
-  if (s_last) {
-    unsigned long long* all = xch + 8;
-    for (int i = threadIdx.x; i < 2 * (int)total; i += NT)
-      __hip_atomic_store(all + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  // count this workgroup out; the last one out clears every slot of the launch and the count
+  xch_count_out<NT>(xch, gridDim.x * gridDim.y * gridDim.z, &s_last);
 }
 
 // Register-window variant applies when groups = 1, Cin*K is 8, 16, 24 or 32, Cout % 16 == 0

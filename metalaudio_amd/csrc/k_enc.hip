@@ -389,6 +389,153 @@ __global__ __launch_bounds__(kRedThreads) void enc_conv_reduce_kernel(
   }
 }
 
+// Split-K finish, GroupNorm(1) and GELU in one launch, for grids resident at once: a workgroup
+// sums the K parts of a tile of kGC channels x kGT positions in split order (as
+// enc_conv_reduce_kernel) and adds the bias, publishes the tile's (mean, M2) through the
+// grid-wide exchange (device_utils.hpp), merges every partial of its batch and writes
+// z^T[b][t][c] = GELU(GroupNorm(y))[c][t] through an LDS transpose: the rewrite GEMM's operand,
+// with no pre-norm y in HBM and no separate normalisation pass. C % kGC == 0, so z^T rows hold
+// exactly C channels (the rewrite's K).
+constexpr int kGT = 64, kGC = 32;    // positions x channels per tile (256 threads, 8 values each)
+constexpr int kGnMaxParts = 2048;    // tiles per batch (LDS: 8 bytes each)
+constexpr int kGnMaxSlots = 4096;    // tiles over all batches
+
+struct EncGnKArgs {
+  const float* ws = nullptr;  // ws[((b * splits + s) * C + c) * N + n]
+  int splits = 1, C = 0, N = 0;
+  const float* bias = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float eps = 1e-5f;
+  float* zt = nullptr;  // [b][N][C]
+  unsigned long long* xch = nullptr;
+  int spin_limit = 0;
+};
+
+// Thread (wave w, lane) holds channels tc * kGC + w + 4 i (i < 8) at position tt * kGT + lane
+// (clamped to the last position for the tail tile).
+__device__ __forceinline__ void gn_tile_values(const EncGnKArgs& a, int b, int tc, int tt,
+                                               float (&v)[8]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t total = (int64_t)a.C * a.N;
+  const float* __restrict__ wb = a.ws + (int64_t)b * a.splits * total;
+  const int n = min(tt * kGT + lane, a.N - 1);
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  // parts added in split order, the loads of up to four parts in flight together
+  auto parts = [&](int s, auto nj) {
+    constexpr int J = decltype(nj)::value;
+    float t[J][8];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        t[j][i] = wb[(int64_t)(s + j) * total + (int64_t)(tc * kGC + w + 4 * i) * a.N + n];
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += t[j][i];
+  };
+  int s = 0;
+  for (; s + 4 <= a.splits; s += 4) parts(s, std::integral_constant<int, 4>{});
+  if (s + 2 <= a.splits) {
+    parts(s, std::integral_constant<int, 2>{});
+    s += 2;
+  }
+  if (s < a.splits) parts(s, std::integral_constant<int, 1>{});
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = acc[i] + a.bias[tc * kGC + w + 4 * i];
+}
+
+// (mean, M2) of a tile (two passes over the registers); every thread returns the same bits.
+__device__ __forceinline__ void gn_tile_stats(const float (&v)[8], bool valid, float n, float* red,
+                                              float& mean, float& m2) {
+  const int wid = threadIdx.x >> 6;
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s += v[i];
+  s = wave_sum_dpp(valid ? s : 0.f);
+  if ((threadIdx.x & 63) == 0) red[wid] = s;
+  lds_barrier();
+  mean = ((red[0] + red[1]) + (red[2] + red[3])) / n;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q = fmaf(v[i] - mean, v[i] - mean, q);
+  q = wave_sum_dpp(valid ? q : 0.f);
+  if ((threadIdx.x & 63) == 0) red[4 + wid] = q;
+  lds_barrier();
+  m2 = (red[4] + red[5]) + (red[6] + red[7]);
+}
+
+__global__ __launch_bounds__(256, 4) void enc_reduce_gn_t_kernel(EncGnKArgs a) {
+  __shared__ float2 sp[kGnMaxParts];
+  __shared__ float tileb[kGC][kGT + 1];
+  __shared__ float red[8];
+  __shared__ float2 s_res;
+  __shared__ float s_gb[2 * kGC];  // gamma, beta of the tile's channels
+  __shared__ unsigned s_tag;
+  const int tt = blockIdx.x, tc = blockIdx.y, b = blockIdx.z;
+  const int ntt = gridDim.x, nparts = gridDim.x * gridDim.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (threadIdx.x == 0) s_tag = xm_tag(a.xch, b);  // read after the statistics' barriers
+  auto tile_count = [&](int v) { return (float)(kGC * min(kGT, a.N - (v % ntt) * kGT)); };
+  if (threadIdx.x < kGC) {
+    const int c = tc * kGC + threadIdx.x;
+    s_gb[threadIdx.x] = a.gamma ? a.gamma[c] : 1.f;
+    s_gb[kGC + threadIdx.x] = a.beta ? a.beta[c] : 0.f;
+  }
+  float v[8];
+  gn_tile_values(a, b, tc, tt, v);
+  const bool valid = tt * kGT + lane < a.N;
+  float mean, m2;
+  gn_tile_stats(v, valid, tile_count(tc * ntt + tt), red, mean, m2);
+  // every partial of the batch computed here from the K parts, as their owners compute them
+  auto all_parts = [&]() {
+    for (int u = 0; u < nparts; ++u) {
+      float vu[8];
+      gn_tile_values(a, b, u / ntt, u % ntt, vu);
+      float mu, m2u;
+      gn_tile_stats(vu, (u % ntt) * kGT + lane < a.N, tile_count(u), red, mu, m2u);
+      if (threadIdx.x == 0) sp[u] = make_float2(mu, m2u);
+    }
+    lds_barrier();
+  };
+  // tile 0 merges and publishes; the others take its result, or compute every partial themselves
+  // when their bounded wait runs out
+  const unsigned tag = s_tag;
+  const int me = tc * ntt + tt;
+  if (threadIdx.x == 0) xm_put(a.xch, b, nparts, me, tag, mean, m2);
+  const bool merger = me == 0;
+  bool self = false;
+  if (merger)
+    xm_collect<256, 4>(a.xch, b, nparts, tag, sp);
+  else
+    self = !xm_wait(a.xch, b, tag, a.spin_limit, &s_res);
+  if (self) all_parts();
+  float2 mr = s_res;
+  if (merger || self) mr = xch_merge(sp, nparts, tile_count, (double)a.C * a.N, a.eps);
+  if (merger && threadIdx.x == 0) xm_publish(a.xch, b, tag, mr);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float sc = s_gb[w + 4 * i] * mr.y;
+    tileb[w + 4 * i][lane] = gelu_tanh_fast(fmaf(v[i], sc, s_gb[kGC + w + 4 * i] - mr.x * sc));
+  }
+  lds_barrier();
+  // stores: thread covers positions tt * kGT + tid / 8 + 32 j, channels 4 (tid % 8) .. + 3
+  float* __restrict__ zb = a.zt + (int64_t)b * a.N * a.C;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int pr = (int)threadIdx.x / 8 + 32 * j, c4 = 4 * ((int)threadIdx.x % 8);
+    const int t = tt * kGT + pr;
+    if (t < a.N) {
+      const float4 z = make_float4(tileb[c4][pr], tileb[c4 + 1][pr], tileb[c4 + 2][pr],
+                                   tileb[c4 + 3][pr]);
+      *reinterpret_cast<float4*>(zb + (int64_t)t * a.C + tc * kGC + c4) = z;
+    }
+  }
+}
+
 // z^T[b][t][k] = GELU(y[b][k][t] * scale_k + shift_k) for k < C, 0 for C <= k < kp. GroupNorm(1)
 // comes from the producer's statistics partials (merged in fp64 in a fixed order, once per
 // workgroup) with gamma / beta, or from per-row coefficients coef[b][k] = (scale, shift).
@@ -725,6 +872,228 @@ __global__ __launch_bounds__(256, 2) void enc_l1_fused_kernel(EncL1KArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- first level, one launch
+// The same level in one launch when its grid is resident at once: every wave computes the conv of
+// its tasks (one or two, with the raw weights and bias), the workgroup publishes the
+// GroupNorm(1) partial of its tiles through the grid-wide exchange (device_utils.hpp) and keeps
+// the pre-norm tiles in LDS; once it has merged every partial of its batch it applies
+// GroupNorm + GELU to the kept tiles and runs the rewrite and GLU as the two-pass form does. No
+// statistics pass, and the input is read once.
+constexpr int kL1MaxTPW = 2;        // tasks per wave
+constexpr int kL1MaxParts = 1024;   // workgroups per batch (LDS: 8 bytes each)
+constexpr int kL1MaxSlots = 4096;   // workgroups over all batches
+
+// The conv (plus bias) of the tasks task0 + k * stride (k < TPW) of one wave; tasks past the
+// last are computed on the last one's columns and never counted or stored.
+template <int CIN, bool REFLECT, int TPW>
+__device__ __forceinline__ void l1_wave_conv(const float* __restrict__ xb, int Ls, int Lo, int pad,
+                                             int task0, int stride, int lane,
+                                             const float (&acv)[2][4 * CIN], const float* s_b1,
+                                             floatx16 (&ac)[TPW][2]) {
+  const int g = lane >> 5;
+  const int tasks = (Lo + 31) / 32;
+  float xv[TPW][4 * CIN];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k)
+    l1_load_x<CIN, REFLECT>(xb, Ls, Lo, pad, min(task0 + k * stride, tasks - 1), lane, xv[k]);
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) ac[k][cb][v] = s_b1[32 * cb + 8 * (v / 4) + 4 * g + (v % 4)];
+    l1_conv<CIN>(acv, xv[k], ac[k]);
+  }
+}
+
+// Element count of workgroup blk's partial: 48 channels x the valid columns of its waves' tasks.
+template <int TPW>
+__device__ __forceinline__ float l1_block_count(int blk, int stride, int Lo) {
+  const int tasks = (Lo + 31) / 32;
+  float n = 0.f;
+  for (int w = 0; w < 4; ++w)
+    for (int k = 0; k < TPW; ++k) {
+      const int t = blk * 4 + w + k * stride;
+      if (t < tasks) n += (float)(kL1C * min(32, Lo - 32 * t));
+    }
+  return n;
+}
+
+// (mean, M2) of the 48 real channels of a workgroup's tasks, two passes over the registers (the
+// mean from a block sum, then M2 about it); every thread returns the same bits. red: 8 floats.
+template <int TPW>
+__device__ __forceinline__ void l1_block_stats(const floatx16 (&ac)[TPW][2], int task0,
+                                               int stride, int Lo, int lane, float n, float* red,
+                                               float& mean, float& m2) {
+  const int wid = threadIdx.x >> 6, l32 = lane & 31;
+  const int tasks = (Lo + 31) / 32;
+  bool valid[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    const int t = task0 + k * stride;
+    valid[k] = t < tasks && t * 32 + l32 < Lo;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    float sk = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sk += ac[k][0][v];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) sk += ac[k][1][v];  // channels 32..47
+    s += valid[k] ? sk : 0.f;
+  }
+  s = wave_sum_dpp(s);
+  if (lane == 0) red[wid] = s;
+  lds_barrier();
+  mean = ((red[0] + red[1]) + (red[2] + red[3])) / n;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    float qk = 0.f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) qk = fmaf(ac[k][0][v] - mean, ac[k][0][v] - mean, qk);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) qk = fmaf(ac[k][1][v] - mean, ac[k][1][v] - mean, qk);
+    q += valid[k] ? qk : 0.f;
+  }
+  q = wave_sum_dpp(q);
+  if (lane == 0) red[4 + wid] = q;
+  lds_barrier();
+  m2 = (red[4] + red[5]) + (red[6] + red[7]);
+}
+
+// TPW tasks per wave: 1 with three workgroups per CU, 2 with two (the pre-norm tiles in LDS:
+// 32 or 64 KiB per workgroup).
+template <int CIN, bool REFLECT, int TPW>
+__global__ __launch_bounds__(256, TPW == 1 ? 3 : 2) void enc_l1_oneshot_kernel(
+    EncL1KArgs a, unsigned long long* xch, int spin_limit) {
+  constexpr int C = kL1C, KS = 4 * CIN, K1 = 8 * CIN;
+  __shared__ float stash[4 * TPW * 32 * 64];  // pre-norm tiles: [wave][task][register][lane]
+  __shared__ float2 sp[kL1MaxParts];
+  __shared__ float red[8];
+  __shared__ float s_b1[64], s_sc[64], s_sh[64], s_rb[2 * kL1C];
+  __shared__ float2 s_res;
+  __shared__ unsigned s_tag;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int b = blockIdx.y, G = gridDim.x;
+  if (tid == 0) s_tag = xm_tag(xch, b);  // read after the barrier below
+  if (tid < 64) {
+    s_b1[tid] = (tid < C && a.b1) ? a.b1[tid] : 0.f;
+  } else if (tid < 64 + 2 * C) {
+    s_rb[tid - 64] = a.rb[tid - 64];
+  }
+  float acv[2][KS];  // raw conv weights (rows 48..63 zero)
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int c = 32 * cb + l32, cc = min(c, C - 1);
+    const float live = c < C ? 1.f : 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acv[cb][s] = a.w1[cc * K1 + 2 * s + g] * live;
+  }
+  lds_barrier();
+  const float* __restrict__ xb = a.x + (int64_t)b * CIN * a.L;
+  const int Ls = (int)a.L, Lo = (int)a.Lout;
+  const int tasks = (Lo + 31) / 32;
+  const int stride = G * 4;
+  const int task0 = blockIdx.x * 4 + wave;
+  const unsigned tag = s_tag;
+  float mean, m2;
+  {
+    floatx16 ac[TPW][2];
+    l1_wave_conv<CIN, REFLECT, TPW>(xb, Ls, Lo, a.pad, task0, stride, lane, acv, s_b1, ac);
+    l1_block_stats(ac, task0, stride, Lo, lane, l1_block_count<TPW>(blockIdx.x, stride, Lo), red, mean,
+                   m2);
+#pragma unroll
+    for (int k = 0; k < TPW; ++k)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          stash[((wave * TPW + k) * 32 + 16 * cb + v) * 64 + lane] = ac[k][cb][v];
+  }
+  // the rewrite operand, in flight while the partials are collected
+  float arw[kL1MB][kL1KP];
+#pragma unroll
+  for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p) arw[mb][p] = a.a_rw[(mb * kL1KP + p) * 64 + lane];
+  // every partial of the batch computed here as its owner does (wave w of this workgroup takes
+  // wave w's tasks)
+  auto all_parts = [&]() {
+    for (int v = 0; v < G; ++v) {
+      floatx16 ac[TPW][2];
+      const int t0 = v * 4 + wave;
+      l1_wave_conv<CIN, REFLECT, TPW>(xb, Ls, Lo, a.pad, t0, stride, lane, acv, s_b1, ac);
+      float mu, m2u;
+      l1_block_stats(ac, t0, stride, Lo, lane, l1_block_count<TPW>(v, stride, Lo), red, mu, m2u);
+      if (tid == 0) sp[v] = make_float2(mu, m2u);
+    }
+    lds_barrier();
+  };
+  auto count = [&](int v) { return l1_block_count<TPW>(v, stride, Lo); };
+  // workgroup 0 merges and publishes; the others take its result, or compute every partial
+  // themselves when their bounded wait runs out
+  if (tid == 0) xm_put(xch, b, G, blockIdx.x, tag, mean, m2);
+  const bool merger = blockIdx.x == 0;
+  bool self = false;
+  if (merger)
+    xm_collect<256, 4>(xch, b, G, tag, sp);
+  else
+    self = !xm_wait(xch, b, tag, spin_limit, &s_res);
+  if (self) all_parts();
+  float2 mr = s_res;
+  if (merger || self) mr = xch_merge(sp, G, count, (double)C * Lo, a.eps);
+  if (merger && tid == 0) xm_publish(xch, b, tag, mr);
+  if (tid < 64) {
+    float sc = 0.f, sh = 0.f;
+    if (tid < C) {
+      sc = (a.gamma ? a.gamma[tid] : 1.f) * mr.y;
+      sh = (a.beta ? a.beta[tid] : 0.f) - mr.x * sc;
+    }
+    s_sc[tid] = sc;
+    s_sh[tid] = sh;
+  }
+  lds_barrier();
+  float* __restrict__ ob = a.out + (int64_t)b * C * a.ldo;
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    const int task = task0 + k * stride;
+    if (task >= tasks) break;
+    float z[kL1KP];
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p) {
+      const int cb = p / 16, v = p % 16;
+      const int ch = 32 * cb + 8 * (v / 4) + 4 * g + (v % 4);
+      const float y = stash[((wave * TPW + k) * 32 + p) * 64 + lane];
+      z[p] = gelu_tanh_fast(fmaf(y, s_sc[ch], s_sh[ch]));
+    }
+    floatx16 ar[kL1MB];
+#pragma unroll
+    for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) ar[mb][v] = 0.f;
+#pragma unroll
+    for (int p = 0; p < kL1KP; ++p)
+#pragma unroll
+      for (int mb = 0; mb < kL1MB; ++mb)
+        ar[mb] = __builtin_amdgcn_mfma_f32_32x32x2f32(arw[mb][p], z[p], ar[mb], 0, 0, 0);
+    const int tc = task * 32 + l32;
+    if (tc < Lo) {
+#pragma unroll
+      for (int mb = 0; mb < kL1MB; ++mb)
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          const int rr = 8 * (v / 4) + 4 * g + (v % 4);
+          const float va = ar[mb][v] + s_rb[32 * mb + rr];
+          const float vb = ar[mb][v + 8] + s_rb[32 * mb + 16 + rr];
+          ob[(int64_t)(16 * mb + rr) * a.ldo + tc] = va * stable_sigmoid(vb);
+        }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- host-side selection
 // Kernel-timing name of an encoder launch tagged with the level's channel count, e.g.
 // "enc_conv_f32[c96]" (timing queries match by substring, so the family name still sums them).
@@ -760,7 +1129,7 @@ struct ConvPlan {
 // Critical path per CU: rounds of concurrent workgroups x per-workgroup time (its stages plus a
 // fixed prologue / epilogue share, scaled by tile area / efficiency), slowed when a CU holds few
 // workgroups, plus the split-K partial traffic (written and read once) in the same units.
-ConvPlan plan_conv(int M, int N, int K, int batch) {
+ConvPlan plan_conv(int M, int N, int K, int batch, int min_splits = 1) {
   const int nk = K / BK;
   const int ft = env_int("MNN_ENC_CONV_TILE"), fs = env_int("MNN_ENC_CONV_SPLIT");
   ConvPlan best;
@@ -771,7 +1140,7 @@ ConvPlan plan_conv(int M, int N, int K, int batch) {
     const int occ = std::max(1, std::min(160 / t.lds_kb, 8));
     for (int s : {1, 2, 3, 4, 6, 8, 12, 16}) {
       // a forced split applies where it divides the stages
-      if (nk % s != 0 || (fs > 0 && nk % fs == 0 && s != fs)) continue;
+      if (nk % s != 0 || s < min_splits || (fs > 0 && nk % fs == 0 && s != fs)) continue;
       const int64_t wgs = (int64_t)tiles * batch * s;
       const double rounds = std::ceil((double)wgs / (kCUs * occ));
       const double fill = std::min(1.0, (double)wgs / (kCUs * occ));
@@ -822,9 +1191,9 @@ bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int grou
 
 int enc_conv_padded_cin(int Cin) { return (Cin + 3) / 4 * 4; }
 
-void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, int* splits, int* bm,
-                        int* bn) {
-  const ConvPlan p = plan_conv(Cout, (int)Lout, enc_conv_padded_cin(Cin) * 8, batch);
+void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, bool gn, int* splits,
+                        int* bm, int* bn) {
+  const ConvPlan p = plan_conv(Cout, (int)Lout, enc_conv_padded_cin(Cin) * 8, batch, gn ? 2 : 1);
   *splits = p.splits;
   *bm = p.t->bm;
   *bn = p.t->bn;
@@ -834,9 +1203,34 @@ int enc_conv_parts(int Cout, int64_t Lout, int K, int batch) {
   return conv_parts(plan_conv(Cout, (int)Lout, K, batch), Cout, (int)Lout);
 }
 
-int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch) {
-  const ConvPlan p = plan_conv(Cout, (int)Lout, K, batch);
+int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch, bool gn) {
+  const ConvPlan p = plan_conv(Cout, (int)Lout, K, batch, gn ? 2 : 1);
   return p.splits > 1 ? (int64_t)p.splits * batch * Cout * Lout : 0;
+}
+
+size_t enc_exchange_bytes() {
+  return 8 * (4 * (size_t)kXmMaxBatch + 2 * (size_t)std::max(kGnMaxSlots, kL1MaxSlots));
+}
+
+bool enc_conv_gn_fits(const LaunchCtx& c, int Cin, int Cout, int64_t L, int64_t Lout, int B) {
+  // workgroups of the finish one CU holds at once (the same for every gfx950 device)
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, enc_reduce_gn_t_kernel, 256, 0) !=
+        hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    return n;
+  }();
+  if (Cout % kGC != 0 || !enc_conv_supported(Cin, Cout, 8, 4, 1, 1, 0, L) || Lout < 1 ||
+      Lout >= (1LL << 24))
+    return false;
+  const int nk = enc_conv_padded_cin(Cin) * 8 / BK;
+  if (nk < 2) return false;  // K cannot be split
+  const int64_t nparts = cdiv(Lout, kGT) * (Cout / kGC);
+  return nparts <= kGnMaxParts && B <= kXmMaxBatch && B * nparts <= kGnMaxSlots &&
+         B * nparts <= (int64_t)per_cu * c.dev->props.multiProcessorCount;
 }
 
 void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
@@ -855,10 +1249,14 @@ void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
   a.y = p.y;
   a.ldy = p.ldy;
   a.y_bs = (int64_t)p.Cout * p.ldy;
-  MNN_REQUIRE(enc_conv_supported(p.Cin, p.Cout, 8, 4, 1, 1, p.pad, p.L) && p.ldy >= p.Lout &&
-                  p.Lout >= 1 && p.bias && p.parts && (p.Lout - 1) * 4 + 8 <= p.L + 2 * p.pad,
+  const bool gn = p.zt != nullptr;
+  MNN_REQUIRE(enc_conv_supported(p.Cin, p.Cout, 8, 4, 1, 1, p.pad, p.L) && p.Lout >= 1 &&
+                  p.bias && (gn || (p.ldy >= p.Lout && p.parts)) &&
+                  (p.Lout - 1) * 4 + 8 <= p.L + 2 * p.pad,
               MNN_ERR_INVALID_ARGUMENT, "enc_conv: unsupported configuration");
-  const ConvPlan plan = plan_conv(a.M, a.N, a.K, p.B);
+  MNN_REQUIRE(!gn || (p.xch && enc_conv_gn_fits(c, p.Cin, p.Cout, p.L, p.Lout, p.B)),
+              MNN_ERR_INVALID_ARGUMENT, "enc_conv: GroupNorm finish outside its contract");
+  const ConvPlan plan = plan_conv(a.M, a.N, a.K, p.B, gn ? 2 : 1);
   a.splits = plan.splits;
   if (plan.splits > 1) {
     MNN_REQUIRE(p.ws, MNN_ERR_INVALID_ARGUMENT, "enc_conv: split-K needs a workspace");
@@ -873,7 +1271,22 @@ void enc_conv(const LaunchCtx& c, const EncConvArgs& p) {
     case 4: launch_conv<1, 4, 1, 1, 4>(c, a, p.B); break;
     default: launch_conv<2, 2, 1, 1, 4>(c, a, p.B); break;
   }
-  if (plan.splits > 1)
+  if (gn) {
+    EncGnKArgs g;
+    g.ws = p.ws;
+    g.splits = plan.splits;
+    g.C = a.M;
+    g.N = a.N;
+    g.bias = p.bias;
+    g.gamma = p.gamma;
+    g.beta = p.beta;
+    g.eps = p.eps;
+    g.zt = p.zt;
+    g.xch = static_cast<unsigned long long*>(p.xch);
+    g.spin_limit = std::max(p.spin_limit, 0);
+    launch(c, level_name("enc_conv_reduce_gn_f32", a.M).c_str(), enc_reduce_gn_t_kernel,
+           dim3(cdiv(a.N, kGT), a.M / kGC, p.B), dim3(256), 0, g);
+  } else if (plan.splits > 1)
     launch(c, level_name("enc_conv_reduce_f32", a.M).c_str(), enc_conv_reduce_kernel,
            dim3(cdiv(a.N, kRedCols), a.M, p.B),
            dim3(kRedThreads), 0, (const float*)p.ws, plan.splits, a.M, a.N, p.bias, p.y, p.ldy,
@@ -903,8 +1316,52 @@ int enc_l1_parts(int64_t Lout) {
   return (int)std::min<int64_t>(cdiv(cdiv(Lout, 32), 4), f > 0 ? f : 2 * kCUs);
 }
 
+namespace {
+// Workgroups per batch of the one-launch first level with TPW tasks per wave (0: it does not
+// apply): as many as the 32-column tasks need at four waves each, within what the device holds at
+// once, with at most TPW tasks per wave.
+template <int CIN, bool R, int TPW>
+int l1_oneshot_grid(const LaunchCtx& c, int64_t tasks, int B) {
+  static const int per_cu = [] {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, enc_l1_oneshot_kernel<CIN, R, TPW>, 256,
+                                                     0) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    return n;
+  }();
+  const int64_t resident = (int64_t)per_cu * c.dev->props.multiProcessorCount / B;
+  const int64_t G = std::min<int64_t>(cdiv(tasks, 4), resident);
+  if (G < 1 || G > kL1MaxParts || B > kXmMaxBatch || G * B > kL1MaxSlots ||
+      cdiv(tasks, 4 * G) > TPW)
+    return 0;
+  return (int)G;
+}
+
+// One task per wave where the device holds enough waves at once, else two.
+template <int CIN, bool R>
+bool l1_oneshot(const LaunchCtx& c, const EncL1Args& p, const EncL1KArgs& a) {
+  if (!p.xch) return false;
+  const int64_t tasks = cdiv(p.Lout, 32);
+  auto go = [&](auto kern, int G) {
+    launch(c, level_name("enc_l1_oneshot_f32", p.C).c_str(), kern, dim3((unsigned)G, p.B),
+           dim3(256), 0, a, static_cast<unsigned long long*>(p.xch), std::max(p.spin_limit, 0));
+  };
+  if (const int G = l1_oneshot_grid<CIN, R, 1>(c, tasks, p.B)) {
+    go(enc_l1_oneshot_kernel<CIN, R, 1>, G);
+    return true;
+  }
+  if (const int G = l1_oneshot_grid<CIN, R, kL1MaxTPW>(c, tasks, p.B)) {
+    go(enc_l1_oneshot_kernel<CIN, R, kL1MaxTPW>, G);
+    return true;
+  }
+  return false;
+}
+}  // namespace
+
 void enc_l1(const LaunchCtx& c, const EncL1Args& p) {
-  MNN_REQUIRE(enc_l1_supported(p.Cin, p.C, 8, 4, 1, 1, p.pad, p.L) && p.parts &&
+  MNN_REQUIRE(enc_l1_supported(p.Cin, p.C, 8, 4, 1, 1, p.pad, p.L) && (p.parts || p.xch) &&
                   p.a_rw && p.rb && p.w1 && p.out && p.ldo >= p.Lout && p.Lout >= 1 &&
                   (p.Lout - 1) * 4 + 8 <= p.L + 2 * p.pad,
               MNN_ERR_INVALID_ARGUMENT, "enc_l1: unsupported configuration");
@@ -925,6 +1382,21 @@ void enc_l1(const LaunchCtx& c, const EncL1Args& p) {
   a.a_rw = p.a_rw;
   a.rb = p.rb;
   a.out = p.out;
+  {
+    bool done = false;
+    switch (p.Cin * 2 + (p.reflect ? 1 : 0)) {
+      case 2: done = l1_oneshot<1, false>(c, p, a); break;
+      case 3: done = l1_oneshot<1, true>(c, p, a); break;
+      case 4: done = l1_oneshot<2, false>(c, p, a); break;
+      case 5: done = l1_oneshot<2, true>(c, p, a); break;
+      case 6: done = l1_oneshot<3, false>(c, p, a); break;
+      case 7: done = l1_oneshot<3, true>(c, p, a); break;
+      case 8: done = l1_oneshot<4, false>(c, p, a); break;
+      default: done = l1_oneshot<4, true>(c, p, a); break;
+    }
+    if (done) return;
+  }
+  MNN_REQUIRE(p.parts, MNN_ERR_INVALID_ARGUMENT, "enc_l1: the two-pass form needs a workspace");
   const int64_t tasks = cdiv(p.Lout, 32);
   {  // statistics pass: one partial per workgroup
     a.nparts = enc_l1_parts(p.Lout);
@@ -964,14 +1436,16 @@ int enc_rewrite_kp(int C) { return (C + 31) / 32 * 32; }
 
 void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& p) {
   MNN_REQUIRE(p.C % 16 == 0 && p.C > 0 && p.kp == enc_rewrite_kp(p.C) && p.zt && p.w && p.bias &&
-                  p.ldy >= p.Lout && p.ldo >= p.Lout && ((p.parts && p.nparts > 0) || p.coef),
+                  p.ldo >= p.Lout &&
+                  (p.zt_ready || (p.ldy >= p.Lout && ((p.parts && p.nparts > 0) || p.coef))),
               MNN_ERR_INVALID_ARGUMENT, "enc_rewrite: unsupported configuration");
-  // about 1024 workgroups in all, each with the same number of tiles
-  const int64_t tiles = (int64_t)cdiv(p.Lout, kTT) * cdiv(p.kp, kTT);
-  const int64_t per = cdiv(tiles, std::max<int64_t>(1, 1024 / p.B));
-  launch(c, level_name("enc_gn_gelu_t_f32", p.C).c_str(), enc_gn_gelu_t_kernel,
-         dim3((unsigned)cdiv(tiles, per), 1, p.B),
-         dim3(256), 0, p);
+  if (!p.zt_ready) {
+    // about 1024 workgroups in all, each with the same number of tiles
+    const int64_t tiles = (int64_t)cdiv(p.Lout, kTT) * cdiv(p.kp, kTT);
+    const int64_t per = cdiv(tiles, std::max<int64_t>(1, 1024 / p.B));
+    launch(c, level_name("enc_gn_gelu_t_f32", p.C).c_str(), enc_gn_gelu_t_kernel,
+           dim3((unsigned)cdiv(tiles, per), 1, p.B), dim3(256), 0, p);
+  }
   GemmArgs g;
   g.M = 2 * p.C;
   g.N = (int)p.Lout;

@@ -371,16 +371,34 @@ struct EncConvArgs {
   int64_t ldy = 0;
   float* parts = nullptr;
   float* ws = nullptr;
+  // GroupNorm(1) + GELU in the split-K finish (enc_conv_gn_fits): when zt is set, the K parts are
+  // summed by one launch that exchanges the statistics between its workgroups and writes
+  // zt [B][Lout][Cout] = GELU(GroupNorm(y))^T (the rewrite's operand); y and parts are unused.
+  // xch: the exchange buffer (enc_exchange_bytes, zero before the first launch; epoch-tagged).
+  float* zt = nullptr;
+  const float* gamma = nullptr;
+  const float* beta = nullptr;
+  float eps = 1e-5f;
+  void* xch = nullptr;
+  int spin_limit = 65536;
 };
+// Bytes of the exchange buffer of the encoder's one-launch GroupNorm forms (first level and the
+// split-K finish); one per layer, zeroed once.
+size_t enc_exchange_bytes();
+// Whether the GroupNorm split-K finish applies: Cout % 32 == 0, a conv the implicit-GEMM kernel
+// takes, and a finish grid that is resident at once on this device.
+bool enc_conv_gn_fits(const LaunchCtx& c, int Cin, int Cout, int64_t L, int64_t Lout, int B);
 bool enc_conv_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,
                         int64_t L);
 int enc_conv_padded_cin(int Cin);
 // Statistics partials per batch the launch writes; K = enc_conv_padded_cin(Cin) * 8.
 int enc_conv_parts(int Cout, int64_t Lout, int K, int batch);
-int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch);
+// Workspace floats of the split-K partial products (0 without a split); gn: the GroupNorm finish
+// (which always splits K).
+int64_t enc_conv_ws_floats(int Cout, int64_t Lout, int K, int batch, bool gn = false);
 // The K split and output tile the conv launcher picks (for measurement accounting).
-void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, int* splits, int* bm,
-                        int* bn);
+void enc_conv_plan_info(int Cin, int Cout, int64_t Lout, int batch, bool gn, int* splits,
+                        int* bm, int* bn);
 void enc_conv(const LaunchCtx& c, const EncConvArgs& a);
 // Rewrite 1x1 conv C -> 2C with GLU: out[b][c][t] = z[c] * sigmoid(z[c + C]),
 // z = w * GELU(GroupNorm(y)) + bias, in two launches: GroupNorm + GELU of y written transposed to
@@ -406,6 +424,7 @@ struct EncRewriteArgs {
   int kp = 0;
   float* out = nullptr;  // [B][C][ldo]
   int64_t ldo = 0;
+  bool zt_ready = false;  // zt already holds GELU(GroupNorm(y))^T: the GEMM only
 };
 int enc_rewrite_kp(int C);
 void enc_rewrite(const LaunchCtx& c, const EncRewriteArgs& a);
@@ -431,6 +450,11 @@ struct EncL1Args {
   const float* a_rw = nullptr;
   const float* rb = nullptr;
   float* out = nullptr;
+  // One launch instead of two when the grid is resident at once: the workgroups exchange their
+  // GroupNorm partials (xch: enc_exchange_bytes, zero before the first launch) and
+  // keep the pre-norm conv in LDS; parts is then unused.
+  void* xch = nullptr;
+  int spin_limit = 65536;
 };
 constexpr int kEncL1PackFloats = 3 * 24 * 64;
 bool enc_l1_supported(int Cin, int Cout, int ks, int stride, int dil, int groups, int pad,

@@ -983,8 +983,10 @@ class EncoderBlockLayer : public Layer {
     if (d_.rewrite && g1 && glu_fused_ && d_.precision == MNN_PRECISION_F32 && l1_pack_.ptr &&
         k::enc_l1_supported(d_.in_channels, Cout, d_.kernel_size, d_.stride, 1, 1,
                             conv_->pad_for(L), L)) {
-      // Few input channels (the first level): a statistics pass, then one fused pass (conv
-      // recomputed with GroupNorm folded in, GELU, rewrite, GLU); only the output is written.
+      // Few input channels (the first level): one launch whose workgroups exchange their
+      // GroupNorm partials when the grid is resident at once, else a statistics pass and a fused
+      // pass (conv recomputed with GroupNorm folded in); either way conv, GroupNorm, GELU,
+      // rewrite and GLU in registers, only the output written.
       partials_.reserve(sizeof(float) * 3 * B * k::enc_l1_parts(lo));
       k::EncL1Args e;
       e.B = (int)B;
@@ -1005,6 +1007,8 @@ class EncoderBlockLayer : public Layer {
       e.a_rw = l1_pack_.f32();
       e.rb = rb_perm_.f32();
       e.out = out.f32();
+      e.xch = exchange(s);
+      e.spin_limit = s.dev->grid_spin_limit.load();
       k::enc_l1(ctx(s), e);
       return;
     }
@@ -1034,8 +1038,35 @@ class EncoderBlockLayer : public Layer {
       r.kp = kp;
       r.out = out.f32();
       r.ldo = lo;
-      if (k::enc_conv_supported(cd.in_channels, Cout, cd.kernel_size, cd.stride, cd.dilation,
-                                cd.groups, pad, L)) {
+      const bool conv_ok = k::enc_conv_supported(cd.in_channels, Cout, cd.kernel_size, cd.stride,
+                                                 cd.dilation, cd.groups, pad, L);
+      if (conv_ok && k::enc_conv_gn_fits(ctx(s), cd.in_channels, Cout, L, lo, (int)B)) {
+        // split-K conv, then one launch that sums the K parts, exchanges the GroupNorm
+        // statistics between its workgroups and writes GELU(GroupNorm(y))^T: no y in HBM and no
+        // separate normalisation pass
+        const int K = k::enc_conv_padded_cin(cd.in_channels) * 8;
+        ws_.reserve(sizeof(float) * k::enc_conv_ws_floats(Cout, lo, K, (int)B, true));
+        k::EncConvArgs c;
+        c.B = (int)B;
+        c.Cin = cd.in_channels;
+        c.Cout = Cout;
+        c.L = L;
+        c.Lout = lo;
+        c.pad = pad;
+        c.reflect = cd.padding_mode == MNN_PAD_REFLECT;
+        c.x = in.f32();
+        c.w = enc_conv_weight();
+        c.bias = conv_->bias_ptr();
+        c.ws = ws_.f32();
+        c.zt = zt_.f32();
+        c.gamma = norm_->gamma();
+        c.beta = norm_->beta();
+        c.eps = norm_->eps();
+        c.xch = exchange(s);
+        c.spin_limit = s.dev->grid_spin_limit.load();
+        k::enc_conv(ctx(s), c);
+        r.zt_ready = true;
+      } else if (conv_ok) {
         const int K = k::enc_conv_padded_cin(cd.in_channels) * 8;
         const int nparts = k::enc_conv_parts(Cout, lo, K, (int)B);
         partials_.reserve(sizeof(float) * 3 * B * nparts);
@@ -1238,7 +1269,19 @@ class EncoderBlockLayer : public Layer {
   Param* rb_ = nullptr;
   bool glu_fused_ = false;
   DevBuf rw_perm_, rb_perm_, rw_pad_, l1_pack_;
-  DevBuf y_, partials_, z_, wpad_, ws_, zt_;
+  DevBuf y_, partials_, z_, wpad_, ws_, zt_, xch_;
+  // Exchange buffer of the one-launch GroupNorm forms (the first level, the split-K finish),
+  // zeroed on the stream when allocated; its words carry per-launch epoch tags, so launches leave
+  // nothing to clear. Forwards of one block that overlap (two streams) would share it, as they
+  // share the workspaces.
+  void* exchange(Stream& s) {
+    if (!xch_.ptr) {
+      const size_t bytes = k::enc_exchange_bytes();
+      xch_.reserve(bytes);
+      k::zero_u32(ctx(s), xch_.as<unsigned>(), (int64_t)(bytes / 4));
+    }
+    return xch_.ptr;
+  }
 };
 
 // ------------------------------------------------------------------ ConvTranspose1D

@@ -1191,3 +1191,59 @@ def run_batch(seq, dev, stream, xx):
     o = seq.forward(nn.Tensor.from_numpy(dev, xx), stream)
     stream.sync(60000)
     return o
+
+
+@pytest.mark.parametrize("cin,cout,L,Ls,B", [
+    (2, 48, 343980, 20001, 1),  # first level (config 4): conv, GroupNorm, GELU, rewrite in one launch
+    (96, 192, 21499, 5003, 1),  # split-K conv + one-launch finish (config 4's third level)
+    (192, 384, 5375, 777, 2),   # fourth level's shape, batch 2
+])
+def test_encoder_one_launch_groupnorm(dev, stream, cin, cout, L, Ls, B):
+    """The encoder block's GroupNorm(1) forms whose workgroups exchange their statistics: the first
+    level in one launch (no statistics pass) and the split-K finish of the deeper levels (no
+    pre-norm y in HBM, no normalisation pass). Checked: the launches; the oracle; repeated calls
+    with a shorter input in between (the exchange buffer returns to zero after each launch); and
+    the bounded wait's other path, forced with a spin limit of 0 (workgroups that arrive before the
+    last one compute every partial themselves), which gives the same bits."""
+    say(f"encoder one-launch GroupNorm {cin}->{cout} L={L} B={B}, spin limit default and 0")
+    x = RNG.uniform(-1, 1, (B, cin, L)).astype(np.float32)
+    xs = RNG.uniform(-1, 1, (B, cin, Ls)).astype(np.float32)
+    w = (RNG.standard_normal((cout, cin, 8)) * np.sqrt(2 / (cin * 8))).astype(np.float32)
+    b = (0.3 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    rw = (RNG.standard_normal((2 * cout, cout, 1)) * np.sqrt(2 / cout)).astype(np.float32)
+    rb = (RNG.standard_normal(2 * cout) * 0.1).astype(np.float32)
+    blk = nn.UNetEncoderBlock(dev, cin, cout, 8, 4, 1, rewrite=True)
+    blk.load_weights(w, b, gm, bt, rw, rb)
+
+    def run(xx):
+        return run_layer(blk, xx, dev, stream)
+
+    names = _launch_names(dev, lambda: run(x))
+    tag = f"[c{cout}]"
+    if cin <= 4:
+        assert names == ["zero_u32", "enc_l1_oneshot_f32" + tag], names
+    else:
+        assert names == ["zero_u32", "enc_conv_f32" + tag, "enc_conv_reduce_gn_f32" + tag,
+                         "enc_rewrite_f32" + tag], names
+    first = run(x)
+    assert_close(first, oracle.encoder_block(x, w, b, gm, bt, 1, rewrite_w=rw, rewrite_b=rb),
+                 ATOL, RTOL, "one-launch GroupNorm")
+    rs = oracle.encoder_block(xs, w, b, gm, bt, 1, rewrite_w=rw, rewrite_b=rb)
+    first_s = run(xs)
+    assert_close(first_s, rs, ATOL, RTOL, "one-launch GroupNorm, shorter input")
+    for _ in range(2):
+        assert np.array_equal(run(x), first), "repeated one-launch calls differ"
+        assert np.array_equal(run(xs), first_s), "repeated one-launch calls differ (shorter)"
+    # self-computed statistics: the first level at full size too (two tasks per wave); the split-K
+    # finish on the shorter input (a workgroup that computes every partial reads every K part)
+    prev = _spin_limit(dev, 0)
+    try:
+        assert prev > 0
+        assert np.array_equal(run(xs), first_s), "self-computed statistics differ"
+        if cin <= 4:
+            assert np.array_equal(run(x), first), "self-computed statistics differ (full size)"
+    finally:
+        _spin_limit(dev, prev)
+    assert np.array_equal(run(x), first)
