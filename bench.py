@@ -260,26 +260,61 @@ def cpu_baseline(m, warmup=3, runs=10, budget_s=40.0):
 
 
 # ------------------------------------------------------------------ per-configuration table
-def time_gpu(fn, stream, reps=50, warmup=5):
-    """GPU ms of one call: `warmup` calls, then `reps` calls back to back, each bracketed by two
-    timing marks (HIP events) on the stream; the median of the per-call times."""
+def time_gpu(fn, stream, reps=50, warmup=5, sample_ms=0.1):
+    """GPU ms of one call: `warmup` calls, then `reps` samples, each a few calls back to back
+    bracketed by two timing marks (HIP events) on the stream, as many calls as make a sample of
+    about sample_ms (a mark pair costs a few microseconds, which would dominate a short call
+    timed alone); the median over the samples of their time per call."""
     import ctypes
     from metalaudio_amd._lib import check, lib
+    ms = ctypes.c_float()
+
+    def samples(n, calls):
+        for i in range(n):
+            check(lib().mnn_debug_stream_mark(stream.handle, 2 * i))
+            for _ in range(calls):
+                fn()
+            check(lib().mnn_debug_stream_mark(stream.handle, 2 * i + 1))
+        stream.sync()
+        ts = []
+        for i in range(n):
+            check(lib().mnn_debug_stream_mark_elapsed(stream.handle, 2 * i, 2 * i + 1,
+                                                      ctypes.byref(ms)))
+            ts.append(ms.value / calls)
+        return ts
     for _ in range(warmup):
         fn()
     stream.sync()
-    for i in range(reps):
-        check(lib().mnn_debug_stream_mark(stream.handle, 2 * i))
-        fn()
-        check(lib().mnn_debug_stream_mark(stream.handle, 2 * i + 1))
-    stream.sync()
-    ms = ctypes.c_float()
-    ts = []
-    for i in range(reps):
-        check(lib().mnn_debug_stream_mark_elapsed(stream.handle, 2 * i, 2 * i + 1,
-                                                  ctypes.byref(ms)))
-        ts.append(ms.value)
-    return statistics.median(ts)
+    est = statistics.median(samples(3, 1))
+    calls = int(min(20, max(1, -(-sample_ms // max(est, 1e-4)))))
+    time_gpu.calls = calls
+    return statistics.median(samples(reps, calls))
+
+
+class Floors:
+    """Measured floors for bandwidth-bound rows: one launch of the library's streaming kernel
+    (mnn_debug_stream_rw) reading and writing the row's algorithmic bytes, timed like the row
+    (event-timed median of 50), and an empty launch. A row's kernel time over its floor says how
+    far it is from what that traffic costs in one launch on this device."""
+
+    def __init__(self, nn, dev, stream, max_bytes=40 << 20):
+        from metalaudio_amd._lib import check, lib
+        self.check, self.lib, self.stream = check, lib, stream
+        n = max_bytes // 4
+        self.src = nn.Tensor.from_numpy(dev, np.ones(n, np.float32))
+        self.dst = nn.Tensor(dev, (n,))
+        self.empty_us = round(time_gpu(lambda: check(lib().mnn_debug_empty_launch(stream.handle)),
+                                       stream) * 1e3, 2)
+
+    def of(self, read_bytes, write_bytes, gpu_ms):
+        rd, wr = int(read_bytes) // 16 * 16, int(write_bytes) // 16 * 16
+
+        def fn():
+            self.check(self.lib().mnn_debug_stream_rw(self.src.handle, rd, self.dst.handle, wr,
+                                                      self.stream.handle))
+        us = time_gpu(fn, self.stream) * 1e3
+        return {"us": round(us, 2), "read_bytes": rd, "write_bytes": wr,
+                "empty_launch_us": self.empty_us, "frac_of_floor": round(us / (gpu_ms * 1e3), 4)}
 
 
 def kernel_table(dev):
@@ -474,13 +509,21 @@ def freq_decoder_oracle(oracle, dec):
 
 def config_table(nn, W, dev, stream, m, cpu=True):
     """GPU ms, achieved rate and roofline fraction of each BASELINE configuration, with the fp32
-    oracle's CPU time on the host beside it (the oracle is only the CPU baseline here)."""
+    oracle's CPU time on the host beside it (the oracle is only the CPU baseline here). gpu_ms:
+    median over 50 event-timed samples after 5 warm-up calls (time_gpu); `kernels`: the row's
+    per-kernel times from a kernel-timing pass; `floor`: the measured floor of a bandwidth-bound
+    row's traffic (Floors)."""
     if cpu:
         import oracle
     out = {}
 
-    def row(name, gpu_ms, flops=None, byts=None, prec="f32", cpu_ms=None, kernels=None):
-        r = {"gpu_ms": round(gpu_ms, 4)}
+    floors = Floors(nn, dev, stream)
+
+    def row(name, gpu_ms, flops=None, byts=None, prec="f32", cpu_ms=None, kernels=None,
+            floor=None):
+        r = {"gpu_ms": round(gpu_ms, 4), "calls_per_sample": getattr(time_gpu, "calls", 1)}
+        if floor is not None:
+            r["floor"] = floors.of(floor[0], floor[1], gpu_ms)
         if flops:
             r["tflops"] = round(flops / gpu_ms / 1e9, 2)
             r["mfma_frac"] = round(flops / (gpu_ms * 1e-3) / PEAK[prec], 4)
@@ -516,7 +559,7 @@ def config_table(nn, W, dev, stream, m, cpu=True):
         c1["gn_b"], dtype=np.float32), dtype=np.float32)) if cpu else None
     b1 = 4.0 * (2 * 44100 + 48 * 11024)
     row("1_conv_gn_gelu", time_gpu(f1, stream), flops=2.0 * 48 * 11024 * 16, byts=b1,
-        cpu_ms=cpu1, kernels=kernel_breakdown(dev, stream, f1, work={
+        cpu_ms=cpu1, floor=(4.0 * 2 * 44100, 4.0 * 48 * 11024), kernels=kernel_breakdown(dev, stream, f1, work={
             "conv_gn_oneshot_f32": (0, b1), "conv_gn_stats_f32": (0, 4.0 * 2 * 44100),
             "conv_gn_apply_f32": (0, b1)}))
 
@@ -549,7 +592,11 @@ def config_table(nn, W, dev, stream, m, cpu=True):
             prec=prec, cpu_ms=cpu2 if prec == "f32" else None,
             kernels=kernel_breakdown(dev, stream, f2, work=w2, prec=prec))
         row(f"2_linear_{prec}", time_gpu(lambda: lin.forward(xin, y2, stream), stream),
-            flops=g2[0], prec=prec, byts=g2[1])
+            flops=g2[0], prec=prec, byts=g2[1],
+            floor=(es * 2048 * 512 * 2, 4.0 * 2048 * 2048) if prec == "bf16" else None)
+    # the LayerNorm over 2048 features alone (16 MB read, 16 MB written)
+    row("2_layernorm_2048", time_gpu(lambda: ln.forward(y2, z2, stream), stream),
+        byts=8.0 * 2048 * 2048, floor=(4.0 * 2048 * 2048, 4.0 * 2048 * 2048))
 
     # config 3: pre-norm MHSA + FFN layer, S 2048, E 512
     c3 = W.config3()
@@ -631,10 +678,14 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     cpu10 = time_cpu(lambda: odsp.istft(X9, 4096, 1024, dtype=np.float32)) if cpu else None
     b9 = 4.0 * xs.size + spec_b
     row("9_stft_b1", time_gpu(fwd, stream), byts=b9, cpu_ms=cpu9,
+        floor=(4.0 * xs.size, spec_b),
         kernels=kernel_breakdown(dev, stream, fwd, work={"stft_forward_f32": (0, b9)}))
     frames_b = 4.0 * 2 * nf * 4096
     sig_b = 4.0 * 2 * plan.output_length(nf)
-    row("10_istft_b1", time_gpu(inv, stream), byts=spec_b + 2 * frames_b + sig_b, cpu_ms=cpu10,
+    # algorithmic bytes of the inverse: the spectra read, the signal written (the frames the
+    # first of its two kernels writes and the second reads are this build's intermediate)
+    row("10_istft_b1", time_gpu(inv, stream), byts=spec_b + sig_b, cpu_ms=cpu10,
+        floor=(spec_b, sig_b),
         kernels=kernel_breakdown(dev, stream, inv, work={
             "istft_frames_f32": (0, spec_b + frames_b),
             "istft_overlap_add_f32": (0, frames_b + sig_b)}))

@@ -59,6 +59,15 @@ mnn_status mnn_debug_kernel_timing_table(mnn_device dev, char* buf, size_t cap, 
 mnn_status mnn_debug_stream_mark(mnn_stream s, int index);
 mnn_status mnn_debug_stream_mark_elapsed(mnn_stream s, int from, int to, float* ms);
 
+/* Measurement floors, enqueued on s: mnn_debug_empty_launch runs an empty kernel (one workgroup
+ * of 64 threads); mnn_debug_stream_rw runs one kernel that reads the first read_bytes of src and
+ * writes write_bytes to dst (16-byte vectors, every load before the stores; both counts multiples
+ * of 16 within their tensors). Timed like a bandwidth-bound kernel of the same traffic, they give
+ * the lowest time that traffic takes in one launch on this device. */
+mnn_status mnn_debug_empty_launch(mnn_stream s);
+mnn_status mnn_debug_stream_rw(mnn_tensor src, int64_t read_bytes, mnn_tensor dst,
+                               int64_t write_bytes, mnn_stream s);
+
 /* Number of device allocations (hipMalloc) the library has made in this process: tensors, layer
  * weights and workspaces. The tests read it around a call to check that the call allocated
  * nothing (the allocation-free entry point). */

@@ -228,6 +228,8 @@ SIGNATURES = {
     "mnn_debug_launch_log": (C.c_int, [P, C.c_char_p, C.c_size_t, C.POINTER(C.c_size_t)]),
     "mnn_debug_set_grid_spin_limit": (C.c_int, [P, C.c_int, C.POINTER(C.c_int)]),
     "mnn_debug_device_allocations": (C.c_int, [I64P]),
+    "mnn_debug_empty_launch": (C.c_int, [P]),
+    "mnn_debug_stream_rw": (C.c_int, [P, C.c_int64, P, C.c_int64, P]),
     "mnn_debug_stream_mark": (C.c_int, [P, C.c_int]),
     "mnn_debug_kernel_timing_table": (C.c_int, [P, C.c_char_p, C.c_size_t,
                                                 C.POINTER(C.c_size_t)]),

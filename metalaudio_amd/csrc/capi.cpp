@@ -1243,6 +1243,33 @@ mnn_status mnn_debug_stream_mark_elapsed(mnn_stream st, int from, int to, float*
   });
 }
 
+mnn_status mnn_debug_empty_launch(mnn_stream st) {
+  return guard([&] {
+    MNN_REQUIRE(st, MNN_ERR_INVALID_ARGUMENT, "a stream is required");
+    Stream* s = S(st);
+    s->dev->check_alive();
+    s->dev->make_current();
+    k::floor_empty(LaunchCtx{s->dev, s->s});
+  });
+}
+
+mnn_status mnn_debug_stream_rw(mnn_tensor src, int64_t read_bytes, mnn_tensor dst,
+                               int64_t write_bytes, mnn_stream st) {
+  return guard([&] {
+    Tensor* a = T(src);
+    Tensor* b = T(dst);
+    MNN_REQUIRE(a->dev == b->dev, MNN_ERR_INVALID_ARGUMENT, "tensors on different devices");
+    MNN_REQUIRE(read_bytes >= 0 && write_bytes >= 0 && read_bytes % 16 == 0 &&
+                    write_bytes % 16 == 0 && (size_t)read_bytes <= a->bytes &&
+                    (size_t)write_bytes <= b->bytes,
+                MNN_ERR_INVALID_ARGUMENT, "byte counts must be multiples of 16 within the tensors");
+    a->dev->check_alive();
+    Stream s = resolve_stream(a->dev, st);
+    a->dev->make_current();
+    k::floor_stream(LaunchCtx{s.dev, s.s}, a->data, read_bytes, b->data, write_bytes);
+  });
+}
+
 mnn_status mnn_debug_device_allocations(int64_t* count) {
   return guard([&] {
     MNN_REQUIRE(count, MNN_ERR_INVALID_ARGUMENT, "count is required");

@@ -127,6 +127,51 @@ void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t ha
   launch(c, "glu_f32", glu_kernel, dim3(gx, (unsigned)batch), dim3(kThreads), 0, x, y, half);
 }
 
+// Floor kernels (measurement aids): an empty launch, and a streaming pass that reads rd and
+// writes wr 16-byte vectors (a copy where both apply, zeros past the read range, reads past the
+// write range kept alive by an empty asm use), four vectors per thread and iteration with every
+// load issued before the stores.
+__global__ void floor_empty_kernel() {}
+
+__global__ __launch_bounds__(kThreads) void floor_stream_kernel(const float4* __restrict__ src,
+                                                                int64_t rd,
+                                                                float4* __restrict__ dst,
+                                                                int64_t wr) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t n = rd > wr ? rd : wr;
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n; i0 += 4 * stride) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = i0 + u * stride;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (rd > 0) {
+        const float4 t = src[i < rd ? i : rd - 1];
+        if (i < rd) v[u] = t;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t i = i0 + u * stride;
+      if (i < wr) dst[i] = v[u];
+      else asm volatile("" ::"v"(v[u].x), "v"(v[u].y), "v"(v[u].z), "v"(v[u].w));
+    }
+  }
+}
+
+void floor_empty(const LaunchCtx& c) {
+  launch(c, "floor_empty", floor_empty_kernel, dim3(1), dim3(64), 0);
+}
+
+void floor_stream(const LaunchCtx& c, const void* src, int64_t read_bytes, void* dst,
+                  int64_t write_bytes) {
+  const int64_t rd = read_bytes / 16, wr = write_bytes / 16;
+  const int64_t n = rd > wr ? rd : wr;
+  if (n <= 0) return;
+  launch(c, "floor_stream", floor_stream_kernel, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0,
+         static_cast<const float4*>(src), rd, static_cast<float4*>(dst), wr);
+}
+
 void zero_u32(const LaunchCtx& c, unsigned* d, int64_t n) {
   if (n <= 0) return;
   launch(c, "zero_u32", zero_u32_kernel, dim3(grid_for(n)), dim3(kThreads), 0, d, n);

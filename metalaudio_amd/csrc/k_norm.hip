@@ -329,6 +329,70 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
   }
 }
 
+// Rows of exactly 256 * NV features, RPW rows per wave (rows w, w + W, ... for W waves in all),
+// software-pipelined: the next row's loads are issued before the current row is reduced and
+// stored, so its reads overlap this row's writes (with one row per wave, every wave loads at
+// once and then stores at once). Every load is unconditional (the row index is clamped), so the
+// compiler's waits count exactly the loads a use needs: the previous row's stores and the next
+// row's loads stay in flight. x, gamma and beta are plain pointers and a scheduling barrier
+// follows the loads: loads through restrict pointers count as invariant and were sunk past the
+// reduction. gamma / beta stay in registers for every row.
+template <int NV, int RPW>
+__global__ __launch_bounds__(kThreads) void layernorm_pipe_kernel(
+    const float* x, float* __restrict__ y, int64_t rows, const float* gamma, const float* beta,
+    float eps) {
+  constexpr int F = 256 * NV;
+  const int lane = threadIdx.x & 63;
+  const int64_t w0 = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int64_t W = (int64_t)gridDim.x * (kThreads / 64);
+  const float4* g4 = reinterpret_cast<const float4*>(gamma);
+  const float4* b4 = reinterpret_cast<const float4*>(beta);
+  float4 gv[NV], bv[NV], v[2][NV];
+  auto load_row = [&](int64_t row, float4 (&d)[NV]) {
+    const float4* xr = reinterpret_cast<const float4*>(x + min(row, rows - 1) * F);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) d[i] = xr[lane + 64 * i];
+  };
+  load_row(w0, v[0]);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    gv[i] = g4[lane + 64 * i];
+    bv[i] = b4[lane + 64 * i];
+  }
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int64_t row = w0 + k * W;
+    float4(&cur)[NV] = v[k & 1];
+    if (k + 1 < RPW) load_row(row + W, v[(k + 1) & 1]);
+    __builtin_amdgcn_sched_barrier(0);  // the loads above stay ahead of this row's work
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) s += (cur[i].x + cur[i].y) + (cur[i].z + cur[i].w);
+    const float mean = wave_sum(s) / (float)F;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const float a = cur[i].x - mean, b = cur[i].y - mean, c = cur[i].z - mean,
+                  d = cur[i].w - mean;
+      q += (a * a + b * b) + (c * c + d * d);
+    }
+    const float rstd = 1.f / sqrtf(wave_sum(q) / (float)F + eps);
+    // unconditional stores: a row past the last one was computed from the last row and writes
+    // the same bytes there (under a branch, the compiler's waits after it would also wait for
+    // these stores)
+    float4* yr = reinterpret_cast<float4*>(y + min(row, rows - 1) * F);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float4 o;
+      o.x = gv[i].x * ((cur[i].x - mean) * rstd) + bv[i].x;
+      o.y = gv[i].y * ((cur[i].y - mean) * rstd) + bv[i].y;
+      o.z = gv[i].z * ((cur[i].z - mean) * rstd) + bv[i].z;
+      o.w = gv[i].w * ((cur[i].w - mean) * rstd) + bv[i].w;
+      yr[lane + 64 * i] = o;
+    }
+  }
+}
+
 // gamma / beta are deliberately not __restrict__: loads through restrict pointers to constant
 // data count as invariant, and the compiler then moves them freely past the wait below.
 // DUAL: a second LayerNorm of the same rows (its own gamma2 / beta2 / eps2) into y2, so two
@@ -605,6 +669,12 @@ void layernorm(const LaunchCtx& c, const float* x, float* y, int64_t rows, int F
   // rows of 64 * NV floats: 16 lanes per row, DPP reductions
   if (vec && F % 64 == 0 && F <= 512)
     return layernorm_row16(c, x, rows, F, y, gamma, beta, eps, nullptr, nullptr, nullptr, 0.f);
+  if (vec && F == 2048 && rows >= 2 * 256 * (kThreads / 64)) {
+    // two rows per wave, pipelined (at least a full device of waves)
+    const dim3 pgrid((unsigned)cdiv(cdiv(rows, 2), kThreads / 64));
+    return launch(c, "layernorm_f32", layernorm_pipe_kernel<8, 2>, pgrid, block, 0, x, y, rows,
+                  gamma, beta, eps);
+  }
   if (vec && nv <= 8) {
     switch (nv) {
       case 1: return launch(c, "layernorm_f32", layernorm_reg_kernel<1>, grid, block, 0, x, y, rows, F, gamma, beta, eps);

@@ -17,6 +17,11 @@ void glu(const LaunchCtx& c, const float* x, float* y, int64_t batch, int64_t ha
 void copy_bytes(const LaunchCtx& c, const void* src, void* dst, int64_t bytes);
 // d[0 .. n) = 0, as a kernel on the stream (no memset node when the stream is captured).
 void zero_u32(const LaunchCtx& c, unsigned* d, int64_t n);
+// Measurement floors: an empty launch; one streaming pass reading read_bytes of src and writing
+// write_bytes to dst (16-byte aligned, multiples of 16).
+void floor_empty(const LaunchCtx& c);
+void floor_stream(const LaunchCtx& c, const void* src, int64_t read_bytes, void* dst,
+                  int64_t write_bytes);
 // fp32 -> bf16 bits, round to nearest even (NaN kept quiet), and bf16 -> fp32 (exact).
 void f32_to_bf16(const LaunchCtx& c, const float* x, uint16_t* y, int64_t n);
 void bf16_to_f32(const LaunchCtx& c, const uint16_t* x, float* y, int64_t n);
