@@ -25,33 +25,43 @@ using namespace dev;
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kStftLdsTwMaxN = 8192;  // LDS twiddles up to 64 KB of LDS per workgroup
-constexpr int kStftStageMaxN = 4096;  // inverse with the spectrum staged in LDS: 48 KB + 8 bytes
+constexpr int kStftLdsTwMaxN = 8192;  // LDS twiddles up to 68 KiB of LDS per workgroup (padded)
+constexpr int kStftStageMaxN = 4096;  // inverse with the spectrum staged in LDS: 51 KiB
 
 __device__ __forceinline__ float2 cmul(float2 a, float2 b) {
   return make_float2(a.x * b.x - a.y * b.y, a.x * b.y + a.y * b.x);
 }
+
+// LDS slot of complex element i of an LDS array (z, the twiddles in LDS): one padding slot per
+// 16 elements. The butterfly passes and the bit-reversed stores access 8-byte elements at
+// power-of-two strides, which without padding fall on a few of the LDS banks (counters showed
+// twice as many bank-conflict cycles as LDS instruction cycles).
+__device__ __forceinline__ int zp(int i) { return i + (i >> 4); }
+constexpr int zslots(int m) { return m + m / 16; }
 
 // In-place radix-2 DIT FFT of z[0..M) (bit-reversed input order) in LDS; inverse uses conjugate
 // twiddles (no scaling). tw[k] = e^{-2 pi i k / N}, N = 2M. Two consecutive stages h and 2h run
 // per barrier: a thread takes the group i0 + {0, h, 2h, 3h} (i0 = 4h q + p, p < h) through stage
 // h (pairs (i0, i0+h), (i0+2h, i0+3h), twiddle W_2h^p) and stage 2h (pairs (i0, i0+2h) with
 // W_4h^p, (i0+h, i0+3h) with W_4h^(p+h)), the same operations in the same order as two radix-2
-// passes; an odd stage count ends with one radix-2 pass.
+// passes; an odd stage count ends with one radix-2 pass. z is addressed through zp(); TWP: tw is
+// the padded LDS copy (zp()), else the plain global table.
+template <bool TWP>
 __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse) {
+  auto twd = [&](int i) { return tw[TWP ? zp(i) : i]; };
   int h = 1;
   for (; 2 * h < M; h <<= 2) {
     const int s1 = M / h, s2 = M / (2 * h);  // W_2h^p = tw[p * s1], W_4h^p = tw[p * s2]
     for (int t = threadIdx.x; t < M / 4; t += kThreads) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 2) + p;
-      float2 w1 = tw[p * s1], w2 = tw[p * s2], w3 = tw[p * s2 + M / 2];
+      float2 w1 = twd(p * s1), w2 = twd(p * s2), w3 = twd(p * s2 + M / 2);
       if (inverse) {
         w1.y = -w1.y;
         w2.y = -w2.y;
         w3.y = -w3.y;
       }
-      float2 a0 = z[i0], a1 = z[i0 + h], a2 = z[i0 + 2 * h], a3 = z[i0 + 3 * h];
+      float2 a0 = z[zp(i0)], a1 = z[zp(i0 + h)], a2 = z[zp(i0 + 2 * h)], a3 = z[zp(i0 + 3 * h)];
       float2 bb = cmul(a1, w1);
       a1 = make_float2(a0.x - bb.x, a0.y - bb.y);
       a0 = make_float2(a0.x + bb.x, a0.y + bb.y);
@@ -59,11 +69,11 @@ __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool in
       a3 = make_float2(a2.x - bb.x, a2.y - bb.y);
       a2 = make_float2(a2.x + bb.x, a2.y + bb.y);
       bb = cmul(a2, w2);
-      z[i0 + 2 * h] = make_float2(a0.x - bb.x, a0.y - bb.y);
-      z[i0] = make_float2(a0.x + bb.x, a0.y + bb.y);
+      z[zp(i0 + 2 * h)] = make_float2(a0.x - bb.x, a0.y - bb.y);
+      z[zp(i0)] = make_float2(a0.x + bb.x, a0.y + bb.y);
       bb = cmul(a3, w3);
-      z[i0 + 3 * h] = make_float2(a1.x - bb.x, a1.y - bb.y);
-      z[i0 + h] = make_float2(a1.x + bb.x, a1.y + bb.y);
+      z[zp(i0 + 3 * h)] = make_float2(a1.x - bb.x, a1.y - bb.y);
+      z[zp(i0 + h)] = make_float2(a1.x + bb.x, a1.y + bb.y);
     }
     __syncthreads();
   }
@@ -72,11 +82,11 @@ __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool in
     for (int t = threadIdx.x; t < M / 2; t += kThreads) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 1) + p, i1 = i0 + h;
-      float2 w = tw[p * stride];
+      float2 w = twd(p * stride);
       if (inverse) w.y = -w.y;
-      const float2 a = z[i0], b = cmul(z[i1], w);
-      z[i0] = make_float2(a.x + b.x, a.y + b.y);
-      z[i1] = make_float2(a.x - b.x, a.y - b.y);
+      const float2 a = z[zp(i0)], b = cmul(z[zp(i1)], w);
+      z[zp(i0)] = make_float2(a.x + b.x, a.y + b.y);
+      z[zp(i1)] = make_float2(a.x - b.x, a.y - b.y);
     }
     __syncthreads();
   }
@@ -104,7 +114,7 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
   const int b = blockIdx.y;
   if (f >= a.frames) return;
   const int M = a.N / 2;
-  float2* tws = z + M;
+  float2* tws = z + zslots(M);
   const float* xs = a.x + (int64_t)b * a.n + (int64_t)f * a.hop;
   // every load of a batch of 8 samples pairs per thread (clamped indices) before any LDS store
   for (int m0 = threadIdx.x; m0 < M; m0 += 8 * kThreads) {
@@ -123,22 +133,22 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
     for (int u = 0; u < 8; ++u) {
       const int m = m0 + u * kThreads;
       if (m < M) {
-        z[bitrev(m, a.logM)] = make_float2(xe[u] * we[u], xo[u] * wo[u]);
-        if (LDS_TW) tws[m] = tv[u];
+        z[zp(bitrev(m, a.logM))] = make_float2(xe[u] * we[u], xo[u] * wo[u]);
+        if (LDS_TW) tws[zp(m)] = tv[u];
       }
     }
   }
   __syncthreads();
-  fft_lds(z, M, LDS_TW ? tws : a.tw, false);
+  fft_lds<LDS_TW>(z, M, LDS_TW ? tws : a.tw, false);
   const int bins = a.onesided ? M + 1 : a.N;
   const int64_t base = (int64_t)b * a.frames * bins;
   for (int k = threadIdx.x; k <= M; k += kThreads) {
-    const float2 zk = z[k == M ? 0 : k];
-    const float2 zc = z[k == 0 ? 0 : M - k];  // Z[M-k], conjugated below
+    const float2 zk = z[zp(k == M ? 0 : k)];
+    const float2 zc = z[zp(k == 0 ? 0 : M - k)];  // Z[M-k], conjugated below
     const float2 fe = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y - zc.y));
     const float2 d = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y + zc.y));  // (Zk - conj Zc)/2
     const float2 fo = make_float2(d.y, -d.x);                                    // -i * d
-    const float2 w = k == M ? make_float2(-1.f, 0.f) : (LDS_TW ? tws[k] : a.tw[k]);
+    const float2 w = k == M ? make_float2(-1.f, 0.f) : (LDS_TW ? tws[zp(k)] : a.tw[k]);
     const float2 t = cmul(w, fo);
     const float re = fe.x + t.x, im = fe.y + t.y;
     auto put = [&](int kk, float r, float i) {
@@ -162,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
   const int b = blockIdx.y;
   if (f >= a.frames) return;
   const int M = a.N / 2;
-  float2* tws = z + M;
+  float2* tws = z + zslots(M);
   const int bins = a.onesided ? M + 1 : a.N;
   const int64_t base = (int64_t)b * a.frames * bins;
   auto get = [&](int kk) {
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
     return h;
   };
   if constexpr (STAGE) {
-    float2* xs = z + a.N;  // X[0 .. M]
+    float2* xs = z + 2 * zslots(M);  // X[0 .. M]
     // every load of a batch of 4 bins per thread (clamped indices) before any LDS store
     for (int k0 = threadIdx.x; k0 <= M; k0 += 4 * kThreads) {
       float2 g[4];
@@ -196,10 +206,10 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
       const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
       const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
       const float2 t = a.tw[k];
-      tws[k] = t;
+      tws[zp(k)] = t;
       const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
       const float2 fo = cmul(d, w);
-      z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+      z[zp(bitrev(k, a.logM))] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
     }
   }
   // every load of a batch of 4 bins per thread (clamped indices) before any LDS store
@@ -226,18 +236,18 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
       const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
       const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
       const float2 t = tv[u];
-      if (LDS_TW) tws[k] = t;
+      if (LDS_TW) tws[zp(k)] = t;
       const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
       const float2 fo = cmul(d, w);
-      z[bitrev(k, a.logM)] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+      z[zp(bitrev(k, a.logM))] = make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
     }
   }
   __syncthreads();
-  fft_lds(z, M, LDS_TW ? tws : a.tw, true);
+  fft_lds<LDS_TW>(z, M, LDS_TW ? tws : a.tw, true);
   const float s = 1.f / (float)M;
   float* out = a.frames_buf + ((int64_t)b * a.frames + f) * a.N;
   for (int m = threadIdx.x; m < M; m += kThreads) {
-    const float2 v = z[m];
+    const float2 v = z[zp(m)];
     out[2 * m] = (v.x * s) * a.win[2 * m];
     out[2 * m + 1] = (v.y * s) * a.win[2 * m + 1];
   }
@@ -279,12 +289,13 @@ void stft_forward(const LaunchCtx& c, const StftArgs& a) {
                   (int64_t)(a.frames - 1) * a.hop + a.N <= a.n,
               MNN_ERR_INVALID_ARGUMENT, "stft_forward: frames exceed the signal");
   const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
+  const int zs = zslots(a.N / 2);
   if (a.N <= kStftLdsTwMaxN)
     launch(c, "stft_forward_f32", stft_forward_kernel<true>, grid, dim3(kThreads),
-           sizeof(float2) * a.N, a);
+           sizeof(float2) * 2 * zs, a);
   else
     launch(c, "stft_forward_f32", stft_forward_kernel<false>, grid, dim3(kThreads),
-           sizeof(float2) * (a.N / 2), a);
+           sizeof(float2) * zs, a);
 }
 
 void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
@@ -292,15 +303,16 @@ void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
   MNN_REQUIRE(a.cre && a.cim && a.frames_buf && a.y, MNN_ERR_INVALID_ARGUMENT,
               "stft_inverse: missing buffers");
   const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
+  const int zs = zslots(a.N / 2);
   if (a.onesided && a.N <= kStftStageMaxN)
     launch(c, "istft_frames_f32", stft_inverse_kernel<true, true>, grid, dim3(kThreads),
-           sizeof(float2) * (a.N + a.N / 2 + 1), a);
+           sizeof(float2) * (2 * zs + a.N / 2 + 1), a);
   else if (a.N <= kStftLdsTwMaxN)
     launch(c, "istft_frames_f32", stft_inverse_kernel<true, false>, grid, dim3(kThreads),
-           sizeof(float2) * a.N, a);
+           sizeof(float2) * 2 * zs, a);
   else
     launch(c, "istft_frames_f32", stft_inverse_kernel<false, false>, grid, dim3(kThreads),
-           sizeof(float2) * (a.N / 2), a);
+           sizeof(float2) * zs, a);
   const int64_t L = (int64_t)(a.frames - 1) * a.hop + a.N;
   launch(c, "istft_overlap_add_f32", stft_overlap_add_kernel,
          dim3((unsigned)cdiv(L, kThreads), (unsigned)a.batch), dim3(kThreads), 0, a);
