@@ -796,6 +796,7 @@ def main():
             log(f"launch log: status {rc}")
             sys.exit(1)
         text = buf.value.decode()
+        Path(args.profile_step).parent.mkdir(parents=True, exist_ok=True)
         Path(args.profile_step).write_text(text)
         work = encoder_work("enc_conv_reduce_gn" in text, "enc_l1_oneshot" in text)
         work = {k: [v[0] * 4, v[1] * 4] for k, v in work.items()}

@@ -227,7 +227,10 @@ typedef struct mnn_encoder_block_desc {
 /* UNetEncoderBlock (UNet.swift:11-174): DynamicConv1D(reflect (k-1)/2) -> GroupNorm -> GELU
  * [-> 1x1 conv C->2C -> GLU]. Weights "conv.weight", "conv.bias", "norm.weight", "norm.bias",
  * "rewrite.weight" [2C, C, 1], "rewrite.bias" [2C]. Input [C, L] or [B, C, L]. The skip output of
- * the reference is the block output itself (UNet.swift:96-97). */
+ * the reference is the block output itself (UNet.swift:96-97). With GroupNorm(1) and the rewrite
+ * (fp32), a grid the device holds at once normalises in one launch per level: the workgroups
+ * exchange their statistics through the block's own exchange buffer, so forwards of one block
+ * must not overlap on two streams (as its workspaces are shared). */
 mnn_status mnn_encoder_block_create(mnn_device dev, const mnn_encoder_block_desc* desc,
                                     mnn_layer* out);
 
@@ -504,8 +507,11 @@ mnn_status mnn_layer_infer_output_shape(mnn_layer layer, int in_rank, const int6
 
 /* ---------------------------------------------------------------- sequential
  * Sequential (Model.swift:65-357). The model references layers; it does not own them.
- * A Conv1D without activation followed by GroupNorm(1 group) [and GELU] runs as one fused group
- * (convolution with GroupNorm statistics in its epilogue, then one apply pass); the results are
+ * A Conv1D without activation followed by GroupNorm(1 group) [and GELU] runs as one fused group:
+ * for a small contraction whose grid the device holds at once, one launch in which the
+ * workgroups exchange their statistics partials through the GroupNorm layer's exchange buffer
+ * (so a GroupNorm layer's forwards must not overlap on two streams); otherwise the convolution
+ * with statistics from its epilogue (or a statistics pass), then one apply pass. The results are
  * those of the layers run one by one. */
 mnn_status mnn_sequential_create(mnn_device dev, mnn_sequential* out);
 mnn_status mnn_sequential_destroy(mnn_sequential seq);

@@ -2306,12 +2306,7 @@ class CrossTransformerImpl : public Layer {
   size_t next_event_ = 0;
 };
 
-// ------------------------------------------------------------------ Sequential fusion
-// Conv1D (no activation, no residual) -> GroupNorm(1 group) [-> GELU] inside a Sequential runs
-// as two launches: the convolution writes its output and GroupNorm statistics partials from its
-// epilogue, then one apply pass merges the partials and writes act(GroupNorm(y)) into the last
-// layer's buffer. Results are those of the layers run one by one (GELU's +-10 clamp and the
-// tanh form agree to float precision beyond |x| = 10).
+// ------------------------------------------------------------------ CrossTransformerEncoder
 // CrossTransformerEncoder with the reference class's own layer structure (TransformerLayer,
 // Transformer.swift:370-560; the encoder's layer loop :626-667). Per layer, in this order:
 //   T += SA_t(LN_ts(T))       (:467-470)
@@ -2428,6 +2423,15 @@ class CrossTransformerEncoderImpl : public Layer {
   DevBuf ht_, hf_;
 };
 
+// ------------------------------------------------------------------ Sequential fusion
+// Conv1D (no activation, no residual) -> GroupNorm(1 group) [-> GELU] inside a Sequential runs as
+// one group. A small contraction (register-window conv) whose grid the device holds at once runs
+// in one launch: each workgroup keeps its conv tile in registers and the workgroups exchange their
+// statistics partials through the GroupNorm layer's own exchange buffer (tagged words, bounded
+// wait); a larger grid takes a statistics pass and an apply pass that recomputes the conv. Other
+// convs write their output and statistics partials from the conv's epilogue, then one apply pass
+// writes act(GroupNorm(y)). Results are those of the layers run one by one (GELU's +-10 clamp and
+// the tanh form agree to float precision beyond |x| = 10).
 int fused_chain_length(const std::vector<Layer*>& v, size_t i) {
   if (i + 1 >= v.size()) return 1;
   auto* c = dynamic_cast<Conv1DLayer*>(v[i]);
