@@ -41,6 +41,10 @@ FAMILIES = [
     ("attn_generic_kernel", "attn_fwd"),
     ("enc_l1_stats_kernel", "enc_l1_stats_f32"),
     ("enc_l1_fused_kernel", "enc_l1_fused_f32"),
+    ("enc_l1_oneshot_kernel", "enc_l1_oneshot_f32"),
+    ("enc_reduce_gn_t_kernel", "enc_conv_reduce_gn_f32"),
+    ("floor_empty_kernel", "floor_empty"),
+    ("floor_stream_kernel", "floor_stream"),
     ("conv_gn_oneshot_kernel", "conv_gn_oneshot_f32"),
     ("conv_gn_stats_kernel", "conv_gn_stats_f32"),
     ("zero_u32_kernel", "zero_u32"),
