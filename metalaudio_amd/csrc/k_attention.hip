@@ -58,8 +58,14 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = lane >> 4, l16 = lane & 15;
-  const int b = blockIdx.z, h = blockIdx.y;
-  const int qw0 = blockIdx.x * BQ + wave * QW;
+  // XCD-aware numbering (workgroups go round robin over the 8 XCDs): consecutive logical work
+  // units, query blocks fastest, land on one XCD, so the query blocks of one (batch, head) share
+  // its K and V in that XCD's L2 instead of every XCD streaming every head's K and V
+  const int nq = gridDim.x, nh = gridDim.y;
+  const int unit = xcd_logical_tile(blockIdx.x + nq * (blockIdx.y + nh * blockIdx.z),
+                                    nq * nh * gridDim.z);
+  const int qblk = unit % nq, h = (unit / nq) % nh, b = unit / (nq * nh);
+  const int qw0 = qblk * BQ + wave * QW;
 
   const float* __restrict__ qb = a.q + (int64_t)b * a.q_bs + h * HD;
   const float* __restrict__ kb = a.k + (int64_t)b * a.kv_bs + h * HD;
