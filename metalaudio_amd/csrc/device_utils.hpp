@@ -458,58 +458,21 @@ __device__ __forceinline__ float2 gn1_merge_one_round(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------- grid-wide statistics exchange
-// One-launch GroupNorm(1): every workgroup publishes the (mean, M2) of its tile, waits until it
-// has seen every partial of its batch, and merges them itself. No cache maintenance is used (an
-// agent-scope acquire fence per wave and a release fence per workgroup cost more than the rest of
-// such kernels): a partial is two 64-bit words (kTileTag << 32 | mean bits), (kTileTag << 32 |
-// M2 bits), each stored and loaded as one relaxed device-scope atomic, so a reader sees either a
-// whole published word or a cleared one. The count of a partial follows from the geometry and is
-// not exchanged.
+// One-launch GroupNorm: every workgroup of a grid that the device holds at once publishes the
+// (mean, M2) of its tile, and the batch's statistics are merged from all of them (xch_merge)
+// before any workgroup normalises. No cache maintenance is used (an agent-scope acquire fence
+// per wave and a release fence per workgroup cost more than the rest of such kernels): a
+// partial is two 64-bit words (tag << 32 | mean bits), (tag << 32 | M2 bits), each stored and
+// loaded as one relaxed device-scope atomic, so a reader sees either a whole word of this launch
+// or one with another tag. The count of a partial follows from the geometry and is not exchanged.
 //
-// Exchange buffer layout (64-bit words): word 0 (low half) counts the workgroups out of the
-// launch; partial slots start at word 8, two words per partial, batch b's partial v at slot
-// b * nparts + v. The buffer is zero before a launch; the last workgroup out clears the slots and
-// the count, so the next launch finds it zero again. Launches that share a buffer must not
-// overlap. The host launches these kernels only when the whole grid is resident at once; each
-// wait is still bounded (xch_collect), and a workgroup that gives up computes every partial
-// itself by the same code as their owners (so the same bits).
-constexpr unsigned kTileTag = 1u;  // high half of a published word (cleared words read 0)
-
-__device__ __forceinline__ void put_tagged(unsigned long long* s, float lo) {
-  __hip_atomic_store(s, ((unsigned long long)kTileTag << 32) | __float_as_uint(lo),
-                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Polls the nparts <= NT * PER partials at `slots` (NT threads, each its share) into sp[] until
-// all are published; returns true when spin_limit polls passed without that (the caller then
-// computes the partials itself). Every thread returns the same value. A thread's PER pairs of
-// words are loaded together (clamped addresses, straight-line code), so one poll costs one round
-// trip to the coherence point, not PER.
-template <int NT, int PER>
-__device__ __forceinline__ bool xch_collect(const unsigned long long* slots, int nparts,
-                                            float2* sp, int spin_limit) {
-  for (int polls = 0;; ++polls) {
-    unsigned long long a[PER], c[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int v = min((int)threadIdx.x + i * NT, nparts - 1);
-      a[i] = __hip_atomic_load(slots + 2 * v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      c[i] = __hip_atomic_load(slots + 2 * v + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int v = (int)threadIdx.x + i * NT;
-      if (v < nparts) {
-        ok = ok && (unsigned)(a[i] >> 32) == kTileTag && (unsigned)(c[i] >> 32) == kTileTag;
-        sp[v] = make_float2(__uint_as_float((unsigned)a[i]), __uint_as_float((unsigned)c[i]));
-      }
-    }
-    if (!__syncthreads_or(!ok)) return false;
-    if (polls >= spin_limit) return true;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
+// Two ways to collect, by grid size. With up to a few hundred workgroups every workgroup polls
+// every partial and merges them itself (fewest round trips). With more, that polling makes
+// traffic at the coherence point that grows with the square of the grid (each 8-byte
+// device-scope load is a transaction of its own), so workgroup 0 of each batch is the merger:
+// it polls the partials, merges them and publishes one result pair (mean, rstd), which is all
+// the others poll. Neither keeps a count by read-modify-writes on one word: those are
+// serialised where the word lives (tens of ns each), microseconds at these grids.
 
 // Merge of the collected (mean, M2) partials in a fixed order, in every wave of the caller (no
 // barrier): fp64 sums over the partials by lane, then over the wave; count(v) is partial v's
@@ -535,43 +498,18 @@ __device__ __forceinline__ float2 xch_merge(const float2* sp, int nparts, CountF
   return make_float2((float)mean, rstd);
 }
 
-// Counts the calling workgroup out of the launch (its reads of the slots are done); the last one
-// out clears the 2 * total slot words and the count. s_last: an int of LDS.
-template <int NT>
-__device__ __forceinline__ void xch_count_out(unsigned long long* xch, unsigned total,
-                                              int* s_last) {
-  unsigned* ctl = reinterpret_cast<unsigned*>(xch);
-  if (threadIdx.x == 0)
-    *s_last = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-              total - 1;
-  lds_barrier();
-  if (*s_last) {
-    unsigned long long* all = xch + 8;
-    for (int i = threadIdx.x; i < 2 * (int)total; i += NT)
-      __hip_atomic_store(all + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (threadIdx.x == 0) __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-}
-
-// ---------------------------------------------------------------- exchange with one merger
-// A variant of the exchange above for grids of several hundred workgroups. There every waiting
-// workgroup polling every partial makes traffic at the coherence point that grows with the square
-// of the grid (each 8-byte device-scope load is a transaction of its own), and any count kept by
-// read-modify-writes on one word serialises there (tens of ns each). Here workgroup 0 of each
-// batch is the merger: every workgroup publishes its partial (two tagged words, no wait, no
-// read-modify-write); the merger polls the batch's partials, merges them and publishes one result
-// pair (mean, rstd), which is all the others poll.
+// Epoch tags: words carry a per-batch epoch tag instead of being cleared. Every workgroup reads
+// the batch's epoch E at its start and tags its words (E mod 2^31) + 1. Once workgroup 0 of the
+// batch has seen every partial, every workgroup has read E, so it advances the epoch then (the
+// merger; in the poll-everything form, workgroup 0 as well). Stale words of earlier launches
+// (graph replays included) never carry the current tag, so nothing is cleared and no workgroup
+// counts out.
 //
-// Words carry a per-batch epoch tag instead of being cleared: every workgroup reads the batch's
-// epoch E at its start and tags its words (E mod 2^31) + 1. Once the merger has seen every
-// partial, every workgroup has read E, so it advances the epoch then. Stale words of earlier
-// launches (graph replays included) never carry the current tag, and no workgroup counts out.
-//
-// Termination: every workgroup publishes before it waits, and the others' waits are bounded
-// (a workgroup whose wait runs out computes every partial itself, by the same code as their
-// owners, so the same bits). So the merger's wait, which is not bounded (it must see every
-// partial before it may advance the epoch), ends once every workgroup has run: if the grid is not
-// resident at once, the bounded waiters finish and free their slots for the rest.
+// Termination: every workgroup publishes before it waits, and the waits of all but workgroup 0
+// are bounded (a workgroup whose wait runs out computes every partial itself, by the same code
+// as their owners, so the same bits). So workgroup 0's wait, which is not bounded (it must see
+// every partial before it may advance the epoch), ends once every workgroup has run: if the grid
+// is not resident at once, the bounded waiters finish and free their slots for the rest.
 //
 // Buffer layout (64-bit words): batch b's epoch at word 4 b (low half), its result at 4 b + 2
 // (tag | mean bits) and 4 b + 3 (tag | rstd bits); partial slots from word 4 * kXmMaxBatch, two
@@ -607,13 +545,16 @@ __device__ __forceinline__ void xm_put(unsigned long long* xch, int b, int npart
   put_tag(sl + 1, tag, m2);
 }
 
-// The merger: polls the nparts partials of batch b into sp[] (NT threads, PER per thread, loaded
-// together) until every one carries this launch's tag.
+// Polls the nparts partials of batch b into sp[] (NT threads, PER per thread, loaded together)
+// until every one carries this launch's tag; spin_limit < 0: without bound (the merger, which
+// must see every partial before it may advance the epoch). Returns false when spin_limit polls
+// passed without that (the caller then computes the partials itself); every thread returns the
+// same value.
 template <int NT, int PER>
-__device__ __forceinline__ void xm_collect(unsigned long long* xch, int b, int nparts,
-                                           unsigned tag, float2* sp) {
+__device__ __forceinline__ bool xm_collect(unsigned long long* xch, int b, int nparts,
+                                           unsigned tag, float2* sp, int spin_limit = -1) {
   const unsigned long long* slots = xm_slots(xch, b, nparts);
-  for (;;) {
+  for (int polls = 0;; ++polls) {
     bool ok = true;
     for (int v0 = 0; v0 < nparts; v0 += NT * PER) {
       unsigned long long a[PER], c[PER];
@@ -632,9 +573,16 @@ __device__ __forceinline__ void xm_collect(unsigned long long* xch, int b, int n
         }
       }
     }
-    if (!__syncthreads_or(!ok)) return;
+    if (!__syncthreads_or(!ok)) return true;
+    if (spin_limit >= 0 && polls >= spin_limit) return false;
     __builtin_amdgcn_s_sleep(1);
   }
+}
+
+// Advances batch b's epoch (thread 0 of a workgroup that has seen every partial of the launch).
+__device__ __forceinline__ void xm_advance(unsigned long long* xch, int b, unsigned tag) {
+  __hip_atomic_store(reinterpret_cast<unsigned*>(xm_batch(xch, b)), tag & 0x7fffffffu,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The merger, with the merged result: publishes it and advances the batch's epoch (thread 0).
@@ -643,8 +591,7 @@ __device__ __forceinline__ void xm_publish(unsigned long long* xch, int b, unsig
   unsigned long long* w = xm_batch(xch, b);
   put_tag(w + 2, tag, mr.x);
   put_tag(w + 3, tag, mr.y);
-  __hip_atomic_store(reinterpret_cast<unsigned*>(w), tag & 0x7fffffffu, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+  xm_advance(xch, b, tag);
 }
 
 // Every other workgroup: polls batch b's result pair (one thread, broadcast through `s_res`)

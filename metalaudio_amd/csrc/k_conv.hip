@@ -367,11 +367,15 @@ __global__ __launch_bounds__(kThreads) void conv_gn_apply_kernel(
 
 // Both passes in one launch. Each workgroup computes a tile of COB channels x 256 positions of
 // the convolution into registers (SPLIT x 256 threads, COB / SPLIT channels each) and publishes
-// the tile's statistics partial; it then collects every partial of its batch through the
-// grid-wide exchange of device_utils.hpp (tagged words, bounded wait), merges them and writes the
-// normalised output from the registers it kept. A workgroup whose wait runs out computes every
-// partial of its batch itself (the same code on the same inputs as their owners, so the same
-// bits), so each workgroup ends with the same result whatever the scheduling.
+// the tile's statistics partial; it then collects every partial of its batch (each workgroup
+// polls them all: at this grid size that is fewer round trips than waiting for one merger),
+// merges them and writes the normalised output from the registers it kept. The words carry the
+// batch's epoch tag (device_utils.hpp, exchange with one merger), so nothing is cleared and no
+// workgroup counts out (one read-modify-write per workgroup on one word serialised at the end of
+// the kernel); workgroup 0 of the batch waits without bound and, having seen every partial,
+// advances the epoch. The others' waits are bounded: a workgroup whose wait runs out computes
+// every partial of its batch itself (the same code on the same inputs as their owners, so the
+// same bits), so each workgroup ends with the same result whatever the scheduling.
 constexpr int kOneMaxParts = 1024;  // partials per batch (LDS: 8 bytes each)
 constexpr int kOneMaxSlots = 4096;  // partials over all batches
 
@@ -416,14 +420,14 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
   __shared__ __attribute__((aligned(16))) float wt[Stage::N];  // weights, bias, gamma, beta
   __shared__ float red[2 * NW];
   __shared__ float2 sp[kOneMaxParts];  // (mean, M2) of every partial of this batch
-  __shared__ int s_last;
+  __shared__ unsigned s_tag;
   const int b = blockIdx.z, cob0 = blockIdx.y * COB;
   const int pos = threadIdx.x & (kThreads - 1), part = threadIdx.x / kThreads;  // part: per wave
   const int t = blockIdx.x * kThreads + pos;
   const bool valid = t < p.Lout;
   const int nparts = gridDim.x * gridDim.y;
   const float* xb = x + (int64_t)b * p.Cin * p.Lin;
-  unsigned long long* slots = xch + 8 + 2 * (int64_t)b * nparts;
+  if (threadIdx.x == 0) s_tag = xm_tag(xch, b);  // read after the barrier below
   Stage st;
   st.fetch(w, cob0, bias, gamma, beta, 0.f, 1.f, 0.f);
   float xv[CK];
@@ -445,21 +449,18 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
       acc[j4 + 3] = fmaf(xv[e], w4.w, acc[j4 + 3]);
     }
   auto tile_count = [&](int vx) { return (float)(COB * min(kThreads, p.Lout - vx * kThreads)); };
+  const unsigned tag = s_tag;
+  const bool advancer = blockIdx.x == 0 && blockIdx.y == 0;
   {
     float mean, m2;
     tile_stats<CPT, NW>(acc, valid, tile_count(blockIdx.x), red, mean, m2);
-    if (threadIdx.x == 0) {
-      const int me = blockIdx.y * gridDim.x + blockIdx.x;
-      put_tagged(slots + 2 * me, mean);
-      put_tagged(slots + 2 * me + 1, m2);
-    }
+    if (threadIdx.x == 0) xm_put(xch, b, nparts, blockIdx.y * gridDim.x + blockIdx.x, tag, mean, m2);
   }
   // collect: every thread polls its share of the partials until all are published
-  const bool late = xch_collect<NT, (kOneMaxParts + NT - 1) / NT>(slots, nparts, sp, spin_limit);
+  const bool late = !xm_collect<NT, (kOneMaxParts + NT - 1) / NT>(xch, b, nparts, tag, sp,
+                                                                   advancer ? -1 : spin_limit);
+  if (advancer && threadIdx.x == 0) xm_advance(xch, b, tag);
   if (late) {
-    // this workgroup never saw its own partial published: let the store land before the
-    // workgroup can count out (the last one out clears the slots)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // compute every partial of this batch here, each as its owner computes it (weights and bias
     // read from global memory hold the values the owner staged in LDS; the fmaf order over the
     // taps is the same)
@@ -511,8 +512,6 @@ __global__ __launch_bounds__(kThreads * SPLIT) void conv_gn_oneshot_kernel(
       }
     }
   }
-  // count this workgroup out; the last one out clears every slot of the launch and the count
-  xch_count_out<NT>(xch, gridDim.x * gridDim.y * gridDim.z, &s_last);
 }
 
 // Register-window variant applies when groups = 1, Cin*K is 8, 16, 24 or 32, Cout % 16 == 0
@@ -645,7 +644,7 @@ bool oneshot_dispatch(const LaunchCtx& c, const ConvParams& p, bool go, const fl
   }();
   const dim3 grid(cdiv(p.Lout, kThreads), p.Cout / kOneCob, p.B);
   const int64_t nparts = (int64_t)grid.x * grid.y, blocks = nparts * grid.z;
-  if (nparts > kOneMaxParts || blocks > kOneMaxSlots ||
+  if (nparts > kOneMaxParts || blocks > kOneMaxSlots || grid.z > (unsigned)kXmMaxBatch ||
       blocks > (int64_t)per_cu * c.dev->props.multiProcessorCount)
     return false;
   if (go)
@@ -679,11 +678,18 @@ bool oneshot(const LaunchCtx& c, const ConvParams& p0, bool go, const float* x, 
 }
 }  // namespace
 
-size_t conv_gn_oneshot_exchange_bytes() { return 8 * (8 + 2 * (size_t)kOneMaxSlots); }
+size_t conv_gn_oneshot_exchange_bytes() {
+  return 8 * (4 * (size_t)kXmMaxBatch + 2 * (size_t)kOneMaxSlots);
+}
 
 bool conv_gn_oneshot_fits(const LaunchCtx& c, const ConvParams& p) {
-  return oneshot(c, p, false, nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr, 0.f, 0,
-                 nullptr);
+  // tuning override: MNN_CONV_GN_ONESHOT=0 takes the two-pass form wherever it applies
+  static const bool off = [] {
+    const char* e = std::getenv("MNN_CONV_GN_ONESHOT");
+    return e && std::atoi(e) == 0;
+  }();
+  return !off && oneshot(c, p, false, nullptr, nullptr, nullptr, nullptr, 0, nullptr, nullptr,
+                         0.f, 0, nullptr);
 }
 
 void conv_gn_oneshot(const LaunchCtx& c, const ConvParams& p, const float* x, const float* w,
