@@ -5,15 +5,17 @@
 // divides by the overlap-added squared window floored at `floor` (values below FLT_MIN counted as
 // zero first).
 //
-// One workgroup per (signal, frame). A real N-point DFT is computed as a complex M = N/2-point
-// FFT of z[m] = x[2m] + i x[2m+1] and the split step
+// A real N-point DFT is computed as a complex M = N/2-point FFT of z[m] = x[2m] + i x[2m+1] and
+// the split step
 //   X[k] = (Z[k] + conj Z[M-k]) / 2 - i e^{-2 pi i k / N} (Z[k] - conj Z[M-k]) / 2,  0 <= k <= M
-// (X[N-k] = conj X[k] for the full spectrum). The M-point FFT is radix-2 decimation in time in
-// LDS (input stored bit-reversed, log2 M butterfly passes, one barrier each). Twiddles
-// e^{-2 pi i k / N}, k < M, come from a table computed on the host in double precision.
-// The inverse runs the same steps backwards (Hermitian fold of the input, merge into Z, inverse
-// FFT with conjugate twiddles, 1/M); the overlap-add is a gather over the frames that cover each
-// output sample, in increasing frame order, so it needs no atomics.
+// (X[N-k] = conj X[k] for the full spectrum). For 128 <= N <= 8192 the M-point FFT is
+// register-resident (Stockham passes of radix 16, each thread holding 16 values, the LDS only
+// between passes; several frames per workgroup); other sizes run one workgroup per frame with
+// radix-2 decimation in time in LDS (input stored bit-reversed, two stages per barrier). Twiddles
+// come from tables computed on the host in double precision. The inverse runs the same steps
+// backwards (Hermitian fold of the input, merge into Z, inverse FFT with conjugate twiddles,
+// 1/M); the overlap-add is a gather over the frames that cover each output sample, in increasing
+// frame order, so it needs no atomics.
 #include "device_utils.hpp"
 #include "kernels.hpp"
 
@@ -46,13 +48,16 @@ constexpr int zslots(int m) { return m + m / 16; }
 // W_4h^p, (i0+h, i0+3h) with W_4h^(p+h)), the same operations in the same order as two radix-2
 // passes; an odd stage count ends with one radix-2 pass. z is addressed through zp(); TWP: tw is
 // the padded LDS copy (zp()), else the plain global table.
-template <bool TWP>
-__device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse) {
+// lt: the thread's index among the NT threads that share z (several groups of NT threads may
+// each run their own transform in lockstep; the barriers are the workgroup's).
+template <bool TWP, int NT = kThreads>
+__device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse,
+                        int lt = threadIdx.x) {
   auto twd = [&](int i) { return tw[TWP ? zp(i) : i]; };
   int h = 1;
   for (; 2 * h < M; h <<= 2) {
     const int s1 = M / h, s2 = M / (2 * h);  // W_2h^p = tw[p * s1], W_4h^p = tw[p * s2]
-    for (int t = threadIdx.x; t < M / 4; t += kThreads) {
+    for (int t = lt; t < M / 4; t += NT) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 2) + p;
       float2 w1 = twd(p * s1), w2 = twd(p * s2), w3 = twd(p * s2 + M / 2);
@@ -79,7 +84,7 @@ __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool in
   }
   if (h < M) {
     const int stride = M / h;  // W_{2h}^p = tw[p * M / h]
-    for (int t = threadIdx.x; t < M / 2; t += kThreads) {
+    for (int t = lt; t < M / 2; t += NT) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 1) + p, i1 = i0 + h;
       float2 w = twd(p * stride);
@@ -253,6 +258,378 @@ __global__ __launch_bounds__(kThreads) void stft_inverse_kernel(StftArgs a) {
   }
 }
 
+// ------------------------------------------------------------ register-resident Stockham FFT
+// A thread holds 16 complex values and runs each pass's radix-R DFTs (R = 16, or the last pass's
+// smaller radix, 16 / R of them) in registers; the LDS carries the data between passes only
+// (M = 2048: 3 passes, against 11 radix-2 stages in LDS). Pass p with radix R after L points
+// are combined (Stockham, natural order in and out):
+//   v_r = in[j + r M / R] * W_{L R}^{r k},  k = j mod L,  r < R
+//   out[(j - k) R + k + s L] = sum_r v_r W_R^{r s},  s < R
+// for the butterflies j < M / R. Pass 0 (L = 1) has no twiddles; the others read them from the
+// plan's table staged in LDS (M - 16 entries, [pass][r - 1][k], computed on the host in double).
+// The inverse uses conjugate twiddles throughout.
+
+constexpr float kC1 = 0.92387953251128674f;  // cos(pi / 8)
+constexpr float kC2 = 0.70710678118654752f;  // cos(pi / 4)
+constexpr float kC3 = 0.38268343236508978f;  // cos(3 pi / 8)
+
+// v * W_16^q (forward, e^{-2 pi i q / 16}) or v * conj(W_16^q) (INV), q < 8 (a constant after
+// unrolling)
+template <bool INV>
+__device__ __forceinline__ float2 w16(float2 v, int q) {
+  if (q == 0) return v;
+  if (q == 4) return INV ? make_float2(-v.y, v.x) : make_float2(v.y, -v.x);
+  const float c = q == 1 ? kC1 : q == 2 ? kC2 : q == 3 ? kC3 : q == 5 ? -kC3 : q == 6 ? -kC2 : -kC1;
+  const float s = q == 1 ? kC3 : q == 2 ? kC2 : q == 3 ? kC1 : q == 5 ? kC1 : q == 6 ? kC2 : kC3;
+  return INV ? make_float2(v.x * c - v.y * s, v.x * s + v.y * c)
+             : make_float2(v.x * c + v.y * s, v.y * c - v.x * s);
+}
+
+constexpr int brev_c(int s, int bits) {
+  int r = 0;
+  for (int i = 0; i < bits; ++i) r |= ((s >> i) & 1) << (bits - 1 - i);
+  return r;
+}
+
+// In-register R-point DFT of v[0..R) (natural order in and out): radix-2 decimation in
+// frequency (stage of half-size h: v_p + v_{p+h}, (v_p - v_{p+h}) W_{2h}^p), then the
+// bit-reversal permutation, which costs nothing after unrolling.
+template <int R, bool INV>
+__device__ __forceinline__ void dft_reg(float2* v) {
+#pragma unroll
+  for (int h = R / 2; h >= 1; h /= 2) {
+#pragma unroll
+    for (int i0 = 0; i0 < R; i0 += 2 * h) {
+#pragma unroll
+      for (int p = 0; p < h; ++p) {
+        const float2 x = v[i0 + p], y = v[i0 + p + h];
+        v[i0 + p] = make_float2(x.x + y.x, x.y + y.y);
+        v[i0 + p + h] = w16<INV>(make_float2(x.x - y.x, x.y - y.y), p * 8 / h);
+      }
+    }
+  }
+  constexpr int bits = R == 16 ? 4 : R == 8 ? 3 : R == 4 ? 2 : R == 2 ? 1 : 0;
+  float2 t[R];
+#pragma unroll
+  for (int s = 0; s < R; ++s) t[s] = v[brev_c(s, bits)];
+#pragma unroll
+  for (int s = 0; s < R; ++s) v[s] = t[s];
+}
+
+template <int LOGM>
+struct SkCfg {
+  static constexpr int M = 1 << LOGM, T = M / 16;    // threads per transform
+  static constexpr int P = stft_sk_passes(LOGM);
+  static constexpr int RL = stft_sk_radix(LOGM, P - 1);  // last pass's radix
+  static constexpr int F = 256 / T < 16 ? 256 / T : 16;  // transforms (frames) per workgroup
+  static constexpr int NT = F * T;
+  static constexpr int ZS = M + M / 16;  // zslots(M)
+  static constexpr int NSTW = M - 16;
+  static constexpr size_t LDS = sizeof(float2) * ((size_t)F * ZS + NSTW);
+  static_assert(LOGM >= kStftSkMinLogM && LOGM <= kStftSkMaxLogM && P >= 2 && P <= 3, "plan");
+};
+
+// Pass (R, L >= 16) of one transform in LDS: every read of the pass, the twiddles and the DFTs,
+// a barrier, then the writes (in place) and a barrier.
+template <int LOGM, int R, int L, bool INV>
+__device__ __forceinline__ void sk_pass(float2* zg, const float2* stwl, int lt) {
+  constexpr int M = 1 << LOGM, T = M / 16, NB = 16 / R;
+  float2 v[16];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[b * R + r] = zg[zp(lt + b * T + r * (M / R))];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int k = (lt + b * T) & (L - 1);
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      float2 w = stwl[(L - 16) + (r - 1) * L + k];
+      if (INV) w.y = -w.y;
+      v[b * R + r] = cmul(v[b * R + r], w);
+    }
+    dft_reg<R, INV>(v + b * R);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const int jj = lt + b * T, k = jj & (L - 1);
+#pragma unroll
+    for (int s = 0; s < R; ++s) zg[zp((jj - k) * R + k + s * L)] = v[b * R + s];
+  }
+  __syncthreads();
+}
+
+// Forward STFT on the register-resident FFT: F frames per workgroup (one per group of T
+// threads). Pass 0 reads the windowed samples from global memory; the last pass leaves Z in LDS
+// in natural order for the split step. Output: frame-major rows (consecutive threads along bins)
+// or bin-major rows (bin k of the workgroup's frames as one vector of up to 4 floats). Frames
+// past the end run on the last frame and store nothing; with a frame count that is not a
+// multiple of F the bin-major vectors are written as scalars.
+template <int LOGM>
+__global__ __launch_bounds__(SkCfg<LOGM>::NT) void stft_forward_sk_kernel(StftArgs a) {
+  using C = SkCfg<LOGM>;
+  constexpr int M = C::M, T = C::T, F = C::F, ZS = C::ZS, NT = C::NT;
+  extern __shared__ float2 z[];
+  float2* stwl = z + F * ZS;
+  const int g = threadIdx.x / T, lt = threadIdx.x % T;
+  const int64_t nblk = (a.frames + F - 1) / F;
+  const int64_t fb = frame_of_block(nblk);
+  const int b = blockIdx.y;
+  if (fb >= nblk) return;
+  const int64_t f0 = fb * F, f = min(f0 + g, a.frames - 1);
+  float2* zg = z + g * ZS;
+  for (int i = threadIdx.x; i < C::NSTW; i += NT) stwl[i] = a.stw[i];
+  // the split step's twiddles W_N^k, loaded now so that their latency hides behind the FFT
+  constexpr int VW = F < 4 ? F : 4, CH = F / VW;
+  constexpr int KW = ((M + 1) * CH + NT - 1) / NT;  // work items per thread (at most)
+  const bool vec = a.frames % F == 0;  // then every block's F frames exist
+  float2 wpre[KW];
+#pragma unroll
+  for (int t = 0; t < KW; ++t) {
+    const int i = threadIdx.x + t * NT;
+    const int k = min(a.layout == 0 ? i : i / CH, M);
+    wpre[t] = k == M ? make_float2(-1.f, 0.f) : a.tw[k];
+  }
+  {
+    const float* xs = a.x + (int64_t)b * a.n + f * a.hop;
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = lt + r * T;
+      const float2 w = *reinterpret_cast<const float2*>(a.win + 2 * m);
+      v[r] = make_float2(xs[2 * m] * w.x, xs[2 * m + 1] * w.y);
+    }
+    dft_reg<16, false>(v);
+#pragma unroll
+    for (int s = 0; s < 16; ++s) zg[zp(lt * 16 + s)] = v[s];
+  }
+  __syncthreads();
+  if constexpr (C::P == 2) {
+    sk_pass<LOGM, C::RL, 16, false>(zg, stwl, lt);
+  } else {
+    sk_pass<LOGM, 16, 16, false>(zg, stwl, lt);
+    sk_pass<LOGM, C::RL, 256, false>(zg, stwl, lt);
+  }
+  // split step: X[k] = (Z[k] + conj Z[M-k]) / 2 - i W_N^k (Z[k] - conj Z[M-k]) / 2; a work item
+  // is bin k of all F frames (frame-major) or of VW of them (bin-major chunk c)
+  const int bins = a.onesided ? M + 1 : a.N;
+  const int64_t base = (int64_t)b * a.frames * bins;
+  auto xk = [&](int j, int k, float2 w) {
+    const float2 zk = z[j * ZS + zp(k == M ? 0 : k)];
+    const float2 zc = z[j * ZS + zp(k == 0 ? 0 : M - k)];  // Z[M-k], conjugated below
+    const float2 fe = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y - zc.y));
+    const float2 d = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y + zc.y));
+    const float2 t = cmul(w, make_float2(d.y, -d.x));  // w * (-i d)
+    return make_float2(fe.x + t.x, fe.y + t.y);
+  };
+  const bool fm = a.layout == 0;
+  const int items = fm ? M + 1 : (M + 1) * CH;
+#pragma unroll
+  for (int t = 0; t < KW; ++t) {
+    const int i = threadIdx.x + t * NT;
+    if (i >= items) break;
+    const int k = fm ? i : i / CH, c = fm ? 0 : i % CH;
+    const float2 w = wpre[t];
+    if (fm) {
+#pragma unroll
+      for (int j = 0; j < F; ++j) {
+        if (f0 + j >= a.frames) break;
+        const float2 x = xk(j, k, w);
+        const int64_t o = base + (f0 + j) * bins;
+        a.re[o + k] = x.x;
+        a.im[o + k] = x.y;
+        if (!a.onesided && k > 0 && k < M) {
+          a.re[o + a.N - k] = x.x;
+          a.im[o + a.N - k] = -x.y;
+        }
+      }
+      continue;
+    }
+    float re[VW], im[VW];
+#pragma unroll
+    for (int u = 0; u < VW; ++u) {
+      const float2 x = xk(c * VW + u, k, w);
+      re[u] = x.x;
+      im[u] = x.y;
+    }
+    auto put = [&](int kk, bool conj) {
+      float* pr = a.re + base + (int64_t)kk * a.frames + f0 + c * VW;
+      float* pi = a.im + base + (int64_t)kk * a.frames + f0 + c * VW;
+      if (vec && VW == 4) {
+        *reinterpret_cast<float4*>(pr) = make_float4(re[0], re[1 % VW], re[2 % VW], re[3 % VW]);
+        *reinterpret_cast<float4*>(pi) =
+            conj ? make_float4(-im[0], -im[1 % VW], -im[2 % VW], -im[3 % VW])
+                 : make_float4(im[0], im[1 % VW], im[2 % VW], im[3 % VW]);
+      } else if (vec && VW == 2) {
+        *reinterpret_cast<float2*>(pr) = make_float2(re[0], re[1 % VW]);
+        *reinterpret_cast<float2*>(pi) = conj ? make_float2(-im[0], -im[1 % VW])
+                                              : make_float2(im[0], im[1 % VW]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < VW; ++u)
+          if (f0 + c * VW + u < a.frames) {
+            pr[u] = re[u];
+            pi[u] = conj ? -im[u] : im[u];
+          }
+      }
+    };
+    put(k, false);
+    if (!a.onesided && k > 0 && k < M) put(a.N - k, true);
+  }
+}
+
+// Inverse frames on the register-resident FFT: F frames per workgroup. The Hermitian fold
+// writes Z in natural order to LDS (a work item loads the pair (k, M - k), and X[N - k],
+// X[N - (M - k)] for full spectra, of one frame, or of up to 4 frames as vectors in the bin-major
+// layout, so every bin is read once); the passes run from LDS and the last one writes the scaled,
+// windowed frame straight to the frame buffer.
+template <int LOGM>
+__global__ __launch_bounds__(SkCfg<LOGM>::NT) void stft_inverse_sk_kernel(StftArgs a) {
+  using C = SkCfg<LOGM>;
+  constexpr int M = C::M, T = C::T, F = C::F, ZS = C::ZS, NT = C::NT;
+  extern __shared__ float2 z[];
+  float2* stwl = z + F * ZS;
+  const int g = threadIdx.x / T, lt = threadIdx.x % T;
+  const int64_t nblk = (a.frames + F - 1) / F;
+  const int64_t fb = frame_of_block(nblk);
+  const int b = blockIdx.y;
+  if (fb >= nblk) return;
+  const int64_t f0 = fb * F;
+  for (int i = threadIdx.x; i < C::NSTW; i += NT) stwl[i] = a.stw[i];
+  // the last pass (radix R, L = M / R) gives thread lt out[j + s L] for its butterflies
+  // j = lt + bb T < L; their window values are loaded now, off the critical path
+  constexpr int R = C::RL, L = M / C::RL, NB = 16 / R;
+  float2 wv[16];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int s = 0; s < R; ++s)
+      wv[bb * R + s] = *reinterpret_cast<const float2*>(a.win + 2 * (lt + bb * T + s * L));
+  const int bins = a.onesided ? M + 1 : a.N;
+  const int64_t base = (int64_t)b * a.frames * bins;
+  auto herm = [&](int kk, float2 gv, float2 cv) {  // cv = X[N - kk] (full spectra)
+    float2 h = gv;
+    if (!a.onesided && kk > 0 && kk < M)
+      h = make_float2(0.5f * (gv.x + cv.x), 0.5f * (gv.y - cv.y));
+    if (kk == 0 || kk == M) h.y = 0.f;
+    return h;
+  };
+  auto fold = [&](float2 hk, float2 hc, float2 t) {  // Z[k] from H[k], H[M - k]
+    const float2 fe = make_float2(0.5f * (hk.x + hc.x), 0.5f * (hk.y - hc.y));
+    const float2 d = make_float2(0.5f * (hk.x - hc.x), 0.5f * (hk.y + hc.y));
+    const float2 w = make_float2(t.x, -t.y);  // e^{+2 pi i k / N}
+    const float2 fo = cmul(d, w);
+    return make_float2(fe.x - fo.y, fe.y + fo.x);  // Fe + i Fo
+  };
+  // Z[k] and Z[M - k] of frame slot j from the bins of the pair
+  auto put_pair = [&](int j, int k, float2 gk, float2 gc, float2 ck, float2 cc) {
+    const int kc = M - k;
+    const float2 hk = herm(k, gk, ck), hc = herm(kc, gc, cc);
+    z[j * ZS + zp(k)] = fold(hk, hc, a.tw[k]);
+    if (kc < M && kc != k) z[j * ZS + zp(kc)] = fold(hc, hk, a.tw[kc]);
+  };
+  const float2 zero = make_float2(0.f, 0.f);
+  if (a.layout == 0) {
+    for (int i = threadIdx.x; i < (M / 2 + 1) * F; i += NT) {
+      const int j = i / (M / 2 + 1), k = i - j * (M / 2 + 1), kc = M - k;
+      const int64_t o = base + min(f0 + j, a.frames - 1) * bins;
+      const float2 gk = make_float2(a.cre[o + k], a.cim[o + k]);
+      const float2 gc = make_float2(a.cre[o + kc], a.cim[o + kc]);
+      float2 ck = zero, cc = zero;
+      if (!a.onesided) {
+        const int nk = k > 0 ? a.N - k : k, nc = kc < M ? a.N - kc : kc;
+        ck = make_float2(a.cre[o + nk], a.cim[o + nk]);
+        cc = make_float2(a.cre[o + nc], a.cim[o + nc]);
+      }
+      put_pair(j, k, gk, gc, ck, cc);
+    }
+  } else {
+    constexpr int VW = F < 4 ? F : 4, CH = F / VW;
+    const bool vec = a.frames % F == 0;  // then every block's F frames exist
+    auto get = [&](int kk, int c, float2 (&x)[VW]) {  // X[kk] of frames c VW .. c VW + VW - 1
+      const float* pr = a.cre + base + (int64_t)kk * a.frames + f0 + c * VW;
+      const float* pi = a.cim + base + (int64_t)kk * a.frames + f0 + c * VW;
+      if (vec && VW == 4) {
+        const float4 r = *reinterpret_cast<const float4*>(pr);
+        const float4 q = *reinterpret_cast<const float4*>(pi);
+        const float rr[4] = {r.x, r.y, r.z, r.w}, qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int u = 0; u < VW; ++u) x[u] = make_float2(rr[u], qq[u]);
+      } else if (vec && VW == 2) {
+        const float2 r = *reinterpret_cast<const float2*>(pr);
+        const float2 q = *reinterpret_cast<const float2*>(pi);
+        const float rr[2] = {r.x, r.y}, qq[2] = {q.x, q.y};
+#pragma unroll
+        for (int u = 0; u < VW; ++u) x[u] = make_float2(rr[u], qq[u]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < VW; ++u) {
+          const int64_t o = min(f0 + c * VW + u, a.frames - 1) - (f0 + c * VW);
+          x[u] = make_float2(pr[o], pi[o]);
+        }
+      }
+    };
+    for (int i = threadIdx.x; i < (M / 2 + 1) * CH; i += NT) {
+      const int k = i / CH, c = i % CH, kc = M - k;
+      float2 gk[VW], gc[VW], ck[VW], cc[VW];
+      get(k, c, gk);
+      get(kc, c, gc);
+      if (!a.onesided) {
+        get(k > 0 ? a.N - k : k, c, ck);
+        get(kc < M ? a.N - kc : kc, c, cc);
+      }
+#pragma unroll
+      for (int u = 0; u < VW; ++u)
+        put_pair(c * VW + u, k, gk[u], gc[u], a.onesided ? zero : ck[u],
+                 a.onesided ? zero : cc[u]);
+    }
+  }
+  __syncthreads();
+  float2* zg = z + g * ZS;
+  {
+    float2 v[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = zg[zp(lt + r * T)];
+    dft_reg<16, true>(v);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) zg[zp(lt * 16 + s)] = v[s];
+    __syncthreads();
+  }
+  if constexpr (C::P == 3) sk_pass<LOGM, 16, 16, true>(zg, stwl, lt);
+  // last pass, into registers
+  float2 v[16];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[bb * R + r] = zg[zp(lt + bb * T + r * L)];
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb) {
+    const int k = lt + bb * T;  // < L
+#pragma unroll
+    for (int r = 1; r < R; ++r) {
+      float2 w = stwl[(L - 16) + (r - 1) * L + k];
+      w.y = -w.y;
+      v[bb * R + r] = cmul(v[bb * R + r], w);
+    }
+    dft_reg<R, true>(v + bb * R);
+  }
+  const int64_t f = f0 + g;
+  if (f >= a.frames) return;
+  const float sc = 1.f / (float)M;
+  float* out = a.frames_buf + ((int64_t)b * a.frames + f) * a.N;
+#pragma unroll
+  for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      const int m = lt + bb * T + s * L;
+      const float2 w = wv[bb * R + s];
+      const float2 x = v[bb * R + s];
+      *reinterpret_cast<float2*>(out + 2 * m) = make_float2((x.x * sc) * w.x, (x.y * sc) * w.y);
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void stft_overlap_add_kernel(StftArgs a) {
   const int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int b = blockIdx.y;
@@ -281,6 +658,39 @@ void check(const StftArgs& a) {
               MNN_ERR_INVALID_ARGUMENT, "stft: invalid configuration");
 }
 
+// Register-resident FFT kernels by log2 M (M = N / 2); null outside their range. Tuning
+// override MNN_STFT_SK=0 keeps the LDS radix-2 kernels.
+bool use_sk(const StftArgs& a) {
+  static const bool on = [] {
+    const char* e = std::getenv("MNN_STFT_SK");
+    return !e || std::atoi(e) != 0;
+  }();
+  return on && a.stw && a.logM >= kStftSkMinLogM && a.logM <= kStftSkMaxLogM;
+}
+
+template <int LOGM>
+void launch_sk(const LaunchCtx& c, const StftArgs& a, bool inverse) {
+  using C = SkCfg<LOGM>;
+  const dim3 grid((unsigned)(8 * cdiv(cdiv(a.frames, C::F), 8)), (unsigned)a.batch);
+  if (inverse)
+    launch(c, "istft_frames_f32", stft_inverse_sk_kernel<LOGM>, grid, dim3(C::NT), C::LDS, a);
+  else
+    launch(c, "stft_forward_f32", stft_forward_sk_kernel<LOGM>, grid, dim3(C::NT), C::LDS, a);
+}
+
+void run_sk(const LaunchCtx& c, const StftArgs& a, bool inverse) {
+  switch (a.logM) {
+    case 6: return launch_sk<6>(c, a, inverse);
+    case 7: return launch_sk<7>(c, a, inverse);
+    case 8: return launch_sk<8>(c, a, inverse);
+    case 9: return launch_sk<9>(c, a, inverse);
+    case 10: return launch_sk<10>(c, a, inverse);
+    case 11: return launch_sk<11>(c, a, inverse);
+    case 12: return launch_sk<12>(c, a, inverse);
+    default: fail(MNN_ERR_INVALID_ARGUMENT, "stft: no register-resident FFT for this size");
+  }
+}
+
 }  // namespace
 
 void stft_forward(const LaunchCtx& c, const StftArgs& a) {
@@ -290,6 +700,7 @@ void stft_forward(const LaunchCtx& c, const StftArgs& a) {
               MNN_ERR_INVALID_ARGUMENT, "stft_forward: frames exceed the signal");
   const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
   const int zs = zslots(a.N / 2);
+  if (use_sk(a)) return run_sk(c, a, false);
   if (a.N <= kStftLdsTwMaxN)
     launch(c, "stft_forward_f32", stft_forward_kernel<true>, grid, dim3(kThreads),
            sizeof(float2) * 2 * zs, a);
@@ -304,7 +715,9 @@ void stft_inverse(const LaunchCtx& c, const StftArgs& a) {
               "stft_inverse: missing buffers");
   const dim3 grid((unsigned)(8 * cdiv(a.frames, 8)), (unsigned)a.batch);
   const int zs = zslots(a.N / 2);
-  if (a.onesided && a.N <= kStftStageMaxN)
+  if (use_sk(a))
+    run_sk(c, a, true);
+  else if (a.onesided && a.N <= kStftStageMaxN)
     launch(c, "istft_frames_f32", stft_inverse_kernel<true, true>, grid, dim3(kThreads),
            sizeof(float2) * (2 * zs + a.N / 2 + 1), a);
   else if (a.N <= kStftLdsTwMaxN)

@@ -288,12 +288,22 @@ void segment_crossfade_store(const LaunchCtx& c, const SegmentArgs& a);
 // tw[k] = e^{-2 pi i k / N}, k < N/2 (float2). Spectra are [batch][frames][bins] (layout 0) or
 // [batch][bins][frames] (layout 1), bins = N/2 + 1 (onesided) or N.
 constexpr int kStftMaxN = 16384;
+// The register-resident FFT of the STFT kernels (M = N / 2 = 2^logm, kStftSkMinLogM <= logm <=
+// kStftSkMaxLogM) runs Stockham passes of radix 16 and one last pass of the remaining radix; pass
+// p >= 1 (L = 16^p points already combined) multiplies by W_{L R}^{r k}, read from the plan's
+// table at (L - 16) + (r - 1) L + k (M - 16 entries in all).
+constexpr int kStftSkMinLogM = 6, kStftSkMaxLogM = 12;
+constexpr int stft_sk_passes(int logm) { return (logm + 3) / 4; }
+constexpr int stft_sk_radix(int logm, int p) {
+  return p < stft_sk_passes(logm) - 1 ? 16 : 1 << (logm - 4 * (stft_sk_passes(logm) - 1));
+}
 struct StftArgs {
   int N = 0, logM = 0, hop = 0, batch = 0, onesided = 1, layout = 0;
   int64_t n = 0;       // forward: samples per signal
   int64_t frames = 0;
   const float* win = nullptr;
   const float2* tw = nullptr;
+  const float2* stw = nullptr;  // Stockham pass twiddles (register-resident FFT sizes)
   const float* x = nullptr;   // forward input [batch][n]
   float* re = nullptr;        // forward outputs
   float* im = nullptr;

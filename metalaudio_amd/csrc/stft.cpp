@@ -40,11 +40,33 @@ StftPlan::StftPlan(Device* d, int fft_size, int hop, int window)
     tw[2 * k] = (float)std::cos(-2.0 * pi * k / N_);
     tw[2 * k + 1] = (float)std::sin(-2.0 * pi * k / N_);
   }
+  // Stockham pass twiddles W_{L R}^{r k} = e^{-2 pi i r k / (L R)}, pass by pass, [r - 1][k]
+  std::vector<float> stw;
+  int logm = 0;
+  while ((2 << logm) < N_) ++logm;
+  if (logm >= k::kStftSkMinLogM && logm <= k::kStftSkMaxLogM) {
+    int L = k::stft_sk_radix(logm, 0);
+    for (int p = 1; p < k::stft_sk_passes(logm); ++p) {
+      const int R = k::stft_sk_radix(logm, p);
+      for (int r = 1; r < R; ++r)
+        for (int kk = 0; kk < L; ++kk) {
+          stw.push_back((float)std::cos(-2.0 * pi * r * kk / ((double)L * R)));
+          stw.push_back((float)std::sin(-2.0 * pi * r * kk / ((double)L * R)));
+        }
+      L *= R;
+    }
+    MNN_REQUIRE(stw.size() == 2 * (size_t)(N_ / 2 - 16), MNN_ERR_INVALID_CONFIGURATION,
+                "Stockham twiddle table size");
+  }
   d->make_current();
   win_.reserve(sizeof(float) * N_);
   tw_.reserve(sizeof(float) * N_);
   HIP_CHECK(hipMemcpy(win_.ptr, win_host_.data(), sizeof(float) * N_, hipMemcpyHostToDevice));
   HIP_CHECK(hipMemcpy(tw_.ptr, tw.data(), sizeof(float) * N_, hipMemcpyHostToDevice));
+  if (!stw.empty()) {
+    stw_.reserve(sizeof(float) * stw.size());
+    HIP_CHECK(hipMemcpy(stw_.ptr, stw.data(), sizeof(float) * stw.size(), hipMemcpyHostToDevice));
+  }
 }
 
 int64_t StftPlan::frame_count(int64_t n) const {
@@ -99,6 +121,7 @@ void StftPlan::forward(const Tensor& x, Tensor& re, Tensor& im, bool onesided, i
   a.frames = F;
   a.win = win_.f32();
   a.tw = static_cast<const float2*>(tw_.ptr);
+  a.stw = static_cast<const float2*>(stw_.ptr);
   a.x = x.f32();
   a.re = re.f32();
   a.im = im.f32();
@@ -134,6 +157,7 @@ void StftPlan::inverse(const Tensor& re, const Tensor& im, bool onesided, int la
   a.frames = F;
   a.win = win_.f32();
   a.tw = static_cast<const float2*>(tw_.ptr);
+  a.stw = static_cast<const float2*>(stw_.ptr);
   a.cre = re.f32();
   a.cim = im.f32();
   a.frames_buf = frames_.f32();

@@ -28,7 +28,7 @@ class StftPlan {
   Device* dev_;
   int N_, hop_, window_;
   std::vector<float> win_host_;
-  DevBuf win_, tw_, frames_;
+  DevBuf win_, tw_, stw_, frames_;
 };
 
 float window_coefficient(int window, int index, int length);

@@ -44,11 +44,15 @@ def spec_close(got, ref, what):
 
 @pytest.mark.parametrize("N,hop,kind,B,n", [
     (4, 1, "hann", 1, 37), (8, 2, "hamming", 2, 100), (64, 16, "hann", 1, 1000),
+    # the register-resident FFT's sizes: 16 frames per workgroup, 90 frames (ragged) and 64
+    (128, 32, "hann", 2, 3000), (256, 64, "hamming", 1, 4288), (2048, 512, "hann", 1, 22016),
     (512, 128, "blackman", 3, 5000), (1024, 256, "none", 1, 4096), (4096, 1024, "hann", 2, 50000),
     (8192, 2048, "hann", 1, 30000),  # largest size with the twiddle table staged in LDS
     (16384, 4096, "hann", 1, 40000),
+    (4096, 1024, "hann", 2, 343980),  # a 7.8 s stereo chunk: 332 frames, whole 4-frame vectors
 ])
-@pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins")])
+@pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins"),
+                                             (False, "bins")])
 def test_stft_forward_parity(dev, stream, N, hop, kind, B, n, onesided, layout):
     say(f"stft N={N} hop={hop} {kind} B={B} n={n} onesided={onesided} layout={layout}")
     x = RNG.standard_normal((B, n)).astype(np.float32)
@@ -81,13 +85,18 @@ def wsum_of(N, hop, kind, F):
     return s
 
 
-@pytest.mark.parametrize("N,hop,kind,B,F", [(8, 2, "hann", 1, 9), (64, 16, "hann", 2, 40),
+@pytest.mark.parametrize("N,hop,kind,B,F", [(4, 1, "hann", 1, 13), (8, 2, "hann", 1, 9),
+                                            (128, 32, "hann", 1, 45), (256, 64, "hann", 2, 32),
+                                            (2048, 512, "blackman", 1, 16),
+                                            (64, 16, "hann", 2, 40),
                                             (512, 256, "hamming", 1, 30),
                                             (4096, 1024, "hann", 2, 20),
+                                            (4096, 1024, "hann", 2, 23),
                                             # twiddles in LDS at its limit, then from global memory
                                             (8192, 2048, "hann", 1, 9),
                                             (16384, 4096, "hann", 1, 7)])
-@pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins")])
+@pytest.mark.parametrize("onesided,layout", [(True, "frames"), (False, "frames"), (True, "bins"),
+                                             (False, "bins")])
 def test_istft_parity(dev, stream, N, hop, kind, B, F, onesided, layout):
     say(f"istft N={N} hop={hop} {kind} B={B} F={F} onesided={onesided} layout={layout}")
     bins = N // 2 + 1 if onesided else N
