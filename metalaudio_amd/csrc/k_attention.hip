@@ -18,6 +18,7 @@
 #include "kernels.hpp"
 #include "lds_dma.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace mnn {
@@ -64,8 +65,13 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   const int nq = gridDim.x, nh = gridDim.y;
   const int unit = xcd_logical_tile(blockIdx.x + nq * (blockIdx.y + nh * blockIdx.z),
                                     nq * nh * gridDim.z);
-  const int qblk = unit % nq, h = (unit / nq) % nh, b = unit / (nq * nh);
+  const int qblk = unit % nq, h = (unit / nq) % nh, bz = unit / (nq * nh);
+  const int ns = a.nsplit, b = bz / ns, sp = bz % ns;
   const int qw0 = qblk * BQ + wave * QW;
+  // key blocks [kb0, kb0 + nl) of this workgroup's key range (all of them without a key split)
+  const int nblk_all = (a.Sk + BKV - 1) / BKV;
+  const int kb0 = (int)((int64_t)sp * nblk_all / ns);
+  const int nblk = (int)((int64_t)(sp + 1) * nblk_all / ns) - kb0;
 
   const float* __restrict__ qb = a.q + (int64_t)b * a.q_bs + h * HD;
   const float* __restrict__ kb = a.k + (int64_t)b * a.kv_bs + h * HD;
@@ -100,10 +106,9 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
       }
     }
   };
-  const int nblk = (a.Sk + BKV - 1) / BKV;
-  issue(0, false, 0);
-  issue(0, true, 0);
-  if (nblk > 1) issue(1, false, 1);
+  issue(kb0, false, 0);
+  issue(kb0, true, 0);
+  if (nblk > 1) issue(kb0 + 1, false, 1);
 
   // Q fragments: B operand of S^T = K Q^T; lane group G owns d in [G*HS, (G+1)*HS)
   const float qscale = a.scale * 1.4426950408889634f;
@@ -154,11 +159,12 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   stage_barrier();
   read_k(0, kfr);
 
-  // One 64-key block; PAR = blk % 2 selects the ring slots at compile time, so every LDS address
-  // below is a lane base plus an immediate offset. The block loop runs the two parities in turn.
+  // One 64-key block (blk counts from the start of the workgroup's key range); PAR = blk % 2
+  // selects the ring slots at compile time, so every LDS address below is a lane base plus an
+  // immediate offset. The block loop runs the two parities in turn.
   auto block_step = [&](int blk, auto parc) {
     constexpr int PAR = decltype(parc)::value;
-    const int kv0 = blk * BKV;
+    const int kv0 = (kb0 + blk) * BKV;
     // S^T tiles: 4 key tiles x NU query tiles, k-steps outermost so the 4*NU independent
     // accumulators interleave and no MFMA waits on the previous one
     // accumulators start at -mref, so the scores come out relative to the reference maximum
@@ -228,8 +234,8 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
     // V(blk) and K(blk+1) have landed for this wave (they are the only loads in flight) ...
     wait_vmcnt<0>();
     stage_barrier();  // ... and for every wave; K(blk) and V(blk-1) are no longer read
-    if (blk + 2 < nblk) issue(blk + 2, false, PAR);
-    if (blk + 1 < nblk) issue(blk + 1, true, 1 - PAR);
+    if (blk + 2 < nblk) issue(kb0 + blk + 2, false, PAR);
+    if (blk + 1 < nblk) issue(kb0 + blk + 1, true, 1 - PAR);
     // PV in four key tiles t. The V rows of tile t+1 (key 16(t+1) + 4G + r, this lane's d) and
     // the K fragments of tile t of the next block are read while tile t's MFMAs run; the
     // scheduling barriers keep each tile's reads next to it, which bounds the live registers.
@@ -281,17 +287,27 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   if (blk < nblk) block_step(blk, std::integral_constant<int, 0>{});
 
   // normalise and write O[b][q][h*HD + d]; for query l16 a lane holds d = dmap(4G + r, w):
-  // 16 consecutive values (head dim 64) or ND runs of 4 (d = 16w + 4G + r)
-  float* __restrict__ ob = a.o + (int64_t)b * a.o_bs + h * HD;
+  // 16 consecutive values (head dim 64) or ND runs of 4 (d = 16w + 4G + r). With a key split the
+  // unnormalised O of the range goes to its partial row, with the range's reference maximum and
+  // sum (attn_combine_kernel merges the ranges).
+  const bool part = ns > 1;
+  const int64_t prow0 = (((int64_t)sp * a.B + b) * a.H + h) * a.Sq;  // partial row of query 0
+  float* __restrict__ ob = part ? a.part + prow0 * HD : a.o + (int64_t)b * a.o_bs + h * HD;
+  const int64_t ors = part ? HD : a.o_rs;
 #pragma unroll
   for (int u = 0; u < NU; ++u) {
     float l = lsum[u];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
-    const float inv = 1.f / (l + 1e-10f);
+    const float inv = part ? 1.f : 1.f / (l + 1e-10f);
     const int q = qw0 + 16 * u + l16;
     if (q < a.Sq) {
-      float* orow = ob + (int64_t)q * a.o_rs;
+      if (part && G == 0) {
+        const int64_t ml = (int64_t)ns * a.B * a.H * a.Sq * HD;  // maxima, then sums
+        a.part[ml + prow0 + q] = mref[u];
+        a.part[ml + (int64_t)ns * a.B * a.H * a.Sq + prow0 + q] = l;
+      }
+      float* orow = ob + (int64_t)q * ors;
       if constexpr (ND == 4) {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
@@ -305,6 +321,36 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
       }
     }
   }
+}
+
+// Merges the key ranges of a key-split attention: with M_s, L_s and O_s the reference maximum
+// (log2 units), sum and unnormalised output of range s, m = max_s M_s and w_s = 2^(M_s - m),
+// O = sum_s w_s O_s / (sum_s w_s L_s + 1e-10). One thread per 4 consecutive d of one query.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+  const int hd4 = a.hd / 4;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int h = blockIdx.y, b = blockIdx.z;
+  if (i >= (int64_t)a.Sq * hd4) return;
+  const int q = (int)(i / hd4), d = 4 * (int)(i % hd4);
+  const int ns = a.nsplit;
+  const int64_t rows = (int64_t)a.B * a.H * a.Sq;  // partial rows per range
+  const int64_t ml = rows * ns * a.hd, row = ((int64_t)b * a.H + h) * a.Sq + q;
+  float m = -INFINITY;
+  for (int sp = 0; sp < ns; ++sp) m = fmaxf(m, a.part[ml + sp * rows + row]);
+  float l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp = 0; sp < ns; ++sp) {
+    const float w = __builtin_amdgcn_exp2f(a.part[ml + sp * rows + row] - m);
+    l += w * a.part[ml + (int64_t)ns * rows + sp * rows + row];
+    const float4 o = *reinterpret_cast<const float4*>(a.part + (sp * rows + row) * a.hd + d);
+    acc.x += w * o.x;
+    acc.y += w * o.y;
+    acc.z += w * o.z;
+    acc.w += w * o.w;
+  }
+  const float inv = 1.f / (l + 1e-10f);
+  *reinterpret_cast<float4*>(a.o + (int64_t)b * a.o_bs + (int64_t)q * a.o_rs + h * a.hd + d) =
+      make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 // Generic path for any head dimension: one wave per (b, h, query), scores staged in LDS,
@@ -346,8 +392,22 @@ __global__ __launch_bounds__(64) void attn_generic_kernel(AttnArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+bool fast_form(const AttnArgs& a) {
+  return aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
+         a.q_rs % 4 == 0 && a.kv_rs % 4 == 0 && a.o_rs % 4 == 0 && a.q_bs % 4 == 0 &&
+         a.kv_bs % 4 == 0 && a.o_bs % 4 == 0 && (a.hd == 48 || a.hd == 64);
+}
+
 template <int HD>
 void launch_hd(const LaunchCtx& c, const AttnArgs& a) {
+  if (a.nsplit > 1) {  // 16 queries per wave, key ranges along grid z, then the merge
+    dim3 grid(cdiv(a.Sq, 64), a.H, a.B * a.nsplit);
+    launch(c, HD == 64 ? "attn_fwd_f32_hd64_q16" : "attn_fwd_f32_hd48_q16",
+           attn_fwd_f32_kernel<HD, 16>, grid, dim3(256), 0, a);
+    launch(c, "attn_combine_f32", attn_combine_kernel,
+           dim3((unsigned)cdiv((int64_t)a.Sq * (HD / 4), 256), a.H, a.B), dim3(256), 0, a);
+    return;
+  }
   // queries per wave: 32 or 16, whichever needs fewer workgroup rounds x queries per workgroup
   // over the chip's workgroup slots (fewer, longer rounds win ties: K fragments are reused twice).
   // At three workgroups per CU (head dim 48) the 32-query form does not fit the register budget.
@@ -371,12 +431,41 @@ void launch_hd(const LaunchCtx& c, const AttnArgs& a) {
 
 bool attention_supported(int hd) { return hd > 0; }
 
+// Key split where the query workgroups leave at least half of the device's workgroup slots idle:
+// n ranges (the largest n <= 4 with n W <= S for W workgroups of 64 queries on S slots, at least 4
+// key blocks per range) fill them. Grids of more than half the slots are not split: filling a
+// last round's idle slots this way (e.g. 1344 workgroups on 768 slots as 4 ranges) lowered the
+// attention's kernel time but made the two-stream transformer step ~1 % slower (the partial
+// outputs' traffic and the merge launches). Config 3's 256 workgroups on 512 slots: 86 -> 78 us
+// + 4 us merge. Tuning override: MNN_ATTN_SPLITS (1 disables).
+int attention_key_splits(const LaunchCtx& c, const AttnArgs& a) {
+  if (a.Sq <= 0 || a.B <= 0 || a.H <= 0 || a.Sk <= 0 || !fast_form(a)) return 1;
+  const int nblk = (a.Sk + BKV - 1) / BKV;
+  static const int forced = [] {
+    const char* e = std::getenv("MNN_ATTN_SPLITS");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (forced > 0) return std::max(1, std::min({forced, 8, nblk}));
+  const int occ = a.hd == 64 ? AttnCfg<64>::OCC : AttnCfg<48>::OCC;
+  const int64_t slots = (int64_t)c.dev->props.multiProcessorCount * occ;
+  const int64_t wg = (int64_t)cdiv(a.Sq, 64) * a.H * a.B;
+  int best = 1;
+  for (int ns = 2; ns <= 4 && nblk >= 4 * ns && wg * ns <= slots; ++ns) best = ns;
+  return best;
+}
+
+int64_t attention_part_floats(const AttnArgs& a, int nsplit) {
+  return nsplit <= 1 ? 0 : (int64_t)nsplit * a.B * a.H * a.Sq * (a.hd + 2);
+}
+
 void attention(const LaunchCtx& c, const AttnArgs& a) {
   if (a.Sq <= 0 || a.B <= 0 || a.H <= 0) return;
   MNN_REQUIRE(a.Sk > 0, MNN_ERR_INVALID_ARGUMENT, "attention: empty key sequence");
-  const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o) &&
-                   a.q_rs % 4 == 0 && a.kv_rs % 4 == 0 && a.o_rs % 4 == 0 && a.q_bs % 4 == 0 &&
-                   a.kv_bs % 4 == 0 && a.o_bs % 4 == 0;
+  const bool vec = fast_form(a);
+  MNN_REQUIRE(a.nsplit >= 1 && (a.nsplit == 1 || (vec && a.part && a.nsplit <= 8 &&
+                                                  a.nsplit <= (a.Sk + BKV - 1) / BKV &&
+                                                  (int64_t)a.B * a.nsplit <= 65535)),
+              MNN_ERR_INVALID_ARGUMENT, "attention: unsupported key split");
   if (vec && a.hd == 64) return launch_hd<64>(c, a);
   if (vec && a.hd == 48) return launch_hd<48>(c, a);
   MNN_REQUIRE(a.Sk <= kMaxGenericSk, MNN_ERR_INVALID_CONFIGURATION,

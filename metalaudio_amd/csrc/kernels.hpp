@@ -489,9 +489,16 @@ struct AttnArgs {
   float* o = nullptr;
   int64_t o_bs = 0, o_rs = 0;
   float scale = 1.f;
+  // key split: nsplit ranges of the keys run as separate workgroups and a combine step merges
+  // them; part is a workspace of attention_part_floats(a, nsplit) floats
+  int nsplit = 1;
+  float* part = nullptr;
 };
 // fp32 throughout (operands, scores, softmax, accumulation).
 bool attention_supported(int hd);
+// Key ranges that fill the device's workgroup slots best for these shapes (1: no split).
+int attention_key_splits(const LaunchCtx& c, const AttnArgs& a);
+int64_t attention_part_floats(const AttnArgs& a, int nsplit);
 void attention(const LaunchCtx& c, const AttnArgs& a);
 
 // ------------------------------------------------------------------ diagnostics (k_probe.hip)

@@ -754,6 +754,12 @@ class MHALayer : public Layer {
     at.o = attn_.f32();
     at.o_rs = E;
     at.o_bs = (int64_t)Sq * E;
+    const int ns = k::attention_key_splits(ctx(s), at);
+    if (ns > 1) {
+      part_.reserve(sizeof(float) * k::attention_part_floats(at, ns));
+      at.nsplit = ns;
+      at.part = part_.f32();
+    }
     k::attention(ctx(s), at);
   }
   // output projection of the last attend() (+ residual / LayerScale)
@@ -816,7 +822,7 @@ class MHALayer : public Layer {
   Param* wout_ = nullptr;
   Param* bin_ = nullptr;
   Param* bout_ = nullptr;
-  DevBuf qkv_, attn_;
+  DevBuf qkv_, attn_, part_;  // part_: key-split partial outputs
 };
 
 // ------------------------------------------------------------------ FeedForward

@@ -39,6 +39,9 @@ from pathlib import Path
 FAMILIES = [
     ("attn_fwd_f32_kernel", "attn_fwd"),
     ("attn_generic_kernel", "attn_fwd"),
+    ("attn_combine_kernel", "attn_combine_f32"),
+    ("stft_forward_sk_kernel", "stft_forward_f32"),
+    ("stft_inverse_sk_kernel", "istft_frames_f32"),
     ("enc_l1_stats_kernel", "enc_l1_stats_f32"),
     ("enc_l1_fused_kernel", "enc_l1_fused_f32"),
     ("enc_l1_oneshot_kernel", "enc_l1_oneshot_f32"),

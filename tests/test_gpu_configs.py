@@ -153,7 +153,9 @@ def test_config5_in_place_and_repeatable(dev, stream):
 # benchmark's 0.02 so that the scores spread over several units (a peaked softmax) and the
 # outputs are O(1): an error in the kernel's key blocks, its online rescale or its query tiling
 # then moves outputs by far more than 1e-4 + 1e-3 |ref|.
-ATTN5_CASES = [(1344, 1344, False), (2688, 2688, False), (1344, 2688, True), (2688, 1344, True)]
+ATTN5_CASES = [(1344, 1344, False), (2688, 2688, False), (1344, 2688, True), (2688, 1344, True),
+               # few query workgroups: the keys split into 4 ranges merged by the combine step
+               (64, 2688, True), (300, 1344, True)]
 
 
 @pytest.mark.parametrize("sq,sk,cross", ATTN5_CASES,

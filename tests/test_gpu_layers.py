@@ -354,6 +354,10 @@ MHA_CASES = [
     (2, 384, 8, 700, 90, True),       # cross, short keys
     (1, 64, 4, 33, 33, False),        # hd 16 (generic kernel)
     (1, 512, 8, 1, 1, False),         # single token
+    # key splits (few query workgroups, long keys): ranges merged by the combine step
+    (1, 512, 8, 64, 1000, True),      # 4 ranges, ragged last block
+    (2, 384, 8, 100, 777, True),      # 3 ranges, hd 48
+    (1, 384, 8, 1, 2000, True),       # one query, 4 ranges
 ]
 
 
