@@ -394,12 +394,13 @@ __global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a
 // (k 0 at i = m + 1, k 2 at i = m). A lane owns four consecutive input cells of one row,
 // (mh, 4g .. 4g + 3), and computes their 2 x 8 outputs of every output channel from input rows mh
 // and mh + 1, columns 4g .. 4g + 4 (zero past the input): per channel and row one 16-byte load
-// (VEC: rows 16-byte aligned) and one scalar. The 64 lanes of a wave cover 4 rows x 16 column
-// groups; the four waves of a workgroup split the input channels (batches of CB, the next
-// batch's loads in flight) and add their accumulators through LDS in wave order; the weights are
-// staged in LDS once and read as broadcasts.
+// (VEC: rows 16-byte aligned) and one scalar. The 64 lanes of a wave take 64 consecutive column
+// groups of the row-major sequence of groups (ceil(W / 4) per row), so no lane idles on a row's
+// end (with 64-column blocks, W = 168 left 1/8 of the lanes idle and needed 774 workgroups for
+// 768 slots, one almost empty second round); the four waves of a workgroup split the input
+// channels (batches of CB, the next batch's loads in flight) and add their accumulators through
+// LDS in wave order; the weights are staged in LDS once and read as broadcasts.
 constexpr int kT2Waves = 4, kT2WMax = 12288;  // at most 48 KB of weights staged in LDS
-constexpr int kT2Rows = 4, kT2Cols = 64;      // input cells per workgroup: 4 rows x 64 columns
 template <int COUT, bool VEC>
 __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArgs a) {
   constexpr int CB = 4;
@@ -408,8 +409,11 @@ __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArg
   __shared__ float part[kT2Waves - 1][COUT * 16][64];
   const int b = blockIdx.z, lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  const int mh = blockIdx.y * kT2Rows + (lane >> 4);
-  const int mw0 = blockIdx.x * kT2Cols + 4 * (lane & 15);
+  const int gw = (a.W + 3) / 4;  // column groups per row
+  const int64_t ng = (int64_t)a.H * gw, gi = (int64_t)blockIdx.x * 64 + lane;
+  const bool live = gi < ng;
+  const int64_t gc = live ? gi : ng - 1;  // lanes past the last group load the last one
+  const int mh = (int)(gc / gw), mw0 = 4 * (int)(gc % gw);
   const int Cin = a.C1 + a.C2;
   const int64_t hw = (int64_t)a.H * a.W;
   const float* x1 = a.x1 + (int64_t)b * a.C1 * hw;
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArg
         for (int e = 0; e < 8; ++e) part[wave - 1][(oc * 2 + rh) * 8 + e][lane] = acc[oc][rh][e];
   }
   __syncthreads();
-  if (wave != 0 || mh >= a.H || mw0 >= a.W) return;
+  if (wave != 0 || !live) return;
 #pragma unroll
   for (int w = 0; w < kT2Waves - 1; ++w)
 #pragma unroll
@@ -840,14 +844,14 @@ bool convt2d_small_supported(const ConvT2DArgs& a) {
   return a.groups == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2 && a.ph == 1 &&
          a.pw == 1 && a.dh == 1 && a.dw == 1 && (a.Cout == 1 || a.Cout == 2 || a.Cout == 4) &&
          (int64_t)(a.C1 + a.C2) * a.Cout * 9 <= kT2WMax && a.Ho <= 2 * a.H && a.Wo <= 2 * a.W &&
-         a.W >= 4 && a.H <= 4 * 65535 && a.B <= 65535;
+         a.W >= 4 && (int64_t)a.H * ((a.W + 3) / 4) <= ((int64_t)1 << 36) && a.B <= 65535;
 }
 
 void convt2d_small(const LaunchCtx& c, const ConvT2DArgs& a) {
   check_convt2d(a);
   MNN_REQUIRE(a.w && convt2d_small_supported(a), MNN_ERR_INVALID_ARGUMENT,
               "convt2d_small: configuration outside the kernel's form");
-  const dim3 grid((unsigned)cdiv(a.W, kT2Cols), (unsigned)cdiv(a.H, kT2Rows), (unsigned)a.B),
+  const dim3 grid((unsigned)cdiv((int64_t)a.H * ((a.W + 3) / 4), 64), 1, (unsigned)a.B),
       block(64 * kT2Waves);
   const size_t lds = sizeof(float) * (size_t)(a.C1 + a.C2) * a.Cout * 9;
   // 16-byte row loads when every row start is 16-byte aligned (a column group past W - 4 loads

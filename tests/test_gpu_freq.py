@@ -141,6 +141,7 @@ CONVT_CASES = [
     (1, 40, 24, 4, 6, 5, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),      # concat, 4 channels
     (1, 9, 0, 1, 5, 66, (3, 3), (2, 2), (1, 1), (0, 0), (1, 1), 1),       # 1 channel, Ho = 2H - 1
     (1, 70, 0, 2, 4, 3, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),       # ragged channel split
+    (1, 48, 48, 2, 21, 168, (3, 3), (2, 2), (1, 1), (1, 1), (1, 1), 1),   # last level's width
 ]
 
 
