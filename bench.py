@@ -507,6 +507,111 @@ def freq_decoder_oracle(oracle, dec):
     return y
 
 
+def next_rows(nn, dev, stream):
+    """Rows 6-10 of the configuration table, the hot path's next rows, on synthetic inputs:
+    name -> {fn (one call), flops or byts (algorithmic), floor (read, write bytes) for the
+    bandwidth-bound rows, work (per-kernel algorithmic flops / bytes), data (the inputs)}."""
+    rows = {}
+    # time-branch decoder: the four UNetDecoderBlock levels at the config-4 lengths of a padded
+    # chunk (344064 samples -> 86016 / 21504 / 5376 / 1344), with synthetic inputs and skips of
+    # those shapes
+    dec = decoder_setup(nn, dev)
+
+    def f6():
+        y = dec["x"]
+        for blk, sk, out in zip(dec["blocks"], dec["skips"], dec["outs"]):
+            blk.forward(y, sk, out, stream)
+            y = out
+    rows["6_time_decoder_b1"] = {"fn": f6, "flops": dec["flops"], "work": dec["work"],
+                                 "data": dec}
+    # frequency branch: the four 2-D encoder levels and the four decoder levels of the
+    # reference's HTDemucs at one chunk's spectrogram (synthetic inputs and skips)
+    fenc, fdec = freq_setup(nn, dev)
+
+    def f7():
+        y = fenc["x"]
+        for blk, out in zip(fenc["blocks"], fenc["outs"]):
+            blk.forward(y, out, stream)
+            y = out
+
+    def f8():
+        y = fdec["x"]
+        for blk, sk, out in zip(fdec["blocks"], fdec["skips"], fdec["outs"]):
+            blk.forward(y, sk, out, stream)
+            y = out
+    rows["7_freq_encoder_b1"] = {"fn": f7, "flops": fenc["flops"], "work": fenc["work"],
+                                 "data": fenc}
+    rows["8_freq_decoder_b1"] = {"fn": f8, "flops": fdec["flops"], "work": fdec["work"],
+                                 "data": fdec}
+    # STFT / iSTFT of one stereo 7.8 s chunk at HTDemucs' nfft 4096 / hop 1024 (bin-major
+    # spectrogram, as the frequency branch consumes it); bytes = signal read + spectra written
+    # (forward), spectra read + signal written (inverse)
+    xs = np.random.default_rng(1008).uniform(-1, 1, (2, 343980)).astype(np.float32)
+    plan = nn.STFT(dev, 4096, 1024, "hann")
+    xst = nn.Tensor.from_numpy(dev, xs)
+    nf = plan.frame_count(343980)
+    re9, im9 = nn.Tensor(dev, (2, 2049, nf)), nn.Tensor(dev, (2, 2049, nf))
+    y9 = nn.Tensor(dev, (2, plan.output_length(nf)))
+    from metalaudio_amd._lib import check as check9, lib as lib9
+
+    def fwd():
+        check9(lib9().mnn_stft_forward(plan.handle, xst.handle, re9.handle, im9.handle, 1, 1,
+                                       stream.handle))
+
+    def inv():
+        check9(lib9().mnn_stft_inverse(plan.handle, re9.handle, im9.handle, 1, 1, 1e-10,
+                                       y9.handle, stream.handle))
+    spec_b = 2 * nf * 2049 * 8.0
+    b9 = 4.0 * xs.size + spec_b
+    rows["9_stft_b1"] = {"fn": fwd, "byts": b9, "floor": (4.0 * xs.size, spec_b),
+                         "work": {"stft_forward_f32": (0, b9)}, "data": xs,
+                         "keep": (plan, xst, re9, im9)}
+    frames_b = 4.0 * 2 * nf * 4096
+    sig_b = 4.0 * 2 * plan.output_length(nf)
+    # algorithmic bytes of the inverse: the spectra read, the signal written (the frames the
+    # first of its two kernels writes and the second reads are this build's intermediate)
+    rows["10_istft_b1"] = {"fn": inv, "byts": spec_b + sig_b, "floor": (spec_b, sig_b),
+                           "work": {"istft_frames_f32": (0, spec_b + frames_b),
+                                    "istft_overlap_add_f32": (0, frames_b + sig_b)},
+                           "keep": (plan, y9)}
+    return rows
+
+
+def profile_rows(nn, dev, stream, path):
+    """Profiling mode of rows 6-10: a warm-up call of each row, then one call each on one stream
+    (kernel timing on: every launch in host order) with the library's launch log on. Writes the
+    log, each launch name prefixed with its row ("8_freq_decoder_b1:convt2d_f32_mfma ..."), to
+    path, and the rows' per-kernel algorithmic work under the same prefixed names to
+    path.work.json, for metalaudio_amd.profsummary pmc."""
+    import ctypes
+    from metalaudio_amd._lib import lib
+    rows = next_rows(nn, dev, stream)
+    for r in rows.values():
+        r["fn"]()
+    stream.sync()
+    dev.set_kernel_timing(True)
+    lines, work = [], {}
+    for name, r in rows.items():
+        lib().mnn_debug_set_launch_log(dev.handle, 1)
+        r["fn"]()
+        stream.sync()
+        lib().mnn_debug_set_launch_log(dev.handle, 0)
+        need = ctypes.c_size_t()
+        lib().mnn_debug_launch_log(dev.handle, None, 0, ctypes.byref(need))
+        buf = ctypes.create_string_buffer(need.value)
+        rc = lib().mnn_debug_launch_log(dev.handle, buf, need.value, ctypes.byref(need))
+        if rc != 0:
+            log(f"launch log: status {rc}")
+            sys.exit(1)
+        lines += [f"{name}:{line}" for line in buf.value.decode().splitlines()]
+        work.update({f"{name}:{k}": [float(v[0]), float(v[1])] for k, v in r["work"].items()})
+    dev.set_kernel_timing(False)
+    Path(path).parent.mkdir(parents=True, exist_ok=True)
+    Path(path).write_text("\n".join(lines) + "\n")
+    Path(path).with_suffix(".work.json").write_text(json.dumps(work))
+    log(f"profile rows: {len(lines)} launches logged to {path}")
+
+
 def config_table(nn, W, dev, stream, m, cpu=True):
     """GPU ms, achieved rate and roofline fraction of each BASELINE configuration, with the fp32
     oracle's CPU time on the host beside it (the oracle is only the CPU baseline here). gpu_ms:
@@ -618,77 +723,26 @@ def config_table(nn, W, dev, stream, m, cpu=True):
         flops=f4)
     f5 = sum(v[0] for v in transformer_work(W.T5_BATCH).values())
     row("5_transformer_b4", time_gpu(lambda: run_transformer(m, stream), stream), flops=f5)
-    # time-branch decoder (next row of the hot path): the four UNetDecoderBlock levels at the
-    # config-4 lengths of a padded chunk (344064 samples -> 86016 / 21504 / 5376 / 1344), with
-    # synthetic inputs and skips of those shapes
-    dec = decoder_setup(nn, dev)
-
-    def f6():
-        y = dec["x"]
-        for blk, sk, out in zip(dec["blocks"], dec["skips"], dec["outs"]):
-            blk.forward(y, sk, out, stream)
-            y = out
-    cpu6 = time_cpu(lambda: decoder_oracle(oracle, dec), max_reps=1) if cpu else None
-    row("6_time_decoder_b1", time_gpu(f6, stream), flops=dec["flops"], cpu_ms=cpu6,
-        kernels=kernel_breakdown(dev, stream, f6, work=dec["work"]))
-    # frequency branch (next rows): the four 2-D encoder levels and the four decoder levels of
-    # the reference's HTDemucs at one chunk's spectrogram (synthetic inputs and skips)
-    fenc, fdec = freq_setup(nn, dev)
-
-    def f7():
-        y = fenc["x"]
-        for blk, out in zip(fenc["blocks"], fenc["outs"]):
-            blk.forward(y, out, stream)
-            y = out
-
-    def f8():
-        y = fdec["x"]
-        for blk, sk, out in zip(fdec["blocks"], fdec["skips"], fdec["outs"]):
-            blk.forward(y, sk, out, stream)
-            y = out
-    cpu7 = time_cpu(lambda: freq_encoder_oracle(oracle, fenc), max_reps=1) if cpu else None
-    cpu8 = time_cpu(lambda: freq_decoder_oracle(oracle, fdec), max_reps=1) if cpu else None
-    row("7_freq_encoder_b1", time_gpu(f7, stream), flops=fenc["flops"], cpu_ms=cpu7,
-        kernels=kernel_breakdown(dev, stream, f7, work=fenc["work"]))
-    row("8_freq_decoder_b1", time_gpu(f8, stream), flops=fdec["flops"], cpu_ms=cpu8,
-        kernels=kernel_breakdown(dev, stream, f8, work=fdec["work"]))
-    # STFT / iSTFT of one stereo 7.8 s chunk at HTDemucs' nfft 4096 / hop 1024 (bin-major
-    # spectrogram, as the frequency branch consumes it); bytes = signal read + spectra written
-    # (forward), spectra read + frames written and re-read + signal written (inverse)
+    nr = next_rows(nn, dev, stream)
     if cpu:
         from oracle import dsp as odsp  # CPU baseline only
-    xs = np.random.default_rng(1008).uniform(-1, 1, (2, 343980)).astype(np.float32)
-    plan = nn.STFT(dev, 4096, 1024, "hann")
-    xst = nn.Tensor.from_numpy(dev, xs)
-    nf = plan.frame_count(343980)
-    re9, im9 = nn.Tensor(dev, (2, 2049, nf)), nn.Tensor(dev, (2, 2049, nf))
-    y9 = nn.Tensor(dev, (2, plan.output_length(nf)))
-    from metalaudio_amd._lib import check as check9, lib as lib9
-
-    def fwd():
-        check9(lib9().mnn_stft_forward(plan.handle, xst.handle, re9.handle, im9.handle, 1, 1,
-                                       stream.handle))
-
-    def inv():
-        check9(lib9().mnn_stft_inverse(plan.handle, re9.handle, im9.handle, 1, 1, 1e-10,
-                                       y9.handle, stream.handle))
-    spec_b = 2 * nf * 2049 * 8.0
-    cpu9 = time_cpu(lambda: odsp.stft(xs, 4096, 1024, dtype=np.float32)) if cpu else None
-    X9 = odsp.stft(xs, 4096, 1024) if cpu else None
-    cpu10 = time_cpu(lambda: odsp.istft(X9, 4096, 1024, dtype=np.float32)) if cpu else None
-    b9 = 4.0 * xs.size + spec_b
-    row("9_stft_b1", time_gpu(fwd, stream), byts=b9, cpu_ms=cpu9,
-        floor=(4.0 * xs.size, spec_b),
-        kernels=kernel_breakdown(dev, stream, fwd, work={"stft_forward_f32": (0, b9)}))
-    frames_b = 4.0 * 2 * nf * 4096
-    sig_b = 4.0 * 2 * plan.output_length(nf)
-    # algorithmic bytes of the inverse: the spectra read, the signal written (the frames the
-    # first of its two kernels writes and the second reads are this build's intermediate)
-    row("10_istft_b1", time_gpu(inv, stream), byts=spec_b + sig_b, cpu_ms=cpu10,
-        floor=(spec_b, sig_b),
-        kernels=kernel_breakdown(dev, stream, inv, work={
-            "istft_frames_f32": (0, spec_b + frames_b),
-            "istft_overlap_add_f32": (0, frames_b + sig_b)}))
+    dec, fenc, fdec = nr["6_time_decoder_b1"]["data"], nr["7_freq_encoder_b1"]["data"], \
+        nr["8_freq_decoder_b1"]["data"]
+    xs = nr["9_stft_b1"]["data"]
+    cpus = {}
+    if cpu:
+        cpus["6_time_decoder_b1"] = time_cpu(lambda: decoder_oracle(oracle, dec), max_reps=1)
+        cpus["7_freq_encoder_b1"] = time_cpu(lambda: freq_encoder_oracle(oracle, fenc),
+                                             max_reps=1)
+        cpus["8_freq_decoder_b1"] = time_cpu(lambda: freq_decoder_oracle(oracle, fdec),
+                                             max_reps=1)
+        cpus["9_stft_b1"] = time_cpu(lambda: odsp.stft(xs, 4096, 1024, dtype=np.float32))
+        X9 = odsp.stft(xs, 4096, 1024)
+        cpus["10_istft_b1"] = time_cpu(lambda: odsp.istft(X9, 4096, 1024, dtype=np.float32))
+    for name, r in nr.items():
+        row(name, time_gpu(r["fn"], stream), flops=r.get("flops"), byts=r.get("byts"),
+            cpu_ms=cpus.get(name), floor=r.get("floor"),
+            kernels=kernel_breakdown(dev, stream, r["fn"], work=r["work"]))
     # long-audio driver: 60 s of stereo audio through the reference's default time-domain
     # HTDemucs (5 levels 48..768, k 8, s 4, 4 stems) in the guide's 30 s segments with 2 s
     # overlap (HTDEMUCS_GUIDE.md:170-191); synthetic weights and audio
@@ -754,6 +808,11 @@ def main():
                          "library's launch log on, write the log (one line per launch: name, "
                          "grid, block) to LOG and exit; metalaudio_amd.profsummary pmc attributes "
                          "a rocprofv3 run of this mode to the kernel names")
+    ap.add_argument("--profile-rows", metavar="LOG",
+                    help="profiling mode: run rows 6-10 of the configuration table once each "
+                         "(after a warm-up call) on one stream with the launch log on, write the "
+                         "log (names prefixed with the row) to LOG and exit; for "
+                         "metalaudio_amd.profsummary pmc")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -766,6 +825,9 @@ def main():
 
     dev = nn.AudioDevice(0)
     stream = nn.Stream(dev)
+    if args.profile_rows:
+        profile_rows(nn, dev, stream, args.profile_rows)
+        return
     log(f"device {dev.name}; building models ({args.precision})")
     m = build_models(nn, W, dev, args.precision)
 

@@ -18,6 +18,7 @@
 
 #include "device_utils.hpp"
 #include "kernels.hpp"
+#include "lds_dma.hpp"
 
 namespace mnn {
 namespace k {
@@ -33,12 +34,16 @@ constexpr int kPC = 64;   // channels per pack tile
 // positions q0 - (T - 1) .. q0 + 63, staged in LDS: every thread issues all its window loads
 // (clamped addresses, out-of-range values zeroed by a select, no load under a branch) before its
 // first LDS store. The unfolded rows are written 16 bytes per thread along the channel dimension.
+// The LDS tile is position-major with an odd pitch (65 channels): the stores (consecutive
+// positions of a channel) and the reads (4 channels of a position, consecutive lanes 4 channels
+// apart, the next position every 16 lanes) fall on distinct banks (a channel-major tile gave 6.4
+// conflict cycles per LDS instruction).
 template <int T>
 __global__ __launch_bounds__(256) void convt_pack_kernel(ConvTPackArgs a) {
   constexpr int W = kPQ + T - 1;  // window positions per channel
-  constexpr int PITCH = W + 1;
+  constexpr int CPITCH = kPC + 1;
   constexpr int NE = (kPC * W + 255) / 256;  // window elements per thread
-  __shared__ float tile[kPC * PITCH];
+  __shared__ float tile[W * CPITCH];
   const int b = blockIdx.z;
   const int64_t q0 = (int64_t)blockIdx.x * kPQ;
   const int c0 = blockIdx.y * kPC;
@@ -63,7 +68,7 @@ __global__ __launch_bounds__(256) void convt_pack_kernel(ConvTPackArgs a) {
 #pragma unroll
   for (int k = 0; k < NE; ++k) {
     const int e = tid + 256 * k;
-    if (e < kPC * W) tile[(e / W) * PITCH + e % W] = v[k];
+    if (e < kPC * W) tile[(e % W) * CPITCH + e / W] = v[k];
   }
   __syncthreads();
   const int kp = T * a.Cp;
@@ -74,8 +79,8 @@ __global__ __launch_bounds__(256) void convt_pack_kernel(ConvTPackArgs a) {
     const int c = c0 + 4 * c4;
     if (q >= a.Lq || c >= a.Cp) continue;
     const int col = qq + (T - 1) - t;
-    const float4 v = make_float4(tile[(4 * c4 + 0) * PITCH + col], tile[(4 * c4 + 1) * PITCH + col],
-                                 tile[(4 * c4 + 2) * PITCH + col], tile[(4 * c4 + 3) * PITCH + col]);
+    const float* tr = tile + col * CPITCH + 4 * c4;
+    const float4 v = make_float4(tr[0], tr[1], tr[2], tr[3]);
     *reinterpret_cast<float4*>(ub + q * kp + t * a.Cp + c) = v;
   }
 }
@@ -125,9 +130,11 @@ __global__ __launch_bounds__(64 * kSmallWaves) void convt_small_kernel(ConvTArgs
   constexpr int CST = COUT * S * T;  // weights per input channel, W[c][oc][r + S*t]
   extern __shared__ __attribute__((aligned(16))) float wl[];  // Cin * CST floats (dynamic)
   __shared__ float part[kSmallWaves - 1][COUT * S][64];
-  const int b = blockIdx.y, lane = threadIdx.x & 63;
+  // XCD-aware numbering: consecutive column blocks (which share a one-sample halo) on one XCD
+  const int unit = xcd_logical_tile(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+  const int bx = unit % gridDim.x, b = unit / gridDim.x, lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-  const int64_t q = (int64_t)blockIdx.x * 64 + lane;
+  const int64_t q = (int64_t)bx * 64 + lane;
   const int Cin = a.C1 + a.C2;
   const int64_t L = a.L;
   const float* x1 = a.x1 + (int64_t)b * a.C1 * L;

@@ -314,10 +314,10 @@ def pmc(args) -> str:
                      write[i]["c"].get("WRITE_SIZE", 0.0) * fac["WRITE_SIZE"]) * 1024.0
     lines = [f"# {args.title}", "", "Commands (repo root, GPU box):", "", "```"] + \
         args.cmd + ["```", "",
-                    f"One bench step ({len(log)} launches, kernel timing on so that every launch "
+                    f"{args.scope} ({len(log)} launches, kernel timing on so that every launch "
                     "runs on one stream in host order), attributed to the library's launch names "
                     "by the launch log (grid and workgroup sizes checked dispatch by dispatch). "
-                    "Per family and step:", "",
+                    f"{args.per}:", "",
                     "* `us`: summed kernel-trace duration; `frac`: algorithmic FLOP/s (MFMA-bound "
                     "rows) or bytes/s (HBM-bound rows) over the MI355X peak (157.3 TFLOP/s fp32, "
                     "8 TB/s);",
@@ -403,6 +403,8 @@ def main(argv=None) -> None:
     q.add_argument("--cmd", action="append", required=True)
     q.add_argument("--title", default="per-family counters of one bench step")
     q.add_argument("--traffic-out")
+    q.add_argument("--scope", default="One bench step", help="what the launch log covers")
+    q.add_argument("--per", default="Per family and step", help="lead-in of the column list")
     q.add_argument("--out")
     a = ap.parse_args(argv)
     if a.cmd_name in ("trace", "stats"):
