@@ -851,7 +851,9 @@ bool convt2d_small_supported(const ConvT2DArgs& a) {
   return a.groups == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2 && a.ph == 1 &&
          a.pw == 1 && a.dh == 1 && a.dw == 1 && (a.Cout == 1 || a.Cout == 2 || a.Cout == 4) &&
          (int64_t)(a.C1 + a.C2) * a.Cout * 9 <= kT2WMax && a.Ho <= 2 * a.H && a.Wo <= 2 * a.W &&
-         a.W >= 4 && (int64_t)a.H * ((a.W + 3) / 4) <= ((int64_t)1 << 36) && a.B <= 65535;
+         a.W >= 4 && a.B <= 65535 &&
+         // the workgroup numbering (column-group blocks x batch) is a 32-bit int
+         cdiv((int64_t)a.H * ((a.W + 3) / 4), 64) * a.B < ((int64_t)1 << 31);
 }
 
 void convt2d_small(const LaunchCtx& c, const ConvT2DArgs& a) {

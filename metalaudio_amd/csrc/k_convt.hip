@@ -296,7 +296,9 @@ bool convt_small_supported(int Cin, int Cout, int K, int stride, int dil, int gr
 
 void convt_small(const LaunchCtx& c, const ConvTArgs& a) {
   MNN_REQUIRE(convt_small_supported(a.C1 + a.C2, a.Cout, a.K, a.stride, a.dil, a.groups) &&
-                  a.x1 && (a.C2 == 0 || a.x2) && a.w && a.y && a.L > 0 && a.Lout > 0,
+                  a.x1 && (a.C2 == 0 || a.x2) && a.w && a.y && a.L > 0 && a.Lout > 0 &&
+                  // the workgroup numbering (column blocks x batch) is a 32-bit int
+                  cdiv(convt_rows(a.Lout, a.stride, a.pad), 64) * a.B < ((int64_t)1 << 31),
               MNN_ERR_INVALID_ARGUMENT, "convt_small: configuration outside the kernel's form");
   const dim3 grid((unsigned)cdiv(convt_rows(a.Lout, a.stride, a.pad), 64), (unsigned)a.B),
       block(64 * kSmallWaves);

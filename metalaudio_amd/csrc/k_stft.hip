@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void stft_forward_kernel(StftArgs a) {
     const float2 fe = make_float2(0.5f * (zk.x + zc.x), 0.5f * (zk.y - zc.y));
     const float2 d = make_float2(0.5f * (zk.x - zc.x), 0.5f * (zk.y + zc.y));  // (Zk - conj Zc)/2
     const float2 fo = make_float2(d.y, -d.x);                                    // -i * d
-    const float2 w = k == M ? make_float2(-1.f, 0.f) : (LDS_TW ? tws[zp(k)] : a.tw[k]);
+    const float2 w = k == M ? make_float2(-1.f, 0.f) : (LDS_TW ? tws[zp(k)] : a.tw[min(k, M - 1)]);
     const float2 t = cmul(w, fo);
     const float re = fe.x + t.x, im = fe.y + t.y;
     auto put = [&](int kk, float r, float i) {
@@ -389,7 +389,8 @@ __global__ __launch_bounds__(SkCfg<LOGM>::NT) void stft_forward_sk_kernel(StftAr
   for (int t = 0; t < KW; ++t) {
     const int i = threadIdx.x + t * NT;
     const int k = min(a.layout == 0 ? i : i / CH, M);
-    wpre[t] = k == M ? make_float2(-1.f, 0.f) : a.tw[k];
+    const float2 tk = a.tw[min(k, M - 1)];  // the table has M entries; W_N^M = -1
+    wpre[t] = k == M ? make_float2(-1.f, 0.f) : tk;
   }
   {
     const float* xs = a.x + (int64_t)b * a.n + f * a.hop;
