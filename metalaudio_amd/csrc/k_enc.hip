@@ -884,18 +884,23 @@ constexpr int kL1MaxParts = 1024;   // workgroups per batch (LDS: 8 bytes each)
 constexpr int kL1MaxSlots = 4096;   // workgroups over all batches
 
 // The conv (plus bias) of the tasks task0 + k * stride (k < TPW) of one wave; tasks past the
-// last are computed on the last one's columns and never counted or stored.
+// last are computed on the last one's columns and never counted or stored. Split into the input
+// loads and the matrix work, so a caller can issue the loads before a barrier.
 template <int CIN, bool REFLECT, int TPW>
-__device__ __forceinline__ void l1_wave_conv(const float* __restrict__ xb, int Ls, int Lo, int pad,
+__device__ __forceinline__ void l1_wave_load(const float* __restrict__ xb, int Ls, int Lo, int pad,
                                              int task0, int stride, int lane,
-                                             const float (&acv)[2][4 * CIN], const float* s_b1,
-                                             floatx16 (&ac)[TPW][2]) {
-  const int g = lane >> 5;
+                                             float (&xv)[TPW][4 * CIN]) {
   const int tasks = (Lo + 31) / 32;
-  float xv[TPW][4 * CIN];
 #pragma unroll
   for (int k = 0; k < TPW; ++k)
     l1_load_x<CIN, REFLECT>(xb, Ls, Lo, pad, min(task0 + k * stride, tasks - 1), lane, xv[k]);
+}
+
+template <int CIN, int TPW>
+__device__ __forceinline__ void l1_wave_mma(const float (&xv)[TPW][4 * CIN], int lane,
+                                            const float (&acv)[2][4 * CIN], const float* s_b1,
+                                            floatx16 (&ac)[TPW][2]) {
+  const int g = lane >> 5;
 #pragma unroll
   for (int k = 0; k < TPW; ++k) {
 #pragma unroll
@@ -904,6 +909,16 @@ __device__ __forceinline__ void l1_wave_conv(const float* __restrict__ xb, int L
       for (int v = 0; v < 16; ++v) ac[k][cb][v] = s_b1[32 * cb + 8 * (v / 4) + 4 * g + (v % 4)];
     l1_conv<CIN>(acv, xv[k], ac[k]);
   }
+}
+
+template <int CIN, bool REFLECT, int TPW>
+__device__ __forceinline__ void l1_wave_conv(const float* __restrict__ xb, int Ls, int Lo, int pad,
+                                             int task0, int stride, int lane,
+                                             const float (&acv)[2][4 * CIN], const float* s_b1,
+                                             floatx16 (&ac)[TPW][2]) {
+  float xv[TPW][4 * CIN];
+  l1_wave_load<CIN, REFLECT, TPW>(xb, Ls, Lo, pad, task0, stride, lane, xv);
+  l1_wave_mma<CIN, TPW>(xv, lane, acv, s_b1, ac);
 }
 
 // Element count of workgroup blk's partial: 48 channels x the valid columns of its waves' tasks.
@@ -992,17 +1007,24 @@ __global__ __launch_bounds__(256, TPW == 1 ? 3 : 2) void enc_l1_oneshot_kernel(
 #pragma unroll
     for (int s = 0; s < KS; ++s) acv[cb][s] = a.w1[cc * K1 + 2 * s + g] * live;
   }
-  lds_barrier();
+  // the input windows and the GroupNorm affine parameters are loaded before the barrier: none
+  // depends on it, and each is otherwise a dependent memory round trip on the workgroup's path
+  // (the window after the barrier, gamma / beta after the statistics exchange)
   const float* __restrict__ xb = a.x + (int64_t)b * CIN * a.L;
   const int Ls = (int)a.L, Lo = (int)a.Lout;
   const int tasks = (Lo + 31) / 32;
   const int stride = G * 4;
   const int task0 = blockIdx.x * 4 + wave;
+  float xv[TPW][KS];
+  l1_wave_load<CIN, REFLECT, TPW>(xb, Ls, Lo, a.pad, task0, stride, lane, xv);
+  const float gam = (tid < C && a.gamma) ? a.gamma[min(tid, C - 1)] : 1.f;
+  const float bet = (tid < C && a.beta) ? a.beta[min(tid, C - 1)] : 0.f;
+  lds_barrier();
   const unsigned tag = s_tag;
   float mean, m2;
   {
     floatx16 ac[TPW][2];
-    l1_wave_conv<CIN, REFLECT, TPW>(xb, Ls, Lo, a.pad, task0, stride, lane, acv, s_b1, ac);
+    l1_wave_mma<CIN, TPW>(xv, lane, acv, s_b1, ac);
     l1_block_stats(ac, task0, stride, Lo, lane, l1_block_count<TPW>(blockIdx.x, stride, Lo), red, mean,
                    m2);
 #pragma unroll
@@ -1049,8 +1071,8 @@ __global__ __launch_bounds__(256, TPW == 1 ? 3 : 2) void enc_l1_oneshot_kernel(
   if (tid < 64) {
     float sc = 0.f, sh = 0.f;
     if (tid < C) {
-      sc = (a.gamma ? a.gamma[tid] : 1.f) * mr.y;
-      sh = (a.beta ? a.beta[tid] : 0.f) - mr.x * sc;
+      sc = gam * mr.y;
+      sh = bet - mr.x * sc;
     }
     s_sc[tid] = sc;
     s_sh[tid] = sh;
