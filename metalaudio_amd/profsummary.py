@@ -183,6 +183,54 @@ def stats(args) -> str:
     return "\n".join(lines) + "\n"
 
 
+def floors(args) -> str:
+    """Measured floors of a configuration-table run (bench.py's Floors): the empty launch and
+    each size of the streaming kernel (its grid follows max(read, write) bytes: 64 bytes per
+    thread), beside the bandwidth-bound rows' own kernels from the same trace."""
+    rows = []
+    for p in _csvs(args.dir, "kernel_trace.csv"):
+        rows += list(csv.DictReader(open(p)))
+    dm = _demangle(sorted({r["Kernel_Name"] for r in rows}))
+    fl = collections.defaultdict(list)
+    rk = collections.defaultdict(list)
+    watch = ("conv_gn_oneshot_f32", "layernorm", "gemm_bf16_mfma_nk", "stft_forward_f32",
+             "istft_frames_f32", "istft_overlap_add_f32")
+    for r in rows:
+        k = _short(dm[r["Kernel_Name"]])
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        threads = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        fam = _family(k)
+        if fam in ("floor_empty", "floor_stream"):
+            fl[(fam, threads if fam == "floor_stream" else 0)].append(us)
+        elif fam in watch:
+            rk[fam].append(us)
+    med = statistics.median
+    lines = [f"# {args.title}", "", "Command (repo root, GPU box):", "", "```", args.cmd, "```", "",
+             "Kernel-trace durations (microseconds) of the floor kernels that bench.py's "
+             "configuration table launches beside its bandwidth-bound rows: an empty launch, and one "
+             "streaming pass (`floor_stream_kernel`, 16-byte loads and stores) per traffic size; "
+             "the pass's grid follows max(read, write) bytes, 64 bytes per thread, so rows with the "
+             "same larger side share a line (the LayerNorm's 16 + 16 MB and the bf16 Linear's 4 + 16 "
+             "MB). The rows' own kernels from the same trace follow.", "",
+             "| floor | max(read, write) MB | rows | calls | median us | min us |",
+             "|---|---|---|---|---|---|"]
+    rows_of = {2.1: "config 1 (0.35 MB read, 2.1 MB written)",
+               10.9: "STFT (2.75 read, 10.9 written), iSTFT (10.9 read, 2.74 written)",
+               16.8: "config-2 LayerNorm (16.8 + 16.8), bf16 Linear (4.2 + 16.8)"}
+    for (fam, threads), v in sorted(fl.items()):
+        mb = threads * 64 / 1e6
+        near = min(rows_of, key=lambda m: abs(m - mb)) if fam == "floor_stream" else None
+        label = rows_of[near] if near is not None and abs(near - mb) < 0.5 else ""
+        lines.append(f"| {'empty launch' if fam == 'floor_empty' else 'streaming pass'} | "
+                     f"{'-' if fam == 'floor_empty' else f'{mb:.1f}'} | {label} | {len(v)} | "
+                     f"{med(v):.2f} | {min(v):.2f} |")
+    lines += ["", "| row kernel (same trace) | calls | median us | min us |", "|---|---|---|---|"]
+    for fam in watch:
+        if rk.get(fam):
+            lines.append(f"| {fam} | {len(rk[fam])} | {med(rk[fam]):.2f} | {min(rk[fam]):.2f} |")
+    return "\n".join(lines) + "\n"
+
+
 def _counter_per_dispatch(d: str, counter: str):
     """{kernel name: [counter value per dispatch]} from a --pmc run."""
     per = collections.defaultdict(float)
@@ -386,6 +434,11 @@ def main(argv=None) -> None:
     st.add_argument("--cmd", required=True)
     st.add_argument("--title", default="rocprofv3 --stats")
     st.add_argument("--out")
+    fo = sub.add_parser("floors")
+    fo.add_argument("dir")
+    fo.add_argument("--cmd", required=True)
+    fo.add_argument("--title", default="measured floors of the configuration table")
+    fo.add_argument("--out")
     c = sub.add_parser("copy")
     c.add_argument("--mib", type=int, default=1024)
     f = sub.add_parser("traffic")
@@ -407,8 +460,8 @@ def main(argv=None) -> None:
     q.add_argument("--per", default="Per family and step", help="lead-in of the column list")
     q.add_argument("--out")
     a = ap.parse_args(argv)
-    if a.cmd_name in ("trace", "stats"):
-        text = trace(a) if a.cmd_name == "trace" else stats(a)
+    if a.cmd_name in ("trace", "stats", "floors"):
+        text = trace(a) if a.cmd_name == "trace" else stats(a) if a.cmd_name == "stats" else floors(a)
         if a.out:
             Path(a.out).write_text(text)
         print(text)
