@@ -48,16 +48,14 @@ constexpr int zslots(int m) { return m + m / 16; }
 // W_4h^p, (i0+h, i0+3h) with W_4h^(p+h)), the same operations in the same order as two radix-2
 // passes; an odd stage count ends with one radix-2 pass. z is addressed through zp(); TWP: tw is
 // the padded LDS copy (zp()), else the plain global table.
-// lt: the thread's index among the NT threads that share z (several groups of NT threads may
-// each run their own transform in lockstep; the barriers are the workgroup's).
-template <bool TWP, int NT = kThreads>
-__device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse,
-                        int lt = threadIdx.x) {
+template <bool TWP>
+__device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool inverse) {
+  const int lt = threadIdx.x;
   auto twd = [&](int i) { return tw[TWP ? zp(i) : i]; };
   int h = 1;
   for (; 2 * h < M; h <<= 2) {
     const int s1 = M / h, s2 = M / (2 * h);  // W_2h^p = tw[p * s1], W_4h^p = tw[p * s2]
-    for (int t = lt; t < M / 4; t += NT) {
+    for (int t = lt; t < M / 4; t += kThreads) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 2) + p;
       float2 w1 = twd(p * s1), w2 = twd(p * s2), w3 = twd(p * s2 + M / 2);
@@ -84,7 +82,7 @@ __device__ void fft_lds(float2* z, int M, const float2* __restrict__ tw, bool in
   }
   if (h < M) {
     const int stride = M / h;  // W_{2h}^p = tw[p * M / h]
-    for (int t = lt; t < M / 2; t += NT) {
+    for (int t = lt; t < M / 2; t += kThreads) {
       const int p = t & (h - 1);
       const int i0 = ((t - p) << 1) + p, i1 = i0 + h;
       float2 w = twd(p * stride);
