@@ -341,54 +341,112 @@ __global__ __launch_bounds__(256) void convt2d_gather_phase_kernel(ConvT2DArgs a
 // ceil(KH/SH) x SW x ceil(KW/SW) values at clamped addresses (taps outside the kernel or the input
 // zeroed by a select), every load in flight at once, and sums them in the same order as the
 // general kernels (kh ascending, then kw ascending).
-template <int KH, int KW, int SH, int SW>
+//
+// STATS: each thread computes CPT cells (cells e + 256 k of its workgroup's block of 256 * CPT,
+// every load issued before any sum), so a workgroup covers CPT times the cells and writes a
+// GroupNorm partial (count, mean, M2) of its outputs for CPT times fewer partials (every apply
+// workgroup merges all of its group's partials): stats[((b * G + g) * nparts + j) * 3],
+// j = (channel within the group) * gridDim.x + blockIdx.x, nparts = Cout / G * gridDim.x
+// (gn_apply_parts' layout), so no statistics pass reads y. The partial comes from sums of the
+// outputs less the channel's bias (the tap sums) and of their squares, reduced by DPP row sums
+// and one LDS exchange between the waves: a Welford merge over lanes (a division and a chain of
+// LDS permutes per step) left every wave waiting ~1 us at its end, which made the gather a third
+// slower.
+template <int KH, int KW, int SH, int SW, bool STATS, int CPT = 1>
 __global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a) {
   constexpr int NJH = (KH + SH - 1) / SH, NJW = (KW + SW - 1) / SW;
+  static_assert(STATS || CPT == 1, "several cells per thread only with the partials");
+  __shared__ float red[STATS ? 3 * (256 / 64) : 1];
   const unsigned nq = ((unsigned)a.Wo + SW - 1) / SW, cells = (unsigned)a.Ho * nq;
-  const unsigned e = blockIdx.x * 256u + threadIdx.x;
-  const unsigned ec = min(e, cells - 1);
   const int oc = blockIdx.y, b = blockIdx.z;
-  const int oh = (int)(ec / nq), q = (int)(ec - (unsigned)oh * nq);
   const int64_t n_in = (int64_t)a.H * a.W;
   const float* zb = a.z + ((int64_t)b * a.Cout + oc) * KH * KW * n_in;
-  const int th = oh + a.ph;
-  float v[NJH][SW][NJW];
-  bool ok[NJH][SW][NJW];
+  float v[CPT][NJH][SW][NJW];
+  bool ok[CPT][NJH][SW][NJW];
+  int ohs[CPT], qs[CPT];
 #pragma unroll
-  for (int jh = 0; jh < NJH; ++jh) {
-    const int kh = th % SH + SH * jh, ih = (th - kh) / SH;
-    const bool okh = kh < KH && th - kh >= 0 && ih < a.H;
-    const int khc = min(kh, KH - 1), ihc = min(max(ih, 0), a.H - 1);
+  for (int c = 0; c < CPT; ++c) {
+    const unsigned e = (blockIdx.x * CPT + c) * 256u + threadIdx.x;
+    const unsigned ec = min(e, cells - 1);
+    const int oh = (int)(ec / nq), q = (int)(ec - (unsigned)oh * nq);
+    ohs[c] = oh;
+    qs[c] = e < cells ? q : -1;  // -1: past the plane
+    const int th = oh + a.ph;
 #pragma unroll
-    for (int r = 0; r < SW; ++r) {
-      const int tw = SW * q + r + a.pw;
+    for (int jh = 0; jh < NJH; ++jh) {
+      const int kh = th % SH + SH * jh, ih = (th - kh) / SH;
+      const bool okh = kh < KH && th - kh >= 0 && ih < a.H;
+      const int khc = min(kh, KH - 1), ihc = min(max(ih, 0), a.H - 1);
 #pragma unroll
-      for (int jw = 0; jw < NJW; ++jw) {
-        const int kw = tw % SW + SW * jw, iw = (tw - kw) / SW;
-        const bool okw = kw < KW && tw - kw >= 0 && iw < a.W;
-        const int kwc = min(kw, KW - 1), iwc = min(max(iw, 0), a.W - 1);
-        v[jh][r][jw] = zb[(int64_t)(khc * KW + kwc) * n_in + (int64_t)ihc * a.W + iwc];
-        ok[jh][r][jw] = okh && okw;
+      for (int r = 0; r < SW; ++r) {
+        const int tw = SW * q + r + a.pw;
+#pragma unroll
+        for (int jw = 0; jw < NJW; ++jw) {
+          const int kw = tw % SW + SW * jw, iw = (tw - kw) / SW;
+          const bool okw = kw < KW && tw - kw >= 0 && iw < a.W;
+          const int kwc = min(kw, KW - 1), iwc = min(max(iw, 0), a.W - 1);
+          v[c][jh][r][jw] = zb[(int64_t)(khc * KW + kwc) * n_in + (int64_t)ihc * a.W + iwc];
+          ok[c][jh][r][jw] = okh && okw;
+        }
       }
     }
   }
-  float acc[SW];
-#pragma unroll
-  for (int r = 0; r < SW; ++r) acc[r] = 0.f;
-#pragma unroll
-  for (int jh = 0; jh < NJH; ++jh)
-#pragma unroll
-    for (int r = 0; r < SW; ++r)
-#pragma unroll
-      for (int jw = 0; jw < NJW; ++jw)
-        if (ok[jh][r][jw]) acc[r] += v[jh][r][jw];
-  if (e >= cells) return;
-  float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + oh) * a.Wo;
   const float bias = a.bias ? a.bias[oc] : 0.f;
+  float sn = 0.f, s1 = 0.f, s2 = 0.f;  // count, sum and sum of squares of acc = y - bias
 #pragma unroll
-  for (int r = 0; r < SW; ++r) {
-    const int ow = SW * q + r;
-    if (ow < a.Wo) yr[ow] = acc[r] + bias;
+  for (int c = 0; c < CPT; ++c) {
+    float acc[SW];
+#pragma unroll
+    for (int r = 0; r < SW; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int jh = 0; jh < NJH; ++jh)
+#pragma unroll
+      for (int r = 0; r < SW; ++r)
+#pragma unroll
+        for (int jw = 0; jw < NJW; ++jw)
+          if (ok[c][jh][r][jw]) acc[r] += v[c][jh][r][jw];
+    if (qs[c] < 0) continue;
+    float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + ohs[c]) * a.Wo;
+#pragma unroll
+    for (int r = 0; r < SW; ++r) {
+      const int ow = SW * qs[c] + r;
+      if (ow < a.Wo) {
+        yr[ow] = acc[r] + bias;
+        if (STATS) {
+          sn += 1.f;
+          s1 += acc[r];
+          s2 = fmaf(acc[r], acc[r], s2);
+        }
+      }
+    }
+  }
+  if (STATS) {
+    sn = wave_sum_dpp(sn);
+    s1 = wave_sum_dpp(s1);
+    s2 = wave_sum_dpp(s2);
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) {
+      red[3 * wid + 0] = sn;
+      red[3 * wid + 1] = s1;
+      red[3 * wid + 2] = s2;
+    }
+    lds_barrier();
+    if (threadIdx.x == 0) {
+      float n = 0.f, t1 = 0.f, t2 = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        n += red[3 * w + 0];
+        t1 += red[3 * w + 1];
+        t2 += red[3 * w + 2];
+      }
+      const float md = n > 0.f ? t1 / n : 0.f;
+      const int cpg = a.Cout / a.stat_groups, g = oc / cpg;
+      const int nparts = cpg * (int)gridDim.x, j = (oc % cpg) * gridDim.x + blockIdx.x;
+      float* o = a.stats + (((int64_t)b * a.stat_groups + g) * nparts + j) * 3;
+      o[0] = n;
+      o[1] = bias + md;
+      o[2] = fmaxf(t2 - t1 * md, 0.f);
+    }
   }
 }
 
@@ -743,6 +801,26 @@ void conv2d_direct(const LaunchCtx& c, const Conv2DArgs& a) {
 
 int convt2d_padded_cin(int Cin) { return (Cin + 31) / 32 * 32; }
 
+namespace {
+// The fixed-kernel gather's form (3x3, stride 2, dilation 1) and its cells (two outputs each).
+bool convt2d_gather_fixed(const ConvT2DArgs& a) {
+  return a.dh == 1 && a.dw == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2;
+}
+int64_t convt2d_gather_cells(const ConvT2DArgs& a) { return (int64_t)a.Ho * ((a.Wo + 1) / 2); }
+#ifndef MNN_GATHER_CPT
+#define MNN_GATHER_CPT 4
+#endif
+constexpr int kGatherStatsCells = MNN_GATHER_CPT;  // cells per thread of the gather with partials
+}  // namespace
+
+int convt2d_stats_parts(const ConvT2DArgs& a) {
+  const int G = a.stat_groups;
+  if (G <= 0 || a.Cout % G != 0 || !convt2d_gemm_supported(a) || convt2d_small_supported(a) ||
+      !convt2d_gather_fixed(a) || a.Ho <= 0 || a.Wo <= 0)
+    return 0;
+  return a.Cout / G * (int)cdiv(convt2d_gather_cells(a), 256 * kGatherStatsCells);
+}
+
 bool convt2d_gemm_supported(const ConvT2DArgs& a) { return a.groups == 1; }
 
 int64_t convt2d_z_floats(const ConvT2DArgs& a) {
@@ -795,10 +873,17 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
   gemm(c, g);
   ConvT2DArgs t = a;
   t.z = z;
-  if (a.dh == 1 && a.dw == 1 && a.KH == 3 && a.KW == 3 && a.sh == 2 && a.sw == 2) {
-    const int64_t cells = (int64_t)a.Ho * ((a.Wo + 1) / 2);
-    launch(c, "convt2d_gather_f32", convt2d_gather_fixed_kernel<3, 3, 2, 2>,
-           plane_grid(cells, a.Cout, a.B), dim3(256), 0, t);
+  if (a.stats) {
+    MNN_REQUIRE(convt2d_stats_parts(a) > 0, MNN_ERR_INVALID_ARGUMENT,
+                "convt2d_gemm: GroupNorm partials outside the fixed-kernel gather");
+    dim3 grid = plane_grid(convt2d_gather_cells(a), a.Cout, a.B);
+    grid.x = (unsigned)cdiv(convt2d_gather_cells(a), 256 * kGatherStatsCells);
+    launch(c, "convt2d_gather_f32",
+           convt2d_gather_fixed_kernel<3, 3, 2, 2, true, kGatherStatsCells>, grid, dim3(256), 0,
+           t);
+  } else if (convt2d_gather_fixed(a)) {
+    launch(c, "convt2d_gather_f32", convt2d_gather_fixed_kernel<3, 3, 2, 2, false>,
+           plane_grid(convt2d_gather_cells(a), a.Cout, a.B), dim3(256), 0, t);
   } else if (a.dh == 1 && a.dw == 1 && a.sw <= 8) {
     const int64_t cells = (int64_t)a.Ho * ((a.Wo + a.sw - 1) / a.sw);
     launch(c, "convt2d_gather_f32", convt2d_gather_phase_kernel, plane_grid(cells, a.Cout, a.B),

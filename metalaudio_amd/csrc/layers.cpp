@@ -1723,13 +1723,46 @@ class ConvTranspose2DLayer : public Layer {
     split_bchw(in.shape, B, C, H, W);
     run(in.f32(), (int)C, nullptr, 0, (int)B, H, W, out.f32(), s);
   }
-  // y from the channel concat [x1 (C1); x2 (C2)], C1 + C2 = in_channels.
+  // GroupNorm partials per (batch, group) that run() writes with stats for G groups (the
+  // matrix-core form's gather, gn_apply_parts' layout); 0 where it writes none.
+  int stats_parts(int B, int64_t H, int64_t W, int G) const {
+    if (!gemm_ || H >= (1 << 30) || W >= (1 << 30)) return 0;
+    k::ConvT2DArgs a = args(nullptr, d_.in_channels, nullptr, 0, B, H, W, nullptr);
+    a.stat_groups = G;
+    return k::convt2d_stats_parts(a);
+  }
+  // y from the channel concat [x1 (C1); x2 (C2)], C1 + C2 = in_channels; with stats
+  // (stats_parts(B, H, W, G) > 0 only), the GroupNorm partials of y for G groups as well.
   void run(const float* x1, int C1, const float* x2, int C2, int B, int64_t H, int64_t W,
-           float* y, Stream& s) {
+           float* y, Stream& s, float* stats = nullptr, int G = 1) {
     MNN_REQUIRE(C1 + C2 == d_.in_channels, MNN_ERR_SHAPE_MISMATCH,
                 "ConvTranspose2D: channel count mismatch");
     MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH,
                 "ConvTranspose2D: input too large");
+    MNN_REQUIRE(!stats || stats_parts(B, H, W, G) > 0, MNN_ERR_INVALID_ARGUMENT,
+                "ConvTranspose2D: GroupNorm partials outside the matrix-core form");
+    k::ConvT2DArgs a = args(x1, C1, x2, C2, B, H, W, y);
+    a.stats = stats;
+    a.stat_groups = G;
+    if (k::convt2d_small_supported(a)) {
+      k::convt2d_small(ctx(s), a);
+    } else if (gemm_) {
+      z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
+      unfold_.reserve(sizeof(float) * k::convt2d_unfold_floats(a));
+      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), unfold_.f32());
+    } else {
+      k::convt2d_direct(ctx(s), a);
+    }
+  }
+
+ protected:
+  void on_loaded(const std::string& name, const float* data, size_t) override {
+    if (name == "weight" && gemm_) pack(data);
+  }
+
+ private:
+  k::ConvT2DArgs args(const float* x1, int C1, const float* x2, int C2, int B, int64_t H,
+                      int64_t W, float* y) const {
     const auto o = out_size(H, W);
     k::ConvT2DArgs a;
     a.B = B;
@@ -1754,23 +1787,8 @@ class ConvTranspose2DLayer : public Layer {
     a.w = w_->ptr();
     a.bias = b_ ? b_->ptr() : nullptr;
     a.y = y;
-    if (k::convt2d_small_supported(a)) {
-      k::convt2d_small(ctx(s), a);
-    } else if (gemm_) {
-      z_.reserve(sizeof(float) * k::convt2d_z_floats(a));
-      unfold_.reserve(sizeof(float) * k::convt2d_unfold_floats(a));
-      k::convt2d_gemm(ctx(s), a, wpack_.f32(), z_.f32(), unfold_.f32());
-    } else {
-      k::convt2d_direct(ctx(s), a);
-    }
+    return a;
   }
-
- protected:
-  void on_loaded(const std::string& name, const float* data, size_t) override {
-    if (name == "weight" && gemm_) pack(data);
-  }
-
- private:
   void pack(const float* w) {
     const int Cp = k::convt2d_padded_cin(d_.in_channels);
     std::vector<float> h((size_t)d_.out_channels * d_.kernel_h * d_.kernel_w * Cp);
@@ -1928,6 +1946,15 @@ class FreqDecoderBlockLayer : public Layer {
     const int Cout = d_.out_channels;
     const int64_t L = os[os.size() - 2] * os.back();
     y_.reserve(sizeof(float) * B * Cout * L);
+    const int G = norm_->groups();
+    if (const int np = convt_->stats_parts((int)B, H, W, G)) {
+      // the transposed conv's gather writes the GroupNorm partials (no statistics pass over y)
+      partials_.reserve(sizeof(float) * 3 * B * G * np);
+      convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, H, W, y_.f32(), s,
+                  partials_.f32(), G);
+      norm_->apply_parts(s, y_.f32(), out->f32(), (int)B, L, partials_.f32(), np, MNN_ACT_GELU);
+      return;
+    }
     convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, H, W, y_.f32(), s);
     FreqEncoderBlockLayer::gn_gelu(norm_.get(), partials_, y_.f32(), out->f32(), (int)B, Cout, L,
                                    s);
