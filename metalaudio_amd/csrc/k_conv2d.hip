@@ -20,6 +20,8 @@
 // packed transposed to [H*W][Cp] by the 1-D transposed conv's pack kernel, then
 // convt2d_gather_kernel sums the taps that land on each output
 // (KH*KW / (sh*sw) of them on average) and adds the bias. No atomics; fixed summation order.
+#include <cstdlib>
+
 #include "device_utils.hpp"
 #include "kernels.hpp"
 #include "lds_dma.hpp"
@@ -661,6 +663,202 @@ __global__ __launch_bounds__(256) void conv2d_split_reduce_kernel(const float* _
   y[(int64_t)b * mn + e] = acc + (bias ? bias[m] : 0.f);
 }
 
+// ---------------------------------------------------------------- implicit-GEMM 3x3 conv
+// 3x3 kernel, padding 1 (reflect or zero), dilation 1, stride sh, sw in {1, 2}, groups 1, without
+// an unfolded operand: y[b][co][n] = bias[co] + sum over (ci, kh, kw) of
+// w[co][ci][kh][kw] * x[b][ci][sh*oh - 1 + kh][sw*ow - 1 + kw], n = oh * Wo + ow.
+//
+// A workgroup (four waves) computes 96 output channels x 128 consecutive positions n (which span
+// at most a few output rows), wave w the positions 32 w .. 32 w + 31 of all 96 channels as three
+// 32x32 blocks on v_mfma_f32_32x32x2_f32. The contraction runs over stages of 4 input channels
+// (36 k). A stage stages in LDS the input window its positions read (input rows
+// sh*oh_first - 1 .. sh*oh_last + 1, full width plus a padding column each side, reflected or
+// zero at load time, so the operand reads need no bounds logic) and the 96 x 36 weight slice.
+// MFMA step t (0..17) gives k slot g the channel 2 (t / 9) + g and tap t % 9, so the two halves
+// of a wave read windows one channel apart; the channel pitch in LDS is odd, so at stride 2 (the
+// 32 positions of a half on even banks) the other half reads the odd banks.
+//
+// Every address is fixed per workgroup: a thread's window and weight elements of a stage are
+// buffer loads at per-thread offsets from the stage's resource (zero padding is an offset past the
+// end, which reads 0), stored to LDS at tid + 256 i; the 18 B operand addresses of a lane are
+// precomputed and the weight slice is laid out per lane ([lane row][block][k]), so its reads take
+// immediate offsets. No VALU address work remains in the loop (VALU issue does not overlap the
+// fp32 MFMAs of a SIMD). The next stage's loads are issued into registers before this stage's
+// MFMAs and written to the other LDS buffer after them; one barrier per stage. With ksplit > 1
+// the stages are split over blockIdx.z and the raw sums go to
+// ws[((b * ksplit + p) * Cout + co) * N + n] for conv2d_split_reduce_kernel.
+constexpr int kIgBM = 96, kIgBN = 128, kIgCc = 4, kIgKS = kIgCc * 9;
+constexpr int kIgWinMax = 1200;  // window words per channel, R * (W + 2) (host-checked)
+constexpr int kIgWinPer = (kIgCc * (kIgWinMax + 1) + 255) / 256;  // window loads per thread
+constexpr int kIgARow = 3 * 37;  // a lane row's three blocks of 36 k (+1 pad each)
+constexpr int kIgAPer = (32 * kIgARow + 255) / 256;               // weight loads per thread
+constexpr unsigned kIgZero = 0x80000000u;  // buffer offset past any stage: reads 0
+constexpr int kIgBufDw = 0x00020000;       // buffer resource word 3 (gfx9 raw 32-bit loads)
+
+__global__ __launch_bounds__(256, 2) void conv2d_igemm_kernel(Conv2DArgs a, float* ws,
+                                                              int ksplit) {
+  __shared__ float win[2][256 * kIgWinPer];
+  __shared__ float as[2][256 * kIgAPer];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int N = a.Ho * a.Wo, K = a.Cin * 9;
+  const int n0 = blockIdx.x * kIgBN, m0 = blockIdx.y * kIgBM;
+  const int b = blockIdx.z / ksplit, part = blockIdx.z % ksplit;
+  const int nst = a.Cin / kIgCc / ksplit, st0 = part * nst;
+  const int WP = a.W + 2;
+  const int oh_first = n0 / a.Wo, oh_last = min(n0 + kIgBN - 1, N - 1) / a.Wo;
+  const int R = a.sh * (oh_last - oh_first) + 3, RWP = R * WP;
+  const int CP = RWP | 1;  // odd channel pitch of the LDS window
+  const int plane = a.H * a.W;
+  const float* xb = a.x + (int64_t)b * a.Cin * plane;
+  const float* wb = a.w + (int64_t)m0 * K;
+
+  // window element e = tid + 256 i: (channel c, row r, column j), its byte offset from the
+  // stage's first channel (kIgZero: zero padding or a pad slot)
+  // (quotients by the run-time pitches through a float reciprocal, corrected by one: exact for
+  // these magnitudes and a fraction of an integer division's instructions)
+  auto qdiv = [](int v, int d, float rd) {
+    int q = (int)((float)v * rd);
+    q -= q * d > v;
+    q += (q + 1) * d <= v;
+    return q;
+  };
+  const float rCP = 1.f / (float)CP, rWP = 1.f / (float)WP;
+  unsigned woff[kIgWinPer];
+#pragma unroll
+  for (int i = 0; i < kIgWinPer; ++i) {
+    const int e = tid + 256 * i;
+    const int c = min(qdiv(e, CP, rCP), kIgCc - 1), rem = e - c * CP, r = qdiv(rem, WP, rWP),
+              j = rem - r * WP;
+    int ih = a.sh * oh_first - 1 + r, iw = j - 1;
+    bool zero = e >= kIgCc * CP || rem >= RWP;
+    if (a.reflect) {
+      ih = reflect_index(ih, a.H);
+      iw = reflect_index(iw, a.W);
+    } else {
+      zero = zero || ih < 0 || ih >= a.H || iw < 0 || iw >= a.W;
+    }
+    ih = min(max(ih, 0), a.H - 1);
+    iw = min(max(iw, 0), a.W - 1);
+    woff[i] = zero ? kIgZero : 4u * (unsigned)(c * plane + ih * a.W + iw);
+  }
+  // weight element p = tid + 256 i at LDS word p of the [lane row][block][37] layout: row
+  // 32 block + lane row, k (the pad word reads k 0)
+  unsigned aoff[kIgAPer];
+#pragma unroll
+  for (int i = 0; i < kIgAPer; ++i) {
+    const int p = min(tid + 256 * i, 32 * kIgARow - 1);
+    const int lr = p / kIgARow, rem = p - lr * kIgARow, blk = rem / 37, kk = min(rem - blk * 37, 35);
+    aoff[i] = 4u * (unsigned)((32 * blk + lr) * K + kk);
+  }
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, kIgBM * K * 4, kIgBufDw);
+  float wv[kIgWinPer], av[kIgAPer];
+  auto load = [&](int st) {
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(xb + (int64_t)(st0 + st) * kIgCc * plane), (short)0, kIgCc * plane * 4, kIgBufDw);
+#pragma unroll
+    for (int i = 0; i < kIgWinPer; ++i)
+      wv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, (int)woff[i], 0, 0));
+    const int so = (st0 + st) * kIgKS * 4;
+#pragma unroll
+    for (int i = 0; i < kIgAPer; ++i)
+      av[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, (int)aoff[i], so, 0));
+  };
+  auto store = [&](float* wd, float* ad) {
+#pragma unroll
+    for (int i = 0; i < kIgWinPer; ++i) wd[tid + 256 * i] = wv[i];
+#pragma unroll
+    for (int i = 0; i < kIgAPer; ++i) ad[tid + 256 * i] = av[i];
+  };
+
+  // this lane's operand addresses: B at position n (clamped) for the 18 steps, A lane row base
+  const int g = lane >> 5, l32 = lane & 31;
+  const int n = min(n0 + 32 * wave + l32, N - 1);
+  const int oh = n / a.Wo, ow = n - oh * a.Wo;
+  const int bbase = a.sh * (oh - oh_first) * WP + a.sw * ow + g * CP;
+  int bptr[18];
+#pragma unroll
+  for (int t = 0; t < 18; ++t) {
+    const int tap = t % 9;
+    bptr[t] = bbase + 2 * (t / 9) * CP + (tap / 3) * WP + tap % 3;
+  }
+  const int abase = l32 * kIgARow + 9 * g;
+
+  floatx16 acc[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
+
+  // one stage on LDS buffer BUF; the next stage's loads in flight meanwhile
+  auto stage = [&](int st, const float* wn, const float* an, float* wd, float* ad) {
+    if (st + 1 < nst) load(st + 1);
+    // operands of 6 steps at a time, the next 6 read while these 6 steps' MFMAs run
+    float fa[2][6][3], fb[2][6];
+    auto read6 = [&](int c, float (&xa)[6][3], float (&xb)[6]) {
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        const int t = 6 * c + u;
+        xb[u] = wn[bptr[t]];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) xa[u][i] = an[abase + 37 * i + 18 * (t / 9) + t % 9];
+      }
+    };
+    read6(0, fa[0], fb[0]);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (c + 1 < 3) read6(c + 1, fa[(c + 1) & 1], fb[(c + 1) & 1]);
+#pragma unroll
+      for (int u = 0; u < 6; ++u)
+#pragma unroll
+        for (int i = 0; i < 3; ++i)
+          acc[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[c & 1][u][i], fb[c & 1][u], acc[i], 0,
+                                                        0, 0);
+      // the next chunk's LDS reads spread between this chunk's MFMAs
+      if (c + 1 < 3) {
+#pragma unroll
+        for (int r = 0; r < 18; ++r) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS reads
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (st + 1 < nst) store(wd, ad);
+    __syncthreads();
+  };
+
+  load(0);
+  store(win[0], as[0]);
+  __syncthreads();
+  for (int st = 0; st < nst; st += 2) {
+    stage(st, win[0], as[0], win[1], as[1]);
+    if (st + 1 < nst) stage(st + 1, win[1], as[1], win[0], as[0]);
+  }
+
+  // lane l, register v of block i: channel m0 + 32 i + 8 (v / 4) + 4 g + v % 4, position n
+  const int nn = n0 + 32 * wave + l32;
+  if (nn >= N) return;
+  if (ksplit > 1) {
+    float* o = ws + ((int64_t)(b * ksplit + part) * a.Cout + m0) * N + nn;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[(int64_t)(32 * i + 8 * (v / 4) + 4 * g + v % 4) * N] = acc[i][v];
+    return;
+  }
+  float* o = a.y + ((int64_t)b * a.Cout + m0) * N + nn;
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int m = 32 * i + 8 * (v / 4) + 4 * g + v % 4;
+      o[(int64_t)m * N] = acc[i][v] + (a.bias ? a.bias[m0 + m] : 0.f);
+    }
+}
+
 // K split of the unfold GEMM for grids too small to fill the chip (few output tiles, long K):
 // parts p with (Kp/32) % p == 0, at least 6 K steps each, at most 1024 tiles in all.
 int conv2d_ksplit(const Conv2DArgs& a) {
@@ -708,13 +906,49 @@ bool conv2d_pointwise(const Conv2DArgs& a) {
          a.pw == 0 && a.Ho == a.H && a.Wo == a.W;
 }
 
+bool conv2d_igemm_supported(const Conv2DArgs& a) {
+  static const bool off = [] {  // tuning override: MNN_CONV2D_IGEMM=0 keeps unfold + GEMM
+    const char* e = std::getenv("MNN_CONV2D_IGEMM");
+    return e && std::atoi(e) == 0;
+  }();
+  if (off || a.groups != 1 || a.KH != 3 || a.KW != 3 || a.dh != 1 || a.dw != 1 || a.ph != 1 ||
+      a.pw != 1 || a.sh < 1 || a.sh > 2 || a.sw < 1 || a.sw > 2 || a.Cin % kIgCc != 0 ||
+      a.Cout % kIgBM != 0 || a.H < 2 || a.W < 2 || a.B > 8191)
+    return false;
+  const int64_t N = (int64_t)a.Ho * a.Wo;
+  // rows of output spanned by 128 consecutive positions, and the window that covers them
+  const int64_t rows = (a.Wo - 1 + kIgBN - 1) / a.Wo + 1;
+  const int64_t R = a.sh * (std::min<int64_t>(rows, a.Ho) - 1) + 3;
+  // buffer resources: a stage's 4 channels and the 96-row weight slice in 32-bit byte ranges
+  return R * (a.W + 2) <= kIgWinMax && (int64_t)a.Cin * a.H * a.W * 4 < (1LL << 31) &&
+         (int64_t)a.Cout * a.Cin * 9 * 4 < (1LL << 31) && N * a.Cout < (1LL << 31) &&
+         cdiv(N, kIgBN) < 65536 * 32;
+}
+
+namespace {
+// K split of the implicit GEMM: the most parts (dividing the stage count, at least 6 stages each)
+// that keep the grid within two workgroups per CU.
+int conv2d_igemm_ksplit(const Conv2DArgs& a) {
+  const int64_t tiles = cdiv((int64_t)a.Ho * a.Wo, kIgBN) * (a.Cout / kIgBM) * a.B;
+  const int nst = a.Cin / kIgCc;
+  int best = 1;
+  for (int p : {2, 3, 4, 6, 8})
+    if (nst % p == 0 && nst / p >= 6 && tiles * p <= 512) best = p;
+  return best;
+}
+}  // namespace
+
 int64_t conv2d_split_ws_floats(const Conv2DArgs& a) {
+  if (conv2d_igemm_supported(a)) {
+    const int p = conv2d_igemm_ksplit(a);
+    return p > 1 ? (int64_t)a.B * p * a.Cout * a.Ho * a.Wo : 0;
+  }
   const int p = conv2d_ksplit(a);
   return p > 1 ? (int64_t)a.B * p * a.Cout * a.Ho * a.Wo : 0;
 }
 
 int64_t conv2d_unfold_floats(const Conv2DArgs& a) {
-  return conv2d_pointwise(a) ? 0 : (int64_t)a.B * a.Ho * a.Wo * conv2d_padded_k(a.Cin, a.KH, a.KW);
+  return conv2d_pointwise(a) || conv2d_igemm_supported(a) ? 0 : (int64_t)a.B * a.Ho * a.Wo * conv2d_padded_k(a.Cin, a.KH, a.KW);
 }
 
 void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out) {
@@ -750,6 +984,19 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
     g.ldb = N;
     g.sB = (int64_t)a.Cin * N;
     return gemm(c, g);
+  }
+  if (conv2d_igemm_supported(a)) {
+    const int parts = conv2d_igemm_ksplit(a);
+    MNN_REQUIRE(parts == 1 || split_ws, MNN_ERR_INVALID_ARGUMENT,
+                "conv2d_gemm: the K split needs a workspace");
+    const dim3 grid((unsigned)cdiv(N, kIgBN), (unsigned)(a.Cout / kIgBM),
+                    (unsigned)(a.B * parts));
+    launch(c, "conv2d_igemm_f32", conv2d_igemm_kernel, grid, dim3(256), 0, a, split_ws, parts);
+    if (parts > 1)
+      launch(c, "conv2d_split_reduce_f32", conv2d_split_reduce_kernel,
+             dim3((unsigned)cdiv(N * a.Cout, 256), (unsigned)a.B), dim3(256), 0, split_ws,
+             a.bias, a.y, a.Cout, (unsigned)N, parts);
+    return;
   }
   MNN_REQUIRE(unfold, MNN_ERR_INVALID_ARGUMENT, "conv2d_gemm: unfold buffer required");
   a.Kp = conv2d_padded_k(a.Cin, a.KH, a.KW);

@@ -233,6 +233,10 @@ void conv2d_small(const LaunchCtx& c, const Conv2DArgs& a, float* stats, int G);
 bool conv2d_gemm_supported(const Conv2DArgs& a);
 bool conv2d_pointwise(const Conv2DArgs& a);
 int64_t conv2d_unfold_floats(const Conv2DArgs& a);
+// The implicit-GEMM form (3x3, padding 1, dilation 1, stride 1 or 2, Cin % 4 == 0,
+// Cout % 96 == 0, the input window of 128 output positions within its LDS budget): conv2d_gemm
+// then reads the input in place (no unfold workspace).
+bool conv2d_igemm_supported(const Conv2DArgs& a);
 // Workspace of the K split conv2d_gemm chooses for small grids (0: no split).
 int64_t conv2d_split_ws_floats(const Conv2DArgs& a);
 void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out);

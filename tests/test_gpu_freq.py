@@ -104,6 +104,14 @@ CONV_CASES = [
     (1, 37, 19, 9, 7, (1, 1), (1, 1), "valid", (0, 0), (1, 1), 1),         # pointwise, odd sizes
     (2, 8, 12, 9, 8, (3, 3), (2, 1), "explicit", (1, 0), (1, 1), 4),       # grouped: direct
     (1, 6, 6, 12, 12, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 6),        # depthwise: direct
+    # 3x3, padding 1, Cin % 4 == 0, Cout % 96 == 0: the implicit GEMM (input windows in LDS)
+    (2, 96, 192, 40, 30, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),   # K split in 4
+    (1, 8, 96, 17, 23, (3, 3), (1, 1), "explicit", (1, 1), (1, 1), 1),   # zeros, stride 1
+    (1, 12, 96, 33, 20, (3, 3), (2, 1), "reflect", (1, 1), (1, 1), 1),   # mixed stride
+    (2, 48, 96, 130, 90, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),  # tiles over 3 rows
+    (1, 192, 384, 24, 20, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),  # K split in 8
+    (1, 4, 96, 9, 9, (3, 3), (1, 1), "same", (0, 0), (1, 1), 1),          # one partial tile
+    (1, 4, 96, 64, 1000, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),  # window too wide: unfold
     # 1 or 2 input channels, 3x3: the register-window kernel (no unfold)
     (2, 2, 48, 64, 32, (3, 3), (2, 2), "reflect", (1, 1), (1, 1), 1),
     (1, 1, 16, 33, 47, (3, 3), (1, 1), "explicit", (1, 1), (1, 1), 1),     # zeros, odd sizes
@@ -119,10 +127,22 @@ def test_conv2d_parity(dev, stream, B, cin, cout, H, W, k, s, mode, pad, d, g):
     b = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
     layer = nn.Conv2D(dev, cin, cout, k, s, mode, pad, d, g)
     layer.load_weights(w, b)
-    got = run_layer(layer, x, dev, stream)
+    res = {}
+    names = launch_names(dev, lambda: res.setdefault("y", run_layer(layer, x, dev, stream)))
+    got = res["y"]
     ref = oracle.conv2d(x, w, b, s, mode, pad, d, g)
     assert got.shape == ref.shape
     assert_close(got, ref, ATOL, RTOL, "conv2d")
+    # the implicit GEMM runs where its form applies and the input window of 128 output positions
+    # (the rows they span, full width plus two padding columns) fits its 1200 words per channel
+    Ho, Wo = ref.shape[-2:]
+    pad1 = (mode in ("reflect", "explicit") and pad == (1, 1)) or (mode == "same" and s == (1, 1))
+    rows = min((Wo - 1 + 127) // Wo + 1, Ho)
+    igemm = (k == (3, 3) and d == (1, 1) and g == 1 and pad1 and cin % 4 == 0 and cout % 96 == 0
+             and s[0] in (1, 2) and s[1] in (1, 2) and (s[0] * (rows - 1) + 3) * (W + 2) <= 1200)
+    assert ("conv2d_igemm_f32" in names) == igemm, names
+    if igemm:
+        assert "conv2d_unfold_f32" not in names, names
 
 
 CONVT_CASES = [
