@@ -680,7 +680,6 @@ constexpr LdsTile kLdsTiles[] = {
     {1, 128, 64, 0.93},   // <2,2,2,1> S3
     {2, 64, 128, 0.93},   // <2,2,1,2> S3
     {3, 64, 64, 0.88},    // <2,2,1,1> S4
-    {4, 96, 128, 0.0},    // <1,4,3,1> S2 (measurement)
 };
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -799,7 +798,6 @@ void gemm_nk_lds(const LaunchCtx& c, const GemmArgs& a) {
     case 0: return launch_lds<2, 2, 2, 2, 2>(c, a);
     case 1: return launch_lds<2, 2, 2, 1, 3>(c, a);
     case 2: return launch_lds<2, 2, 1, 2, 3>(c, a);
-    case 4: return launch_lds<1, 4, 3, 1, 2>(c, a);
     default: return launch_lds<2, 2, 1, 1, 4>(c, a);
   }
 }
