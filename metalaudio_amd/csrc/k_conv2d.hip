@@ -663,6 +663,67 @@ __global__ __launch_bounds__(256) void conv2d_split_reduce_kernel(const float* _
   y[(int64_t)b * mn + e] = acc + (bias ? bias[m] : 0.f);
 }
 
+// The same sum for one output channel per workgroup row (grid (ceil(N / 1024), M, B), four
+// positions per thread), which also writes the GroupNorm partial (count, mean, M2) of its outputs
+// for the group of its channel (G groups of M / G channels): stats[((b * G + g) * nparts + j) * 3],
+// j = (m mod (M / G)) * gridDim.x + blockIdx.x, nparts = (M / G) * gridDim.x (gn_apply_parts'
+// layout), so no statistics pass reads y. The partial comes from sums of the K-part sums (the
+// outputs less the bias) and of their squares, reduced by DPP row sums and one LDS exchange.
+constexpr int kRedGnPer = 4;  // positions per thread
+__global__ __launch_bounds__(256) void conv2d_split_reduce_gn_kernel(
+    const float* __restrict__ ws, const float* __restrict__ bias, float* __restrict__ y, int M,
+    int N, int parts, float* __restrict__ stats, int G) {
+  __shared__ float red[3 * 4];
+  const int m = blockIdx.y, b = blockIdx.z;
+  const int64_t mn = (int64_t)M * N;
+  const float* w = ws + (int64_t)b * parts * mn + (int64_t)m * N;
+  float* yr = y + (int64_t)b * mn + (int64_t)m * N;
+  const float bv = bias ? bias[m] : 0.f;
+  float acc[kRedGnPer];
+#pragma unroll
+  for (int j = 0; j < kRedGnPer; ++j) acc[j] = 0.f;
+  const int n0 = blockIdx.x * 256 * kRedGnPer + threadIdx.x;
+  for (int q = 0; q < parts; ++q)  // every load of a part in flight together
+#pragma unroll
+    for (int j = 0; j < kRedGnPer; ++j) acc[j] += w[q * mn + min(n0 + 256 * j, N - 1)];
+  float sn = 0.f, s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRedGnPer; ++j) {
+    if (n0 + 256 * j < N) {
+      yr[n0 + 256 * j] = acc[j] + bv;
+      sn += 1.f;
+      s1 += acc[j];
+      s2 = fmaf(acc[j], acc[j], s2);
+    }
+  }
+  sn = wave_sum_dpp(sn);
+  s1 = wave_sum_dpp(s1);
+  s2 = wave_sum_dpp(s2);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (lane == 0) {
+    red[3 * wid + 0] = sn;
+    red[3 * wid + 1] = s1;
+    red[3 * wid + 2] = s2;
+  }
+  lds_barrier();
+  if (threadIdx.x == 0) {
+    float n = 0.f, t1 = 0.f, t2 = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      n += red[3 * v + 0];
+      t1 += red[3 * v + 1];
+      t2 += red[3 * v + 2];
+    }
+    const float md = n > 0.f ? t1 / n : 0.f;
+    const int cpg = M / G, g = m / cpg;
+    const int nparts = cpg * (int)gridDim.x, j = (m % cpg) * gridDim.x + blockIdx.x;
+    float* o = stats + (((int64_t)b * G + g) * nparts + j) * 3;
+    o[0] = n;
+    o[1] = bv + md;
+    o[2] = fmaxf(t2 - t1 * md, 0.f);
+  }
+}
+
 // ---------------------------------------------------------------- implicit-GEMM 3x3 conv
 // 3x3 kernel, padding 1 (reflect or zero), dilation 1, stride sh, sw in {1, 2}, groups 1, without
 // an unfolded operand: y[b][co][n] = bias[co] + sum over (ci, kh, kw) of
@@ -927,7 +988,9 @@ bool conv2d_igemm_supported(const Conv2DArgs& a) {
 
 namespace {
 // K split of the implicit GEMM: the most parts (dividing the stage count, at least 6 stages each)
-// that keep the grid within two workgroups per CU.
+// that keep the grid within two workgroups per CU. (Splitting further where GroupNorm partials
+// are wanted, so that the reduce pass replaces a statistics pass, measured slower: the frequency
+// encoder's second level in two parts and the deeper ones in more lost 24 us over the row.)
 int conv2d_igemm_ksplit(const Conv2DArgs& a) {
   const int64_t tiles = cdiv((int64_t)a.Ho * a.Wo, kIgBN) * (a.Cout / kIgBM) * a.B;
   const int nst = a.Cin / kIgCc;
@@ -937,6 +1000,13 @@ int conv2d_igemm_ksplit(const Conv2DArgs& a) {
   return best;
 }
 }  // namespace
+
+int conv2d_gemm_stats_parts(const Conv2DArgs& a) {
+  const int G = a.stat_groups;
+  if (G <= 0 || a.Cout % G != 0 || !conv2d_igemm_supported(a) || conv2d_igemm_ksplit(a) < 2)
+    return 0;
+  return a.Cout / G * (int)cdiv((int64_t)a.Ho * a.Wo, 256 * kRedGnPer);
+}
 
 int64_t conv2d_split_ws_floats(const Conv2DArgs& a) {
   if (conv2d_igemm_supported(a)) {
@@ -986,13 +1056,19 @@ void conv2d_gemm(const LaunchCtx& c, const Conv2DArgs& a_in, const float* wpack,
     return gemm(c, g);
   }
   if (conv2d_igemm_supported(a)) {
+    MNN_REQUIRE(!a.stats || conv2d_gemm_stats_parts(a) > 0, MNN_ERR_INVALID_ARGUMENT,
+                "conv2d_gemm: GroupNorm partials outside the implicit GEMM's split form");
     const int parts = conv2d_igemm_ksplit(a);
     MNN_REQUIRE(parts == 1 || split_ws, MNN_ERR_INVALID_ARGUMENT,
                 "conv2d_gemm: the K split needs a workspace");
     const dim3 grid((unsigned)cdiv(N, kIgBN), (unsigned)(a.Cout / kIgBM),
                     (unsigned)(a.B * parts));
     launch(c, "conv2d_igemm_f32", conv2d_igemm_kernel, grid, dim3(256), 0, a, split_ws, parts);
-    if (parts > 1)
+    if (a.stats)
+      launch(c, "conv2d_split_reduce_f32", conv2d_split_reduce_gn_kernel,
+             dim3((unsigned)cdiv(N, 256 * kRedGnPer), (unsigned)a.Cout, (unsigned)a.B), dim3(256),
+             0, split_ws, a.bias, a.y, a.Cout, (int)N, parts, a.stats, a.stat_groups);
+    else if (parts > 1)
       launch(c, "conv2d_split_reduce_f32", conv2d_split_reduce_kernel,
              dim3((unsigned)cdiv(N * a.Cout, 256), (unsigned)a.B), dim3(256), 0, split_ws,
              a.bias, a.y, a.Cout, (unsigned)N, parts);

@@ -219,6 +219,11 @@ struct Conv2DArgs {
   float* y = nullptr;
   int Kp = 0;            // unfold row length (set by conv2d_gemm)
   float* u = nullptr;    // unfold [B][Ho*Wo][Kp] (set by conv2d_gemm)
+  // GroupNorm statistics partials of y (count, mean, M2) for stat_groups groups of output
+  // channels, conv2d_gemm_stats_parts(a) per (batch, group) in gn_apply_parts' layout, written by
+  // the implicit GEMM's split-K reduce (conv2d_gemm)
+  float* stats = nullptr;
+  int stat_groups = 1;
 };
 // Matrix-core form (groups 1): weights packed [Cout][conv2d_padded_k] (zero columns past
 // Cin*KH*KW) by conv2d_pack_weights; unfold workspace of conv2d_unfold_floats floats (0 for
@@ -237,6 +242,9 @@ int64_t conv2d_unfold_floats(const Conv2DArgs& a);
 // Cout % 96 == 0, the input window of 128 output positions within its LDS budget): conv2d_gemm
 // then reads the input in place (no unfold workspace).
 bool conv2d_igemm_supported(const Conv2DArgs& a);
+// Statistics partials per (batch, group) that conv2d_gemm writes when a.stats is set (the
+// implicit GEMM split over K, whose reduce pass writes them); 0 where it writes none.
+int conv2d_gemm_stats_parts(const Conv2DArgs& a);
 // Workspace of the K split conv2d_gemm chooses for small grids (0: no split).
 int64_t conv2d_split_ws_floats(const Conv2DArgs& a);
 void conv2d_pack_weights(const float* w, int Cout, int Cin, int KH, int KW, float* out);

@@ -1604,17 +1604,23 @@ class Conv2DLayer : public Layer {
   // GroupNorm partials per (batch, group) that run() writes for G groups (0: this configuration
   // does not produce them; the caller runs a statistics pass).
   int stats_parts(int B, int64_t H, int64_t W, int G) const {
-    return k::conv2d_small_parts(args(nullptr, B, H, W, nullptr), G);
+    k::Conv2DArgs a = args(nullptr, B, H, W, nullptr);
+    if (k::conv2d_small_supported(a)) return k::conv2d_small_parts(a, G);
+    if (!gemm_) return 0;
+    a.stat_groups = G;
+    return k::conv2d_gemm_stats_parts(a);
   }
   void run(const float* x, int B, int64_t H, int64_t W, float* y, Stream& s,
            float* stats = nullptr, int G = 0) {
     MNN_REQUIRE(H < (1 << 30) && W < (1 << 30), MNN_ERR_SHAPE_MISMATCH, "Conv2D: input too large");
-    const k::Conv2DArgs a = args(x, B, H, W, y);
-    MNN_REQUIRE(!stats || k::conv2d_small_parts(a, G) > 0, MNN_ERR_INVALID_ARGUMENT,
+    k::Conv2DArgs a = args(x, B, H, W, y);
+    MNN_REQUIRE(!stats || stats_parts(B, H, W, G) > 0, MNN_ERR_INVALID_ARGUMENT,
                 "Conv2D: this configuration writes no GroupNorm partials");
     if (k::conv2d_small_supported(a)) {
       k::conv2d_small(ctx(s), a, stats, G);
     } else if (gemm_) {
+      a.stats = stats;
+      a.stat_groups = G;
       const int64_t uf = k::conv2d_unfold_floats(a);
       if (uf > 0) unfold_.reserve(sizeof(float) * uf);
       const int64_t wf = k::conv2d_split_ws_floats(a);
@@ -1851,7 +1857,8 @@ class FreqEncoderBlockLayer : public Layer {
     y_.reserve(sizeof(float) * B * Cout * L);
     const int G = norm_->groups();
     if (const int np = conv_->stats_parts((int)B, H, W, G)) {
-      // few input channels: the direct conv writes the GroupNorm partials (no statistics pass)
+      // the direct conv (few input channels) or the implicit GEMM's split-K reduce writes the
+      // GroupNorm partials (no statistics pass)
       partials_.reserve(sizeof(float) * 3 * B * G * np);
       conv_->run(in.f32(), (int)B, H, W, y_.f32(), s, partials_.f32(), G);
       norm_->apply_parts(s, y_.f32(), out.f32(), (int)B, L, partials_.f32(), np, MNN_ACT_GELU);

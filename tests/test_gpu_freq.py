@@ -268,6 +268,33 @@ def test_freq_encoder_htdemucs_level_shapes(dev, stream):
         x = got
 
 
+@pytest.mark.parametrize("B,cin,cout,H,W,groups,split", [
+    (1, 48, 96, 1032, 168, 8, False),  # the second level on a 336-frame chunk: 339 tiles, no split
+    (2, 96, 192, 64, 70, 8, True),     # batch 2, group partials over 1024-position blocks
+    (1, 192, 384, 40, 30, 4, True),
+    (1, 8, 96, 300, 100, 3, False),    # 2 channel stages: no K split, a statistics pass
+])
+def test_freq_encoder_block_implicit_gemm(dev, stream, B, cin, cout, H, W, groups, split):
+    """3x3 / 2 levels with Cin % 4 == 0 and Cout % 96 == 0: the implicit-GEMM conv. Split over K
+    (stages of 4 input channels, at least 6 per part), its reduce pass writes the GroupNorm
+    partials, so no statistics pass reads the conv output; unsplit, the statistics pass runs."""
+    say(f"freq encoder block implicit GEMM B={B} {cin}->{cout} {H}x{W} G={groups}")
+    x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
+    w = scaled((cout, cin, 3, 3), cin * 9)
+    b = (0.3 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    gm = (1 + 0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    bt = (0.1 * RNG.standard_normal(cout)).astype(np.float32)
+    blk = nn.FreqUNetEncoderBlock2D(dev, cin, cout, (3, 3), (2, 2), groups)
+    blk.load_weights(w, b, gm, bt)
+    res = {}
+    names = launch_names(dev, lambda: res.setdefault("y", run_layer(blk, x, dev, stream)))
+    assert "conv2d_igemm_f32" in names and "conv2d_unfold_f32" not in names, names
+    assert ("conv2d_split_reduce_f32" in names) == split, names
+    assert ("gn_stats_partial" in names) != split, names
+    ref = oracle.freq_encoder_block(x, w, b, gm, bt, groups, (3, 3), (2, 2))
+    assert_close(res["y"], ref, ATOL, RTOL, "freq encoder block, implicit GEMM")
+
+
 @pytest.mark.parametrize("B,cin,cout,H,W,groups", [(1, 2, 48, 130, 90, 2),
                                                    (2, 1, 16, 40, 34, 1),
                                                    (1, 2, 48, 64, 32, 8)])
