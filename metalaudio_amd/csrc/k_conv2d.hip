@@ -740,12 +740,13 @@ __global__ __launch_bounds__(256) void conv2d_split_reduce_gn_kernel(
 // 32 positions of a half on even banks) the other half reads the odd banks.
 //
 // Every address is fixed per workgroup: a thread's window and weight elements of a stage are
-// buffer loads at per-thread offsets from the stage's resource (zero padding is an offset past the
-// end, which reads 0), stored to LDS at tid + 256 i; the 18 B operand addresses of a lane are
-// precomputed and the weight slice is laid out per lane ([lane row][block][k]), so its reads take
-// immediate offsets. No VALU address work remains in the loop (VALU issue does not overlap the
-// fp32 MFMAs of a SIMD). The next stage's loads are issued into registers before this stage's
-// MFMAs and written to the other LDS buffer after them; one barrier per stage. With ksplit > 1
+// LDS-DMA buffer loads (buffer_load_dword ... lds) at per-thread offsets from the stage's resource
+// (zero padding is an offset past the end, which reads 0) into LDS word tid + 256 i; the 18 B
+// operand addresses of a lane are precomputed and the weight slice is laid out per lane
+// ([lane row][block][k]), so its reads take immediate offsets. No VALU address work remains in
+// the loop (VALU issue does not overlap the fp32 MFMAs of a SIMD), and no registers or LDS stores
+// stage the operands: the next stage's copies go to the other LDS buffer while this stage's
+// MFMAs run; one wait and one barrier per stage. With ksplit > 1
 // the stages are split over blockIdx.z and the raw sums go to
 // ws[((b * ksplit + p) * Cout + co) * N + n] for conv2d_split_reduce_kernel.
 constexpr int kIgBM = 96, kIgBN = 128, kIgCc = 4, kIgKS = kIgCc * 9;
@@ -814,23 +815,19 @@ __global__ __launch_bounds__(256, 2) void conv2d_igemm_kernel(Conv2DArgs a, floa
   }
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)wb, (short)0, kIgBM * K * 4, kIgBufDw);
-  float wv[kIgWinPer], av[kIgAPer];
-  auto load = [&](int st) {
+  // stage st's window and weights into LDS buffer buf by LDS-DMA: element tid + 256 i lands at
+  // word tid + 256 i, i.e. wave w's 64 lanes at words 64 w + 256 i onwards
+  const unsigned win_lds = lds_address(&win[0][0]), as_lds = lds_address(&as[0][0]);
+  auto issue = [&](int st, int buf) {
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(xb + (int64_t)(st0 + st) * kIgCc * plane), (short)0, kIgCc * plane * 4, kIgBufDw);
+    const unsigned wl = win_lds + 4u * (unsigned)(buf * 256 * kIgWinPer + 64 * wave);
 #pragma unroll
-    for (int i = 0; i < kIgWinPer; ++i)
-      wv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(xrs, (int)woff[i], 0, 0));
-    const int so = (st0 + st) * kIgKS * 4;
+    for (int i = 0; i < kIgWinPer; ++i) lds_dma4_buf(xrs, woff[i], 0u, wl + 1024u * i);
+    const unsigned so = (unsigned)(st0 + st) * kIgKS * 4u;
+    const unsigned al = as_lds + 4u * (unsigned)(buf * 256 * kIgAPer + 64 * wave);
 #pragma unroll
-    for (int i = 0; i < kIgAPer; ++i)
-      av[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(wrs, (int)aoff[i], so, 0));
-  };
-  auto store = [&](float* wd, float* ad) {
-#pragma unroll
-    for (int i = 0; i < kIgWinPer; ++i) wd[tid + 256 * i] = wv[i];
-#pragma unroll
-    for (int i = 0; i < kIgAPer; ++i) ad[tid + 256 * i] = av[i];
+    for (int i = 0; i < kIgAPer; ++i) lds_dma4_buf(wrs, aoff[i], so, al + 1024u * i);
   };
 
   // this lane's operand addresses: B at position n (clamped) for the 18 steps, A lane row base
@@ -852,9 +849,9 @@ __global__ __launch_bounds__(256, 2) void conv2d_igemm_kernel(Conv2DArgs a, floa
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[i][v] = 0.f;
 
-  // one stage on LDS buffer BUF; the next stage's loads in flight meanwhile
-  auto stage = [&](int st, const float* wn, const float* an, float* wd, float* ad) {
-    if (st + 1 < nst) load(st + 1);
+  // one stage on LDS buffer st % 2; the next stage's loads in flight meanwhile
+  auto stage = [&](int st, const float* wn, const float* an) {
+    if (st + 1 < nst) issue(st + 1, (st + 1) & 1);
     // operands of 6 steps at a time, the next 6 read while these 6 steps' MFMAs run
     float fa[2][6][3], fb[2][6];
     auto read6 = [&](int c, float (&xa)[6][3], float (&xb)[6]) {
@@ -887,16 +884,16 @@ __global__ __launch_bounds__(256, 2) void conv2d_igemm_kernel(Conv2DArgs a, floa
       }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (st + 1 < nst) store(wd, ad);
-    __syncthreads();
+    wait_vmcnt<0>();  // this wave's copies of the next stage have landed ...
+    __syncthreads();  // ... and every wave's; every wave is done with this stage's buffer
   };
 
-  load(0);
-  store(win[0], as[0]);
+  issue(0, 0);
+  wait_vmcnt<0>();
   __syncthreads();
   for (int st = 0; st < nst; st += 2) {
-    stage(st, win[0], as[0], win[1], as[1]);
-    if (st + 1 < nst) stage(st + 1, win[1], as[1], win[0], as[0]);
+    stage(st, win[0], as[0]);
+    if (st + 1 < nst) stage(st + 1, win[1], as[1]);
   }
 
   // lane l, register v of block i: channel m0 + 32 i + 8 (v / 4) + 4 g + v % 4, position n

@@ -50,6 +50,15 @@ __device__ __forceinline__ void lds_dma16_s(const float* sbase, unsigned voff, u
                "s"(lds)
                : "memory", "m0");
 }
+// 4 bytes per lane through a buffer resource at per-lane byte offset `voff` (+ `soff`) into LDS at
+// byte address `lds` + 4 * lane (`lds` wave-uniform). An offset past the resource's range reads
+// zero, so padding needs no branch.
+__device__ __forceinline__ void lds_dma4_buf(__amdgpu_buffer_rsrc_t rsrc, unsigned voff,
+                                             unsigned soff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(rsrc),
+               "s"(soff), "s"(lds)
+               : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 // LDS byte address of a __shared__ object.
