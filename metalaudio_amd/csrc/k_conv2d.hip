@@ -463,7 +463,10 @@ __global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a
 // end (with 64-column blocks, W = 168 left 1/8 of the lanes idle and needed 774 workgroups for
 // 768 slots, one almost empty second round); the four waves of a workgroup split the input
 // channels (batches of CB, the next batch's loads in flight) and add their accumulators through
-// LDS in wave order; the weights are staged in LDS once and read as broadcasts.
+// LDS in wave order; the weights are staged in LDS once and read as broadcasts. With a.stats, the
+// first wave (which stores the workgroup's outputs) also writes each channel's GroupNorm partial
+// (count, mean, M2) over them: a.stats[((b * G + g) * nparts + j) * 3], j = (channel within the
+// group) * gridDim.x + block, nparts = (Cout / G) * gridDim.x (gn_apply_parts' layout).
 constexpr int kT2Waves = 4, kT2WMax = 12288;  // at most 48 KB of weights staged in LDS
 template <int COUT, bool VEC>
 __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArgs a) {
@@ -578,7 +581,7 @@ __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArg
         for (int e = 0; e < 8; ++e) part[wave - 1][(oc * 2 + rh) * 8 + e][lane] = acc[oc][rh][e];
   }
   __syncthreads();
-  if (wave != 0 || !live) return;
+  if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < kT2Waves - 1; ++w)
 #pragma unroll
@@ -590,15 +593,35 @@ __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArg
 #pragma unroll
   for (int oc = 0; oc < COUT; ++oc) {
     const float bv = a.bias ? a.bias[oc] : 0.f;
+    float sn = 0.f, s1 = 0.f, s2 = 0.f;  // count, sum and sum of squares of acc = y - bias
 #pragma unroll
     for (int rh = 0; rh < 2; ++rh) {
       const int oh = 2 * mh + rh;
-      if (oh >= a.Ho) continue;
+      if (!live || oh >= a.Ho) continue;
       float* yr = a.y + (((int64_t)b * a.Cout + oc) * a.Ho + oh) * a.Wo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int ow = 2 * mw0 + e;
-        if (ow < a.Wo) yr[ow] = acc[oc][rh][e] + bv;
+        if (ow < a.Wo) {
+          yr[ow] = acc[oc][rh][e] + bv;
+          sn += 1.f;
+          s1 += acc[oc][rh][e];
+          s2 = fmaf(acc[oc][rh][e], acc[oc][rh][e], s2);
+        }
+      }
+    }
+    if (a.stats) {  // uniform: the channel's GroupNorm partial over this workgroup's outputs
+      sn = wave_sum_dpp(sn);
+      s1 = wave_sum_dpp(s1);
+      s2 = wave_sum_dpp(s2);
+      if (lane == 0) {
+        const float md = sn > 0.f ? s1 / sn : 0.f;
+        const int cpg = a.Cout / a.stat_groups, g = oc / cpg;
+        const int nparts = cpg * (int)gridDim.x, j = (oc % cpg) * (int)gridDim.x + bx;
+        float* o = a.stats + (((int64_t)b * a.stat_groups + g) * nparts + j) * 3;
+        o[0] = sn;
+        o[1] = bv + md;
+        o[2] = fmaxf(s2 - s1 * md, 0.f);
       }
     }
   }
@@ -1135,9 +1158,10 @@ constexpr int kGatherStatsCells = MNN_GATHER_CPT;  // cells per thread of the ga
 
 int convt2d_stats_parts(const ConvT2DArgs& a) {
   const int G = a.stat_groups;
-  if (G <= 0 || a.Cout % G != 0 || !convt2d_gemm_supported(a) || convt2d_small_supported(a) ||
-      !convt2d_gather_fixed(a) || a.Ho <= 0 || a.Wo <= 0)
-    return 0;
+  if (G <= 0 || a.Cout % G != 0 || a.Ho <= 0 || a.Wo <= 0) return 0;
+  if (convt2d_small_supported(a))  // one partial per channel of each workgroup
+    return a.Cout / G * (int)cdiv((int64_t)a.H * ((a.W + 3) / 4), 64);
+  if (!convt2d_gemm_supported(a) || !convt2d_gather_fixed(a)) return 0;
   return a.Cout / G * (int)cdiv(convt2d_gather_cells(a), 256 * kGatherStatsCells);
 }
 

@@ -265,7 +265,7 @@ struct ConvT2DArgs {
   const float* z = nullptr;  // GEMM form: tap products [B][Cout*KH*KW][H*W] (set by convt2d_gemm)
   // GroupNorm statistics partials of y (count, mean, M2) for stat_groups groups of output
   // channels, convt2d_stats_parts(a) per (batch, group) at stats[((b * G + g) * parts + j) * 3]
-  // (gn_apply_parts' layout), written by the GEMM form's gather
+  // (gn_apply_parts' layout), written by the few-channel kernel or the GEMM form's gather
   float* stats = nullptr;
   int stat_groups = 1;
 };
@@ -279,8 +279,9 @@ int64_t convt2d_unfold_floats(const ConvT2DArgs& a);
 void convt2d_pack_weights(const float* w, int Cin, int Cout, int KH, int KW, float* out);
 void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, float* z,
                   float* unfold);
-// Statistics partials per (batch, group) that convt2d_gemm writes when a.stats is set (the
-// fixed-kernel gather: 3x3, stride 2, dilation 1); 0 where it writes none.
+// Statistics partials per (batch, group) that convt2d_small or convt2d_gemm writes when a.stats is
+// set (the few-channel kernel, or the GEMM form's fixed-kernel gather: 3x3, stride 2, dilation 1);
+// 0 where none are written.
 int convt2d_stats_parts(const ConvT2DArgs& a);
 void convt2d_direct(const LaunchCtx& c, const ConvT2DArgs& a);
 // Few output channels (1, 2, 4), 3x3 kernel, stride 2, padding 1, dilation 1, groups 1: a

@@ -1730,11 +1730,13 @@ class ConvTranspose2DLayer : public Layer {
     run(in.f32(), (int)C, nullptr, 0, (int)B, H, W, out.f32(), s);
   }
   // GroupNorm partials per (batch, group) that run() writes with stats for G groups (the
-  // matrix-core form's gather, gn_apply_parts' layout); 0 where it writes none.
+  // few-channel kernel or the matrix-core form's gather, gn_apply_parts' layout); 0 where it
+  // writes none.
   int stats_parts(int B, int64_t H, int64_t W, int G) const {
-    if (!gemm_ || H >= (1 << 30) || W >= (1 << 30)) return 0;
+    if (H >= (1 << 30) || W >= (1 << 30)) return 0;
     k::ConvT2DArgs a = args(nullptr, d_.in_channels, nullptr, 0, B, H, W, nullptr);
     a.stat_groups = G;
+    if (!k::convt2d_small_supported(a) && !gemm_) return 0;
     return k::convt2d_stats_parts(a);
   }
   // y from the channel concat [x1 (C1); x2 (C2)], C1 + C2 = in_channels; with stats
@@ -1955,7 +1957,8 @@ class FreqDecoderBlockLayer : public Layer {
     y_.reserve(sizeof(float) * B * Cout * L);
     const int G = norm_->groups();
     if (const int np = convt_->stats_parts((int)B, H, W, G)) {
-      // the transposed conv's gather writes the GroupNorm partials (no statistics pass over y)
+      // the transposed conv (its few-channel kernel or its gather) writes the GroupNorm partials
+      // (no statistics pass over y)
       partials_.reserve(sizeof(float) * 3 * B * G * np);
       convt_->run(in->f32(), (int)C, skip->f32(), (int)Cs, (int)B, H, W, y_.f32(), s,
                   partials_.f32(), G);

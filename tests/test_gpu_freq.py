@@ -223,8 +223,8 @@ def launch_names(dev, fn):
                                                          (1, 48, 48, 48, 200, 120, 8),
                                                          (2, 32, 0, 16, 130, 150, 1)])
 def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, groups):
-    """The block against the oracle; where the matrix-core form runs, its gather writes the
-    GroupNorm partials (no statistics pass over y), the few-channel kernel keeps the pass."""
+    """The block against the oracle; the few-channel kernel or, where the matrix-core form runs,
+    its gather writes the GroupNorm partials (no statistics pass over y)."""
     say(f"freq decoder block B={B} {cin}+{cskip}->{cout} {H}x{W} G={groups}")
     x = RNG.standard_normal((B, cin, H, W)).astype(np.float32)
     sk = RNG.standard_normal((B, cskip, H, W)).astype(np.float32)
@@ -244,7 +244,7 @@ def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, group
     out = res["out"]
     small = cout in (1, 2, 4)
     assert ("convt2d_small_f32" in names) == small, names
-    assert ("gn_stats_partial" in names) == small, names
+    assert "gn_stats_partial" not in names, names
     ref = oracle.freq_decoder_block(x, sk, w, b, gm, bt, groups)
     assert out.shape == ref.shape == (B, cout, 2 * H, 2 * W)
     assert_close(out.to_numpy(), ref, ATOL, RTOL, "freq decoder block")
