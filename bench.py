@@ -458,6 +458,8 @@ def freq_setup(nn, dev):
         ho_wo = (H // 2) * (W // 2)
         if cin <= 2:  # direct register-window level (also writes the GroupNorm partials)
             _acc(enc["work"], "conv2d_small_f32", lf, 4.0 * (cin * H * W + cout * ho_wo))
+        elif cin % 4 == 0 and cout % 96 == 0:  # implicit GEMM over LDS-staged input windows
+            _acc(enc["work"], "conv2d_igemm_f32", lf, 0)
         else:  # unfolded operand (written once) + matrix-core GEMM
             _acc(enc["work"], "conv2d_f32_mfma", lf, 0)
             _acc(enc["work"], "conv2d_unfold_f32", 0, 4.0 * (cin * H * W + 9 * cin * ho_wo))

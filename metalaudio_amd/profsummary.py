@@ -66,6 +66,8 @@ FAMILIES = [
     ("conv2d_unfold_tiled_kernel", "conv2d_unfold_f32"),
     ("conv2d_small_kernel", "conv2d_small_f32"),
     ("conv2d_split_reduce_kernel", "conv2d_split_reduce_f32"),
+    ("conv2d_split_reduce_gn_kernel", "conv2d_split_reduce_f32"),
+    ("conv2d_igemm_kernel", "conv2d_igemm_f32"),
     ("convt2d_gather_fixed_kernel", "convt2d_gather_f32"),
     ("convt2d_small_kernel", "convt2d_small_f32"),
     ("conv2d_direct_kernel", "conv2d_direct_f32"),
