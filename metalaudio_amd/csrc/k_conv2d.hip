@@ -1187,17 +1187,6 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
   const int Cin = a.C1 + a.C2, Cp = convt2d_padded_cin(Cin);
   MNN_REQUIRE(n_in * Cp < (1LL << 31) && a.B <= 65535, MNN_ERR_INVALID_ARGUMENT,
               "convt2d_gemm: input too large");
-  // operand [H*W][Cp]: the input (and the decoder's skip) transposed, channels zero-padded
-  ConvTPackArgs p;
-  p.x1 = a.x1;
-  p.x2 = a.C2 ? a.x2 : nullptr;
-  p.C1 = a.C1;
-  p.C2 = a.C2;
-  p.Cp = Cp;
-  p.L = n_in;
-  p.Lq = n_in;
-  p.u = unfold;
-  convt_pack_t1(c, p, a.B);
   const int ks = a.KH * a.KW;
   GemmArgs g;
   g.M = a.Cout * ks;
@@ -1206,14 +1195,42 @@ void convt2d_gemm(const LaunchCtx& c, const ConvT2DArgs& a, const float* wpack, 
   g.batch = a.B;
   g.A = wpack;
   g.lda = Cp;
-  g.B = unfold;
-  g.blayout = B_NK;
-  g.ldb = Cp;
-  g.sB = n_in * Cp;
   g.C = z;
   g.ldc = n_in;
   g.sC = (int64_t)g.M * n_in;
   g.name = "convt2d_f32_mfma";
+  // B = the input and the decoder's skip read in place as k-major rows [channel][H*W] (their
+  // concat and the channel padding resolved by the GEMM's loader, whose zero weight columns
+  // cancel the padding rows), where the LDS-DMA path takes them
+  g.blayout = B_KN;
+  g.bkn_lds = true;
+  g.B = a.x1;
+  g.sB = (int64_t)a.C1 * n_in;
+  g.B2 = a.C2 ? a.x2 : nullptr;
+  g.sB2 = (int64_t)a.C2 * n_in;
+  g.kc1 = a.C1;
+  g.kvalid = Cin;
+  g.ldb = n_in;
+  if (!gemm_nk_lds_supported(g)) {
+    // operand [H*W][Cp]: the input (and the decoder's skip) transposed, channels zero-padded
+    ConvTPackArgs p;
+    p.x1 = a.x1;
+    p.x2 = a.C2 ? a.x2 : nullptr;
+    p.C1 = a.C1;
+    p.C2 = a.C2;
+    p.Cp = Cp;
+    p.L = n_in;
+    p.Lq = n_in;
+    p.u = unfold;
+    convt_pack_t1(c, p, a.B);
+    g.blayout = B_NK;
+    g.bkn_lds = false;
+    g.B = unfold;
+    g.B2 = nullptr;
+    g.sB2 = 0;
+    g.ldb = Cp;
+    g.sB = n_in * Cp;
+  }
   gemm(c, g);
   ConvT2DArgs t = a;
   t.z = z;

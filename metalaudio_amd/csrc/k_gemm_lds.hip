@@ -438,7 +438,13 @@ __device__ __forceinline__ void store_part(const GemmArgs& a, const floatx16 (&a
 // consecutive k, exactly the operand of one v_mfma_f32_32x32x16_bf16 (lane group g supplies k
 // slots 8g..8g+7), so chunk c = 4g + q4 of a stage feeds MFMA step q4 for A and B alike.
 // The second launch bound asks for two workgroups per CU where two rings fit the 160 KB of LDS.
-template <int WMW, int WNW, int WM, int WN, int S, int EPI, bool BF = false>
+// BKN: B is k-major, [K][N] rows of stride ldb (the input of a transposed 2-D conv read in place,
+// with a second matrix for rows kc1 .. kvalid - 1: the decoder's skip concat; rows past kvalid
+// repeat the last valid one, whose products the zero columns of A cancel). A stage then holds
+// B as [32 k rows][BN n], 16-byte chunk c of row r stored at slot c ^ (8 * ((r / 16) mod 2)), so
+// the two lane groups (rows r and r + 16) read opposite halves of the 64 banks; each lane reads
+// its 4 k of column n with four 4-byte LDS reads at row offsets that are immediates.
+template <int WMW, int WNW, int WM, int WN, int S, int EPI, bool BF = false, bool BKN = false>
 __global__ __launch_bounds__(WMW* WNW * 64,
                              (2 * S * (WMW * WM + WNW * WN) * 32 * BK * 4 <= 160 * 1024) ? 2 : 1)
 void gemm_nk_lds_kernel(GemmArgs a) {
@@ -486,6 +492,22 @@ void gemm_nk_lds_kernel(GemmArgs a) {
     const int gn = min(n0 + rr, N - 1);
     boffg[i] = (unsigned)(ES * gn * a.ldb + 16 * (ls ^ chunk_swizzle(rr)));
   }
+  // BKN: instruction i of this wave fills stage rows (wave * B_INS + i) * RPI + lane / CPR
+  // (CPR 16-byte chunks per row), slot lane % CPR: that row's column chunk slot ^ swizzle,
+  // clamped to the last whole chunk of the row (columns past N are never stored)
+  constexpr int CPR = BN / 4, RPI = 64 / CPR;
+  static_assert(!BKN || (BN >= 64 && !BF && EPI == 0), "k-major B: 64+ columns, fp32, plain epilogue");
+  int bkr[BKN ? B_INS : 1], bkc[BKN ? B_INS : 1];
+  if constexpr (BKN) {
+#pragma unroll
+    for (int i = 0; i < B_INS; ++i) {
+      const int r = (wave * B_INS + i) * RPI + lane / CPR, slot = lane % CPR;
+      bkr[i] = r;
+      bkc[i] = min(n0 + 4 * (slot ^ (8 * ((r >> 4) & 1))), N - 4);
+    }
+  }
+  const float* B1 = a.B + (int64_t)bz * a.sB;
+  const float* B2 = a.B2 ? a.B2 + (int64_t)bz * a.sB2 : B1;
   const unsigned lds0 = lds_address(smem);
   auto issue = [&](int kt, int slot) {
     const unsigned base = lds0 + 4u * (unsigned)(slot * STAGE);
@@ -495,10 +517,21 @@ void gemm_nk_lds_kernel(GemmArgs a) {
     for (int i = 0; i < A_INS; ++i)
       lds_dma16_s(ak, aoffg[i],
                   __builtin_amdgcn_readfirstlane(base + 4u * ((wave * A_INS + i) * 8 * BK)));
+    if constexpr (BKN) {
 #pragma unroll
-    for (int i = 0; i < B_INS; ++i)
-      lds_dma16_s(bk, boffg[i],
-                  __builtin_amdgcn_readfirstlane(base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
+      for (int i = 0; i < B_INS; ++i) {
+        const int k = min((kt0 + kt) * BK + bkr[i], a.kvalid - 1);
+        const float* src = (k < a.kc1 ? B1 + (int64_t)k * a.ldb
+                                      : B2 + (int64_t)(k - a.kc1) * a.ldb) + bkc[i];
+        lds_dma16(src, __builtin_amdgcn_readfirstlane(
+                           base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < B_INS; ++i)
+        lds_dma16_s(bk, boffg[i], __builtin_amdgcn_readfirstlane(
+                                      base + 4u * (BM * BK + (wave * B_INS + i) * 8 * BK)));
+    }
   };
 
   floatx16 acc[WM][WN];
@@ -521,8 +554,13 @@ void gemm_nk_lds_kernel(GemmArgs a) {
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
     const int rr = wn * WN * 32 + 32 * j + l32;
-    boff[j] = BM * BK + rr * BK;
-    bsw[j] = chunk_swizzle(rr);
+    if constexpr (BKN) {  // column rr of row 16 g of the stage's B
+      boff[j] = BM * BK + 16 * g * BN + ((((rr >> 2) ^ (8 * g)) << 2) | (rr & 3));
+      bsw[j] = 0;
+    } else {
+      boff[j] = BM * BK + rr * BK;
+      bsw[j] = chunk_swizzle(rr);
+    }
   }
 
   // Software pipeline: the fragments of stage kt sit in registers while the matrix cores work on
@@ -546,8 +584,14 @@ void gemm_nk_lds_kernel(GemmArgs a) {
       for (int i = 0; i < WM; ++i)
         xa[q4][i] = *reinterpret_cast<const float4*>(base + aoff[i] + 4 * (c ^ asw[i]));
 #pragma unroll
-      for (int j = 0; j < WN; ++j)
-        xb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
+      for (int j = 0; j < WN; ++j) {
+        if constexpr (BKN) {  // k = 16 g + 4 q4 + s: rows 4 q4 + s below the lane's row base
+          const float* bp = base + boff[j] + 4 * q4 * BN;
+          xb[q4][j] = make_float4(bp[0], bp[BN], bp[2 * BN], bp[3 * BN]);
+        } else {
+          xb[q4][j] = *reinterpret_cast<const float4*>(base + boff[j] + 4 * (c ^ bsw[j]));
+        }
+      }
     }
   };
   auto mfma_slice = [&](const float4 (&xa)[4][WM], const float4 (&xb)[4][WN], int q4) {
@@ -595,7 +639,7 @@ void gemm_nk_lds_kernel(GemmArgs a) {
         mfma_slice(fa[cur], fb[cur], 3);
         // fragment reads alternate with the first MFMAs of the second half, so the last read has
         // the remaining MFMAs to complete before the next stage needs it
-        constexpr int kReads = 4 * (WM + WN), kMfma = 8 * WM * WN;
+        constexpr int kReads = 4 * WM + (BKN ? 16 : 4) * WN, kMfma = 8 * WM * WN;
         if constexpr (BF) {
           // bf16: one MFMA per fragment pair and k step, 2 * WM * WN in the second half; the
           // reads are spread over them
@@ -722,7 +766,9 @@ void launch_lds(const LaunchCtx& c, const GemmArgs& a) {
            gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0, true>, grid, block, 0, a);
   } else {
     const char* name = a.name ? a.name : "gemm_f32_mfma_nk";
-    if (a.ksplit > 1)
+    if (a.blayout == B_KN)
+      launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 0, false, true>, grid, block, 0, a);
+    else if (a.ksplit > 1)
       launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 3>, grid, block, 0, a);
     else if (a.glu) launch(c, name, gemm_nk_lds_kernel<WMW, WNW, WM, WN, S, 1>, grid, block, 0, a);
     else if (a.ct_stride > 0)
@@ -765,6 +811,16 @@ bool gemm_nk_lds_supported(const GemmArgs& a) {
   // per-lane load offsets are 32-bit byte offsets from the operand (batch) base
   const bool off32 = ((int64_t)(a.M - 1) * a.lda + a.K) * 4 < ((int64_t)1 << 32) &&
                      ((int64_t)(a.N - 1) * a.ldb + a.K) * 4 < ((int64_t)1 << 32);
+  if (a.blayout == B_KN) {
+    // k-major B read in place (opt-in): plain epilogue, whole 16-byte chunks per row
+    return a.bkn_lds && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 && a.N >= 4 &&
+           a.N % 4 == 0 && a.ldb % 4 == 0 && a.sB % 4 == 0 && a.sB2 % 4 == 0 && aligned16(a.B) &&
+           (!a.B2 || aligned16(a.B2)) && a.kvalid >= 1 && a.kc1 >= 0 && a.kc1 <= a.kvalid &&
+           ((int64_t)(a.M - 1) * a.lda + a.K) * 4 < ((int64_t)1 << 32) && a.lda % 4 == 0 &&
+           a.sA % 4 == 0 && aligned16(a.A) && a.pro_coef == nullptr && a.pro_stats == nullptr &&
+           !a.glu && a.ct_stride == 0 && a.ksplit == 1 && a.stats == nullptr && !a.ln_parts &&
+           !a.row_parts && a.bias_mode != BIAS_M && a.R == nullptr && a.act == 0;
+  }
   return off32 && a.blayout == B_NK && a.precision == MNN_PRECISION_F32 && a.K % BK == 0 &&
          a.lda % 4 == 0 && a.ldb % 4 == 0 && a.sA % 4 == 0 && a.sB % 4 == 0 && aligned16(a.A) &&
          aligned16(a.B) && a.pro_coef == nullptr && a.pro_stats == nullptr &&

@@ -133,6 +133,13 @@ struct GemmArgs {
   const float* B = nullptr;
   int64_t ldb = 0, sB = 0;
   int blayout = B_NK;
+  // B_KN on the LDS-DMA path (opt-in, bkn_lds): rows k < kc1 from B, rows kc1 .. kvalid - 1 from
+  // B2 (row k - kc1, batch stride sB2), rows past kvalid repeat the last valid row (A's columns
+  // there must be zero)
+  bool bkn_lds = false;
+  const float* B2 = nullptr;
+  int64_t sB2 = 0;
+  int kc1 = 0, kvalid = 0;
   int conv_L = 0, conv_ks = 1, conv_stride = 1, conv_pad = 0, conv_dil = 1;
   bool conv_reflect = false;
   // Optional prologue on B (B_KN / B_CONVREC): B[k][n] <- act(B[k][n]*scale_k + shift_k); this
