@@ -221,7 +221,9 @@ def launch_names(dev, fn):
                                                          # (beyond 512: the merge's second pass)
                                                          (1, 96, 96, 48, 100, 120, 8),
                                                          (1, 48, 48, 48, 200, 120, 8),
-                                                         (2, 32, 0, 16, 130, 150, 1)])
+                                                         (2, 32, 0, 16, 130, 150, 1),
+                                                         # H * W odd: the packed operand
+                                                         (1, 40, 40, 24, 33, 21, 8)])
 def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, groups):
     """The block against the oracle; the few-channel kernel or, where the matrix-core form runs,
     its gather writes the GroupNorm partials (no statistics pass over y)."""
@@ -245,6 +247,9 @@ def test_freq_decoder_block_parity(dev, stream, B, cin, cskip, cout, H, W, group
     small = cout in (1, 2, 4)
     assert ("convt2d_small_f32" in names) == small, names
     assert "gn_stats_partial" not in names, names
+    # the tap GEMM reads the input and skip in place when H * W is a multiple of 4 (whole 16-byte
+    # chunks per row); otherwise they are packed transposed first
+    assert ("convt_pack_f32" in names) == (not small and (H * W) % 4 != 0), names
     ref = oracle.freq_decoder_block(x, sk, w, b, gm, bt, groups)
     assert out.shape == ref.shape == (B, cout, 2 * H, 2 * W)
     assert_close(out.to_numpy(), ref, ATOL, RTOL, "freq decoder block")
