@@ -291,47 +291,37 @@ __device__ __forceinline__ void welford_combine(float& n, float& mean, float& m2
   n = nt;
 }
 
-// Workgroup-wide (count, mean, M2) of per-thread values, merged with Chan's formula.
-// Each thread passes its own (n, mean, m2); thread 0 receives the workgroup result.
-// `red` must hold 3 * (blockDim.x / 64) floats of LDS.
+// Workgroup-wide (count, mean, M2) of per-thread values: the workgroup mean from DPP sums of the
+// counts and of count * mean, then M2 = sum of (M2 + count * (mean - workgroup mean)^2), Chan's
+// merge written about the final mean, so no term cancels. Two DPP wave sums and two LDS exchanges
+// in a fixed order: a merge over the lanes (a division and an LDS permute chain per step) left
+// every wave ~1 us at its end in short kernels.
+// Each thread passes its own (n, mean, m2); thread 0 receives the workgroup result. Every lane of
+// every wave must be active. `red` must hold 3 * (blockDim.x / 64) floats of LDS.
 __device__ __forceinline__ void block_welford(float& n, float& mean, float& m2, float* red) {
-  // wave level: tree over lanes
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float n2 = __shfl_xor(n, off, kWave);
-    float mean2 = __shfl_xor(mean, off, kWave);
-    float m22 = __shfl_xor(m2, off, kWave);
-    float nt = n + n2;
-    if (nt > 0.f) {
-      float d = mean2 - mean;
-      float w = n2 / nt;
-      mean = mean + d * w;
-      m2 = m2 + m22 + d * d * n * w;
-    }
-    n = nt;
-  }
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const float c = wave_sum_dpp(n), s = wave_sum_dpp(n * mean);
   if (lane == 0) {
-    red[wid * 3 + 0] = n;
-    red[wid * 3 + 1] = mean;
-    red[wid * 3 + 2] = m2;
+    red[wid * 3 + 0] = c;
+    red[wid * 3 + 1] = s;
   }
   __syncthreads();
+  float C = 0.f, S = 0.f;
+  for (int w = 0; w < nw; ++w) {
+    C += red[w * 3 + 0];
+    S += red[w * 3 + 1];
+  }
+  const float M = C > 0.f ? S / C : 0.f;
+  const float d = mean - M;
+  const float q = wave_sum_dpp(n > 0.f ? fmaf(n * d, d, m2) : 0.f);
+  if (lane == 0) red[wid * 3 + 2] = q;
+  __syncthreads();
   if (threadIdx.x == 0) {
-    n = red[0];
-    mean = red[1];
-    m2 = red[2];
-    for (int w = 1; w < nw; ++w) {
-      float n2 = red[w * 3 + 0], mean2 = red[w * 3 + 1], m22 = red[w * 3 + 2];
-      float nt = n + n2;
-      if (nt > 0.f) {
-        float d = mean2 - mean;
-        float wt = n2 / nt;
-        mean = mean + d * wt;
-        m2 = m2 + m22 + d * d * n * wt;
-      }
-      n = nt;
-    }
+    float Q = 0.f;
+    for (int w = 0; w < nw; ++w) Q += red[w * 3 + 2];
+    n = C;
+    mean = M;
+    m2 = Q;
   }
 }
 
