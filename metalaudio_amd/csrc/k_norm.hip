@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
       v[i] = gv[i] = bv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  const float mean = wave_sum(s) / (float)F;
+  const float mean = wave_sum_dpp(s) / (float)F;
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_reg_kernel(const float* __
       q += (a * a + b * b) + (c * c + d * d);
     }
   }
-  const float var = wave_sum(q) / (float)F;
+  const float var = wave_sum_dpp(q) / (float)F;
   const float rstd = 1.f / sqrtf(var + eps);
   float4* yr = reinterpret_cast<float4*>(y + row * F);
   wait_vmcnt<0>();  // every load has landed: the stores below need no waits between them
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_pipe_kernel(
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) s += (cur[i].x + cur[i].y) + (cur[i].z + cur[i].w);
-    const float mean = wave_sum(s) / (float)F;
+    const float mean = wave_sum_dpp(s) / (float)F;
     float q = 0.f;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(kThreads) void layernorm_pipe_kernel(
                   d = cur[i].w - mean;
       q += (a * a + b * b) + (c * c + d * d);
     }
-    const float rstd = 1.f / sqrtf(wave_sum(q) / (float)F + eps);
+    const float rstd = 1.f / sqrtf(wave_sum_dpp(q) / (float)F + eps);
     // unconditional stores: a row past the last one was computed from the last row and writes
     // the same bytes there (under a branch, the compiler's waits after it would also wait for
     // these stores)
@@ -478,13 +478,13 @@ __global__ __launch_bounds__(kThreads) void layernorm_generic_kernel(
   const float* xr = x + row * F;
   float s = 0.f;
   for (int i = lane; i < F; i += 64) s += xr[i];
-  const float mean = wave_sum(s) / (float)F;
+  const float mean = wave_sum_dpp(s) / (float)F;
   float q = 0.f;
   for (int i = lane; i < F; i += 64) {
     float d = xr[i] - mean;
     q += d * d;
   }
-  const float var = wave_sum(q) / (float)F;
+  const float var = wave_sum_dpp(q) / (float)F;
   const float rstd = 1.f / sqrtf(var + eps);
   float* yr = y + row * F;
   for (int i = lane; i < F; i += 64) yr[i] = gamma[i] * ((xr[i] - mean) * rstd) + beta[i];
