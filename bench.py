@@ -482,9 +482,10 @@ def freq_setup(nn, dev):
         dec["params"].append((w, b, gm, bt, g, sk))
         lf = 2.0 * 2 * cin * cout * 9 * h * w_
         dec["flops"] += lf
-        if cout >= 8:  # tap GEMM over the packed [input; skip], then the gather of the taps
+        if cout >= 8:  # tap GEMM over [input; skip], then the gather of the taps
             _acc(dec["work"], "convt2d_f32_mfma", lf, 0)
-            _acc(dec["work"], "convt_pack_f32", 0, 4.0 * 2 * cin * h * w_ * 2)
+            if (h * w_) % 4:  # the GEMM reads them in place unless rows are not 16-byte multiples
+                _acc(dec["work"], "convt_pack_f32", 0, 4.0 * 2 * cin * h * w_ * 2)
             _acc(dec["work"], "convt2d_gather_f32", 0, 4.0 * (9 * cout * h * w_ + cout * 4 * h * w_))
         else:
             _acc(dec["work"], "convt2d_small_f32", lf, 4.0 * (2 * cin * h * w_ + cout * 4 * h * w_))
