@@ -143,29 +143,27 @@ __global__ __launch_bounds__(256) void conv2d_unfold_tiled_kernel(Conv2DArgs a) 
 // partial (count, mean, M2) of its outputs (two passes over a thread's registers, then the
 // workgroup merge) for the group its COB channels belong to (the host checks that COB divides the
 // group's channel count): parts[((b * G + g) * nparts + j) * 3], j = (channel block within the
-// group) * gridDim.x + position block, nparts = (C / G / COB) * gridDim.x. Workgroups of 1024 threads
-// keep the partial count (which every apply workgroup merges) low.
-constexpr int kC2Threads = 1024;  // output positions per workgroup (one per thread)
-template <int CIN, int COB, bool REFLECT>
-__global__ __launch_bounds__(kC2Threads) void conv2d_small_kernel(Conv2DArgs a, float* stats,
-                                                                 int G) {
+// group) * gridDim.x + position block, nparts = (C / G / COB) * gridDim.x. Large workgroups (NT
+// threads, 512 or 1024) keep the partial count (which every apply workgroup merges) low.
+template <int CIN, int COB, bool REFLECT, int NT>
+__global__ __launch_bounds__(NT) void conv2d_small_kernel(Conv2DArgs a, float* stats, int G) {
   constexpr int CK = CIN * 9;
   __shared__ __attribute__((aligned(16))) float wt[CK * COB + COB];  // [tap][co], then bias
-  __shared__ float red[3 * (kC2Threads / 64)];
+  __shared__ float red[3 * (NT / 64)];
   // (numbering the workgroups that read one input window, one per block of COB output channels,
   // onto one XCD measured 11 % slower)
   const int nx = gridDim.x, bx = blockIdx.x, b = blockIdx.z, co0 = blockIdx.y * COB;
   const unsigned hw = (unsigned)a.Ho * (unsigned)a.Wo;
-  const unsigned n = bx * (unsigned)kC2Threads + threadIdx.x;
+  const unsigned n = bx * (unsigned)NT + threadIdx.x;
   const bool valid = n < hw;
   const unsigned nc = valid ? n : hw - 1;
   const int oh = (int)(nc / (unsigned)a.Wo), ow = (int)(nc - (unsigned)oh * a.Wo);
   // weights and bias of this workgroup's channels (issued first)
-  constexpr int NW = CK * COB + COB, PER = (NW + kC2Threads - 1) / kC2Threads;
+  constexpr int NW = CK * COB + COB, PER = (NW + NT - 1) / NT;
   float wv[PER];
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
-    const int i = threadIdx.x + kC2Threads * r;
+    const int i = threadIdx.x + NT * r;
     const int iw = min(i, CK * COB - 1), co = iw / CK, e = iw - co * CK;
     const float* src = i < CK * COB ? a.w + (int64_t)(co0 + co) * CK + e
                                     : (a.bias ? a.bias + co0 + min(i - CK * COB, COB - 1)
@@ -196,7 +194,7 @@ __global__ __launch_bounds__(kC2Threads) void conv2d_small_kernel(Conv2DArgs a, 
       }
 #pragma unroll
   for (int r = 0; r < PER; ++r) {
-    const int i = threadIdx.x + kC2Threads * r;
+    const int i = threadIdx.x + NT * r;
     if (i < CK * COB) {
       const int co = i / CK, e = i - co * CK;
       wt[e * COB + co] = wv[r];
@@ -1260,7 +1258,17 @@ int64_t convt2d_unfold_floats(const ConvT2DArgs& a) {
 }
 
 namespace {
-constexpr int kC2Cob = 8;  // output channels per thread of conv2d_small_kernel
+constexpr int kC2Cob = 8;  // output channels per thread of conv2d_small_kernel (the smaller form)
+// (output channels per thread, threads per workgroup): 24 x 512 where the channels (and the
+// GroupNorm's groups) split into blocks of 24, else 8 x 1024. On the frequency encoder's first
+// level (48 channels, 2 groups) 24 x 512 took 16.0 + 15.7 us (conv + apply) against 19.0 + 15.7:
+// a thread's window loads and index work serve three times as many outputs, and 512-thread
+// workgroups keep the partials the apply merges at 339 per group (256 threads: 678, apply 17.2).
+struct C2Shape { int cob, nt; };
+C2Shape small_shape(const Conv2DArgs& a, int G) {
+  const bool by24 = a.Cout % 24 == 0 && (G <= 0 || (a.Cout % G == 0 && (a.Cout / G) % 24 == 0));
+  return by24 ? C2Shape{24, 512} : C2Shape{kC2Cob, 1024};
+}
 }
 
 bool conv2d_small_supported(const Conv2DArgs& a) {
@@ -1272,24 +1280,30 @@ bool conv2d_small_supported(const Conv2DArgs& a) {
 int conv2d_small_parts(const Conv2DArgs& a, int G) {
   if (!conv2d_small_supported(a) || G <= 0 || a.Cout % G != 0 || (a.Cout / G) % kC2Cob != 0)
     return 0;
-  return (a.Cout / G / kC2Cob) * (int)cdiv((int64_t)a.Ho * a.Wo, kC2Threads);
+  const C2Shape sh = small_shape(a, G);
+  return (a.Cout / G / sh.cob) * (int)cdiv((int64_t)a.Ho * a.Wo, sh.nt);
 }
 
 void conv2d_small(const LaunchCtx& c, const Conv2DArgs& a, float* stats, int G) {
   check_conv2d(a);
   MNN_REQUIRE(conv2d_small_supported(a) && a.w && (!stats || conv2d_small_parts(a, G) > 0),
               MNN_ERR_INVALID_ARGUMENT, "conv2d_small: configuration outside the kernel's form");
-  const dim3 grid((unsigned)cdiv((int64_t)a.Ho * a.Wo, kC2Threads), (unsigned)(a.Cout / kC2Cob),
+  const C2Shape sh = small_shape(a, G);
+  const dim3 grid((unsigned)cdiv((int64_t)a.Ho * a.Wo, sh.nt), (unsigned)(a.Cout / sh.cob),
                   (unsigned)a.B);
-#define MNN_C2S(CI, R) \
-  return launch(c, "conv2d_small_f32", conv2d_small_kernel<CI, kC2Cob, R>, grid, \
-                dim3(kC2Threads), 0, a, stats, G)
+#define MNN_C2S(CI, R, COB, NT) \
+  return launch(c, "conv2d_small_f32", conv2d_small_kernel<CI, COB, R, NT>, grid, dim3(NT), 0, a, \
+                stats, G)
+#define MNN_C2S_CI(CI, R) \
+  if (sh.cob == 24) MNN_C2S(CI, R, 24, 512); \
+  MNN_C2S(CI, R, 8, 1024)
   if (a.Cin == 1) {
-    if (a.reflect) MNN_C2S(1, true);
-    MNN_C2S(1, false);
+    if (a.reflect) { MNN_C2S_CI(1, true); }
+    MNN_C2S_CI(1, false);
   }
-  if (a.reflect) MNN_C2S(2, true);
-  MNN_C2S(2, false);
+  if (a.reflect) { MNN_C2S_CI(2, true); }
+  MNN_C2S_CI(2, false);
+#undef MNN_C2S_CI
 #undef MNN_C2S
 }
 
