@@ -510,6 +510,34 @@ def freq_decoder_oracle(oracle, dec):
     return y
 
 
+def long_audio_setup():
+    """The long-audio row's model: the reference's default time-domain HTDemucs (5 levels,
+    48..768 channels, k 8, s 4, 4 stems, 8 groups) with seeded synthetic weights in the
+    Separator's state-dict naming; returns (generator for the audio, config, state)."""
+    r11 = np.random.default_rng(1009)
+    ch11 = [48, 96, 192, 384, 768]
+    cfg11 = {"input_channels": 2, "num_stems": 4, "channels": ch11, "kernel_size": 8,
+             "stride": 4, "num_groups": 8}
+    P11, chans = {}, [2] + ch11
+    for i in range(5):
+        ci, co = chans[i], chans[i + 1]
+        P11[f"time_encoder.{i}"] = {
+            "conv.weight": (r11.standard_normal((co, ci, 8)) * np.sqrt(2 / (8 * ci))).astype(
+                np.float32), "conv.bias": np.zeros(co, np.float32),
+            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
+    for j in range(5):
+        i = 4 - j
+        ci, co = chans[i + 1], (2 if i == 0 else chans[i])
+        P11[f"time_decoder.{j}"] = {
+            "conv_transpose.weight": (r11.standard_normal((2 * ci, co, 8)) * np.sqrt(
+                1 / (4 * ci))).astype(np.float32), "conv_transpose.bias": np.zeros(co, np.float32),
+            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
+    for h in range(4):
+        P11[f"output_heads.{h}"] = {"weight": r11.standard_normal((2, 2, 1)).astype(np.float32),
+                                    "bias": np.zeros(2, np.float32)}
+    return r11, cfg11, P11
+
+
 def next_rows(nn, dev, stream):
     """Rows 6-10 of the configuration table, the hot path's next rows, on synthetic inputs:
     name -> {fn (one call), flops or byts (algorithmic), floor (read, write bytes) for the
@@ -751,27 +779,7 @@ def config_table(nn, W, dev, stream, m, cpu=True):
     # overlap (HTDEMUCS_GUIDE.md:170-191); synthetic weights and audio
     if cpu:
         from oracle import separate as osep  # CPU baseline only
-    r11 = np.random.default_rng(1009)
-    ch11 = [48, 96, 192, 384, 768]
-    cfg11 = {"input_channels": 2, "num_stems": 4, "channels": ch11, "kernel_size": 8,
-             "stride": 4, "num_groups": 8}
-    P11, chans = {}, [2] + ch11
-    for i in range(5):
-        ci, co = chans[i], chans[i + 1]
-        P11[f"time_encoder.{i}"] = {
-            "conv.weight": (r11.standard_normal((co, ci, 8)) * np.sqrt(2 / (8 * ci))).astype(
-                np.float32), "conv.bias": np.zeros(co, np.float32),
-            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
-    for j in range(5):
-        i = 4 - j
-        ci, co = chans[i + 1], (2 if i == 0 else chans[i])
-        P11[f"time_decoder.{j}"] = {
-            "conv_transpose.weight": (r11.standard_normal((2 * ci, co, 8)) * np.sqrt(
-                1 / (4 * ci))).astype(np.float32), "conv_transpose.bias": np.zeros(co, np.float32),
-            "norm.weight": np.ones(co, np.float32), "norm.bias": np.zeros(co, np.float32)}
-    for h in range(4):
-        P11[f"output_heads.{h}"] = {"weight": r11.standard_normal((2, 2, 1)).astype(np.float32),
-                                    "bias": np.zeros(2, np.float32)}
+    r11, cfg11, P11 = long_audio_setup()
     sep = nn.Separator(dev)
     sep.load_state(P11)
     n11 = 44100 * 60

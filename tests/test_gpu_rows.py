@@ -82,3 +82,21 @@ def test_freq_decoder_row_full_size(dev, stream):
         ref = oracle.freq_decoder_block(y.to_numpy(), skh, w, b, gm, bt, g)
         assert_close(out.to_numpy(), ref, ATOL, RTOL, f"frequency decoder level {lvl}")
         y = out
+
+
+def test_long_audio_row_full_size(dev, stream):
+    """The long-audio row: 60 s of stereo audio through the reference's default time-domain
+    HTDemucs (5 levels, 48..768 channels) in 30 s segments with 2 s overlap, as bench.py times it,
+    against the fp64 oracle's segmentation and blend (oracle/separate.py) over the whole run."""
+    from oracle import separate as osep
+    r11, cfg, P = bench.long_audio_setup()
+    n = 44100 * 60
+    x = r11.uniform(-1, 1, 2 * n).astype(np.float32)
+    say(f"long audio: 2 x {n} samples, segments {44100 * 30}, overlap {44100 * 2}")
+    sep = nn.Separator(dev)
+    sep.load_state(P)
+    out = sep.separate_long(nn.Tensor.from_numpy(dev, x), 44100 * 30, 44100 * 2, stream)
+    stream.sync(60000)
+    ref = osep.separate_long(x, 2, 44100 * 30, 44100 * 2, lambda s: osep.separate_time(s, P, cfg))
+    assert out.shape == ref.shape == (4, 2 * n)
+    assert_close(out.to_numpy(), ref, ATOL, RTOL, "long audio 60 s")
