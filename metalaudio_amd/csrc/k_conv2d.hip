@@ -468,7 +468,8 @@ __global__ __launch_bounds__(256) void convt2d_gather_fixed_kernel(ConvT2DArgs a
 constexpr int kT2Waves = 4, kT2WMax = 12288;  // at most 48 KB of weights staged in LDS
 template <int COUT, bool VEC>
 __global__ __launch_bounds__(64 * kT2Waves) void convt2d_small_kernel(ConvT2DArgs a) {
-  constexpr int CB = 4;
+  // channels per load batch (the frequency decoder's last level: 26.3 us at 2, 27.9 at 3, 28.1 at 4)
+  constexpr int CB = 2;
   constexpr int CST = COUT * 9;  // weights per input channel, w[c][oc][kh][kw]
   extern __shared__ __attribute__((aligned(16))) float wl[];  // Cin * CST floats (dynamic)
   __shared__ float part[kT2Waves - 1][COUT * 16][64];
