@@ -15,26 +15,20 @@ typedef short shortx8 __attribute__((ext_vector_type(8)));
 constexpr int kWave = 64;
 
 // sigmoid with the +-88 clamp of the reference's stable_sigmoid (Shaders/NN.metal:32-47);
-// 1/(1+e^-x) and e^x/(1+e^x) are the same number, so one branchless form suffices.
+// 1/(1+e^-x) and e^x/(1+e^x) are the same number, so one branchless form suffices. The reciprocal
+// is the hardware's (v_rcp_f32, about 1 ulp): an IEEE division is ten instructions, which the
+// GLU epilogues of the matrix-core kernels pay in full beside their MFMAs.
 __device__ __forceinline__ float stable_sigmoid(float x) {
   x = fminf(fmaxf(x, -88.f), 88.f);
-  return 1.f / (1.f + __expf(-x));
+  return __builtin_amdgcn_rcpf(1.f + __expf(-x));
 }
 
 // tanh-approximation GELU: 0.5 x (1 + tanh(u)), u = sqrt(2/pi)(x + 0.044715 x^3).
 // Evaluated as x * sigmoid(2u), the same function (1 + tanh(u) = 2 sigmoid(2u)), which needs one
-// exp and no cancellation near u = 0. For |x| large the exp saturates to 0 / inf and the result
-// is x / -0, as the clamped reference form (Activations.swift:124-137) gives.
+// exp and no cancellation near u = 0; the hardware reciprocal as in stable_sigmoid. For |x| large
+// the exp saturates to 0 / inf and the result is x / -0, as the clamped reference form
+// (Activations.swift:124-137) gives.
 __device__ __forceinline__ float gelu_tanh(float x) {
-  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
-  const float k1 = 0.044715f;
-  float u = k0 * (x + k1 * x * x * x);
-  return x / (1.f + __expf(-2.f * u));
-}
-
-// The same function with the division replaced by the hardware reciprocal (about 1 ulp): for
-// operand transforms inside matrix-core loops, where an IEEE division would dominate the work.
-__device__ __forceinline__ float gelu_tanh_fast(float x) {
   const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
   const float k1 = 0.044715f;
   const float u = k0 * fmaf(k1 * x, x * x, x);

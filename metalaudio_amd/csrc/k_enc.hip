@@ -519,7 +519,7 @@ __global__ __launch_bounds__(256, 4) void enc_reduce_gn_t_kernel(EncGnKArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float sc = s_gb[w + 4 * i] * mr.y;
-    tileb[w + 4 * i][lane] = gelu_tanh_fast(fmaf(v[i], sc, s_gb[kGC + w + 4 * i] - mr.x * sc));
+    tileb[w + 4 * i][lane] = gelu_tanh(fmaf(v[i], sc, s_gb[kGC + w + 4 * i] - mr.x * sc));
   }
   lds_barrier();
   // stores: thread covers positions tt * kGT + tid / 8 + 32 j, channels 4 (tid % 8) .. + 3
@@ -610,10 +610,10 @@ __global__ __launch_bounds__(256) void enc_gn_gelu_t_kernel(EncRewriteArgs a) {
       const float2 c = cf[r];
       const bool live = k0 + r < a.C;  // padded rows stay zero
       float4 z;
-      z.x = live ? gelu_tanh_fast(fmaf(cur[i].x, c.x, c.y)) : 0.f;
-      z.y = live ? gelu_tanh_fast(fmaf(cur[i].y, c.x, c.y)) : 0.f;
-      z.z = live ? gelu_tanh_fast(fmaf(cur[i].z, c.x, c.y)) : 0.f;
-      z.w = live ? gelu_tanh_fast(fmaf(cur[i].w, c.x, c.y)) : 0.f;
+      z.x = live ? gelu_tanh(fmaf(cur[i].x, c.x, c.y)) : 0.f;
+      z.y = live ? gelu_tanh(fmaf(cur[i].y, c.x, c.y)) : 0.f;
+      z.z = live ? gelu_tanh(fmaf(cur[i].z, c.x, c.y)) : 0.f;
+      z.w = live ? gelu_tanh(fmaf(cur[i].w, c.x, c.y)) : 0.f;
       tileb[r][lc + 0] = z.x;
       tileb[r][lc + 1] = z.y;
       tileb[r][lc + 2] = z.z;
@@ -844,7 +844,7 @@ __global__ __launch_bounds__(256, 2) void enc_l1_fused_kernel(EncL1KArgs a) {
     l1_conv<CIN>(acv, xv, ac);
     float z[kL1KP];
 #pragma unroll
-    for (int p = 0; p < kL1KP; ++p) z[p] = gelu_tanh_fast(ac[p / 16][p % 16]);
+    for (int p = 0; p < kL1KP; ++p) z[p] = gelu_tanh(ac[p / 16][p % 16]);
     floatx16 ar[kL1MB];
 #pragma unroll
     for (int mb = 0; mb < kL1MB; ++mb)
@@ -1089,7 +1089,7 @@ __global__ __launch_bounds__(256, TPW == 1 ? 3 : 2) void enc_l1_oneshot_kernel(
       const int cb = p / 16, v = p % 16;
       const int ch = 32 * cb + 8 * (v / 4) + 4 * g + (v % 4);
       const float y = stash[((wave * TPW + k) * 32 + p) * 64 + lane];
-      z[p] = gelu_tanh_fast(fmaf(y, s_sc[ch], s_sh[ch]));
+      z[p] = gelu_tanh(fmaf(y, s_sc[ch], s_sh[ch]));
     }
     floatx16 ar[kL1MB];
 #pragma unroll
