@@ -91,18 +91,25 @@ __global__ __launch_bounds__(256, AttnCfg<HD>::OCC) void attn_fwd_f32_kernel(Att
   auto issue = [&](int blk, bool isv, int par) {
     const unsigned base = lds0 + 4u * (unsigned)(((isv ? 2 : 0) + par) * SLOT);
     const float* src = (isv ? vb : kb) + (int64_t)blk * BKV * a.kv_rs;
-    const bool tail = blk * BKV + BKV > a.Sk;
+    // The tail block's clamped offsets are computed in a branch of their own, around their own
+    // loads: with only the offset under the branch the compiler if-converted it, and every block
+    // paid the clamp arithmetic (~50 VALU instructions per 64-key block, beside 96 MFMAs).
+    if (blk * BKV + BKV > a.Sk) {  // rows past the last key re-read the last key (scores masked)
 #pragma unroll
-    for (int i = 0; i < LW; ++i) {
-      const int j = i * NW + wave;
-      if (j < PC) {
-        unsigned off = soff[i];
-        if (tail) {  // rows past the last key re-read the last key (their scores are masked)
+      for (int i = 0; i < LW; ++i) {
+        const int j = i * NW + wave;
+        if (j < PC) {
           const int e = j * 64 + lane;
-          off = 4u * (unsigned)(min(e / PC, a.Sk - 1 - blk * BKV) * (int)a.kv_rs +
-                                4 * min(e % PC, PC - 2));
+          const unsigned off = 4u * (unsigned)(min(e / PC, a.Sk - 1 - blk * BKV) * (int)a.kv_rs +
+                                               4 * min(e % PC, PC - 2));
+          lds_dma16_s(src, off, base + 4u * (unsigned)(j * 256));
         }
-        lds_dma16_s(src, off, base + 4u * (unsigned)(j * 256));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < LW; ++i) {
+        const int j = i * NW + wave;
+        if (j < PC) lds_dma16_s(src, soff[i], base + 4u * (unsigned)(j * 256));
       }
     }
   };
