@@ -134,18 +134,29 @@ __global__ __launch_bounds__(WMW* WNW * 64) void enc_conv_kernel(ConvKArgs a) {
     const unsigned base = lds0 + 4u * (unsigned)((kl % S) * STAGE);
     const float* asrc = a.W + kt * BK;
     const float* bsrc = xb + (int64_t)(4 * kt) * Ls;
-    const bool chan_tail = 4 * kt + 4 > a.Cin;  // padded input channels read the last real one
+    // padded input channels read the last real one; that stage's offsets are computed in a branch
+    // of its own, around its own loads (with only the offset under the branch the compiler
+    // if-converted it, and every stage paid the clamp arithmetic)
+    if (4 * kt + 4 > a.Cin) {
 #pragma unroll
-    for (int i = 0; i < L; ++i) {
-      const int j = i * NW + wave;
-      if (j < A_WL) {
-        lds_dma16_s(asrc, off[i], base + 4u * (unsigned)(j * 256));
-      } else if (j < T) {
-        unsigned o = off[i];
-        if (chan_tail)
-          o = 4u * (unsigned)((min(4 * kt + bch[i], a.Cin - 1) - 4 * kt) * Ls +
-                              min(max(bpos[i], 0), Ls - 4));
-        lds_dma16_s(bsrc, o, base + 4u * (unsigned)(Cfg::A_FLOATS + (j - A_WL) * 256));
+      for (int i = 0; i < L; ++i) {
+        const int j = i * NW + wave;
+        if (j < A_WL) {
+          lds_dma16_s(asrc, off[i], base + 4u * (unsigned)(j * 256));
+        } else if (j < T) {
+          const unsigned o = 4u * (unsigned)((min(4 * kt + bch[i], a.Cin - 1) - 4 * kt) * Ls +
+                                             min(max(bpos[i], 0), Ls - 4));
+          lds_dma16_s(bsrc, o, base + 4u * (unsigned)(Cfg::A_FLOATS + (j - A_WL) * 256));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < L; ++i) {
+        const int j = i * NW + wave;
+        if (j < A_WL)
+          lds_dma16_s(asrc, off[i], base + 4u * (unsigned)(j * 256));
+        else if (j < T)
+          lds_dma16_s(bsrc, off[i], base + 4u * (unsigned)(Cfg::A_FLOATS + (j - A_WL) * 256));
       }
     }
   };
